@@ -1,0 +1,125 @@
+"""ctypes binding of libtfq (include/tfq.h, include/tfq_runtime.h).
+
+The shared library is built in-tree by edgeexpert_amd.build into
+edgeexpert_amd/lib/. There is no fallback: if libtfq.so or its code object is
+missing, loading raises TfqNotBuilt.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libtfq.so")
+CODE_OBJECT_PATH = os.path.join(LIB_DIR, "tfq_kernels.co")
+
+TFQ_OK = 0
+TFQ_E_INVAL = 1
+TFQ_E_UNSUPPORTED = 2
+TFQ_E_HIP = 3
+TFQ_E_NOT_LOADED = 4
+ROUTER_WORKSPACE_BYTES = 4096
+
+
+class TfqNotBuilt(RuntimeError):
+    pass
+
+
+class TfqError(RuntimeError):
+    def __init__(self, status: int, where: str):
+        lib = _load()
+        self.status = status
+        self.hip_error = lib.tfq_last_hip_error()
+        msg = lib.tfq_last_error_message().decode(errors="replace")
+        super().__init__(f"{where}: {lib.tfq_status_string(status).decode()} ({msg})")
+
+
+class Q4Matrix(C.Structure):
+    _fields_ = [("weights", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p)]
+
+
+class ExpertOffsets(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b")]
+
+
+class ExpertPoolDesc(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("stride", C.c_uint64), ("num_experts", C.c_uint32),
+                ("offsets", ExpertOffsets)]
+
+
+_P = C.c_void_p
+_U32 = C.c_uint32
+_I = C.c_int
+
+# name -> argtypes (restype int unless listed in _RES)
+SIGNATURES = {
+    "tfq_create": [C.POINTER(C.c_void_p), C.c_char_p],
+    "tfq_destroy": [_P],
+    "tfq_status_string": [_I],
+    "tfq_last_hip_error": [],
+    "tfq_last_error_message": [],
+    "tfq_gemv_q4g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32],
+    "tfq_gemv_q4g64_qkv": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
+                           _P, _P, _P, _P, _U32, _U32, _U32],
+    "tfq_gemv_q8g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32],
+    "tfq_router_topk": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
+    "tfq_moe_phase1": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _U32, _U32, _U32],
+    "tfq_moe_phase1_subset": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _P, _U32, _U32, _U32,
+                              _U32],
+    "tfq_moe_phase2": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _P, _P, _U32, _U32, _U32],
+    "tfq_moe_decode": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
+    "tfq_shared_expert_q4": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
+                             _P, _P, _U32, _U32, _P],
+    "tfq_convert_bf16_to_f16": [_P, _P, _P, _P, C.c_uint64, _P],
+    "tfq_rt_device_count": [C.POINTER(_I)],
+    "tfq_rt_set_device": [_I],
+    "tfq_rt_device_info": [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t],
+    "tfq_rt_malloc": [C.POINTER(C.c_void_p), C.c_size_t],
+    "tfq_rt_free": [_P],
+    "tfq_rt_memcpy_htod": [_P, _P, C.c_size_t],
+    "tfq_rt_memcpy_dtoh": [_P, _P, C.c_size_t],
+    "tfq_rt_memcpy_dtod": [_P, _P, C.c_size_t, _P],
+    "tfq_rt_memset": [_P, _I, C.c_size_t],
+    "tfq_rt_stream_create": [C.POINTER(C.c_void_p)],
+    "tfq_rt_stream_destroy": [_P],
+    "tfq_rt_stream_sync": [_P],
+    "tfq_rt_device_sync": [],
+    "tfq_rt_event_create": [C.POINTER(C.c_void_p)],
+    "tfq_rt_event_destroy": [_P],
+    "tfq_rt_event_record": [_P, _P],
+    "tfq_rt_event_sync": [_P],
+    "tfq_rt_event_elapsed_ms": [C.POINTER(C.c_float), _P, _P],
+    "tfq_rt_capture_begin": [_P],
+    "tfq_rt_capture_end": [_P, C.POINTER(C.c_void_p)],
+    "tfq_rt_graph_launch": [_P, _P],
+    "tfq_rt_graph_destroy": [_P],
+}
+_RES = {"tfq_destroy": None, "tfq_status_string": C.c_char_p,
+        "tfq_last_error_message": C.c_char_p}
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not (os.path.exists(LIB_PATH) and os.path.exists(CODE_OBJECT_PATH)):
+            raise TfqNotBuilt(f"{LIB_PATH} / {CODE_OBJECT_PATH} missing: run "
+                              "`python -m edgeexpert_amd.build` first")
+        lib = C.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            f = getattr(lib, name)
+            f.argtypes = args
+            f.restype = _RES.get(name, C.c_int)
+        _lib = lib
+    return _lib
+
+
+def lib():
+    return _load()
+
+
+def check(status: int, where: str):
+    if status != TFQ_OK:
+        raise TfqError(status, where)

@@ -1,0 +1,90 @@
+// module.hpp — the loaded gfx950 code object and the launch/error plumbing
+// shared by the operator classes (ops.hpp) and the C ABI (tfq.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <unordered_map>
+
+#include "../../../include/tfq.h"
+
+namespace tfq {
+
+// Per-thread record of the last failure (returned through tfq_last_*()).
+struct ErrorState {
+    int hip = 0;
+    char message[512] = {0};
+};
+ErrorState& error_state();
+
+inline int fail(int status, const char* fmt, ...) {
+    ErrorState& e = error_state();
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(e.message, sizeof(e.message), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+inline int hip_check(hipError_t err, const char* what) {
+    if (err == hipSuccess) return TFQ_OK;
+    ErrorState& e = error_state();
+    e.hip = (int)err;
+    std::snprintf(e.message, sizeof(e.message), "%s: %s", what, hipGetErrorString(err));
+    return TFQ_E_HIP;
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+inline uint32_t pow2ceil(uint32_t v) {
+    uint32_t p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+// The code object: every kernel resolved by name once, at creation.
+class Module {
+public:
+    int load(const char* path);
+    ~Module();
+    hipFunction_t get(const std::string& name) const {
+        auto it = fns_.find(name);
+        return it == fns_.end() ? nullptr : it->second;
+    }
+    int device() const { return device_; }
+
+private:
+    hipModule_t module_ = nullptr;
+    int device_ = -1;
+    std::unordered_map<std::string, hipFunction_t> fns_;
+};
+
+// Launch with kernel arguments given as an array of pointers to values.
+inline int launch(hipFunction_t f, uint32_t grid, uint32_t block, uint32_t lds, void* stream,
+                  void** args, const char* name) {
+    if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
+    return hip_check(hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, lds, (hipStream_t)stream,
+                                           args, nullptr),
+                     name);
+}
+
+// Instantiation picked for a reduction of `chunks` 16-byte chunks per row:
+// SEG lanes per row (power of two <= 64) and P chunks per lane.
+struct SegShape {
+    uint32_t seg;
+    uint32_t p;
+};
+
+inline SegShape seg_shape(uint32_t chunks, uint32_t min_seg) {
+    if (chunks <= 64) {
+        uint32_t s = pow2ceil(chunks);
+        return {s < min_seg ? min_seg : s, 1};
+    }
+    return {64, (chunks + 63) / 64};
+}
+
+}  // namespace tfq

@@ -1,0 +1,258 @@
+// ops.hpp — C++ operator classes mirroring the reference's Swift kernel
+// wrappers (S/Kernels/**): same class names, same argument meaning, one
+// `encode` per reference `encode`. Where the Swift wrapper traps on a
+// precondition these return TFQ_E_INVAL; where it would silently skip they
+// return an error too. A stream replaces the command buffer; device
+// pointers replace (MTLBuffer, offset) pairs.
+#pragma once
+
+#include "../kernels/abi_types.h"
+#include "module.hpp"
+
+namespace tfq {
+
+constexpr uint32_t kBlock = 256;          // 4 wavefronts per block for every GEMV-family kernel
+constexpr uint32_t kMaxGridBlocks = 4096;
+constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident in LDS
+
+inline uint32_t grid_for_rows(uint64_t rows, uint32_t rows_per_block) {
+    uint64_t g = (rows + rows_per_block - 1) / rows_per_block;
+    if (g < 1) g = 1;
+    return (uint32_t)(g > kMaxGridBlocks ? kMaxGridBlocks : g);
+}
+
+// S/Kernels/Quant/DequantInt4GEMV.swift:5-181 (encode and encodeTgx share one kernel here:
+// x always lives in LDS) and S/Kernels/Fusions/FusedQKVGEMV.swift:4-157.
+class DequantInt4GEMV {
+public:
+    explicit DequantInt4GEMV(const Module& m) : m_(m) {}
+
+    // DequantInt4GEMV.encode (DequantInt4GEMV.swift:84-127).
+    int encode(void* stream, const void* weights, const uint16_t* scales, const uint16_t* biases,
+               const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n) const {
+        Q4Multi mats{};
+        mats.m[0] = {static_cast<const uint8_t*>(weights), scales, biases, y, m, 0};
+        mats.nmat = 1;
+        mats.total_rows = m;
+        return launch_multi(stream, mats, x, n);
+    }
+
+    // FusedQKVGEMV.encode (FusedQKVGEMV.swift:92-156): rows mq + 2*mkv in one launch.
+    int encode_qkv(void* stream, const tfq_q4_matrix& q, const tfq_q4_matrix& k,
+                   const tfq_q4_matrix& v, const uint16_t* x, uint16_t* yq, uint16_t* yk,
+                   uint16_t* yv, uint32_t mq, uint32_t mkv, uint32_t n) const {
+        Q4Multi mats{};
+        mats.m[0] = {static_cast<const uint8_t*>(q.weights), q.scales, q.biases, yq, mq, 0};
+        mats.m[1] = {static_cast<const uint8_t*>(k.weights), k.scales, k.biases, yk, mkv, 0};
+        mats.m[2] = {static_cast<const uint8_t*>(v.weights), v.scales, v.biases, yv, mkv, 0};
+        mats.nmat = 3;
+        mats.total_rows = mq + 2 * mkv;
+        return launch_multi(stream, mats, x, n);
+    }
+
+private:
+    int launch_multi(void* stream, Q4Multi& mats, const uint16_t* x, uint32_t n) const {
+        if (n == 0 || n % TFQ_GROUP_SIZE != 0)
+            return fail(TFQ_E_INVAL, "n=%u must be a positive multiple of 64", n);
+        if (n > kMaxN) return fail(TFQ_E_UNSUPPORTED, "n=%u exceeds %u", n, kMaxN);
+        if (!x || !aligned(x, 2)) return fail(TFQ_E_INVAL, "x must be non-null and 2-byte aligned");
+        for (uint32_t i = 0; i < mats.nmat; ++i) {
+            const Q4Mat& q = mats.m[i];
+            if (q.rows == 0) return fail(TFQ_E_INVAL, "matrix %u has zero rows", i);
+            if (!q.w || !q.s || !q.b || !q.y)
+                return fail(TFQ_E_INVAL, "matrix %u has a null pointer", i);
+            // 128-bit weight loads (the reference needs only 2-byte alignment, DequantInt4GEMV.swift:97-102).
+            if (!aligned(q.w, 16)) return fail(TFQ_E_INVAL, "weights of matrix %u are not 16-byte aligned", i);
+            if (!aligned(q.s, 2) || !aligned(q.b, 2) || !aligned(q.y, 2))
+                return fail(TFQ_E_INVAL, "scales/biases/y of matrix %u are not 2-byte aligned", i);
+        }
+        const SegShape sh = seg_shape(n / 32, 2);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_q4_gemv_s%u_p%u", sh.seg, sh.p);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        uint32_t nn = n;
+        void* args[] = {&mats, &x, &nn};
+        return launch(m_.get(name), grid_for_rows(mats.total_rows, rows_per_block), kBlock, n * 4,
+                      stream, args, name);
+    }
+
+    const Module& m_;
+};
+
+// S/Kernels/Quant/DequantInt8GEMV.swift:16-82.
+class DequantInt8GEMV {
+public:
+    explicit DequantInt8GEMV(const Module& m) : m_(m) {}
+
+    int encode(void* stream, const uint8_t* weights, const uint16_t* scales, const uint16_t* biases,
+               const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n) const {
+        if (n == 0 || n % TFQ_GROUP_SIZE != 0)
+            return fail(TFQ_E_INVAL, "n=%u must be a positive multiple of 64", n);
+        if (n > 4096) return fail(TFQ_E_UNSUPPORTED, "int8 GEMV n=%u exceeds 4096", n);
+        if (m == 0) return fail(TFQ_E_INVAL, "m must be positive");
+        if (!weights || !scales || !biases || !x || !y)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(weights, 16)) return fail(TFQ_E_INVAL, "weights are not 16-byte aligned");
+        if (!aligned(scales, 2) || !aligned(biases, 2) || !aligned(x, 2) || !aligned(y, 2))
+            return fail(TFQ_E_INVAL, "fp16 operands must be 2-byte aligned");
+        const SegShape sh = seg_shape(n / 16, 4);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_q8_gemv_s%u_p%u", sh.seg, sh.p);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        void* args[] = {&weights, &scales, &biases, &x, &y, &m, &n};
+        return launch(m_.get(name), grid_for_rows(m, rows_per_block), kBlock, n * 4, stream, args,
+                      name);
+    }
+
+private:
+    const Module& m_;
+};
+
+// S/Kernels/MoE/MoE.swift:31-414: router + routed decode phases.
+class MoE {
+public:
+    explicit MoE(const Module& m) : m_(m) {}
+
+    // MoE.encodeRouterGemma4 (MoE.swift:147-197), GEMV and selection fused.
+    int encode_router_gemma4(void* stream, const uint8_t* weights, const uint16_t* scales,
+                             const uint16_t* biases, const uint16_t* hidden,
+                             const uint16_t* effective_scale, const uint16_t* per_expert_scale,
+                             uint32_t* out_indices, uint16_t* out_weights, float* out_weights_f32,
+                             float* out_logits, uint32_t num_experts, uint32_t d, uint32_t top_k,
+                             void* workspace) const {
+        if (d == 0 || d % TFQ_GROUP_SIZE != 0)
+            return fail(TFQ_E_INVAL, "d=%u must be a positive multiple of 64", d);
+        if (d > 4096) return fail(TFQ_E_UNSUPPORTED, "router d=%u exceeds 4096", d);
+        if (num_experts == 0 || num_experts > 256)
+            return fail(TFQ_E_INVAL, "numExperts=%u must be in 1...256", num_experts);
+        if (top_k == 0 || top_k > 64 || top_k > num_experts)
+            return fail(TFQ_E_INVAL, "topK=%u must be in 1...min(64, numExperts)", top_k);
+        if (!weights || !scales || !biases || !hidden || !out_indices || !out_weights || !workspace)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(weights, 16)) return fail(TFQ_E_INVAL, "weights are not 16-byte aligned");
+        if (!aligned(workspace, 16)) return fail(TFQ_E_INVAL, "workspace is not 16-byte aligned");
+        if (!aligned(out_indices, 4)) return fail(TFQ_E_INVAL, "indices are not 4-byte aligned");
+        const SegShape sh = seg_shape(d / 16, 4);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_router_topk_s%u_p%u", sh.seg, sh.p);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        const uint32_t grid = (num_experts + rows_per_block - 1) / rows_per_block;
+        void* args[] = {&weights, &scales, &biases, &hidden, &effective_scale, &per_expert_scale,
+                        &out_indices, &out_weights, &out_weights_f32, &out_logits, &num_experts,
+                        &d, &top_k, &workspace};
+        // LDS holds x (d floats) and, in the selecting block, the E logits.
+        const uint32_t lds = (d > 256 ? d : 256) * 4;
+        return launch(m_.get(name), grid, kBlock, lds, stream, args, name);
+    }
+
+    // encodeRoutedPersistentPhase1U16Load / ...SubsetU16Load (MoE.swift:234-310).
+    int encode_phase1(void* stream, const tfq_expert_pool& pool, const uint32_t* indices,
+                      const uint16_t* x, float* acts, const uint32_t* active_slots,
+                      uint32_t active_count, uint32_t d, uint32_t f, uint32_t top_k) const {
+        int rc = check_pool(pool, d, f, top_k);
+        if (rc) return rc;
+        if (d > kMaxN) return fail(TFQ_E_UNSUPPORTED, "d=%u exceeds %u", d, kMaxN);
+        if (!indices || !x || !acts) return fail(TFQ_E_INVAL, "null pointer argument");
+        if (active_count == 0) return TFQ_OK;               // nothing to do (MoE.swift:283)
+        if (active_slots == nullptr && active_count != top_k)
+            return fail(TFQ_E_INVAL, "full phase 1 covers exactly topK slots");
+        if (active_count > top_k) return fail(TFQ_E_INVAL, "activeCount > topK");
+        ExpertPool kp = to_kernel_pool(pool);
+        const SegShape sh = seg_shape(d / 32, 2);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_moe_phase1_s%u_p%u", sh.seg, sh.p);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        void* args[] = {&kp, &indices, &active_slots, &active_count, &top_k, &x, &acts, &d, &f};
+        return launch(m_.get(name), grid_for_rows((uint64_t)active_count * f, rows_per_block),
+                      kBlock, d * 4, stream, args, name);
+    }
+
+    // encodeRoutedPersistentPhase2Reduce (MoE.swift:312-362).
+    int encode_phase2(void* stream, const tfq_expert_pool& pool, const uint32_t* indices,
+                      const float* acts, const uint16_t* routing_weights, const uint16_t* residual,
+                      uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k) const {
+        int rc = check_pool(pool, d, f, top_k);
+        if (rc) return rc;
+        if (f > 1024) return fail(TFQ_E_UNSUPPORTED, "phase 2 f=%u exceeds 1024", f);
+        if (!indices || !acts || !routing_weights || !y)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        ExpertPool kp = to_kernel_pool(pool);
+        const uint32_t p = ((f / 32) + 7) / 8;
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_moe_phase2_p%u", p);
+        void* args[] = {&kp, &indices, &acts, &routing_weights, &residual, &y, &d, &f, &top_k};
+        return launch(m_.get(name), grid_for_rows(d, kBlock / 64), kBlock, top_k * f * 4, stream,
+                      args, name);
+    }
+
+private:
+    int check_pool(const tfq_expert_pool& pool, uint32_t d, uint32_t f, uint32_t top_k) const {
+        if (top_k == 0 || top_k > 8) return fail(TFQ_E_INVAL, "topK=%u must be in 1...8", top_k);
+        if (d == 0 || d % TFQ_GROUP_SIZE != 0 || f == 0 || f % TFQ_GROUP_SIZE != 0)
+            return fail(TFQ_E_INVAL, "d=%u and f=%u must be positive multiples of 64", d, f);
+        if (!pool.base || pool.num_experts == 0) return fail(TFQ_E_INVAL, "empty expert pool");
+        const tfq_expert_offsets& o = pool.offsets;
+        if (!aligned(pool.base, 16) || pool.stride % 16 != 0 || o.gate_w % 16 || o.up_w % 16 ||
+            o.down_w % 16)
+            return fail(TFQ_E_INVAL, "pool base, stride and weight offsets must be 16-byte aligned");
+        if ((o.gate_s | o.gate_b | o.up_s | o.up_b | o.down_s | o.down_b) & 1u)
+            return fail(TFQ_E_INVAL, "scale/bias offsets must be 2-byte aligned");
+        // every sub-tensor must lie inside one blob
+        const uint64_t wbytes = (uint64_t)f * d / 2, sbytes = (uint64_t)f * (d / 64) * 2;
+        const uint64_t ends[9] = {o.gate_w + wbytes, o.gate_s + sbytes, o.gate_b + sbytes,
+                                  o.up_w + wbytes,   o.up_s + sbytes,   o.up_b + sbytes,
+                                  o.down_w + wbytes, o.down_s + (uint64_t)d * (f / 64) * 2,
+                                  o.down_b + (uint64_t)d * (f / 64) * 2};
+        for (uint64_t e : ends)
+            if (e > pool.stride) return fail(TFQ_E_INVAL, "expert sub-tensor exceeds the pool stride");
+        return TFQ_OK;
+    }
+
+    static ExpertPool to_kernel_pool(const tfq_expert_pool& p) {
+        ExpertPool k{};
+        k.base = static_cast<const uint8_t*>(p.base);
+        k.stride = p.stride;
+        k.num_experts = p.num_experts;
+        const tfq_expert_offsets& o = p.offsets;
+        k.off = {o.gate_w, o.gate_s, o.gate_b, o.up_w, o.up_s, o.up_b, o.down_w, o.down_s, o.down_b};
+        return k;
+    }
+
+    const Module& m_;
+};
+
+// S/Kernels/MoE/SharedExpertInt4.swift:21-95.
+class SharedExpertInt4 {
+public:
+    explicit SharedExpertInt4(const Module& m) : m_(m), gemv_(m) {}
+
+    int encode(void* stream, const uint16_t* x, const tfq_q4_matrix& gate, const tfq_q4_matrix& up,
+               const tfq_q4_matrix& down, uint16_t* y, uint32_t d, uint32_t f,
+               uint16_t* act_scratch) const {
+        if (d == 0 || f == 0 || d % 64 || f % 64)
+            return fail(TFQ_E_INVAL, "dimension mismatch: d=%u f=%u must be multiples of 64", d, f);
+        if (d > kMaxN || f > kMaxN) return fail(TFQ_E_UNSUPPORTED, "d/f exceed %u", kMaxN);
+        if (!x || !y || !act_scratch || !gate.weights || !up.weights || !down.weights ||
+            !gate.scales || !gate.biases || !up.scales || !up.biases)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(gate.weights, 16) || !aligned(up.weights, 16))
+            return fail(TFQ_E_INVAL, "gate/up weights must be 16-byte aligned");
+        Q4Mat g = {static_cast<const uint8_t*>(gate.weights), gate.scales, gate.biases, nullptr, f, 0};
+        Q4Mat u = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases, nullptr, f, 0};
+        const SegShape sh = seg_shape(d / 32, 2);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_gate_up_act_s%u_p%u", sh.seg, sh.p);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        void* args[] = {&g, &u, &x, &act_scratch, &d, &f};
+        int rc = launch(m_.get(name), grid_for_rows(f, rows_per_block), kBlock, d * 4, stream, args,
+                        name);
+        if (rc) return rc;
+        return gemv_.encode(stream, down.weights, down.scales, down.biases, act_scratch, y, d, f);
+    }
+
+private:
+    const Module& m_;
+    DequantInt4GEMV gemv_;
+};
+
+}  // namespace tfq

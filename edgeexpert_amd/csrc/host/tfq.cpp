@@ -1,0 +1,307 @@
+// tfq.cpp — libtfq: the C ABI of include/tfq.h and include/tfq_runtime.h.
+//
+// Loads the gfx950 code object (hipModuleLoad), resolves every kernel once
+// (hipModuleGetFunction), and forwards each C entry point to the operator
+// class that mirrors the reference wrapper (ops.hpp). No entry point
+// allocates device memory or synchronises the caller's stream.
+#include <dlfcn.h>
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../../include/tfq_runtime.h"
+#include "ops.hpp"
+
+namespace tfq {
+
+ErrorState& error_state() {
+    static thread_local ErrorState s;
+    return s;
+}
+
+static std::vector<std::string> kernel_names() {
+    std::vector<std::string> names;
+    const char* q4_shapes[] = {"s2_p1", "s4_p1", "s8_p1", "s16_p1", "s32_p1",
+                               "s64_p1", "s64_p2", "s64_p3", "s64_p4"};
+    const char* q8_shapes[] = {"s4_p1", "s8_p1", "s16_p1", "s32_p1",
+                               "s64_p1", "s64_p2", "s64_p3", "s64_p4"};
+    for (const char* s : q4_shapes) {
+        names.push_back(std::string("tfq_q4_gemv_") + s);
+        names.push_back(std::string("tfq_moe_phase1_") + s);
+        names.push_back(std::string("tfq_gate_up_act_") + s);
+    }
+    for (const char* s : q8_shapes) {
+        names.push_back(std::string("tfq_q8_gemv_") + s);
+        names.push_back(std::string("tfq_router_topk_") + s);
+    }
+    for (int p = 1; p <= 4; ++p) names.push_back("tfq_moe_phase2_p" + std::to_string(p));
+    names.push_back("tfq_convert_bf16_f16");
+    return names;
+}
+
+int Module::load(const char* path) {
+    int rc = hip_check(hipGetDevice(&device_), "hipGetDevice");
+    if (rc) return rc;
+    rc = hip_check(hipModuleLoad(&module_, path), "hipModuleLoad");
+    if (rc) {
+        module_ = nullptr;
+        return rc;
+    }
+    for (const std::string& n : kernel_names()) {
+        hipFunction_t f = nullptr;
+        if (hipModuleGetFunction(&f, module_, n.c_str()) != hipSuccess || !f)
+            return fail(TFQ_E_NOT_LOADED, "kernel %s missing from %s", n.c_str(), path);
+        fns_[n] = f;
+    }
+    return TFQ_OK;
+}
+
+Module::~Module() {
+    if (module_) (void)hipModuleUnload(module_);
+}
+
+static std::string default_code_object() {
+    Dl_info info{};
+    if (dladdr(reinterpret_cast<void*>(&default_code_object), &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t slash = p.rfind('/');
+        return (slash == std::string::npos ? std::string(".") : p.substr(0, slash)) +
+               "/tfq_kernels.co";
+    }
+    return "tfq_kernels.co";
+}
+
+}  // namespace tfq
+
+using namespace tfq;
+
+struct tfq_ctx {
+    Module module;
+    DequantInt4GEMV* int4 = nullptr;
+    DequantInt8GEMV* int8 = nullptr;
+    MoE* moe = nullptr;
+    SharedExpertInt4* shared = nullptr;
+    ~tfq_ctx() {
+        delete int4;
+        delete int8;
+        delete moe;
+        delete shared;
+    }
+};
+
+#define TFQ_REQUIRE_CTX(ctx) \
+    if (!(ctx)) return fail(TFQ_E_INVAL, "null context")
+
+extern "C" {
+
+int tfq_create(tfq_ctx** out, const char* code_object_path) {
+    if (!out) return fail(TFQ_E_INVAL, "null output pointer");
+    *out = nullptr;
+    tfq_ctx* c = new (std::nothrow) tfq_ctx();
+    if (!c) return fail(TFQ_E_INVAL, "out of host memory");
+    const std::string path = code_object_path ? code_object_path : default_code_object();
+    int rc = c->module.load(path.c_str());
+    if (rc) {
+        delete c;
+        return rc;
+    }
+    c->int4 = new DequantInt4GEMV(c->module);
+    c->int8 = new DequantInt8GEMV(c->module);
+    c->moe = new MoE(c->module);
+    c->shared = new SharedExpertInt4(c->module);
+    *out = c;
+    return TFQ_OK;
+}
+
+void tfq_destroy(tfq_ctx* ctx) { delete ctx; }
+
+const char* tfq_status_string(int status) {
+    switch (status) {
+        case TFQ_OK: return "ok";
+        case TFQ_E_INVAL: return "invalid argument (shape, alignment or null pointer)";
+        case TFQ_E_UNSUPPORTED: return "shape not compiled into the code object";
+        case TFQ_E_HIP: return "HIP runtime error";
+        case TFQ_E_NOT_LOADED: return "kernel not loaded";
+        default: return "unknown status";
+    }
+}
+
+int tfq_last_hip_error(void) { return error_state().hip; }
+const char* tfq_last_error_message(void) { return error_state().message; }
+
+int tfq_gemv_q4g64(tfq_ctx* ctx, void* stream, const void* weights, const uint16_t* scales,
+                   const uint16_t* biases, const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->int4->encode(stream, weights, scales, biases, x, y, m, n);
+}
+
+int tfq_gemv_q4g64_qkv(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* q, const tfq_q4_matrix* k,
+                       const tfq_q4_matrix* v, const uint16_t* x, uint16_t* yq, uint16_t* yk,
+                       uint16_t* yv, uint32_t mq, uint32_t mkv, uint32_t n) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!q || !k || !v) return fail(TFQ_E_INVAL, "null matrix descriptor");
+    return ctx->int4->encode_qkv(stream, *q, *k, *v, x, yq, yk, yv, mq, mkv, n);
+}
+
+int tfq_gemv_q8g64(tfq_ctx* ctx, void* stream, const uint8_t* weights, const uint16_t* scales,
+                   const uint16_t* biases, const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->int8->encode(stream, weights, scales, biases, x, y, m, n);
+}
+
+int tfq_router_topk(tfq_ctx* ctx, void* stream, const uint8_t* weights, const uint16_t* scales,
+                    const uint16_t* biases, const uint16_t* hidden, const uint16_t* effective_scale,
+                    const uint16_t* per_expert_scale, uint32_t* out_indices, uint16_t* out_weights,
+                    float* out_weights_f32, float* out_logits_f32, uint32_t num_experts, uint32_t d,
+                    uint32_t top_k, void* workspace) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->moe->encode_router_gemma4(stream, weights, scales, biases, hidden, effective_scale,
+                                          per_expert_scale, out_indices, out_weights,
+                                          out_weights_f32, out_logits_f32, num_experts, d, top_k,
+                                          workspace);
+}
+
+int tfq_moe_phase1(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, const uint32_t* indices,
+                   const uint16_t* x, float* acts, uint32_t d, uint32_t f, uint32_t top_k) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!pool) return fail(TFQ_E_INVAL, "null pool");
+    return ctx->moe->encode_phase1(stream, *pool, indices, x, acts, nullptr, top_k, d, f, top_k);
+}
+
+int tfq_moe_phase1_subset(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool,
+                          const uint32_t* indices, const uint16_t* x, float* acts,
+                          const uint32_t* active_slots, uint32_t active_count, uint32_t d,
+                          uint32_t f, uint32_t top_k) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!pool) return fail(TFQ_E_INVAL, "null pool");
+    if (!active_slots && active_count) return fail(TFQ_E_INVAL, "null active slot list");
+    return ctx->moe->encode_phase1(stream, *pool, indices, x, acts, active_slots, active_count, d,
+                                   f, top_k);
+}
+
+int tfq_moe_phase2(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, const uint32_t* indices,
+                   const float* acts, const uint16_t* routing_weights, const uint16_t* residual,
+                   uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!pool) return fail(TFQ_E_INVAL, "null pool");
+    return ctx->moe->encode_phase2(stream, *pool, indices, acts, routing_weights, residual, y, d, f,
+                                   top_k);
+}
+
+int tfq_moe_decode(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, const uint32_t* indices,
+                   const uint16_t* routing_weights, const uint16_t* x, const uint16_t* residual,
+                   uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k, float* acts_scratch) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!pool) return fail(TFQ_E_INVAL, "null pool");
+    int rc = ctx->moe->encode_phase1(stream, *pool, indices, x, acts_scratch, nullptr, top_k, d, f,
+                                     top_k);
+    if (rc) return rc;
+    return ctx->moe->encode_phase2(stream, *pool, indices, acts_scratch, routing_weights, residual,
+                                   y, d, f, top_k);
+}
+
+int tfq_shared_expert_q4(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* gate,
+                         const tfq_q4_matrix* up, const tfq_q4_matrix* down, const uint16_t* x,
+                         uint16_t* y, uint32_t d, uint32_t f, uint16_t* act_scratch) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!gate || !up || !down) return fail(TFQ_E_INVAL, "null matrix descriptor");
+    return ctx->shared->encode(stream, x, *gate, *up, *down, y, d, f, act_scratch);
+}
+
+int tfq_convert_bf16_to_f16(tfq_ctx* ctx, void* stream, const uint16_t* src, uint16_t* dst,
+                            uint64_t count, uint32_t* inexact_count_dev) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (count == 0) return TFQ_OK;
+    if (!src || !dst) return fail(TFQ_E_INVAL, "null pointer argument");
+    if (!aligned(src, 2) || !aligned(dst, 2)) return fail(TFQ_E_INVAL, "2-byte alignment required");
+    uint64_t blocks = (count + 255) / 256;
+    uint32_t grid = blocks > 2048 ? 2048u : (uint32_t)blocks;
+    void* args[] = {&src, &dst, &count, &inexact_count_dev};
+    return launch(ctx->module.get("tfq_convert_bf16_f16"), grid, 256, 0, stream, args,
+                  "tfq_convert_bf16_f16");
+}
+
+// ------------------------------------------------------------ runtime ----
+
+int tfq_rt_device_count(int* count) { return hip_check(hipGetDeviceCount(count), "hipGetDeviceCount"); }
+int tfq_rt_set_device(int device) { return hip_check(hipSetDevice(device), "hipSetDevice"); }
+
+int tfq_rt_device_info(char* name, size_t name_len, char* arch, size_t arch_len) {
+    int dev = 0;
+    int rc = hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    hipDeviceProp_t prop;
+    rc = hip_check(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+    if (rc) return rc;
+    if (name && name_len) std::snprintf(name, name_len, "%s", prop.name);
+    if (arch && arch_len) std::snprintf(arch, arch_len, "%s", prop.gcnArchName);
+    return TFQ_OK;
+}
+
+int tfq_rt_malloc(void** ptr, size_t bytes) { return hip_check(hipMalloc(ptr, bytes), "hipMalloc"); }
+int tfq_rt_free(void* ptr) { return hip_check(hipFree(ptr), "hipFree"); }
+int tfq_rt_memcpy_htod(void* dst, const void* src, size_t bytes) {
+    return hip_check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpyHtoD");
+}
+int tfq_rt_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+    return hip_check(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpyDtoH");
+}
+int tfq_rt_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream) {
+    return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+                     "hipMemcpyDtoD");
+}
+int tfq_rt_memset(void* dst, int value, size_t bytes) {
+    return hip_check(hipMemset(dst, value, bytes), "hipMemset");
+}
+int tfq_rt_stream_create(void** stream) {
+    return hip_check(hipStreamCreateWithFlags((hipStream_t*)stream, hipStreamNonBlocking),
+                     "hipStreamCreate");
+}
+int tfq_rt_stream_destroy(void* stream) {
+    return hip_check(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+}
+int tfq_rt_stream_sync(void* stream) {
+    return hip_check(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+int tfq_rt_device_sync(void) { return hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+int tfq_rt_event_create(void** event) {
+    return hip_check(hipEventCreate((hipEvent_t*)event), "hipEventCreate");
+}
+int tfq_rt_event_destroy(void* event) {
+    return hip_check(hipEventDestroy((hipEvent_t)event), "hipEventDestroy");
+}
+int tfq_rt_event_record(void* event, void* stream) {
+    return hip_check(hipEventRecord((hipEvent_t)event, (hipStream_t)stream), "hipEventRecord");
+}
+int tfq_rt_event_sync(void* event) {
+    return hip_check(hipEventSynchronize((hipEvent_t)event), "hipEventSynchronize");
+}
+int tfq_rt_event_elapsed_ms(float* ms, void* start, void* end) {
+    return hip_check(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end),
+                     "hipEventElapsedTime");
+}
+int tfq_rt_capture_begin(void* stream) {
+    return hip_check(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal),
+                     "hipStreamBeginCapture");
+}
+int tfq_rt_capture_end(void* stream, void** graph_exec) {
+    hipGraph_t g = nullptr;
+    int rc = hip_check(hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture");
+    if (rc) return rc;
+    hipGraphExec_t ex = nullptr;
+    rc = hip_check(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    (void)hipGraphDestroy(g);
+    if (rc) return rc;
+    *graph_exec = ex;
+    return TFQ_OK;
+}
+int tfq_rt_graph_launch(void* graph_exec, void* stream) {
+    return hip_check(hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream),
+                     "hipGraphLaunch");
+}
+int tfq_rt_graph_destroy(void* graph_exec) {
+    return hip_check(hipGraphExecDestroy((hipGraphExec_t)graph_exec), "hipGraphExecDestroy");
+}
+
+}  // extern "C"

@@ -1,0 +1,75 @@
+// tfq_kernels.hip — gfx950 code object: every kernel entry point of libtfq.
+//
+// Built by edgeexpert_amd/build.py into edgeexpert_amd/lib/tfq_kernels.co and
+// loaded at run time with hipModuleLoad; entry points have C names so the
+// host resolves them with hipModuleGetFunction. Shapes are compile-time
+// template parameters: SEG = lanes per output row (power of two, <= 64) and
+// P = 16-byte chunks per lane; the host picks the instantiation from n.
+#include "abi_types.h"
+#include "moe_decode.hpp"
+
+using namespace tfq;
+
+#define TFQ_Q4_GEMV(SEG, P)                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void tfq_q4_gemv_s##SEG##_p##P(                 \
+        Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
+        q4_gemv_multi<SEG, P>(mats, x, n);                                                        \
+    }
+
+#define TFQ_Q8_GEMV(SEG, P)                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void tfq_q8_gemv_s##SEG##_p##P(                 \
+        const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* x, uint16_t* y,  \
+        uint32_t m, uint32_t n) {                                                                 \
+        q8_gemv<SEG, P>(W, S, B, x, y, m, n);                                                     \
+    }
+
+#define TFQ_ROUTER(SEG, P)                                                                       \
+    extern "C" __global__ __launch_bounds__(256) void tfq_router_topk_s##SEG##_p##P(             \
+        const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* h,               \
+        const uint16_t* eff, const uint16_t* gain, uint32_t* out_idx, uint16_t* out_w,           \
+        float* out_wf, float* out_logits, uint32_t E, uint32_t d, uint32_t k, uint8_t* ws) {     \
+        router_topk<SEG, P>(W, S, B, h, eff, gain, out_idx, out_w, out_wf, out_logits, E, d, k, \
+                            ws);                                                                  \
+    }
+
+#define TFQ_PHASE1(SEG, P)                                                                       \
+    extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase1_s##SEG##_p##P(              \
+        ExpertPool pool, const uint32_t* indices, const uint32_t* active_slots,                  \
+        uint32_t n_active, uint32_t top_k, const uint16_t* x, float* acts, uint32_t D,           \
+        uint32_t F) {                                                                             \
+        moe_phase1<SEG, P>(pool, indices, active_slots, n_active, top_k, x, acts, D, F);         \
+    }
+
+#define TFQ_PHASE2(P)                                                                            \
+    extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase2_p##P(                       \
+        ExpertPool pool, const uint32_t* indices, const float* acts, const uint16_t* rw,         \
+        const uint16_t* residual, uint16_t* y, uint32_t D, uint32_t F, uint32_t top_k) {         \
+        moe_phase2<P>(pool, indices, acts, rw, residual, y, D, F, top_k);                         \
+    }
+
+#define TFQ_GATE_UP(SEG, P)                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void tfq_gate_up_act_s##SEG##_p##P(             \
+        Q4Mat gate, Q4Mat up, const uint16_t* x, uint16_t* act, uint32_t D, uint32_t F) {        \
+        q4_gate_up_act<SEG, P>(gate.w, gate.s, gate.b, up.w, up.s, up.b, x, act, D, F);          \
+    }
+
+// int4: n/32 chunks per row.
+#define TFQ_Q4_TABLE(X) X(2, 1) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 3) X(64, 4)
+// int8: n/16 chunks per row (n <= 4096).
+#define TFQ_Q8_TABLE(X) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 3) X(64, 4)
+
+TFQ_Q4_TABLE(TFQ_Q4_GEMV)
+TFQ_Q4_TABLE(TFQ_PHASE1)
+TFQ_Q4_TABLE(TFQ_GATE_UP)
+TFQ_Q8_TABLE(TFQ_Q8_GEMV)
+TFQ_Q8_TABLE(TFQ_ROUTER)
+TFQ_PHASE2(1)
+TFQ_PHASE2(2)
+TFQ_PHASE2(3)
+TFQ_PHASE2(4)
+
+extern "C" __global__ __launch_bounds__(256) void tfq_convert_bf16_f16(const uint16_t* src,
+                                                                         uint16_t* dst, uint64_t n,
+                                                                         uint32_t* inexact) {
+    convert_bf16_to_f16(src, dst, n, inexact);
+}

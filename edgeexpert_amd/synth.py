@@ -1,0 +1,185 @@
+"""Seeded synthetic inputs for the BASELINE configurations (host side, numpy).
+
+The streams are the reference's own test PRNG: SplitMix64 seeded through
+SeedTree's FNV-1a label hash (V/PRNG/SplitMix64.swift:11-23,
+V/PRNG/SeedTree.swift:12-19 in the reference checkout). SplitMix64 is a
+counter-based generator — output i of a stream seeded with `key` is
+mix(key + (i + 1) * GAMMA) — so a whole stream is produced with one vectorised
+numpy expression instead of a Python loop.
+
+Tensor streams are named "<config>/<tensor>" under SeedTree(seed), so each
+tensor can be regenerated independently and the GPU and the CPU see the same
+bits. Distributions follow BASELINE.json:
+  int4 weights: q ~ U{0..15} (each SplitMix64 output supplies 8 packed
+                bytes, i.e. 16 codes, little-endian); scale = |N(0, 0.02)| (fp16);
+                bias = -8*scale + N(0, 0.002) (fp16), one pair per 64 along K.
+  int8 router:  q ~ U{0..255} (8 codes per output); scale = |N(0, 0.02)|/16; bias = -128*scale + N(0, 0.002).
+  activations:  N(0, 1), rounded to fp16 (or bf16 for the prefill GEMM).
+Normals use Box–Muller on two 24-bit uniforms, evaluated in float64.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+GAMMA = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+MASK64 = (1 << 64) - 1
+GROUP = 64
+
+
+def seed_key(root: int, label: str) -> int:
+    """SeedTree(root).key(label) -> initial SplitMix64 state."""
+    h = 0xCBF29CE484222325
+    for byte in label.encode():
+        h ^= byte
+        h = (h * 0x100000001B3) & MASK64
+    return (root ^ h) & MASK64
+
+
+def splitmix64(key: int, n: int, start: int = 0) -> np.ndarray:
+    """Outputs start .. start+n-1 of the SplitMix64 stream seeded with `key`."""
+    with np.errstate(over="ignore"):
+        i = np.arange(start + 1, start + n + 1, dtype=np.uint64)
+        z = np.uint64(key) + i * GAMMA
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        return z ^ (z >> np.uint64(31))
+
+
+def uniform24(key: int, n: int, lo: float = 0.0, hi: float = 1.0) -> np.ndarray:
+    """SplitMix64.uniform(lo, hi): lo + (hi - lo) * (next() >> 40) / 2^24, in float32."""
+    u = (splitmix64(key, n) >> np.uint64(40)).astype(np.float32) / np.float32(1 << 24)
+    return np.float32(lo) + (np.float32(hi) - np.float32(lo)) * u
+
+
+def normal(key: int, n: int, std: float = 1.0) -> np.ndarray:
+    """Box–Muller over output pairs (2i, 2i+1); float32 result."""
+    r = splitmix64(key, 2 * n) >> np.uint64(40)
+    u1 = (r[0::2].astype(np.float64) + 1.0) / float(1 << 24)      # (0, 1]
+    u2 = r[1::2].astype(np.float64) / float(1 << 24)              # [0, 1)
+    z = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+    return (z * std).astype(np.float32)
+
+
+def f16_bits(x) -> np.ndarray:
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def bf16_bits(x) -> np.ndarray:
+    """Round-half-even to bfloat16 (Quantization.swift:16-23 rounding)."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    lsb = (u >> np.uint64(16)) & np.uint64(1)
+    return ((u + np.uint64(0x7FFF) + lsb) >> np.uint64(16)).astype(np.uint16)
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def f16_to_f32(bits) -> np.ndarray:
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def pack_int4(q: np.ndarray) -> np.ndarray:
+    """Codes [..., K] (0..15) -> bytes [..., K/2]; low nibble = even element.
+    Equivalently 8 nibbles per little-endian uint32 word along K."""
+    q = np.asarray(q, np.uint8)
+    return (q[..., 0::2] | (q[..., 1::2] << 4)).astype(np.uint8)
+
+
+def unpack_int4(packed: np.ndarray) -> np.ndarray:
+    p = np.asarray(packed, np.uint8)
+    out = np.empty(p.shape[:-1] + (p.shape[-1] * 2,), np.uint8)
+    out[..., 0::2] = p & 0x0F
+    out[..., 1::2] = p >> 4
+    return out
+
+
+def int4_matrix(seed: int, label: str, rows: int, k: int):
+    """Affine int4 g64 matrix [rows][k] with the BASELINE distributions.
+    Returns (packed u8 [rows][k/2], scales fp16 bits [rows][k/64], biases fp16 bits)."""
+    assert k % GROUP == 0
+    # Each 64-bit output is 8 packed bytes = 16 uniform codes, in memory order.
+    packed = splitmix64(seed_key(seed, label + "/q"), rows * k // 16).view(np.uint8)
+    packed = packed.reshape(rows, k // 2)
+    g = rows * (k // GROUP)
+    s = np.abs(normal(seed_key(seed, label + "/s"), g, 0.02))
+    s16 = f16_bits(s)
+    b = np.float32(-8.0) * f16_to_f32(s16) + normal(seed_key(seed, label + "/b"), g, 0.002)
+    return packed, s16.reshape(rows, -1), f16_bits(b).reshape(rows, -1)
+
+
+def int8_matrix(seed: int, label: str, rows: int, k: int):
+    """Affine int8 g64 router matrix: q ~ U{0..255}, scale = |N(0,0.02)|/16,
+    bias = -128*scale + N(0, 0.002) (fp16)."""
+    assert k % GROUP == 0
+    # Each 64-bit output is 8 uniform byte codes, in memory order.
+    q = splitmix64(seed_key(seed, label + "/q"), rows * k // 8).view(np.uint8)
+    g = rows * (k // GROUP)
+    s = np.abs(normal(seed_key(seed, label + "/s"), g, 0.02)) / np.float32(16.0)
+    s16 = f16_bits(s)
+    b = np.float32(-128.0) * f16_to_f32(s16) + normal(seed_key(seed, label + "/b"), g, 0.002)
+    return q.reshape(rows, k), s16.reshape(rows, -1), f16_bits(b).reshape(rows, -1)
+
+
+def f16_vector(seed: int, label: str, n: int, std: float = 1.0) -> np.ndarray:
+    return f16_bits(normal(seed_key(seed, label), n, std))
+
+
+def bf16_vector(seed: int, label: str, n: int, std: float = 1.0) -> np.ndarray:
+    return bf16_bits(normal(seed_key(seed, label), n, std))
+
+
+# ------------------------------------------------------------------ experts ----
+
+def expert_layout(d: int, f: int, align: int = 16384):
+    """Blob layout of one routed expert: [gateW, gateS, gateB, upW, upS, upB,
+    downW, downS, downB], each sub-tensor contiguous, blob padded to `align`
+    (the repacker's 16 KiB expert stride). Returns (offsets dict, stride)."""
+    gw = f * d // 2
+    gs = f * (d // GROUP) * 2
+    dw = d * f // 2
+    ds = d * (f // GROUP) * 2
+    o = {}
+    cur = 0
+    for name, size in (("gate_w", gw), ("gate_s", gs), ("gate_b", gs), ("up_w", gw), ("up_s", gs),
+                       ("up_b", gs), ("down_w", dw), ("down_s", ds), ("down_b", ds)):
+        o[name] = cur
+        cur += size
+    stride = (cur + align - 1) // align * align
+    return o, stride
+
+
+OFFSET_ORDER = ("gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b")
+
+
+def expert_blob(seed: int, label: str, d: int, f: int, offsets: dict, stride: int) -> np.ndarray:
+    """One expert blob of `stride` bytes with BASELINE-distributed gate/up/down."""
+    blob = np.zeros(stride, np.uint8)
+    for proj, rows, cols in (("gate", f, d), ("up", f, d), ("down", d, f)):
+        w, s, b = int4_matrix(seed, f"{label}/{proj}", rows, cols)
+        for part, arr in (("w", w), ("s", s), ("b", b)):
+            raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
+            off = offsets[f"{proj}_{part}"]
+            blob[off:off + raw.size] = raw
+    return blob
+
+
+def expert_pool(seed: int, label: str, num_experts: int, d: int, f: int, align: int = 16384):
+    """All experts of one layer, concatenated at a fixed stride."""
+    offsets, stride = expert_layout(d, f, align)
+    pool = np.zeros(num_experts * stride, np.uint8)
+    for e in range(num_experts):
+        pool[e * stride:(e + 1) * stride] = expert_blob(seed, f"{label}/e{e}", d, f, offsets, stride)
+    return pool, offsets, stride
+
+
+def blob_views(blob: np.ndarray, offsets: dict, d: int, f: int, proj: str):
+    """(W u8 [rows][cols/2], S u16 [rows][cols/64], B u16) views into one expert blob."""
+    rows, cols = (f, d) if proj in ("gate", "up") else (d, f)
+    w = blob[offsets[f"{proj}_w"]:offsets[f"{proj}_w"] + rows * cols // 2].reshape(rows, cols // 2)
+    ng = rows * (cols // GROUP)
+    s = blob[offsets[f"{proj}_s"]:offsets[f"{proj}_s"] + 2 * ng].view(np.uint16).reshape(rows, -1)
+    b = blob[offsets[f"{proj}_b"]:offsets[f"{proj}_b"] + 2 * ng].view(np.uint16).reshape(rows, -1)
+    return w, s, b

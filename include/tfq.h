@@ -1,0 +1,193 @@
+/*
+ * tfq.h — C ABI of the MI355X (gfx950) quantized-matmul library.
+ *
+ * Drop-in replacement for the Metal quantized-matmul entry points of the
+ * TurboFieldfare / edgeexpert runtime. Each entry point below names the
+ * reference wrapper it replaces (paths relative to the reference checkout,
+ * S/ = Sources/TurboFieldfare/).
+ *
+ * Conventions (shared by every entry point)
+ *  - Weight format: MLX affine, group 64 along the reduction axis. int4 rows
+ *    pack 2 codes per byte (low nibble = even element), i.e. 8 codes per
+ *    little-endian uint32 word along K; int8 rows hold one code per byte.
+ *    Scale and bias are IEEE fp16, one pair per group: w = q*scale + bias.
+ *    (The reference stores BF16; BF16 -> fp16 is exact for |v| in
+ *    [2^-14, 65504], see tfq_convert_bf16_to_f16.)
+ *  - Axis names follow the reference wrappers: for a GEMV `m` is the number
+ *    of output rows and `n` the reduction length (DequantInt4GEMV.swift:95-96);
+ *    for a GEMM `t`/`m` counts tokens, `n` outputs, `k` the reduction.
+ *  - All pointers are device pointers (hipMalloc'd), all work is enqueued
+ *    asynchronously on `stream` (a hipStream_t; NULL = the null stream).
+ *    The caller owns every buffer; nothing is allocated per call.
+ *  - Every call returns a status. Shape, alignment and null-pointer contract
+ *    violations return TFQ_E_INVAL (the reference traps with `precondition`);
+ *    shapes no kernel is compiled for return TFQ_E_UNSUPPORTED; a failing
+ *    HIP call returns TFQ_E_HIP and its code is kept for tfq_last_hip_error().
+ *    Nothing aborts the process.
+ *  - A context is immutable after tfq_create and may be shared by threads
+ *    that use distinct streams. Calls that take a `workspace` must not run
+ *    concurrently with another call using the same workspace.
+ */
+#ifndef TFQ_H
+#define TFQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TFQ_OK 0
+#define TFQ_E_INVAL 1
+#define TFQ_E_UNSUPPORTED 2
+#define TFQ_E_HIP 3
+#define TFQ_E_NOT_LOADED 4
+
+#define TFQ_GROUP_SIZE 64
+
+typedef struct tfq_ctx tfq_ctx;
+
+/* Loads the gfx950 code object and resolves every kernel (hipModuleLoad +
+ * hipModuleGetFunction). code_object_path == NULL loads tfq_kernels.co from
+ * the directory holding libtfq.so. Replaces MetalContext pipeline creation
+ * (S/Infrastructure/Metal/MetalContext.swift:104-201). */
+int tfq_create(tfq_ctx **out, const char *code_object_path);
+void tfq_destroy(tfq_ctx *ctx);
+const char *tfq_status_string(int status);
+/* hipError_t of the last failing HIP call on this thread (0 if none). */
+int tfq_last_hip_error(void);
+/* Human-readable reason of the last non-OK status on this thread. */
+const char *tfq_last_error_message(void);
+
+/* ---------------------------------------------------------------- decode -- */
+
+/* y[m] = W[m][n] · x[n]; int4 g64 weights, fp16 x/y, fp32 accumulate.
+ * Replaces DequantInt4GEMV.encode and .encodeTgx
+ * (S/Kernels/Quant/DequantInt4GEMV.swift:84-180).
+ * Contract: n % 64 == 0, n <= 8192, m >= 1, weights 16-byte aligned,
+ * scales/biases/x/y 2-byte aligned. */
+int tfq_gemv_q4g64(tfq_ctx *ctx, void *stream, const void *weights, const uint16_t *scales,
+                   const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m,
+                   uint32_t n);
+
+/* One int4 matrix (weights, scales, biases). */
+typedef struct {
+    const void *weights;
+    const uint16_t *scales;
+    const uint16_t *biases;
+} tfq_q4_matrix;
+
+/* q, k and v projections of one token in one launch over the concatenated
+ * rows mq + 2*mkv. Replaces FusedQKVGEMV.encode
+ * (S/Kernels/Fusions/FusedQKVGEMV.swift:92-156). Same contract as
+ * tfq_gemv_q4g64 for each matrix. */
+int tfq_gemv_q4g64_qkv(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *q,
+                       const tfq_q4_matrix *k, const tfq_q4_matrix *v, const uint16_t *x,
+                       uint16_t *yq, uint16_t *yk, uint16_t *yv, uint32_t mq, uint32_t mkv,
+                       uint32_t n);
+
+/* y[m] = W8[m][n] · x[n]; int8 g64 weights. Replaces DequantInt8GEMV.encode
+ * (S/Kernels/Quant/DequantInt8GEMV.swift:50-81).
+ * Contract: n % 64 == 0, n <= 4096, weights 16-byte aligned. */
+int tfq_gemv_q8g64(tfq_ctx *ctx, void *stream, const uint8_t *weights, const uint16_t *scales,
+                   const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m,
+                   uint32_t n);
+
+/* Bytes of workspace tfq_router_topk needs. The workspace must be zeroed once
+ * (hipMemset) before its first use; each call leaves it ready for the next. */
+#define TFQ_ROUTER_WORKSPACE_BYTES 4096u
+
+/* Router GEMV + top-k + softmax over the k + per-expert gain, in one launch.
+ * logits[e] = Σ_g s·Σ q·(h⊙eff) + b·Σ(h⊙eff) (fp32); indices sorted by
+ * logit descending, ties to the lower expert index; weights[i] =
+ * fp16(softmax_i × per_expert_scale[idx_i]). effective_scale /
+ * per_expert_scale may be NULL (= all ones). Replaces MoE.encodeRouterGemma4
+ * (S/Kernels/MoE/MoE.swift:147-197).
+ * Contract: d % 64 == 0, d <= 4096, 1 <= num_experts <= 256,
+ * 1 <= top_k <= 64 (the reference decode path requires top_k == 8),
+ * weights 16-byte aligned. out_logits_f32 (may be NULL) receives the fp32
+ * logits; out_weights_f32 (may be NULL) the unrounded weights. */
+int tfq_router_topk(tfq_ctx *ctx, void *stream, const uint8_t *weights, const uint16_t *scales,
+                    const uint16_t *biases, const uint16_t *hidden,
+                    const uint16_t *effective_scale, const uint16_t *per_expert_scale,
+                    uint32_t *out_indices, uint16_t *out_weights, float *out_weights_f32,
+                    float *out_logits_f32, uint32_t num_experts, uint32_t d, uint32_t top_k,
+                    void *workspace);
+
+/* Sub-tensor byte offsets inside one routed-expert blob
+ * (MoEExpertOffsets, S/Kernels/MoE/MoE.swift:4-29). */
+typedef struct {
+    uint32_t gate_w, gate_s, gate_b;
+    uint32_t up_w, up_s, up_b;
+    uint32_t down_w, down_s, down_b;
+} tfq_expert_offsets;
+
+/* All routed experts of one layer, resident in HBM: expert e's blob starts
+ * at base + e*stride. Replaces the argument buffer of per-slot blob
+ * pointers (S/Kernels/MoE/MoE.swift:398-409): the address is computed on the
+ * device from the router's index buffer, so no host round trip is needed.
+ * Contract: base, stride and the *_w offsets 16-byte aligned; *_s/*_b
+ * offsets 2-byte aligned. */
+typedef struct {
+    const void *base;
+    uint64_t stride;
+    uint32_t num_experts;
+    tfq_expert_offsets offsets;
+} tfq_expert_pool;
+
+/* Phase 1: acts[slot][f] = gelu_tanh(gate_e[f]·x) * (up_e[f]·x), e =
+ * indices[slot], fp32 accumulate; acts is fp32 [top_k][f].
+ * Replaces MoE.encodeRoutedPersistentPhase1U16Load (MoE.swift:234-266).
+ * Contract: d % 64 == 0, d <= 8192, f % 64 == 0, 1 <= top_k <= 8. */
+int tfq_moe_phase1(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
+                   const uint32_t *indices, const uint16_t *x, float *acts, uint32_t d,
+                   uint32_t f, uint32_t top_k);
+
+/* Phase 1 over a subset of slots (active_slots: device uint32 [active_count]).
+ * Replaces MoE.encodeRoutedPersistentPhase1SubsetU16Load (MoE.swift:268-310). */
+int tfq_moe_phase1_subset(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
+                          const uint32_t *indices, const uint16_t *x, float *acts,
+                          const uint32_t *active_slots, uint32_t active_count, uint32_t d,
+                          uint32_t f, uint32_t top_k);
+
+/* Phase 2: y[d] = fp16(residual[d] + Σ_{slot=0..top_k-1} w[slot]·(down_e[d]·acts[slot])),
+ * slots summed in fixed order. routing_weights fp16 [top_k]; residual may be
+ * NULL (zeros). Replaces MoE.encodeRoutedPersistentPhase2Reduce
+ * (MoE.swift:312-362). Contract: f % 64 == 0, f <= 1024, top_k == 8 or
+ * top_k <= 8. */
+int tfq_moe_phase2(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
+                   const uint32_t *indices, const float *acts, const uint16_t *routing_weights,
+                   const uint16_t *residual, uint16_t *y, uint32_t d, uint32_t f,
+                   uint32_t top_k);
+
+/* Phase 1 then phase 2 (acts_scratch: fp32 [top_k][f] device buffer). */
+int tfq_moe_decode(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
+                   const uint32_t *indices, const uint16_t *routing_weights, const uint16_t *x,
+                   const uint16_t *residual, uint16_t *y, uint32_t d, uint32_t f,
+                   uint32_t top_k, float *acts_scratch);
+
+/* Shared expert, int4 form: act[i] = fp16(gelu_tanh(gate[i]·x) * (up[i]·x))
+ * with gate/up kept in fp32 (one fused launch), then y = fp16(down·act).
+ * gate/up are [f][d], down is [d][f]; act_scratch: fp16 [f].
+ * Replaces SharedExpertInt4.encode (S/Kernels/MoE/SharedExpertInt4.swift:30-94),
+ * which rounds gate and up to fp16 before the activation.
+ * Contract: d, f multiples of 64 and <= 8192. */
+int tfq_shared_expert_q4(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *gate,
+                         const tfq_q4_matrix *up, const tfq_q4_matrix *down, const uint16_t *x,
+                         uint16_t *y, uint32_t d, uint32_t f, uint16_t *act_scratch);
+
+/* ----------------------------------------------------------------- loader -- */
+
+/* fp16 <- BF16, elementwise on the device. Values outside the exactly
+ * representable fp16 range are still converted (round to nearest even /
+ * saturate to inf) and counted: *inexact_count_dev (device uint32, may be
+ * NULL) is incremented once per inexact element. Converts the reference's
+ * BF16 scales/biases (S/Infrastructure/ModelIO/Quantization.swift:32-45). */
+int tfq_convert_bf16_to_f16(tfq_ctx *ctx, void *stream, const uint16_t *src, uint16_t *dst,
+                            uint64_t count, uint32_t *inexact_count_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TFQ_H */

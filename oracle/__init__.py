@@ -1,0 +1,439 @@
+"""ctypes front end of the CPU oracle (tfq_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: this is the checker. Only tests/, the smoke() of
+__graft_entry__ and the cpu_baseline leg of bench.py may import it; the
+product (edgeexpert_amd, libtfq) never does.
+
+Each wrapper names the reference function it restates (paths relative to the
+reference checkout; S/ = Sources/TurboFieldfare/, V/ =
+Sources/TurboFieldfareValidation/Support/, T/ = Tests/TurboFieldfare/Core/).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libtfq_oracle.so")
+
+FMT_F16 = 0
+FMT_BF16 = 1
+GROUP = 64
+
+# PrefillMoEGroupingError cases (S/Kernels/Prefill/MoE/PrefillMoEGrouping.swift:52-88)
+GROUP_ERRORS = {
+    1: "invalidQueryCount",
+    2: "invalidTopK",
+    3: "invalidNumExperts",
+    4: "invalidTileExpertCount",
+    5: "pairCountMismatch",
+    6: "tokenOutOfRange",
+    7: "rankOutOfRange",
+    8: "expertOutOfRange",
+    9: "duplicateTokenRank",
+    10: "expertSortKeyCountMismatch",
+}
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = C.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class ExpertOffsets(C.Structure):
+    """MoEExpertOffsets (S/Kernels/MoE/MoE.swift:4-29)."""
+    _fields_ = [(n, C.c_uint32) for n in (
+        "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b")]
+
+
+PAIR_DTYPE = np.dtype([("token", "<u4"), ("expert", "<u4"), ("rank", "<u4"), ("weight_bits", "<u4")])
+GROUP_DTYPE = np.dtype([("expert", "<u4"), ("pair_start", "<u4"), ("pair_count", "<u4")])
+TILE_DTYPE = np.dtype([("group_start", "<u4"), ("group_count", "<u4"),
+                       ("pair_start", "<u4"), ("pair_count", "<u4")])
+
+_P = C.c_void_p
+
+
+def _declare(L):
+    def d(name, res, *args):
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = list(args)
+    u64p = C.POINTER(C.c_uint64)
+    d("tfo_splitmix64_next", C.c_uint64, u64p)
+    d("tfo_splitmix64_uniform", C.c_float, u64p, C.c_float, C.c_float)
+    d("tfo_seedtree_key", C.c_uint64, C.c_uint64, C.c_char_p)
+    d("tfo_f32_to_bf16", C.c_uint16, C.c_float)
+    d("tfo_bf16_to_f32", C.c_float, C.c_uint16)
+    d("tfo_f32_to_f16", C.c_uint16, C.c_float)
+    d("tfo_f16_to_f32", C.c_float, C.c_uint16)
+    d("tfo_quantize_int4_row", None, _P, C.c_int, _P, _P, _P)
+    d("tfo_quantize_int8_row", None, _P, C.c_int, _P, _P, _P)
+    d("tfo_dequantize_int4_row", None, _P, _P, _P, C.c_int, C.c_int, _P)
+    d("tfo_dequantize_int8_row", None, _P, _P, _P, C.c_int, C.c_int, _P)
+    d("tfo_int4_code", C.c_uint32, _P, C.c_size_t)
+    for n in ("tfo_gemv_int4", "tfo_gemv_int8", "tfo_gemv_int4_f64", "tfo_gemv_int8_f64"):
+        d(n, None, _P, _P, _P, C.c_int, _P, C.c_int, C.c_int, _P)
+    d("tfo_gemv_int4_mt", None, _P, _P, _P, C.c_int, _P, C.c_int, C.c_int, _P, C.c_int)
+    d("tfo_router_logits", None, _P, _P, _P, C.c_int, _P, _P, C.c_int, C.c_int, _P)
+    d("tfo_topk_softmax", C.c_int, _P, C.c_int, C.c_int, _P, _P, _P)
+    d("tfo_gelu_tanh", C.c_float, C.c_float)
+    d("tfo_ffn_int4", None, _P, C.POINTER(ExpertOffsets), C.c_int, _P, C.c_int, C.c_int, _P)
+    d("tfo_moe_routed", None, _P, C.c_uint64, C.POINTER(ExpertOffsets), C.c_int, _P, _P, _P, _P,
+      C.c_int, C.c_int, C.c_int, _P)
+    d("tfo_shared_expert_int4", None, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int,
+      C.c_int, _P)
+    d("tfo_group_pairs", C.c_int, _P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
+      _P, C.c_int64, _P, _P, _P, _P, C.POINTER(C.c_int64), _P, C.POINTER(C.c_int64),
+      C.POINTER(C.c_int64))
+    d("tfo_prefill_router", C.c_int, _P, _P, _P, C.c_int, _P, C.c_int, _P, _P, C.c_int, C.c_int,
+      C.c_int, C.c_int, _P, _P)
+    d("tfo_grouped_route_partials", None, _P, C.c_int64, _P, C.c_int, _P, C.c_uint64,
+      C.POINTER(ExpertOffsets), C.c_int, C.c_int, C.c_int, C.c_int, _P)
+    d("tfo_reduce_token_major", None, _P, _P, C.c_int, C.c_int, C.c_int, _P)
+    d("tfo_gemm_int4", None, _P, _P, _P, C.c_int, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int,
+      C.c_int)
+    d("tfo_rel_error", C.c_float, _P, _P, C.c_size_t)
+    d("tfo_max_abs_diff", C.c_float, _P, _P, C.c_size_t)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---------------------------------------------------------------- PRNG ----
+
+class SplitMix64:
+    """V/PRNG/SplitMix64.swift:4-25."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF)
+
+    def next(self) -> int:
+        return lib().tfo_splitmix64_next(C.byref(self.state))
+
+    def uniform(self, lo: float, hi: float) -> float:
+        return lib().tfo_splitmix64_uniform(C.byref(self.state), lo, hi)
+
+    def uniforms(self, n: int, lo: float, hi: float) -> np.ndarray:
+        f = lib().tfo_splitmix64_uniform
+        return np.array([f(C.byref(self.state), lo, hi) for _ in range(n)], dtype=np.float32)
+
+
+def seed_tree_key(root: int, label: str) -> SplitMix64:
+    """V/PRNG/SeedTree.swift:12-19."""
+    return SplitMix64(lib().tfo_seedtree_key(root & 0xFFFFFFFFFFFFFFFF, label.encode()))
+
+
+# --------------------------------------------------------- conversions ----
+
+def f32_to_bf16(x: float) -> int:
+    return lib().tfo_f32_to_bf16(x)
+
+
+def bf16_to_f32(b: int) -> float:
+    return lib().tfo_bf16_to_f32(b)
+
+
+def f32_to_f16(x: float) -> int:
+    return lib().tfo_f32_to_f16(x)
+
+
+def f16_to_f32(h: int) -> float:
+    return lib().tfo_f16_to_f32(h)
+
+
+# ------------------------------------------------------------- format ----
+
+def quantize_int4_row(row):
+    """Quantization.quantizeInt4Affine (Quantization.swift:50-102) -> (packed u8[n/2], s bf16, b bf16)."""
+    row = _c(row, np.float32)
+    n = row.size
+    packed = np.zeros(n // 2, np.uint8)
+    s = np.zeros(n // GROUP, np.uint16)
+    b = np.zeros(n // GROUP, np.uint16)
+    lib().tfo_quantize_int4_row(_ptr(row), n, _ptr(packed), _ptr(s), _ptr(b))
+    return packed, s, b
+
+
+def quantize_int8_row(row):
+    """Quantization.quantizeInt8Affine (Quantization.swift:135-177)."""
+    row = _c(row, np.float32)
+    n = row.size
+    packed = np.zeros(n, np.uint8)
+    s = np.zeros(n // GROUP, np.uint16)
+    b = np.zeros(n // GROUP, np.uint16)
+    lib().tfo_quantize_int8_row(_ptr(row), n, _ptr(packed), _ptr(s), _ptr(b))
+    return packed, s, b
+
+
+def quantize_int4_matrix(rows):
+    rows = _c(rows, np.float32)
+    out = [quantize_int4_row(r) for r in rows]
+    return (np.stack([o[0] for o in out]), np.stack([o[1] for o in out]),
+            np.stack([o[2] for o in out]))
+
+
+def quantize_int8_matrix(rows):
+    rows = _c(rows, np.float32)
+    out = [quantize_int8_row(r) for r in rows]
+    return (np.stack([o[0] for o in out]), np.stack([o[1] for o in out]),
+            np.stack([o[2] for o in out]))
+
+
+def dequantize_int4_row(packed, s, b, fmt, n):
+    out = np.zeros(n, np.float32)
+    lib().tfo_dequantize_int4_row(_ptr(_c(packed, np.uint8)), _ptr(_c(s, np.uint16)),
+                                  _ptr(_c(b, np.uint16)), fmt, n, _ptr(out))
+    return out
+
+
+def dequantize_int8_row(packed, s, b, fmt, n):
+    out = np.zeros(n, np.float32)
+    lib().tfo_dequantize_int8_row(_ptr(_c(packed, np.uint8)), _ptr(_c(s, np.uint16)),
+                                  _ptr(_c(b, np.uint16)), fmt, n, _ptr(out))
+    return out
+
+
+def int4_code(packed_row, j: int) -> int:
+    return lib().tfo_int4_code(_ptr(_c(packed_row, np.uint8)), j)
+
+
+# --------------------------------------------------------------- GEMV ----
+
+def _gemv(name, W, S, B, fmt, x, m, n, out_dtype):
+    W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16); x = _c(x, np.float32)
+    y = np.zeros(m, out_dtype)
+    getattr(lib(), name)(_ptr(W), _ptr(S), _ptr(B), fmt, _ptr(x), m, n, _ptr(y))
+    return y
+
+
+def gemv_int4(W, S, B, x, fmt=FMT_F16):
+    """DequantInt4GemvRef.apply (V/Reference/Quant/DequantInt4Gemv.swift:12-42). W: [m][n/2] u8."""
+    m, n = W.shape[0], np.asarray(x).size
+    return _gemv("tfo_gemv_int4", W, S, B, fmt, x, m, n, np.float32)
+
+
+def gemv_int4_f64(W, S, B, x, fmt=FMT_F16):
+    m, n = W.shape[0], np.asarray(x).size
+    return _gemv("tfo_gemv_int4_f64", W, S, B, fmt, x, m, n, np.float64)
+
+
+def gemv_int4_mt(W, S, B, x, fmt=FMT_F16, threads=1):
+    W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16); x = _c(x, np.float32)
+    m, n = W.shape[0], x.size
+    y = np.zeros(m, np.float32)
+    lib().tfo_gemv_int4_mt(_ptr(W), _ptr(S), _ptr(B), fmt, _ptr(x), m, n, _ptr(y), threads)
+    return y
+
+
+def gemv_int8(W, S, B, x, fmt=FMT_F16):
+    """DequantInt8GemvRef.apply (V/Reference/Quant/DequantInt8Gemv.swift:12-40)."""
+    m, n = W.shape[0], np.asarray(x).size
+    return _gemv("tfo_gemv_int8", W, S, B, fmt, x, m, n, np.float32)
+
+
+def gemv_int8_f64(W, S, B, x, fmt=FMT_F16):
+    m, n = W.shape[0], np.asarray(x).size
+    return _gemv("tfo_gemv_int8_f64", W, S, B, fmt, x, m, n, np.float64)
+
+
+# ------------------------------------------------------------- router ----
+
+def router_logits(W, S, B, h, eff=None, fmt=FMT_F16):
+    """RouterTopKTests.reference, logits part (T/Kernels/MoE/RouterTopKTests.swift:76-80)."""
+    W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16); h = _c(h, np.float32)
+    E, D = W.shape
+    e = None if eff is None else _c(eff, np.float32)
+    out = np.zeros(E, np.float32)
+    lib().tfo_router_logits(_ptr(W), _ptr(S), _ptr(B), fmt, _ptr(h), _ptr(e), E, D, _ptr(out))
+    return out
+
+
+def topk_softmax(logits, k, expert_scale=None):
+    """RouterTopKTests.reference, selection part (RouterTopKTests.swift:81-96)."""
+    logits = _c(logits, np.float32)
+    es = None if expert_scale is None else _c(expert_scale, np.float32)
+    idx = np.zeros(k, np.uint32)
+    w = np.zeros(k, np.float32)
+    rc = lib().tfo_topk_softmax(_ptr(logits), logits.size, k, _ptr(es), _ptr(idx), _ptr(w))
+    if rc != 0:
+        raise ValueError("k out of range")
+    return idx, w
+
+
+def prefill_router(W, S, B, hidden, k, eff=None, expert_scale=None, fmt=FMT_F16):
+    W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16)
+    hidden = _c(hidden, np.float32)
+    T, stride = hidden.shape
+    E, D = W.shape
+    e = None if eff is None else _c(eff, np.float32)
+    es = None if expert_scale is None else _c(expert_scale, np.float32)
+    idx = np.zeros((T, k), np.uint32)
+    w = np.zeros((T, k), np.float32)
+    rc = lib().tfo_prefill_router(_ptr(W), _ptr(S), _ptr(B), fmt, _ptr(hidden), stride, _ptr(e),
+                                  _ptr(es), T, E, D, k, _ptr(idx), _ptr(w))
+    if rc != 0:
+        raise ValueError("k out of range")
+    return idx, w
+
+
+# ---------------------------------------------------------------- MoE ----
+
+def gelu_tanh(x: float) -> float:
+    return lib().tfo_gelu_tanh(x)
+
+
+def _offsets(off) -> ExpertOffsets:
+    if isinstance(off, ExpertOffsets):
+        return off
+    if isinstance(off, dict):
+        return ExpertOffsets(**off)
+    return ExpertOffsets(*[int(v) for v in off])
+
+
+def ffn_int4(blob, off, x, d, f, fmt=FMT_F16):
+    blob = _c(blob, np.uint8); x = _c(x, np.float32)
+    out = np.zeros(d, np.float32)
+    o = _offsets(off)
+    lib().tfo_ffn_int4(_ptr(blob), C.byref(o), fmt, _ptr(x), d, f, _ptr(out))
+    return out
+
+
+def moe_routed(pool, stride, off, x, idx, w, d, f, residual=None, fmt=FMT_F16):
+    """MoeRef.applyStreamedRouted (V/Reference/MoE/Moe.swift:58-88)."""
+    pool = _c(pool, np.uint8); x = _c(x, np.float32)
+    idx = _c(idx, np.uint32); w = _c(w, np.float32)
+    r = None if residual is None else _c(residual, np.float32)
+    y = np.zeros(d, np.float32)
+    o = _offsets(off)
+    lib().tfo_moe_routed(_ptr(pool), int(stride), C.byref(o), fmt, _ptr(x), _ptr(r), _ptr(idx),
+                         _ptr(w), idx.size, d, f, _ptr(y))
+    return y
+
+
+def shared_expert_int4(gate, up, down, x, d, f, fmt=FMT_F16):
+    """SharedExpertInt4Tests reference (T/Kernels/MoE/SharedExpertInt4Tests.swift:21-28).
+    gate/up/down: (W, S, B) tuples."""
+    args = []
+    for (W, S, B) in (gate, up, down):
+        args += [_c(W, np.uint8), _c(S, np.uint16), _c(B, np.uint16)]
+    x = _c(x, np.float32)
+    y = np.zeros(d, np.float32)
+    lib().tfo_shared_expert_int4(*[_ptr(a) for a in args], fmt, _ptr(x), d, f, _ptr(y))
+    return y
+
+
+# ------------------------------------------------------------ prefill ----
+
+class GroupingError(Exception):
+    def __init__(self, code, a, b):
+        self.code = code
+        self.name = GROUP_ERRORS.get(code, str(code))
+        self.values = (a, b)
+        super().__init__(f"{self.name}{self.values}")
+
+
+def group_pairs(pairs, query_count, top_k, num_experts, tile_expert_count=16, sort_keys=None):
+    """PrefillMoEGrouping.groupTokenExpertPairs (PrefillMoEGrouping.swift:91-192).
+    pairs: structured array of PAIR_DTYPE. Returns dict of sorted/offsets/counts/groups/tiles."""
+    pairs = np.ascontiguousarray(pairs, dtype=PAIR_DTYPE)
+    n = pairs.size
+    sorted_ = np.zeros(max(n, 1), PAIR_DTYPE)
+    ne = max(int(num_experts), 1)
+    offsets = np.zeros(ne, np.uint32)
+    counts = np.zeros(ne, np.uint32)
+    groups = np.zeros(ne, GROUP_DTYPE)
+    tiles = np.zeros(ne, TILE_DTYPE)
+    ng = C.c_int64(0)
+    nt = C.c_int64(0)
+    err = (C.c_int64 * 2)()
+    sk = None if sort_keys is None else _c(sort_keys, np.uint64)
+    rc = lib().tfo_group_pairs(_ptr(pairs), n, query_count, top_k, num_experts, tile_expert_count,
+                               _ptr(sk), 0 if sk is None else sk.size, _ptr(sorted_),
+                               _ptr(offsets), _ptr(counts), _ptr(groups), C.byref(ng),
+                               _ptr(tiles), C.byref(nt), err)
+    if rc != 0:
+        raise GroupingError(rc, err[0], err[1])
+    return {
+        "sorted": sorted_[:n], "offsets": offsets[:num_experts], "counts": counts[:num_experts],
+        "groups": groups[:ng.value], "tiles": tiles[:nt.value], "query_count": query_count,
+    }
+
+
+def grouped_route_partials(sorted_pairs, hidden_f16, hidden_stride, pool, stride, off, top_k, d, f,
+                           query_count, fmt=FMT_F16):
+    """cpuSyntheticRoutePartials (T/Kernels/Prefill/PrefillGroupedRoutedMoETests.swift:229-279).
+    Unwritten (token, rank) slots keep the sentinel -99 as in the reference."""
+    sp = np.ascontiguousarray(sorted_pairs, dtype=PAIR_DTYPE)
+    hidden_f16 = _c(hidden_f16, np.uint16)
+    pool = _c(pool, np.uint8)
+    out = np.full(query_count * top_k * d, np.float16(-99).view(np.uint16), np.uint16)
+    o = _offsets(off)
+    lib().tfo_grouped_route_partials(_ptr(sp), sp.size, _ptr(hidden_f16), hidden_stride,
+                                     _ptr(pool), int(stride), C.byref(o), fmt, top_k, d, f,
+                                     _ptr(out))
+    return out
+
+
+def reduce_token_major(partials_f16, weights_f16, rows, top_k, d):
+    """cpuReduce (T/Kernels/Prefill/PrefillMoETests.swift:46-58). fp16 bits in and out."""
+    p = _c(partials_f16, np.uint16); w = _c(weights_f16, np.uint16)
+    out = np.zeros(rows * d, np.uint16)
+    lib().tfo_reduce_token_major(_ptr(p), _ptr(w), rows, top_k, d, _ptr(out))
+    return out
+
+
+def gemm_int4(W, S, B, X, fmt=FMT_F16, rows=None):
+    """MPPPrefillInt4QMMTests.cpuReference (T/Kernels/TensorCore/MPPPrefillInt4QMMTests.swift:80-105),
+    fp32 accumulator (unrounded). rows=(r0, r1) computes a bounded sample of token rows."""
+    W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16); X = _c(X, np.float32)
+    M, K = X.shape
+    N = W.shape[0]
+    r0, r1 = (0, M) if rows is None else rows
+    Y = np.zeros((M, N), np.float32)
+    lib().tfo_gemm_int4(_ptr(W), _ptr(S), _ptr(B), fmt, _ptr(X), M, N, K, _ptr(Y), r0, r1)
+    return Y
+
+
+def rel_error(actual, reference) -> float:
+    """RelError.compute (V/Tolerance/RelError.swift:7-16)."""
+    a = _c(actual, np.float32).ravel(); r = _c(reference, np.float32).ravel()
+    assert a.size == r.size
+    return lib().tfo_rel_error(_ptr(a), _ptr(r), a.size)
+
+
+def max_abs_diff(a, b) -> float:
+    a = _c(a, np.float32).ravel(); b = _c(b, np.float32).ravel()
+    return lib().tfo_max_abs_diff(_ptr(a), _ptr(b), a.size)
+
+
+class Tolerance:
+    """V/Tolerance/Tolerances.swift:4-21, plus the north-star bar."""
+    identity = 1e-5
+    fp16_reduction = 5e-3
+    fp16_chained_reduction = 1e-2
+    quant_int4 = 1.5e-3
+    quant_int8 = 1e-3
+    north_star = 1e-3     # max relative error for floating-point outputs

@@ -1,0 +1,644 @@
+/*
+ * tfq_oracle.c — CPU restatement of the reference's quantized-matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the product): see tfq_oracle.h.
+ * Build with -ffp-contract=off (oracle/Makefile) so that every `a * b + c`
+ * below rounds twice, as Swift evaluates it.
+ */
+#include "tfq_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* PRNG                                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* V/PRNG/SplitMix64.swift:11-17 */
+uint64_t tfo_splitmix64_next(uint64_t *state) {
+    *state += 0x9E3779B97F4A7C15ULL;
+    uint64_t z = *state;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+/* V/PRNG/SplitMix64.swift:20-23: u = Float(next() >> 40) / 2^24; lo + (hi - lo) * u */
+float tfo_splitmix64_uniform(uint64_t *state, float lo, float hi) {
+    float u = (float)(tfo_splitmix64_next(state) >> 40) / (float)(1u << 24);
+    float span = hi - lo;
+    float scaled = span * u;
+    return lo + scaled;
+}
+
+/* V/PRNG/SeedTree.swift:12-19: FNV-1a-64 of the UTF-8 label, xor the root. */
+uint64_t tfo_seedtree_key(uint64_t root, const char *label) {
+    uint64_t h = 0xCBF29CE484222325ULL;
+    for (const unsigned char *p = (const unsigned char *)label; *p; ++p) {
+        h ^= (uint64_t)*p;
+        h *= 0x100000001B3ULL;
+    }
+    return root ^ h;
+}
+
+/* ------------------------------------------------------------------------ */
+/* 16-bit floats                                                             */
+/* ------------------------------------------------------------------------ */
+
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* Quantization.swift:16-23: RNE by adding 0x7FFF + lsb, no NaN special case. */
+uint16_t tfo_f32_to_bf16(float x) {
+    uint32_t bits = f2u(x);
+    uint32_t lsb = (bits >> 16) & 1u;
+    uint32_t rounded = (bits + 0x7FFFu + lsb) >> 16;
+    return (uint16_t)rounded;
+}
+
+/* Quantization.swift:25-28 */
+float tfo_bf16_to_f32(uint16_t bits) { return u2f((uint32_t)bits << 16); }
+
+/* IEEE-754 binary32 -> binary16, round to nearest, ties to even. */
+uint16_t tfo_f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) {                       /* inf / nan */
+        if (ax == 0x7F800000u) return (uint16_t)(sign | 0x7C00u);
+        return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+    }
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);   /* rounds to inf */
+    int e = (int)(ax >> 23) - 127;
+    uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+    if (e < -14) {                                  /* binary16 subnormal or zero */
+        if (ax == 0) return (uint16_t)sign;
+        int s = -(e + 1);                           /* value / 2^-24 = m >> s */
+        if (s > 31) return (uint16_t)sign;
+        uint32_t h = m >> s;
+        uint32_t rem = m & ((1u << s) - 1u);
+        uint32_t half = 1u << (s - 1);
+        if (rem > half || (rem == half && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = ((uint32_t)(e + 15) << 10) | ((m >> 13) & 0x3FFu);
+    uint32_t rem = m & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;   /* carry may bump the exponent */
+    return (uint16_t)(sign | h);
+}
+
+float tfo_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    if (e == 0) {
+        if (m == 0) return u2f(sign);
+        /* subnormal: m * 2^-24, exact in fp32 */
+        float v = (float)m * (1.0f / 16777216.0f);
+        return sign ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7F800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+float tfo_decode_scale(uint16_t bits, int scale_fmt) {
+    return scale_fmt == TFO_FMT_BF16 ? tfo_bf16_to_f32(bits) : tfo_f16_to_f32(bits);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Affine format                                                             */
+/* ------------------------------------------------------------------------ */
+
+/* Per-group min/max affine quantiser shared by the 4- and 8-bit fixtures:
+ * Quantization.swift:59-100 (int4) and :144-175 (int8). */
+static void quantize_affine_row(const float *row, int n, int levels, int bits,
+                                uint8_t *packed, uint16_t *scales, uint16_t *biases) {
+    int n_groups = n / TFO_GROUP;
+    if (bits == 4) memset(packed, 0, (size_t)n / 2);
+    for (int g = 0; g < n_groups; ++g) {
+        float wmin = INFINITY, wmax = -INFINITY;
+        for (int k = 0; k < TFO_GROUP; ++k) {
+            float w = row[g * TFO_GROUP + k];
+            if (w < wmin) wmin = w;
+            if (w > wmax) wmax = w;
+        }
+        float scale_f, bias_f;
+        if (wmax == wmin) { scale_f = 1.0f; bias_f = wmin; }
+        else { scale_f = (wmax - wmin) / (float)levels; bias_f = wmin; }
+        uint16_t sb = tfo_f32_to_bf16(scale_f), bb = tfo_f32_to_bf16(bias_f);
+        scales[g] = sb;
+        biases[g] = bb;
+        float scale = tfo_bf16_to_f32(sb), bias = tfo_bf16_to_f32(bb);
+        float inv = scale == 0.0f ? 0.0f : 1.0f / scale;
+        for (int k = 0; k < TFO_GROUP; ++k) {
+            float w = row[g * TFO_GROUP + k];
+            float t = (w - bias) * inv;
+            long q = (long)roundf(t);               /* Swift .rounded(): ties away from zero */
+            if (q < 0) q = 0;
+            if (q > levels) q = levels;
+            if (bits == 4) {
+                int byte_idx = g * (TFO_GROUP / 2) + k / 2;
+                uint8_t nib = (uint8_t)(q & 0x0F);
+                if ((k & 1) == 0) packed[byte_idx] = (uint8_t)((packed[byte_idx] & 0xF0) | nib);
+                else packed[byte_idx] = (uint8_t)((packed[byte_idx] & 0x0F) | (nib << 4));
+            } else {
+                packed[g * TFO_GROUP + k] = (uint8_t)q;
+            }
+        }
+    }
+}
+
+void tfo_quantize_int4_row(const float *row, int n, uint8_t *packed, uint16_t *s, uint16_t *b) {
+    quantize_affine_row(row, n, 15, 4, packed, s, b);
+}
+
+void tfo_quantize_int8_row(const float *row, int n, uint8_t *packed, uint16_t *s, uint16_t *b) {
+    quantize_affine_row(row, n, 255, 8, packed, s, b);
+}
+
+/* Element j of a packed int4 row: low nibble of byte j/2 for even j, high for
+ * odd j (Quantization.swift:112-114). On a little-endian host this is bits
+ * 4*(j%8) .. 4*(j%8)+3 of 32-bit word j/8. */
+uint32_t tfo_int4_code(const uint8_t *packed_row, size_t j) {
+    uint8_t b = packed_row[j >> 1];
+    return (j & 1) ? (uint32_t)(b >> 4) : (uint32_t)(b & 0x0F);
+}
+
+/* Quantization.swift:104-119: w = Float(nibble) * scale + bias (two roundings). */
+void tfo_dequantize_int4_row(const uint8_t *packed, const uint16_t *scales, const uint16_t *biases,
+                             int scale_fmt, int n, float *out) {
+    for (int g = 0; g < n / TFO_GROUP; ++g) {
+        float scale = tfo_decode_scale(scales[g], scale_fmt);
+        float bias = tfo_decode_scale(biases[g], scale_fmt);
+        for (int k = 0; k < TFO_GROUP; ++k) {
+            size_t j = (size_t)g * TFO_GROUP + k;
+            float prod = (float)tfo_int4_code(packed, j) * scale;
+            out[j] = prod + bias;
+        }
+    }
+}
+
+/* Quantization.swift:179-191 */
+void tfo_dequantize_int8_row(const uint8_t *packed, const uint16_t *scales, const uint16_t *biases,
+                             int scale_fmt, int n, float *out) {
+    for (int g = 0; g < n / TFO_GROUP; ++g) {
+        float scale = tfo_decode_scale(scales[g], scale_fmt);
+        float bias = tfo_decode_scale(biases[g], scale_fmt);
+        for (int k = 0; k < TFO_GROUP; ++k) {
+            size_t j = (size_t)g * TFO_GROUP + k;
+            float prod = (float)packed[j] * scale;
+            out[j] = prod + bias;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* GEMV references                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* V/Reference/Quant/DequantInt4Gemv.swift:26-40: per row, dequantise to fp32,
+ * then dot in index order (the scalar loop that pins vDSP_dotpr,
+ * T/Validation/Reference/DequantInt4GEMVReferenceTests.swift:13-27). */
+static void gemv_int4_rows(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                           const float *x, int r0, int r1, int n, float *y) {
+    float *w = (float *)malloc(sizeof(float) * (size_t)n);
+    size_t row_bytes = (size_t)n / 2, groups = (size_t)n / TFO_GROUP;
+    for (int r = r0; r < r1; ++r) {
+        tfo_dequantize_int4_row(W + (size_t)r * row_bytes, S + (size_t)r * groups,
+                                B + (size_t)r * groups, fmt, n, w);
+        float sum = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            float p = w[i] * x[i];
+            sum = sum + p;
+        }
+        y[r] = sum;
+    }
+    free(w);
+}
+
+void tfo_gemv_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                   const float *x, int m, int n, float *y) {
+    gemv_int4_rows(W, S, B, fmt, x, 0, m, n, y);
+}
+
+void tfo_gemv_int4_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                       const float *x, int m, int n, double *y) {
+    float *w = (float *)malloc(sizeof(float) * (size_t)n);
+    size_t row_bytes = (size_t)n / 2, groups = (size_t)n / TFO_GROUP;
+    for (int r = 0; r < m; ++r) {
+        tfo_dequantize_int4_row(W + (size_t)r * row_bytes, S + (size_t)r * groups,
+                                B + (size_t)r * groups, fmt, n, w);
+        double sum = 0.0;
+        for (int i = 0; i < n; ++i) sum += (double)w[i] * (double)x[i];
+        y[r] = sum;
+    }
+    free(w);
+}
+
+/* V/Reference/Quant/DequantInt8Gemv.swift:24-38 */
+void tfo_gemv_int8(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                   const float *x, int m, int n, float *y) {
+    float *w = (float *)malloc(sizeof(float) * (size_t)n);
+    size_t groups = (size_t)n / TFO_GROUP;
+    for (int r = 0; r < m; ++r) {
+        tfo_dequantize_int8_row(W + (size_t)r * n, S + (size_t)r * groups, B + (size_t)r * groups,
+                                fmt, n, w);
+        float sum = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            float p = w[i] * x[i];
+            sum = sum + p;
+        }
+        y[r] = sum;
+    }
+    free(w);
+}
+
+void tfo_gemv_int8_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                       const float *x, int m, int n, double *y) {
+    float *w = (float *)malloc(sizeof(float) * (size_t)n);
+    size_t groups = (size_t)n / TFO_GROUP;
+    for (int r = 0; r < m; ++r) {
+        tfo_dequantize_int8_row(W + (size_t)r * n, S + (size_t)r * groups, B + (size_t)r * groups,
+                                fmt, n, w);
+        double sum = 0.0;
+        for (int i = 0; i < n; ++i) sum += (double)w[i] * (double)x[i];
+        y[r] = sum;
+    }
+    free(w);
+}
+
+typedef struct {
+    const uint8_t *W; const uint16_t *S, *B; int fmt; const float *x;
+    int r0, r1, n; float *y;
+} gemv_job;
+
+static void *gemv_worker(void *arg) {
+    gemv_job *j = (gemv_job *)arg;
+    gemv_int4_rows(j->W, j->S, j->B, j->fmt, j->x, j->r0, j->r1, j->n, j->y);
+    return NULL;
+}
+
+void tfo_gemv_int4_mt(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                      const float *x, int m, int n, float *y, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    pthread_t tid[256];
+    gemv_job jobs[256];
+    int per = (m + threads - 1) / threads;
+    int launched = 0;
+    for (int t = 0; t < threads; ++t) {
+        int r0 = t * per, r1 = r0 + per > m ? m : r0 + per;
+        if (r0 >= r1) break;
+        jobs[t] = (gemv_job){W, S, B, fmt, x, r0, r1, n, y};
+        if (pthread_create(&tid[t], NULL, gemv_worker, &jobs[t]) != 0) {
+            gemv_worker(&jobs[t]);
+            tid[t] = 0;
+        }
+        launched = t + 1;
+    }
+    for (int t = 0; t < launched; ++t)
+        if (tid[t]) pthread_join(tid[t], NULL);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Router                                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* T/Kernels/MoE/RouterTopKTests.swift:76-80: scaled = h ⊙ eff, then the int8
+ * GEMV reference over the expert rows. */
+void tfo_router_logits(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                       const float *h, const float *eff, int num_experts, int d, float *logits) {
+    float *scaled = (float *)malloc(sizeof(float) * (size_t)d);
+    for (int i = 0; i < d; ++i) scaled[i] = eff ? h[i] * eff[i] : h[i];
+    tfo_gemv_int8(W, S, B, fmt, scaled, num_experts, d, logits);
+    free(scaled);
+}
+
+/* T/Kernels/MoE/RouterTopKTests.swift:81-96: sort by (logit desc, index asc),
+ * keep k, weights = exp(l - max) / Σ exp × expert_scale[idx]. */
+int tfo_topk_softmax(const float *logits, int num_experts, int k, const float *expert_scale,
+                     uint32_t *idx, float *weights) {
+    if (k <= 0 || k > num_experts) return -1;
+    /* selection by repeated scan keeps the (desc, asc-index) order exactly */
+    unsigned char *taken = (unsigned char *)calloc((size_t)num_experts, 1);
+    for (int r = 0; r < k; ++r) {
+        int best = -1;
+        for (int e = 0; e < num_experts; ++e) {
+            if (taken[e]) continue;
+            if (best < 0 || logits[e] > logits[best]) best = e;   /* strict: ties keep lower index */
+        }
+        taken[best] = 1;
+        idx[r] = (uint32_t)best;
+    }
+    free(taken);
+    float maximum = logits[idx[0]];
+    float *ex = (float *)malloc(sizeof(float) * (size_t)k);
+    float sum = 0.0f;
+    for (int r = 0; r < k; ++r) { ex[r] = expf(logits[idx[r]] - maximum); }
+    for (int r = 0; r < k; ++r) sum = sum + ex[r];               /* reduce(0, +) in order */
+    for (int r = 0; r < k; ++r) {
+        float gain = expert_scale ? expert_scale[idx[r]] : 1.0f;
+        float v = ex[r] / sum;
+        weights[r] = v * gain;
+    }
+    free(ex);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MoE                                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* V/Reference/MoE/Moe.swift:17-29:
+ * inner = c * (x + k * x * x * x); y = 0.5 * x * (1 + tanh(inner)) */
+float tfo_gelu_tanh(float xv) {
+    const float c = 0.7978845608028654f, k3 = 0.044715f;
+    float cube_term = k3 * xv;
+    cube_term = cube_term * xv;
+    cube_term = cube_term * xv;
+    float inner_sum = xv + cube_term;
+    float inner = c * inner_sum;
+    float half_x = 0.5f * xv;
+    float one_plus = 1.0f + tanhf(inner);
+    return half_x * one_plus;
+}
+
+/* Moe.swift:33-52 on one expert blob. */
+void tfo_ffn_int4(const uint8_t *blob, const tfo_expert_offsets *o, int fmt, const float *x,
+                  int d, int f, float *out) {
+    float *gate = (float *)malloc(sizeof(float) * (size_t)f);
+    float *up = (float *)malloc(sizeof(float) * (size_t)f);
+    float *act = (float *)malloc(sizeof(float) * (size_t)f);
+    tfo_gemv_int4(blob + o->gate_w, (const uint16_t *)(blob + o->gate_s),
+                  (const uint16_t *)(blob + o->gate_b), fmt, x, f, d, gate);
+    tfo_gemv_int4(blob + o->up_w, (const uint16_t *)(blob + o->up_s),
+                  (const uint16_t *)(blob + o->up_b), fmt, x, f, d, up);
+    for (int i = 0; i < f; ++i) act[i] = tfo_gelu_tanh(gate[i]) * up[i];   /* vDSP_vmul */
+    tfo_gemv_int4(blob + o->down_w, (const uint16_t *)(blob + o->down_s),
+                  (const uint16_t *)(blob + o->down_b), fmt, act, d, f, out);
+    free(gate); free(up); free(act);
+}
+
+/* Moe.swift:58-88 */
+void tfo_moe_routed(const uint8_t *pool, uint64_t stride, const tfo_expert_offsets *off, int fmt,
+                    const float *x, const float *residual, const uint32_t *idx, const float *w,
+                    int k, int d, int f, float *y) {
+    float *out = (float *)malloc(sizeof(float) * (size_t)d);
+    for (int i = 0; i < d; ++i) y[i] = residual ? residual[i] : 0.0f;
+    for (int slot = 0; slot < k; ++slot) {
+        tfo_ffn_int4(pool + (uint64_t)idx[slot] * stride, off, fmt, x, d, f, out);
+        for (int i = 0; i < d; ++i) {
+            float scaled = out[i] * w[slot];      /* vDSP_vsmul */
+            y[i] = y[i] + scaled;                 /* vDSP_vadd */
+        }
+    }
+    free(out);
+}
+
+/* T/Kernels/MoE/SharedExpertInt4Tests.swift:21-28 */
+void tfo_shared_expert_int4(const uint8_t *gW, const uint16_t *gS, const uint16_t *gB,
+                            const uint8_t *uW, const uint16_t *uS, const uint16_t *uB,
+                            const uint8_t *dW, const uint16_t *dS, const uint16_t *dB,
+                            int fmt, const float *x, int d, int f, float *y) {
+    float *g = (float *)malloc(sizeof(float) * (size_t)f);
+    float *u = (float *)malloc(sizeof(float) * (size_t)f);
+    float *act = (float *)malloc(sizeof(float) * (size_t)f);
+    tfo_gemv_int4(gW, gS, gB, fmt, x, f, d, g);
+    tfo_gemv_int4(uW, uS, uB, fmt, x, f, d, u);
+    for (int i = 0; i < f; ++i) {
+        float gv = g[i];
+        float cube = gv * gv;
+        cube = cube * gv;
+        float k3c = 0.044715f * cube;
+        float inner_f = gv + k3c;
+        double inner = 0.7978845608028654 * (double)inner_f;
+        double gelu = 0.5 * (double)gv * (1.0 + tanh(inner));
+        float prod = (float)gelu * u[i];
+        act[i] = tfo_f16_to_f32(tfo_f32_to_f16(prod));
+    }
+    tfo_gemv_int4(dW, dS, dB, fmt, act, d, f, y);
+    free(g); free(u); free(act);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Prefill grouping                                                          */
+/* ------------------------------------------------------------------------ */
+
+static const uint64_t *g_sort_keys;   /* comparator context (single-threaded use) */
+
+/* PrefillMoEGrouping.swift:145-154: (sortKey[expert]?, expert, token, rank) ascending. */
+static int pair_cmp(const void *pa, const void *pb) {
+    const tfo_pair *a = (const tfo_pair *)pa, *b = (const tfo_pair *)pb;
+    if (g_sort_keys) {
+        uint64_t ka = g_sort_keys[a->expert], kb = g_sort_keys[b->expert];
+        if (ka != kb) return ka < kb ? -1 : 1;
+    }
+    if (a->expert != b->expert) return a->expert < b->expert ? -1 : 1;
+    if (a->token != b->token) return a->token < b->token ? -1 : 1;
+    if (a->rank != b->rank) return a->rank < b->rank ? -1 : 1;
+    return 0;
+}
+
+/* PrefillMoEGrouping.swift:91-192 */
+int tfo_group_pairs(const tfo_pair *pairs, int64_t n_pairs, int64_t query_count, int64_t top_k,
+                    int64_t num_experts, int64_t tile_expert_count,
+                    const uint64_t *sort_keys, int64_t n_sort_keys,
+                    tfo_pair *sorted, uint32_t *offsets, uint32_t *counts,
+                    tfo_group *groups, int64_t *n_groups, tfo_tile *tiles, int64_t *n_tiles,
+                    int64_t err[2]) {
+    err[0] = err[1] = 0;
+    if (query_count < 0) { err[0] = query_count; return TFO_GROUP_INVALID_QUERY_COUNT; }
+    if (top_k <= 0) { err[0] = top_k; return TFO_GROUP_INVALID_TOPK; }
+    if (num_experts <= 0) { err[0] = num_experts; return TFO_GROUP_INVALID_NUM_EXPERTS; }
+    if (tile_expert_count < 1 || tile_expert_count > 16) {
+        err[0] = tile_expert_count; return TFO_GROUP_INVALID_TILE_EXPERT_COUNT;
+    }
+    if (sort_keys && n_sort_keys != num_experts) {
+        err[0] = num_experts; err[1] = n_sort_keys; return TFO_GROUP_SORT_KEY_COUNT_MISMATCH;
+    }
+    int64_t expected = query_count * top_k;
+    if (n_pairs != expected) { err[0] = expected; err[1] = n_pairs; return TFO_GROUP_PAIR_COUNT_MISMATCH; }
+
+    unsigned char *seen = (unsigned char *)calloc((size_t)(expected > 0 ? expected : 1), 1);
+    for (int64_t i = 0; i < n_pairs; ++i) {
+        const tfo_pair *p = &pairs[i];
+        if ((int64_t)p->token >= query_count) { free(seen); err[0] = p->token; return TFO_GROUP_TOKEN_OUT_OF_RANGE; }
+        if ((int64_t)p->rank >= top_k) { free(seen); err[0] = p->rank; return TFO_GROUP_RANK_OUT_OF_RANGE; }
+        if ((int64_t)p->expert >= num_experts) { free(seen); err[0] = p->expert; return TFO_GROUP_EXPERT_OUT_OF_RANGE; }
+        int64_t key = (int64_t)p->token * top_k + p->rank;
+        if (seen[key]) { free(seen); err[0] = p->token; err[1] = p->rank; return TFO_GROUP_DUPLICATE_TOKEN_RANK; }
+        seen[key] = 1;
+    }
+    free(seen);
+
+    memcpy(sorted, pairs, sizeof(tfo_pair) * (size_t)n_pairs);
+    g_sort_keys = sort_keys;
+    qsort(sorted, (size_t)n_pairs, sizeof(tfo_pair), pair_cmp);
+    g_sort_keys = NULL;
+
+    for (int64_t e = 0; e < num_experts; ++e) { offsets[e] = 0xFFFFFFFFu; counts[e] = 0; }
+    int64_t ng = 0;
+    int64_t i = 0;
+    while (i < n_pairs) {
+        uint32_t expert = sorted[i].expert;
+        int64_t start = i;
+        while (i < n_pairs && sorted[i].expert == expert) ++i;
+        offsets[expert] = (uint32_t)start;
+        counts[expert] = (uint32_t)(i - start);
+        groups[ng].expert = expert;
+        groups[ng].pair_start = (uint32_t)start;
+        groups[ng].pair_count = (uint32_t)(i - start);
+        ++ng;
+    }
+    int64_t nt = 0;
+    for (int64_t gs = 0; gs < ng;) {
+        int64_t ge = gs + tile_expert_count < ng ? gs + tile_expert_count : ng;
+        uint32_t ps = groups[gs].pair_start;
+        uint32_t pe = groups[ge - 1].pair_start + groups[ge - 1].pair_count;
+        tiles[nt].group_start = (uint32_t)gs;
+        tiles[nt].group_count = (uint32_t)(ge - gs);
+        tiles[nt].pair_start = ps;
+        tiles[nt].pair_count = pe - ps;
+        ++nt;
+        gs = ge;
+    }
+    *n_groups = ng;
+    *n_tiles = nt;
+    return TFO_GROUP_OK;
+}
+
+int tfo_prefill_router(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                       const float *hidden, int hidden_stride, const float *eff,
+                       const float *expert_scale, int T, int num_experts, int d, int k,
+                       uint32_t *idx, float *weights) {
+    float *logits = (float *)malloc(sizeof(float) * (size_t)num_experts);
+    int rc = 0;
+    for (int t = 0; t < T && rc == 0; ++t) {
+        tfo_router_logits(W, S, B, fmt, hidden + (size_t)t * hidden_stride, eff, num_experts, d,
+                          logits);
+        rc = tfo_topk_softmax(logits, num_experts, k, expert_scale, idx + (size_t)t * k,
+                              weights + (size_t)t * k);
+    }
+    free(logits);
+    return rc;
+}
+
+/* cpuInt4Dot (PrefillGroupedRoutedMoETests.swift:281-303): acc += (q*s + b) * x. */
+static float int4_dot_blob(const uint8_t *blob, uint32_t w_off, uint32_t s_off, uint32_t b_off,
+                           int fmt, int row, int n, const float *x) {
+    int groups = n / TFO_GROUP;
+    const uint8_t *w_row = blob + w_off + (size_t)row * (n / 2);
+    const uint16_t *s_row = (const uint16_t *)(blob + s_off) + (size_t)row * groups;
+    const uint16_t *b_row = (const uint16_t *)(blob + b_off) + (size_t)row * groups;
+    float acc = 0.0f;
+    for (int g = 0; g < groups; ++g) {
+        float scale = tfo_decode_scale(s_row[g], fmt), bias = tfo_decode_scale(b_row[g], fmt);
+        for (int k = 0; k < TFO_GROUP; ++k) {
+            int col = g * TFO_GROUP + k;
+            float q = (float)tfo_int4_code(w_row, (size_t)col);
+            float w = q * scale;
+            w = w + bias;
+            float p = w * x[col];
+            acc = acc + p;
+        }
+    }
+    return acc;
+}
+
+/* PrefillGroupedRoutedMoETests.swift:229-279 */
+void tfo_grouped_route_partials(const tfo_pair *sorted, int64_t n_pairs,
+                                const uint16_t *hidden_f16, int hidden_stride,
+                                const uint8_t *pool, uint64_t stride,
+                                const tfo_expert_offsets *o, int fmt,
+                                int top_k, int d, int f, uint16_t *partials) {
+    float *x = (float *)malloc(sizeof(float) * (size_t)d);
+    float *act = (float *)malloc(sizeof(float) * (size_t)f);
+    for (int64_t p = 0; p < n_pairs; ++p) {
+        const tfo_pair *pr = &sorted[p];
+        const uint8_t *blob = pool + (uint64_t)pr->expert * stride;
+        for (int i = 0; i < d; ++i)
+            x[i] = tfo_f16_to_f32(hidden_f16[(size_t)pr->token * hidden_stride + i]);
+        for (int r = 0; r < f; ++r) {
+            float gate = int4_dot_blob(blob, o->gate_w, o->gate_s, o->gate_b, fmt, r, d, x);
+            float up = int4_dot_blob(blob, o->up_w, o->up_s, o->up_b, fmt, r, d, x);
+            float a = tfo_gelu_tanh(gate) * up;
+            act[r] = tfo_f16_to_f32(tfo_f32_to_f16(a));
+        }
+        size_t out_base = ((size_t)pr->token * top_k + pr->rank) * d;
+        for (int r = 0; r < d; ++r) {
+            float v = int4_dot_blob(blob, o->down_w, o->down_s, o->down_b, fmt, r, f, act);
+            partials[out_base + r] = tfo_f32_to_f16(v);
+        }
+    }
+    free(x); free(act);
+}
+
+/* PrefillMoETests.swift:46-58 */
+void tfo_reduce_token_major(const uint16_t *partials, const uint16_t *weights, int rows, int top_k,
+                            int d, uint16_t *h2) {
+    for (int t = 0; t < rows; ++t) {
+        for (int c = 0; c < d; ++c) {
+            float acc = 0.0f;
+            for (int r = 0; r < top_k; ++r) {
+                size_t pi = ((size_t)t * top_k + r) * d + c;
+                float p = tfo_f16_to_f32(weights[t * top_k + r]) * tfo_f16_to_f32(partials[pi]);
+                acc = acc + p;
+            }
+            h2[(size_t)t * d + c] = tfo_f32_to_f16(acc);
+        }
+    }
+}
+
+/* MPPPrefillInt4QMMTests.swift:80-105: weight = q*s + b (two roundings),
+ * accumulator.addProduct(weight, x) (fused). */
+void tfo_gemm_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                   const float *X, int M, int N, int K, float *Y, int row0, int row1) {
+    int groups = K / TFO_GROUP;
+    size_t row_bytes = (size_t)K / 2;
+    if (row0 < 0) row0 = 0;
+    if (row1 > M) row1 = M;
+    for (int t = row0; t < row1; ++t) {
+        const float *xr = X + (size_t)t * K;
+        for (int n = 0; n < N; ++n) {
+            const uint8_t *wr = W + (size_t)n * row_bytes;
+            float acc = 0.0f;
+            for (int g = 0; g < groups; ++g) {
+                float scale = tfo_decode_scale(S[(size_t)n * groups + g], fmt);
+                float bias = tfo_decode_scale(B[(size_t)n * groups + g], fmt);
+                for (int lk = 0; lk < TFO_GROUP; ++lk) {
+                    int col = g * TFO_GROUP + lk;
+                    float w = (float)tfo_int4_code(wr, (size_t)col) * scale;
+                    w = w + bias;
+                    acc = fmaf(w, xr[col], acc);
+                }
+            }
+            Y[(size_t)t * N + n] = acc;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Tolerance helpers (V/Tolerance/RelError.swift:7-27)                       */
+/* ------------------------------------------------------------------------ */
+
+float tfo_rel_error(const float *actual, const float *reference, size_t n) {
+    float max_abs = 0.0f, ref_norm = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        float d = fabsf(actual[i] - reference[i]);
+        if (d > max_abs || d != d) max_abs = d;
+        float r = fabsf(reference[i]);
+        if (r > ref_norm) ref_norm = r;
+    }
+    return max_abs / (ref_norm > 1e-6f ? ref_norm : 1e-6f);
+}
+
+float tfo_max_abs_diff(const float *a, const float *b, size_t n) {
+    float m = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        float d = fabsf(a[i] - b[i]);
+        if (d > m || d != d) m = d;
+    }
+    return m;
+}

@@ -1,0 +1,178 @@
+/*
+ * tfq_oracle.h — CPU restatement of the reference's quantized-matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product (libtfq, the HIP kernels,
+ * the edgeexpert_amd package) links, loads or calls this library. It is the
+ * checker: tests/, __graft_entry__.smoke() and the cpu_baseline leg of
+ * bench.py use it to verify and to time the CPU path.
+ *
+ * Every function follows one reference function; the file:line it restates is
+ * cited beside it (paths relative to the reference checkout):
+ *   S/ = Sources/TurboFieldfare/
+ *   V/ = Sources/TurboFieldfareValidation/Support/
+ *   T/ = Tests/TurboFieldfare/Core/
+ *
+ * Scale/bias words: the reference stores BF16 scale and bias per group of 64
+ * (S/Infrastructure/ModelIO/Quantization.swift:32-45); the MI355X library
+ * stores fp16. Every dequantising function therefore takes `scale_fmt`
+ * (TFO_FMT_F16 or TFO_FMT_BF16) and decodes the 16-bit words accordingly; the
+ * arithmetic after decoding is the reference's.
+ *
+ * Floating point: this file is compiled with -ffp-contract=off so that
+ * `a * b + c` rounds twice, exactly as Swift evaluates it; where the
+ * reference calls a fused multiply-add (Swift `addProduct`, Metal `fma`)
+ * the restatement calls fmaf explicitly.
+ */
+#ifndef TFQ_ORACLE_H
+#define TFQ_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { TFO_FMT_F16 = 0, TFO_FMT_BF16 = 1 };
+enum { TFO_GROUP = 64 };
+
+/* ---- PRNG (V/PRNG/SplitMix64.swift:11-23, V/PRNG/SeedTree.swift:12-19) ---- */
+uint64_t tfo_splitmix64_next(uint64_t *state);
+float tfo_splitmix64_uniform(uint64_t *state, float lo, float hi);
+uint64_t tfo_seedtree_key(uint64_t root, const char *label);
+
+/* ---- 16-bit float conversions ---- */
+uint16_t tfo_f32_to_bf16(float x);            /* Quantization.swift:16-23 */
+float tfo_bf16_to_f32(uint16_t bits);         /* Quantization.swift:25-28 */
+uint16_t tfo_f32_to_f16(float x);             /* IEEE binary16, round-half-even (Swift Float16(_:)) */
+float tfo_f16_to_f32(uint16_t bits);
+float tfo_decode_scale(uint16_t bits, int scale_fmt);
+
+/* ---- affine format (Quantization.swift:50-191) ---- */
+void tfo_quantize_int4_row(const float *row, int n, uint8_t *packed,
+                           uint16_t *scales_bf16, uint16_t *biases_bf16);
+void tfo_quantize_int8_row(const float *row, int n, uint8_t *packed,
+                           uint16_t *scales_bf16, uint16_t *biases_bf16);
+void tfo_dequantize_int4_row(const uint8_t *packed, const uint16_t *scales,
+                             const uint16_t *biases, int scale_fmt, int n, float *out);
+void tfo_dequantize_int8_row(const uint8_t *packed, const uint16_t *scales,
+                             const uint16_t *biases, int scale_fmt, int n, float *out);
+uint32_t tfo_int4_code(const uint8_t *packed_row, size_t j);
+
+/* ---- GEMV: dequantise row to fp32, then fp32 dot in index order ----
+ * V/Reference/Quant/DequantInt4Gemv.swift:12-42 and DequantInt8Gemv.swift:12-40
+ * (vDSP_dotpr, pinned to a scalar index-order loop within 1e-5 by
+ * T/Validation/Reference/DequantInt4GEMVReferenceTests.swift:38-53).
+ * W rows are contiguous: row r starts at W + r*n/2 (int4) or W + r*n (int8);
+ * scales/biases rows at S + r*n/64. The _f64 variants accumulate in double
+ * (the "truth" used to bound the fp32 paths). */
+void tfo_gemv_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
+                   const float *x, int m, int n, float *y);
+void tfo_gemv_int4_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
+                       const float *x, int m, int n, double *y);
+void tfo_gemv_int8(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
+                   const float *x, int m, int n, float *y);
+void tfo_gemv_int8_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
+                       const float *x, int m, int n, double *y);
+/* Row-partitioned multithreaded variant of tfo_gemv_int4 (same per-row arithmetic). */
+void tfo_gemv_int4_mt(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
+                      const float *x, int m, int n, float *y, int threads);
+
+/* ---- router (T/Kernels/MoE/RouterTopKTests.swift:72-97) ----
+ * logits = int8-GEMV(W, h ⊙ eff); eff == NULL means all ones. */
+void tfo_router_logits(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
+                       const float *h, const float *eff, int num_experts, int d, float *logits);
+/* sort (score desc, index asc), keep k, softmax over the k, × expert_scale
+ * (NULL = ones). Returns 0, or -1 when k > num_experts or k <= 0. */
+int tfo_topk_softmax(const float *logits, int num_experts, int k, const float *expert_scale,
+                     uint32_t *idx, float *weights);
+
+/* ---- MoE (V/Reference/MoE/Moe.swift:16-88) ---- */
+float tfo_gelu_tanh(float x);                                 /* Moe.swift:21-29 */
+
+typedef struct {
+    uint32_t gate_w, gate_s, gate_b;
+    uint32_t up_w, up_s, up_b;
+    uint32_t down_w, down_s, down_b;
+} tfo_expert_offsets;                                         /* S/Kernels/MoE/MoE.swift:4-29 */
+
+/* runFFN (Moe.swift:33-52) for one expert blob: out = down(gelu(gate·x) ⊙ (up·x)). */
+void tfo_ffn_int4(const uint8_t *blob, const tfo_expert_offsets *off, int scale_fmt,
+                  const float *x, int d, int f, float *out);
+/* applyStreamedRouted (Moe.swift:58-88): y = residual + Σ_slot w[slot]·ffn(expert idx[slot]).
+ * Expert e's blob is pool + e*stride. residual == NULL means zeros. */
+void tfo_moe_routed(const uint8_t *pool, uint64_t stride, const tfo_expert_offsets *off,
+                    int scale_fmt, const float *x, const float *residual,
+                    const uint32_t *idx, const float *w, int k, int d, int f, float *y);
+/* Shared expert reference (T/Kernels/MoE/SharedExpertInt4Tests.swift:21-28):
+ * gate/up by the GEMV reference, act rounded to fp16, down by the GEMV reference.
+ * The GELU here is evaluated in double as that test does. */
+void tfo_shared_expert_int4(const uint8_t *gW, const uint16_t *gS, const uint16_t *gB,
+                            const uint8_t *uW, const uint16_t *uS, const uint16_t *uB,
+                            const uint8_t *dW, const uint16_t *dS, const uint16_t *dB,
+                            int scale_fmt, const float *x, int d, int f, float *y);
+
+/* ---- prefill grouping (S/Kernels/Prefill/MoE/PrefillMoEGrouping.swift:91-192) ---- */
+typedef struct { uint32_t token, expert, rank, weight_bits; } tfo_pair;   /* PrefillRouter.swift:5-28 */
+typedef struct { uint32_t expert, pair_start, pair_count; } tfo_group;   /* PrefillMoEGrouping.swift:3-14 */
+typedef struct { uint32_t group_start, group_count, pair_start, pair_count; } tfo_tile; /* :16-29 */
+
+enum {
+    TFO_GROUP_OK = 0,
+    TFO_GROUP_INVALID_QUERY_COUNT = 1,
+    TFO_GROUP_INVALID_TOPK = 2,
+    TFO_GROUP_INVALID_NUM_EXPERTS = 3,
+    TFO_GROUP_INVALID_TILE_EXPERT_COUNT = 4,
+    TFO_GROUP_PAIR_COUNT_MISMATCH = 5,
+    TFO_GROUP_TOKEN_OUT_OF_RANGE = 6,
+    TFO_GROUP_RANK_OUT_OF_RANGE = 7,
+    TFO_GROUP_EXPERT_OUT_OF_RANGE = 8,
+    TFO_GROUP_DUPLICATE_TOKEN_RANK = 9,
+    TFO_GROUP_SORT_KEY_COUNT_MISMATCH = 10,
+};
+
+/* Returns a TFO_GROUP_* code; on error err[0], err[1] carry the values the
+ * Swift error case carries. sort_keys may be NULL; n_sort_keys is its length.
+ * Outputs: sorted[n_pairs], offsets[num_experts], counts[num_experts],
+ * groups[<= num_experts], tiles[<= num_experts]. */
+int tfo_group_pairs(const tfo_pair *pairs, int64_t n_pairs, int64_t query_count, int64_t top_k,
+                    int64_t num_experts, int64_t tile_expert_count,
+                    const uint64_t *sort_keys, int64_t n_sort_keys,
+                    tfo_pair *sorted, uint32_t *offsets, uint32_t *counts,
+                    tfo_group *groups, int64_t *n_groups, tfo_tile *tiles, int64_t *n_tiles,
+                    int64_t err[2]);
+
+/* Per-token block router (S/Metal/Prefill/prefill.metal:478-573 semantics,
+ * restated with the decode router reference per token): idx/w are [T][k]. */
+int tfo_prefill_router(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
+                       const float *hidden, int hidden_stride, const float *eff,
+                       const float *expert_scale, int T, int num_experts, int d, int k,
+                       uint32_t *idx, float *weights);
+
+/* cpuSyntheticRoutePartials (T/Kernels/Prefill/PrefillGroupedRoutedMoETests.swift:229-303):
+ * for each sorted pair, act = fp16(gelu(gate)·up), partial = fp16(down·act),
+ * written at partials[(token*top_k + rank)*d + row]. hidden is fp16 bits. */
+void tfo_grouped_route_partials(const tfo_pair *sorted, int64_t n_pairs,
+                                const uint16_t *hidden_f16, int hidden_stride,
+                                const uint8_t *pool, uint64_t stride,
+                                const tfo_expert_offsets *off, int scale_fmt,
+                                int top_k, int d, int f, uint16_t *partials_f16);
+
+/* cpuReduce (T/Kernels/Prefill/PrefillMoETests.swift:46-58). */
+void tfo_reduce_token_major(const uint16_t *partials_f16, const uint16_t *weights_f16,
+                            int rows, int top_k, int d, uint16_t *h2_f16);
+
+/* MPP GEMM cpuReference (T/Kernels/TensorCore/MPPPrefillInt4QMMTests.swift:80-105):
+ * Y[t][n] = Σ_k fma(q·s + b, X[t][k]) over k in index order (fp32, unrounded).
+ * Rows of Y in [row0, row1) are computed (a bounded sample for timing). */
+void tfo_gemm_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
+                   const float *X, int M, int N, int K, float *Y, int row0, int row1);
+
+/* RelError.compute (V/Tolerance/RelError.swift:7-16). */
+float tfo_rel_error(const float *actual, const float *reference, size_t n);
+float tfo_max_abs_diff(const float *a, const float *b, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
