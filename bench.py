@@ -44,7 +44,7 @@ def moe_bytes():
     proj = F * D // 2 + 2 * F * (D // 64) * 2               # 991,232 + 123,904 per projection
     phase1 = K * 2 * proj                                   # gate + up of 8 experts
     phase2 = K * proj                                       # down of 8 experts
-    acts = K * F * 4
+    acts = K * F * 2                                        # fp16 activations
     return {"router": router + 2 * D, "phase1": phase1 + 2 * D + acts,
             "phase2": phase2 + acts + 2 * D, "total": router + phase1 + phase2 + 2 * D * 2}
 
@@ -85,7 +85,7 @@ def main():
     ws.fill(0)
     idx = DeviceBuffer(K * 4)
     w16 = DeviceBuffer(K * 2)
-    acts = DeviceBuffer(K * F * 4)
+    acts = DeviceBuffer(K * F * 2)
     moe = ops.MoE(ctx)
 
     def token(t):

@@ -14,6 +14,7 @@ namespace tfq {
 constexpr uint32_t kBlock = 256;          // 4 wavefronts per block for every GEMV-family kernel
 constexpr uint32_t kMaxGridBlocks = 4096;
 constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident in LDS
+constexpr uint32_t kRowsInFlight = 2;     // rows per segment per group (tfq_kernels.hip)
 
 inline uint32_t grid_for_rows(uint64_t rows, uint32_t rows_per_block) {
     uint64_t g = (rows + rows_per_block - 1) / rows_per_block;
@@ -69,10 +70,10 @@ private:
         const SegShape sh = seg_shape(n / 32, 2);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_q4_gemv_s%u_p%u", sh.seg, sh.p);
-        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         uint32_t nn = n;
         void* args[] = {&mats, &x, &nn};
-        return launch(m_.get(name), grid_for_rows(mats.total_rows, rows_per_block), kBlock, n * 4,
+        return launch(m_.get(name), grid_for_rows(mats.total_rows, rows_per_block), kBlock, n * 2,
                       stream, args, name);
     }
 
@@ -98,7 +99,7 @@ public:
         const SegShape sh = seg_shape(n / 16, 4);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_q8_gemv_s%u_p%u", sh.seg, sh.p);
-        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&weights, &scales, &biases, &x, &y, &m, &n};
         return launch(m_.get(name), grid_for_rows(m, rows_per_block), kBlock, n * 4, stream, args,
                       name);
@@ -132,22 +133,26 @@ public:
         if (!aligned(weights, 16)) return fail(TFQ_E_INVAL, "weights are not 16-byte aligned");
         if (!aligned(workspace, 16)) return fail(TFQ_E_INVAL, "workspace is not 16-byte aligned");
         if (!aligned(out_indices, 4)) return fail(TFQ_E_INVAL, "indices are not 4-byte aligned");
+        // Logits land in out_logits when given, else in the workspace; a
+        // one-wavefront launch then selects (stream order is the only sync).
+        float* logits = out_logits ? out_logits : static_cast<float*>(workspace);
         const SegShape sh = seg_shape(d / 16, 4);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_router_topk_s%u_p%u", sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_router_logits_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
         const uint32_t grid = (num_experts + rows_per_block - 1) / rows_per_block;
-        void* args[] = {&weights, &scales, &biases, &hidden, &effective_scale, &per_expert_scale,
-                        &out_indices, &out_weights, &out_weights_f32, &out_logits, &num_experts,
-                        &d, &top_k, &workspace};
-        // LDS holds x (d floats) and, in the selecting block, the E logits.
-        const uint32_t lds = (d > 256 ? d : 256) * 4;
-        return launch(m_.get(name), grid, kBlock, lds, stream, args, name);
+        void* args[] = {&weights, &scales, &biases, &hidden, &effective_scale, &logits,
+                        &num_experts, &d};
+        int rc = launch(m_.get(name), grid, kBlock, d * 4, stream, args, name);
+        if (rc) return rc;
+        void* sargs[] = {&logits, &per_expert_scale, &out_indices, &out_weights, &out_weights_f32,
+                         &num_experts, &top_k};
+        return launch(m_.get("tfq_router_select"), 1, 64, 0, stream, sargs, "tfq_router_select");
     }
 
     // encodeRoutedPersistentPhase1U16Load / ...SubsetU16Load (MoE.swift:234-310).
     int encode_phase1(void* stream, const tfq_expert_pool& pool, const uint32_t* indices,
-                      const uint16_t* x, float* acts, const uint32_t* active_slots,
+                      const uint16_t* x, uint16_t* acts, const uint32_t* active_slots,
                       uint32_t active_count, uint32_t d, uint32_t f, uint32_t top_k) const {
         int rc = check_pool(pool, d, f, top_k);
         if (rc) return rc;
@@ -161,15 +166,15 @@ public:
         const SegShape sh = seg_shape(d / 32, 2);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_moe_phase1_s%u_p%u", sh.seg, sh.p);
-        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&kp, &indices, &active_slots, &active_count, &top_k, &x, &acts, &d, &f};
         return launch(m_.get(name), grid_for_rows((uint64_t)active_count * f, rows_per_block),
-                      kBlock, d * 4, stream, args, name);
+                      kBlock, d * 2, stream, args, name);
     }
 
     // encodeRoutedPersistentPhase2Reduce (MoE.swift:312-362).
     int encode_phase2(void* stream, const tfq_expert_pool& pool, const uint32_t* indices,
-                      const float* acts, const uint16_t* routing_weights, const uint16_t* residual,
+                      const uint16_t* acts, const uint16_t* routing_weights, const uint16_t* residual,
                       uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k) const {
         int rc = check_pool(pool, d, f, top_k);
         if (rc) return rc;
@@ -181,8 +186,8 @@ public:
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_moe_phase2_p%u", p);
         void* args[] = {&kp, &indices, &acts, &routing_weights, &residual, &y, &d, &f, &top_k};
-        return launch(m_.get(name), grid_for_rows(d, kBlock / 64), kBlock, top_k * f * 4, stream,
-                      args, name);
+        return launch(m_.get(name), grid_for_rows(d, (kBlock / 64) * kRowsInFlight), kBlock,
+                      top_k * f * 2, stream, args, name);
     }
 
 private:
@@ -242,9 +247,9 @@ public:
         const SegShape sh = seg_shape(d / 32, 2);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_gate_up_act_s%u_p%u", sh.seg, sh.p);
-        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&g, &u, &x, &act_scratch, &d, &f};
-        int rc = launch(m_.get(name), grid_for_rows(f, rows_per_block), kBlock, d * 4, stream, args,
+        int rc = launch(m_.get(name), grid_for_rows(f, rows_per_block), kBlock, d * 2, stream, args,
                         name);
         if (rc) return rc;
         return gemv_.encode(stream, down.weights, down.scales, down.biases, act_scratch, y, d, f);

@@ -33,9 +33,10 @@ static std::vector<std::string> kernel_names() {
     }
     for (const char* s : q8_shapes) {
         names.push_back(std::string("tfq_q8_gemv_") + s);
-        names.push_back(std::string("tfq_router_topk_") + s);
+        names.push_back(std::string("tfq_router_logits_") + s);
     }
     for (int p = 1; p <= 4; ++p) names.push_back("tfq_moe_phase2_p" + std::to_string(p));
+    names.push_back("tfq_router_select");
     names.push_back("tfq_convert_bf16_f16");
     return names;
 }
@@ -163,14 +164,14 @@ int tfq_router_topk(tfq_ctx* ctx, void* stream, const uint8_t* weights, const ui
 }
 
 int tfq_moe_phase1(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, const uint32_t* indices,
-                   const uint16_t* x, float* acts, uint32_t d, uint32_t f, uint32_t top_k) {
+                   const uint16_t* x, uint16_t* acts, uint32_t d, uint32_t f, uint32_t top_k) {
     TFQ_REQUIRE_CTX(ctx);
     if (!pool) return fail(TFQ_E_INVAL, "null pool");
     return ctx->moe->encode_phase1(stream, *pool, indices, x, acts, nullptr, top_k, d, f, top_k);
 }
 
 int tfq_moe_phase1_subset(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool,
-                          const uint32_t* indices, const uint16_t* x, float* acts,
+                          const uint32_t* indices, const uint16_t* x, uint16_t* acts,
                           const uint32_t* active_slots, uint32_t active_count, uint32_t d,
                           uint32_t f, uint32_t top_k) {
     TFQ_REQUIRE_CTX(ctx);
@@ -181,7 +182,7 @@ int tfq_moe_phase1_subset(tfq_ctx* ctx, void* stream, const tfq_expert_pool* poo
 }
 
 int tfq_moe_phase2(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, const uint32_t* indices,
-                   const float* acts, const uint16_t* routing_weights, const uint16_t* residual,
+                   const uint16_t* acts, const uint16_t* routing_weights, const uint16_t* residual,
                    uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k) {
     TFQ_REQUIRE_CTX(ctx);
     if (!pool) return fail(TFQ_E_INVAL, "null pool");
@@ -191,7 +192,7 @@ int tfq_moe_phase2(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, cons
 
 int tfq_moe_decode(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, const uint32_t* indices,
                    const uint16_t* routing_weights, const uint16_t* x, const uint16_t* residual,
-                   uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k, float* acts_scratch) {
+                   uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k, uint16_t* acts_scratch) {
     TFQ_REQUIRE_CTX(ctx);
     if (!pool) return fail(TFQ_E_INVAL, "null pool");
     int rc = ctx->moe->encode_phase1(stream, *pool, indices, x, acts_scratch, nullptr, top_k, d, f,

@@ -13,6 +13,9 @@ namespace tfq {
 constexpr int kGroup = 64;       // affine group size along the reduction axis
 constexpr int kWave = 64;        // CDNA wavefront width
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
 __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
@@ -46,26 +49,62 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-// Σ_i q_i * x_i over the 32 int4 codes of one 16-byte chunk (8 codes per
-// 32-bit word, element 8j+i in bits 4i..4i+3 of word j), fp32 FMA chain in
-// element order.
-__device__ __forceinline__ float dot32_q4(const uint4 w, const float* x) {
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    float d = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = ws[i] & 0x0F0F0F0Fu;
-        const uint32_t hi = (ws[i] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            d = fmaf((float)((lo >> (8 * b)) & 0xFFu), x[8 * i + 2 * b], d);
-            d = fmaf((float)((hi >> (8 * b)) & 0xFFu), x[8 * i + 2 * b + 1], d);
-        }
-    }
-    return d;
+__device__ __forceinline__ uint4 ldg16(const uint8_t* p) {
+    return *reinterpret_cast<const uint4*>(p);
 }
 
-// Σ_i q_i * x_i over the 16 int8 codes of one 16-byte chunk.
+// ------------------------------------------------------------ int4 chunk ----
+//
+// A chunk is 16 bytes of a weight row: 32 int4 codes, four 32-bit words, code
+// 8j+i in bits 4i..4i+3 of word j. ((w >> 4i) & 0x000F000F) isolates codes
+// 8j+i (low half) and 8j+i+4 (high half); OR-ing 0x6400 into each half gives
+// the fp16 values 1024+q exactly, and subtracting 1024 (v_pk_add_f16) leaves
+// q exactly. v_dot2_f32_f16 then multiplies with the matching activation
+// pair and accumulates in fp32; every product q·x is exact in fp32.
+// The activations of a chunk are therefore held as 16 fp16 pairs
+// xp[4j+i] = (x[8j+i], x[8j+i+4]).
+
+struct XChunk {
+    h2 p[16];
+    float sum;      // Σ of the 32 activations in element order (fp32)
+};
+
+// Builds the pair layout of chunk c from an fp16 vector in LDS.
+__device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ lds_xh, uint32_t c,
+                                            XChunk& xc) {
+    const h8* src = reinterpret_cast<const h8*>(lds_xh + 32u * c);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const h8 v = src[j];
+        xc.p[4 * j + 0] = __builtin_shufflevector(v, v, 0, 4);
+        xc.p[4 * j + 1] = __builtin_shufflevector(v, v, 1, 5);
+        xc.p[4 * j + 2] = __builtin_shufflevector(v, v, 2, 6);
+        xc.p[4 * j + 3] = __builtin_shufflevector(v, v, 3, 7);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += (float)v[e];
+    }
+    xc.sum = s;
+}
+
+// Σ_k q_k x_k over the 32 codes of a chunk (fp32 accumulate).
+__device__ __forceinline__ float dot_q4_chunk(const uint4 w, const XChunk& xc) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = ((ws[j] >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+            const h2 qh = __builtin_bit_cast(h2, q) - k1024;
+            acc = __builtin_amdgcn_fdot2(qh, xc.p[4 * j + i], acc, false);
+        }
+    }
+    return acc;
+}
+
+// Σ_i q_i * x_i over the 16 int8 codes of one 16-byte chunk, fp32 operands.
 __device__ __forceinline__ float dot16_q8(const uint4 w, const float* x) {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
     float d = 0.0f;
@@ -77,8 +116,18 @@ __device__ __forceinline__ float dot16_q8(const uint4 w, const float* x) {
     return d;
 }
 
-__device__ __forceinline__ uint4 ldg16(const uint8_t* p) {
-    return *reinterpret_cast<const uint4*>(p);
+// Copies n fp16 values to LDS (16-byte transfers when x is 16-byte aligned),
+// then synchronises the block.
+__device__ __forceinline__ void stage_xh(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
+                                         uint32_t n) {
+    if ((((uintptr_t)x) & 15u) == 0 && (n & 7u) == 0) {
+        const uint4* src = reinterpret_cast<const uint4*>(x);
+        uint4* dst = reinterpret_cast<uint4*>(lds);
+        for (uint32_t i = threadIdx.x; i < (n >> 3); i += blockDim.x) dst[i] = src[i];
+    } else {
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lds[i] = x[i];
+    }
+    __syncthreads();
 }
 
 }  // namespace tfq

@@ -10,47 +10,49 @@
 
 using namespace tfq;
 
+// Rows each segment keeps in flight (loads issued before the previous rows are reduced).
+constexpr int kRowsInFlight = 2;
+
 #define TFQ_Q4_GEMV(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_q4_gemv_s##SEG##_p##P(                 \
         Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
-        q4_gemv_multi<SEG, P>(mats, x, n);                                                        \
+        q4_gemv_multi<SEG, P, kRowsInFlight>(mats, x, n);                                         \
     }
 
 #define TFQ_Q8_GEMV(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_q8_gemv_s##SEG##_p##P(                 \
         const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* x, uint16_t* y,  \
         uint32_t m, uint32_t n) {                                                                 \
-        q8_gemv<SEG, P>(W, S, B, x, y, m, n);                                                     \
+        q8_gemv<SEG, P, kRowsInFlight>(W, S, B, x, y, m, n);                                      \
     }
 
 #define TFQ_ROUTER(SEG, P)                                                                       \
-    extern "C" __global__ __launch_bounds__(256) void tfq_router_topk_s##SEG##_p##P(             \
+    extern "C" __global__ __launch_bounds__(256) void tfq_router_logits_s##SEG##_p##P(           \
         const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* h,               \
-        const uint16_t* eff, const uint16_t* gain, uint32_t* out_idx, uint16_t* out_w,           \
-        float* out_wf, float* out_logits, uint32_t E, uint32_t d, uint32_t k, uint8_t* ws) {     \
-        router_topk<SEG, P>(W, S, B, h, eff, gain, out_idx, out_w, out_wf, out_logits, E, d, k, \
-                            ws);                                                                  \
+        const uint16_t* eff, float* logits, uint32_t E, uint32_t d) {                            \
+        router_logits<SEG, P>(W, S, B, h, eff, logits, E, d);                                     \
     }
 
 #define TFQ_PHASE1(SEG, P)                                                                       \
     extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase1_s##SEG##_p##P(              \
         ExpertPool pool, const uint32_t* indices, const uint32_t* active_slots,                  \
-        uint32_t n_active, uint32_t top_k, const uint16_t* x, float* acts, uint32_t D,           \
+        uint32_t n_active, uint32_t top_k, const uint16_t* x, uint16_t* acts, uint32_t D,        \
         uint32_t F) {                                                                             \
-        moe_phase1<SEG, P>(pool, indices, active_slots, n_active, top_k, x, acts, D, F);         \
+        moe_phase1<SEG, P, kRowsInFlight>(pool, indices, active_slots, n_active, top_k, x, acts, \
+                                          D, F);                                                  \
     }
 
 #define TFQ_PHASE2(P)                                                                            \
     extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase2_p##P(                       \
-        ExpertPool pool, const uint32_t* indices, const float* acts, const uint16_t* rw,         \
+        ExpertPool pool, const uint32_t* indices, const uint16_t* acts, const uint16_t* rw,      \
         const uint16_t* residual, uint16_t* y, uint32_t D, uint32_t F, uint32_t top_k) {         \
-        moe_phase2<P>(pool, indices, acts, rw, residual, y, D, F, top_k);                         \
+        moe_phase2<P, kRowsInFlight>(pool, indices, acts, rw, residual, y, D, F, top_k);          \
     }
 
 #define TFQ_GATE_UP(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_gate_up_act_s##SEG##_p##P(             \
         Q4Mat gate, Q4Mat up, const uint16_t* x, uint16_t* act, uint32_t D, uint32_t F) {        \
-        q4_gate_up_act<SEG, P>(gate.w, gate.s, gate.b, up.w, up.s, up.b, x, act, D, F);          \
+        q4_gate_up_act<SEG, P, kRowsInFlight>(gate, up, x, act, D, F);                            \
     }
 
 // int4: n/32 chunks per row.
@@ -67,6 +69,15 @@ TFQ_PHASE2(1)
 TFQ_PHASE2(2)
 TFQ_PHASE2(3)
 TFQ_PHASE2(4)
+
+extern "C" __global__ __launch_bounds__(64) void tfq_router_select(const float* logits,
+                                                                    const uint16_t* gain,
+                                                                    uint32_t* out_idx,
+                                                                    uint16_t* out_w,
+                                                                    float* out_wf, uint32_t E,
+                                                                    uint32_t k) {
+    router_select(logits, gain, out_idx, out_w, out_wf, E, k);
+}
 
 extern "C" __global__ __launch_bounds__(256) void tfq_convert_bf16_f16(const uint16_t* src,
                                                                          uint16_t* dst, uint64_t n,

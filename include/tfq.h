@@ -94,11 +94,12 @@ int tfq_gemv_q8g64(tfq_ctx *ctx, void *stream, const uint8_t *weights, const uin
                    const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m,
                    uint32_t n);
 
-/* Bytes of workspace tfq_router_topk needs. The workspace must be zeroed once
- * (hipMemset) before its first use; each call leaves it ready for the next. */
+/* Bytes of workspace tfq_router_topk needs (holds the fp32 logits when
+ * out_logits_f32 is NULL). */
 #define TFQ_ROUTER_WORKSPACE_BYTES 4096u
 
-/* Router GEMV + top-k + softmax over the k + per-expert gain, in one launch.
+/* Router GEMV, then top-k + softmax over the k + per-expert gain (two
+ * launches on `stream`: a many-block int8 GEMV and a one-wavefront select).
  * logits[e] = Σ_g s·Σ q·(h⊙eff) + b·Σ(h⊙eff) (fp32); indices sorted by
  * logit descending, ties to the lower expert index; weights[i] =
  * fp16(softmax_i × per_expert_scale[idx_i]). effective_scale /
@@ -136,18 +137,19 @@ typedef struct {
     tfq_expert_offsets offsets;
 } tfq_expert_pool;
 
-/* Phase 1: acts[slot][f] = gelu_tanh(gate_e[f]·x) * (up_e[f]·x), e =
- * indices[slot], fp32 accumulate; acts is fp32 [top_k][f].
+/* Phase 1: acts[slot][f] = fp16(gelu_tanh(gate_e[f]·x) * (up_e[f]·x)), e =
+ * indices[slot], fp32 accumulate; acts is fp16 [top_k][f] (moe.metal:368).
+ * An out-of-range expert index yields NaN activations instead of a fault.
  * Replaces MoE.encodeRoutedPersistentPhase1U16Load (MoE.swift:234-266).
  * Contract: d % 64 == 0, d <= 8192, f % 64 == 0, 1 <= top_k <= 8. */
 int tfq_moe_phase1(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
-                   const uint32_t *indices, const uint16_t *x, float *acts, uint32_t d,
+                   const uint32_t *indices, const uint16_t *x, uint16_t *acts, uint32_t d,
                    uint32_t f, uint32_t top_k);
 
 /* Phase 1 over a subset of slots (active_slots: device uint32 [active_count]).
  * Replaces MoE.encodeRoutedPersistentPhase1SubsetU16Load (MoE.swift:268-310). */
 int tfq_moe_phase1_subset(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
-                          const uint32_t *indices, const uint16_t *x, float *acts,
+                          const uint32_t *indices, const uint16_t *x, uint16_t *acts,
                           const uint32_t *active_slots, uint32_t active_count, uint32_t d,
                           uint32_t f, uint32_t top_k);
 
@@ -157,15 +159,15 @@ int tfq_moe_phase1_subset(tfq_ctx *ctx, void *stream, const tfq_expert_pool *poo
  * (MoE.swift:312-362). Contract: f % 64 == 0, f <= 1024, top_k == 8 or
  * top_k <= 8. */
 int tfq_moe_phase2(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
-                   const uint32_t *indices, const float *acts, const uint16_t *routing_weights,
+                   const uint32_t *indices, const uint16_t *acts, const uint16_t *routing_weights,
                    const uint16_t *residual, uint16_t *y, uint32_t d, uint32_t f,
                    uint32_t top_k);
 
-/* Phase 1 then phase 2 (acts_scratch: fp32 [top_k][f] device buffer). */
+/* Phase 1 then phase 2 (acts_scratch: fp16 [top_k][f] device buffer). */
 int tfq_moe_decode(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
                    const uint32_t *indices, const uint16_t *routing_weights, const uint16_t *x,
                    const uint16_t *residual, uint16_t *y, uint32_t d, uint32_t f,
-                   uint32_t top_k, float *acts_scratch);
+                   uint32_t top_k, uint16_t *acts_scratch);
 
 /* Shared expert, int4 form: act[i] = fp16(gelu_tanh(gate[i]·x) * (up[i]·x))
  * with gate/up kept in fp32 (one fused launch), then y = fp16(down·act).
