@@ -74,5 +74,6 @@ def test_code_object_is_gfx950_and_holds_all_kernels():
     src = open(os.path.join(ROOT, "edgeexpert_amd", "csrc", "host", "tfq.cpp")).read()
     assert "kernel_names" in src
     for fam in ("tfq_q4_gemv_s64_p2", "tfq_moe_phase1_s64_p2", "tfq_moe_phase2_p3",
-                "tfq_router_topk_s64_p3", "tfq_gate_up_act_s64_p2", "tfq_convert_bf16_f16"):
+                "tfq_router_logits_s64_p3", "tfq_router_select", "tfq_gate_up_act_s64_p2",
+                "tfq_convert_bf16_f16"):
         assert fam in out
