@@ -55,6 +55,8 @@ def main():
     ap.add_argument("--steps", type=int, default=4096)
     ap.add_argument("--warmup", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--launch", choices=("graph", "stream"), default="graph",
+                    help="replay the 64-token step from a HIP graph, or issue it from the host")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
@@ -83,27 +85,31 @@ def main():
     ybuf = DeviceBuffer(TOKENS * D * 2)
     ws = DeviceBuffer(ROUTER_WORKSPACE_BYTES)
     ws.fill(0)
-    idx = DeviceBuffer(K * 4)
-    w16 = DeviceBuffer(K * 2)
-    acts = DeviceBuffer(K * F * 2)
-    moe = ops.MoE(ctx)
+
+    router = ops.Router(rW, rS, rB, E)
+    idx_all = DeviceBuffer(TOKENS * K * 4)
+    w16_all = DeviceBuffer(TOKENS * K * 2)
+    acts_all = DeviceBuffer(TOKENS * K * F * 2)
 
     def token(t):
-        h = hbuf.ptr(t * D * 2)
-        moe.encode_router_gemma4(stream, rW, rS, rB, h, None, None, idx, w16, E, D, K, ws)
-        moe.encode_routed_phase1(stream, pool, idx, h, acts, D, F, K)
-        moe.encode_routed_phase2(stream, pool, idx, acts, w16, None, ybuf.ptr(t * D * 2), D, F, K)
+        ops.moe_decode_token(ctx, stream, router, pool, hbuf.ptr(t * D * 2), None,
+                             ybuf.ptr(t * D * 2), D, F, K, idx_all.ptr(t * K * 4),
+                             w16_all.ptr(t * K * 2), acts_all.ptr(t * K * F * 2), ws)
 
     def all_tokens():
         for t in range(TOKENS):
             token(t)
 
-    graph = Graph(stream, all_tokens)
     reps_w = max(1, args.warmup // TOKENS)
     reps = max(1, args.steps // TOKENS)
     steps = reps * TOKENS
+    if args.launch == "graph":
+        graph = Graph(stream, all_tokens)
+        run = lambda: graph.launch(stream)
+    else:
+        run = all_tokens
     for _ in range(reps_w):
-        graph.launch(stream)
+        run()
     stream.sync()
 
     # -------------------------------------------------------- timed region ----
@@ -112,36 +118,50 @@ def main():
     wall0 = time.perf_counter()
     e0.record(stream)
     for _ in range(reps):
-        graph.launch(stream)
+        run()
     e1.record(stream)
     stream.sync()
     synchronize()
     wall = time.perf_counter() - wall0
     gpu_ms = e0.elapsed_ms(e1)
     us_per_token = gpu_ms * 1e3 / steps
-    log(f"MoE decode: {steps} tokens in {gpu_ms:.2f} ms (events), wall {wall * 1e3:.2f} ms -> "
-        f"{us_per_token:.2f} us/token")
+    log(f"MoE decode ({args.launch}): {steps} tokens in {gpu_ms:.2f} ms (events), wall "
+        f"{wall * 1e3:.2f} ms -> {us_per_token:.2f} us/token")
 
-    # -------------------------------- per-kernel durations (HIP events) ----
+    # ------------------------------ per-kernel durations (HIP events) ----
+    # Each kernel of the block, launched back to back for the 64 tokens (whose
+    # routing is already in idx_all / w16_all) between two events on `stream`;
+    # the average includes the launch gap between consecutive kernels.
     nb = moe_bytes()
-    ev = [Event() for _ in range(2 * TOKENS)]
-    kernel_ms = {"router": [], "phase1": [], "phase2": []}
-    for rep in range(4):
-        for t in range(TOKENS):
-            h = hbuf.ptr(t * D * 2)
-            a, b = ev[2 * t], ev[2 * t + 1]
-            # router (untimed here) so that phase 1/2 see this token's experts
-            moe.encode_router_gemma4(stream, rW, rS, rB, h, None, None, idx, w16, E, D, K, ws)
+    moe = ops.MoE(ctx)
+
+    def batch_avg_us(launch_one, count, reps_=5):
+        best = []
+        for _ in range(reps_):
+            a, b = Event(), Event()
             a.record(stream)
-            moe.encode_routed_phase1(stream, pool, idx, h, acts, D, F, K)
+            for t in range(count):
+                launch_one(t)
             b.record(stream)
-            moe.encode_routed_phase2(stream, pool, idx, acts, w16, None, ybuf.ptr(t * D * 2), D, F, K)
-        stream.sync()
-        for t in range(TOKENS):
-            kernel_ms["phase1"].append(ev[2 * t].elapsed_ms(ev[2 * t + 1]))
-    p1_us = float(np.mean(kernel_ms["phase1"]) * 1e3)
+            stream.sync()
+            best.append(a.elapsed_ms(b) * 1e3 / count)
+        return float(np.median(best))
+
+    k_us = {
+        "router": batch_avg_us(lambda t: moe.encode_router_gemma4(
+            stream, rW, rS, rB, hbuf.ptr(t * D * 2), None, None, idx_all.ptr(t * K * 4),
+            w16_all.ptr(t * K * 2), E, D, K, ws), TOKENS),
+        "phase1": batch_avg_us(lambda t: moe.encode_routed_phase1(
+            stream, pool, idx_all.ptr(t * K * 4), hbuf.ptr(t * D * 2), acts_all.ptr(t * K * F * 2),
+            D, F, K), TOKENS),
+        "phase2": batch_avg_us(lambda t: moe.encode_routed_phase2(
+            stream, pool, idx_all.ptr(t * K * 4), acts_all.ptr(t * K * F * 2), w16_all.ptr(t * K * 2),
+            None, ybuf.ptr(t * D * 2), D, F, K), TOKENS),
+    }
+    p1_us = k_us["phase1"]
     p1_gbs = nb["phase1"] / (p1_us * 1e-6) / 1e9
-    log(f"phase1 avg {p1_us:.2f} us -> {p1_gbs:.0f} GB/s ({nb['phase1']} B/launch)")
+    log("kernel avg (back-to-back): " + ", ".join(f"{k} {v:.2f} us" for k, v in k_us.items())
+        + f"; phase1 {p1_gbs:.0f} GB/s ({nb['phase1']} B/launch)")
 
     # ------------------------------------------------ GEMV config 0 (extra) ----
     gemv = ops.DequantInt4GEMV(ctx)
@@ -157,27 +177,18 @@ def main():
         big.upload(S0, base + wsz)
         big.upload(B0, base + wsz + ssz)
     gemv_bytes = wsz + 2 * ssz + 2 * 2816 * 2
-    evg = [Event() for _ in range(2 * n_copies)]
 
-    def time_gemv(copy_of):
-        durs = []
-        for rep in range(3):
-            for i in range(n_copies):
-                base = copy_of(i) * (wsz + 2 * ssz)
-                evg[2 * i].record(stream)
-                gemv.encode(stream, big, big, big, x0, y0, 2816, 2816, weights_offset=base,
-                            scales_offset=base + wsz, biases_offset=base + wsz + ssz)
-                evg[2 * i + 1].record(stream)
-            stream.sync()
-            if rep:
-                durs += [evg[2 * i].elapsed_ms(evg[2 * i + 1]) for i in range(n_copies)]
-        return float(np.mean(durs) * 1e3)
+    def gemv_launch(copy):
+        base = copy * (wsz + 2 * ssz)
+        gemv.encode(stream, big, big, big, x0, y0, 2816, 2816, weights_offset=base,
+                    scales_offset=base + wsz, biases_offset=base + wsz + ssz)
 
-    cold_us = time_gemv(lambda i: i)
-    warm_us = time_gemv(lambda i: 0)
+    cold_us = batch_avg_us(gemv_launch, n_copies)
+    warm_us = batch_avg_us(lambda i: gemv_launch(0), n_copies)
     cold_gbs = gemv_bytes / (cold_us * 1e-6) / 1e9
     warm_gbs = gemv_bytes / (warm_us * 1e-6) / 1e9
-    log(f"GEMV C0: cold {cold_us:.2f} us ({cold_gbs:.0f} GB/s), warm {warm_us:.2f} us ({warm_gbs:.0f} GB/s)")
+    log(f"GEMV C0 (back-to-back): cold {cold_us:.2f} us ({cold_gbs:.0f} GB/s), warm {warm_us:.2f} us "
+        f"({warm_gbs:.0f} GB/s)")
 
     # ------------------------------------------------------ CPU baseline ----
     cpu = None
@@ -210,11 +221,13 @@ def main():
         "dtype": "int4/int8 weights x fp16 activations, fp32 accumulate",
         "data": "synthetic (seeded SplitMix64, BASELINE distributions)",
         "config": {"workload": "config1_moe_decode", "experts": E, "top_k": K, "d": D, "f": F,
-                   "tokens_rotated": TOKENS, "graph": "64 tokens x 3 kernels"},
+                   "tokens_rotated": TOKENS, "launch": args.launch,
+                   "kernels_per_token": "router_logits, router_select, moe_phase1, moe_phase2"},
         "roofline": {"kernel": "tfq_moe_phase1 (gate/up of 8 experts)", "bound": "hbm",
                      "achieved": round(p1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(p1_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes": nb["phase1"], "avg_launch_us": round(p1_us, 3)},
+                     "algorithmic_bytes": nb["phase1"], "avg_launch_us": round(p1_us, 3),
+                     "kernel_avg_us": {k: round(v, 3) for k, v in k_us.items()}},
         "cpu_baseline": cpu,
         "token_bytes": nb["total"],
         "token_gbs": round(nb["total"] / (us_per_token * 1e-6) / 1e9, 1),

@@ -48,6 +48,12 @@ class ExpertPoolDesc(C.Structure):
                 ("offsets", ExpertOffsets)]
 
 
+class RouterDesc(C.Structure):
+    _fields_ = [("weights", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("effective_scale", C.c_void_p), ("per_expert_scale", C.c_void_p),
+                ("num_experts", C.c_uint32)]
+
+
 _P = C.c_void_p
 _U32 = C.c_uint32
 _I = C.c_int
@@ -69,6 +75,8 @@ SIGNATURES = {
                               _U32],
     "tfq_moe_phase2": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _P, _P, _U32, _U32, _U32],
     "tfq_moe_decode": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
+    "tfq_moe_decode_token": [_P, _P, C.POINTER(RouterDesc), C.POINTER(ExpertPoolDesc), _P, _P, _P,
+                             _U32, _U32, _U32, _P, _P, _P, _P],
     "tfq_shared_expert_q4": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
                              _P, _P, _U32, _U32, _P],
     "tfq_convert_bf16_to_f16": [_P, _P, _P, _P, C.c_uint64, _P],

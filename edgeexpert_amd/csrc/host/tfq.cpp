@@ -202,6 +202,27 @@ int tfq_moe_decode(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, cons
                                    y, d, f, top_k);
 }
 
+int tfq_moe_decode_token(tfq_ctx* ctx, void* stream, const tfq_router* router,
+                         const tfq_expert_pool* pool, const uint16_t* x, const uint16_t* residual,
+                         uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k, uint32_t* out_indices,
+                         uint16_t* out_weights, uint16_t* acts_scratch, void* workspace) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!router || !pool) return fail(TFQ_E_INVAL, "null router or pool");
+    if (router->num_experts != pool->num_experts)
+        return fail(TFQ_E_INVAL, "router has %u experts, pool %u", router->num_experts,
+                    pool->num_experts);
+    int rc = ctx->moe->encode_router_gemma4(stream, router->weights, router->scales, router->biases,
+                                            x, router->effective_scale, router->per_expert_scale,
+                                            out_indices, out_weights, nullptr, nullptr,
+                                            router->num_experts, d, top_k, workspace);
+    if (rc) return rc;
+    rc = ctx->moe->encode_phase1(stream, *pool, out_indices, x, acts_scratch, nullptr, top_k, d, f,
+                                 top_k);
+    if (rc) return rc;
+    return ctx->moe->encode_phase2(stream, *pool, out_indices, acts_scratch, out_weights, residual,
+                                   y, d, f, top_k);
+}
+
 int tfq_shared_expert_q4(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* gate,
                          const tfq_q4_matrix* up, const tfq_q4_matrix* down, const uint16_t* x,
                          uint16_t* y, uint32_t d, uint32_t f, uint16_t* act_scratch) {

@@ -11,7 +11,8 @@ from __future__ import annotations
 import ctypes as C
 from dataclasses import dataclass
 
-from ._lib import (CODE_OBJECT_PATH, ExpertOffsets, ExpertPoolDesc, Q4Matrix, check, lib)
+from ._lib import (CODE_OBJECT_PATH, ExpertOffsets, ExpertPoolDesc, Q4Matrix, RouterDesc, check,
+                   lib)
 from .runtime import DeviceBuffer, Stream
 
 
@@ -166,6 +167,31 @@ class MoE:
         check(lib().tfq_moe_decode(self.ctx.handle, _s(stream), C.byref(p), _addr(indices),
                                    _addr(routing_weights), _addr(x), _addr(residual), _addr(y), d, f,
                                    top_k, _addr(acts)), "tfq_moe_decode")
+
+
+@dataclass
+class Router:
+    """int8 router of one layer (weights [num_experts][d]); eff / gain may be None."""
+    weights: object
+    scales: object
+    biases: object
+    num_experts: int
+    effective_scale: object = None
+    per_expert_scale: object = None
+
+    def desc(self) -> RouterDesc:
+        return RouterDesc(_addr(self.weights), _addr(self.scales), _addr(self.biases),
+                          _addr(self.effective_scale), _addr(self.per_expert_scale), self.num_experts)
+
+
+def moe_decode_token(context: Context, stream, router: Router, pool: ExpertPool, x, residual, y, d,
+                     f, top_k, out_indices, out_weights, acts, workspace):
+    """Router -> top-k -> phase 1 -> phase 2 for one token, indices kept on the device."""
+    r, p = router.desc(), pool.desc()
+    check(lib().tfq_moe_decode_token(context.handle, _s(stream), C.byref(r), C.byref(p), _addr(x),
+                                     _addr(residual), _addr(y), d, f, top_k, _addr(out_indices),
+                                     _addr(out_weights), _addr(acts), _addr(workspace)),
+          "tfq_moe_decode_token")
 
 
 class SharedExpertInt4:

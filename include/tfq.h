@@ -169,6 +169,31 @@ int tfq_moe_decode(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
                    const uint16_t *residual, uint16_t *y, uint32_t d, uint32_t f,
                    uint32_t top_k, uint16_t *acts_scratch);
 
+/* int8 router of one MoE layer (weights [num_experts][d], fp16 scale/bias per
+ * 64). effective_scale [d] / per_expert_scale [num_experts] may be NULL. */
+typedef struct {
+    const uint8_t *weights;
+    const uint16_t *scales;
+    const uint16_t *biases;
+    const uint16_t *effective_scale;
+    const uint16_t *per_expert_scale;
+    uint32_t num_experts;
+} tfq_router;
+
+/* The whole routed decode block of one token, all on the device: router
+ * GEMV + top-k + softmax (tfq_router_topk), phase 1, phase 2. Replaces the
+ * decode sequence encodeRouterGemma4 -> CPU readback of the indices -> expert
+ * fetch -> Phase1U16Load -> Phase2Reduce (S/Runtime/Inference/
+ * RealForwardRunner.swift:2390-2401, 2491-2521, 2822-2864); the indices never
+ * leave HBM. out_indices [top_k] / out_weights fp16 [top_k] receive the
+ * routing; acts_scratch is fp16 [top_k][f]; workspace is
+ * TFQ_ROUTER_WORKSPACE_BYTES. Contracts as for the individual calls. */
+int tfq_moe_decode_token(tfq_ctx *ctx, void *stream, const tfq_router *router,
+                         const tfq_expert_pool *pool, const uint16_t *x,
+                         const uint16_t *residual, uint16_t *y, uint32_t d, uint32_t f,
+                         uint32_t top_k, uint32_t *out_indices, uint16_t *out_weights,
+                         uint16_t *acts_scratch, void *workspace);
+
 /* Shared expert, int4 form: act[i] = fp16(gelu_tanh(gate[i]·x) * (up[i]·x))
  * with gate/up kept in fp32 (one fused launch), then y = fp16(down·act).
  * gate/up are [f][d], down is [d][f]; act_scratch: fp16 [f].
