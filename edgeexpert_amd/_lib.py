@@ -80,6 +80,7 @@ SIGNATURES = {
     "tfq_shared_expert_q4": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
                              _P, _P, _U32, _U32, _P],
     "tfq_convert_bf16_to_f16": [_P, _P, _P, _P, C.c_uint64, _P],
+    "tfq_read_ceiling": [_P, _P, _P, C.c_uint64, _P, _U32],
     "tfq_rt_device_count": [C.POINTER(_I)],
     "tfq_rt_set_device": [_I],
     "tfq_rt_device_info": [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t],

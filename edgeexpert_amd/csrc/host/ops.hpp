@@ -147,7 +147,7 @@ public:
         if (rc) return rc;
         void* sargs[] = {&logits, &per_expert_scale, &out_indices, &out_weights, &out_weights_f32,
                          &num_experts, &top_k};
-        return launch(m_.get("tfq_router_select"), 1, 64, 0, stream, sargs, "tfq_router_select");
+        return launch(m_.get("tfq_router_select"), 1, 256, 0, stream, sargs, "tfq_router_select");
     }
 
     // encodeRoutedPersistentPhase1U16Load / ...SubsetU16Load (MoE.swift:234-310).

@@ -37,6 +37,7 @@ static std::vector<std::string> kernel_names() {
     }
     for (int p = 1; p <= 4; ++p) names.push_back("tfq_moe_phase2_p" + std::to_string(p));
     names.push_back("tfq_router_select");
+    names.push_back("tfq_read_ceiling");
     names.push_back("tfq_convert_bf16_f16");
     return names;
 }
@@ -242,6 +243,21 @@ int tfq_convert_bf16_to_f16(tfq_ctx* ctx, void* stream, const uint16_t* src, uin
     void* args[] = {&src, &dst, &count, &inexact_count_dev};
     return launch(ctx->module.get("tfq_convert_bf16_f16"), grid, 256, 0, stream, args,
                   "tfq_convert_bf16_f16");
+}
+
+int tfq_read_ceiling(tfq_ctx* ctx, void* stream, const void* src, uint64_t bytes, uint32_t* sink,
+                     uint32_t sink_blocks) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!src || !sink || sink_blocks == 0) return fail(TFQ_E_INVAL, "null pointer or empty sink");
+    if (!aligned(src, 16) || bytes % 16) return fail(TFQ_E_INVAL, "src and bytes must be 16-byte aligned");
+    const uint64_t n16 = bytes / 16;
+    uint64_t blocks = (n16 + 256 * 4 - 1) / (256 * 4);     // one pass: 4 loads per lane
+    if (blocks > sink_blocks) blocks = sink_blocks;
+    if (blocks < 1) blocks = 1;
+    uint32_t grid = (uint32_t)blocks;
+    void* args[] = {&src, (void*)&n16, &sink};
+    return launch(ctx->module.get("tfq_read_ceiling"), grid, 256, 0, stream, args,
+                  "tfq_read_ceiling");
 }
 
 // ------------------------------------------------------------ runtime ----

@@ -253,50 +253,50 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
         [&](uint32_t row, float v) { logits[row] = v; });
 }
 
-// Top-k of E logits by (value desc, index asc) in one wavefront.
-__device__ __forceinline__ void wave_topk(const float* logits, uint32_t E, uint32_t k,
-                                          uint32_t* sel_idx, float* sel_val) {
-    const uint32_t lane = threadIdx.x & 63u;
-    constexpr uint32_t NONE = 0xFFFFFFFFu;
-    float v[4];
-    uint32_t id[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t e = lane + 64u * j;
-        v[j] = e < E ? logits[e] : -INFINITY;
-        id[j] = e < E ? e : NONE;
-    }
-    for (uint32_t r = 0; r < k; ++r) {
-        float bv = -INFINITY;
-        uint32_t bi = NONE;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (id[j] != NONE && (bi == NONE || v[j] > bv || (v[j] == bv && id[j] < bi))) {
-                bv = v[j];
-                bi = id[j];
-            }
+// Top-k of E <= 256 logits by (value desc, index asc), in parallel: thread t
+// owns logit t and counts the logits ranked above it (a broadcast scan of the
+// LDS copy); ranks are unique, so the k threads with rank < k each write
+// their slot. `stage` holds the logits; `sel_idx`/`sel_val` receive the k
+// winners in rank order. Ends with a block barrier.
+__device__ __forceinline__ void block_topk(const float* stage, uint32_t E, uint32_t k,
+                                           uint32_t* sel_idx, float* sel_val) {
+    for (uint32_t t = threadIdx.x; t < E; t += blockDim.x) {
+        const float v = stage[t];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < E; ++j) {
+            const float o = stage[j];
+            rank += (o > v || (o == v && j < t)) ? 1u : 0u;
         }
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ov = __shfl_xor(bv, m, kWave);
-            const uint32_t oi = (uint32_t)__shfl_xor((int)bi, m, kWave);
-            if (oi != NONE && (bi == NONE || ov > bv || (ov == bv && oi < bi))) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (id[j] == bi) id[j] = NONE;
-        if (lane == 0) {
-            sel_idx[r] = bi;
-            sel_val[r] = bv;
+        if (rank < k) {
+            sel_idx[rank] = t;
+            sel_val[rank] = v;
         }
     }
+    __syncthreads();
 }
 
-// One wavefront (block of 64): top-k, softmax over the k, × per-expert gain
-// (S/Metal/MoE/moe.metal:135-185; ties to the lower index as at :157).
+// Softmax over the k selected logits times the per-expert gain
+// (S/Metal/MoE/moe.metal:169-184): weights[r] = exp(v_r - v_0) / Σ exp × gain.
+// Exponentials in parallel, their sum in rank order by one thread.
+__device__ __forceinline__ void block_softmax_gain(const uint32_t* sel_idx, const float* sel_val,
+                                                   uint32_t k, const uint16_t* __restrict__ gain,
+                                                   float* ex, float* sel_w) {
+    const float vmax = sel_val[0];
+    for (uint32_t r = threadIdx.x; r < k; r += blockDim.x) ex[r] = expf(sel_val[r] - vmax);
+    __syncthreads();
+    __shared__ float total;
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        for (uint32_t r = 0; r < k; ++r) sum += ex[r];
+        total = sum;
+    }
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < k; r += blockDim.x)
+        sel_w[r] = ex[r] / total * (gain ? h2f(gain[sel_idx[r]]) : 1.0f);
+    __syncthreads();
+}
+
+// Selection kernel body: logits (global) -> indices, fp16 weights, fp32 weights.
 __device__ __forceinline__ void router_select(const float* __restrict__ logits,
                                               const uint16_t* __restrict__ gain,
                                               uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w,
@@ -304,22 +304,47 @@ __device__ __forceinline__ void router_select(const float* __restrict__ logits,
     __shared__ float stage[kRouterMaxExperts];
     __shared__ uint32_t sel_idx[kRouterMaxTopK];
     __shared__ float sel_val[kRouterMaxTopK];
+    __shared__ float ex[kRouterMaxTopK];
+    __shared__ float sel_w[kRouterMaxTopK];
     for (uint32_t e = threadIdx.x; e < E; e += blockDim.x) stage[e] = logits[e];
     __syncthreads();
-    wave_topk(stage, E, k, sel_idx, sel_val);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const float vmax = sel_val[0];
-        float sum = 0.0f;
-        for (uint32_t r = 0; r < k; ++r) sum += expf(sel_val[r] - vmax);
-        for (uint32_t r = 0; r < k; ++r) {
-            const uint32_t e = sel_idx[r];
-            const float wgt = expf(sel_val[r] - vmax) / sum * (gain ? h2f(gain[e]) : 1.0f);
-            out_idx[r] = e;
-            out_w[r] = f2h(wgt);
-            if (out_wf) out_wf[r] = wgt;
-        }
+    block_topk(stage, E, k, sel_idx, sel_val);
+    block_softmax_gain(sel_idx, sel_val, k, gain, ex, sel_w);
+    for (uint32_t r = threadIdx.x; r < k; r += blockDim.x) {
+        out_idx[r] = sel_idx[r];
+        out_w[r] = f2h(sel_w[r]);
+        if (out_wf) out_wf[r] = sel_w[r];
     }
+}
+
+// ------------------------------------------------------------ read probe ----
+
+// Pure HBM read ceiling (the role of bw_ceiling_read, S/Metal/Quant/
+// dequant_int4.metal:487-502): every lane reads U 16-byte chunks with one
+// coalesced 128-bit load each, all issued before any is consumed; the xor of
+// everything read goes to sink[block] so nothing is optimised away.
+template <int U>
+__device__ __forceinline__ void read_ceiling(const uint4* __restrict__ src, uint64_t n16,
+                                             uint32_t* __restrict__ sink) {
+    const uint64_t nthreads = (uint64_t)gridDim.x * blockDim.x;
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i < n16; i += nthreads * U) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t j = i + (uint64_t)u * nthreads;
+            v[u] = j < n16 ? src[j] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    __shared__ uint32_t red;
+    if (threadIdx.x == 0) red = 0;
+    __syncthreads();
+    atomicXor(&red, acc);
+    __syncthreads();
+    if (threadIdx.x == 0) sink[blockIdx.x] = red;
 }
 
 // ------------------------------------------------------------- convert ----

@@ -70,13 +70,18 @@ TFQ_PHASE2(2)
 TFQ_PHASE2(3)
 TFQ_PHASE2(4)
 
-extern "C" __global__ __launch_bounds__(64) void tfq_router_select(const float* logits,
+extern "C" __global__ __launch_bounds__(256) void tfq_router_select(const float* logits,
                                                                     const uint16_t* gain,
                                                                     uint32_t* out_idx,
                                                                     uint16_t* out_w,
                                                                     float* out_wf, uint32_t E,
                                                                     uint32_t k) {
     router_select(logits, gain, out_idx, out_w, out_wf, E, k);
+}
+
+extern "C" __global__ __launch_bounds__(256) void tfq_read_ceiling(const uint4* src, uint64_t n16,
+                                                                     uint32_t* sink) {
+    read_ceiling<4>(src, n16, sink);
 }
 
 extern "C" __global__ __launch_bounds__(256) void tfq_convert_bf16_f16(const uint16_t* src,

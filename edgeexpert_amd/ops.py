@@ -212,3 +212,9 @@ def convert_bf16_to_f16(context: Context, stream, src, dst, count, inexact_count
     """Exact BF16 -> fp16 conversion of scale/bias words at load time."""
     check(lib().tfq_convert_bf16_to_f16(context.handle, _s(stream), _addr(src), _addr(dst), count,
                                         _addr(inexact_counter)), "tfq_convert_bf16_to_f16")
+
+
+def read_ceiling(context: Context, stream, src, nbytes: int, sink, sink_blocks: int, src_offset=0):
+    """HBM read-ceiling probe (one pass over nbytes with 128-bit loads)."""
+    check(lib().tfq_read_ceiling(context.handle, _s(stream), _addr(src, src_offset), nbytes,
+                                 _addr(sink), sink_blocks), "tfq_read_ceiling")

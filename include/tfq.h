@@ -214,6 +214,16 @@ int tfq_shared_expert_q4(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *gate,
 int tfq_convert_bf16_to_f16(tfq_ctx *ctx, void *stream, const uint16_t *src, uint16_t *dst,
                             uint64_t count, uint32_t *inexact_count_dev);
 
+/* ------------------------------------------------------------ measurement -- */
+
+/* Pure read of `bytes` (16-byte aligned) with 128-bit coalesced loads, one
+ * pass, xor-reduced into sink[0..blocks) (device uint32, sink_blocks
+ * entries; the launch uses at most that many blocks). The HBM read ceiling
+ * the GEMVs are compared with; replaces bw_ceiling_read
+ * (S/Metal/Quant/dequant_int4.metal:487-502). */
+int tfq_read_ceiling(tfq_ctx *ctx, void *stream, const void *src, uint64_t bytes, uint32_t *sink,
+                     uint32_t sink_blocks);
+
 #ifdef __cplusplus
 }
 #endif
