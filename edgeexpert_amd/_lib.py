@@ -19,6 +19,8 @@ TFQ_E_UNSUPPORTED = 2
 TFQ_E_HIP = 3
 TFQ_E_NOT_LOADED = 4
 ROUTER_WORKSPACE_BYTES = 4096
+DTYPE_F16 = 0
+DTYPE_BF16 = 1
 
 
 class TfqNotBuilt(RuntimeError):
@@ -81,6 +83,7 @@ SIGNATURES = {
                              _P, _P, _U32, _U32, _P],
     "tfq_convert_bf16_to_f16": [_P, _P, _P, _P, C.c_uint64, _P],
     "tfq_read_ceiling": [_P, _P, _P, C.c_uint64, _P, _U32],
+    "tfq_gemm_q4g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _I],
     "tfq_rt_device_count": [C.POINTER(_I)],
     "tfq_rt_set_device": [_I],
     "tfq_rt_device_info": [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t],

@@ -260,4 +260,37 @@ private:
     DequantInt4GEMV gemv_;
 };
 
+// S/Kernels/Prefill/Primitives/PrefillPrimitives.swift:73-123 (PrefillInt4QMM) and
+// S/Kernels/TensorCore/MPPPrefillInt4QMM.swift:4-83: one MFMA kernel serves both.
+class PrefillInt4QMM {
+public:
+    explicit PrefillInt4QMM(const Module& m) : m_(m) {}
+
+    int encode(void* stream, const void* weights, const uint16_t* scales, const uint16_t* biases,
+               const uint16_t* x, uint16_t* y, uint32_t t, uint32_t n, uint32_t k, int dtype) const {
+        if (k == 0 || k % TFQ_GROUP_SIZE != 0)
+            return fail(TFQ_E_INVAL, "k=%u must be a positive multiple of 64", k);
+        if (n == 0) return fail(TFQ_E_INVAL, "output count must be positive");
+        if (t == 0) return fail(TFQ_E_INVAL, "token count must be positive");
+        if (dtype != TFQ_DTYPE_F16 && dtype != TFQ_DTYPE_BF16)
+            return fail(TFQ_E_INVAL, "dtype %d is neither fp16 nor bf16", dtype);
+        if (!weights || !scales || !biases || !x || !y) return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(weights, 16) || !aligned(x, 16))
+            return fail(TFQ_E_INVAL, "weights and x must be 16-byte aligned");
+        if (!aligned(scales, 2) || !aligned(biases, 2) || !aligned(y, 2))
+            return fail(TFQ_E_INVAL, "scales/biases/y must be 2-byte aligned");
+        const char* name = dtype == TFQ_DTYPE_BF16 ? "tfq_gemm_q4_bf16" : "tfq_gemm_q4_f16";
+        hipFunction_t f = m_.get(name);
+        if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
+        const uint32_t gx = (n + 127) / 128, gy = (t + 127) / 128;
+        void* args[] = {&x, &weights, &scales, &biases, &y, &t, &n, &k};
+        return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, (hipStream_t)stream, args,
+                                               nullptr),
+                         name);
+    }
+
+private:
+    const Module& m_;
+};
+
 }  // namespace tfq

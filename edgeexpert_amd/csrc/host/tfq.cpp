@@ -38,6 +38,8 @@ static std::vector<std::string> kernel_names() {
     for (int p = 1; p <= 4; ++p) names.push_back("tfq_moe_phase2_p" + std::to_string(p));
     names.push_back("tfq_router_select");
     names.push_back("tfq_read_ceiling");
+    names.push_back("tfq_gemm_q4_f16");
+    names.push_back("tfq_gemm_q4_bf16");
     names.push_back("tfq_convert_bf16_f16");
     return names;
 }
@@ -84,7 +86,9 @@ struct tfq_ctx {
     DequantInt8GEMV* int8 = nullptr;
     MoE* moe = nullptr;
     SharedExpertInt4* shared = nullptr;
+    PrefillInt4QMM* qmm = nullptr;
     ~tfq_ctx() {
+        delete qmm;
         delete int4;
         delete int8;
         delete moe;
@@ -112,6 +116,7 @@ int tfq_create(tfq_ctx** out, const char* code_object_path) {
     c->int8 = new DequantInt8GEMV(c->module);
     c->moe = new MoE(c->module);
     c->shared = new SharedExpertInt4(c->module);
+    c->qmm = new PrefillInt4QMM(c->module);
     *out = c;
     return TFQ_OK;
 }
@@ -230,6 +235,13 @@ int tfq_shared_expert_q4(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* gate,
     TFQ_REQUIRE_CTX(ctx);
     if (!gate || !up || !down) return fail(TFQ_E_INVAL, "null matrix descriptor");
     return ctx->shared->encode(stream, x, *gate, *up, *down, y, d, f, act_scratch);
+}
+
+int tfq_gemm_q4g64(tfq_ctx* ctx, void* stream, const void* weights, const uint16_t* scales,
+                   const uint16_t* biases, const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n,
+                   uint32_t k, int dtype) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->qmm->encode(stream, weights, scales, biases, x, y, m, n, k, dtype);
 }
 
 int tfq_convert_bf16_to_f16(tfq_ctx* ctx, void* stream, const uint16_t* src, uint16_t* dst,

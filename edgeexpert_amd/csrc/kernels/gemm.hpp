@@ -1,0 +1,192 @@
+// gemm.hpp — prefill dequant-fused GEMM: Y[t][n] = Σ_k X[t][k] · W[n][k],
+// W affine int4 g64 (fp16 scale/bias), X and Y fp16 or bf16, fp32 accumulate
+// on the matrix cores (S/Metal/TensorCore/tensorops.metal:13-105 and
+// S/Metal/Prefill/prefill.metal:672-709 compute the same product).
+//
+// Block tile 128 (tokens) x 128 (outputs), one affine group (64 along K) per
+// step, 4 wavefronts each owning a 64x64 quarter as 2x2 v_mfma_f32_32x32x16_f16
+// tiles. Per step the block
+//   * loads the X tile (16 B per load, coalesced) and the W tile (16 B = 32
+//     codes per lane) plus the 128 scale/bias pairs into registers,
+//   * dequantises in registers: (0x6400 | q) - 1024 gives q exactly as fp16,
+//     then v_pk_fma_f16(q, s, b) rounds q·s + b once to fp16 — the same
+//     fp16 weight tile the reference's tensor-op kernel stages
+//     (tensorops.metal:57-80),
+//   * writes both tiles to the other half of a double-buffered LDS, while
+//     the MFMAs consume the current half.
+// Within every 8-element run along K the unpack yields element order
+// (0,4,1,5,2,6,3,7); the X tile is stored with the same permutation, so
+// each MFMA k-slice pairs the right operands (a dot product is order-free).
+// bf16 activations are converted to fp16 while staging; the conversion is
+// exact for |x| in [2^-14, 65504] (the range of the reference's fp16 path).
+#pragma once
+
+#include "common.hpp"
+
+namespace tfq {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+constexpr int kGemmBM = 128;
+constexpr int kGemmBN = 128;
+constexpr int kGemmBK = 64;
+constexpr int kGemmLdsStride = kGemmBK + 8;       // halves per LDS row (16-byte pad)
+constexpr int kGemmThreads = 256;
+
+// Permute one 8-element run from natural order to (0,4,1,5,2,6,3,7).
+__device__ __forceinline__ h8 perm_0415(h8 v) {
+    return __builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7);
+}
+
+// 8 bf16 -> 8 fp16 (exact inside the fp16 normal range).
+__device__ __forceinline__ h8 bf16x8_to_f16(uint4 raw) {
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    h8 out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = __builtin_bit_cast(float, w[i] << 16);
+        const float hi = __builtin_bit_cast(float, w[i] & 0xFFFF0000u);
+        out[2 * i] = (_Float16)lo;
+        out[2 * i + 1] = (_Float16)hi;
+    }
+    return out;
+}
+
+// Dequantise the 32 codes of one 16-byte chunk into 4 runs of 8 fp16 weights
+// (permuted order 0,4,1,5,2,6,3,7 inside each run).
+__device__ __forceinline__ void dequant_chunk_f16(uint4 w, uint16_t s_bits, uint16_t b_bits, h8 (&out)[4]) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    const _Float16 s = __builtin_bit_cast(_Float16, s_bits);
+    const _Float16 b = __builtin_bit_cast(_Float16, b_bits);
+    const h2 s2 = {s, s}, b2 = {b, b};
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        h8 run;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = ((ws[j] >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+            const h2 qh = __builtin_bit_cast(h2, q) - k1024;             // exact q pair
+            const h2 wv = __builtin_elementwise_fma(qh, s2, b2);         // one rounding
+            run[2 * i] = wv[0];
+            run[2 * i + 1] = wv[1];
+        }
+        out[j] = run;
+    }
+}
+
+template <bool X_BF16>
+__device__ __forceinline__ void gemm_q4(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+                                        const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
+                                        uint16_t* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][kGemmBM * kGemmLdsStride];
+    __shared__ __attribute__((aligned(16))) _Float16 wsm[2][kGemmBN * kGemmLdsStride];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = tid >> 6;
+    const uint32_t m0 = blockIdx.y * kGemmBM;
+    const uint32_t n0 = blockIdx.x * kGemmBN;
+    const uint32_t groups = K >> 6;
+    const uint32_t row_bytes = K >> 1;
+
+    // global -> register staging: X rows (tid/8 + 32p), 16-byte column chunk tid%8;
+    // W row tid/2, 16-byte half tid%2 of the group's 32 bytes.
+    const uint32_t xr = tid >> 3, xc = tid & 7u;
+    const uint32_t wr = tid >> 1, wh = tid & 1u;
+    const bool w_live = n0 + wr < N;
+    uint4 xreg[4];
+    uint4 wreg;
+    uint16_t sreg = 0, breg = 0;
+
+    auto load_global = [&](uint32_t g) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t row = m0 + xr + 32u * p;
+            xreg[p] = row < M ? *reinterpret_cast<const uint4*>(X + (size_t)row * K + g * 64u + 8u * xc)
+                              : make_uint4(0, 0, 0, 0);
+        }
+        if (w_live) {
+            const size_t n = n0 + wr;
+            wreg = ldg16(W + n * row_bytes + g * 32u + 16u * wh);
+            sreg = S[n * groups + g];
+            breg = B[n * groups + g];
+        } else {
+            wreg = make_uint4(0, 0, 0, 0);
+            sreg = 0;
+            breg = 0;
+        }
+    };
+    auto store_lds = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            h8 v = X_BF16 ? bf16x8_to_f16(xreg[p]) : __builtin_bit_cast(h8, xreg[p]);
+            *reinterpret_cast<h8*>(&xs[buf][(xr + 32u * p) * kGemmLdsStride + 8u * xc]) = perm_0415(v);
+        }
+        h8 wruns[4];
+        dequant_chunk_f16(wreg, sreg, breg, wruns);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<h8*>(&wsm[buf][wr * kGemmLdsStride + 32u * wh + 8u * j]) = wruns[j];
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const uint32_t wm = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;
+    const uint32_t arow = lane & 31u, akoff = (lane >> 5) * 8u;
+
+    load_global(0);
+    store_lds(0);
+    __syncthreads();
+    for (uint32_t g = 0; g < groups; ++g) {
+        const int cur = g & 1;
+        if (g + 1 < groups) load_global(g + 1);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            h8 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const h8*>(
+                    &xs[cur][(wm + 32u * i + arow) * kGemmLdsStride + 16u * ks + akoff]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const h8*>(
+                    &wsm[cur][(wn + 32u * j + arow) * kGemmLdsStride + 16u * ks + akoff]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (g + 1 < groups) store_lds(cur ^ 1);
+        __syncthreads();
+    }
+
+    // D layout (32x32 tile): column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t col = n0 + wn + 32u * j + (lane & 31u);
+            if (col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = m0 + wm + 32u * i + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3);
+                if (row < M) {
+                    const float v = acc[i][j][r];
+                    Y[(size_t)row * N + col] =
+                        X_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)v) : f2h(v);
+                }
+            }
+        }
+    }
+}
+
+}  // namespace tfq

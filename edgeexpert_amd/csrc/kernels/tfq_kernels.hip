@@ -6,6 +6,7 @@
 // template parameters: SEG = lanes per output row (power of two, <= 64) and
 // P = 16-byte chunks per lane; the host picks the instantiation from n.
 #include "abi_types.h"
+#include "gemm.hpp"
 #include "moe_decode.hpp"
 
 using namespace tfq;
@@ -77,6 +78,18 @@ extern "C" __global__ __launch_bounds__(256) void tfq_router_select(const float*
                                                                     float* out_wf, uint32_t E,
                                                                     uint32_t k) {
     router_select(logits, gain, out_idx, out_w, out_wf, E, k);
+}
+
+extern "C" __global__ __launch_bounds__(kGemmThreads) void tfq_gemm_q4_f16(
+    const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
+    uint32_t M, uint32_t N, uint32_t K) {
+    gemm_q4<false>(X, W, S, B, Y, M, N, K);
+}
+
+extern "C" __global__ __launch_bounds__(kGemmThreads) void tfq_gemm_q4_bf16(
+    const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
+    uint32_t M, uint32_t N, uint32_t K) {
+    gemm_q4<true>(X, W, S, B, Y, M, N, K);
 }
 
 extern "C" __global__ __launch_bounds__(256) void tfq_read_ceiling(const uint4* src, uint64_t n16,

@@ -106,6 +106,24 @@ class DequantInt8GEMV:
               "DequantInt8GEMV.encode")
 
 
+class PrefillInt4QMM:
+    """S/Kernels/Prefill/Primitives/PrefillPrimitives.swift:73-123 and
+    S/Kernels/TensorCore/MPPPrefillInt4QMM.swift:4-83 (one MFMA kernel)."""
+
+    def __init__(self, context: Context):
+        self.ctx = context
+
+    def encode(self, stream, weights, scales, biases, x, y, t, n, k, dtype=0, weights_offset=0,
+               scales_offset=0, biases_offset=0, x_offset=0, y_offset=0):
+        check(lib().tfq_gemm_q4g64(self.ctx.handle, _s(stream), _addr(weights, weights_offset),
+                                   _addr(scales, scales_offset), _addr(biases, biases_offset),
+                                   _addr(x, x_offset), _addr(y, y_offset), t, n, k, dtype),
+              "PrefillInt4QMM.encode")
+
+
+MPPPrefillInt4QMM = PrefillInt4QMM
+
+
 @dataclass
 class ExpertPool:
     """All routed experts of a layer resident in one device buffer:

@@ -204,6 +204,23 @@ int tfq_shared_expert_q4(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *gate,
                          const tfq_q4_matrix *up, const tfq_q4_matrix *down, const uint16_t *x,
                          uint16_t *y, uint32_t d, uint32_t f, uint16_t *act_scratch);
 
+/* ---------------------------------------------------------------- prefill -- */
+
+#define TFQ_DTYPE_F16 0
+#define TFQ_DTYPE_BF16 1
+
+/* Y[t][n] = Σ_k X[t][k]·W[n][k] for t < m tokens, n < n outputs, k < k:
+ * W int4 g64 [n][k] (fp16 scale/bias [n][k/64]), X [m][k] and Y [m][n] in
+ * `dtype` (fp16 or bf16), fp32 accumulate on the matrix cores (weights are
+ * dequantised to fp16 tiles in LDS; bf16 activations are converted to fp16
+ * exactly within fp16's normal range). Replaces PrefillInt4QMM.encode
+ * (S/Kernels/Prefill/Primitives/PrefillPrimitives.swift:82-122) and
+ * MPPPrefillInt4QMM.encode (S/Kernels/TensorCore/MPPPrefillInt4QMM.swift:34-78).
+ * Contract: k % 64 == 0, n >= 1, m >= 1; W and X 16-byte aligned. */
+int tfq_gemm_q4g64(tfq_ctx *ctx, void *stream, const void *weights, const uint16_t *scales,
+                   const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m, uint32_t n,
+                   uint32_t k, int dtype);
+
 /* ----------------------------------------------------------------- loader -- */
 
 /* fp16 <- BF16, elementwise on the device. Values outside the exactly
