@@ -190,6 +190,20 @@ def main():
     log(f"GEMV C0 (back-to-back): cold {cold_us:.2f} us ({cold_gbs:.0f} GB/s), warm {warm_us:.2f} us "
         f"({warm_gbs:.0f} GB/s)")
 
+    # ------------------------------------------------ GEMM config 2 (extra) ----
+    qmm = ops.PrefillInt4QMM(ctx)
+    from edgeexpert_amd._lib import DTYPE_BF16
+    Mg, Ng, Kg = 512, 8192, 2816
+    Wg, Sg, Bg = synth.int4_matrix(0, "c2/w", Ng, Kg)
+    gW, gS, gB = (DeviceBuffer.from_array(a) for a in (Wg, Sg, Bg))
+    gX = DeviceBuffer.from_array(synth.bf16_vector(0, "c2/x", Mg * Kg))
+    gY = DeviceBuffer(Mg * Ng * 2)
+    gemm_us = batch_avg_us(lambda i: qmm.encode(stream, gW, gS, gB, gX, gY, Mg, Ng, Kg, DTYPE_BF16), 20)
+    gemm_flop = 2.0 * Mg * Ng * Kg
+    gemm_tflops = gemm_flop / (gemm_us * 1e-6) / 1e12
+    log(f"GEMM C2 (bf16, back-to-back): {gemm_us:.2f} us -> {gemm_tflops:.1f} TFLOP/s "
+        f"({gemm_tflops / 2500.0 * 100:.1f}% of 2.5 PFLOP/s dense fp16/bf16)")
+
     # ------------------------------------------------------ CPU baseline ----
     cpu = None
     if not args.no_cpu:
@@ -235,6 +249,9 @@ def main():
                     "cold_gbs": round(cold_gbs, 1), "cold_frac": round(cold_gbs / HBM_PEAK_GBS, 4),
                     "warm_us": round(warm_us, 3), "warm_gbs": round(warm_gbs, 1),
                     "copies_rotated": n_copies},
+        "gemm_c2": {"shape": [Mg, Ng, Kg], "dtype": "bf16 in/out, fp16 MFMA, fp32 acc",
+                    "us": round(gemm_us, 3), "tflops": round(gemm_tflops, 1),
+                    "frac_of_dense_peak": round(gemm_tflops / 2500.0, 4)},
         "wall_s": round(wall, 4),
         "device": f"{name} {arch}",
     }

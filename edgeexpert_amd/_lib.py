@@ -56,6 +56,11 @@ class RouterDesc(C.Structure):
                 ("num_experts", C.c_uint32)]
 
 
+class PairT(C.Structure):
+    _fields_ = [("token", C.c_uint32), ("expert", C.c_uint32), ("rank", C.c_uint32),
+                ("weight_bits", C.c_uint32)]
+
+
 _P = C.c_void_p
 _U32 = C.c_uint32
 _I = C.c_int
@@ -84,6 +89,17 @@ SIGNATURES = {
     "tfq_convert_bf16_to_f16": [_P, _P, _P, _P, C.c_uint64, _P],
     "tfq_read_ceiling": [_P, _P, _P, C.c_uint64, _P, _U32],
     "tfq_gemm_q4g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _I],
+    "tfq_prefill_router": [_P, _P, C.POINTER(RouterDesc), _P, _U32, _U32, _U32, _U32, _P, _P, _P, _P],
+    "tfq_moe_group": [_P, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _P],
+    "tfq_group_pairs_host": [_P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _P,
+                             C.c_int64, _P, _P, _P, _P, C.POINTER(C.c_int64), _P,
+                             C.POINTER(C.c_int64), C.POINTER(C.c_int64)],
+    "tfq_moe_grouped": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _U32, _P, _U32, _U32, _U32,
+                        _U32, _P, _P],
+    "tfq_moe_combine": [_P, _P, _P, _P, _P, _U32, _U32, _U32],
+    "tfq_moe_prefill_workspace_bytes": [_U32, _U32, _U32, _U32, _U32],
+    "tfq_moe_prefill": [_P, _P, C.POINTER(RouterDesc), C.POINTER(ExpertPoolDesc), _P, _U32, _U32,
+                        _U32, _U32, _U32, _P, _P, _P, _P, C.c_size_t],
     "tfq_rt_device_count": [C.POINTER(_I)],
     "tfq_rt_set_device": [_I],
     "tfq_rt_device_info": [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t],
@@ -108,6 +124,7 @@ SIGNATURES = {
     "tfq_rt_graph_destroy": [_P],
 }
 _RES = {"tfq_destroy": None, "tfq_status_string": C.c_char_p,
+        "tfq_moe_prefill_workspace_bytes": C.c_size_t,
         "tfq_last_error_message": C.c_char_p}
 
 _lib = None

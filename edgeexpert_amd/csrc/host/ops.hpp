@@ -293,4 +293,144 @@ private:
     const Module& m_;
 };
 
+// Shared pool checks / conversion for the MoE operators.
+inline int check_expert_pool(const tfq_expert_pool& pool, uint32_t d, uint32_t f) {
+    if (d == 0 || d % TFQ_GROUP_SIZE != 0 || f == 0 || f % TFQ_GROUP_SIZE != 0)
+        return fail(TFQ_E_INVAL, "d=%u and f=%u must be positive multiples of 64", d, f);
+    if (!pool.base || pool.num_experts == 0) return fail(TFQ_E_INVAL, "empty expert pool");
+    const tfq_expert_offsets& o = pool.offsets;
+    if (!aligned(pool.base, 16) || pool.stride % 16 != 0 || o.gate_w % 16 || o.up_w % 16 ||
+        o.down_w % 16)
+        return fail(TFQ_E_INVAL, "pool base, stride and weight offsets must be 16-byte aligned");
+    if ((o.gate_s | o.gate_b | o.up_s | o.up_b | o.down_s | o.down_b) & 1u)
+        return fail(TFQ_E_INVAL, "scale/bias offsets must be 2-byte aligned");
+    const uint64_t wbytes = (uint64_t)f * d / 2, sbytes = (uint64_t)f * (d / 64) * 2;
+    const uint64_t ends[9] = {o.gate_w + wbytes, o.gate_s + sbytes, o.gate_b + sbytes,
+                              o.up_w + wbytes,   o.up_s + sbytes,   o.up_b + sbytes,
+                              o.down_w + wbytes, o.down_s + (uint64_t)d * (f / 64) * 2,
+                              o.down_b + (uint64_t)d * (f / 64) * 2};
+    for (uint64_t e : ends)
+        if (e > pool.stride) return fail(TFQ_E_INVAL, "expert sub-tensor exceeds the pool stride");
+    return TFQ_OK;
+}
+
+inline ExpertPool kernel_pool(const tfq_expert_pool& p) {
+    ExpertPool k{};
+    k.base = static_cast<const uint8_t*>(p.base);
+    k.stride = p.stride;
+    k.num_experts = p.num_experts;
+    const tfq_expert_offsets& o = p.offsets;
+    k.off = {o.gate_w, o.gate_s, o.gate_b, o.up_w, o.up_s, o.up_b, o.down_w, o.down_s, o.down_b};
+    return k;
+}
+
+inline int launch2(const Module& m, const char* name, uint32_t gx, uint32_t gy, uint32_t block,
+                   uint32_t lds, void* stream, void** args) {
+    hipFunction_t f = m.get(name);
+    if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
+    return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, lds, (hipStream_t)stream, args,
+                                           nullptr),
+                     name);
+}
+
+// S/Kernels/Prefill/MoE/PrefillRouter.swift:30-112.
+class PrefillRouter {
+public:
+    explicit PrefillRouter(const Module& m) : m_(m) {}
+
+    // PrefillRouter.encodeGemma4Block (PrefillRouter.swift:37-89).
+    int encode_gemma4_block(void* stream, const tfq_router& r, const uint16_t* hidden,
+                            uint32_t stride, uint32_t T, uint32_t d, uint32_t top_k,
+                            uint32_t* out_idx, uint16_t* out_w, float* out_wf, float* logits) const {
+        if (T == 0) return fail(TFQ_E_INVAL, "queryCount must be positive");
+        if (r.num_experts == 0 || r.num_experts > 256)
+            return fail(TFQ_E_INVAL, "numExperts > 256 is not supported");
+        if (top_k == 0 || top_k > 64 || top_k > r.num_experts)
+            return fail(TFQ_E_INVAL, "topK must be in 1...64");
+        if (d == 0 || d % TFQ_GROUP_SIZE) return fail(TFQ_E_INVAL, "D must be a multiple of 64");
+        if (d > 4096) return fail(TFQ_E_UNSUPPORTED, "router d=%u exceeds 4096", d);
+        if (stride < d) return fail(TFQ_E_INVAL, "hidden stride is too small");
+        if (!r.weights || !r.scales || !r.biases || !hidden || !out_idx || !out_w || !logits)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(r.weights, 16)) return fail(TFQ_E_INVAL, "weights are not 16-byte aligned");
+        const SegShape sh = seg_shape(d / 16, 4);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_prefill_router_logits_s%u_p%u", sh.seg, sh.p);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
+        const uint32_t gx = (r.num_experts + rows_per_block - 1) / rows_per_block;
+        uint32_t E = r.num_experts;
+        void* args[] = {(void*)&r.weights, (void*)&r.scales, (void*)&r.biases, &hidden, &stride,
+                        (void*)&r.effective_scale, &logits, &E, &d};
+        int rc = launch2(m_, name, gx, T, kBlock, d * 4, stream, args);
+        if (rc) return rc;
+        void* sargs[] = {&logits, (void*)&r.per_expert_scale, &out_idx, &out_w, &out_wf, &E, &top_k};
+        return launch2(m_, "tfq_prefill_select", T, 1, 256, 0, stream, sargs);
+    }
+
+private:
+    const Module& m_;
+};
+
+// Device counterpart of PrefillMoEGrouping.groupTokenExpertPairs
+// (S/Kernels/Prefill/MoE/PrefillMoEGrouping.swift:91-192).
+class PrefillMoEGrouping {
+public:
+    explicit PrefillMoEGrouping(const Module& m) : m_(m) {}
+
+    int encode(void* stream, const uint32_t* idx, const uint16_t* w, uint32_t T, uint32_t k, uint32_t E,
+               tfq_pair* sorted, uint32_t* offsets, uint32_t* counts, tfq_tile* tiles,
+               uint32_t* n_tiles, uint32_t* status) const {
+        if (T == 0) return fail(TFQ_E_INVAL, "queryCount must be positive");
+        if (k == 0) return fail(TFQ_E_INVAL, "topK must be positive");
+        if (E == 0 || E > 256) return fail(TFQ_E_INVAL, "numExperts must be in 1...256");
+        if ((uint64_t)T * k > 8192) return fail(TFQ_E_UNSUPPORTED, "more than 8192 pairs");
+        if (!idx || !w || !sorted || !offsets || !counts || !tiles || !n_tiles || !status)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        void* args[] = {&idx, &w, &T, &k, &E, &sorted, &offsets, &counts, &tiles, &n_tiles, &status};
+        return launch2(m_, "tfq_moe_group", 1, 1, 1024, 0, stream, args);
+    }
+
+private:
+    const Module& m_;
+};
+
+// S/Kernels/Prefill/MoE/PrefillGroupedRoutedMoE.swift:390-529 (gate/up + down over tiles)
+// and S/Kernels/Prefill/MoE/PrefillMoE.swift:4-40 (token-major combine).
+class PrefillGroupedRoutedMoE {
+public:
+    explicit PrefillGroupedRoutedMoE(const Module& m) : m_(m) {}
+
+    int encode(void* stream, const tfq_expert_pool& pool, const tfq_pair* sorted,
+               const tfq_tile* tiles, const uint32_t* n_tiles, uint32_t max_tiles,
+               const uint16_t* hidden, uint32_t stride, uint32_t d, uint32_t f, uint32_t k,
+               uint16_t* act, uint16_t* partials) const {
+        int rc = check_expert_pool(pool, d, f);
+        if (rc) return rc;
+        if (!sorted || !tiles || !n_tiles || !hidden || !act || !partials)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (stride < d || stride % 8) return fail(TFQ_E_INVAL, "hidden stride must be >= d and a multiple of 8");
+        if (!aligned(hidden, 16) || !aligned(act, 16))
+            return fail(TFQ_E_INVAL, "hidden and act must be 16-byte aligned");
+        if (max_tiles == 0) return TFQ_OK;
+        ExpertPool kp = kernel_pool(pool);
+        void* a1[] = {&kp, &sorted, &tiles, &n_tiles, &hidden, &stride, &act, &d, &f};
+        rc = launch2(m_, "tfq_moe_grouped_gate_up", max_tiles, (f + 127) / 128, 256, 0, stream, a1);
+        if (rc) return rc;
+        void* a2[] = {&kp, &sorted, &tiles, &n_tiles, &act, &partials, &d, &f, &k};
+        return launch2(m_, "tfq_moe_grouped_down", max_tiles, (d + 127) / 128, 256, 0, stream, a2);
+    }
+
+    // PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38).
+    int encode_reduce_token_major(void* stream, const uint16_t* partials, const uint16_t* w,
+                                  uint16_t* h2, uint32_t T, uint32_t k, uint32_t d) const {
+        if (T == 0 || k == 0 || d == 0) return fail(TFQ_E_INVAL, "empty reduce");
+        if (!partials || !w || !h2) return fail(TFQ_E_INVAL, "null pointer argument");
+        void* args[] = {&partials, &w, &h2, &T, &k, &d};
+        return launch2(m_, "tfq_moe_combine", (d + 255) / 256, T, 256, 0, stream, args);
+    }
+
+private:
+    const Module& m_;
+};
+
 }  // namespace tfq

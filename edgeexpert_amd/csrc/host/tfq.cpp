@@ -6,6 +6,7 @@
 // allocates device memory or synchronises the caller's stream.
 #include <dlfcn.h>
 
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -34,12 +35,16 @@ static std::vector<std::string> kernel_names() {
     for (const char* s : q8_shapes) {
         names.push_back(std::string("tfq_q8_gemv_") + s);
         names.push_back(std::string("tfq_router_logits_") + s);
+        names.push_back(std::string("tfq_prefill_router_logits_") + s);
     }
     for (int p = 1; p <= 4; ++p) names.push_back("tfq_moe_phase2_p" + std::to_string(p));
     names.push_back("tfq_router_select");
     names.push_back("tfq_read_ceiling");
     names.push_back("tfq_gemm_q4_f16");
     names.push_back("tfq_gemm_q4_bf16");
+    for (const char* n : {"tfq_prefill_select", "tfq_moe_group", "tfq_moe_grouped_gate_up",
+                          "tfq_moe_grouped_down", "tfq_moe_combine"})
+        names.push_back(n);
     names.push_back("tfq_convert_bf16_f16");
     return names;
 }
@@ -87,8 +92,14 @@ struct tfq_ctx {
     MoE* moe = nullptr;
     SharedExpertInt4* shared = nullptr;
     PrefillInt4QMM* qmm = nullptr;
+    PrefillRouter* prouter = nullptr;
+    PrefillMoEGrouping* grouping = nullptr;
+    PrefillGroupedRoutedMoE* grouped = nullptr;
     ~tfq_ctx() {
         delete qmm;
+        delete prouter;
+        delete grouping;
+        delete grouped;
         delete int4;
         delete int8;
         delete moe;
@@ -117,6 +128,9 @@ int tfq_create(tfq_ctx** out, const char* code_object_path) {
     c->moe = new MoE(c->module);
     c->shared = new SharedExpertInt4(c->module);
     c->qmm = new PrefillInt4QMM(c->module);
+    c->prouter = new PrefillRouter(c->module);
+    c->grouping = new PrefillMoEGrouping(c->module);
+    c->grouped = new PrefillGroupedRoutedMoE(c->module);
     *out = c;
     return TFQ_OK;
 }
@@ -242,6 +256,184 @@ int tfq_gemm_q4g64(tfq_ctx* ctx, void* stream, const void* weights, const uint16
                    uint32_t k, int dtype) {
     TFQ_REQUIRE_CTX(ctx);
     return ctx->qmm->encode(stream, weights, scales, biases, x, y, m, n, k, dtype);
+}
+
+int tfq_prefill_router(tfq_ctx* ctx, void* stream, const tfq_router* router, const uint16_t* hidden,
+                       uint32_t hidden_stride, uint32_t T, uint32_t d, uint32_t top_k,
+                       uint32_t* out_indices, uint16_t* out_weights, float* out_weights_f32,
+                       float* logits_scratch) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!router) return fail(TFQ_E_INVAL, "null router");
+    return ctx->prouter->encode_gemma4_block(stream, *router, hidden, hidden_stride, T, d, top_k,
+                                             out_indices, out_weights, out_weights_f32,
+                                             logits_scratch);
+}
+
+int tfq_moe_group(tfq_ctx* ctx, void* stream, const uint32_t* indices, const uint16_t* weights,
+                  uint32_t T, uint32_t top_k, uint32_t num_experts, tfq_pair* sorted,
+                  uint32_t* offsets, uint32_t* counts, tfq_tile* tiles, uint32_t* n_tiles,
+                  uint32_t* status) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->grouping->encode(stream, indices, weights, T, top_k, num_experts, sorted, offsets,
+                                 counts, tiles, n_tiles, status);
+}
+
+int tfq_moe_grouped(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, const tfq_pair* sorted,
+                    const tfq_tile* tiles, const uint32_t* n_tiles, uint32_t max_tiles,
+                    const uint16_t* hidden, uint32_t hidden_stride, uint32_t d, uint32_t f,
+                    uint32_t top_k, uint16_t* act_scratch, uint16_t* route_partials) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!pool) return fail(TFQ_E_INVAL, "null pool");
+    return ctx->grouped->encode(stream, *pool, sorted, tiles, n_tiles, max_tiles, hidden,
+                                hidden_stride, d, f, top_k, act_scratch, route_partials);
+}
+
+int tfq_moe_combine(tfq_ctx* ctx, void* stream, const uint16_t* route_partials,
+                    const uint16_t* route_weights, uint16_t* h2, uint32_t T, uint32_t top_k,
+                    uint32_t d) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->grouped->encode_reduce_token_major(stream, route_partials, route_weights, h2, T,
+                                                   top_k, d);
+}
+
+// Workspace of tfq_moe_prefill: 256-byte aligned segments in this order.
+namespace {
+struct PrefillLayout {
+    size_t logits, sorted, tiles, offsets, counts, n_tiles, status, act, partials, total;
+};
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+PrefillLayout prefill_layout(uint32_t T, uint32_t k, uint32_t E, uint32_t d, uint32_t f) {
+    PrefillLayout L{};
+    const size_t n = (size_t)T * k;
+    size_t cur = 0;
+    auto take = [&](size_t bytes) { size_t at = cur; cur = align256(cur + bytes); return at; };
+    L.logits = take((size_t)T * E * 4);
+    L.sorted = take(n * 16);
+    L.tiles = take((size_t)TFQ_MOE_MAX_TILES(T, k, E) * 16);
+    L.offsets = take((size_t)E * 4);
+    L.counts = take((size_t)E * 4);
+    L.n_tiles = take(4);
+    L.status = take(4);
+    L.act = take(n * f * 2);
+    L.partials = take(n * d * 2);
+    L.total = cur;
+    return L;
+}
+}  // namespace
+
+size_t tfq_moe_prefill_workspace_bytes(uint32_t T, uint32_t top_k, uint32_t num_experts, uint32_t d,
+                                       uint32_t f) {
+    return prefill_layout(T, top_k, num_experts, d, f).total;
+}
+
+int tfq_moe_prefill(tfq_ctx* ctx, void* stream, const tfq_router* router, const tfq_expert_pool* pool,
+                    const uint16_t* hidden, uint32_t hidden_stride, uint32_t T, uint32_t d, uint32_t f,
+                    uint32_t top_k, uint16_t* h2, uint32_t* out_indices, uint16_t* out_weights,
+                    void* workspace, size_t workspace_bytes) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!router || !pool || !workspace) return fail(TFQ_E_INVAL, "null router, pool or workspace");
+    if (router->num_experts != pool->num_experts)
+        return fail(TFQ_E_INVAL, "router has %u experts, pool %u", router->num_experts,
+                    pool->num_experts);
+    const uint32_t E = pool->num_experts;
+    const PrefillLayout L = prefill_layout(T, top_k, E, d, f);
+    if (workspace_bytes < L.total)
+        return fail(TFQ_E_INVAL, "workspace of %zu bytes < %zu required", workspace_bytes, L.total);
+    if (!aligned(workspace, 256)) return fail(TFQ_E_INVAL, "workspace must be 256-byte aligned");
+    char* ws = static_cast<char*>(workspace);
+    int rc = ctx->prouter->encode_gemma4_block(stream, *router, hidden, hidden_stride, T, d, top_k,
+                                               out_indices, out_weights, nullptr,
+                                               reinterpret_cast<float*>(ws + L.logits));
+    if (rc) return rc;
+    auto* sorted = reinterpret_cast<tfq_pair*>(ws + L.sorted);
+    auto* tiles = reinterpret_cast<tfq_tile*>(ws + L.tiles);
+    auto* n_tiles = reinterpret_cast<uint32_t*>(ws + L.n_tiles);
+    rc = ctx->grouping->encode(stream, out_indices, out_weights, T, top_k, E, sorted,
+                               reinterpret_cast<uint32_t*>(ws + L.offsets),
+                               reinterpret_cast<uint32_t*>(ws + L.counts), tiles, n_tiles,
+                               reinterpret_cast<uint32_t*>(ws + L.status));
+    if (rc) return rc;
+    auto* partials = reinterpret_cast<uint16_t*>(ws + L.partials);
+    rc = ctx->grouped->encode(stream, *pool, sorted, tiles, n_tiles, TFQ_MOE_MAX_TILES(T, top_k, E),
+                              hidden, hidden_stride, d, f, top_k,
+                              reinterpret_cast<uint16_t*>(ws + L.act), partials);
+    if (rc) return rc;
+    return ctx->grouped->encode_reduce_token_major(stream, partials, out_weights, h2, T, top_k, d);
+}
+
+int tfq_group_pairs_host(const tfq_pair* pairs, int64_t n_pairs, int64_t query_count, int64_t top_k,
+                         int64_t num_experts, int64_t tile_expert_count, const uint64_t* sort_keys,
+                         int64_t n_sort_keys, tfq_pair* sorted, uint32_t* offsets, uint32_t* counts,
+                         tfq_group* groups, int64_t* n_groups, tfq_group_tile* tiles,
+                         int64_t* n_tiles, int64_t err[2]) {
+    // PrefillMoEGrouping.swift:91-192: validation in the reference's order.
+    err[0] = err[1] = 0;
+    if (query_count < 0) { err[0] = query_count; return TFQ_GROUP_INVALID_QUERY_COUNT; }
+    if (top_k <= 0) { err[0] = top_k; return TFQ_GROUP_INVALID_TOPK; }
+    if (num_experts <= 0) { err[0] = num_experts; return TFQ_GROUP_INVALID_NUM_EXPERTS; }
+    if (tile_expert_count < 1 || tile_expert_count > 16) {
+        err[0] = tile_expert_count;
+        return TFQ_GROUP_INVALID_TILE_EXPERT_COUNT;
+    }
+    if (sort_keys && n_sort_keys != num_experts) {
+        err[0] = num_experts;
+        err[1] = n_sort_keys;
+        return TFQ_GROUP_SORT_KEY_COUNT_MISMATCH;
+    }
+    const int64_t expected = query_count * top_k;
+    if (n_pairs != expected) {
+        err[0] = expected;
+        err[1] = n_pairs;
+        return TFQ_GROUP_PAIR_COUNT_MISMATCH;
+    }
+    std::vector<uint8_t> seen((size_t)std::max<int64_t>(expected, 1), 0);
+    for (int64_t i = 0; i < n_pairs; ++i) {
+        const tfq_pair& p = pairs[i];
+        if ((int64_t)p.token >= query_count) { err[0] = p.token; return TFQ_GROUP_TOKEN_OUT_OF_RANGE; }
+        if ((int64_t)p.rank >= top_k) { err[0] = p.rank; return TFQ_GROUP_RANK_OUT_OF_RANGE; }
+        if ((int64_t)p.expert >= num_experts) { err[0] = p.expert; return TFQ_GROUP_EXPERT_OUT_OF_RANGE; }
+        const int64_t key = (int64_t)p.token * top_k + p.rank;
+        if (seen[key]) {
+            err[0] = p.token;
+            err[1] = p.rank;
+            return TFQ_GROUP_DUPLICATE_TOKEN_RANK;
+        }
+        seen[key] = 1;
+    }
+    std::copy(pairs, pairs + n_pairs, sorted);
+    std::sort(sorted, sorted + n_pairs, [&](const tfq_pair& a, const tfq_pair& b) {
+        if (sort_keys) {
+            const uint64_t ka = sort_keys[a.expert], kb = sort_keys[b.expert];
+            if (ka != kb) return ka < kb;
+        }
+        if (a.expert != b.expert) return a.expert < b.expert;
+        if (a.token != b.token) return a.token < b.token;
+        return a.rank < b.rank;
+    });
+    for (int64_t e = 0; e < num_experts; ++e) {
+        offsets[e] = 0xFFFFFFFFu;
+        counts[e] = 0;
+    }
+    int64_t ng = 0;
+    for (int64_t i = 0; i < n_pairs;) {
+        const uint32_t expert = sorted[i].expert;
+        const int64_t start = i;
+        while (i < n_pairs && sorted[i].expert == expert) ++i;
+        offsets[expert] = (uint32_t)start;
+        counts[expert] = (uint32_t)(i - start);
+        groups[ng++] = {expert, (uint32_t)start, (uint32_t)(i - start)};
+    }
+    int64_t nt = 0;
+    for (int64_t gs = 0; gs < ng;) {
+        const int64_t ge = std::min(ng, gs + tile_expert_count);
+        const uint32_t ps = groups[gs].pair_start;
+        const uint32_t pe = groups[ge - 1].pair_start + groups[ge - 1].pair_count;
+        tiles[nt++] = {(uint32_t)gs, (uint32_t)(ge - gs), ps, pe - ps};
+        gs = ge;
+    }
+    *n_groups = ng;
+    *n_tiles = nt;
+    return TFQ_GROUP_OK;
 }
 
 int tfq_convert_bf16_to_f16(tfq_ctx* ctx, void* stream, const uint16_t* src, uint16_t* dst,

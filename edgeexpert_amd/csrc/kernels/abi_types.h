@@ -38,4 +38,20 @@ struct ExpertPool {
     ExpertOffsets off;
 };
 
+// PrefillTokenExpertPair (S/Kernels/Prefill/MoE/PrefillRouter.swift:5-28).
+struct Pair {
+    uint32_t token;
+    uint32_t expert;
+    uint32_t rank;
+    uint32_t weight_bits;
+};
+
+// One 128-row MFMA tile of one expert's run in the sorted pair list.
+struct Tile {
+    uint32_t expert;
+    uint32_t start;
+    uint32_t count;
+    uint32_t pad_;
+};
+
 }  // namespace tfq

@@ -1,22 +1,24 @@
-// gemm.hpp — prefill dequant-fused GEMM: Y[t][n] = Σ_k X[t][k] · W[n][k],
-// W affine int4 g64 (fp16 scale/bias), X and Y fp16 or bf16, fp32 accumulate
-// on the matrix cores (S/Metal/TensorCore/tensorops.metal:13-105 and
+// gemm.hpp — dequant-fused int4 GEMM tile on the matrix cores, used by the
+// prefill projection GEMM and by the grouped MoE prefill:
+//     C[j][n] = Σ_k X[row_j][k] · W_m[n][k]     (m = 0..NMAT-1 weight matrices)
+// W affine int4 g64 with fp16 scale/bias, X fp16 (or bf16, converted),
+// fp32 accumulate (S/Metal/TensorCore/tensorops.metal:13-105 and
 // S/Metal/Prefill/prefill.metal:672-709 compute the same product).
 //
-// Block tile 128 (tokens) x 128 (outputs), one affine group (64 along K) per
-// step, 4 wavefronts each owning a 64x64 quarter as 2x2 v_mfma_f32_32x32x16_f16
-// tiles. Per step the block
-//   * loads the X tile (16 B per load, coalesced) and the W tile (16 B = 32
-//     codes per lane) plus the 128 scale/bias pairs into registers,
+// Block tile 128 rows x 128 outputs, one affine group (64 along K) per step,
+// 4 wavefronts each owning a 64x64 quarter as 2x2 v_mfma_f32_32x32x16_f16
+// tiles per matrix. Per step the block
+//   * loads the X tile (16 B per load, coalesced; rows come from a caller
+//     supplied row table, so gathered rows cost nothing extra) and each W
+//     tile (16 B = 32 codes per lane) with its 128 scale/bias pairs,
 //   * dequantises in registers: (0x6400 | q) - 1024 gives q exactly as fp16,
-//     then v_pk_fma_f16(q, s, b) rounds q·s + b once to fp16 — the same
-//     fp16 weight tile the reference's tensor-op kernel stages
-//     (tensorops.metal:57-80),
-//   * writes both tiles to the other half of a double-buffered LDS, while
-//     the MFMAs consume the current half.
+//     then v_pk_fma_f16(q, s, b) rounds q·s + b once to fp16 — the fp16
+//     weight tile the reference's tensor-op kernel stages (tensorops.metal:57-80),
+//   * writes the tiles to the other half of a double-buffered LDS while the
+//     MFMAs consume the current half.
 // Within every 8-element run along K the unpack yields element order
-// (0,4,1,5,2,6,3,7); the X tile is stored with the same permutation, so
-// each MFMA k-slice pairs the right operands (a dot product is order-free).
+// (0,4,1,5,2,6,3,7); X is stored with the same permutation, so each MFMA
+// k-slice pairs the right operands (a dot product is order-free).
 // bf16 activations are converted to fp16 while staging; the conversion is
 // exact for |x| in [2^-14, 65504] (the range of the reference's fp16 path).
 #pragma once
@@ -26,13 +28,13 @@
 namespace tfq {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 
 constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
 constexpr int kGemmBK = 64;
 constexpr int kGemmLdsStride = kGemmBK + 8;       // halves per LDS row (16-byte pad)
 constexpr int kGemmThreads = 256;
+constexpr int kGemmTile = kGemmBM * kGemmLdsStride;
 
 // Permute one 8-element run from natural order to (0,4,1,5,2,6,3,7).
 __device__ __forceinline__ h8 perm_0415(h8 v) {
@@ -76,68 +78,88 @@ __device__ __forceinline__ void dequant_chunk_f16(uint4 w, uint16_t s_bits, uint
     }
 }
 
-template <bool X_BF16>
-__device__ __forceinline__ void gemm_q4(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
-                                        const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
-                                        uint16_t* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][kGemmBM * kGemmLdsStride];
-    __shared__ __attribute__((aligned(16))) _Float16 wsm[2][kGemmBN * kGemmLdsStride];
+// One int4 weight matrix as seen by a tile: row n of W starts at w + n*K/2.
+struct Q4Tile {
+    const uint8_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+};
 
+// LDS of one tile with NMAT weight matrices (double buffered).
+template <int NMAT>
+struct GemmLds {
+    _Float16 x[2][kGemmTile];
+    _Float16 w[NMAT][2][kGemmTile];
+};
+
+// Computes the 128x128 tile (rows: row_ptr[0..rows), outputs n0..n0+127 < N)
+// and calls out(j, n, v[NMAT]) for every valid element. row_ptr holds the
+// address of each X row (K elements). Must be called by all 256 threads.
+template <bool X_BF16, int NMAT, typename Out>
+__device__ __forceinline__ void gemm_tile(GemmLds<NMAT>& L, const uint16_t* const* row_ptr,
+                                          uint32_t rows, const Q4Tile (&mats)[NMAT], uint32_t n0,
+                                          uint32_t N, uint32_t K, Out out) {
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = tid >> 6;
-    const uint32_t m0 = blockIdx.y * kGemmBM;
-    const uint32_t n0 = blockIdx.x * kGemmBN;
     const uint32_t groups = K >> 6;
     const uint32_t row_bytes = K >> 1;
 
-    // global -> register staging: X rows (tid/8 + 32p), 16-byte column chunk tid%8;
-    // W row tid/2, 16-byte half tid%2 of the group's 32 bytes.
+    // global -> registers: X rows (tid/8 + 32p), 16-byte chunk tid%8 of the
+    // group; W row tid/2, 16-byte half tid%2 of the group's 32 bytes.
     const uint32_t xr = tid >> 3, xc = tid & 7u;
     const uint32_t wr = tid >> 1, wh = tid & 1u;
     const bool w_live = n0 + wr < N;
     uint4 xreg[4];
-    uint4 wreg;
-    uint16_t sreg = 0, breg = 0;
+    uint4 wreg[NMAT];
+    uint16_t sreg[NMAT], breg[NMAT];
 
     auto load_global = [&](uint32_t g) {
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const uint32_t row = m0 + xr + 32u * p;
-            xreg[p] = row < M ? *reinterpret_cast<const uint4*>(X + (size_t)row * K + g * 64u + 8u * xc)
-                              : make_uint4(0, 0, 0, 0);
+            const uint32_t j = xr + 32u * p;
+            xreg[p] = j < rows ? *reinterpret_cast<const uint4*>(row_ptr[j] + g * 64u + 8u * xc)
+                               : make_uint4(0, 0, 0, 0);
         }
-        if (w_live) {
-            const size_t n = n0 + wr;
-            wreg = ldg16(W + n * row_bytes + g * 32u + 16u * wh);
-            sreg = S[n * groups + g];
-            breg = B[n * groups + g];
-        } else {
-            wreg = make_uint4(0, 0, 0, 0);
-            sreg = 0;
-            breg = 0;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            if (w_live) {
+                const size_t n = n0 + wr;
+                wreg[m] = ldg16(mats[m].w + n * row_bytes + g * 32u + 16u * wh);
+                sreg[m] = mats[m].s[n * groups + g];
+                breg[m] = mats[m].b[n * groups + g];
+            } else {
+                wreg[m] = make_uint4(0, 0, 0, 0);
+                sreg[m] = 0;
+                breg[m] = 0;
+            }
         }
     };
     auto store_lds = [&](int buf) {
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            h8 v = X_BF16 ? bf16x8_to_f16(xreg[p]) : __builtin_bit_cast(h8, xreg[p]);
-            *reinterpret_cast<h8*>(&xs[buf][(xr + 32u * p) * kGemmLdsStride + 8u * xc]) = perm_0415(v);
+            const h8 v = X_BF16 ? bf16x8_to_f16(xreg[p]) : __builtin_bit_cast(h8, xreg[p]);
+            *reinterpret_cast<h8*>(&L.x[buf][(xr + 32u * p) * kGemmLdsStride + 8u * xc]) = perm_0415(v);
         }
-        h8 wruns[4];
-        dequant_chunk_f16(wreg, sreg, breg, wruns);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<h8*>(&wsm[buf][wr * kGemmLdsStride + 32u * wh + 8u * j]) = wruns[j];
+        for (int m = 0; m < NMAT; ++m) {
+            h8 runs[4];
+            dequant_chunk_f16(wreg[m], sreg[m], breg[m], runs);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<h8*>(&L.w[m][buf][wr * kGemmLdsStride + 32u * wh + 8u * j]) = runs[j];
+        }
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[NMAT][2][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[m][i][j][r] = 0.0f;
 
     const uint32_t wm = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;
     const uint32_t arow = lane & 31u, akoff = (lane >> 5) * 8u;
@@ -150,20 +172,24 @@ __device__ __forceinline__ void gemm_q4(const uint16_t* __restrict__ X, const ui
         if (g + 1 < groups) load_global(g + 1);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            h8 a[2], b[2];
+            h8 a[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
                 a[i] = *reinterpret_cast<const h8*>(
-                    &xs[cur][(wm + 32u * i + arow) * kGemmLdsStride + 16u * ks + akoff]);
+                    &L.x[cur][(wm + 32u * i + arow) * kGemmLdsStride + 16u * ks + akoff]);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                b[j] = *reinterpret_cast<const h8*>(
-                    &wsm[cur][(wn + 32u * j + arow) * kGemmLdsStride + 16u * ks + akoff]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int m = 0; m < NMAT; ++m) {
+                h8 b[2];
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                    b[j] = *reinterpret_cast<const h8*>(
+                        &L.w[m][cur][(wn + 32u * j + arow) * kGemmLdsStride + 16u * ks + akoff]);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[m][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[m][i][j], 0, 0, 0);
+            }
         }
         if (g + 1 < groups) store_lds(cur ^ 1);
         __syncthreads();
@@ -178,15 +204,35 @@ __device__ __forceinline__ void gemm_q4(const uint16_t* __restrict__ X, const ui
             if (col >= N) continue;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t row = m0 + wm + 32u * i + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3);
-                if (row < M) {
-                    const float v = acc[i][j][r];
-                    Y[(size_t)row * N + col] =
-                        X_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)v) : f2h(v);
+                const uint32_t row = wm + 32u * i + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3);
+                if (row < rows) {
+                    float v[NMAT];
+#pragma unroll
+                    for (int m = 0; m < NMAT; ++m) v[m] = acc[m][i][j][r];
+                    out(row, col, v);
                 }
             }
         }
     }
+}
+
+// Prefill projection: Y[t][n] = X[t] · W[n] for tokens t < M.
+template <bool X_BF16>
+__device__ __forceinline__ void gemm_q4(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+                                        const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
+                                        uint16_t* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K) {
+    __shared__ __attribute__((aligned(16))) GemmLds<1> L;
+    __shared__ const uint16_t* rows_ptr[kGemmBM];
+    const uint32_t m0 = blockIdx.y * kGemmBM;
+    const uint32_t rows = M - m0 < (uint32_t)kGemmBM ? M - m0 : (uint32_t)kGemmBM;
+    if (threadIdx.x < kGemmBM) rows_ptr[threadIdx.x] = X + (size_t)(m0 + threadIdx.x) * K;
+    __syncthreads();
+    const Q4Tile mats[1] = {{W, S, B}};
+    gemm_tile<X_BF16, 1>(L, rows_ptr, rows, mats, blockIdx.x * kGemmBN, N, K,
+                         [&](uint32_t j, uint32_t n, const float* v) {
+                             Y[(size_t)(m0 + j) * N + n] =
+                                 X_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)v[0]) : f2h(v[0]);
+                         });
 }
 
 }  // namespace tfq

@@ -8,6 +8,7 @@
 #include "abi_types.h"
 #include "gemm.hpp"
 #include "moe_decode.hpp"
+#include "moe_prefill.hpp"
 
 using namespace tfq;
 
@@ -32,6 +33,15 @@ constexpr int kRowsInFlight = 2;
         const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* h,               \
         const uint16_t* eff, float* logits, uint32_t E, uint32_t d) {                            \
         router_logits<SEG, P>(W, S, B, h, eff, logits, E, d);                                     \
+    }
+
+// Prefill router: blockIdx.y selects the token (row stride `stride` halves).
+#define TFQ_PREFILL_ROUTER(SEG, P)                                                               \
+    extern "C" __global__ __launch_bounds__(256) void tfq_prefill_router_logits_s##SEG##_p##P(   \
+        const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* hidden,          \
+        uint32_t stride, const uint16_t* eff, float* logits, uint32_t E, uint32_t d) {           \
+        router_logits<SEG, P>(W, S, B, hidden + (size_t)blockIdx.y * stride, eff,               \
+                              logits + (size_t)blockIdx.y * E, E, d);                            \
     }
 
 #define TFQ_PHASE1(SEG, P)                                                                       \
@@ -66,6 +76,7 @@ TFQ_Q4_TABLE(TFQ_PHASE1)
 TFQ_Q4_TABLE(TFQ_GATE_UP)
 TFQ_Q8_TABLE(TFQ_Q8_GEMV)
 TFQ_Q8_TABLE(TFQ_ROUTER)
+TFQ_Q8_TABLE(TFQ_PREFILL_ROUTER)
 TFQ_PHASE2(1)
 TFQ_PHASE2(2)
 TFQ_PHASE2(3)
@@ -90,6 +101,42 @@ extern "C" __global__ __launch_bounds__(kGemmThreads) void tfq_gemm_q4_bf16(
     const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
     uint32_t M, uint32_t N, uint32_t K) {
     gemm_q4<true>(X, W, S, B, Y, M, N, K);
+}
+
+// Per-token selection for a prefill chunk: one block per token.
+extern "C" __global__ __launch_bounds__(256) void tfq_prefill_select(const float* logits,
+                                                                     const uint16_t* gain,
+                                                                     uint32_t* out_idx,
+                                                                     uint16_t* out_w,
+                                                                     float* out_wf, uint32_t E,
+                                                                     uint32_t k) {
+    const size_t t = blockIdx.x;
+    router_select(logits + t * E, gain, out_idx + t * k, out_w + t * k, out_wf ? out_wf + t * k : nullptr,
+                  E, k);
+}
+
+extern "C" __global__ __launch_bounds__(kGroupThreads) void tfq_moe_group(
+    const uint32_t* idx, const uint16_t* w, uint32_t T, uint32_t k, uint32_t E, Pair* sorted,
+    uint32_t* offsets, uint32_t* counts, Tile* tiles, uint32_t* n_tiles, uint32_t* status) {
+    moe_group(idx, w, T, k, E, sorted, offsets, counts, tiles, n_tiles, status);
+}
+
+extern "C" __global__ __launch_bounds__(kGemmThreads) void tfq_moe_grouped_gate_up(
+    ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,
+    const uint16_t* hidden, uint32_t stride, uint16_t* act, uint32_t D, uint32_t F) {
+    moe_grouped_gate_up(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F);
+}
+
+extern "C" __global__ __launch_bounds__(kGemmThreads) void tfq_moe_grouped_down(
+    ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,
+    const uint16_t* act, uint16_t* partials, uint32_t D, uint32_t F, uint32_t k) {
+    moe_grouped_down(pool, sorted, tiles, n_tiles, act, partials, D, F, k);
+}
+
+extern "C" __global__ __launch_bounds__(256) void tfq_moe_combine(const uint16_t* partials,
+                                                                  const uint16_t* w, uint16_t* h2,
+                                                                  uint32_t T, uint32_t k, uint32_t D) {
+    moe_combine(partials, w, h2, T, k, D);
 }
 
 extern "C" __global__ __launch_bounds__(256) void tfq_read_ceiling(const uint4* src, uint64_t n16,

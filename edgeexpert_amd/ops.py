@@ -11,6 +11,8 @@ from __future__ import annotations
 import ctypes as C
 from dataclasses import dataclass
 
+import numpy as np
+
 from ._lib import (CODE_OBJECT_PATH, ExpertOffsets, ExpertPoolDesc, Q4Matrix, RouterDesc, check,
                    lib)
 from .runtime import DeviceBuffer, Stream
@@ -236,3 +238,133 @@ def read_ceiling(context: Context, stream, src, nbytes: int, sink, sink_blocks: 
     """HBM read-ceiling probe (one pass over nbytes with 128-bit loads)."""
     check(lib().tfq_read_ceiling(context.handle, _s(stream), _addr(src, src_offset), nbytes,
                                  _addr(sink), sink_blocks), "tfq_read_ceiling")
+
+
+# ----------------------------------------------------------------- prefill ----
+
+PAIR_DTYPE = np.dtype([("token", "<u4"), ("expert", "<u4"), ("rank", "<u4"), ("weight_bits", "<u4")])
+TILE_DTYPE = np.dtype([("expert", "<u4"), ("start", "<u4"), ("count", "<u4"), ("reserved", "<u4")])
+GROUP_DTYPE = np.dtype([("expert", "<u4"), ("pair_start", "<u4"), ("pair_count", "<u4")])
+GROUP_TILE_DTYPE = np.dtype([("group_start", "<u4"), ("group_count", "<u4"), ("pair_start", "<u4"),
+                             ("pair_count", "<u4")])
+GROUP_ERRORS = {1: "invalidQueryCount", 2: "invalidTopK", 3: "invalidNumExperts",
+                4: "invalidTileExpertCount", 5: "pairCountMismatch", 6: "tokenOutOfRange",
+                7: "rankOutOfRange", 8: "expertOutOfRange", 9: "duplicateTokenRank",
+                10: "expertSortKeyCountMismatch"}
+
+
+def max_tiles(T: int, k: int, num_experts: int) -> int:
+    n = T * k
+    return (n + 127) // 128 + min(num_experts, n)
+
+
+class PrefillRouter:
+    """S/Kernels/Prefill/MoE/PrefillRouter.swift:30-112."""
+
+    def __init__(self, context: Context):
+        self.ctx = context
+
+    def encode_gemma4_block(self, stream, router: "Router", hidden, hidden_stride, query_count, d,
+                            top_k, out_indices, out_weights, logits_scratch, out_weights_f32=None):
+        r = router.desc()
+        check(lib().tfq_prefill_router(self.ctx.handle, _s(stream), C.byref(r), _addr(hidden),
+                                       hidden_stride, query_count, d, top_k, _addr(out_indices),
+                                       _addr(out_weights), _addr(out_weights_f32),
+                                       _addr(logits_scratch)), "PrefillRouter.encodeGemma4Block")
+
+    @staticmethod
+    def make_token_expert_pairs(indices, weights_f16_bits, query_count, top_k):
+        """makeTokenExpertPairs (PrefillRouter.swift:91-111): token-major pairs."""
+        idx = np.asarray(indices, np.uint32).reshape(query_count, top_k)
+        wb = np.asarray(weights_f16_bits, np.uint16).reshape(query_count, top_k)
+        pairs = np.zeros(query_count * top_k, PAIR_DTYPE)
+        pairs["token"] = np.repeat(np.arange(query_count, dtype=np.uint32), top_k)
+        pairs["rank"] = np.tile(np.arange(top_k, dtype=np.uint32), query_count)
+        pairs["expert"] = idx.ravel()
+        pairs["weight_bits"] = wb.ravel()
+        return pairs
+
+
+class GroupingError(Exception):
+    def __init__(self, code, a, b):
+        self.code = code
+        self.name = GROUP_ERRORS.get(code, str(code))
+        self.values = (a, b)
+        super().__init__(f"{self.name}{self.values}")
+
+
+class PrefillMoEGrouping:
+    """PrefillMoEGrouping (S/Kernels/Prefill/MoE/PrefillMoEGrouping.swift:90-193):
+    group_token_expert_pairs runs the host restatement in libtfq; encode runs
+    the device counting sort."""
+
+    def __init__(self, context: Context | None = None):
+        self.ctx = context
+
+    @staticmethod
+    def group_token_expert_pairs(pairs, query_count, top_k, num_experts, tile_expert_count=16,
+                                 expert_sort_keys=None):
+        pairs = np.ascontiguousarray(pairs, dtype=PAIR_DTYPE)
+        n = pairs.size
+        ne = max(int(num_experts), 1)
+        sorted_ = np.zeros(max(n, 1), PAIR_DTYPE)
+        offsets = np.zeros(ne, np.uint32)
+        counts = np.zeros(ne, np.uint32)
+        groups = np.zeros(ne, GROUP_DTYPE)
+        tiles = np.zeros(ne, GROUP_TILE_DTYPE)
+        ng, nt = C.c_int64(0), C.c_int64(0)
+        err = (C.c_int64 * 2)()
+        sk = None if expert_sort_keys is None else np.ascontiguousarray(expert_sort_keys, np.uint64)
+        rc = lib().tfq_group_pairs_host(
+            pairs.ctypes.data, n, query_count, top_k, num_experts, tile_expert_count,
+            None if sk is None else sk.ctypes.data, 0 if sk is None else sk.size,
+            sorted_.ctypes.data, offsets.ctypes.data, counts.ctypes.data, groups.ctypes.data,
+            C.byref(ng), tiles.ctypes.data, C.byref(nt), err)
+        if rc != 0:
+            raise GroupingError(rc, err[0], err[1])
+        return {"sorted": sorted_[:n], "offsets": offsets[:num_experts],
+                "counts": counts[:num_experts], "groups": groups[:ng.value],
+                "tiles": tiles[:nt.value], "query_count": query_count}
+
+    def encode(self, stream, indices, weights, query_count, top_k, num_experts, sorted_pairs,
+               offsets, counts, tiles, n_tiles, status):
+        check(lib().tfq_moe_group(self.ctx.handle, _s(stream), _addr(indices), _addr(weights),
+                                  query_count, top_k, num_experts, _addr(sorted_pairs),
+                                  _addr(offsets), _addr(counts), _addr(tiles), _addr(n_tiles),
+                                  _addr(status)), "tfq_moe_group")
+
+
+class PrefillGroupedRoutedMoE:
+    """S/Kernels/Prefill/MoE/PrefillGroupedRoutedMoE.swift:390-529 and
+    S/Kernels/Prefill/MoE/PrefillMoE.swift:4-40."""
+
+    def __init__(self, context: Context):
+        self.ctx = context
+
+    def encode(self, stream, pool: "ExpertPool", sorted_pairs, tiles, n_tiles, max_tiles_, hidden,
+               hidden_stride, d, f, top_k, act_scratch, route_partials):
+        p = pool.desc()
+        check(lib().tfq_moe_grouped(self.ctx.handle, _s(stream), C.byref(p), _addr(sorted_pairs),
+                                    _addr(tiles), _addr(n_tiles), max_tiles_, _addr(hidden),
+                                    hidden_stride, d, f, top_k, _addr(act_scratch),
+                                    _addr(route_partials)), "PrefillGroupedRoutedMoE.encode")
+
+    def encode_reduce_token_major(self, stream, route_partials, route_weights, h2, query_count,
+                                  top_k, d):
+        check(lib().tfq_moe_combine(self.ctx.handle, _s(stream), _addr(route_partials),
+                                    _addr(route_weights), _addr(h2), query_count, top_k, d),
+              "PrefillMoE.encodeReduceTokenMajor")
+
+
+def moe_prefill_workspace_bytes(T, top_k, num_experts, d, f) -> int:
+    return lib().tfq_moe_prefill_workspace_bytes(T, top_k, num_experts, d, f)
+
+
+def moe_prefill(context: Context, stream, router: "Router", pool: "ExpertPool", hidden, hidden_stride,
+                T, d, f, top_k, h2, out_indices, out_weights, workspace, workspace_bytes):
+    """Router -> device grouping -> grouped experts -> combine for T tokens."""
+    r, p = router.desc(), pool.desc()
+    check(lib().tfq_moe_prefill(context.handle, _s(stream), C.byref(r), C.byref(p), _addr(hidden),
+                                hidden_stride, T, d, f, top_k, _addr(h2), _addr(out_indices),
+                                _addr(out_weights), _addr(workspace), workspace_bytes),
+          "tfq_moe_prefill")

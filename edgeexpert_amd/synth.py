@@ -183,3 +183,26 @@ def blob_views(blob: np.ndarray, offsets: dict, d: int, f: int, proj: str):
     s = blob[offsets[f"{proj}_s"]:offsets[f"{proj}_s"] + 2 * ng].view(np.uint16).reshape(rows, -1)
     b = blob[offsets[f"{proj}_b"]:offsets[f"{proj}_b"] + 2 * ng].view(np.uint16).reshape(rows, -1)
     return w, s, b
+
+
+# ---------------------------------------------------------------- routing ----
+
+def zipf_routing(seed: int, label: str, tokens: int, num_experts: int, top_k: int, s: float = 1.1):
+    """Skewed prefill routing: expert popularity p ∝ r^-s
+    over a seeded rank permutation; each token takes top_k distinct experts
+    by Gumbel-top-k over log p, ties to the lower expert index; its weights are
+    the softmax of the selected perturbed logits, rounded to fp16.
+    Returns (indices u32 [tokens][top_k], weights fp16 bits [tokens][top_k])."""
+    perm = np.argsort(uniform24(seed_key(seed, label + "/perm"), num_experts), kind="stable")
+    rank_of = np.empty(num_experts, np.int64)
+    rank_of[perm] = np.arange(num_experts)
+    logp = -s * np.log(rank_of + 1.0)
+    u = (splitmix64(seed_key(seed, label + "/gumbel"), tokens * num_experts) >> np.uint64(11))
+    u = (u.astype(np.float64) + 0.5) / float(1 << 53)                 # (0, 1)
+    z = logp[None, :] + (-np.log(-np.log(u))).reshape(tokens, num_experts)
+    order = np.lexsort((np.broadcast_to(np.arange(num_experts), z.shape), -z), axis=1)
+    idx = order[:, :top_k].astype(np.uint32)
+    sel = np.take_along_axis(z, order[:, :top_k], axis=1)
+    w = np.exp(sel - sel[:, :1])
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    return idx, f16_bits(w)

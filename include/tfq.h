@@ -221,6 +221,121 @@ int tfq_gemm_q4g64(tfq_ctx *ctx, void *stream, const void *weights, const uint16
                    const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m, uint32_t n,
                    uint32_t k, int dtype);
 
+/* (token, expert, rank, fp16 routing weight bits in the low half) — the
+ * 16-byte PrefillTokenExpertPair (S/Kernels/Prefill/MoE/PrefillRouter.swift:5-28). */
+typedef struct {
+    uint32_t token;
+    uint32_t expert;
+    uint32_t rank;
+    uint32_t weight_bits;
+} tfq_pair;
+
+/* One 128-row MFMA tile of one expert: sorted pairs [start, start+count). */
+typedef struct {
+    uint32_t expert;
+    uint32_t start;
+    uint32_t count;
+    uint32_t reserved;
+} tfq_tile;
+
+/* Upper bound of the tile count for T*top_k pairs over num_experts experts. */
+#define TFQ_MOE_MAX_TILES(T, top_k, num_experts)                                   \
+    (((T) * (top_k) + 127u) / 128u +                                               \
+     ((num_experts) < (T) * (top_k) ? (num_experts) : (T) * (top_k)))
+
+/* Router for a chunk of T tokens: hidden [T] rows of hidden_stride fp16
+ * elements -> indices [T][top_k] and fp16 weights [T][top_k] (fp32 copy to
+ * out_weights_f32 if non-NULL). logits_scratch: fp32 [T][num_experts].
+ * Same arithmetic per token as tfq_router_topk. Replaces
+ * PrefillRouter.encodeGemma4Block (S/Kernels/Prefill/MoE/PrefillRouter.swift:37-89).
+ * Contract: T >= 1, hidden_stride >= d, d % 64 == 0, d <= 4096,
+ * 1 <= num_experts <= 256, 1 <= top_k <= min(64, num_experts). */
+int tfq_prefill_router(tfq_ctx *ctx, void *stream, const tfq_router *router,
+                       const uint16_t *hidden, uint32_t hidden_stride, uint32_t T, uint32_t d,
+                       uint32_t top_k, uint32_t *out_indices, uint16_t *out_weights,
+                       float *out_weights_f32, float *logits_scratch);
+
+/* Status written by tfq_moe_group (values of PrefillMoEGroupingError the
+ * device can detect; same numbering as tfq_group_pairs_host). */
+#define TFQ_GROUP_OK 0
+#define TFQ_GROUP_INVALID_QUERY_COUNT 1
+#define TFQ_GROUP_INVALID_TOPK 2
+#define TFQ_GROUP_INVALID_NUM_EXPERTS 3
+#define TFQ_GROUP_INVALID_TILE_EXPERT_COUNT 4
+#define TFQ_GROUP_PAIR_COUNT_MISMATCH 5
+#define TFQ_GROUP_TOKEN_OUT_OF_RANGE 6
+#define TFQ_GROUP_RANK_OUT_OF_RANGE 7
+#define TFQ_GROUP_EXPERT_OUT_OF_RANGE 8
+#define TFQ_GROUP_DUPLICATE_TOKEN_RANK 9
+#define TFQ_GROUP_SORT_KEY_COUNT_MISMATCH 10
+
+/* Device grouping of the token-major pairs (token t, rank r) -> expert
+ * indices[t*top_k + r] with weight weights[t*top_k + r]: a stable counting
+ * sort giving the order (expert, token, rank) of PrefillMoEGrouping
+ * .groupTokenExpertPairs (S/Kernels/Prefill/MoE/PrefillMoEGrouping.swift:91-192,
+ * no sort keys). offsets/counts [num_experts] (offset 0xFFFFFFFF for an empty
+ * expert), tiles [TFQ_MOE_MAX_TILES], *n_tiles and *status on the device. An
+ * out-of-range expert index groups nothing and sets *status =
+ * TFQ_GROUP_EXPERT_OUT_OF_RANGE. Contract: 1 <= T*top_k <= 8192,
+ * 1 <= num_experts <= 256. */
+int tfq_moe_group(tfq_ctx *ctx, void *stream, const uint32_t *indices, const uint16_t *weights,
+                  uint32_t T, uint32_t top_k, uint32_t num_experts, tfq_pair *sorted,
+                  uint32_t *offsets, uint32_t *counts, tfq_tile *tiles, uint32_t *n_tiles,
+                  uint32_t *status);
+
+/* A group of equal-expert pairs and a tile of <= tile_expert_count groups, as
+ * returned by the host grouping (PrefillMoEGroup / PrefillMoETile,
+ * PrefillMoEGrouping.swift:3-29). */
+typedef struct { uint32_t expert, pair_start, pair_count; } tfq_group;
+typedef struct { uint32_t group_start, group_count, pair_start, pair_count; } tfq_group_tile;
+
+/* Host-side grouping with the reference's exact contract, validation order
+ * and error cases (PrefillMoEGrouping.groupTokenExpertPairs,
+ * PrefillMoEGrouping.swift:91-192): returns TFQ_GROUP_*; err[0..1] carry the
+ * values of the Swift error case. sort_keys may be NULL. Output arrays:
+ * sorted [n_pairs], offsets/counts/groups/tiles [num_experts]. */
+int tfq_group_pairs_host(const tfq_pair *pairs, int64_t n_pairs, int64_t query_count,
+                         int64_t top_k, int64_t num_experts, int64_t tile_expert_count,
+                         const uint64_t *sort_keys, int64_t n_sort_keys, tfq_pair *sorted,
+                         uint32_t *offsets, uint32_t *counts, tfq_group *groups,
+                         int64_t *n_groups, tfq_group_tile *tiles, int64_t *n_tiles,
+                         int64_t err[2]);
+
+/* Grouped routed experts over the sorted pairs: for every tile, gate/up on
+ * the MFMA cores with act = fp16(gelu(gate)·up) into act_scratch
+ * [T*top_k][f] (row = sorted position), then down with each row written to
+ * route_partials[(token*top_k + rank)*d ...] (fp16 [T*top_k][d]); rows of
+ * (token, rank) slots without a pair are left untouched. max_tiles is the
+ * launch bound (TFQ_MOE_MAX_TILES); the device *n_tiles decides. Replaces
+ * PrefillGroupedRoutedMoE.encodeStreamedBatched
+ * (S/Kernels/Prefill/MoE/PrefillGroupedRoutedMoE.swift:446-527).
+ * Contract: d, f multiples of 64; hidden rows 16-byte aligned. */
+int tfq_moe_grouped(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
+                    const tfq_pair *sorted, const tfq_tile *tiles, const uint32_t *n_tiles,
+                    uint32_t max_tiles, const uint16_t *hidden, uint32_t hidden_stride,
+                    uint32_t d, uint32_t f, uint32_t top_k, uint16_t *act_scratch,
+                    uint16_t *route_partials);
+
+/* h2[t][d] = fp16(Σ_r fma(w[t][r], partials[(t*top_k + r)*d + ...])) in rank
+ * order. Replaces PrefillMoE.encodeReduceTokenMajor
+ * (S/Kernels/Prefill/MoE/PrefillMoE.swift:11-38). */
+int tfq_moe_combine(tfq_ctx *ctx, void *stream, const uint16_t *route_partials,
+                    const uint16_t *route_weights, uint16_t *h2, uint32_t T, uint32_t top_k,
+                    uint32_t d);
+
+/* Workspace bytes of tfq_moe_prefill. */
+size_t tfq_moe_prefill_workspace_bytes(uint32_t T, uint32_t top_k, uint32_t num_experts,
+                                       uint32_t d, uint32_t f);
+
+/* Routed MoE of a prefill chunk, all on the device: tfq_prefill_router ->
+ * tfq_moe_group -> tfq_moe_grouped -> tfq_moe_combine. out_indices /
+ * out_weights [T][top_k] receive the routing; h2 [T][d] fp16. */
+int tfq_moe_prefill(tfq_ctx *ctx, void *stream, const tfq_router *router,
+                    const tfq_expert_pool *pool, const uint16_t *hidden,
+                    uint32_t hidden_stride, uint32_t T, uint32_t d, uint32_t f, uint32_t top_k,
+                    uint16_t *h2, uint32_t *out_indices, uint16_t *out_weights, void *workspace,
+                    size_t workspace_bytes);
+
 /* ----------------------------------------------------------------- loader -- */
 
 /* fp16 <- BF16, elementwise on the device. Values outside the exactly

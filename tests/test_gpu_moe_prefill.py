@@ -1,0 +1,232 @@
+"""GPU parity of the routed-MoE prefill path: prefill router, device
+grouping, grouped gate/up/down on the matrix cores and the token-major
+combine, against the CPU oracle (tests mirror
+T/Kernels/Prefill/PrefillRouterTests.swift, PrefillMoEGroupingTests.swift,
+PrefillGroupedRoutedMoETests+Execution.swift and PrefillMoETests.swift).
+Routing indices and the grouping are bit-exact; floating-point outputs are
+held to max relative error <= 1e-3 (RelError.compute)."""
+import numpy as np
+import pytest
+
+import oracle
+from edgeexpert_amd import ops, synth
+from edgeexpert_amd.runtime import DeviceBuffer
+from helpers import bf16_to_f16_exact, from_f16_bits
+
+pytestmark = pytest.mark.gpu
+TOL = oracle.Tolerance.north_star
+
+
+def _dev(a):
+    return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def _oracle_pool(pool_bytes, offs, stride):
+    return pool_bytes, oracle.ExpertOffsets(*[int(offs[k]) for k in synth.OFFSET_ORDER]), stride
+
+
+# ------------------------------------------------------------- router ----
+
+@pytest.mark.parametrize("T,E,D,k", [(7, 16, 128, 8), (512, 128, 2816, 8), (33, 256, 512, 64)])
+def test_prefill_router_matches_per_token_reference(ctx, stream, T, E, D, k):
+    # PrefillRouterTests.swift:33-101: block router == per-row router
+    W, S, B = synth.int8_matrix(2, f"pr/{E}x{D}", E, D)
+    stride = D + 64
+    H = np.zeros((T, stride), np.uint16)
+    H[:, :D] = synth.f16_vector(2, f"pr/h{T}", T * D).reshape(T, D)
+    eff = synth.f16_bits(np.abs(synth.normal(synth.seed_key(2, "pr/eff"), D)) + 0.5)
+    gain = synth.f16_bits(synth.uniform24(synth.seed_key(2, "pr/gain"), E, 0.6, 1.4))
+    router = ops.Router(_dev(W), _dev(S), _dev(B), E, _dev(eff), _dev(gain))
+    idx, w16 = _dev(np.zeros(T * k, np.uint32)), _dev(np.zeros(T * k, np.uint16))
+    wf, logits = _dev(np.zeros(T * k, np.float32)), _dev(np.zeros(T * E, np.float32))
+    ops.PrefillRouter(ctx).encode_gemma4_block(stream, router, _dev(H), stride, T, D, k, idx, w16, logits,
+                                               out_weights_f32=wf)
+    stream.sync()
+    got_idx = idx.download(np.uint32).reshape(T, k)
+    got_w = wf.download(np.float32).reshape(T, k)
+    ref_idx, ref_w = oracle.prefill_router(W, S, B, from_f16_bits(H[:, :D]), k, eff=from_f16_bits(eff),
+                                           expert_scale=from_f16_bits(gain))
+    assert np.array_equal(got_idx, ref_idx)
+    assert np.max(np.abs(got_w - ref_w)) < 1e-5
+    lg = logits.download(np.float32).reshape(T, E)
+    for t in (0, T - 1):
+        ref_l = oracle.router_logits(W, S, B, from_f16_bits(H[t, :D]), from_f16_bits(eff))
+        assert oracle.rel_error(lg[t], ref_l) < 1e-5
+
+
+# ----------------------------------------------------------- grouping ----
+
+def _device_group(ctx, stream, idx, w16, T, k, E):
+    n = T * k
+    mt = ops.max_tiles(T, k, E)
+    bufs = dict(sorted=_dev(np.zeros(n, ops.PAIR_DTYPE)), offsets=_dev(np.zeros(E, np.uint32)),
+                counts=_dev(np.zeros(E, np.uint32)), tiles=_dev(np.zeros(mt, ops.TILE_DTYPE)),
+                n_tiles=_dev(np.zeros(1, np.uint32)), status=_dev(np.full(1, 77, np.uint32)))
+    ops.PrefillMoEGrouping(ctx).encode(stream, _dev(idx), _dev(w16), T, k, E, bufs["sorted"],
+                                       bufs["offsets"], bufs["counts"], bufs["tiles"],
+                                       bufs["n_tiles"], bufs["status"])
+    stream.sync()
+    out = {"sorted": bufs["sorted"].download(np.uint8, n * 16).view(ops.PAIR_DTYPE),
+           "offsets": bufs["offsets"].download(np.uint32, E), "counts": bufs["counts"].download(np.uint32, E),
+           "n_tiles": int(bufs["n_tiles"].download(np.uint32, 1)[0]),
+           "status": int(bufs["status"].download(np.uint32, 1)[0])}
+    out["tiles"] = bufs["tiles"].download(np.uint8, mt * 16).view(ops.TILE_DTYPE)[:out["n_tiles"]]
+    return out, bufs
+
+
+@pytest.mark.parametrize("T,k,E,label", [(512, 8, 128, "zipf"), (32, 8, 128, "t32"), (1, 8, 16, "one"),
+                                         (1024, 8, 256, "big"), (4, 3, 6, "kat")])
+def test_device_grouping_bit_exact(ctx, stream, T, k, E, label):
+    if label == "t32":
+        # PrefillMoEGroupingTests.swift:175-203 pressure pattern
+        idx = np.array([[(t + r * 7) % 74 for r in range(8)] for t in range(32)], np.uint32)
+        w16 = np.arange(T * k, dtype=np.uint16).reshape(T, k)
+    elif label == "kat":
+        # PrefillMoEGroupingTests.swift:5-53, token-major input
+        idx = np.array([[3, 1, 4], [1, 3, 2], [4, 3, 1], [5, 1, 4]], np.uint32)
+        w16 = np.arange(10, 22, dtype=np.uint16).reshape(4, 3)
+    else:
+        idx, w16 = synth.zipf_routing(4, f"dg/{label}", T, E, k)
+    got, _ = _device_group(ctx, stream, idx, w16, T, k, E)
+    pairs = ops.PrefillRouter.make_token_expert_pairs(idx, w16, T, k)
+    ref = oracle.group_pairs(pairs.astype(oracle.PAIR_DTYPE), T, k, E, 16)
+    assert got["status"] == 0
+    assert got["sorted"].tobytes() == ref["sorted"].tobytes()
+    assert np.array_equal(got["offsets"], ref["offsets"])
+    assert np.array_equal(got["counts"], ref["counts"])
+    # tiles: every expert's run cut into <=128-row tiles, in expert order
+    exp_tiles = []
+    for e in range(E):
+        c = int(ref["counts"][e])
+        for s0 in range(0, c, 128):
+            exp_tiles.append((e, int(ref["offsets"][e]) + s0, min(128, c - s0), 0))
+    assert [tuple(int(v) for v in t) for t in got["tiles"]] == exp_tiles
+    if label == "kat":
+        assert list(got["sorted"]["expert"]) == [1, 1, 1, 1, 2, 3, 3, 3, 4, 4, 4, 5]
+        assert list(got["offsets"]) == [0xFFFFFFFF, 0, 4, 5, 8, 11]
+
+
+def test_device_grouping_rejects_out_of_range_expert(ctx, stream):
+    idx = np.array([[0, 1], [2, 9]], np.uint32)
+    got, _ = _device_group(ctx, stream, idx, np.zeros((2, 2), np.uint16), 2, 2, 4)
+    assert got["status"] == 8 and got["n_tiles"] == 0          # expertOutOfRange
+    assert list(got["counts"]) == [0, 0, 0, 0]
+
+
+# ----------------------------------------------------- grouped experts ----
+
+def _synthetic_rows(rows, cols, expert, role):
+    # PrefillGroupedRoutedMoETests.syntheticRows (PrefillGroupedRoutedMoETests.swift:207-216)
+    r = np.arange(rows)[:, None]
+    c = np.arange(cols)[None, :]
+    return (np.float32(expert + 1) * np.float32(0.001) + np.float32(role + 1) * np.float32(0.003)
+            + ((r % 7) - 3).astype(np.float32) * np.float32(0.0004)
+            + ((c % 11) - 5).astype(np.float32) * np.float32(0.0002)).astype(np.float32)
+
+
+def _synthetic_pool(num_experts, d, f):
+    # makeSyntheticExpertPool (PrefillGroupedRoutedMoETests.swift:113-175), fp16 scale words
+    offsets, stride = synth.expert_layout(d, f, align=256)
+    pool = np.zeros(num_experts * stride, np.uint8)
+    for e in range(num_experts):
+        for role, (proj, rows, cols) in enumerate((("gate", f, d), ("up", f, d), ("down", d, f))):
+            W, S, B = oracle.quantize_int4_matrix(_synthetic_rows(rows, cols, e, role))
+            for part, arr in (("w", W), ("s", bf16_to_f16_exact(S)), ("b", bf16_to_f16_exact(B))):
+                raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
+                o = e * stride + offsets[f"{proj}_{part}"]
+                pool[o:o + raw.size] = raw
+    return pool, offsets, stride
+
+
+def _run_grouped(ctx, stream, pool_bytes, offs, stride, E, idx, w16, hidden16, stride_h, T, k, d, f):
+    got, bufs = _device_group(ctx, stream, idx, w16, T, k, E)
+    pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs)
+    act = _dev(np.zeros(T * k * f, np.uint16))
+    partials = _dev(np.full(T * k * d, np.float16(-77).view(np.uint16), np.uint16))
+    h2 = _dev(np.zeros(T * d, np.uint16))
+    g = ops.PrefillGroupedRoutedMoE(ctx)
+    g.encode(stream, pool, bufs["sorted"], bufs["tiles"], bufs["n_tiles"], ops.max_tiles(T, k, E),
+             _dev(hidden16), stride_h, d, f, k, act, partials)
+    g.encode_reduce_token_major(stream, partials, _dev(w16), h2, T, k, d)
+    stream.sync()
+    return got, partials.download(np.uint16), h2.download(np.uint16)
+
+
+def test_grouped_partials_match_reference_small(ctx, stream):
+    # PrefillGroupedRoutedMoETests+Execution.swift:8-103 (d=64, f=64, 3 tokens, top-2, 16 experts)
+    d, f, T, k, E = 64, 64, 3, 2, 16
+    pool_bytes, offs, stride = _synthetic_pool(E, d, f)
+    idx = np.array([[2, 0], [1, 2], [0, 1]], np.uint32)
+    w16 = synth.f16_bits(np.array([[0.125, 0.1875]] * 3, np.float32))
+    hidden = (((np.arange(T * d) % 17) - 8) * 0.01).astype(np.float16).view(np.uint16)
+    got, parts, h2 = _run_grouped(ctx, stream, pool_bytes, offs, stride, E, idx, w16, hidden, d, T, k, d, f)
+    ref = oracle.grouped_route_partials(got["sorted"].astype(oracle.PAIR_DTYPE), hidden, d,
+                                        *_oracle_pool(pool_bytes, offs, stride), k, d, f, T)
+    gp, rp = from_f16_bits(parts), from_f16_bits(ref)
+    assert np.max(np.abs(gp - rp)) <= 0.0015                       # the reference's bound
+    assert oracle.rel_error(gp, rp) < TOL
+    ref_h2 = from_f16_bits(oracle.reduce_token_major(ref, w16.ravel(), T, k, d))
+    assert oracle.rel_error(from_f16_bits(h2), ref_h2) < TOL
+
+
+def test_combine_matches_reference(ctx, stream):
+    # PrefillMoETests.swift:8-44 (SplitMix64 seed 0x4D0E2026, 3 tokens x top-8 x 64)
+    rows, k, d = 3, 8, 64
+    r = oracle.SplitMix64(0x4D0E2026)
+    partials = r.uniforms(rows * k * d, -2.0, 2.0).astype(np.float16).view(np.uint16)
+    weights = r.uniforms(rows * k, -1.0, 1.0).astype(np.float16).view(np.uint16)
+    h2 = _dev(np.full(rows * d, np.float16(-19.0).view(np.uint16), np.uint16))
+    ops.PrefillGroupedRoutedMoE(ctx).encode_reduce_token_major(stream, _dev(partials), _dev(weights), h2,
+                                                               rows, k, d)
+    stream.sync()
+    got = from_f16_bits(h2.download(np.uint16))
+    ref = from_f16_bits(oracle.reduce_token_major(partials, weights, rows, k, d))
+    assert np.max(np.abs(got - ref)) <= 2e-3                        # the reference's bound
+    assert oracle.rel_error(got, ref) < TOL
+
+
+def test_grouped_moe_baseline_config3_sampled(ctx, stream):
+    # 512 tokens x top-8 over 128 experts (D=2816, F=704),
+    # Zipf(1.1) popularity; oracle on the pairs of 12 sampled tokens.
+    T, k, E, d, f = 512, 8, 128, 2816, 704
+    pool_bytes, offs, stride = synth.expert_pool(0, "c3/experts", E, d, f)
+    idx, w16 = synth.zipf_routing(0, "c3/route", T, E, k)
+    hidden = synth.f16_vector(0, "c3/x", T * d)
+    got, parts, h2 = _run_grouped(ctx, stream, pool_bytes, offs, stride, E, idx, w16, hidden, d, T, k, d, f)
+    assert got["status"] == 0
+    toks = np.array([0, 1, 77, 128, 255, 256, 300, 383, 400, 450, 510, 511])
+    sel = got["sorted"][np.isin(got["sorted"]["token"], toks)]
+    ref = oracle.grouped_route_partials(sel.astype(oracle.PAIR_DTYPE), hidden, d,
+                                        *_oracle_pool(pool_bytes, offs, stride), k, d, f, T)
+    gp, rp = from_f16_bits(parts).reshape(T, k, d), from_f16_bits(ref).reshape(T, k, d)
+    rel = oracle.rel_error(gp[toks], rp[toks])
+    assert rel < TOL, f"partials rel={rel}"
+    ref_h2 = from_f16_bits(oracle.reduce_token_major(ref, w16.ravel(), T, k, d)).reshape(T, d)
+    rel = oracle.rel_error(from_f16_bits(h2).reshape(T, d)[toks], ref_h2[toks])
+    assert rel < TOL, f"h2 rel={rel}"
+
+
+def test_moe_prefill_end_to_end(ctx, stream):
+    # router -> grouping -> grouped experts -> combine through one call
+    T, k, E, d, f = 64, 8, 32, 512, 256
+    pool_bytes, offs, stride = synth.expert_pool(1, "pf/experts", E, d, f)
+    Wr, Sr, Br = synth.int8_matrix(1, "pf/router", E, d)
+    hidden = synth.f16_vector(1, "pf/x", T * d)
+    router = ops.Router(_dev(Wr), _dev(Sr), _dev(Br), E)
+    pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs)
+    wsb = ops.moe_prefill_workspace_bytes(T, k, E, d, f)
+    ws = DeviceBuffer(wsb)
+    idx, w16, h2 = _dev(np.zeros(T * k, np.uint32)), _dev(np.zeros(T * k, np.uint16)), _dev(np.zeros(T * d, np.uint16))
+    ops.moe_prefill(ctx, stream, router, pool, _dev(hidden), d, T, d, f, k, h2, idx, w16, ws, wsb)
+    stream.sync()
+    ref_idx, ref_w = oracle.prefill_router(Wr, Sr, Br, from_f16_bits(hidden).reshape(T, d), k)
+    got_idx = idx.download(np.uint32).reshape(T, k)
+    assert np.array_equal(got_idx, ref_idx)
+    w_dev = w16.download(np.uint16)
+    pairs = ops.PrefillRouter.make_token_expert_pairs(got_idx, w_dev, T, k)
+    grp = oracle.group_pairs(pairs.astype(oracle.PAIR_DTYPE), T, k, E, 16)
+    ref = oracle.grouped_route_partials(grp["sorted"], hidden, d, *_oracle_pool(pool_bytes, offs, stride),
+                                        k, d, f, T)
+    ref_h2 = from_f16_bits(oracle.reduce_token_major(ref, w_dev, T, k, d))
+    rel = oracle.rel_error(from_f16_bits(h2.download(np.uint16)), ref_h2)
+    assert rel < TOL, f"rel={rel}"
