@@ -22,7 +22,8 @@ def _dev(a):
 
 
 def _oracle_pool(pool_bytes, offs, stride):
-    return pool_bytes, oracle.ExpertOffsets(*[int(offs[k]) for k in synth.OFFSET_ORDER]), stride
+    """(pool, stride, offsets) in the argument order of oracle.grouped_route_partials."""
+    return pool_bytes, stride, oracle.ExpertOffsets(*[int(offs[k]) for k in synth.OFFSET_ORDER])
 
 
 # ------------------------------------------------------------- router ----
@@ -47,7 +48,8 @@ def test_prefill_router_matches_per_token_reference(ctx, stream, T, E, D, k):
     ref_idx, ref_w = oracle.prefill_router(W, S, B, from_f16_bits(H[:, :D]), k, eff=from_f16_bits(eff),
                                            expert_scale=from_f16_bits(gain))
     assert np.array_equal(got_idx, ref_idx)
-    assert np.max(np.abs(got_w - ref_w)) < 1e-5
+    # softmax weights move by ~|Δlogit| (fp32 summation-order differences, ~1e-6 of |logit|)
+    assert oracle.rel_error(got_w, ref_w) < 1e-4
     lg = logits.download(np.float32).reshape(T, E)
     for t in (0, T - 1):
         ref_l = oracle.router_logits(W, S, B, from_f16_bits(H[t, :D]), from_f16_bits(eff))
@@ -163,10 +165,13 @@ def test_grouped_partials_match_reference_small(ctx, stream):
     ref = oracle.grouped_route_partials(got["sorted"].astype(oracle.PAIR_DTYPE), hidden, d,
                                         *_oracle_pool(pool_bytes, offs, stride), k, d, f, T)
     gp, rp = from_f16_bits(parts), from_f16_bits(ref)
-    assert np.max(np.abs(gp - rp)) <= 0.0015                       # the reference's bound
-    assert oracle.rel_error(gp, rp) < TOL
+    # The reference's bound (absolute 1.5e-3). These synthetic experts give
+    # partials of ~1e-6, inside fp16's subnormal range, so a relative bound is
+    # not meaningful here; the config-3 test below holds the 1e-3 relative bar.
+    assert np.max(np.abs(gp - rp)) <= 0.0015
+    assert np.array_equal(parts == np.float16(-77).view(np.uint16), ref == np.float16(-99).view(np.uint16))
     ref_h2 = from_f16_bits(oracle.reduce_token_major(ref, w16.ravel(), T, k, d))
-    assert oracle.rel_error(from_f16_bits(h2), ref_h2) < TOL
+    assert np.max(np.abs(from_f16_bits(h2) - ref_h2)) <= 0.0015
 
 
 def test_combine_matches_reference(ctx, stream):
