@@ -61,6 +61,24 @@ class PairT(C.Structure):
                 ("weight_bits", C.c_uint32)]
 
 
+class DecodeLayerWeights(C.Structure):
+    """tfq_decode_layer_weights (include/tfq.h)."""
+    _fields_ = [("input_norm", C.c_void_p), ("q_proj", Q4Matrix), ("k_proj", Q4Matrix),
+                ("v_proj", Q4Matrix), ("q_norm", C.c_void_p), ("k_norm", C.c_void_p),
+                ("o_proj", Q4Matrix), ("post_attention_norm", C.c_void_p), ("pre_ffn_norm", C.c_void_p),
+                ("pre_ffn2_norm", C.c_void_p), ("router", RouterDesc), ("experts", ExpertPoolDesc),
+                ("shared_gate", Q4Matrix), ("shared_up", Q4Matrix), ("shared_down", Q4Matrix),
+                ("post_ffn1_norm", C.c_void_p), ("post_ffn2_norm", C.c_void_p),
+                ("post_ffn_norm", C.c_void_p), ("layer_scalar", C.c_float)]
+
+
+class DecodeLayerShape(C.Structure):
+    """tfq_decode_layer_shape (include/tfq.h)."""
+    _fields_ = [(n, C.c_uint32) for n in ("d", "num_q_heads", "num_kv_heads", "head_dim", "rotated_pairs",
+                                          "window", "expert_f", "shared_f", "top_k")] + \
+               [(n, C.c_float) for n in ("eps", "rope_theta", "attn_scale")]
+
+
 _P = C.c_void_p
 _U32 = C.c_uint32
 _I = C.c_int
@@ -100,6 +118,12 @@ SIGNATURES = {
     "tfq_moe_prefill_workspace_bytes": [_U32, _U32, _U32, _U32, _U32],
     "tfq_moe_prefill": [_P, _P, C.POINTER(RouterDesc), C.POINTER(ExpertPoolDesc), _P, _U32, _U32,
                         _U32, _U32, _U32, _P, _P, _P, _P, C.c_size_t],
+    "tfq_attention_workspace_bytes": [_U32, _U32, _U32, _U32],
+    "tfq_attention_decode": [_P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, C.c_float, _P,
+                             C.c_size_t],
+    "tfq_decode_layer_workspace_bytes": [C.POINTER(DecodeLayerShape), _U32],
+    "tfq_decode_layer": [_P, _P, C.POINTER(DecodeLayerWeights), C.POINTER(DecodeLayerShape), _P, _P, _P,
+                         _P, _U32, _P, _P, _P, C.c_size_t],
     "tfq_rt_device_count": [C.POINTER(_I)],
     "tfq_rt_set_device": [_I],
     "tfq_rt_device_info": [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t],
@@ -125,6 +149,8 @@ SIGNATURES = {
 }
 _RES = {"tfq_destroy": None, "tfq_status_string": C.c_char_p,
         "tfq_moe_prefill_workspace_bytes": C.c_size_t,
+        "tfq_attention_workspace_bytes": C.c_size_t,
+        "tfq_decode_layer_workspace_bytes": C.c_size_t,
         "tfq_last_error_message": C.c_char_p}
 
 _lib = None

@@ -22,6 +22,27 @@ inline uint32_t grid_for_rows(uint64_t rows, uint32_t rows_per_block) {
     return (uint32_t)(g > kMaxGridBlocks ? kMaxGridBlocks : g);
 }
 
+// Validates how a kernel stages its activation vector (NormArg, abi_types.h).
+inline int check_stage(const NormArg& na) {
+    switch (na.mode) {
+    case kStageCopy:
+        return TFQ_OK;
+    case kStageNorm:
+        break;
+    case kStagePostAttn:
+    case kStageResidual:
+        if (!na.attn || !na.attn_w)
+            return fail(TFQ_E_INVAL, "post-attention staging needs the attention output and its norm weight");
+        break;
+    default:
+        return fail(TFQ_E_INVAL, "unknown staging mode %u", na.mode);
+    }
+    if (!(na.eps > 0.0f)) return fail(TFQ_E_INVAL, "RMSNorm eps must be positive");
+    return TFQ_OK;
+}
+
+inline NormArg stage_copy() { return NormArg{nullptr, nullptr, nullptr, 0.0f, kStageCopy}; }
+
 // S/Kernels/Quant/DequantInt4GEMV.swift:5-181 (encode and encodeTgx share one kernel here:
 // x always lives in LDS) and S/Kernels/Fusions/FusedQKVGEMV.swift:4-157.
 class DequantInt4GEMV {
@@ -29,25 +50,30 @@ public:
     explicit DequantInt4GEMV(const Module& m) : m_(m) {}
 
     // DequantInt4GEMV.encode (DequantInt4GEMV.swift:84-127).
+    // residual (may be null): y = fp16(residual + W·x); stage: how x is staged.
     int encode(void* stream, const void* weights, const uint16_t* scales, const uint16_t* biases,
-               const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n) const {
+               const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n,
+               const uint16_t* residual = nullptr, const NormArg& stage = stage_copy()) const {
         Q4Multi mats{};
-        mats.m[0] = {static_cast<const uint8_t*>(weights), scales, biases, y, m, 0};
+        mats.m[0] = {static_cast<const uint8_t*>(weights), scales, biases, y, residual, m, 0};
         mats.nmat = 1;
         mats.total_rows = m;
+        mats.norm = stage;
         return launch_multi(stream, mats, x, n);
     }
 
     // FusedQKVGEMV.encode (FusedQKVGEMV.swift:92-156): rows mq + 2*mkv in one launch.
     int encode_qkv(void* stream, const tfq_q4_matrix& q, const tfq_q4_matrix& k,
                    const tfq_q4_matrix& v, const uint16_t* x, uint16_t* yq, uint16_t* yk,
-                   uint16_t* yv, uint32_t mq, uint32_t mkv, uint32_t n) const {
+                   uint16_t* yv, uint32_t mq, uint32_t mkv, uint32_t n,
+                   const NormArg& stage = stage_copy()) const {
         Q4Multi mats{};
-        mats.m[0] = {static_cast<const uint8_t*>(q.weights), q.scales, q.biases, yq, mq, 0};
-        mats.m[1] = {static_cast<const uint8_t*>(k.weights), k.scales, k.biases, yk, mkv, 0};
-        mats.m[2] = {static_cast<const uint8_t*>(v.weights), v.scales, v.biases, yv, mkv, 0};
+        mats.m[0] = {static_cast<const uint8_t*>(q.weights), q.scales, q.biases, yq, nullptr, mq, 0};
+        mats.m[1] = {static_cast<const uint8_t*>(k.weights), k.scales, k.biases, yk, nullptr, mkv, 0};
+        mats.m[2] = {static_cast<const uint8_t*>(v.weights), v.scales, v.biases, yv, nullptr, mkv, 0};
         mats.nmat = 3;
         mats.total_rows = mq + 2 * mkv;
+        mats.norm = stage;
         return launch_multi(stream, mats, x, n);
     }
 
@@ -57,6 +83,7 @@ private:
             return fail(TFQ_E_INVAL, "n=%u must be a positive multiple of 64", n);
         if (n > kMaxN) return fail(TFQ_E_UNSUPPORTED, "n=%u exceeds %u", n, kMaxN);
         if (!x || !aligned(x, 2)) return fail(TFQ_E_INVAL, "x must be non-null and 2-byte aligned");
+        if (int rc = check_stage(mats.norm)) return rc;
         for (uint32_t i = 0; i < mats.nmat; ++i) {
             const Q4Mat& q = mats.m[i];
             if (q.rows == 0) return fail(TFQ_E_INVAL, "matrix %u has zero rows", i);
@@ -64,7 +91,7 @@ private:
                 return fail(TFQ_E_INVAL, "matrix %u has a null pointer", i);
             // 128-bit weight loads (the reference needs only 2-byte alignment, DequantInt4GEMV.swift:97-102).
             if (!aligned(q.w, 16)) return fail(TFQ_E_INVAL, "weights of matrix %u are not 16-byte aligned", i);
-            if (!aligned(q.s, 2) || !aligned(q.b, 2) || !aligned(q.y, 2))
+            if (!aligned(q.s, 2) || !aligned(q.b, 2) || !aligned(q.y, 2) || !aligned(q.r, 2))
                 return fail(TFQ_E_INVAL, "scales/biases/y of matrix %u are not 2-byte aligned", i);
         }
         const SegShape sh = seg_shape(n / 32, 2);
@@ -120,7 +147,7 @@ public:
                              const uint16_t* effective_scale, const uint16_t* per_expert_scale,
                              uint32_t* out_indices, uint16_t* out_weights, float* out_weights_f32,
                              float* out_logits, uint32_t num_experts, uint32_t d, uint32_t top_k,
-                             void* workspace) const {
+                             void* workspace, const NormArg& stage = stage_copy()) const {
         if (d == 0 || d % TFQ_GROUP_SIZE != 0)
             return fail(TFQ_E_INVAL, "d=%u must be a positive multiple of 64", d);
         if (d > 4096) return fail(TFQ_E_UNSUPPORTED, "router d=%u exceeds 4096", d);
@@ -133,6 +160,7 @@ public:
         if (!aligned(weights, 16)) return fail(TFQ_E_INVAL, "weights are not 16-byte aligned");
         if (!aligned(workspace, 16)) return fail(TFQ_E_INVAL, "workspace is not 16-byte aligned");
         if (!aligned(out_indices, 4)) return fail(TFQ_E_INVAL, "indices are not 4-byte aligned");
+        if (int rc = check_stage(stage)) return rc;
         // Logits land in out_logits when given, else in the workspace; a
         // one-wavefront launch then selects (stream order is the only sync).
         float* logits = out_logits ? out_logits : static_cast<float*>(workspace);
@@ -141,9 +169,10 @@ public:
         std::snprintf(name, sizeof(name), "tfq_router_logits_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
         const uint32_t grid = (num_experts + rows_per_block - 1) / rows_per_block;
+        NormArg na = stage;
         void* args[] = {&weights, &scales, &biases, &hidden, &effective_scale, &logits,
-                        &num_experts, &d};
-        int rc = launch(m_.get(name), grid, kBlock, d * 4, stream, args, name);
+                        &num_experts, &d, &na};
+        int rc = launch(m_.get(name), grid, kBlock, d * 6, stream, args, name);
         if (rc) return rc;
         void* sargs[] = {&logits, &per_expert_scale, &out_indices, &out_weights, &out_weights_f32,
                          &num_experts, &top_k};
@@ -153,9 +182,11 @@ public:
     // encodeRoutedPersistentPhase1U16Load / ...SubsetU16Load (MoE.swift:234-310).
     int encode_phase1(void* stream, const tfq_expert_pool& pool, const uint32_t* indices,
                       const uint16_t* x, uint16_t* acts, const uint32_t* active_slots,
-                      uint32_t active_count, uint32_t d, uint32_t f, uint32_t top_k) const {
+                      uint32_t active_count, uint32_t d, uint32_t f, uint32_t top_k,
+                      const NormArg& stage = stage_copy()) const {
         int rc = check_pool(pool, d, f, top_k);
         if (rc) return rc;
+        if ((rc = check_stage(stage))) return rc;
         if (d > kMaxN) return fail(TFQ_E_UNSUPPORTED, "d=%u exceeds %u", d, kMaxN);
         if (!indices || !x || !acts) return fail(TFQ_E_INVAL, "null pointer argument");
         if (active_count == 0) return TFQ_OK;               // nothing to do (MoE.swift:283)
@@ -167,7 +198,8 @@ public:
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_moe_phase1_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
-        void* args[] = {&kp, &indices, &active_slots, &active_count, &top_k, &x, &acts, &d, &f};
+        NormArg na = stage;
+        void* args[] = {&kp, &indices, &active_slots, &active_count, &top_k, &x, &acts, &d, &f, &na};
         return launch(m_.get(name), grid_for_rows((uint64_t)active_count * f, rows_per_block),
                       kBlock, d * 2, stream, args, name);
     }
@@ -233,7 +265,7 @@ public:
 
     int encode(void* stream, const uint16_t* x, const tfq_q4_matrix& gate, const tfq_q4_matrix& up,
                const tfq_q4_matrix& down, uint16_t* y, uint32_t d, uint32_t f,
-               uint16_t* act_scratch) const {
+               uint16_t* act_scratch, const NormArg& stage = stage_copy()) const {
         if (d == 0 || f == 0 || d % 64 || f % 64)
             return fail(TFQ_E_INVAL, "dimension mismatch: d=%u f=%u must be multiples of 64", d, f);
         if (d > kMaxN || f > kMaxN) return fail(TFQ_E_UNSUPPORTED, "d/f exceed %u", kMaxN);
@@ -242,13 +274,15 @@ public:
             return fail(TFQ_E_INVAL, "null pointer argument");
         if (!aligned(gate.weights, 16) || !aligned(up.weights, 16))
             return fail(TFQ_E_INVAL, "gate/up weights must be 16-byte aligned");
-        Q4Mat g = {static_cast<const uint8_t*>(gate.weights), gate.scales, gate.biases, nullptr, f, 0};
-        Q4Mat u = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases, nullptr, f, 0};
+        if (int rc = check_stage(stage)) return rc;
+        Q4Mat g = {static_cast<const uint8_t*>(gate.weights), gate.scales, gate.biases, nullptr, nullptr, f, 0};
+        Q4Mat u = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases, nullptr, nullptr, f, 0};
+        NormArg na = stage;
         const SegShape sh = seg_shape(d / 32, 2);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_gate_up_act_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
-        void* args[] = {&g, &u, &x, &act_scratch, &d, &f};
+        void* args[] = {&g, &u, &x, &act_scratch, &d, &f, &na};
         int rc = launch(m_.get(name), grid_for_rows(f, rows_per_block), kBlock, d * 2, stream, args,
                         name);
         if (rc) return rc;
@@ -361,7 +395,7 @@ public:
         uint32_t E = r.num_experts;
         void* args[] = {(void*)&r.weights, (void*)&r.scales, (void*)&r.biases, &hidden, &stride,
                         (void*)&r.effective_scale, &logits, &E, &d};
-        int rc = launch2(m_, name, gx, T, kBlock, d * 4, stream, args);
+        int rc = launch2(m_, name, gx, T, kBlock, d * 6, stream, args);
         if (rc) return rc;
         void* sargs[] = {&logits, (void*)&r.per_expert_scale, &out_idx, &out_w, &out_wf, &E, &top_k};
         return launch2(m_, "tfq_prefill_select", T, 1, 256, 0, stream, sargs);
@@ -431,6 +465,211 @@ public:
 
 private:
     const Module& m_;
+};
+
+// S/Kernels/Attention/Attention.swift:26-420: encodeFull (window 0) and
+// encodeSWA (window > 0) as split-K partial + combine launches.
+class Attention {
+public:
+    explicit Attention(const Module& m) : m_(m) {}
+
+    static uint32_t kv_start(uint32_t seq_len, uint32_t window) {
+        return (window > 0 && seq_len > window) ? seq_len - window : 0;   // Attention.swift:254
+    }
+    static uint32_t chunks(uint32_t seq_len, uint32_t window) {
+        return (seq_len - kv_start(seq_len, window) + 63) / 64;
+    }
+    static size_t workspace_bytes(uint32_t head_dim, uint32_t nq, uint32_t seq_len, uint32_t window) {
+        if (seq_len == 0) return 0;
+        const size_t nc = chunks(seq_len, window);
+        return ((size_t)nq * nc * head_dim * 4 + 255) / 256 * 256 + ((size_t)nq * nc * 2 * 4 + 255) / 256 * 256;
+    }
+
+    // q: fp16 [nq][hd]; caches fp16 [capacity][nkv][hd]; out fp16 [nq][hd].
+    // With epi.q_norm set, q is the raw projection and position seq_len-1 of
+    // the caches holds the raw k/v of the new token (rewritten in place).
+    int encode(void* stream, const uint16_t* q, uint16_t* k_cache, uint16_t* v_cache, uint16_t* out,
+               uint32_t hd, uint32_t nq, uint32_t nkv, uint32_t seq_len, uint32_t window, float scale,
+               const AttnEpilogue& epi, void* workspace, size_t workspace_bytes_given) const {
+        if (nkv == 0 || nq == 0 || nq % nkv != 0)
+            return fail(TFQ_E_INVAL, "numQHeads must be a multiple of numKVHeads for GQA");
+        const uint32_t G = nq / nkv;
+        if (hd != 128 && hd != 256) return fail(TFQ_E_UNSUPPORTED, "head_dim=%u (supported: 128, 256)", hd);
+        if (G != 1 && G != 2 && G != 4)
+            return fail(TFQ_E_UNSUPPORTED, "GQA group %u (supported: 1, 2, 4)", G);
+        if (seq_len == 0) return fail(TFQ_E_INVAL, "attention requires at least one KV position");
+        if (!q || !k_cache || !v_cache || !out || !workspace) return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(workspace, 16))
+            return fail(TFQ_E_INVAL, "KV caches and workspace must be 16-byte aligned");
+        if (!aligned(q, 2) || !aligned(out, 2)) return fail(TFQ_E_INVAL, "q/out must be 2-byte aligned");
+        if (!(scale > 0.0f) && !(scale < 0.0f)) return fail(TFQ_E_INVAL, "scale must be non-zero");
+        if (epi.q_norm) {
+            if (!epi.k_norm) return fail(TFQ_E_INVAL, "q/k epilogue needs both norm weights");
+            if (epi.rotated_pairs > hd / 2) return fail(TFQ_E_INVAL, "rotatedPairs exceeds head_dim/2");
+            if (!(epi.eps > 0.0f) || !(epi.theta > 0.0f))
+                return fail(TFQ_E_INVAL, "epilogue eps and rope theta must be positive");
+        }
+        const uint32_t nc = chunks(seq_len, window);
+        if (nc > 1024) return fail(TFQ_E_UNSUPPORTED, "more than 65536 visible keys");
+        if (workspace_bytes_given < workspace_bytes(hd, nq, seq_len, window))
+            return fail(TFQ_E_INVAL, "attention workspace too small");
+        float* part_o = static_cast<float*>(workspace);
+        float* part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                  ((size_t)nq * nc * hd * 4 + 255) / 256 * 256);
+        uint32_t ks = kv_start(seq_len, window);
+        AttnEpilogue e = epi;
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_attn_partial_h%u_g%u", hd, G);
+        void* a1[] = {&q, &k_cache, &v_cache, &nkv, &seq_len, &ks, &scale, &e, &part_o, &part_ml};
+        int rc = launch2(m_, name, nc, nkv, 256, 0, stream, a1);
+        if (rc) return rc;
+        std::snprintf(name, sizeof(name), "tfq_attn_combine_h%u", hd);
+        uint32_t ncu = nc;
+        void* a2[] = {&part_o, &part_ml, &out, &ncu};
+        return launch2(m_, name, nq, 1, hd, 0, stream, a2);
+    }
+
+private:
+    const Module& m_;
+};
+
+// One Gemma 4 decoder layer for one token (RealForwardRunner.swift:2265-2862):
+// input norm + QKV, q/k/v epilogue + attention, o projection, post-attention
+// setup, router, shared expert (on a second stream), routed experts, tail.
+// The norms that the reference runs as separate kernels are recomputed while
+// each consumer stages its activation vector (NormArg), so the layer is nine
+// launches on `stream` and two on the side stream.
+class DecodeLayer {
+public:
+    DecodeLayer(const Module& m, DequantInt4GEMV& gemv, MoE& moe, SharedExpertInt4& shared, Attention& attn)
+        : m_(m), gemv_(gemv), moe_(moe), shared_(shared), attn_(attn) {}
+    ~DecodeLayer() {
+        if (fork_) (void)hipEventDestroy(fork_);
+        if (join_) (void)hipEventDestroy(join_);
+        if (side_) (void)hipStreamDestroy(side_);
+    }
+
+    struct Layout {
+        size_t q, attn, parts, parts_bytes, o, logits, idx, w, acts, sact, h1, h2, total;
+    };
+    static Layout layout(const tfq_decode_layer_shape& s, uint32_t max_seq) {
+        auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+        Layout L{};
+        size_t off = 0;
+        const size_t qd = (size_t)s.num_q_heads * s.head_dim;
+        L.q = off;      off += up(qd * 2);
+        L.attn = off;   off += up(qd * 2);
+        L.parts = off;  L.parts_bytes = Attention::workspace_bytes(s.head_dim, s.num_q_heads, max_seq, s.window);
+        off += up(L.parts_bytes);
+        L.o = off;      off += up((size_t)s.d * 2);
+        L.logits = off; off += up(TFQ_ROUTER_WORKSPACE_BYTES);
+        L.idx = off;    off += up((size_t)s.top_k * 4);
+        L.w = off;      off += up((size_t)s.top_k * 2);
+        L.acts = off;   off += up((size_t)s.top_k * s.expert_f * 2);
+        L.sact = off;   off += up((size_t)s.shared_f * 2);
+        L.h1 = off;     off += up((size_t)s.d * 2);
+        L.h2 = off;     off += up((size_t)s.d * 2);
+        L.total = off;
+        return L;
+    }
+
+    int encode(void* stream, const tfq_decode_layer_weights& w, const tfq_decode_layer_shape& s,
+               const uint16_t* hidden_in, uint16_t* hidden_out, uint16_t* k_cache, uint16_t* v_cache,
+               uint32_t position, uint32_t* out_indices, uint16_t* out_weights, void* workspace,
+               size_t workspace_bytes) {
+        if (!hidden_in || !hidden_out || !k_cache || !v_cache || !workspace)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!w.input_norm || !w.q_norm || !w.k_norm || !w.post_attention_norm || !w.pre_ffn_norm ||
+            !w.pre_ffn2_norm || !w.post_ffn1_norm || !w.post_ffn2_norm || !w.post_ffn_norm)
+            return fail(TFQ_E_INVAL, "every norm weight is required");
+        if (s.d == 0 || s.d % 64 || s.d > 4096) return fail(TFQ_E_INVAL, "d=%u must be a multiple of 64 <= 4096", s.d);
+        if (!aligned(workspace, 256)) return fail(TFQ_E_INVAL, "workspace must be 256-byte aligned");
+        const uint32_t seq_len = position + 1;
+        const Layout L = layout(s, seq_len);
+        if (workspace_bytes < L.total) return fail(TFQ_E_INVAL, "decode-layer workspace too small");
+        if (int rc = ensure_side_stream()) return rc;
+        char* ws = static_cast<char*>(workspace);
+        uint16_t* q = reinterpret_cast<uint16_t*>(ws + L.q);
+        uint16_t* attn = reinterpret_cast<uint16_t*>(ws + L.attn);
+        uint16_t* o = reinterpret_cast<uint16_t*>(ws + L.o);
+        float* logits = reinterpret_cast<float*>(ws + L.logits);
+        uint32_t* idx = out_indices ? out_indices : reinterpret_cast<uint32_t*>(ws + L.idx);
+        uint16_t* rw = out_weights ? out_weights : reinterpret_cast<uint16_t*>(ws + L.w);
+        uint16_t* acts = reinterpret_cast<uint16_t*>(ws + L.acts);
+        uint16_t* sact = reinterpret_cast<uint16_t*>(ws + L.sact);
+        uint16_t* h1 = reinterpret_cast<uint16_t*>(ws + L.h1);
+        uint16_t* h2 = reinterpret_cast<uint16_t*>(ws + L.h2);
+        const uint32_t qd = s.num_q_heads * s.head_dim, kvd = s.num_kv_heads * s.head_dim;
+        const size_t slot = (size_t)position * kvd;
+
+        // 1. input RMSNorm fused into the QKV GEMV; k and v land in the cache slot
+        const NormArg in_norm{w.input_norm, nullptr, nullptr, s.eps, kStageNorm};
+        int rc = gemv_.encode_qkv(stream, w.q_proj, w.k_proj, w.v_proj, hidden_in, q, k_cache + slot,
+                                  v_cache + slot, qd, kvd, s.d, in_norm);
+        if (rc) return rc;
+        // 2. q/k/v epilogue + attention
+        const AttnEpilogue epi{w.q_norm, w.k_norm, s.eps, s.rope_theta, s.rotated_pairs, 0};
+        rc = attn_.encode(stream, q, k_cache, v_cache, attn, s.head_dim, s.num_q_heads, s.num_kv_heads,
+                          seq_len, s.window, s.attn_scale, epi, ws + L.parts, L.parts_bytes);
+        if (rc) return rc;
+        // 3. o projection
+        rc = gemv_.encode(stream, w.o_proj.weights, w.o_proj.scales, w.o_proj.biases, attn, o, s.d, qd);
+        if (rc) return rc;
+        // 4. shared expert on the side stream, input = pre_feedforward_layernorm(h)
+        rc = hip_check(hipEventRecord(fork_, (hipStream_t)stream), "hipEventRecord");
+        if (rc) return rc;
+        rc = hip_check(hipStreamWaitEvent(side_, fork_, 0), "hipStreamWaitEvent");
+        if (rc) return rc;
+        const NormArg dense{w.pre_ffn_norm, o, w.post_attention_norm, s.eps, kStagePostAttn};
+        rc = shared_.encode(side_, hidden_in, w.shared_gate, w.shared_up, w.shared_down, h1, s.d,
+                            s.shared_f, sact, dense);
+        if (rc) return rc;
+        rc = hip_check(hipEventRecord(join_, side_), "hipEventRecord");
+        if (rc) return rc;
+        // 5. router on the no-scale norm of h
+        const NormArg router_x{nullptr, o, w.post_attention_norm, s.eps, kStagePostAttn};
+        const tfq_router& r = w.router;
+        rc = moe_.encode_router_gemma4(stream, r.weights, r.scales, r.biases, hidden_in, r.effective_scale,
+                                       r.per_expert_scale, idx, rw, nullptr, logits, r.num_experts, s.d,
+                                       s.top_k, logits, router_x);
+        if (rc) return rc;
+        // 6. routed experts on pre_feedforward_layernorm_2(h); phase 2 without residual
+        const NormArg routed{w.pre_ffn2_norm, o, w.post_attention_norm, s.eps, kStagePostAttn};
+        rc = moe_.encode_phase1(stream, w.experts, idx, hidden_in, acts, nullptr, s.top_k, s.d, s.expert_f,
+                                s.top_k, routed);
+        if (rc) return rc;
+        rc = moe_.encode_phase2(stream, w.experts, idx, acts, rw, nullptr, h2, s.d, s.expert_f, s.top_k);
+        if (rc) return rc;
+        // 7. tail
+        rc = hip_check(hipStreamWaitEvent((hipStream_t)stream, join_, 0), "hipStreamWaitEvent");
+        if (rc) return rc;
+        float eps = s.eps, scalar = w.layer_scalar;
+        uint32_t d = s.d;
+        void* ta[] = {(void*)&hidden_in, &o, (void*)&w.post_attention_norm, &h1, (void*)&w.post_ffn1_norm,
+                      &h2, (void*)&w.post_ffn2_norm, (void*)&w.post_ffn_norm, &eps, &scalar, &hidden_out, &d};
+        return launch2(m_, "tfq_layer_tail", 1, 1, 1024, 3 * s.d * 2, stream, ta);
+    }
+
+    // Creates the side stream and its fork/join events (tfq_create calls it,
+    // so that no stream is created while the caller captures a graph).
+    int ensure_side_stream() {
+        if (side_) return TFQ_OK;
+        int rc = hip_check(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking), "hipStreamCreate");
+        if (rc) return rc;
+        rc = hip_check(hipEventCreateWithFlags(&fork_, hipEventDisableTiming), "hipEventCreate");
+        if (rc) return rc;
+        return hip_check(hipEventCreateWithFlags(&join_, hipEventDisableTiming), "hipEventCreate");
+    }
+
+private:
+
+    const Module& m_;
+    DequantInt4GEMV& gemv_;
+    MoE& moe_;
+    SharedExpertInt4& shared_;
+    Attention& attn_;
+    hipStream_t side_ = nullptr;
+    hipEvent_t fork_ = nullptr, join_ = nullptr;
 };
 
 }  // namespace tfq

@@ -46,6 +46,12 @@ static std::vector<std::string> kernel_names() {
                           "tfq_moe_grouped_down", "tfq_moe_combine"})
         names.push_back(n);
     names.push_back("tfq_convert_bf16_f16");
+    for (const char* hd : {"128", "256"}) {
+        for (const char* g : {"1", "2", "4"})
+            names.push_back(std::string("tfq_attn_partial_h") + hd + "_g" + g);
+        names.push_back(std::string("tfq_attn_combine_h") + hd);
+    }
+    names.push_back("tfq_layer_tail");
     return names;
 }
 
@@ -95,7 +101,11 @@ struct tfq_ctx {
     PrefillRouter* prouter = nullptr;
     PrefillMoEGrouping* grouping = nullptr;
     PrefillGroupedRoutedMoE* grouped = nullptr;
+    Attention* attn = nullptr;
+    DecodeLayer* layer = nullptr;
     ~tfq_ctx() {
+        delete layer;
+        delete attn;
         delete qmm;
         delete prouter;
         delete grouping;
@@ -131,6 +141,13 @@ int tfq_create(tfq_ctx** out, const char* code_object_path) {
     c->prouter = new PrefillRouter(c->module);
     c->grouping = new PrefillMoEGrouping(c->module);
     c->grouped = new PrefillGroupedRoutedMoE(c->module);
+    c->attn = new Attention(c->module);
+    c->layer = new DecodeLayer(c->module, *c->int4, *c->moe, *c->shared, *c->attn);
+    rc = c->layer->ensure_side_stream();
+    if (rc) {
+        delete c;
+        return rc;
+    }
     *out = c;
     return TFQ_OK;
 }
@@ -249,6 +266,39 @@ int tfq_shared_expert_q4(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* gate,
     TFQ_REQUIRE_CTX(ctx);
     if (!gate || !up || !down) return fail(TFQ_E_INVAL, "null matrix descriptor");
     return ctx->shared->encode(stream, x, *gate, *up, *down, y, d, f, act_scratch);
+}
+
+size_t tfq_attention_workspace_bytes(uint32_t head_dim, uint32_t num_q_heads, uint32_t seq_len,
+                                     uint32_t window) {
+    return Attention::workspace_bytes(head_dim, num_q_heads, seq_len, window);
+}
+
+int tfq_attention_decode(tfq_ctx* ctx, void* stream, const uint16_t* q, const uint16_t* k_cache,
+                         const uint16_t* v_cache, uint16_t* out, uint32_t head_dim,
+                         uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t seq_len,
+                         uint32_t window, float scale, void* workspace, size_t workspace_bytes) {
+    TFQ_REQUIRE_CTX(ctx);
+    const AttnEpilogue none{nullptr, nullptr, 0.0f, 0.0f, 0, 0};
+    // without the epilogue the kernels only read the caches
+    return ctx->attn->encode(stream, q, const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache),
+                             out, head_dim, num_q_heads, num_kv_heads, seq_len, window, scale, none,
+                             workspace, workspace_bytes);
+}
+
+size_t tfq_decode_layer_workspace_bytes(const tfq_decode_layer_shape* shape, uint32_t max_seq_len) {
+    if (!shape || max_seq_len == 0) return 0;
+    return DecodeLayer::layout(*shape, max_seq_len).total;
+}
+
+int tfq_decode_layer(tfq_ctx* ctx, void* stream, const tfq_decode_layer_weights* weights,
+                     const tfq_decode_layer_shape* shape, const uint16_t* hidden_in,
+                     uint16_t* hidden_out, uint16_t* k_cache, uint16_t* v_cache, uint32_t position,
+                     uint32_t* out_indices, uint16_t* out_weights, void* workspace,
+                     size_t workspace_bytes) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!weights || !shape) return fail(TFQ_E_INVAL, "null weights or shape");
+    return ctx->layer->encode(stream, *weights, *shape, hidden_in, hidden_out, k_cache, v_cache, position,
+                              out_indices, out_weights, workspace, workspace_bytes);
 }
 
 int tfq_gemm_q4g64(tfq_ctx* ctx, void* stream, const void* weights, const uint16_t* scales,

@@ -5,13 +5,50 @@
 
 namespace tfq {
 
-// One int4 matrix and its fp16 output, as seen by a multi-matrix launch.
+// One int4 matrix and its fp16 output, as seen by a multi-matrix launch;
+// r (may be null) is an fp16 residual added to the fp32 result before the
+// output is rounded: y = fp16(r + W·x).
 struct Q4Mat {
     const uint8_t* w;
     const uint16_t* s;
     const uint16_t* b;
     uint16_t* y;
+    const uint16_t* r;
     uint32_t rows;
+    uint32_t pad_;
+};
+
+// How a kernel forms its fp16 activation vector a from x while staging it
+// to LDS (r(v) = 1/sqrt(mean(v^2) + eps), every intermediate rounded to fp16
+// where a separate kernel would have stored it):
+//   kStageCopy      a = x
+//   kStageNorm      a = fp16(x * w * r(x))                (w == null: no scale)
+//   kStagePostAttn  h = fp16(x + fp16(attn * attn_w * r(attn)));
+//                   a = fp16(h * w * r(h))                (w == null: no scale)
+// kStagePostAttn is the decode layer's post-attention residual + pre-FFN (or
+// router) norm, recomputed by every block that consumes it.
+//   kStageResidual  a = h (the post-attention residual stream, no norm)
+enum StageMode : uint32_t { kStageCopy = 0, kStageNorm = 1, kStagePostAttn = 2, kStageResidual = 3 };
+
+struct NormArg {
+    const uint16_t* w;
+    const uint16_t* attn;
+    const uint16_t* attn_w;
+    float eps;
+    uint32_t mode;
+};
+
+// Gemma 4 q/k/v epilogue applied inside the decode attention kernel
+// (fused_qkv_epilogue, S/Metal/Fusions/fused.metal:86-180): per-head RMSNorm
+// of q and k with the shared head-dim weights, NeoX RoPE of the first
+// rotated_pairs pairs at the new token's position, no-scale RMSNorm of v.
+// q_norm == null disables it (plain attention).
+struct AttnEpilogue {
+    const uint16_t* q_norm;
+    const uint16_t* k_norm;
+    float eps;
+    float theta;
+    uint32_t rotated_pairs;
     uint32_t pad_;
 };
 
@@ -20,6 +57,7 @@ struct Q4Multi {
     Q4Mat m[3];
     uint32_t nmat;
     uint32_t total_rows;
+    NormArg norm;
 };
 
 // Sub-tensor byte offsets inside one routed-expert blob (MoEExpertOffsets).

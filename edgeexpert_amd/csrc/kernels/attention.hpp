@@ -1,0 +1,321 @@
+// attention.hpp — single-token GQA decode attention over an fp16 KV cache
+// (split-K over the keys), the Gemma 4 q/k/v epilogue fused into it, and the
+// decode layer's tail.
+//
+// Cache layout [capacity][num_kv_heads][HD] fp16 for K and for V (the
+// reference's, S/Metal/Attention/attention.metal:316-580). Keys
+// [kv_start, seq_len) are cut into 64-key chunks; block (chunk, kv head)
+// computes, for each of the G query heads sharing that kv head,
+//     m = max_j s_j,  l = Σ_j e^{s_j - m},  O[d] = Σ_j e^{s_j - m} V[j][d],
+// s_j = scale · q·k_j (fp32 accumulate of exact fp16 products), and stores
+// (m, l, O) in fp32. A second kernel merges the chunks of each query head:
+//     out[d] = fp16(Σ_c e^{m_c - M} O_c[d] / Σ_c e^{m_c - M} l_c),  M = max_c m_c,
+// which is the exact softmax of AttentionRef.apply
+// (V/Reference/Attention/Attention.swift:14-104) regrouped by chunk.
+//
+// Mapping inside a block (256 threads): for q·k, 16 lanes own one key (each
+// lane two 16-byte pieces of the 512-byte row, so one load instruction covers
+// 4 whole rows); for p·V, HD/8 threads own one key row with 16-byte loads and
+// 2048/HD groups of them split the 64 keys, reduced through LDS in group
+// order. K and V loads of the whole chunk are issued before anything else.
+#pragma once
+
+#include "common.hpp"
+
+namespace tfq {
+
+constexpr uint32_t kAttnChunk = 64;
+constexpr uint32_t kAttnThreads = 256;
+constexpr uint32_t kAttnKeyLanes = 16;
+
+// NeoX rotation of pair i at `pos`: angle = pos · theta^(-2i/HD)
+// (fused.metal:58-72; V/Reference/Attention/RoPE.swift:70-110). The angle is
+// formed in fp64 so that it carries no fp32 error at long positions.
+__device__ __forceinline__ void rope_table(float* __restrict__ c, float* __restrict__ s, uint32_t pairs,
+                                           uint32_t hd, uint32_t pos, float theta) {
+    for (uint32_t i = threadIdx.x; i < pairs; i += blockDim.x) {
+        const double ang = (double)pos * pow((double)theta, -2.0 * (double)i / (double)hd);
+        c[i] = (float)cos(ang);
+        s[i] = (float)sin(ang);
+    }
+}
+
+// Per-head RMSNorm of one fp16 vector of HD values by one wavefront:
+// dst[i] = fp16(src[i] * w[i] * r(src)) (w == null: no scale).
+template <int HD>
+__device__ __forceinline__ void wave_head_norm(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                               const uint16_t* __restrict__ w, float eps) {
+    const uint32_t lane = threadIdx.x & 63u;
+    constexpr int PER = HD / 64;
+    float v[PER];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        v[i] = h2f(src[lane + 64 * i]);
+        ss = fmaf(v[i], v[i], ss);
+    }
+    ss = seg_sum<kWave>(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const uint32_t e = lane + 64 * i;
+        const float xw = w ? v[i] * h2f(w[e]) : v[i];
+        dst[e] = f2h(xw * inv);
+    }
+}
+
+template <int HD, int G>
+struct AttnLds {
+    uint16_t q[G][HD];
+    uint16_t kp[HD];
+    uint16_t vp[HD];
+    float rc[HD / 2];
+    float rs[HD / 2];
+    float p[G][kAttnChunk];
+    float ml[G][2];
+    float red[2048 / HD][G][HD];
+};
+
+// One (chunk, kv head) block. q: fp16 [num_q_heads][HD] (raw projection when
+// the epilogue is on); part_o: fp32 [num_q_heads][nchunks][HD];
+// part_ml: fp32 [num_q_heads][nchunks][2].
+template <int HD, int G>
+__device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uint16_t* __restrict__ kc,
+                                             uint16_t* __restrict__ vc, uint32_t nkv, uint32_t seq_len,
+                                             uint32_t kv_start, float scale, const AttnEpilogue& epi,
+                                             float* __restrict__ part_o, float* __restrict__ part_ml) {
+    static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
+    constexpr uint32_t CPL = HD / 128;                 // 16-byte pieces per lane per key (q·k)
+    constexpr uint32_t TPR = HD / 8;                   // threads per V row
+    constexpr uint32_t VGROUPS = kAttnThreads / TPR;
+    constexpr uint32_t KPG = kAttnChunk / VGROUPS;     // keys per V group
+    constexpr uint32_t KSTEPS = kAttnChunk / (kAttnThreads / kAttnKeyLanes);
+    __shared__ __attribute__((aligned(16))) AttnLds<HD, G> L;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t chunk = blockIdx.x, h = blockIdx.y, nchunks = gridDim.x;
+    const uint32_t c0 = kv_start + chunk * kAttnChunk;
+    const uint32_t n = seq_len - c0 < kAttnChunk ? seq_len - c0 : kAttnChunk;
+    const size_t row = (size_t)nkv * HD;               // halves between consecutive positions
+    const uint16_t* kbase = kc + (size_t)c0 * row + (size_t)h * HD;
+    const uint16_t* vbase = vc + (size_t)c0 * row + (size_t)h * HD;
+    const bool epi_on = epi.q_norm != nullptr;
+    const uint32_t pos = seq_len - 1;                  // the new token
+    const bool own_pos = epi_on && pos >= c0 && pos < c0 + n;
+
+    // 1. issue the chunk's K and V loads
+    const uint32_t sl = lane & (kAttnKeyLanes - 1);
+    uint4 kr[KSTEPS][CPL];
+#pragma unroll
+    for (uint32_t st = 0; st < KSTEPS; ++st) {
+        const uint32_t j = st * (kAttnThreads / kAttnKeyLanes) + (tid >> 4);
+#pragma unroll
+        for (uint32_t cc = 0; cc < CPL; ++cc)
+            kr[st][cc] = j < n ? *reinterpret_cast<const uint4*>(kbase + j * row + 8u * (sl + 16u * cc))
+                               : make_uint4(0, 0, 0, 0);
+    }
+    const uint32_t vg = tid / TPR, vl = tid % TPR;
+    uint4 vr[KPG];
+#pragma unroll
+    for (uint32_t i = 0; i < KPG; ++i) {
+        const uint32_t j = vg * KPG + i;
+        vr[i] = j < n ? *reinterpret_cast<const uint4*>(vbase + j * row + 8u * vl) : make_uint4(0, 0, 0, 0);
+    }
+
+    // 2. queries (and the new token's k/v) through the epilogue
+    for (uint32_t i = tid; i < G * HD; i += kAttnThreads)
+        (&L.q[0][0])[i] = q[(size_t)h * G * HD + i];
+    if (epi_on) {
+        rope_table(L.rc, L.rs, epi.rotated_pairs, HD, pos, epi.theta);
+        if (own_pos) {
+            const uint16_t* kn = kc + (size_t)pos * row + (size_t)h * HD;
+            const uint16_t* vn = vc + (size_t)pos * row + (size_t)h * HD;
+            for (uint32_t i = tid; i < HD; i += kAttnThreads) {
+                L.kp[i] = kn[i];
+                L.vp[i] = vn[i];
+            }
+        }
+        __syncthreads();
+        const uint32_t nvec = G + (own_pos ? 2u : 0u);
+        for (uint32_t v = wave; v < nvec; v += kAttnThreads / 64) {
+            uint16_t* buf = v < G ? L.q[v] : (v == G ? L.kp : L.vp);
+            const uint16_t* w = v < G ? epi.q_norm : (v == G ? epi.k_norm : nullptr);
+            wave_head_norm<HD>(buf, buf, w, epi.eps);
+        }
+        __syncthreads();
+        const uint32_t nrot = G + (own_pos ? 1u : 0u);
+        for (uint32_t i = tid; i < nrot * epi.rotated_pairs; i += kAttnThreads) {
+            const uint32_t v = i / epi.rotated_pairs, pr = i % epi.rotated_pairs;
+            uint16_t* buf = v < G ? L.q[v] : L.kp;
+            const float x0 = h2f(buf[pr]), x1 = h2f(buf[pr + HD / 2]);
+            buf[pr] = f2h(x0 * L.rc[pr] - x1 * L.rs[pr]);
+            buf[pr + HD / 2] = f2h(x0 * L.rs[pr] + x1 * L.rc[pr]);
+        }
+        __syncthreads();
+        if (own_pos) {            // the cache keeps the processed k/v of the new token
+            uint16_t* kn = kc + (size_t)pos * row + (size_t)h * HD;
+            uint16_t* vn = vc + (size_t)pos * row + (size_t)h * HD;
+            for (uint32_t i = tid; i < HD; i += kAttnThreads) {
+                kn[i] = L.kp[i];
+                vn[i] = L.vp[i];
+            }
+        }
+    } else {
+        __syncthreads();
+    }
+
+    // 3. scores
+    h2 qv[G][CPL][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (uint32_t cc = 0; cc < CPL; ++cc) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(&L.q[g][8u * (sl + 16u * cc)]);
+            qv[g][cc][0] = __builtin_bit_cast(h2, raw.x);
+            qv[g][cc][1] = __builtin_bit_cast(h2, raw.y);
+            qv[g][cc][2] = __builtin_bit_cast(h2, raw.z);
+            qv[g][cc][3] = __builtin_bit_cast(h2, raw.w);
+        }
+#pragma unroll
+    for (uint32_t st = 0; st < KSTEPS; ++st) {
+        const uint32_t j = st * (kAttnThreads / kAttnKeyLanes) + (tid >> 4);
+        float acc[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+#pragma unroll
+        for (uint32_t cc = 0; cc < CPL; ++cc) {
+            uint4 kk = kr[st][cc];
+            if (own_pos && c0 + j == pos) kk = *reinterpret_cast<const uint4*>(&L.kp[8u * (sl + 16u * cc)]);
+            const h2 k4[4] = {__builtin_bit_cast(h2, kk.x), __builtin_bit_cast(h2, kk.y),
+                              __builtin_bit_cast(h2, kk.z), __builtin_bit_cast(h2, kk.w)};
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[g] = __builtin_amdgcn_fdot2(k4[e], qv[g][cc][e], acc[g], false);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float sdot = seg_sum<kAttnKeyLanes>(acc[g]);
+            if (sl == 0) L.p[g][j] = j < n ? sdot * scale : -__builtin_inff();
+        }
+    }
+    __syncthreads();
+
+    // 4. chunk softmax statistics, one wavefront per query head
+    for (uint32_t g = wave; g < (uint32_t)G; g += kAttnThreads / 64) {
+        const float sv = L.p[g][lane];
+        float m = sv;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+        const float e = lane < n ? expf(sv - m) : 0.0f;
+        const float l = seg_sum<kWave>(e);
+        L.p[g][lane] = e;
+        if (lane == 0) {
+            L.ml[g][0] = m;
+            L.ml[g][1] = l;
+        }
+    }
+    __syncthreads();
+
+    // 5. p·V
+    float o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < KPG; ++i) {
+        const uint32_t j = vg * KPG + i;
+        uint4 vv = vr[i];
+        if (own_pos && c0 + j == pos) vv = *reinterpret_cast<const uint4*>(&L.vp[8u * vl]);
+        const h8 v8 = __builtin_bit_cast(h8, vv);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float pj = L.p[g][j];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pj, (float)v8[e], o[g][e]);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) L.red[vg][g][8u * vl + e] = o[g][e];
+    __syncthreads();
+    for (uint32_t i = tid; i < G * HD; i += kAttnThreads) {
+        const uint32_t g = i / HD, d = i % HD;
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t r = 0; r < VGROUPS; ++r) s += L.red[r][g][d];
+        const size_t qh = (size_t)h * G + g;
+        part_o[(qh * nchunks + chunk) * HD + d] = s;
+    }
+    if (tid < (uint32_t)G) {
+        const size_t qh = (size_t)h * G + tid;
+        part_ml[(qh * nchunks + chunk) * 2 + 0] = L.ml[tid][0];
+        part_ml[(qh * nchunks + chunk) * 2 + 1] = L.ml[tid][1];
+    }
+}
+
+// Merge of the chunks of query head blockIdx.x; HD threads, d = threadIdx.x.
+template <int HD>
+__device__ __forceinline__ void attn_combine(const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                                             uint16_t* __restrict__ out, uint32_t nchunks) {
+    __shared__ float wgt[1024];
+    __shared__ float tot;
+    const uint32_t qh = blockIdx.x, d = threadIdx.x;
+    const float* ml = part_ml + (size_t)qh * nchunks * 2;
+    if (threadIdx.x < 64) {
+        float m = -__builtin_inff();
+        for (uint32_t c = threadIdx.x; c < nchunks; c += 64) m = fmaxf(m, ml[2 * c]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+        float l = 0.0f;
+        for (uint32_t c = threadIdx.x; c < nchunks; c += 64) {
+            const float w = expf(ml[2 * c] - m);
+            wgt[c] = w;
+            l = fmaf(w, ml[2 * c + 1], l);
+        }
+        l = seg_sum<kWave>(l);
+        if (threadIdx.x == 0) tot = l;
+    }
+    __syncthreads();
+    const float* po = part_o + (size_t)qh * nchunks * HD + d;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (uint32_t c = 0; c < nchunks; ++c) acc = fmaf(wgt[c], po[(size_t)c * HD], acc);
+    out[(size_t)qh * HD + d] = f2h(acc / tot);
+}
+
+// Decode-layer tail (one block): recomputes the post-attention residual
+// stream h = fp16(hidden + fp16(attn·w_post_attn·r(attn))), normalises the
+// shared-expert output h1 (post_feedforward_layernorm_1) and the routed output
+// h2 (post_feedforward_layernorm_2), adds them, normalises the sum
+// (post_feedforward_layernorm), adds it to h and scales by the layer scalar:
+//     out = fp16(fp16(h + fp16(h12·w_post_ffn·r(h12))) · fp16(layer_scalar)),
+//     h12 = fp16(fp16(h1·w_sp·r(h1)) + fp16(h2·w_pf2·r(h2)))
+// (fused_post_attn_setup / rmsnorm / fused_layer_tail,
+// S/Metal/Fusions/fused.metal:199-231,270-375). Dynamic LDS: 3·D halves.
+__device__ __forceinline__ void layer_tail(const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ attn,
+                                           const uint16_t* __restrict__ w_post_attn,
+                                           const uint16_t* __restrict__ h1, const uint16_t* __restrict__ w_sp,
+                                           const uint16_t* __restrict__ h2, const uint16_t* __restrict__ w_pf2,
+                                           const uint16_t* __restrict__ w_pf, float eps, float layer_scalar,
+                                           uint16_t* __restrict__ out, uint32_t D) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t tail_lds[];
+    uint16_t* hb = tail_lds;
+    uint16_t* ab = tail_lds + D;
+    uint16_t* bb = tail_lds + 2 * D;
+    stage_act(hidden, hb, D, {nullptr, attn, w_post_attn, eps, kStageResidual});
+    stage_act(h1, ab, D, {w_sp, nullptr, nullptr, eps, kStageNorm});
+    stage_act(h2, bb, D, {w_pf2, nullptr, nullptr, eps, kStageNorm});
+    for (uint32_t i = threadIdx.x; i < D; i += blockDim.x) bb[i] = f2h(h2f(ab[i]) + h2f(bb[i]));
+    __syncthreads();
+    rmsnorm_lds(bb, D, w_pf, eps);
+    const float sc = h2f(f2h(layer_scalar));
+    for (uint32_t i = threadIdx.x; i < D; i += blockDim.x) {
+        const float r = h2f(f2h(h2f(hb[i]) + h2f(bb[i])));
+        out[i] = f2h(r * sc);
+    }
+}
+
+}  // namespace tfq

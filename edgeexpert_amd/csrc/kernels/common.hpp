@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "abi_types.h"
+
 namespace tfq {
 
 constexpr int kGroup = 64;       // affine group size along the reduction axis
@@ -116,10 +118,35 @@ __device__ __forceinline__ float dot16_q8(const uint4 w, const float* x) {
     return d;
 }
 
-// Copies n fp16 values to LDS (16-byte transfers when x is 16-byte aligned),
-// then synchronises the block.
-__device__ __forceinline__ void stage_xh(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
-                                         uint32_t n) {
+// Sum of v over the block (every thread receives it); wave sums first, then
+// the per-wave totals in wave order (deterministic).
+__device__ __forceinline__ float block_sum(float v) {
+    __shared__ float part[16];
+    v = seg_sum<kWave>(v);
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) part[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (uint32_t i = 0; i < nwaves; ++i) t += part[i];
+    return t;
+}
+
+// 1/sqrt(mean(x^2) + eps) of an fp16 vector held in LDS
+// (V/Reference/Primitives/RmsNorm.swift:18-22 in the reference checkout).
+__device__ __forceinline__ float lds_inv_rms(const uint16_t* __restrict__ lds, uint32_t n, float eps) {
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = h2f(lds[i]);
+        ss = fmaf(v, v, ss);
+    }
+    const float total = block_sum(ss);
+    return 1.0f / sqrtf(total / (float)n + eps);
+}
+
+// Copies n fp16 values to LDS (16-byte transfers when x is 16-byte aligned).
+__device__ __forceinline__ void copy_to_lds(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
+                                            uint32_t n) {
     if ((((uintptr_t)x) & 15u) == 0 && (n & 7u) == 0) {
         const uint4* src = reinterpret_cast<const uint4*>(x);
         uint4* dst = reinterpret_cast<uint4*>(lds);
@@ -127,6 +154,48 @@ __device__ __forceinline__ void stage_xh(const uint16_t* __restrict__ x, uint16_
     } else {
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lds[i] = x[i];
     }
+}
+
+// lds[i] <- fp16(lds[i] * w[i] * r(lds)) in place (w == null: no scale);
+// RmsNorm.swift:14-43 forms the product x·w first, then applies the scale.
+__device__ __forceinline__ void rmsnorm_lds(uint16_t* __restrict__ lds, uint32_t n,
+                                            const uint16_t* __restrict__ w, float eps) {
+    const float inv = lds_inv_rms(lds, n, eps);
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float xw = w ? h2f(lds[i]) * h2f(w[i]) : h2f(lds[i]);
+        lds[i] = f2h(xw * inv);
+    }
+    __syncthreads();
+}
+
+// Stages the activation vector of a kernel into LDS as NormArg describes.
+// Synchronises the block.
+__device__ __forceinline__ void stage_act(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
+                                          uint32_t n, const NormArg& na) {
+    copy_to_lds(x, lds, n);
+    __syncthreads();
+    if (na.mode == kStagePostAttn || na.mode == kStageResidual) {
+        // attention-output norm, then the residual add, each rounded to fp16
+        // (fused_post_attn_setup, S/Metal/Fusions/fused.metal:199-231)
+        float ss = 0.0f;
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+            const float v = h2f(na.attn[i]);
+            ss = fmaf(v, v, ss);
+        }
+        const float inv = 1.0f / sqrtf(block_sum(ss) / (float)n + na.eps);
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+            const uint16_t an = f2h(h2f(na.attn[i]) * h2f(na.attn_w[i]) * inv);
+            lds[i] = f2h(h2f(lds[i]) + h2f(an));
+        }
+        __syncthreads();
+    }
+    if (na.mode == kStageNorm || na.mode == kStagePostAttn) rmsnorm_lds(lds, n, na.w, na.eps);
+}
+
+// Plain staging (no normalisation).
+__device__ __forceinline__ void stage_xh(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
+                                         uint32_t n) {
+    copy_to_lds(x, lds, n);
     __syncthreads();
 }
 

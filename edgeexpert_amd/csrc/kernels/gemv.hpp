@@ -22,12 +22,13 @@
 
 namespace tfq {
 
-// Row r of a multi-matrix launch -> (weights row, scales row, biases row, y slot).
+// Row r of a multi-matrix launch -> (weights row, scales row, biases row, y slot, residual slot).
 struct Q4Row {
     const uint8_t* w;
     const uint16_t* s;
     const uint16_t* b;
     uint16_t* y;
+    const uint16_t* r;
 };
 
 __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, uint32_t row_bytes,
@@ -37,15 +38,17 @@ __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, 
     const uint16_t* s = mats.m[0].s;
     const uint16_t* b = mats.m[0].b;
     uint16_t* y = mats.m[0].y;
+    const uint16_t* res = mats.m[0].r;
     if (mats.nmat > 1 && r >= mats.m[0].rows) {
         r -= mats.m[0].rows;
-        w = mats.m[1].w; s = mats.m[1].s; b = mats.m[1].b; y = mats.m[1].y;
+        w = mats.m[1].w; s = mats.m[1].s; b = mats.m[1].b; y = mats.m[1].y; res = mats.m[1].r;
         if (mats.nmat > 2 && r >= mats.m[1].rows) {
             r -= mats.m[1].rows;
-            w = mats.m[2].w; s = mats.m[2].s; b = mats.m[2].b; y = mats.m[2].y;
+            w = mats.m[2].w; s = mats.m[2].s; b = mats.m[2].b; y = mats.m[2].y; res = mats.m[2].r;
         }
     }
-    return {w + (size_t)r * row_bytes, s + (size_t)r * ngroups, b + (size_t)r * ngroups, y + r};
+    return {w + (size_t)r * row_bytes, s + (size_t)r * ngroups, b + (size_t)r * ngroups, y + r,
+            res ? res + r : nullptr};
 }
 
 // int4 GEMV over 1..3 matrices with a shared x. Dynamic LDS: n halves.
@@ -86,7 +89,7 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
         }
     };
     issue(0);
-    stage_xh(x, lds_xh, n);
+    stage_act(x, lds_xh, n, mats.norm);
     XChunk xc[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -114,7 +117,10 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
         for (int r = 0; r < R; ++r) {
             const float v = seg_sum<SEG>(acc[r]);
             const uint32_t row = seg_id + (grp * R + r) * seg_total;
-            if (sl == 0 && row < total) *resolve_row(mats, row, row_bytes, ngroups).y = f2h(v);
+            if (sl == 0 && row < total) {
+                const Q4Row q = resolve_row(mats, row, row_bytes, ngroups);
+                *q.y = f2h(q.r ? h2f(*q.r) + v : v);
+            }
         }
     }
 }
@@ -235,17 +241,22 @@ constexpr uint32_t kRouterMaxTopK = 64;
 
 // logits[e] = Σ_g s·Σ q·(h⊙eff) + b·Σ(h⊙eff), fp32 (S/Metal/MoE/moe.metal:78-116).
 // Dynamic LDS: d floats.
+// With norm.w set, h is first RMS-normalised (to fp16, as a separate norm
+// kernel would store it). Dynamic LDS: d floats + d halves.
 template <int SEG, int P>
 __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
                                               const uint16_t* __restrict__ B, const uint16_t* __restrict__ h,
                                               const uint16_t* __restrict__ eff,
-                                              float* __restrict__ logits, uint32_t E, uint32_t d) {
+                                              float* __restrict__ logits, uint32_t E, uint32_t d,
+                                              NormArg norm = {nullptr, nullptr, nullptr, 0.0f, kStageCopy}) {
     extern __shared__ float lds_x[];
     q8_rows<SEG, P, 1>(
         W, S, B, lds_x, E, d,
         [&]() {
+            uint16_t* hs = reinterpret_cast<uint16_t*>(lds_x + d);
+            stage_act(h, hs, d, norm);
             for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
-                const float hv = h2f(h[i]);
+                const float hv = h2f(hs[i]);
                 lds_x[i] = eff ? hv * h2f(eff[i]) : hv;
             }
             __syncthreads();

@@ -36,7 +36,7 @@ struct GateUpRow {
 // `rowfn(row)` -> GateUpRow, `out(row, act)` for live rows (lane 0 of the segment).
 template <int SEG, int P, int R, typename RowFn, typename OutFn>
 __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uint32_t D, uint32_t total,
-                                             RowFn rowfn, OutFn out) {
+                                             const NormArg& norm, RowFn rowfn, OutFn out) {
     extern __shared__ uint16_t lds_xh[];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
@@ -73,7 +73,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
         }
     };
     issue(0);
-    stage_xh(x, lds_xh, D);
+    stage_act(x, lds_xh, D, norm);
     XChunk xc[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -118,7 +118,8 @@ template <int SEG, int P, int R>
 __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint32_t* __restrict__ active_slots, uint32_t n_active,
                                            uint32_t top_k, const uint16_t* __restrict__ x,
-                                           uint16_t* __restrict__ acts, uint32_t D, uint32_t F) {
+                                           uint16_t* __restrict__ acts, uint32_t D, uint32_t F,
+                                           const NormArg& norm) {
     const uint32_t row_bytes = D >> 1;
     const uint32_t ngroups = D >> 6;
     auto slot_of = [&](uint32_t row) {
@@ -126,7 +127,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
         return active_slots ? active_slots[a] : a;
     };
     gate_up_rows<SEG, P, R>(
-        x, D, n_active * F,
+        x, D, n_active * F, norm,
         [&](uint32_t row) {
             const uint32_t slot = slot_of(row);
             const uint32_t f = row % F;
@@ -151,11 +152,11 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
 template <int SEG, int P, int R>
 __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& up,
                                                const uint16_t* __restrict__ x, uint16_t* __restrict__ act,
-                                               uint32_t D, uint32_t F) {
+                                               uint32_t D, uint32_t F, const NormArg& norm) {
     const uint32_t row_bytes = D >> 1;
     const uint32_t ngroups = D >> 6;
     gate_up_rows<SEG, P, R>(
-        x, D, F,
+        x, D, F, norm,
         [&](uint32_t f) {
             GateUpRow q{};
             q.live = true;

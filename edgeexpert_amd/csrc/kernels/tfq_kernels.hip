@@ -6,6 +6,7 @@
 // template parameters: SEG = lanes per output row (power of two, <= 64) and
 // P = 16-byte chunks per lane; the host picks the instantiation from n.
 #include "abi_types.h"
+#include "attention.hpp"
 #include "gemm.hpp"
 #include "moe_decode.hpp"
 #include "moe_prefill.hpp"
@@ -31,8 +32,21 @@ constexpr int kRowsInFlight = 2;
 #define TFQ_ROUTER(SEG, P)                                                                       \
     extern "C" __global__ __launch_bounds__(256) void tfq_router_logits_s##SEG##_p##P(           \
         const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* h,               \
-        const uint16_t* eff, float* logits, uint32_t E, uint32_t d) {                            \
-        router_logits<SEG, P>(W, S, B, h, eff, logits, E, d);                                     \
+        const uint16_t* eff, float* logits, uint32_t E, uint32_t d, NormArg norm) {              \
+        router_logits<SEG, P>(W, S, B, h, eff, logits, E, d, norm);                               \
+    }
+
+#define TFQ_ATTN(HD, G)                                                                          \
+    extern "C" __global__ __launch_bounds__(kAttnThreads) void tfq_attn_partial_h##HD##_g##G(    \
+        const uint16_t* q, uint16_t* kc, uint16_t* vc, uint32_t nkv, uint32_t seq_len,           \
+        uint32_t kv_start, float scale, AttnEpilogue epi, float* part_o, float* part_ml) {        \
+        attn_partial<HD, G>(q, kc, vc, nkv, seq_len, kv_start, scale, epi, part_o, part_ml);      \
+    }
+
+#define TFQ_ATTN_COMBINE(HD)                                                                     \
+    extern "C" __global__ __launch_bounds__(HD) void tfq_attn_combine_h##HD(                     \
+        const float* part_o, const float* part_ml, uint16_t* out, uint32_t nchunks) {             \
+        attn_combine<HD>(part_o, part_ml, out, nchunks);                                          \
     }
 
 // Prefill router: blockIdx.y selects the token (row stride `stride` halves).
@@ -48,9 +62,9 @@ constexpr int kRowsInFlight = 2;
     extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase1_s##SEG##_p##P(              \
         ExpertPool pool, const uint32_t* indices, const uint32_t* active_slots,                  \
         uint32_t n_active, uint32_t top_k, const uint16_t* x, uint16_t* acts, uint32_t D,        \
-        uint32_t F) {                                                                             \
+        uint32_t F, NormArg norm) {                                                               \
         moe_phase1<SEG, P, kRowsInFlight>(pool, indices, active_slots, n_active, top_k, x, acts, \
-                                          D, F);                                                  \
+                                          D, F, norm);                                            \
     }
 
 #define TFQ_PHASE2(P)                                                                            \
@@ -62,8 +76,9 @@ constexpr int kRowsInFlight = 2;
 
 #define TFQ_GATE_UP(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_gate_up_act_s##SEG##_p##P(             \
-        Q4Mat gate, Q4Mat up, const uint16_t* x, uint16_t* act, uint32_t D, uint32_t F) {        \
-        q4_gate_up_act<SEG, P, kRowsInFlight>(gate, up, x, act, D, F);                            \
+        Q4Mat gate, Q4Mat up, const uint16_t* x, uint16_t* act, uint32_t D, uint32_t F,          \
+        NormArg norm) {                                                                           \
+        q4_gate_up_act<SEG, P, kRowsInFlight>(gate, up, x, act, D, F, norm);                      \
     }
 
 // int4: n/32 chunks per row.
@@ -77,6 +92,14 @@ TFQ_Q4_TABLE(TFQ_GATE_UP)
 TFQ_Q8_TABLE(TFQ_Q8_GEMV)
 TFQ_Q8_TABLE(TFQ_ROUTER)
 TFQ_Q8_TABLE(TFQ_PREFILL_ROUTER)
+TFQ_ATTN(128, 1)
+TFQ_ATTN(128, 2)
+TFQ_ATTN(128, 4)
+TFQ_ATTN(256, 1)
+TFQ_ATTN(256, 2)
+TFQ_ATTN(256, 4)
+TFQ_ATTN_COMBINE(128)
+TFQ_ATTN_COMBINE(256)
 TFQ_PHASE2(1)
 TFQ_PHASE2(2)
 TFQ_PHASE2(3)
@@ -148,4 +171,11 @@ extern "C" __global__ __launch_bounds__(256) void tfq_convert_bf16_f16(const uin
                                                                          uint16_t* dst, uint64_t n,
                                                                          uint32_t* inexact) {
     convert_bf16_to_f16(src, dst, n, inexact);
+}
+
+extern "C" __global__ __launch_bounds__(1024) void tfq_layer_tail(
+    const uint16_t* hidden, const uint16_t* attn, const uint16_t* w_post_attn, const uint16_t* h1,
+    const uint16_t* w_sp, const uint16_t* h2, const uint16_t* w_pf2, const uint16_t* w_pf, float eps,
+    float layer_scalar, uint16_t* out, uint32_t D) {
+    layer_tail(hidden, attn, w_post_attn, h1, w_sp, h2, w_pf2, w_pf, eps, layer_scalar, out, D);
 }

@@ -13,8 +13,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from ._lib import (CODE_OBJECT_PATH, ExpertOffsets, ExpertPoolDesc, Q4Matrix, RouterDesc, check,
-                   lib)
+from ._lib import (CODE_OBJECT_PATH, DecodeLayerShape, DecodeLayerWeights, ExpertOffsets,
+                   ExpertPoolDesc, Q4Matrix, RouterDesc, check, lib)
 from .runtime import DeviceBuffer, Stream
 
 
@@ -368,3 +368,127 @@ def moe_prefill(context: Context, stream, router: "Router", pool: "ExpertPool", 
                                 hidden_stride, T, d, f, top_k, _addr(h2), _addr(out_indices),
                                 _addr(out_weights), _addr(workspace), workspace_bytes),
           "tfq_moe_prefill")
+
+
+# -------------------------------------------------------------- decode layer --
+
+class Attention:
+    """S/Kernels/Attention/Attention.swift:26-420 (encodeFull / encodeSWA)."""
+
+    def __init__(self, context: Context):
+        self.ctx = context
+
+    @staticmethod
+    def workspace_bytes(head_dim, num_q_heads, seq_len, window=0) -> int:
+        return lib().tfq_attention_workspace_bytes(head_dim, num_q_heads, seq_len, window)
+
+    def encode(self, stream, q, k, v, out, head_dim, num_q_heads, num_kv_heads, seq_len, workspace,
+               workspace_bytes, window=0, scale=None):
+        """window 0 = encodeFull; scale None = 1/sqrt(head_dim) (Attention.defaultScale)."""
+        if scale is None:
+            scale = 1.0 / float(np.sqrt(head_dim))
+        check(lib().tfq_attention_decode(self.ctx.handle, _s(stream), _addr(q), _addr(k), _addr(v),
+                                         _addr(out), head_dim, num_q_heads, num_kv_heads, seq_len,
+                                         window, scale, _addr(workspace), workspace_bytes),
+              "Attention.encode")
+
+
+@dataclass
+class DecodeLayerShapeSpec:
+    d: int
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    expert_f: int
+    shared_f: int
+    top_k: int
+    rotated_pairs: int | None = None
+    window: int = 0
+    eps: float = 1e-6
+    rope_theta: float = 10000.0
+    attn_scale: float = 1.0
+
+    def desc(self) -> DecodeLayerShape:
+        rp = self.head_dim // 2 if self.rotated_pairs is None else self.rotated_pairs
+        return DecodeLayerShape(self.d, self.num_q_heads, self.num_kv_heads, self.head_dim, rp,
+                                self.window, self.expert_f, self.shared_f, self.top_k, self.eps,
+                                self.rope_theta, self.attn_scale)
+
+
+@dataclass
+class DecodeLayerWeightsSpec:
+    """Device buffers of one Gemma 4 decoder layer (norm weights fp16)."""
+    input_norm: object
+    q_proj: Q4Projection
+    k_proj: Q4Projection
+    v_proj: Q4Projection
+    q_norm: object
+    k_norm: object
+    o_proj: Q4Projection
+    post_attention_norm: object
+    pre_ffn_norm: object
+    pre_ffn2_norm: object
+    router: "Router"
+    experts: "ExpertPool"
+    shared_gate: Q4Projection
+    shared_up: Q4Projection
+    shared_down: Q4Projection
+    post_ffn1_norm: object
+    post_ffn2_norm: object
+    post_ffn_norm: object
+    layer_scalar: float = 1.0
+
+    @classmethod
+    def upload(cls, w: dict) -> "DecodeLayerWeightsSpec":
+        """Copies host arrays (the keys of edgeexpert_amd.synth.decode_layer)
+        into device buffers that this spec keeps alive."""
+        def buf(a):
+            return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+        def q4(t):
+            W, S, B = t
+            rows, cols = W.shape[0], W.shape[1] * 2
+            return Q4Projection(buf(W), buf(S), buf(B), rows, cols)
+
+        E = int(w["num_experts"])
+        router = Router(buf(w["router_w"]), buf(w["router_s"]), buf(w["router_b"]), E,
+                        buf(w["router_eff"]) if w.get("router_eff") is not None else None,
+                        buf(w["router_gain"]) if w.get("router_gain") is not None else None)
+        pool = ExpertPool(buf(w["pool"]), int(w["stride"]), E, dict(w["off"]))
+        return cls(buf(w["input_norm"]), q4(w["q"]), q4(w["k"]), q4(w["v"]), buf(w["q_norm"]),
+                   buf(w["k_norm"]), q4(w["o"]), buf(w["post_attention_norm"]), buf(w["pre_ffn_norm"]),
+                   buf(w["pre_ffn2_norm"]), router, pool, q4(w["shared_gate"]), q4(w["shared_up"]),
+                   q4(w["shared_down"]), buf(w["post_ffn1_norm"]), buf(w["post_ffn2_norm"]),
+                   buf(w["post_ffn_norm"]), float(w["layer_scalar"]))
+
+    def desc(self) -> DecodeLayerWeights:
+        return DecodeLayerWeights(
+            _addr(self.input_norm), self.q_proj.desc(), self.k_proj.desc(), self.v_proj.desc(),
+            _addr(self.q_norm), _addr(self.k_norm), self.o_proj.desc(), _addr(self.post_attention_norm),
+            _addr(self.pre_ffn_norm), _addr(self.pre_ffn2_norm), self.router.desc(), self.experts.desc(),
+            self.shared_gate.desc(), self.shared_up.desc(), self.shared_down.desc(),
+            _addr(self.post_ffn1_norm), _addr(self.post_ffn2_norm), _addr(self.post_ffn_norm),
+            float(self.layer_scalar))
+
+
+def decode_layer_workspace_bytes(shape: DecodeLayerShapeSpec, max_seq_len: int) -> int:
+    sd = shape.desc()
+    return lib().tfq_decode_layer_workspace_bytes(C.byref(sd), max_seq_len)
+
+
+class DecodeLayer:
+    """One decoder layer per call: the per-layer decode sequence of
+    RealForwardRunner (S/Runtime/Inference/RealForwardRunner.swift:2265-2862)."""
+
+    def __init__(self, context: Context, weights: DecodeLayerWeightsSpec, shape: DecodeLayerShapeSpec):
+        self.ctx = context
+        self._w = weights.desc()
+        self._s = shape.desc()
+        self.keep = weights
+
+    def encode(self, stream, hidden_in, hidden_out, k_cache, v_cache, position, workspace, workspace_bytes,
+               out_indices=None, out_weights=None):
+        check(lib().tfq_decode_layer(self.ctx.handle, _s(stream), C.byref(self._w), C.byref(self._s),
+                                     _addr(hidden_in), _addr(hidden_out), _addr(k_cache), _addr(v_cache),
+                                     position, _addr(out_indices), _addr(out_weights), _addr(workspace),
+                                     workspace_bytes), "DecodeLayer.encode")

@@ -206,3 +206,46 @@ def zipf_routing(seed: int, label: str, tokens: int, num_experts: int, top_k: in
     w = np.exp(sel - sel[:, :1])
     w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
     return idx, f16_bits(w)
+
+
+def norm_weight(seed: int, label: str, n: int, lo: float = 0.5, hi: float = 1.5) -> np.ndarray:
+    """RMSNorm weight vector (fp16 bits), uniform in [lo, hi)."""
+    return f16_bits(uniform24(seed_key(seed, label), n, lo, hi))
+
+
+def decode_layer(seed: int, label: str, d: int, nq: int, nkv: int, hd: int, num_experts: int,
+                 f: int, fs: int, layer_scalar: float = 0.75) -> dict:
+    """Weights of one Gemma 4 decoder layer with the BASELINE distributions:
+    int4 g64 projections as in config 0, an int8 g64 router, num_experts
+    routed experts in one pool, an int4 shared expert, and RMSNorm weights
+    uniform in [0.5, 1.5) (so that a weight applied to the wrong element is
+    visible). Keys follow the CPU oracle's tfo_layer_weights."""
+    L = label
+    qd, kvd = nq * hd, nkv * hd
+    w = {
+        "input_norm": norm_weight(seed, L + "/input_norm", d),
+        "q": int4_matrix(seed, L + "/q", qd, d),
+        "k": int4_matrix(seed, L + "/k", kvd, d),
+        "v": int4_matrix(seed, L + "/v", kvd, d),
+        "o": int4_matrix(seed, L + "/o", d, qd),
+        "q_norm": norm_weight(seed, L + "/q_norm", hd),
+        "k_norm": norm_weight(seed, L + "/k_norm", hd),
+        "post_attention_norm": norm_weight(seed, L + "/post_attention_norm", d),
+        "pre_ffn_norm": norm_weight(seed, L + "/pre_ffn_norm", d),
+        "pre_ffn2_norm": norm_weight(seed, L + "/pre_ffn2_norm", d),
+        "post_ffn1_norm": norm_weight(seed, L + "/post_ffn1_norm", d),
+        "post_ffn2_norm": norm_weight(seed, L + "/post_ffn2_norm", d),
+        "post_ffn_norm": norm_weight(seed, L + "/post_ffn_norm", d),
+        "shared_gate": int4_matrix(seed, L + "/shared_gate", fs, d),
+        "shared_up": int4_matrix(seed, L + "/shared_up", fs, d),
+        "shared_down": int4_matrix(seed, L + "/shared_down", d, fs),
+        "num_experts": num_experts,
+        "layer_scalar": layer_scalar,
+    }
+    rw, rs, rb = int8_matrix(seed, L + "/router", num_experts, d)
+    w.update(router_w=rw, router_s=rs, router_b=rb,
+             router_eff=norm_weight(seed, L + "/router_eff", d),
+             router_gain=norm_weight(seed, L + "/router_gain", num_experts))
+    pool, offsets, stride = expert_pool(seed, L + "/experts", num_experts, d, f)
+    w.update(pool=pool, off=offsets, stride=stride)
+    return w

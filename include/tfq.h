@@ -204,6 +204,79 @@ int tfq_shared_expert_q4(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *gate,
                          const tfq_q4_matrix *up, const tfq_q4_matrix *down, const uint16_t *x,
                          uint16_t *y, uint32_t d, uint32_t f, uint16_t *act_scratch);
 
+/* -------------------------------------------------------- decode layer -- */
+
+/* Workspace bytes of tfq_attention_decode for `seq_len` positions. */
+size_t tfq_attention_workspace_bytes(uint32_t head_dim, uint32_t num_q_heads, uint32_t seq_len,
+                                     uint32_t window);
+
+/* Single-token GQA attention over an fp16 KV cache:
+ * out[h] = Σ_j softmax_j(scale · q[h]·K[j][h/G]) V[j][h/G] over the visible
+ * keys j in [max(0, seq_len - window), seq_len) (window 0: all), G =
+ * num_q_heads / num_kv_heads. q, out fp16 [num_q_heads][head_dim]; caches
+ * fp16 [capacity][num_kv_heads][head_dim]. fp32 scores and accumulation, one
+ * fp16 rounding of the output. Replaces Attention.encodeFull /
+ * Attention.encodeSWA (S/Kernels/Attention/Attention.swift:238-370).
+ * Contract: head_dim 128 or 256; G in {1, 2, 4}; seq_len in 1...65536;
+ * caches and workspace 16-byte aligned. */
+int tfq_attention_decode(tfq_ctx *ctx, void *stream, const uint16_t *q, const uint16_t *k_cache,
+                         const uint16_t *v_cache, uint16_t *out, uint32_t head_dim,
+                         uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t seq_len,
+                         uint32_t window, float scale, void *workspace, size_t workspace_bytes);
+
+/* Weights of one Gemma 4 decoder layer (all device pointers; norm weights
+ * fp16, converted from the checkpoint's BF16 with tfq_convert_bf16_to_f16). */
+typedef struct {
+    const uint16_t *input_norm;          /* [d] input_layernorm */
+    tfq_q4_matrix q_proj, k_proj, v_proj; /* [nq*hd][d], [nkv*hd][d], [nkv*hd][d] */
+    const uint16_t *q_norm, *k_norm;     /* [head_dim] per-head q/k RMSNorm */
+    tfq_q4_matrix o_proj;                /* [d][nq*hd] */
+    const uint16_t *post_attention_norm; /* [d] */
+    const uint16_t *pre_ffn_norm;        /* [d] shared-expert input (pre_feedforward_layernorm) */
+    const uint16_t *pre_ffn2_norm;       /* [d] routed-expert input (pre_feedforward_layernorm_2) */
+    tfq_router router;                   /* input: no-scale RMSNorm of the residual stream */
+    tfq_expert_pool experts;
+    tfq_q4_matrix shared_gate, shared_up, shared_down; /* [fs][d], [fs][d], [d][fs] */
+    const uint16_t *post_ffn1_norm;      /* [d] shared-expert output norm */
+    const uint16_t *post_ffn2_norm;      /* [d] routed output norm */
+    const uint16_t *post_ffn_norm;       /* [d] */
+    float layer_scalar;
+} tfq_decode_layer_weights;
+
+typedef struct {
+    uint32_t d, num_q_heads, num_kv_heads, head_dim;
+    uint32_t rotated_pairs;              /* NeoX RoPE pairs (head_dim/2: full rotation) */
+    uint32_t window;                     /* 0: full causal attention */
+    uint32_t expert_f, shared_f, top_k;
+    float eps, rope_theta, attn_scale;   /* Gemma 4: eps 1e-6, scale 1.0 */
+} tfq_decode_layer_shape;
+
+/* Workspace bytes of tfq_decode_layer for positions < max_seq_len. */
+size_t tfq_decode_layer_workspace_bytes(const tfq_decode_layer_shape *shape, uint32_t max_seq_len);
+
+/* One decoder layer for the token at `position` (keys 0..position visible):
+ *   q,k,v = QKV(rmsnorm(hidden, input_norm)); k, v written to cache slot `position`
+ *   q,k <- rope(rmsnorm_head(.., q_norm/k_norm)); v <- rmsnorm_head(v) (no scale)
+ *   a = o_proj(attention(q, K, V));  h = hidden + rmsnorm(a, post_attention_norm)
+ *   router on rmsnorm(h) (no scale) -> top_k experts and weights
+ *   h1 = shared(rmsnorm(h, pre_ffn_norm));  h2 = Σ w·expert(rmsnorm(h, pre_ffn2_norm))
+ *   out = (h + rmsnorm(rmsnorm(h1, post_ffn1) + rmsnorm(h2, post_ffn2), post_ffn)) * layer_scalar
+ * with fp16 rounding wherever the reference stores a buffer. The shared
+ * expert runs on a second stream of the context (fork/join by events, so the
+ * call can be captured into a graph); concurrent calls on one context race.
+ * hidden_out may alias hidden_in. out_indices/out_weights (may be NULL)
+ * receive the routing. Replaces the per-layer decode sequence of
+ * RealForwardRunner (S/Runtime/Inference/RealForwardRunner.swift:2265-2862:
+ * gInputNorm, gQKV, gQKVEpilogue, gAttention, gOProj, gPostAttnSetup,
+ * gRouter, gSharedFFN + gSharedNorm, routed phases 1/2, gTail).
+ * Contract: d multiple of 64, <= 4096; attention as tfq_attention_decode;
+ * experts as tfq_moe_decode; workspace 256-byte aligned. */
+int tfq_decode_layer(tfq_ctx *ctx, void *stream, const tfq_decode_layer_weights *weights,
+                     const tfq_decode_layer_shape *shape, const uint16_t *hidden_in,
+                     uint16_t *hidden_out, uint16_t *k_cache, uint16_t *v_cache, uint32_t position,
+                     uint32_t *out_indices, uint16_t *out_weights, void *workspace,
+                     size_t workspace_bytes);
+
 /* ---------------------------------------------------------------- prefill -- */
 
 #define TFQ_DTYPE_F16 0

@@ -71,6 +71,31 @@ TILE_DTYPE = np.dtype([("group_start", "<u4"), ("group_count", "<u4"),
 _P = C.c_void_p
 
 
+class Q4(C.Structure):
+    _fields_ = [("w", _P), ("s", _P), ("b", _P)]
+
+
+class LayerWeights(C.Structure):
+    """tfo_layer_weights (tfq_oracle.h)."""
+    _fields_ = [("input_norm", _P), ("q", Q4), ("k", Q4), ("v", Q4), ("o", Q4),
+                ("q_norm", _P), ("k_norm", _P), ("post_attention_norm", _P), ("pre_ffn_norm", _P),
+                ("pre_ffn2_norm", _P), ("router_w", _P), ("router_s", _P), ("router_b", _P),
+                ("router_eff", _P), ("router_gain", _P), ("num_experts", C.c_int),
+                ("pool", _P), ("stride", C.c_uint64), ("off", ExpertOffsets),
+                ("shared_gate", Q4), ("shared_up", Q4), ("shared_down", Q4),
+                ("post_ffn1_norm", _P), ("post_ffn2_norm", _P), ("post_ffn_norm", _P),
+                ("layer_scalar", C.c_float)]
+
+
+class LayerShape(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("d", "nq", "nkv", "hd", "rotated_pairs", "window", "f", "fs", "k")] + \
+               [(n, C.c_float) for n in ("eps", "theta", "scale")]
+
+
+class LayerTrace(C.Structure):
+    _fields_ = [(n, _P) for n in ("q", "attn", "o", "h", "h1", "h2")]
+
+
 def _declare(L):
     def d(name, res, *args):
         f = getattr(L, name)
@@ -110,6 +135,11 @@ def _declare(L):
     d("tfo_reduce_token_major", None, _P, _P, C.c_int, C.c_int, C.c_int, _P)
     d("tfo_gemm_int4", None, _P, _P, _P, C.c_int, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int,
       C.c_int)
+    d("tfo_rmsnorm", None, _P, _P, C.c_int, C.c_float, _P)
+    d("tfo_rope_neox", None, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float)
+    d("tfo_attention", None, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _P)
+    d("tfo_decode_layer", None, C.POINTER(LayerWeights), C.POINTER(LayerShape), _P, _P, _P, C.c_int,
+      _P, _P, _P, C.POINTER(LayerTrace))
     d("tfo_rel_error", C.c_float, _P, _P, C.c_size_t)
     d("tfo_max_abs_diff", C.c_float, _P, _P, C.c_size_t)
 
@@ -343,6 +373,84 @@ def shared_expert_int4(gate, up, down, x, d, f, fmt=FMT_F16):
     y = np.zeros(d, np.float32)
     lib().tfo_shared_expert_int4(*[_ptr(a) for a in args], fmt, _ptr(x), d, f, _ptr(y))
     return y
+
+
+# ------------------------------------------------------- decode layer ----
+
+def rmsnorm(x, w, eps):
+    """RmsNormRef.apply (V/Reference/Primitives/RmsNorm.swift:14-44); w None: no scale."""
+    x = _c(x, np.float32)
+    wv = None if w is None else _c(w, np.float32)
+    y = np.zeros_like(x)
+    lib().tfo_rmsnorm(_ptr(x), _ptr(wv), x.size, eps, _ptr(y))
+    return y
+
+
+def rope_neox(x, num_heads, head_dim, rotated_pairs, position, theta):
+    """RopeRef.applyNeox (V/Reference/Attention/RoPE.swift:70-110) on a copy of x."""
+    y = _c(x, np.float32).copy()
+    lib().tfo_rope_neox(_ptr(y), num_heads, head_dim, rotated_pairs, position, theta)
+    return y
+
+
+def attention(q, k, v, head_dim, nq, nkv, seq_len, window=0, scale=None):
+    """AttentionRef.apply (V/Reference/Attention/Attention.swift:14-104)."""
+    if scale is None:
+        scale = 1.0 / float(np.sqrt(head_dim))
+    q = _c(q, np.float32); k = _c(k, np.float32); v = _c(v, np.float32)
+    out = np.zeros(nq * head_dim, np.float32)
+    lib().tfo_attention(_ptr(q), _ptr(k), _ptr(v), head_dim, nq, nkv, seq_len, window or 0, scale,
+                        _ptr(out))
+    return out
+
+
+
+def decode_layer(w: dict, shape: dict, hidden_f16, k_cache_f16, v_cache_f16, position, trace=False):
+    """One Gemma 4 decoder layer (tfo_decode_layer). w: dict of numpy arrays
+    (fp16 bits for norms; (W, S, B) tuples for int4 matrices; 'pool', 'stride',
+    'off' for the routed experts; router_* arrays). The caches are updated in
+    place at slot `position`. Returns (out_f16, idx, weights, trace dict)."""
+    keep = []
+
+    def arr(a, dt):
+        if a is None:
+            return None
+        a = _c(a, dt)
+        keep.append(a)
+        return _ptr(a)
+
+    def q4(t):
+        W, S, B = (_c(t[0], np.uint8), _c(t[1], np.uint16), _c(t[2], np.uint16))
+        keep.extend([W, S, B])
+        return Q4(_ptr(W), _ptr(S), _ptr(B))
+
+    lw = LayerWeights(
+        input_norm=arr(w["input_norm"], np.uint16), q=q4(w["q"]), k=q4(w["k"]), v=q4(w["v"]), o=q4(w["o"]),
+        q_norm=arr(w["q_norm"], np.uint16), k_norm=arr(w["k_norm"], np.uint16),
+        post_attention_norm=arr(w["post_attention_norm"], np.uint16),
+        pre_ffn_norm=arr(w["pre_ffn_norm"], np.uint16), pre_ffn2_norm=arr(w["pre_ffn2_norm"], np.uint16),
+        router_w=arr(w["router_w"], np.uint8), router_s=arr(w["router_s"], np.uint16),
+        router_b=arr(w["router_b"], np.uint16), router_eff=arr(w.get("router_eff"), np.uint16),
+        router_gain=arr(w.get("router_gain"), np.uint16), num_experts=int(w["num_experts"]),
+        pool=arr(w["pool"], np.uint8), stride=int(w["stride"]), off=_offsets(w["off"]),
+        shared_gate=q4(w["shared_gate"]), shared_up=q4(w["shared_up"]), shared_down=q4(w["shared_down"]),
+        post_ffn1_norm=arr(w["post_ffn1_norm"], np.uint16), post_ffn2_norm=arr(w["post_ffn2_norm"], np.uint16),
+        post_ffn_norm=arr(w["post_ffn_norm"], np.uint16), layer_scalar=float(w["layer_scalar"]))
+    ls = LayerShape(**{k_: shape[k_] for k_ in ("d", "nq", "nkv", "hd", "rotated_pairs", "window", "f", "fs",
+                                                 "k", "eps", "theta", "scale")})
+    d, qd = shape["d"], shape["nq"] * shape["hd"]
+    hidden = _c(hidden_f16, np.uint16)
+    assert k_cache_f16.dtype == np.uint16 and k_cache_f16.flags.c_contiguous
+    assert v_cache_f16.dtype == np.uint16 and v_cache_f16.flags.c_contiguous
+    out = np.zeros(d, np.uint16)
+    idx = np.zeros(shape["k"], np.uint32)
+    wts = np.zeros(shape["k"], np.float32)
+    tr = {"q": np.zeros(qd, np.uint16), "attn": np.zeros(qd, np.uint16), "o": np.zeros(d, np.uint16),
+          "h": np.zeros(d, np.uint16), "h1": np.zeros(d, np.uint16), "h2": np.zeros(d, np.uint16)}
+    lt = LayerTrace(**{n: _ptr(a) for n, a in tr.items()})
+    lib().tfo_decode_layer(C.byref(lw), C.byref(ls), _ptr(hidden), _ptr(k_cache_f16), _ptr(v_cache_f16),
+                           int(position), _ptr(out), _ptr(idx), _ptr(wts), C.byref(lt) if trace else None)
+    return out, idx, wts, (tr if trace else None)
 
 
 # ------------------------------------------------------------ prefill ----

@@ -620,6 +620,204 @@ void tfo_gemm_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int f
 }
 
 /* ------------------------------------------------------------------------ */
+/* Decode layer                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* RmsNorm.swift:14-44 (vDSP_svesq, vDSP_vmul then vDSP_vsmul). */
+void tfo_rmsnorm(const float *x, const float *w, int n, float eps, float *y) {
+    double ss = 0.0;
+    for (int i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+    const float inv = 1.0f / sqrtf((float)(ss / (double)n) + eps);
+    for (int i = 0; i < n; ++i) {
+        float xw = w ? x[i] * w[i] : x[i];
+        y[i] = xw * inv;
+    }
+}
+
+/* RoPE.swift:70-110 (applyNeox). */
+void tfo_rope_neox(float *x, int num_heads, int head_dim, int rotated_pairs, int position,
+                   float theta) {
+    const int half = head_dim / 2;
+    for (int i = 0; i < rotated_pairs; ++i) {
+        const double ang = (double)position * pow((double)theta, -2.0 * (double)i / (double)head_dim);
+        const float c = (float)cos(ang), sn = (float)sin(ang);
+        for (int h = 0; h < num_heads; ++h) {
+            float *b = x + (size_t)h * head_dim;
+            const float x0 = b[i], x1 = b[half + i];
+            b[i] = x0 * c - x1 * sn;
+            b[half + i] = x0 * sn + x1 * c;
+        }
+    }
+}
+
+/* Attention.swift:14-104. */
+void tfo_attention(const float *q, const float *k, const float *v, int hd, int nq, int nkv,
+                   int seq_len, int window, float scale, float *out) {
+    const int group = nq / nkv;
+    const int start = (window > 0 && seq_len > window) ? seq_len - window : 0;
+    const int n = seq_len - start;
+    double *p = (double *)malloc(sizeof(double) * (size_t)n);
+    for (int qh = 0; qh < nq; ++qh) {
+        const int kvh = qh / group;
+        const float *qv = q + (size_t)qh * hd;
+        double mx = -INFINITY;
+        for (int j = 0; j < n; ++j) {
+            const float *kv = k + ((size_t)(start + j) * nkv + kvh) * hd;
+            double dot = 0.0;
+            for (int e = 0; e < hd; ++e) dot += (double)qv[e] * (double)kv[e];
+            p[j] = dot * (double)scale;
+            if (p[j] > mx) mx = p[j];
+        }
+        double sum = 0.0;
+        for (int j = 0; j < n; ++j) {
+            p[j] = exp(p[j] - mx);
+            sum += p[j];
+        }
+        for (int e = 0; e < hd; ++e) {
+            double acc = 0.0;
+            for (int j = 0; j < n; ++j)
+                acc += p[j] * (double)v[((size_t)(start + j) * nkv + kvh) * hd + e];
+            out[(size_t)qh * hd + e] = (float)(acc / sum);
+        }
+    }
+    free(p);
+}
+
+static float r16(float x) { return tfo_f16_to_f32(tfo_f32_to_f16(x)); }
+
+static float *f16_to_f32_vec(const uint16_t *src, size_t n) {
+    float *o = (float *)calloc(n ? n : 1, sizeof(float));
+    for (size_t i = 0; i < n; ++i) o[i] = tfo_f16_to_f32(src[i]);
+    return o;
+}
+
+static void round_vec(float *x, size_t n) {
+    for (size_t i = 0; i < n; ++i) x[i] = r16(x[i]);
+}
+
+static void store_f16(uint16_t *dst, const float *x, size_t n) {
+    if (!dst) return;
+    for (size_t i = 0; i < n; ++i) dst[i] = tfo_f32_to_f16(x[i]);
+}
+
+/* rmsnorm of an fp32 vector with fp16 weights (NULL: no scale), rounded to fp16. */
+static void norm16(const float *x, const uint16_t *w16, int n, float eps, float *y) {
+    float *w = w16 ? f16_to_f32_vec(w16, (size_t)n) : NULL;
+    tfo_rmsnorm(x, w, n, eps, y);
+    round_vec(y, (size_t)n);
+    free(w);
+}
+
+void tfo_decode_layer(const tfo_layer_weights *w, const tfo_layer_shape *s,
+                      const uint16_t *hidden16, uint16_t *k_cache, uint16_t *v_cache, int position,
+                      uint16_t *out16, uint32_t *idx_out, float *w_out, tfo_layer_trace *trace) {
+    const int d = s->d, hd = s->hd, qd = s->nq * s->hd, kvd = s->nkv * s->hd;
+    const int seq = position + 1;
+    const float eps = s->eps;
+    float *hidden = f16_to_f32_vec(hidden16, (size_t)d);
+    float *normed = (float *)malloc(sizeof(float) * (size_t)d);
+    float *q = (float *)malloc(sizeof(float) * (size_t)qd);
+    float *kn = (float *)malloc(sizeof(float) * (size_t)kvd);
+    float *vn = (float *)malloc(sizeof(float) * (size_t)kvd);
+
+    /* gInputNorm + gQKV (RealForwardRunner.swift:2273-2300) */
+    norm16(hidden, w->input_norm, d, eps, normed);
+    tfo_gemv_int4(w->q.w, w->q.s, w->q.b, TFO_FMT_F16, normed, qd, d, q);
+    tfo_gemv_int4(w->k.w, w->k.s, w->k.b, TFO_FMT_F16, normed, kvd, d, kn);
+    tfo_gemv_int4(w->v.w, w->v.s, w->v.b, TFO_FMT_F16, normed, kvd, d, vn);
+    round_vec(q, (size_t)qd);
+    round_vec(kn, (size_t)kvd);
+    round_vec(vn, (size_t)kvd);
+
+    /* gQKVEpilogue (:2302-2322; fused.metal:86-180) */
+    for (int h = 0; h < s->nq; ++h) norm16(q + (size_t)h * hd, w->q_norm, hd, eps, q + (size_t)h * hd);
+    for (int h = 0; h < s->nkv; ++h) {
+        norm16(kn + (size_t)h * hd, w->k_norm, hd, eps, kn + (size_t)h * hd);
+        norm16(vn + (size_t)h * hd, NULL, hd, eps, vn + (size_t)h * hd);
+    }
+    tfo_rope_neox(q, s->nq, hd, s->rotated_pairs, position, s->theta);
+    tfo_rope_neox(kn, s->nkv, hd, s->rotated_pairs, position, s->theta);
+    round_vec(q, (size_t)qd);
+    round_vec(kn, (size_t)kvd);
+    store_f16(k_cache + (size_t)position * kvd, kn, (size_t)kvd);
+    store_f16(v_cache + (size_t)position * kvd, vn, (size_t)kvd);
+    if (trace) store_f16(trace->q, q, (size_t)qd);
+
+    /* gAttention (:2324-2362) */
+    float *K = f16_to_f32_vec(k_cache, (size_t)seq * kvd);
+    float *V = f16_to_f32_vec(v_cache, (size_t)seq * kvd);
+    float *attn = (float *)malloc(sizeof(float) * (size_t)qd);
+    tfo_attention(q, K, V, hd, s->nq, s->nkv, seq, s->window, s->scale, attn);
+    round_vec(attn, (size_t)qd);
+    if (trace) store_f16(trace->attn, attn, (size_t)qd);
+    free(K);
+    free(V);
+
+    /* gOProj + gPostAttnSetup (:2363-2386; fused.metal:199-268) */
+    float *o = (float *)malloc(sizeof(float) * (size_t)d);
+    float *an = (float *)malloc(sizeof(float) * (size_t)d);
+    float *h = (float *)malloc(sizeof(float) * (size_t)d);
+    tfo_gemv_int4(w->o.w, w->o.s, w->o.b, TFO_FMT_F16, attn, d, qd, o);
+    round_vec(o, (size_t)d);
+    norm16(o, w->post_attention_norm, d, eps, an);
+    for (int i = 0; i < d; ++i) h[i] = r16(hidden[i] + an[i]);
+    float *dense_x = (float *)malloc(sizeof(float) * (size_t)d);
+    float *routed_x = (float *)malloc(sizeof(float) * (size_t)d);
+    float *router_x = (float *)malloc(sizeof(float) * (size_t)d);
+    norm16(h, w->pre_ffn_norm, d, eps, dense_x);
+    norm16(h, w->pre_ffn2_norm, d, eps, routed_x);
+    norm16(h, NULL, d, eps, router_x);
+    if (trace) {
+        store_f16(trace->o, o, (size_t)d);
+        store_f16(trace->h, h, (size_t)d);
+    }
+
+    /* gRouter (:2388-2400): logits on router_x ⊙ eff, top-k softmax × gain */
+    const int E = w->num_experts, k = s->k;
+    float *eff = w->router_eff ? f16_to_f32_vec(w->router_eff, (size_t)d) : NULL;
+    float *gain = w->router_gain ? f16_to_f32_vec(w->router_gain, (size_t)E) : NULL;
+    float *logits = (float *)malloc(sizeof(float) * (size_t)E);
+    uint32_t idx[64];
+    float rw[64];
+    tfo_router_logits(w->router_w, w->router_s, w->router_b, TFO_FMT_F16, router_x, eff, E, d, logits);
+    tfo_topk_softmax(logits, E, k, gain, idx, rw);
+    for (int i = 0; i < k; ++i) {
+        rw[i] = r16(rw[i]);
+        if (idx_out) idx_out[i] = idx[i];
+        if (w_out) w_out[i] = rw[i];
+    }
+
+    /* gSharedFFN + gSharedNorm (:2418-2440) */
+    float *h1 = (float *)malloc(sizeof(float) * (size_t)d);
+    tfo_shared_expert_int4(w->shared_gate.w, w->shared_gate.s, w->shared_gate.b, w->shared_up.w,
+                           w->shared_up.s, w->shared_up.b, w->shared_down.w, w->shared_down.s,
+                           w->shared_down.b, TFO_FMT_F16, dense_x, d, s->fs, h1);
+    round_vec(h1, (size_t)d);
+    /* routed phases (:2849-2862), zero residual */
+    float *h2 = (float *)malloc(sizeof(float) * (size_t)d);
+    tfo_moe_routed(w->pool, w->stride, &w->off, TFO_FMT_F16, routed_x, NULL, idx, rw, k, d, s->f, h2);
+    round_vec(h2, (size_t)d);
+    if (trace) {
+        store_f16(trace->h1, h1, (size_t)d);
+        store_f16(trace->h2, h2, (size_t)d);
+    }
+
+    /* gTail (fused.metal:270-375) */
+    float *t = (float *)malloc(sizeof(float) * (size_t)d);
+    float *h12 = (float *)malloc(sizeof(float) * (size_t)d);
+    norm16(h1, w->post_ffn1_norm, d, eps, h12);
+    norm16(h2, w->post_ffn2_norm, d, eps, t);
+    for (int i = 0; i < d; ++i) h12[i] = r16(h12[i] + t[i]);
+    norm16(h12, w->post_ffn_norm, d, eps, t);
+    const float sc = r16(w->layer_scalar);
+    for (int i = 0; i < d; ++i) out16[i] = tfo_f32_to_f16(r16(h[i] + t[i]) * sc);
+
+    free(hidden); free(normed); free(q); free(kn); free(vn); free(attn); free(o); free(an); free(h);
+    free(dense_x); free(routed_x); free(router_x); free(eff); free(gain); free(logits); free(h1);
+    free(h2); free(t); free(h12);
+}
+
+/* ------------------------------------------------------------------------ */
 /* Tolerance helpers (V/Tolerance/RelError.swift:7-27)                       */
 /* ------------------------------------------------------------------------ */
 

@@ -168,6 +168,82 @@ void tfo_reduce_token_major(const uint16_t *partials_f16, const uint16_t *weight
 void tfo_gemm_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
                    const float *X, int M, int N, int K, float *Y, int row0, int row1);
 
+/* ---- decode layer (config 4) ----
+ * RmsNormRef.apply (V/Reference/Primitives/RmsNorm.swift:14-44):
+ *   y[i] = x[i] * w[i] * 1/sqrt(Σx²/n + eps); w == NULL: no scale (the
+ *   rmsnorm_no_scale form of S/Metal/Fusions/fused.metal:86-180). */
+void tfo_rmsnorm(const float *x, const float *w, int n, float eps, float *y);
+/* RopeRef.applyNeox (V/Reference/Attention/RoPE.swift:70-110), in place over
+ * num_heads heads: pairs (i, i + head_dim/2), i < rotated_pairs, rotated by
+ * position * theta^(-2i/head_dim). The angle and its cos/sin are evaluated
+ * in double (the reference's vForce tables carry fp32 angle error at long
+ * positions). */
+void tfo_rope_neox(float *x, int num_heads, int head_dim, int rotated_pairs, int position,
+                   float theta);
+/* AttentionRef.apply (V/Reference/Attention/Attention.swift:14-104):
+ * q [nq][hd], k/v [seq_len][nkv][hd] (fp32), out [nq][hd]; keys
+ * [max(0, seq_len - window), seq_len) (window 0: all). Dot products and the
+ * output sums accumulate in double; softmax is the stable form. */
+void tfo_attention(const float *q, const float *k, const float *v, int head_dim, int nq, int nkv,
+                   int seq_len, int window, float scale, float *out);
+
+typedef struct {
+    const uint8_t *w;
+    const uint16_t *s, *b;
+} tfo_q4;
+
+/* Gemma 4 decoder-layer weights (fp16 bits for every norm weight). */
+typedef struct {
+    const uint16_t *input_norm;
+    tfo_q4 q, k, v, o;
+    const uint16_t *q_norm, *k_norm;
+    const uint16_t *post_attention_norm, *pre_ffn_norm, *pre_ffn2_norm;
+    const uint8_t *router_w;
+    const uint16_t *router_s, *router_b, *router_eff, *router_gain;  /* eff/gain may be NULL */
+    int num_experts;
+    const uint8_t *pool;
+    uint64_t stride;
+    tfo_expert_offsets off;
+    tfo_q4 shared_gate, shared_up, shared_down;
+    const uint16_t *post_ffn1_norm, *post_ffn2_norm, *post_ffn_norm;
+    float layer_scalar;
+} tfo_layer_weights;
+
+typedef struct {
+    int d, nq, nkv, hd, rotated_pairs, window, f, fs, k;
+    float eps, theta, scale;
+} tfo_layer_shape;
+
+/* Optional intermediate outputs (each may be NULL), fp16 bits. */
+typedef struct {
+    uint16_t *q;        /* [nq*hd] after the epilogue */
+    uint16_t *attn;     /* [nq*hd] attention output */
+    uint16_t *o;        /* [d] o projection */
+    uint16_t *h;        /* [d] post-attention residual stream */
+    uint16_t *h1;       /* [d] shared-expert output */
+    uint16_t *h2;       /* [d] routed output */
+} tfo_layer_trace;
+
+/* One decoder layer for the token at `position`, composed from the
+ * references above in the per-layer order of RealForwardRunner
+ * (S/Runtime/Inference/RealForwardRunner.swift:2273-2862) with an fp16
+ * rounding wherever that sequence stores a buffer:
+ *   normed = f16(rmsnorm(hidden, input_norm)); q,k,v = f16(GEMV(·, normed))
+ *   q,k = f16(rope(f16(rmsnorm_head(·, q_norm/k_norm)))); v = f16(rmsnorm_head(v))
+ *   (k, v stored into cache slot `position`)
+ *   attn = f16(attention(q, K[0..position], V[0..position]))
+ *   o = f16(GEMV(o_proj, attn)); h = f16(hidden + f16(rmsnorm(o, post_attention_norm)))
+ *   router on f16(rmsnorm(h)) (no scale), weights rounded to fp16
+ *   h1 = f16(shared(f16(rmsnorm(h, pre_ffn_norm))))
+ *   h2 = f16(Σ w·ffn(f16(rmsnorm(h, pre_ffn2_norm))))
+ *   h12 = f16(f16(rmsnorm(h1, post_ffn1)) + f16(rmsnorm(h2, post_ffn2)))
+ *   out = f16(f16(h + f16(rmsnorm(h12, post_ffn))) * f16(layer_scalar))
+ * (fused.metal:86-375 for the fusion boundaries). Caches are fp16 bits
+ * [capacity][nkv][hd]. idx/w (may be NULL) receive the routing. */
+void tfo_decode_layer(const tfo_layer_weights *w, const tfo_layer_shape *s,
+                      const uint16_t *hidden, uint16_t *k_cache, uint16_t *v_cache, int position,
+                      uint16_t *out, uint32_t *idx, float *weights, tfo_layer_trace *trace);
+
 /* RelError.compute (V/Tolerance/RelError.swift:7-16). */
 float tfo_rel_error(const float *actual, const float *reference, size_t n);
 float tfo_max_abs_diff(const float *a, const float *b, size_t n);

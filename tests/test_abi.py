@@ -54,16 +54,24 @@ def test_status_strings_and_null_context_without_gpu():
 def test_struct_layouts_match_header(tmp_path):
     # compile the header with the system C compiler and compare with the ctypes mirror
     src = tmp_path / "layout.c"
+    fields = ["sizeof(tfq_expert_offsets)", "sizeof(tfq_expert_pool)", "offsetof(tfq_expert_pool, offsets)",
+              "sizeof(tfq_q4_matrix)", "offsetof(tfq_expert_pool, num_experts)", "sizeof(tfq_router)",
+              "sizeof(tfq_decode_layer_weights)", "offsetof(tfq_decode_layer_weights, router)",
+              "offsetof(tfq_decode_layer_weights, experts)", "offsetof(tfq_decode_layer_weights, shared_gate)",
+              "offsetof(tfq_decode_layer_weights, layer_scalar)", "sizeof(tfq_decode_layer_shape)",
+              "offsetof(tfq_decode_layer_shape, eps)"]
+    body = "".join(f'printf("%zu\\n", (size_t)({f}));' for f in fields)
     src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "tfq.h"\n'
-                   'int main(void){printf("%zu %zu %zu %zu %zu\\n", sizeof(tfq_expert_offsets),'
-                   ' sizeof(tfq_expert_pool), offsetof(tfq_expert_pool, offsets),'
-                   ' sizeof(tfq_q4_matrix), offsetof(tfq_expert_pool, num_experts));return 0;}\n')
+                   'int main(void){' + body + 'return 0;}\n')
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
     got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()]
+    W, S = _lib.DecodeLayerWeights, _lib.DecodeLayerShape
     assert got == [C.sizeof(_lib.ExpertOffsets), C.sizeof(_lib.ExpertPoolDesc),
                    _lib.ExpertPoolDesc.offsets.offset, C.sizeof(_lib.Q4Matrix),
-                   _lib.ExpertPoolDesc.num_experts.offset]
+                   _lib.ExpertPoolDesc.num_experts.offset, C.sizeof(_lib.RouterDesc),
+                   C.sizeof(W), W.router.offset, W.experts.offset, W.shared_gate.offset,
+                   W.layer_scalar.offset, C.sizeof(S), S.eps.offset]
 
 
 @pytest.mark.skipif(not shutil.which("/opt/rocm/llvm/bin/llvm-readelf"), reason="no llvm-readelf")
@@ -75,5 +83,6 @@ def test_code_object_is_gfx950_and_holds_all_kernels():
     assert "kernel_names" in src
     for fam in ("tfq_q4_gemv_s64_p2", "tfq_moe_phase1_s64_p2", "tfq_moe_phase2_p3",
                 "tfq_router_logits_s64_p3", "tfq_router_select", "tfq_gate_up_act_s64_p2",
-                "tfq_convert_bf16_f16"):
+                "tfq_convert_bf16_f16", "tfq_attn_partial_h256_g2", "tfq_attn_combine_h256",
+                "tfq_layer_tail"):
         assert fam in out

@@ -1,0 +1,246 @@
+"""GPU parity of the config-4 decode layer: split-K GQA decode attention and
+the whole Gemma 4 decoder layer (tfq_decode_layer) against the CPU oracle,
+through libtfq's C ABI.
+
+Bars: routing indices bit-exact; every stage's output (the intermediate
+buffers are read back from the documented workspace layout) within
+rel_error 1e-3 (north star) of the oracle fed with the GPU's own stored
+inputs of that stage; the whole chain (ten fp16-stored stages) within
+Tolerance.fp16_chained_reduction (1e-2) of the pure oracle."""
+import numpy as np
+import pytest
+
+import oracle
+from edgeexpert_amd import ops, synth
+from edgeexpert_amd._lib import TfqError
+from edgeexpert_amd.runtime import DeviceBuffer, Graph
+from helpers import f16_round, from_f16_bits
+
+pytestmark = pytest.mark.gpu
+TOL = oracle.Tolerance.north_star
+
+
+def _dev(a):
+    return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+# ---------------------------------------------------------------- attention ----
+
+def _run_attention(ctx, stream, q16, k16, v16, hd, nq, nkv, seq, window, scale):
+    ws_bytes = ops.Attention.workspace_bytes(hd, nq, seq, window)
+    ws = DeviceBuffer(ws_bytes)
+    out = _dev(np.full(nq * hd, 0x7E00, np.uint16))
+    ops.Attention(ctx).encode(stream, _dev(q16), _dev(k16), _dev(v16), out, hd, nq, nkv, seq, ws, ws_bytes,
+                              window=window, scale=scale)
+    stream.sync()
+    return from_f16_bits(out.download(np.uint16, nq * hd))
+
+
+@pytest.mark.parametrize("hd,nq,nkv,seq,window,scale", [
+    (256, 16, 8, 4096, 0, None),        # config 4 attention at full context
+    (256, 16, 8, 4096, 0, 1.0),         # Gemma 4 scale 1.0
+    (256, 16, 8, 1000, 512, None),      # sliding window (encodeSWA)
+    (256, 16, 4, 300, 0, None),         # GQA group 4
+    (256, 4, 4, 1, 0, None),            # one key
+    (128, 8, 2, 77, 0, None),           # ragged last chunk
+    (128, 8, 8, 64, 0, 1.0),            # exactly one chunk
+    (128, 4, 1, 129, 100, None),        # window cuts a chunk boundary
+])
+def test_attention_matches_reference(ctx, stream, hd, nq, nkv, seq, window, scale):
+    tag = f"attn-h{hd}-q{nq}-kv{nkv}-T{seq}-w{window}"
+    q16 = synth.f16_vector(0, tag + "/q", nq * hd)
+    k16 = synth.f16_vector(0, tag + "/k", seq * nkv * hd)
+    v16 = synth.f16_vector(0, tag + "/v", seq * nkv * hd)
+    got = _run_attention(ctx, stream, q16, k16, v16, hd, nq, nkv, seq, window, scale)
+    ref = oracle.attention(from_f16_bits(q16), from_f16_bits(k16), from_f16_bits(v16), hd, nq, nkv, seq,
+                           window, scale)
+    rel = oracle.rel_error(got, ref)
+    assert rel < TOL, f"{tag}: rel={rel}"
+
+
+def test_attention_is_deterministic(ctx, stream):
+    hd, nq, nkv, seq = 256, 16, 8, 2048
+    q16 = synth.f16_vector(1, "det/q", nq * hd)
+    k16 = synth.f16_vector(1, "det/k", seq * nkv * hd)
+    v16 = synth.f16_vector(1, "det/v", seq * nkv * hd)
+    a = _run_attention(ctx, stream, q16, k16, v16, hd, nq, nkv, seq, 0, None)
+    b = _run_attention(ctx, stream, q16, k16, v16, hd, nq, nkv, seq, 0, None)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_attention_rejects_bad_contract(ctx, stream):
+    att = ops.Attention(ctx)
+    ws = DeviceBuffer(1 << 20)
+    buf = DeviceBuffer(1 << 20)
+    bad = [dict(hd=64, nq=4, nkv=2, seq=8), dict(hd=128, nq=6, nkv=2, seq=8),
+           dict(hd=128, nq=4, nkv=3, seq=8), dict(hd=128, nq=4, nkv=2, seq=0)]
+    for b in bad:
+        with pytest.raises(TfqError):
+            att.encode(stream, buf, buf, buf, buf, b["hd"], b["nq"], b["nkv"], b["seq"], ws, 1 << 20)
+    with pytest.raises(TfqError):       # workspace too small
+        att.encode(stream, buf, buf, buf, buf, 256, 16, 8, 4096, ws, 1024)
+
+
+# -------------------------------------------------------------------- layer ----
+
+def _layout(shape, seq):
+    """Mirror of DecodeLayer::layout (edgeexpert_amd/csrc/host/ops.hpp): 256-byte
+    aligned segments q, attn, parts, o, logits, idx, w, acts, sact, h1, h2."""
+    up = lambda v: (v + 255) // 256 * 256
+    qd = shape["nq"] * shape["hd"]
+    sizes = [("q", qd * 2), ("attn", qd * 2),
+             ("parts", ops.Attention.workspace_bytes(shape["hd"], shape["nq"], seq, shape["window"])),
+             ("o", shape["d"] * 2), ("logits", 4096), ("idx", shape["k"] * 4), ("w", shape["k"] * 2),
+             ("acts", shape["k"] * shape["f"] * 2), ("sact", shape["fs"] * 2), ("h1", shape["d"] * 2),
+             ("h2", shape["d"] * 2)]
+    off, L = 0, {}
+    for n, sz in sizes:
+        L[n] = off
+        off += up(sz)
+    L["total"] = off
+    return L
+
+
+def _spec(shape):
+    return ops.DecodeLayerShapeSpec(d=shape["d"], num_q_heads=shape["nq"], num_kv_heads=shape["nkv"],
+                                    head_dim=shape["hd"], expert_f=shape["f"], shared_f=shape["fs"],
+                                    top_k=shape["k"], rotated_pairs=shape["rotated_pairs"],
+                                    window=shape["window"], eps=shape["eps"], rope_theta=shape["theta"],
+                                    attn_scale=shape["scale"])
+
+
+def _layer_case(ctx, stream, shape, E, pos, cap, seed, label, in_place=False):
+    w = synth.decode_layer(seed, label, shape["d"], shape["nq"], shape["nkv"], shape["hd"], E, shape["f"],
+                           shape["fs"])
+    kvd = shape["nkv"] * shape["hd"]
+    kc = synth.f16_vector(seed, label + "/kc", cap * kvd)
+    vc = synth.f16_vector(seed, label + "/vc", cap * kvd)
+    hidden = synth.f16_vector(seed, label + "/hidden", shape["d"])
+    print(f"[layer] {label} pos={pos} E={E} shape={shape}", flush=True)
+    spec = _spec(shape)
+    L = _layout(shape, pos + 1)
+    ws_bytes = ops.decode_layer_workspace_bytes(spec, pos + 1)
+    assert ws_bytes == L["total"]
+    ws = DeviceBuffer(ws_bytes)
+    ws.fill(0)
+    kb, vb, hb = _dev(kc), _dev(vc), _dev(hidden)
+    ob = hb if in_place else _dev(np.full(shape["d"], 0x7E00, np.uint16))
+    layer = ops.DecodeLayer(ctx, ops.DecodeLayerWeightsSpec.upload(w), spec)
+    layer.encode(stream, hb, ob, kb, vb, pos, ws, ws_bytes)
+    stream.sync()
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    out_ref, idx_ref, w_ref, tr = oracle.decode_layer(w, shape, hidden, kc_ref, vc_ref, pos, trace=True)
+    got = {
+        "out": from_f16_bits(ob.download(np.uint16, shape["d"])),
+        "idx": ws.download(np.uint32, shape["k"], offset=L["idx"]),
+        "w": from_f16_bits(ws.download(np.uint16, shape["k"], offset=L["w"])),
+        "attn": from_f16_bits(ws.download(np.uint16, shape["nq"] * shape["hd"], offset=L["attn"])),
+        "o": from_f16_bits(ws.download(np.uint16, shape["d"], offset=L["o"])),
+        "h1": from_f16_bits(ws.download(np.uint16, shape["d"], offset=L["h1"])),
+        "h2": from_f16_bits(ws.download(np.uint16, shape["d"], offset=L["h2"])),
+        "kslot": from_f16_bits(kb.download(np.uint16, kvd, offset=pos * kvd * 2)),
+        "vslot": from_f16_bits(vb.download(np.uint16, kvd, offset=pos * kvd * 2)),
+        "kcache": kb.download(np.uint16, cap * kvd),
+    }
+    ref = {"out": from_f16_bits(out_ref), "idx": idx_ref, "w": w_ref,
+           "attn": from_f16_bits(tr["attn"]), "o": from_f16_bits(tr["o"]), "h1": from_f16_bits(tr["h1"]),
+           "h2": from_f16_bits(tr["h2"]),
+           "kslot": from_f16_bits(kc_ref[pos * kvd:(pos + 1) * kvd]),
+           "vslot": from_f16_bits(vc_ref[pos * kvd:(pos + 1) * kvd])}
+    # slots other than `pos` are untouched
+    assert np.array_equal(np.delete(got["kcache"].reshape(cap, kvd), pos, 0),
+                          np.delete(kc.reshape(cap, kvd), pos, 0))
+    return got, ref, w, hidden
+
+
+def _n16(x, w16, eps=1e-6):
+    return f16_round(oracle.rmsnorm(x, None if w16 is None else from_f16_bits(w16), eps))
+
+
+def _check_layer(got, ref, w, shape, hidden, label):
+    """Each stage against the oracle fed with the GPU's own stored inputs
+    then the whole chain against the pure oracle."""
+    assert list(got["idx"]) == list(ref["idx"]), f"{label}: routing differs"
+    d, eps = shape["d"], shape["eps"]
+    h_in = from_f16_bits(hidden)
+    # stages fed directly by `hidden` and the caches
+    for key in ("kslot", "vslot", "attn"):
+        rel = oracle.rel_error(got[key], ref[key])
+        assert rel < TOL, f"{label}: {key} rel={rel}"
+    stage = {}
+    stage["o"] = f16_round(oracle.gemv_int4(*w["o"], got["attn"]))
+    h = f16_round(h_in + _n16(got["o"], w["post_attention_norm"], eps))
+    logits = oracle.router_logits(w["router_w"], w["router_s"], w["router_b"], _n16(h, None, eps),
+                                  from_f16_bits(w["router_eff"]))
+    ridx, rw = oracle.topk_softmax(logits, shape["k"], from_f16_bits(w["router_gain"]))
+    assert list(ridx) == list(got["idx"]), f"{label}: routing of the GPU's h differs"
+    stage["w"] = f16_round(rw)
+    sh = (w["shared_gate"], w["shared_up"], w["shared_down"])
+    stage["h1"] = f16_round(oracle.shared_expert_int4(*sh, _n16(h, w["pre_ffn_norm"], eps), d, shape["fs"]))
+    stage["h2"] = f16_round(oracle.moe_routed(w["pool"], w["stride"], w["off"], _n16(h, w["pre_ffn2_norm"], eps),
+                                              ridx, got["w"], d, shape["f"]))
+    h12 = f16_round(_n16(got["h1"], w["post_ffn1_norm"], eps) + _n16(got["h2"], w["post_ffn2_norm"], eps))
+    stage["out"] = f16_round(f16_round(h + _n16(h12, w["post_ffn_norm"], eps)) *
+                             f16_round(np.float32(w["layer_scalar"])))
+    for key, expect in stage.items():
+        rel = oracle.rel_error(got[key], expect)
+        assert rel < TOL, f"{label}: stage {key} rel={rel}"
+    chained = oracle.rel_error(got["out"], ref["out"])
+    print(f"[layer] {label}: end-to-end rel={chained:.3g}", flush=True)
+    assert chained < oracle.Tolerance.fp16_chained_reduction, f"{label}: end-to-end rel={chained}"
+
+
+SMALL = dict(d=256, nq=4, nkv=2, hd=128, rotated_pairs=64, window=0, f=128, fs=192, k=2,
+             eps=1e-6, theta=10000.0, scale=1.0)
+CONFIG4 = dict(d=2816, nq=16, nkv=8, hd=256, rotated_pairs=128, window=0, f=704, fs=2112, k=8,
+               eps=1e-6, theta=10000.0, scale=1.0)
+
+
+@pytest.mark.parametrize("pos", [0, 70, 130])
+def test_layer_small_matches_reference(ctx, stream, pos):
+    got, ref, w, hid = _layer_case(ctx, stream, SMALL, 8, pos, 160, 3, f"small-{pos}")
+    _check_layer(got, ref, w, SMALL, hid, f"small pos={pos}")
+
+
+def test_layer_small_window_and_partial_rotary(ctx, stream):
+    shape = dict(SMALL, window=64, rotated_pairs=16, theta=1e6)
+    got, ref, w, hid = _layer_case(ctx, stream, shape, 8, 200, 256, 4, "small-swa")
+    _check_layer(got, ref, w, shape, hid, "small window")
+
+
+def test_layer_in_place_equals_out_of_place(ctx, stream):
+    a = _layer_case(ctx, stream, SMALL, 8, 33, 64, 5, "inplace")[0]
+    b = _layer_case(ctx, stream, SMALL, 8, 33, 64, 5, "inplace", in_place=True)[0]
+    assert np.array_equal(a["out"].view(np.uint32), b["out"].view(np.uint32))
+
+
+def test_layer_config4_full_context(ctx, stream):
+    # d 2816, 16 q / 8 kv heads x 256, context 4096 (the
+    # new token at position 4095), shared expert 2112, top-8 of 128 experts
+    got, ref, w, hid = _layer_case(ctx, stream, CONFIG4, 128, 4095, 4096, 0, "c4")
+    _check_layer(got, ref, w, CONFIG4, hid, "config 4")
+
+
+def test_layer_graph_replays_match_eager(ctx, stream):
+    shape, E, pos, cap = SMALL, 8, 90, 128
+    w = synth.decode_layer(6, "graph", shape["d"], shape["nq"], shape["nkv"], shape["hd"], E, shape["f"],
+                           shape["fs"])
+    kvd = shape["nkv"] * shape["hd"]
+    kb = _dev(synth.f16_vector(6, "graph/kc", cap * kvd))
+    vb = _dev(synth.f16_vector(6, "graph/vc", cap * kvd))
+    hb = _dev(synth.f16_vector(6, "graph/hidden", shape["d"]))
+    spec = _spec(shape)
+    ws_bytes = ops.decode_layer_workspace_bytes(spec, pos + 1)
+    ws = DeviceBuffer(ws_bytes)
+    ob = _dev(np.zeros(shape["d"], np.uint16))
+    layer = ops.DecodeLayer(ctx, ops.DecodeLayerWeightsSpec.upload(w), spec)
+    layer.encode(stream, hb, ob, kb, vb, pos, ws, ws_bytes)
+    stream.sync()
+    eager = ob.download(np.uint16, shape["d"]).copy()
+    g = Graph(stream, lambda: layer.encode(stream, hb, ob, kb, vb, pos, ws, ws_bytes))
+    for r in range(3):
+        ob.fill(0)
+        ws.fill(0xFF)
+        g.launch(stream)
+        stream.sync()
+        assert np.array_equal(ob.download(np.uint16, shape["d"]), eager), f"replay {r}"
