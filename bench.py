@@ -11,7 +11,10 @@ holds 64 tokens (3 kernels each).
 
 Also measured (extra fields): BASELINE config 0, the int4 g64 GEMV
 [2816 x 2816], cold (rotating through 256 weight copies, 1.14 GB) and warm,
-per-launch with HIP events.
+per-launch with HIP events; config 2, the bf16 prefill GEMM; config 4, the
+full Gemma 4 decoder layer for one token at position 4095 (context 4096),
+chained through 8 resident copies of the layer so that every token reads
+cold weights and KV cache, as consecutive layers of a model do.
 
 Prints ONE JSON line on stdout. Data are synthetic (seeded SplitMix64, see
 edgeexpert_amd/synth.py).
@@ -49,12 +52,120 @@ def moe_bytes():
             "phase2": phase2 + acts + 2 * D, "total": router + phase1 + phase2 + 2 * D * 2}
 
 
+C4 = dict(d=2816, nq=16, nkv=8, hd=256, rotated_pairs=128, window=0, f=704, fs=2112, k=8,
+          eps=1e-6, theta=10000.0, scale=1.0)
+C4_CTX = 4096
+C4_LAYERS = 8
+
+
+def c4_bytes():
+    """Algorithmic HBM bytes of one config-4 layer token (weights fp16 scale+bias,
+    fp16 KV cache read once; activations and norm vectors are a few KB)."""
+    d, qd, kvd = C4["d"], C4["nq"] * C4["hd"], C4["nkv"] * C4["hd"]
+    q4 = lambda m, n: m * n // 2 + 2 * m * (n // 64) * 2
+    parts = {
+        "qkv": q4(qd + 2 * kvd, d),
+        "attention_kv": 2 * C4_CTX * kvd * 2,
+        "o_proj": q4(d, qd),
+        "router": E * d + 2 * E * (d // 64) * 2,
+        "routed": C4["k"] * 3 * q4(C4["f"], d),
+        "shared": 2 * q4(C4["fs"], d) + q4(d, C4["fs"]),
+    }
+    parts["total"] = sum(parts.values())
+    return parts
+
+
+def bench_c4(ctx, stream, launch, batch_avg_us):
+    from edgeexpert_amd import ops, synth
+    from edgeexpert_amd.runtime import DeviceBuffer, Event, Graph
+    t0 = time.time()
+    w = synth.decode_layer(0, "c4", C4["d"], C4["nq"], C4["nkv"], C4["hd"], E, C4["f"], C4["fs"])
+    kvd = C4["nkv"] * C4["hd"]
+    kc = synth.f16_vector(0, "c4/kc", C4_CTX * kvd)
+    vc = synth.f16_vector(0, "c4/vc", C4_CTX * kvd)
+    spec = ops.DecodeLayerShapeSpec(d=C4["d"], num_q_heads=C4["nq"], num_kv_heads=C4["nkv"],
+                                    head_dim=C4["hd"], expert_f=C4["f"], shared_f=C4["fs"], top_k=C4["k"],
+                                    rotated_pairs=C4["rotated_pairs"], window=C4["window"], eps=C4["eps"],
+                                    rope_theta=C4["theta"], attn_scale=C4["scale"])
+    # distinct device copies (same values, different addresses): each token's
+    # layer reads weights and KV that the previous layers evicted from L2/MALL
+    layers, caches = [], []
+    for _ in range(C4_LAYERS):
+        layers.append(ops.DecodeLayer(ctx, ops.DecodeLayerWeightsSpec.upload(w), spec))
+        caches.append((DeviceBuffer.from_array(kc), DeviceBuffer.from_array(vc)))
+    ws_bytes = ops.decode_layer_workspace_bytes(spec, C4_CTX)
+    ws = DeviceBuffer(ws_bytes)
+    hid = DeviceBuffer.from_array(synth.f16_vector(0, "c4/hidden", C4["d"]))
+    log(f"config 4: {C4_LAYERS} layer copies resident, set up in {time.time() - t0:.1f}s")
+    pos = C4_CTX - 1
+
+    def stack():
+        for L in range(C4_LAYERS):
+            kb, vb = caches[L]
+            layers[L].encode(stream, hid, hid, kb, vb, pos, ws, ws_bytes)
+
+    run = stack
+    if launch == "graph":
+        g = Graph(stream, stack)
+        run = lambda: g.launch(stream)
+    for _ in range(4):
+        run()
+    stream.sync()
+    reps = 32
+    a, b = Event(), Event()
+    a.record(stream)
+    for _ in range(reps):
+        run()
+    b.record(stream)
+    stream.sync()
+    us = a.elapsed_ms(b) * 1e3 / (reps * C4_LAYERS)
+    nb = c4_bytes()
+    gbs = nb["total"] / (us * 1e-6) / 1e9
+    floor_us = nb["total"] / (HBM_PEAK_GBS * 1e9) * 1e6
+    # attention alone (split-K partial + combine over the 4096-key cache), back to back
+    att = ops.Attention(ctx)
+    q = DeviceBuffer.from_array(synth.f16_vector(0, "c4/q", C4["nq"] * C4["hd"]))
+    out = DeviceBuffer(C4["nq"] * C4["hd"] * 2)
+    aws = ops.Attention.workspace_bytes(C4["hd"], C4["nq"], C4_CTX)
+    awsb = DeviceBuffer(aws)
+    attn_us = batch_avg_us(lambda i: att.encode(stream, q, caches[i % C4_LAYERS][0], caches[i % C4_LAYERS][1],
+                                                out, C4["hd"], C4["nq"], C4["nkv"], C4_CTX, awsb, aws,
+                                                scale=1.0), 64)
+    attn_gbs = nb["attention_kv"] / (attn_us * 1e-6) / 1e9
+    log(f"decode layer C4 ({launch}): {us:.2f} us/token ({gbs:.0f} GB/s of {nb['total']} B; "
+        f"8 TB/s floor {floor_us:.2f} us); attention alone {attn_us:.2f} us ({attn_gbs:.0f} GB/s)")
+    return {"us_per_token": round(us, 3), "bytes_per_token": nb["total"], "gbs": round(gbs, 1),
+            "hbm_floor_us": round(floor_us, 3), "frac_of_floor": round(floor_us / us, 4),
+            "bytes": {k: v for k, v in nb.items() if k != "total"}, "layers_rotated": C4_LAYERS,
+            "context": C4_CTX, "position": pos, "launch": launch,
+            "attention_us": round(attn_us, 3), "attention_gbs": round(attn_gbs, 1)}
+
+
+TRAFFIC_FILE = "profiles/hbm_traffic_moe_decode_c1.txt"
+
+
+def read_traffic():
+    """HBM bytes per launch measured by two rocprofv3 --pmc runs of this
+    script (FETCH_SIZE, WRITE_SIZE), scaled by the calibration kernels; read
+    from the committed summary. Lines: `traffic <kernel> <bytes>`."""
+    path = os.path.join(ROOT, TRAFFIC_FILE)
+    if not os.path.exists(path):
+        return None
+    out = {}
+    for line in open(path):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic":
+            out[f[1]] = int(float(f[2]))
+    return out or None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=4096)
     ap.add_argument("--warmup", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-c4", action="store_true", help="skip the config-4 decode-layer leg")
     ap.add_argument("--launch", choices=("graph", "stream"), default="graph",
                     help="replay the 64-token step from a HIP graph, or issue it from the host")
     args = ap.parse_args()
@@ -135,10 +246,23 @@ def main():
     nb = moe_bytes()
     moe = ops.MoE(ctx)
 
+    # A one-block read of 64 MiB (~1 ms of GPU time, one launch) queued ahead
+    # of every timed batch: the host enqueues the whole batch while the GPU is
+    # still busy with it, so the events see kernels back to back with no
+    # host launch gaps (also under a profiler, where launches are slower).
+    pad_bytes = 64 << 20
+    pad_buf = DeviceBuffer(pad_bytes)
+    pad_buf.fill(0)
+    pad_sink = DeviceBuffer(256)
+
+    def pad():
+        ops.read_ceiling(ctx, stream, pad_buf, pad_bytes, pad_sink, 1)
+
     def batch_avg_us(launch_one, count, reps_=5):
         best = []
         for _ in range(reps_):
             a, b = Event(), Event()
+            pad()
             a.record(stream)
             for t in range(count):
                 launch_one(t)
@@ -204,6 +328,22 @@ def main():
     log(f"GEMM C2 (bf16, back-to-back): {gemm_us:.2f} us -> {gemm_tflops:.1f} TFLOP/s "
         f"({gemm_tflops / 2500.0 * 100:.1f}% of 2.5 PFLOP/s dense fp16/bf16)")
 
+    # ------------------------------------------------ decode layer config 4 ----
+    c4 = None if args.no_c4 else bench_c4(ctx, stream, args.launch, batch_avg_us)
+
+    # -------------------------------------- HBM counter calibration kernels ----
+    # One plain read (64 MiB) and one plain copy (32 MiB in, 32 MiB out) of
+    # known size, launched once so that a rocprofv3 --pmc run of this command
+    # can scale FETCH_SIZE / WRITE_SIZE of the other kernels to bytes.
+    cal_bytes = 64 << 20
+    cal = DeviceBuffer(cal_bytes)
+    cal.fill(0)
+    sink = DeviceBuffer(4 * 8192)
+    ops.read_ceiling(ctx, stream, cal, cal_bytes, sink, 8192)
+    ops.convert_bf16_to_f16(ctx, stream, cal, cal.ptr(cal_bytes // 2), cal_bytes // 4)
+    stream.sync()
+    traffic = read_traffic()
+
     # ------------------------------------------------------ CPU baseline ----
     cpu = None
     if not args.no_cpu:
@@ -239,7 +379,9 @@ def main():
                    "kernels_per_token": "router_logits, router_select, moe_phase1, moe_phase2"},
         "roofline": {"kernel": "tfq_moe_phase1 (gate/up of 8 experts)", "bound": "hbm",
                      "achieved": round(p1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(p1_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(p1_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("tfq_moe_phase1") if traffic else None,
+                     "traffic_source": TRAFFIC_FILE if traffic else None,
                      "algorithmic_bytes": nb["phase1"], "avg_launch_us": round(p1_us, 3),
                      "kernel_avg_us": {k: round(v, 3) for k, v in k_us.items()}},
         "cpu_baseline": cpu,
@@ -252,6 +394,7 @@ def main():
         "gemm_c2": {"shape": [Mg, Ng, Kg], "dtype": "bf16 in/out, fp16 MFMA, fp32 acc",
                     "us": round(gemm_us, 3), "tflops": round(gemm_tflops, 1),
                     "frac_of_dense_peak": round(gemm_tflops / 2500.0, 4)},
+        "decode_layer_c4": c4,
         "wall_s": round(wall, 4),
         "device": f"{name} {arch}",
     }

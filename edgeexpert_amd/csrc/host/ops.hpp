@@ -128,7 +128,7 @@ public:
         std::snprintf(name, sizeof(name), "tfq_q8_gemv_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&weights, &scales, &biases, &x, &y, &m, &n};
-        return launch(m_.get(name), grid_for_rows(m, rows_per_block), kBlock, n * 4, stream, args,
+        return launch(m_.get(name), grid_for_rows(m, rows_per_block), kBlock, n * 6, stream, args,
                       name);
     }
 
@@ -501,7 +501,7 @@ public:
         if (!q || !k_cache || !v_cache || !out || !workspace) return fail(TFQ_E_INVAL, "null pointer argument");
         if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(workspace, 16))
             return fail(TFQ_E_INVAL, "KV caches and workspace must be 16-byte aligned");
-        if (!aligned(q, 2) || !aligned(out, 2)) return fail(TFQ_E_INVAL, "q/out must be 2-byte aligned");
+        if (!aligned(q, 16) || !aligned(out, 2)) return fail(TFQ_E_INVAL, "q must be 16-byte and out 2-byte aligned");
         if (!(scale > 0.0f) && !(scale < 0.0f)) return fail(TFQ_E_INVAL, "scale must be non-zero");
         if (epi.q_norm) {
             if (!epi.k_norm) return fail(TFQ_E_INVAL, "q/k epilogue needs both norm weights");
@@ -583,6 +583,11 @@ public:
             !w.pre_ffn2_norm || !w.post_ffn1_norm || !w.post_ffn2_norm || !w.post_ffn_norm)
             return fail(TFQ_E_INVAL, "every norm weight is required");
         if (s.d == 0 || s.d % 64 || s.d > 4096) return fail(TFQ_E_INVAL, "d=%u must be a multiple of 64 <= 4096", s.d);
+        for (const void* p : {(const void*)hidden_in, (const void*)hidden_out, (const void*)w.input_norm,
+                              (const void*)w.post_attention_norm, (const void*)w.pre_ffn_norm,
+                              (const void*)w.pre_ffn2_norm, (const void*)w.post_ffn1_norm,
+                              (const void*)w.post_ffn2_norm, (const void*)w.post_ffn_norm})
+            if (!aligned(p, 16)) return fail(TFQ_E_INVAL, "hidden vectors and norm weights must be 16-byte aligned");
         if (!aligned(workspace, 256)) return fail(TFQ_E_INVAL, "workspace must be 256-byte aligned");
         const uint32_t seq_len = position + 1;
         const Layout L = layout(s, seq_len);
@@ -647,7 +652,7 @@ public:
         uint32_t d = s.d;
         void* ta[] = {(void*)&hidden_in, &o, (void*)&w.post_attention_norm, &h1, (void*)&w.post_ffn1_norm,
                       &h2, (void*)&w.post_ffn2_norm, (void*)&w.post_ffn_norm, &eps, &scalar, &hidden_out, &d};
-        return launch2(m_, "tfq_layer_tail", 1, 1, 1024, 3 * s.d * 2, stream, ta);
+        return launch2(m_, "tfq_layer_tail", 1, 1, 1024, 0, stream, ta);
     }
 
     // Creates the side stream and its fork/join events (tfq_create calls it,

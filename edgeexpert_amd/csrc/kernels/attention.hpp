@@ -122,19 +122,23 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
         vr[i] = j < n ? *reinterpret_cast<const uint4*>(vbase + j * row + 8u * vl) : make_uint4(0, 0, 0, 0);
     }
 
+    // the queries (16-byte chunks; G*HD/8 <= 128 of them) and, in the block
+    // that owns it, the new token's raw k and v rows
+    constexpr uint32_t QCH = G * HD / 8;
+    static_assert(QCH <= kAttnThreads && 2 * (HD / 8) <= kAttnThreads, "one chunk per thread");
+    uint4 qraw = make_uint4(0, 0, 0, 0), kvraw = make_uint4(0, 0, 0, 0);
+    if (tid < QCH) qraw = reinterpret_cast<const uint4*>(q + (size_t)h * G * HD)[tid];
+    if (own_pos && tid < 2 * (HD / 8)) {
+        const uint16_t* src = (tid < HD / 8 ? kc : vc) + (size_t)pos * row + (size_t)h * HD;
+        kvraw = reinterpret_cast<const uint4*>(src)[tid % (HD / 8)];
+    }
+
     // 2. queries (and the new token's k/v) through the epilogue
-    for (uint32_t i = tid; i < G * HD; i += kAttnThreads)
-        (&L.q[0][0])[i] = q[(size_t)h * G * HD + i];
+    if (tid < QCH) reinterpret_cast<uint4*>(&L.q[0][0])[tid] = qraw;
     if (epi_on) {
         rope_table(L.rc, L.rs, epi.rotated_pairs, HD, pos, epi.theta);
-        if (own_pos) {
-            const uint16_t* kn = kc + (size_t)pos * row + (size_t)h * HD;
-            const uint16_t* vn = vc + (size_t)pos * row + (size_t)h * HD;
-            for (uint32_t i = tid; i < HD; i += kAttnThreads) {
-                L.kp[i] = kn[i];
-                L.vp[i] = vn[i];
-            }
-        }
+        if (own_pos && tid < 2 * (HD / 8))
+            reinterpret_cast<uint4*>(tid < HD / 8 ? L.kp : L.vp)[tid % (HD / 8)] = kvraw;
         __syncthreads();
         const uint32_t nvec = G + (own_pos ? 2u : 0u);
         for (uint32_t v = wave; v < nvec; v += kAttnThreads / 64) {
@@ -152,13 +156,10 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
             buf[pr + HD / 2] = f2h(x0 * L.rs[pr] + x1 * L.rc[pr]);
         }
         __syncthreads();
-        if (own_pos) {            // the cache keeps the processed k/v of the new token
-            uint16_t* kn = kc + (size_t)pos * row + (size_t)h * HD;
-            uint16_t* vn = vc + (size_t)pos * row + (size_t)h * HD;
-            for (uint32_t i = tid; i < HD; i += kAttnThreads) {
-                kn[i] = L.kp[i];
-                vn[i] = L.vp[i];
-            }
+        if (own_pos && tid < 2 * (HD / 8)) {   // the cache keeps the processed k/v of the new token
+            uint16_t* dst = (tid < HD / 8 ? kc : vc) + (size_t)pos * row + (size_t)h * HD;
+            reinterpret_cast<uint4*>(dst)[tid % (HD / 8)] =
+                reinterpret_cast<const uint4*>(tid < HD / 8 ? L.kp : L.vp)[tid % (HD / 8)];
         }
     } else {
         __syncthreads();
@@ -294,28 +295,63 @@ __device__ __forceinline__ void attn_combine(const float* __restrict__ part_o, c
 //     out = fp16(fp16(h + fp16(h12·w_post_ffn·r(h12))) · fp16(layer_scalar)),
 //     h12 = fp16(fp16(h1·w_sp·r(h1)) + fp16(h2·w_pf2·r(h2)))
 // (fused_post_attn_setup / rmsnorm / fused_layer_tail,
-// S/Metal/Fusions/fused.metal:199-231,270-375). Dynamic LDS: 3·D halves.
+// S/Metal/Fusions/fused.metal:199-231,270-375). Each thread owns one 16-byte
+// chunk of every vector and loads all eight at once; requires D % 8 == 0,
+// D <= 8·blockDim and 16-byte aligned vectors (the host checks).
 __device__ __forceinline__ void layer_tail(const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ attn,
                                            const uint16_t* __restrict__ w_post_attn,
                                            const uint16_t* __restrict__ h1, const uint16_t* __restrict__ w_sp,
                                            const uint16_t* __restrict__ h2, const uint16_t* __restrict__ w_pf2,
                                            const uint16_t* __restrict__ w_pf, float eps, float layer_scalar,
                                            uint16_t* __restrict__ out, uint32_t D) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t tail_lds[];
-    uint16_t* hb = tail_lds;
-    uint16_t* ab = tail_lds + D;
-    uint16_t* bb = tail_lds + 2 * D;
-    stage_act(hidden, hb, D, {nullptr, attn, w_post_attn, eps, kStageResidual});
-    stage_act(h1, ab, D, {w_sp, nullptr, nullptr, eps, kStageNorm});
-    stage_act(h2, bb, D, {w_pf2, nullptr, nullptr, eps, kStageNorm});
-    for (uint32_t i = threadIdx.x; i < D; i += blockDim.x) bb[i] = f2h(h2f(ab[i]) + h2f(bb[i]));
-    __syncthreads();
-    rmsnorm_lds(bb, D, w_pf, eps);
-    const float sc = h2f(f2h(layer_scalar));
-    for (uint32_t i = threadIdx.x; i < D; i += blockDim.x) {
-        const float r = h2f(f2h(h2f(hb[i]) + h2f(bb[i])));
-        out[i] = f2h(r * sc);
+    const uint32_t c = threadIdx.x;
+    const bool live = c < (D >> 3);
+    h8 hv{}, av{}, paw{}, h1v{}, spw{}, h2v{}, pf2w{}, pfw{};
+    if (live) {
+        hv = __builtin_bit_cast(h8, ld16h(hidden, c));
+        av = __builtin_bit_cast(h8, ld16h(attn, c));
+        paw = __builtin_bit_cast(h8, ld16h(w_post_attn, c));
+        h1v = __builtin_bit_cast(h8, ld16h(h1, c));
+        spw = __builtin_bit_cast(h8, ld16h(w_sp, c));
+        h2v = __builtin_bit_cast(h8, ld16h(h2, c));
+        pf2w = __builtin_bit_cast(h8, ld16h(w_pf2, c));
+        pfw = __builtin_bit_cast(h8, ld16h(w_pf, c));
     }
+    const float n = (float)D;
+    float ss[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        ss[0] = fmaf((float)av[e], (float)av[e], ss[0]);
+        ss[1] = fmaf((float)h1v[e], (float)h1v[e], ss[1]);
+        ss[2] = fmaf((float)h2v[e], (float)h2v[e], ss[2]);
+    }
+    block_sums<3>(ss);
+    const float inv_a = 1.0f / sqrtf(ss[0] / n + eps);
+    const float inv_1 = 1.0f / sqrtf(ss[1] / n + eps);
+    const float inv_2 = 1.0f / sqrtf(ss[2] / n + eps);
+    h8 h12;
+    float s12[1] = {0.0f};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const _Float16 an = (_Float16)((float)av[e] * (float)paw[e] * inv_a);
+        hv[e] = (_Float16)((float)hv[e] + (float)an);
+        const _Float16 a1 = (_Float16)((float)h1v[e] * (float)spw[e] * inv_1);
+        const _Float16 a2 = (_Float16)((float)h2v[e] * (float)pf2w[e] * inv_2);
+        h12[e] = (_Float16)((float)a1 + (float)a2);
+        s12[0] = fmaf((float)h12[e], (float)h12[e], s12[0]);
+    }
+    if (!live) s12[0] = 0.0f;
+    block_sums<1>(s12);
+    const float inv_12 = 1.0f / sqrtf(s12[0] / n + eps);
+    const float sc = (float)(_Float16)layer_scalar;
+    h8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const _Float16 t2 = (_Float16)((float)h12[e] * (float)pfw[e] * inv_12);
+        const _Float16 r = (_Float16)((float)hv[e] + (float)t2);
+        o[e] = (_Float16)((float)r * sc);
+    }
+    if (live) reinterpret_cast<h8*>(out)[c] = o;
 }
 
 }  // namespace tfq

@@ -132,6 +132,26 @@ __device__ __forceinline__ float block_sum(float v) {
     return t;
 }
 
+// N independent block sums at once (one pair of barriers for all of them).
+template <int N>
+__device__ __forceinline__ void block_sums(float (&v)[N]) {
+    __shared__ float partn[16][N];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] = seg_sum<kWave>(v[k]);
+    __syncthreads();
+    if (lane == 0)
+#pragma unroll
+        for (int k = 0; k < N; ++k) partn[wave][k] = v[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        float t = 0.0f;
+        for (uint32_t i = 0; i < nwaves; ++i) t += partn[i][k];
+        v[k] = t;
+    }
+}
+
 // 1/sqrt(mean(x^2) + eps) of an fp16 vector held in LDS
 // (V/Reference/Primitives/RmsNorm.swift:18-22 in the reference checkout).
 __device__ __forceinline__ float lds_inv_rms(const uint16_t* __restrict__ lds, uint32_t n, float eps) {
@@ -144,13 +164,24 @@ __device__ __forceinline__ float lds_inv_rms(const uint16_t* __restrict__ lds, u
     return 1.0f / sqrtf(total / (float)n + eps);
 }
 
-// Copies n fp16 values to LDS (16-byte transfers when x is 16-byte aligned).
+// Copies n fp16 values to LDS (16-byte transfers when x is 16-byte aligned;
+// each thread issues up to four loads before its first store, so a copy of
+// up to 4·8·blockDim values costs one memory latency).
 __device__ __forceinline__ void copy_to_lds(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
                                             uint32_t n) {
     if ((((uintptr_t)x) & 15u) == 0 && (n & 7u) == 0) {
         const uint4* src = reinterpret_cast<const uint4*>(x);
         uint4* dst = reinterpret_cast<uint4*>(lds);
-        for (uint32_t i = threadIdx.x; i < (n >> 3); i += blockDim.x) dst[i] = src[i];
+        const uint32_t nch = n >> 3, bd = blockDim.x;
+        for (uint32_t base = threadIdx.x; base < nch; base += 4 * bd) {
+            uint4 v[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k)
+                if (base + k * bd < nch) v[k] = src[base + k * bd];
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k)
+                if (base + k * bd < nch) dst[base + k * bd] = v[k];
+        }
     } else {
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lds[i] = x[i];
     }
@@ -168,15 +199,12 @@ __device__ __forceinline__ void rmsnorm_lds(uint16_t* __restrict__ lds, uint32_t
     __syncthreads();
 }
 
-// Stages the activation vector of a kernel into LDS as NormArg describes.
-// Synchronises the block.
-__device__ __forceinline__ void stage_act(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
-                                          uint32_t n, const NormArg& na) {
+// Scalar form of stage_act (any alignment, any n).
+__device__ __forceinline__ void stage_act_scalar(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
+                                                 uint32_t n, const NormArg& na) {
     copy_to_lds(x, lds, n);
     __syncthreads();
     if (na.mode == kStagePostAttn || na.mode == kStageResidual) {
-        // attention-output norm, then the residual add, each rounded to fp16
-        // (fused_post_attn_setup, S/Metal/Fusions/fused.metal:199-231)
         float ss = 0.0f;
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
             const float v = h2f(na.attn[i]);
@@ -190,6 +218,81 @@ __device__ __forceinline__ void stage_act(const uint16_t* __restrict__ x, uint16
         __syncthreads();
     }
     if (na.mode == kStageNorm || na.mode == kStagePostAttn) rmsnorm_lds(lds, n, na.w, na.eps);
+}
+
+constexpr uint32_t kStageChunks = 2;     // 16-byte chunks per thread on the vector path
+
+__device__ __forceinline__ uint4 ld16h(const uint16_t* p, uint32_t chunk) {
+    return reinterpret_cast<const uint4*>(p)[chunk];
+}
+
+// Stages the activation vector of a kernel into LDS as NormArg describes
+// (attention-output norm and residual add: fused_post_attn_setup,
+// S/Metal/Fusions/fused.metal:199-231). Vector path: every thread issues the
+// 16-byte loads of all its chunks of every input at once, then reduces from
+// registers, so the staging costs one memory latency instead of one per
+// element. Synchronises the block.
+__device__ __forceinline__ void stage_act(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
+                                          uint32_t n, const NormArg& na) {
+    const uint32_t nch = n >> 3;
+    const uintptr_t align = (uintptr_t)x | (uintptr_t)na.w | (uintptr_t)na.attn | (uintptr_t)na.attn_w;
+    if ((align & 15u) != 0 || (n & 7u) != 0 || nch > kStageChunks * blockDim.x) {
+        stage_act_scalar(x, lds, n, na);
+        return;
+    }
+    const bool post = na.mode == kStagePostAttn || na.mode == kStageResidual;
+    const bool norm = na.mode == kStageNorm || na.mode == kStagePostAttn;
+    h8 xv[kStageChunks], av[kStageChunks], awv[kStageChunks], wv[kStageChunks];
+#pragma unroll
+    for (uint32_t i = 0; i < kStageChunks; ++i) {
+        const uint32_t c = threadIdx.x + i * blockDim.x;
+        if (c < nch) {
+            xv[i] = __builtin_bit_cast(h8, ld16h(x, c));
+            if (post) {
+                av[i] = __builtin_bit_cast(h8, ld16h(na.attn, c));
+                awv[i] = __builtin_bit_cast(h8, ld16h(na.attn_w, c));
+            }
+            if (norm && na.w) wv[i] = __builtin_bit_cast(h8, ld16h(na.w, c));
+        }
+    }
+    if (post) {
+        float ss = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < kStageChunks; ++i)
+            if (threadIdx.x + i * blockDim.x < nch)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = fmaf((float)av[i][e], (float)av[i][e], ss);
+        const float inv = 1.0f / sqrtf(block_sum(ss) / (float)n + na.eps);
+#pragma unroll
+        for (uint32_t i = 0; i < kStageChunks; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const _Float16 an = (_Float16)((float)av[i][e] * (float)awv[i][e] * inv);
+                xv[i][e] = (_Float16)((float)xv[i][e] + (float)an);
+            }
+    }
+    if (norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < kStageChunks; ++i)
+            if (threadIdx.x + i * blockDim.x < nch)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = fmaf((float)xv[i][e], (float)xv[i][e], ss);
+        const float inv = 1.0f / sqrtf(block_sum(ss) / (float)n + na.eps);
+#pragma unroll
+        for (uint32_t i = 0; i < kStageChunks; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float xw = na.w ? (float)xv[i][e] * (float)wv[i][e] : (float)xv[i][e];
+                xv[i][e] = (_Float16)(xw * inv);
+            }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kStageChunks; ++i) {
+        const uint32_t c = threadIdx.x + i * blockDim.x;
+        if (c < nch) reinterpret_cast<h8*>(lds)[c] = xv[i];
+    }
+    __syncthreads();
 }
 
 // Plain staging (no normalisation).

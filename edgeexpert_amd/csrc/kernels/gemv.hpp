@@ -228,7 +228,9 @@ __device__ __forceinline__ void q8_gemv(const uint8_t* __restrict__ W, const uin
     q8_rows<SEG, P, R>(
         W, S, B, lds_x, M, n,
         [&]() {
-            for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lds_x[i] = h2f(x[i]);
+            uint16_t* xs = reinterpret_cast<uint16_t*>(lds_x + n);
+            stage_xh(x, xs, n);
+            for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lds_x[i] = h2f(xs[i]);
             __syncthreads();
         },
         [&](uint32_t row, float v) { y[row] = f2h(v); });
@@ -254,10 +256,32 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
         W, S, B, lds_x, E, d,
         [&]() {
             uint16_t* hs = reinterpret_cast<uint16_t*>(lds_x + d);
+            // the effective-scale chunks are loaded before the staging latency
+            const bool vec = (((uintptr_t)eff) & 15u) == 0 && (d >> 3) <= kStageChunks * blockDim.x;
+            h8 ev[kStageChunks];
+            if (eff && vec)
+#pragma unroll
+                for (uint32_t i = 0; i < kStageChunks; ++i) {
+                    const uint32_t c = threadIdx.x + i * blockDim.x;
+                    if (c < (d >> 3)) ev[i] = __builtin_bit_cast(h8, ld16h(eff, c));
+                }
             stage_act(h, hs, d, norm);
-            for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
-                const float hv = h2f(hs[i]);
-                lds_x[i] = eff ? hv * h2f(eff[i]) : hv;
+            if (vec) {
+#pragma unroll
+                for (uint32_t i = 0; i < kStageChunks; ++i) {
+                    const uint32_t c = threadIdx.x + i * blockDim.x;
+                    if (c < (d >> 3)) {
+                        const h8 hv = reinterpret_cast<const h8*>(hs)[c];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            lds_x[8 * c + e] = eff ? (float)hv[e] * (float)ev[i][e] : (float)hv[e];
+                    }
+                }
+            } else {
+                for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
+                    const float hv = h2f(hs[i]);
+                    lds_x[i] = eff ? hv * h2f(eff[i]) : hv;
+                }
             }
             __syncthreads();
         },

@@ -218,7 +218,7 @@ size_t tfq_attention_workspace_bytes(uint32_t head_dim, uint32_t num_q_heads, ui
  * fp16 rounding of the output. Replaces Attention.encodeFull /
  * Attention.encodeSWA (S/Kernels/Attention/Attention.swift:238-370).
  * Contract: head_dim 128 or 256; G in {1, 2, 4}; seq_len in 1...65536;
- * caches and workspace 16-byte aligned. */
+ * q, caches and workspace 16-byte aligned. */
 int tfq_attention_decode(tfq_ctx *ctx, void *stream, const uint16_t *q, const uint16_t *k_cache,
                          const uint16_t *v_cache, uint16_t *out, uint32_t head_dim,
                          uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t seq_len,
