@@ -7,7 +7,8 @@ step: int8 router [128 x 2816] + softmax top-8, then 8 int4 g64 experts
 experts (430 MB) are resident in HBM; the token changes every step (64
 distinct hidden states, rotated) so the selected experts change and mostly
 miss the 256 MB last-level cache. Steps are replayed from a HIP graph that
-holds 64 tokens (3 kernels each).
+holds 64 tokens (3 kernels each: router GEMV, phase 1 with the top-k
+selection folded in, phase 2).
 
 Also measured (extra fields): BASELINE config 0, the int4 g64 GEMV
 [2816 x 2816], cold (rotating through 256 weight copies, 1.14 GB) and warm,
@@ -271,13 +272,13 @@ def main():
             best.append(a.elapsed_ms(b) * 1e3 / count)
         return float(np.median(best))
 
+    logits_all = DeviceBuffer(TOKENS * E * 4)
     k_us = {
-        "router": batch_avg_us(lambda t: moe.encode_router_gemma4(
-            stream, rW, rS, rB, hbuf.ptr(t * D * 2), None, None, idx_all.ptr(t * K * 4),
-            w16_all.ptr(t * K * 2), E, D, K, ws), TOKENS),
-        "phase1": batch_avg_us(lambda t: moe.encode_routed_phase1(
-            stream, pool, idx_all.ptr(t * K * 4), hbuf.ptr(t * D * 2), acts_all.ptr(t * K * F * 2),
-            D, F, K), TOKENS),
+        "router_logits": batch_avg_us(lambda t: moe.encode_router_logits(
+            stream, rW, rS, rB, hbuf.ptr(t * D * 2), None, logits_all.ptr(t * E * 4), E, D), TOKENS),
+        "phase1": batch_avg_us(lambda t: moe.encode_routed_phase1_with_selection(
+            stream, pool, logits_all.ptr(t * E * 4), None, E, idx_all.ptr(t * K * 4), w16_all.ptr(t * K * 2),
+            hbuf.ptr(t * D * 2), acts_all.ptr(t * K * F * 2), D, F, K), TOKENS),
         "phase2": batch_avg_us(lambda t: moe.encode_routed_phase2(
             stream, pool, idx_all.ptr(t * K * 4), acts_all.ptr(t * K * F * 2), w16_all.ptr(t * K * 2),
             None, ybuf.ptr(t * D * 2), D, F, K), TOKENS),
@@ -376,11 +377,13 @@ def main():
         "data": "synthetic (seeded SplitMix64, BASELINE distributions)",
         "config": {"workload": "config1_moe_decode", "experts": E, "top_k": K, "d": D, "f": F,
                    "tokens_rotated": TOKENS, "launch": args.launch,
-                   "kernels_per_token": "router_logits, router_select, moe_phase1, moe_phase2"},
-        "roofline": {"kernel": "tfq_moe_phase1 (gate/up of 8 experts)", "bound": "hbm",
+                   "kernels_per_token": "router_logits, moe_phase1_routed (top-k selection + gate/up), "
+                                        "moe_phase2"},
+        "roofline": {"kernel": "tfq_moe_phase1_routed (top-8 selection + gate/up of 8 experts)",
+                     "bound": "hbm",
                      "achieved": round(p1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(p1_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get("tfq_moe_phase1") if traffic else None,
+                     "traffic": traffic.get("tfq_moe_phase1_routed") if traffic else None,
                      "traffic_source": TRAFFIC_FILE if traffic else None,
                      "algorithmic_bytes": nb["phase1"], "avg_launch_us": round(p1_us, 3),
                      "kernel_avg_us": {k: round(v, 3) for k, v in k_us.items()}},

@@ -96,6 +96,9 @@ SIGNATURES = {
     "tfq_gemv_q8g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32],
     "tfq_router_topk": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
     "tfq_moe_phase1": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _U32, _U32, _U32],
+    "tfq_router_logits": [_P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32],
+    "tfq_moe_phase1_routed": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _U32, _P, _P, _P, _P, _P, _U32,
+                              _U32, _U32],
     "tfq_moe_phase1_subset": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _P, _U32, _U32, _U32,
                               _U32],
     "tfq_moe_phase2": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _P, _P, _U32, _U32, _U32],

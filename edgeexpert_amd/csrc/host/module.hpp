@@ -87,4 +87,26 @@ inline SegShape seg_shape(uint32_t chunks, uint32_t min_seg) {
     return {64, (chunks + 63) / 64};
 }
 
+// int4 families: the (SEG >= 8, P <= 4) pair with the fewest idle chunk
+// slots (SEG·P - chunks); ties go to the larger SEG (fewer registers).
+inline SegShape seg_shape_fit(uint32_t chunks, uint32_t min_seg) {
+#ifdef TFQ_SEG_MAX64
+    return seg_shape(chunks, min_seg);
+#else
+    if (chunks <= 8) return seg_shape(chunks, min_seg);
+    SegShape best{64, (chunks + 63) / 64};
+    uint32_t best_waste = best.seg * best.p - chunks;
+    for (uint32_t seg = 32; seg >= 8; seg >>= 1) {
+        const uint32_t p = (chunks + seg - 1) / seg;
+        if (p > 4) continue;
+        const uint32_t waste = seg * p - chunks;
+        if (waste < best_waste) {
+            best = {seg, p};
+            best_waste = waste;
+        }
+    }
+    return best;
+#endif
+}
+
 }  // namespace tfq

@@ -14,7 +14,10 @@ namespace tfq {
 constexpr uint32_t kBlock = 256;          // 4 wavefronts per block for every GEMV-family kernel
 constexpr uint32_t kMaxGridBlocks = 4096;
 constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident in LDS
-constexpr uint32_t kRowsInFlight = 2;     // rows per segment per group (tfq_kernels.hip)
+#ifndef TFQ_ROWS_IN_FLIGHT
+#define TFQ_ROWS_IN_FLIGHT 1
+#endif
+constexpr uint32_t kRowsInFlight = TFQ_ROWS_IN_FLIGHT;   // rows per segment per group (tfq_kernels.hip)
 
 inline uint32_t grid_for_rows(uint64_t rows, uint32_t rows_per_block) {
     uint64_t g = (rows + rows_per_block - 1) / rows_per_block;
@@ -94,7 +97,7 @@ private:
             if (!aligned(q.s, 2) || !aligned(q.b, 2) || !aligned(q.y, 2) || !aligned(q.r, 2))
                 return fail(TFQ_E_INVAL, "scales/biases/y of matrix %u are not 2-byte aligned", i);
         }
-        const SegShape sh = seg_shape(n / 32, 2);
+        const SegShape sh = seg_shape_fit(n / 32, 2);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_q4_gemv_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
@@ -141,13 +144,32 @@ class MoE {
 public:
     explicit MoE(const Module& m) : m_(m) {}
 
-    // MoE.encodeRouterGemma4 (MoE.swift:147-197), GEMV and selection fused.
+    // MoE.encodeRouterGemma4 (MoE.swift:147-197): the logits GEMV (many
+    // blocks), then a one-block selection; stream order is the only sync.
     int encode_router_gemma4(void* stream, const uint8_t* weights, const uint16_t* scales,
                              const uint16_t* biases, const uint16_t* hidden,
                              const uint16_t* effective_scale, const uint16_t* per_expert_scale,
                              uint32_t* out_indices, uint16_t* out_weights, float* out_weights_f32,
                              float* out_logits, uint32_t num_experts, uint32_t d, uint32_t top_k,
                              void* workspace, const NormArg& stage = stage_copy()) const {
+        float* logits = nullptr;
+        int rc = encode_router_logits(stream, weights, scales, biases, hidden, effective_scale, out_logits,
+                                      num_experts, d, top_k, workspace, stage, &logits);
+        if (rc) return rc;
+        if (!out_indices || !out_weights) return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(out_indices, 4)) return fail(TFQ_E_INVAL, "indices are not 4-byte aligned");
+        void* sargs[] = {&logits, &per_expert_scale, &out_indices, &out_weights, &out_weights_f32,
+                         &num_experts, &top_k};
+        return launch(m_.get("tfq_router_select"), 1, 256, 0, stream, sargs, "tfq_router_select");
+    }
+
+    // The router GEMV alone (the selection then runs inside phase 1); the
+    // logits land in out_logits, or the workspace when it is null.
+    int encode_router_logits(void* stream, const uint8_t* weights, const uint16_t* scales,
+                             const uint16_t* biases, const uint16_t* hidden,
+                             const uint16_t* effective_scale, float* out_logits, uint32_t num_experts,
+                             uint32_t d, uint32_t top_k, void* workspace, const NormArg& stage,
+                             float** logits_used) const {
         if (d == 0 || d % TFQ_GROUP_SIZE != 0)
             return fail(TFQ_E_INVAL, "d=%u must be a positive multiple of 64", d);
         if (d > 4096) return fail(TFQ_E_UNSUPPORTED, "router d=%u exceeds 4096", d);
@@ -155,28 +177,21 @@ public:
             return fail(TFQ_E_INVAL, "numExperts=%u must be in 1...256", num_experts);
         if (top_k == 0 || top_k > 64 || top_k > num_experts)
             return fail(TFQ_E_INVAL, "topK=%u must be in 1...min(64, numExperts)", top_k);
-        if (!weights || !scales || !biases || !hidden || !out_indices || !out_weights || !workspace)
+        if (!weights || !scales || !biases || !hidden || !workspace)
             return fail(TFQ_E_INVAL, "null pointer argument");
         if (!aligned(weights, 16)) return fail(TFQ_E_INVAL, "weights are not 16-byte aligned");
         if (!aligned(workspace, 16)) return fail(TFQ_E_INVAL, "workspace is not 16-byte aligned");
-        if (!aligned(out_indices, 4)) return fail(TFQ_E_INVAL, "indices are not 4-byte aligned");
         if (int rc = check_stage(stage)) return rc;
-        // Logits land in out_logits when given, else in the workspace; a
-        // one-wavefront launch then selects (stream order is the only sync).
         float* logits = out_logits ? out_logits : static_cast<float*>(workspace);
+        *logits_used = logits;
         const SegShape sh = seg_shape(d / 16, 4);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_router_logits_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
         const uint32_t grid = (num_experts + rows_per_block - 1) / rows_per_block;
         NormArg na = stage;
-        void* args[] = {&weights, &scales, &biases, &hidden, &effective_scale, &logits,
-                        &num_experts, &d, &na};
-        int rc = launch(m_.get(name), grid, kBlock, d * 6, stream, args, name);
-        if (rc) return rc;
-        void* sargs[] = {&logits, &per_expert_scale, &out_indices, &out_weights, &out_weights_f32,
-                         &num_experts, &top_k};
-        return launch(m_.get("tfq_router_select"), 1, 256, 0, stream, sargs, "tfq_router_select");
+        void* args[] = {&weights, &scales, &biases, &hidden, &effective_scale, &logits, &num_experts, &d, &na};
+        return launch(m_.get(name), grid, kBlock, d * 6, stream, args, name);
     }
 
     // encodeRoutedPersistentPhase1U16Load / ...SubsetU16Load (MoE.swift:234-310).
@@ -194,7 +209,7 @@ public:
             return fail(TFQ_E_INVAL, "full phase 1 covers exactly topK slots");
         if (active_count > top_k) return fail(TFQ_E_INVAL, "activeCount > topK");
         ExpertPool kp = to_kernel_pool(pool);
-        const SegShape sh = seg_shape(d / 32, 2);
+        const SegShape sh = seg_shape_fit(d / 32, 2);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_moe_phase1_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
@@ -202,6 +217,36 @@ public:
         void* args[] = {&kp, &indices, &active_slots, &active_count, &top_k, &x, &acts, &d, &f, &na};
         return launch(m_.get(name), grid_for_rows((uint64_t)active_count * f, rows_per_block),
                       kBlock, d * 2, stream, args, name);
+    }
+
+    // Phase 1 that also performs the router's selection from `logits`
+    // (every block selects; block 0 writes out_indices / out_weights /
+    // out_weights_f32 for phase 2 and the caller).
+    int encode_phase1_routed(void* stream, const tfq_expert_pool& pool, const float* logits,
+                             const uint16_t* per_expert_scale, uint32_t num_experts, uint32_t* out_indices,
+                             uint16_t* out_weights, float* out_weights_f32, const uint16_t* x,
+                             uint16_t* acts, uint32_t d, uint32_t f, uint32_t top_k,
+                             const NormArg& stage = stage_copy()) const {
+        int rc = check_pool(pool, d, f, top_k);
+        if (rc) return rc;
+        if ((rc = check_stage(stage))) return rc;
+        if (d > kMaxN) return fail(TFQ_E_UNSUPPORTED, "d=%u exceeds %u", d, kMaxN);
+        if (!logits || !out_indices || !out_weights || !x || !acts)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (num_experts != pool.num_experts)
+            return fail(TFQ_E_INVAL, "router has %u experts, pool %u", num_experts, pool.num_experts);
+        if (num_experts > 256 || top_k > num_experts)
+            return fail(TFQ_E_INVAL, "numExperts must be <= 256 and >= topK");
+        ExpertPool kp = to_kernel_pool(pool);
+        const SegShape sh = seg_shape_fit(d / 32, 2);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_moe_phase1_routed_s%u_p%u", sh.seg, sh.p);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
+        NormArg na = stage;
+        void* args[] = {&kp,   &logits, &per_expert_scale, &num_experts, &top_k, &out_indices, &out_weights,
+                        &out_weights_f32, &x, &acts, &d, &f, &na};
+        return launch(m_.get(name), grid_for_rows((uint64_t)top_k * f, rows_per_block), kBlock, d * 2,
+                      stream, args, name);
     }
 
     // encodeRoutedPersistentPhase2Reduce (MoE.swift:312-362).
@@ -278,7 +323,7 @@ public:
         Q4Mat g = {static_cast<const uint8_t*>(gate.weights), gate.scales, gate.biases, nullptr, nullptr, f, 0};
         Q4Mat u = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases, nullptr, nullptr, f, 0};
         NormArg na = stage;
-        const SegShape sh = seg_shape(d / 32, 2);
+        const SegShape sh = seg_shape_fit(d / 32, 2);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_gate_up_act_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
@@ -634,14 +679,15 @@ public:
         // 5. router on the no-scale norm of h
         const NormArg router_x{nullptr, o, w.post_attention_norm, s.eps, kStagePostAttn};
         const tfq_router& r = w.router;
-        rc = moe_.encode_router_gemma4(stream, r.weights, r.scales, r.biases, hidden_in, r.effective_scale,
-                                       r.per_expert_scale, idx, rw, nullptr, logits, r.num_experts, s.d,
-                                       s.top_k, logits, router_x);
+        float* logits_used = nullptr;
+        rc = moe_.encode_router_logits(stream, r.weights, r.scales, r.biases, hidden_in, r.effective_scale,
+                                       logits, r.num_experts, s.d, s.top_k, logits, router_x, &logits_used);
         if (rc) return rc;
-        // 6. routed experts on pre_feedforward_layernorm_2(h); phase 2 without residual
+        // 6. routed experts on pre_feedforward_layernorm_2(h), the top-k selected inside
+        //    phase 1; phase 2 without residual
         const NormArg routed{w.pre_ffn2_norm, o, w.post_attention_norm, s.eps, kStagePostAttn};
-        rc = moe_.encode_phase1(stream, w.experts, idx, hidden_in, acts, nullptr, s.top_k, s.d, s.expert_f,
-                                s.top_k, routed);
+        rc = moe_.encode_phase1_routed(stream, w.experts, logits, r.per_expert_scale, r.num_experts, idx, rw,
+                                       nullptr, hidden_in, acts, s.d, s.expert_f, s.top_k, routed);
         if (rc) return rc;
         rc = moe_.encode_phase2(stream, w.experts, idx, acts, rw, nullptr, h2, s.d, s.expert_f, s.top_k);
         if (rc) return rc;

@@ -23,13 +23,15 @@ ErrorState& error_state() {
 
 static std::vector<std::string> kernel_names() {
     std::vector<std::string> names;
-    const char* q4_shapes[] = {"s2_p1", "s4_p1", "s8_p1", "s16_p1", "s32_p1",
-                               "s64_p1", "s64_p2", "s64_p3", "s64_p4"};
+    const char* q4_shapes[] = {"s2_p1",  "s4_p1",  "s8_p1",  "s8_p2",  "s8_p3",  "s8_p4",
+                               "s16_p1", "s16_p2", "s16_p3", "s16_p4", "s32_p1", "s32_p2",
+                               "s32_p3", "s32_p4", "s64_p1", "s64_p2", "s64_p3", "s64_p4"};
     const char* q8_shapes[] = {"s4_p1", "s8_p1", "s16_p1", "s32_p1",
                                "s64_p1", "s64_p2", "s64_p3", "s64_p4"};
     for (const char* s : q4_shapes) {
         names.push_back(std::string("tfq_q4_gemv_") + s);
         names.push_back(std::string("tfq_moe_phase1_") + s);
+        names.push_back(std::string("tfq_moe_phase1_routed_") + s);
         names.push_back(std::string("tfq_gate_up_act_") + s);
     }
     for (const char* s : q8_shapes) {
@@ -239,6 +241,26 @@ int tfq_moe_decode(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, cons
                                    y, d, f, top_k);
 }
 
+int tfq_router_logits(tfq_ctx* ctx, void* stream, const uint8_t* weights, const uint16_t* scales,
+                      const uint16_t* biases, const uint16_t* hidden, const uint16_t* effective_scale,
+                      float* logits, uint32_t num_experts, uint32_t d) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!logits) return fail(TFQ_E_INVAL, "null logits");
+    float* used = nullptr;
+    return ctx->moe->encode_router_logits(stream, weights, scales, biases, hidden, effective_scale, logits,
+                                          num_experts, d, 1, logits, stage_copy(), &used);
+}
+
+int tfq_moe_phase1_routed(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, const float* logits,
+                          const uint16_t* per_expert_scale, uint32_t num_experts, uint32_t* out_indices,
+                          uint16_t* out_weights, float* out_weights_f32, const uint16_t* x, uint16_t* acts,
+                          uint32_t d, uint32_t f, uint32_t top_k) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!pool) return fail(TFQ_E_INVAL, "null pool");
+    return ctx->moe->encode_phase1_routed(stream, *pool, logits, per_expert_scale, num_experts, out_indices,
+                                          out_weights, out_weights_f32, x, acts, d, f, top_k);
+}
+
 int tfq_moe_decode_token(tfq_ctx* ctx, void* stream, const tfq_router* router,
                          const tfq_expert_pool* pool, const uint16_t* x, const uint16_t* residual,
                          uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k, uint32_t* out_indices,
@@ -248,13 +270,13 @@ int tfq_moe_decode_token(tfq_ctx* ctx, void* stream, const tfq_router* router,
     if (router->num_experts != pool->num_experts)
         return fail(TFQ_E_INVAL, "router has %u experts, pool %u", router->num_experts,
                     pool->num_experts);
-    int rc = ctx->moe->encode_router_gemma4(stream, router->weights, router->scales, router->biases,
-                                            x, router->effective_scale, router->per_expert_scale,
-                                            out_indices, out_weights, nullptr, nullptr,
-                                            router->num_experts, d, top_k, workspace);
+    float* logits = nullptr;
+    int rc = ctx->moe->encode_router_logits(stream, router->weights, router->scales, router->biases, x,
+                                            router->effective_scale, nullptr, router->num_experts, d, top_k,
+                                            workspace, stage_copy(), &logits);
     if (rc) return rc;
-    rc = ctx->moe->encode_phase1(stream, *pool, out_indices, x, acts_scratch, nullptr, top_k, d, f,
-                                 top_k);
+    rc = ctx->moe->encode_phase1_routed(stream, *pool, logits, router->per_expert_scale, router->num_experts,
+                                        out_indices, out_weights, nullptr, x, acts_scratch, d, f, top_k);
     if (rc) return rc;
     return ctx->moe->encode_phase2(stream, *pool, out_indices, acts_scratch, out_weights, residual,
                                    y, d, f, top_k);

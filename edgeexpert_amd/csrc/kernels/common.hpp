@@ -58,24 +58,32 @@ __device__ __forceinline__ uint4 ldg16(const uint8_t* p) {
 // ------------------------------------------------------------ int4 chunk ----
 //
 // A chunk is 16 bytes of a weight row: 32 int4 codes, four 32-bit words, code
-// 8j+i in bits 4i..4i+3 of word j. ((w >> 4i) & 0x000F000F) isolates codes
-// 8j+i (low half) and 8j+i+4 (high half); OR-ing 0x6400 into each half gives
-// the fp16 values 1024+q exactly, and subtracting 1024 (v_pk_add_f16) leaves
-// q exactly. v_dot2_f32_f16 then multiplies with the matching activation
-// pair and accumulates in fp32; every product q·x is exact in fp32.
+// 8j+i in bits 4i..4i+3 of word j. Masking a word with 0x000F000F keeps codes
+// 8j (low half) and 8j+4 (high half) in mantissa bits 0-3 of two fp16
+// lanes; OR-ing 0x6400 makes them the exact fp16 values 1024 + q. Masking
+// with 0x00F000F0 keeps codes 8j+1 / 8j+5 in mantissa bits 4-7: 1024 + 16q,
+// also exact. The word shifted right by 8 gives codes 8j+2 / 8j+6 and
+// 8j+3 / 8j+7 the same way. So a word costs 5 bit operations for its 8
+// codes; v_dot2_f32_f16 multiplies each fp16 pair with the matching
+// activation pair (exact products) and accumulates in fp32, into accA for
+// the 1024 + q form and accB for the 1024 + 16q form. The offsets are
+// removed per chunk with the activation sums of the two position classes:
+//     Σ q·x = (accA − 1024·SA) + (accB − 1024·SB) / 16.
 // The activations of a chunk are therefore held as 16 fp16 pairs
 // xp[4j+i] = (x[8j+i], x[8j+i+4]).
 
 struct XChunk {
     h2 p[16];
     float sum;      // Σ of the 32 activations in element order (fp32)
+    float ca;       // 1024 · Σ of the activations at positions 8j+{0,2,4,6}
+    float cb;       // 1024 · Σ of the activations at positions 8j+{1,3,5,7}
 };
 
 // Builds the pair layout of chunk c from an fp16 vector in LDS.
 __device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ lds_xh, uint32_t c,
                                             XChunk& xc) {
     const h8* src = reinterpret_cast<const h8*>(lds_xh + 32u * c);
-    float s = 0.0f;
+    float s = 0.0f, sa = 0.0f, sb = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const h8 v = src[j];
@@ -84,26 +92,34 @@ __device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ lds_xh,
         xc.p[4 * j + 2] = __builtin_shufflevector(v, v, 2, 6);
         xc.p[4 * j + 3] = __builtin_shufflevector(v, v, 3, 7);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += (float)v[e];
+        for (int e = 0; e < 8; ++e) {
+            s += (float)v[e];
+            if (e & 1) sb += (float)v[e];
+            else sa += (float)v[e];
+        }
     }
     xc.sum = s;
+    xc.ca = 1024.0f * sa;
+    xc.cb = 1024.0f * sb;
 }
 
 // Σ_k q_k x_k over the 32 codes of a chunk (fp32 accumulate).
 __device__ __forceinline__ float dot_q4_chunk(const uint4 w, const XChunk& xc) {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-    float acc = 0.0f;
+    float acc_a = 0.0f, acc_b = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t q = ((ws[j] >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
-            const h2 qh = __builtin_bit_cast(h2, q) - k1024;
-            acc = __builtin_amdgcn_fdot2(qh, xc.p[4 * j + i], acc, false);
-        }
+        const uint32_t w8 = ws[j] >> 8;
+        const h2 q0 = __builtin_bit_cast(h2, (ws[j] & 0x000F000Fu) | 0x64006400u);   // 1024 + q
+        const h2 q1 = __builtin_bit_cast(h2, (ws[j] & 0x00F000F0u) | 0x64006400u);   // 1024 + 16q
+        const h2 q2 = __builtin_bit_cast(h2, (w8 & 0x000F000Fu) | 0x64006400u);
+        const h2 q3 = __builtin_bit_cast(h2, (w8 & 0x00F000F0u) | 0x64006400u);
+        acc_a = __builtin_amdgcn_fdot2(q0, xc.p[4 * j + 0], acc_a, false);
+        acc_b = __builtin_amdgcn_fdot2(q1, xc.p[4 * j + 1], acc_b, false);
+        acc_a = __builtin_amdgcn_fdot2(q2, xc.p[4 * j + 2], acc_a, false);
+        acc_b = __builtin_amdgcn_fdot2(q3, xc.p[4 * j + 3], acc_b, false);
     }
-    return acc;
+    return fmaf(acc_b - xc.cb, 0.0625f, acc_a - xc.ca);
 }
 
 // Σ_i q_i * x_i over the 16 int8 codes of one 16-byte chunk, fp32 operands.
@@ -166,21 +182,26 @@ __device__ __forceinline__ float lds_inv_rms(const uint16_t* __restrict__ lds, u
 
 // Copies n fp16 values to LDS (16-byte transfers when x is 16-byte aligned;
 // each thread issues up to four loads before its first store, so a copy of
-// up to 4·8·blockDim values costs one memory latency).
+// up to 4·8·blockDim values costs one memory latency). The loads use clamped
+// (always valid) chunk indices and plain scalars, so the compiler keeps them
+// in registers and in flight together.
 __device__ __forceinline__ void copy_to_lds(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
                                             uint32_t n) {
     if ((((uintptr_t)x) & 15u) == 0 && (n & 7u) == 0) {
         const uint4* src = reinterpret_cast<const uint4*>(x);
         uint4* dst = reinterpret_cast<uint4*>(lds);
         const uint32_t nch = n >> 3, bd = blockDim.x;
+        if (nch == 0) return;
         for (uint32_t base = threadIdx.x; base < nch; base += 4 * bd) {
-            uint4 v[4];
-#pragma unroll
-            for (uint32_t k = 0; k < 4; ++k)
-                if (base + k * bd < nch) v[k] = src[base + k * bd];
-#pragma unroll
-            for (uint32_t k = 0; k < 4; ++k)
-                if (base + k * bd < nch) dst[base + k * bd] = v[k];
+            const uint32_t c1 = base + bd, c2 = base + 2 * bd, c3 = base + 3 * bd;
+            const uint4 v0 = src[base];
+            const uint4 v1 = src[c1 < nch ? c1 : base];
+            const uint4 v2 = src[c2 < nch ? c2 : base];
+            const uint4 v3 = src[c3 < nch ? c3 : base];
+            dst[base] = v0;
+            if (c1 < nch) dst[c1] = v1;
+            if (c2 < nch) dst[c2] = v2;
+            if (c3 < nch) dst[c3] = v3;
         }
     } else {
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lds[i] = x[i];
@@ -236,24 +257,25 @@ __device__ __forceinline__ void stage_act(const uint16_t* __restrict__ x, uint16
                                           uint32_t n, const NormArg& na) {
     const uint32_t nch = n >> 3;
     const uintptr_t align = (uintptr_t)x | (uintptr_t)na.w | (uintptr_t)na.attn | (uintptr_t)na.attn_w;
-    if ((align & 15u) != 0 || (n & 7u) != 0 || nch > kStageChunks * blockDim.x) {
+    if ((align & 15u) != 0 || (n & 7u) != 0 || nch == 0 || nch > kStageChunks * blockDim.x) {
         stage_act_scalar(x, lds, n, na);
         return;
     }
     const bool post = na.mode == kStagePostAttn || na.mode == kStageResidual;
     const bool norm = na.mode == kStageNorm || na.mode == kStagePostAttn;
-    h8 xv[kStageChunks], av[kStageChunks], awv[kStageChunks], wv[kStageChunks];
+    // clamped chunk indices: every load is valid and unconditional (chunks
+    // past the end are loaded twice and never stored or counted)
+    h8 xv[kStageChunks], av[kStageChunks] = {}, awv[kStageChunks] = {}, wv[kStageChunks] = {};
 #pragma unroll
     for (uint32_t i = 0; i < kStageChunks; ++i) {
-        const uint32_t c = threadIdx.x + i * blockDim.x;
-        if (c < nch) {
-            xv[i] = __builtin_bit_cast(h8, ld16h(x, c));
-            if (post) {
-                av[i] = __builtin_bit_cast(h8, ld16h(na.attn, c));
-                awv[i] = __builtin_bit_cast(h8, ld16h(na.attn_w, c));
-            }
-            if (norm && na.w) wv[i] = __builtin_bit_cast(h8, ld16h(na.w, c));
+        const uint32_t c0 = threadIdx.x + i * blockDim.x;
+        const uint32_t c = c0 < nch ? c0 : nch - 1;
+        xv[i] = __builtin_bit_cast(h8, ld16h(x, c));
+        if (post) {
+            av[i] = __builtin_bit_cast(h8, ld16h(na.attn, c));
+            awv[i] = __builtin_bit_cast(h8, ld16h(na.attn_w, c));
         }
+        if (norm && na.w) wv[i] = __builtin_bit_cast(h8, ld16h(na.w, c));
     }
     if (post) {
         float ss = 0.0f;

@@ -288,23 +288,49 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
         [&](uint32_t row, float v) { logits[row] = v; });
 }
 
-// Top-k of E <= 256 logits by (value desc, index asc), in parallel: thread t
-// owns logit t and counts the logits ranked above it (a broadcast scan of the
-// LDS copy); ranks are unique, so the k threads with rank < k each write
-// their slot. `stage` holds the logits; `sel_idx`/`sel_val` receive the k
-// winners in rank order. Ends with a block barrier.
+// Order key of logit v at index t: larger key = ranked first. The float
+// bits are mapped to an unsigned order (sign-magnitude -> biased), and the
+// low half holds ~t so that equal logits rank by lower index.
+__device__ __forceinline__ uint64_t topk_key(float v, uint32_t t) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)(0xFFFFFFFFu - t);
+}
+
+// Top-k of E <= 256 logits by (value desc, index asc), in parallel: the
+// logits become unique 64-bit order keys in LDS, and candidate t's rank is
+// the number of keys above its own (two threads per candidate when the block
+// has them, each scanning half the keys with 16-byte LDS reads; the halves
+// meet with one shuffle). Ranks are unique, so the k candidates with
+// rank < k each write their slot. `stage` holds the E logits; `sel_idx` /
+// `sel_val` receive the k winners in rank order. Ends with a block barrier.
 __device__ __forceinline__ void block_topk(const float* stage, uint32_t E, uint32_t k,
                                            uint32_t* sel_idx, float* sel_val) {
-    for (uint32_t t = threadIdx.x; t < E; t += blockDim.x) {
-        const float v = stage[t];
-        uint32_t rank = 0;
-        for (uint32_t j = 0; j < E; ++j) {
-            const float o = stage[j];
-            rank += (o > v || (o == v && j < t)) ? 1u : 0u;
-        }
-        if (rank < k) {
-            sel_idx[rank] = t;
-            sel_val[rank] = v;
+    __shared__ __attribute__((aligned(16))) uint64_t keys[kRouterMaxExperts];
+    const uint32_t ep = (E + 1) & ~1u;
+    for (uint32_t t = threadIdx.x; t < ep; t += blockDim.x) keys[t] = t < E ? topk_key(stage[t], t) : 0ull;
+    __syncthreads();
+    const uint32_t split = (2 * E <= blockDim.x) ? 2u : 1u;
+    const uint32_t pairs = ep >> 1, per = (pairs + split - 1) / split;
+    for (uint32_t base = 0; base < E * split; base += blockDim.x) {
+        const uint32_t slot = base + threadIdx.x;
+        const uint32_t t = slot / split, half = slot % split;
+        if (t < E) {
+            const uint64_t kt = keys[t];
+            const uint32_t p0 = half * per, p1 = p0 + per < pairs ? p0 + per : pairs;
+            const ulonglong2* k2 = reinterpret_cast<const ulonglong2*>(keys);
+            uint32_t rank = 0;
+#pragma unroll 8
+            for (uint32_t p = p0; p < p1; ++p) {
+                const ulonglong2 kk = k2[p];
+                rank += kk.x > kt ? 1u : 0u;
+                rank += kk.y > kt ? 1u : 0u;
+            }
+            if (split == 2) rank += __shfl_xor(rank, 1, kWave);
+            if (half == 0 && rank < k) {
+                sel_idx[rank] = t;
+                sel_val[rank] = stage[t];
+            }
         }
     }
     __syncthreads();
@@ -331,20 +357,38 @@ __device__ __forceinline__ void block_softmax_gain(const uint32_t* sel_idx, cons
     __syncthreads();
 }
 
+// Selection of one block from logits already staged in LDS (16-byte
+// aligned, padded to a multiple of 4 with -inf): top-k indices and
+// softmax × gain weights into the caller's LDS arrays (k entries).
+// Deterministic: every block that runs it on the same logits gets the same
+// bits.
+__device__ __forceinline__ void router_select_staged(const float* stage, const uint16_t* __restrict__ gain,
+                                                     uint32_t E, uint32_t k, uint32_t* sel_idx, float* sel_w) {
+    __shared__ float sel_val[kRouterMaxTopK];
+    __shared__ float ex[kRouterMaxTopK];
+    block_topk(stage, E, k, sel_idx, sel_val);
+    block_softmax_gain(sel_idx, sel_val, k, gain, ex, sel_w);
+}
+
+// As router_select_staged, reading the logits from global memory.
+__device__ __forceinline__ void router_select_lds(const float* __restrict__ logits,
+                                                  const uint16_t* __restrict__ gain, uint32_t E, uint32_t k,
+                                                  uint32_t* sel_idx, float* sel_w) {
+    __shared__ __attribute__((aligned(16))) float stage[kRouterMaxExperts];
+    for (uint32_t e = threadIdx.x; e < ((E + 3) & ~3u); e += blockDim.x)
+        stage[e] = e < E ? logits[e] : -__builtin_inff();
+    __syncthreads();
+    router_select_staged(stage, gain, E, k, sel_idx, sel_w);
+}
+
 // Selection kernel body: logits (global) -> indices, fp16 weights, fp32 weights.
 __device__ __forceinline__ void router_select(const float* __restrict__ logits,
                                               const uint16_t* __restrict__ gain,
                                               uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w,
                                               float* __restrict__ out_wf, uint32_t E, uint32_t k) {
-    __shared__ float stage[kRouterMaxExperts];
     __shared__ uint32_t sel_idx[kRouterMaxTopK];
-    __shared__ float sel_val[kRouterMaxTopK];
-    __shared__ float ex[kRouterMaxTopK];
     __shared__ float sel_w[kRouterMaxTopK];
-    for (uint32_t e = threadIdx.x; e < E; e += blockDim.x) stage[e] = logits[e];
-    __syncthreads();
-    block_topk(stage, E, k, sel_idx, sel_val);
-    block_softmax_gain(sel_idx, sel_val, k, gain, ex, sel_w);
+    router_select_lds(logits, gain, E, k, sel_idx, sel_w);
     for (uint32_t r = threadIdx.x; r < k; r += blockDim.x) {
         out_idx[r] = sel_idx[r];
         out_w[r] = f2h(sel_w[r]);

@@ -34,7 +34,8 @@ struct GateUpRow {
 
 // Streams gate/up row pairs of length D against x (fp16 in LDS):
 // `rowfn(row)` -> GateUpRow, `out(row, act)` for live rows (lane 0 of the segment).
-template <int SEG, int P, int R, typename RowFn, typename OutFn>
+// X_STAGED: the caller has already staged x into the dynamic LDS.
+template <int SEG, int P, int R, bool X_STAGED = false, typename RowFn, typename OutFn>
 __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uint32_t D, uint32_t total,
                                              const NormArg& norm, RowFn rowfn, OutFn out) {
     extern __shared__ uint16_t lds_xh[];
@@ -73,7 +74,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
         }
     };
     issue(0);
-    stage_act(x, lds_xh, D, norm);
+    if (!X_STAGED) stage_act(x, lds_xh, D, norm);
     XChunk xc[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -114,7 +115,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
 }
 
 // Phase 1 over n_active slots (active_slots == nullptr: slots 0..n_active-1).
-template <int SEG, int P, int R>
+template <int SEG, int P, int R, bool X_STAGED = false>
 __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint32_t* __restrict__ active_slots, uint32_t n_active,
                                            uint32_t top_k, const uint16_t* __restrict__ x,
@@ -126,7 +127,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
         const uint32_t a = row / F;
         return active_slots ? active_slots[a] : a;
     };
-    gate_up_rows<SEG, P, R>(
+    gate_up_rows<SEG, P, R, X_STAGED>(
         x, D, n_active * F, norm,
         [&](uint32_t row) {
             const uint32_t slot = slot_of(row);
@@ -146,6 +147,41 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
             return q;
         },
         [&](uint32_t row, float act) { acts[(size_t)slot_of(row) * F + row % F] = f2h(act); });
+}
+
+// Phase 1 with the router's selection folded in: every block selects the
+// top-k experts from the logits itself (block_topk, identical bits in every
+// block), so routing costs no launch of its own between the router GEMV and
+// the experts. Block 0 publishes indices and fp16 / fp32 weights for
+// phase 2 and the caller (MoE.encodeRouterGemma4's outputs,
+// S/Kernels/MoE/MoE.swift:147-197).
+template <int SEG, int P, int R>
+__device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const float* __restrict__ logits,
+                                                  const uint16_t* __restrict__ gain, uint32_t E, uint32_t top_k,
+                                                  uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w,
+                                                  float* __restrict__ out_wf, const uint16_t* __restrict__ x,
+                                                  uint16_t* __restrict__ acts, uint32_t D, uint32_t F,
+                                                  const NormArg& norm) {
+    // phase 1 needs only the indices; the routing weights (for phase 2) are
+    // formed by block 0 alone
+    __shared__ __attribute__((aligned(16))) float stage[kRouterMaxExperts];
+    __shared__ uint32_t sel_idx[kRouterMaxTopK];
+    __shared__ float sel_val[kRouterMaxTopK];
+    for (uint32_t e = threadIdx.x; e < ((E + 3) & ~3u); e += blockDim.x)
+        stage[e] = e < E ? logits[e] : -__builtin_inff();
+    __syncthreads();
+    block_topk(stage, E, top_k, sel_idx, sel_val);
+    if (blockIdx.x == 0) {
+        __shared__ float ex[kRouterMaxTopK];
+        __shared__ float sel_w[kRouterMaxTopK];
+        block_softmax_gain(sel_idx, sel_val, top_k, gain, ex, sel_w);
+        for (uint32_t r = threadIdx.x; r < top_k; r += blockDim.x) {
+            out_idx[r] = sel_idx[r];
+            out_w[r] = f2h(sel_w[r]);
+            if (out_wf) out_wf[r] = sel_w[r];
+        }
+    }
+    moe_phase1<SEG, P, R>(pool, sel_idx, nullptr, top_k, top_k, x, acts, D, F, norm);
 }
 
 // Shared-expert gate/up/act: act[i] = fp16(gelu(gate[i]·x) · (up[i]·x)).

@@ -14,7 +14,10 @@
 using namespace tfq;
 
 // Rows each segment keeps in flight (loads issued before the previous rows are reduced).
-constexpr int kRowsInFlight = 2;
+#ifndef TFQ_ROWS_IN_FLIGHT
+#define TFQ_ROWS_IN_FLIGHT 1
+#endif
+constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
 
 #define TFQ_Q4_GEMV(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_q4_gemv_s##SEG##_p##P(                 \
@@ -67,6 +70,15 @@ constexpr int kRowsInFlight = 2;
                                           D, F, norm);                                            \
     }
 
+#define TFQ_PHASE1_ROUTED(SEG, P)                                                                \
+    extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase1_routed_s##SEG##_p##P(       \
+        ExpertPool pool, const float* logits, const uint16_t* gain, uint32_t E, uint32_t top_k,  \
+        uint32_t* out_idx, uint16_t* out_w, float* out_wf, const uint16_t* x, uint16_t* acts,    \
+        uint32_t D, uint32_t F, NormArg norm) {                                                   \
+        moe_phase1_routed<SEG, P, kRowsInFlight>(pool, logits, gain, E, top_k, out_idx, out_w,   \
+                                                 out_wf, x, acts, D, F, norm);                    \
+    }
+
 #define TFQ_PHASE2(P)                                                                            \
     extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase2_p##P(                       \
         ExpertPool pool, const uint32_t* indices, const uint16_t* acts, const uint16_t* rw,      \
@@ -81,13 +93,16 @@ constexpr int kRowsInFlight = 2;
         q4_gate_up_act<SEG, P, kRowsInFlight>(gate, up, x, act, D, F, norm);                      \
     }
 
-// int4: n/32 chunks per row.
-#define TFQ_Q4_TABLE(X) X(2, 1) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 3) X(64, 4)
+// int4: n/32 chunks per row; (SEG, P) with SEG·P >= chunks (the host picks
+// the pair that wastes the fewest lanes).
+#define TFQ_Q4_TABLE(X) X(2, 1) X(4, 1) X(8, 1) X(8, 2) X(8, 3) X(8, 4) X(16, 1) X(16, 2) X(16, 3) \
+    X(16, 4) X(32, 1) X(32, 2) X(32, 3) X(32, 4) X(64, 1) X(64, 2) X(64, 3) X(64, 4)
 // int8: n/16 chunks per row (n <= 4096).
 #define TFQ_Q8_TABLE(X) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 3) X(64, 4)
 
 TFQ_Q4_TABLE(TFQ_Q4_GEMV)
 TFQ_Q4_TABLE(TFQ_PHASE1)
+TFQ_Q4_TABLE(TFQ_PHASE1_ROUTED)
 TFQ_Q4_TABLE(TFQ_GATE_UP)
 TFQ_Q8_TABLE(TFQ_Q8_GEMV)
 TFQ_Q8_TABLE(TFQ_ROUTER)
@@ -105,15 +120,6 @@ TFQ_PHASE2(2)
 TFQ_PHASE2(3)
 TFQ_PHASE2(4)
 
-extern "C" __global__ __launch_bounds__(256) void tfq_router_select(const float* logits,
-                                                                    const uint16_t* gain,
-                                                                    uint32_t* out_idx,
-                                                                    uint16_t* out_w,
-                                                                    float* out_wf, uint32_t E,
-                                                                    uint32_t k) {
-    router_select(logits, gain, out_idx, out_w, out_wf, E, k);
-}
-
 extern "C" __global__ __launch_bounds__(kGemmThreads) void tfq_gemm_q4_f16(
     const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
     uint32_t M, uint32_t N, uint32_t K) {
@@ -124,6 +130,15 @@ extern "C" __global__ __launch_bounds__(kGemmThreads) void tfq_gemm_q4_bf16(
     const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
     uint32_t M, uint32_t N, uint32_t K) {
     gemm_q4<true>(X, W, S, B, Y, M, N, K);
+}
+
+extern "C" __global__ __launch_bounds__(256) void tfq_router_select(const float* logits,
+                                                                    const uint16_t* gain,
+                                                                    uint32_t* out_idx,
+                                                                    uint16_t* out_w,
+                                                                    float* out_wf, uint32_t E,
+                                                                    uint32_t k) {
+    router_select(logits, gain, out_idx, out_w, out_wf, E, k);
 }
 
 // Per-token selection for a prefill chunk: one block per token.

@@ -160,6 +160,23 @@ class MoE:
                                     _addr(out_weights_f32), _addr(out_logits), num_experts, d, top_k,
                                     _addr(workspace)), "MoE.encodeRouterGemma4")
 
+    def encode_router_logits(self, stream, weights, scales, biases, hidden, effective_scale, logits,
+                             num_experts, d):
+        """The router GEMV alone (router_gemv_gemma4_r4)."""
+        check(lib().tfq_router_logits(self.ctx.handle, _s(stream), _addr(weights), _addr(scales),
+                                      _addr(biases), _addr(hidden), _addr(effective_scale), _addr(logits),
+                                      num_experts, d), "MoE.encodeRouterLogits")
+
+    def encode_routed_phase1_with_selection(self, stream, pool: ExpertPool, logits, per_expert_scale,
+                                            num_experts, out_indices, out_weights, x, acts, d, f, top_k,
+                                            out_weights_f32=None):
+        """Top-k selection folded into phase 1 (every block selects; block 0 publishes)."""
+        p = pool.desc()
+        check(lib().tfq_moe_phase1_routed(self.ctx.handle, _s(stream), C.byref(p), _addr(logits),
+                                          _addr(per_expert_scale), num_experts, _addr(out_indices),
+                                          _addr(out_weights), _addr(out_weights_f32), _addr(x), _addr(acts),
+                                          d, f, top_k), "MoE.encodeRoutedPhase1WithSelection")
+
     def encode_routed_phase1(self, stream, pool: ExpertPool, indices, x, acts, d, f, top_k):
         p = pool.desc()
         check(lib().tfq_moe_phase1(self.ctx.handle, _s(stream), C.byref(p), _addr(indices),

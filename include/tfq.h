@@ -116,6 +116,12 @@ int tfq_router_topk(tfq_ctx *ctx, void *stream, const uint8_t *weights, const ui
                     float *out_logits_f32, uint32_t num_experts, uint32_t d, uint32_t top_k,
                     void *workspace);
 
+/* The router GEMV alone: logits[e] (fp32) as in tfq_router_topk
+ * (router_gemv_gemma4_r4, S/Metal/MoE/moe.metal:78-133). Same contract. */
+int tfq_router_logits(tfq_ctx *ctx, void *stream, const uint8_t *weights, const uint16_t *scales,
+                      const uint16_t *biases, const uint16_t *hidden, const uint16_t *effective_scale,
+                      float *logits, uint32_t num_experts, uint32_t d);
+
 /* Sub-tensor byte offsets inside one routed-expert blob
  * (MoEExpertOffsets, S/Kernels/MoE/MoE.swift:4-29). */
 typedef struct {
@@ -153,6 +159,19 @@ int tfq_moe_phase1_subset(tfq_ctx *ctx, void *stream, const tfq_expert_pool *poo
                           const uint32_t *active_slots, uint32_t active_count, uint32_t d,
                           uint32_t f, uint32_t top_k);
 
+/* Phase 1 with the router's selection folded in: every block selects the
+ * top_k experts from `logits` exactly as tfq_router_topk does (identical
+ * results in every block) and block 0 writes out_indices / out_weights
+ * (fp16) / out_weights_f32 (may be NULL). One launch replaces
+ * router_topk_select_k8 + Phase1U16Load (S/Metal/MoE/moe.metal:135-185,
+ * S/Kernels/MoE/MoE.swift:147-266). Contract: as tfq_moe_phase1;
+ * num_experts == pool->num_experts <= 256. */
+int tfq_moe_phase1_routed(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
+                          const float *logits, const uint16_t *per_expert_scale,
+                          uint32_t num_experts, uint32_t *out_indices, uint16_t *out_weights,
+                          float *out_weights_f32, const uint16_t *x, uint16_t *acts, uint32_t d,
+                          uint32_t f, uint32_t top_k);
+
 /* Phase 2: y[d] = fp16(residual[d] + Σ_{slot=0..top_k-1} w[slot]·(down_e[d]·acts[slot])),
  * slots summed in fixed order. routing_weights fp16 [top_k]; residual may be
  * NULL (zeros). Replaces MoE.encodeRoutedPersistentPhase2Reduce
@@ -180,10 +199,12 @@ typedef struct {
     uint32_t num_experts;
 } tfq_router;
 
-/* The whole routed decode block of one token, all on the device: router
- * GEMV + top-k + softmax (tfq_router_topk), phase 1, phase 2. Replaces the
- * decode sequence encodeRouterGemma4 -> CPU readback of the indices -> expert
- * fetch -> Phase1U16Load -> Phase2Reduce (S/Runtime/Inference/
+/* The whole routed decode block of one token, all on the device, in three
+ * launches: router GEMV (logits into the workspace), phase 1 with the top-k
+ * selection folded in (every block selects from the logits; block 0
+ * publishes out_indices / out_weights), phase 2. Replaces the decode
+ * sequence encodeRouterGemma4 -> CPU readback of the indices -> expert fetch
+ * -> Phase1U16Load -> Phase2Reduce (S/Runtime/Inference/
  * RealForwardRunner.swift:2390-2401, 2491-2521, 2822-2864); the indices never
  * leave HBM. out_indices [top_k] / out_weights fp16 [top_k] receive the
  * routing; acts_scratch is fp16 [top_k][f]; workspace is

@@ -155,9 +155,10 @@ def test_gemv_q8_sweep(ctx, stream, m, n):
 
 # ------------------------------------------------------------- router ----
 
-def _run_router(ctx, stream, W, S16, B16, h16, eff16, gain16, E, d, k):
-    ws = DeviceBuffer(ROUTER_WORKSPACE_BYTES)
-    ws.fill(0)
+def _run_router(ctx, stream, W, S16, B16, h16, eff16, gain16, E, d, k, ws=None):
+    if ws is None:
+        ws = DeviceBuffer(ROUTER_WORKSPACE_BYTES)
+        ws.fill(0)
     bufs = [_dev(W), _dev(S16), _dev(B16), _dev(h16)]
     effb = _dev(eff16) if eff16 is not None else None
     gb = _dev(gain16) if gain16 is not None else None
@@ -223,7 +224,7 @@ def test_router_baseline_config1_and_workspace_reuse(ctx, stream):
     ws = None
     for t in range(4):
         h16 = synth.f16_vector(0, f"c1/h{t}", D)
-        idx, w, wf, logits, ws = _run_router(ctx, stream, W, S, B, h16, None, None, E, D, K)
+        idx, w, wf, logits, ws = _run_router(ctx, stream, W, S, B, h16, None, None, E, D, K, ws)
         ref_logits = oracle.router_logits(W, S, B, from_f16_bits(h16))
         ref_idx, ref_w = oracle.topk_softmax(ref_logits, K)
         srt = np.sort(ref_logits)[::-1]
@@ -405,3 +406,41 @@ def test_convert_bf16_to_f16_exact_and_counts_inexact(ctx, stream):
     exact = synth.bf16_to_f32(bits)
     assert np.array_equal(out[:6], exact[:6])
     assert cnt.download(np.uint32, 1)[0] == 3
+
+
+def test_phase1_with_selection_equals_router_select_then_phase1(ctx, stream):
+    # the selection folded into phase 1 must give the routing of
+    # tfq_router_topk and the activations of tfq_moe_phase1, bit for bit
+    E, D, F, K = 128, 2816, 704, 8
+    pool_bytes, offs, stride = synth.expert_pool(3, "sel/experts", E, D, F)
+    Wr, Sr, Br = synth.int8_matrix(3, "sel/router", E, D)
+    gain16 = f16_bits(synth.uniform24(synth.seed_key(3, "sel/gain"), E, 0.5, 1.5))
+    pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs)
+    moe = ops.MoE(ctx)
+    rb = [_dev(Wr), _dev(Sr), _dev(Br)]
+    gb = _dev(gain16)
+    for t in range(3):
+        h16 = synth.f16_vector(3, f"sel/h{t}", D)
+        hb = _dev(h16)
+        ws = DeviceBuffer(ROUTER_WORKSPACE_BYTES)
+        ws.fill(0)
+        logits_a, logits_b = _dev(np.zeros(E, np.float32)), _dev(np.zeros(E, np.float32))
+        i1, w1, f1 = _dev(np.zeros(K, np.uint32)), _dev(np.zeros(K, np.uint16)), _dev(np.zeros(K, np.float32))
+        i2, w2, f2 = _dev(np.zeros(K, np.uint32)), _dev(np.zeros(K, np.uint16)), _dev(np.zeros(K, np.float32))
+        a1, a2 = _dev(np.zeros(K * F, np.uint16)), _dev(np.full(K * F, 0x7E00, np.uint16))
+        moe.encode_router_gemma4(stream, *rb, hb, None, gb, i1, w1, E, D, K, ws, out_weights_f32=f1,
+                                 out_logits=logits_a)
+        moe.encode_routed_phase1(stream, pool, i1, hb, a1, D, F, K)
+        moe.encode_router_logits(stream, *rb, hb, None, logits_b, E, D)
+        moe.encode_routed_phase1_with_selection(stream, pool, logits_b, gb, E, i2, w2, hb, a2, D, F, K,
+                                                out_weights_f32=f2)
+        stream.sync()
+        assert np.array_equal(logits_a.download(np.float32, E).view(np.uint32),
+                              logits_b.download(np.float32, E).view(np.uint32))
+        assert np.array_equal(i1.download(np.uint32, K), i2.download(np.uint32, K))
+        assert np.array_equal(w1.download(np.uint16, K), w2.download(np.uint16, K))
+        assert np.array_equal(f1.download(np.float32, K).view(np.uint32), f2.download(np.float32, K).view(np.uint32))
+        assert np.array_equal(a1.download(np.uint16, K * F), a2.download(np.uint16, K * F))
+        ref_idx, _ = oracle.topk_softmax(oracle.router_logits(Wr, Sr, Br, from_f16_bits(h16)), K,
+                                         from_f16_bits(gain16))
+        assert list(i2.download(np.uint32, K)) == list(ref_idx)

@@ -141,6 +141,9 @@ def _layer_case(ctx, stream, shape, E, pos, cap, seed, label, in_place=False):
         "kslot": from_f16_bits(kb.download(np.uint16, kvd, offset=pos * kvd * 2)),
         "vslot": from_f16_bits(vb.download(np.uint16, kvd, offset=pos * kvd * 2)),
         "kcache": kb.download(np.uint16, cap * kvd),
+        "vcache": vb.download(np.uint16, cap * kvd),
+        "q_raw": from_f16_bits(ws.download(np.uint16, shape["nq"] * shape["hd"], offset=L["q"])),
+        "pos": pos,
     }
     ref = {"out": from_f16_bits(out_ref), "idx": idx_ref, "w": w_ref,
            "attn": from_f16_bits(tr["attn"]), "o": from_f16_bits(tr["o"]), "h1": from_f16_bits(tr["h1"]),
@@ -163,11 +166,19 @@ def _check_layer(got, ref, w, shape, hidden, label):
     assert list(got["idx"]) == list(ref["idx"]), f"{label}: routing differs"
     d, eps = shape["d"], shape["eps"]
     h_in = from_f16_bits(hidden)
-    # stages fed directly by `hidden` and the caches
-    for key in ("kslot", "vslot", "attn"):
+    # the projection (with its fused input norm) and the k/v epilogue, fed by `hidden`
+    for key in ("kslot", "vslot"):
         rel = oracle.rel_error(got[key], ref[key])
         assert rel < TOL, f"{label}: {key} rel={rel}"
     stage = {}
+    # attention: the GPU's raw q through the oracle epilogue, the GPU's caches
+    hd, nq, nkv, pos = shape["hd"], shape["nq"], shape["nkv"], got["pos"]
+    qn = np.concatenate([_n16(got["q_raw"][h * hd:(h + 1) * hd], w["q_norm"], eps) for h in range(nq)])
+    q = f16_round(oracle.rope_neox(qn, nq, hd, shape["rotated_pairs"], pos, shape["theta"]))
+    kvd = nkv * hd
+    K = from_f16_bits(got["kcache"][:(pos + 1) * kvd])
+    V = from_f16_bits(got["vcache"][:(pos + 1) * kvd])
+    stage["attn"] = f16_round(oracle.attention(q, K, V, hd, nq, nkv, pos + 1, shape["window"], shape["scale"]))
     stage["o"] = f16_round(oracle.gemv_int4(*w["o"], got["attn"]))
     h = f16_round(h_in + _n16(got["o"], w["post_attention_norm"], eps))
     logits = oracle.router_logits(w["router_w"], w["router_s"], w["router_b"], _n16(h, None, eps),
