@@ -76,6 +76,45 @@ def c4_bytes():
     return parts
 
 
+def bench_c3(ctx, stream, batch_avg_us):
+    """Config 3: 512 tokens x top-8 of 128 experts with Zipf(1.1) popularity;
+    device grouping -> grouped gate/up + GeGLU -> grouped down -> token-major
+    combine (4 launches), timed back to back over rotated hidden states."""
+    from edgeexpert_amd import ops, synth
+    from edgeexpert_amd.runtime import DeviceBuffer
+    T, k = 512, 8
+    pool_bytes, offs, stride = synth.expert_pool(0, "c1/experts", E, D, F)
+    pool = ops.ExpertPool(DeviceBuffer.from_array(pool_bytes), stride, E, offs)
+    idx, w16 = synth.zipf_routing(0, "c3/route", T, E, k)
+    active = np.unique(idx)
+    n_hidden = 4
+    hid = DeviceBuffer.from_array(np.stack([synth.f16_vector(0, f"c3/x{i}", T * D) for i in range(n_hidden)]))
+    n, mt = T * k, ops.max_tiles(T, k, E)
+    sorted_p = DeviceBuffer(n * 16)
+    offsets, counts = DeviceBuffer(E * 4), DeviceBuffer(E * 4)
+    tiles, n_tiles, status = DeviceBuffer(mt * 16), DeviceBuffer(4), DeviceBuffer(4)
+    act, partials, h2 = DeviceBuffer(n * F * 2), DeviceBuffer(n * D * 2), DeviceBuffer(T * D * 2)
+    idx_b, w_b = DeviceBuffer.from_array(idx), DeviceBuffer.from_array(w16)
+    grouping, grouped = ops.PrefillMoEGrouping(ctx), ops.PrefillGroupedRoutedMoE(ctx)
+
+    def chunk(i):
+        grouping.encode(stream, idx_b, w_b, T, k, E, sorted_p, offsets, counts, tiles, n_tiles, status)
+        grouped.encode(stream, pool, sorted_p, tiles, n_tiles, mt, hid.ptr((i % n_hidden) * T * D * 2), D, D, F,
+                       k, act, partials)
+        grouped.encode_reduce_token_major(stream, partials, w_b, h2, T, k, D)
+
+    us = batch_avg_us(chunk, 8, reps_=3)
+    flop = 2.0 * n * 3 * D * F
+    wbytes = len(active) * 3 * (F * D // 2 + 2 * F * (D // 64) * 2)
+    nbytes = wbytes + 2 * T * D * 2
+    log(f"grouped MoE prefill C3: {us:.1f} us per 512-token chunk ({flop / (us * 1e-6) / 1e12:.1f} TFLOP/s, "
+        f"{nbytes / (us * 1e-6) / 1e9:.0f} GB/s of {len(active)} active experts' weights)")
+    return {"us_per_chunk": round(us, 2), "tokens": T, "top_k": k, "active_experts": int(len(active)),
+            "tflops": round(flop / (us * 1e-6) / 1e12, 1), "weight_bytes": wbytes,
+            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "us_per_token": round(us / T, 3),
+            "kernels": "moe_group, moe_grouped_gate_up, moe_grouped_down, moe_combine"}
+
+
 def bench_c4(ctx, stream, launch, batch_avg_us):
     from edgeexpert_amd import ops, synth
     from edgeexpert_amd.runtime import DeviceBuffer, Event, Graph
@@ -167,6 +206,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 decode-layer leg")
+    ap.add_argument("--no-c3", action="store_true", help="skip the config-3 grouped-prefill leg")
     ap.add_argument("--launch", choices=("graph", "stream"), default="graph",
                     help="replay the 64-token step from a HIP graph, or issue it from the host")
     args = ap.parse_args()
@@ -329,6 +369,28 @@ def main():
     log(f"GEMM C2 (bf16, back-to-back): {gemm_us:.2f} us -> {gemm_tflops:.1f} TFLOP/s "
         f"({gemm_tflops / 2500.0 * 100:.1f}% of 2.5 PFLOP/s dense fp16/bf16)")
 
+    # ------------------------------------ large GEMV: LM-head shape (extra) ----
+    # 262144 x 2816 int4 (415 MB, larger than every cache): the steady-state
+    # streaming rate of the decode GEMV, launched back to back.
+    Ml = 262144
+    Wl, Sl, Bl = synth.int4_matrix(0, "lmhead/w", 4096, 2816)        # 4096-row tile, replicated
+    big_l = DeviceBuffer(Ml * 1408)
+    sl_b, bl_b = DeviceBuffer(Ml * 88), DeviceBuffer(Ml * 88)
+    for r0 in range(0, Ml, 4096):
+        big_l.upload(Wl, r0 * 1408)
+        sl_b.upload(Sl, r0 * 88)
+        bl_b.upload(Bl, r0 * 88)
+    yl = DeviceBuffer(Ml * 2)
+    lm_bytes = Ml * 1408 + 2 * Ml * 88 + 2816 * 2 + Ml * 2
+    lm_us = batch_avg_us(lambda i: gemv.encode(stream, big_l, sl_b, bl_b, x0, yl, Ml, 2816), 8, reps_=3)
+    lm_gbs = lm_bytes / (lm_us * 1e-6) / 1e9
+    log(f"GEMV LM-head shape {Ml}x2816: {lm_us:.1f} us ({lm_gbs:.0f} GB/s, "
+        f"{lm_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+    del big_l, sl_b, bl_b, yl
+
+    # ----------------------------------------- grouped MoE prefill, config 3 ----
+    c3 = None if args.no_c3 else bench_c3(ctx, stream, batch_avg_us)
+
     # ------------------------------------------------ decode layer config 4 ----
     c4 = None if args.no_c4 else bench_c4(ctx, stream, args.launch, batch_avg_us)
 
@@ -397,6 +459,9 @@ def main():
         "gemm_c2": {"shape": [Mg, Ng, Kg], "dtype": "bf16 in/out, fp16 MFMA, fp32 acc",
                     "us": round(gemm_us, 3), "tflops": round(gemm_tflops, 1),
                     "frac_of_dense_peak": round(gemm_tflops / 2500.0, 4)},
+        "gemv_lmhead": {"shape": [Ml, 2816], "bytes": lm_bytes, "us": round(lm_us, 2),
+                        "gbs": round(lm_gbs, 1), "frac": round(lm_gbs / HBM_PEAK_GBS, 4)},
+        "grouped_prefill_c3": c3,
         "decode_layer_c4": c4,
         "wall_s": round(wall, 4),
         "device": f"{name} {arch}",

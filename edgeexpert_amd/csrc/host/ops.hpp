@@ -12,7 +12,10 @@
 namespace tfq {
 
 constexpr uint32_t kBlock = 256;          // 4 wavefronts per block for every GEMV-family kernel
-constexpr uint32_t kMaxGridBlocks = 4096;
+#ifndef TFQ_MAX_GRID_BLOCKS
+#define TFQ_MAX_GRID_BLOCKS 1024
+#endif
+constexpr uint32_t kMaxGridBlocks = TFQ_MAX_GRID_BLOCKS;
 constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident in LDS
 #ifndef TFQ_ROWS_IN_FLIGHT
 #define TFQ_ROWS_IN_FLIGHT 1
