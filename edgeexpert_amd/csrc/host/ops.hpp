@@ -20,7 +20,8 @@ constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident i
 #ifndef TFQ_ROWS_IN_FLIGHT
 #define TFQ_ROWS_IN_FLIGHT 1
 #endif
-constexpr uint32_t kRowsInFlight = TFQ_ROWS_IN_FLIGHT;   // rows per segment per group (tfq_kernels.hip)
+constexpr uint32_t kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
+constexpr uint32_t kGemmBlock = 512;       // threads of the MFMA GEMM tile (gemm.hpp kGemmThreads)   // rows per segment per group (tfq_kernels.hip)
 
 inline uint32_t grid_for_rows(uint64_t rows, uint32_t rows_per_block) {
     uint64_t g = (rows + rows_per_block - 1) / rows_per_block;
@@ -366,7 +367,7 @@ public:
         if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
         const uint32_t gx = (n + 127) / 128, gy = (t + 127) / 128;
         void* args[] = {&x, &weights, &scales, &biases, &y, &t, &n, &k};
-        return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, (hipStream_t)stream, args,
+        return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, kGemmBlock, 1, 1, 0, (hipStream_t)stream, args,
                                                nullptr),
                          name);
     }
@@ -496,10 +497,10 @@ public:
         if (max_tiles == 0) return TFQ_OK;
         ExpertPool kp = kernel_pool(pool);
         void* a1[] = {&kp, &sorted, &tiles, &n_tiles, &hidden, &stride, &act, &d, &f};
-        rc = launch2(m_, "tfq_moe_grouped_gate_up", max_tiles, (f + 127) / 128, 256, 0, stream, a1);
+        rc = launch2(m_, "tfq_moe_grouped_gate_up", max_tiles, (f + 127) / 128, kGemmBlock, 0, stream, a1);
         if (rc) return rc;
         void* a2[] = {&kp, &sorted, &tiles, &n_tiles, &act, &partials, &d, &f, &k};
-        return launch2(m_, "tfq_moe_grouped_down", max_tiles, (d + 127) / 128, 256, 0, stream, a2);
+        return launch2(m_, "tfq_moe_grouped_down", max_tiles, (d + 127) / 128, kGemmBlock, 0, stream, a2);
     }
 
     // PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38).

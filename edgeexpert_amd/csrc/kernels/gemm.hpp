@@ -6,11 +6,13 @@
 // S/Metal/Prefill/prefill.metal:672-709 compute the same product).
 //
 // Block tile 128 rows x 128 outputs, one affine group (64 along K) per step,
-// 4 wavefronts each owning a 64x64 quarter as 2x2 v_mfma_f32_32x32x16_f16
-// tiles per matrix. Per step the block
+// 8 wavefronts (two per SIMD, so one wave's loads and dequantisation overlap
+// the other's MFMAs), each owning a 32x64 slice of the tile as 1x2
+// v_mfma_f32_32x32x16_f16 tiles per matrix. Per step the block
 //   * loads the X tile (16 B per load, coalesced; rows come from a caller
 //     supplied row table, so gathered rows cost nothing extra) and each W
-//     tile (16 B = 32 codes per lane) with its 128 scale/bias pairs,
+//     tile (16 B = 32 codes per lane) with its 128 scale/bias pairs, two
+//     steps ahead of their use (two register stages),
 //   * dequantises in registers: (0x6400 | q) - 1024 gives q exactly as fp16,
 //     then v_pk_fma_f16(q, s, b) rounds q·s + b once to fp16 — the fp16
 //     weight tile the reference's tensor-op kernel stages (tensorops.metal:57-80),
@@ -23,6 +25,8 @@
 // exact for |x| in [2^-14, 65504] (the range of the reference's fp16 path).
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace tfq {
@@ -33,7 +37,7 @@ constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
 constexpr int kGemmBK = 64;
 constexpr int kGemmLdsStride = kGemmBK + 8;       // halves per LDS row (16-byte pad)
-constexpr int kGemmThreads = 256;
+constexpr int kGemmThreads = 512;
 constexpr int kGemmTile = kGemmBM * kGemmLdsStride;
 
 // Permute one 8-element run from natural order to (0,4,1,5,2,6,3,7).
@@ -94,7 +98,7 @@ struct GemmLds {
 
 // Computes the 128x128 tile (rows: row_ptr[0..rows), outputs n0..n0+127 < N)
 // and calls out(j, n, v[NMAT]) for every valid element. row_ptr holds the
-// address of each X row (K elements). Must be called by all 256 threads.
+// address of each X row (K elements). Must be called by all 512 threads.
 template <bool X_BF16, int NMAT, typename Out>
 __device__ __forceinline__ void gemm_tile(GemmLds<NMAT>& L, const uint16_t* const* row_ptr,
                                           uint32_t rows, const Q4Tile (&mats)[NMAT], uint32_t n0,
@@ -105,78 +109,73 @@ __device__ __forceinline__ void gemm_tile(GemmLds<NMAT>& L, const uint16_t* cons
     const uint32_t groups = K >> 6;
     const uint32_t row_bytes = K >> 1;
 
-    // global -> registers: X rows (tid/8 + 32p), 16-byte chunk tid%8 of the
-    // group; W row tid/2, 16-byte half tid%2 of the group's 32 bytes.
+    // global -> registers: X rows tid/8 and tid/8 + 64, 16-byte chunk tid%8
+    // of the group; threads < 256 also load W row tid/2, 16-byte half tid%2
+    // of the group's 32 bytes, with its scale and bias.
     const uint32_t xr = tid >> 3, xc = tid & 7u;
-    const uint32_t wr = tid >> 1, wh = tid & 1u;
-    const bool w_live = n0 + wr < N;
-    uint4 xreg[4];
-    uint4 wreg[NMAT];
-    uint16_t sreg[NMAT], breg[NMAT];
+    const bool w_thread = tid < 256u;
+    const uint32_t wr = (tid & 255u) >> 1, wh = tid & 1u;
+    const bool w_live = w_thread && n0 + wr < N;
+    uint4 xreg[2][2];
+    uint4 wreg[2][NMAT];
+    uint16_t sreg[2][NMAT], breg[2][NMAT];
 
-    auto load_global = [&](uint32_t g) {
+    auto load_global = [&](uint32_t g, int st) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const uint32_t j = xr + 32u * p;
-            xreg[p] = j < rows ? *reinterpret_cast<const uint4*>(row_ptr[j] + g * 64u + 8u * xc)
-                               : make_uint4(0, 0, 0, 0);
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t j = xr + 64u * p;
+            xreg[st][p] = j < rows ? *reinterpret_cast<const uint4*>(row_ptr[j] + g * 64u + 8u * xc)
+                                   : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
             if (w_live) {
                 const size_t n = n0 + wr;
-                wreg[m] = ldg16(mats[m].w + n * row_bytes + g * 32u + 16u * wh);
-                sreg[m] = mats[m].s[n * groups + g];
-                breg[m] = mats[m].b[n * groups + g];
+                wreg[st][m] = ldg16(mats[m].w + n * row_bytes + g * 32u + 16u * wh);
+                sreg[st][m] = mats[m].s[n * groups + g];
+                breg[st][m] = mats[m].b[n * groups + g];
             } else {
-                wreg[m] = make_uint4(0, 0, 0, 0);
-                sreg[m] = 0;
-                breg[m] = 0;
+                wreg[st][m] = make_uint4(0, 0, 0, 0);
+                sreg[st][m] = 0;
+                breg[st][m] = 0;
             }
         }
     };
-    auto store_lds = [&](int buf) {
+    auto store_lds = [&](int st, int buf) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const h8 v = X_BF16 ? bf16x8_to_f16(xreg[p]) : __builtin_bit_cast(h8, xreg[p]);
-            *reinterpret_cast<h8*>(&L.x[buf][(xr + 32u * p) * kGemmLdsStride + 8u * xc]) = perm_0415(v);
+        for (int p = 0; p < 2; ++p) {
+            const h8 v = X_BF16 ? bf16x8_to_f16(xreg[st][p]) : __builtin_bit_cast(h8, xreg[st][p]);
+            *reinterpret_cast<h8*>(&L.x[buf][(xr + 64u * p) * kGemmLdsStride + 8u * xc]) = perm_0415(v);
         }
+        if (w_thread) {
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-            h8 runs[4];
-            dequant_chunk_f16(wreg[m], sreg[m], breg[m], runs);
+            for (int m = 0; m < NMAT; ++m) {
+                h8 runs[4];
+                dequant_chunk_f16(wreg[st][m], sreg[st][m], breg[st][m], runs);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<h8*>(&L.w[m][buf][wr * kGemmLdsStride + 32u * wh + 8u * j]) = runs[j];
+                for (int j = 0; j < 4; ++j)
+                    *reinterpret_cast<h8*>(&L.w[m][buf][wr * kGemmLdsStride + 32u * wh + 8u * j]) = runs[j];
+            }
         }
     };
 
-    f32x16 acc[NMAT][2][2];
+    f32x16 acc[NMAT][2];
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[m][i][j][r] = 0.0f;
+            for (int r = 0; r < 16; ++r) acc[m][j][r] = 0.0f;
 
-    const uint32_t wm = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;
+    // wave w: rows 32·(w/2) .. +31, outputs 64·(w%2) .. +63
+    const uint32_t wm = (wave >> 1) * 32u, wn = (wave & 1u) * 64u;
     const uint32_t arow = lane & 31u, akoff = (lane >> 5) * 8u;
 
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-    for (uint32_t g = 0; g < groups; ++g) {
-        const int cur = g & 1;
-        if (g + 1 < groups) load_global(g + 1);
+    auto mma_step = [&](int cur) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            h8 a[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                a[i] = *reinterpret_cast<const h8*>(
-                    &L.x[cur][(wm + 32u * i + arow) * kGemmLdsStride + 16u * ks + akoff]);
+            const h8 a = *reinterpret_cast<const h8*>(
+                &L.x[cur][(wm + arow) * kGemmLdsStride + 16u * ks + akoff]);
 #pragma unroll
             for (int m = 0; m < NMAT; ++m) {
                 h8 b[2];
@@ -185,32 +184,45 @@ __device__ __forceinline__ void gemm_tile(GemmLds<NMAT>& L, const uint16_t* cons
                     b[j] = *reinterpret_cast<const h8*>(
                         &L.w[m][cur][(wn + 32u * j + arow) * kGemmLdsStride + 16u * ks + akoff]);
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[m][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[m][i][j], 0, 0, 0);
+                for (int j = 0; j < 2; ++j)
+                    acc[m][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[j], acc[m][j], 0, 0, 0);
             }
         }
-        if (g + 1 < groups) store_lds(cur ^ 1);
+    };
+
+    // one step: register stage and LDS buffer `cur` hold group g; refill the
+    // stage with g+2, multiply, store the other stage (g+1) into the other
+    // buffer. Stage indices are compile-time (the loop is unrolled by two),
+    // so the register stages never go to scratch.
+    auto step = [&](uint32_t g, auto cur_c) {
+        constexpr int cur = decltype(cur_c)::value;
+        if (g + 2 < groups) load_global(g + 2, cur);
+        mma_step(cur);
+        if (g + 1 < groups) store_lds(cur ^ 1, cur ^ 1);
         __syncthreads();
+    };
+    load_global(0, 0);
+    if (groups > 1) load_global(1, 1);
+    store_lds(0, 0);
+    __syncthreads();
+    for (uint32_t g = 0; g < groups; g += 2) {
+        step(g, std::integral_constant<int, 0>{});
+        if (g + 1 < groups) step(g + 1, std::integral_constant<int, 1>{});
     }
 
     // D layout (32x32 tile): column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4.
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t col = n0 + wn + 32u * j + (lane & 31u);
+        if (col >= N) continue;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t col = n0 + wn + 32u * j + (lane & 31u);
-            if (col >= N) continue;
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = wm + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3);
+            if (row < rows) {
+                float v[NMAT];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t row = wm + 32u * i + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3);
-                if (row < rows) {
-                    float v[NMAT];
-#pragma unroll
-                    for (int m = 0; m < NMAT; ++m) v[m] = acc[m][i][j][r];
-                    out(row, col, v);
-                }
+                for (int m = 0; m < NMAT; ++m) v[m] = acc[m][j][r];
+                out(row, col, v);
             }
         }
     }
