@@ -287,11 +287,11 @@ def main():
     nb = moe_bytes()
     moe = ops.MoE(ctx)
 
-    # A one-block read of 64 MiB (~1 ms of GPU time, one launch) queued ahead
+    # A one-block read of 256 MiB (a few ms of GPU time, one launch) queued ahead
     # of every timed batch: the host enqueues the whole batch while the GPU is
     # still busy with it, so the events see kernels back to back with no
     # host launch gaps (also under a profiler, where launches are slower).
-    pad_bytes = 64 << 20
+    pad_bytes = 256 << 20
     pad_buf = DeviceBuffer(pad_bytes)
     pad_buf.fill(0)
     pad_sink = DeviceBuffer(256)
