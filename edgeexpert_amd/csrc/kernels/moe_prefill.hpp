@@ -45,15 +45,28 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
     __shared__ uint8_t rank_in_chunk[kGroupMaxPairs];
     __shared__ uint32_t base[kGroupMaxExperts], tot[kGroupMaxExperts], tile_base[kGroupMaxExperts + 1];
     __shared__ uint32_t bad;
+    constexpr uint32_t kPer = kGroupMaxPairs / kGroupThreads;     // pairs per thread (8)
     const uint32_t tid = threadIdx.x;
     const uint32_t n = T * k;
     const uint32_t nchunks = (n + 63) / 64;
+    // every thread loads its pairs' experts and weights once, all loads in flight together
+    uint32_t my_e[kPer];
+    uint16_t my_w[kPer];
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j) {
+        const uint32_t i = tid + j * kGroupThreads;
+        my_e[j] = i < n ? idx[i] : 0u;
+        my_w[j] = i < n ? w[i] : (uint16_t)0;
+    }
     if (tid == 0) bad = 0;
     for (uint32_t i = tid; i < nchunks * kGroupMaxExperts; i += blockDim.x)
         (&cnt[0][0])[i] = 0;
+    uint32_t my_bad = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j)
+        if (tid + j * kGroupThreads < n && my_e[j] >= E) my_bad = 1;
     __syncthreads();
-    for (uint32_t i = tid; i < n; i += blockDim.x)
-        if (idx[i] >= E) atomicOr(&bad, 1u);
+    if (my_bad) atomicOr(&bad, 1u);
     __syncthreads();
     if (bad) {
         for (uint32_t e = tid; e < E; e += blockDim.x) {
@@ -67,30 +80,35 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
         return;
     }
 
-    const uint32_t lane = tid & 63u, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    // rank of each pair among equal experts inside its 64-pair chunk: pair
+    // i = tid + j·1024 sits in chunk i/64 = (tid/64) + 16j, lane tid%64. The
+    // lanes holding the same expert are found with one ballot per bit of the
+    // expert id (a wave-wide match), so the cost does not grow with the
+    // number of distinct experts in the chunk.
+    const uint32_t lane = tid & 63u;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (uint32_t c = wave; c < nchunks; c += nwaves) {
-        const uint32_t i = c * 64 + lane;
+    const uint32_t ebits = E > 1 ? 32u - (uint32_t)__clz((int)(E - 1)) : 1u;
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j) {
+        const uint32_t i = tid + j * kGroupThreads;
+        const uint32_t c = i >> 6;
+        if (c >= nchunks) continue;                       // wave-uniform
         const bool valid = i < n;
-        const uint32_t e = valid ? idx[i] : 0xFFFFFFFFu;
-        bool active = valid;
-        uint32_t my_rank = 0;
-        while (true) {
-            const uint64_t act = __ballot(active);
-            if (act == 0) break;
-            const int leader = __ffsll((unsigned long long)act) - 1;
-            const uint32_t e0 = (uint32_t)__shfl((int)e, leader, kWave);
-            const bool mine = active && e == e0;
-            const uint64_t m = __ballot(mine);
-            if (mine) {
-                my_rank = (uint32_t)__popcll(m & lt_mask);
-                active = false;
-            }
-            if ((int)lane == leader) cnt[c][e0] = (uint16_t)__popcll(m);
+        const uint32_t e = my_e[j];
+        uint64_t same = __ballot(valid);
+        for (uint32_t b = 0; b < ebits; ++b) {
+            const bool bit = (e >> b) & 1u;
+            const uint64_t set = __ballot(bit);
+            same &= bit ? set : ~set;
         }
-        if (valid) rank_in_chunk[i] = (uint8_t)my_rank;
+        if (valid) {
+            const uint32_t my_rank = (uint32_t)__popcll(same & lt_mask);
+            if (my_rank == 0) cnt[c][e] = (uint16_t)__popcll(same);
+            rank_in_chunk[i] = (uint8_t)my_rank;
+        }
     }
     __syncthreads();
+    // per expert: exclusive scan over the chunks (in chunk order)
     for (uint32_t e = tid; e < E; e += blockDim.x) {
         uint32_t run = 0;
         for (uint32_t c = 0; c < nchunks; ++c) {
@@ -101,17 +119,36 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
         tot[e] = run;
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t s = 0, ts = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            base[e] = s;
-            tile_base[e] = ts;
-            s += tot[e];
-            ts += (tot[e] + kGemmBM - 1) / kGemmBM;
+    // exclusive scans over the experts of the pair counts and tile counts:
+    // one wavefront, 64 experts per pass with a shuffle scan
+    if (tid < 64) {
+        uint32_t carry_p = 0, carry_t = 0;
+        for (uint32_t e0 = 0; e0 < E; e0 += 64) {
+            const uint32_t e = e0 + tid;
+            const uint32_t p = e < E ? tot[e] : 0u;
+            const uint32_t t = (p + kGemmBM - 1) / kGemmBM;
+            uint32_t sp = p, st = t;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t up = (uint32_t)__shfl_up((int)sp, o, kWave);
+                const uint32_t ut = (uint32_t)__shfl_up((int)st, o, kWave);
+                if ((int)tid >= o) {
+                    sp += up;
+                    st += ut;
+                }
+            }
+            if (e < E) {
+                base[e] = carry_p + sp - p;
+                tile_base[e] = carry_t + st - t;
+            }
+            carry_p += (uint32_t)__shfl((int)sp, 63, kWave);
+            carry_t += (uint32_t)__shfl((int)st, 63, kWave);
         }
-        tile_base[E] = ts;
-        *n_tiles = ts;
-        *status = kGroupOk;
+        if (tid == 0) {
+            tile_base[E] = carry_t;
+            *n_tiles = carry_t;
+            *status = kGroupOk;
+        }
     }
     __syncthreads();
     for (uint32_t e = tid; e < E; e += blockDim.x) {
@@ -123,10 +160,14 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
             tiles[t] = {e, start, left < (uint32_t)kGemmBM ? left : (uint32_t)kGemmBM, 0u};
         }
     }
-    for (uint32_t i = tid; i < n; i += blockDim.x) {
-        const uint32_t e = idx[i];
-        const uint32_t pos = base[e] + cnt[i / 64][e] + rank_in_chunk[i];
-        sorted[pos] = {i / k, e, i % k, (uint32_t)w[i]};
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j) {
+        const uint32_t i = tid + j * kGroupThreads;
+        if (i < n) {
+            const uint32_t e = my_e[j];
+            const uint32_t pos = base[e] + cnt[i / 64][e] + rank_in_chunk[i];
+            sorted[pos] = {i / k, e, i % k, (uint32_t)my_w[j]};
+        }
     }
 }
 
