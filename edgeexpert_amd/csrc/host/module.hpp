@@ -7,8 +7,11 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <map>
+#include <mutex>
 #include <string>
 #include <unordered_map>
+#include <utility>
 
 #include "../../../include/tfq.h"
 
@@ -57,10 +60,18 @@ public:
     }
     int device() const { return device_; }
 
+    // Blocks of `block` threads and `lds` dynamic LDS bytes that the whole GPU
+    // holds resident at once for kernel f (occupancy per CU x CUs); cached
+    // per (kernel, lds), at least 1.
+    uint32_t resident_blocks(hipFunction_t f, uint32_t block, uint32_t lds) const;
+
 private:
     hipModule_t module_ = nullptr;
     int device_ = -1;
+    uint32_t cus_ = 1;
     std::unordered_map<std::string, hipFunction_t> fns_;
+    mutable std::mutex occ_mu_;
+    mutable std::map<std::pair<hipFunction_t, uint64_t>, uint32_t> occ_;
 };
 
 // Launch with kernel arguments given as an array of pointers to values.

@@ -12,10 +12,6 @@
 namespace tfq {
 
 constexpr uint32_t kBlock = 256;          // 4 wavefronts per block for every GEMV-family kernel
-#ifndef TFQ_MAX_GRID_BLOCKS
-#define TFQ_MAX_GRID_BLOCKS 1024
-#endif
-constexpr uint32_t kMaxGridBlocks = TFQ_MAX_GRID_BLOCKS;
 constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident in LDS
 #ifndef TFQ_ROWS_IN_FLIGHT
 #define TFQ_ROWS_IN_FLIGHT 1
@@ -23,10 +19,18 @@ constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident i
 constexpr uint32_t kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
 constexpr uint32_t kGemmBlock = 512;       // threads of the MFMA GEMM tile (gemm.hpp kGemmThreads)   // rows per segment per group (tfq_kernels.hip)
 
-inline uint32_t grid_for_rows(uint64_t rows, uint32_t rows_per_block) {
+// Grid of a row-loop kernel (blocks of kBlock threads, `lds` dynamic LDS
+// bytes): one block per rows_per_block rows, but no more blocks than the GPU
+// holds resident at once; the blocks then loop over the rows. A grid beyond
+// that adds a partial second round of blocks, each re-staging x, and leaves
+// most CUs idle while it drains.
+inline uint32_t grid_for_rows(const Module& m, hipFunction_t f, uint32_t lds, uint64_t rows,
+                              uint32_t rows_per_block) {
     uint64_t g = (rows + rows_per_block - 1) / rows_per_block;
     if (g < 1) g = 1;
-    return (uint32_t)(g > kMaxGridBlocks ? kMaxGridBlocks : g);
+    if (!f) return (uint32_t)(g < 1024 ? g : 1024);     // launch() reports the missing kernel
+    const uint32_t cap = m.resident_blocks(f, kBlock, lds);
+    return (uint32_t)(g > cap ? cap : g);
 }
 
 // Validates how a kernel stages its activation vector (NormArg, abi_types.h).
@@ -107,8 +111,10 @@ private:
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         uint32_t nn = n;
         void* args[] = {&mats, &x, &nn};
-        return launch(m_.get(name), grid_for_rows(mats.total_rows, rows_per_block), kBlock, n * 2,
-                      stream, args, name);
+        hipFunction_t fn = m_.get(name);
+        const uint32_t lds = xpairs_lds_bytes(n);
+        return launch(fn, grid_for_rows(m_, fn, lds, mats.total_rows, rows_per_block), kBlock, lds, stream,
+                      args, name);
     }
 
     const Module& m_;
@@ -135,7 +141,8 @@ public:
         std::snprintf(name, sizeof(name), "tfq_q8_gemv_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&weights, &scales, &biases, &x, &y, &m, &n};
-        return launch(m_.get(name), grid_for_rows(m, rows_per_block), kBlock, n * 6, stream, args,
+        hipFunction_t fn = m_.get(name);
+        return launch(fn, grid_for_rows(m_, fn, n * 6, m, rows_per_block), kBlock, n * 6, stream, args,
                       name);
     }
 
@@ -219,8 +226,10 @@ public:
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         NormArg na = stage;
         void* args[] = {&kp, &indices, &active_slots, &active_count, &top_k, &x, &acts, &d, &f, &na};
-        return launch(m_.get(name), grid_for_rows((uint64_t)active_count * f, rows_per_block),
-                      kBlock, d * 2, stream, args, name);
+        hipFunction_t fn = m_.get(name);
+        const uint32_t lds = xpairs_lds_bytes(d);
+        return launch(fn, grid_for_rows(m_, fn, lds, (uint64_t)active_count * f, rows_per_block), kBlock,
+                      lds, stream, args, name);
     }
 
     // Phase 1 that also performs the router's selection from `logits`
@@ -249,7 +258,9 @@ public:
         NormArg na = stage;
         void* args[] = {&kp,   &logits, &per_expert_scale, &num_experts, &top_k, &out_indices, &out_weights,
                         &out_weights_f32, &x, &acts, &d, &f, &na};
-        return launch(m_.get(name), grid_for_rows((uint64_t)top_k * f, rows_per_block), kBlock, d * 2,
+        hipFunction_t fn = m_.get(name);
+        const uint32_t lds = xpairs_lds_bytes(d);
+        return launch(fn, grid_for_rows(m_, fn, lds, (uint64_t)top_k * f, rows_per_block), kBlock, lds,
                       stream, args, name);
     }
 
@@ -267,8 +278,10 @@ public:
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_moe_phase2_p%u", p);
         void* args[] = {&kp, &indices, &acts, &routing_weights, &residual, &y, &d, &f, &top_k};
-        return launch(m_.get(name), grid_for_rows(d, (kBlock / 64) * kRowsInFlight), kBlock,
-                      top_k * f * 2, stream, args, name);
+        hipFunction_t fn = m_.get(name);
+        const uint32_t lds = xpairs_lds_bytes(top_k * f);
+        return launch(fn, grid_for_rows(m_, fn, lds, d, (kBlock / 64) * kRowsInFlight), kBlock, lds, stream,
+                      args, name);
     }
 
 private:
@@ -332,8 +345,9 @@ public:
         std::snprintf(name, sizeof(name), "tfq_gate_up_act_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&g, &u, &x, &act_scratch, &d, &f, &na};
-        int rc = launch(m_.get(name), grid_for_rows(f, rows_per_block), kBlock, d * 2, stream, args,
-                        name);
+        hipFunction_t fn = m_.get(name);
+        const uint32_t lds = xpairs_lds_bytes(d);
+        int rc = launch(fn, grid_for_rows(m_, fn, lds, f, rows_per_block), kBlock, lds, stream, args, name);
         if (rc) return rc;
         return gemv_.encode(stream, down.weights, down.scales, down.biases, act_scratch, y, d, f);
     }

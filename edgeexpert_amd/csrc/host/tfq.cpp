@@ -60,6 +60,11 @@ static std::vector<std::string> kernel_names() {
 int Module::load(const char* path) {
     int rc = hip_check(hipGetDevice(&device_), "hipGetDevice");
     if (rc) return rc;
+    int cus = 0;
+    rc = hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_),
+                   "hipDeviceGetAttribute(multiProcessorCount)");
+    if (rc) return rc;
+    cus_ = cus > 0 ? (uint32_t)cus : 1u;
     rc = hip_check(hipModuleLoad(&module_, path), "hipModuleLoad");
     if (rc) {
         module_ = nullptr;
@@ -72,6 +77,20 @@ int Module::load(const char* path) {
         fns_[n] = f;
     }
     return TFQ_OK;
+}
+
+uint32_t Module::resident_blocks(hipFunction_t f, uint32_t block, uint32_t lds) const {
+    const auto key = std::make_pair(f, ((uint64_t)block << 32) | lds);
+    std::lock_guard<std::mutex> lock(occ_mu_);
+    auto it = occ_.find(key);
+    if (it != occ_.end()) return it->second;
+    int per_cu = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, (int)block, lds) != hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    const uint32_t total = (uint32_t)per_cu * cus_;
+    occ_.emplace(key, total);
+    return total;
 }
 
 Module::~Module() {

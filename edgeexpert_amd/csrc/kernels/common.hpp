@@ -103,6 +103,56 @@ __device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ lds_xh,
     xc.cb = 1024.0f * sb;
 }
 
+// The activations of the int4 dot as the dot consumes them, in LDS (so the
+// x values need no registers of their own across the row loop, which keeps
+// the GEMV kernels' register count, and with it their occupancy, in check).
+// Chunk c (32 values) is stored as 4 planes of 16 bytes, plane j holding the
+// pairs (v[8j+i], v[8j+i+4]) for i = 0..3 at byte 16·(j·nch + c): lanes that
+// read consecutive chunks read consecutive 16-byte slots. sums[3c..3c+2]
+// hold the chunk's XChunk sum, ca and cb.
+struct XPairs {
+    const uint4* planes;
+    const float* sums;
+    uint32_t nch;
+};
+
+// Builds the paired copy of the n staged halves at lds_xh into the LDS that
+// follows them (layout of xpairs_lds_bytes). Every thread of the block calls
+// it after staging; it ends with a barrier.
+__device__ __forceinline__ XPairs build_xpairs(uint16_t* lds_xh, uint32_t n) {
+    const uint32_t nch = n >> 5;
+    uint4* planes = reinterpret_cast<uint4*>(lds_xh + n);
+    float* sums = reinterpret_cast<float*>(planes + 4 * nch);
+    for (uint32_t c = threadIdx.x; c < nch; c += blockDim.x) {
+        XChunk xc;
+        load_xchunk(lds_xh, c, xc);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            planes[j * nch + c] = make_uint4(
+                __builtin_bit_cast(uint32_t, xc.p[4 * j + 0]), __builtin_bit_cast(uint32_t, xc.p[4 * j + 1]),
+                __builtin_bit_cast(uint32_t, xc.p[4 * j + 2]), __builtin_bit_cast(uint32_t, xc.p[4 * j + 3]));
+        sums[3 * c] = xc.sum;
+        sums[3 * c + 1] = xc.ca;
+        sums[3 * c + 2] = xc.cb;
+    }
+    __syncthreads();
+    return {planes, sums, nch};
+}
+
+__device__ __forceinline__ void read_xpairs(const XPairs& xp, uint32_t c, XChunk& xc) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint4 v = xp.planes[j * xp.nch + c];
+        xc.p[4 * j + 0] = __builtin_bit_cast(h2, v.x);
+        xc.p[4 * j + 1] = __builtin_bit_cast(h2, v.y);
+        xc.p[4 * j + 2] = __builtin_bit_cast(h2, v.z);
+        xc.p[4 * j + 3] = __builtin_bit_cast(h2, v.w);
+    }
+    xc.sum = xp.sums[3 * c];
+    xc.ca = xp.sums[3 * c + 1];
+    xc.cb = xp.sums[3 * c + 2];
+}
+
 // Σ_k q_k x_k over the 32 codes of a chunk (fp32 accumulate).
 __device__ __forceinline__ float dot_q4_chunk(const uint4 w, const XChunk& xc) {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};

@@ -51,11 +51,11 @@ __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, 
             res ? res + r : nullptr};
 }
 
-// int4 GEMV over 1..3 matrices with a shared x. Dynamic LDS: n halves.
+// int4 GEMV over 1..3 matrices with a shared x. Dynamic LDS: xpairs_lds_bytes(n).
 template <int SEG, int P, int R>
 __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_t* __restrict__ x,
                                               uint32_t n) {
-    extern __shared__ uint16_t lds_xh[];
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t nwaves = blockDim.x >> 6;
@@ -90,12 +90,7 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
     };
     issue(0);
     stage_act(x, lds_xh, n, mats.norm);
-    XChunk xc[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const uint32_t c = sl + p * SEG;
-        if (c < lpr) load_xchunk(lds_xh, c, xc[p]);
-    }
+    const XPairs xp = build_xpairs(lds_xh, n);
 
     for (uint32_t grp = 0; seg_id + grp * R * seg_total < total; ++grp) {
         float acc[R];
@@ -106,9 +101,11 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
             for (int p = 0; p < P; ++p) {
                 const uint32_t c = sl + p * SEG;
                 if (c < lpr) {
-                    const float d = dot_q4_chunk(wv[r][p], xc[p]);
+                    XChunk xc;
+                    read_xpairs(xp, c, xc);
+                    const float d = dot_q4_chunk(wv[r][p], xc);
                     acc[r] = fmaf(sv[r][p], d, acc[r]);
-                    acc[r] = fmaf(bv[r][p], xc[p].sum, acc[r]);
+                    acc[r] = fmaf(bv[r][p], xc.sum, acc[r]);
                 }
             }
         }
@@ -224,7 +221,7 @@ template <int SEG, int P, int R>
 __device__ __forceinline__ void q8_gemv(const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
                                         const uint16_t* __restrict__ B, const uint16_t* __restrict__ x,
                                         uint16_t* __restrict__ y, uint32_t M, uint32_t n) {
-    extern __shared__ float lds_x[];
+    extern __shared__ __attribute__((aligned(16))) float lds_x[];
     q8_rows<SEG, P, R>(
         W, S, B, lds_x, M, n,
         [&]() {
@@ -251,7 +248,7 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
                                               const uint16_t* __restrict__ eff,
                                               float* __restrict__ logits, uint32_t E, uint32_t d,
                                               NormArg norm = {nullptr, nullptr, nullptr, 0.0f, kStageCopy}) {
-    extern __shared__ float lds_x[];
+    extern __shared__ __attribute__((aligned(16))) float lds_x[];
     q8_rows<SEG, P, 1>(
         W, S, B, lds_x, E, d,
         [&]() {

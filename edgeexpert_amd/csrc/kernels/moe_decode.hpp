@@ -34,11 +34,10 @@ struct GateUpRow {
 
 // Streams gate/up row pairs of length D against x (fp16 in LDS):
 // `rowfn(row)` -> GateUpRow, `out(row, act)` for live rows (lane 0 of the segment).
-// X_STAGED: the caller has already staged x into the dynamic LDS.
-template <int SEG, int P, int R, bool X_STAGED = false, typename RowFn, typename OutFn>
+template <int SEG, int P, int R, typename RowFn, typename OutFn>
 __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uint32_t D, uint32_t total,
                                              const NormArg& norm, RowFn rowfn, OutFn out) {
-    extern __shared__ uint16_t lds_xh[];
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t nwaves = blockDim.x >> 6;
@@ -74,13 +73,8 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
         }
     };
     issue(0);
-    if (!X_STAGED) stage_act(x, lds_xh, D, norm);
-    XChunk xc[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const uint32_t c = sl + p * SEG;
-        if (c < lpr) load_xchunk(lds_xh, c, xc[p]);
-    }
+    stage_act(x, lds_xh, D, norm);
+    const XPairs xp = build_xpairs(lds_xh, D);
     for (uint32_t grp = 0; seg_id + grp * R * seg_total < total; ++grp) {
         float ga[R], ua[R];
 #pragma unroll
@@ -91,12 +85,14 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
             for (int p = 0; p < P; ++p) {
                 const uint32_t c = sl + p * SEG;
                 if (c < lpr) {
-                    const float gd = dot_q4_chunk(gv[r][p], xc[p]);
-                    const float ud = dot_q4_chunk(uv[r][p], xc[p]);
+                    XChunk xc;
+                    read_xpairs(xp, c, xc);
+                    const float gd = dot_q4_chunk(gv[r][p], xc);
+                    const float ud = dot_q4_chunk(uv[r][p], xc);
                     ga[r] = fmaf(gsv[r][p], gd, ga[r]);
-                    ga[r] = fmaf(gbv[r][p], xc[p].sum, ga[r]);
+                    ga[r] = fmaf(gbv[r][p], xc.sum, ga[r]);
                     ua[r] = fmaf(usv[r][p], ud, ua[r]);
-                    ua[r] = fmaf(ubv[r][p], xc[p].sum, ua[r]);
+                    ua[r] = fmaf(ubv[r][p], xc.sum, ua[r]);
                 }
             }
         }
@@ -115,7 +111,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
 }
 
 // Phase 1 over n_active slots (active_slots == nullptr: slots 0..n_active-1).
-template <int SEG, int P, int R, bool X_STAGED = false>
+template <int SEG, int P, int R>
 __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint32_t* __restrict__ active_slots, uint32_t n_active,
                                            uint32_t top_k, const uint16_t* __restrict__ x,
@@ -127,7 +123,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
         const uint32_t a = row / F;
         return active_slots ? active_slots[a] : a;
     };
-    gate_up_rows<SEG, P, R, X_STAGED>(
+    gate_up_rows<SEG, P, R>(
         x, D, n_active * F, norm,
         [&](uint32_t row) {
             const uint32_t slot = slot_of(row);
@@ -209,7 +205,8 @@ __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& u
 }
 
 // Phase 2: 8 slots × 8-lane segments per wave; P chunks of 32 per lane
-// (F <= 256*P); R output rows per wave in flight. Dynamic LDS: top_k*F halves.
+// (F <= 256*P); R output rows per wave in flight. Dynamic LDS:
+// xpairs_lds_bytes(top_k*F).
 template <int P, int R>
 __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint16_t* __restrict__ acts,
@@ -218,7 +215,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                                            uint16_t* __restrict__ y, uint32_t D, uint32_t F,
                                            uint32_t top_k) {
     constexpr int SEG = 8;
-    extern __shared__ uint16_t lds_a[];
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds_a[];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t nwaves = blockDim.x >> 6;
@@ -258,12 +255,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
     };
     issue(0);
     stage_xh(acts, lds_a, top_k * F);
-    XChunk xc[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const uint32_t c = sl + p * SEG;
-        if (live && c < lpr) load_xchunk(lds_a + (size_t)slot * F, c, xc[p]);
-    }
+    const XPairs xp = build_xpairs(lds_a, top_k * F);      // slot s owns chunks s·lpr ..
     const float w_slot = live ? h2f(rw[slot]) : 0.0f;
 
     for (uint32_t grp = 0; wave_id + grp * R * wave_total < D; ++grp) {
@@ -276,9 +268,11 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                 for (int p = 0; p < P; ++p) {
                     const uint32_t c = sl + p * SEG;
                     if (c < lpr) {
-                        const float dd = dot_q4_chunk(wv[r][p], xc[p]);
+                        XChunk xc;
+                        read_xpairs(xp, slot * lpr + c, xc);
+                        const float dd = dot_q4_chunk(wv[r][p], xc);
                         acc[r] = fmaf(sv[r][p], dd, acc[r]);
-                        acc[r] = fmaf(bv[r][p], xc[p].sum, acc[r]);
+                        acc[r] = fmaf(bv[r][p], xc.sum, acc[r]);
                     }
                 }
             } else if (live) {
