@@ -69,7 +69,7 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
     const uint32_t total = mats.total_rows;
 
     uint4 wv[R][P];
-    float sv[R][P], bv[R][P];
+    uint32_t sbv[R][P];      // fp16 scale (low half) and bias (high half)
     auto issue = [&](uint32_t grp) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -81,8 +81,7 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
                     const uint32_t c = sl + p * SEG;
                     if (c < lpr) {
                         wv[r][p] = ldg16(q.w + 16u * c);
-                        sv[r][p] = h2f(q.s[c >> 1]);
-                        bv[r][p] = h2f(q.b[c >> 1]);
+                        sbv[r][p] = (uint32_t)q.s[c >> 1] | ((uint32_t)q.b[c >> 1] << 16);
                     }
                 }
             }
@@ -104,8 +103,9 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
                     XChunk xc;
                     read_xpairs(xp, c, xc);
                     const float d = dot_q4_chunk(wv[r][p], xc);
-                    acc[r] = fmaf(sv[r][p], d, acc[r]);
-                    acc[r] = fmaf(bv[r][p], xc.sum, acc[r]);
+                    const h2 sb = __builtin_bit_cast(h2, sbv[r][p]);
+                    acc[r] = fmaf((float)sb[0], d, acc[r]);
+                    acc[r] = fmaf((float)sb[1], xc.sum, acc[r]);
                 }
             }
         }

@@ -48,7 +48,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
     const uint32_t seg_total = gridDim.x * nwaves * spw;
 
     uint4 gv[R][P], uv[R][P];
-    float gsv[R][P], gbv[R][P], usv[R][P], ubv[R][P];
+    uint32_t gsb[R][P], usb[R][P];      // fp16 scale (low half) and bias (high half)
     auto issue = [&](uint32_t grp) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -62,10 +62,8 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
                         if (c < lpr) {
                             gv[r][p] = ldg16(q.gw + 16u * c);
                             uv[r][p] = ldg16(q.uw + 16u * c);
-                            gsv[r][p] = h2f(q.gs[c >> 1]);
-                            gbv[r][p] = h2f(q.gb[c >> 1]);
-                            usv[r][p] = h2f(q.us[c >> 1]);
-                            ubv[r][p] = h2f(q.ub[c >> 1]);
+                            gsb[r][p] = (uint32_t)q.gs[c >> 1] | ((uint32_t)q.gb[c >> 1] << 16);
+                            usb[r][p] = (uint32_t)q.us[c >> 1] | ((uint32_t)q.ub[c >> 1] << 16);
                         }
                     }
                 }
@@ -89,10 +87,12 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
                     read_xpairs(xp, c, xc);
                     const float gd = dot_q4_chunk(gv[r][p], xc);
                     const float ud = dot_q4_chunk(uv[r][p], xc);
-                    ga[r] = fmaf(gsv[r][p], gd, ga[r]);
-                    ga[r] = fmaf(gbv[r][p], xc.sum, ga[r]);
-                    ua[r] = fmaf(usv[r][p], ud, ua[r]);
-                    ua[r] = fmaf(ubv[r][p], xc.sum, ua[r]);
+                    const h2 g2 = __builtin_bit_cast(h2, gsb[r][p]);
+                    const h2 u2 = __builtin_bit_cast(h2, usb[r][p]);
+                    ga[r] = fmaf((float)g2[0], gd, ga[r]);
+                    ga[r] = fmaf((float)g2[1], xc.sum, ga[r]);
+                    ua[r] = fmaf((float)u2[0], ud, ua[r]);
+                    ua[r] = fmaf((float)u2[1], xc.sum, ua[r]);
                 }
             }
         }
@@ -235,7 +235,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
     const uint32_t wave_total = gridDim.x * nwaves;
 
     uint4 wv[R][P];
-    float sv[R][P], bv[R][P];
+    uint32_t sbv[R][P];      // fp16 scale (low half) and bias (high half)
     auto issue = [&](uint32_t grp) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -246,8 +246,8 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                     const uint32_t c = sl + p * SEG;
                     if (c < lpr) {
                         wv[r][p] = ldg16(dw + (size_t)d * row_bytes + 16u * c);
-                        sv[r][p] = h2f(ds[(size_t)d * ngroups + (c >> 1)]);
-                        bv[r][p] = h2f(db[(size_t)d * ngroups + (c >> 1)]);
+                        sbv[r][p] = (uint32_t)ds[(size_t)d * ngroups + (c >> 1)] |
+                                    ((uint32_t)db[(size_t)d * ngroups + (c >> 1)] << 16);
                     }
                 }
             }
@@ -271,8 +271,9 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                         XChunk xc;
                         read_xpairs(xp, slot * lpr + c, xc);
                         const float dd = dot_q4_chunk(wv[r][p], xc);
-                        acc[r] = fmaf(sv[r][p], dd, acc[r]);
-                        acc[r] = fmaf(bv[r][p], xc.sum, acc[r]);
+                        const h2 sb = __builtin_bit_cast(h2, sbv[r][p]);
+                        acc[r] = fmaf((float)sb[0], dd, acc[r]);
+                        acc[r] = fmaf((float)sb[1], xc.sum, acc[r]);
                     }
                 }
             } else if (live) {
