@@ -40,9 +40,9 @@ struct NormArg {
 
 // Dynamic LDS of the int4 GEMV-family kernels for an activation vector of n
 // halves (n a multiple of 32): the staged fp16 vector (2n bytes), its paired
-// copy in the order the int4 dot consumes it (2n bytes) and three fp32 sums
-// per 32-element chunk (12 bytes each).
-constexpr uint32_t xpairs_lds_bytes(uint32_t n) { return 4u * n + 12u * (n >> 5); }
+// copy in the order the int4 dot consumes it (2n bytes) and four fp32 words
+// of sums per 32-element chunk (16 bytes each).
+constexpr uint32_t xpairs_lds_bytes(uint32_t n) { return 4u * n + 16u * (n >> 5); }
 
 // Gemma 4 q/k/v epilogue applied inside the decode attention kernel
 // (fused_qkv_epilogue, S/Metal/Fusions/fused.metal:86-180): per-head RMSNorm

@@ -26,6 +26,7 @@ namespace tfq {
 
 constexpr uint32_t kAttnChunk = 64;
 constexpr uint32_t kAttnThreads = 256;
+constexpr uint32_t kLayerTailThreads = 1024;     // threads of the one-block layer tail
 constexpr uint32_t kAttnKeyLanes = 16;
 
 // NeoX rotation of pair i at `pos`: angle = pos · theta^(-2i/HD)
@@ -33,7 +34,7 @@ constexpr uint32_t kAttnKeyLanes = 16;
 // formed in fp64 so that it carries no fp32 error at long positions.
 __device__ __forceinline__ void rope_table(float* __restrict__ c, float* __restrict__ s, uint32_t pairs,
                                            uint32_t hd, uint32_t pos, float theta) {
-    for (uint32_t i = threadIdx.x; i < pairs; i += blockDim.x) {
+    for (uint32_t i = threadIdx.x; i < pairs; i += kAttnThreads) {
         const double ang = (double)pos * pow((double)theta, -2.0 * (double)i / (double)hd);
         c[i] = (float)cos(ang);
         s[i] = (float)sin(ang);
@@ -297,7 +298,7 @@ __device__ __forceinline__ void attn_combine(const float* __restrict__ part_o, c
 // (fused_post_attn_setup / rmsnorm / fused_layer_tail,
 // S/Metal/Fusions/fused.metal:199-231,270-375). Each thread owns one 16-byte
 // chunk of every vector and loads all eight at once; requires D % 8 == 0,
-// D <= 8·blockDim and 16-byte aligned vectors (the host checks).
+// D <= 8·kLayerTailThreads and 16-byte aligned vectors (the host checks).
 __device__ __forceinline__ void layer_tail(const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ attn,
                                            const uint16_t* __restrict__ w_post_attn,
                                            const uint16_t* __restrict__ h1, const uint16_t* __restrict__ w_sp,
@@ -325,7 +326,7 @@ __device__ __forceinline__ void layer_tail(const uint16_t* __restrict__ hidden, 
         ss[1] = fmaf((float)h1v[e], (float)h1v[e], ss[1]);
         ss[2] = fmaf((float)h2v[e], (float)h2v[e], ss[2]);
     }
-    block_sums<3>(ss);
+    block_sums<3, kLayerTailThreads>(ss);
     const float inv_a = 1.0f / sqrtf(ss[0] / n + eps);
     const float inv_1 = 1.0f / sqrtf(ss[1] / n + eps);
     const float inv_2 = 1.0f / sqrtf(ss[2] / n + eps);
@@ -341,7 +342,7 @@ __device__ __forceinline__ void layer_tail(const uint16_t* __restrict__ hidden, 
         s12[0] = fmaf((float)h12[e], (float)h12[e], s12[0]);
     }
     if (!live) s12[0] = 0.0f;
-    block_sums<1>(s12);
+    block_sums<1, kLayerTailThreads>(s12);
     const float inv_12 = 1.0f / sqrtf(s12[0] / n + eps);
     const float sc = (float)(_Float16)layer_scalar;
     h8 o;

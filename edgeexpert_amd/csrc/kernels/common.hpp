@@ -3,6 +3,11 @@
 // Wave64 throughout: a "segment" is a power-of-two group of SEG lanes inside
 // one wavefront that cooperates on one output row; several segments share a
 // wave when a row needs fewer than 64 lanes.
+//
+// Block sizes are compile-time constants (template parameter NT, default
+// kThreads): reading blockDim.x costs a load from the dispatch's implicit
+// arguments, and the wait for it would sit in front of every kernel's first
+// weight load.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -12,11 +17,13 @@
 
 namespace tfq {
 
-constexpr int kGroup = 64;       // affine group size along the reduction axis
-constexpr int kWave = 64;        // CDNA wavefront width
+constexpr int kGroup = 64;        // affine group size along the reduction axis
+constexpr int kWave = 64;         // CDNA wavefront width
+constexpr uint32_t kThreads = 256;     // threads per block of every GEMV-family kernel
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
@@ -55,6 +62,13 @@ __device__ __forceinline__ uint4 ldg16(const uint8_t* p) {
     return *reinterpret_cast<const uint4*>(p);
 }
 
+// 128-bit load of weights that are read once per token: non-temporal, so the
+// stream does not evict the activations and small vectors the caches hold.
+__device__ __forceinline__ uint4 ldg16_stream(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // ------------------------------------------------------------ int4 chunk ----
 //
 // A chunk is 16 bytes of a weight row: 32 int4 codes, four 32-bit words, code
@@ -74,66 +88,76 @@ __device__ __forceinline__ uint4 ldg16(const uint8_t* p) {
 
 struct XChunk {
     h2 p[16];
-    float sum;      // Σ of the 32 activations in element order (fp32)
+    float sum;      // Σ of the 32 activations (fp32)
     float ca;       // 1024 · Σ of the activations at positions 8j+{0,2,4,6}
     float cb;       // 1024 · Σ of the activations at positions 8j+{1,3,5,7}
 };
-
-// Builds the pair layout of chunk c from an fp16 vector in LDS.
-__device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ lds_xh, uint32_t c,
-                                            XChunk& xc) {
-    const h8* src = reinterpret_cast<const h8*>(lds_xh + 32u * c);
-    float s = 0.0f, sa = 0.0f, sb = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const h8 v = src[j];
-        xc.p[4 * j + 0] = __builtin_shufflevector(v, v, 0, 4);
-        xc.p[4 * j + 1] = __builtin_shufflevector(v, v, 1, 5);
-        xc.p[4 * j + 2] = __builtin_shufflevector(v, v, 2, 6);
-        xc.p[4 * j + 3] = __builtin_shufflevector(v, v, 3, 7);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            s += (float)v[e];
-            if (e & 1) sb += (float)v[e];
-            else sa += (float)v[e];
-        }
-    }
-    xc.sum = s;
-    xc.ca = 1024.0f * sa;
-    xc.cb = 1024.0f * sb;
-}
 
 // The activations of the int4 dot as the dot consumes them, in LDS (so the
 // x values need no registers of their own across the row loop, which keeps
 // the GEMV kernels' register count, and with it their occupancy, in check).
 // Chunk c (32 values) is stored as 4 planes of 16 bytes, plane j holding the
 // pairs (v[8j+i], v[8j+i+4]) for i = 0..3 at byte 16·(j·nch + c): lanes that
-// read consecutive chunks read consecutive 16-byte slots. sums[3c..3c+2]
-// hold the chunk's XChunk sum, ca and cb.
+// read consecutive chunks read consecutive 16-byte slots. sums[c] holds the
+// chunk's (sum, ca, cb, 0).
 struct XPairs {
     const uint4* planes;
-    const float* sums;
+    const float4* sums;
     uint32_t nch;
 };
 
-// Builds the paired copy of the n staged halves at lds_xh into the LDS that
-// follows them (layout of xpairs_lds_bytes). Every thread of the block calls
-// it after staging; it ends with a barrier.
-__device__ __forceinline__ XPairs build_xpairs(uint16_t* lds_xh, uint32_t n) {
-    const uint32_t nch = n >> 5;
-    uint4* planes = reinterpret_cast<uint4*>(lds_xh + n);
-    float* sums = reinterpret_cast<float*>(planes + 4 * nch);
-    for (uint32_t c = threadIdx.x; c < nch; c += blockDim.x) {
-        XChunk xc;
-        load_xchunk(lds_xh, c, xc);
+// The per-16-byte part of a chunk's sums: Σ of the 8 values and of the 4 at
+// even / odd positions, in element order.
+__device__ __forceinline__ void h8_sums(const h8 v, float& s, float& sa, float& sb) {
+    s = 0.0f;
+    sa = 0.0f;
+    sb = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            planes[j * nch + c] = make_uint4(
-                __builtin_bit_cast(uint32_t, xc.p[4 * j + 0]), __builtin_bit_cast(uint32_t, xc.p[4 * j + 1]),
-                __builtin_bit_cast(uint32_t, xc.p[4 * j + 2]), __builtin_bit_cast(uint32_t, xc.p[4 * j + 3]));
-        sums[3 * c] = xc.sum;
-        sums[3 * c + 1] = xc.ca;
-        sums[3 * c + 2] = xc.cb;
+    for (int e = 0; e < 8; ++e) {
+        s += (float)v[e];
+        if (e & 1) sb += (float)v[e];
+        else sa += (float)v[e];
+    }
+}
+
+__device__ __forceinline__ uint4 h8_pairs(const h8 v) {
+    return make_uint4(__builtin_bit_cast(uint32_t, __builtin_shufflevector(v, v, 0, 4)),
+                      __builtin_bit_cast(uint32_t, __builtin_shufflevector(v, v, 1, 5)),
+                      __builtin_bit_cast(uint32_t, __builtin_shufflevector(v, v, 2, 6)),
+                      __builtin_bit_cast(uint32_t, __builtin_shufflevector(v, v, 3, 7)));
+}
+
+// The chunk sums of 16-byte piece q (= 4c + j) combine over the four pieces of
+// chunk c as (p0 + p1) + (p2 + p3).
+__device__ __forceinline__ float4 chunk_sums(const float s, const float sa, const float sb) {
+    float t = s + __shfl_xor(s, 1, kWave);
+    float ta = sa + __shfl_xor(sa, 1, kWave);
+    float tb = sb + __shfl_xor(sb, 1, kWave);
+    t += __shfl_xor(t, 2, kWave);
+    ta += __shfl_xor(ta, 2, kWave);
+    tb += __shfl_xor(tb, 2, kWave);
+    return make_float4(t, 1024.0f * ta, 1024.0f * tb, 0.0f);
+}
+
+// Builds the paired copy of the n staged halves at lds_xh into the LDS that
+// follows them (layout of xpairs_lds_bytes): one 16-byte piece per thread and
+// step, the four pieces of a chunk in four consecutive lanes. Every thread of
+// the block calls it after staging; it ends with a barrier.
+template <uint32_t NT = kThreads>
+__device__ __forceinline__ XPairs build_xpairs(uint16_t* lds_xh, uint32_t n) {
+    const uint32_t nch = n >> 5, npc = n >> 3;
+    uint4* planes = reinterpret_cast<uint4*>(lds_xh + n);
+    float4* sums = reinterpret_cast<float4*>(planes + 4 * nch);
+    for (uint32_t base = 0; base < npc; base += NT) {
+        const uint32_t q = base + threadIdx.x;      // npc is a multiple of 8: a chunk's pieces are all live or all not
+        const h8 v = q < npc ? reinterpret_cast<const h8*>(lds_xh)[q] : h8{};
+        float s, sa, sb;
+        h8_sums(v, s, sa, sb);
+        const float4 cs = chunk_sums(s, sa, sb);
+        if (q < npc) {
+            planes[(q & 3u) * nch + (q >> 2)] = h8_pairs(v);
+            if ((q & 3u) == 0) sums[q >> 2] = cs;
+        }
     }
     __syncthreads();
     return {planes, sums, nch};
@@ -148,9 +172,10 @@ __device__ __forceinline__ void read_xpairs(const XPairs& xp, uint32_t c, XChunk
         xc.p[4 * j + 2] = __builtin_bit_cast(h2, v.z);
         xc.p[4 * j + 3] = __builtin_bit_cast(h2, v.w);
     }
-    xc.sum = xp.sums[3 * c];
-    xc.ca = xp.sums[3 * c + 1];
-    xc.cb = xp.sums[3 * c + 2];
+    const float4 s = xp.sums[c];
+    xc.sum = s.x;
+    xc.ca = s.y;
+    xc.cb = s.z;
 }
 
 // Σ_k q_k x_k over the 32 codes of a chunk (fp32 accumulate).
@@ -186,23 +211,25 @@ __device__ __forceinline__ float dot16_q8(const uint4 w, const float* x) {
 
 // Sum of v over the block (every thread receives it); wave sums first, then
 // the per-wave totals in wave order (deterministic).
+template <uint32_t NT = kThreads>
 __device__ __forceinline__ float block_sum(float v) {
     __shared__ float part[16];
     v = seg_sum<kWave>(v);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     __syncthreads();
     if (lane == 0) part[wave] = v;
     __syncthreads();
     float t = 0.0f;
-    for (uint32_t i = 0; i < nwaves; ++i) t += part[i];
+#pragma unroll
+    for (uint32_t i = 0; i < NT / 64; ++i) t += part[i];
     return t;
 }
 
 // N independent block sums at once (one pair of barriers for all of them).
-template <int N>
+template <int N, uint32_t NT = kThreads>
 __device__ __forceinline__ void block_sums(float (&v)[N]) {
     __shared__ float partn[16][N];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int k = 0; k < N; ++k) v[k] = seg_sum<kWave>(v[k]);
     __syncthreads();
@@ -213,37 +240,40 @@ __device__ __forceinline__ void block_sums(float (&v)[N]) {
 #pragma unroll
     for (int k = 0; k < N; ++k) {
         float t = 0.0f;
-        for (uint32_t i = 0; i < nwaves; ++i) t += partn[i][k];
+#pragma unroll
+        for (uint32_t i = 0; i < NT / 64; ++i) t += partn[i][k];
         v[k] = t;
     }
 }
 
 // 1/sqrt(mean(x^2) + eps) of an fp16 vector held in LDS
 // (V/Reference/Primitives/RmsNorm.swift:18-22 in the reference checkout).
+template <uint32_t NT = kThreads>
 __device__ __forceinline__ float lds_inv_rms(const uint16_t* __restrict__ lds, uint32_t n, float eps) {
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+    for (uint32_t i = threadIdx.x; i < n; i += NT) {
         const float v = h2f(lds[i]);
         ss = fmaf(v, v, ss);
     }
-    const float total = block_sum(ss);
+    const float total = block_sum<NT>(ss);
     return 1.0f / sqrtf(total / (float)n + eps);
 }
 
 // Copies n fp16 values to LDS (16-byte transfers when x is 16-byte aligned;
 // each thread issues up to four loads before its first store, so a copy of
-// up to 4·8·blockDim values costs one memory latency). The loads use clamped
+// up to 4·8·NT values costs one memory latency). The loads use clamped
 // (always valid) chunk indices and plain scalars, so the compiler keeps them
 // in registers and in flight together.
+template <uint32_t NT = kThreads>
 __device__ __forceinline__ void copy_to_lds(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
                                             uint32_t n) {
     if ((((uintptr_t)x) & 15u) == 0 && (n & 7u) == 0) {
         const uint4* src = reinterpret_cast<const uint4*>(x);
         uint4* dst = reinterpret_cast<uint4*>(lds);
-        const uint32_t nch = n >> 3, bd = blockDim.x;
+        const uint32_t nch = n >> 3;
         if (nch == 0) return;
-        for (uint32_t base = threadIdx.x; base < nch; base += 4 * bd) {
-            const uint32_t c1 = base + bd, c2 = base + 2 * bd, c3 = base + 3 * bd;
+        for (uint32_t base = threadIdx.x; base < nch; base += 4 * NT) {
+            const uint32_t c1 = base + NT, c2 = base + 2 * NT, c3 = base + 3 * NT;
             const uint4 v0 = src[base];
             const uint4 v1 = src[c1 < nch ? c1 : base];
             const uint4 v2 = src[c2 < nch ? c2 : base];
@@ -254,123 +284,191 @@ __device__ __forceinline__ void copy_to_lds(const uint16_t* __restrict__ x, uint
             if (c3 < nch) dst[c3] = v3;
         }
     } else {
-        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lds[i] = x[i];
+        for (uint32_t i = threadIdx.x; i < n; i += NT) lds[i] = x[i];
     }
 }
 
 // lds[i] <- fp16(lds[i] * w[i] * r(lds)) in place (w == null: no scale);
 // RmsNorm.swift:14-43 forms the product x·w first, then applies the scale.
+template <uint32_t NT = kThreads>
 __device__ __forceinline__ void rmsnorm_lds(uint16_t* __restrict__ lds, uint32_t n,
                                             const uint16_t* __restrict__ w, float eps) {
-    const float inv = lds_inv_rms(lds, n, eps);
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const float inv = lds_inv_rms<NT>(lds, n, eps);
+    for (uint32_t i = threadIdx.x; i < n; i += NT) {
         const float xw = w ? h2f(lds[i]) * h2f(w[i]) : h2f(lds[i]);
         lds[i] = f2h(xw * inv);
     }
     __syncthreads();
 }
 
-// Scalar form of stage_act (any alignment, any n).
+// Scalar form of the staging (any alignment, any n): the fp16 activation
+// vector as NormArg describes, into lds[0..n).
+template <uint32_t NT = kThreads>
 __device__ __forceinline__ void stage_act_scalar(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
                                                  uint32_t n, const NormArg& na) {
-    copy_to_lds(x, lds, n);
+    copy_to_lds<NT>(x, lds, n);
     __syncthreads();
     if (na.mode == kStagePostAttn || na.mode == kStageResidual) {
         float ss = 0.0f;
-        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
             const float v = h2f(na.attn[i]);
             ss = fmaf(v, v, ss);
         }
-        const float inv = 1.0f / sqrtf(block_sum(ss) / (float)n + na.eps);
-        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float inv = 1.0f / sqrtf(block_sum<NT>(ss) / (float)n + na.eps);
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
             const uint16_t an = f2h(h2f(na.attn[i]) * h2f(na.attn_w[i]) * inv);
             lds[i] = f2h(h2f(lds[i]) + h2f(an));
         }
         __syncthreads();
     }
-    if (na.mode == kStageNorm || na.mode == kStagePostAttn) rmsnorm_lds(lds, n, na.w, na.eps);
+    if (na.mode == kStageNorm || na.mode == kStagePostAttn) rmsnorm_lds<NT>(lds, n, na.w, na.eps);
 }
-
-constexpr uint32_t kStageChunks = 2;     // 16-byte chunks per thread on the vector path
 
 __device__ __forceinline__ uint4 ld16h(const uint16_t* p, uint32_t chunk) {
     return reinterpret_cast<const uint4*>(p)[chunk];
 }
 
-// Stages the activation vector of a kernel into LDS as NormArg describes
-// (attention-output norm and residual add: fused_post_attn_setup,
-// S/Metal/Fusions/fused.metal:199-231). Vector path: every thread issues the
-// 16-byte loads of all its chunks of every input at once, then reduces from
-// registers, so the staging costs one memory latency instead of one per
-// element. Synchronises the block.
+// Staging of a kernel's activation vector in two steps, so that the loads of
+// x (and of the norm inputs) are in flight together with the weight loads
+// the kernel issues between the two:
+//   load()   issues the 16-byte loads of every input chunk the thread owns
+//            (chunks t, t + NT, …, CH per thread; vector path only);
+//   pairs()  forms the vector as NormArg says (attention-output norm and
+//            residual add, fused_post_attn_setup, S/Metal/Fusions/
+//            fused.metal:199-231; RMSNorm) in registers and writes it to
+//            LDS directly in the paired layout the int4 dot reads
+//            (XPairs), plus the plain fp16 copy when `plain` is set;
+//   plain()  the same, writing only the plain fp16 copy.
+// Both end with a block barrier. Inputs that are not 16-byte aligned, or
+// longer than 8·CH·NT halves, take the scalar path instead (two passes).
+// NORM == false compiles the copy-only form (NormArg ignored).
+template <uint32_t NT, uint32_t CH, bool NORM = true>
+struct XStage {
+    h8 xv[CH], av[CH], awv[CH], wv[CH];
+    bool vec;
+
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ x, uint32_t n, const NormArg& na) {
+        const uint32_t nch = n >> 3;
+        const uintptr_t align = (uintptr_t)x | (uintptr_t)na.w | (uintptr_t)na.attn | (uintptr_t)na.attn_w;
+        vec = ((NORM ? align : (uintptr_t)x) & 15u) == 0 && (n & 7u) == 0 && nch != 0 && nch <= CH * NT;
+        if (!vec) return;
+        const bool post = NORM && (na.mode == kStagePostAttn || na.mode == kStageResidual);
+        const bool norm = NORM && (na.mode == kStageNorm || na.mode == kStagePostAttn);
+        // clamped chunk indices: every load is valid and unconditional (chunks
+        // past the end are loaded twice and never stored or counted)
+#pragma unroll
+        for (uint32_t i = 0; i < CH; ++i) {
+            const uint32_t c0 = threadIdx.x + i * NT;
+            const uint32_t c = c0 < nch ? c0 : nch - 1;
+            xv[i] = __builtin_bit_cast(h8, ld16h(x, c));
+            if (post) {
+                av[i] = __builtin_bit_cast(h8, ld16h(na.attn, c));
+                awv[i] = __builtin_bit_cast(h8, ld16h(na.attn_w, c));
+            }
+            if (norm && na.w) wv[i] = __builtin_bit_cast(h8, ld16h(na.w, c));
+        }
+    }
+
+    // Applies the NormArg transform to the loaded chunks (vector path).
+    __device__ __forceinline__ void transform(uint32_t n, const NormArg& na) {
+        if (!NORM) return;
+        const uint32_t nch = n >> 3;
+        const bool post = na.mode == kStagePostAttn || na.mode == kStageResidual;
+        const bool norm = na.mode == kStageNorm || na.mode == kStagePostAttn;
+        if (post) {
+            float ss = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i)
+                if (threadIdx.x + i * NT < nch)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ss = fmaf((float)av[i][e], (float)av[i][e], ss);
+            const float inv = 1.0f / sqrtf(block_sum<NT>(ss) / (float)n + na.eps);
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const _Float16 an = (_Float16)((float)av[i][e] * (float)awv[i][e] * inv);
+                    xv[i][e] = (_Float16)((float)xv[i][e] + (float)an);
+                }
+        }
+        if (norm) {
+            float ss = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i)
+                if (threadIdx.x + i * NT < nch)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ss = fmaf((float)xv[i][e], (float)xv[i][e], ss);
+            const float inv = 1.0f / sqrtf(block_sum<NT>(ss) / (float)n + na.eps);
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float xw = na.w ? (float)xv[i][e] * (float)wv[i][e] : (float)xv[i][e];
+                    xv[i][e] = (_Float16)(xw * inv);
+                }
+        }
+    }
+
+    // LDS layout: xpairs_lds_bytes(n) at lds (plain copy, planes, sums).
+    __device__ __forceinline__ XPairs pairs(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
+                                            uint32_t n, const NormArg& na, bool plain = false) {
+        if (!vec) {
+            stage_act_scalar<NT>(x, lds, n, NORM ? na : NormArg{nullptr, nullptr, nullptr, 0.0f, kStageCopy});
+            return build_xpairs<NT>(lds, n);
+        }
+        transform(n, na);
+        const uint32_t npc = n >> 3, nch = n >> 5;
+        uint4* planes = reinterpret_cast<uint4*>(lds + n);
+        float4* sums = reinterpret_cast<float4*>(planes + 4 * nch);
+#pragma unroll
+        for (uint32_t i = 0; i < CH; ++i) {
+            const uint32_t q = threadIdx.x + i * NT;     // npc is a multiple of 8: all four pieces of a chunk agree
+            const h8 v = q < npc ? xv[i] : h8{};
+            float s, sa, sb;
+            h8_sums(v, s, sa, sb);
+            const float4 cs = chunk_sums(s, sa, sb);
+            if (q < npc) {
+                planes[(q & 3u) * nch + (q >> 2)] = h8_pairs(v);
+                if ((q & 3u) == 0) sums[q >> 2] = cs;
+                if (plain) reinterpret_cast<h8*>(lds)[q] = v;
+            }
+        }
+        __syncthreads();
+        return {planes, sums, nch};
+    }
+
+    __device__ __forceinline__ void plain(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds, uint32_t n,
+                                          const NormArg& na) {
+        if (!vec) {
+            stage_act_scalar<NT>(x, lds, n, NORM ? na : NormArg{nullptr, nullptr, nullptr, 0.0f, kStageCopy});
+            return;
+        }
+        transform(n, na);
+#pragma unroll
+        for (uint32_t i = 0; i < CH; ++i) {
+            const uint32_t q = threadIdx.x + i * NT;
+            if (q < (n >> 3)) reinterpret_cast<h8*>(lds)[q] = xv[i];
+        }
+        __syncthreads();
+    }
+};
+
+constexpr uint32_t kStageChunks = 2;     // 16-byte chunks per thread of the GEMV-family staging (n <= 4096)
+
+// One-call staging of the fp16 vector (no pairs): lds[0..n).
+template <uint32_t NT = kThreads>
 __device__ __forceinline__ void stage_act(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
                                           uint32_t n, const NormArg& na) {
-    const uint32_t nch = n >> 3;
-    const uintptr_t align = (uintptr_t)x | (uintptr_t)na.w | (uintptr_t)na.attn | (uintptr_t)na.attn_w;
-    if ((align & 15u) != 0 || (n & 7u) != 0 || nch == 0 || nch > kStageChunks * blockDim.x) {
-        stage_act_scalar(x, lds, n, na);
-        return;
-    }
-    const bool post = na.mode == kStagePostAttn || na.mode == kStageResidual;
-    const bool norm = na.mode == kStageNorm || na.mode == kStagePostAttn;
-    // clamped chunk indices: every load is valid and unconditional (chunks
-    // past the end are loaded twice and never stored or counted)
-    h8 xv[kStageChunks], av[kStageChunks] = {}, awv[kStageChunks] = {}, wv[kStageChunks] = {};
-#pragma unroll
-    for (uint32_t i = 0; i < kStageChunks; ++i) {
-        const uint32_t c0 = threadIdx.x + i * blockDim.x;
-        const uint32_t c = c0 < nch ? c0 : nch - 1;
-        xv[i] = __builtin_bit_cast(h8, ld16h(x, c));
-        if (post) {
-            av[i] = __builtin_bit_cast(h8, ld16h(na.attn, c));
-            awv[i] = __builtin_bit_cast(h8, ld16h(na.attn_w, c));
-        }
-        if (norm && na.w) wv[i] = __builtin_bit_cast(h8, ld16h(na.w, c));
-    }
-    if (post) {
-        float ss = 0.0f;
-#pragma unroll
-        for (uint32_t i = 0; i < kStageChunks; ++i)
-            if (threadIdx.x + i * blockDim.x < nch)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ss = fmaf((float)av[i][e], (float)av[i][e], ss);
-        const float inv = 1.0f / sqrtf(block_sum(ss) / (float)n + na.eps);
-#pragma unroll
-        for (uint32_t i = 0; i < kStageChunks; ++i)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const _Float16 an = (_Float16)((float)av[i][e] * (float)awv[i][e] * inv);
-                xv[i][e] = (_Float16)((float)xv[i][e] + (float)an);
-            }
-    }
-    if (norm) {
-        float ss = 0.0f;
-#pragma unroll
-        for (uint32_t i = 0; i < kStageChunks; ++i)
-            if (threadIdx.x + i * blockDim.x < nch)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ss = fmaf((float)xv[i][e], (float)xv[i][e], ss);
-        const float inv = 1.0f / sqrtf(block_sum(ss) / (float)n + na.eps);
-#pragma unroll
-        for (uint32_t i = 0; i < kStageChunks; ++i)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float xw = na.w ? (float)xv[i][e] * (float)wv[i][e] : (float)xv[i][e];
-                xv[i][e] = (_Float16)(xw * inv);
-            }
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < kStageChunks; ++i) {
-        const uint32_t c = threadIdx.x + i * blockDim.x;
-        if (c < nch) reinterpret_cast<h8*>(lds)[c] = xv[i];
-    }
-    __syncthreads();
+    XStage<NT, kStageChunks> st;
+    st.load(x, n, na);
+    st.plain(x, lds, n, na);
 }
 
 // Plain staging (no normalisation).
+template <uint32_t NT = kThreads>
 __device__ __forceinline__ void stage_xh(const uint16_t* __restrict__ x, uint16_t* __restrict__ lds,
                                          uint32_t n) {
-    copy_to_lds(x, lds, n);
+    copy_to_lds<NT>(x, lds, n);
     __syncthreads();
 }
 

@@ -52,13 +52,17 @@ __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, 
 }
 
 // int4 GEMV over 1..3 matrices with a shared x. Dynamic LDS: xpairs_lds_bytes(n).
+// Order of work: the x loads, then every weight / scale / bias load of the
+// first R rows (scale and bias kept raw, so nothing waits on them), then the
+// staging, which waits for x alone; the weights arrive meanwhile.
 template <int SEG, int P, int R>
 __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_t* __restrict__ x,
                                               uint32_t n) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
+    constexpr uint32_t NT = kThreads;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t nwaves = blockDim.x >> 6;
+    constexpr uint32_t nwaves = NT / 64;
     const uint32_t sl = lane & (SEG - 1);
     const uint32_t lpr = n >> 5;              // 16-byte chunks per row
     const uint32_t row_bytes = n >> 1;
@@ -69,7 +73,7 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
     const uint32_t total = mats.total_rows;
 
     uint4 wv[R][P];
-    uint32_t sbv[R][P];      // fp16 scale (low half) and bias (high half)
+    uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
     auto issue = [&](uint32_t grp) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -80,16 +84,18 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
                 for (int p = 0; p < P; ++p) {
                     const uint32_t c = sl + p * SEG;
                     if (c < lpr) {
-                        wv[r][p] = ldg16(q.w + 16u * c);
-                        sbv[r][p] = (uint32_t)q.s[c >> 1] | ((uint32_t)q.b[c >> 1] << 16);
+                        wv[r][p] = ldg16_stream(q.w + 16u * c);
+                        sr[r][p] = q.s[c >> 1];
+                        br[r][p] = q.b[c >> 1];
                     }
                 }
             }
         }
     };
+    XStage<NT, kStageChunks> xs;
+    xs.load(x, n, mats.norm);
     issue(0);
-    stage_act(x, lds_xh, n, mats.norm);
-    const XPairs xp = build_xpairs(lds_xh, n);
+    const XPairs xp = xs.pairs(x, lds_xh, n, mats.norm);
 
     for (uint32_t grp = 0; seg_id + grp * R * seg_total < total; ++grp) {
         float acc[R];
@@ -103,9 +109,8 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
                     XChunk xc;
                     read_xpairs(xp, c, xc);
                     const float d = dot_q4_chunk(wv[r][p], xc);
-                    const h2 sb = __builtin_bit_cast(h2, sbv[r][p]);
-                    acc[r] = fmaf((float)sb[0], d, acc[r]);
-                    acc[r] = fmaf((float)sb[1], xc.sum, acc[r]);
+                    acc[r] = fmaf(h2f((uint16_t)sr[r][p]), d, acc[r]);
+                    acc[r] = fmaf(h2f((uint16_t)br[r][p]), xc.sum, acc[r]);
                 }
             }
         }
@@ -146,16 +151,18 @@ __device__ __forceinline__ void load_x16(const float* __restrict__ lds, uint32_t
     xs = s;
 }
 
-// Rows of an int8 GEMV. `stage()` must fill lds_x (fp32, n values) and
-// synchronise; it runs after the first row group's loads are in flight.
+// Rows of an int8 GEMV. `stage(issue0)` must fill lds_x (fp32, n values) and
+// synchronise; it calls issue0() (the first row group's loads) once its own
+// input loads are in flight, before it waits for them.
 // Emits fp32 results through `out(row, value)` from lane 0 of each segment.
 template <int SEG, int P, int R, typename Stage, typename Out>
 __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
                                         const uint16_t* __restrict__ B, float* __restrict__ lds_x,
                                         uint32_t M, uint32_t n, Stage stage, Out out) {
+    constexpr uint32_t NT = kThreads;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t nwaves = blockDim.x >> 6;
+    constexpr uint32_t nwaves = NT / 64;
     const uint32_t sl = lane & (SEG - 1);
     const uint32_t lpr = n >> 4;
     const uint32_t ngroups = n >> 6;
@@ -164,7 +171,7 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
     const uint32_t seg_total = gridDim.x * nwaves * spw;
 
     uint4 wv[R][P];
-    float sv[R][P], bv[R][P];
+    uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
     auto issue = [&](uint32_t grp) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -174,16 +181,15 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
                 for (int p = 0; p < P; ++p) {
                     const uint32_t c = sl + p * SEG;
                     if (c < lpr) {
-                        wv[r][p] = ldg16(W + (size_t)row * n + 16u * c);
-                        sv[r][p] = h2f(S[(size_t)row * ngroups + (c >> 2)]);
-                        bv[r][p] = h2f(B[(size_t)row * ngroups + (c >> 2)]);
+                        wv[r][p] = ldg16_stream(W + (size_t)row * n + 16u * c);
+                        sr[r][p] = S[(size_t)row * ngroups + (c >> 2)];
+                        br[r][p] = B[(size_t)row * ngroups + (c >> 2)];
                     }
                 }
             }
         }
     };
-    issue(0);
-    stage();
+    stage([&]() { issue(0); });
     float xr[P][16];
     float xs[P];
 #pragma unroll
@@ -202,8 +208,8 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
                 const uint32_t c = sl + p * SEG;
                 if (c < lpr) {
                     const float d = dot16_q8(wv[r][p], xr[p]);
-                    acc[r] = fmaf(sv[r][p], d, acc[r]);
-                    acc[r] = fmaf(bv[r][p], xs[p], acc[r]);
+                    acc[r] = fmaf(h2f((uint16_t)sr[r][p]), d, acc[r]);
+                    acc[r] = fmaf(h2f((uint16_t)br[r][p]), xs[p], acc[r]);
                 }
             }
         }
@@ -224,10 +230,14 @@ __device__ __forceinline__ void q8_gemv(const uint8_t* __restrict__ W, const uin
     extern __shared__ __attribute__((aligned(16))) float lds_x[];
     q8_rows<SEG, P, R>(
         W, S, B, lds_x, M, n,
-        [&]() {
+        [&](auto issue0) {
             uint16_t* xs = reinterpret_cast<uint16_t*>(lds_x + n);
-            stage_xh(x, xs, n);
-            for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) lds_x[i] = h2f(xs[i]);
+            const NormArg copy{nullptr, nullptr, nullptr, 0.0f, kStageCopy};
+            XStage<kThreads, kStageChunks> st;
+            st.load(x, n, copy);
+            issue0();
+            st.plain(x, xs, n, copy);
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) lds_x[i] = h2f(xs[i]);
             __syncthreads();
         },
         [&](uint32_t row, float v) { y[row] = f2h(v); });
@@ -251,22 +261,26 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
     extern __shared__ __attribute__((aligned(16))) float lds_x[];
     q8_rows<SEG, P, 1>(
         W, S, B, lds_x, E, d,
-        [&]() {
+        [&](auto issue0) {
+            constexpr uint32_t NT = kThreads;
             uint16_t* hs = reinterpret_cast<uint16_t*>(lds_x + d);
-            // the effective-scale chunks are loaded before the staging latency
-            const bool vec = (((uintptr_t)eff) & 15u) == 0 && (d >> 3) <= kStageChunks * blockDim.x;
+            XStage<NT, kStageChunks> st;
+            st.load(h, d, norm);
+            // the effective-scale chunks are loaded with h, before the weights
+            const bool vec = (((uintptr_t)eff) & 15u) == 0 && (d & 7u) == 0 && (d >> 3) <= kStageChunks * NT;
             h8 ev[kStageChunks];
             if (eff && vec)
 #pragma unroll
                 for (uint32_t i = 0; i < kStageChunks; ++i) {
-                    const uint32_t c = threadIdx.x + i * blockDim.x;
-                    if (c < (d >> 3)) ev[i] = __builtin_bit_cast(h8, ld16h(eff, c));
+                    const uint32_t c = threadIdx.x + i * NT;
+                    ev[i] = __builtin_bit_cast(h8, ld16h(eff, c < (d >> 3) ? c : (d >> 3) - 1));
                 }
-            stage_act(h, hs, d, norm);
+            issue0();
+            st.plain(h, hs, d, norm);
             if (vec) {
 #pragma unroll
                 for (uint32_t i = 0; i < kStageChunks; ++i) {
-                    const uint32_t c = threadIdx.x + i * blockDim.x;
+                    const uint32_t c = threadIdx.x + i * NT;
                     if (c < (d >> 3)) {
                         const h8 hv = reinterpret_cast<const h8*>(hs)[c];
 #pragma unroll
@@ -275,7 +289,7 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
                     }
                 }
             } else {
-                for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
+                for (uint32_t i = threadIdx.x; i < d; i += NT) {
                     const float hv = h2f(hs[i]);
                     lds_x[i] = eff ? hv * h2f(eff[i]) : hv;
                 }
@@ -305,11 +319,11 @@ __device__ __forceinline__ void block_topk(const float* stage, uint32_t E, uint3
                                            uint32_t* sel_idx, float* sel_val) {
     __shared__ __attribute__((aligned(16))) uint64_t keys[kRouterMaxExperts];
     const uint32_t ep = (E + 1) & ~1u;
-    for (uint32_t t = threadIdx.x; t < ep; t += blockDim.x) keys[t] = t < E ? topk_key(stage[t], t) : 0ull;
+    for (uint32_t t = threadIdx.x; t < ep; t += kThreads) keys[t] = t < E ? topk_key(stage[t], t) : 0ull;
     __syncthreads();
-    const uint32_t split = (2 * E <= blockDim.x) ? 2u : 1u;
+    const uint32_t split = (2 * E <= kThreads) ? 2u : 1u;
     const uint32_t pairs = ep >> 1, per = (pairs + split - 1) / split;
-    for (uint32_t base = 0; base < E * split; base += blockDim.x) {
+    for (uint32_t base = 0; base < E * split; base += kThreads) {
         const uint32_t slot = base + threadIdx.x;
         const uint32_t t = slot / split, half = slot % split;
         if (t < E) {
@@ -340,7 +354,7 @@ __device__ __forceinline__ void block_softmax_gain(const uint32_t* sel_idx, cons
                                                    uint32_t k, const uint16_t* __restrict__ gain,
                                                    float* ex, float* sel_w) {
     const float vmax = sel_val[0];
-    for (uint32_t r = threadIdx.x; r < k; r += blockDim.x) ex[r] = expf(sel_val[r] - vmax);
+    for (uint32_t r = threadIdx.x; r < k; r += kThreads) ex[r] = expf(sel_val[r] - vmax);
     __syncthreads();
     __shared__ float total;
     if (threadIdx.x == 0) {
@@ -349,7 +363,7 @@ __device__ __forceinline__ void block_softmax_gain(const uint32_t* sel_idx, cons
         total = sum;
     }
     __syncthreads();
-    for (uint32_t r = threadIdx.x; r < k; r += blockDim.x)
+    for (uint32_t r = threadIdx.x; r < k; r += kThreads)
         sel_w[r] = ex[r] / total * (gain ? h2f(gain[sel_idx[r]]) : 1.0f);
     __syncthreads();
 }
@@ -372,7 +386,7 @@ __device__ __forceinline__ void router_select_lds(const float* __restrict__ logi
                                                   const uint16_t* __restrict__ gain, uint32_t E, uint32_t k,
                                                   uint32_t* sel_idx, float* sel_w) {
     __shared__ __attribute__((aligned(16))) float stage[kRouterMaxExperts];
-    for (uint32_t e = threadIdx.x; e < ((E + 3) & ~3u); e += blockDim.x)
+    for (uint32_t e = threadIdx.x; e < ((E + 3) & ~3u); e += kThreads)
         stage[e] = e < E ? logits[e] : -__builtin_inff();
     __syncthreads();
     router_select_staged(stage, gain, E, k, sel_idx, sel_w);
@@ -386,7 +400,7 @@ __device__ __forceinline__ void router_select(const float* __restrict__ logits,
     __shared__ uint32_t sel_idx[kRouterMaxTopK];
     __shared__ float sel_w[kRouterMaxTopK];
     router_select_lds(logits, gain, E, k, sel_idx, sel_w);
-    for (uint32_t r = threadIdx.x; r < k; r += blockDim.x) {
+    for (uint32_t r = threadIdx.x; r < k; r += kThreads) {
         out_idx[r] = sel_idx[r];
         out_w[r] = f2h(sel_w[r]);
         if (out_wf) out_wf[r] = sel_w[r];
@@ -397,20 +411,21 @@ __device__ __forceinline__ void router_select(const float* __restrict__ logits,
 
 // Pure HBM read ceiling (the role of bw_ceiling_read, S/Metal/Quant/
 // dequant_int4.metal:487-502): every lane reads U 16-byte chunks with one
-// coalesced 128-bit load each, all issued before any is consumed; the xor of
+// coalesced non-temporal 128-bit load each (the load the GEMVs stream their
+// weights with), all issued before any is consumed; the xor of
 // everything read goes to sink[block] so nothing is optimised away.
 template <int U>
 __device__ __forceinline__ void read_ceiling(const uint4* __restrict__ src, uint64_t n16,
                                              uint32_t* __restrict__ sink) {
-    const uint64_t nthreads = (uint64_t)gridDim.x * blockDim.x;
-    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t nthreads = (uint64_t)gridDim.x * kThreads;
+    uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
     uint32_t acc = 0;
     for (; i < n16; i += nthreads * U) {
         uint4 v[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint64_t j = i + (uint64_t)u * nthreads;
-            v[u] = j < n16 ? src[j] : make_uint4(0, 0, 0, 0);
+            v[u] = j < n16 ? ldg16_stream(reinterpret_cast<const uint8_t*>(src + j)) : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
@@ -429,8 +444,8 @@ __device__ __forceinline__ void convert_bf16_to_f16(const uint16_t* __restrict__
                                                     uint16_t* __restrict__ dst, uint64_t n,
                                                     uint32_t* __restrict__ inexact) {
     uint32_t bad = 0;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * kThreads) {
         const float v = bf2f(src[i]);
         const uint16_t hbits = f2h(v);
         dst[i] = hbits;

@@ -13,7 +13,9 @@
 //   8-lane segments each own one slot's down row d, so the eight expert dot
 //   products finish inside one wave and lane 0 adds
 //   residual + Σ_slot w[slot]·dot[slot] in fixed slot order.
-// Both issue the weight loads of their first rows before staging activations.
+// Both start with the loads that nothing depends on (activations, expert
+// indices, routing weights), issue the weight loads as soon as the indices
+// are in, and stage the activations into LDS while the weights arrive.
 #pragma once
 
 #include "gemv.hpp"
@@ -32,15 +34,18 @@ struct GateUpRow {
     bool valid;    // its expert index is in range (else the output is NaN)
 };
 
-// Streams gate/up row pairs of length D against x (fp16 in LDS):
-// `rowfn(row)` -> GateUpRow, `out(row, act)` for live rows (lane 0 of the segment).
-template <int SEG, int P, int R, typename RowFn, typename OutFn>
+// Streams gate/up row pairs of length D against x (fp16, staged to LDS):
+// `rowfn(row)` -> GateUpRow, `out(row, act)` for live rows (lane 0 of the
+// segment). `prologue()` runs after the x loads are issued and before the
+// first weight loads (routing: it makes rowfn's expert indices available).
+template <int SEG, int P, int R, typename Pro, typename RowFn, typename OutFn>
 __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uint32_t D, uint32_t total,
-                                             const NormArg& norm, RowFn rowfn, OutFn out) {
+                                             const NormArg& norm, Pro prologue, RowFn rowfn, OutFn out) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
+    constexpr uint32_t NT = kThreads;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t nwaves = blockDim.x >> 6;
+    constexpr uint32_t nwaves = NT / 64;
     const uint32_t sl = lane & (SEG - 1);
     const uint32_t lpr = D >> 5;
     constexpr uint32_t spw = kWave / SEG;
@@ -48,7 +53,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
     const uint32_t seg_total = gridDim.x * nwaves * spw;
 
     uint4 gv[R][P], uv[R][P];
-    uint32_t gsb[R][P], usb[R][P];      // fp16 scale (low half) and bias (high half)
+    uint32_t gsr[R][P], gbr[R][P], usr[R][P], ubr[R][P];    // raw fp16 scales / biases
     auto issue = [&](uint32_t grp) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -60,19 +65,23 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
                     for (int p = 0; p < P; ++p) {
                         const uint32_t c = sl + p * SEG;
                         if (c < lpr) {
-                            gv[r][p] = ldg16(q.gw + 16u * c);
-                            uv[r][p] = ldg16(q.uw + 16u * c);
-                            gsb[r][p] = (uint32_t)q.gs[c >> 1] | ((uint32_t)q.gb[c >> 1] << 16);
-                            usb[r][p] = (uint32_t)q.us[c >> 1] | ((uint32_t)q.ub[c >> 1] << 16);
+                            gv[r][p] = ldg16_stream(q.gw + 16u * c);
+                            uv[r][p] = ldg16_stream(q.uw + 16u * c);
+                            gsr[r][p] = q.gs[c >> 1];
+                            gbr[r][p] = q.gb[c >> 1];
+                            usr[r][p] = q.us[c >> 1];
+                            ubr[r][p] = q.ub[c >> 1];
                         }
                     }
                 }
             }
         }
     };
+    XStage<NT, kStageChunks> xs;
+    xs.load(x, D, norm);
+    prologue();
     issue(0);
-    stage_act(x, lds_xh, D, norm);
-    const XPairs xp = build_xpairs(lds_xh, D);
+    const XPairs xp = xs.pairs(x, lds_xh, D, norm);
     for (uint32_t grp = 0; seg_id + grp * R * seg_total < total; ++grp) {
         float ga[R], ua[R];
 #pragma unroll
@@ -87,12 +96,10 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
                     read_xpairs(xp, c, xc);
                     const float gd = dot_q4_chunk(gv[r][p], xc);
                     const float ud = dot_q4_chunk(uv[r][p], xc);
-                    const h2 g2 = __builtin_bit_cast(h2, gsb[r][p]);
-                    const h2 u2 = __builtin_bit_cast(h2, usb[r][p]);
-                    ga[r] = fmaf((float)g2[0], gd, ga[r]);
-                    ga[r] = fmaf((float)g2[1], xc.sum, ga[r]);
-                    ua[r] = fmaf((float)u2[0], ud, ua[r]);
-                    ua[r] = fmaf((float)u2[1], xc.sum, ua[r]);
+                    ga[r] = fmaf(h2f((uint16_t)gsr[r][p]), gd, ga[r]);
+                    ga[r] = fmaf(h2f((uint16_t)gbr[r][p]), xc.sum, ga[r]);
+                    ua[r] = fmaf(h2f((uint16_t)usr[r][p]), ud, ua[r]);
+                    ua[r] = fmaf(h2f((uint16_t)ubr[r][p]), xc.sum, ua[r]);
                 }
             }
         }
@@ -110,39 +117,51 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
     }
 }
 
+// Row `row` of phase 1 given the slot it belongs to and that slot's expert.
+__device__ __forceinline__ GateUpRow expert_gate_up_row(const ExpertPool& pool, uint32_t slot, uint32_t e,
+                                                        uint32_t f, uint32_t top_k, uint32_t D) {
+    const uint32_t row_bytes = D >> 1;
+    const uint32_t ngroups = D >> 6;
+    GateUpRow q{};
+    q.live = slot < top_k;                          // moe.metal:387 semantics
+    q.valid = q.live && e < pool.num_experts;
+    const uint8_t* blob = pool.base + (uint64_t)(q.valid ? e : 0u) * pool.stride;
+    const ExpertOffsets& o = pool.off;
+    q.gw = blob + o.gate_w + (size_t)f * row_bytes;
+    q.gs = reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f * ngroups;
+    q.gb = reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (size_t)f * ngroups;
+    q.uw = blob + o.up_w + (size_t)f * row_bytes;
+    q.us = reinterpret_cast<const uint16_t*>(blob + o.up_s) + (size_t)f * ngroups;
+    q.ub = reinterpret_cast<const uint16_t*>(blob + o.up_b) + (size_t)f * ngroups;
+    return q;
+}
+
 // Phase 1 over n_active slots (active_slots == nullptr: slots 0..n_active-1).
+// The (slot, expert) of every active index is read once per block into LDS
+// (n_active <= kRouterMaxTopK, checked by the host).
 template <int SEG, int P, int R>
 __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint32_t* __restrict__ active_slots, uint32_t n_active,
                                            uint32_t top_k, const uint16_t* __restrict__ x,
                                            uint16_t* __restrict__ acts, uint32_t D, uint32_t F,
                                            const NormArg& norm) {
-    const uint32_t row_bytes = D >> 1;
-    const uint32_t ngroups = D >> 6;
-    auto slot_of = [&](uint32_t row) {
-        const uint32_t a = row / F;
-        return active_slots ? active_slots[a] : a;
-    };
+    __shared__ uint32_t act_slot[kRouterMaxTopK];
+    __shared__ uint32_t act_expert[kRouterMaxTopK];
     gate_up_rows<SEG, P, R>(
         x, D, n_active * F, norm,
-        [&](uint32_t row) {
-            const uint32_t slot = slot_of(row);
-            const uint32_t f = row % F;
-            GateUpRow q{};
-            q.live = slot < top_k;                          // moe.metal:387 semantics
-            const uint32_t e = q.live ? indices[slot] : 0u;
-            q.valid = q.live && e < pool.num_experts;
-            const uint8_t* blob = pool.base + (uint64_t)(q.valid ? e : 0u) * pool.stride;
-            const ExpertOffsets& o = pool.off;
-            q.gw = blob + o.gate_w + (size_t)f * row_bytes;
-            q.gs = reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f * ngroups;
-            q.gb = reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (size_t)f * ngroups;
-            q.uw = blob + o.up_w + (size_t)f * row_bytes;
-            q.us = reinterpret_cast<const uint16_t*>(blob + o.up_s) + (size_t)f * ngroups;
-            q.ub = reinterpret_cast<const uint16_t*>(blob + o.up_b) + (size_t)f * ngroups;
-            return q;
+        [&]() {
+            if (threadIdx.x < n_active) {
+                const uint32_t slot = active_slots ? active_slots[threadIdx.x] : threadIdx.x;
+                act_slot[threadIdx.x] = slot;
+                act_expert[threadIdx.x] = slot < top_k ? indices[slot] : 0u;
+            }
+            __syncthreads();
         },
-        [&](uint32_t row, float act) { acts[(size_t)slot_of(row) * F + row % F] = f2h(act); });
+        [&](uint32_t row) {
+            const uint32_t a = row / F;
+            return expert_gate_up_row(pool, act_slot[a], act_expert[a], row % F, top_k, D);
+        },
+        [&](uint32_t row, float act) { acts[(size_t)act_slot[row / F] * F + row % F] = f2h(act); });
 }
 
 // Phase 1 with the router's selection folded in: every block selects the
@@ -158,26 +177,31 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
                                                   float* __restrict__ out_wf, const uint16_t* __restrict__ x,
                                                   uint16_t* __restrict__ acts, uint32_t D, uint32_t F,
                                                   const NormArg& norm) {
-    // phase 1 needs only the indices; the routing weights (for phase 2) are
-    // formed by block 0 alone
     __shared__ __attribute__((aligned(16))) float stage[kRouterMaxExperts];
     __shared__ uint32_t sel_idx[kRouterMaxTopK];
     __shared__ float sel_val[kRouterMaxTopK];
-    for (uint32_t e = threadIdx.x; e < ((E + 3) & ~3u); e += blockDim.x)
-        stage[e] = e < E ? logits[e] : -__builtin_inff();
-    __syncthreads();
-    block_topk(stage, E, top_k, sel_idx, sel_val);
-    if (blockIdx.x == 0) {
-        __shared__ float ex[kRouterMaxTopK];
-        __shared__ float sel_w[kRouterMaxTopK];
-        block_softmax_gain(sel_idx, sel_val, top_k, gain, ex, sel_w);
-        for (uint32_t r = threadIdx.x; r < top_k; r += blockDim.x) {
-            out_idx[r] = sel_idx[r];
-            out_w[r] = f2h(sel_w[r]);
-            if (out_wf) out_wf[r] = sel_w[r];
-        }
-    }
-    moe_phase1<SEG, P, R>(pool, sel_idx, nullptr, top_k, top_k, x, acts, D, F, norm);
+    gate_up_rows<SEG, P, R>(
+        x, D, top_k * F, norm,
+        [&]() {
+            for (uint32_t e = threadIdx.x; e < ((E + 3) & ~3u); e += kThreads)
+                stage[e] = e < E ? logits[e] : -__builtin_inff();
+            __syncthreads();
+            block_topk(stage, E, top_k, sel_idx, sel_val);
+            // phase 1 needs only the indices; the routing weights (for
+            // phase 2) are formed by block 0 alone
+            if (blockIdx.x == 0) {
+                __shared__ float ex[kRouterMaxTopK];
+                __shared__ float sel_w[kRouterMaxTopK];
+                block_softmax_gain(sel_idx, sel_val, top_k, gain, ex, sel_w);
+                for (uint32_t r = threadIdx.x; r < top_k; r += kThreads) {
+                    out_idx[r] = sel_idx[r];
+                    out_w[r] = f2h(sel_w[r]);
+                    if (out_wf) out_wf[r] = sel_w[r];
+                }
+            }
+        },
+        [&](uint32_t row) { return expert_gate_up_row(pool, row / F, sel_idx[row / F], row % F, top_k, D); },
+        [&](uint32_t row, float act) { acts[(size_t)(row / F) * F + row % F] = f2h(act); });
 }
 
 // Shared-expert gate/up/act: act[i] = fp16(gelu(gate[i]·x) · (up[i]·x)).
@@ -188,7 +212,7 @@ __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& u
     const uint32_t row_bytes = D >> 1;
     const uint32_t ngroups = D >> 6;
     gate_up_rows<SEG, P, R>(
-        x, D, F, norm,
+        x, D, F, norm, [] {},
         [&](uint32_t f) {
             GateUpRow q{};
             q.live = true;
@@ -204,6 +228,8 @@ __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& u
         [&](uint32_t f, float a) { act[f] = f2h(a); });
 }
 
+constexpr uint32_t kPhase2Chunks = 4;     // 16-byte act pieces per thread: top_k·F <= 8192
+
 // Phase 2: 8 slots × 8-lane segments per wave; P chunks of 32 per lane
 // (F <= 256*P); R output rows per wave in flight. Dynamic LDS:
 // xpairs_lds_bytes(top_k*F).
@@ -215,27 +241,35 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                                            uint16_t* __restrict__ y, uint32_t D, uint32_t F,
                                            uint32_t top_k) {
     constexpr int SEG = 8;
+    constexpr uint32_t NT = kThreads;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_a[];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t nwaves = blockDim.x >> 6;
+    constexpr uint32_t nwaves = NT / 64;
     const uint32_t slot = lane >> 3;
     const uint32_t sl = lane & (SEG - 1);
     const uint32_t lpr = F >> 5;
     const uint32_t row_bytes = F >> 1;
     const uint32_t ngroups = F >> 6;
     const bool live = slot < top_k;
+    const uint32_t wave_id = blockIdx.x * nwaves + wave;
+    const uint32_t wave_total = gridDim.x * nwaves;
+    const uint32_t n_acts = top_k * F;
+
+    // independent loads first: the activations, the slot's expert index and weight
+    XStage<NT, kPhase2Chunks, false> xs;
+    const NormArg copy{nullptr, nullptr, nullptr, 0.0f, kStageCopy};
+    xs.load(acts, n_acts, copy);
     const uint32_t e = live ? indices[slot] : 0u;
+    const uint16_t w_raw = live ? rw[slot] : (uint16_t)0;
     const bool valid = live && e < pool.num_experts;
     const uint8_t* blob = pool.base + (uint64_t)(valid ? e : 0u) * pool.stride;
     const uint8_t* dw = blob + pool.off.down_w;
     const uint16_t* ds = reinterpret_cast<const uint16_t*>(blob + pool.off.down_s);
     const uint16_t* db = reinterpret_cast<const uint16_t*>(blob + pool.off.down_b);
-    const uint32_t wave_id = blockIdx.x * nwaves + wave;
-    const uint32_t wave_total = gridDim.x * nwaves;
 
     uint4 wv[R][P];
-    uint32_t sbv[R][P];      // fp16 scale (low half) and bias (high half)
+    uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
     auto issue = [&](uint32_t grp) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -245,18 +279,17 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                 for (int p = 0; p < P; ++p) {
                     const uint32_t c = sl + p * SEG;
                     if (c < lpr) {
-                        wv[r][p] = ldg16(dw + (size_t)d * row_bytes + 16u * c);
-                        sbv[r][p] = (uint32_t)ds[(size_t)d * ngroups + (c >> 1)] |
-                                    ((uint32_t)db[(size_t)d * ngroups + (c >> 1)] << 16);
+                        wv[r][p] = ldg16_stream(dw + (size_t)d * row_bytes + 16u * c);
+                        sr[r][p] = ds[(size_t)d * ngroups + (c >> 1)];
+                        br[r][p] = db[(size_t)d * ngroups + (c >> 1)];
                     }
                 }
             }
         }
     };
     issue(0);
-    stage_xh(acts, lds_a, top_k * F);
-    const XPairs xp = build_xpairs(lds_a, top_k * F);      // slot s owns chunks s·lpr ..
-    const float w_slot = live ? h2f(rw[slot]) : 0.0f;
+    const XPairs xp = xs.pairs(acts, lds_a, n_acts, copy);      // slot s owns chunks s·lpr ..
+    const float w_slot = live ? h2f(w_raw) : 0.0f;
 
     for (uint32_t grp = 0; wave_id + grp * R * wave_total < D; ++grp) {
         float acc[R];
@@ -271,9 +304,8 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                         XChunk xc;
                         read_xpairs(xp, slot * lpr + c, xc);
                         const float dd = dot_q4_chunk(wv[r][p], xc);
-                        const h2 sb = __builtin_bit_cast(h2, sbv[r][p]);
-                        acc[r] = fmaf((float)sb[0], dd, acc[r]);
-                        acc[r] = fmaf((float)sb[1], xc.sum, acc[r]);
+                        acc[r] = fmaf(h2f((uint16_t)sr[r][p]), dd, acc[r]);
+                        acc[r] = fmaf(h2f((uint16_t)br[r][p]), xc.sum, acc[r]);
                     }
                 }
             } else if (live) {

@@ -59,7 +59,7 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
         my_w[j] = i < n ? w[i] : (uint16_t)0;
     }
     if (tid == 0) bad = 0;
-    for (uint32_t i = tid; i < nchunks * kGroupMaxExperts; i += blockDim.x)
+    for (uint32_t i = tid; i < nchunks * kGroupMaxExperts; i += kGroupThreads)
         (&cnt[0][0])[i] = 0;
     uint32_t my_bad = 0;
 #pragma unroll
@@ -69,7 +69,7 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
     if (my_bad) atomicOr(&bad, 1u);
     __syncthreads();
     if (bad) {
-        for (uint32_t e = tid; e < E; e += blockDim.x) {
+        for (uint32_t e = tid; e < E; e += kGroupThreads) {
             offsets[e] = 0xFFFFFFFFu;
             counts[e] = 0;
         }
@@ -109,7 +109,7 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
     }
     __syncthreads();
     // per expert: exclusive scan over the chunks (in chunk order)
-    for (uint32_t e = tid; e < E; e += blockDim.x) {
+    for (uint32_t e = tid; e < E; e += kGroupThreads) {
         uint32_t run = 0;
         for (uint32_t c = 0; c < nchunks; ++c) {
             const uint32_t v = cnt[c][e];
@@ -151,7 +151,7 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
         }
     }
     __syncthreads();
-    for (uint32_t e = tid; e < E; e += blockDim.x) {
+    for (uint32_t e = tid; e < E; e += kGroupThreads) {
         offsets[e] = tot[e] ? base[e] : 0xFFFFFFFFu;
         counts[e] = tot[e];
         for (uint32_t t = tile_base[e]; t < tile_base[e + 1]; ++t) {
@@ -234,7 +234,7 @@ __device__ __forceinline__ void moe_grouped_down(const ExpertPool& pool, const P
 __device__ __forceinline__ void moe_combine(const uint16_t* __restrict__ partials,
                                             const uint16_t* __restrict__ w, uint16_t* __restrict__ h2,
                                             uint32_t T, uint32_t k, uint32_t D) {
-    const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t d = blockIdx.x * kThreads + threadIdx.x;
     const uint32_t t = blockIdx.y;
     if (t >= T || d >= D) return;
     float acc = 0.0f;

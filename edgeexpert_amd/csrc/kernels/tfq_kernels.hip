@@ -188,7 +188,7 @@ extern "C" __global__ __launch_bounds__(256) void tfq_convert_bf16_f16(const uin
     convert_bf16_to_f16(src, dst, n, inexact);
 }
 
-extern "C" __global__ __launch_bounds__(1024) void tfq_layer_tail(
+extern "C" __global__ __launch_bounds__(kLayerTailThreads) void tfq_layer_tail(
     const uint16_t* hidden, const uint16_t* attn, const uint16_t* w_post_attn, const uint16_t* h1,
     const uint16_t* w_sp, const uint16_t* h2, const uint16_t* w_pf2, const uint16_t* w_pf, float eps,
     float layer_scalar, uint16_t* out, uint32_t D) {
