@@ -54,6 +54,10 @@ inline int check_stage(const NormArg& na) {
 
 inline NormArg stage_copy() { return NormArg{nullptr, nullptr, nullptr, 0.0f, kStageCopy}; }
 
+// Kernel-name infix of the GEMV-family form that stages x as `na` says:
+// "" for a plain copy, "norm_" for the forms that normalise while staging.
+inline const char* form_prefix(const NormArg& na) { return na.mode == kStageCopy ? "" : "norm_"; }
+
 // S/Kernels/Quant/DequantInt4GEMV.swift:5-181 (encode and encodeTgx share one kernel here:
 // x always lives in LDS) and S/Kernels/Fusions/FusedQKVGEMV.swift:4-157.
 class DequantInt4GEMV {
@@ -107,7 +111,7 @@ private:
         }
         const SegShape sh = seg_shape_fit(n / 32, 2);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_q4_gemv_s%u_p%u", sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_q4_gemv_%ss%u_p%u", form_prefix(mats.norm), sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         uint32_t nn = n;
         void* args[] = {&mats, &x, &nn};
@@ -222,7 +226,7 @@ public:
         ExpertPool kp = to_kernel_pool(pool);
         const SegShape sh = seg_shape_fit(d / 32, 2);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_moe_phase1_s%u_p%u", sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_moe_phase1_%ss%u_p%u", form_prefix(stage), sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         NormArg na = stage;
         void* args[] = {&kp, &indices, &active_slots, &active_count, &top_k, &x, &acts, &d, &f, &na};
@@ -253,7 +257,7 @@ public:
         ExpertPool kp = to_kernel_pool(pool);
         const SegShape sh = seg_shape_fit(d / 32, 2);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_moe_phase1_routed_s%u_p%u", sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_moe_phase1_routed_%ss%u_p%u", form_prefix(stage), sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         NormArg na = stage;
         void* args[] = {&kp,   &logits, &per_expert_scale, &num_experts, &top_k, &out_indices, &out_weights,
@@ -342,7 +346,7 @@ public:
         NormArg na = stage;
         const SegShape sh = seg_shape_fit(d / 32, 2);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_gate_up_act_s%u_p%u", sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_gate_up_act_%ss%u_p%u", form_prefix(na), sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&g, &u, &x, &act_scratch, &d, &f, &na};
         hipFunction_t fn = m_.get(name);

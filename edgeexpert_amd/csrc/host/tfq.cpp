@@ -28,12 +28,13 @@ static std::vector<std::string> kernel_names() {
                                "s32_p3", "s32_p4", "s64_p1", "s64_p2", "s64_p3", "s64_p4"};
     const char* q8_shapes[] = {"s4_p1", "s8_p1", "s16_p1", "s32_p1",
                                "s64_p1", "s64_p2", "s64_p3", "s64_p4"};
-    for (const char* s : q4_shapes) {
-        names.push_back(std::string("tfq_q4_gemv_") + s);
-        names.push_back(std::string("tfq_moe_phase1_") + s);
-        names.push_back(std::string("tfq_moe_phase1_routed_") + s);
-        names.push_back(std::string("tfq_gate_up_act_") + s);
-    }
+    for (const char* s : q4_shapes)
+        for (const char* form : {"", "norm_"}) {
+            names.push_back(std::string("tfq_q4_gemv_") + form + s);
+            names.push_back(std::string("tfq_moe_phase1_") + form + s);
+            names.push_back(std::string("tfq_moe_phase1_routed_") + form + s);
+            names.push_back(std::string("tfq_gate_up_act_") + form + s);
+        }
     for (const char* s : q8_shapes) {
         names.push_back(std::string("tfq_q8_gemv_") + s);
         names.push_back(std::string("tfq_router_logits_") + s);

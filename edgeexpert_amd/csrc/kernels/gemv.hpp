@@ -55,7 +55,9 @@ __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, 
 // Order of work: the x loads, then every weight / scale / bias load of the
 // first R rows (scale and bias kept raw, so nothing waits on them), then the
 // staging, which waits for x alone; the weights arrive meanwhile.
-template <int SEG, int P, int R>
+// NORM == false: the staging only copies x (mats.norm is ignored), which
+// keeps the norm inputs' registers out of the kernel and its occupancy up.
+template <int SEG, int P, int R, bool NORM>
 __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_t* __restrict__ x,
                                               uint32_t n) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
@@ -92,7 +94,7 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
             }
         }
     };
-    XStage<NT, kStageChunks> xs;
+    XStage<NT, kStageChunks, NORM> xs;
     xs.load(x, n, mats.norm);
     issue(0);
     const XPairs xp = xs.pairs(x, lds_xh, n, mats.norm);

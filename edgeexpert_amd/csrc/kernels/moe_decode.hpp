@@ -38,7 +38,8 @@ struct GateUpRow {
 // `rowfn(row)` -> GateUpRow, `out(row, act)` for live rows (lane 0 of the
 // segment). `prologue()` runs after the x loads are issued and before the
 // first weight loads (routing: it makes rowfn's expert indices available).
-template <int SEG, int P, int R, typename Pro, typename RowFn, typename OutFn>
+// NORM == false: x is staged as is (norm ignored).
+template <int SEG, int P, int R, bool NORM, typename Pro, typename RowFn, typename OutFn>
 __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uint32_t D, uint32_t total,
                                              const NormArg& norm, Pro prologue, RowFn rowfn, OutFn out) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
@@ -77,7 +78,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
             }
         }
     };
-    XStage<NT, kStageChunks> xs;
+    XStage<NT, kStageChunks, NORM> xs;
     xs.load(x, D, norm);
     prologue();
     issue(0);
@@ -139,7 +140,7 @@ __device__ __forceinline__ GateUpRow expert_gate_up_row(const ExpertPool& pool, 
 // Phase 1 over n_active slots (active_slots == nullptr: slots 0..n_active-1).
 // The (slot, expert) of every active index is read once per block into LDS
 // (n_active <= kRouterMaxTopK, checked by the host).
-template <int SEG, int P, int R>
+template <int SEG, int P, int R, bool NORM>
 __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint32_t* __restrict__ active_slots, uint32_t n_active,
                                            uint32_t top_k, const uint16_t* __restrict__ x,
@@ -147,7 +148,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
                                            const NormArg& norm) {
     __shared__ uint32_t act_slot[kRouterMaxTopK];
     __shared__ uint32_t act_expert[kRouterMaxTopK];
-    gate_up_rows<SEG, P, R>(
+    gate_up_rows<SEG, P, R, NORM>(
         x, D, n_active * F, norm,
         [&]() {
             if (threadIdx.x < n_active) {
@@ -170,7 +171,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
 // the experts. Block 0 publishes indices and fp16 / fp32 weights for
 // phase 2 and the caller (MoE.encodeRouterGemma4's outputs,
 // S/Kernels/MoE/MoE.swift:147-197).
-template <int SEG, int P, int R>
+template <int SEG, int P, int R, bool NORM>
 __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const float* __restrict__ logits,
                                                   const uint16_t* __restrict__ gain, uint32_t E, uint32_t top_k,
                                                   uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w,
@@ -180,7 +181,7 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
     __shared__ __attribute__((aligned(16))) float stage[kRouterMaxExperts];
     __shared__ uint32_t sel_idx[kRouterMaxTopK];
     __shared__ float sel_val[kRouterMaxTopK];
-    gate_up_rows<SEG, P, R>(
+    gate_up_rows<SEG, P, R, NORM>(
         x, D, top_k * F, norm,
         [&]() {
             for (uint32_t e = threadIdx.x; e < ((E + 3) & ~3u); e += kThreads)
@@ -205,13 +206,13 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
 }
 
 // Shared-expert gate/up/act: act[i] = fp16(gelu(gate[i]·x) · (up[i]·x)).
-template <int SEG, int P, int R>
+template <int SEG, int P, int R, bool NORM>
 __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& up,
                                                const uint16_t* __restrict__ x, uint16_t* __restrict__ act,
                                                uint32_t D, uint32_t F, const NormArg& norm) {
     const uint32_t row_bytes = D >> 1;
     const uint32_t ngroups = D >> 6;
-    gate_up_rows<SEG, P, R>(
+    gate_up_rows<SEG, P, R, NORM>(
         x, D, F, norm, [] {},
         [&](uint32_t f) {
             GateUpRow q{};

@@ -19,10 +19,17 @@ using namespace tfq;
 #endif
 constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
 
+// Each int4 GEMV-family shape comes in two forms: plain (x staged as is) and
+// _norm (x normalised while staged, NormArg); the plain form needs fewer
+// registers and so runs more wavefronts per SIMD.
 #define TFQ_Q4_GEMV(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_q4_gemv_s##SEG##_p##P(                 \
         Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
-        q4_gemv_multi<SEG, P, kRowsInFlight>(mats, x, n);                                         \
+        q4_gemv_multi<SEG, P, kRowsInFlight, false>(mats, x, n);                                  \
+    }                                                                                            \
+    extern "C" __global__ __launch_bounds__(256) void tfq_q4_gemv_norm_s##SEG##_p##P(            \
+        Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
+        q4_gemv_multi<SEG, P, kRowsInFlight, true>(mats, x, n);                                   \
     }
 
 #define TFQ_Q8_GEMV(SEG, P)                                                                      \
@@ -61,23 +68,29 @@ constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
                               logits + (size_t)blockIdx.y * E, E, d);                            \
     }
 
-#define TFQ_PHASE1(SEG, P)                                                                       \
-    extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase1_s##SEG##_p##P(              \
+#define TFQ_PHASE1_FORM(NAME, NORM, SEG, P)                                                      \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         ExpertPool pool, const uint32_t* indices, const uint32_t* active_slots,                  \
         uint32_t n_active, uint32_t top_k, const uint16_t* x, uint16_t* acts, uint32_t D,        \
         uint32_t F, NormArg norm) {                                                               \
-        moe_phase1<SEG, P, kRowsInFlight>(pool, indices, active_slots, n_active, top_k, x, acts, \
-                                          D, F, norm);                                            \
+        moe_phase1<SEG, P, kRowsInFlight, NORM>(pool, indices, active_slots, n_active, top_k, x,  \
+                                                acts, D, F, norm);                                \
     }
+#define TFQ_PHASE1(SEG, P)                                                                       \
+    TFQ_PHASE1_FORM(tfq_moe_phase1_s##SEG##_p##P, false, SEG, P)                                 \
+    TFQ_PHASE1_FORM(tfq_moe_phase1_norm_s##SEG##_p##P, true, SEG, P)
 
-#define TFQ_PHASE1_ROUTED(SEG, P)                                                                \
-    extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase1_routed_s##SEG##_p##P(       \
+#define TFQ_PHASE1_ROUTED_FORM(NAME, NORM, SEG, P)                                               \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         ExpertPool pool, const float* logits, const uint16_t* gain, uint32_t E, uint32_t top_k,  \
         uint32_t* out_idx, uint16_t* out_w, float* out_wf, const uint16_t* x, uint16_t* acts,    \
         uint32_t D, uint32_t F, NormArg norm) {                                                   \
-        moe_phase1_routed<SEG, P, kRowsInFlight>(pool, logits, gain, E, top_k, out_idx, out_w,   \
-                                                 out_wf, x, acts, D, F, norm);                    \
+        moe_phase1_routed<SEG, P, kRowsInFlight, NORM>(pool, logits, gain, E, top_k, out_idx,    \
+                                                       out_w, out_wf, x, acts, D, F, norm);       \
     }
+#define TFQ_PHASE1_ROUTED(SEG, P)                                                                \
+    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_s##SEG##_p##P, false, SEG, P)                   \
+    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_norm_s##SEG##_p##P, true, SEG, P)
 
 #define TFQ_PHASE2(P)                                                                            \
     extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase2_p##P(                       \
@@ -86,12 +99,15 @@ constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
         moe_phase2<P, kRowsInFlight>(pool, indices, acts, rw, residual, y, D, F, top_k);          \
     }
 
-#define TFQ_GATE_UP(SEG, P)                                                                      \
-    extern "C" __global__ __launch_bounds__(256) void tfq_gate_up_act_s##SEG##_p##P(             \
+#define TFQ_GATE_UP_FORM(NAME, NORM, SEG, P)                                                     \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         Q4Mat gate, Q4Mat up, const uint16_t* x, uint16_t* act, uint32_t D, uint32_t F,          \
         NormArg norm) {                                                                           \
-        q4_gate_up_act<SEG, P, kRowsInFlight>(gate, up, x, act, D, F, norm);                      \
+        q4_gate_up_act<SEG, P, kRowsInFlight, NORM>(gate, up, x, act, D, F, norm);                \
     }
+#define TFQ_GATE_UP(SEG, P)                                                                      \
+    TFQ_GATE_UP_FORM(tfq_gate_up_act_s##SEG##_p##P, false, SEG, P)                               \
+    TFQ_GATE_UP_FORM(tfq_gate_up_act_norm_s##SEG##_p##P, true, SEG, P)
 
 // int4: n/32 chunks per row; (SEG, P) with SEG·P >= chunks (the host picks
 // the pair that wastes the fewest lanes).

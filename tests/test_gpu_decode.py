@@ -444,3 +444,73 @@ def test_phase1_with_selection_equals_router_select_then_phase1(ctx, stream):
         ref_idx, _ = oracle.topk_softmax(oracle.router_logits(Wr, Sr, Br, from_f16_bits(h16)), K,
                                          from_f16_bits(gain16))
         assert list(i2.download(np.uint32, K)) == list(ref_idx)
+
+
+# --------------------------------------------- fused decode token (C ABI) ----
+#
+# tfq_moe_decode_token: router GEMV (each router block also publishes its
+# best 8 keys) -> phase 1 ranking those candidate lists -> phase 2. The
+# selection must equal the oracle's top-k over all logits bit for bit,
+# including ties that span router blocks (lower expert index first).
+
+def _decode_token(ctx, stream, Wr, Sr, Br, h16, E, D, F, K, seed, label, gain16=None):
+    pool_bytes, offs, stride = synth.expert_pool(seed, label, E, D, F)
+    pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs)
+    router = ops.Router(_dev(Wr), _dev(Sr), _dev(Br), E, None, None if gain16 is None else _dev(gain16))
+    y = _dev(np.full(D, 0x7E00, np.uint16))
+    idx, w16 = _dev(np.full(K, 0xFFFFFFFF, np.uint32)), _dev(np.zeros(K, np.uint16))
+    acts = _dev(np.full(K * F, 0x7E00, np.uint16))
+    ws = DeviceBuffer(ROUTER_WORKSPACE_BYTES)
+    ws.fill(0xFF)
+    ops.moe_decode_token(ctx, stream, router, pool, _dev(h16), None, y, D, F, K, idx, w16, acts, ws)
+    stream.sync()
+    h = from_f16_bits(h16)
+    gain = None if gain16 is None else from_f16_bits(gain16)
+    ref_idx, ref_w = oracle.topk_softmax(oracle.router_logits(Wr, Sr, Br, h), K, gain)
+    got_idx = idx.download(np.uint32, K)
+    assert list(got_idx) == list(ref_idx), f"{label}: {list(got_idx)} != {list(ref_idx)}"
+    w_dev = from_f16_bits(w16.download(np.uint16, K))
+    assert np.max(np.abs(w_dev - ref_w)) < 2e-3
+    ref = oracle.moe_routed(pool_bytes, stride, offs, h, ref_idx, w_dev, D, F)
+    rel = oracle.rel_error(from_f16_bits(y.download(np.uint16, D)), ref)
+    assert rel < TOL, f"{label}: rel={rel}"
+    return list(got_idx)
+
+
+def test_decode_token_baseline_config1(ctx, stream):
+    E, D, F, K = 128, 2816, 704, 8
+    W, S, B = synth.int8_matrix(0, "c1/router", E, D)
+    for t in range(2):
+        _decode_token(ctx, stream, W, S, B, synth.f16_vector(0, f"c1/h{t}", D), E, D, F, K, 0, "c1/experts")
+
+
+def test_decode_token_all_logits_equal(ctx, stream):
+    # every router row identical: 128 equal logits across all router blocks
+    E, D, F, K = 128, 512, 128, 8
+    W, S, B = synth.int8_matrix(11, "tie/router", E, D)
+    W[:], S[:], B[:] = W[0], S[0], B[0]
+    got = _decode_token(ctx, stream, W, S, B, synth.f16_vector(11, "tie/h", D), E, D, F, K, 11, "tie/experts")
+    assert got == list(range(K))
+
+
+def test_decode_token_ties_across_router_blocks(ctx, stream):
+    # copies of the best row in several router blocks (16 rows per block at
+    # d = 512): the equal logits must come out in expert-index order
+    E, D, F, K = 128, 512, 128, 8
+    W, S, B = synth.int8_matrix(12, "tie2/router", E, D)
+    h16 = synth.f16_vector(12, "tie2/h", D)
+    best = int(np.argmax(oracle.router_logits(W, S, B, from_f16_bits(h16))))
+    for e in (100, 3, 50, 19, 120, 64):
+        W[e], S[e], B[e] = W[best], S[best], B[best]
+    got = _decode_token(ctx, stream, W, S, B, h16, E, D, F, K, 12, "tie2/experts")
+    tied = sorted({best, 100, 3, 50, 19, 120, 64})
+    assert got[:len(tied)] == tied
+
+
+@pytest.mark.parametrize("E,D,K", [(100, 256, 6), (40, 2816, 8), (256, 1024, 8)])
+def test_decode_token_odd_shapes(ctx, stream, E, D, K):
+    F = 128
+    W, S, B = synth.int8_matrix(13, f"odd/router{E}", E, D)
+    gain16 = f16_bits(synth.uniform24(synth.seed_key(13, f"odd/gain{E}"), E, 0.5, 1.5))
+    _decode_token(ctx, stream, W, S, B, synth.f16_vector(13, f"odd/h{E}", D), E, D, F, K, 13,
+                  f"odd/experts{E}", gain16)
