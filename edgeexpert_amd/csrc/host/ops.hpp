@@ -17,7 +17,12 @@ constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident i
 #define TFQ_ROWS_IN_FLIGHT 1
 #endif
 constexpr uint32_t kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
-constexpr uint32_t kGemmBlock = 512;       // threads of the MFMA GEMM tile (gemm.hpp kGemmThreads)   // rows per segment per group (tfq_kernels.hip)
+constexpr uint32_t kGemmBlock = 512;       // threads of the grouped-MoE MFMA tile (gemm.hpp kGemmThreads)
+constexpr uint32_t kProjBM = 64;           // projection GEMM tile: tokens (gemm.hpp kProjBM)
+constexpr uint32_t kProjBN = 256;          // outputs (gemm.hpp kProjBN)
+constexpr uint32_t kProjThreads = 256;     // threads (gemm.hpp kProjThreads)
+constexpr uint32_t kProjMaxK = 8192;       // longest reduction (gemm.hpp kProjMaxK)
+constexpr uint32_t proj_lds_bytes(uint32_t k) { return 2u * kProjBM * 72u * 2u + 2u * kProjBN * (k / 64u) * 2u; }
 
 // Grid of a row-loop kernel (blocks of kBlock threads, `lds` dynamic LDS
 // bytes): one block per rows_per_block rows, but no more blocks than the GPU
@@ -383,10 +388,14 @@ public:
         const char* name = dtype == TFQ_DTYPE_BF16 ? "tfq_gemm_q4_bf16" : "tfq_gemm_q4_f16";
         hipFunction_t f = m_.get(name);
         if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
-        const uint32_t gx = (n + 127) / 128, gy = (t + 127) / 128;
+        // blockIdx.x walks the outputs, so the token tiles that share a weight
+        // slice are dispatched to the same XCD (and its L2)
+        if (k > kProjMaxK) return fail(TFQ_E_UNSUPPORTED, "k=%u exceeds %u", k, kProjMaxK);
+        const uint32_t gx = (n + kProjBN - 1) / kProjBN, gy = (t + kProjBM - 1) / kProjBM;
+        const uint32_t lds = proj_lds_bytes(k);
         void* args[] = {&x, &weights, &scales, &biases, &y, &t, &n, &k};
-        return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, kGemmBlock, 1, 1, 0, (hipStream_t)stream, args,
-                                               nullptr),
+        return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, kProjThreads, 1, 1, lds, (hipStream_t)stream,
+                                               args, nullptr),
                          name);
     }
 
