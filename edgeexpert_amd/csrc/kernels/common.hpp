@@ -62,6 +62,15 @@ __device__ __forceinline__ uint4 ldg16(const uint8_t* p) {
     return *reinterpret_cast<const uint4*>(p);
 }
 
+// 16-byte load through a pointer the compiler cannot prove global (one read
+// from LDS, say): naming the global address space makes it a global_load,
+// counted by vmcnt only, instead of a flat load, whose completion every LDS
+// wait (lgkmcnt) would also have to wait for.
+typedef __attribute__((address_space(1))) const uint4 global_uint4;
+__device__ __forceinline__ uint4 ldg16_global(const void* p) {
+    return *reinterpret_cast<global_uint4*>(reinterpret_cast<uintptr_t>(p));
+}
+
 // 128-bit load of weights that are read once per token: non-temporal, so the
 // stream does not evict the activations and small vectors the caches hold.
 __device__ __forceinline__ uint4 ldg16_stream(const uint8_t* p) {

@@ -11,7 +11,7 @@
 // v_mfma_f32_32x32x16_f16 tiles per matrix. Per step the block
 //   * loads the X tile (16 B per load, coalesced; rows come from a caller
 //     supplied row table, so gathered rows cost nothing extra) and each W
-//     tile (16 B = 32 codes per lane) with its 128 scale/bias pairs, two
+//     tile (8 B = 16 codes per thread) with its 128 scale/bias pairs, two
 //     steps ahead of their use (two register stages),
 //   * dequantises in registers: (0x6400 | q) - 1024 gives q exactly as fp16,
 //     then v_pk_fma_f16(q, s, b) rounds q·s + b once to fp16 — the fp16
@@ -110,35 +110,30 @@ __device__ __forceinline__ void gemm_tile(GemmLds<NMAT>& L, const uint16_t* cons
     const uint32_t row_bytes = K >> 1;
 
     // global -> registers: X rows tid/8 and tid/8 + 64, 16-byte chunk tid%8
-    // of the group; threads < 256 also load W row tid/2, 16-byte half tid%2
-    // of the group's 32 bytes, with its scale and bias.
+    // of the group; W row tid/4, 8-byte quarter tid%4 of the group's 32 bytes
+    // (all 512 threads, no two loading the same bytes), with its scale and
+    // bias. Every load is unconditional (groups past the end re-read the last
+    // one, rows past `rows` read row 0, outputs past N read row N-1; none of
+    // them is stored), so the number of loads per step is fixed and the
+    // compiler waits for exactly the stage it consumes.
     const uint32_t xr = tid >> 3, xc = tid & 7u;
-    const bool w_thread = tid < 256u;
-    const uint32_t wr = (tid & 255u) >> 1, wh = tid & 1u;
-    const bool w_live = w_thread && n0 + wr < N;
+    const uint32_t wr = tid >> 2, wq = tid & 3u;
     uint4 xreg[2][2];
-    uint4 wreg[2][NMAT];
+    uint2 wreg[2][NMAT];
     uint16_t sreg[2][NMAT], breg[2][NMAT];
-
+    const size_t wn_row = (size_t)(n0 + wr < N ? n0 + wr : N - 1);
     auto load_global = [&](uint32_t g, int st) {
+        const uint32_t gg = g < groups ? g : groups - 1;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const uint32_t j = xr + 64u * p;
-            xreg[st][p] = j < rows ? *reinterpret_cast<const uint4*>(row_ptr[j] + g * 64u + 8u * xc)
-                                   : make_uint4(0, 0, 0, 0);
+            xreg[st][p] = ldg16_global(row_ptr[j < rows ? j : 0u] + gg * 64u + 8u * xc);
         }
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
-            if (w_live) {
-                const size_t n = n0 + wr;
-                wreg[st][m] = ldg16(mats[m].w + n * row_bytes + g * 32u + 16u * wh);
-                sreg[st][m] = mats[m].s[n * groups + g];
-                breg[st][m] = mats[m].b[n * groups + g];
-            } else {
-                wreg[st][m] = make_uint4(0, 0, 0, 0);
-                sreg[st][m] = 0;
-                breg[st][m] = 0;
-            }
+            wreg[st][m] = *reinterpret_cast<const uint2*>(mats[m].w + wn_row * row_bytes + gg * 32u + 8u * wq);
+            sreg[st][m] = mats[m].s[wn_row * groups + gg];
+            breg[st][m] = mats[m].b[wn_row * groups + gg];
         }
     };
     auto store_lds = [&](int st, int buf) {
@@ -147,15 +142,13 @@ __device__ __forceinline__ void gemm_tile(GemmLds<NMAT>& L, const uint16_t* cons
             const h8 v = X_BF16 ? bf16x8_to_f16(xreg[st][p]) : __builtin_bit_cast(h8, xreg[st][p]);
             *reinterpret_cast<h8*>(&L.x[buf][(xr + 64u * p) * kGemmLdsStride + 8u * xc]) = perm_0415(v);
         }
-        if (w_thread) {
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) {
-                h8 runs[4];
-                dequant_chunk_f16(wreg[st][m], sreg[st][m], breg[st][m], runs);
+        for (int m = 0; m < NMAT; ++m) {
+            h8 runs[4];
+            dequant_chunk_f16(make_uint4(wreg[st][m].x, wreg[st][m].y, 0u, 0u), sreg[st][m], breg[st][m], runs);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    *reinterpret_cast<h8*>(&L.w[m][buf][wr * kGemmLdsStride + 32u * wh + 8u * j]) = runs[j];
-            }
+            for (int j = 0; j < 2; ++j)
+                *reinterpret_cast<h8*>(&L.w[m][buf][wr * kGemmLdsStride + 16u * wq + 8u * j]) = runs[j];
         }
     };
 
@@ -193,22 +186,29 @@ __device__ __forceinline__ void gemm_tile(GemmLds<NMAT>& L, const uint16_t* cons
     // one step: register stage and LDS buffer `cur` hold group g; refill the
     // stage with g+2, multiply, store the other stage (g+1) into the other
     // buffer. Stage indices are compile-time (the loop is unrolled by two),
-    // so the register stages never go to scratch.
+    // so the register stages never go to scratch. The main loop runs whole
+    // pairs of steps with no branch inside (past the end the steps re-read
+    // and stage the last group, which nobody uses); an odd last group takes
+    // a checked step after it.
     auto step = [&](uint32_t g, auto cur_c) {
         constexpr int cur = decltype(cur_c)::value;
-        if (g + 2 < groups) load_global(g + 2, cur);
+        load_global(g + 2, cur);
+        // keep the refill loads ahead of the MFMAs that follow
+        __builtin_amdgcn_sched_barrier(0);
         mma_step(cur);
-        if (g + 1 < groups) store_lds(cur ^ 1, cur ^ 1);
+        store_lds(cur ^ 1, cur ^ 1);
         __syncthreads();
     };
     load_global(0, 0);
-    if (groups > 1) load_global(1, 1);
+    load_global(1, 1);
     store_lds(0, 0);
     __syncthreads();
-    for (uint32_t g = 0; g < groups; g += 2) {
+    uint32_t g = 0;
+    for (; g + 2 <= groups; g += 2) {
         step(g, std::integral_constant<int, 0>{});
-        if (g + 1 < groups) step(g + 1, std::integral_constant<int, 1>{});
+        step(g + 1, std::integral_constant<int, 1>{});
     }
+    if (g < groups) step(g, std::integral_constant<int, 0>{});
 
     // D layout (32x32 tile): column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4.
 #pragma unroll
@@ -382,8 +382,8 @@ __device__ __forceinline__ void gemm_q4_proj(const uint16_t* __restrict__ X, con
     auto load = [&](uint32_t g, auto st_c) {
         constexpr int ST = decltype(st_c)::value;
         const uint32_t gg = g < G ? g : G - 1;
-        w0[ST] = ldg16_stream(wp0 + 32u * gg);
-        w1[ST] = ldg16_stream(wp1 + 32u * gg);
+        w0[ST] = ldg16(wp0 + 32u * gg);          // plain loads: the 8 token tiles of an
+        w1[ST] = ldg16(wp1 + 32u * gg);          // output slice share it through L2
         xa[ST] = *reinterpret_cast<const uint4*>(xp + 64u * gg);
         xb[ST] = *reinterpret_cast<const uint4*>(xp + 64u * gg + 8u);
     };
