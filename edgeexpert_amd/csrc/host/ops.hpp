@@ -17,7 +17,6 @@ constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident i
 #define TFQ_ROWS_IN_FLIGHT 1
 #endif
 constexpr uint32_t kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
-constexpr uint32_t kGemmBlock = 512;       // threads of the grouped-MoE MFMA tile (gemm.hpp kGemmThreads)
 constexpr uint32_t kProjBM = 64;           // projection GEMM tile: tokens (gemm.hpp kProjBM)
 constexpr uint32_t kProjBN = 256;          // outputs (gemm.hpp kProjBN)
 constexpr uint32_t kProjThreads = 256;     // threads (gemm.hpp kProjThreads)
@@ -521,13 +520,19 @@ public:
         if (stride < d || stride % 8) return fail(TFQ_E_INVAL, "hidden stride must be >= d and a multiple of 8");
         if (!aligned(hidden, 16) || !aligned(act, 16))
             return fail(TFQ_E_INVAL, "hidden and act must be 16-byte aligned");
+        if (d > kProjMaxK || f > kProjMaxK)
+            return fail(TFQ_E_UNSUPPORTED, "d=%u and f=%u must be at most %u", d, f, kProjMaxK);
         if (max_tiles == 0) return TFQ_OK;
         ExpertPool kp = kernel_pool(pool);
+        // two 64-row halves per grouping tile; gate/up: 128 features per block,
+        // down: 256 outputs per block
         void* a1[] = {&kp, &sorted, &tiles, &n_tiles, &hidden, &stride, &act, &d, &f};
-        rc = launch2(m_, "tfq_moe_grouped_gate_up", max_tiles, (f + 127) / 128, kGemmBlock, 0, stream, a1);
+        rc = launch2(m_, "tfq_moe_grouped_gate_up", 2 * max_tiles, (f + 127) / 128, kProjThreads,
+                     proj_lds_bytes(d), stream, a1);
         if (rc) return rc;
         void* a2[] = {&kp, &sorted, &tiles, &n_tiles, &act, &partials, &d, &f, &k};
-        return launch2(m_, "tfq_moe_grouped_down", max_tiles, (d + 127) / 128, kGemmBlock, 0, stream, a2);
+        return launch2(m_, "tfq_moe_grouped_down", 2 * max_tiles, (d + kProjBN - 1) / kProjBN, kProjThreads,
+                       proj_lds_bytes(f), stream, a2);
     }
 
     // PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38).

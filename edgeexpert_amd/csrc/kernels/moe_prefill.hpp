@@ -8,8 +8,8 @@
 // PrefillGroupedRoutedMoE.encodeStreamedBatched
 // (PrefillGroupedRoutedMoE.swift:446-527; kernels S/Metal/Prefill/prefill.metal:598-670)
 // and PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38; prefill.metal:575-596).
-// Here the pairs never leave the device and every expert's rows become one
-// or more 128-row MFMA tiles.
+// Here the pairs never leave the device; every expert's rows become one or
+// more 128-row tiles, each run as two 64-row halves on the matrix cores.
 #pragma once
 
 #include "abi_types.h"
@@ -171,62 +171,113 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
     }
 }
 
-// Grouped gate/up + GeGLU over one expert tile (blockIdx.x) and 128 outputs of
-// F (blockIdx.y): act[p][f] = fp16(gelu(gate_e[f]·x_p) · (up_e[f]·x_p)) for
-// sorted pairs p of the tile, x_p = hidden row of the pair's token
-// (prefill.metal:598-637).
+// The grouped GEMMs run each 128-row grouping tile as two 64-row halves
+// (blockIdx.x = 2·tile + half) on the projection tile of gemm.hpp, so an
+// expert with few rows costs one half's matrix work, not a full tile's.
+// Returns false for a half with no rows (block-uniform).
+struct GroupedRows {
+    uint32_t first;   // index of the half's first row in the sorted pairs
+    uint32_t count;   // rows in this half (1..64)
+    uint32_t expert;
+};
+
+__device__ __forceinline__ bool grouped_rows(const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
+                                             GroupedRows& gr) {
+    const uint32_t tile = blockIdx.x >> 1, half = blockIdx.x & 1u;
+    if (tile >= *n_tiles) return false;
+    const Tile t = tiles[tile];
+    if (t.count <= kProjBM * half) return false;
+    const uint32_t left = t.count - kProjBM * half;
+    gr = {t.start + kProjBM * half, left < kProjBM ? left : kProjBM, t.expert};
+    return true;
+}
+
+// Grouped gate/up + GeGLU over one 64-row half tile (blockIdx.x) and 128
+// features of F (blockIdx.y): act[p][f] = fp16(gelu(gate_e[f]·x_p) · (up_e[f]·x_p))
+// for sorted pairs p of the half, x_p = hidden row of the pair's token
+// (prefill.metal:598-637). Wave w takes features f0 + 32w .. +31 with the gate
+// rows as its first 32-output sub-tile and the up rows as its second, so each
+// lane holds gate and up of the same (pair, feature) and applies the GeGLU
+// in registers. LDS table rows 0..127: gate scales/biases, 128..255: up.
 __device__ __forceinline__ void moe_grouped_gate_up(const ExpertPool& pool, const Pair* __restrict__ sorted,
                                                     const Tile* __restrict__ tiles,
                                                     const uint32_t* __restrict__ n_tiles,
                                                     const uint16_t* __restrict__ hidden, uint32_t stride,
                                                     uint16_t* __restrict__ act, uint32_t D, uint32_t F) {
-    if (blockIdx.x >= *n_tiles) return;                  // block-uniform
-    __shared__ __attribute__((aligned(16))) GemmLds<2> L;
-    __shared__ const uint16_t* rows_ptr[kGemmBM];
-    const Tile t = tiles[blockIdx.x];
-    if (threadIdx.x < t.count)
-        rows_ptr[threadIdx.x] = hidden + (size_t)sorted[t.start + threadIdx.x].token * stride;
-    __syncthreads();
-    const uint8_t* blob = pool.base + (uint64_t)t.expert * pool.stride;
+    GroupedRows gr;
+    if (!grouped_rows(tiles, n_tiles, gr)) return;
+    extern __shared__ __attribute__((aligned(16))) _Float16 proj_lds[];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+    const uint32_t G = D >> 6, f0 = blockIdx.y * 128u;
+    const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
     const ExpertOffsets& o = pool.off;
-    const Q4Tile mats[2] = {
-        {blob + o.gate_w, reinterpret_cast<const uint16_t*>(blob + o.gate_s),
-         reinterpret_cast<const uint16_t*>(blob + o.gate_b)},
-        {blob + o.up_w, reinterpret_cast<const uint16_t*>(blob + o.up_s),
-         reinterpret_cast<const uint16_t*>(blob + o.up_b)}};
-    gemm_tile<false, 2>(L, rows_ptr, t.count, mats, blockIdx.y * kGemmBN, F, D,
-                        [&](uint32_t j, uint32_t f, const float* v) {
-                            act[(size_t)(t.start + j) * F + f] = f2h(gelu_tanh(v[0]) * v[1]);
-                        });
+    const uint16_t* gs = reinterpret_cast<const uint16_t*>(blob + o.gate_s);
+    const uint16_t* gb = reinterpret_cast<const uint16_t*>(blob + o.gate_b);
+    const uint16_t* us = reinterpret_cast<const uint16_t*>(blob + o.up_s);
+    const uint16_t* ub = reinterpret_cast<const uint16_t*>(blob + o.up_b);
+    uint16_t* s_lds = reinterpret_cast<uint16_t*>(proj_lds + 2 * kProjBM * kGemmLdsStride);
+    uint16_t* b_lds = s_lds + kProjBN * G;
+    const uint32_t nf = F - f0 < 128u ? F - f0 : 128u;
+    copy_pair_to_lds<kProjThreads>(gs + (size_t)f0 * G, gb + (size_t)f0 * G, s_lds, b_lds, nf * G);
+    copy_pair_to_lds<kProjThreads>(us + (size_t)f0 * G, ub + (size_t)f0 * G, s_lds + 128u * G, b_lds + 128u * G,
+                                   nf * G);
+    const uint32_t col = lane & 31u, h = lane >> 5;
+    const uint32_t f = f0 + 32u * wave + col, fc = f < F ? f : F - 1;   // features past F: clamped, not stored
+    ProjLanes pl;
+    pl.wp0 = blob + o.gate_w + (size_t)fc * (D >> 1) + 16u * h;
+    pl.wp1 = blob + o.up_w + (size_t)fc * (D >> 1) + 16u * h;
+    pl.sidx0 = (fc - f0) * G;
+    pl.sidx1 = (128u + fc - f0) * G;
+    // rows past the half's count read its first row: their results are never stored
+    const uint32_t xrow = tid >> 2;
+    const uint32_t tok = sorted[gr.first + (xrow < gr.count ? xrow : 0u)].token;
+    const uint16_t* xp = hidden + (size_t)tok * stride + 16u * (tid & 3u);
+    f32x16 acc[2][2];
+    proj_core<false>(acc, proj_lds, s_lds, b_lds, pl, xp, G);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t m = 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
+            if (m < gr.count && f < F)
+                act[(size_t)(gr.first + m) * F + f] = f2h(gelu_tanh(acc[i][0][r]) * acc[i][1][r]);
+        }
 }
 
-// Grouped down projection over one expert tile (blockIdx.x) and 128 outputs of
-// D (blockIdx.y): partials[(token*k + rank)*D + d] = fp16(down_e[d]·act_p)
+// Grouped down projection over one 64-row half tile (blockIdx.x) and 256
+// outputs of D (blockIdx.y): partials[(token*k + rank)*D + d] = fp16(down_e[d]·act_p)
 // (prefill.metal:639-670).
 __device__ __forceinline__ void moe_grouped_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
                                                  const Tile* __restrict__ tiles,
                                                  const uint32_t* __restrict__ n_tiles,
                                                  const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
                                                  uint32_t D, uint32_t F, uint32_t k) {
-    if (blockIdx.x >= *n_tiles) return;
-    __shared__ __attribute__((aligned(16))) GemmLds<1> L;
-    __shared__ const uint16_t* rows_ptr[kGemmBM];
-    __shared__ uint32_t dst_row[kGemmBM];
-    const Tile t = tiles[blockIdx.x];
-    if (threadIdx.x < t.count) {
-        const Pair p = sorted[t.start + threadIdx.x];
-        rows_ptr[threadIdx.x] = act + (size_t)(t.start + threadIdx.x) * F;
-        dst_row[threadIdx.x] = p.token * k + p.rank;
-    }
-    __syncthreads();
-    const uint8_t* blob = pool.base + (uint64_t)t.expert * pool.stride;
+    GroupedRows gr;
+    if (!grouped_rows(tiles, n_tiles, gr)) return;
+    extern __shared__ __attribute__((aligned(16))) _Float16 proj_lds[];
+    __shared__ uint32_t dst_row[kProjBM];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+    const uint32_t G = F >> 6, n0 = blockIdx.y * kProjBN;
+    const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
     const ExpertOffsets& o = pool.off;
-    const Q4Tile mats[1] = {{blob + o.down_w, reinterpret_cast<const uint16_t*>(blob + o.down_s),
-                             reinterpret_cast<const uint16_t*>(blob + o.down_b)}};
-    gemm_tile<false, 1>(L, rows_ptr, t.count, mats, blockIdx.y * kGemmBN, D, F,
-                        [&](uint32_t j, uint32_t d, const float* v) {
-                            partials[(size_t)dst_row[j] * D + d] = f2h(v[0]);
-                        });
+    uint16_t* s_lds = reinterpret_cast<uint16_t*>(proj_lds + 2 * kProjBM * kGemmLdsStride);
+    uint16_t* b_lds = s_lds + kProjBN * G;
+    if (tid < gr.count) {
+        const Pair p = sorted[gr.first + tid];
+        dst_row[tid] = p.token * k + p.rank;
+    }
+    const uint32_t nrows = D - n0 < kProjBN ? D - n0 : kProjBN;
+    copy_pair_to_lds<kProjThreads>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)n0 * G,
+                                   reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)n0 * G, s_lds,
+                                   b_lds, nrows * G);
+    const ProjLanes pl = proj_lanes(blob + o.down_w, F >> 1, n0, wave, D, 0, G);
+    const uint32_t xrow = tid >> 2;
+    const uint16_t* xp = act + (size_t)(gr.first + (xrow < gr.count ? xrow : 0u)) * F + 16u * (tid & 3u);
+    f32x16 acc[2][2];
+    proj_core<false>(acc, proj_lds, s_lds, b_lds, pl, xp, G);     // its barriers publish dst_row
+    proj_for_each(acc, [&](uint32_t m, uint32_t n, float v) {
+        if (m < gr.count && n0 + n < D) partials[(size_t)dst_row[m] * D + n0 + n] = f2h(v);
+    });
 }
 
 // h2[t][d] = fp16(Σ_r fma(w[t][r], partials[(t*k+r)*D + d])) in rank order

@@ -175,13 +175,13 @@ extern "C" __global__ __launch_bounds__(kGroupThreads) void tfq_moe_group(
     moe_group(idx, w, T, k, E, sorted, offsets, counts, tiles, n_tiles, status);
 }
 
-extern "C" __global__ __launch_bounds__(kGemmThreads) void tfq_moe_grouped_gate_up(
+extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_gate_up(
     ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,
     const uint16_t* hidden, uint32_t stride, uint16_t* act, uint32_t D, uint32_t F) {
     moe_grouped_gate_up(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F);
 }
 
-extern "C" __global__ __launch_bounds__(kGemmThreads) void tfq_moe_grouped_down(
+extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_down(
     ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,
     const uint16_t* act, uint16_t* partials, uint32_t D, uint32_t F, uint32_t k) {
     moe_grouped_down(pool, sorted, tiles, n_tiles, act, partials, D, F, k);

@@ -403,7 +403,8 @@ int tfq_group_pairs_host(const tfq_pair *pairs, int64_t n_pairs, int64_t query_c
  * launch bound (TFQ_MOE_MAX_TILES); the device *n_tiles decides. Replaces
  * PrefillGroupedRoutedMoE.encodeStreamedBatched
  * (S/Kernels/Prefill/MoE/PrefillGroupedRoutedMoE.swift:446-527).
- * Contract: d, f multiples of 64; hidden rows 16-byte aligned. */
+ * Contract: d, f multiples of 64 and at most 8192 (TFQ_E_UNSUPPORTED
+ * beyond); hidden rows 16-byte aligned. */
 int tfq_moe_grouped(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
                     const tfq_pair *sorted, const tfq_tile *tiles, const uint32_t *n_tiles,
                     uint32_t max_tiles, const uint16_t *hidden, uint32_t hidden_stride,
