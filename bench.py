@@ -217,7 +217,7 @@ def main():
         sys.exit(2)
 
     from edgeexpert_amd import ops, synth
-    from edgeexpert_amd._lib import ROUTER_WORKSPACE_BYTES
+    from edgeexpert_amd._lib import LM_HEAD_WORKSPACE_BYTES, ROUTER_WORKSPACE_BYTES
     from edgeexpert_amd.runtime import DeviceBuffer, Event, Graph, Stream, device_info, synchronize
 
     name, arch = device_info()
@@ -386,7 +386,18 @@ def main():
     lm_gbs = lm_bytes / (lm_us * 1e-6) / 1e9
     log(f"GEMV LM-head shape {Ml}x2816: {lm_us:.1f} us ({lm_gbs:.0f} GB/s, "
         f"{lm_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
-    del big_l, sl_b, bl_b, yl
+    # the greedy decode head over the same rows: RMSNorm folded into the
+    # activation staging, per-block argmax, one-block reduce (2 launches)
+    head = ops.LMHeadGreedyInt4(ctx)
+    tok_b, lm_ws = DeviceBuffer(4), DeviceBuffer(LM_HEAD_WORKSPACE_BYTES)
+    norm_w = DeviceBuffer.from_array(synth.f16_vector(0, "lmhead/norm", 2816, std=0.5))
+    greedy_us = batch_avg_us(lambda i: head.encode_greedy_decode(stream, x0, norm_w, big_l, sl_b, bl_b, tok_b,
+                                                                 2816, Ml, lm_ws), 8, reps_=3)
+    greedy_bytes = Ml * 1408 + 2 * Ml * 88 + 2 * 2816 * 2 + 4
+    greedy_gbs = greedy_bytes / (greedy_us * 1e-6) / 1e9
+    log(f"greedy LM head {Ml}x2816 (norm + rows + argmax, 2 launches): {greedy_us:.1f} us "
+        f"({greedy_gbs:.0f} GB/s, {greedy_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+    del big_l, sl_b, bl_b, yl, lm_ws
 
     # ----------------------------------------- grouped MoE prefill, config 3 ----
     c3 = None if args.no_c3 else bench_c3(ctx, stream, batch_avg_us)
@@ -461,6 +472,9 @@ def main():
                     "frac_of_dense_peak": round(gemm_tflops / 2500.0, 4)},
         "gemv_lmhead": {"shape": [Ml, 2816], "bytes": lm_bytes, "us": round(lm_us, 2),
                         "gbs": round(lm_gbs, 1), "frac": round(lm_gbs / HBM_PEAK_GBS, 4)},
+        "lm_head_greedy": {"shape": [Ml, 2816], "bytes": greedy_bytes, "us": round(greedy_us, 2),
+                           "gbs": round(greedy_gbs, 1), "frac": round(greedy_gbs / HBM_PEAK_GBS, 4),
+                           "kernels": "lm_head_greedy (norm staging + rows + block argmax), lm_head_reduce"},
         "grouped_prefill_c3": c3,
         "decode_layer_c4": c4,
         "wall_s": round(wall, 4),

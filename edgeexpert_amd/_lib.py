@@ -19,6 +19,7 @@ TFQ_E_UNSUPPORTED = 2
 TFQ_E_HIP = 3
 TFQ_E_NOT_LOADED = 4
 ROUTER_WORKSPACE_BYTES = 4096
+LM_HEAD_WORKSPACE_BYTES = 65536
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
 
@@ -94,6 +95,7 @@ SIGNATURES = {
     "tfq_gemv_q4g64_qkv": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
                            _P, _P, _P, _P, _U32, _U32, _U32],
     "tfq_gemv_q8g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32],
+    "tfq_lm_head_greedy": [_P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, C.c_float, _P],
     "tfq_router_topk": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
     "tfq_moe_phase1": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _U32, _U32, _U32],
     "tfq_router_logits": [_P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32],

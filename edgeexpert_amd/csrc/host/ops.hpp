@@ -158,6 +158,57 @@ private:
     const Module& m_;
 };
 
+// S/Kernels/Fusions/LMHeadChainInt4.swift:62-135 (encodeGreedyDecode): the
+// reference's RMSNorm launch is folded into the rows' activation staging;
+// then the int4 rows with a per-block argmax (logit.metal:688-737) and a
+// one-block reduce to the token (logit.metal:740-787).
+class LMHeadGreedyInt4 {
+public:
+    explicit LMHeadGreedyInt4(const Module& m) : m_(m) {}
+
+    int encode(void* stream, const uint16_t* hidden, const uint16_t* norm_weight, const void* weights,
+               const uint16_t* scales, const uint16_t* biases, uint32_t* out_token, uint32_t d, uint32_t vocab,
+               float eps, void* workspace, size_t workspace_bytes) const {
+        if (d == 0 || d % TFQ_GROUP_SIZE != 0)
+            return fail(TFQ_E_INVAL, "d=%u must be a positive multiple of 64", d);
+        if (d > kMaxN) return fail(TFQ_E_UNSUPPORTED, "d=%u exceeds %u", d, kMaxN);
+        if (vocab == 0) return fail(TFQ_E_INVAL, "vocab must be positive");
+        if (!(eps > 0.0f)) return fail(TFQ_E_INVAL, "RMSNorm eps must be positive");
+        if (!hidden || !weights || !scales || !biases || !out_token || !workspace)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(weights, 16)) return fail(TFQ_E_INVAL, "weights are not 16-byte aligned");
+        if (!aligned(hidden, 2) || !aligned(norm_weight, 2) || !aligned(scales, 2) || !aligned(biases, 2))
+            return fail(TFQ_E_INVAL, "hidden/norm/scales/biases are not 2-byte aligned");
+        if (!aligned(out_token, 4) || !aligned(workspace, 8))
+            return fail(TFQ_E_INVAL, "out_token must be 4-byte and workspace 8-byte aligned");
+        if (workspace_bytes < 8) return fail(TFQ_E_INVAL, "workspace too small");
+        Q4Multi mats{};
+        mats.m[0] = {static_cast<const uint8_t*>(weights), scales, biases, nullptr, nullptr, vocab, 0};
+        mats.nmat = 1;
+        mats.total_rows = vocab;
+        mats.norm = NormArg{norm_weight, nullptr, nullptr, eps, kStageNorm};
+        const SegShape sh = seg_shape_fit(d / 32, 2);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_lm_head_greedy_s%u_p%u", sh.seg, sh.p);
+        hipFunction_t fn = m_.get(name);
+        const uint32_t lds = xpairs_lds_bytes(d);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
+        uint32_t grid = grid_for_rows(m_, fn, lds, vocab, rows_per_block);
+        const uint64_t max_blocks = workspace_bytes / 8;
+        if (grid > max_blocks) grid = (uint32_t)max_blocks;      // the row loop covers the rest
+        uint64_t* summaries = static_cast<uint64_t*>(workspace);
+        uint32_t dd = d;
+        void* args[] = {&mats, &hidden, &dd, &summaries};
+        int rc = launch(fn, grid, kBlock, lds, stream, args, name);
+        if (rc) return rc;
+        void* rargs[] = {&summaries, &grid, &out_token};
+        return launch(m_.get("tfq_lm_head_reduce"), 1, kBlock, 0, stream, rargs, "tfq_lm_head_reduce");
+    }
+
+private:
+    const Module& m_;
+};
+
 // S/Kernels/MoE/MoE.swift:31-414: router + routed decode phases.
 class MoE {
 public:

@@ -35,6 +35,8 @@ static std::vector<std::string> kernel_names() {
             names.push_back(std::string("tfq_moe_phase1_routed_") + form + s);
             names.push_back(std::string("tfq_gate_up_act_") + form + s);
         }
+    for (const char* s : q4_shapes) names.push_back(std::string("tfq_lm_head_greedy_") + s);
+    names.push_back("tfq_lm_head_reduce");
     for (const char* s : q8_shapes) {
         names.push_back(std::string("tfq_q8_gemv_") + s);
         names.push_back(std::string("tfq_router_logits_") + s);
@@ -125,7 +127,9 @@ struct tfq_ctx {
     PrefillGroupedRoutedMoE* grouped = nullptr;
     Attention* attn = nullptr;
     DecodeLayer* layer = nullptr;
+    LMHeadGreedyInt4* lmhead = nullptr;
     ~tfq_ctx() {
+        delete lmhead;
         delete layer;
         delete attn;
         delete qmm;
@@ -156,6 +160,7 @@ int tfq_create(tfq_ctx** out, const char* code_object_path) {
         return rc;
     }
     c->int4 = new DequantInt4GEMV(c->module);
+    c->lmhead = new LMHeadGreedyInt4(c->module);
     c->int8 = new DequantInt8GEMV(c->module);
     c->moe = new MoE(c->module);
     c->shared = new SharedExpertInt4(c->module);
@@ -202,6 +207,14 @@ int tfq_gemv_q4g64_qkv(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* q, const
     TFQ_REQUIRE_CTX(ctx);
     if (!q || !k || !v) return fail(TFQ_E_INVAL, "null matrix descriptor");
     return ctx->int4->encode_qkv(stream, *q, *k, *v, x, yq, yk, yv, mq, mkv, n);
+}
+
+int tfq_lm_head_greedy(tfq_ctx* ctx, void* stream, const uint16_t* hidden, const uint16_t* norm_weight,
+                       const void* weights, const uint16_t* scales, const uint16_t* biases, uint32_t* out_token,
+                       uint32_t d, uint32_t vocab, float eps, void* workspace) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->lmhead->encode(stream, hidden, norm_weight, weights, scales, biases, out_token, d, vocab, eps,
+                               workspace, TFQ_LM_HEAD_WORKSPACE_BYTES);
 }
 
 int tfq_gemv_q8g64(tfq_ctx* ctx, void* stream, const uint8_t* weights, const uint16_t* scales,

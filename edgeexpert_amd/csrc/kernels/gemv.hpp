@@ -57,9 +57,13 @@ __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, 
 // staging, which waits for x alone; the weights arrive meanwhile.
 // NORM == false: the staging only copies x (mats.norm is ignored), which
 // keeps the norm inputs' registers out of the kernel and its occupancy up.
-template <int SEG, int P, int R, bool NORM>
-__device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_t* __restrict__ x,
-                                              uint32_t n) {
+// The row loop; out(row, v) receives each row's fp32 result on lane 0 of its
+// segment. STAGE_FIRST: finish staging x before the first weight loads, so
+// the staging's registers are free before the weight registers fill (one
+// memory latency later start, worth it for long launches: higher occupancy).
+template <int SEG, int P, int R, bool NORM, bool STAGE_FIRST = false, typename Out>
+__device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __restrict__ x, uint32_t n,
+                                        Out out) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
     constexpr uint32_t NT = kThreads;
     const uint32_t lane = threadIdx.x & 63u;
@@ -96,8 +100,9 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
     };
     XStage<NT, kStageChunks, NORM> xs;
     xs.load(x, n, mats.norm);
-    issue(0);
+    if (!STAGE_FIRST) issue(0);
     const XPairs xp = xs.pairs(x, lds_xh, n, mats.norm);
+    if (STAGE_FIRST) issue(0);
 
     for (uint32_t grp = 0; seg_id + grp * R * seg_total < total; ++grp) {
         float acc[R];
@@ -121,12 +126,19 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
         for (int r = 0; r < R; ++r) {
             const float v = seg_sum<SEG>(acc[r]);
             const uint32_t row = seg_id + (grp * R + r) * seg_total;
-            if (sl == 0 && row < total) {
-                const Q4Row q = resolve_row(mats, row, row_bytes, ngroups);
-                *q.y = f2h(q.r ? h2f(*q.r) + v : v);
-            }
+            if (sl == 0 && row < total) out(row, v);
         }
     }
+}
+
+template <int SEG, int P, int R, bool NORM>
+__device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_t* __restrict__ x,
+                                              uint32_t n) {
+    const uint32_t row_bytes = n >> 1, ngroups = n >> 6;
+    q4_rows<SEG, P, R, NORM>(mats, x, n, [&](uint32_t row, float v) {
+        const Q4Row q = resolve_row(mats, row, row_bytes, ngroups);
+        *q.y = f2h(q.r ? h2f(*q.r) + v : v);
+    });
 }
 
 // ---------------------------------------------------------------- int8 ----
@@ -308,6 +320,61 @@ __device__ __forceinline__ uint64_t topk_key(float v, uint32_t t) {
     const uint32_t b = __builtin_bit_cast(uint32_t, v);
     const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((uint64_t)o << 32) | (uint32_t)(0xFFFFFFFFu - t);
+}
+
+// Greedy int4 LM head, rows stage (logit.metal:688-737): z = W·x for every
+// vocab row, x the RMSNorm of the hidden state staged like every GEMV input
+// (fp16, as the reference's xNormed buffer); each block writes the largest
+// finite z of its rows with the lowest row on ties as a topk_key
+// (0 = no finite z) to summaries[blockIdx.x].
+template <int SEG, int P, int R>
+__device__ __forceinline__ void lm_head_greedy_rows(const Q4Multi& mats, const uint16_t* __restrict__ x,
+                                                    uint32_t n, uint64_t* __restrict__ summaries) {
+    // a lane's rows arrive in increasing order, so a strict > keeps the lowest
+    // row among equal values (and -0 vs +0, which compare equal)
+    float best_v = -__builtin_inff();
+    uint32_t best_row = 0xFFFFFFFFu;
+    q4_rows<SEG, P, R, true, true>(mats, x, n, [&](uint32_t row, float v) {
+        if (__builtin_isfinite(v) && (best_row == 0xFFFFFFFFu || v > best_v)) {
+            best_v = v;
+            best_row = row;
+        }
+    });
+    uint64_t best = best_row == 0xFFFFFFFFu ? 0ull : topk_key(best_v == 0.0f ? 0.0f : best_v, best_row);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint64_t other = __shfl_xor(best, o, kWave);
+        best = other > best ? other : best;
+    }
+    __shared__ uint64_t wave_best[kThreads / 64];
+    if ((threadIdx.x & 63u) == 0) wave_best[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = wave_best[0];
+        for (uint32_t w = 1; w < kThreads / 64; ++w) b = wave_best[w] > b ? wave_best[w] : b;
+        summaries[blockIdx.x] = b;
+    }
+}
+
+// Greedy int4 LM head, reduce stage (logit.metal:740-787): the token of the
+// largest key over n block summaries, 0 when none holds a finite z.
+__device__ __forceinline__ void lm_head_greedy_reduce(const uint64_t* __restrict__ summaries, uint32_t n,
+                                                      uint32_t* __restrict__ out_token) {
+    uint64_t best = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += kThreads) best = summaries[i] > best ? summaries[i] : best;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint64_t other = __shfl_xor(best, o, kWave);
+        best = other > best ? other : best;
+    }
+    __shared__ uint64_t wave_best[kThreads / 64];
+    if ((threadIdx.x & 63u) == 0) wave_best[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = wave_best[0];
+        for (uint32_t w = 1; w < kThreads / 64; ++w) b = wave_best[w] > b ? wave_best[w] : b;
+        *out_token = b ? ~(uint32_t)b : 0u;      // the key's low word is ~row
+    }
 }
 
 // Top-k of E <= 256 logits by (value desc, index asc), in parallel: the

@@ -99,6 +99,12 @@ constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
         moe_phase2<P, kRowsInFlight>(pool, indices, acts, rw, residual, y, D, F, top_k);          \
     }
 
+#define TFQ_LM_HEAD(SEG, P)                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void tfq_lm_head_greedy_s##SEG##_p##P(          \
+        Q4Multi mats, const uint16_t* x, uint32_t n, uint64_t* summaries) {                      \
+        lm_head_greedy_rows<SEG, P, kRowsInFlight>(mats, x, n, summaries);                       \
+    }
+
 #define TFQ_GATE_UP_FORM(NAME, NORM, SEG, P)                                                     \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         Q4Mat gate, Q4Mat up, const uint16_t* x, uint16_t* act, uint32_t D, uint32_t F,          \
@@ -120,6 +126,7 @@ TFQ_Q4_TABLE(TFQ_Q4_GEMV)
 TFQ_Q4_TABLE(TFQ_PHASE1)
 TFQ_Q4_TABLE(TFQ_PHASE1_ROUTED)
 TFQ_Q4_TABLE(TFQ_GATE_UP)
+TFQ_Q4_TABLE(TFQ_LM_HEAD)
 TFQ_Q8_TABLE(TFQ_Q8_GEMV)
 TFQ_Q8_TABLE(TFQ_ROUTER)
 TFQ_Q8_TABLE(TFQ_PREFILL_ROUTER)
@@ -146,6 +153,11 @@ extern "C" __global__ __launch_bounds__(kProjThreads) void tfq_gemm_q4_bf16(
     const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
     uint32_t M, uint32_t N, uint32_t K) {
     gemm_q4_proj<true>(X, W, S, B, Y, M, N, K);
+}
+
+extern "C" __global__ __launch_bounds__(256) void tfq_lm_head_reduce(const uint64_t* summaries, uint32_t n,
+                                                                     uint32_t* out_token) {
+    lm_head_greedy_reduce(summaries, n, out_token);
 }
 
 extern "C" __global__ __launch_bounds__(256) void tfq_router_select(const float* logits,

@@ -221,6 +221,20 @@ class Router:
                           _addr(self.effective_scale), _addr(self.per_expert_scale), self.num_experts)
 
 
+class LMHeadGreedyInt4:
+    """S/Kernels/Fusions/LMHeadChainInt4.swift:5-136 (encodeGreedyDecode)."""
+
+    def __init__(self, context: Context):
+        self.ctx = context
+
+    def encode_greedy_decode(self, stream, hidden, norm_weight, weights, scales, biases, out_token, d,
+                             vocab, workspace, rms_eps=1e-6, hidden_offset=0, out_token_offset=0):
+        check(lib().tfq_lm_head_greedy(self.ctx.handle, _s(stream), _addr(hidden, hidden_offset),
+                                       _addr(norm_weight), _addr(weights), _addr(scales), _addr(biases),
+                                       _addr(out_token, out_token_offset), d, vocab, rms_eps,
+                                       _addr(workspace)), "LMHeadChainInt4.encodeGreedyDecode")
+
+
 def moe_decode_token(context: Context, stream, router: Router, pool: ExpertPool, x, residual, y, d,
                      f, top_k, out_indices, out_weights, acts, workspace):
     """Router -> top-k -> phase 1 -> phase 2 for one token, indices kept on the device."""

@@ -98,6 +98,26 @@ int tfq_gemv_q8g64(tfq_ctx *ctx, void *stream, const uint8_t *weights, const uin
  * out_logits_f32 is NULL). */
 #define TFQ_ROUTER_WORKSPACE_BYTES 4096u
 
+/* Bytes of workspace tfq_lm_head_greedy needs (per-block argmax summaries). */
+#define TFQ_LM_HEAD_WORKSPACE_BYTES 65536u
+
+/* Greedy decode head: out_token[0] = the vocab row with the largest finite
+ * z = W·f16(rmsnorm(hidden, norm_weight)) (z in fp32; W int4 g64
+ * [vocab][d]), the lowest row among equal z (-0 equals +0), 0 when no z is
+ * finite. norm_weight may be NULL (no scale). Two launches on `stream`: the
+ * rows with the RMSNorm folded into their activation staging and a
+ * per-block argmax, then a one-block reduce. Replaces
+ * LMHeadChainInt4.encodeGreedyDecode
+ * (S/Kernels/Fusions/LMHeadChainInt4.swift:62-135; kernels
+ * S/Metal/Sampling/logit.metal:688-787; its separate RMSNorm launch is
+ * folded in). Contract: d % 64 == 0, d <= 8192, vocab >= 1, eps > 0,
+ * weights 16-byte aligned, out_token 4-byte aligned, workspace
+ * TFQ_LM_HEAD_WORKSPACE_BYTES bytes, 8-byte aligned. */
+int tfq_lm_head_greedy(tfq_ctx *ctx, void *stream, const uint16_t *hidden,
+                       const uint16_t *norm_weight, const void *weights, const uint16_t *scales,
+                       const uint16_t *biases, uint32_t *out_token, uint32_t d, uint32_t vocab,
+                       float eps, void *workspace);
+
 /* Router GEMV, then top-k + softmax over the k + per-expert gain (two
  * launches on `stream`: a many-block int8 GEMV and a one-wavefront select).
  * logits[e] = Σ_g s·Σ q·(h⊙eff) + b·Σ(h⊙eff) (fp32); indices sorted by

@@ -136,6 +136,8 @@ def _declare(L):
     d("tfo_gemm_int4", None, _P, _P, _P, C.c_int, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int,
       C.c_int)
     d("tfo_rmsnorm", None, _P, _P, C.c_int, C.c_float, _P)
+    d("tfo_greedy_argmax", C.c_uint32, _P, C.c_int)
+    d("tfo_lm_head_greedy", C.c_uint32, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_float, _P)
     d("tfo_rope_neox", None, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float)
     d("tfo_attention", None, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _P)
     d("tfo_decode_layer", None, C.POINTER(LayerWeights), C.POINTER(LayerShape), _P, _P, _P, C.c_int,
@@ -384,6 +386,22 @@ def rmsnorm(x, w, eps):
     y = np.zeros_like(x)
     lib().tfo_rmsnorm(_ptr(x), _ptr(wv), x.size, eps, _ptr(y))
     return y
+
+
+def greedy_argmax(z) -> int:
+    """logit.metal:706-784: largest finite value, lowest index on ties, 0 if none finite."""
+    z = _c(z, np.float32)
+    return int(lib().tfo_greedy_argmax(_ptr(z), z.size))
+
+
+def lm_head_greedy(hidden_f16, norm_w_f16, W, S, B, eps=1e-6, fmt=FMT_F16):
+    """LMHeadChainInt4.encodeGreedyDecode (LMHeadChainInt4.swift:62-135): (token, z)."""
+    h = _c(hidden_f16, np.uint16); w = None if norm_w_f16 is None else _c(norm_w_f16, np.uint16)
+    W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16)
+    vocab, d = W.shape[0], h.size
+    z = np.zeros(vocab, np.float32)
+    tok = lib().tfo_lm_head_greedy(_ptr(h), _ptr(w), _ptr(W), _ptr(S), _ptr(B), fmt, d, vocab, eps, _ptr(z))
+    return int(tok), z
 
 
 def rope_neox(x, num_heads, head_dim, rotated_pairs, position, theta):

@@ -634,6 +634,45 @@ void tfo_rmsnorm(const float *x, const float *w, int n, float eps, float *y) {
     }
 }
 
+/* logit.metal:706-716 (finite rows only), 758-763 / 743-746 (larger value,
+ * then lower index), 784 (no finite value -> token 0). */
+uint32_t tfo_greedy_argmax(const float *z, int n) {
+    uint32_t best_i = 0xFFFFFFFFu;
+    float best_v = -INFINITY;
+    for (int i = 0; i < n; ++i) {
+        if (!isfinite(z[i])) continue;
+        if (best_i == 0xFFFFFFFFu || z[i] > best_v) {
+            best_v = z[i];
+            best_i = (uint32_t)i;
+        }
+    }
+    return best_i == 0xFFFFFFFFu ? 0u : best_i;
+}
+
+/* LMHeadChainInt4.swift:105-134: RMSNorm into a half buffer, then the
+ * int4 rows and the greedy reduction. */
+uint32_t tfo_lm_head_greedy(const uint16_t *hidden_f16, const uint16_t *norm_w_f16, const uint8_t *W,
+                            const uint16_t *S, const uint16_t *B, int fmt, int d, int vocab,
+                            float eps, float *z) {
+    float *h = (float *)calloc((size_t)d, sizeof(float));
+    float *w = (float *)calloc((size_t)d, sizeof(float));
+    float *x = (float *)calloc((size_t)d, sizeof(float));
+    float *zz = z ? z : (float *)malloc(sizeof(float) * (size_t)vocab);
+    for (int i = 0; i < d; ++i) {
+        h[i] = tfo_f16_to_f32(hidden_f16[i]);
+        w[i] = norm_w_f16 ? tfo_f16_to_f32(norm_w_f16[i]) : 1.0f;
+    }
+    tfo_rmsnorm(h, norm_w_f16 ? w : NULL, d, eps, x);
+    for (int i = 0; i < d; ++i) x[i] = tfo_f16_to_f32(tfo_f32_to_f16(x[i]));
+    tfo_gemv_int4(W, S, B, fmt, x, vocab, d, zz);
+    const uint32_t token = tfo_greedy_argmax(zz, vocab);
+    if (!z) free(zz);
+    free(h);
+    free(w);
+    free(x);
+    return token;
+}
+
 /* RoPE.swift:70-110 (applyNeox). */
 void tfo_rope_neox(float *x, int num_heads, int head_dim, int rotated_pairs, int position,
                    float theta) {

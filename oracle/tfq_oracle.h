@@ -173,6 +173,19 @@ void tfo_gemm_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int s
  *   y[i] = x[i] * w[i] * 1/sqrt(Σx²/n + eps); w == NULL: no scale (the
  *   rmsnorm_no_scale form of S/Metal/Fusions/fused.metal:86-180). */
 void tfo_rmsnorm(const float *x, const float *w, int n, float eps, float *y);
+/* ---- greedy int4 LM head (S/Metal/Sampling/logit.metal:688-787,
+ * S/Kernels/Fusions/LMHeadChainInt4.swift:62-135) ----
+ * tfo_greedy_argmax: the index of the largest finite z[i], the lowest index
+ * among equal values (logit.metal:713-716,758-763); 0 when no z is finite
+ * (logit.metal:784). tfo_lm_head_greedy: normed = f16(rmsnorm(hidden,
+ * norm_w)) (the reference's half xNormed buffer; norm_w NULL: no scale),
+ * z = tfo_gemv_int4 rows
+ * over it, token = tfo_greedy_argmax(z); z (may be NULL) receives the
+ * vocab logits. */
+uint32_t tfo_greedy_argmax(const float *z, int n);
+uint32_t tfo_lm_head_greedy(const uint16_t *hidden_f16, const uint16_t *norm_w_f16, const uint8_t *W,
+                            const uint16_t *S, const uint16_t *B, int scale_fmt, int d, int vocab,
+                            float eps, float *z);
 /* RopeRef.applyNeox (V/Reference/Attention/RoPE.swift:70-110), in place over
  * num_heads heads: pairs (i, i + head_dim/2), i < rotated_pairs, rotated by
  * position * theta^(-2i/head_dim). The angle and its cos/sin are evaluated

@@ -433,3 +433,62 @@ def test_rel_error_definition():
     # V/Tolerance/RelError.swift:7-16
     assert oracle.rel_error([1.0, 2.0], [1.0, 2.5]) == pytest.approx(0.2)
     assert oracle.rel_error([1e-9], [0.0]) == pytest.approx(1e-3)
+
+
+# ------------------------------------------------ greedy LM head (argmax) ----
+# logit.metal:706-787: the largest finite row value wins, the lowest row among
+# equal values (v == best, so -0 ties with +0), token 0 when nothing is finite.
+
+def _argmax_brute(z):
+    best, best_i = None, None
+    for i, v in enumerate(z):
+        if not math.isfinite(v):
+            continue
+        if best is None or v > best:
+            best, best_i = v, i
+    return 0 if best_i is None else best_i
+
+
+def test_greedy_argmax_brute_force_with_nonfinite_and_ties():
+    rng = np.random.default_rng(7)
+    for trial in range(300):
+        n = int(rng.integers(1, 40))
+        z = rng.integers(-3, 4, n).astype(np.float32)       # many exact ties
+        for _ in range(int(rng.integers(0, 4))):
+            z[int(rng.integers(0, n))] = rng.choice([np.nan, np.inf, -np.inf])
+        assert oracle.greedy_argmax(z) == _argmax_brute(z), z
+
+
+def test_greedy_argmax_special_cases():
+    assert oracle.greedy_argmax(np.array([np.nan, np.inf, -np.inf], np.float32)) == 0
+    assert oracle.greedy_argmax(np.array([-np.inf, 5.0, np.nan, 5.0], np.float32)) == 1
+    assert oracle.greedy_argmax(np.array([1.0, -0.0, 0.0, -1.0], np.float32)) == 0
+    assert oracle.greedy_argmax(np.array([-2.0, -0.0, 0.0, -1.0], np.float32)) == 1   # -0 == +0
+    assert oracle.greedy_argmax(np.array([-3.0e38, -1.0e38], np.float32)) == 1
+    # numpy's first-occurrence argmax over the finite values
+    z = np.random.default_rng(8).standard_normal(10000).astype(np.float32)
+    z[::97] = np.nan
+    assert oracle.greedy_argmax(z) == int(np.argmax(np.where(np.isfinite(z), z, -np.inf)))
+
+
+def test_lm_head_greedy_is_norm_then_rows_then_argmax():
+    d, vocab = 256, 777
+    W, S, B = synth.int4_matrix(3, "pin/lmhead", vocab, d)
+    h16 = synth.f16_vector(3, "pin/lmhead/h", d)
+    w16 = synth.f16_vector(3, "pin/lmhead/w", d, std=0.5)
+    tok, z = oracle.lm_head_greedy(h16, w16, W, S, B, eps=1e-6)
+    # independent numpy: RMSNorm (float64 sum of squares, as RmsNorm.swift), fp16 rounding,
+    # then the dequantised rows in float64
+    h = h16.view(np.float16).astype(np.float32)
+    w = w16.view(np.float16).astype(np.float32)
+    inv = np.float32(1.0) / np.sqrt(np.float32(np.sum(h.astype(np.float64) ** 2) / d) + np.float32(1e-6))
+    x = ((h * w) * inv).astype(np.float16).astype(np.float64)
+    z64 = dequant_int4_np(W, S, B).astype(np.float64) @ x
+    assert np.max(np.abs(z - z64)) <= 1e-5 * max(1.0, np.max(np.abs(z64)))
+    order = np.argsort(-z64)
+    assert z64[order[0]] - z64[order[1]] > 1e-3             # no near tie at this seed
+    assert tok == int(order[0])
+    # no scale: the same rows over the unweighted norm
+    tok0, z0 = oracle.lm_head_greedy(h16, None, W, S, B)
+    x0 = (h * inv).astype(np.float16).astype(np.float64)
+    assert tok0 == int(np.argmax(dequant_int4_np(W, S, B).astype(np.float64) @ x0))
