@@ -20,8 +20,12 @@ constexpr uint32_t kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
 constexpr uint32_t kProjBM = 64;           // projection GEMM tile: tokens (gemm.hpp kProjBM)
 constexpr uint32_t kProjBN = 256;          // outputs (gemm.hpp kProjBN)
 constexpr uint32_t kProjThreads = 256;     // threads (gemm.hpp kProjThreads)
+constexpr uint32_t kProjGemmThreads = 512; // threads of the prefill GEMM's tile (gemm.hpp kProjGemmThreads)
 constexpr uint32_t kProjMaxK = 8192;       // longest reduction (gemm.hpp kProjMaxK)
 constexpr uint32_t proj_lds_bytes(uint32_t k) { return 2u * kProjBM * 72u * 2u + 2u * kProjBN * (k / 64u) * 2u; }
+// the pipelined tile of the prefill GEMM (gemm.hpp proj_pl_lds_bytes)
+constexpr uint32_t proj_pl_lds_bytes(uint32_t k) { return 3u * kProjBM * 72u * 2u + 4u * kProjBN * (k / 64u); }
+static_assert(proj_pl_lds_bytes(kProjMaxK) <= 160u * 1024u, "pipelined tile exceeds the LDS of a CU");
 
 // Grid of a row-loop kernel (blocks of kBlock threads, `lds` dynamic LDS
 // bytes): one block per rows_per_block rows, but no more blocks than the GPU
@@ -442,9 +446,9 @@ public:
         // slice are dispatched to the same XCD (and its L2)
         if (k > kProjMaxK) return fail(TFQ_E_UNSUPPORTED, "k=%u exceeds %u", k, kProjMaxK);
         const uint32_t gx = (n + kProjBN - 1) / kProjBN, gy = (t + kProjBM - 1) / kProjBM;
-        const uint32_t lds = proj_lds_bytes(k);
+        const uint32_t lds = proj_pl_lds_bytes(k);
         void* args[] = {&x, &weights, &scales, &biases, &y, &t, &n, &k};
-        return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, kProjThreads, 1, 1, lds, (hipStream_t)stream,
+        return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, kProjGemmThreads, 1, 1, lds, (hipStream_t)stream,
                                                args, nullptr),
                          name);
     }

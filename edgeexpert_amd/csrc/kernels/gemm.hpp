@@ -124,6 +124,7 @@ __device__ __forceinline__ void copy_pair_to_lds(const uint16_t* __restrict__ a,
 constexpr uint32_t kProjBM = 64;
 constexpr uint32_t kProjBN = 256;
 constexpr uint32_t kProjThreads = 256;
+constexpr uint32_t kProjGemmThreads = 512;   // the prefill GEMM's eight-wave tile
 constexpr uint32_t kProjDepth = 4;          // weight groups in flight per wave (register ring)
 constexpr uint32_t kProjXDepth = 2;         // activation groups in flight (mostly L2 hits)
 constexpr uint32_t kProjMaxK = 8192;        // scale/bias LDS: 2 x 256 x K/64 halves
@@ -170,13 +171,14 @@ struct ProjLanes {
 };
 
 // The K loop of the projection tile (all 256 threads): acc[i][j] receives the
-// 32x32 product of token sub-tile i (rows 32i.. of the block's 64) and the
-// wave's output sub-tile j. lds: the tile's dynamic LDS (X double buffer,
+// 32x32 product of token sub-tile i (rows 32i.. of the block's 64; MI = 1:
+// only the first 32 rows, half the MFMAs and activation reads, for blocks
+// with at most 32 valid rows) and the wave's output sub-tile j. lds: the tile's dynamic LDS (X double buffer,
 // then the s/b table, filled by the caller before the call and synchronised
 // by the first barrier inside); xp: this thread's activation row (token row
 // tid/4 of the block, already clamped to a valid row) + 16·(tid%4) halves.
-template <bool X_BF16>
-__device__ __forceinline__ void proj_core(f32x16 (&acc)[2][2], _Float16* lds, const uint16_t* s_lds,
+template <bool X_BF16, int MI = 2>
+__device__ __forceinline__ void proj_core(f32x16 (&acc)[MI][2], _Float16* lds, const uint16_t* s_lds,
                                           const uint16_t* b_lds, const ProjLanes& pl,
                                           const uint16_t* __restrict__ xp, uint32_t G) {
     _Float16* xs0 = lds;
@@ -216,7 +218,7 @@ __device__ __forceinline__ void proj_core(f32x16 (&acc)[2][2], _Float16* lds, co
     };
 
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -240,16 +242,16 @@ __device__ __forceinline__ void proj_core(f32x16 (&acc)[2][2], _Float16* lds, co
         constexpr int P = ST & 1;
         constexpr int XS = (ST + 1) % kProjXDepth;
         const _Float16* cur = P ? xs1 : xs0;
-        h8 a[2][4];
+        h8 a[MI][4];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < MI; ++i)
                 a[i][s] = *reinterpret_cast<const h8*>(&cur[(32u * i + col) * kGemmLdsStride + 32u * h + 8u * s]);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][s], bw[P][j][s], acc[i][j], 0, 0, 0);
@@ -259,7 +261,7 @@ __device__ __forceinline__ void proj_core(f32x16 (&acc)[2][2], _Float16* lds, co
         load_x(g + 3, std::integral_constant<int, XS>{});
         // interleave: each MFMA followed by a share of the VALU work
 #pragma unroll
-        for (int m = 0; m < 16; ++m) {
+        for (int m = 0; m < 8 * MI; ++m) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);    // VALU
         }
@@ -290,33 +292,263 @@ __device__ __forceinline__ void proj_core(f32x16 (&acc)[2][2], _Float16* lds, co
     if (g + 2 < G) step(g + 2, std::integral_constant<int, 2>{});
 }
 
+// ------------------------------------------- pipelined projection tile ----
+//
+// The same tile with every LDS round trip taken off the group's critical
+// path: three activation buffers, so that a group's A operands are read
+// into registers one step before its MFMAs, and a scale/bias table of one
+// word per (row, group) (scale | bias << 16) read two groups ahead. The only
+// wait left in a step is its closing barrier, by which time the step's own
+// LDS traffic has long completed. Step g: read A(g+1) and the scale/bias
+// words of group g+2, run the 16 MFMAs of group g interleaved with the
+// dequantisation of group g+1 (its B operands), stage the activations of
+// group g+2, refill the rings, barrier.
+
+// Dynamic LDS of the pipelined tile: three activation buffers, then the
+// scale/bias table (kProjBN rows x K/64 words).
+constexpr uint32_t proj_pl_lds_bytes(uint32_t K) {
+    return 3u * kProjBM * kGemmLdsStride * 2u + 4u * kProjBN * (K / 64u);
+}
+
+// dst[i] = a[i] | b[i] << 16 for i < count, into LDS (16-byte loads and
+// stores when the sources are 16-byte aligned and count % 8 == 0).
+template <uint32_t NT>
+__device__ __forceinline__ void copy_sb_to_lds(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+                                               uint32_t* __restrict__ dst, uint32_t count) {
+    constexpr uint32_t U = 8;
+    if (((((uintptr_t)a) | ((uintptr_t)b)) & 15u) == 0 && (count & 7u) == 0) {
+        const uint32_t n16 = count >> 3;
+        const uint4* sa = reinterpret_cast<const uint4*>(a);
+        const uint4* sbp = reinterpret_cast<const uint4*>(b);
+        uint4* t = reinterpret_cast<uint4*>(dst);
+        for (uint32_t base = 0; base < n16; base += U * NT) {
+            uint4 va[U], vb[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const uint32_t i = base + u * NT + threadIdx.x;
+                const uint32_t c = i < n16 ? i : n16 - 1;
+                va[u] = sa[c];
+                vb[u] = sbp[c];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const uint32_t i = base + u * NT + threadIdx.x;
+                if (i < n16) {
+                    // v_perm: bytes 0-3 from the second operand, 4-7 from the first
+                    t[2 * i] = make_uint4(__builtin_amdgcn_perm(vb[u].x, va[u].x, 0x05040100u),
+                                          __builtin_amdgcn_perm(vb[u].x, va[u].x, 0x07060302u),
+                                          __builtin_amdgcn_perm(vb[u].y, va[u].y, 0x05040100u),
+                                          __builtin_amdgcn_perm(vb[u].y, va[u].y, 0x07060302u));
+                    t[2 * i + 1] = make_uint4(__builtin_amdgcn_perm(vb[u].z, va[u].z, 0x05040100u),
+                                              __builtin_amdgcn_perm(vb[u].z, va[u].z, 0x07060302u),
+                                              __builtin_amdgcn_perm(vb[u].w, va[u].w, 0x05040100u),
+                                              __builtin_amdgcn_perm(vb[u].w, va[u].w, 0x07060302u));
+                }
+            }
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < count; i += NT) dst[i] = (uint32_t)a[i] | ((uint32_t)b[i] << 16);
+    }
+}
+
+// dequant_chunk_f16_v with the scale and bias taken from one table word.
+__device__ __forceinline__ void dequant_chunk_sb(uint4 w, uint32_t sb, uint32_t magic_v, h8 (&out)[4]) {
+    const h2 s2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x01000100u));
+    const h2 b2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x03020302u));
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        h8 run;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = ((ws[j] >> (4 * i)) & 0x000F000Fu) | magic_v;
+            const h2 qh = __builtin_bit_cast(h2, q) - k1024;             // exact q pair
+            const h2 wv = __builtin_elementwise_fma(qh, s2, b2);         // one rounding
+            run[2 * i] = wv[0];
+            run[2 * i + 1] = wv[1];
+        }
+        out[j] = run;
+    }
+}
+
+// The K loop of the pipelined tile. J = 32-output sub-tiles per wave: J = 2
+// is the four-wave tile of proj_core; J = 1 runs eight waves (two per SIMD,
+// so one wave's MFMAs overlap another's dequantisation and staging; a
+// single wave does not overlap its own). With J = 1 a wave keeps two
+// accumulator sets per token sub-tile (even and odd k-steps, summed at the
+// end): a 32x32 MFMA chain on one accumulator issues at half rate, four
+// independent chains per wave keep the matrix core busy; its A operands are
+// then read at the start of each step (the other wave on the SIMD covers
+// that wait) to stay within 256 registers. acc[i][j]: token sub-tile i, the
+// wave's output sub-tile j; pl.wp0/sidx0 (and wp1/sidx1 for J = 2) index
+// sb_lds (filled by the caller before the call and published by the first
+// barrier inside); xp: this thread's activation row (token row
+// tid / (64/XH) of the block, clamped to a valid row) + XH·(tid % (64/XH))
+// halves, XH = halves it stages per group. lds: the three activation buffers.
+template <bool X_BF16, int J>
+__device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds, const uint32_t* sb_lds,
+                                             const ProjLanes& pl, const uint16_t* __restrict__ xp, uint32_t G) {
+    constexpr uint32_t T = kProjBM * kGemmLdsStride;         // halves per activation buffer
+    constexpr uint32_t NT = 64u * (8u / J);                  // threads of the block
+    constexpr uint32_t XH = kProjBM * 64u / NT;              // activation halves staged per thread (16 or 8)
+    constexpr uint32_t XV = XH / 8u;                         // of them, 16-byte pieces
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t h = lane >> 5, col = lane & 31u;
+    const uint32_t xrow = tid / (64u / XH), xq = tid % (64u / XH);
+    uint32_t magic_v;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_v));
+
+    constexpr int KS = J == 1 ? 2 : 1;                        // accumulator sets (k-step parity)
+    constexpr int AB = J == 1 ? 1 : 2;                        // A-operand buffers
+    uint4 wr[J][kProjDepth], xr[2][XV];
+    h8 a[AB][2][4];         // [group parity][token sub-tile][k-step]
+    f32x16 accs[2][J][KS];
+    h8 bw[2][J][4];         // [group parity][output sub-tile][k-step]
+    uint32_t sbw[2][J];     // [group parity][output sub-tile]
+    auto load_w = [&](uint32_t g, auto st_c) {
+        constexpr int ST = decltype(st_c)::value;
+        const uint32_t gg = g < G ? g : G - 1;
+        wr[0][ST] = ldg16(pl.wp0 + 32u * gg);
+        if constexpr (J == 2) wr[J - 1][ST] = ldg16(pl.wp1 + 32u * gg);
+    };
+    auto load_x = [&](uint32_t g, auto sl_c) {
+        constexpr int SL = decltype(sl_c)::value;
+        const uint32_t gg = g < G ? g : G - 1;
+#pragma unroll
+        for (uint32_t v = 0; v < XV; ++v) xr[SL][v] = ldg16_global(xp + 64u * gg + 8u * v);
+    };
+    auto buf = [&](uint32_t g) { return lds + (g % 3u) * T; };
+    auto store_x = [&](const uint4 (&v)[XV], _Float16* dst) {
+#pragma unroll
+        for (uint32_t u = 0; u < XV; ++u) {
+            const h8 hv = X_BF16 ? bf16x8_to_f16(v[u]) : __builtin_bit_cast(h8, v[u]);
+            *reinterpret_cast<h8*>(&dst[xrow * kGemmLdsStride + XH * xq + 8u * u]) = perm_0415(hv);
+        }
+    };
+    auto read_a = [&](const _Float16* src, h8 (&dst)[2][4]) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                dst[i][s] = *reinterpret_cast<const h8*>(&src[(32u * i + col) * kGemmLdsStride + 32u * h + 8u * s]);
+    };
+    auto read_sb = [&](uint32_t g, uint32_t (&dst)[J]) {
+        const uint32_t gg = g < G ? g : G - 1;
+        dst[0] = sb_lds[pl.sidx0 + gg];
+        if constexpr (J == 2) dst[J - 1] = sb_lds[pl.sidx1 + gg];
+    };
+    auto dequant = [&](int st, const uint32_t (&sw)[J], h8 (&dst)[J][4]) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) dequant_chunk_sb(wr[j][st], sw[j], magic_v, dst[j]);
+    };
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) accs[i][j][k][r] = 0.0f;
+
+    // Step g (compile-time weight-ring stage ST = g % kProjDepth, parity P =
+    // ST & 1; the activation ring slot of group g + 2 is P as well).
+    auto step = [&](uint32_t g, auto st_c) {
+        constexpr int ST = decltype(st_c)::value;
+        constexpr int NW = (ST + 1) % kProjDepth;
+        constexpr int P = ST & 1;
+        constexpr int PA = AB == 2 ? P : 0;
+        if constexpr (AB == 2) read_a(buf(g + 1), a[P ^ 1]);
+        else read_a(buf(g), a[0]);
+        read_sb(g + 2, sbw[P]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+                    accs[i][j][s % KS] =
+                        __builtin_amdgcn_mfma_f32_32x32x16_f16(a[PA][i][s], bw[P][j][s], accs[i][j][s % KS], 0, 0, 0);
+        dequant(NW, sbw[P ^ 1], bw[P ^ 1]);
+        store_x(xr[P], buf(g + 2));
+        load_w(g + kProjDepth, st_c);
+        load_x(g + 4, std::integral_constant<int, P>{});
+        __builtin_amdgcn_sched_group_barrier(0x100, 8 + J, 0);    // LDS reads first
+#pragma unroll
+        for (int m = 0; m < 8 * J; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);     // VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+    };
+    load_x(0, std::integral_constant<int, 0>{});
+    load_x(1, std::integral_constant<int, 1>{});
+    load_w(0, std::integral_constant<int, 0>{});
+    load_w(1, std::integral_constant<int, 1>{});
+    load_w(2, std::integral_constant<int, 2>{});
+    load_w(3, std::integral_constant<int, 3>{});
+    store_x(xr[0], buf(0));
+    store_x(xr[1], buf(1));
+    load_x(2, std::integral_constant<int, 0>{});
+    load_x(3, std::integral_constant<int, 1>{});
+    __syncthreads();                 // scale/bias table and the first two activation groups
+    read_sb(0, sbw[0]);
+    read_sb(1, sbw[1]);
+    if constexpr (AB == 2) read_a(buf(0), a[0]);
+    dequant(0, sbw[0], bw[0]);
+    // no LDS read may be pending at the loop head, or the wait analysis keeps
+    // waiting for the prologue's reads in every iteration (lgkmcnt(0))
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    uint32_t g = 0;
+    for (; g + kProjDepth <= G; g += kProjDepth) {
+        step(g, std::integral_constant<int, 0>{});
+        step(g + 1, std::integral_constant<int, 1>{});
+        step(g + 2, std::integral_constant<int, 2>{});
+        step(g + 3, std::integral_constant<int, 3>{});
+    }
+    if (g < G) step(g, std::integral_constant<int, 0>{});
+    if (g + 1 < G) step(g + 1, std::integral_constant<int, 1>{});
+    if (g + 2 < G) step(g + 2, std::integral_constant<int, 2>{});
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            acc[i][j] = accs[i][j][0];
+#pragma unroll
+            for (int k = 1; k < KS; ++k) acc[i][j] += accs[i][j][k];
+        }
+}
+
 // Calls fn(m, n, v) for every element of the tile held by this lane:
-// m = token row in the block (0..63), n = output in the block (wave's
-// 64-output slice), per the 32x32 MFMA D layout (column = lane % 32,
+// m = token row in the block (0..63), n = output in the block (the wave's
+// 32·J-output slice), per the 32x32 MFMA D layout (column = lane % 32,
 // row = 8*(r/4) + 4*(lane/32) + r%4).
-template <typename Fn>
-__device__ __forceinline__ void proj_for_each(const f32x16 (&acc)[2][2], Fn fn) {
+template <int J, int MI, typename Fn>
+__device__ __forceinline__ void proj_for_each(const f32x16 (&acc)[MI][J], Fn fn) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-                fn(32u * i + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3), 64u * wave + 32u * j + (lane & 31u),
+                fn(32u * i + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3), 32u * J * wave + 32u * j + (lane & 31u),
                    acc[i][j][r]);
 }
 
-// Lanes of wave `wave` over the outputs n_base + 64·wave' + 32j + lane%32 of a
-// matrix with `nrows` outputs (clamped to the last one), K/2-byte rows, the
-// table rows of those outputs starting at table_base.
+// Lanes of a wave over the outputs n_base + 32·J·wave_in_mat + 32j + lane%32
+// (j < J) of a matrix with `nrows` outputs (clamped to the last one), K/2-byte
+// rows, the table rows of those outputs starting at table_base.
+template <int J>
 __device__ __forceinline__ ProjLanes proj_lanes(const uint8_t* W, uint32_t row_bytes, uint32_t n_base,
                                                 uint32_t wave_in_mat, uint32_t nrows, uint32_t table_base,
                                                 uint32_t G) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t h = lane >> 5, col = lane & 31u;
     ProjLanes pl;
-    const uint32_t na = n_base + 64u * wave_in_mat + col, nb = na + 32u;
+    const uint32_t na = n_base + 32u * J * wave_in_mat + col, nb = na + 32u;
     const uint32_t ra = na < nrows ? na : nrows - 1, rb = nb < nrows ? nb : nrows - 1;
     pl.wp0 = W + (size_t)ra * row_bytes + 16u * h;
     pl.wp1 = W + (size_t)rb * row_bytes + 16u * h;
@@ -325,6 +557,7 @@ __device__ __forceinline__ ProjLanes proj_lanes(const uint8_t* W, uint32_t row_b
     return pl;
 }
 
+// Eight waves (kProjGemmThreads), one 32-output sub-tile each.
 template <bool X_BF16>
 __device__ __forceinline__ void gemm_q4_proj(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
                                              const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
@@ -333,18 +566,17 @@ __device__ __forceinline__ void gemm_q4_proj(const uint16_t* __restrict__ X, con
     const uint32_t tid = threadIdx.x, wave = tid >> 6;
     const uint32_t G = K >> 6;
     const uint32_t n0 = blockIdx.x * kProjBN, m0 = blockIdx.y * kProjBM;
-    uint16_t* s_lds = reinterpret_cast<uint16_t*>(proj_lds + 2 * kProjBM * kGemmLdsStride);
-    uint16_t* b_lds = s_lds + kProjBN * G;
+    uint32_t* sb_lds = reinterpret_cast<uint32_t*>(proj_lds + 3 * kProjBM * kGemmLdsStride);
     // scales / biases of rows n0 .. n0+255 (clamped to N): contiguous in S and B
     const uint32_t nrows = N - n0 < kProjBN ? N - n0 : kProjBN;
-    copy_pair_to_lds<kProjThreads>(S + (size_t)n0 * G, B + (size_t)n0 * G, s_lds, b_lds, nrows * G);
-    const ProjLanes pl = proj_lanes(W, K >> 1, n0, wave, N, 0, G);
+    copy_sb_to_lds<kProjGemmThreads>(S + (size_t)n0 * G, B + (size_t)n0 * G, sb_lds, nrows * G);
+    const ProjLanes pl = proj_lanes<1>(W, K >> 1, n0, wave, N, 0, G);
     // token rows past M read row 0: their results are never stored
-    const uint32_t xrow = tid >> 2;
-    const uint16_t* xp = X + (size_t)(m0 + xrow < M ? m0 + xrow : 0u) * K + 16u * (tid & 3u);
-    f32x16 acc[2][2];
-    proj_core<X_BF16>(acc, proj_lds, s_lds, b_lds, pl, xp, G);
-    proj_for_each(acc, [&](uint32_t m, uint32_t n, float v) {
+    const uint32_t xrow = tid >> 3;
+    const uint16_t* xp = X + (size_t)(m0 + xrow < M ? m0 + xrow : 0u) * K + 8u * (tid & 7u);
+    f32x16 acc[2][1];
+    proj_core_pl<X_BF16, 1>(acc, proj_lds, sb_lds, pl, xp, G);
+    proj_for_each<1>(acc, [&](uint32_t m, uint32_t n, float v) {
         if (m0 + m < M && n0 + n < N)
             Y[(size_t)(m0 + m) * N + n0 + n] = X_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)v) : f2h(v);
     });

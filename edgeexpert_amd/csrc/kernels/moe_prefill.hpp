@@ -232,16 +232,22 @@ __device__ __forceinline__ void moe_grouped_gate_up(const ExpertPool& pool, cons
     const uint32_t xrow = tid >> 2;
     const uint32_t tok = sorted[gr.first + (xrow < gr.count ? xrow : 0u)].token;
     const uint16_t* xp = hidden + (size_t)tok * stride + 16u * (tid & 3u);
-    f32x16 acc[2][2];
-    proj_core<false>(acc, proj_lds, s_lds, b_lds, pl, xp, G);
+    // a half with at most 32 rows runs one token sub-tile (block-uniform)
+    auto run = [&](auto mi_c) {
+        constexpr int MI = decltype(mi_c)::value;
+        f32x16 acc[MI][2];
+        proj_core<false, MI>(acc, proj_lds, s_lds, b_lds, pl, xp, G);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t m = 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
-            if (m < gr.count && f < F)
-                act[(size_t)(gr.first + m) * F + f] = f2h(gelu_tanh(acc[i][0][r]) * acc[i][1][r]);
-        }
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t m = 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
+                if (m < gr.count && f < F)
+                    act[(size_t)(gr.first + m) * F + f] = f2h(gelu_tanh(acc[i][0][r]) * acc[i][1][r]);
+            }
+    };
+    if (gr.count <= 32u) run(std::integral_constant<int, 1>{});
+    else run(std::integral_constant<int, 2>{});
 }
 
 // Grouped down projection over one 64-row half tile (blockIdx.x) and 256
@@ -270,14 +276,20 @@ __device__ __forceinline__ void moe_grouped_down(const ExpertPool& pool, const P
     copy_pair_to_lds<kProjThreads>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)n0 * G,
                                    reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)n0 * G, s_lds,
                                    b_lds, nrows * G);
-    const ProjLanes pl = proj_lanes(blob + o.down_w, F >> 1, n0, wave, D, 0, G);
+    const ProjLanes pl = proj_lanes<2>(blob + o.down_w, F >> 1, n0, wave, D, 0, G);
     const uint32_t xrow = tid >> 2;
     const uint16_t* xp = act + (size_t)(gr.first + (xrow < gr.count ? xrow : 0u)) * F + 16u * (tid & 3u);
-    f32x16 acc[2][2];
-    proj_core<false>(acc, proj_lds, s_lds, b_lds, pl, xp, G);     // its barriers publish dst_row
-    proj_for_each(acc, [&](uint32_t m, uint32_t n, float v) {
-        if (m < gr.count && n0 + n < D) partials[(size_t)dst_row[m] * D + n0 + n] = f2h(v);
-    });
+    // a half with at most 32 rows runs one token sub-tile (block-uniform)
+    auto run = [&](auto mi_c) {
+        constexpr int MI = decltype(mi_c)::value;
+        f32x16 acc[MI][2];
+        proj_core<false, MI>(acc, proj_lds, s_lds, b_lds, pl, xp, G);     // its barriers publish dst_row
+        proj_for_each<2>(acc, [&](uint32_t m, uint32_t n, float v) {
+            if (m < gr.count && n0 + n < D) partials[(size_t)dst_row[m] * D + n0 + n] = f2h(v);
+        });
+    };
+    if (gr.count <= 32u) run(std::integral_constant<int, 1>{});
+    else run(std::integral_constant<int, 2>{});
 }
 
 // h2[t][d] = fp16(Σ_r fma(w[t][r], partials[(t*k+r)*D + d])) in rank order

@@ -143,13 +143,13 @@ TFQ_PHASE2(2)
 TFQ_PHASE2(3)
 TFQ_PHASE2(4)
 
-extern "C" __global__ __launch_bounds__(kProjThreads) void tfq_gemm_q4_f16(
+extern "C" __global__ __launch_bounds__(kProjGemmThreads) void tfq_gemm_q4_f16(
     const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
     uint32_t M, uint32_t N, uint32_t K) {
     gemm_q4_proj<false>(X, W, S, B, Y, M, N, K);
 }
 
-extern "C" __global__ __launch_bounds__(kProjThreads) void tfq_gemm_q4_bf16(
+extern "C" __global__ __launch_bounds__(kProjGemmThreads) void tfq_gemm_q4_bf16(
     const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
     uint32_t M, uint32_t N, uint32_t K) {
     gemm_q4_proj<true>(X, W, S, B, Y, M, N, K);
