@@ -18,6 +18,7 @@ TFQ_E_INVAL = 1
 TFQ_E_UNSUPPORTED = 2
 TFQ_E_HIP = 3
 TFQ_E_NOT_LOADED = 4
+TFQ_E_IO = 5
 ROUTER_WORKSPACE_BYTES = 4096
 LM_HEAD_WORKSPACE_BYTES = 65536
 DTYPE_F16 = 0
@@ -96,6 +97,17 @@ SIGNATURES = {
                            _P, _P, _P, _P, _U32, _U32, _U32],
     "tfq_gemv_q8g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32],
     "tfq_lm_head_greedy": [_P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, C.c_float, _P],
+    "tfq_expert_layout_load": [C.c_char_p, C.c_uint64, C.POINTER(C.c_void_p)],
+    "tfq_expert_layout_free": [_P],
+    "tfq_expert_layout_info": [_P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                               C.POINTER(C.c_uint32)],
+    "tfq_expert_layout_expert": [_P, _U32, _U32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                                 C.POINTER(C.c_uint64)],
+    "tfq_expert_layout_offsets": [_P, _U32, C.POINTER(ExpertOffsets), C.c_char_p, C.c_size_t],
+    "tfq_expert_pool_bytes": [_P, _U32, _U32, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)],
+    "tfq_expert_pool_load": [_P, _P, _P, C.c_char_p, _U32, _U32, _U32, _P, C.c_uint64,
+                             C.POINTER(ExpertPoolDesc), _P],
+    "tfq_resident_load": [_P, C.c_char_p, C.c_uint64, C.c_uint64, _P],
     "tfq_router_topk": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
     "tfq_moe_phase1": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _U32, _U32, _U32],
     "tfq_router_logits": [_P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32],
@@ -152,7 +164,7 @@ SIGNATURES = {
     "tfq_rt_graph_launch": [_P, _P],
     "tfq_rt_graph_destroy": [_P],
 }
-_RES = {"tfq_destroy": None, "tfq_status_string": C.c_char_p,
+_RES = {"tfq_destroy": None, "tfq_status_string": C.c_char_p, "tfq_expert_layout_free": None,
         "tfq_moe_prefill_workspace_bytes": C.c_size_t,
         "tfq_attention_workspace_bytes": C.c_size_t,
         "tfq_decode_layer_workspace_bytes": C.c_size_t,

@@ -47,10 +47,10 @@ def build_code_object(extra=()):
 
 
 def build_host_lib():
-    src = os.path.join(CSRC, "host", "tfq.cpp")
+    srcs = [os.path.join(CSRC, "host", n) for n in ("tfq.cpp", "loader.cpp")]
     tmp = HOST_LIB + ".tmp"
     _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
-          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", src, "-o", tmp,
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", *srcs, "-o", tmp,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
     os.replace(tmp, HOST_LIB)
     return HOST_LIB

@@ -613,7 +613,7 @@ public:
         return (window > 0 && seq_len > window) ? seq_len - window : 0;   // Attention.swift:254
     }
     static uint32_t chunks(uint32_t seq_len, uint32_t window) {
-        return (seq_len - kv_start(seq_len, window) + 63) / 64;
+        return (seq_len - kv_start(seq_len, window) + kAttnChunk - 1) / kAttnChunk;
     }
     static size_t workspace_bytes(uint32_t head_dim, uint32_t nq, uint32_t seq_len, uint32_t window) {
         if (seq_len == 0) return 0;
@@ -646,7 +646,7 @@ public:
                 return fail(TFQ_E_INVAL, "epilogue eps and rope theta must be positive");
         }
         const uint32_t nc = chunks(seq_len, window);
-        if (nc > 1024) return fail(TFQ_E_UNSUPPORTED, "more than 65536 visible keys");
+        if (nc > kAttnMaxChunks) return fail(TFQ_E_UNSUPPORTED, "more than 65536 visible keys");
         if (workspace_bytes_given < workspace_bytes(hd, nq, seq_len, window))
             return fail(TFQ_E_INVAL, "attention workspace too small");
         float* part_o = static_cast<float*>(workspace);

@@ -188,6 +188,7 @@ const char* tfq_status_string(int status) {
         case TFQ_E_UNSUPPORTED: return "shape not compiled into the code object";
         case TFQ_E_HIP: return "HIP runtime error";
         case TFQ_E_NOT_LOADED: return "kernel not loaded";
+        case TFQ_E_IO: return "checkpoint file missing, unreadable or short";
         default: return "unknown status";
     }
 }

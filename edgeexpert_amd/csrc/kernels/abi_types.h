@@ -44,6 +44,11 @@ struct NormArg {
 // of sums per 32-element chunk (16 bytes each).
 constexpr uint32_t xpairs_lds_bytes(uint32_t n) { return 4u * n + 16u * (n >> 5); }
 
+// Keys per split-K attention block (attention.hpp) and the most chunks the
+// combine merges (its weight table in LDS): 65536 visible keys.
+constexpr uint32_t kAttnChunk = 64;
+constexpr uint32_t kAttnMaxChunks = 65536 / kAttnChunk;
+
 // Gemma 4 q/k/v epilogue applied inside the decode attention kernel
 // (fused_qkv_epilogue, S/Metal/Fusions/fused.metal:86-180): per-head RMSNorm
 // of q and k with the shared head-dim weights, NeoX RoPE of the first

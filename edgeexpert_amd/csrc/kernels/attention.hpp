@@ -4,7 +4,7 @@
 //
 // Cache layout [capacity][num_kv_heads][HD] fp16 for K and for V (the
 // reference's, S/Metal/Attention/attention.metal:316-580). Keys
-// [kv_start, seq_len) are cut into 64-key chunks; block (chunk, kv head)
+// [kv_start, seq_len) are cut into kAttnChunk-key chunks; block (chunk, kv head)
 // computes, for each of the G query heads sharing that kv head,
 //     m = max_j s_j,  l = Σ_j e^{s_j - m},  O[d] = Σ_j e^{s_j - m} V[j][d],
 // s_j = scale · q·k_j (fp32 accumulate of exact fp16 products), and stores
@@ -16,7 +16,7 @@
 // Mapping inside a block (256 threads): for q·k, 16 lanes own one key (each
 // lane two 16-byte pieces of the 512-byte row, so one load instruction covers
 // 4 whole rows); for p·V, HD/8 threads own one key row with 16-byte loads and
-// 2048/HD groups of them split the 64 keys, reduced through LDS in group
+// 2048/HD groups of them split the chunk's keys, reduced through LDS in group
 // order. K and V loads of the whole chunk are issued before anything else.
 #pragma once
 
@@ -24,7 +24,6 @@
 
 namespace tfq {
 
-constexpr uint32_t kAttnChunk = 64;
 constexpr uint32_t kAttnThreads = 256;
 constexpr uint32_t kLayerTailThreads = 1024;     // threads of the one-block layer tail
 constexpr uint32_t kAttnKeyLanes = 16;
@@ -205,13 +204,13 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
 
     // 4. chunk softmax statistics, one wavefront per query head
     for (uint32_t g = wave; g < (uint32_t)G; g += kAttnThreads / 64) {
-        const float sv = L.p[g][lane];
+        const float sv = lane < kAttnChunk ? L.p[g][lane] : -__builtin_inff();
         float m = sv;
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
         const float e = lane < n ? expf(sv - m) : 0.0f;
         const float l = seg_sum<kWave>(e);
-        L.p[g][lane] = e;
+        if (lane < kAttnChunk) L.p[g][lane] = e;
         if (lane == 0) {
             L.ml[g][0] = m;
             L.ml[g][1] = l;
@@ -262,7 +261,7 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
 template <int HD>
 __device__ __forceinline__ void attn_combine(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                                              uint16_t* __restrict__ out, uint32_t nchunks) {
-    __shared__ float wgt[1024];
+    __shared__ float wgt[kAttnMaxChunks];
     __shared__ float tot;
     const uint32_t qh = blockIdx.x, d = threadIdx.x;
     const float* ml = part_ml + (size_t)qh * nchunks * 2;

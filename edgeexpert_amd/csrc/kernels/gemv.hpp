@@ -509,8 +509,9 @@ __device__ __forceinline__ void read_ceiling(const uint4* __restrict__ src, uint
 
 // ------------------------------------------------------------- convert ----
 
-__device__ __forceinline__ void convert_bf16_to_f16(const uint16_t* __restrict__ src,
-                                                    uint16_t* __restrict__ dst, uint64_t n,
+// src and dst may be the same buffer (each element is read, then written, by
+// one thread).
+__device__ __forceinline__ void convert_bf16_to_f16(const uint16_t* src, uint16_t* dst, uint64_t n,
                                                     uint32_t* __restrict__ inexact) {
     uint32_t bad = 0;
     for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < n;

@@ -9,6 +9,7 @@ goes to the HIP kernels in libtfq; a non-OK status raises TfqError.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from dataclasses import dataclass
 
 import numpy as np
@@ -140,6 +141,72 @@ class ExpertPool:
         o = ExpertOffsets(*[int(self.offsets[k]) for k in (
             "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b")])
         return ExpertPoolDesc(_addr(self.buffer, self.base_offset), self.stride, self.num_experts, o)
+
+
+class PackedExpertsLayout:
+    """packed_experts/layout.json of a repacked model directory
+    (S/Infrastructure/ModelIO/PackedExpertsLayout.swift:38-150), parsed by
+    libtfq with the reader's checks (tfq_loader.h)."""
+
+    def __init__(self, model_dir: str, max_bytes: int = 0):
+        h = C.c_void_p()
+        check(lib().tfq_expert_layout_load(os.fsencode(model_dir), max_bytes, C.byref(h)),
+              "PackedExpertsLayoutReader.load")
+        self.handle = h
+        self.model_dir = model_dir
+        stride, nl, epl, entries = C.c_uint64(), C.c_uint32(), C.c_uint32(), C.c_uint32()
+        check(lib().tfq_expert_layout_info(h, C.byref(stride), C.byref(nl), C.byref(epl), C.byref(entries)),
+              "tfq_expert_layout_info")
+        self.expert_stride, self.num_layers = stride.value, nl.value
+        self.experts_per_layer, self.layer_entries = epl.value, entries.value
+
+    def expert(self, layer: int, expert: int):
+        """(physicalRank, offset, size) of layout.expert(layer:expert:)."""
+        r, off, size = C.c_uint32(), C.c_uint64(), C.c_uint64()
+        check(lib().tfq_expert_layout_expert(self.handle, layer, expert, C.byref(r), C.byref(off),
+                                             C.byref(size)), "PackedExpertsLayout.expert")
+        return r.value, off.value, size.value
+
+    def routed_expert_offsets(self, layer: int):
+        """Model.routedExpertOffsets (ModelExpertIO.swift:40-61) and the layer's file name."""
+        o = ExpertOffsets()
+        name = C.create_string_buffer(4096)
+        check(lib().tfq_expert_layout_offsets(self.handle, layer, C.byref(o), name, len(name)),
+              "routedExpertOffsets")
+        return {k: getattr(o, k) for k, _ in ExpertOffsets._fields_}, name.value.decode()
+
+    def pool_bytes(self, d: int, f: int):
+        stride, total = C.c_uint64(), C.c_uint64()
+        check(lib().tfq_expert_pool_bytes(self.handle, d, f, C.byref(stride), C.byref(total)),
+              "tfq_expert_pool_bytes")
+        return stride.value, total.value
+
+    def load_pool(self, context, stream, layer: int, d: int, f: int, pool, inexact_counter=None):
+        """Loads one layer's experts into the device buffer `pool`; returns the ExpertPool."""
+        desc = ExpertPoolDesc()
+        check(lib().tfq_expert_pool_load(context.handle, _s(stream), self.handle, os.fsencode(self.model_dir),
+                                         layer, d, f, _addr(pool), pool.nbytes, C.byref(desc),
+                                         _addr(inexact_counter)), "tfq_expert_pool_load")
+        offs = {k: getattr(desc.offsets, k) for k, _ in ExpertOffsets._fields_}
+        return ExpertPool(pool, desc.stride, desc.num_experts, offs)
+
+    def close(self):
+        if self.handle:
+            lib().tfq_expert_layout_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def resident_load(stream, path: str, file_offset: int, size: int, dst):
+    """The resident tensor bytes [file_offset, file_offset + size) of `path` into device memory
+    (ResidentBuffer.init, S/Infrastructure/ModelIO/ResidentBuffer.swift:15-57)."""
+    check(lib().tfq_resident_load(_s(stream), os.fsencode(path), file_offset, size, _addr(dst)),
+          "tfq_resident_load")
 
 
 class MoE:

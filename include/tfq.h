@@ -43,6 +43,7 @@ extern "C" {
 #define TFQ_E_UNSUPPORTED 2
 #define TFQ_E_HIP 3
 #define TFQ_E_NOT_LOADED 4
+#define TFQ_E_IO 5          /* a checkpoint file is missing, unreadable or short (tfq_loader.h) */
 
 #define TFQ_GROUP_SIZE 64
 
@@ -456,8 +457,9 @@ int tfq_moe_prefill(tfq_ctx *ctx, void *stream, const tfq_router *router,
 /* fp16 <- BF16, elementwise on the device. Values outside the exactly
  * representable fp16 range are still converted (round to nearest even /
  * saturate to inf) and counted: *inexact_count_dev (device uint32, may be
- * NULL) is incremented once per inexact element. Converts the reference's
- * BF16 scales/biases (S/Infrastructure/ModelIO/Quantization.swift:32-45). */
+ * NULL) is incremented once per inexact element. src and dst may be the
+ * same buffer. Converts the reference's BF16 scales/biases
+ * (S/Infrastructure/ModelIO/Quantization.swift:32-45). */
 int tfq_convert_bf16_to_f16(tfq_ctx *ctx, void *stream, const uint16_t *src, uint16_t *dst,
                             uint64_t count, uint32_t *inexact_count_dev);
 
