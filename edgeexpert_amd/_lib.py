@@ -49,7 +49,7 @@ class ExpertOffsets(C.Structure):
 
 class ExpertPoolDesc(C.Structure):
     _fields_ = [("base", C.c_void_p), ("stride", C.c_uint64), ("num_experts", C.c_uint32),
-                ("offsets", ExpertOffsets)]
+                ("offsets", ExpertOffsets), ("weight_bits", C.c_uint32)]
 
 
 class RouterDesc(C.Structure):
@@ -95,6 +95,9 @@ SIGNATURES = {
     "tfq_gemv_q4g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32],
     "tfq_gemv_q4g64_qkv": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
                            _P, _P, _P, _P, _U32, _U32, _U32],
+    "tfq_gemv_qg64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32],
+    "tfq_gemv_qg64_qkv": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
+                          _P, _P, _P, _P, _U32, _U32, _U32, _U32],
     "tfq_gemv_q8g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32],
     "tfq_lm_head_greedy": [_P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, C.c_float, _P],
     "tfq_expert_layout_load": [C.c_char_p, C.c_uint64, C.POINTER(C.c_void_p)],

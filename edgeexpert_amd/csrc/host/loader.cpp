@@ -184,9 +184,9 @@ struct PoolForm {
     tfq_expert_offsets off{};
 };
 
-bool pool_form(uint32_t d, uint32_t f, PoolForm& p) {
+bool pool_form(uint32_t d, uint32_t f, uint32_t bits, PoolForm& p) {
     if (d == 0 || f == 0 || d % TFQ_GROUP_SIZE || f % TFQ_GROUP_SIZE) return false;
-    p.wb = (uint64_t)f * d / 2;
+    p.wb = (uint64_t)f * d / 8 * bits;
     p.sbg = (uint64_t)f * (d / 64) * 2;
     p.sbd = (uint64_t)d * (f / 64) * 2;
     p.blob = 3 * p.wb + 4 * p.sbg + 2 * p.sbd;
@@ -210,7 +210,19 @@ struct Part {
     uint64_t src = 0;
 };
 
-int check_part(const tfq_expert_layout::Expert& ex, Part& p) {
+// Code width of a layer's routed experts: the `bits` of its first expert's
+// gate weights (the repacker writes 4, TurboFieldfareRebits 2 or 3,
+// Rebits/main.swift:437-441); 0 if absent or not 2..4 (check_part reports it).
+uint32_t layer_bits(const tfq_expert_layout::Layer& l) {
+    if (l.experts.empty()) return 0;
+    auto it = l.experts[0].tensors.find("gate");
+    if (it == l.experts[0].tensors.end() || !it->second.has_bits) return 0;
+    const int64_t b = it->second.bits;
+    return b >= 2 && b <= 4 ? (uint32_t)b : 0u;
+}
+
+// Every weight tensor must hold `bits`-bit codes (one width per pool).
+int check_part(const tfq_expert_layout::Expert& ex, Part& p, uint32_t bits) {
     auto it = ex.tensors.find(p.role);
     if (it == ex.tensors.end())
         return fail(TFQ_E_INVAL, "expert %lld has no tensor %s", (long long)ex.expert, p.role);
@@ -219,9 +231,12 @@ int check_part(const tfq_expert_layout::Expert& ex, Part& p) {
                                        (uint64_t)t.shape[1] == p.cols)
                                     : (t.shape.size() == 2 && (uint64_t)t.shape[0] == p.rows &&
                                        (uint64_t)t.shape[1] == p.cols / 64);
-    if (p.weights && (t.dtype != "U32" || !t.has_bits || t.bits != 4))
-        return fail(TFQ_E_UNSUPPORTED, "expert %lld %s: %s weights of %lld bits (int4 U32 only)", (long long)ex.expert,
-                    p.role, t.dtype.c_str(), (long long)t.bits);
+    if (p.weights && (t.dtype != "U32" || !t.has_bits || t.bits < 2 || t.bits > 4))
+        return fail(TFQ_E_UNSUPPORTED, "expert %lld %s: %s weights of %lld bits (U32 of 2, 3 or 4 bits only)",
+                    (long long)ex.expert, p.role, t.dtype.c_str(), (long long)t.bits);
+    if (p.weights && (uint32_t)t.bits != bits)
+        return fail(TFQ_E_UNSUPPORTED, "expert %lld %s: %lld-bit weights in a layer of %u-bit experts",
+                    (long long)ex.expert, p.role, (long long)t.bits, bits);
     if (!p.weights && t.dtype != "BF16")
         return fail(TFQ_E_INVAL, "expert %lld %s: dtype %s, expected BF16", (long long)ex.expert, p.role,
                     t.dtype.c_str());
@@ -334,8 +349,11 @@ int tfq_expert_layout_offsets(const tfq_expert_layout* L, uint32_t layer, tfq_ex
 
 int tfq_expert_pool_bytes(const tfq_expert_layout* L, uint32_t d, uint32_t f, uint64_t* stride, uint64_t* bytes) {
     if (!L) return fail(TFQ_E_INVAL, "null layout");
+    // the widest layer sets the size (every layer's pool then fits)
+    uint32_t bits = 2;
+    for (const tfq_expert_layout::Layer& l : L->layers) bits = std::max(bits, layer_bits(l) ? layer_bits(l) : 4u);
     PoolForm p;
-    if (!pool_form(d, f, p)) return fail(TFQ_E_INVAL, "d=%u and f=%u must be positive multiples of 64", d, f);
+    if (!pool_form(d, f, bits, p)) return fail(TFQ_E_INVAL, "d=%u and f=%u must be positive multiples of 64", d, f);
     if (stride) *stride = p.stride;
     if (bytes) *bytes = p.stride * (uint64_t)L->experts_per_layer;
     return TFQ_OK;
@@ -346,10 +364,11 @@ int tfq_expert_pool_load(tfq_ctx* ctx, void* stream, const tfq_expert_layout* L,
                          tfq_expert_pool* desc, uint32_t* inexact_count_dev) {
     if (!ctx || !L || !model_dir || !pool || !desc) return fail(TFQ_E_INVAL, "null pointer argument");
     if (layer >= L->layers.size()) return fail(TFQ_E_INVAL, "layer %u of %zu", layer, L->layers.size());
-    PoolForm pf;
-    if (!pool_form(d, f, pf)) return fail(TFQ_E_INVAL, "d=%u and f=%u must be positive multiples of 64", d, f);
-    if (!tfq::aligned(pool, 256)) return fail(TFQ_E_INVAL, "pool must be 256-byte aligned");
     const tfq_expert_layout::Layer& l = L->layers[layer];
+    const uint32_t bits = layer_bits(l) ? layer_bits(l) : 4u;      // a bad width fails in check_part
+    PoolForm pf;
+    if (!pool_form(d, f, bits, pf)) return fail(TFQ_E_INVAL, "d=%u and f=%u must be positive multiples of 64", d, f);
+    if (!tfq::aligned(pool, 256)) return fail(TFQ_E_INVAL, "pool must be 256-byte aligned");
     const uint64_t E = l.experts.size();
     if (E == 0) return fail(TFQ_E_INVAL, "layer %u has no experts", layer);
     if (E > UINT32_MAX || pool_bytes < pf.stride * E) return fail(TFQ_E_INVAL, "pool smaller than %llu bytes",
@@ -365,7 +384,7 @@ int tfq_expert_pool_load(tfq_ctx* ctx, void* stream, const tfq_expert_layout* L,
                     {"up_biases", false, f, d, pf.off.up_b, pf.sbg},     {"down_scales", false, d, f, pf.off.down_s, pf.sbd},
                     {"down_biases", false, d, f, pf.off.down_b, pf.sbd}};
         for (Part& p : parts[e])
-            if (int rc = check_part(ex, p)) return rc;
+            if (int rc = check_part(ex, p, bits)) return rc;
         max_blob = std::max(max_blob, ex.size);
     }
     const std::string rel = "packed_experts/" + l.file;
@@ -406,6 +425,7 @@ int tfq_expert_pool_load(tfq_ctx* ctx, void* stream, const tfq_expert_layout* L,
     desc->stride = pf.stride;
     desc->num_experts = (uint32_t)E;
     desc->offsets = pf.off;
+    desc->weight_bits = bits;
     return TFQ_OK;
 }
 

@@ -72,24 +72,26 @@ class DequantInt4GEMV {
 public:
     explicit DequantInt4GEMV(const Module& m) : m_(m) {}
 
-    // DequantInt4GEMV.encode (DequantInt4GEMV.swift:84-127).
-    // residual (may be null): y = fp16(residual + W·x); stage: how x is staged.
+    // DequantInt4GEMV.encode (DequantInt4GEMV.swift:84-127, bits: 3 or 4 as
+    // at :145-157). residual (may be null): y = fp16(residual + W·x); stage:
+    // how x is staged.
     int encode(void* stream, const void* weights, const uint16_t* scales, const uint16_t* biases,
                const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n,
-               const uint16_t* residual = nullptr, const NormArg& stage = stage_copy()) const {
+               const uint16_t* residual = nullptr, const NormArg& stage = stage_copy(),
+               uint32_t bits = 4) const {
         Q4Multi mats{};
         mats.m[0] = {static_cast<const uint8_t*>(weights), scales, biases, y, residual, m, 0};
         mats.nmat = 1;
         mats.total_rows = m;
         mats.norm = stage;
-        return launch_multi(stream, mats, x, n);
+        return launch_multi(stream, mats, x, n, bits);
     }
 
     // FusedQKVGEMV.encode (FusedQKVGEMV.swift:92-156): rows mq + 2*mkv in one launch.
     int encode_qkv(void* stream, const tfq_q4_matrix& q, const tfq_q4_matrix& k,
                    const tfq_q4_matrix& v, const uint16_t* x, uint16_t* yq, uint16_t* yk,
                    uint16_t* yv, uint32_t mq, uint32_t mkv, uint32_t n,
-                   const NormArg& stage = stage_copy()) const {
+                   const NormArg& stage = stage_copy(), uint32_t bits = 4) const {
         Q4Multi mats{};
         mats.m[0] = {static_cast<const uint8_t*>(q.weights), q.scales, q.biases, yq, nullptr, mq, 0};
         mats.m[1] = {static_cast<const uint8_t*>(k.weights), k.scales, k.biases, yk, nullptr, mkv, 0};
@@ -97,11 +99,13 @@ public:
         mats.nmat = 3;
         mats.total_rows = mq + 2 * mkv;
         mats.norm = stage;
-        return launch_multi(stream, mats, x, n);
+        return launch_multi(stream, mats, x, n, bits);
     }
 
 private:
-    int launch_multi(void* stream, Q4Multi& mats, const uint16_t* x, uint32_t n) const {
+    int launch_multi(void* stream, Q4Multi& mats, const uint16_t* x, uint32_t n, uint32_t bits) const {
+        // the reference's attention kernels exist at 3 and 4 bits (DequantInt4GEMV.swift:149-150)
+        if (bits != 3 && bits != 4) return fail(TFQ_E_INVAL, "unsupported attention weight bits %u", bits);
         if (n == 0 || n % TFQ_GROUP_SIZE != 0)
             return fail(TFQ_E_INVAL, "n=%u must be a positive multiple of 64", n);
         if (n > kMaxN) return fail(TFQ_E_UNSUPPORTED, "n=%u exceeds %u", n, kMaxN);
@@ -119,7 +123,7 @@ private:
         }
         const SegShape sh = seg_shape_fit(n / 32, 2);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_q4_gemv_%ss%u_p%u", form_prefix(mats.norm), sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_q%u_gemv_%ss%u_p%u", bits, form_prefix(mats.norm), sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         uint32_t nn = n;
         void* args[] = {&mats, &x, &nn};
@@ -213,6 +217,45 @@ private:
     const Module& m_;
 };
 
+// Code width of a pool's rows: weight_bits, 0 meaning 4 (the `bits: Int = 4`
+// default of S/Kernels/MoE/MoE.swift:244).
+inline uint32_t pool_bits(const tfq_expert_pool& pool) { return pool.weight_bits ? pool.weight_bits : 4u; }
+
+// Shared pool checks / conversion for the MoE operators.
+inline int check_expert_pool(const tfq_expert_pool& pool, uint32_t d, uint32_t f) {
+    const uint32_t bits = pool_bits(pool);
+    if (bits < 2 || bits > 4)     // MoE.swift:365-375: 4, or the 2/3-bit variants
+        return fail(TFQ_E_INVAL, "unsupported routed expert weight bits %u", pool.weight_bits);
+    if (d == 0 || d % TFQ_GROUP_SIZE != 0 || f == 0 || f % TFQ_GROUP_SIZE != 0)
+        return fail(TFQ_E_INVAL, "d=%u and f=%u must be positive multiples of 64", d, f);
+    if (!pool.base || pool.num_experts == 0) return fail(TFQ_E_INVAL, "empty expert pool");
+    const tfq_expert_offsets& o = pool.offsets;
+    if (!aligned(pool.base, 16) || pool.stride % 16 != 0 || o.gate_w % 16 || o.up_w % 16 ||
+        o.down_w % 16)
+        return fail(TFQ_E_INVAL, "pool base, stride and weight offsets must be 16-byte aligned");
+    if ((o.gate_s | o.gate_b | o.up_s | o.up_b | o.down_s | o.down_b) & 1u)
+        return fail(TFQ_E_INVAL, "scale/bias offsets must be 2-byte aligned");
+    // every sub-tensor must lie inside one blob
+    const uint64_t wbytes = (uint64_t)f * d / 8 * bits, sbytes = (uint64_t)f * (d / 64) * 2;
+    const uint64_t ends[9] = {o.gate_w + wbytes, o.gate_s + sbytes, o.gate_b + sbytes,
+                              o.up_w + wbytes,   o.up_s + sbytes,   o.up_b + sbytes,
+                              o.down_w + wbytes, o.down_s + (uint64_t)d * (f / 64) * 2,
+                              o.down_b + (uint64_t)d * (f / 64) * 2};
+    for (uint64_t e : ends)
+        if (e > pool.stride) return fail(TFQ_E_INVAL, "expert sub-tensor exceeds the pool stride");
+    return TFQ_OK;
+}
+
+inline ExpertPool kernel_pool(const tfq_expert_pool& p) {
+    ExpertPool k{};
+    k.base = static_cast<const uint8_t*>(p.base);
+    k.stride = p.stride;
+    k.num_experts = p.num_experts;
+    const tfq_expert_offsets& o = p.offsets;
+    k.off = {o.gate_w, o.gate_s, o.gate_b, o.up_w, o.up_s, o.up_b, o.down_w, o.down_s, o.down_b};
+    return k;
+}
+
 // S/Kernels/MoE/MoE.swift:31-414: router + routed decode phases.
 class MoE {
 public:
@@ -282,10 +325,11 @@ public:
         if (active_slots == nullptr && active_count != top_k)
             return fail(TFQ_E_INVAL, "full phase 1 covers exactly topK slots");
         if (active_count > top_k) return fail(TFQ_E_INVAL, "activeCount > topK");
-        ExpertPool kp = to_kernel_pool(pool);
+        ExpertPool kp = kernel_pool(pool);
         const SegShape sh = seg_shape_fit(d / 32, 2);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_moe_phase1_%ss%u_p%u", form_prefix(stage), sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_moe_phase1_%s%ss%u_p%u", bits_infix(pool), form_prefix(stage),
+                      sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         NormArg na = stage;
         void* args[] = {&kp, &indices, &active_slots, &active_count, &top_k, &x, &acts, &d, &f, &na};
@@ -313,10 +357,11 @@ public:
             return fail(TFQ_E_INVAL, "router has %u experts, pool %u", num_experts, pool.num_experts);
         if (num_experts > 256 || top_k > num_experts)
             return fail(TFQ_E_INVAL, "numExperts must be <= 256 and >= topK");
-        ExpertPool kp = to_kernel_pool(pool);
+        ExpertPool kp = kernel_pool(pool);
         const SegShape sh = seg_shape_fit(d / 32, 2);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_moe_phase1_routed_%ss%u_p%u", form_prefix(stage), sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_moe_phase1_routed_%s%ss%u_p%u", bits_infix(pool),
+                      form_prefix(stage), sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         NormArg na = stage;
         void* args[] = {&kp,   &logits, &per_expert_scale, &num_experts, &top_k, &out_indices, &out_weights,
@@ -336,10 +381,10 @@ public:
         if (f > 1024) return fail(TFQ_E_UNSUPPORTED, "phase 2 f=%u exceeds 1024", f);
         if (!indices || !acts || !routing_weights || !y)
             return fail(TFQ_E_INVAL, "null pointer argument");
-        ExpertPool kp = to_kernel_pool(pool);
+        ExpertPool kp = kernel_pool(pool);
         const uint32_t p = ((f / 32) + 7) / 8;
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_moe_phase2_p%u", p);
+        std::snprintf(name, sizeof(name), "tfq_moe_phase2_%sp%u", bits_infix(pool), p);
         void* args[] = {&kp, &indices, &acts, &routing_weights, &residual, &y, &d, &f, &top_k};
         hipFunction_t fn = m_.get(name);
         const uint32_t lds = xpairs_lds_bytes(top_k * f);
@@ -348,36 +393,15 @@ public:
     }
 
 private:
-    int check_pool(const tfq_expert_pool& pool, uint32_t d, uint32_t f, uint32_t top_k) const {
-        if (top_k == 0 || top_k > 8) return fail(TFQ_E_INVAL, "topK=%u must be in 1...8", top_k);
-        if (d == 0 || d % TFQ_GROUP_SIZE != 0 || f == 0 || f % TFQ_GROUP_SIZE != 0)
-            return fail(TFQ_E_INVAL, "d=%u and f=%u must be positive multiples of 64", d, f);
-        if (!pool.base || pool.num_experts == 0) return fail(TFQ_E_INVAL, "empty expert pool");
-        const tfq_expert_offsets& o = pool.offsets;
-        if (!aligned(pool.base, 16) || pool.stride % 16 != 0 || o.gate_w % 16 || o.up_w % 16 ||
-            o.down_w % 16)
-            return fail(TFQ_E_INVAL, "pool base, stride and weight offsets must be 16-byte aligned");
-        if ((o.gate_s | o.gate_b | o.up_s | o.up_b | o.down_s | o.down_b) & 1u)
-            return fail(TFQ_E_INVAL, "scale/bias offsets must be 2-byte aligned");
-        // every sub-tensor must lie inside one blob
-        const uint64_t wbytes = (uint64_t)f * d / 2, sbytes = (uint64_t)f * (d / 64) * 2;
-        const uint64_t ends[9] = {o.gate_w + wbytes, o.gate_s + sbytes, o.gate_b + sbytes,
-                                  o.up_w + wbytes,   o.up_s + sbytes,   o.up_b + sbytes,
-                                  o.down_w + wbytes, o.down_s + (uint64_t)d * (f / 64) * 2,
-                                  o.down_b + (uint64_t)d * (f / 64) * 2};
-        for (uint64_t e : ends)
-            if (e > pool.stride) return fail(TFQ_E_INVAL, "expert sub-tensor exceeds the pool stride");
-        return TFQ_OK;
+    // Kernel-name infix of the pool's code width: "" (4 bits), "b2_", "b3_".
+    static const char* bits_infix(const tfq_expert_pool& pool) {
+        const uint32_t b = pool_bits(pool);
+        return b == 2 ? "b2_" : b == 3 ? "b3_" : "";
     }
 
-    static ExpertPool to_kernel_pool(const tfq_expert_pool& p) {
-        ExpertPool k{};
-        k.base = static_cast<const uint8_t*>(p.base);
-        k.stride = p.stride;
-        k.num_experts = p.num_experts;
-        const tfq_expert_offsets& o = p.offsets;
-        k.off = {o.gate_w, o.gate_s, o.gate_b, o.up_w, o.up_s, o.up_b, o.down_w, o.down_s, o.down_b};
-        return k;
+    int check_pool(const tfq_expert_pool& pool, uint32_t d, uint32_t f, uint32_t top_k) const {
+        if (top_k == 0 || top_k > 8) return fail(TFQ_E_INVAL, "topK=%u must be in 1...8", top_k);
+        return check_expert_pool(pool, d, f);
     }
 
     const Module& m_;
@@ -456,37 +480,6 @@ public:
 private:
     const Module& m_;
 };
-
-// Shared pool checks / conversion for the MoE operators.
-inline int check_expert_pool(const tfq_expert_pool& pool, uint32_t d, uint32_t f) {
-    if (d == 0 || d % TFQ_GROUP_SIZE != 0 || f == 0 || f % TFQ_GROUP_SIZE != 0)
-        return fail(TFQ_E_INVAL, "d=%u and f=%u must be positive multiples of 64", d, f);
-    if (!pool.base || pool.num_experts == 0) return fail(TFQ_E_INVAL, "empty expert pool");
-    const tfq_expert_offsets& o = pool.offsets;
-    if (!aligned(pool.base, 16) || pool.stride % 16 != 0 || o.gate_w % 16 || o.up_w % 16 ||
-        o.down_w % 16)
-        return fail(TFQ_E_INVAL, "pool base, stride and weight offsets must be 16-byte aligned");
-    if ((o.gate_s | o.gate_b | o.up_s | o.up_b | o.down_s | o.down_b) & 1u)
-        return fail(TFQ_E_INVAL, "scale/bias offsets must be 2-byte aligned");
-    const uint64_t wbytes = (uint64_t)f * d / 2, sbytes = (uint64_t)f * (d / 64) * 2;
-    const uint64_t ends[9] = {o.gate_w + wbytes, o.gate_s + sbytes, o.gate_b + sbytes,
-                              o.up_w + wbytes,   o.up_s + sbytes,   o.up_b + sbytes,
-                              o.down_w + wbytes, o.down_s + (uint64_t)d * (f / 64) * 2,
-                              o.down_b + (uint64_t)d * (f / 64) * 2};
-    for (uint64_t e : ends)
-        if (e > pool.stride) return fail(TFQ_E_INVAL, "expert sub-tensor exceeds the pool stride");
-    return TFQ_OK;
-}
-
-inline ExpertPool kernel_pool(const tfq_expert_pool& p) {
-    ExpertPool k{};
-    k.base = static_cast<const uint8_t*>(p.base);
-    k.stride = p.stride;
-    k.num_experts = p.num_experts;
-    const tfq_expert_offsets& o = p.offsets;
-    k.off = {o.gate_w, o.gate_s, o.gate_b, o.up_w, o.up_s, o.up_b, o.down_w, o.down_s, o.down_b};
-    return k;
-}
 
 inline int launch2(const Module& m, const char* name, uint32_t gx, uint32_t gy, uint32_t block,
                    uint32_t lds, void* stream, void** args) {
@@ -570,6 +563,8 @@ public:
                uint16_t* act, uint16_t* partials) const {
         int rc = check_expert_pool(pool, d, f);
         if (rc) return rc;
+        if (pool_bits(pool) != 4)
+            return fail(TFQ_E_UNSUPPORTED, "grouped prefill experts are 4-bit only (pool has %u)", pool_bits(pool));
         if (!sorted || !tiles || !n_tiles || !hidden || !act || !partials)
             return fail(TFQ_E_INVAL, "null pointer argument");
         if (stride < d || stride % 8) return fail(TFQ_E_INVAL, "hidden stride must be >= d and a multiple of 8");

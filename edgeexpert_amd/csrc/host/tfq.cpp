@@ -31,8 +31,11 @@ static std::vector<std::string> kernel_names() {
     for (const char* s : q4_shapes)
         for (const char* form : {"", "norm_"}) {
             names.push_back(std::string("tfq_q4_gemv_") + form + s);
-            names.push_back(std::string("tfq_moe_phase1_") + form + s);
-            names.push_back(std::string("tfq_moe_phase1_routed_") + form + s);
+            names.push_back(std::string("tfq_q3_gemv_") + form + s);
+            for (const char* b : {"", "b2_", "b3_"}) {
+                names.push_back(std::string("tfq_moe_phase1_") + b + form + s);
+                names.push_back(std::string("tfq_moe_phase1_routed_") + b + form + s);
+            }
             names.push_back(std::string("tfq_gate_up_act_") + form + s);
         }
     for (const char* s : q4_shapes) names.push_back(std::string("tfq_lm_head_greedy_") + s);
@@ -42,7 +45,8 @@ static std::vector<std::string> kernel_names() {
         names.push_back(std::string("tfq_router_logits_") + s);
         names.push_back(std::string("tfq_prefill_router_logits_") + s);
     }
-    for (int p = 1; p <= 4; ++p) names.push_back("tfq_moe_phase2_p" + std::to_string(p));
+    for (int p = 1; p <= 4; ++p)
+        for (const char* b : {"", "b2_", "b3_"}) names.push_back(std::string("tfq_moe_phase2_") + b + "p" + std::to_string(p));
     names.push_back("tfq_router_select");
     names.push_back("tfq_read_ceiling");
     names.push_back("tfq_gemm_q4_f16");
@@ -208,6 +212,20 @@ int tfq_gemv_q4g64_qkv(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* q, const
     TFQ_REQUIRE_CTX(ctx);
     if (!q || !k || !v) return fail(TFQ_E_INVAL, "null matrix descriptor");
     return ctx->int4->encode_qkv(stream, *q, *k, *v, x, yq, yk, yv, mq, mkv, n);
+}
+
+int tfq_gemv_qg64(tfq_ctx* ctx, void* stream, const void* weights, const uint16_t* scales,
+                  const uint16_t* biases, const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n, uint32_t bits) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->int4->encode(stream, weights, scales, biases, x, y, m, n, nullptr, stage_copy(), bits);
+}
+
+int tfq_gemv_qg64_qkv(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* q, const tfq_q4_matrix* k,
+                      const tfq_q4_matrix* v, const uint16_t* x, uint16_t* yq, uint16_t* yk, uint16_t* yv,
+                      uint32_t mq, uint32_t mkv, uint32_t n, uint32_t bits) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!q || !k || !v) return fail(TFQ_E_INVAL, "null matrix descriptor");
+    return ctx->int4->encode_qkv(stream, *q, *k, *v, x, yq, yk, yv, mq, mkv, n, stage_copy(), bits);
 }
 
 int tfq_lm_head_greedy(tfq_ctx* ctx, void* stream, const uint16_t* hidden, const uint16_t* norm_weight,
@@ -441,6 +459,9 @@ int tfq_moe_prefill(tfq_ctx* ctx, void* stream, const tfq_router* router, const 
     if (router->num_experts != pool->num_experts)
         return fail(TFQ_E_INVAL, "router has %u experts, pool %u", router->num_experts,
                     pool->num_experts);
+    if (int rc = check_expert_pool(*pool, d, f)) return rc;
+    if (pool_bits(*pool) != 4)      // checked before any launch: nothing is queued on failure
+        return fail(TFQ_E_UNSUPPORTED, "grouped prefill experts are 4-bit only (pool has %u)", pool_bits(*pool));
     const uint32_t E = pool->num_experts;
     const PrefillLayout L = prefill_layout(T, top_k, E, d, f);
     if (workspace_bytes < L.total)

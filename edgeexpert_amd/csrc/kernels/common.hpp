@@ -206,6 +206,103 @@ __device__ __forceinline__ float dot_q4_chunk(const uint4 w, const XChunk& xc) {
     return fmaf(acc_b - xc.cb, 0.0625f, acc_a - xc.ca);
 }
 
+// ------------------------------------------------- 2-, 3- and 4-bit chunks ----
+//
+// The 32 codes of activation chunk c (positions 32c..32c+31) take 4·BITS
+// bytes of a BITS-bit row, codes packed from the least significant bit up
+// (S/Infrastructure/ModelIO/Quantization.swift:198-201,296-320): 16 bytes at
+// 4 bits, 12 at 3 bits (code i of the chunk in bits 3i..3i+2 of the 96-bit
+// little-endian value), 8 at 2 bits. Chunk c of a row starts at byte
+// 4·BITS·c, so a lane's chunk is one 128-, 96- or 64-bit load.
+template <int BITS>
+struct QChunk {
+    uint32_t w[BITS];
+};
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Non-temporal load of chunk c of a row (4-byte aligned for every BITS: rows
+// of n codes start at multiples of n·BITS/8, a multiple of 8 bytes for n %
+// 64 == 0, and chunks at multiples of 4·BITS). Three separate words at 3
+// bits: a 3-wide vector load may be widened to 16 bytes, past the row.
+template <int BITS>
+__device__ __forceinline__ QChunk<BITS> ldg_chunk(const uint8_t* row, uint32_t c) {
+    QChunk<BITS> q;
+    const uint8_t* p = row + 4u * BITS * c;
+    if constexpr (BITS == 4) {
+        const uint4 v = ldg16_stream(p);
+        q.w[0] = v.x;
+        q.w[1] = v.y;
+        q.w[2] = v.z;
+        q.w[3] = v.w;
+    } else if constexpr (BITS == 2) {
+        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        q.w[0] = v.x;
+        q.w[1] = v.y;
+    } else {
+        static_assert(BITS == 3, "2, 3 or 4 bits");
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
+        q.w[0] = __builtin_nontemporal_load(w);
+        q.w[1] = __builtin_nontemporal_load(w + 1);
+        q.w[2] = __builtin_nontemporal_load(w + 2);
+    }
+    return q;
+}
+
+// Codes 8j..8j+7 of a chunk in the int4 word form: a word whose low half
+// holds codes 8j..8j+3 and whose high half holds 8j+4..8j+7, at BITS-bit
+// spacing from bit 0 and bit 16 (bits between or above the codes may hold
+// anything; the dot masks them off).
+template <int BITS>
+__device__ __forceinline__ uint32_t block_word(const QChunk<BITS>& q, int j) {
+    if constexpr (BITS == 4) {
+        return q.w[j];
+    } else if constexpr (BITS == 2) {
+        // byte 2(j&1) -> byte 0, byte 2(j&1)+1 -> byte 2 of the result
+        const uint32_t w = q.w[j >> 1];
+        return __builtin_amdgcn_perm(w, w, (j & 1) ? 0x03030202u : 0x01010000u);
+    } else {
+        // the 24 bits of codes 8j..8j+7 start at bit 24j of the 96-bit chunk
+        uint32_t u;
+        if (j == 0) u = q.w[0];
+        else if (j == 1) u = (uint32_t)((((uint64_t)q.w[1] << 32) | q.w[0]) >> 24);
+        else if (j == 2) u = (uint32_t)((((uint64_t)q.w[2] << 32) | q.w[1]) >> 16);
+        else u = q.w[2] >> 8;
+        // codes 4..7 (bits 12..23) move up to bits 16..27
+        return (u & 0x0000FFFFu) | ((u << 4) & 0xFFFF0000u);
+    }
+}
+
+// Σ_k q_k x_k over the 32 codes of a BITS-bit chunk (fp32 accumulate), the
+// int4 dot generalised: with t = block_word(j) and M = 2^BITS − 1 in both
+// halves, (t & M) | 0x6400 pairs give codes 8j, 8j+4 as 1024 + q and
+// (t & M<<BITS) | 0x6400 gives 8j+1, 8j+5 as 1024 + 2^BITS·q (all exact
+// fp16); t >> 2·BITS gives 8j+2, 8j+6 and 8j+3, 8j+7 the same way. The
+// activation pairs and offsets are the int4 chunk's, so
+//     Σ q·x = (accA − ca) + (accB − cb) / 2^BITS.
+// At BITS == 4 this is dot_q4_chunk operation for operation.
+template <int BITS>
+__device__ __forceinline__ float dot_chunk(const QChunk<BITS>& q, const XChunk& xc) {
+    constexpr uint32_t M = (1u << BITS) - 1u;
+    constexpr uint32_t MA = M | (M << 16);
+    constexpr uint32_t MB = MA << BITS;
+    float acc_a = 0.0f, acc_b = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t t = block_word<BITS>(q, j);
+        const uint32_t t2 = t >> (2 * BITS);
+        const h2 q0 = __builtin_bit_cast(h2, (t & MA) | 0x64006400u);
+        const h2 q1 = __builtin_bit_cast(h2, (t & MB) | 0x64006400u);
+        const h2 q2 = __builtin_bit_cast(h2, (t2 & MA) | 0x64006400u);
+        const h2 q3 = __builtin_bit_cast(h2, (t2 & MB) | 0x64006400u);
+        acc_a = __builtin_amdgcn_fdot2(q0, xc.p[4 * j + 0], acc_a, false);
+        acc_b = __builtin_amdgcn_fdot2(q1, xc.p[4 * j + 1], acc_b, false);
+        acc_a = __builtin_amdgcn_fdot2(q2, xc.p[4 * j + 2], acc_a, false);
+        acc_b = __builtin_amdgcn_fdot2(q3, xc.p[4 * j + 3], acc_b, false);
+    }
+    return fmaf(acc_b - xc.cb, 1.0f / (float)(1u << BITS), acc_a - xc.ca);
+}
+
 // Σ_i q_i * x_i over the 16 int8 codes of one 16-byte chunk, fp32 operands.
 __device__ __forceinline__ float dot16_q8(const uint4 w, const float* x) {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};

@@ -61,7 +61,8 @@ __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, 
 // segment. STAGE_FIRST: finish staging x before the first weight loads, so
 // the staging's registers are free before the weight registers fill (one
 // memory latency later start, worth it for long launches: higher occupancy).
-template <int SEG, int P, int R, bool NORM, bool STAGE_FIRST = false, typename Out>
+// BITS: code width of the weight rows (2, 3 or 4; rows of n·BITS/8 bytes).
+template <int SEG, int P, int R, bool NORM, bool STAGE_FIRST = false, int BITS = 4, typename Out>
 __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __restrict__ x, uint32_t n,
                                         Out out) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
@@ -70,15 +71,15 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
     const uint32_t wave = threadIdx.x >> 6;
     constexpr uint32_t nwaves = NT / 64;
     const uint32_t sl = lane & (SEG - 1);
-    const uint32_t lpr = n >> 5;              // 16-byte chunks per row
-    const uint32_t row_bytes = n >> 1;
+    const uint32_t lpr = n >> 5;              // 32-code chunks per row
+    const uint32_t row_bytes = (n >> 3) * BITS;
     const uint32_t ngroups = n >> 6;
     constexpr uint32_t spw = kWave / SEG;     // segments per wave
     const uint32_t seg_id = (blockIdx.x * nwaves + wave) * spw + lane / SEG;
     const uint32_t seg_total = gridDim.x * nwaves * spw;
     const uint32_t total = mats.total_rows;
 
-    uint4 wv[R][P];
+    QChunk<BITS> wv[R][P];
     uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
     auto issue = [&](uint32_t grp) {
 #pragma unroll
@@ -90,7 +91,7 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
                 for (int p = 0; p < P; ++p) {
                     const uint32_t c = sl + p * SEG;
                     if (c < lpr) {
-                        wv[r][p] = ldg16_stream(q.w + 16u * c);
+                        wv[r][p] = ldg_chunk<BITS>(q.w, c);
                         sr[r][p] = q.s[c >> 1];
                         br[r][p] = q.b[c >> 1];
                     }
@@ -115,7 +116,7 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
                 if (c < lpr) {
                     XChunk xc;
                     read_xpairs(xp, c, xc);
-                    const float d = dot_q4_chunk(wv[r][p], xc);
+                    const float d = dot_chunk<BITS>(wv[r][p], xc);
                     acc[r] = fmaf(h2f((uint16_t)sr[r][p]), d, acc[r]);
                     acc[r] = fmaf(h2f((uint16_t)br[r][p]), xc.sum, acc[r]);
                 }
@@ -131,11 +132,11 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
     }
 }
 
-template <int SEG, int P, int R, bool NORM>
+template <int SEG, int P, int R, bool NORM, int BITS = 4>
 __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_t* __restrict__ x,
                                               uint32_t n) {
-    const uint32_t row_bytes = n >> 1, ngroups = n >> 6;
-    q4_rows<SEG, P, R, NORM>(mats, x, n, [&](uint32_t row, float v) {
+    const uint32_t row_bytes = (n >> 3) * BITS, ngroups = n >> 6;
+    q4_rows<SEG, P, R, NORM, false, BITS>(mats, x, n, [&](uint32_t row, float v) {
         const Q4Row q = resolve_row(mats, row, row_bytes, ngroups);
         *q.y = f2h(q.r ? h2f(*q.r) + v : v);
     });

@@ -38,8 +38,9 @@ struct GateUpRow {
 // `rowfn(row)` -> GateUpRow, `out(row, act)` for live rows (lane 0 of the
 // segment). `prologue()` runs after the x loads are issued and before the
 // first weight loads (routing: it makes rowfn's expert indices available).
-// NORM == false: x is staged as is (norm ignored).
-template <int SEG, int P, int R, bool NORM, typename Pro, typename RowFn, typename OutFn>
+// NORM == false: x is staged as is (norm ignored). BITS: code width of the
+// rows (2, 3 or 4).
+template <int SEG, int P, int R, bool NORM, int BITS, typename Pro, typename RowFn, typename OutFn>
 __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uint32_t D, uint32_t total,
                                              const NormArg& norm, Pro prologue, RowFn rowfn, OutFn out) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
@@ -53,7 +54,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
     const uint32_t seg_id = (blockIdx.x * nwaves + wave) * spw + lane / SEG;
     const uint32_t seg_total = gridDim.x * nwaves * spw;
 
-    uint4 gv[R][P], uv[R][P];
+    QChunk<BITS> gv[R][P], uv[R][P];
     uint32_t gsr[R][P], gbr[R][P], usr[R][P], ubr[R][P];    // raw fp16 scales / biases
     auto issue = [&](uint32_t grp) {
 #pragma unroll
@@ -66,8 +67,8 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
                     for (int p = 0; p < P; ++p) {
                         const uint32_t c = sl + p * SEG;
                         if (c < lpr) {
-                            gv[r][p] = ldg16_stream(q.gw + 16u * c);
-                            uv[r][p] = ldg16_stream(q.uw + 16u * c);
+                            gv[r][p] = ldg_chunk<BITS>(q.gw, c);
+                            uv[r][p] = ldg_chunk<BITS>(q.uw, c);
                             gsr[r][p] = q.gs[c >> 1];
                             gbr[r][p] = q.gb[c >> 1];
                             usr[r][p] = q.us[c >> 1];
@@ -95,8 +96,8 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
                 if (c < lpr) {
                     XChunk xc;
                     read_xpairs(xp, c, xc);
-                    const float gd = dot_q4_chunk(gv[r][p], xc);
-                    const float ud = dot_q4_chunk(uv[r][p], xc);
+                    const float gd = dot_chunk<BITS>(gv[r][p], xc);
+                    const float ud = dot_chunk<BITS>(uv[r][p], xc);
                     ga[r] = fmaf(h2f((uint16_t)gsr[r][p]), gd, ga[r]);
                     ga[r] = fmaf(h2f((uint16_t)gbr[r][p]), xc.sum, ga[r]);
                     ua[r] = fmaf(h2f((uint16_t)usr[r][p]), ud, ua[r]);
@@ -119,9 +120,10 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
 }
 
 // Row `row` of phase 1 given the slot it belongs to and that slot's expert.
+template <int BITS>
 __device__ __forceinline__ GateUpRow expert_gate_up_row(const ExpertPool& pool, uint32_t slot, uint32_t e,
                                                         uint32_t f, uint32_t top_k, uint32_t D) {
-    const uint32_t row_bytes = D >> 1;
+    const uint32_t row_bytes = (D >> 3) * BITS;
     const uint32_t ngroups = D >> 6;
     GateUpRow q{};
     q.live = slot < top_k;                          // moe.metal:387 semantics
@@ -140,7 +142,7 @@ __device__ __forceinline__ GateUpRow expert_gate_up_row(const ExpertPool& pool, 
 // Phase 1 over n_active slots (active_slots == nullptr: slots 0..n_active-1).
 // The (slot, expert) of every active index is read once per block into LDS
 // (n_active <= kRouterMaxTopK, checked by the host).
-template <int SEG, int P, int R, bool NORM>
+template <int SEG, int P, int R, bool NORM, int BITS = 4>
 __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint32_t* __restrict__ active_slots, uint32_t n_active,
                                            uint32_t top_k, const uint16_t* __restrict__ x,
@@ -148,7 +150,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
                                            const NormArg& norm) {
     __shared__ uint32_t act_slot[kRouterMaxTopK];
     __shared__ uint32_t act_expert[kRouterMaxTopK];
-    gate_up_rows<SEG, P, R, NORM>(
+    gate_up_rows<SEG, P, R, NORM, BITS>(
         x, D, n_active * F, norm,
         [&]() {
             if (threadIdx.x < n_active) {
@@ -160,7 +162,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
         },
         [&](uint32_t row) {
             const uint32_t a = row / F;
-            return expert_gate_up_row(pool, act_slot[a], act_expert[a], row % F, top_k, D);
+            return expert_gate_up_row<BITS>(pool, act_slot[a], act_expert[a], row % F, top_k, D);
         },
         [&](uint32_t row, float act) { acts[(size_t)act_slot[row / F] * F + row % F] = f2h(act); });
 }
@@ -171,7 +173,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
 // the experts. Block 0 publishes indices and fp16 / fp32 weights for
 // phase 2 and the caller (MoE.encodeRouterGemma4's outputs,
 // S/Kernels/MoE/MoE.swift:147-197).
-template <int SEG, int P, int R, bool NORM>
+template <int SEG, int P, int R, bool NORM, int BITS = 4>
 __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const float* __restrict__ logits,
                                                   const uint16_t* __restrict__ gain, uint32_t E, uint32_t top_k,
                                                   uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w,
@@ -181,7 +183,7 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
     __shared__ __attribute__((aligned(16))) float stage[kRouterMaxExperts];
     __shared__ uint32_t sel_idx[kRouterMaxTopK];
     __shared__ float sel_val[kRouterMaxTopK];
-    gate_up_rows<SEG, P, R, NORM>(
+    gate_up_rows<SEG, P, R, NORM, BITS>(
         x, D, top_k * F, norm,
         [&]() {
             for (uint32_t e = threadIdx.x; e < ((E + 3) & ~3u); e += kThreads)
@@ -201,7 +203,9 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
                 }
             }
         },
-        [&](uint32_t row) { return expert_gate_up_row(pool, row / F, sel_idx[row / F], row % F, top_k, D); },
+        [&](uint32_t row) {
+            return expert_gate_up_row<BITS>(pool, row / F, sel_idx[row / F], row % F, top_k, D);
+        },
         [&](uint32_t row, float act) { acts[(size_t)(row / F) * F + row % F] = f2h(act); });
 }
 
@@ -212,7 +216,7 @@ __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& u
                                                uint32_t D, uint32_t F, const NormArg& norm) {
     const uint32_t row_bytes = D >> 1;
     const uint32_t ngroups = D >> 6;
-    gate_up_rows<SEG, P, R, NORM>(
+    gate_up_rows<SEG, P, R, NORM, 4>(
         x, D, F, norm, [] {},
         [&](uint32_t f) {
             GateUpRow q{};
@@ -233,8 +237,8 @@ constexpr uint32_t kPhase2Chunks = 4;     // 16-byte act pieces per thread: top_
 
 // Phase 2: 8 slots × 8-lane segments per wave; P chunks of 32 per lane
 // (F <= 256*P); R output rows per wave in flight. Dynamic LDS:
-// xpairs_lds_bytes(top_k*F).
-template <int P, int R>
+// xpairs_lds_bytes(top_k*F). BITS: code width of the down rows.
+template <int P, int R, int BITS = 4>
 __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint16_t* __restrict__ acts,
                                            const uint16_t* __restrict__ rw,
@@ -250,7 +254,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
     const uint32_t slot = lane >> 3;
     const uint32_t sl = lane & (SEG - 1);
     const uint32_t lpr = F >> 5;
-    const uint32_t row_bytes = F >> 1;
+    const uint32_t row_bytes = (F >> 3) * BITS;
     const uint32_t ngroups = F >> 6;
     const bool live = slot < top_k;
     const uint32_t wave_id = blockIdx.x * nwaves + wave;
@@ -269,7 +273,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
     const uint16_t* ds = reinterpret_cast<const uint16_t*>(blob + pool.off.down_s);
     const uint16_t* db = reinterpret_cast<const uint16_t*>(blob + pool.off.down_b);
 
-    uint4 wv[R][P];
+    QChunk<BITS> wv[R][P];
     uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
     auto issue = [&](uint32_t grp) {
 #pragma unroll
@@ -280,7 +284,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                 for (int p = 0; p < P; ++p) {
                     const uint32_t c = sl + p * SEG;
                     if (c < lpr) {
-                        wv[r][p] = ldg16_stream(dw + (size_t)d * row_bytes + 16u * c);
+                        wv[r][p] = ldg_chunk<BITS>(dw + (size_t)d * row_bytes, c);
                         sr[r][p] = ds[(size_t)d * ngroups + (c >> 1)];
                         br[r][p] = db[(size_t)d * ngroups + (c >> 1)];
                     }
@@ -304,7 +308,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                     if (c < lpr) {
                         XChunk xc;
                         read_xpairs(xp, slot * lpr + c, xc);
-                        const float dd = dot_q4_chunk(wv[r][p], xc);
+                        const float dd = dot_chunk<BITS>(wv[r][p], xc);
                         acc[r] = fmaf(h2f((uint16_t)sr[r][p]), dd, acc[r]);
                         acc[r] = fmaf(h2f((uint16_t)br[r][p]), xc.sum, acc[r]);
                     }

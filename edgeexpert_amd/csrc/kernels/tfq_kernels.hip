@@ -21,16 +21,19 @@ constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
 
 // Each int4 GEMV-family shape comes in two forms: plain (x staged as is) and
 // _norm (x normalised while staged, NormArg); the plain form needs fewer
-// registers and so runs more wavefronts per SIMD.
-#define TFQ_Q4_GEMV(SEG, P)                                                                      \
-    extern "C" __global__ __launch_bounds__(256) void tfq_q4_gemv_s##SEG##_p##P(                 \
+// registers and so runs more wavefronts per SIMD. The 2- and 3-bit forms of
+// a kernel carry the width in the name (tfq_q3_gemv_*, tfq_moe_phase1_b3_*).
+#define TFQ_GEMV_FORMS(TAG, BITS, SEG, P)                                                        \
+    extern "C" __global__ __launch_bounds__(256) void tfq_##TAG##_gemv_s##SEG##_p##P(            \
         Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
-        q4_gemv_multi<SEG, P, kRowsInFlight, false>(mats, x, n);                                  \
+        q4_gemv_multi<SEG, P, kRowsInFlight, false, BITS>(mats, x, n);                            \
     }                                                                                            \
-    extern "C" __global__ __launch_bounds__(256) void tfq_q4_gemv_norm_s##SEG##_p##P(            \
+    extern "C" __global__ __launch_bounds__(256) void tfq_##TAG##_gemv_norm_s##SEG##_p##P(       \
         Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
-        q4_gemv_multi<SEG, P, kRowsInFlight, true>(mats, x, n);                                   \
+        q4_gemv_multi<SEG, P, kRowsInFlight, true, BITS>(mats, x, n);                             \
     }
+#define TFQ_Q4_GEMV(SEG, P) TFQ_GEMV_FORMS(q4, 4, SEG, P)
+#define TFQ_Q3_GEMV(SEG, P) TFQ_GEMV_FORMS(q3, 3, SEG, P)
 
 #define TFQ_Q8_GEMV(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_q8_gemv_s##SEG##_p##P(                 \
@@ -68,36 +71,51 @@ constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
                               logits + (size_t)blockIdx.y * E, E, d);                            \
     }
 
-#define TFQ_PHASE1_FORM(NAME, NORM, SEG, P)                                                      \
+#define TFQ_PHASE1_FORM(NAME, NORM, BITS, SEG, P)                                                \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         ExpertPool pool, const uint32_t* indices, const uint32_t* active_slots,                  \
         uint32_t n_active, uint32_t top_k, const uint16_t* x, uint16_t* acts, uint32_t D,        \
         uint32_t F, NormArg norm) {                                                               \
-        moe_phase1<SEG, P, kRowsInFlight, NORM>(pool, indices, active_slots, n_active, top_k, x,  \
-                                                acts, D, F, norm);                                \
+        moe_phase1<SEG, P, kRowsInFlight, NORM, BITS>(pool, indices, active_slots, n_active,     \
+                                                      top_k, x, acts, D, F, norm);                \
     }
 #define TFQ_PHASE1(SEG, P)                                                                       \
-    TFQ_PHASE1_FORM(tfq_moe_phase1_s##SEG##_p##P, false, SEG, P)                                 \
-    TFQ_PHASE1_FORM(tfq_moe_phase1_norm_s##SEG##_p##P, true, SEG, P)
+    TFQ_PHASE1_FORM(tfq_moe_phase1_s##SEG##_p##P, false, 4, SEG, P)                              \
+    TFQ_PHASE1_FORM(tfq_moe_phase1_norm_s##SEG##_p##P, true, 4, SEG, P)
+#define TFQ_PHASE1_B(SEG, P)                                                                     \
+    TFQ_PHASE1_FORM(tfq_moe_phase1_b2_s##SEG##_p##P, false, 2, SEG, P)                           \
+    TFQ_PHASE1_FORM(tfq_moe_phase1_b2_norm_s##SEG##_p##P, true, 2, SEG, P)                       \
+    TFQ_PHASE1_FORM(tfq_moe_phase1_b3_s##SEG##_p##P, false, 3, SEG, P)                           \
+    TFQ_PHASE1_FORM(tfq_moe_phase1_b3_norm_s##SEG##_p##P, true, 3, SEG, P)
 
-#define TFQ_PHASE1_ROUTED_FORM(NAME, NORM, SEG, P)                                               \
+#define TFQ_PHASE1_ROUTED_FORM(NAME, NORM, BITS, SEG, P)                                         \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         ExpertPool pool, const float* logits, const uint16_t* gain, uint32_t E, uint32_t top_k,  \
         uint32_t* out_idx, uint16_t* out_w, float* out_wf, const uint16_t* x, uint16_t* acts,    \
         uint32_t D, uint32_t F, NormArg norm) {                                                   \
-        moe_phase1_routed<SEG, P, kRowsInFlight, NORM>(pool, logits, gain, E, top_k, out_idx,    \
-                                                       out_w, out_wf, x, acts, D, F, norm);       \
+        moe_phase1_routed<SEG, P, kRowsInFlight, NORM, BITS>(pool, logits, gain, E, top_k,       \
+                                                             out_idx, out_w, out_wf, x, acts, D, \
+                                                             F, norm);                            \
     }
 #define TFQ_PHASE1_ROUTED(SEG, P)                                                                \
-    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_s##SEG##_p##P, false, SEG, P)                   \
-    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_norm_s##SEG##_p##P, true, SEG, P)
+    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_s##SEG##_p##P, false, 4, SEG, P)                \
+    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_norm_s##SEG##_p##P, true, 4, SEG, P)
+#define TFQ_PHASE1_ROUTED_B(SEG, P)                                                              \
+    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_b2_s##SEG##_p##P, false, 2, SEG, P)             \
+    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_b2_norm_s##SEG##_p##P, true, 2, SEG, P)         \
+    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_b3_s##SEG##_p##P, false, 3, SEG, P)             \
+    TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_b3_norm_s##SEG##_p##P, true, 3, SEG, P)
 
-#define TFQ_PHASE2(P)                                                                            \
-    extern "C" __global__ __launch_bounds__(256) void tfq_moe_phase2_p##P(                       \
+#define TFQ_PHASE2_FORM(NAME, BITS, P)                                                           \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         ExpertPool pool, const uint32_t* indices, const uint16_t* acts, const uint16_t* rw,      \
         const uint16_t* residual, uint16_t* y, uint32_t D, uint32_t F, uint32_t top_k) {         \
-        moe_phase2<P, kRowsInFlight>(pool, indices, acts, rw, residual, y, D, F, top_k);          \
+        moe_phase2<P, kRowsInFlight, BITS>(pool, indices, acts, rw, residual, y, D, F, top_k);    \
     }
+#define TFQ_PHASE2(P)                                                                            \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_p##P, 4, P)                                                   \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_b2_p##P, 2, P)                                                \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_b3_p##P, 3, P)
 
 #define TFQ_LM_HEAD(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_lm_head_greedy_s##SEG##_p##P(          \
@@ -115,7 +133,7 @@ constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
     TFQ_GATE_UP_FORM(tfq_gate_up_act_s##SEG##_p##P, false, SEG, P)                               \
     TFQ_GATE_UP_FORM(tfq_gate_up_act_norm_s##SEG##_p##P, true, SEG, P)
 
-// int4: n/32 chunks per row; (SEG, P) with SEG·P >= chunks (the host picks
+// n/32 chunks (of 32 codes) per row at every code width; (SEG, P) with SEG·P >= chunks (the host picks
 // the pair that wastes the fewest lanes).
 #define TFQ_Q4_TABLE(X) X(2, 1) X(4, 1) X(8, 1) X(8, 2) X(8, 3) X(8, 4) X(16, 1) X(16, 2) X(16, 3) \
     X(16, 4) X(32, 1) X(32, 2) X(32, 3) X(32, 4) X(64, 1) X(64, 2) X(64, 3) X(64, 4)
@@ -123,8 +141,11 @@ constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
 #define TFQ_Q8_TABLE(X) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 3) X(64, 4)
 
 TFQ_Q4_TABLE(TFQ_Q4_GEMV)
+TFQ_Q4_TABLE(TFQ_Q3_GEMV)
 TFQ_Q4_TABLE(TFQ_PHASE1)
+TFQ_Q4_TABLE(TFQ_PHASE1_B)
 TFQ_Q4_TABLE(TFQ_PHASE1_ROUTED)
+TFQ_Q4_TABLE(TFQ_PHASE1_ROUTED_B)
 TFQ_Q4_TABLE(TFQ_GATE_UP)
 TFQ_Q4_TABLE(TFQ_LM_HEAD)
 TFQ_Q8_TABLE(TFQ_Q8_GEMV)

@@ -78,21 +78,27 @@ class DequantInt4GEMV:
         self.ctx = context
 
     def encode(self, stream, weights, scales, biases, x, y, m, n, weights_offset=0,
-               scales_offset=0, biases_offset=0, x_offset=0, y_offset=0):
-        check(lib().tfq_gemv_q4g64(self.ctx.handle, _s(stream), _addr(weights, weights_offset),
-                                   _addr(scales, scales_offset), _addr(biases, biases_offset),
-                                   _addr(x, x_offset), _addr(y, y_offset), m, n),
-              "DequantInt4GEMV.encode")
+               scales_offset=0, biases_offset=0, x_offset=0, y_offset=0, bits=4):
+        """bits: 4, or 3 for the 3-bit rows (DequantInt4GEMV.swift:140-180)."""
+        args = (self.ctx.handle, _s(stream), _addr(weights, weights_offset), _addr(scales, scales_offset),
+                _addr(biases, biases_offset), _addr(x, x_offset), _addr(y, y_offset), m, n)
+        if bits == 4:
+            check(lib().tfq_gemv_q4g64(*args), "DequantInt4GEMV.encode")
+        else:
+            check(lib().tfq_gemv_qg64(*args, bits), "DequantInt4GEMV.encode")
 
     encode_tgx = encode   # x always staged in LDS: encodeTgx is the same launch
 
     def encode_qkv(self, stream, q: Q4Projection, k: Q4Projection, v: Q4Projection, x, yq, yk, yv,
-                   mq, mkv, n):
+                   mq, mkv, n, bits=4):
         """FusedQKVGEMV.encode (S/Kernels/Fusions/FusedQKVGEMV.swift:92-156)."""
         qd, kd, vd = q.desc(), k.desc(), v.desc()
-        check(lib().tfq_gemv_q4g64_qkv(self.ctx.handle, _s(stream), C.byref(qd), C.byref(kd),
-                                       C.byref(vd), _addr(x), _addr(yq), _addr(yk), _addr(yv), mq,
-                                       mkv, n), "FusedQKVGEMV.encode")
+        args = (self.ctx.handle, _s(stream), C.byref(qd), C.byref(kd), C.byref(vd), _addr(x), _addr(yq),
+                _addr(yk), _addr(yv), mq, mkv, n)
+        if bits == 4:
+            check(lib().tfq_gemv_q4g64_qkv(*args), "FusedQKVGEMV.encode")
+        else:
+            check(lib().tfq_gemv_qg64_qkv(*args, bits), "FusedQKVGEMV.encode")
 
 
 class DequantInt8GEMV:
@@ -136,11 +142,13 @@ class ExpertPool:
     num_experts: int
     offsets: dict
     base_offset: int = 0
+    weight_bits: int = 4      # code width of the rows: 2, 3 or 4 (MoE.swift:244 bits:)
 
     def desc(self) -> ExpertPoolDesc:
         o = ExpertOffsets(*[int(self.offsets[k]) for k in (
             "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b")])
-        return ExpertPoolDesc(_addr(self.buffer, self.base_offset), self.stride, self.num_experts, o)
+        return ExpertPoolDesc(_addr(self.buffer, self.base_offset), self.stride, self.num_experts, o,
+                              self.weight_bits)
 
 
 class PackedExpertsLayout:
@@ -188,7 +196,7 @@ class PackedExpertsLayout:
                                          layer, d, f, _addr(pool), pool.nbytes, C.byref(desc),
                                          _addr(inexact_counter)), "tfq_expert_pool_load")
         offs = {k: getattr(desc.offsets, k) for k, _ in ExpertOffsets._fields_}
-        return ExpertPool(pool, desc.stride, desc.num_experts, offs)
+        return ExpertPool(pool, desc.stride, desc.num_experts, offs, weight_bits=desc.weight_bits)
 
     def close(self):
         if self.handle:

@@ -110,6 +110,24 @@ def int4_matrix(seed: int, label: str, rows: int, k: int):
     return packed, s16.reshape(rows, -1), f16_bits(b).reshape(rows, -1)
 
 
+def affine_matrix(seed: int, label: str, rows: int, k: int, bits: int):
+    """Affine g64 matrix of `bits`-bit codes (2, 3 or 4; rows of k*bits/8 bytes,
+    codes packed from the least significant bit). bits == 4 is int4_matrix.
+    Uniform random bytes are uniform codes at every width; scale =
+    |N(0,0.02)|·16/2^bits and bias = -2^(bits-1)·scale + N(0, 0.002) keep the
+    weights' spread that of the int4 matrices."""
+    if bits == 4:
+        return int4_matrix(seed, label, rows, k)
+    assert bits in (2, 3) and k % GROUP == 0
+    nbytes = rows * k * bits // 8
+    packed = splitmix64(seed_key(seed, label + "/q"), (nbytes + 7) // 8).view(np.uint8)[:nbytes]
+    g = rows * (k // GROUP)
+    s = np.abs(normal(seed_key(seed, label + "/s"), g, 0.02)) * np.float32(16 >> bits)
+    s16 = f16_bits(s)
+    b = np.float32(-(1 << (bits - 1))) * f16_to_f32(s16) + normal(seed_key(seed, label + "/b"), g, 0.002)
+    return packed.reshape(rows, -1), s16.reshape(rows, -1), f16_bits(b).reshape(rows, -1)
+
+
 def int8_matrix(seed: int, label: str, rows: int, k: int):
     """Affine int8 g64 router matrix: q ~ U{0..255}, scale = |N(0,0.02)|/16,
     bias = -128*scale + N(0, 0.002) (fp16)."""
@@ -133,13 +151,14 @@ def bf16_vector(seed: int, label: str, n: int, std: float = 1.0) -> np.ndarray:
 
 # ------------------------------------------------------------------ experts ----
 
-def expert_layout(d: int, f: int, align: int = 16384):
+def expert_layout(d: int, f: int, align: int = 16384, bits: int = 4):
     """Blob layout of one routed expert: [gateW, gateS, gateB, upW, upS, upB,
     downW, downS, downB], each sub-tensor contiguous, blob padded to `align`
-    (the repacker's 16 KiB expert stride). Returns (offsets dict, stride)."""
-    gw = f * d // 2
+    (the repacker's 16 KiB expert stride); weights of `bits`-bit codes.
+    Returns (offsets dict, stride)."""
+    gw = f * d * bits // 8
     gs = f * (d // GROUP) * 2
-    dw = d * f // 2
+    dw = d * f * bits // 8
     ds = d * (f // GROUP) * 2
     o = {}
     cur = 0
@@ -154,11 +173,12 @@ def expert_layout(d: int, f: int, align: int = 16384):
 OFFSET_ORDER = ("gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b")
 
 
-def expert_blob(seed: int, label: str, d: int, f: int, offsets: dict, stride: int) -> np.ndarray:
+def expert_blob(seed: int, label: str, d: int, f: int, offsets: dict, stride: int,
+                bits: int = 4) -> np.ndarray:
     """One expert blob of `stride` bytes with BASELINE-distributed gate/up/down."""
     blob = np.zeros(stride, np.uint8)
     for proj, rows, cols in (("gate", f, d), ("up", f, d), ("down", d, f)):
-        w, s, b = int4_matrix(seed, f"{label}/{proj}", rows, cols)
+        w, s, b = affine_matrix(seed, f"{label}/{proj}", rows, cols, bits)
         for part, arr in (("w", w), ("s", s), ("b", b)):
             raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
             off = offsets[f"{proj}_{part}"]
@@ -166,19 +186,21 @@ def expert_blob(seed: int, label: str, d: int, f: int, offsets: dict, stride: in
     return blob
 
 
-def expert_pool(seed: int, label: str, num_experts: int, d: int, f: int, align: int = 16384):
+def expert_pool(seed: int, label: str, num_experts: int, d: int, f: int, align: int = 16384,
+                bits: int = 4):
     """All experts of one layer, concatenated at a fixed stride."""
-    offsets, stride = expert_layout(d, f, align)
+    offsets, stride = expert_layout(d, f, align, bits)
     pool = np.zeros(num_experts * stride, np.uint8)
     for e in range(num_experts):
-        pool[e * stride:(e + 1) * stride] = expert_blob(seed, f"{label}/e{e}", d, f, offsets, stride)
+        pool[e * stride:(e + 1) * stride] = expert_blob(seed, f"{label}/e{e}", d, f, offsets, stride, bits)
     return pool, offsets, stride
 
 
-def blob_views(blob: np.ndarray, offsets: dict, d: int, f: int, proj: str):
-    """(W u8 [rows][cols/2], S u16 [rows][cols/64], B u16) views into one expert blob."""
+def blob_views(blob: np.ndarray, offsets: dict, d: int, f: int, proj: str, bits: int = 4):
+    """(W u8 [rows][cols*bits/8], S u16 [rows][cols/64], B u16) views into one expert blob."""
     rows, cols = (f, d) if proj in ("gate", "up") else (d, f)
-    w = blob[offsets[f"{proj}_w"]:offsets[f"{proj}_w"] + rows * cols // 2].reshape(rows, cols // 2)
+    rb = cols * bits // 8
+    w = blob[offsets[f"{proj}_w"]:offsets[f"{proj}_w"] + rows * rb].reshape(rows, rb)
     ng = rows * (cols // GROUP)
     s = blob[offsets[f"{proj}_s"]:offsets[f"{proj}_s"] + 2 * ng].view(np.uint16).reshape(rows, -1)
     b = blob[offsets[f"{proj}_b"]:offsets[f"{proj}_b"] + 2 * ng].view(np.uint16).reshape(rows, -1)

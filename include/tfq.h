@@ -88,6 +88,21 @@ int tfq_gemv_q4g64_qkv(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *q,
                        uint16_t *yq, uint16_t *yk, uint16_t *yv, uint32_t mq, uint32_t mkv,
                        uint32_t n);
 
+/* tfq_gemv_q4g64 at `bits` = 3 or 4 bits per code (rows of n*bits/8 bytes,
+ * codes packed from the least significant bit, Quantization.swift:195-201).
+ * Replaces DequantInt4GEMV.encode(..., bits:) with its 3-bit kernels
+ * (DequantInt4GEMV.swift:140-180, dequant_int4.metal:512-717). Other bit
+ * widths: TFQ_E_INVAL (the reference's precondition, :149-150). */
+int tfq_gemv_qg64(tfq_ctx *ctx, void *stream, const void *weights, const uint16_t *scales,
+                  const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m, uint32_t n,
+                  uint32_t bits);
+
+/* tfq_gemv_q4g64_qkv at `bits` = 3 or 4. Replaces FusedQKVGEMV.encode(...,
+ * bits:) (FusedQKVGEMV.swift:100-156). */
+int tfq_gemv_qg64_qkv(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *q, const tfq_q4_matrix *k,
+                      const tfq_q4_matrix *v, const uint16_t *x, uint16_t *yq, uint16_t *yk,
+                      uint16_t *yv, uint32_t mq, uint32_t mkv, uint32_t n, uint32_t bits);
+
 /* y[m] = W8[m][n] · x[n]; int8 g64 weights. Replaces DequantInt8GEMV.encode
  * (S/Kernels/Quant/DequantInt8GEMV.swift:50-81).
  * Contract: n % 64 == 0, n <= 4096, weights 16-byte aligned. */
@@ -155,6 +170,12 @@ typedef struct {
  * at base + e*stride. Replaces the argument buffer of per-slot blob
  * pointers (S/Kernels/MoE/MoE.swift:398-409): the address is computed on the
  * device from the router's index buffer, so no host round trip is needed.
+ * weight_bits: code width of every gate/up/down row, 2, 3 or 4 (0 means 4,
+ * the default of the reference's `bits:` argument, MoE.swift:244,281,324);
+ * a row of n codes takes n*bits/8 bytes, codes packed from the least
+ * significant bit (Quantization.swift:195-201). The decode entry points
+ * (phase 1, phase 2 and the fused forms) run every width; the grouped
+ * prefill ones run 4 bits and return TFQ_E_UNSUPPORTED otherwise.
  * Contract: base, stride and the *_w offsets 16-byte aligned; *_s/*_b
  * offsets 2-byte aligned. */
 typedef struct {
@@ -162,6 +183,7 @@ typedef struct {
     uint64_t stride;
     uint32_t num_experts;
     tfq_expert_offsets offsets;
+    uint32_t weight_bits;
 } tfq_expert_pool;
 
 /* Phase 1: acts[slot][f] = fp16(gelu_tanh(gate_e[f]·x) * (up_e[f]·x)), e =

@@ -52,7 +52,8 @@ int tfq_expert_layout_offsets(const tfq_expert_layout *layout, uint32_t layer, t
                               char *file, size_t file_capacity);
 
 /* Stride and total bytes of the device pool tfq_expert_pool_load writes for
- * one layer of experts with hidden size d and intermediate size f. */
+ * one layer of experts with hidden size d and intermediate size f, at the
+ * widest code width of the layout's layers (so any layer fits). */
 int tfq_expert_pool_bytes(const tfq_expert_layout *layout, uint32_t d, uint32_t f, uint64_t *stride,
                           uint64_t *bytes);
 
@@ -64,10 +65,13 @@ int tfq_expert_pool_bytes(const tfq_expert_layout *layout, uint32_t d, uint32_t 
  * scales/biases converted from the file's BF16 to fp16 on `stream` by
  * tfq_convert_bf16_to_f16 (inexact_count_dev, device uint32 or NULL, counts
  * the values fp16 does not hold exactly). Checks each expert's nine
- * sub-tensors: U32 4-bit weights of logical shape [f, d] (gate, up) and
- * [d, f] (down), BF16 scales/biases [rows, cols/64], extents inside the
- * blob; TFQ_E_IO for a missing or short layer file
- * (ModelError.missingFile "packed_experts/<file>"). Fills *desc for the MoE
+ * sub-tensors: U32 weights of logical shape [f, d] (gate, up) and [d, f]
+ * (down) whose `bits` is 4 (the repacker) or 2 / 3 (TurboFieldfareRebits,
+ * Sources/TurboFieldfareRebits/main.swift:418-441: rows of cols*bits/8
+ * bytes), one width for the whole layer (else TFQ_E_UNSUPPORTED), BF16
+ * scales/biases [rows, cols/64], extents inside the blob; TFQ_E_IO for a
+ * missing or short layer file (ModelError.missingFile
+ * "packed_experts/<file>"). Fills *desc, weight_bits included, for the MoE
  * calls. Reads the file on the calling thread; the copies and conversions
  * are queued on `stream`, which the call synchronises before returning. */
 int tfq_expert_pool_load(tfq_ctx *ctx, void *stream, const tfq_expert_layout *layout, const char *model_dir,

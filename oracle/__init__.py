@@ -114,6 +114,12 @@ def _declare(L):
     d("tfo_dequantize_int4_row", None, _P, _P, _P, C.c_int, C.c_int, _P)
     d("tfo_dequantize_int8_row", None, _P, _P, _P, C.c_int, C.c_int, _P)
     d("tfo_int4_code", C.c_uint32, _P, C.c_size_t)
+    d("tfo_affine_row_bytes", C.c_size_t, C.c_size_t, C.c_int)
+    d("tfo_pack_affine_code", None, _P, C.c_size_t, C.c_uint32, C.c_size_t, C.c_int)
+    d("tfo_affine_code", C.c_uint32, _P, C.c_size_t, C.c_size_t, C.c_int)
+    d("tfo_quantize_affine_row", None, _P, C.c_int, C.c_int, _P, _P, _P)
+    d("tfo_dequantize_affine_row", None, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P)
+    d("tfo_gemv_affine", None, _P, _P, _P, C.c_int, C.c_int, _P, C.c_int, C.c_int, _P)
     for n in ("tfo_gemv_int4", "tfo_gemv_int8", "tfo_gemv_int4_f64", "tfo_gemv_int8_f64"):
         d(n, None, _P, _P, _P, C.c_int, _P, C.c_int, C.c_int, _P)
     d("tfo_gemv_int4_mt", None, _P, _P, _P, C.c_int, _P, C.c_int, C.c_int, _P, C.c_int)
@@ -123,6 +129,8 @@ def _declare(L):
     d("tfo_ffn_int4", None, _P, C.POINTER(ExpertOffsets), C.c_int, _P, C.c_int, C.c_int, _P)
     d("tfo_moe_routed", None, _P, C.c_uint64, C.POINTER(ExpertOffsets), C.c_int, _P, _P, _P, _P,
       C.c_int, C.c_int, C.c_int, _P)
+    d("tfo_moe_routed_bits", None, _P, C.c_uint64, C.POINTER(ExpertOffsets), C.c_int, C.c_int, _P, _P, _P,
+      _P, C.c_int, C.c_int, C.c_int, _P)
     d("tfo_shared_expert_int4", None, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int,
       C.c_int, _P)
     d("tfo_group_pairs", C.c_int, _P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
@@ -252,6 +260,49 @@ def int4_code(packed_row, j: int) -> int:
     return lib().tfo_int4_code(_ptr(_c(packed_row, np.uint8)), j)
 
 
+# 2-, 3- and 4-bit rows (QuantizedAffineRow, Quantization.swift:195-349)
+
+def affine_row_bytes(n: int, bits: int) -> int:
+    return lib().tfo_affine_row_bytes(n, bits)
+
+
+def pack_affine_codes(codes, bits: int):
+    """packCode (Quantization.swift:295-320) of every code in order -> u8[packedRowBytes]."""
+    codes = _c(codes, np.uint32)
+    nbytes = affine_row_bytes(codes.size, bits)
+    buf = np.zeros(max(nbytes, 1), np.uint8)
+    L = lib()
+    for j, q in enumerate(codes.tolist()):
+        L.tfo_pack_affine_code(_ptr(buf), nbytes, q, j, bits)
+    return buf[:nbytes]
+
+
+def affine_codes(row, n: int, bits: int):
+    """unpackCode (Quantization.swift:322-349) of codes 0..n-1."""
+    row = _c(row, np.uint8)
+    L = lib()
+    return np.array([L.tfo_affine_code(_ptr(row), row.size, j, bits) for j in range(n)], np.uint32)
+
+
+def quantize_affine_row(row, bits: int):
+    """quantizeAffine (Quantization.swift:229-273) -> (packed, s bf16, b bf16)."""
+    row = _c(row, np.float32)
+    n = row.size
+    packed = np.zeros(affine_row_bytes(n, bits), np.uint8)
+    s = np.zeros(n // GROUP, np.uint16)
+    b = np.zeros(n // GROUP, np.uint16)
+    lib().tfo_quantize_affine_row(_ptr(row), n, bits, _ptr(packed), _ptr(s), _ptr(b))
+    return packed, s, b
+
+
+def dequantize_affine_row(packed, s, b, fmt, bits: int, n: int):
+    """dequantizeAffine (Quantization.swift:275-293)."""
+    out = np.zeros(n, np.float32)
+    lib().tfo_dequantize_affine_row(_ptr(_c(packed, np.uint8)), _ptr(_c(s, np.uint16)),
+                                    _ptr(_c(b, np.uint16)), fmt, bits, n, _ptr(out))
+    return out
+
+
 # --------------------------------------------------------------- GEMV ----
 
 def _gemv(name, W, S, B, fmt, x, m, n, out_dtype):
@@ -265,6 +316,15 @@ def gemv_int4(W, S, B, x, fmt=FMT_F16):
     """DequantInt4GemvRef.apply (V/Reference/Quant/DequantInt4Gemv.swift:12-42). W: [m][n/2] u8."""
     m, n = W.shape[0], np.asarray(x).size
     return _gemv("tfo_gemv_int4", W, S, B, fmt, x, m, n, np.float32)
+
+
+def gemv_affine(W, S, B, x, bits, fmt=FMT_F16):
+    """gemv_int4 over bits-bit rows (W: [m][n*bits/8] u8)."""
+    W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16); x = _c(x, np.float32)
+    m, n = W.shape[0], x.size
+    y = np.zeros(m, np.float32)
+    lib().tfo_gemv_affine(_ptr(W), _ptr(S), _ptr(B), fmt, bits, _ptr(x), m, n, _ptr(y))
+    return y
 
 
 def gemv_int4_f64(W, S, B, x, fmt=FMT_F16):
@@ -353,15 +413,16 @@ def ffn_int4(blob, off, x, d, f, fmt=FMT_F16):
     return out
 
 
-def moe_routed(pool, stride, off, x, idx, w, d, f, residual=None, fmt=FMT_F16):
-    """MoeRef.applyStreamedRouted (V/Reference/MoE/Moe.swift:58-88)."""
+def moe_routed(pool, stride, off, x, idx, w, d, f, residual=None, fmt=FMT_F16, bits=4):
+    """MoeRef.applyStreamedRouted (V/Reference/MoE/Moe.swift:58-88); experts of
+    `bits`-bit rows (2, 3, 4)."""
     pool = _c(pool, np.uint8); x = _c(x, np.float32)
     idx = _c(idx, np.uint32); w = _c(w, np.float32)
     r = None if residual is None else _c(residual, np.float32)
     y = np.zeros(d, np.float32)
     o = _offsets(off)
-    lib().tfo_moe_routed(_ptr(pool), int(stride), C.byref(o), fmt, _ptr(x), _ptr(r), _ptr(idx),
-                         _ptr(w), idx.size, d, f, _ptr(y))
+    lib().tfo_moe_routed_bits(_ptr(pool), int(stride), C.byref(o), fmt, bits, _ptr(x), _ptr(r), _ptr(idx),
+                              _ptr(w), idx.size, d, f, _ptr(y))
     return y
 
 

@@ -180,6 +180,84 @@ void tfo_dequantize_int4_row(const uint8_t *packed, const uint16_t *scales, cons
     }
 }
 
+/* ---- 2-, 3- and 4-bit rows (Quantization.swift:195-349) ---- */
+
+/* QuantizedAffineRow.packedRowBytes (Quantization.swift:219-222). */
+size_t tfo_affine_row_bytes(size_t n, int bits) { return (n * (size_t)bits + 7) / 8; }
+
+/* Quantization.swift:295-320 (packCode): code j at bits j*bits.. of the
+ * little-endian row, OR-ed in (3-bit: into the byte after as well when the
+ * code straddles a byte boundary and that byte exists). */
+void tfo_pack_affine_code(uint8_t *buf, size_t nbytes, uint32_t code, size_t j, int bits) {
+    if (bits == 4) {
+        size_t i = j / 2;
+        uint8_t nib = (uint8_t)(code & 0x0F);
+        buf[i] = (j & 1) == 0 ? (uint8_t)((buf[i] & 0xF0) | nib) : (uint8_t)((buf[i] & 0x0F) | (nib << 4));
+    } else if (bits == 2) {
+        size_t i = j / 4;
+        unsigned sh = (unsigned)(j % 4) * 2;
+        buf[i] = (uint8_t)((buf[i] & ~(0x03u << sh)) | ((code & 0x03u) << sh));
+    } else {
+        size_t bit = j * 3, i = bit / 8;
+        uint32_t v = (code & 0x07u) << (bit % 8);
+        buf[i] |= (uint8_t)(v & 0xFF);
+        if (i + 1 < nbytes) buf[i + 1] |= (uint8_t)((v >> 8) & 0xFF);
+    }
+}
+
+/* Quantization.swift:322-349 (unpackCode); bytes past the row read as 0. */
+uint32_t tfo_affine_code(const uint8_t *row, size_t nbytes, size_t j, int bits) {
+    if (bits == 4) return (j & 1) ? (uint32_t)(row[j / 2] >> 4) : (uint32_t)(row[j / 2] & 0x0F);
+    if (bits == 2) return (uint32_t)(row[j / 4] >> ((j % 4) * 2)) & 0x03u;
+    size_t bit = j * 3, i = bit / 8;
+    uint32_t b0 = row[i], b1 = i + 1 < nbytes ? row[i + 1] : 0, b2 = i + 2 < nbytes ? row[i + 2] : 0;
+    return ((b0 | (b1 << 8) | (b2 << 16)) >> (bit % 8)) & 0x07u;
+}
+
+/* Quantization.swift:229-273 (quantizeAffine): BF16-rounded scale/bias first,
+ * codes against the rounded values, qMax = 2^bits - 1. */
+void tfo_quantize_affine_row(const float *row, int n, int bits, uint8_t *packed, uint16_t *scales,
+                             uint16_t *biases) {
+    const int qmax = (1 << bits) - 1;
+    const size_t nbytes = tfo_affine_row_bytes((size_t)n, bits);
+    memset(packed, 0, nbytes);
+    for (int g = 0; g < n / TFO_GROUP; ++g) {
+        float wmin = INFINITY, wmax = -INFINITY;
+        for (int k = 0; k < TFO_GROUP; ++k) {
+            float w = row[g * TFO_GROUP + k];
+            if (w < wmin) wmin = w;
+            if (w > wmax) wmax = w;
+        }
+        float scale_f = wmax == wmin ? 1.0f : (wmax - wmin) / (float)qmax;
+        uint16_t sb = tfo_f32_to_bf16(scale_f), bb = tfo_f32_to_bf16(wmin);
+        scales[g] = sb;
+        biases[g] = bb;
+        float scale = tfo_bf16_to_f32(sb), bias = tfo_bf16_to_f32(bb);
+        float inv = scale == 0.0f ? 0.0f : 1.0f / scale;
+        for (int k = 0; k < TFO_GROUP; ++k) {
+            long q = (long)roundf((row[g * TFO_GROUP + k] - bias) * inv);
+            if (q < 0) q = 0;
+            if (q > qmax) q = qmax;
+            tfo_pack_affine_code(packed, nbytes, (uint32_t)q, (size_t)g * TFO_GROUP + k, bits);
+        }
+    }
+}
+
+/* Quantization.swift:275-293 (dequantizeAffine): Float(code) * scale + bias. */
+void tfo_dequantize_affine_row(const uint8_t *packed, const uint16_t *scales, const uint16_t *biases,
+                               int scale_fmt, int bits, int n, float *out) {
+    const size_t nbytes = tfo_affine_row_bytes((size_t)n, bits);
+    for (int g = 0; g < n / TFO_GROUP; ++g) {
+        float scale = tfo_decode_scale(scales[g], scale_fmt);
+        float bias = tfo_decode_scale(biases[g], scale_fmt);
+        for (int k = 0; k < TFO_GROUP; ++k) {
+            size_t j = (size_t)g * TFO_GROUP + k;
+            float prod = (float)tfo_affine_code(packed, nbytes, j, bits) * scale;
+            out[j] = prod + bias;
+        }
+    }
+}
+
 /* Quantization.swift:179-191 */
 void tfo_dequantize_int8_row(const uint8_t *packed, const uint16_t *scales, const uint16_t *biases,
                              int scale_fmt, int n, float *out) {
@@ -201,13 +279,17 @@ void tfo_dequantize_int8_row(const uint8_t *packed, const uint16_t *scales, cons
 /* V/Reference/Quant/DequantInt4Gemv.swift:26-40: per row, dequantise to fp32,
  * then dot in index order (the scalar loop that pins vDSP_dotpr,
  * T/Validation/Reference/DequantInt4GEMVReferenceTests.swift:13-27). */
-static void gemv_int4_rows(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
-                           const float *x, int r0, int r1, int n, float *y) {
+static void gemv_affine_rows(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt, int bits,
+                             const float *x, int r0, int r1, int n, float *y) {
     float *w = (float *)malloc(sizeof(float) * (size_t)n);
-    size_t row_bytes = (size_t)n / 2, groups = (size_t)n / TFO_GROUP;
+    size_t row_bytes = tfo_affine_row_bytes((size_t)n, bits), groups = (size_t)n / TFO_GROUP;
     for (int r = r0; r < r1; ++r) {
-        tfo_dequantize_int4_row(W + (size_t)r * row_bytes, S + (size_t)r * groups,
-                                B + (size_t)r * groups, fmt, n, w);
+        if (bits == 4)
+            tfo_dequantize_int4_row(W + (size_t)r * row_bytes, S + (size_t)r * groups,
+                                    B + (size_t)r * groups, fmt, n, w);
+        else
+            tfo_dequantize_affine_row(W + (size_t)r * row_bytes, S + (size_t)r * groups,
+                                      B + (size_t)r * groups, fmt, bits, n, w);
         float sum = 0.0f;
         for (int i = 0; i < n; ++i) {
             float p = w[i] * x[i];
@@ -220,7 +302,16 @@ static void gemv_int4_rows(const uint8_t *W, const uint16_t *S, const uint16_t *
 
 void tfo_gemv_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
                    const float *x, int m, int n, float *y) {
-    gemv_int4_rows(W, S, B, fmt, x, 0, m, n, y);
+    gemv_affine_rows(W, S, B, fmt, 4, x, 0, m, n, y);
+}
+
+/* The same GEMV over 2-, 3- or 4-bit rows of tfo_affine_row_bytes(n, bits)
+ * bytes: dequantizeAffine, then the dot in index order (the b3 GEMV and
+ * b2/b3 expert kernels compute this function: dequant_int4.metal:512-717,
+ * moe.metal:644-1180). */
+void tfo_gemv_affine(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt, int bits,
+                     const float *x, int m, int n, float *y) {
+    gemv_affine_rows(W, S, B, fmt, bits, x, 0, m, n, y);
 }
 
 void tfo_gemv_int4_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
@@ -276,7 +367,7 @@ typedef struct {
 
 static void *gemv_worker(void *arg) {
     gemv_job *j = (gemv_job *)arg;
-    gemv_int4_rows(j->W, j->S, j->B, j->fmt, j->x, j->r0, j->r1, j->n, j->y);
+    gemv_affine_rows(j->W, j->S, j->B, j->fmt, 4, j->x, j->r0, j->r1, j->n, j->y);
     return NULL;
 }
 
@@ -365,30 +456,42 @@ float tfo_gelu_tanh(float xv) {
     return half_x * one_plus;
 }
 
-/* Moe.swift:33-52 on one expert blob. */
-void tfo_ffn_int4(const uint8_t *blob, const tfo_expert_offsets *o, int fmt, const float *x,
-                  int d, int f, float *out) {
+/* Moe.swift:33-52 on one expert blob whose gate/up/down rows hold `bits`-bit
+ * codes (the b2/b3 experts of moe.metal:644-1180 compute the same FFN). */
+static void ffn_affine(const uint8_t *blob, const tfo_expert_offsets *o, int fmt, int bits, const float *x,
+                       int d, int f, float *out) {
     float *gate = (float *)malloc(sizeof(float) * (size_t)f);
     float *up = (float *)malloc(sizeof(float) * (size_t)f);
     float *act = (float *)malloc(sizeof(float) * (size_t)f);
-    tfo_gemv_int4(blob + o->gate_w, (const uint16_t *)(blob + o->gate_s),
-                  (const uint16_t *)(blob + o->gate_b), fmt, x, f, d, gate);
-    tfo_gemv_int4(blob + o->up_w, (const uint16_t *)(blob + o->up_s),
-                  (const uint16_t *)(blob + o->up_b), fmt, x, f, d, up);
+    tfo_gemv_affine(blob + o->gate_w, (const uint16_t *)(blob + o->gate_s),
+                    (const uint16_t *)(blob + o->gate_b), fmt, bits, x, f, d, gate);
+    tfo_gemv_affine(blob + o->up_w, (const uint16_t *)(blob + o->up_s),
+                    (const uint16_t *)(blob + o->up_b), fmt, bits, x, f, d, up);
     for (int i = 0; i < f; ++i) act[i] = tfo_gelu_tanh(gate[i]) * up[i];   /* vDSP_vmul */
-    tfo_gemv_int4(blob + o->down_w, (const uint16_t *)(blob + o->down_s),
-                  (const uint16_t *)(blob + o->down_b), fmt, act, d, f, out);
+    tfo_gemv_affine(blob + o->down_w, (const uint16_t *)(blob + o->down_s),
+                    (const uint16_t *)(blob + o->down_b), fmt, bits, act, d, f, out);
     free(gate); free(up); free(act);
+}
+
+void tfo_ffn_int4(const uint8_t *blob, const tfo_expert_offsets *o, int fmt, const float *x,
+                  int d, int f, float *out) {
+    ffn_affine(blob, o, fmt, 4, x, d, f, out);
 }
 
 /* Moe.swift:58-88 */
 void tfo_moe_routed(const uint8_t *pool, uint64_t stride, const tfo_expert_offsets *off, int fmt,
                     const float *x, const float *residual, const uint32_t *idx, const float *w,
                     int k, int d, int f, float *y) {
+    tfo_moe_routed_bits(pool, stride, off, fmt, 4, x, residual, idx, w, k, d, f, y);
+}
+
+void tfo_moe_routed_bits(const uint8_t *pool, uint64_t stride, const tfo_expert_offsets *off, int fmt,
+                         int bits, const float *x, const float *residual, const uint32_t *idx,
+                         const float *w, int k, int d, int f, float *y) {
     float *out = (float *)malloc(sizeof(float) * (size_t)d);
     for (int i = 0; i < d; ++i) y[i] = residual ? residual[i] : 0.0f;
     for (int slot = 0; slot < k; ++slot) {
-        tfo_ffn_int4(pool + (uint64_t)idx[slot] * stride, off, fmt, x, d, f, out);
+        ffn_affine(pool + (uint64_t)idx[slot] * stride, off, fmt, bits, x, d, f, out);
         for (int i = 0; i < d; ++i) {
             float scaled = out[i] * w[slot];      /* vDSP_vsmul */
             y[i] = y[i] + scaled;                 /* vDSP_vadd */

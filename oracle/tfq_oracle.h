@@ -59,6 +59,15 @@ void tfo_dequantize_int8_row(const uint8_t *packed, const uint16_t *scales,
                              const uint16_t *biases, int scale_fmt, int n, float *out);
 uint32_t tfo_int4_code(const uint8_t *packed_row, size_t j);
 
+/* ---- 2-, 3- and 4-bit rows (Quantization.swift:195-349) ---- */
+size_t tfo_affine_row_bytes(size_t n, int bits);
+void tfo_pack_affine_code(uint8_t *buf, size_t nbytes, uint32_t code, size_t j, int bits);
+uint32_t tfo_affine_code(const uint8_t *row, size_t nbytes, size_t j, int bits);
+void tfo_quantize_affine_row(const float *row, int n, int bits, uint8_t *packed,
+                             uint16_t *scales_bf16, uint16_t *biases_bf16);
+void tfo_dequantize_affine_row(const uint8_t *packed, const uint16_t *scales, const uint16_t *biases,
+                               int scale_fmt, int bits, int n, float *out);
+
 /* ---- GEMV: dequantise row to fp32, then fp32 dot in index order ----
  * V/Reference/Quant/DequantInt4Gemv.swift:12-42 and DequantInt8Gemv.swift:12-40
  * (vDSP_dotpr, pinned to a scalar index-order loop within 1e-5 by
@@ -74,6 +83,10 @@ void tfo_gemv_int8(const uint8_t *W, const uint16_t *S, const uint16_t *B, int s
                    const float *x, int m, int n, float *y);
 void tfo_gemv_int8_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
                        const float *x, int m, int n, double *y);
+/* tfo_gemv_int4 over 2-, 3- or 4-bit rows: row r starts at
+ * W + r*tfo_affine_row_bytes(n, bits). */
+void tfo_gemv_affine(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt, int bits,
+                     const float *x, int m, int n, float *y);
 /* Row-partitioned multithreaded variant of tfo_gemv_int4 (same per-row arithmetic). */
 void tfo_gemv_int4_mt(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
                       const float *x, int m, int n, float *y, int threads);
@@ -104,6 +117,10 @@ void tfo_ffn_int4(const uint8_t *blob, const tfo_expert_offsets *off, int scale_
 void tfo_moe_routed(const uint8_t *pool, uint64_t stride, const tfo_expert_offsets *off,
                     int scale_fmt, const float *x, const float *residual,
                     const uint32_t *idx, const float *w, int k, int d, int f, float *y);
+/* tfo_moe_routed over experts whose rows hold `bits`-bit codes (2, 3, 4). */
+void tfo_moe_routed_bits(const uint8_t *pool, uint64_t stride, const tfo_expert_offsets *off,
+                         int scale_fmt, int bits, const float *x, const float *residual,
+                         const uint32_t *idx, const float *w, int k, int d, int f, float *y);
 /* Shared expert reference (T/Kernels/MoE/SharedExpertInt4Tests.swift:21-28):
  * gate/up by the GEMV reference, act rounded to fp16, down by the GEMV reference.
  * The GELU here is evaluated in double as that test does. */

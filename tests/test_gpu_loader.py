@@ -39,12 +39,14 @@ def _load(ctx, stream, root, layer, d, f):
     return L, p, int(inexact.download(np.uint32, 1)[0])
 
 
-@pytest.mark.parametrize("d,f,experts,order", [(256, 128, 4, [3, 1, 0, 2]), (2816, 704, 8, [5, 2, 7, 0, 1, 6, 4, 3])])
-def test_pool_holds_each_logical_expert(ctx, stream, tmp_path, d, f, experts, order):
-    data, _ = gturbo.write_model(str(tmp_path), d, f, experts, layers=2, physical_order=order)
+@pytest.mark.parametrize("d,f,experts,order,bits", [(256, 128, 4, [3, 1, 0, 2], 4),
+                                                    (2816, 704, 8, [5, 2, 7, 0, 1, 6, 4, 3], 4),
+                                                    (256, 128, 4, [2, 3, 1, 0], 3), (320, 192, 3, [1, 2, 0], 2)])
+def test_pool_holds_each_logical_expert(ctx, stream, tmp_path, d, f, experts, order, bits):
+    data, _ = gturbo.write_model(str(tmp_path), d, f, experts, layers=2, physical_order=order, bits=bits)
     L, pool, inexact = _load(ctx, stream, str(tmp_path), 1, d, f)
     assert inexact == 0
-    assert pool.num_experts == experts and pool.stride % 256 == 0
+    assert pool.num_experts == experts and pool.stride % 256 == 0 and pool.weight_bits == bits
     assert all(pool.offsets[k] % 16 == 0 for k in ("gate_w", "up_w", "down_w"))
     raw = pool.buffer.download(np.uint8, pool.stride * experts)
     for e in range(experts):
@@ -59,9 +61,10 @@ def test_pool_holds_each_logical_expert(ctx, stream, tmp_path, d, f, experts, or
                 assert np.array_equal(got, _bf16_to_f16(bf.ravel())), (e, role + key)
 
 
-def test_loaded_pool_runs_the_decode_phases(ctx, stream, tmp_path):
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_loaded_pool_runs_the_decode_phases(ctx, stream, tmp_path, bits):
     D, F, E, K = 2816, 704, 8, 8
-    gturbo.write_model(str(tmp_path), D, F, E, physical_order=[1, 0, 3, 2, 5, 4, 7, 6])
+    gturbo.write_model(str(tmp_path), D, F, E, physical_order=[1, 0, 3, 2, 5, 4, 7, 6], bits=bits)
     L, pool, _ = _load(ctx, stream, str(tmp_path), 0, D, F)
     pool_bytes = pool.buffer.download(np.uint8, pool.stride * E)
     rng = np.random.default_rng(3)
@@ -77,7 +80,7 @@ def test_loaded_pool_runs_the_decode_phases(ctx, stream, tmp_path):
     stream.sync()
     got = from_f16_bits(y.download(np.uint16, D))
     ref = oracle.moe_routed(pool_bytes, pool.stride, pool.offsets, from_f16_bits(x16), idx16,
-                            from_f16_bits(rw16), D, F)
+                            from_f16_bits(rw16), D, F, bits=bits)
     assert oracle.rel_error(got, ref) < TOL
 
 
@@ -115,7 +118,9 @@ def test_pool_load_checks_the_tensors(ctx, stream, tmp_path):
     _, layout = gturbo.write_model(root, 256, 128, 2)
     pool = DeviceBuffer(ops.PackedExpertsLayout(root).pool_bytes(256, 128)[1])
     cases = [
-        (lambda t: t["up"].update(bits=3), TFQ_E_UNSUPPORTED),          # not 4-bit weights
+        (lambda t: t["up"].update(bits=3), TFQ_E_UNSUPPORTED),          # widths mixed in one layer
+        (lambda t: t["gate"].update(bits=8), TFQ_E_UNSUPPORTED),        # not 2, 3 or 4 bits
+        (lambda t: t["down"].update(dtype="U8"), TFQ_E_UNSUPPORTED),    # not U32 words
         (lambda t: t["down_scales"].update(dtype="F16"), TFQ_E_INVAL),  # scales not BF16
         (lambda t: t["gate"].update(shape=[128, 128]), TFQ_E_INVAL),    # shape vs d, f
         (lambda t: t["up_biases"].update(offset=10 ** 9), TFQ_E_INVAL), # outside the blob

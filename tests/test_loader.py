@@ -37,6 +37,19 @@ def test_reads_the_repacker_layout(tmp_path):
     L.close()
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_pool_bytes_follow_the_code_width(tmp_path, bits):
+    d, f, E = 256, 128, 4
+    gturbo.write_model(str(tmp_path), d, f, E, bits=bits)
+    L = ops.PackedExpertsLayout(str(tmp_path))
+    stride, total = L.pool_bytes(d, f)
+    blob = 3 * f * d * bits // 8 + 4 * f * (d // 64) * 2 + 2 * d * (f // 64) * 2
+    assert stride == (blob + 255) // 256 * 256 and total == E * stride
+    offs, _ = L.routed_expert_offsets(0)
+    plan, _ = gturbo.blob_plan(d, f, bits)
+    assert offs["up_w"] == dict((k, o) for k, o, *_ in plan)["up"]
+
+
 def test_missing_expert_and_rank_keys_take_the_reader_defaults(tmp_path):
     _, layout = _layout(tmp_path, layers=1)
     lay = copy.deepcopy(layout)

@@ -1,0 +1,109 @@
+"""Pins of the oracle's 2-, 3- and 4-bit affine rows (QuantizedAffineRow,
+S/Infrastructure/ModelIO/Quantization.swift:195-349) and of the b-bit
+GEMV / routed-MoE restatements built on them.
+
+The reference ships no test or fixture for its 2/3-bit paths, so these pin
+the oracle on what the format's definition fixes: hand-packed bytes, the
+packing as one little-endian integer (low element index = least significant
+bits), quantise -> dequantise -> quantise idempotence, and equality with the
+int4 oracle (itself pinned by the reference's golden vectors) on the same
+codes stored as nibbles.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from edgeexpert_amd import synth
+
+
+def test_known_answer_bytes():
+    # codes 1..7, 0 at 3 bits: 1 | 2<<3 | 3<<6 | 4<<9 | 5<<12 | 6<<15 | 7<<18 = 0x1F58D1
+    assert oracle.pack_affine_codes([1, 2, 3, 4, 5, 6, 7, 0], 3).tolist() == [0xD1, 0x58, 0x1F]
+    # 2 bits: 1 | 2<<2 | 3<<4 | 0<<6 = 0x39; then 3, 3, 3, 3 = 0xFF
+    assert oracle.pack_affine_codes([1, 2, 3, 0, 3, 3, 3, 3], 2).tolist() == [0x39, 0xFF]
+    # 4 bits: low nibble = even index (Quantization.swift:199)
+    assert oracle.pack_affine_codes([1, 2, 0xF, 0], 4).tolist() == [0x21, 0x0F]
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("n", [1, 7, 8, 21, 64, 192])
+def test_packing_is_one_little_endian_integer(bits, n):
+    rng = np.random.default_rng(bits * 1000 + n)
+    codes = rng.integers(0, 1 << bits, n)
+    value = sum(int(q) << (bits * j) for j, q in enumerate(codes))
+    nbytes = (n * bits + 7) // 8
+    assert oracle.affine_row_bytes(n, bits) == nbytes
+    expect = np.frombuffer(value.to_bytes(nbytes, "little"), np.uint8)
+    packed = oracle.pack_affine_codes(codes, bits)
+    assert np.array_equal(packed, expect)
+    assert np.array_equal(oracle.affine_codes(packed, n, bits), codes)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_quantize_reproduces_its_codes(bits):
+    # quantizeAffine rounds scale/bias through BF16 first so that decoding
+    # reproduces the stored codes (Quantization.swift:224-228): quantising the
+    # dequantised row gives the same bytes and words back.
+    rng = np.random.default_rng(40 + bits)
+    row = rng.normal(0, 0.05, 256).astype(np.float32)
+    row[64:128] = 0.25                                   # a constant group (scale 1, bias = value)
+    p, s, b = oracle.quantize_affine_row(row, bits)
+    deq = oracle.dequantize_affine_row(p, s, b, oracle.FMT_BF16, bits, row.size)
+    p2, s2, b2 = oracle.quantize_affine_row(deq, bits)
+    assert np.array_equal(p, p2) and np.array_equal(s, s2) and np.array_equal(b, b2)
+    codes = oracle.affine_codes(p, row.size, bits)
+    assert codes.max() <= (1 << bits) - 1
+    assert np.all(codes[64:128] == 0) and oracle.bf16_to_f32(int(s[1])) == 1.0
+    # per element: code * scale + bias, two roundings (Quantization.swift:286-289)
+    sf = synth.bf16_to_f32(s).repeat(64)
+    bf = synth.bf16_to_f32(b).repeat(64)
+    assert np.array_equal(deq, (codes.astype(np.float32) * sf) + bf)
+    if bits == 4:       # the 4-bit path is quantizeInt4Affine's exactly
+        p4, s4, b4 = oracle.quantize_int4_row(row)
+        assert np.array_equal(p, p4) and np.array_equal(s, s4) and np.array_equal(b, b4)
+
+
+def _as_nibbles(packed_rows, n, bits):
+    return np.stack([oracle.pack_affine_codes(oracle.affine_codes(r, n, bits), 4) for r in packed_rows])
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_gemv_matches_int4_oracle_on_the_same_codes(bits):
+    m, n = 24, 320
+    W, S, B = synth.affine_matrix(5, f"pin/b{bits}", m, n, bits)
+    x = synth.normal(synth.seed_key(5, "pin/x"), n)
+    y = oracle.gemv_affine(W, S, B, x, bits)
+    y4 = oracle.gemv_int4(_as_nibbles(W, n, bits), S, B, x)
+    assert np.array_equal(y.view(np.uint32), y4.view(np.uint32))
+    assert np.array_equal(oracle.gemv_affine(_as_nibbles(W, n, bits), S, B, x, 4).view(np.uint32),
+                          y4.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_moe_matches_int4_oracle_on_the_same_codes(bits):
+    D, F, E = 128, 64, 4
+    pool, offs, stride = synth.expert_pool(9, f"pin/moe{bits}", E, D, F, align=256, bits=bits)
+    offs4, stride4 = synth.expert_layout(D, F, align=256)
+    pool4 = np.zeros(E * stride4, np.uint8)
+    for e in range(E):
+        blob = pool[e * stride:(e + 1) * stride]
+        for proj in ("gate", "up", "down"):
+            w, s, b = synth.blob_views(blob, offs, D, F, proj, bits)
+            cols = D if proj != "down" else F
+            for key, arr in (("w", _as_nibbles(w, cols, bits)), ("s", s), ("b", b)):
+                raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
+                o = e * stride4 + offs4[f"{proj}_{key}"]
+                pool4[o:o + raw.size] = raw
+    x = synth.normal(synth.seed_key(9, "pin/moe/x"), D)
+    idx = np.array([3, 0, 2], np.uint32)
+    w = np.array([0.5, 0.3, 0.2], np.float32)
+    y = oracle.moe_routed(pool, stride, offs, x, idx, w, D, F, bits=bits)
+    y4 = oracle.moe_routed(pool4, stride4, offs4, x, idx, w, D, F)
+    assert np.array_equal(y.view(np.uint32), y4.view(np.uint32))
+    assert np.isfinite(y).all() and np.abs(y).max() > 0
+
+
+def test_synth_affine_matrix_shapes():
+    for bits in (2, 3, 4):
+        W, S, B = synth.affine_matrix(1, "shape", 3, 128, bits)
+        assert W.shape == (3, 128 * bits // 8) and S.shape == (3, 2) and B.shape == (3, 2)
