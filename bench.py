@@ -12,8 +12,8 @@ selection folded in, phase 2).
 
 Also measured (extra fields): BASELINE config 0, the int4 g64 GEMV
 [2816 x 2816], cold (rotating through 256 weight copies, 1.14 GB) and warm,
-per-launch with HIP events; config 2, the bf16 prefill GEMM; config 4, the
-full Gemma 4 decoder layer for one token at position 4095 (context 4096),
+per-launch with HIP events; config 2, the bf16 prefill GEMM; the 2- and
+3-bit expert / GEMV variants; config 4, the full Gemma 4 decoder layer for one token at position 4095 (context 4096),
 chained through 8 resident copies of the layer so that every token reads
 cold weights and KV cache, as consecutive layers of a model do.
 
@@ -115,6 +115,68 @@ def bench_c3(ctx, stream, batch_avg_us):
             "kernels": "moe_group, moe_grouped_gate_up, moe_grouped_down, moe_combine"}
 
 
+def bench_bits(ctx, stream, batch_avg_us, router, hbuf):
+    """The 2- and 3-bit variants: config 1's decode token over 128 experts of
+    2/3-bit rows (router + phase 1 with selection + phase 2, back to back
+    over the 64 rotated tokens; per-kernel averages), and the 3-bit GEMV at
+    the LM-head shape (262144 x 2816, 277 MB)."""
+    from edgeexpert_amd import ops, synth
+    from edgeexpert_amd._lib import ROUTER_WORKSPACE_BYTES
+    from edgeexpert_amd.runtime import DeviceBuffer
+    out = {}
+    moe = ops.MoE(ctx)
+    ws = DeviceBuffer(ROUTER_WORKSPACE_BYTES)
+    ws.fill(0)
+    y = DeviceBuffer(TOKENS * D * 2)
+    idx, w16 = DeviceBuffer(TOKENS * K * 4), DeviceBuffer(TOKENS * K * 2)
+    acts, logits = DeviceBuffer(TOKENS * K * F * 2), DeviceBuffer(TOKENS * E * 4)
+    rW, rS, rB = router.weights, router.scales, router.biases
+    for bits in (3, 2):
+        pool_bytes, offs, stride = synth.expert_pool(0, f"c1b{bits}/experts", E, D, F, bits=bits)
+        pool = ops.ExpertPool(DeviceBuffer.from_array(pool_bytes), stride, E, offs, weight_bits=bits)
+        del pool_bytes
+        token_us = batch_avg_us(lambda t: ops.moe_decode_token(
+            ctx, stream, router, pool, hbuf.ptr(t * D * 2), None, y.ptr(t * D * 2), D, F, K, idx.ptr(t * K * 4),
+            w16.ptr(t * K * 2), acts.ptr(t * K * F * 2), ws), TOKENS)
+        for t in range(TOKENS):
+            moe.encode_router_logits(stream, rW, rS, rB, hbuf.ptr(t * D * 2), None, logits.ptr(t * E * 4), E, D)
+        p1 = batch_avg_us(lambda t: moe.encode_routed_phase1_with_selection(
+            stream, pool, logits.ptr(t * E * 4), None, E, idx.ptr(t * K * 4), w16.ptr(t * K * 2),
+            hbuf.ptr(t * D * 2), acts.ptr(t * K * F * 2), D, F, K), TOKENS)
+        p2 = batch_avg_us(lambda t: moe.encode_routed_phase2(
+            stream, pool, idx.ptr(t * K * 4), acts.ptr(t * K * F * 2), w16.ptr(t * K * 2), None,
+            y.ptr(t * D * 2), D, F, K), TOKENS)
+        proj = F * D * bits // 8 + 2 * F * (D // 64) * 2
+        p1_bytes = K * 2 * proj + 2 * D + K * F * 2
+        p1_gbs = p1_bytes / (p1 * 1e-6) / 1e9
+        log(f"{bits}-bit experts: decode token {token_us:.2f} us (back-to-back), phase1 {p1:.2f} us "
+            f"({p1_gbs:.0f} GB/s), phase2 {p2:.2f} us")
+        out[f"moe_decode_b{bits}"] = {"us_per_token": round(token_us, 3), "phase1_us": round(p1, 3),
+                                      "phase2_us": round(p2, 3), "phase1_bytes": p1_bytes,
+                                      "phase1_gbs": round(p1_gbs, 1),
+                                      "phase1_frac": round(p1_gbs / HBM_PEAK_GBS, 4)}
+        del pool
+    # 3-bit GEMV streaming rate at the LM-head shape
+    Ml, n = 262144, 2816
+    rb = n * 3 // 8
+    Wl, Sl, Bl = synth.affine_matrix(0, "lmhead/w3", 4096, n, 3)
+    big, sb, bb = DeviceBuffer(Ml * rb), DeviceBuffer(Ml * 88), DeviceBuffer(Ml * 88)
+    for r0 in range(0, Ml, 4096):
+        big.upload(Wl, r0 * rb)
+        sb.upload(Sl, r0 * 88)
+        bb.upload(Bl, r0 * 88)
+    x = DeviceBuffer.from_array(synth.f16_vector(0, "c0/x", n))
+    yl = DeviceBuffer(Ml * 2)
+    gemv = ops.DequantInt4GEMV(ctx)
+    us = batch_avg_us(lambda i: gemv.encode(stream, big, sb, bb, x, yl, Ml, n, bits=3), 8, reps_=3)
+    nbytes = Ml * rb + 2 * Ml * 88 + n * 2 + Ml * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"3-bit GEMV {Ml}x{n}: {us:.1f} us ({gbs:.0f} GB/s, {gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+    out["gemv_b3_lmhead"] = {"shape": [Ml, n], "bytes": nbytes, "us": round(us, 2), "gbs": round(gbs, 1),
+                             "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def bench_c4(ctx, stream, launch, batch_avg_us):
     from edgeexpert_amd import ops, synth
     from edgeexpert_amd.runtime import DeviceBuffer, Event, Graph
@@ -207,6 +269,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 decode-layer leg")
     ap.add_argument("--no-c3", action="store_true", help="skip the config-3 grouped-prefill leg")
+    ap.add_argument("--no-bits", action="store_true", help="skip the 2/3-bit variant legs")
     ap.add_argument("--launch", choices=("graph", "stream"), default="graph",
                     help="replay the 64-token step from a HIP graph, or issue it from the host")
     args = ap.parse_args()
@@ -405,6 +468,9 @@ def main():
     # ------------------------------------------------ decode layer config 4 ----
     c4 = None if args.no_c4 else bench_c4(ctx, stream, args.launch, batch_avg_us)
 
+    # ------------------------------------------------- 2/3-bit variants ----
+    bits_legs = None if args.no_bits else bench_bits(ctx, stream, batch_avg_us, router, hbuf)
+
     # -------------------------------------- HBM counter calibration kernels ----
     # One plain read (64 MiB) and one plain copy (32 MiB in, 32 MiB out) of
     # known size, launched once so that a rocprofv3 --pmc run of this command
@@ -477,6 +543,7 @@ def main():
                            "kernels": "lm_head_greedy (norm staging + rows + block argmax), lm_head_reduce"},
         "grouped_prefill_c3": c3,
         "decode_layer_c4": c4,
+        "bit_variants": bits_legs,
         "wall_s": round(wall, 4),
         "device": f"{name} {arch}",
     }

@@ -187,25 +187,6 @@ __device__ __forceinline__ void read_xpairs(const XPairs& xp, uint32_t c, XChunk
     xc.cb = s.z;
 }
 
-// Σ_k q_k x_k over the 32 codes of a chunk (fp32 accumulate).
-__device__ __forceinline__ float dot_q4_chunk(const uint4 w, const XChunk& xc) {
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    float acc_a = 0.0f, acc_b = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t w8 = ws[j] >> 8;
-        const h2 q0 = __builtin_bit_cast(h2, (ws[j] & 0x000F000Fu) | 0x64006400u);   // 1024 + q
-        const h2 q1 = __builtin_bit_cast(h2, (ws[j] & 0x00F000F0u) | 0x64006400u);   // 1024 + 16q
-        const h2 q2 = __builtin_bit_cast(h2, (w8 & 0x000F000Fu) | 0x64006400u);
-        const h2 q3 = __builtin_bit_cast(h2, (w8 & 0x00F000F0u) | 0x64006400u);
-        acc_a = __builtin_amdgcn_fdot2(q0, xc.p[4 * j + 0], acc_a, false);
-        acc_b = __builtin_amdgcn_fdot2(q1, xc.p[4 * j + 1], acc_b, false);
-        acc_a = __builtin_amdgcn_fdot2(q2, xc.p[4 * j + 2], acc_a, false);
-        acc_b = __builtin_amdgcn_fdot2(q3, xc.p[4 * j + 3], acc_b, false);
-    }
-    return fmaf(acc_b - xc.cb, 0.0625f, acc_a - xc.ca);
-}
-
 // ------------------------------------------------- 2-, 3- and 4-bit chunks ----
 //
 // The 32 codes of activation chunk c (positions 32c..32c+31) take 4·BITS
@@ -263,10 +244,13 @@ __device__ __forceinline__ uint32_t block_word(const QChunk<BITS>& q, int j) {
         return __builtin_amdgcn_perm(w, w, (j & 1) ? 0x03030202u : 0x01010000u);
     } else {
         // the 24 bits of codes 8j..8j+7 start at bit 24j of the 96-bit chunk
+        // (v_alignbit_b32 on 32-bit halves: a 64-bit shift of the words lets
+        // the compiler fuse their reads into one 64-bit access, which keeps
+        // the chunk arrays in scratch memory)
         uint32_t u;
         if (j == 0) u = q.w[0];
-        else if (j == 1) u = (uint32_t)((((uint64_t)q.w[1] << 32) | q.w[0]) >> 24);
-        else if (j == 2) u = (uint32_t)((((uint64_t)q.w[2] << 32) | q.w[1]) >> 16);
+        else if (j == 1) u = __builtin_amdgcn_alignbit(q.w[1], q.w[0], 24);
+        else if (j == 2) u = __builtin_amdgcn_alignbit(q.w[2], q.w[1], 16);
         else u = q.w[2] >> 8;
         // codes 4..7 (bits 12..23) move up to bits 16..27
         return (u & 0x0000FFFFu) | ((u << 4) & 0xFFFF0000u);
@@ -280,21 +264,31 @@ __device__ __forceinline__ uint32_t block_word(const QChunk<BITS>& q, int j) {
 // fp16); t >> 2·BITS gives 8j+2, 8j+6 and 8j+3, 8j+7 the same way. The
 // activation pairs and offsets are the int4 chunk's, so
 //     Σ q·x = (accA − ca) + (accB − cb) / 2^BITS.
-// At BITS == 4 this is dot_q4_chunk operation for operation.
-template <int BITS>
+// MAGIC_V: the magic 0x64006400 sits in a VGPR. gfx950's VOP3 encodings
+// take no literal, so with both the mask and the magic as literals each pair
+// costs a v_and_b32 and a v_or_b32; with the mask in an SGPR and the magic in
+// a VGPR it is one v_and_or_b32 (which kernel runs faster with which form is
+// measured, not assumed: the schedules differ).
+template <int BITS, bool MAGIC_V = true>
 __device__ __forceinline__ float dot_chunk(const QChunk<BITS>& q, const XChunk& xc) {
     constexpr uint32_t M = (1u << BITS) - 1u;
     constexpr uint32_t MA = M | (M << 16);
     constexpr uint32_t MB = MA << BITS;
+    uint32_t magic = 0x64006400u;
+    if constexpr (MAGIC_V) asm("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     float acc_a = 0.0f, acc_b = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t t = block_word<BITS>(q, j);
+        uint32_t t = block_word<BITS>(q, j);
+        // opaque to the optimiser: otherwise it distributes the masks below
+        // over the shifts and merges that built t (3-bit: ~50% more bit ops
+        // than the one v_and_or_b32 per pair)
+        if constexpr (BITS != 4) asm("" : "+v"(t));
         const uint32_t t2 = t >> (2 * BITS);
-        const h2 q0 = __builtin_bit_cast(h2, (t & MA) | 0x64006400u);
-        const h2 q1 = __builtin_bit_cast(h2, (t & MB) | 0x64006400u);
-        const h2 q2 = __builtin_bit_cast(h2, (t2 & MA) | 0x64006400u);
-        const h2 q3 = __builtin_bit_cast(h2, (t2 & MB) | 0x64006400u);
+        const h2 q0 = __builtin_bit_cast(h2, (t & MA) | magic);
+        const h2 q1 = __builtin_bit_cast(h2, (t & MB) | magic);
+        const h2 q2 = __builtin_bit_cast(h2, (t2 & MA) | magic);
+        const h2 q3 = __builtin_bit_cast(h2, (t2 & MB) | magic);
         acc_a = __builtin_amdgcn_fdot2(q0, xc.p[4 * j + 0], acc_a, false);
         acc_b = __builtin_amdgcn_fdot2(q1, xc.p[4 * j + 1], acc_b, false);
         acc_a = __builtin_amdgcn_fdot2(q2, xc.p[4 * j + 2], acc_a, false);

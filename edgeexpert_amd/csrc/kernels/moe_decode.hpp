@@ -308,7 +308,9 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                     if (c < lpr) {
                         XChunk xc;
                         read_xpairs(xp, slot * lpr + c, xc);
-                        const float dd = dot_chunk<BITS>(wv[r][p], xc);
+                        // literal magic: measured 6.2 us per config-1 launch
+                        // against 6.8 us with the magic in a VGPR
+                        const float dd = dot_chunk<BITS, false>(wv[r][p], xc);
                         acc[r] = fmaf(h2f((uint16_t)sr[r][p]), dd, acc[r]);
                         acc[r] = fmaf(h2f((uint16_t)br[r][p]), xc.sum, acc[r]);
                     }
