@@ -127,6 +127,7 @@ SIGNATURES = {
     "tfq_convert_bf16_to_f16": [_P, _P, _P, _P, C.c_uint64, _P],
     "tfq_read_ceiling": [_P, _P, _P, C.c_uint64, _P, _U32],
     "tfq_gemm_q4g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _I],
+    "tfq_gemm_qg64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _I, _U32],
     "tfq_prefill_router": [_P, _P, C.POINTER(RouterDesc), _P, _U32, _U32, _U32, _U32, _P, _P, _P, _P],
     "tfq_moe_group": [_P, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _P],
     "tfq_group_pairs_host": [_P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _P,

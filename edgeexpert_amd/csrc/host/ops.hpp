@@ -450,8 +450,11 @@ class PrefillInt4QMM {
 public:
     explicit PrefillInt4QMM(const Module& m) : m_(m) {}
 
+    // bits: 4, or 3 (PrefillPrimitives.swift:91-99; prefill.metal:711-757).
     int encode(void* stream, const void* weights, const uint16_t* scales, const uint16_t* biases,
-               const uint16_t* x, uint16_t* y, uint32_t t, uint32_t n, uint32_t k, int dtype) const {
+               const uint16_t* x, uint16_t* y, uint32_t t, uint32_t n, uint32_t k, int dtype,
+               uint32_t bits = 4) const {
+        if (bits != 3 && bits != 4) return fail(TFQ_E_INVAL, "unsupported attention weight bits %u", bits);
         if (k == 0 || k % TFQ_GROUP_SIZE != 0)
             return fail(TFQ_E_INVAL, "k=%u must be a positive multiple of 64", k);
         if (n == 0) return fail(TFQ_E_INVAL, "output count must be positive");
@@ -463,7 +466,8 @@ public:
             return fail(TFQ_E_INVAL, "weights and x must be 16-byte aligned");
         if (!aligned(scales, 2) || !aligned(biases, 2) || !aligned(y, 2))
             return fail(TFQ_E_INVAL, "scales/biases/y must be 2-byte aligned");
-        const char* name = dtype == TFQ_DTYPE_BF16 ? "tfq_gemm_q4_bf16" : "tfq_gemm_q4_f16";
+        const char* name = bits == 3 ? (dtype == TFQ_DTYPE_BF16 ? "tfq_gemm_q3_bf16" : "tfq_gemm_q3_f16")
+                                     : (dtype == TFQ_DTYPE_BF16 ? "tfq_gemm_q4_bf16" : "tfq_gemm_q4_f16");
         hipFunction_t f = m_.get(name);
         if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
         // blockIdx.x walks the outputs, so the token tiles that share a weight
@@ -563,8 +567,6 @@ public:
                uint16_t* act, uint16_t* partials) const {
         int rc = check_expert_pool(pool, d, f);
         if (rc) return rc;
-        if (pool_bits(pool) != 4)
-            return fail(TFQ_E_UNSUPPORTED, "grouped prefill experts are 4-bit only (pool has %u)", pool_bits(pool));
         if (!sorted || !tiles || !n_tiles || !hidden || !act || !partials)
             return fail(TFQ_E_INVAL, "null pointer argument");
         if (stride < d || stride % 8) return fail(TFQ_E_INVAL, "hidden stride must be >= d and a multiple of 8");
@@ -577,12 +579,16 @@ public:
         // two 64-row halves per grouping tile; gate/up: 128 features per block,
         // down: 256 outputs per block
         void* a1[] = {&kp, &sorted, &tiles, &n_tiles, &hidden, &stride, &act, &d, &f};
-        rc = launch2(m_, "tfq_moe_grouped_gate_up", 2 * max_tiles, (f + 127) / 128, kProjThreads,
-                     proj_lds_bytes(d), stream, a1);
+        const uint32_t bits = pool_bits(pool);
+        const char* gu = bits == 2 ? "tfq_moe_grouped_gate_up_b2" : bits == 3 ? "tfq_moe_grouped_gate_up_b3"
+                                                                           : "tfq_moe_grouped_gate_up";
+        const char* dn = bits == 2 ? "tfq_moe_grouped_down_b2" : bits == 3 ? "tfq_moe_grouped_down_b3"
+                                                                        : "tfq_moe_grouped_down";
+        rc = launch2(m_, gu, 2 * max_tiles, (f + 127) / 128, kProjThreads, proj_lds_bytes(d), stream, a1);
         if (rc) return rc;
         void* a2[] = {&kp, &sorted, &tiles, &n_tiles, &act, &partials, &d, &f, &k};
-        return launch2(m_, "tfq_moe_grouped_down", 2 * max_tiles, (d + kProjBN - 1) / kProjBN, kProjThreads,
-                       proj_lds_bytes(f), stream, a2);
+        return launch2(m_, dn, 2 * max_tiles, (d + kProjBN - 1) / kProjBN, kProjThreads, proj_lds_bytes(f),
+                       stream, a2);
     }
 
     // PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38).

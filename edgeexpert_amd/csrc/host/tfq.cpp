@@ -49,10 +49,11 @@ static std::vector<std::string> kernel_names() {
         for (const char* b : {"", "b2_", "b3_"}) names.push_back(std::string("tfq_moe_phase2_") + b + "p" + std::to_string(p));
     names.push_back("tfq_router_select");
     names.push_back("tfq_read_ceiling");
-    names.push_back("tfq_gemm_q4_f16");
-    names.push_back("tfq_gemm_q4_bf16");
-    for (const char* n : {"tfq_prefill_select", "tfq_moe_group", "tfq_moe_grouped_gate_up",
-                          "tfq_moe_grouped_down", "tfq_moe_combine"})
+    for (const char* n : {"tfq_gemm_q4_f16", "tfq_gemm_q4_bf16", "tfq_gemm_q3_f16", "tfq_gemm_q3_bf16"})
+        names.push_back(n);
+    for (const char* n : {"tfq_prefill_select", "tfq_moe_group", "tfq_moe_grouped_gate_up", "tfq_moe_grouped_down",
+                          "tfq_moe_grouped_gate_up_b2", "tfq_moe_grouped_down_b2", "tfq_moe_grouped_gate_up_b3",
+                          "tfq_moe_grouped_down_b3", "tfq_moe_combine"})
         names.push_back(n);
     names.push_back("tfq_convert_bf16_f16");
     for (const char* hd : {"128", "256"}) {
@@ -382,6 +383,12 @@ int tfq_gemm_q4g64(tfq_ctx* ctx, void* stream, const void* weights, const uint16
     return ctx->qmm->encode(stream, weights, scales, biases, x, y, m, n, k, dtype);
 }
 
+int tfq_gemm_qg64(tfq_ctx* ctx, void* stream, const void* weights, const uint16_t* scales, const uint16_t* biases,
+                  const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n, uint32_t k, int dtype, uint32_t bits) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->qmm->encode(stream, weights, scales, biases, x, y, m, n, k, dtype, bits);
+}
+
 int tfq_prefill_router(tfq_ctx* ctx, void* stream, const tfq_router* router, const uint16_t* hidden,
                        uint32_t hidden_stride, uint32_t T, uint32_t d, uint32_t top_k,
                        uint32_t* out_indices, uint16_t* out_weights, float* out_weights_f32,
@@ -459,9 +466,7 @@ int tfq_moe_prefill(tfq_ctx* ctx, void* stream, const tfq_router* router, const 
     if (router->num_experts != pool->num_experts)
         return fail(TFQ_E_INVAL, "router has %u experts, pool %u", router->num_experts,
                     pool->num_experts);
-    if (int rc = check_expert_pool(*pool, d, f)) return rc;
-    if (pool_bits(*pool) != 4)      // checked before any launch: nothing is queued on failure
-        return fail(TFQ_E_UNSUPPORTED, "grouped prefill experts are 4-bit only (pool has %u)", pool_bits(*pool));
+    if (int rc = check_expert_pool(*pool, d, f)) return rc;     // before any launch: nothing queued on failure
     const uint32_t E = pool->num_experts;
     const PrefillLayout L = prefill_layout(T, top_k, E, d, f);
     if (workspace_bytes < L.total)

@@ -206,26 +206,28 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // of n codes start at multiples of n·BITS/8, a multiple of 8 bytes for n %
 // 64 == 0, and chunks at multiples of 4·BITS). Three separate words at 3
 // bits: a 3-wide vector load may be widened to 16 bytes, past the row.
-template <int BITS>
+// STREAM: non-temporal (weights read once per token); plain loads where
+// several token tiles share the rows through L2 (the prefill tiles).
+template <int BITS, bool STREAM = true>
 __device__ __forceinline__ QChunk<BITS> ldg_chunk(const uint8_t* row, uint32_t c) {
     QChunk<BITS> q;
     const uint8_t* p = row + 4u * BITS * c;
     if constexpr (BITS == 4) {
-        const uint4 v = ldg16_stream(p);
+        const uint4 v = STREAM ? ldg16_stream(p) : ldg16(p);
         q.w[0] = v.x;
         q.w[1] = v.y;
         q.w[2] = v.z;
         q.w[3] = v.w;
     } else if constexpr (BITS == 2) {
-        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        const u32x2* vp = reinterpret_cast<const u32x2*>(p);
+        const u32x2 v = STREAM ? __builtin_nontemporal_load(vp) : *vp;
         q.w[0] = v.x;
         q.w[1] = v.y;
     } else {
         static_assert(BITS == 3, "2, 3 or 4 bits");
         const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
-        q.w[0] = __builtin_nontemporal_load(w);
-        q.w[1] = __builtin_nontemporal_load(w + 1);
-        q.w[2] = __builtin_nontemporal_load(w + 2);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) q.w[i] = STREAM ? __builtin_nontemporal_load(w + i) : w[i];
     }
     return q;
 }

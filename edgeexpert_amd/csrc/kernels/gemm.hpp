@@ -134,23 +134,27 @@ constexpr uint32_t proj_lds_bytes(uint32_t K) {
     return 2u * kProjBM * kGemmLdsStride * 2u + 2u * kProjBN * (K / 64u) * 2u;
 }
 
-// Dequantises the 32 codes of one 16-byte chunk into 4 runs of 8 fp16
-// weights (order 0,4,1,5,2,6,3,7 inside each run), with the fp16 exponent
-// pattern held in a VGPR so that each nibble pair costs one v_and_or_b32
-// (gfx9 VOP3 takes no literal and one scalar operand).
-__device__ __forceinline__ void dequant_chunk_f16_v(uint4 w, uint16_t s_bits, uint16_t b_bits, uint32_t magic_v,
-                                                    h8 (&out)[4]) {
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+// Dequantises the 32 codes of one chunk (16 bytes at 4 bits, 12 at 3, 8 at
+// 2) into 4 runs of 8 fp16 weights (order 0,4,1,5,2,6,3,7 inside each run),
+// with the fp16 exponent pattern held in a VGPR so that each code pair costs
+// one v_and_or_b32 (gfx9 VOP3 takes no literal and one scalar operand). Run
+// j is block_word(j): codes 8j+i and 8j+i+4 at bit BITS·i of its halves.
+template <int BITS>
+__device__ __forceinline__ void dequant_chunk_f16_v(const QChunk<BITS>& w, uint16_t s_bits, uint16_t b_bits,
+                                                    uint32_t magic_v, h8 (&out)[4]) {
+    constexpr uint32_t MA = ((1u << BITS) - 1u) * 0x00010001u;
     const _Float16 s = __builtin_bit_cast(_Float16, s_bits);
     const _Float16 b = __builtin_bit_cast(_Float16, b_bits);
     const h2 s2 = {s, s}, b2 = {b, b};
     const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+        uint32_t t = block_word<BITS>(w, j);
+        if constexpr (BITS != 4) asm("" : "+v"(t));
         h8 run;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t q = ((ws[j] >> (4 * i)) & 0x000F000Fu) | magic_v;
+            const uint32_t q = ((t >> (BITS * i)) & MA) | magic_v;
             const h2 qh = __builtin_bit_cast(h2, q) - k1024;             // exact q pair
             const h2 wv = __builtin_elementwise_fma(qh, s2, b2);         // one rounding
             run[2 * i] = wv[0];
@@ -177,7 +181,7 @@ struct ProjLanes {
 // then the s/b table, filled by the caller before the call and synchronised
 // by the first barrier inside); xp: this thread's activation row (token row
 // tid/4 of the block, already clamped to a valid row) + 16·(tid%4) halves.
-template <bool X_BF16, int MI = 2>
+template <bool X_BF16, int MI = 2, int BITS = 4>
 __device__ __forceinline__ void proj_core(f32x16 (&acc)[MI][2], _Float16* lds, const uint16_t* s_lds,
                                           const uint16_t* b_lds, const ProjLanes& pl,
                                           const uint16_t* __restrict__ xp, uint32_t G) {
@@ -189,12 +193,13 @@ __device__ __forceinline__ void proj_core(f32x16 (&acc)[MI][2], _Float16* lds, c
     uint32_t magic_v;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_v));
 
-    uint4 w0[kProjDepth], w1[kProjDepth], xa[kProjXDepth], xb[kProjXDepth];
+    QChunk<BITS> w0[kProjDepth], w1[kProjDepth];
+    uint4 xa[kProjXDepth], xb[kProjXDepth];
     auto load_w = [&](uint32_t g, auto st_c) {
         constexpr int ST = decltype(st_c)::value;
         const uint32_t gg = g < G ? g : G - 1;
-        w0[ST] = ldg16(pl.wp0 + 32u * gg);       // plain loads: the token tiles of an
-        w1[ST] = ldg16(pl.wp1 + 32u * gg);       // output slice share them through L2
+        w0[ST] = ldg_chunk<BITS, false>(pl.wp0, 2u * gg);   // plain loads: the token tiles of an
+        w1[ST] = ldg_chunk<BITS, false>(pl.wp1, 2u * gg);   // output slice share them through L2
     };
     auto load_x = [&](uint32_t g, auto st_c) {
         constexpr int ST = decltype(st_c)::value;
@@ -211,7 +216,7 @@ __device__ __forceinline__ void proj_core(f32x16 (&acc)[MI][2], _Float16* lds, c
     // B operands of one group: [sub-tile j][k-step s]; two buffers so that the
     // next group's dequantisation overlaps this group's MFMAs
     h8 bw[2][2][4];
-    auto dequant = [&](uint32_t g, const uint4 wa, const uint4 wb, h8 (&dst)[2][4]) {
+    auto dequant = [&](uint32_t g, const QChunk<BITS>& wa, const QChunk<BITS>& wb, h8 (&dst)[2][4]) {
         const uint32_t gg = g < G ? g : G - 1;
         dequant_chunk_f16_v(wa, s_lds[pl.sidx0 + gg], b_lds[pl.sidx0 + gg], magic_v, dst[0]);
         dequant_chunk_f16_v(wb, s_lds[pl.sidx1 + gg], b_lds[pl.sidx1 + gg], magic_v, dst[1]);
@@ -352,17 +357,21 @@ __device__ __forceinline__ void copy_sb_to_lds(const uint16_t* __restrict__ a, c
 }
 
 // dequant_chunk_f16_v with the scale and bias taken from one table word.
-__device__ __forceinline__ void dequant_chunk_sb(uint4 w, uint32_t sb, uint32_t magic_v, h8 (&out)[4]) {
+template <int BITS>
+__device__ __forceinline__ void dequant_chunk_sb(const QChunk<BITS>& w, uint32_t sb, uint32_t magic_v,
+                                                 h8 (&out)[4]) {
+    constexpr uint32_t MA = ((1u << BITS) - 1u) * 0x00010001u;
     const h2 s2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x01000100u));
     const h2 b2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x03020302u));
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
     const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+        uint32_t t = block_word<BITS>(w, j);
+        if constexpr (BITS != 4) asm("" : "+v"(t));
         h8 run;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t q = ((ws[j] >> (4 * i)) & 0x000F000Fu) | magic_v;
+            const uint32_t q = ((t >> (BITS * i)) & MA) | magic_v;
             const h2 qh = __builtin_bit_cast(h2, q) - k1024;             // exact q pair
             const h2 wv = __builtin_elementwise_fma(qh, s2, b2);         // one rounding
             run[2 * i] = wv[0];
@@ -386,7 +395,7 @@ __device__ __forceinline__ void dequant_chunk_sb(uint4 w, uint32_t sb, uint32_t 
 // barrier inside); xp: this thread's activation row (token row
 // tid / (64/XH) of the block, clamped to a valid row) + XH·(tid % (64/XH))
 // halves, XH = halves it stages per group. lds: the three activation buffers.
-template <bool X_BF16, int J>
+template <bool X_BF16, int J, int BITS = 4>
 __device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds, const uint32_t* sb_lds,
                                              const ProjLanes& pl, const uint16_t* __restrict__ xp, uint32_t G) {
     constexpr uint32_t T = kProjBM * kGemmLdsStride;         // halves per activation buffer
@@ -401,7 +410,8 @@ __device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds,
 
     constexpr int KS = J == 1 ? 2 : 1;                        // accumulator sets (k-step parity)
     constexpr int AB = J == 1 ? 1 : 2;                        // A-operand buffers
-    uint4 wr[J][kProjDepth], xr[2][XV];
+    QChunk<BITS> wr[J][kProjDepth];
+    uint4 xr[2][XV];
     h8 a[AB][2][4];         // [group parity][token sub-tile][k-step]
     f32x16 accs[2][J][KS];
     h8 bw[2][J][4];         // [group parity][output sub-tile][k-step]
@@ -409,8 +419,8 @@ __device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds,
     auto load_w = [&](uint32_t g, auto st_c) {
         constexpr int ST = decltype(st_c)::value;
         const uint32_t gg = g < G ? g : G - 1;
-        wr[0][ST] = ldg16(pl.wp0 + 32u * gg);
-        if constexpr (J == 2) wr[J - 1][ST] = ldg16(pl.wp1 + 32u * gg);
+        wr[0][ST] = ldg_chunk<BITS, false>(pl.wp0, 2u * gg);
+        if constexpr (J == 2) wr[J - 1][ST] = ldg_chunk<BITS, false>(pl.wp1, 2u * gg);
     };
     auto load_x = [&](uint32_t g, auto sl_c) {
         constexpr int SL = decltype(sl_c)::value;
@@ -539,9 +549,10 @@ __device__ __forceinline__ void proj_for_each(const f32x16 (&acc)[MI][J], Fn fn)
 }
 
 // Lanes of a wave over the outputs n_base + 32·J·wave_in_mat + 32j + lane%32
-// (j < J) of a matrix with `nrows` outputs (clamped to the last one), K/2-byte
-// rows, the table rows of those outputs starting at table_base.
-template <int J>
+// (j < J) of a matrix with `nrows` outputs (clamped to the last one), rows of
+// row_bytes (K·BITS/8), the table rows of those outputs starting at
+// table_base. The lane's half h of each 64-code group is chunk 2g + h.
+template <int J, int BITS = 4>
 __device__ __forceinline__ ProjLanes proj_lanes(const uint8_t* W, uint32_t row_bytes, uint32_t n_base,
                                                 uint32_t wave_in_mat, uint32_t nrows, uint32_t table_base,
                                                 uint32_t G) {
@@ -550,15 +561,15 @@ __device__ __forceinline__ ProjLanes proj_lanes(const uint8_t* W, uint32_t row_b
     ProjLanes pl;
     const uint32_t na = n_base + 32u * J * wave_in_mat + col, nb = na + 32u;
     const uint32_t ra = na < nrows ? na : nrows - 1, rb = nb < nrows ? nb : nrows - 1;
-    pl.wp0 = W + (size_t)ra * row_bytes + 16u * h;
-    pl.wp1 = W + (size_t)rb * row_bytes + 16u * h;
+    pl.wp0 = W + (size_t)ra * row_bytes + 4u * BITS * h;
+    pl.wp1 = W + (size_t)rb * row_bytes + 4u * BITS * h;
     pl.sidx0 = (table_base + ra - n_base) * G;
     pl.sidx1 = (table_base + rb - n_base) * G;
     return pl;
 }
 
-// Eight waves (kProjGemmThreads), one 32-output sub-tile each.
-template <bool X_BF16>
+// Eight waves (kProjGemmThreads), one 32-output sub-tile each; BITS-bit rows.
+template <bool X_BF16, int BITS = 4>
 __device__ __forceinline__ void gemm_q4_proj(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
                                              const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
                                              uint16_t* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K) {
@@ -570,12 +581,12 @@ __device__ __forceinline__ void gemm_q4_proj(const uint16_t* __restrict__ X, con
     // scales / biases of rows n0 .. n0+255 (clamped to N): contiguous in S and B
     const uint32_t nrows = N - n0 < kProjBN ? N - n0 : kProjBN;
     copy_sb_to_lds<kProjGemmThreads>(S + (size_t)n0 * G, B + (size_t)n0 * G, sb_lds, nrows * G);
-    const ProjLanes pl = proj_lanes<1>(W, K >> 1, n0, wave, N, 0, G);
+    const ProjLanes pl = proj_lanes<1, BITS>(W, (K >> 3) * BITS, n0, wave, N, 0, G);
     // token rows past M read row 0: their results are never stored
     const uint32_t xrow = tid >> 3;
     const uint16_t* xp = X + (size_t)(m0 + xrow < M ? m0 + xrow : 0u) * K + 8u * (tid & 7u);
     f32x16 acc[2][1];
-    proj_core_pl<X_BF16, 1>(acc, proj_lds, sb_lds, pl, xp, G);
+    proj_core_pl<X_BF16, 1, BITS>(acc, proj_lds, sb_lds, pl, xp, G);
     proj_for_each<1>(acc, [&](uint32_t m, uint32_t n, float v) {
         if (m0 + m < M && n0 + n < N)
             Y[(size_t)(m0 + m) * N + n0 + n] = X_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)v) : f2h(v);

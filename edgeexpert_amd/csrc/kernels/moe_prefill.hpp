@@ -199,6 +199,9 @@ __device__ __forceinline__ bool grouped_rows(const Tile* __restrict__ tiles, con
 // rows as its first 32-output sub-tile and the up rows as its second, so each
 // lane holds gate and up of the same (pair, feature) and applies the GeGLU
 // in registers. LDS table rows 0..127: gate scales/biases, 128..255: up.
+// BITS: code width of the expert rows (2, 3 or 4; prefill.metal:1304-1450
+// for the 2/3-bit experts).
+template <int BITS = 4>
 __device__ __forceinline__ void moe_grouped_gate_up(const ExpertPool& pool, const Pair* __restrict__ sorted,
                                                     const Tile* __restrict__ tiles,
                                                     const uint32_t* __restrict__ n_tiles,
@@ -224,8 +227,8 @@ __device__ __forceinline__ void moe_grouped_gate_up(const ExpertPool& pool, cons
     const uint32_t col = lane & 31u, h = lane >> 5;
     const uint32_t f = f0 + 32u * wave + col, fc = f < F ? f : F - 1;   // features past F: clamped, not stored
     ProjLanes pl;
-    pl.wp0 = blob + o.gate_w + (size_t)fc * (D >> 1) + 16u * h;
-    pl.wp1 = blob + o.up_w + (size_t)fc * (D >> 1) + 16u * h;
+    pl.wp0 = blob + o.gate_w + (size_t)fc * ((D >> 3) * BITS) + 4u * BITS * h;
+    pl.wp1 = blob + o.up_w + (size_t)fc * ((D >> 3) * BITS) + 4u * BITS * h;
     pl.sidx0 = (fc - f0) * G;
     pl.sidx1 = (128u + fc - f0) * G;
     // rows past the half's count read its first row: their results are never stored
@@ -236,7 +239,7 @@ __device__ __forceinline__ void moe_grouped_gate_up(const ExpertPool& pool, cons
     auto run = [&](auto mi_c) {
         constexpr int MI = decltype(mi_c)::value;
         f32x16 acc[MI][2];
-        proj_core<false, MI>(acc, proj_lds, s_lds, b_lds, pl, xp, G);
+        proj_core<false, MI, BITS>(acc, proj_lds, s_lds, b_lds, pl, xp, G);
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -252,7 +255,8 @@ __device__ __forceinline__ void moe_grouped_gate_up(const ExpertPool& pool, cons
 
 // Grouped down projection over one 64-row half tile (blockIdx.x) and 256
 // outputs of D (blockIdx.y): partials[(token*k + rank)*D + d] = fp16(down_e[d]·act_p)
-// (prefill.metal:639-670).
+// (prefill.metal:639-670). BITS as for moe_grouped_gate_up.
+template <int BITS = 4>
 __device__ __forceinline__ void moe_grouped_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
                                                  const Tile* __restrict__ tiles,
                                                  const uint32_t* __restrict__ n_tiles,
@@ -276,14 +280,14 @@ __device__ __forceinline__ void moe_grouped_down(const ExpertPool& pool, const P
     copy_pair_to_lds<kProjThreads>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)n0 * G,
                                    reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)n0 * G, s_lds,
                                    b_lds, nrows * G);
-    const ProjLanes pl = proj_lanes<2>(blob + o.down_w, F >> 1, n0, wave, D, 0, G);
+    const ProjLanes pl = proj_lanes<2, BITS>(blob + o.down_w, (F >> 3) * BITS, n0, wave, D, 0, G);
     const uint32_t xrow = tid >> 2;
     const uint16_t* xp = act + (size_t)(gr.first + (xrow < gr.count ? xrow : 0u)) * F + 16u * (tid & 3u);
     // a half with at most 32 rows runs one token sub-tile (block-uniform)
     auto run = [&](auto mi_c) {
         constexpr int MI = decltype(mi_c)::value;
         f32x16 acc[MI][2];
-        proj_core<false, MI>(acc, proj_lds, s_lds, b_lds, pl, xp, G);     // its barriers publish dst_row
+        proj_core<false, MI, BITS>(acc, proj_lds, s_lds, b_lds, pl, xp, G);   // its barriers publish dst_row
         proj_for_each<2>(acc, [&](uint32_t m, uint32_t n, float v) {
             if (m < gr.count && n0 + n < D) partials[(size_t)dst_row[m] * D + n0 + n] = f2h(v);
         });

@@ -164,17 +164,16 @@ TFQ_PHASE2(2)
 TFQ_PHASE2(3)
 TFQ_PHASE2(4)
 
-extern "C" __global__ __launch_bounds__(kProjGemmThreads) void tfq_gemm_q4_f16(
-    const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
-    uint32_t M, uint32_t N, uint32_t K) {
-    gemm_q4_proj<false>(X, W, S, B, Y, M, N, K);
-}
-
-extern "C" __global__ __launch_bounds__(kProjGemmThreads) void tfq_gemm_q4_bf16(
-    const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,
-    uint32_t M, uint32_t N, uint32_t K) {
-    gemm_q4_proj<true>(X, W, S, B, Y, M, N, K);
-}
+#define TFQ_GEMM(TAG, BITS, DT, X_BF16)                                                          \
+    extern "C" __global__ __launch_bounds__(kProjGemmThreads) void tfq_gemm_##TAG##_##DT(        \
+        const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,  \
+        uint32_t M, uint32_t N, uint32_t K) {                                                     \
+        gemm_q4_proj<X_BF16, BITS>(X, W, S, B, Y, M, N, K);                                       \
+    }
+TFQ_GEMM(q4, 4, f16, false)
+TFQ_GEMM(q4, 4, bf16, true)
+TFQ_GEMM(q3, 3, f16, false)
+TFQ_GEMM(q3, 3, bf16, true)
 
 extern "C" __global__ __launch_bounds__(256) void tfq_lm_head_reduce(const uint64_t* summaries, uint32_t n,
                                                                      uint32_t* out_token) {
@@ -208,17 +207,20 @@ extern "C" __global__ __launch_bounds__(kGroupThreads) void tfq_moe_group(
     moe_group(idx, w, T, k, E, sorted, offsets, counts, tiles, n_tiles, status);
 }
 
-extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_gate_up(
-    ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,
-    const uint16_t* hidden, uint32_t stride, uint16_t* act, uint32_t D, uint32_t F) {
-    moe_grouped_gate_up(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F);
-}
-
-extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_down(
-    ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,
-    const uint16_t* act, uint16_t* partials, uint32_t D, uint32_t F, uint32_t k) {
-    moe_grouped_down(pool, sorted, tiles, n_tiles, act, partials, D, F, k);
-}
+#define TFQ_GROUPED(SUFFIX, BITS)                                                                \
+    extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_gate_up##SUFFIX( \
+        ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,         \
+        const uint16_t* hidden, uint32_t stride, uint16_t* act, uint32_t D, uint32_t F) {        \
+        moe_grouped_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F);      \
+    }                                                                                            \
+    extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_down##SUFFIX(  \
+        ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,         \
+        const uint16_t* act, uint16_t* partials, uint32_t D, uint32_t F, uint32_t k) {           \
+        moe_grouped_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k);            \
+    }
+TFQ_GROUPED(, 4)
+TFQ_GROUPED(_b2, 2)
+TFQ_GROUPED(_b3, 3)
 
 extern "C" __global__ __launch_bounds__(256) void tfq_moe_combine(const uint16_t* partials,
                                                                   const uint16_t* w, uint16_t* h2,

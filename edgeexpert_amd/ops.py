@@ -123,11 +123,14 @@ class PrefillInt4QMM:
         self.ctx = context
 
     def encode(self, stream, weights, scales, biases, x, y, t, n, k, dtype=0, weights_offset=0,
-               scales_offset=0, biases_offset=0, x_offset=0, y_offset=0):
-        check(lib().tfq_gemm_q4g64(self.ctx.handle, _s(stream), _addr(weights, weights_offset),
-                                   _addr(scales, scales_offset), _addr(biases, biases_offset),
-                                   _addr(x, x_offset), _addr(y, y_offset), t, n, k, dtype),
-              "PrefillInt4QMM.encode")
+               scales_offset=0, biases_offset=0, x_offset=0, y_offset=0, bits=4):
+        """bits: 4, or 3 for 3-bit rows (PrefillPrimitives.swift:91-99)."""
+        args = (self.ctx.handle, _s(stream), _addr(weights, weights_offset), _addr(scales, scales_offset),
+                _addr(biases, biases_offset), _addr(x, x_offset), _addr(y, y_offset), t, n, k, dtype)
+        if bits == 4:
+            check(lib().tfq_gemm_q4g64(*args), "PrefillInt4QMM.encode")
+        else:
+            check(lib().tfq_gemm_qg64(*args, bits), "PrefillInt4QMM.encode")
 
 
 MPPPrefillInt4QMM = PrefillInt4QMM

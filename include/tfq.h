@@ -173,9 +173,8 @@ typedef struct {
  * weight_bits: code width of every gate/up/down row, 2, 3 or 4 (0 means 4,
  * the default of the reference's `bits:` argument, MoE.swift:244,281,324);
  * a row of n codes takes n*bits/8 bytes, codes packed from the least
- * significant bit (Quantization.swift:195-201). The decode entry points
- * (phase 1, phase 2 and the fused forms) run every width; the grouped
- * prefill ones run 4 bits and return TFQ_E_UNSUPPORTED otherwise.
+ * significant bit (Quantization.swift:195-201). The decode
+ * and grouped prefill entry points run every width.
  * Contract: base, stride and the *_w offsets 16-byte aligned; *_s/*_b
  * offsets 2-byte aligned. */
 typedef struct {
@@ -357,6 +356,15 @@ int tfq_decode_layer(tfq_ctx *ctx, void *stream, const tfq_decode_layer_weights 
 int tfq_gemm_q4g64(tfq_ctx *ctx, void *stream, const void *weights, const uint16_t *scales,
                    const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m, uint32_t n,
                    uint32_t k, int dtype);
+
+/* tfq_gemm_q4g64 at `bits` = 3 or 4 bits per code (rows of k*bits/8 bytes,
+ * codes packed from the least significant bit). Replaces
+ * PrefillInt4QMM.encode(..., bits: 3) (PrefillPrimitives.swift:82-122 with
+ * prefill_dequant_int4_qmm_f16_block_b3, prefill.metal:711-757); other
+ * widths: TFQ_E_INVAL (the reference's precondition, :94-95). */
+int tfq_gemm_qg64(tfq_ctx *ctx, void *stream, const void *weights, const uint16_t *scales,
+                  const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m, uint32_t n,
+                  uint32_t k, int dtype, uint32_t bits);
 
 /* (token, expert, rank, fp16 routing weight bits in the low half) — the
  * 16-byte PrefillTokenExpertPair (S/Kernels/Prefill/MoE/PrefillRouter.swift:5-28). */

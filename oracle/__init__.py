@@ -140,8 +140,12 @@ def _declare(L):
       C.c_int, C.c_int, _P, _P)
     d("tfo_grouped_route_partials", None, _P, C.c_int64, _P, C.c_int, _P, C.c_uint64,
       C.POINTER(ExpertOffsets), C.c_int, C.c_int, C.c_int, C.c_int, _P)
+    d("tfo_grouped_route_partials_bits", None, _P, C.c_int64, _P, C.c_int, _P, C.c_uint64,
+      C.POINTER(ExpertOffsets), C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _P)
     d("tfo_reduce_token_major", None, _P, _P, C.c_int, C.c_int, C.c_int, _P)
     d("tfo_gemm_int4", None, _P, _P, _P, C.c_int, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int,
+      C.c_int)
+    d("tfo_gemm_affine", None, _P, _P, _P, C.c_int, C.c_int, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int,
       C.c_int)
     d("tfo_rmsnorm", None, _P, _P, C.c_int, C.c_float, _P)
     d("tfo_greedy_argmax", C.c_uint32, _P, C.c_int)
@@ -570,7 +574,7 @@ def group_pairs(pairs, query_count, top_k, num_experts, tile_expert_count=16, so
 
 
 def grouped_route_partials(sorted_pairs, hidden_f16, hidden_stride, pool, stride, off, top_k, d, f,
-                           query_count, fmt=FMT_F16):
+                           query_count, fmt=FMT_F16, bits=4):
     """cpuSyntheticRoutePartials (T/Kernels/Prefill/PrefillGroupedRoutedMoETests.swift:229-279).
     Unwritten (token, rank) slots keep the sentinel -99 as in the reference."""
     sp = np.ascontiguousarray(sorted_pairs, dtype=PAIR_DTYPE)
@@ -578,9 +582,9 @@ def grouped_route_partials(sorted_pairs, hidden_f16, hidden_stride, pool, stride
     pool = _c(pool, np.uint8)
     out = np.full(query_count * top_k * d, np.float16(-99).view(np.uint16), np.uint16)
     o = _offsets(off)
-    lib().tfo_grouped_route_partials(_ptr(sp), sp.size, _ptr(hidden_f16), hidden_stride,
-                                     _ptr(pool), int(stride), C.byref(o), fmt, top_k, d, f,
-                                     _ptr(out))
+    lib().tfo_grouped_route_partials_bits(_ptr(sp), sp.size, _ptr(hidden_f16), hidden_stride,
+                                          _ptr(pool), int(stride), C.byref(o), fmt, bits, top_k, d, f,
+                                          _ptr(out))
     return out
 
 
@@ -592,7 +596,7 @@ def reduce_token_major(partials_f16, weights_f16, rows, top_k, d):
     return out
 
 
-def gemm_int4(W, S, B, X, fmt=FMT_F16, rows=None):
+def gemm_int4(W, S, B, X, fmt=FMT_F16, rows=None, bits=4):
     """MPPPrefillInt4QMMTests.cpuReference (T/Kernels/TensorCore/MPPPrefillInt4QMMTests.swift:80-105),
     fp32 accumulator (unrounded). rows=(r0, r1) computes a bounded sample of token rows."""
     W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16); X = _c(X, np.float32)
@@ -600,7 +604,7 @@ def gemm_int4(W, S, B, X, fmt=FMT_F16, rows=None):
     N = W.shape[0]
     r0, r1 = (0, M) if rows is None else rows
     Y = np.zeros((M, N), np.float32)
-    lib().tfo_gemm_int4(_ptr(W), _ptr(S), _ptr(B), fmt, _ptr(X), M, N, K, _ptr(Y), r0, r1)
+    lib().tfo_gemm_affine(_ptr(W), _ptr(S), _ptr(B), fmt, bits, _ptr(X), M, N, K, _ptr(Y), r0, r1)
     return Y
 
 

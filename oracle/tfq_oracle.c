@@ -630,9 +630,10 @@ int tfo_prefill_router(const uint8_t *W, const uint16_t *S, const uint16_t *B, i
 
 /* cpuInt4Dot (PrefillGroupedRoutedMoETests.swift:281-303): acc += (q*s + b) * x. */
 static float int4_dot_blob(const uint8_t *blob, uint32_t w_off, uint32_t s_off, uint32_t b_off,
-                           int fmt, int row, int n, const float *x) {
+                           int fmt, int bits, int row, int n, const float *x) {
     int groups = n / TFO_GROUP;
-    const uint8_t *w_row = blob + w_off + (size_t)row * (n / 2);
+    size_t rb = tfo_affine_row_bytes((size_t)n, bits);
+    const uint8_t *w_row = blob + w_off + (size_t)row * rb;
     const uint16_t *s_row = (const uint16_t *)(blob + s_off) + (size_t)row * groups;
     const uint16_t *b_row = (const uint16_t *)(blob + b_off) + (size_t)row * groups;
     float acc = 0.0f;
@@ -640,7 +641,7 @@ static float int4_dot_blob(const uint8_t *blob, uint32_t w_off, uint32_t s_off, 
         float scale = tfo_decode_scale(s_row[g], fmt), bias = tfo_decode_scale(b_row[g], fmt);
         for (int k = 0; k < TFO_GROUP; ++k) {
             int col = g * TFO_GROUP + k;
-            float q = (float)tfo_int4_code(w_row, (size_t)col);
+            float q = (float)tfo_affine_code(w_row, rb, (size_t)col, bits);
             float w = q * scale;
             w = w + bias;
             float p = w * x[col];
@@ -656,6 +657,17 @@ void tfo_grouped_route_partials(const tfo_pair *sorted, int64_t n_pairs,
                                 const uint8_t *pool, uint64_t stride,
                                 const tfo_expert_offsets *o, int fmt,
                                 int top_k, int d, int f, uint16_t *partials) {
+    tfo_grouped_route_partials_bits(sorted, n_pairs, hidden_f16, hidden_stride, pool, stride, o, fmt, 4,
+                                    top_k, d, f, partials);
+}
+
+/* The same over experts of `bits`-bit rows (the b2/b3 grouped kernels,
+ * prefill.metal:1223-1450, compute this per pair). */
+void tfo_grouped_route_partials_bits(const tfo_pair *sorted, int64_t n_pairs,
+                                     const uint16_t *hidden_f16, int hidden_stride,
+                                     const uint8_t *pool, uint64_t stride,
+                                     const tfo_expert_offsets *o, int fmt, int bits,
+                                     int top_k, int d, int f, uint16_t *partials) {
     float *x = (float *)malloc(sizeof(float) * (size_t)d);
     float *act = (float *)malloc(sizeof(float) * (size_t)f);
     for (int64_t p = 0; p < n_pairs; ++p) {
@@ -664,14 +676,14 @@ void tfo_grouped_route_partials(const tfo_pair *sorted, int64_t n_pairs,
         for (int i = 0; i < d; ++i)
             x[i] = tfo_f16_to_f32(hidden_f16[(size_t)pr->token * hidden_stride + i]);
         for (int r = 0; r < f; ++r) {
-            float gate = int4_dot_blob(blob, o->gate_w, o->gate_s, o->gate_b, fmt, r, d, x);
-            float up = int4_dot_blob(blob, o->up_w, o->up_s, o->up_b, fmt, r, d, x);
+            float gate = int4_dot_blob(blob, o->gate_w, o->gate_s, o->gate_b, fmt, bits, r, d, x);
+            float up = int4_dot_blob(blob, o->up_w, o->up_s, o->up_b, fmt, bits, r, d, x);
             float a = tfo_gelu_tanh(gate) * up;
             act[r] = tfo_f16_to_f32(tfo_f32_to_f16(a));
         }
         size_t out_base = ((size_t)pr->token * top_k + pr->rank) * d;
         for (int r = 0; r < d; ++r) {
-            float v = int4_dot_blob(blob, o->down_w, o->down_s, o->down_b, fmt, r, f, act);
+            float v = int4_dot_blob(blob, o->down_w, o->down_s, o->down_b, fmt, bits, r, f, act);
             partials[out_base + r] = tfo_f32_to_f16(v);
         }
     }
@@ -698,8 +710,15 @@ void tfo_reduce_token_major(const uint16_t *partials, const uint16_t *weights, i
  * accumulator.addProduct(weight, x) (fused). */
 void tfo_gemm_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
                    const float *X, int M, int N, int K, float *Y, int row0, int row1) {
+    tfo_gemm_affine(W, S, B, fmt, 4, X, M, N, K, Y, row0, row1);
+}
+
+/* tfo_gemm_int4 over `bits`-bit rows: the 3-bit prefill QMM
+ * (prefill.metal:711-757) computes the same sum. */
+void tfo_gemm_affine(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt, int bits,
+                     const float *X, int M, int N, int K, float *Y, int row0, int row1) {
     int groups = K / TFO_GROUP;
-    size_t row_bytes = (size_t)K / 2;
+    size_t row_bytes = tfo_affine_row_bytes((size_t)K, bits);
     if (row0 < 0) row0 = 0;
     if (row1 > M) row1 = M;
     for (int t = row0; t < row1; ++t) {
@@ -712,7 +731,7 @@ void tfo_gemm_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int f
                 float bias = tfo_decode_scale(B[(size_t)n * groups + g], fmt);
                 for (int lk = 0; lk < TFO_GROUP; ++lk) {
                     int col = g * TFO_GROUP + lk;
-                    float w = (float)tfo_int4_code(wr, (size_t)col) * scale;
+                    float w = (float)tfo_affine_code(wr, row_bytes, (size_t)col, bits) * scale;
                     w = w + bias;
                     acc = fmaf(w, xr[col], acc);
                 }

@@ -174,6 +174,12 @@ void tfo_grouped_route_partials(const tfo_pair *sorted, int64_t n_pairs,
                                 const uint8_t *pool, uint64_t stride,
                                 const tfo_expert_offsets *off, int scale_fmt,
                                 int top_k, int d, int f, uint16_t *partials_f16);
+/* tfo_grouped_route_partials over experts of `bits`-bit rows (2, 3, 4). */
+void tfo_grouped_route_partials_bits(const tfo_pair *sorted, int64_t n_pairs,
+                                     const uint16_t *hidden_f16, int hidden_stride,
+                                     const uint8_t *pool, uint64_t stride,
+                                     const tfo_expert_offsets *off, int scale_fmt, int bits,
+                                     int top_k, int d, int f, uint16_t *partials);
 
 /* cpuReduce (T/Kernels/Prefill/PrefillMoETests.swift:46-58). */
 void tfo_reduce_token_major(const uint16_t *partials_f16, const uint16_t *weights_f16,
@@ -184,6 +190,9 @@ void tfo_reduce_token_major(const uint16_t *partials_f16, const uint16_t *weight
  * Rows of Y in [row0, row1) are computed (a bounded sample for timing). */
 void tfo_gemm_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
                    const float *X, int M, int N, int K, float *Y, int row0, int row1);
+/* tfo_gemm_int4 over `bits`-bit rows (2, 3, 4). */
+void tfo_gemm_affine(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt, int bits,
+                     const float *X, int M, int N, int K, float *Y, int row0, int row1);
 
 /* ---- decode layer (config 4) ----
  * RmsNormRef.apply (V/Reference/Primitives/RmsNorm.swift:14-44):

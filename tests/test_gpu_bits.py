@@ -14,7 +14,7 @@ import pytest
 
 import oracle
 from edgeexpert_amd import ops, synth
-from edgeexpert_amd._lib import ROUTER_WORKSPACE_BYTES, TfqError, TFQ_E_INVAL, TFQ_E_UNSUPPORTED
+from edgeexpert_amd._lib import DTYPE_BF16, DTYPE_F16, ROUTER_WORKSPACE_BYTES, TfqError, TFQ_E_INVAL
 from edgeexpert_amd.runtime import DeviceBuffer
 from helpers import from_f16_bits
 
@@ -179,12 +179,94 @@ def test_pool_width_checks(ctx, stream):
     with pytest.raises(TfqError) as e:
         moe.encode_routed_phase1(stream, small, idx, x, acts, D, F, K)
     assert e.value.status == TFQ_E_INVAL
-    # the grouped prefill kernels are 4-bit only
-    ws_bytes = ops.moe_prefill_workspace_bytes(4, K, E, D, F)
-    Wr, Sr, Br = synth.int8_matrix(3, "chk/router", E, D)
-    router = ops.Router(_dev(Wr), _dev(Sr), _dev(Br), E)
+
+
+# ---------------------------------------------------------------- prefill ----
+
+@pytest.mark.parametrize("t,n,k,dtype", [(1, 64, 64, DTYPE_F16), (37, 300, 320, DTYPE_BF16),
+                                         (512, 8192, 2816, DTYPE_BF16), (130, 1024, 8192, DTYPE_F16)])
+def test_prefill_gemm_b3(ctx, stream, t, n, k, dtype):
+    # PrefillInt4QMM.encode(..., bits: 3) (prefill.metal:711-757); config 2's
+    # shape among them, rows checked on a sample of tokens
+    W, S, B = synth.affine_matrix(7, f"b3/gemm/{n}x{k}", n, k, 3)
+    xf = synth.normal(synth.seed_key(7, f"b3/gemm/x{t}x{k}"), t * k)
+    xbits = synth.bf16_bits(xf) if dtype == DTYPE_BF16 else synth.f16_bits(xf)
+    xr = (synth.bf16_to_f32(xbits) if dtype == DTYPE_BF16 else from_f16_bits(xbits)).reshape(t, k)
+    y = _dev(np.full(t * n, 0x7E00, np.uint16))
+    ops.PrefillInt4QMM(ctx).encode(stream, _dev(W), _dev(S), _dev(B), _dev(xbits), y, t, n, k, dtype, bits=3)
+    stream.sync()
+    yb = y.download(np.uint16).reshape(t, n)
+    got = synth.bf16_to_f32(yb) if dtype == DTYPE_BF16 else from_f16_bits(yb)
+    rows = (0, t) if t <= 64 else (t - 40, t)
+    ref = oracle.gemm_int4(W, S, B, xr, rows=rows, bits=3)[rows[0]:rows[1]]
+    got = got[rows[0]:rows[1]]
+    if dtype == DTYPE_F16:
+        rel = oracle.rel_error(got, ref)
+        assert rel < TOL, f"t={t} n={n} k={k}: rel={rel}"
+    else:   # bf16 output: the bar plus bf16's own rounding (2^-8 relative), as for the int4 QMM
+        bound = TOL * np.abs(ref).max() + 2.0 ** -8 * np.abs(ref)
+        assert np.all(np.abs(got - ref) <= bound), f"max excess {np.max(np.abs(got - ref) - bound)}"
+
+
+def test_prefill_gemm_rejects_other_widths(ctx, stream):
+    W, S, B = synth.affine_matrix(7, "b3/gemm/bad", 64, 64, 2)
     with pytest.raises(TfqError) as e:
-        ops.moe_prefill(ctx, stream, router, pool, _dev(np.zeros(4 * D, np.uint16)), D, 4, D, F, K,
-                        _dev(np.zeros(4 * D, np.uint16)), _dev(np.zeros(4 * K, np.uint32)),
-                        _dev(np.zeros(4 * K, np.uint16)), DeviceBuffer(ws_bytes), ws_bytes)
-    assert e.value.status == TFQ_E_UNSUPPORTED
+        ops.PrefillInt4QMM(ctx).encode(stream, _dev(W), _dev(S), _dev(B), _dev(np.zeros(64, np.uint16)),
+                                       _dev(np.zeros(64, np.uint16)), 1, 64, 64, DTYPE_F16, bits=2)
+    assert e.value.status == TFQ_E_INVAL
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_moe_prefill_end_to_end_bits(ctx, stream, bits):
+    # router -> grouping -> grouped 2/3-bit experts -> combine (tfq_moe_prefill;
+    # prefill.metal:1304-1450 for the reference's 2/3-bit grouped experts)
+    T, k, E, d, f = 96, 8, 32, 512, 256
+    pool_bytes, pool, offs, stride = _pool(bits, E, d, f, f"pf{bits}/experts", seed=1)
+    Wr, Sr, Br = synth.int8_matrix(1, "pf/router", E, d)
+    hidden = synth.f16_vector(1, f"pf{bits}/x", T * d)
+    router = ops.Router(_dev(Wr), _dev(Sr), _dev(Br), E)
+    wsb = ops.moe_prefill_workspace_bytes(T, k, E, d, f)
+    idx, w16 = _dev(np.zeros(T * k, np.uint32)), _dev(np.zeros(T * k, np.uint16))
+    h2 = _dev(np.zeros(T * d, np.uint16))
+    ops.moe_prefill(ctx, stream, router, pool, _dev(hidden), d, T, d, f, k, h2, idx, w16, DeviceBuffer(wsb), wsb)
+    stream.sync()
+    got_idx = idx.download(np.uint32).reshape(T, k)
+    ref_idx, _ = oracle.prefill_router(Wr, Sr, Br, from_f16_bits(hidden).reshape(T, d), k)
+    assert np.array_equal(got_idx, ref_idx)
+    w_dev = w16.download(np.uint16)
+    pairs = ops.PrefillRouter.make_token_expert_pairs(got_idx, w_dev, T, k)
+    grp = oracle.group_pairs(pairs.astype(oracle.PAIR_DTYPE), T, k, E, 16)
+    o = oracle.ExpertOffsets(*[int(offs[n]) for n in synth.OFFSET_ORDER])
+    ref = oracle.grouped_route_partials(grp["sorted"], hidden, d, pool_bytes, stride, o, k, d, f, T, bits=bits)
+    ref_h2 = from_f16_bits(oracle.reduce_token_major(ref, w_dev, T, k, d))
+    rel = oracle.rel_error(from_f16_bits(h2.download(np.uint16)), ref_h2)
+    assert rel < TOL, f"bits={bits}: rel={rel}"
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_grouped_experts_config3_shape_sampled(ctx, stream, bits):
+    # config 3's shape (512 tokens x top-8 of 128 experts, Zipf routing) with
+    # 2/3-bit experts: the grouped partials of 8 sampled tokens
+    T, k, E, d, f = 512, 8, 128, 2816, 704
+    pool_bytes, pool, offs, stride = _pool(bits, E, d, f, f"c3b{bits}/experts", seed=0)
+    idx, w16 = synth.zipf_routing(0, "c3/route", T, E, k)
+    hidden = synth.f16_vector(0, "c3/x", T * d)
+    n, mt = T * k, ops.max_tiles(T, k, E)
+    b = {n_: DeviceBuffer(sz) for n_, sz in (("sorted", n * 16), ("offsets", E * 4), ("counts", E * 4),
+                                            ("tiles", mt * 16), ("n_tiles", 4), ("status", 4))}
+    ops.PrefillMoEGrouping(ctx).encode(stream, _dev(idx), _dev(w16), T, k, E, b["sorted"], b["offsets"],
+                                       b["counts"], b["tiles"], b["n_tiles"], b["status"])
+    act = _dev(np.zeros(n * f, np.uint16))
+    parts = _dev(np.zeros(n * d, np.uint16))
+    ops.PrefillGroupedRoutedMoE(ctx).encode(stream, pool, b["sorted"], b["tiles"], b["n_tiles"], mt, _dev(hidden),
+                                            d, d, f, k, act, parts)
+    stream.sync()
+    sorted_p = np.frombuffer(b["sorted"].download(np.uint8, n * 16).tobytes(), oracle.PAIR_DTYPE)
+    toks = np.array([0, 5, 100, 255, 256, 400, 500, 511])
+    sel = sorted_p[np.isin(sorted_p["token"], toks)]
+    o = oracle.ExpertOffsets(*[int(offs[n_]) for n_ in synth.OFFSET_ORDER])
+    ref = oracle.grouped_route_partials(sel, hidden, d, pool_bytes, stride, o, k, d, f, T, bits=bits)
+    gp = from_f16_bits(parts.download(np.uint16)).reshape(T, k, d)
+    rp = from_f16_bits(ref).reshape(T, k, d)
+    rel = oracle.rel_error(gp[toks], rp[toks])
+    assert rel < TOL, f"bits={bits}: rel={rel}"

@@ -103,6 +103,41 @@ def test_moe_matches_int4_oracle_on_the_same_codes(bits):
     assert np.isfinite(y).all() and np.abs(y).max() > 0
 
 
+@pytest.mark.parametrize("bits", [2, 3])
+def test_gemm_matches_int4_oracle_on_the_same_codes(bits):
+    M, N, K = 5, 16, 192
+    W, S, B = synth.affine_matrix(6, f"pin/gemm{bits}", N, K, bits)
+    X = synth.normal(synth.seed_key(6, "pin/gemm/x"), M * K).reshape(M, K)
+    Y = oracle.gemm_int4(W, S, B, X, bits=bits)
+    Y4 = oracle.gemm_int4(_as_nibbles(W, K, bits), S, B, X)
+    assert np.array_equal(Y.view(np.uint32), Y4.view(np.uint32)) and np.abs(Y).max() > 0
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_grouped_partials_match_int4_oracle_on_the_same_codes(bits):
+    D, F, E, T, k = 128, 64, 4, 3, 2
+    pool, offs, stride = synth.expert_pool(8, f"pin/gp{bits}", E, D, F, align=256, bits=bits)
+    offs4, stride4 = synth.expert_layout(D, F, align=256)
+    pool4 = np.zeros(E * stride4, np.uint8)
+    for e in range(E):
+        blob = pool[e * stride:(e + 1) * stride]
+        for proj in ("gate", "up", "down"):
+            w, s, b = synth.blob_views(blob, offs, D, F, proj, bits)
+            cols = D if proj != "down" else F
+            for key, arr in (("w", _as_nibbles(w, cols, bits)), ("s", s), ("b", b)):
+                raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
+                o = e * stride4 + offs4[f"{proj}_{key}"]
+                pool4[o:o + raw.size] = raw
+    pairs = np.zeros(T * k, oracle.PAIR_DTYPE)
+    pairs["token"] = np.repeat(np.arange(T), k)
+    pairs["rank"] = np.tile(np.arange(k), T)
+    pairs["expert"] = [3, 1, 0, 3, 2, 1]
+    hidden = synth.f16_vector(8, "pin/gp/h", T * D)
+    got = oracle.grouped_route_partials(pairs, hidden, D, pool, stride, offs, k, D, F, T, bits=bits)
+    ref = oracle.grouped_route_partials(pairs, hidden, D, pool4, stride4, offs4, k, D, F, T)
+    assert np.array_equal(got, ref)
+
+
 def test_synth_affine_matrix_shapes():
     for bits in (2, 3, 4):
         W, S, B = synth.affine_matrix(1, "shape", 3, 128, bits)
