@@ -76,15 +76,17 @@ def c4_bytes():
     return parts
 
 
-def bench_c3(ctx, stream, batch_avg_us):
+def bench_c3(ctx, stream, batch_avg_us, bits=4):
     """Config 3: 512 tokens x top-8 of 128 experts with Zipf(1.1) popularity;
     device grouping -> grouped gate/up + GeGLU -> grouped down -> token-major
-    combine (4 launches), timed back to back over rotated hidden states."""
+    combine (4 launches), timed back to back over rotated hidden states.
+    bits: code width of the experts (4, or the 2/3-bit variants)."""
     from edgeexpert_amd import ops, synth
     from edgeexpert_amd.runtime import DeviceBuffer
     T, k = 512, 8
-    pool_bytes, offs, stride = synth.expert_pool(0, "c1/experts", E, D, F)
-    pool = ops.ExpertPool(DeviceBuffer.from_array(pool_bytes), stride, E, offs)
+    label = "c1/experts" if bits == 4 else f"c1b{bits}/experts"
+    pool_bytes, offs, stride = synth.expert_pool(0, label, E, D, F, bits=bits)
+    pool = ops.ExpertPool(DeviceBuffer.from_array(pool_bytes), stride, E, offs, weight_bits=bits)
     idx, w16 = synth.zipf_routing(0, "c3/route", T, E, k)
     active = np.unique(idx)
     n_hidden = 4
@@ -105,9 +107,9 @@ def bench_c3(ctx, stream, batch_avg_us):
 
     us = batch_avg_us(chunk, 8, reps_=3)
     flop = 2.0 * n * 3 * D * F
-    wbytes = len(active) * 3 * (F * D // 2 + 2 * F * (D // 64) * 2)
+    wbytes = len(active) * 3 * (F * D * bits // 8 + 2 * F * (D // 64) * 2)
     nbytes = wbytes + 2 * T * D * 2
-    log(f"grouped MoE prefill C3: {us:.1f} us per 512-token chunk ({flop / (us * 1e-6) / 1e12:.1f} TFLOP/s, "
+    log(f"grouped MoE prefill C3 ({bits}-bit experts): {us:.1f} us per 512-token chunk ({flop / (us * 1e-6) / 1e12:.1f} TFLOP/s, "
         f"{nbytes / (us * 1e-6) / 1e9:.0f} GB/s of {len(active)} active experts' weights)")
     return {"us_per_chunk": round(us, 2), "tokens": T, "top_k": k, "active_experts": int(len(active)),
             "tflops": round(flop / (us * 1e-6) / 1e12, 1), "weight_bytes": wbytes,
@@ -174,6 +176,19 @@ def bench_bits(ctx, stream, batch_avg_us, router, hbuf):
     log(f"3-bit GEMV {Ml}x{n}: {us:.1f} us ({gbs:.0f} GB/s, {gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
     out["gemv_b3_lmhead"] = {"shape": [Ml, n], "bytes": nbytes, "us": round(us, 2), "gbs": round(gbs, 1),
                              "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del big, sb, bb, yl
+    # 3-bit prefill GEMM at config 2's shape (bf16 activations)
+    from edgeexpert_amd._lib import DTYPE_BF16
+    Mg, Ng, Kg = 512, 8192, 2816
+    Wg, Sg, Bg = synth.affine_matrix(0, "c2/w3", Ng, Kg, 3)
+    gW, gS, gB = (DeviceBuffer.from_array(a) for a in (Wg, Sg, Bg))
+    gX = DeviceBuffer.from_array(synth.bf16_vector(0, "c2/x", Mg * Kg))
+    gY = DeviceBuffer(Mg * Ng * 2)
+    qmm = ops.PrefillInt4QMM(ctx)
+    g_us = batch_avg_us(lambda i: qmm.encode(stream, gW, gS, gB, gX, gY, Mg, Ng, Kg, DTYPE_BF16, bits=3), 20)
+    tf = 2.0 * Mg * Ng * Kg / (g_us * 1e-6) / 1e12
+    log(f"3-bit GEMM C2 (bf16): {g_us:.2f} us -> {tf:.1f} TFLOP/s")
+    out["gemm_b3_c2"] = {"shape": [Mg, Ng, Kg], "us": round(g_us, 3), "tflops": round(tf, 1)}
     return out
 
 
@@ -470,6 +485,8 @@ def main():
 
     # ------------------------------------------------- 2/3-bit variants ----
     bits_legs = None if args.no_bits else bench_bits(ctx, stream, batch_avg_us, router, hbuf)
+    if bits_legs is not None and not args.no_c3:
+        bits_legs["grouped_prefill_c3_b3"] = bench_c3(ctx, stream, batch_avg_us, bits=3)
 
     # -------------------------------------- HBM counter calibration kernels ----
     # One plain read (64 MiB) and one plain copy (32 MiB in, 32 MiB out) of
