@@ -3,7 +3,9 @@
 //     Y[t][n] = Σ_k X[t][k] · W[n][k]
 // W affine int4 g64 with fp16 scale/bias, X fp16 (or bf16, converted),
 // fp32 accumulate (S/Metal/TensorCore/tensorops.metal:13-105 and
-// S/Metal/Prefill/prefill.metal:672-709 compute the same product).
+// S/Metal/Prefill/prefill.metal:672-709 compute the same product). The
+// 3-bit and 2-bit rows (prefill.metal:711-757,1223-1450) run the same tiles
+// with the chunk load and unpack of common.hpp (template parameter BITS).
 //
 // Weights are dequantised in registers: (0x6400 | q) - 1024 gives q exactly
 // as fp16, then v_pk_fma_f16(q, s, b) rounds q·s + b once to fp16 — the fp16

@@ -1,9 +1,10 @@
 // gemv.hpp — decode-side GEMVs: int4 g64 (plain and fused QKV), int8 g64,
 // the int8 router logits + top-k selection, and the BF16 -> fp16 converter.
 //
-// Mapping (all GEMVs): one 16-byte chunk of a weight row per lane, so every
-// weight byte arrives through a 128-bit load and a segment's lanes read one
-// contiguous run of the row. A row of n codes has n/32 (int4) or n/16 (int8)
+// Mapping (all GEMVs): one chunk of a weight row per lane — 32 codes, 16
+// bytes at 4 bits (12 at 3, 8 at 2; 16 int8 codes) — so every weight byte
+// arrives through one wide load and a segment's lanes read one contiguous
+// run of the row. A row of n codes has n/32 (2/3/4-bit) or n/16 (int8)
 // chunks; a segment of SEG lanes walks them with stride SEG (P chunks per
 // lane). Lane <-> chunk is fixed for the whole kernel, so each lane keeps the
 // activations of its P chunks in registers (staged once through LDS) together

@@ -16,6 +16,9 @@
 // Both start with the loads that nothing depends on (activations, expert
 // indices, routing weights), issue the weight loads as soon as the indices
 // are in, and stage the activations into LDS while the weights arrive.
+// Every phase is templated on the experts' code width (BITS = 4, or the
+// 2/3-bit variants of moe.metal:644-1180); only the chunk load and unpack
+// differ (common.hpp QChunk / dot_chunk).
 #pragma once
 
 #include "gemv.hpp"
