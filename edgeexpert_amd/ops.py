@@ -563,7 +563,8 @@ class DecodeLayerWeightsSpec:
         router = Router(buf(w["router_w"]), buf(w["router_s"]), buf(w["router_b"]), E,
                         buf(w["router_eff"]) if w.get("router_eff") is not None else None,
                         buf(w["router_gain"]) if w.get("router_gain") is not None else None)
-        pool = ExpertPool(buf(w["pool"]), int(w["stride"]), E, dict(w["off"]))
+        pool = ExpertPool(buf(w["pool"]), int(w["stride"]), E, dict(w["off"]),
+                          weight_bits=int(w.get("expert_bits", 4)))
         return cls(buf(w["input_norm"]), q4(w["q"]), q4(w["k"]), q4(w["v"]), buf(w["q_norm"]),
                    buf(w["k_norm"]), q4(w["o"]), buf(w["post_attention_norm"]), buf(w["pre_ffn_norm"]),
                    buf(w["pre_ffn2_norm"]), router, pool, q4(w["shared_gate"]), q4(w["shared_up"]),

@@ -236,7 +236,7 @@ def norm_weight(seed: int, label: str, n: int, lo: float = 0.5, hi: float = 1.5)
 
 
 def decode_layer(seed: int, label: str, d: int, nq: int, nkv: int, hd: int, num_experts: int,
-                 f: int, fs: int, layer_scalar: float = 0.75) -> dict:
+                 f: int, fs: int, layer_scalar: float = 0.75, expert_bits: int = 4) -> dict:
     """Weights of one Gemma 4 decoder layer with the BASELINE distributions:
     int4 g64 projections as in config 0, an int8 g64 router, num_experts
     routed experts in one pool, an int4 shared expert, and RMSNorm weights
@@ -268,6 +268,6 @@ def decode_layer(seed: int, label: str, d: int, nq: int, nkv: int, hd: int, num_
     w.update(router_w=rw, router_s=rs, router_b=rb,
              router_eff=norm_weight(seed, L + "/router_eff", d),
              router_gain=norm_weight(seed, L + "/router_gain", num_experts))
-    pool, offsets, stride = expert_pool(seed, L + "/experts", num_experts, d, f)
-    w.update(pool=pool, off=offsets, stride=stride)
+    pool, offsets, stride = expert_pool(seed, L + "/experts", num_experts, d, f, bits=expert_bits)
+    w.update(pool=pool, off=offsets, stride=stride, expert_bits=expert_bits)
     return w

@@ -84,7 +84,7 @@ class LayerWeights(C.Structure):
                 ("pool", _P), ("stride", C.c_uint64), ("off", ExpertOffsets),
                 ("shared_gate", Q4), ("shared_up", Q4), ("shared_down", Q4),
                 ("post_ffn1_norm", _P), ("post_ffn2_norm", _P), ("post_ffn_norm", _P),
-                ("layer_scalar", C.c_float)]
+                ("layer_scalar", C.c_float), ("expert_bits", C.c_int)]
 
 
 class LayerShape(C.Structure):
@@ -518,7 +518,8 @@ def decode_layer(w: dict, shape: dict, hidden_f16, k_cache_f16, v_cache_f16, pos
         pool=arr(w["pool"], np.uint8), stride=int(w["stride"]), off=_offsets(w["off"]),
         shared_gate=q4(w["shared_gate"]), shared_up=q4(w["shared_up"]), shared_down=q4(w["shared_down"]),
         post_ffn1_norm=arr(w["post_ffn1_norm"], np.uint16), post_ffn2_norm=arr(w["post_ffn2_norm"], np.uint16),
-        post_ffn_norm=arr(w["post_ffn_norm"], np.uint16), layer_scalar=float(w["layer_scalar"]))
+        post_ffn_norm=arr(w["post_ffn_norm"], np.uint16), layer_scalar=float(w["layer_scalar"]),
+        expert_bits=int(w.get("expert_bits", 4)))
     ls = LayerShape(**{k_: shape[k_] for k_ in ("d", "nq", "nkv", "hd", "rotated_pairs", "window", "f", "fs",
                                                  "k", "eps", "theta", "scale")})
     d, qd = shape["d"], shape["nq"] * shape["hd"]

@@ -956,7 +956,8 @@ void tfo_decode_layer(const tfo_layer_weights *w, const tfo_layer_shape *s,
     round_vec(h1, (size_t)d);
     /* routed phases (:2849-2862), zero residual */
     float *h2 = (float *)malloc(sizeof(float) * (size_t)d);
-    tfo_moe_routed(w->pool, w->stride, &w->off, TFO_FMT_F16, routed_x, NULL, idx, rw, k, d, s->f, h2);
+    tfo_moe_routed_bits(w->pool, w->stride, &w->off, TFO_FMT_F16, w->expert_bits ? w->expert_bits : 4, routed_x,
+                        NULL, idx, rw, k, d, s->f, h2);
     round_vec(h2, (size_t)d);
     if (trace) {
         store_f16(trace->h1, h1, (size_t)d);

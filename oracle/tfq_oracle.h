@@ -246,6 +246,7 @@ typedef struct {
     tfo_q4 shared_gate, shared_up, shared_down;
     const uint16_t *post_ffn1_norm, *post_ffn2_norm, *post_ffn_norm;
     float layer_scalar;
+    int expert_bits;    /* code width of the routed experts: 2, 3 or 4 (0 reads as 4) */
 } tfo_layer_weights;
 
 typedef struct {

@@ -109,9 +109,9 @@ def _spec(shape):
                                     attn_scale=shape["scale"])
 
 
-def _layer_case(ctx, stream, shape, E, pos, cap, seed, label, in_place=False):
+def _layer_case(ctx, stream, shape, E, pos, cap, seed, label, in_place=False, expert_bits=4):
     w = synth.decode_layer(seed, label, shape["d"], shape["nq"], shape["nkv"], shape["hd"], E, shape["f"],
-                           shape["fs"])
+                           shape["fs"], expert_bits=expert_bits)
     kvd = shape["nkv"] * shape["hd"]
     kc = synth.f16_vector(seed, label + "/kc", cap * kvd)
     vc = synth.f16_vector(seed, label + "/vc", cap * kvd)
@@ -189,7 +189,7 @@ def _check_layer(got, ref, w, shape, hidden, label):
     sh = (w["shared_gate"], w["shared_up"], w["shared_down"])
     stage["h1"] = f16_round(oracle.shared_expert_int4(*sh, _n16(h, w["pre_ffn_norm"], eps), d, shape["fs"]))
     stage["h2"] = f16_round(oracle.moe_routed(w["pool"], w["stride"], w["off"], _n16(h, w["pre_ffn2_norm"], eps),
-                                              ridx, got["w"], d, shape["f"]))
+                                              ridx, got["w"], d, shape["f"], bits=w.get("expert_bits", 4)))
     h12 = f16_round(_n16(got["h1"], w["post_ffn1_norm"], eps) + _n16(got["h2"], w["post_ffn2_norm"], eps))
     stage["out"] = f16_round(f16_round(h + _n16(h12, w["post_ffn_norm"], eps)) *
                              f16_round(np.float32(w["layer_scalar"])))
@@ -217,6 +217,14 @@ def test_layer_small_window_and_partial_rotary(ctx, stream):
     shape = dict(SMALL, window=64, rotated_pairs=16, theta=1e6)
     got, ref, w, hid = _layer_case(ctx, stream, shape, 8, 200, 256, 4, "small-swa")
     _check_layer(got, ref, w, shape, hid, "small window")
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_layer_small_with_2_3_bit_experts(ctx, stream, bits):
+    # the routed experts of the layer at 2/3 bits (the pool's weight_bits;
+    # quant.routedExpert.weightBits, Model.swift:61-63)
+    got, ref, w, hid = _layer_case(ctx, stream, SMALL, 8, 70, 160, 7, f"small-b{bits}", expert_bits=bits)
+    _check_layer(got, ref, w, SMALL, hid, f"small {bits}-bit experts")
 
 
 def test_layer_in_place_equals_out_of_place(ctx, stream):
