@@ -453,7 +453,8 @@ int tfq_group_pairs_host(const tfq_pair *pairs, int64_t n_pairs, int64_t query_c
  * (token, rank) slots without a pair are left untouched. max_tiles is the
  * launch bound (TFQ_MOE_MAX_TILES); the device *n_tiles decides. Replaces
  * PrefillGroupedRoutedMoE.encodeStreamedBatched
- * (S/Kernels/Prefill/MoE/PrefillGroupedRoutedMoE.swift:446-527).
+ * (S/Kernels/Prefill/MoE/PrefillGroupedRoutedMoE.swift:446-527), and its
+ * 2/3-bit forms (prefill.metal:1304-1450) when pool->weight_bits is 2 or 3.
  * Contract: d, f multiples of 64 and at most 8192 (TFQ_E_UNSUPPORTED
  * beyond); hidden rows 16-byte aligned. */
 int tfq_moe_grouped(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
