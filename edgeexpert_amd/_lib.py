@@ -11,7 +11,11 @@ import os
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libtfq.so")
-CODE_OBJECT_PATH = os.path.join(LIB_DIR, "tfq_kernels.co")
+# the code objects edgeexpert_amd.build writes (one per kernel translation unit)
+CODE_OBJECT_UNITS = ("tfq_gemv", "tfq_int8", "tfq_phase1", "tfq_phase1_routed", "tfq_moe", "tfq_gemm",
+                     "tfq_prefill", "tfq_attention")
+CODE_OBJECT_PATHS = [os.path.join(LIB_DIR, u + ".co") for u in CODE_OBJECT_UNITS]
+CODE_OBJECT_PATH = LIB_DIR
 
 TFQ_OK = 0
 TFQ_E_INVAL = 1
@@ -23,6 +27,10 @@ ROUTER_WORKSPACE_BYTES = 4096
 LM_HEAD_WORKSPACE_BYTES = 65536
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
+GEMM_PATH_AUTO = 0
+GEMM_PATH_TILE = 1
+GEMM_PATH_SKINNY = 2
+GEMM_PATH_SKINNY32 = 3
 
 
 class TfqNotBuilt(RuntimeError):
@@ -71,7 +79,7 @@ class DecodeLayerWeights(C.Structure):
                 ("pre_ffn2_norm", C.c_void_p), ("router", RouterDesc), ("experts", ExpertPoolDesc),
                 ("shared_gate", Q4Matrix), ("shared_up", Q4Matrix), ("shared_down", Q4Matrix),
                 ("post_ffn1_norm", C.c_void_p), ("post_ffn2_norm", C.c_void_p),
-                ("post_ffn_norm", C.c_void_p), ("layer_scalar", C.c_float)]
+                ("post_ffn_norm", C.c_void_p), ("layer_scalar", C.c_float), ("shared_bits", C.c_uint32)]
 
 
 class DecodeLayerShape(C.Structure):
@@ -124,10 +132,16 @@ SIGNATURES = {
                              _U32, _U32, _U32, _P, _P, _P, _P],
     "tfq_shared_expert_q4": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
                              _P, _P, _U32, _U32, _P],
+    "tfq_shared_expert_q8": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
+                             _P, _P, _U32, _U32, _P],
+    "tfq_prefill_shared_expert_workspace_bytes": [_U32, _U32, _U32],
+    "tfq_prefill_shared_expert": [_P, _P, _U32, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
+                                  _P, _U32, _P, _U32, _U32, _U32, _U32, _P, C.c_size_t],
     "tfq_convert_bf16_to_f16": [_P, _P, _P, _P, C.c_uint64, _P],
     "tfq_read_ceiling": [_P, _P, _P, C.c_uint64, _P, _U32],
     "tfq_gemm_q4g64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _I],
     "tfq_gemm_qg64": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _I, _U32],
+    "tfq_gemm_qg64_path": [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _I, _U32, _I],
     "tfq_prefill_router": [_P, _P, C.POINTER(RouterDesc), _P, _U32, _U32, _U32, _U32, _P, _P, _P, _P],
     "tfq_moe_group": [_P, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _P],
     "tfq_group_pairs_host": [_P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _P,
@@ -172,6 +186,7 @@ _RES = {"tfq_destroy": None, "tfq_status_string": C.c_char_p, "tfq_expert_layout
         "tfq_moe_prefill_workspace_bytes": C.c_size_t,
         "tfq_attention_workspace_bytes": C.c_size_t,
         "tfq_decode_layer_workspace_bytes": C.c_size_t,
+        "tfq_prefill_shared_expert_workspace_bytes": C.c_size_t,
         "tfq_last_error_message": C.c_char_p}
 
 _lib = None
@@ -180,9 +195,9 @@ _lib = None
 def _load():
     global _lib
     if _lib is None:
-        if not (os.path.exists(LIB_PATH) and os.path.exists(CODE_OBJECT_PATH)):
-            raise TfqNotBuilt(f"{LIB_PATH} / {CODE_OBJECT_PATH} missing: run "
-                              "`python -m edgeexpert_amd.build` first")
+        missing = [p for p in [LIB_PATH, *CODE_OBJECT_PATHS] if not os.path.exists(p)]
+        if missing:
+            raise TfqNotBuilt(f"{', '.join(missing)} missing: run `python -m edgeexpert_amd.build` first")
         lib = C.CDLL(LIB_PATH)
         for name, args in SIGNATURES.items():
             f = getattr(lib, name)

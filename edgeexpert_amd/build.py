@@ -1,6 +1,7 @@
-"""Build libtfq: the gfx950 code object and the host C-ABI library, in-tree.
+"""Build libtfq: the gfx950 code objects and the host C-ABI library, in-tree.
 
-  edgeexpert_amd/lib/tfq_kernels.co   hipcc --offload-arch=gfx950 (device code only)
+  edgeexpert_amd/lib/tfq_*.co         hipcc --offload-arch=gfx950 (device code only),
+                                      one per csrc/kernels/tfq_*.hip, compiled in parallel
   edgeexpert_amd/lib/libtfq.so        g++ host library over the HIP runtime
 
 Run `python -m edgeexpert_amd.build` (or __graft_entry__.build()). No GPU is
@@ -19,7 +20,11 @@ LIB_DIR = os.path.join(PKG, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-CODE_OBJECT = os.path.join(LIB_DIR, "tfq_kernels.co")
+KERNEL_DIR = os.path.join(CSRC, "kernels")
+# one code object per translation unit; libtfq resolves kernels across all of them
+UNITS = ("tfq_gemv", "tfq_int8", "tfq_phase1", "tfq_phase1_routed", "tfq_moe", "tfq_gemm", "tfq_prefill",
+         "tfq_attention")
+CODE_OBJECTS = [os.path.join(LIB_DIR, u + ".co") for u in UNITS]
 HOST_LIB = os.path.join(LIB_DIR, "libtfq.so")
 
 DEVICE_FLAGS = [
@@ -38,12 +43,19 @@ def _run(cmd):
     return r
 
 
-def build_code_object(extra=()):
-    src = os.path.join(CSRC, "kernels", "tfq_kernels.hip")
-    tmp = CODE_OBJECT + ".tmp"
+def build_code_object(unit, extra=()):
+    src = os.path.join(KERNEL_DIR, unit + ".hip")
+    out = os.path.join(LIB_DIR, unit + ".co")
+    tmp = out + ".tmp"
     _run([os.path.join(ROCM, "bin", "hipcc"), *DEVICE_FLAGS, *extra, src, "-o", tmp])
-    os.replace(tmp, CODE_OBJECT)
-    return CODE_OBJECT
+    os.replace(tmp, out)
+    return out
+
+
+def build_code_objects(extra=()):
+    workers = min(len(UNITS), max(1, os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        return list(ex.map(lambda u: build_code_object(u, extra), UNITS))
 
 
 def build_host_lib():
@@ -58,9 +70,13 @@ def build_host_lib():
 
 def build():
     os.makedirs(LIB_DIR, exist_ok=True)
+    stale = os.path.join(LIB_DIR, "tfq_kernels.co")        # the former single code object
+    if os.path.exists(stale):
+        os.remove(stale)
     with ThreadPoolExecutor(max_workers=2) as ex:
-        futs = [ex.submit(build_code_object), ex.submit(build_host_lib)]
-        return [f.result() for f in futs]
+        host = ex.submit(build_host_lib)
+        cos = build_code_objects()
+        return cos + [host.result()]
 
 
 if __name__ == "__main__":

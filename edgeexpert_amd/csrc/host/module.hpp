@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -12,6 +13,7 @@
 #include <string>
 #include <unordered_map>
 #include <utility>
+#include <vector>
 
 #include "../../../include/tfq.h"
 
@@ -49,10 +51,12 @@ inline uint32_t pow2ceil(uint32_t v) {
     return p;
 }
 
-// The code object: every kernel resolved by name once, at creation.
+// The code objects (one per kernel translation unit, lib/tfq_*.co): every
+// kernel resolved by name once, at creation, across all of them.
 class Module {
 public:
-    int load(const char* path);
+    // dir: the directory holding the code objects.
+    int load(const std::string& dir);
     ~Module();
     hipFunction_t get(const std::string& name) const {
         auto it = fns_.find(name);
@@ -66,7 +70,7 @@ public:
     uint32_t resident_blocks(hipFunction_t f, uint32_t block, uint32_t lds) const;
 
 private:
-    hipModule_t module_ = nullptr;
+    std::vector<hipModule_t> modules_;
     int device_ = -1;
     uint32_t cus_ = 1;
     std::unordered_map<std::string, hipFunction_t> fns_;
@@ -101,9 +105,6 @@ inline SegShape seg_shape(uint32_t chunks, uint32_t min_seg) {
 // int4 families: the (SEG >= 8, P <= 4) pair with the fewest idle chunk
 // slots (SEG·P - chunks); ties go to the larger SEG (fewer registers).
 inline SegShape seg_shape_fit(uint32_t chunks, uint32_t min_seg) {
-#ifdef TFQ_SEG_MAX64
-    return seg_shape(chunks, min_seg);
-#else
     if (chunks <= 8) return seg_shape(chunks, min_seg);
     SegShape best{64, (chunks + 63) / 64};
     uint32_t best_waste = best.seg * best.p - chunks;
@@ -117,7 +118,6 @@ inline SegShape seg_shape_fit(uint32_t chunks, uint32_t min_seg) {
         }
     }
     return best;
-#endif
 }
 
 }  // namespace tfq

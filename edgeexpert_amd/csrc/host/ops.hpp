@@ -13,10 +13,7 @@ namespace tfq {
 
 constexpr uint32_t kBlock = 256;          // 4 wavefronts per block for every GEMV-family kernel
 constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident in LDS
-#ifndef TFQ_ROWS_IN_FLIGHT
-#define TFQ_ROWS_IN_FLIGHT 1
-#endif
-constexpr uint32_t kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
+constexpr uint32_t kRowsInFlight = 1;     // rows per segment in flight (entry_points.hpp kRowsInFlight)
 constexpr uint32_t kProjBM = 64;           // projection GEMM tile: tokens (gemm.hpp kProjBM)
 constexpr uint32_t kProjBN = 256;          // outputs (gemm.hpp kProjBN)
 constexpr uint32_t kProjThreads = 256;     // threads (gemm.hpp kProjThreads)
@@ -141,12 +138,16 @@ class DequantInt8GEMV {
 public:
     explicit DequantInt8GEMV(const Module& m) : m_(m) {}
 
+    // tokens > 1: the same GEMV for `tokens` inputs x + t·x_stride into
+    // y + t·y_stride (one launch; blockIdx.y is the token).
     int encode(void* stream, const uint8_t* weights, const uint16_t* scales, const uint16_t* biases,
-               const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n) const {
+               const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n, uint32_t tokens = 1,
+               uint32_t x_stride = 0, uint32_t y_stride = 0) const {
         if (n == 0 || n % TFQ_GROUP_SIZE != 0)
             return fail(TFQ_E_INVAL, "n=%u must be a positive multiple of 64", n);
         if (n > 4096) return fail(TFQ_E_UNSUPPORTED, "int8 GEMV n=%u exceeds 4096", n);
         if (m == 0) return fail(TFQ_E_INVAL, "m must be positive");
+        if (tokens == 0 || tokens > 65535) return fail(TFQ_E_INVAL, "token count %u must be in 1...65535", tokens);
         if (!weights || !scales || !biases || !x || !y)
             return fail(TFQ_E_INVAL, "null pointer argument");
         if (!aligned(weights, 16)) return fail(TFQ_E_INVAL, "weights are not 16-byte aligned");
@@ -156,10 +157,12 @@ public:
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_q8_gemv_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
-        void* args[] = {&weights, &scales, &biases, &x, &y, &m, &n};
+        void* args[] = {&weights, &scales, &biases, &x, &x_stride, &y, &y_stride, &m, &n};
         hipFunction_t fn = m_.get(name);
-        return launch(fn, grid_for_rows(m_, fn, n * 6, m, rows_per_block), kBlock, n * 6, stream, args,
-                      name);
+        if (!fn) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
+        return hip_check(hipModuleLaunchKernel(fn, grid_for_rows(m_, fn, n * 6, m, rows_per_block), tokens, 1,
+                                               kBlock, 1, 1, n * 6, (hipStream_t)stream, args, nullptr),
+                         name);
     }
 
 private:
@@ -444,16 +447,119 @@ private:
     DequantInt4GEMV gemv_;
 };
 
+// S/Kernels/MoE/SharedExpertInt8.swift:55-210: the fused int8 gate/up/act
+// (shared_int8_gate_up_act_simd; gate and up kept in fp32 up to the
+// activation) and the int8 down GEMV. tokens > 1 runs the same for a block
+// of inputs x + t·x_stride into y + t·y_stride, act_scratch [tokens][f].
+class SharedExpertInt8 {
+public:
+    explicit SharedExpertInt8(const Module& m) : m_(m), gemv_(m) {}
+
+    int encode(void* stream, const uint16_t* x, const tfq_q4_matrix& gate, const tfq_q4_matrix& up,
+               const tfq_q4_matrix& down, uint16_t* y, uint32_t d, uint32_t f, uint16_t* act_scratch,
+               const NormArg& stage = stage_copy(), uint32_t tokens = 1, uint32_t x_stride = 0,
+               uint32_t y_stride = 0) const {
+        if (d == 0 || f == 0 || d % 64 || f % 64)
+            return fail(TFQ_E_INVAL, "SharedExpertInt8 dimension mismatch: d=%u f=%u must be multiples of 64", d, f);
+        if (d > 4096 || f > 4096) return fail(TFQ_E_UNSUPPORTED, "int8 shared expert d/f exceed 4096");
+        if (tokens == 0 || tokens > 65535) return fail(TFQ_E_INVAL, "token count %u must be in 1...65535", tokens);
+        if (!x || !y || !act_scratch || !gate.weights || !up.weights || !down.weights || !gate.scales ||
+            !gate.biases || !up.scales || !up.biases || !down.scales || !down.biases)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(gate.weights, 16) || !aligned(up.weights, 16))
+            return fail(TFQ_E_INVAL, "gate/up weights must be 16-byte aligned");
+        if (tokens > 1 && (x_stride < d || y_stride < d))
+            return fail(TFQ_E_INVAL, "x/y strides must be at least d");
+        if (int rc = check_stage(stage)) return rc;
+        Q8Mat g = {static_cast<const uint8_t*>(gate.weights), gate.scales, gate.biases};
+        Q8Mat u = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases};
+        NormArg na = stage;
+        const SegShape sh = seg_shape(d / 16, 4);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_q8_gate_up_act_%ss%u_p%u", form_prefix(na), sh.seg, sh.p);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
+        void* args[] = {&g, &u, &x, &x_stride, &act_scratch, &d, &f, &na};
+        hipFunction_t fn = m_.get(name);
+        if (!fn) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
+        const uint32_t lds = d * 6;
+        int rc = hip_check(hipModuleLaunchKernel(fn, grid_for_rows(m_, fn, lds, f, rows_per_block), tokens, 1,
+                                                 kBlock, 1, 1, lds, (hipStream_t)stream, args, nullptr),
+                           name);
+        if (rc) return rc;
+        return gemv_.encode(stream, static_cast<const uint8_t*>(down.weights), down.scales, down.biases,
+                            act_scratch, y, d, f, tokens, f, tokens > 1 ? y_stride : 0);
+    }
+
+private:
+    const Module& m_;
+    DequantInt8GEMV gemv_;
+};
+
+inline int launch2(const Module& m, const char* name, uint32_t gx, uint32_t gy, uint32_t block,
+                   uint32_t lds, void* stream, void** args) {
+    hipFunction_t f = m.get(name);
+    if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
+    return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, lds, (hipStream_t)stream, args,
+                                           nullptr),
+                     name);
+}
+
+constexpr uint32_t kSkinnyTok = 16;         // tokens per skinny block row (gemm_skinny.hpp kSkinnyTok)
+constexpr uint32_t kSkinnyThreads = 512;    // (gemm_skinny.hpp kSkinnyThreads)
+
+// The prefill projection's kernel choice by token count, the role of
+// PrefillProjectionDispatchPolicy (S/Runtime/Inference/RealForwardRunner.swift:
+// 217-230, 1411-1492: repeated GEMV below 32 tokens, QMM / MPP above). Here
+// the two kernels are the few-token weight stream (gemm_skinny.hpp: every
+// weight dequantised once per 16 tokens, 8 K-slices per block, N/16 or N/32
+// blocks) and the 64-token projection tile (gemm.hpp: N/256 blocks per
+// token tile). Both multiply the same fp16 weights, so the choice changes
+// time, not results beyond fp32 summation order. The skinny form is used up
+// to the largest token count at which it measured faster on MI355X for that
+// output count (K = 2816; see skinny_max_tokens).
+struct GemmPlan {
+    int path;        // TFQ_GEMM_PATH_TILE, _SKINNY (16 rows per wave) or _SKINNY32 (32)
+};
+
+// Largest token count at which the weight stream beat the tile on MI355X
+// (bf16 activations, K = 2816, back-to-back launches; the tile takes ~28 us
+// at any token count up to 448 at these shapes, the stream grows by one
+// weight pass per 16 tokens): N = 2048: 320, 2816: 192, 4096: 160, 8192: 80.
+// Other N follow the measured ~1/N trend. The crossover is taken to be
+// independent of K: both kernels' times scale with K.
+inline uint32_t skinny_max_tokens(uint32_t n, uint32_t k) {
+    (void)k;
+    if (n <= 2048) return 320;
+    if (n <= 2816) return 192;
+    if (n <= 4096) return 160;
+    if (n <= 8192) return 80;
+    const uint32_t t = 655360u / n / 16u * 16u;
+    return t < 16 ? 16 : t;
+}
+
+inline GemmPlan plan_gemm(uint32_t t, uint32_t n, uint32_t k) {
+    if (t > skinny_max_tokens(n, k)) return {TFQ_GEMM_PATH_TILE};
+    // 16 rows per wave keeps more blocks for narrow matrices and few tokens;
+    // 32 rows per wave halves the activation reads and wins elsewhere
+    const bool rows16 = (t <= 16 && n < 8192) || (t <= 32 && n <= 2048);
+    return {rows16 ? TFQ_GEMM_PATH_SKINNY : TFQ_GEMM_PATH_SKINNY32};
+}
+
 // S/Kernels/Prefill/Primitives/PrefillPrimitives.swift:73-123 (PrefillInt4QMM) and
-// S/Kernels/TensorCore/MPPPrefillInt4QMM.swift:4-83: one MFMA kernel serves both.
+// S/Kernels/TensorCore/MPPPrefillInt4QMM.swift:4-83, with the GEMV-vs-QMM
+// choice of RealForwardRunner.swift:217-230 made inside (plan_gemm).
 class PrefillInt4QMM {
 public:
     explicit PrefillInt4QMM(const Module& m) : m_(m) {}
 
     // bits: 4, or 3 (PrefillPrimitives.swift:91-99; prefill.metal:711-757).
+    // path: TFQ_GEMM_PATH_AUTO (plan_gemm) or a forced kernel.
+    // ldx / ldy: halves between token rows of x / y (0: k / n).
     int encode(void* stream, const void* weights, const uint16_t* scales, const uint16_t* biases,
                const uint16_t* x, uint16_t* y, uint32_t t, uint32_t n, uint32_t k, int dtype,
-               uint32_t bits = 4) const {
+               uint32_t bits = 4, int path = TFQ_GEMM_PATH_AUTO, uint32_t ldx = 0, uint32_t ldy = 0) const {
+        if (ldx == 0) ldx = k;
+        if (ldy == 0) ldy = n;
         if (bits != 3 && bits != 4) return fail(TFQ_E_INVAL, "unsupported attention weight bits %u", bits);
         if (k == 0 || k % TFQ_GROUP_SIZE != 0)
             return fail(TFQ_E_INVAL, "k=%u must be a positive multiple of 64", k);
@@ -466,16 +572,29 @@ public:
             return fail(TFQ_E_INVAL, "weights and x must be 16-byte aligned");
         if (!aligned(scales, 2) || !aligned(biases, 2) || !aligned(y, 2))
             return fail(TFQ_E_INVAL, "scales/biases/y must be 2-byte aligned");
+        if (ldx < k || ldx % 8 != 0) return fail(TFQ_E_INVAL, "x row stride %u must be >= k and a multiple of 8", ldx);
+        if (ldy < n) return fail(TFQ_E_INVAL, "y row stride %u must be >= n", ldy);
+        if (k > kProjMaxK) return fail(TFQ_E_UNSUPPORTED, "k=%u exceeds %u", k, kProjMaxK);
+        if (path == TFQ_GEMM_PATH_AUTO) path = plan_gemm(t, n, k).path;
+        if (path == TFQ_GEMM_PATH_SKINNY || path == TFQ_GEMM_PATH_SKINNY32) {
+            const uint32_t rt = path == TFQ_GEMM_PATH_SKINNY32 ? 2 : 1;
+            char sname[64];
+            std::snprintf(sname, sizeof(sname), "tfq_gemm_skinny_q%u_%s_r%u_c%u", bits,
+                          dtype == TFQ_DTYPE_BF16 ? "bf16" : "f16", rt, (k + 1023) / 1024);
+            const uint32_t gx = (n + 16 * rt - 1) / (16 * rt), gy = (t + kSkinnyTok - 1) / kSkinnyTok;
+            void* args[] = {&x, &weights, &scales, &biases, &y, &t, &n, &k, &ldx, &ldy};
+            return launch2(m_, sname, gx, gy, kSkinnyThreads, 0, stream, args);
+        }
+        if (path != TFQ_GEMM_PATH_TILE) return fail(TFQ_E_INVAL, "unknown GEMM path %d", path);
         const char* name = bits == 3 ? (dtype == TFQ_DTYPE_BF16 ? "tfq_gemm_q3_bf16" : "tfq_gemm_q3_f16")
                                      : (dtype == TFQ_DTYPE_BF16 ? "tfq_gemm_q4_bf16" : "tfq_gemm_q4_f16");
         hipFunction_t f = m_.get(name);
         if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
         // blockIdx.x walks the outputs, so the token tiles that share a weight
         // slice are dispatched to the same XCD (and its L2)
-        if (k > kProjMaxK) return fail(TFQ_E_UNSUPPORTED, "k=%u exceeds %u", k, kProjMaxK);
         const uint32_t gx = (n + kProjBN - 1) / kProjBN, gy = (t + kProjBM - 1) / kProjBM;
         const uint32_t lds = proj_pl_lds_bytes(k);
-        void* args[] = {&x, &weights, &scales, &biases, &y, &t, &n, &k};
+        void* args[] = {&x, &weights, &scales, &biases, &y, &t, &n, &k, &ldx, &ldy};
         return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, kProjGemmThreads, 1, 1, lds, (hipStream_t)stream,
                                                args, nullptr),
                          name);
@@ -485,14 +604,60 @@ private:
     const Module& m_;
 };
 
-inline int launch2(const Module& m, const char* name, uint32_t gx, uint32_t gy, uint32_t block,
-                   uint32_t lds, void* stream, void** args) {
-    hipFunction_t f = m.get(name);
-    if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
-    return hip_check(hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, lds, (hipStream_t)stream, args,
-                                           nullptr),
-                     name);
-}
+
+// S/Kernels/Prefill/MoE/PrefillSharedExpert.swift:4-60 (encodeBlock): the
+// shared expert over `tokens` rows x + t·x_stride -> y + t·y_stride. The
+// reference runs the decode form once per row; here int8 weights run the
+// decode kernels with a token dimension (one launch each for gate/up/act and
+// down), and int4 weights run the prefill GEMM (gate, up -> fp16 in the
+// workspace, gelu_mul_fp16 as in SharedExpertInt4's GPU sequence, then
+// down), whose kernel choice by token count picks the weight stream for few
+// tokens.
+class PrefillSharedExpert {
+public:
+    PrefillSharedExpert(const Module& m, const SharedExpertInt8& int8, const PrefillInt4QMM& qmm)
+        : m_(m), int8_(int8), qmm_(qmm) {}
+
+    static size_t workspace_bytes(uint32_t bits, uint32_t tokens, uint32_t f) {
+        const size_t one = ((size_t)tokens * f * 2 + 255) / 256 * 256;
+        return bits == 8 ? one : 2 * one;
+    }
+
+    int encode(void* stream, uint32_t bits, const tfq_q4_matrix& gate, const tfq_q4_matrix& up,
+               const tfq_q4_matrix& down, const uint16_t* x, uint32_t x_stride, uint16_t* y, uint32_t y_stride,
+               uint32_t tokens, uint32_t d, uint32_t f, void* workspace, size_t workspace_size) const {
+        if (bits != 4 && bits != 8) return fail(TFQ_E_INVAL, "SharedExpert unsupported weight bits: %u", bits);
+        if (tokens == 0) return TFQ_OK;                         // queryCount 0: nothing to encode
+        if (x_stride < d) return fail(TFQ_E_INVAL, "x stride is too small");
+        if (y_stride < d) return fail(TFQ_E_INVAL, "y stride is too small");
+        if (!workspace || !aligned(workspace, 256)) return fail(TFQ_E_INVAL, "workspace must be 256-byte aligned");
+        if (workspace_size < workspace_bytes(bits, tokens, f))
+            return fail(TFQ_E_INVAL, "SharedExpert scratch too small");
+        uint16_t* a = static_cast<uint16_t*>(workspace);
+        if (bits == 8)
+            return int8_.encode(stream, x, gate, up, down, y, d, f, a, stage_copy(), tokens, x_stride, y_stride);
+        if (!gate.weights || !up.weights || !down.weights) return fail(TFQ_E_INVAL, "null pointer argument");
+        uint16_t* u = a + ((size_t)tokens * f * 2 + 255) / 256 * 128;
+        int rc = qmm_.encode(stream, gate.weights, gate.scales, gate.biases, x, a, tokens, f, d, TFQ_DTYPE_F16, 4,
+                             TFQ_GEMM_PATH_AUTO, x_stride, f);
+        if (rc) return rc;
+        rc = qmm_.encode(stream, up.weights, up.scales, up.biases, x, u, tokens, f, d, TFQ_DTYPE_F16, 4,
+                         TFQ_GEMM_PATH_AUTO, x_stride, f);
+        if (rc) return rc;
+        uint64_t n = (uint64_t)tokens * f;
+        void* args[] = {&a, &u, &a, &n};
+        const uint32_t grid = (uint32_t)std::min<uint64_t>((n + kBlock - 1) / kBlock, 4096);
+        rc = launch2(m_, "tfq_gelu_mul_f16", grid, 1, kBlock, 0, stream, args);
+        if (rc) return rc;
+        return qmm_.encode(stream, down.weights, down.scales, down.biases, a, y, tokens, d, f, TFQ_DTYPE_F16, 4,
+                           TFQ_GEMM_PATH_AUTO, f, y_stride);
+    }
+
+private:
+    const Module& m_;
+    const SharedExpertInt8& int8_;
+    const PrefillInt4QMM& qmm_;
+};
 
 // S/Kernels/Prefill/MoE/PrefillRouter.swift:30-112.
 class PrefillRouter {
@@ -678,8 +843,9 @@ private:
 // launches on `stream` and two on the side stream.
 class DecodeLayer {
 public:
-    DecodeLayer(const Module& m, DequantInt4GEMV& gemv, MoE& moe, SharedExpertInt4& shared, Attention& attn)
-        : m_(m), gemv_(gemv), moe_(moe), shared_(shared), attn_(attn) {}
+    DecodeLayer(const Module& m, DequantInt4GEMV& gemv, MoE& moe, SharedExpertInt4& shared,
+                SharedExpertInt8& shared8, Attention& attn)
+        : m_(m), gemv_(gemv), moe_(moe), shared_(shared), shared8_(shared8), attn_(attn) {}
     ~DecodeLayer() {
         if (fork_) (void)hipEventDestroy(fork_);
         if (join_) (void)hipEventDestroy(join_);
@@ -726,6 +892,10 @@ public:
                               (const void*)w.post_ffn2_norm, (const void*)w.post_ffn_norm})
             if (!aligned(p, 16)) return fail(TFQ_E_INVAL, "hidden vectors and norm weights must be 16-byte aligned");
         if (!aligned(workspace, 256)) return fail(TFQ_E_INVAL, "workspace must be 256-byte aligned");
+        // shared expert width: Model.sharedExpertWeightBits (S/Runtime/Inference/Model.swift:59)
+        const uint32_t shared_bits = w.shared_bits ? w.shared_bits : 4u;
+        if (shared_bits != 4 && shared_bits != 8)
+            return fail(TFQ_E_INVAL, "SharedExpert unsupported weight bits: %u", w.shared_bits);
         const uint32_t seq_len = position + 1;
         const Layout L = layout(s, seq_len);
         if (workspace_bytes < L.total) return fail(TFQ_E_INVAL, "decode-layer workspace too small");
@@ -763,8 +933,10 @@ public:
         rc = hip_check(hipStreamWaitEvent(side_, fork_, 0), "hipStreamWaitEvent");
         if (rc) return rc;
         const NormArg dense{w.pre_ffn_norm, o, w.post_attention_norm, s.eps, kStagePostAttn};
-        rc = shared_.encode(side_, hidden_in, w.shared_gate, w.shared_up, w.shared_down, h1, s.d,
-                            s.shared_f, sact, dense);
+        rc = shared_bits == 8 ? shared8_.encode(side_, hidden_in, w.shared_gate, w.shared_up, w.shared_down, h1,
+                                                s.d, s.shared_f, sact, dense)
+                              : shared_.encode(side_, hidden_in, w.shared_gate, w.shared_up, w.shared_down, h1,
+                                               s.d, s.shared_f, sact, dense);
         if (rc) return rc;
         rc = hip_check(hipEventRecord(join_, side_), "hipEventRecord");
         if (rc) return rc;
@@ -810,6 +982,7 @@ private:
     DequantInt4GEMV& gemv_;
     MoE& moe_;
     SharedExpertInt4& shared_;
+    SharedExpertInt8& shared8_;
     Attention& attn_;
     hipStream_t side_ = nullptr;
     hipEvent_t fork_ = nullptr, join_ = nullptr;

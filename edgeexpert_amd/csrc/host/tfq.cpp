@@ -5,6 +5,7 @@
 // class that mirrors the reference wrapper (ops.hpp). No entry point
 // allocates device memory or synchronises the caller's stream.
 #include <dlfcn.h>
+#include <sys/stat.h>
 
 #include <algorithm>
 #include <cstring>
@@ -42,6 +43,8 @@ static std::vector<std::string> kernel_names() {
     names.push_back("tfq_lm_head_reduce");
     for (const char* s : q8_shapes) {
         names.push_back(std::string("tfq_q8_gemv_") + s);
+        names.push_back(std::string("tfq_q8_gate_up_act_") + s);
+        names.push_back(std::string("tfq_q8_gate_up_act_norm_") + s);
         names.push_back(std::string("tfq_router_logits_") + s);
         names.push_back(std::string("tfq_prefill_router_logits_") + s);
     }
@@ -49,8 +52,15 @@ static std::vector<std::string> kernel_names() {
         for (const char* b : {"", "b2_", "b3_"}) names.push_back(std::string("tfq_moe_phase2_") + b + "p" + std::to_string(p));
     names.push_back("tfq_router_select");
     names.push_back("tfq_read_ceiling");
+    names.push_back("tfq_gelu_mul_f16");
     for (const char* n : {"tfq_gemm_q4_f16", "tfq_gemm_q4_bf16", "tfq_gemm_q3_f16", "tfq_gemm_q3_bf16"})
         names.push_back(n);
+    for (const char* b : {"q4", "q3"})
+        for (const char* dt : {"f16", "bf16"})
+            for (const char* rt : {"r1", "r2"})
+                for (int c = 1; c <= 8; ++c)
+                    names.push_back(std::string("tfq_gemm_skinny_") + b + "_" + dt + "_" + rt + "_c" +
+                                    std::to_string(c));
     for (const char* n : {"tfq_prefill_select", "tfq_moe_group", "tfq_moe_grouped_gate_up", "tfq_moe_grouped_down",
                           "tfq_moe_grouped_gate_up_b2", "tfq_moe_grouped_down_b2", "tfq_moe_grouped_gate_up_b3",
                           "tfq_moe_grouped_down_b3", "tfq_moe_combine"})
@@ -65,7 +75,11 @@ static std::vector<std::string> kernel_names() {
     return names;
 }
 
-int Module::load(const char* path) {
+// The code objects edgeexpert_amd/build.py writes next to libtfq.so.
+static const char* const kCodeObjects[] = {"tfq_gemv",  "tfq_int8", "tfq_phase1",  "tfq_phase1_routed",
+                                           "tfq_moe",   "tfq_gemm", "tfq_prefill", "tfq_attention"};
+
+int Module::load(const std::string& dir) {
     int rc = hip_check(hipGetDevice(&device_), "hipGetDevice");
     if (rc) return rc;
     int cus = 0;
@@ -73,17 +87,21 @@ int Module::load(const char* path) {
                    "hipDeviceGetAttribute(multiProcessorCount)");
     if (rc) return rc;
     cus_ = cus > 0 ? (uint32_t)cus : 1u;
-    rc = hip_check(hipModuleLoad(&module_, path), "hipModuleLoad");
-    if (rc) {
-        module_ = nullptr;
-        return rc;
+    for (const char* unit : kCodeObjects) {
+        const std::string path = dir + "/" + unit + ".co";
+        hipModule_t m = nullptr;
+        rc = hip_check(hipModuleLoad(&m, path.c_str()), "hipModuleLoad");
+        if (rc) return fail(rc, "hipModuleLoad(%s): %s", path.c_str(), error_state().message);
+        modules_.push_back(m);
     }
     for (const std::string& n : kernel_names()) {
         hipFunction_t f = nullptr;
-        if (hipModuleGetFunction(&f, module_, n.c_str()) != hipSuccess || !f)
-            return fail(TFQ_E_NOT_LOADED, "kernel %s missing from %s", n.c_str(), path);
+        for (hipModule_t m : modules_)
+            if (hipModuleGetFunction(&f, m, n.c_str()) == hipSuccess && f) break;
+        if (!f) return fail(TFQ_E_NOT_LOADED, "kernel %s missing from the code objects in %s", n.c_str(), dir.c_str());
         fns_[n] = f;
     }
+    (void)hipGetLastError();     // the lookups above leave a not-found status behind
     return TFQ_OK;
 }
 
@@ -102,18 +120,28 @@ uint32_t Module::resident_blocks(hipFunction_t f, uint32_t block, uint32_t lds) 
 }
 
 Module::~Module() {
-    if (module_) (void)hipModuleUnload(module_);
+    for (hipModule_t m : modules_) (void)hipModuleUnload(m);
 }
 
-static std::string default_code_object() {
+// The directory of libtfq.so.
+static std::string library_dir() {
     Dl_info info{};
-    if (dladdr(reinterpret_cast<void*>(&default_code_object), &info) && info.dli_fname) {
+    if (dladdr(reinterpret_cast<void*>(&library_dir), &info) && info.dli_fname) {
         std::string p(info.dli_fname);
         size_t slash = p.rfind('/');
-        return (slash == std::string::npos ? std::string(".") : p.substr(0, slash)) +
-               "/tfq_kernels.co";
+        return slash == std::string::npos ? std::string(".") : p.substr(0, slash);
     }
-    return "tfq_kernels.co";
+    return ".";
+}
+
+// A directory is used as is; a file path names the directory holding it.
+static std::string code_object_dir(const char* path) {
+    if (!path) return library_dir();
+    struct stat st {};
+    std::string p(path);
+    if (stat(path, &st) == 0 && S_ISDIR(st.st_mode)) return p;
+    size_t slash = p.rfind('/');
+    return slash == std::string::npos ? std::string(".") : p.substr(0, slash);
 }
 
 }  // namespace tfq
@@ -126,7 +154,9 @@ struct tfq_ctx {
     DequantInt8GEMV* int8 = nullptr;
     MoE* moe = nullptr;
     SharedExpertInt4* shared = nullptr;
+    SharedExpertInt8* shared8 = nullptr;
     PrefillInt4QMM* qmm = nullptr;
+    PrefillSharedExpert* pshared = nullptr;
     PrefillRouter* prouter = nullptr;
     PrefillMoEGrouping* grouping = nullptr;
     PrefillGroupedRoutedMoE* grouped = nullptr;
@@ -136,6 +166,8 @@ struct tfq_ctx {
     ~tfq_ctx() {
         delete lmhead;
         delete layer;
+        delete pshared;
+        delete shared8;
         delete attn;
         delete qmm;
         delete prouter;
@@ -158,8 +190,7 @@ int tfq_create(tfq_ctx** out, const char* code_object_path) {
     *out = nullptr;
     tfq_ctx* c = new (std::nothrow) tfq_ctx();
     if (!c) return fail(TFQ_E_INVAL, "out of host memory");
-    const std::string path = code_object_path ? code_object_path : default_code_object();
-    int rc = c->module.load(path.c_str());
+    int rc = c->module.load(code_object_dir(code_object_path));
     if (rc) {
         delete c;
         return rc;
@@ -169,12 +200,14 @@ int tfq_create(tfq_ctx** out, const char* code_object_path) {
     c->int8 = new DequantInt8GEMV(c->module);
     c->moe = new MoE(c->module);
     c->shared = new SharedExpertInt4(c->module);
+    c->shared8 = new SharedExpertInt8(c->module);
     c->qmm = new PrefillInt4QMM(c->module);
+    c->pshared = new PrefillSharedExpert(c->module, *c->shared8, *c->qmm);
     c->prouter = new PrefillRouter(c->module);
     c->grouping = new PrefillMoEGrouping(c->module);
     c->grouped = new PrefillGroupedRoutedMoE(c->module);
     c->attn = new Attention(c->module);
-    c->layer = new DecodeLayer(c->module, *c->int4, *c->moe, *c->shared, *c->attn);
+    c->layer = new DecodeLayer(c->module, *c->int4, *c->moe, *c->shared, *c->shared8, *c->attn);
     rc = c->layer->ensure_side_stream();
     if (rc) {
         delete c;
@@ -343,6 +376,28 @@ int tfq_shared_expert_q4(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* gate,
     return ctx->shared->encode(stream, x, *gate, *up, *down, y, d, f, act_scratch);
 }
 
+int tfq_shared_expert_q8(tfq_ctx* ctx, void* stream, const tfq_q8_matrix* gate, const tfq_q8_matrix* up,
+                         const tfq_q8_matrix* down, const uint16_t* x, uint16_t* y, uint32_t d, uint32_t f,
+                         uint16_t* act_scratch) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!gate || !up || !down) return fail(TFQ_E_INVAL, "null matrix descriptor");
+    return ctx->shared8->encode(stream, x, *gate, *up, *down, y, d, f, act_scratch);
+}
+
+size_t tfq_prefill_shared_expert_workspace_bytes(uint32_t weight_bits, uint32_t tokens, uint32_t f) {
+    return PrefillSharedExpert::workspace_bytes(weight_bits, tokens, f);
+}
+
+int tfq_prefill_shared_expert(tfq_ctx* ctx, void* stream, uint32_t weight_bits, const tfq_q4_matrix* gate,
+                              const tfq_q4_matrix* up, const tfq_q4_matrix* down, const uint16_t* x,
+                              uint32_t x_stride, uint16_t* y, uint32_t y_stride, uint32_t tokens, uint32_t d,
+                              uint32_t f, void* workspace, size_t workspace_bytes) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!gate || !up || !down) return fail(TFQ_E_INVAL, "null matrix descriptor");
+    return ctx->pshared->encode(stream, weight_bits, *gate, *up, *down, x, x_stride, y, y_stride, tokens, d, f,
+                                workspace, workspace_bytes);
+}
+
 size_t tfq_attention_workspace_bytes(uint32_t head_dim, uint32_t num_q_heads, uint32_t seq_len,
                                      uint32_t window) {
     return Attention::workspace_bytes(head_dim, num_q_heads, seq_len, window);
@@ -387,6 +442,13 @@ int tfq_gemm_qg64(tfq_ctx* ctx, void* stream, const void* weights, const uint16_
                   const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n, uint32_t k, int dtype, uint32_t bits) {
     TFQ_REQUIRE_CTX(ctx);
     return ctx->qmm->encode(stream, weights, scales, biases, x, y, m, n, k, dtype, bits);
+}
+
+int tfq_gemm_qg64_path(tfq_ctx* ctx, void* stream, const void* weights, const uint16_t* scales,
+                       const uint16_t* biases, const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n,
+                       uint32_t k, int dtype, uint32_t bits, int path) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->qmm->encode(stream, weights, scales, biases, x, y, m, n, k, dtype, bits, path);
 }
 
 int tfq_prefill_router(tfq_ctx* ctx, void* stream, const tfq_router* router, const uint16_t* hidden,

@@ -18,6 +18,13 @@ struct Q4Mat {
     uint32_t pad_;
 };
 
+// One int8 g64 matrix (rows of n bytes, fp16 scale/bias per 64 codes).
+struct Q8Mat {
+    const uint8_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+};
+
 // How a kernel forms its fp16 activation vector a from x while staging it
 // to LDS (r(v) = 1/sqrt(mean(v^2) + eps), every intermediate rounded to fp16
 // where a separate kernel would have stored it):

@@ -1,23 +1,28 @@
-// tfq_kernels.hip — gfx950 code object: every kernel entry point of libtfq.
+// entry_points.hpp — the macros that instantiate libtfq's kernel entry
+// points, shared by the tfq_*.hip translation units.
 //
-// Built by edgeexpert_amd/build.py into edgeexpert_amd/lib/tfq_kernels.co and
-// loaded at run time with hipModuleLoad; entry points have C names so the
-// host resolves them with hipModuleGetFunction. Shapes are compile-time
-// template parameters: SEG = lanes per output row (power of two, <= 64) and
-// P = 16-byte chunks per lane; the host picks the instantiation from n.
+// Each tfq_*.hip file is built by edgeexpert_amd/build.py into its own gfx950
+// code object (edgeexpert_amd/lib/tfq_*.co, compiled in parallel) and loaded
+// at run time with hipModuleLoad; entry points have C names so the host
+// resolves them with hipModuleGetFunction across the loaded objects. Shapes
+// are compile-time template parameters: SEG = lanes per output row (power of
+// two, <= 64) and P = 16-byte chunks per lane; the host picks the
+// instantiation from n.
+#pragma once
+
 #include "abi_types.h"
 #include "attention.hpp"
 #include "gemm.hpp"
+#include "gemm_skinny.hpp"
 #include "moe_decode.hpp"
 #include "moe_prefill.hpp"
 
 using namespace tfq;
 
-// Rows each segment keeps in flight (loads issued before the previous rows are reduced).
-#ifndef TFQ_ROWS_IN_FLIGHT
-#define TFQ_ROWS_IN_FLIGHT 1
-#endif
-constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
+// Rows each segment keeps in flight (loads issued before the previous rows
+// are reduced): one; the next row's loads are issued while this row's partial
+// sums are reduced and stored.
+constexpr int kRowsInFlight = 1;
 
 // Each int4 GEMV-family shape comes in two forms: plain (x staged as is) and
 // _norm (x normalised while staged, NormArg); the plain form needs fewer
@@ -37,10 +42,21 @@ constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
 
 #define TFQ_Q8_GEMV(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_q8_gemv_s##SEG##_p##P(                 \
-        const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* x, uint16_t* y,  \
-        uint32_t m, uint32_t n) {                                                                 \
-        q8_gemv<SEG, P, kRowsInFlight>(W, S, B, x, y, m, n);                                      \
+        const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* x,               \
+        uint32_t x_stride, uint16_t* y, uint32_t y_stride, uint32_t m, uint32_t n) {              \
+        q8_gemv<SEG, P, kRowsInFlight>(W, S, B, x, x_stride, y, y_stride, m, n);                  \
     }
+
+// Shared expert, int8 rows: fused gate/up/act in the plain and norm staging forms.
+#define TFQ_Q8_GATE_UP_FORM(NAME, NORM, SEG, P)                                                  \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
+        Q8Mat gate, Q8Mat up, const uint16_t* x, uint32_t x_stride, uint16_t* act, uint32_t D,   \
+        uint32_t F, NormArg norm) {                                                               \
+        q8_gate_up_act<SEG, P, kRowsInFlight, NORM>(gate, up, x, x_stride, act, D, F, norm);      \
+    }
+#define TFQ_Q8_GATE_UP(SEG, P)                                                                   \
+    TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_s##SEG##_p##P, false, SEG, P)                         \
+    TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_norm_s##SEG##_p##P, true, SEG, P)
 
 #define TFQ_ROUTER(SEG, P)                                                                       \
     extern "C" __global__ __launch_bounds__(256) void tfq_router_logits_s##SEG##_p##P(           \
@@ -139,109 +155,3 @@ constexpr int kRowsInFlight = TFQ_ROWS_IN_FLIGHT;
     X(16, 4) X(32, 1) X(32, 2) X(32, 3) X(32, 4) X(64, 1) X(64, 2) X(64, 3) X(64, 4)
 // int8: n/16 chunks per row (n <= 4096).
 #define TFQ_Q8_TABLE(X) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 3) X(64, 4)
-
-TFQ_Q4_TABLE(TFQ_Q4_GEMV)
-TFQ_Q4_TABLE(TFQ_Q3_GEMV)
-TFQ_Q4_TABLE(TFQ_PHASE1)
-TFQ_Q4_TABLE(TFQ_PHASE1_B)
-TFQ_Q4_TABLE(TFQ_PHASE1_ROUTED)
-TFQ_Q4_TABLE(TFQ_PHASE1_ROUTED_B)
-TFQ_Q4_TABLE(TFQ_GATE_UP)
-TFQ_Q4_TABLE(TFQ_LM_HEAD)
-TFQ_Q8_TABLE(TFQ_Q8_GEMV)
-TFQ_Q8_TABLE(TFQ_ROUTER)
-TFQ_Q8_TABLE(TFQ_PREFILL_ROUTER)
-TFQ_ATTN(128, 1)
-TFQ_ATTN(128, 2)
-TFQ_ATTN(128, 4)
-TFQ_ATTN(256, 1)
-TFQ_ATTN(256, 2)
-TFQ_ATTN(256, 4)
-TFQ_ATTN_COMBINE(128)
-TFQ_ATTN_COMBINE(256)
-TFQ_PHASE2(1)
-TFQ_PHASE2(2)
-TFQ_PHASE2(3)
-TFQ_PHASE2(4)
-
-#define TFQ_GEMM(TAG, BITS, DT, X_BF16)                                                          \
-    extern "C" __global__ __launch_bounds__(kProjGemmThreads) void tfq_gemm_##TAG##_##DT(        \
-        const uint16_t* X, const uint8_t* W, const uint16_t* S, const uint16_t* B, uint16_t* Y,  \
-        uint32_t M, uint32_t N, uint32_t K) {                                                     \
-        gemm_q4_proj<X_BF16, BITS>(X, W, S, B, Y, M, N, K);                                       \
-    }
-TFQ_GEMM(q4, 4, f16, false)
-TFQ_GEMM(q4, 4, bf16, true)
-TFQ_GEMM(q3, 3, f16, false)
-TFQ_GEMM(q3, 3, bf16, true)
-
-extern "C" __global__ __launch_bounds__(256) void tfq_lm_head_reduce(const uint64_t* summaries, uint32_t n,
-                                                                     uint32_t* out_token) {
-    lm_head_greedy_reduce(summaries, n, out_token);
-}
-
-extern "C" __global__ __launch_bounds__(256) void tfq_router_select(const float* logits,
-                                                                    const uint16_t* gain,
-                                                                    uint32_t* out_idx,
-                                                                    uint16_t* out_w,
-                                                                    float* out_wf, uint32_t E,
-                                                                    uint32_t k) {
-    router_select(logits, gain, out_idx, out_w, out_wf, E, k);
-}
-
-// Per-token selection for a prefill chunk: one block per token.
-extern "C" __global__ __launch_bounds__(256) void tfq_prefill_select(const float* logits,
-                                                                     const uint16_t* gain,
-                                                                     uint32_t* out_idx,
-                                                                     uint16_t* out_w,
-                                                                     float* out_wf, uint32_t E,
-                                                                     uint32_t k) {
-    const size_t t = blockIdx.x;
-    router_select(logits + t * E, gain, out_idx + t * k, out_w + t * k, out_wf ? out_wf + t * k : nullptr,
-                  E, k);
-}
-
-extern "C" __global__ __launch_bounds__(kGroupThreads) void tfq_moe_group(
-    const uint32_t* idx, const uint16_t* w, uint32_t T, uint32_t k, uint32_t E, Pair* sorted,
-    uint32_t* offsets, uint32_t* counts, Tile* tiles, uint32_t* n_tiles, uint32_t* status) {
-    moe_group(idx, w, T, k, E, sorted, offsets, counts, tiles, n_tiles, status);
-}
-
-#define TFQ_GROUPED(SUFFIX, BITS)                                                                \
-    extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_gate_up##SUFFIX( \
-        ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,         \
-        const uint16_t* hidden, uint32_t stride, uint16_t* act, uint32_t D, uint32_t F) {        \
-        moe_grouped_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F);      \
-    }                                                                                            \
-    extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_down##SUFFIX(  \
-        ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,         \
-        const uint16_t* act, uint16_t* partials, uint32_t D, uint32_t F, uint32_t k) {           \
-        moe_grouped_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k);            \
-    }
-TFQ_GROUPED(, 4)
-TFQ_GROUPED(_b2, 2)
-TFQ_GROUPED(_b3, 3)
-
-extern "C" __global__ __launch_bounds__(256) void tfq_moe_combine(const uint16_t* partials,
-                                                                  const uint16_t* w, uint16_t* h2,
-                                                                  uint32_t T, uint32_t k, uint32_t D) {
-    moe_combine(partials, w, h2, T, k, D);
-}
-
-extern "C" __global__ __launch_bounds__(256) void tfq_read_ceiling(const uint4* src, uint64_t n16,
-                                                                     uint32_t* sink) {
-    read_ceiling<4>(src, n16, sink);
-}
-
-extern "C" __global__ __launch_bounds__(256) void tfq_convert_bf16_f16(const uint16_t* src,
-                                                                         uint16_t* dst, uint64_t n,
-                                                                         uint32_t* inexact) {
-    convert_bf16_to_f16(src, dst, n, inexact);
-}
-
-extern "C" __global__ __launch_bounds__(kLayerTailThreads) void tfq_layer_tail(
-    const uint16_t* hidden, const uint16_t* attn, const uint16_t* w_post_attn, const uint16_t* h1,
-    const uint16_t* w_sp, const uint16_t* h2, const uint16_t* w_pf2, const uint16_t* w_pf, float eps,
-    float layer_scalar, uint16_t* out, uint32_t D) {
-    layer_tail(hidden, attn, w_post_attn, h1, w_sp, h2, w_pf2, w_pf, eps, layer_scalar, out, D);
-}

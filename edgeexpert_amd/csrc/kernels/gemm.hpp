@@ -571,10 +571,12 @@ __device__ __forceinline__ ProjLanes proj_lanes(const uint8_t* W, uint32_t row_b
 }
 
 // Eight waves (kProjGemmThreads), one 32-output sub-tile each; BITS-bit rows.
+// Row t of X starts at X + t·ldx, row t of Y at Y + t·ldy (halves).
 template <bool X_BF16, int BITS = 4>
 __device__ __forceinline__ void gemm_q4_proj(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
                                              const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
-                                             uint16_t* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K) {
+                                             uint16_t* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K,
+                                             uint32_t ldx, uint32_t ldy) {
     extern __shared__ __attribute__((aligned(16))) _Float16 proj_lds[];
     const uint32_t tid = threadIdx.x, wave = tid >> 6;
     const uint32_t G = K >> 6;
@@ -586,12 +588,12 @@ __device__ __forceinline__ void gemm_q4_proj(const uint16_t* __restrict__ X, con
     const ProjLanes pl = proj_lanes<1, BITS>(W, (K >> 3) * BITS, n0, wave, N, 0, G);
     // token rows past M read row 0: their results are never stored
     const uint32_t xrow = tid >> 3;
-    const uint16_t* xp = X + (size_t)(m0 + xrow < M ? m0 + xrow : 0u) * K + 8u * (tid & 7u);
+    const uint16_t* xp = X + (size_t)(m0 + xrow < M ? m0 + xrow : 0u) * ldx + 8u * (tid & 7u);
     f32x16 acc[2][1];
     proj_core_pl<X_BF16, 1, BITS>(acc, proj_lds, sb_lds, pl, xp, G);
     proj_for_each<1>(acc, [&](uint32_t m, uint32_t n, float v) {
         if (m0 + m < M && n0 + n < N)
-            Y[(size_t)(m0 + m) * N + n0 + n] = X_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)v) : f2h(v);
+            Y[(size_t)(m0 + m) * ldy + n0 + n] = X_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)v) : f2h(v);
     });
 }
 

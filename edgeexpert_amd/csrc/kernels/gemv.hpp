@@ -239,11 +239,15 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
     }
 }
 
+// blockIdx.y selects the token of a block of inputs: x + y·x_stride, y + y·y_stride.
 template <int SEG, int P, int R>
 __device__ __forceinline__ void q8_gemv(const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
                                         const uint16_t* __restrict__ B, const uint16_t* __restrict__ x,
-                                        uint16_t* __restrict__ y, uint32_t M, uint32_t n) {
+                                        uint32_t x_stride, uint16_t* __restrict__ y, uint32_t y_stride,
+                                        uint32_t M, uint32_t n) {
     extern __shared__ __attribute__((aligned(16))) float lds_x[];
+    x += (size_t)blockIdx.y * x_stride;
+    y += (size_t)blockIdx.y * y_stride;
     q8_rows<SEG, P, R>(
         W, S, B, lds_x, M, n,
         [&](auto issue0) {
@@ -317,10 +321,16 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
 
 // Order key of logit v at index t: larger key = ranked first. The float
 // bits are mapped to an unsigned order (sign-magnitude -> biased), and the
-// low half holds ~t so that equal logits rank by lower index.
+// low half holds ~t so that equal logits rank by lower index. -0 ranks as
+// +0 (they compare equal, so the lower index wins), and NaN ranks below
+// -inf: router_topk_select_k8 (S/Metal/MoE/moe.metal:152-168) never prefers
+// a NaN score to a number. Every finite or infinite v gets a key > 0.
 __device__ __forceinline__ uint64_t topk_key(float v, uint32_t t) {
-    const uint32_t b = __builtin_bit_cast(uint32_t, v);
-    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t mag = b & 0x7FFFFFFFu;
+    if (mag == 0) b = 0;
+    uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    if (mag > 0x7F800000u) o = 0;
     return ((uint64_t)o << 32) | (uint32_t)(0xFFFFFFFFu - t);
 }
 
@@ -342,7 +352,7 @@ __device__ __forceinline__ void lm_head_greedy_rows(const Q4Multi& mats, const u
             best_row = row;
         }
     });
-    uint64_t best = best_row == 0xFFFFFFFFu ? 0ull : topk_key(best_v == 0.0f ? 0.0f : best_v, best_row);
+    uint64_t best = best_row == 0xFFFFFFFFu ? 0ull : topk_key(best_v, best_row);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const uint64_t other = __shfl_xor(best, o, kWave);

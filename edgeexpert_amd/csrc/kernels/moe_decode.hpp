@@ -42,7 +42,8 @@ struct GateUpRow {
 // segment). `prologue()` runs after the x loads are issued and before the
 // first weight loads (routing: it makes rowfn's expert indices available).
 // NORM == false: x is staged as is (norm ignored). BITS: code width of the
-// rows (2, 3 or 4).
+// rows (2, 3 or 4). Gate and up stay in fp32 up to the activation, as in
+// moe.metal:368 and in the CPU references of every form.
 template <int SEG, int P, int R, bool NORM, int BITS, typename Pro, typename RowFn, typename OutFn>
 __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uint32_t D, uint32_t total,
                                              const NormArg& norm, Pro prologue, RowFn rowfn, OutFn out) {
@@ -212,7 +213,10 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
         [&](uint32_t row, float act) { acts[(size_t)(row / F) * F + row % F] = f2h(act); });
 }
 
-// Shared-expert gate/up/act: act[i] = fp16(gelu(gate[i]·x) · (up[i]·x)).
+// Shared-expert gate/up/act, int4 rows: act[i] = fp16(gelu(g)·u), g =
+// gate[i]·x and u = up[i]·x in fp32 (SharedExpertInt4.swift:30-94 computes
+// the same product; its GPU sequence stores g and u as fp16 first, which
+// moves the expert's output ~8e-4 from the CPU reference, so they stay fp32).
 template <int SEG, int P, int R, bool NORM>
 __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& up,
                                                const uint16_t* __restrict__ x, uint16_t* __restrict__ act,
@@ -234,6 +238,111 @@ __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& u
             return q;
         },
         [&](uint32_t f, float a) { act[f] = f2h(a); });
+}
+
+// Shared-expert gate/up/act, int8 rows (shared_int8_gate_up_act_simd,
+// S/Metal/Quant/dequant_int8.metal:99-154): act[i] = fp16(gelu(g)·u) with
+// g, u the fp32 dot products of gate/up row i with x (the reference kernel
+// rounds g and u to fp16 first, :150-152, which moves the expert's output
+// ~4e-4 from its CPU reference; here they stay fp32). Rows of D bytes,
+// 16 codes per lane-chunk (q8_rows' mapping); x is staged as NormArg says
+// and held as fp32 in LDS, each lane keeping its chunks' activations in
+// registers across rows. blockIdx.y selects the token of a prefill block
+// (x + y·x_stride, act + y·F). Dynamic LDS: D floats + D halves.
+template <int SEG, int P, int R, bool NORM>
+__device__ __forceinline__ void q8_gate_up_act(const Q8Mat& gate, const Q8Mat& up, const uint16_t* __restrict__ x,
+                                               uint32_t x_stride, uint16_t* __restrict__ act, uint32_t D,
+                                               uint32_t F, const NormArg& norm) {
+    extern __shared__ __attribute__((aligned(16))) float lds_x[];
+    constexpr uint32_t NT = kThreads;
+    x += (size_t)blockIdx.y * x_stride;
+    act += (size_t)blockIdx.y * F;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    constexpr uint32_t nwaves = NT / 64;
+    const uint32_t sl = lane & (SEG - 1);
+    const uint32_t lpr = D >> 4;              // 16-code chunks per row
+    const uint32_t ngroups = D >> 6;
+    constexpr uint32_t spw = kWave / SEG;
+    const uint32_t seg_id = (blockIdx.x * nwaves + wave) * spw + lane / SEG;
+    const uint32_t seg_total = gridDim.x * nwaves * spw;
+
+    uint4 gv[R][P], uv[R][P];
+    uint32_t gsr[R][P], gbr[R][P], usr[R][P], ubr[R][P];     // raw fp16 scales / biases
+    auto issue = [&](uint32_t grp) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = seg_id + (grp * R + r) * seg_total;
+            if (row < F) {
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const uint32_t c = sl + p * SEG;
+                    if (c < lpr) {
+                        gv[r][p] = ldg16_stream(gate.w + (size_t)row * D + 16u * c);
+                        uv[r][p] = ldg16_stream(up.w + (size_t)row * D + 16u * c);
+                        gsr[r][p] = gate.s[(size_t)row * ngroups + (c >> 2)];
+                        gbr[r][p] = gate.b[(size_t)row * ngroups + (c >> 2)];
+                        usr[r][p] = up.s[(size_t)row * ngroups + (c >> 2)];
+                        ubr[r][p] = up.b[(size_t)row * ngroups + (c >> 2)];
+                    }
+                }
+            }
+        }
+    };
+    {
+        uint16_t* hs = reinterpret_cast<uint16_t*>(lds_x + D);
+        XStage<NT, kStageChunks, NORM> st;
+        st.load(x, D, norm);
+        issue(0);
+        st.plain(x, hs, D, norm);
+        for (uint32_t i = threadIdx.x; i < D; i += NT) lds_x[i] = h2f(hs[i]);
+        __syncthreads();
+    }
+    float xr[P][16];
+    float xs[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const uint32_t c = sl + p * SEG;
+        if (c < lpr) load_x16(lds_x, c, xr[p], xs[p]);
+        else xs[p] = 0.0f;
+    }
+    for (uint32_t grp = 0; seg_id + grp * R * seg_total < F; ++grp) {
+        float ga[R], ua[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ga[r] = 0.0f;
+            ua[r] = 0.0f;
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const uint32_t c = sl + p * SEG;
+                if (c < lpr) {
+                    const float gd = dot16_q8(gv[r][p], xr[p]);
+                    const float ud = dot16_q8(uv[r][p], xr[p]);
+                    ga[r] = fmaf(h2f((uint16_t)gsr[r][p]), gd, ga[r]);
+                    ga[r] = fmaf(h2f((uint16_t)gbr[r][p]), xs[p], ga[r]);
+                    ua[r] = fmaf(h2f((uint16_t)usr[r][p]), ud, ua[r]);
+                    ua[r] = fmaf(h2f((uint16_t)ubr[r][p]), xs[p], ua[r]);
+                }
+            }
+        }
+        issue(grp + 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float g = seg_sum<SEG>(ga[r]);
+            const float u = seg_sum<SEG>(ua[r]);
+            const uint32_t row = seg_id + (grp * R + r) * seg_total;
+            if (sl == 0 && row < F) act[row] = f2h(gelu_tanh(g) * u);
+        }
+    }
+}
+
+// act[t][i] = fp16(gelu(g[t][i])·u[t][i]) over fp16 g and u (gelu_mul_fp16,
+// S/Metal/Primitives/utility.metal:7-18): the activation between the gate/up
+// and down GEMMs of the prefill shared expert. act may alias g.
+__device__ __forceinline__ void gelu_mul_f16(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                             uint16_t* act, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kThreads)
+        act[i] = f2h(gelu_tanh(h2f(g[i])) * h2f(u[i]));
 }
 
 constexpr uint32_t kPhase2Chunks = 4;     // 16-byte act pieces per thread: top_k·F <= 8192

@@ -1,0 +1,24 @@
+// tfq_prefill.hip — grouped MoE prefill: device grouping of the routed pairs and the
+// grouped gate/up and down MFMA tiles at 4, 3 and 2 bits.
+#include "entry_points.hpp"
+
+extern "C" __global__ __launch_bounds__(kGroupThreads) void tfq_moe_group(
+    const uint32_t* idx, const uint16_t* w, uint32_t T, uint32_t k, uint32_t E, Pair* sorted,
+    uint32_t* offsets, uint32_t* counts, Tile* tiles, uint32_t* n_tiles, uint32_t* status) {
+    moe_group(idx, w, T, k, E, sorted, offsets, counts, tiles, n_tiles, status);
+}
+
+#define TFQ_GROUPED(SUFFIX, BITS)                                                                \
+    extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_gate_up##SUFFIX( \
+        ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,         \
+        const uint16_t* hidden, uint32_t stride, uint16_t* act, uint32_t D, uint32_t F) {        \
+        moe_grouped_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F);      \
+    }                                                                                            \
+    extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_down##SUFFIX(  \
+        ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,         \
+        const uint16_t* act, uint16_t* partials, uint32_t D, uint32_t F, uint32_t k) {           \
+        moe_grouped_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k);            \
+    }
+TFQ_GROUPED(, 4)
+TFQ_GROUPED(_b2, 2)
+TFQ_GROUPED(_b3, 3)

@@ -123,11 +123,14 @@ class PrefillInt4QMM:
         self.ctx = context
 
     def encode(self, stream, weights, scales, biases, x, y, t, n, k, dtype=0, weights_offset=0,
-               scales_offset=0, biases_offset=0, x_offset=0, y_offset=0, bits=4):
-        """bits: 4, or 3 for 3-bit rows (PrefillPrimitives.swift:91-99)."""
+               scales_offset=0, biases_offset=0, x_offset=0, y_offset=0, bits=4, path=None):
+        """bits: 4, or 3 for 3-bit rows (PrefillPrimitives.swift:91-99). path:
+        None (the library's choice by token count) or a GEMM_PATH_* kernel."""
         args = (self.ctx.handle, _s(stream), _addr(weights, weights_offset), _addr(scales, scales_offset),
                 _addr(biases, biases_offset), _addr(x, x_offset), _addr(y, y_offset), t, n, k, dtype)
-        if bits == 4:
+        if path is not None:
+            check(lib().tfq_gemm_qg64_path(*args, bits, path), "PrefillInt4QMM.encode")
+        elif bits == 4:
             check(lib().tfq_gemm_q4g64(*args), "PrefillInt4QMM.encode")
         else:
             check(lib().tfq_gemm_qg64(*args, bits), "PrefillInt4QMM.encode")
@@ -335,6 +338,43 @@ class SharedExpertInt4:
         check(lib().tfq_shared_expert_q4(self.ctx.handle, _s(stream), C.byref(g), C.byref(u),
                                          C.byref(dn), _addr(x), _addr(y), gate.cols, gate.rows,
                                          _addr(scratch_act)), "SharedExpertInt4.encode")
+
+
+class SharedExpertInt8:
+    """S/Kernels/MoE/SharedExpertInt8.swift:55-210 (int8 rows: Q4Projection
+    descriptors whose weights hold one byte per code)."""
+
+    def __init__(self, context: Context):
+        self.ctx = context
+
+    def encode(self, stream, x, gate: Q4Projection, up: Q4Projection, down: Q4Projection, y,
+               scratch_act):
+        g, u, dn = gate.desc(), up.desc(), down.desc()
+        check(lib().tfq_shared_expert_q8(self.ctx.handle, _s(stream), C.byref(g), C.byref(u),
+                                         C.byref(dn), _addr(x), _addr(y), gate.cols, gate.rows,
+                                         _addr(scratch_act)), "SharedExpertInt8.encode")
+
+
+def prefill_shared_expert_workspace_bytes(weight_bits: int, tokens: int, f: int) -> int:
+    return lib().tfq_prefill_shared_expert_workspace_bytes(weight_bits, tokens, f)
+
+
+class PrefillSharedExpert:
+    """S/Kernels/Prefill/MoE/PrefillSharedExpert.swift:4-60 (weightBits 8 by default)."""
+
+    def __init__(self, context: Context, weight_bits: int = 8):
+        self.ctx = context
+        self.weight_bits = weight_bits
+
+    def encode_block(self, stream, x, y, gate: Q4Projection, up: Q4Projection, down: Q4Projection,
+                     workspace, workspace_bytes, query_count, d, intermediate, x_stride_elements,
+                     y_stride_elements, x_offset=0, y_offset=0):
+        g, u, dn = gate.desc(), up.desc(), down.desc()
+        check(lib().tfq_prefill_shared_expert(self.ctx.handle, _s(stream), self.weight_bits, C.byref(g),
+                                              C.byref(u), C.byref(dn), _addr(x, x_offset), x_stride_elements,
+                                              _addr(y, y_offset), y_stride_elements, query_count, d,
+                                              intermediate, _addr(workspace), workspace_bytes),
+              "PrefillSharedExpert.encodeBlock")
 
 
 def convert_bf16_to_f16(context: Context, stream, src, dst, count, inexact_counter=None):
@@ -546,6 +586,7 @@ class DecodeLayerWeightsSpec:
     post_ffn2_norm: object
     post_ffn_norm: object
     layer_scalar: float = 1.0
+    shared_bits: int = 4
 
     @classmethod
     def upload(cls, w: dict) -> "DecodeLayerWeightsSpec":
@@ -554,10 +595,12 @@ class DecodeLayerWeightsSpec:
         def buf(a):
             return DeviceBuffer.from_array(np.ascontiguousarray(a))
 
-        def q4(t):
+        def q4(t, bits=4):
             W, S, B = t
-            rows, cols = W.shape[0], W.shape[1] * 2
+            rows, cols = W.shape[0], W.shape[1] * 8 // bits
             return Q4Projection(buf(W), buf(S), buf(B), rows, cols)
+
+        sb = int(w.get("shared_bits", 4))
 
         E = int(w["num_experts"])
         router = Router(buf(w["router_w"]), buf(w["router_s"]), buf(w["router_b"]), E,
@@ -567,9 +610,9 @@ class DecodeLayerWeightsSpec:
                           weight_bits=int(w.get("expert_bits", 4)))
         return cls(buf(w["input_norm"]), q4(w["q"]), q4(w["k"]), q4(w["v"]), buf(w["q_norm"]),
                    buf(w["k_norm"]), q4(w["o"]), buf(w["post_attention_norm"]), buf(w["pre_ffn_norm"]),
-                   buf(w["pre_ffn2_norm"]), router, pool, q4(w["shared_gate"]), q4(w["shared_up"]),
-                   q4(w["shared_down"]), buf(w["post_ffn1_norm"]), buf(w["post_ffn2_norm"]),
-                   buf(w["post_ffn_norm"]), float(w["layer_scalar"]))
+                   buf(w["pre_ffn2_norm"]), router, pool, q4(w["shared_gate"], sb), q4(w["shared_up"], sb),
+                   q4(w["shared_down"], sb), buf(w["post_ffn1_norm"]), buf(w["post_ffn2_norm"]),
+                   buf(w["post_ffn_norm"]), float(w["layer_scalar"]), sb)
 
     def desc(self) -> DecodeLayerWeights:
         return DecodeLayerWeights(
@@ -578,7 +621,7 @@ class DecodeLayerWeightsSpec:
             _addr(self.pre_ffn_norm), _addr(self.pre_ffn2_norm), self.router.desc(), self.experts.desc(),
             self.shared_gate.desc(), self.shared_up.desc(), self.shared_down.desc(),
             _addr(self.post_ffn1_norm), _addr(self.post_ffn2_norm), _addr(self.post_ffn_norm),
-            float(self.layer_scalar))
+            float(self.layer_scalar), int(self.shared_bits))
 
 
 def decode_layer_workspace_bytes(shape: DecodeLayerShapeSpec, max_seq_len: int) -> int:

@@ -236,12 +236,16 @@ def norm_weight(seed: int, label: str, n: int, lo: float = 0.5, hi: float = 1.5)
 
 
 def decode_layer(seed: int, label: str, d: int, nq: int, nkv: int, hd: int, num_experts: int,
-                 f: int, fs: int, layer_scalar: float = 0.75, expert_bits: int = 4) -> dict:
+                 f: int, fs: int, layer_scalar: float = 0.75, expert_bits: int = 4,
+                 shared_bits: int = 4) -> dict:
     """Weights of one Gemma 4 decoder layer with the BASELINE distributions:
     int4 g64 projections as in config 0, an int8 g64 router, num_experts
-    routed experts in one pool, an int4 shared expert, and RMSNorm weights
-    uniform in [0.5, 1.5) (so that a weight applied to the wrong element is
-    visible). Keys follow the CPU oracle's tfo_layer_weights."""
+    routed experts in one pool, a shared expert of int4 (config 0
+    distributions) or int8 rows (shared_bits 8, the router's distributions),
+    and RMSNorm weights uniform in [0.5, 1.5) (so that a weight applied to
+    the wrong element is visible). Keys follow the CPU oracle's
+    tfo_layer_weights."""
+    shared = int4_matrix if shared_bits == 4 else int8_matrix
     L = label
     qd, kvd = nq * hd, nkv * hd
     w = {
@@ -258,9 +262,10 @@ def decode_layer(seed: int, label: str, d: int, nq: int, nkv: int, hd: int, num_
         "post_ffn1_norm": norm_weight(seed, L + "/post_ffn1_norm", d),
         "post_ffn2_norm": norm_weight(seed, L + "/post_ffn2_norm", d),
         "post_ffn_norm": norm_weight(seed, L + "/post_ffn_norm", d),
-        "shared_gate": int4_matrix(seed, L + "/shared_gate", fs, d),
-        "shared_up": int4_matrix(seed, L + "/shared_up", fs, d),
-        "shared_down": int4_matrix(seed, L + "/shared_down", d, fs),
+        "shared_gate": shared(seed, L + "/shared_gate", fs, d),
+        "shared_up": shared(seed, L + "/shared_up", fs, d),
+        "shared_down": shared(seed, L + "/shared_down", d, fs),
+        "shared_bits": shared_bits,
         "num_experts": num_experts,
         "layer_scalar": layer_scalar,
     }

@@ -49,10 +49,11 @@ extern "C" {
 
 typedef struct tfq_ctx tfq_ctx;
 
-/* Loads the gfx950 code object and resolves every kernel (hipModuleLoad +
- * hipModuleGetFunction). code_object_path == NULL loads tfq_kernels.co from
- * the directory holding libtfq.so. Replaces MetalContext pipeline creation
- * (S/Infrastructure/Metal/MetalContext.swift:104-201). */
+/* Loads the gfx950 code objects (tfq_*.co, one per kernel translation unit)
+ * and resolves every kernel (hipModuleLoad + hipModuleGetFunction) on the
+ * current device. code_object_path: the directory holding them, or a file in
+ * that directory; NULL = the directory holding libtfq.so. Replaces
+ * MetalContext pipeline creation (S/Infrastructure/Metal/MetalContext.swift:104-201). */
 int tfq_create(tfq_ctx **out, const char *code_object_path);
 void tfq_destroy(tfq_ctx *ctx);
 const char *tfq_status_string(int status);
@@ -261,10 +262,29 @@ int tfq_moe_decode_token(tfq_ctx *ctx, void *stream, const tfq_router *router,
  * with gate/up kept in fp32 (one fused launch), then y = fp16(down·act).
  * gate/up are [f][d], down is [d][f]; act_scratch: fp16 [f].
  * Replaces SharedExpertInt4.encode (S/Kernels/MoE/SharedExpertInt4.swift:30-94),
- * which rounds gate and up to fp16 before the activation.
+ * whose GPU sequence rounds gate and up to fp16 before the activation (its
+ * CPU reference does not; the rounding moves the output ~8e-4 from it).
  * Contract: d, f multiples of 64 and <= 8192. */
 int tfq_shared_expert_q4(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *gate,
                          const tfq_q4_matrix *up, const tfq_q4_matrix *down, const uint16_t *x,
+                         uint16_t *y, uint32_t d, uint32_t f, uint16_t *act_scratch);
+
+/* One int8 g64 matrix: rows of n bytes (one code per byte), fp16 scale/bias
+ * per 64 codes (the layout of tfq_q4_matrix with 8-bit codes). */
+typedef tfq_q4_matrix tfq_q8_matrix;
+
+/* Shared expert, int8 form (the reference's default width,
+ * S/Runtime/Inference/Model.swift:59): act[i] = fp16(gelu_tanh(g)·u) with
+ * g = gate[i]·x, u = up[i]·x in fp32 in one fused launch (the reference
+ * kernel rounds g and u to fp16 first, dequant_int8.metal:150-152, which its
+ * CPU reference does not; that rounding moves the output ~4e-4 from it),
+ * then the int8 down GEMV y = fp16(down·act). gate/up [f][d], down [d][f]; act_scratch
+ * fp16 [f]. Replaces SharedExpertInt8.encode
+ * (S/Kernels/MoE/SharedExpertInt8.swift:90-130; kernel
+ * shared_int8_gate_up_act_simd, S/Metal/Quant/dequant_int8.metal:99-154).
+ * Contract: d, f multiples of 64 and <= 4096; gate/up weights 16-byte aligned. */
+int tfq_shared_expert_q8(tfq_ctx *ctx, void *stream, const tfq_q8_matrix *gate,
+                         const tfq_q8_matrix *up, const tfq_q8_matrix *down, const uint16_t *x,
                          uint16_t *y, uint32_t d, uint32_t f, uint16_t *act_scratch);
 
 /* -------------------------------------------------------- decode layer -- */
@@ -304,6 +324,8 @@ typedef struct {
     const uint16_t *post_ffn2_norm;      /* [d] routed output norm */
     const uint16_t *post_ffn_norm;       /* [d] */
     float layer_scalar;
+    uint32_t shared_bits;                /* shared expert rows: 4 (int4, also 0) or 8 (int8,
+                                            shared_gate/up/down as tfq_q8_matrix) */
 } tfq_decode_layer_weights;
 
 typedef struct {
@@ -347,15 +369,29 @@ int tfq_decode_layer(tfq_ctx *ctx, void *stream, const tfq_decode_layer_weights 
 
 /* Y[t][n] = Σ_k X[t][k]·W[n][k] for t < m tokens, n < n outputs, k < k:
  * W int4 g64 [n][k] (fp16 scale/bias [n][k/64]), X [m][k] and Y [m][n] in
- * `dtype` (fp16 or bf16), fp32 accumulate on the matrix cores (weights are
- * dequantised to fp16 tiles in LDS; bf16 activations are converted to fp16
- * exactly within fp16's normal range). Replaces PrefillInt4QMM.encode
+ * `dtype` (fp16 or bf16), fp32 accumulate on the matrix cores. Weights are
+ * dequantised in registers to fp16 (q*s + b, one rounding) and multiplied
+ * with fp16 activations; bf16 activations are converted to fp16 on the way
+ * (round to nearest even: exact for |x| in [2^-14, 65504]; smaller values
+ * keep fewer bits and larger ones become +-inf, as in the reference's fp16
+ * activation path; callers that need to know can run
+ * tfq_convert_bf16_to_f16 with its inexact counter on X). The kernel is
+ * chosen by token count, as PrefillProjectionDispatchPolicy does
+ * (S/Runtime/Inference/RealForwardRunner.swift:217-230, 1411-1492): a
+ * few-token weight stream below the measured crossover of the shape, the
+ * 64-token MFMA tile above it. Replaces PrefillInt4QMM.encode
  * (S/Kernels/Prefill/Primitives/PrefillPrimitives.swift:82-122) and
  * MPPPrefillInt4QMM.encode (S/Kernels/TensorCore/MPPPrefillInt4QMM.swift:34-78).
- * Contract: k % 64 == 0, n >= 1, m >= 1; W and X 16-byte aligned. */
+ * Contract: k % 64 == 0, k <= 8192, n >= 1, m >= 1; W and X 16-byte aligned. */
 int tfq_gemm_q4g64(tfq_ctx *ctx, void *stream, const void *weights, const uint16_t *scales,
                    const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m, uint32_t n,
                    uint32_t k, int dtype);
+
+/* Kernel choices of the prefill GEMM (tfq_gemm_qg64_path). */
+#define TFQ_GEMM_PATH_AUTO 0      /* by token count and shape, as tfq_gemm_q4g64 / tfq_gemm_qg64 do */
+#define TFQ_GEMM_PATH_TILE 1      /* the 64-token x 256-output MFMA projection tile */
+#define TFQ_GEMM_PATH_SKINNY 2    /* few-token weight stream: 16 rows x 16 tokens per wave, K split in 8 */
+#define TFQ_GEMM_PATH_SKINNY32 3  /* the same with 32 rows per wave */
 
 /* tfq_gemm_q4g64 at `bits` = 3 or 4 bits per code (rows of k*bits/8 bytes,
  * codes packed from the least significant bit). Replaces
@@ -365,6 +401,35 @@ int tfq_gemm_q4g64(tfq_ctx *ctx, void *stream, const void *weights, const uint16
 int tfq_gemm_qg64(tfq_ctx *ctx, void *stream, const void *weights, const uint16_t *scales,
                   const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m, uint32_t n,
                   uint32_t k, int dtype, uint32_t bits);
+
+/* tfq_gemm_qg64 with the kernel named by `path` (TFQ_GEMM_PATH_*) instead of
+ * the built-in choice: for measuring the crossover and for tests that hold
+ * both kernels to the same reference. Same contract; results of the two
+ * kernels differ only by fp32 summation order. */
+int tfq_gemm_qg64_path(tfq_ctx *ctx, void *stream, const void *weights, const uint16_t *scales,
+                       const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m, uint32_t n,
+                       uint32_t k, int dtype, uint32_t bits, int path);
+
+/* Workspace bytes of tfq_prefill_shared_expert. */
+size_t tfq_prefill_shared_expert_workspace_bytes(uint32_t weight_bits, uint32_t tokens, uint32_t f);
+
+/* The shared expert over a block of `tokens` rows: y + t*y_stride =
+ * shared(x + t*x_stride) for t < tokens (strides in halves), each row as
+ * tfq_shared_expert_q4 / _q8 compute it for weight_bits 4 / 8. int8 weights
+ * run the decode kernels over all rows in one launch each; int4 weights run
+ * the prefill GEMM (gate and up into the workspace as fp16, gelu_mul, down),
+ * whose kernel follows the token count. Replaces
+ * PrefillSharedExpert.encodeBlock
+ * (S/Kernels/Prefill/MoE/PrefillSharedExpert.swift:11-60), which encodes the
+ * decode form once per row. Contract: as the decode forms; x_stride >= d and
+ * y_stride >= d (a multiple of 8 for int4, with x 16-byte aligned);
+ * workspace 256-byte aligned, tfq_prefill_shared_expert_workspace_bytes
+ * long; tokens == 0 does nothing. */
+int tfq_prefill_shared_expert(tfq_ctx *ctx, void *stream, uint32_t weight_bits,
+                              const tfq_q4_matrix *gate, const tfq_q4_matrix *up,
+                              const tfq_q4_matrix *down, const uint16_t *x, uint32_t x_stride,
+                              uint16_t *y, uint32_t y_stride, uint32_t tokens, uint32_t d, uint32_t f,
+                              void *workspace, size_t workspace_bytes);
 
 /* (token, expert, rank, fp16 routing weight bits in the low half) — the
  * 16-byte PrefillTokenExpertPair (S/Kernels/Prefill/MoE/PrefillRouter.swift:5-28). */

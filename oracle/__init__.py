@@ -84,7 +84,7 @@ class LayerWeights(C.Structure):
                 ("pool", _P), ("stride", C.c_uint64), ("off", ExpertOffsets),
                 ("shared_gate", Q4), ("shared_up", Q4), ("shared_down", Q4),
                 ("post_ffn1_norm", _P), ("post_ffn2_norm", _P), ("post_ffn_norm", _P),
-                ("layer_scalar", C.c_float), ("expert_bits", C.c_int)]
+                ("layer_scalar", C.c_float), ("expert_bits", C.c_int), ("shared_bits", C.c_int)]
 
 
 class LayerShape(C.Structure):
@@ -131,7 +131,9 @@ def _declare(L):
       C.c_int, C.c_int, C.c_int, _P)
     d("tfo_moe_routed_bits", None, _P, C.c_uint64, C.POINTER(ExpertOffsets), C.c_int, C.c_int, _P, _P, _P,
       _P, C.c_int, C.c_int, C.c_int, _P)
-    d("tfo_shared_expert_int4", None, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int,
+    for n in ("tfo_shared_expert_int4", "tfo_shared_expert_int8"):
+        d(n, None, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int, C.c_int, _P)
+    d("tfo_shared_expert", None, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_int,
       C.c_int, _P)
     d("tfo_group_pairs", C.c_int, _P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
       _P, C.c_int64, _P, _P, _P, _P, C.POINTER(C.c_int64), _P, C.POINTER(C.c_int64),
@@ -430,16 +432,38 @@ def moe_routed(pool, stride, off, x, idx, w, d, f, residual=None, fmt=FMT_F16, b
     return y
 
 
-def shared_expert_int4(gate, up, down, x, d, f, fmt=FMT_F16):
-    """SharedExpertInt4Tests reference (T/Kernels/MoE/SharedExpertInt4Tests.swift:21-28).
-    gate/up/down: (W, S, B) tuples."""
+def _shared_expert(name, gate, up, down, x, d, f, fmt):
     args = []
     for (W, S, B) in (gate, up, down):
         args += [_c(W, np.uint8), _c(S, np.uint16), _c(B, np.uint16)]
     x = _c(x, np.float32)
     y = np.zeros(d, np.float32)
-    lib().tfo_shared_expert_int4(*[_ptr(a) for a in args], fmt, _ptr(x), d, f, _ptr(y))
+    getattr(lib(), name)(*[_ptr(a) for a in args], fmt, _ptr(x), d, f, _ptr(y))
     return y
+
+
+def shared_expert(gate, up, down, x, d, f, bits=4, round_gu=False, fmt=FMT_F16):
+    """The shared expert at `bits` 4 or 8; round_gu rounds gate and up to fp16
+    first (the reference's GPU storage points, tfo_shared_expert)."""
+    args = []
+    for (W, S, B) in (gate, up, down):
+        args += [_c(W, np.uint8), _c(S, np.uint16), _c(B, np.uint16)]
+    x = _c(x, np.float32)
+    y = np.zeros(d, np.float32)
+    lib().tfo_shared_expert(*[_ptr(a) for a in args], fmt, bits, int(round_gu), _ptr(x), d, f, _ptr(y))
+    return y
+
+
+def shared_expert_int4(gate, up, down, x, d, f, fmt=FMT_F16):
+    """SharedExpertInt4Tests reference (T/Kernels/MoE/SharedExpertInt4Tests.swift:21-28).
+    gate/up/down: (W, S, B) tuples."""
+    return _shared_expert("tfo_shared_expert_int4", gate, up, down, x, d, f, fmt)
+
+
+def shared_expert_int8(gate, up, down, x, d, f, fmt=FMT_F16):
+    """SharedExpertInt8Tests reference (T/Kernels/MoE/SharedExpertInt8Tests.swift:57-68).
+    gate/up/down: (W, S, B) tuples of int8 rows (W [rows][cols] u8)."""
+    return _shared_expert("tfo_shared_expert_int8", gate, up, down, x, d, f, fmt)
 
 
 # ------------------------------------------------------- decode layer ----
@@ -519,7 +543,7 @@ def decode_layer(w: dict, shape: dict, hidden_f16, k_cache_f16, v_cache_f16, pos
         shared_gate=q4(w["shared_gate"]), shared_up=q4(w["shared_up"]), shared_down=q4(w["shared_down"]),
         post_ffn1_norm=arr(w["post_ffn1_norm"], np.uint16), post_ffn2_norm=arr(w["post_ffn2_norm"], np.uint16),
         post_ffn_norm=arr(w["post_ffn_norm"], np.uint16), layer_scalar=float(w["layer_scalar"]),
-        expert_bits=int(w.get("expert_bits", 4)))
+        expert_bits=int(w.get("expert_bits", 4)), shared_bits=int(w.get("shared_bits", 4)))
     ls = LayerShape(**{k_: shape[k_] for k_ in ("d", "nq", "nkv", "hd", "rotated_pairs", "window", "f", "fs",
                                                  "k", "eps", "theta", "scale")})
     d, qd = shape["d"], shape["nq"] * shape["hd"]

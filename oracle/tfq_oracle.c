@@ -412,13 +412,19 @@ void tfo_router_logits(const uint8_t *W, const uint16_t *S, const uint16_t *B, i
 int tfo_topk_softmax(const float *logits, int num_experts, int k, const float *expert_scale,
                      uint32_t *idx, float *weights) {
     if (k <= 0 || k > num_experts) return -1;
-    /* selection by repeated scan keeps the (desc, asc-index) order exactly */
+    /* selection by repeated scan keeps the (desc, asc-index) order exactly.
+     * The reference's sort (RouterTopKTests.swift:85-87) has no defined
+     * order for NaN; here NaN ranks below every number, as in the GPU
+     * selector router_topk_select_k8 (S/Metal/MoE/moe.metal:152-168), which
+     * never prefers a NaN score. -0 == +0, so they tie by index. */
     unsigned char *taken = (unsigned char *)calloc((size_t)num_experts, 1);
     for (int r = 0; r < k; ++r) {
         int best = -1;
         for (int e = 0; e < num_experts; ++e) {
             if (taken[e]) continue;
-            if (best < 0 || logits[e] > logits[best]) best = e;   /* strict: ties keep lower index */
+            /* strict: ties keep the lower index */
+            if (best < 0 || (!isnan(logits[e]) && (isnan(logits[best]) || logits[e] > logits[best])))
+                best = e;
         }
         taken[best] = 1;
         idx[r] = (uint32_t)best;
@@ -500,29 +506,58 @@ void tfo_moe_routed_bits(const uint8_t *pool, uint64_t stride, const tfo_expert_
     free(out);
 }
 
-/* T/Kernels/MoE/SharedExpertInt4Tests.swift:21-28 */
-void tfo_shared_expert_int4(const uint8_t *gW, const uint16_t *gS, const uint16_t *gB,
-                            const uint8_t *uW, const uint16_t *uS, const uint16_t *uB,
-                            const uint8_t *dW, const uint16_t *dS, const uint16_t *dB,
-                            int fmt, const float *x, int d, int f, float *y) {
+/* The shared expert: gate/up by the GEMV reference of `bits` (4: DequantInt4GemvRef,
+ * 8: DequantInt8GemvRef), act = Float(Float16(Float(gelu) * u)) with the GELU
+ * in double, then the down GEMV over act (T/Kernels/MoE/SharedExpertInt4Tests.swift:21-28,
+ * SharedExpertInt8Tests.swift:57-68). round_gu: gate and up are first rounded
+ * to fp16, as the reference's GPU sequence stores them (SharedExpertInt4's
+ * fp16 scratchGate/scratchUp, SharedExpertInt4.swift:67-80 + utility.metal:7-18;
+ * shared_int8_gate_up_act_simd, dequant_int8.metal:150-152). */
+void tfo_shared_expert(const uint8_t *gW, const uint16_t *gS, const uint16_t *gB,
+                       const uint8_t *uW, const uint16_t *uS, const uint16_t *uB,
+                       const uint8_t *dW, const uint16_t *dS, const uint16_t *dB,
+                       int fmt, int bits, int round_gu, const float *x, int d, int f, float *y) {
     float *g = (float *)malloc(sizeof(float) * (size_t)f);
     float *u = (float *)malloc(sizeof(float) * (size_t)f);
     float *act = (float *)malloc(sizeof(float) * (size_t)f);
-    tfo_gemv_int4(gW, gS, gB, fmt, x, f, d, g);
-    tfo_gemv_int4(uW, uS, uB, fmt, x, f, d, u);
+    if (bits == 8) {
+        tfo_gemv_int8(gW, gS, gB, fmt, x, f, d, g);
+        tfo_gemv_int8(uW, uS, uB, fmt, x, f, d, u);
+    } else {
+        tfo_gemv_int4(gW, gS, gB, fmt, x, f, d, g);
+        tfo_gemv_int4(uW, uS, uB, fmt, x, f, d, u);
+    }
     for (int i = 0; i < f; ++i) {
-        float gv = g[i];
+        float gv = round_gu ? tfo_f16_to_f32(tfo_f32_to_f16(g[i])) : g[i];
+        float uv = round_gu ? tfo_f16_to_f32(tfo_f32_to_f16(u[i])) : u[i];
         float cube = gv * gv;
         cube = cube * gv;
         float k3c = 0.044715f * cube;
         float inner_f = gv + k3c;
         double inner = 0.7978845608028654 * (double)inner_f;
         double gelu = 0.5 * (double)gv * (1.0 + tanh(inner));
-        float prod = (float)gelu * u[i];
+        float prod = (float)gelu * uv;
         act[i] = tfo_f16_to_f32(tfo_f32_to_f16(prod));
     }
-    tfo_gemv_int4(dW, dS, dB, fmt, act, d, f, y);
+    if (bits == 8) tfo_gemv_int8(dW, dS, dB, fmt, act, d, f, y);
+    else tfo_gemv_int4(dW, dS, dB, fmt, act, d, f, y);
     free(g); free(u); free(act);
+}
+
+/* T/Kernels/MoE/SharedExpertInt4Tests.swift:21-28 */
+void tfo_shared_expert_int4(const uint8_t *gW, const uint16_t *gS, const uint16_t *gB,
+                            const uint8_t *uW, const uint16_t *uS, const uint16_t *uB,
+                            const uint8_t *dW, const uint16_t *dS, const uint16_t *dB,
+                            int fmt, const float *x, int d, int f, float *y) {
+    tfo_shared_expert(gW, gS, gB, uW, uS, uB, dW, dS, dB, fmt, 4, 0, x, d, f, y);
+}
+
+/* T/Kernels/MoE/SharedExpertInt8Tests.swift:57-68 */
+void tfo_shared_expert_int8(const uint8_t *gW, const uint16_t *gS, const uint16_t *gB,
+                            const uint8_t *uW, const uint16_t *uS, const uint16_t *uB,
+                            const uint8_t *dW, const uint16_t *dS, const uint16_t *dB,
+                            int fmt, const float *x, int d, int f, float *y) {
+    tfo_shared_expert(gW, gS, gB, uW, uS, uB, dW, dS, dB, fmt, 8, 0, x, d, f, y);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -950,9 +985,9 @@ void tfo_decode_layer(const tfo_layer_weights *w, const tfo_layer_shape *s,
 
     /* gSharedFFN + gSharedNorm (:2418-2440) */
     float *h1 = (float *)malloc(sizeof(float) * (size_t)d);
-    tfo_shared_expert_int4(w->shared_gate.w, w->shared_gate.s, w->shared_gate.b, w->shared_up.w,
-                           w->shared_up.s, w->shared_up.b, w->shared_down.w, w->shared_down.s,
-                           w->shared_down.b, TFO_FMT_F16, dense_x, d, s->fs, h1);
+    tfo_shared_expert(w->shared_gate.w, w->shared_gate.s, w->shared_gate.b, w->shared_up.w, w->shared_up.s,
+                      w->shared_up.b, w->shared_down.w, w->shared_down.s, w->shared_down.b, TFO_FMT_F16,
+                      w->shared_bits == 8 ? 8 : 4, 0, dense_x, d, s->fs, h1);
     round_vec(h1, (size_t)d);
     /* routed phases (:2849-2862), zero residual */
     float *h2 = (float *)malloc(sizeof(float) * (size_t)d);

@@ -128,6 +128,19 @@ void tfo_shared_expert_int4(const uint8_t *gW, const uint16_t *gS, const uint16_
                             const uint8_t *uW, const uint16_t *uS, const uint16_t *uB,
                             const uint8_t *dW, const uint16_t *dS, const uint16_t *dB,
                             int scale_fmt, const float *x, int d, int f, float *y);
+/* The shared expert at `bits` 4 or 8 (the two above are round_gu = 0);
+ * round_gu = 1 rounds gate and up to fp16 before the activation, as the
+ * reference's GPU sequence stores them (SharedExpertInt4.swift:67-80,
+ * dequant_int8.metal:150-152). */
+void tfo_shared_expert(const uint8_t *gW, const uint16_t *gS, const uint16_t *gB,
+                       const uint8_t *uW, const uint16_t *uS, const uint16_t *uB,
+                       const uint8_t *dW, const uint16_t *dS, const uint16_t *dB,
+                       int scale_fmt, int bits, int round_gu, const float *x, int d, int f, float *y);
+/* T/Kernels/MoE/SharedExpertInt8Tests.swift:57-68 (int8 gate/up/down) */
+void tfo_shared_expert_int8(const uint8_t *gW, const uint16_t *gS, const uint16_t *gB,
+                            const uint8_t *uW, const uint16_t *uS, const uint16_t *uB,
+                            const uint8_t *dW, const uint16_t *dS, const uint16_t *dB,
+                            int scale_fmt, const float *x, int d, int f, float *y);
 
 /* ---- prefill grouping (S/Kernels/Prefill/MoE/PrefillMoEGrouping.swift:91-192) ---- */
 typedef struct { uint32_t token, expert, rank, weight_bits; } tfo_pair;   /* PrefillRouter.swift:5-28 */
@@ -247,6 +260,7 @@ typedef struct {
     const uint16_t *post_ffn1_norm, *post_ffn2_norm, *post_ffn_norm;
     float layer_scalar;
     int expert_bits;    /* code width of the routed experts: 2, 3 or 4 (0 reads as 4) */
+    int shared_bits;    /* shared expert: 4 (int4, also 0) or 8 (int8 rows of d bytes), Model.swift:59 */
 } tfo_layer_weights;
 
 typedef struct {
@@ -274,7 +288,8 @@ typedef struct {
  *   attn = f16(attention(q, K[0..position], V[0..position]))
  *   o = f16(GEMV(o_proj, attn)); h = f16(hidden + f16(rmsnorm(o, post_attention_norm)))
  *   router on f16(rmsnorm(h)) (no scale), weights rounded to fp16
- *   h1 = f16(shared(f16(rmsnorm(h, pre_ffn_norm))))
+ *   h1 = f16(shared(f16(rmsnorm(h, pre_ffn_norm)))) (the CPU references' shared
+ *        expert, gate/up in fp32), int4 or int8 rows by shared_bits
  *   h2 = f16(Σ w·ffn(f16(rmsnorm(h, pre_ffn2_norm))))
  *   h12 = f16(f16(rmsnorm(h1, post_ffn1)) + f16(rmsnorm(h2, post_ffn2)))
  *   out = f16(f16(h + f16(rmsnorm(h12, post_ffn))) * f16(layer_scalar))

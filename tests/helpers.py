@@ -59,3 +59,11 @@ def dequant_int4_np(W, S, B, scale_fmt=oracle.FMT_F16):
     s = np.repeat(to32(S), 64, axis=-1)
     b = np.repeat(to32(B), 64, axis=-1)
     return (q * s + b).astype(np.float32)
+
+
+def bf16_half_ulp(v) -> np.ndarray:
+    """Half a bf16 ulp at |v|: bf16 keeps 8 significant bits, so a value in
+    [2^e, 2^(e+1)) rounds to within 2^(e-8) (between 2^-9 and 2^-8 of |v|)."""
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.where(a > 0, a, 2.0 ** -126)))
+    return np.ldexp(1.0, (e - 8).astype(np.int64))

@@ -76,13 +76,16 @@ def test_struct_layouts_match_header(tmp_path):
 
 @pytest.mark.skipif(not shutil.which("/opt/rocm/llvm/bin/llvm-readelf"), reason="no llvm-readelf")
 def test_code_object_is_gfx950_and_holds_all_kernels():
-    out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--symbols", "--notes",
-                          _lib.CODE_OBJECT_PATH], capture_output=True, text=True, check=True).stdout
+    out = "".join(subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--symbols", "--notes", p],
+                                 capture_output=True, text=True, check=True).stdout
+                  for p in _lib.CODE_OBJECT_PATHS)
+    assert out.count("gfx950") >= len(_lib.CODE_OBJECT_PATHS)
     assert "gfx950" in out
     src = open(os.path.join(ROOT, "edgeexpert_amd", "csrc", "host", "tfq.cpp")).read()
     assert "kernel_names" in src
     for fam in ("tfq_q4_gemv_s64_p2", "tfq_moe_phase1_s64_p2", "tfq_moe_phase2_p3",
                 "tfq_router_logits_s64_p3", "tfq_router_select", "tfq_gate_up_act_s64_p2",
                 "tfq_convert_bf16_f16", "tfq_attn_partial_h256_g2", "tfq_attn_combine_h256",
-                "tfq_layer_tail"):
+                "tfq_layer_tail", "tfq_gemm_skinny_q4_bf16_r1_c3", "tfq_q8_gate_up_act_norm_s64_p3",
+                "tfq_gelu_mul_f16"):
         assert fam in out

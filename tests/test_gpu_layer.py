@@ -5,8 +5,11 @@ through libtfq's C ABI.
 Bars: routing indices bit-exact; every stage's output (the intermediate
 buffers are read back from the documented workspace layout) within
 rel_error 1e-3 (north star) of the oracle fed with the GPU's own stored
-inputs of that stage; the whole chain (ten fp16-stored stages) within
-Tolerance.fp16_chained_reduction (1e-2) of the pure oracle."""
+inputs of that stage; the whole chain (ten fp16-stored stages) against the
+pure oracle elementwise within the same 1e-3 of max|ref| plus two fp16 ulps
+of the element (each chain rounds its output to fp16 last; one output ulp
+is 2^-11..2^-10 of |out|, i.e. 2-5e-4 of max|out| near the top of its
+range). Measured end-to-end rel_error: 4e-4 .. 1.1e-3."""
 import numpy as np
 import pytest
 
@@ -109,9 +112,9 @@ def _spec(shape):
                                     attn_scale=shape["scale"])
 
 
-def _layer_case(ctx, stream, shape, E, pos, cap, seed, label, in_place=False, expert_bits=4):
+def _layer_case(ctx, stream, shape, E, pos, cap, seed, label, in_place=False, expert_bits=4, shared_bits=4):
     w = synth.decode_layer(seed, label, shape["d"], shape["nq"], shape["nkv"], shape["hd"], E, shape["f"],
-                           shape["fs"], expert_bits=expert_bits)
+                           shape["fs"], expert_bits=expert_bits, shared_bits=shared_bits)
     kvd = shape["nkv"] * shape["hd"]
     kc = synth.f16_vector(seed, label + "/kc", cap * kvd)
     vc = synth.f16_vector(seed, label + "/vc", cap * kvd)
@@ -187,7 +190,8 @@ def _check_layer(got, ref, w, shape, hidden, label):
     assert list(ridx) == list(got["idx"]), f"{label}: routing of the GPU's h differs"
     stage["w"] = f16_round(rw)
     sh = (w["shared_gate"], w["shared_up"], w["shared_down"])
-    stage["h1"] = f16_round(oracle.shared_expert_int4(*sh, _n16(h, w["pre_ffn_norm"], eps), d, shape["fs"]))
+    shared = oracle.shared_expert_int8 if w.get("shared_bits", 4) == 8 else oracle.shared_expert_int4
+    stage["h1"] = f16_round(shared(*sh, _n16(h, w["pre_ffn_norm"], eps), d, shape["fs"]))
     stage["h2"] = f16_round(oracle.moe_routed(w["pool"], w["stride"], w["off"], _n16(h, w["pre_ffn2_norm"], eps),
                                               ridx, got["w"], d, shape["f"], bits=w.get("expert_bits", 4)))
     h12 = f16_round(_n16(got["h1"], w["post_ffn1_norm"], eps) + _n16(got["h2"], w["post_ffn2_norm"], eps))
@@ -198,7 +202,10 @@ def _check_layer(got, ref, w, shape, hidden, label):
         assert rel < TOL, f"{label}: stage {key} rel={rel}"
     chained = oracle.rel_error(got["out"], ref["out"])
     print(f"[layer] {label}: end-to-end rel={chained:.3g}", flush=True)
-    assert chained < oracle.Tolerance.fp16_chained_reduction, f"{label}: end-to-end rel={chained}"
+    ulp16 = np.abs(got["out"] - np.nextafter(got["out"].astype(np.float16), np.float16(np.inf)).astype(np.float32))
+    bound = TOL * np.abs(ref["out"]).max() + 2 * np.maximum(ulp16, 2.0 ** -24)
+    excess = np.abs(got["out"] - ref["out"]) - bound
+    assert np.all(excess <= 0), f"{label}: end-to-end rel={chained}, max excess {excess.max()}"
 
 
 SMALL = dict(d=256, nq=4, nkv=2, hd=128, rotated_pairs=64, window=0, f=128, fs=192, k=2,
@@ -227,6 +234,13 @@ def test_layer_small_with_2_3_bit_experts(ctx, stream, bits):
     _check_layer(got, ref, w, SMALL, hid, f"small {bits}-bit experts")
 
 
+def test_layer_small_with_int8_shared_expert(ctx, stream):
+    # the shared expert at 8 bits, the reference's default width when the
+    # manifest has no quant block (Model.swift:59)
+    got, ref, w, hid = _layer_case(ctx, stream, SMALL, 8, 70, 160, 8, "small-s8", shared_bits=8)
+    _check_layer(got, ref, w, SMALL, hid, "small int8 shared")
+
+
 def test_layer_in_place_equals_out_of_place(ctx, stream):
     a = _layer_case(ctx, stream, SMALL, 8, 33, 64, 5, "inplace")[0]
     b = _layer_case(ctx, stream, SMALL, 8, 33, 64, 5, "inplace", in_place=True)[0]
@@ -238,6 +252,12 @@ def test_layer_config4_full_context(ctx, stream):
     # new token at position 4095), shared expert 2112, top-8 of 128 experts
     got, ref, w, hid = _layer_case(ctx, stream, CONFIG4, 128, 4095, 4096, 0, "c4")
     _check_layer(got, ref, w, CONFIG4, hid, "config 4")
+
+
+def test_layer_config4_int8_shared_expert(ctx, stream):
+    # config 4 with the shared expert [2112 x 2816] at 8 bits
+    got, ref, w, hid = _layer_case(ctx, stream, CONFIG4, 128, 4095, 4096, 9, "c4-s8", shared_bits=8)
+    _check_layer(got, ref, w, CONFIG4, hid, "config 4, int8 shared")
 
 
 def test_layer_graph_replays_match_eager(ctx, stream):
