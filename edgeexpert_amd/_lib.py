@@ -25,6 +25,7 @@ TFQ_E_NOT_LOADED = 4
 TFQ_E_IO = 5
 ROUTER_WORKSPACE_BYTES = 4096
 LM_HEAD_WORKSPACE_BYTES = 65536
+NOALLOC_SCRATCH_BYTES = 16384 + ROUTER_WORKSPACE_BYTES
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
 GEMM_PATH_AUTO = 0
@@ -130,6 +131,8 @@ SIGNATURES = {
     "tfq_moe_decode": [_P, _P, C.POINTER(ExpertPoolDesc), _P, _P, _P, _P, _P, _U32, _U32, _U32, _P],
     "tfq_moe_decode_token": [_P, _P, C.POINTER(RouterDesc), C.POINTER(ExpertPoolDesc), _P, _P, _P,
                              _U32, _U32, _U32, _P, _P, _P, _P],
+    "tfq_moe_decode_token_noalloc": [_P, _P, C.POINTER(RouterDesc), C.POINTER(ExpertPoolDesc), _P, _P, _P,
+                                     _U32, _U32, _U32, _P, _P],
     "tfq_shared_expert_q4": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),
                              _P, _P, _U32, _U32, _P],
     "tfq_shared_expert_q8": [_P, _P, C.POINTER(Q4Matrix), C.POINTER(Q4Matrix), C.POINTER(Q4Matrix),

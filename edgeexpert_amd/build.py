@@ -60,11 +60,18 @@ def build_code_objects(extra=()):
 
 def build_host_lib():
     srcs = [os.path.join(CSRC, "host", n) for n in ("tfq.cpp", "loader.cpp")]
+    # the allocation-free entry point's device scratch: host + device compile
+    # (a fat binary with one __device__ array), linked into the same library
+    noalloc = os.path.join(LIB_DIR, "noalloc.o")
+    _run([os.path.join(ROCM, "bin", "hipcc"), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-c", os.path.join(CSRC, "host", "noalloc.hip"), "-o", noalloc])
     tmp = HOST_LIB + ".tmp"
     _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
-          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", *srcs, "-o", tmp,
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", *srcs, noalloc, "-o", tmp,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
     os.replace(tmp, HOST_LIB)
+    os.remove(noalloc)
     return HOST_LIB
 
 

@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "../../../include/tfq_runtime.h"
+#include "noalloc.hpp"
 #include "ops.hpp"
 
 namespace tfq {
@@ -163,6 +164,9 @@ struct tfq_ctx {
     Attention* attn = nullptr;
     DecodeLayer* layer = nullptr;
     LMHeadGreedyInt4* lmhead = nullptr;
+    void* scratch = nullptr;           // this device's copy of the noalloc scratch array
+    int scratch_status = TFQ_OK;       // hipGetSymbolAddress's outcome at creation
+    char scratch_error[256] = {0};
     ~tfq_ctx() {
         delete lmhead;
         delete layer;
@@ -212,6 +216,13 @@ int tfq_create(tfq_ctx** out, const char* code_object_path) {
     if (rc) {
         delete c;
         return rc;
+    }
+    // the allocation-free entry point's scratch on this device; a failure is
+    // reported by that entry point, not by the context
+    c->scratch_status = noalloc_scratch_address(&c->scratch);
+    if (c->scratch_status != TFQ_OK) {
+        std::snprintf(c->scratch_error, sizeof(c->scratch_error), "%s", error_state().message);
+        c->scratch = nullptr;
     }
     *out = c;
     return TFQ_OK;
@@ -366,6 +377,22 @@ int tfq_moe_decode_token(tfq_ctx* ctx, void* stream, const tfq_router* router,
     if (rc) return rc;
     return ctx->moe->encode_phase2(stream, *pool, out_indices, acts_scratch, out_weights, residual,
                                    y, d, f, top_k);
+}
+
+int tfq_moe_decode_token_noalloc(tfq_ctx* ctx, void* stream, const tfq_router* router,
+                                 const tfq_expert_pool* pool, const uint16_t* x, const uint16_t* residual,
+                                 uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k, uint32_t* out_indices,
+                                 uint16_t* out_weights) {
+    TFQ_REQUIRE_CTX(ctx);
+    if (!ctx->scratch)
+        return fail(ctx->scratch_status ? ctx->scratch_status : TFQ_E_HIP, "noalloc scratch unavailable: %s",
+                    ctx->scratch_error);
+    if ((uint64_t)top_k * f * 2 > kNoAllocActsBytes)
+        return fail(TFQ_E_INVAL, "top_k * f * 2 = %llu bytes exceeds the %zu-byte scratch of the allocation-free "
+                    "entry point", (unsigned long long)top_k * f * 2, kNoAllocActsBytes);
+    uint8_t* base = static_cast<uint8_t*>(ctx->scratch);
+    return tfq_moe_decode_token(ctx, stream, router, pool, x, residual, y, d, f, top_k, out_indices, out_weights,
+                                reinterpret_cast<uint16_t*>(base), base + kNoAllocLogitsOffset);
 }
 
 int tfq_shared_expert_q4(tfq_ctx* ctx, void* stream, const tfq_q4_matrix* gate,

@@ -326,6 +326,15 @@ def moe_decode_token(context: Context, stream, router: Router, pool: ExpertPool,
           "tfq_moe_decode_token")
 
 
+def moe_decode_token_noalloc(context: Context, stream, router: Router, pool: ExpertPool, x, residual, y, d,
+                             f, top_k, out_indices, out_weights):
+    """moe_decode_token with its scratch in libtfq's fixed device array (no allocation)."""
+    r, p = router.desc(), pool.desc()
+    check(lib().tfq_moe_decode_token_noalloc(context.handle, _s(stream), C.byref(r), C.byref(p), _addr(x),
+                                             _addr(residual), _addr(y), d, f, top_k, _addr(out_indices),
+                                             _addr(out_weights)), "tfq_moe_decode_token_noalloc")
+
+
 class SharedExpertInt4:
     """S/Kernels/MoE/SharedExpertInt4.swift:21-95."""
 

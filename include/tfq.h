@@ -258,6 +258,28 @@ int tfq_moe_decode_token(tfq_ctx *ctx, void *stream, const tfq_router *router,
                          uint32_t top_k, uint32_t *out_indices, uint16_t *out_weights,
                          uint16_t *acts_scratch, void *workspace);
 
+/* Bytes of the device scratch array of tfq_moe_decode_token_noalloc (one
+ * per GPU, held until the process ends). */
+#define TFQ_NOALLOC_SCRATCH_BYTES (16384u + TFQ_ROUTER_WORKSPACE_BYTES)
+
+/* tfq_moe_decode_token with no scratch arguments and no allocation: the
+ * routed activations and the router logits live in a fixed device array
+ * inside libtfq (TFQ_NOALLOC_SCRATCH_BYTES, one copy per GPU, resolved once
+ * per context at tfq_create). This entry point has no counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It calls no hipMalloc/hipFree. Limit: top_k * f * 2 <= 16384
+ * bytes (every shape the decode phases accept: f <= 1024, top_k <= 8);
+ * larger shapes return TFQ_E_INVAL. Every call on one GPU shares that GPU's
+ * array, through every context: calls that overlap on one GPU (concurrent
+ * streams or threads) race. Nothing in the array needs to start at zero
+ * (each call writes what it reads), and the last call's contents remain.
+ * Contracts otherwise as tfq_moe_decode_token. */
+int tfq_moe_decode_token_noalloc(tfq_ctx *ctx, void *stream, const tfq_router *router,
+                                 const tfq_expert_pool *pool, const uint16_t *x,
+                                 const uint16_t *residual, uint16_t *y, uint32_t d, uint32_t f,
+                                 uint32_t top_k, uint32_t *out_indices, uint16_t *out_weights);
+
 /* Shared expert, int4 form: act[i] = fp16(gelu_tanh(gate[i]·x) * (up[i]·x))
  * with gate/up kept in fp32 (one fused launch), then y = fp16(down·act).
  * gate/up are [f][d], down is [d][f]; act_scratch: fp16 [f].
