@@ -1,14 +1,15 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X quantized-matmul hot path (one GPU).
 
-Workload: decode MoE expert block, one token per
-step: int8 router [128 x 2816] + softmax top-8, then 8 int4 g64 experts
-(gate/up [704 x 2816], GeGLU, down [2816 x 704]) weighted-summed. All 128
-experts (430 MB) are resident in HBM; the token changes every step (64
-distinct hidden states, rotated) so the selected experts change and mostly
-miss the 256 MB last-level cache. Steps are replayed from a HIP graph that
-holds 64 tokens (3 kernels each: router GEMV, phase 1 with the top-k
-selection folded in, phase 2).
+Workload: decode MoE expert block: int8 router
+[128 x 2816] + softmax top-8, then 8 int4 g64 experts (gate/up [704 x 2816],
+GeGLU, down [2816 x 704]) weighted-summed, one token at a time. All 128
+experts (430 MB) are resident in HBM. A step is one batch of 64 decode
+tokens (64 distinct hidden states, so the selected experts change and
+mostly miss the 256 MB last-level cache), replayed from one HIP graph (3
+kernels per token: router GEMV, phase 1 with the top-k selection folded in,
+phase 2). --warmup W replays run untimed, then exactly --steps K replays
+are timed; value = us per token = time / (64 K).
 
 Also measured (extra fields): BASELINE config 0, the int4 g64 GEMV
 [2816 x 2816], cold (rotating through 256 weight copies, 1.14 GB) and warm,
@@ -25,6 +26,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -59,18 +61,19 @@ C4_CTX = 4096
 C4_LAYERS = 8
 
 
-def c4_bytes():
+def c4_bytes(shared_bits=4):
     """Algorithmic HBM bytes of one config-4 layer token (weights fp16 scale+bias,
     fp16 KV cache read once; activations and norm vectors are a few KB)."""
     d, qd, kvd = C4["d"], C4["nq"] * C4["hd"], C4["nkv"] * C4["hd"]
     q4 = lambda m, n: m * n // 2 + 2 * m * (n // 64) * 2
+    qs = (lambda m, n: m * n + 2 * m * (n // 64) * 2) if shared_bits == 8 else q4
     parts = {
         "qkv": q4(qd + 2 * kvd, d),
         "attention_kv": 2 * C4_CTX * kvd * 2,
         "o_proj": q4(d, qd),
         "router": E * d + 2 * E * (d // 64) * 2,
         "routed": C4["k"] * 3 * q4(C4["f"], d),
-        "shared": 2 * q4(C4["fs"], d) + q4(d, C4["fs"]),
+        "shared": 2 * qs(C4["fs"], d) + qs(d, C4["fs"]),
     }
     parts["total"] = sum(parts.values())
     return parts
@@ -192,11 +195,14 @@ def bench_bits(ctx, stream, batch_avg_us, router, hbuf):
     return out
 
 
-def bench_c4(ctx, stream, launch, batch_avg_us):
+def bench_c4(ctx, stream, launch, batch_avg_us, shared_bits=4):
+    """Config 4's decoder layer; shared_bits 8 runs the shared expert at
+    8 bits (the reference's default width) instead of 4."""
     from edgeexpert_amd import ops, synth
     from edgeexpert_amd.runtime import DeviceBuffer, Event, Graph
     t0 = time.time()
-    w = synth.decode_layer(0, "c4", C4["d"], C4["nq"], C4["nkv"], C4["hd"], E, C4["f"], C4["fs"])
+    w = synth.decode_layer(0, "c4", C4["d"], C4["nq"], C4["nkv"], C4["hd"], E, C4["f"], C4["fs"],
+                           shared_bits=shared_bits)
     kvd = C4["nkv"] * C4["hd"]
     kc = synth.f16_vector(0, "c4/kc", C4_CTX * kvd)
     vc = synth.f16_vector(0, "c4/vc", C4_CTX * kvd)
@@ -236,7 +242,7 @@ def bench_c4(ctx, stream, launch, batch_avg_us):
     b.record(stream)
     stream.sync()
     us = a.elapsed_ms(b) * 1e3 / (reps * C4_LAYERS)
-    nb = c4_bytes()
+    nb = c4_bytes(shared_bits)
     gbs = nb["total"] / (us * 1e-6) / 1e9
     floor_us = nb["total"] / (HBM_PEAK_GBS * 1e9) * 1e6
     # attention alone (split-K partial + combine over the 4096-key cache), back to back
@@ -249,13 +255,170 @@ def bench_c4(ctx, stream, launch, batch_avg_us):
                                                 out, C4["hd"], C4["nq"], C4["nkv"], C4_CTX, awsb, aws,
                                                 scale=1.0), 64)
     attn_gbs = nb["attention_kv"] / (attn_us * 1e-6) / 1e9
-    log(f"decode layer C4 ({launch}): {us:.2f} us/token ({gbs:.0f} GB/s of {nb['total']} B; "
+    log(f"decode layer C4 ({launch}, {shared_bits}-bit shared expert): {us:.2f} us/token ({gbs:.0f} GB/s of {nb['total']} B; "
         f"8 TB/s floor {floor_us:.2f} us); attention alone {attn_us:.2f} us ({attn_gbs:.0f} GB/s)")
-    return {"us_per_token": round(us, 3), "bytes_per_token": nb["total"], "gbs": round(gbs, 1),
+    return {"us_per_token": round(us, 3), "shared_expert_bits": shared_bits, "bytes_per_token": nb["total"],
+            "gbs": round(gbs, 1),
             "hbm_floor_us": round(floor_us, 3), "frac_of_floor": round(floor_us / us, 4),
             "bytes": {k: v for k, v in nb.items() if k != "total"}, "layers_rotated": C4_LAYERS,
             "context": C4_CTX, "position": pos, "launch": launch,
             "attention_us": round(attn_us, 3), "attention_gbs": round(attn_gbs, 1)}
+
+
+def host_cpu():
+    """(lscpu model name, logical CPUs visible, threads this job may use)."""
+    model = "unknown"
+    try:
+        for line in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    visible = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    usable = min(visible, int(omp)) if omp.isdigit() and int(omp) > 0 else visible
+    return model, visible, usable
+
+
+def cpu_baseline(Wr, Sr, Br, pool_bytes, stride, offs, H, W0, S0, B0):
+    """The reference's CPU path (oracle/cpu_baseline.c: the oracle's row
+    arithmetic, -O3 -march=native built on this host, rows split over
+    threads) timed on the host cores at 1 thread and at every usable core:
+    config 1 (one decode token: router + 8 experts) and config 0 (the int4
+    GEMV). Medians of >= 20 runs after warmup."""
+    import oracle   # the checker, timed as the CPU restatement of the reference path
+    from edgeexpert_amd import synth
+    model, visible, usable = host_cpu()
+    oracle.baseline_lib(rebuild=True)       # -march=native for this host
+    hs = [H[t].view(np.float16).astype(np.float32) for t in range(TOKENS)]
+    x0 = synth.f16_to_f32(synth.f16_vector(0, "c0/x", 2816))
+
+    def median_us(fn, n, warm=2):
+        for i in range(warm):
+            fn(i)
+        ts = []
+        for i in range(n):
+            t0 = time.perf_counter()
+            fn(i)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)) * 1e6
+
+    res = {}
+    for threads in sorted({1, usable}):
+        tok = median_us(lambda i: oracle.baseline_moe_decode_token(Wr, Sr, Br, pool_bytes, stride, offs,
+                                                                   hs[i % TOKENS], D, F, K, threads), 20)
+        gemv = median_us(lambda i: oracle.baseline_gemv_int4(W0, S0, B0, x0, threads), 40)
+        res[threads] = (tok, gemv)
+        log(f"CPU baseline, {threads} thread(s): config 1 {tok:.0f} us/token, config 0 GEMV {gemv:.0f} us")
+    tok_all, gemv_all = res[usable]
+    tok_1, gemv_1 = res[1]
+    return {"value": round(tok_all, 1), "unit": "us/token", "cores": usable, "kind": "port",
+            "sample": f"config 1: median of 20 decode tokens (router + 8 experts; 64 rotated hidden states), "
+                      f"rows split over {usable} threads; oracle/cpu_baseline.c, gcc -O3 -march=native "
+                      f"-ffp-contract=off -fopenmp",
+            "cpu_model": model, "logical_cpus_visible": visible, "threads_all_cores": usable,
+            "one_thread": {"config1_us_per_token": round(tok_1, 1), "config0_gemv_us": round(gemv_1, 1)},
+            "all_cores": {"config1_us_per_token": round(tok_all, 1), "config0_gemv_us": round(gemv_all, 1)}}
+
+
+def trace_summary(csv_path, out=sys.stdout, b2b_gap_us=None):
+    """Per (kernel, grid, workgroup) dispatch statistics of a rocprofv3
+    --kernel-trace CSV: the same kernel launched at several shapes (the
+    int4 GEMV at config 0 and at the LM-head shape, say) is reported once
+    per shape. b2b_gap_us: keep only dispatches that start within that many
+    microseconds of the previous dispatch's end (launched back to back, as
+    in bench.py's per-kernel batches)."""
+    import csv
+    rows = []
+    with open(csv_path, newline="") as fh:
+        for row in csv.DictReader(fh):
+            rows.append((int(row["Start_Timestamp"]), int(row["End_Timestamp"]), row["Kernel_Name"],
+                         tuple(int(row[f"Grid_Size_{a}"]) for a in "XYZ"),
+                         tuple(int(row[f"Workgroup_Size_{a}"]) for a in "XYZ")))
+    rows.sort()
+    groups = {}
+    prev_end = None
+    for start, end, name, grid, wg in rows:
+        keep = b2b_gap_us is None or (prev_end is not None and start - prev_end <= b2b_gap_us * 1e3)
+        prev_end = end if prev_end is None else max(prev_end, end)
+        if keep:
+            groups.setdefault((name, grid, wg), []).append((end - start) / 1e3)
+    total = sum(sum(v) for v in groups.values()) or 1.0
+    out.write(f"{'kernel':44s} {'grid (threads)':>20s} {'wg':>5s} {'calls':>6s} {'avg us':>9s} "
+              f"{'median':>9s} {'min us':>8s} {'max us':>9s} {'% time':>7s}\n")
+    for (name, grid, wg), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        a = np.array(v)
+        g = "x".join(str(d) for d in grid if d > 1) or "1"
+        out.write(f"{name[:44]:44s} {g:>20s} {wg[0]:>5d} {len(a):>6d} {a.mean():>9.2f} {np.median(a):>9.2f} "
+                  f"{a.min():>8.2f} {a.max():>9.2f} {100 * a.sum() / total:>7.2f}\n")
+
+
+def pmc_summary(csv_path, out=sys.stdout, simds=1024, xcds=8):
+    """Per (kernel, grid) averages of the counters in a rocprofv3 --pmc
+    counter_collection CSV, per dispatch, with the matrix-core busy fraction
+    of rocprofv3's MfmaUtil: SQ_VALU_MFMA_BUSY_CYCLES / (cycles x SIMDs),
+    cycles = GRBM_GUI_ACTIVE / XCDs (MI355X: 8 XCDs, whose GUI_ACTIVE counts
+    the profiler sums; 1024 SIMDs). A busy cycle is 1024 fp16 FLOP of one
+    SIMD, so the fraction equals achieved / dense-peak FLOP/s, which
+    SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 (the dispatch's MFMA FLOP) cross-checks."""
+    import csv
+    acc = {}
+    with open(csv_path, newline="") as fh:
+        for row in csv.DictReader(fh):
+            key = (row["Kernel_Name"], int(row["Grid_Size"]), int(row["Workgroup_Size"]))
+            d = acc.setdefault(key, {})
+            d.setdefault(row["Counter_Name"], {})[row["Dispatch_Id"]] = float(row["Counter_Value"])
+            d.setdefault("_dur", {})[row["Dispatch_Id"]] = (int(row["End_Timestamp"]) -
+                                                            int(row["Start_Timestamp"])) / 1e3
+    for (name, grid, wg), d in sorted(acc.items(), key=lambda kv: -sum(kv[1]["_dur"].values())):
+        n = len(d["_dur"])
+        mean = {c: sum(v.values()) / len(v) for c, v in d.items()}
+        line = f"{name[:40]:40s} grid {grid:>8d} wg {wg:>4d} n {n:>5d} avg {mean['_dur']:8.2f} us"
+        for c in sorted(k for k in mean if not k.startswith("_")):
+            line += f" {c}={mean[c]:.4g}"
+        gui = mean.get("GRBM_GUI_ACTIVE")
+        if gui and "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+            line += f" | MFMA busy {100 * mean['SQ_VALU_MFMA_BUSY_CYCLES'] * xcds / (gui * simds):.1f}%"
+        if "SQ_INSTS_VALU_MFMA_MOPS_F16" in mean and mean["_dur"] > 0:
+            tf = mean["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512 / (mean["_dur"] * 1e-6) / 1e12
+            line += f" | MFMA {tf:.0f} TFLOP/s"
+        out.write(line + "\n")
+
+
+def bench_gemm_policy(ctx, stream, batch_avg_us):
+    """The prefill GEMM's kernel choice by token count (config 2's weights,
+    N 8192 x K 2816, bf16): the library's choice at token counts on both
+    sides of its crossover (80 tokens at this N), and both kernels forced at
+    the two counts next to it."""
+    from edgeexpert_amd import ops, synth
+    from edgeexpert_amd._lib import DTYPE_BF16, GEMM_PATH_SKINNY32, GEMM_PATH_TILE
+    from edgeexpert_amd.runtime import DeviceBuffer
+    N, Kd = 8192, 2816
+    W, S, B = synth.int4_matrix(0, "c2/w", N, Kd)
+    copies = 8                 # rotate weight copies: each launch reads weights the last ones evicted
+    bufs = [tuple(DeviceBuffer.from_array(a) for a in (W, S, B)) for _ in range(copies)]
+    X = DeviceBuffer.from_array(synth.bf16_vector(0, "c2/x", 512 * Kd))
+    Y = DeviceBuffer(512 * N * 2)
+    q = ops.PrefillInt4QMM(ctx)
+    wbytes = N * Kd // 2 + 2 * N * (Kd // 64) * 2
+    out = {"shape": [None, N, Kd], "crossover_tokens": 80, "auto": {}, "forced": {}}
+
+    def run(m, path):
+        return batch_avg_us(lambda i: q.encode(stream, *bufs[i % copies], X, Y, m, N, Kd, DTYPE_BF16, path=path),
+                            32, reps_=3)
+    for m in (1, 16, 64, 80, 96, 128, 512):
+        us = run(m, None)
+        out["auto"][str(m)] = {"us": round(us, 2), "tflops": round(2.0 * m * N * Kd / (us * 1e-6) / 1e12, 1),
+                               "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1),
+                               "kernel": "skinny" if m <= 80 else "tile"}
+    for m in (64, 96):
+        out["forced"][str(m)] = {"skinny32_us": round(run(m, GEMM_PATH_SKINNY32), 2),
+                                 "tile_us": round(run(m, GEMM_PATH_TILE), 2)}
+    log("GEMM by token count (N 8192, K 2816, bf16): " +
+        ", ".join(f"M={m} {v['us']:.1f} us ({v['kernel']})" for m, v in out["auto"].items()) +
+        "; forced " + ", ".join(f"M={m}: skinny {v['skinny32_us']:.1f} / tile {v['tile_us']:.1f} us"
+                                for m, v in out["forced"].items()))
+    return out
 
 
 TRAFFIC_FILE = "profiles/hbm_traffic_moe_decode_c1.txt"
@@ -279,15 +442,27 @@ def read_traffic():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4096)
-    ap.add_argument("--warmup", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=64, help="timed 64-token graph replays")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed replays before them")
+    ap.add_argument("--legs", default="all",
+                    help="comma list of the extra legs to run besides the headline: c0, c2, lmhead, c3, c4, "
+                         "policy, bits, cpu (default all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-c4", action="store_true", help="skip the config-4 decode-layer leg")
-    ap.add_argument("--no-c3", action="store_true", help="skip the config-3 grouped-prefill leg")
-    ap.add_argument("--no-bits", action="store_true", help="skip the 2/3-bit variant legs")
     ap.add_argument("--launch", choices=("graph", "stream"), default="graph",
                     help="replay the 64-token step from a HIP graph, or issue it from the host")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="print per (kernel, grid) statistics of a rocprofv3 kernel-trace CSV and exit")
+    ap.add_argument("--b2b-gap-us", type=float, default=None,
+                    help="with --trace-summary: only dispatches starting within this gap of the previous end")
+    ap.add_argument("--pmc-summary", metavar="CSV",
+                    help="print per (kernel, grid) averages of a rocprofv3 --pmc counter CSV and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
+    if args.trace_summary:
+        trace_summary(args.trace_summary, b2b_gap_us=args.b2b_gap_us)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               "sharding of this path is a design note, not a measured configuration.",
@@ -297,6 +472,11 @@ def main():
     from edgeexpert_amd import ops, synth
     from edgeexpert_amd._lib import LM_HEAD_WORKSPACE_BYTES, ROUTER_WORKSPACE_BYTES
     from edgeexpert_amd.runtime import DeviceBuffer, Event, Graph, Stream, device_info, synchronize
+
+    legs = set(args.legs.split(","))
+
+    def want(leg):
+        return ("all" in legs or leg in legs) and not (leg == "cpu" and args.no_cpu)
 
     name, arch = device_info()
     log(f"device {name} {arch}")
@@ -330,9 +510,9 @@ def main():
         for t in range(TOKENS):
             token(t)
 
-    reps_w = max(1, args.warmup // TOKENS)
-    reps = max(1, args.steps // TOKENS)
-    steps = reps * TOKENS
+    reps_w = max(0, args.warmup)
+    reps = max(1, args.steps)
+    steps = reps
     if args.launch == "graph":
         graph = Graph(stream, all_tokens)
         run = lambda: graph.launch(stream)
@@ -354,8 +534,8 @@ def main():
     synchronize()
     wall = time.perf_counter() - wall0
     gpu_ms = e0.elapsed_ms(e1)
-    us_per_token = gpu_ms * 1e3 / steps
-    log(f"MoE decode ({args.launch}): {steps} tokens in {gpu_ms:.2f} ms (events), wall "
+    us_per_token = gpu_ms * 1e3 / (steps * TOKENS)
+    log(f"MoE decode ({args.launch}): {steps} steps x {TOKENS} tokens in {gpu_ms:.2f} ms (events), wall "
         f"{wall * 1e3:.2f} ms -> {us_per_token:.2f} us/token")
 
     # ------------------------------ per-kernel durations (HIP events) ----
@@ -406,86 +586,98 @@ def main():
     log("kernel avg (back-to-back): " + ", ".join(f"{k} {v:.2f} us" for k, v in k_us.items())
         + f"; phase1 {p1_gbs:.0f} GB/s ({nb['phase1']} B/launch)")
 
-    # ------------------------------------------------ GEMV config 0 (extra) ----
-    gemv = ops.DequantInt4GEMV(ctx)
-    n_copies = 256
     W0, S0, B0 = synth.int4_matrix(0, "c0/w", 2816, 2816)
     x0 = DeviceBuffer.from_array(synth.f16_vector(0, "c0/x", 2816))
-    y0 = DeviceBuffer(2816 * 2)
-    wsz, ssz = W0.nbytes, S0.nbytes
-    big = DeviceBuffer(n_copies * (wsz + 2 * ssz))
-    for i in range(n_copies):
-        base = i * (wsz + 2 * ssz)
-        big.upload(W0, base)
-        big.upload(S0, base + wsz)
-        big.upload(B0, base + wsz + ssz)
-    gemv_bytes = wsz + 2 * ssz + 2 * 2816 * 2
+    gemv = ops.DequantInt4GEMV(ctx)
 
-    def gemv_launch(copy):
-        base = copy * (wsz + 2 * ssz)
-        gemv.encode(stream, big, big, big, x0, y0, 2816, 2816, weights_offset=base,
-                    scales_offset=base + wsz, biases_offset=base + wsz + ssz)
+    def leg_c0():
+        """Config 0: the int4 GEMV [2816 x 2816], cold (256 rotating weight
+        copies, 1.1 GB) and warm, back to back."""
+        n_copies = 256
+        y0 = DeviceBuffer(2816 * 2)
+        wsz, ssz = W0.nbytes, S0.nbytes
+        big = DeviceBuffer(n_copies * (wsz + 2 * ssz))
+        for i in range(n_copies):
+            base = i * (wsz + 2 * ssz)
+            big.upload(W0, base)
+            big.upload(S0, base + wsz)
+            big.upload(B0, base + wsz + ssz)
+        gemv_bytes = wsz + 2 * ssz + 2 * 2816 * 2
 
-    cold_us = batch_avg_us(gemv_launch, n_copies)
-    warm_us = batch_avg_us(lambda i: gemv_launch(0), n_copies)
-    cold_gbs = gemv_bytes / (cold_us * 1e-6) / 1e9
-    warm_gbs = gemv_bytes / (warm_us * 1e-6) / 1e9
-    log(f"GEMV C0 (back-to-back): cold {cold_us:.2f} us ({cold_gbs:.0f} GB/s), warm {warm_us:.2f} us "
-        f"({warm_gbs:.0f} GB/s)")
+        def gemv_launch(copy):
+            base = copy * (wsz + 2 * ssz)
+            gemv.encode(stream, big, big, big, x0, y0, 2816, 2816, weights_offset=base,
+                        scales_offset=base + wsz, biases_offset=base + wsz + ssz)
 
-    # ------------------------------------------------ GEMM config 2 (extra) ----
-    qmm = ops.PrefillInt4QMM(ctx)
-    from edgeexpert_amd._lib import DTYPE_BF16
-    Mg, Ng, Kg = 512, 8192, 2816
-    Wg, Sg, Bg = synth.int4_matrix(0, "c2/w", Ng, Kg)
-    gW, gS, gB = (DeviceBuffer.from_array(a) for a in (Wg, Sg, Bg))
-    gX = DeviceBuffer.from_array(synth.bf16_vector(0, "c2/x", Mg * Kg))
-    gY = DeviceBuffer(Mg * Ng * 2)
-    gemm_us = batch_avg_us(lambda i: qmm.encode(stream, gW, gS, gB, gX, gY, Mg, Ng, Kg, DTYPE_BF16), 20)
-    gemm_flop = 2.0 * Mg * Ng * Kg
-    gemm_tflops = gemm_flop / (gemm_us * 1e-6) / 1e12
-    log(f"GEMM C2 (bf16, back-to-back): {gemm_us:.2f} us -> {gemm_tflops:.1f} TFLOP/s "
-        f"({gemm_tflops / 2500.0 * 100:.1f}% of 2.5 PFLOP/s dense fp16/bf16)")
+        cold_us = batch_avg_us(gemv_launch, n_copies)
+        warm_us = batch_avg_us(lambda i: gemv_launch(0), n_copies)
+        cold_gbs = gemv_bytes / (cold_us * 1e-6) / 1e9
+        warm_gbs = gemv_bytes / (warm_us * 1e-6) / 1e9
+        log(f"GEMV C0 (back-to-back): cold {cold_us:.2f} us ({cold_gbs:.0f} GB/s), warm {warm_us:.2f} us "
+            f"({warm_gbs:.0f} GB/s)")
+        return {"shape": [2816, 2816], "bytes": gemv_bytes, "cold_us": round(cold_us, 3),
+                "cold_gbs": round(cold_gbs, 1), "cold_frac": round(cold_gbs / HBM_PEAK_GBS, 4),
+                "warm_us": round(warm_us, 3), "warm_gbs": round(warm_gbs, 1), "copies_rotated": n_copies}
 
-    # ------------------------------------ large GEMV: LM-head shape (extra) ----
-    # 262144 x 2816 int4 (415 MB, larger than every cache): the steady-state
-    # streaming rate of the decode GEMV, launched back to back.
-    Ml = 262144
-    Wl, Sl, Bl = synth.int4_matrix(0, "lmhead/w", 4096, 2816)        # 4096-row tile, replicated
-    big_l = DeviceBuffer(Ml * 1408)
-    sl_b, bl_b = DeviceBuffer(Ml * 88), DeviceBuffer(Ml * 88)
-    for r0 in range(0, Ml, 4096):
-        big_l.upload(Wl, r0 * 1408)
-        sl_b.upload(Sl, r0 * 88)
-        bl_b.upload(Bl, r0 * 88)
-    yl = DeviceBuffer(Ml * 2)
-    lm_bytes = Ml * 1408 + 2 * Ml * 88 + 2816 * 2 + Ml * 2
-    lm_us = batch_avg_us(lambda i: gemv.encode(stream, big_l, sl_b, bl_b, x0, yl, Ml, 2816), 8, reps_=3)
-    lm_gbs = lm_bytes / (lm_us * 1e-6) / 1e9
-    log(f"GEMV LM-head shape {Ml}x2816: {lm_us:.1f} us ({lm_gbs:.0f} GB/s, "
-        f"{lm_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
-    # the greedy decode head over the same rows: RMSNorm folded into the
-    # activation staging, per-block argmax, one-block reduce (2 launches)
-    head = ops.LMHeadGreedyInt4(ctx)
-    tok_b, lm_ws = DeviceBuffer(4), DeviceBuffer(LM_HEAD_WORKSPACE_BYTES)
-    norm_w = DeviceBuffer.from_array(synth.f16_vector(0, "lmhead/norm", 2816, std=0.5))
-    greedy_us = batch_avg_us(lambda i: head.encode_greedy_decode(stream, x0, norm_w, big_l, sl_b, bl_b, tok_b,
-                                                                 2816, Ml, lm_ws), 8, reps_=3)
-    greedy_bytes = Ml * 1408 + 2 * Ml * 88 + 2 * 2816 * 2 + 4
-    greedy_gbs = greedy_bytes / (greedy_us * 1e-6) / 1e9
-    log(f"greedy LM head {Ml}x2816 (norm + rows + argmax, 2 launches): {greedy_us:.1f} us "
-        f"({greedy_gbs:.0f} GB/s, {greedy_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
-    del big_l, sl_b, bl_b, yl, lm_ws
+    def leg_c2():
+        """Config 2: the bf16 prefill GEMM 512 x 8192 x 2816."""
+        from edgeexpert_amd._lib import DTYPE_BF16
+        qmm = ops.PrefillInt4QMM(ctx)
+        Mg, Ng, Kg = 512, 8192, 2816
+        Wg, Sg, Bg = synth.int4_matrix(0, "c2/w", Ng, Kg)
+        gW, gS, gB = (DeviceBuffer.from_array(a) for a in (Wg, Sg, Bg))
+        gX = DeviceBuffer.from_array(synth.bf16_vector(0, "c2/x", Mg * Kg))
+        gY = DeviceBuffer(Mg * Ng * 2)
+        gemm_us = batch_avg_us(lambda i: qmm.encode(stream, gW, gS, gB, gX, gY, Mg, Ng, Kg, DTYPE_BF16), 20)
+        gemm_tflops = 2.0 * Mg * Ng * Kg / (gemm_us * 1e-6) / 1e12
+        log(f"GEMM C2 (bf16, back-to-back): {gemm_us:.2f} us -> {gemm_tflops:.1f} TFLOP/s "
+            f"({gemm_tflops / 2500.0 * 100:.1f}% of 2.5 PFLOP/s dense fp16/bf16)")
+        return {"shape": [Mg, Ng, Kg], "dtype": "bf16 in/out, fp16 MFMA, fp32 acc", "us": round(gemm_us, 3),
+                "tflops": round(gemm_tflops, 1), "frac_of_dense_peak": round(gemm_tflops / 2500.0, 4)}
 
-    # ----------------------------------------- grouped MoE prefill, config 3 ----
-    c3 = None if args.no_c3 else bench_c3(ctx, stream, batch_avg_us)
+    def leg_lmhead():
+        """262144 x 2816 int4 (415 MB, larger than every cache): the steady-state
+        streaming rate of the decode GEMV, and the greedy decode head over the
+        same rows (RMSNorm folded into the staging, per-block argmax, one-block
+        reduce: 2 launches), back to back."""
+        Ml = 262144
+        Wl, Sl, Bl = synth.int4_matrix(0, "lmhead/w", 4096, 2816)        # 4096-row tile, replicated
+        big_l = DeviceBuffer(Ml * 1408)
+        sl_b, bl_b = DeviceBuffer(Ml * 88), DeviceBuffer(Ml * 88)
+        for r0 in range(0, Ml, 4096):
+            big_l.upload(Wl, r0 * 1408)
+            sl_b.upload(Sl, r0 * 88)
+            bl_b.upload(Bl, r0 * 88)
+        yl = DeviceBuffer(Ml * 2)
+        lm_bytes = Ml * 1408 + 2 * Ml * 88 + 2816 * 2 + Ml * 2
+        lm_us = batch_avg_us(lambda i: gemv.encode(stream, big_l, sl_b, bl_b, x0, yl, Ml, 2816), 8, reps_=3)
+        lm_gbs = lm_bytes / (lm_us * 1e-6) / 1e9
+        log(f"GEMV LM-head shape {Ml}x2816: {lm_us:.1f} us ({lm_gbs:.0f} GB/s, "
+            f"{lm_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+        head = ops.LMHeadGreedyInt4(ctx)
+        tok_b, lm_ws = DeviceBuffer(4), DeviceBuffer(LM_HEAD_WORKSPACE_BYTES)
+        norm_w = DeviceBuffer.from_array(synth.f16_vector(0, "lmhead/norm", 2816, std=0.5))
+        greedy_us = batch_avg_us(lambda i: head.encode_greedy_decode(stream, x0, norm_w, big_l, sl_b, bl_b, tok_b,
+                                                                     2816, Ml, lm_ws), 8, reps_=3)
+        greedy_bytes = Ml * 1408 + 2 * Ml * 88 + 2 * 2816 * 2 + 4
+        greedy_gbs = greedy_bytes / (greedy_us * 1e-6) / 1e9
+        log(f"greedy LM head {Ml}x2816 (norm + rows + argmax, 2 launches): {greedy_us:.1f} us "
+            f"({greedy_gbs:.0f} GB/s, {greedy_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+        return ({"shape": [Ml, 2816], "bytes": lm_bytes, "us": round(lm_us, 2), "gbs": round(lm_gbs, 1),
+                 "frac": round(lm_gbs / HBM_PEAK_GBS, 4)},
+                {"shape": [Ml, 2816], "bytes": greedy_bytes, "us": round(greedy_us, 2), "gbs": round(greedy_gbs, 1),
+                 "frac": round(greedy_gbs / HBM_PEAK_GBS, 4),
+                 "kernels": "lm_head_greedy (norm staging + rows + block argmax), lm_head_reduce"})
 
-    # ------------------------------------------------ decode layer config 4 ----
-    c4 = None if args.no_c4 else bench_c4(ctx, stream, args.launch, batch_avg_us)
-
-    # ------------------------------------------------- 2/3-bit variants ----
-    bits_legs = None if args.no_bits else bench_bits(ctx, stream, batch_avg_us, router, hbuf)
-    if bits_legs is not None and not args.no_c3:
+    gemv_c0 = leg_c0() if want("c0") else None
+    gemm_c2 = leg_c2() if want("c2") else None
+    gemv_lmhead, lm_head_greedy = leg_lmhead() if want("lmhead") else (None, None)
+    c3 = bench_c3(ctx, stream, batch_avg_us) if want("c3") else None
+    c4 = bench_c4(ctx, stream, args.launch, batch_avg_us) if want("c4") else None
+    c4_s8 = bench_c4(ctx, stream, args.launch, batch_avg_us, shared_bits=8) if want("c4") else None
+    gemm_policy = bench_gemm_policy(ctx, stream, batch_avg_us) if want("policy") else None
+    bits_legs = bench_bits(ctx, stream, batch_avg_us, router, hbuf) if want("bits") else None
+    if bits_legs is not None and want("c3"):
         bits_legs["grouped_prefill_c3_b3"] = bench_c3(ctx, stream, batch_avg_us, bits=3)
 
     # -------------------------------------- HBM counter calibration kernels ----
@@ -502,29 +694,14 @@ def main():
     traffic = read_traffic()
 
     # ------------------------------------------------------ CPU baseline ----
-    cpu = None
-    if not args.no_cpu:
-        import oracle   # the checker, timed as the CPU restatement of the reference path
-        hs = [H[t].view(np.float16).astype(np.float32) for t in range(TOKENS)]
-        done, c0 = 0, time.perf_counter()
-        while (time.perf_counter() - c0 < 10.0 and done < 200) or done < 3:
-            h = hs[done % TOKENS]
-            ridx, rw = oracle.topk_softmax(oracle.router_logits(Wr, Sr, Br, h), K)
-            oracle.moe_routed(pool_bytes, stride, offs, h, ridx, rw, D, F)
-            done += 1
-        cpu_us = (time.perf_counter() - c0) / done * 1e6
-        cpu = {"value": round(cpu_us, 1), "unit": "us/token", "cores": 1, "kind": "port",
-               "sample": f"{done} tokens of config 1 (router + 8 experts), oracle/tfq_oracle.c, "
-                         f"1 thread, host {os.cpu_count()} logical CPUs"}
-        log(f"CPU baseline: {cpu_us:.0f} us/token over {done} tokens")
-
+    cpu = cpu_baseline(Wr, Sr, Br, pool_bytes, stride, offs, H, W0, S0, B0) if want("cpu") else None
     out = {
         "metric": "MoE decode layer us/token (BASELINE config 1: int8 router + top-8 of 128 int4 g64 experts)",
         "value": round(us_per_token, 3),
         "unit": "us/token",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": reps_w * TOKENS,
+        "warmup": reps_w,
         "ms_per_step": round(gpu_ms / steps, 6),
         "higher_is_better": False,
         "scaling": "weak",
@@ -532,7 +709,7 @@ def main():
         "dtype": "int4/int8 weights x fp16 activations, fp32 accumulate",
         "data": "synthetic (seeded SplitMix64, BASELINE distributions)",
         "config": {"workload": "config1_moe_decode", "experts": E, "top_k": K, "d": D, "f": F,
-                   "tokens_rotated": TOKENS, "launch": args.launch,
+                   "tokens_per_step": TOKENS, "tokens_rotated": TOKENS, "launch": args.launch,
                    "kernels_per_token": "router_logits, moe_phase1_routed (top-k selection + gate/up), "
                                         "moe_phase2"},
         "roofline": {"kernel": "tfq_moe_phase1_routed (top-8 selection + gate/up of 8 experts)",
@@ -546,20 +723,14 @@ def main():
         "cpu_baseline": cpu,
         "token_bytes": nb["total"],
         "token_gbs": round(nb["total"] / (us_per_token * 1e-6) / 1e9, 1),
-        "gemv_c0": {"shape": [2816, 2816], "bytes": gemv_bytes, "cold_us": round(cold_us, 3),
-                    "cold_gbs": round(cold_gbs, 1), "cold_frac": round(cold_gbs / HBM_PEAK_GBS, 4),
-                    "warm_us": round(warm_us, 3), "warm_gbs": round(warm_gbs, 1),
-                    "copies_rotated": n_copies},
-        "gemm_c2": {"shape": [Mg, Ng, Kg], "dtype": "bf16 in/out, fp16 MFMA, fp32 acc",
-                    "us": round(gemm_us, 3), "tflops": round(gemm_tflops, 1),
-                    "frac_of_dense_peak": round(gemm_tflops / 2500.0, 4)},
-        "gemv_lmhead": {"shape": [Ml, 2816], "bytes": lm_bytes, "us": round(lm_us, 2),
-                        "gbs": round(lm_gbs, 1), "frac": round(lm_gbs / HBM_PEAK_GBS, 4)},
-        "lm_head_greedy": {"shape": [Ml, 2816], "bytes": greedy_bytes, "us": round(greedy_us, 2),
-                           "gbs": round(greedy_gbs, 1), "frac": round(greedy_gbs / HBM_PEAK_GBS, 4),
-                           "kernels": "lm_head_greedy (norm staging + rows + block argmax), lm_head_reduce"},
+        "gemv_c0": gemv_c0,
+        "gemm_c2": gemm_c2,
+        "gemv_lmhead": gemv_lmhead,
+        "lm_head_greedy": lm_head_greedy,
         "grouped_prefill_c3": c3,
         "decode_layer_c4": c4,
+        "decode_layer_c4_int8_shared": c4_s8,
+        "gemm_by_token_count": gemm_policy,
         "bit_variants": bits_legs,
         "wall_s": round(wall, 4),
         "device": f"{name} {arch}",

@@ -653,3 +653,52 @@ class Tolerance:
     quant_int4 = 1.5e-3
     quant_int8 = 1e-3
     north_star = 1e-3     # max relative error for floating-point outputs
+
+
+# ------------------------------------------------------- CPU baseline ----
+#
+# oracle/libtfq_cpu_baseline.so: the same row arithmetic split over host
+# threads (cpu_baseline.c), built -O3 -march=native on the host that times it.
+
+_BASELINE_PATH = os.path.join(_HERE, "libtfq_cpu_baseline.so")
+_baseline = None
+
+
+def baseline_lib(rebuild: bool = False):
+    """Builds (make cpu_baseline, on this host) and loads the CPU baseline library."""
+    global _baseline
+    if _baseline is None or rebuild:
+        subprocess.run(["make", "-s"] + (["-B"] if rebuild else []) + ["-C", _HERE, "cpu_baseline"], check=True)
+        L = C.CDLL(_BASELINE_PATH)
+        L.tfb_gemv_int4.restype = None
+        L.tfb_gemv_int4.argtypes = [_P, _P, _P, C.c_int, _P, C.c_int, C.c_int, _P, C.c_int]
+        L.tfb_moe_decode_token.restype = None
+        L.tfb_moe_decode_token.argtypes = [_P, _P, _P, C.c_int, _P, C.c_uint64, C.POINTER(ExpertOffsets), C.c_int,
+                                           _P, _P, C.c_int, C.c_int, C.c_int, _P, _P, _P, C.c_int]
+        _baseline = L
+    return _baseline
+
+
+def baseline_gemv_int4(W, S, B, x, threads=1, fmt=FMT_F16):
+    """tfb_gemv_int4: DequantInt4GemvRef.apply with the rows split over `threads`."""
+    W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16); x = _c(x, np.float32)
+    m, n = W.shape[0], W.shape[1] * 2
+    y = np.zeros(m, np.float32)
+    baseline_lib().tfb_gemv_int4(_ptr(W), _ptr(S), _ptr(B), fmt, _ptr(x), m, n, _ptr(y), int(threads))
+    return y
+
+
+def baseline_moe_decode_token(rW, rS, rB, pool, stride, off, h, d, f, k, threads=1, residual=None, fmt=FMT_F16):
+    """tfb_moe_decode_token: router -> top-k -> routed experts for one token,
+    rows split over `threads`. Returns (y, idx, weights)."""
+    rW = _c(rW, np.uint8); rS = _c(rS, np.uint16); rB = _c(rB, np.uint16)
+    pool = _c(pool, np.uint8); h = _c(h, np.float32)
+    r = None if residual is None else _c(residual, np.float32)
+    idx = np.zeros(k, np.uint32)
+    w = np.zeros(k, np.float32)
+    y = np.zeros(d, np.float32)
+    o = _offsets(off)
+    baseline_lib().tfb_moe_decode_token(_ptr(rW), _ptr(rS), _ptr(rB), rW.shape[0], _ptr(pool), int(stride),
+                                        C.byref(o), fmt, _ptr(h), _ptr(r), d, f, k, _ptr(idx), _ptr(w), _ptr(y),
+                                        int(threads))
+    return y, idx, w
