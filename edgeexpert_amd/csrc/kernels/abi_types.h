@@ -110,4 +110,13 @@ struct Tile {
     uint32_t pad_;
 };
 
+// Block split of one grouped launch (moe_prefill.hpp): the first
+// 2·max_tiles·ty blocks run the MFMA tile, the next max_tiles·sx the
+// weight stream.
+struct GroupedLaunch {
+    uint32_t max_tiles;
+    uint32_t ty;      // output blocks of the MFMA tile
+    uint32_t sx;      // row blocks of the stream
+};
+
 }  // namespace tfq

@@ -318,11 +318,11 @@ constexpr uint32_t proj_pl_lds_bytes(uint32_t K) {
 }
 
 // dst[i] = a[i] | b[i] << 16 for i < count, into LDS (16-byte loads and
-// stores when the sources are 16-byte aligned and count % 8 == 0).
-template <uint32_t NT>
+// stores when the sources are 16-byte aligned and count % 8 == 0; U loads
+// per thread and array in flight).
+template <uint32_t NT, uint32_t U = 8>
 __device__ __forceinline__ void copy_sb_to_lds(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
                                                uint32_t* __restrict__ dst, uint32_t count) {
-    constexpr uint32_t U = 8;
     if (((((uintptr_t)a) | ((uintptr_t)b)) & 15u) == 0 && (count & 7u) == 0) {
         const uint32_t n16 = count >> 3;
         const uint4* sa = reinterpret_cast<const uint4*>(a);

@@ -14,6 +14,7 @@
 
 #include "abi_types.h"
 #include "gemm.hpp"
+#include "gemm_skinny.hpp"
 #include "gemv.hpp"
 
 namespace tfq {
@@ -25,6 +26,11 @@ constexpr uint32_t kGroupThreads = 1024;
 // status codes (the PrefillMoEGroupingError cases the device can detect)
 constexpr uint32_t kGroupOk = 0;
 constexpr uint32_t kGroupExpertOutOfRange = 8;
+// grouping tiles of at most kGroupStreamMax pairs run as a weight stream
+// (moe_stream_*), larger ones on the matrix-core tile (moe_grouped_*)
+constexpr uint32_t kGroupStreamMax = 32;
+constexpr uint32_t kGroupStreamThreads = 256;  // 4 wavefronts, 64 weight rows each
+constexpr uint32_t kGroupStreamRows = 64 * (kGroupStreamThreads / 64);   // rows per block
 
 // Stable counting sort of the token-major pairs (token t, rank r) -> expert
 // idx[t*k + r], one block of 1024 threads. Pairs come out ordered by
@@ -172,7 +178,7 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
 }
 
 // The grouped GEMMs run each 128-row grouping tile as two 64-row halves
-// (blockIdx.x = 2·tile + half) on the projection tile of gemm.hpp, so an
+// (block x = 2·tile + half) on the projection tile of gemm.hpp, so an
 // expert with few rows costs one half's matrix work, not a full tile's.
 // Returns false for a half with no rows (block-uniform).
 struct GroupedRows {
@@ -182,18 +188,18 @@ struct GroupedRows {
 };
 
 __device__ __forceinline__ bool grouped_rows(const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
-                                             GroupedRows& gr) {
-    const uint32_t tile = blockIdx.x >> 1, half = blockIdx.x & 1u;
+                                             uint32_t bx, GroupedRows& gr) {
+    const uint32_t tile = bx >> 1, half = bx & 1u;
     if (tile >= *n_tiles) return false;
     const Tile t = tiles[tile];
-    if (t.count <= kProjBM * half) return false;
+    if (t.count <= kGroupStreamMax || t.count <= kProjBM * half) return false;   // small tiles: the stream
     const uint32_t left = t.count - kProjBM * half;
     gr = {t.start + kProjBM * half, left < kProjBM ? left : kProjBM, t.expert};
     return true;
 }
 
-// Grouped gate/up + GeGLU over one 64-row half tile (blockIdx.x) and 128
-// features of F (blockIdx.y): act[p][f] = fp16(gelu(gate_e[f]·x_p) · (up_e[f]·x_p))
+// Grouped gate/up + GeGLU over one 64-row half tile (block x) and 128
+// features of F (block y): act[p][f] = fp16(gelu(gate_e[f]·x_p) · (up_e[f]·x_p))
 // for sorted pairs p of the half, x_p = hidden row of the pair's token
 // (prefill.metal:598-637). Wave w takes features f0 + 32w .. +31 with the gate
 // rows as its first 32-output sub-tile and the up rows as its second, so each
@@ -206,12 +212,13 @@ __device__ __forceinline__ void moe_grouped_gate_up(const ExpertPool& pool, cons
                                                     const Tile* __restrict__ tiles,
                                                     const uint32_t* __restrict__ n_tiles,
                                                     const uint16_t* __restrict__ hidden, uint32_t stride,
-                                                    uint16_t* __restrict__ act, uint32_t D, uint32_t F) {
+                                                    uint16_t* __restrict__ act, uint32_t D, uint32_t F, uint32_t bx,
+                                                    uint32_t by) {
     GroupedRows gr;
-    if (!grouped_rows(tiles, n_tiles, gr)) return;
+    if (!grouped_rows(tiles, n_tiles, bx, gr)) return;
     extern __shared__ __attribute__((aligned(16))) _Float16 proj_lds[];
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
-    const uint32_t G = D >> 6, f0 = blockIdx.y * 128u;
+    const uint32_t G = D >> 6, f0 = by * 128u;
     const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
     const ExpertOffsets& o = pool.off;
     const uint16_t* gs = reinterpret_cast<const uint16_t*>(blob + o.gate_s);
@@ -253,21 +260,21 @@ __device__ __forceinline__ void moe_grouped_gate_up(const ExpertPool& pool, cons
     else run(std::integral_constant<int, 2>{});
 }
 
-// Grouped down projection over one 64-row half tile (blockIdx.x) and 256
-// outputs of D (blockIdx.y): partials[(token*k + rank)*D + d] = fp16(down_e[d]·act_p)
+// Grouped down projection over one 64-row half tile (block x) and 256
+// outputs of D (block y): partials[(token*k + rank)*D + d] = fp16(down_e[d]·act_p)
 // (prefill.metal:639-670). BITS as for moe_grouped_gate_up.
 template <int BITS = 4>
 __device__ __forceinline__ void moe_grouped_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
                                                  const Tile* __restrict__ tiles,
                                                  const uint32_t* __restrict__ n_tiles,
                                                  const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
-                                                 uint32_t D, uint32_t F, uint32_t k) {
+                                                 uint32_t D, uint32_t F, uint32_t k, uint32_t bx, uint32_t by) {
     GroupedRows gr;
-    if (!grouped_rows(tiles, n_tiles, gr)) return;
+    if (!grouped_rows(tiles, n_tiles, bx, gr)) return;
     extern __shared__ __attribute__((aligned(16))) _Float16 proj_lds[];
     __shared__ uint32_t dst_row[kProjBM];
     const uint32_t tid = threadIdx.x, wave = tid >> 6;
-    const uint32_t G = F >> 6, n0 = blockIdx.y * kProjBN;
+    const uint32_t G = F >> 6, n0 = by * kProjBN;
     const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
     const ExpertOffsets& o = pool.off;
     uint16_t* s_lds = reinterpret_cast<uint16_t*>(proj_lds + 2 * kProjBM * kGemmLdsStride);
@@ -294,6 +301,286 @@ __device__ __forceinline__ void moe_grouped_down(const ExpertPool& pool, const P
     };
     if (gr.count <= 32u) run(std::integral_constant<int, 1>{});
     else run(std::integral_constant<int, 2>{});
+}
+
+// ------------------------------------------- weight stream for small tiles ----
+//
+// Under a skewed popularity most experts see a handful of tokens (config 3:
+// 101 of 128 experts take at most 32 of the 4096 pairs, yet hold 80% of the
+// active weights). On the matrix-core tile such an expert costs a 64-row
+// half of MFMA work and the tile's per-group barriers for a few rows; the
+// work is a weight stream instead. A grouping tile with at most
+// kGroupStreamMax pairs is skipped by the two kernels above and run here:
+// each wavefront owns 64 weight rows (four 16-row v_mfma_f32_16x16x32_f16
+// A operands) and the whole K loop, the pairs as one or two 16-token B
+// operands (NTT), so every activation load feeds four row tiles. Lane l
+// holds row l%16 of each A operand and the quarter q = l/16 of every
+// 128-code k-tile (chunk 4m + q: one 16-byte load at 4 bits, word j feeds
+// k-step j), the B lane (pair l%16 of the sub-tile, quarter q) the matching
+// 32 activations, permuted like the unpack. The block's scales and biases
+// sit in an LDS table (one word per row and group), so the loop issues only
+// 16-byte loads. Weights are dequantised as everywhere else (fp16(q·s + b),
+// one rounding), so the result differs from the tile's only in the fp32
+// summation order. DEPTH k-tiles are in flight per wave.
+
+template <int BITS, int NTT>
+struct StreamStage {
+    QChunk<BITS> w[4];
+    uint4 x[NTT][4];
+};
+
+// acc[i][j]: 16x16 D tile of row tile i and token sub-tile j (column =
+// lane % 16 = token, rows 4·(lane/16) + r). sbt[i]: the LDS table row
+// (scale | bias << 16 per group) of this lane's row in tile i, published by
+// the barrier that `publish` runs once the first DEPTH k-tiles' loads are in
+// flight.
+template <int BITS, int NTT, typename Publish, int DEPTH = (NTT == 1 ? 3 : 2)>
+__device__ __forceinline__ void stream_rows(const uint8_t* const (&wrow)[4], const uint32_t* const (&sbt)[4],
+                                            const uint16_t* const (&xrow)[NTT], uint32_t K, f32x4 (&acc)[4][NTT],
+                                            Publish publish) {
+    const uint32_t q = (threadIdx.x & 63u) >> 4;
+    const uint32_t nch = K >> 5;                       // 32-code chunks per row
+    const uint32_t nk = (nch + 3u) >> 2;               // 128-code k-tiles
+    uint32_t magic_v;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_v));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NTT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // k-tiles past the end re-read the last chunk (and are not computed);
+    // the missing quarters of a half-filled last k-tile are masked to zero
+    auto load = [&](uint32_t m, StreamStage<BITS, NTT>& st) {
+        const uint32_t c = 4u * m + q, cc = c < nch ? c : nch - 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st.w[i] = ldg_chunk<BITS, false>(wrow[i], cc);
+#pragma unroll
+        for (int j = 0; j < NTT; ++j) {
+            const uint4* xp = reinterpret_cast<const uint4*>(xrow[j] + 32u * cc);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) st.x[j][u] = xp[u];
+        }
+    };
+    auto compute = [&](uint32_t m, const StreamStage<BITS, NTT>& st, auto mask_c) {
+        constexpr bool MASK = decltype(mask_c)::value;
+        const uint32_t c = 4u * m + q, g = (c < nch ? c : nch - 1) >> 1;
+        const uint32_t mask = MASK && c >= nch ? 0u : 0xFFFFFFFFu;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h8 a[4];
+            dequant_chunk_sb(st.w[i], sbt[i][g], magic_v, a);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const h8 ai = MASK ? mask_h8(a[u], mask) : a[u];
+#pragma unroll
+                for (int j = 0; j < NTT; ++j) {
+                    const h8 bj = perm_0415(__builtin_bit_cast(h8, st.x[j][u]));
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ai, MASK ? mask_h8(bj, mask) : bj, acc[i][j],
+                                                                       0, 0, 0);
+                }
+            }
+        }
+    };
+    // the last k-tile is masked when K is not a multiple of 128 codes
+    const uint32_t nfull = (nch & 3u) ? nk - 1 : nk;
+    StreamStage<BITS, NTT> st[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load((uint32_t)d, st[d]);
+    publish();
+    uint32_t m = 0;
+    for (; m + DEPTH <= nfull; m += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            compute(m + (uint32_t)d, st[d], std::false_type{});
+            load(m + (uint32_t)(d + DEPTH), st[d]);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+        const uint32_t mm = m + (uint32_t)d;
+        if (mm < nfull) compute(mm, st[d], std::false_type{});
+        else if (mm < nk) compute(mm, st[d], std::true_type{});
+    }
+}
+
+// Grouping tile `by` if it takes the weight stream (block-uniform).
+__device__ __forceinline__ bool stream_tile(const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
+                                            uint32_t by, Tile& t) {
+    if (by >= *n_tiles) return false;
+    t = tiles[by];
+    return t.count > 0 && t.count <= kGroupStreamMax;
+}
+
+// Dynamic LDS of the stream kernels: the scale/bias table of a block's
+// kGroupStreamRows rows (gate/up: the gate rows, then the up rows).
+constexpr uint32_t stream_lds_bytes(uint32_t K) { return 4u * kGroupStreamRows * (K / 64u); }
+
+// Gate/up + GeGLU of one small tile (block y) over kGroupStreamRows/2
+// features (block x): wave w takes features f = f_blk + 32w + (0..31),
+// its gate rows as row tiles 0, 1 and its up rows as row tiles 2, 3, so each
+// lane holds gate and up of the same (pair, feature).
+template <int BITS, int NTT>
+__device__ __forceinline__ void stream_gate_up_tile(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                                    const Tile& t, const uint16_t* __restrict__ hidden,
+                                                    uint32_t stride, uint16_t* __restrict__ act, uint32_t D,
+                                                    uint32_t F, uint32_t bx) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t stream_sb[];
+    constexpr uint32_t NF = kGroupStreamRows / 2u;                       // features per block
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t r16 = lane & 15u, q = lane >> 4;
+    const uint32_t G = D >> 6, row_bytes = (D >> 3) * BITS;
+    const uint32_t f_blk = bx * NF;
+    const uint32_t fb = f_blk + 32u * wave;
+    const uint8_t* blob = pool.base + (uint64_t)t.expert * pool.stride;
+    const ExpertOffsets& o = pool.off;
+    const uint8_t* wrow[4];
+    const uint32_t* sbt[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t f = fb + 16u * i + r16, fc = f < F ? f : F - 1;   // features past F: clamped, not stored
+        wrow[i] = blob + o.gate_w + (size_t)fc * row_bytes;
+        wrow[2 + i] = blob + o.up_w + (size_t)fc * row_bytes;
+        sbt[i] = stream_sb + (fc - f_blk) * G;
+        sbt[2 + i] = stream_sb + (NF + fc - f_blk) * G;
+    }
+    const uint16_t* xrow[NTT];
+#pragma unroll
+    for (int j = 0; j < NTT; ++j) {
+        const uint32_t p = 16u * j + r16;                                // pairs past the tile: row 0, not stored
+        xrow[j] = hidden + (size_t)sorted[t.start + (p < t.count ? p : 0u)].token * stride;
+    }
+    f32x4 acc[4][NTT];
+    stream_rows<BITS, NTT>(wrow, sbt, xrow, D, acc, [&]() {
+        const uint32_t nf = F - f_blk < NF ? F - f_blk : NF;
+        copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f_blk * G,
+                                               reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (size_t)f_blk * G,
+                                               stream_sb, nf * G);
+        copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.up_s) + (size_t)f_blk * G,
+                                               reinterpret_cast<const uint16_t*>(blob + o.up_b) + (size_t)f_blk * G,
+                                               stream_sb + NF * G, nf * G);
+        __syncthreads();
+    });
+#pragma unroll
+    for (int j = 0; j < NTT; ++j) {
+        const uint32_t p = 16u * j + r16;
+        if (p >= t.count) continue;
+        uint16_t* dst = act + (size_t)(t.start + p) * F;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t fo = fb + 16u * i + 4u * q + (uint32_t)r;
+                if (fo < F) dst[fo] = f2h(gelu_tanh(acc[i][j][r]) * acc[2 + i][j][r]);
+            }
+    }
+}
+
+// Down projection of one small tile (block y) over kGroupStreamRows
+// outputs of D (block x): wave w takes rows d = d_blk + 64w + (0..63).
+template <int BITS, int NTT>
+__device__ __forceinline__ void stream_down_tile(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                                 const Tile& t, const uint16_t* __restrict__ act,
+                                                 uint16_t* __restrict__ partials, uint32_t D, uint32_t F,
+                                                 uint32_t k, uint32_t bx) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t stream_sb[];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t r16 = lane & 15u, q = lane >> 4;
+    const uint32_t G = F >> 6, row_bytes = (F >> 3) * BITS;
+    const uint32_t d_blk = bx * kGroupStreamRows;
+    const uint32_t db = d_blk + 64u * wave;
+    const uint8_t* blob = pool.base + (uint64_t)t.expert * pool.stride;
+    const ExpertOffsets& o = pool.off;
+    const uint8_t* wrow[4];
+    const uint32_t* sbt[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t d = db + 16u * i + r16, dc = d < D ? d : D - 1;   // rows past D: clamped, not stored
+        wrow[i] = blob + o.down_w + (size_t)dc * row_bytes;
+        sbt[i] = stream_sb + (dc - d_blk) * G;
+    }
+    const uint16_t* xrow[NTT];
+#pragma unroll
+    for (int j = 0; j < NTT; ++j) {
+        const uint32_t p = 16u * j + r16;
+        xrow[j] = act + (size_t)(t.start + (p < t.count ? p : 0u)) * F;
+    }
+    f32x4 acc[4][NTT];
+    stream_rows<BITS, NTT>(wrow, sbt, xrow, F, acc, [&]() {
+        const uint32_t nd = D - d_blk < kGroupStreamRows ? D - d_blk : kGroupStreamRows;
+        copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)d_blk * G,
+                                               reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)d_blk * G,
+                                               stream_sb, nd * G);
+        __syncthreads();
+    });
+#pragma unroll
+    for (int j = 0; j < NTT; ++j) {
+        const uint32_t p = 16u * j + r16;
+        if (p >= t.count) continue;
+        const Pair pr = sorted[t.start + p];
+        uint16_t* dst = partials + (size_t)(pr.token * k + pr.rank) * D;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t d = db + 16u * i + 4u * q + (uint32_t)r;
+                if (d < D) dst[d] = f2h(acc[i][j][r]);
+            }
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ void moe_stream_gate_up(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                                   const Tile* __restrict__ tiles,
+                                                   const uint32_t* __restrict__ n_tiles,
+                                                   const uint16_t* __restrict__ hidden, uint32_t stride,
+                                                   uint16_t* __restrict__ act, uint32_t D, uint32_t F, uint32_t bx,
+                                                   uint32_t by) {
+    Tile t;
+    if (!stream_tile(tiles, n_tiles, by, t)) return;
+    if (t.count <= 16u) stream_gate_up_tile<BITS, 1>(pool, sorted, t, hidden, stride, act, D, F, bx);
+    else stream_gate_up_tile<BITS, 2>(pool, sorted, t, hidden, stride, act, D, F, bx);
+}
+
+template <int BITS>
+__device__ __forceinline__ void moe_stream_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                                const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
+                                                const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
+                                                uint32_t D, uint32_t F, uint32_t k, uint32_t bx, uint32_t by) {
+    Tile t;
+    if (!stream_tile(tiles, n_tiles, by, t)) return;
+    if (t.count <= 16u) stream_down_tile<BITS, 1>(pool, sorted, t, act, partials, D, F, k, bx);
+    else stream_down_tile<BITS, 2>(pool, sorted, t, act, partials, D, F, k, bx);
+}
+
+// One launch per projection runs both: blocks 0 .. 2·max_tiles·ty - 1 are
+// the MFMA tile's (x = b mod 2·max_tiles, y = b / 2·max_tiles; ty blocks of
+// outputs), the rest the stream's (x = b' mod sx, y = b' / sx; sx blocks of
+// rows). The tile blocks come first: they run longest, and the stream's fill
+// the CUs around them (GroupedLaunch, abi_types.h).
+static_assert(kGroupStreamThreads == kProjThreads, "one launch runs both roles");
+
+template <int BITS>
+__device__ __forceinline__ void moe_grouped_gate_up_launch(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                                           const Tile* __restrict__ tiles,
+                                                           const uint32_t* __restrict__ n_tiles,
+                                                           const uint16_t* __restrict__ hidden, uint32_t stride,
+                                                           uint16_t* __restrict__ act, uint32_t D, uint32_t F,
+                                                           GroupedLaunch gl) {
+    const uint32_t b = blockIdx.x, tx = 2u * gl.max_tiles;
+    if (b < tx * gl.ty) moe_grouped_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, b % tx, b / tx);
+    else moe_stream_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, (b - tx * gl.ty) % gl.sx,
+                                  (b - tx * gl.ty) / gl.sx);
+}
+
+template <int BITS>
+__device__ __forceinline__ void moe_grouped_down_launch(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                                        const Tile* __restrict__ tiles,
+                                                        const uint32_t* __restrict__ n_tiles,
+                                                        const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
+                                                        uint32_t D, uint32_t F, uint32_t k, GroupedLaunch gl) {
+    const uint32_t b = blockIdx.x, tx = 2u * gl.max_tiles;
+    if (b < tx * gl.ty) moe_grouped_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, b % tx, b / tx);
+    else moe_stream_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, (b - tx * gl.ty) % gl.sx,
+                               (b - tx * gl.ty) / gl.sx);
 }
 
 // h2[t][d] = fp16(Σ_r fma(w[t][r], partials[(t*k+r)*D + d])) in rank order

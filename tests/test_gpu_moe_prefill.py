@@ -211,6 +211,41 @@ def test_grouped_moe_baseline_config3_sampled(ctx, stream):
     assert rel < TOL, f"h2 rel={rel}"
 
 
+@pytest.mark.parametrize("bits", [4, 3])
+def test_grouped_tile_and_stream_split(ctx, stream, bits):
+    # experts whose grouping tiles fall on both sides of the stream cut (32
+    # pairs): 1, 16, 17, 32 pairs (the weight stream, one and two 16-pair
+    # sub-tiles), 33, 72, 100 (the MFMA tile), 129 (a full tile plus a
+    # one-pair tile on the stream). f = 192 leaves a partial block of
+    # features (gate/up) and a half-filled last 128-code k-tile (down); every
+    # pair is checked against the oracle.
+    d, f, k, E = 256, 192, 2, 8
+    counts = [129, 33, 32, 17, 16, 1, 72, 100]
+    T = sum(counts) // k
+    order = np.repeat(np.arange(E, dtype=np.uint32), counts)
+    idx = np.stack([order[:T], order[T:]], axis=1)
+    assert np.all(idx[:, 0] != idx[:, 1])
+    w16 = synth.f16_bits(synth.uniform24(synth.seed_key(9, "split/w"), T * k, 0.1, 0.9)).reshape(T, k)
+    pool_bytes, offs, stride = synth.expert_pool(9, f"split/b{bits}", E, d, f, bits=bits)
+    hidden = synth.f16_vector(9, "split/x", T * d)
+    got, bufs = _device_group(ctx, stream, idx, w16, T, k, E)
+    assert got["status"] == 0
+    pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs, weight_bits=bits)
+    act = _dev(np.zeros(T * k * f, np.uint16))
+    partials = _dev(np.full(T * k * d, np.float16(-77).view(np.uint16), np.uint16))
+    ops.PrefillGroupedRoutedMoE(ctx).encode(stream, pool, bufs["sorted"], bufs["tiles"], bufs["n_tiles"],
+                                            ops.max_tiles(T, k, E), _dev(hidden), d, d, f, k, act, partials)
+    stream.sync()
+    ref = oracle.grouped_route_partials(got["sorted"].astype(oracle.PAIR_DTYPE), hidden, d,
+                                        *_oracle_pool(pool_bytes, offs, stride), k, d, f, T, bits=bits)
+    gp, rp = from_f16_bits(partials.download(np.uint16)).reshape(T * k, d), from_f16_bits(ref).reshape(T * k, d)
+    for e, c in enumerate(counts):
+        rows = [int(p["token"]) * k + int(p["rank"]) for p in got["sorted"] if p["expert"] == e]
+        assert len(rows) == c
+        rel = oracle.rel_error(gp[rows], rp[rows])
+        assert rel < TOL, f"expert {e} ({c} pairs): rel={rel}"
+
+
 def test_moe_prefill_end_to_end(ctx, stream):
     # router -> grouping -> grouped experts -> combine through one call
     T, k, E, d, f = 64, 8, 32, 512, 256
