@@ -47,10 +47,15 @@ inline int check_stage(const NormArg& na) {
         return TFQ_OK;
     case kStageNorm:
         break;
+    case kStageScaled:
+        if (!na.inv) return fail(TFQ_E_INVAL, "scaled staging needs the exported r(h)");
+        return TFQ_OK;
     case kStagePostAttn:
     case kStageResidual:
         if (!na.attn || !na.attn_w)
             return fail(TFQ_E_INVAL, "post-attention staging needs the attention output and its norm weight");
+        if (na.export_h && (na.mode != kStagePostAttn || !na.export_inv))
+            return fail(TFQ_E_INVAL, "exporting h needs post-attention staging and a place for r(h)");
         break;
     default:
         return fail(TFQ_E_INVAL, "unknown staging mode %u", na.mode);
@@ -59,7 +64,7 @@ inline int check_stage(const NormArg& na) {
     return TFQ_OK;
 }
 
-inline NormArg stage_copy() { return NormArg{nullptr, nullptr, nullptr, 0.0f, kStageCopy}; }
+inline NormArg stage_copy() { return NormArg{nullptr, nullptr, nullptr, 0.0f, kStageCopy, nullptr, nullptr, nullptr}; }
 
 // Kernel-name infix of the GEMV-family form that stages x as `na` says:
 // "" for a plain copy, "norm_" for the forms that normalise while staging.
@@ -861,7 +866,7 @@ public:
     }
 
     struct Layout {
-        size_t q, attn, parts, parts_bytes, o, logits, idx, w, acts, sact, h1, h2, total;
+        size_t q, attn, parts, parts_bytes, o, logits, idx, w, acts, sact, h1, h2, hmid, inv, total;
     };
     static Layout layout(const tfq_decode_layer_shape& s, uint32_t max_seq) {
         auto up = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -880,6 +885,8 @@ public:
         L.sact = off;   off += up((size_t)s.shared_f * 2);
         L.h1 = off;     off += up((size_t)s.d * 2);
         L.h2 = off;     off += up((size_t)s.d * 2);
+        L.hmid = off;   off += up((size_t)s.d * 2);
+        L.inv = off;    off += up(4);
         L.total = off;
         return L;
     }
@@ -919,6 +926,8 @@ public:
         uint16_t* sact = reinterpret_cast<uint16_t*>(ws + L.sact);
         uint16_t* h1 = reinterpret_cast<uint16_t*>(ws + L.h1);
         uint16_t* h2 = reinterpret_cast<uint16_t*>(ws + L.h2);
+        uint16_t* hmid = reinterpret_cast<uint16_t*>(ws + L.hmid);
+        float* hinv = reinterpret_cast<float*>(ws + L.inv);
         const uint32_t qd = s.num_q_heads * s.head_dim, kvd = s.num_kv_heads * s.head_dim;
         const size_t slot = (size_t)position * kvd;
 
@@ -948,8 +957,9 @@ public:
         if (rc) return rc;
         rc = hip_check(hipEventRecord(join_, side_), "hipEventRecord");
         if (rc) return rc;
-        // 5. router on the no-scale norm of h
-        const NormArg router_x{nullptr, o, w.post_attention_norm, s.eps, kStagePostAttn};
+        // 5. router on the no-scale norm of h; its block 0 also stores h and
+        //    r(h), so the routed experts form their input without the reductions
+        const NormArg router_x{nullptr, o, w.post_attention_norm, s.eps, kStagePostAttn, nullptr, hmid, hinv};
         const tfq_router& r = w.router;
         float* logits_used = nullptr;
         rc = moe_.encode_router_logits(stream, r.weights, r.scales, r.biases, hidden_in, r.effective_scale,
@@ -957,9 +967,9 @@ public:
         if (rc) return rc;
         // 6. routed experts on pre_feedforward_layernorm_2(h), the top-k selected inside
         //    phase 1; phase 2 without residual
-        const NormArg routed{w.pre_ffn2_norm, o, w.post_attention_norm, s.eps, kStagePostAttn};
+        const NormArg routed{w.pre_ffn2_norm, nullptr, nullptr, s.eps, kStageScaled, hinv, nullptr, nullptr};
         rc = moe_.encode_phase1_routed(stream, w.experts, logits, r.per_expert_scale, r.num_experts, idx, rw,
-                                       nullptr, hidden_in, acts, s.d, s.expert_f, s.top_k, routed);
+                                       nullptr, hmid, acts, s.d, s.expert_f, s.top_k, routed);
         if (rc) return rc;
         rc = moe_.encode_phase2(stream, w.experts, idx, acts, rw, nullptr, h2, s.d, s.expert_f, s.top_k);
         if (rc) return rc;

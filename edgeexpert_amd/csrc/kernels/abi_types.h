@@ -33,9 +33,15 @@ struct Q8Mat {
 //   kStagePostAttn  h = fp16(x + fp16(attn * attn_w * r(attn)));
 //                   a = fp16(h * w * r(h))                (w == null: no scale)
 // kStagePostAttn is the decode layer's post-attention residual + pre-FFN (or
-// router) norm, recomputed by every block that consumes it.
+// router) norm, recomputed by every block that consumes it. With export_h
+// set, block 0 of the launch also stores h (fp16) to export_h and r(h)
+// (fp32) to *export_inv, so a later kernel can form a = fp16(h * w * r(h))
+// for another w without the reductions:
 //   kStageResidual  a = h (the post-attention residual stream, no norm)
-enum StageMode : uint32_t { kStageCopy = 0, kStageNorm = 1, kStagePostAttn = 2, kStageResidual = 3 };
+//   kStageScaled    a = fp16(x * w * inv[0])              (w == null: no scale;
+//                   x = an exported h, inv its exported r(h))
+enum StageMode : uint32_t { kStageCopy = 0, kStageNorm = 1, kStagePostAttn = 2, kStageResidual = 3,
+                            kStageScaled = 4 };
 
 struct NormArg {
     const uint16_t* w;
@@ -43,6 +49,9 @@ struct NormArg {
     const uint16_t* attn_w;
     float eps;
     uint32_t mode;
+    const float* inv;          // kStageScaled: r(h)
+    uint16_t* export_h;        // kStagePostAttn: h and r(h) from block 0 (nullable)
+    float* export_inv;
 };
 
 // Dynamic LDS of the int4 GEMV-family kernels for an activation vector of n

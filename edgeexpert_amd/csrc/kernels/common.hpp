@@ -410,6 +410,15 @@ __device__ __forceinline__ void stage_act_scalar(const uint16_t* __restrict__ x,
                                                  uint32_t n, const NormArg& na) {
     copy_to_lds<NT>(x, lds, n);
     __syncthreads();
+    if (na.mode == kStageScaled) {
+        const float inv = *na.inv;
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            const float xw = na.w ? h2f(lds[i]) * h2f(na.w[i]) : h2f(lds[i]);
+            lds[i] = f2h(xw * inv);
+        }
+        __syncthreads();
+        return;
+    }
     if (na.mode == kStagePostAttn || na.mode == kStageResidual) {
         float ss = 0.0f;
         for (uint32_t i = threadIdx.x; i < n; i += NT) {
@@ -422,6 +431,20 @@ __device__ __forceinline__ void stage_act_scalar(const uint16_t* __restrict__ x,
             lds[i] = f2h(h2f(lds[i]) + h2f(an));
         }
         __syncthreads();
+    }
+    if (na.mode == kStagePostAttn && na.export_h) {
+        // h and r(h) for later kernels (kStageScaled), then the norm with that r(h)
+        const float inv = lds_inv_rms<NT>(lds, n, na.eps);
+        if (blockIdx.x == 0) {
+            for (uint32_t i = threadIdx.x; i < n; i += NT) na.export_h[i] = lds[i];
+            if (threadIdx.x == 0) *na.export_inv = inv;
+        }
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            const float xw = na.w ? h2f(lds[i]) * h2f(na.w[i]) : h2f(lds[i]);
+            lds[i] = f2h(xw * inv);
+        }
+        __syncthreads();
+        return;
     }
     if (na.mode == kStageNorm || na.mode == kStagePostAttn) rmsnorm_lds<NT>(lds, n, na.w, na.eps);
 }
@@ -447,15 +470,18 @@ __device__ __forceinline__ uint4 ld16h(const uint16_t* p, uint32_t chunk) {
 template <uint32_t NT, uint32_t CH, bool NORM = true>
 struct XStage {
     h8 xv[CH], av[CH], awv[CH], wv[CH];
+    float inv_in;      // kStageScaled: r(h), loaded with the chunks
     bool vec;
 
     __device__ __forceinline__ void load(const uint16_t* __restrict__ x, uint32_t n, const NormArg& na) {
         const uint32_t nch = n >> 3;
-        const uintptr_t align = (uintptr_t)x | (uintptr_t)na.w | (uintptr_t)na.attn | (uintptr_t)na.attn_w;
+        const uintptr_t align =
+            (uintptr_t)x | (uintptr_t)na.w | (uintptr_t)na.attn | (uintptr_t)na.attn_w | (uintptr_t)na.export_h;
         vec = ((NORM ? align : (uintptr_t)x) & 15u) == 0 && (n & 7u) == 0 && nch != 0 && nch <= CH * NT;
         if (!vec) return;
         const bool post = NORM && (na.mode == kStagePostAttn || na.mode == kStageResidual);
-        const bool norm = NORM && (na.mode == kStageNorm || na.mode == kStagePostAttn);
+        const bool norm = NORM && (na.mode == kStageNorm || na.mode == kStagePostAttn || na.mode == kStageScaled);
+        if (NORM && na.mode == kStageScaled) inv_in = *na.inv;
         // clamped chunk indices: every load is valid and unconditional (chunks
         // past the end are loaded twice and never stored or counted)
 #pragma unroll
@@ -477,6 +503,16 @@ struct XStage {
         const uint32_t nch = n >> 3;
         const bool post = na.mode == kStagePostAttn || na.mode == kStageResidual;
         const bool norm = na.mode == kStageNorm || na.mode == kStagePostAttn;
+        if (na.mode == kStageScaled) {
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float xw = na.w ? (float)xv[i][e] * (float)wv[i][e] : (float)xv[i][e];
+                    xv[i][e] = (_Float16)(xw * inv_in);
+                }
+            return;
+        }
         if (post) {
             float ss = 0.0f;
 #pragma unroll
@@ -501,6 +537,13 @@ struct XStage {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) ss = fmaf((float)xv[i][e], (float)xv[i][e], ss);
             const float inv = 1.0f / sqrtf(block_sum<NT>(ss) / (float)n + na.eps);
+            if (post && na.export_h && blockIdx.x == 0) {
+#pragma unroll
+                for (uint32_t i = 0; i < CH; ++i)
+                    if (threadIdx.x + i * NT < nch)
+                        reinterpret_cast<h8*>(na.export_h)[threadIdx.x + i * NT] = xv[i];
+                if (threadIdx.x == 0) *na.export_inv = inv;
+            }
 #pragma unroll
             for (uint32_t i = 0; i < CH; ++i)
 #pragma unroll

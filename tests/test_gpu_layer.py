@@ -95,7 +95,7 @@ def _layout(shape, seq):
              ("parts", ops.Attention.workspace_bytes(shape["hd"], shape["nq"], seq, shape["window"])),
              ("o", shape["d"] * 2), ("logits", 4096), ("idx", shape["k"] * 4), ("w", shape["k"] * 2),
              ("acts", shape["k"] * shape["f"] * 2), ("sact", shape["fs"] * 2), ("h1", shape["d"] * 2),
-             ("h2", shape["d"] * 2)]
+             ("h2", shape["d"] * 2), ("hmid", shape["d"] * 2), ("inv", 4)]
     off, L = 0, {}
     for n, sz in sizes:
         L[n] = off
