@@ -851,9 +851,11 @@ private:
 // One Gemma 4 decoder layer for one token (RealForwardRunner.swift:2265-2862):
 // input norm + QKV, q/k/v epilogue + attention, o projection, post-attention
 // setup, router, shared expert (on a second stream), routed experts, tail.
-// The norms that the reference runs as separate kernels are recomputed while
-// each consumer stages its activation vector (NormArg), so the layer is nine
-// launches on `stream` and two on the side stream.
+// The norms that the reference runs as separate kernels are formed while
+// each consumer stages its activation vector (NormArg); the router also
+// stores the post-attention h and r(h), from which the routed experts form
+// their input without the reductions. Eight launches on `stream`, two on the
+// side stream.
 class DecodeLayer {
 public:
     DecodeLayer(const Module& m, DequantInt4GEMV& gemv, MoE& moe, SharedExpertInt4& shared,
