@@ -120,8 +120,8 @@ struct Tile {
 };
 
 // Block split of one grouped launch (moe_prefill.hpp): the first
-// 2·max_tiles·ty blocks run the MFMA tile, the next max_tiles·sx the
-// weight stream.
+// max_tiles·sx blocks run the weight stream, the next 2·max_tiles·ty the
+// MFMA tile.
 struct GroupedLaunch {
     uint32_t max_tiles;
     uint32_t ty;      // output blocks of the MFMA tile

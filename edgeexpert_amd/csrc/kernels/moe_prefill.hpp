@@ -551,11 +551,11 @@ __device__ __forceinline__ void moe_stream_down(const ExpertPool& pool, const Pa
     else stream_down_tile<BITS, 2>(pool, sorted, t, act, partials, D, F, k, bx);
 }
 
-// One launch per projection runs both: blocks 0 .. 2·max_tiles·ty - 1 are
-// the MFMA tile's (x = b mod 2·max_tiles, y = b / 2·max_tiles; ty blocks of
-// outputs), the rest the stream's (x = b' mod sx, y = b' / sx; sx blocks of
-// rows). The tile blocks come first: they run longest, and the stream's fill
-// the CUs around them (GroupedLaunch, abi_types.h).
+// One launch per projection runs both, so the stream's weight reads overlap
+// the tile's matrix work: blocks 0 .. max_tiles·sx - 1 are the stream's
+// (x = b mod sx, y = b / sx; sx blocks of rows), the rest the MFMA tile's
+// (x = b' mod 2·max_tiles, y = b' / 2·max_tiles; ty blocks of outputs)
+// (GroupedLaunch, abi_types.h). Either order measures the same on config 3.
 static_assert(kGroupStreamThreads == kProjThreads, "one launch runs both roles");
 
 template <int BITS>
@@ -565,10 +565,9 @@ __device__ __forceinline__ void moe_grouped_gate_up_launch(const ExpertPool& poo
                                                            const uint16_t* __restrict__ hidden, uint32_t stride,
                                                            uint16_t* __restrict__ act, uint32_t D, uint32_t F,
                                                            GroupedLaunch gl) {
-    const uint32_t b = blockIdx.x, tx = 2u * gl.max_tiles;
-    if (b < tx * gl.ty) moe_grouped_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, b % tx, b / tx);
-    else moe_stream_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, (b - tx * gl.ty) % gl.sx,
-                                  (b - tx * gl.ty) / gl.sx);
+    const uint32_t b = blockIdx.x, tx = 2u * gl.max_tiles, ns = gl.max_tiles * gl.sx;
+    if (b < ns) moe_stream_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, b % gl.sx, b / gl.sx);
+    else moe_grouped_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, (b - ns) % tx, (b - ns) / tx);
 }
 
 template <int BITS>
@@ -577,10 +576,9 @@ __device__ __forceinline__ void moe_grouped_down_launch(const ExpertPool& pool, 
                                                         const uint32_t* __restrict__ n_tiles,
                                                         const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
                                                         uint32_t D, uint32_t F, uint32_t k, GroupedLaunch gl) {
-    const uint32_t b = blockIdx.x, tx = 2u * gl.max_tiles;
-    if (b < tx * gl.ty) moe_grouped_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, b % tx, b / tx);
-    else moe_stream_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, (b - tx * gl.ty) % gl.sx,
-                               (b - tx * gl.ty) / gl.sx);
+    const uint32_t b = blockIdx.x, tx = 2u * gl.max_tiles, ns = gl.max_tiles * gl.sx;
+    if (b < ns) moe_stream_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, b % gl.sx, b / gl.sx);
+    else moe_grouped_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, (b - ns) % tx, (b - ns) / tx);
 }
 
 // h2[t][d] = fp16(Σ_r fma(w[t][r], partials[(t*k+r)*D + d])) in rank order
