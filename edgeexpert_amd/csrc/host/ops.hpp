@@ -21,6 +21,8 @@ constexpr uint32_t kProjGemmThreads = 512; // threads of the prefill GEMM's tile
 constexpr uint32_t kProjMaxK = 8192;       // longest reduction (gemm.hpp kProjMaxK)
 constexpr uint32_t kGroupStreamThreads = 256;   // grouped weight stream (moe_prefill.hpp)
 constexpr uint32_t kGroupStreamRows = 256;      // its weight rows per block
+constexpr uint32_t kGroupWideRows = 128;        // grouped wide role: weight rows per block (moe_prefill.hpp)
+constexpr uint32_t kWideBufHalves = 64 * (128 + 8);   // its activation buffer (two of them)
 constexpr uint32_t proj_lds_bytes(uint32_t k) { return 2u * kProjBM * 72u * 2u + 2u * kProjBN * (k / 64u) * 2u; }
 // the pipelined tile of the prefill GEMM (gemm.hpp proj_pl_lds_bytes)
 constexpr uint32_t proj_pl_lds_bytes(uint32_t k) { return 3u * kProjBM * 72u * 2u + 4u * kProjBN * (k / 64u); }
@@ -748,25 +750,28 @@ public:
             return fail(TFQ_E_UNSUPPORTED, "d=%u and f=%u must be at most %u", d, f, kProjMaxK);
         if (max_tiles == 0) return TFQ_OK;
         ExpertPool kp = kernel_pool(pool);
-        // one launch per projection: grouping tiles of more than
-        // kGroupStreamMax pairs as two 64-row halves on the MFMA tile
-        // (gate/up: 128 features per block, down: 256 outputs per block),
-        // smaller ones as a weight stream (128 features / 256 outputs per
-        // block); each role skips the other's tiles
+        // one launch per projection: grouping tiles of at most kGroupStreamMax
+        // pairs as a weight stream (128 features / 256 outputs per block),
+        // larger ones as 64-pair halves on the wide role (64 features / 128
+        // outputs per block); each role skips the other's tiles
         const uint32_t bits = pool_bits(pool);
         const char* gu = bits == 2 ? "tfq_moe_grouped_gate_up_b2" : bits == 3 ? "tfq_moe_grouped_gate_up_b3"
                                                                            : "tfq_moe_grouped_gate_up";
         const char* dn = bits == 2 ? "tfq_moe_grouped_down_b2" : bits == 3 ? "tfq_moe_grouped_down_b3"
                                                                         : "tfq_moe_grouped_down";
-        GroupedLaunch g1{max_tiles, (f + 127) / 128, (f + kGroupStreamRows / 2 - 1) / (kGroupStreamRows / 2)};
+        auto lds_for = [](uint32_t K) {
+            return std::max(4u * kGroupStreamRows * (K / 64u), 2u * kWideBufHalves * 2u + 4u * kGroupWideRows * (K / 64u));
+        };
+        GroupedLaunch g1{max_tiles, (f + kGroupWideRows / 2 - 1) / (kGroupWideRows / 2),
+                         (f + kGroupStreamRows / 2 - 1) / (kGroupStreamRows / 2)};
         void* a1[] = {&kp, &sorted, &tiles, &n_tiles, &hidden, &stride, &act, &d, &f, &g1};
-        const uint32_t lds1 = std::max(proj_lds_bytes(d), 4u * kGroupStreamRows * (d / 64u));
-        rc = launch2(m_, gu, 2 * max_tiles * g1.ty + max_tiles * g1.sx, 1, kProjThreads, lds1, stream, a1);
+        rc = launch2(m_, gu, max_tiles * g1.sx + 2 * max_tiles * g1.wx, 1, kGroupStreamThreads, lds_for(d), stream, a1);
         if (rc) return rc;
-        GroupedLaunch g2{max_tiles, (d + kProjBN - 1) / kProjBN, (d + kGroupStreamRows - 1) / kGroupStreamRows};
+        GroupedLaunch g2{max_tiles, (d + kGroupWideRows - 1) / kGroupWideRows,
+                         (d + kGroupStreamRows - 1) / kGroupStreamRows};
         void* a2[] = {&kp, &sorted, &tiles, &n_tiles, &act, &partials, &d, &f, &k, &g2};
-        const uint32_t lds2 = std::max(proj_lds_bytes(f), 4u * kGroupStreamRows * (f / 64u));
-        return launch2(m_, dn, 2 * max_tiles * g2.ty + max_tiles * g2.sx, 1, kProjThreads, lds2, stream, a2);
+        return launch2(m_, dn, max_tiles * g2.sx + 2 * max_tiles * g2.wx, 1, kGroupStreamThreads, lds_for(f), stream,
+                       a2);
     }
 
     // PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38).

@@ -120,11 +120,11 @@ struct Tile {
 };
 
 // Block split of one grouped launch (moe_prefill.hpp): the first
-// max_tiles·sx blocks run the weight stream, the next 2·max_tiles·ty the
-// MFMA tile.
+// max_tiles·sx blocks run the weight stream (small tiles), the next
+// 2·max_tiles·wx the wide role (halves of the large tiles).
 struct GroupedLaunch {
     uint32_t max_tiles;
-    uint32_t ty;      // output blocks of the MFMA tile
+    uint32_t wx;      // row blocks of the wide role
     uint32_t sx;      // row blocks of the stream
 };
 

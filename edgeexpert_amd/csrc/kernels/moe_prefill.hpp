@@ -32,6 +32,21 @@ constexpr uint32_t kGroupStreamMax = 32;
 constexpr uint32_t kGroupStreamThreads = 256;  // 4 wavefronts, 64 weight rows each
 constexpr uint32_t kGroupStreamRows = 64 * (kGroupStreamThreads / 64);   // rows per block
 
+// dst[n + e] = fp16(v[e]) for e < 4 and n + e < lim: one 8-byte store when
+// all four are in range and dst + n is 8-byte aligned, else per element.
+__device__ __forceinline__ void store_f16x4(uint16_t* __restrict__ dst, uint32_t n, uint32_t lim, const float (&v)[4]) {
+    const uint16_t o0 = f2h(v[0]), o1 = f2h(v[1]), o2 = f2h(v[2]), o3 = f2h(v[3]);
+    if (n + 3 < lim && ((reinterpret_cast<uintptr_t>(dst + n) & 7u) == 0)) {
+        *reinterpret_cast<uint2*>(dst + n) =
+            make_uint2((uint32_t)o0 | ((uint32_t)o1 << 16), (uint32_t)o2 | ((uint32_t)o3 << 16));
+    } else {
+        const uint16_t o[4] = {o0, o1, o2, o3};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (n + e < lim) dst[n + e] = o[e];
+    }
+}
+
 // Stable counting sort of the token-major pairs (token t, rank r) -> expert
 // idx[t*k + r], one block of 1024 threads. Pairs come out ordered by
 // (expert, token, rank) exactly as the reference's sort
@@ -465,12 +480,12 @@ __device__ __forceinline__ void stream_gate_up_tile(const ExpertPool& pool, cons
         if (p >= t.count) continue;
         uint16_t* dst = act + (size_t)(t.start + p) * F;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i) {
+            float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t fo = fb + 16u * i + 4u * q + (uint32_t)r;
-                if (fo < F) dst[fo] = f2h(gelu_tanh(acc[i][j][r]) * acc[2 + i][j][r]);
-            }
+            for (int r = 0; r < 4; ++r) v[r] = gelu_tanh(acc[i][j][r]) * acc[2 + i][j][r];
+            store_f16x4(dst, fb + 16u * i + 4u * q, F, v);
+        }
     }
 }
 
@@ -498,10 +513,13 @@ __device__ __forceinline__ void stream_down_tile(const ExpertPool& pool, const P
         sbt[i] = stream_sb + (dc - d_blk) * G;
     }
     const uint16_t* xrow[NTT];
+    uint32_t dst_row[NTT];          // partials row of each pair, loaded before the K loop
 #pragma unroll
     for (int j = 0; j < NTT; ++j) {
-        const uint32_t p = 16u * j + r16;
-        xrow[j] = act + (size_t)(t.start + (p < t.count ? p : 0u)) * F;
+        const uint32_t p = 16u * j + r16, pc = p < t.count ? p : 0u;
+        xrow[j] = act + (size_t)(t.start + pc) * F;
+        const Pair pr = sorted[t.start + pc];
+        dst_row[j] = pr.token * k + pr.rank;
     }
     f32x4 acc[4][NTT];
     stream_rows<BITS, NTT>(wrow, sbt, xrow, F, acc, [&]() {
@@ -515,15 +533,12 @@ __device__ __forceinline__ void stream_down_tile(const ExpertPool& pool, const P
     for (int j = 0; j < NTT; ++j) {
         const uint32_t p = 16u * j + r16;
         if (p >= t.count) continue;
-        const Pair pr = sorted[t.start + p];
-        uint16_t* dst = partials + (size_t)(pr.token * k + pr.rank) * D;
+        uint16_t* dst = partials + (size_t)dst_row[j] * D;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t d = db + 16u * i + 4u * q + (uint32_t)r;
-                if (d < D) dst[d] = f2h(acc[i][j][r]);
-            }
+        for (int i = 0; i < 4; ++i) {
+            const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            store_f16x4(dst, db + 16u * i + 4u * q, D, v);
+        }
     }
 }
 
@@ -551,6 +566,269 @@ __device__ __forceinline__ void moe_stream_down(const ExpertPool& pool, const Pa
     else stream_down_tile<BITS, 2>(pool, sorted, t, act, partials, D, F, k, bx);
 }
 
+// ----------------------------------------------- wide role for large tiles ----
+//
+// A grouping tile of more than kGroupStreamMax pairs runs as 64-pair halves
+// (block y = 2·tile + half), each block over kGroupWideRows weight rows
+// (block x): gate/up 64 features (gate and up rows), down 128 outputs. Wave
+// w owns 32 rows as two 16-row A operands of v_mfma_f32_16x16x32_f16 (lane
+// l: row l%16, the quarter q = l/16 of every 128-code k-tile, chunk 4m + q
+// from a DEPTH-deep register ring, dequantised exactly as in the stream);
+// the half's activations (NTT 16-pair sub-tiles) are staged per k-tile into
+// a double-buffered LDS tile [64 pairs][128 codes + 8] in the unpack order,
+// from a two-deep register ring, one barrier per k-tile; the B lane (pair
+// l%16 of sub-tile j, quarter q) reads its 16 bytes of k-step u at column
+// 32q + 8u. Codes past K (a half-filled last k-tile) are zero in both
+// operands. Per k-tile a wave issues 8·NTT MFMAs and dequantises 64 codes
+// per lane.
+template <int B, int E, typename Fn>
+__device__ __forceinline__ void sfor_w(Fn&& f) {             // f(integral_constant<B>) ... f(<E-1>)
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        sfor_w<B + 1, E>(f);
+    }
+}
+
+constexpr uint32_t kGroupWideRows = 128;                  // weight rows per block (4 waves x 32)
+constexpr uint32_t kGroupWidePairs = 64;                  // pairs per block (a half tile)
+constexpr uint32_t kWideStride = 128 + 8;                 // halves per LDS activation row
+constexpr uint32_t kWideBuf = kGroupWidePairs * kWideStride;   // halves per activation buffer
+// Dynamic LDS of the wide role: two activation buffers, then the scale/bias
+// table of the block's rows.
+constexpr uint32_t wide_lds_bytes(uint32_t K) { return 2u * kWideBuf * 2u + 4u * kGroupWideRows * (K / 64u); }
+
+// Rows of half `by` of a large tile (false: nothing to do; block-uniform).
+__device__ __forceinline__ bool wide_rows(const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
+                                          uint32_t by, GroupedRows& gr) {
+    const uint32_t tile = by >> 1, half = by & 1u;
+    if (tile >= *n_tiles) return false;
+    const Tile t = tiles[tile];
+    if (t.count <= kGroupStreamMax || t.count <= kGroupWidePairs * half) return false;
+    const uint32_t left = t.count - kGroupWidePairs * half;
+    gr = {t.start + kGroupWidePairs * half, left < kGroupWidePairs ? left : kGroupWidePairs, t.expert};
+    return true;
+}
+
+// acc[i][j]: row tile i, pair sub-tile j (16x16 D layout). xrow(p): the
+// activation row of pair p (< NTT·16; past the half's count: any valid row,
+// not stored). sbt[i]: this lane's row of the scale/bias table.
+template <int BITS, int NTT, typename XRow, typename Publish, int DEPTH = 3>
+__device__ __forceinline__ void wide_rows_loop(const uint8_t* const (&wrow)[2], const uint32_t* const (&sbt)[2],
+                                               XRow xrow, uint32_t K, _Float16* __restrict__ xs,
+                                               f32x4 (&acc)[2][NTT], Publish publish) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, q = lane >> 4, r16 = lane & 15u;
+    const uint32_t nch = K >> 5, nk = (nch + 3u) >> 2;
+    constexpr uint32_t NP = NTT * 16u;                     // staged pairs
+    constexpr uint32_t PIECES = NP * 16u / kGroupStreamThreads;   // 16-byte activation pieces per thread
+    uint32_t magic_v;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_v));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NTT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // activation piece p of this thread: pair (p·256 + tid) / 16, 16-byte column (tid % 16)
+    const uint16_t* xr_row[PIECES];
+#pragma unroll
+    for (uint32_t p = 0; p < PIECES; ++p) xr_row[p] = xrow((p * kGroupStreamThreads + tid) >> 4);
+    const uint32_t xcol = tid & 15u;
+    QChunk<BITS> wr[DEPTH][2];
+    uint4 xr[2][PIECES];
+    auto load_w = [&](uint32_t m, QChunk<BITS> (&dst)[2]) {
+        const uint32_t c = 4u * m + q, cc = c < nch ? c : nch - 1;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dst[i] = ldg_chunk<BITS, false>(wrow[i], cc);
+    };
+    // columns past K load a valid piece and are stored as zeros
+    auto load_x = [&](uint32_t m, uint4 (&dst)[PIECES]) {
+        const uint32_t col = 128u * (m < nk ? m : nk - 1) + 8u * xcol;
+        const uint32_t cc = col < K ? col : 0u;
+#pragma unroll
+        for (uint32_t p = 0; p < PIECES; ++p) dst[p] = *reinterpret_cast<const uint4*>(xr_row[p] + cc);
+    };
+    auto store_x = [&](uint32_t m, const uint4 (&src)[PIECES], _Float16* buf) {
+        const bool live = 128u * m + 8u * xcol < K;
+#pragma unroll
+        for (uint32_t p = 0; p < PIECES; ++p) {
+            const uint32_t pr = (p * kGroupStreamThreads + tid) >> 4;
+            const h8 v = live ? perm_0415(__builtin_bit_cast(h8, src[p])) : h8{};
+            *reinterpret_cast<h8*>(buf + pr * kWideStride + 8u * xcol) = v;
+        }
+    };
+    auto compute = [&](uint32_t m, const QChunk<BITS> (&w)[2], const _Float16* buf) {
+        const uint32_t c = 4u * m + q, g = (c < nch ? c : nch - 1) >> 1;
+        const uint32_t mask = c < nch ? 0xFFFFFFFFu : 0u;
+        h8 a[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            dequant_chunk_sb(w[i], sbt[i][g], magic_v, a[i]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) a[i][u] = mask_h8(a[i][u], mask);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < NTT; ++j) {
+                const h8 b = *reinterpret_cast<const h8*>(buf + (16u * j + r16) * kWideStride + 32u * q + 8u * u);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][u], b, acc[i][j], 0, 0, 0);
+            }
+    };
+
+    // prologue: weights of k-tiles 0..DEPTH-1, activations of 0 and 1; stage 0
+    load_x(0, xr[0]);
+    load_x(1, xr[1]);
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load_w((uint32_t)d, wr[d]);
+    publish();                                   // the scale/bias table (ends with a barrier)
+    store_x(0, xr[0], xs);
+    load_x(2, xr[0]);
+    __syncthreads();
+    // step m: k-tile m from buffer m%2 and ring stage m%DEPTH; stage k-tile
+    // m+1 into the other buffer; refill the rings (weights m+DEPTH,
+    // activations m+3)
+    auto step = [&](uint32_t m, auto st_c, auto pa_c) {
+        constexpr int ST = decltype(st_c)::value, PA = decltype(pa_c)::value;
+        compute(m, wr[ST], xs + PA * kWideBuf);
+        store_x(m + 1, xr[PA ^ 1], xs + (PA ^ 1) * kWideBuf);
+        load_w(m + DEPTH, wr[ST]);
+        load_x(m + 3, xr[PA ^ 1]);
+        __syncthreads();
+    };
+    constexpr int U = DEPTH * 2;                 // steps per unrolled run (ring stage and buffer parity)
+    uint32_t m = 0;
+    for (; m + U <= nk; m += U)
+        sfor_w<0, U>([&](auto c) {
+            step(m + c.value, std::integral_constant<int, c.value % DEPTH>{}, std::integral_constant<int, c.value & 1>{});
+        });
+    sfor_w<0, U - 1>([&](auto c) {
+        if (m + c.value < nk)
+            step(m + c.value, std::integral_constant<int, c.value % DEPTH>{}, std::integral_constant<int, c.value & 1>{});
+    });
+}
+
+// Gate/up + GeGLU of one large-tile half (block y) over 64 features (block
+// x): wave w takes features f_blk + 16w + (0..15), its gate rows as row tile
+// 0 and its up rows as row tile 1.
+template <int BITS, int NTT>
+__device__ __forceinline__ void wide_gate_up_half(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                                  const GroupedRows& gr, const uint16_t* __restrict__ hidden,
+                                                  uint32_t stride, uint16_t* __restrict__ act, uint32_t D, uint32_t F,
+                                                  uint32_t bx) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 wide_lds[];
+    constexpr uint32_t NF = kGroupWideRows / 2u;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t r16 = lane & 15u, q = lane >> 4;
+    const uint32_t G = D >> 6, row_bytes = (D >> 3) * BITS;
+    const uint32_t f_blk = bx * NF, fb = f_blk + 16u * wave;
+    const uint32_t f = fb + r16, fc = f < F ? f : F - 1;                 // features past F: clamped, not stored
+    const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
+    const ExpertOffsets& o = pool.off;
+    uint32_t* sb_lds = reinterpret_cast<uint32_t*>(wide_lds + 2u * kWideBuf);
+    const uint8_t* const wrow[2] = {blob + o.gate_w + (size_t)fc * row_bytes, blob + o.up_w + (size_t)fc * row_bytes};
+    const uint32_t* const sbt[2] = {sb_lds + (fc - f_blk) * G, sb_lds + (NF + fc - f_blk) * G};
+    f32x4 acc[2][NTT];
+    wide_rows_loop<BITS, NTT>(
+        wrow, sbt,
+        [&](uint32_t p) { return hidden + (size_t)sorted[gr.first + (p < gr.count ? p : 0u)].token * stride; }, D,
+        wide_lds, acc, [&]() {
+            const uint32_t nf = F - f_blk < NF ? F - f_blk : NF;
+            copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f_blk * G,
+                                                   reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (size_t)f_blk * G,
+                                                   sb_lds, nf * G);
+            copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.up_s) + (size_t)f_blk * G,
+                                                   reinterpret_cast<const uint16_t*>(blob + o.up_b) + (size_t)f_blk * G,
+                                                   sb_lds + NF * G, nf * G);
+            __syncthreads();
+        });
+#pragma unroll
+    for (int j = 0; j < NTT; ++j) {
+        const uint32_t p = 16u * j + r16;
+        if (p >= gr.count) continue;
+        uint16_t* dst = act + (size_t)(gr.first + p) * F;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = gelu_tanh(acc[0][j][r]) * acc[1][j][r];
+        store_f16x4(dst, fb + 4u * q, F, v);
+    }
+}
+
+// Down projection of one large-tile half (block y) over 128 outputs of D
+// (block x): wave w takes rows d_blk + 32w + (0..31).
+template <int BITS, int NTT>
+__device__ __forceinline__ void wide_down_half(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                               const GroupedRows& gr, const uint16_t* __restrict__ act,
+                                               uint16_t* __restrict__ partials, uint32_t D, uint32_t F, uint32_t k,
+                                               uint32_t bx) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 wide_lds[];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t r16 = lane & 15u, q = lane >> 4;
+    const uint32_t G = F >> 6, row_bytes = (F >> 3) * BITS;
+    const uint32_t d_blk = bx * kGroupWideRows, db = d_blk + 32u * wave;
+    const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
+    const ExpertOffsets& o = pool.off;
+    uint32_t* sb_lds = reinterpret_cast<uint32_t*>(wide_lds + 2u * kWideBuf);
+    const uint8_t* wrow[2];
+    const uint32_t* sbt[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t d = db + 16u * i + r16, dc = d < D ? d : D - 1;   // rows past D: clamped, not stored
+        wrow[i] = blob + o.down_w + (size_t)dc * row_bytes;
+        sbt[i] = sb_lds + (dc - d_blk) * G;
+    }
+    uint32_t dst_row[NTT];          // partials row of each pair, loaded before the K loop
+#pragma unroll
+    for (int j = 0; j < NTT; ++j) {
+        const uint32_t p = 16u * j + r16;
+        const Pair pr = sorted[gr.first + (p < gr.count ? p : 0u)];
+        dst_row[j] = pr.token * k + pr.rank;
+    }
+    f32x4 acc[2][NTT];
+    wide_rows_loop<BITS, NTT>(
+        wrow, sbt, [&](uint32_t p) { return act + (size_t)(gr.first + (p < gr.count ? p : 0u)) * F; }, F, wide_lds, acc,
+        [&]() {
+            const uint32_t nd = D - d_blk < kGroupWideRows ? D - d_blk : kGroupWideRows;
+            copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)d_blk * G,
+                                                   reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)d_blk * G,
+                                                   sb_lds, nd * G);
+            __syncthreads();
+        });
+#pragma unroll
+    for (int j = 0; j < NTT; ++j) {
+        const uint32_t p = 16u * j + r16;
+        if (p >= gr.count) continue;
+        uint16_t* dst = partials + (size_t)dst_row[j] * D;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            store_f16x4(dst, db + 16u * i + 4u * q, D, v);
+        }
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ void moe_wide_gate_up(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                                 const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
+                                                 const uint16_t* __restrict__ hidden, uint32_t stride,
+                                                 uint16_t* __restrict__ act, uint32_t D, uint32_t F, uint32_t bx,
+                                                 uint32_t by) {
+    GroupedRows gr;
+    if (!wide_rows(tiles, n_tiles, by, gr)) return;
+    if (gr.count <= 32u) wide_gate_up_half<BITS, 2>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+    else wide_gate_up_half<BITS, 4>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+}
+
+template <int BITS>
+__device__ __forceinline__ void moe_wide_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                              const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
+                                              const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
+                                              uint32_t D, uint32_t F, uint32_t k, uint32_t bx, uint32_t by) {
+    GroupedRows gr;
+    if (!wide_rows(tiles, n_tiles, by, gr)) return;
+    if (gr.count <= 32u) wide_down_half<BITS, 2>(pool, sorted, gr, act, partials, D, F, k, bx);
+    else wide_down_half<BITS, 4>(pool, sorted, gr, act, partials, D, F, k, bx);
+}
+
 // One launch per projection runs both, so the stream's weight reads overlap
 // the tile's matrix work: blocks 0 .. max_tiles·sx - 1 are the stream's
 // (x = b mod sx, y = b / sx; sx blocks of rows), the rest the MFMA tile's
@@ -565,9 +843,9 @@ __device__ __forceinline__ void moe_grouped_gate_up_launch(const ExpertPool& poo
                                                            const uint16_t* __restrict__ hidden, uint32_t stride,
                                                            uint16_t* __restrict__ act, uint32_t D, uint32_t F,
                                                            GroupedLaunch gl) {
-    const uint32_t b = blockIdx.x, tx = 2u * gl.max_tiles, ns = gl.max_tiles * gl.sx;
+    const uint32_t b = blockIdx.x, ns = gl.max_tiles * gl.sx;
     if (b < ns) moe_stream_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, b % gl.sx, b / gl.sx);
-    else moe_grouped_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, (b - ns) % tx, (b - ns) / tx);
+    else moe_wide_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, (b - ns) % gl.wx, (b - ns) / gl.wx);
 }
 
 template <int BITS>
@@ -576,9 +854,9 @@ __device__ __forceinline__ void moe_grouped_down_launch(const ExpertPool& pool, 
                                                         const uint32_t* __restrict__ n_tiles,
                                                         const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
                                                         uint32_t D, uint32_t F, uint32_t k, GroupedLaunch gl) {
-    const uint32_t b = blockIdx.x, tx = 2u * gl.max_tiles, ns = gl.max_tiles * gl.sx;
+    const uint32_t b = blockIdx.x, ns = gl.max_tiles * gl.sx;
     if (b < ns) moe_stream_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, b % gl.sx, b / gl.sx);
-    else moe_grouped_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, (b - ns) % tx, (b - ns) / tx);
+    else moe_wide_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, (b - ns) % gl.wx, (b - ns) / gl.wx);
 }
 
 // h2[t][d] = fp16(Σ_r fma(w[t][r], partials[(t*k+r)*D + d])) in rank order
