@@ -97,7 +97,7 @@ def bench_c3(ctx, stream, batch_avg_us, bits=4):
     n, mt = T * k, ops.max_tiles(T, k, E)
     sorted_p = DeviceBuffer(n * 16)
     offsets, counts = DeviceBuffer(E * 4), DeviceBuffer(E * 4)
-    tiles, n_tiles, status = DeviceBuffer(mt * 16), DeviceBuffer(4), DeviceBuffer(4)
+    tiles, n_tiles, status = DeviceBuffer(mt * 16), DeviceBuffer(ops.GROUP_STATE_BYTES), DeviceBuffer(4)
     act, partials, h2 = DeviceBuffer(n * F * 2), DeviceBuffer(n * D * 2), DeviceBuffer(T * D * 2)
     idx_b, w_b = DeviceBuffer.from_array(idx), DeviceBuffer.from_array(w16)
     grouping, grouped = ops.PrefillMoEGrouping(ctx), ops.PrefillGroupedRoutedMoE(ctx)

@@ -19,10 +19,9 @@ constexpr uint32_t kProjBN = 256;          // outputs (gemm.hpp kProjBN)
 constexpr uint32_t kProjThreads = 256;     // threads (gemm.hpp kProjThreads)
 constexpr uint32_t kProjGemmThreads = 512; // threads of the prefill GEMM's tile (gemm.hpp kProjGemmThreads)
 constexpr uint32_t kProjMaxK = 8192;       // longest reduction (gemm.hpp kProjMaxK)
-constexpr uint32_t kGroupStreamThreads = 256;   // grouped weight stream (moe_prefill.hpp)
-constexpr uint32_t kGroupStreamRows = 256;      // its weight rows per block
-constexpr uint32_t kGroupWideRows = 128;        // grouped wide role: weight rows per block (moe_prefill.hpp)
-constexpr uint32_t kWideBufHalves = 64 * (128 + 8);   // its activation buffer (two of them)
+constexpr uint32_t kUnitThreads = 256;          // grouped MoE units (moe_prefill.hpp)
+constexpr uint32_t kUnitStride = 128 + 8;       // halves per LDS activation row of a unit
+constexpr uint32_t kGroupMaxTiles = 8192 / 128 + 256;  // tiles the device planner takes (moe_prefill.hpp)
 constexpr uint32_t proj_lds_bytes(uint32_t k) { return 2u * kProjBM * 72u * 2u + 2u * kProjBN * (k / 64u) * 2u; }
 // the pipelined tile of the prefill GEMM (gemm.hpp proj_pl_lds_bytes)
 constexpr uint32_t proj_pl_lds_bytes(uint32_t k) { return 3u * kProjBM * 72u * 2u + 4u * kProjBN * (k / 64u); }
@@ -736,7 +735,7 @@ public:
     explicit PrefillGroupedRoutedMoE(const Module& m) : m_(m) {}
 
     int encode(void* stream, const tfq_expert_pool& pool, const tfq_pair* sorted,
-               const tfq_tile* tiles, const uint32_t* n_tiles, uint32_t max_tiles,
+               const tfq_tile* tiles, uint32_t* n_tiles, uint32_t max_tiles,
                const uint16_t* hidden, uint32_t stride, uint32_t d, uint32_t f, uint32_t k,
                uint16_t* act, uint16_t* partials) const {
         int rc = check_expert_pool(pool, d, f);
@@ -744,34 +743,52 @@ public:
         if (!sorted || !tiles || !n_tiles || !hidden || !act || !partials)
             return fail(TFQ_E_INVAL, "null pointer argument");
         if (stride < d || stride % 8) return fail(TFQ_E_INVAL, "hidden stride must be >= d and a multiple of 8");
-        if (!aligned(hidden, 16) || !aligned(act, 16))
-            return fail(TFQ_E_INVAL, "hidden and act must be 16-byte aligned");
+        if (!aligned(hidden, 16) || !aligned(act, 16) || !aligned(partials, 16))
+            return fail(TFQ_E_INVAL, "hidden, act and partials must be 16-byte aligned");
         if (d > kProjMaxK || f > kProjMaxK)
             return fail(TFQ_E_UNSUPPORTED, "d=%u and f=%u must be at most %u", d, f, kProjMaxK);
         if (max_tiles == 0) return TFQ_OK;
+        if (max_tiles > kGroupMaxTiles)
+            return fail(TFQ_E_UNSUPPORTED, "max_tiles=%u exceeds %u (8192 pairs over 256 experts)", max_tiles,
+                        kGroupMaxTiles);
         ExpertPool kp = kernel_pool(pool);
-        // one launch per projection: grouping tiles of at most kGroupStreamMax
-        // pairs as a weight stream (128 features / 256 outputs per block),
-        // larger ones as 64-pair halves on the wide role (64 features / 128
-        // outputs per block); each role skips the other's tiles
+        // one launch per projection over the work list of the tiles: tiles of
+        // at most 32 pairs as stream units (RT 4: 128 features / 256 outputs
+        // per unit, NTT 1 or 2 pair sub-tiles), larger ones as 64-pair halves
+        // on wide units (RT 2: 64 features / 128 outputs, NTT 2 or 4); the
+        // grid is the blocks the GPU holds resident, at most the units the
+        // tile bound allows
         const uint32_t bits = pool_bits(pool);
         const char* gu = bits == 2 ? "tfq_moe_grouped_gate_up_b2" : bits == 3 ? "tfq_moe_grouped_gate_up_b3"
                                                                            : "tfq_moe_grouped_gate_up";
         const char* dn = bits == 2 ? "tfq_moe_grouped_down_b2" : bits == 3 ? "tfq_moe_grouped_down_b3"
                                                                         : "tfq_moe_grouped_down";
+        // dynamic LDS: the largest unit (two activation buffers of 16·NTT
+        // rows, then the table of 64·RT rows of K/64 words)
         auto lds_for = [](uint32_t K) {
-            return std::max(4u * kGroupStreamRows * (K / 64u), 2u * kWideBufHalves * 2u + 4u * kGroupWideRows * (K / 64u));
+            auto unit = [K](uint32_t rt, uint32_t ntt) { return 2u * 16u * ntt * kUnitStride * 2u + 4u * 64u * rt * (K / 64u); };
+            return std::max(unit(2, 4), unit(4, 2));
         };
-        GroupedLaunch g1{max_tiles, (f + kGroupWideRows / 2 - 1) / (kGroupWideRows / 2),
-                         (f + kGroupStreamRows / 2 - 1) / (kGroupStreamRows / 2)};
-        void* a1[] = {&kp, &sorted, &tiles, &n_tiles, &hidden, &stride, &act, &d, &f, &g1};
-        rc = launch2(m_, gu, max_tiles * g1.sx + 2 * max_tiles * g1.wx, 1, kGroupStreamThreads, lds_for(d), stream, a1);
+        auto grid_for = [&](const char* name, const GroupedLaunch& g, uint32_t lds, uint32_t& grid) {
+            hipFunction_t fn = m_.get(name);
+            if (!fn) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
+            const uint32_t p = m_.resident_blocks(fn, kUnitThreads, lds);
+            const uint32_t units = 2u * max_tiles * std::max(g.wx, g.sx);
+            grid = std::min(p, units);
+            return TFQ_OK;
+        };
+        GroupedLaunch g1{max_tiles, (f + 63) / 64, (f + 127) / 128};
+        uint32_t grid1 = 0, grid2 = 0;
+        rc = grid_for(gu, g1, lds_for(d), grid1);
         if (rc) return rc;
-        GroupedLaunch g2{max_tiles, (d + kGroupWideRows - 1) / kGroupWideRows,
-                         (d + kGroupStreamRows - 1) / kGroupStreamRows};
+        void* a1[] = {&kp, &sorted, &tiles, &n_tiles, &hidden, &stride, &act, &d, &f, &g1};
+        rc = launch2(m_, gu, grid1, 1, kUnitThreads, lds_for(d), stream, a1);
+        if (rc) return rc;
+        GroupedLaunch g2{max_tiles, (d + 127) / 128, (d + 255) / 256};
+        rc = grid_for(dn, g2, lds_for(f), grid2);
+        if (rc) return rc;
         void* a2[] = {&kp, &sorted, &tiles, &n_tiles, &act, &partials, &d, &f, &k, &g2};
-        return launch2(m_, dn, max_tiles * g2.sx + 2 * max_tiles * g2.wx, 1, kGroupStreamThreads, lds_for(f), stream,
-                       a2);
+        return launch2(m_, dn, grid2, 1, kUnitThreads, lds_for(f), stream, a2);
     }
 
     // PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38).

@@ -499,7 +499,7 @@ int tfq_moe_group(tfq_ctx* ctx, void* stream, const uint32_t* indices, const uin
 }
 
 int tfq_moe_grouped(tfq_ctx* ctx, void* stream, const tfq_expert_pool* pool, const tfq_pair* sorted,
-                    const tfq_tile* tiles, const uint32_t* n_tiles, uint32_t max_tiles,
+                    const tfq_tile* tiles, uint32_t* n_tiles, uint32_t max_tiles,
                     const uint16_t* hidden, uint32_t hidden_stride, uint32_t d, uint32_t f,
                     uint32_t top_k, uint16_t* act_scratch, uint16_t* route_partials) {
     TFQ_REQUIRE_CTX(ctx);
@@ -532,7 +532,7 @@ PrefillLayout prefill_layout(uint32_t T, uint32_t k, uint32_t E, uint32_t d, uin
     L.tiles = take((size_t)TFQ_MOE_MAX_TILES(T, k, E) * 16);
     L.offsets = take((size_t)E * 4);
     L.counts = take((size_t)E * 4);
-    L.n_tiles = take(4);
+    L.n_tiles = take(4 * TFQ_MOE_GROUP_STATE_WORDS);
     L.status = take(4);
     L.act = take(n * f * 2);
     L.partials = take(n * d * 2);

@@ -119,9 +119,9 @@ struct Tile {
     uint32_t pad_;
 };
 
-// Block split of one grouped launch (moe_prefill.hpp): the first
-// max_tiles·sx blocks run the weight stream (small tiles), the next
-// 2·max_tiles·wx the wide role (halves of the large tiles).
+// Shape of one grouped launch (moe_prefill.hpp): the tile list's bound and
+// the row blocks per entry of the two roles; the grid is the resident
+// blocks, which walk the work list.
 struct GroupedLaunch {
     uint32_t max_tiles;
     uint32_t wx;      // row blocks of the wide role

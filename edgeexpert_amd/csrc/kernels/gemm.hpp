@@ -319,10 +319,11 @@ constexpr uint32_t proj_pl_lds_bytes(uint32_t K) {
 
 // dst[i] = a[i] | b[i] << 16 for i < count, into LDS (16-byte loads and
 // stores when the sources are 16-byte aligned and count % 8 == 0; U loads
-// per thread and array in flight).
+// per thread and array in flight). tid: the thread's index in the block.
 template <uint32_t NT, uint32_t U = 8>
 __device__ __forceinline__ void copy_sb_to_lds(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
-                                               uint32_t* __restrict__ dst, uint32_t count) {
+                                               uint32_t* __restrict__ dst, uint32_t count,
+                                               uint32_t tid = threadIdx.x) {
     if (((((uintptr_t)a) | ((uintptr_t)b)) & 15u) == 0 && (count & 7u) == 0) {
         const uint32_t n16 = count >> 3;
         const uint4* sa = reinterpret_cast<const uint4*>(a);
@@ -332,14 +333,14 @@ __device__ __forceinline__ void copy_sb_to_lds(const uint16_t* __restrict__ a, c
             uint4 va[U], vb[U];
 #pragma unroll
             for (uint32_t u = 0; u < U; ++u) {
-                const uint32_t i = base + u * NT + threadIdx.x;
+                const uint32_t i = base + u * NT + tid;
                 const uint32_t c = i < n16 ? i : n16 - 1;
                 va[u] = sa[c];
                 vb[u] = sbp[c];
             }
 #pragma unroll
             for (uint32_t u = 0; u < U; ++u) {
-                const uint32_t i = base + u * NT + threadIdx.x;
+                const uint32_t i = base + u * NT + tid;
                 if (i < n16) {
                     // v_perm: bytes 0-3 from the second operand, 4-7 from the first
                     t[2 * i] = make_uint4(__builtin_amdgcn_perm(vb[u].x, va[u].x, 0x05040100u),
@@ -354,8 +355,73 @@ __device__ __forceinline__ void copy_sb_to_lds(const uint16_t* __restrict__ a, c
             }
         }
     } else {
-        for (uint32_t i = threadIdx.x; i < count; i += NT) dst[i] = (uint32_t)a[i] | ((uint32_t)b[i] << 16);
+        for (uint32_t i = tid; i < count; i += NT) dst[i] = (uint32_t)a[i] | ((uint32_t)b[i] << 16);
     }
+}
+
+// Field i of a block word (codes 8j+i in the low half, 8j+i+4 in the high
+// half, BITS bits each) read without a shift where it lies inside the fp16
+// mantissa: OR-ed into the exponent of 2^(10-o) (o: the field's bit offset
+// after an optional 8-bit shift of the word) it reads as 2^(10-o) + q, and
+// one subtraction leaves q exactly. 4 bits: offsets 0, 4, 0, 4 (the upper
+// two after a shift by 8); 3 bits: 0, 3, 6, then 1 after a shift; 2 bits: 0,
+// 2, 4, 6.
+template <int BITS>
+struct DqField {
+    static constexpr uint32_t shift(int i) { return (BITS == 4 && i >= 2) || (BITS == 3 && i == 3) ? 8u : 0u; }
+    static constexpr uint32_t offset(int i) {
+        return BITS == 4 ? 4u * (uint32_t)(i & 1) : BITS == 3 ? (i == 3 ? 1u : 3u * (uint32_t)i) : 2u * (uint32_t)i;
+    }
+    static constexpr uint32_t mask(int i) { return (((1u << BITS) - 1u) << offset(i)) * 0x00010001u; }
+    static constexpr uint32_t magic(int i) { return ((25u - offset(i)) << 10) * 0x00010001u; }   // 2^(10-o) pairs
+    static constexpr float base(int i) { return (float)(1u << (10u - offset(i))); }
+};
+
+// The magic pairs in VGPRs (v_and_or_b32 takes one scalar operand, the mask):
+// fields with equal offsets share one register.
+template <int BITS>
+struct DequantConsts {
+    uint32_t magic[4];
+};
+
+template <int BITS>
+__device__ __forceinline__ DequantConsts<BITS> dequant_consts() {
+    DequantConsts<BITS> dc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (BITS == 4 && i >= 2) {
+            dc.magic[i] = dc.magic[i - 2];
+        } else {
+            uint32_t v;
+            asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "i"(DqField<BITS>::magic(i)));
+            dc.magic[i] = v;
+        }
+    }
+    return dc;
+}
+
+// Word j of a chunk (codes 8j..8j+7, in the order 8j+0, +4, +1, +5, +2, +6,
+// +3, +7) dequantised as fp16(q·s + b) with one rounding, s and b from one
+// table word (scale | bias << 16).
+template <int BITS>
+__device__ __forceinline__ h8 dequant_word_sb(const QChunk<BITS>& w, int j, uint32_t sb, const DequantConsts<BITS>& dc) {
+    const h2 s2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x01000100u));
+    const h2 b2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x03020302u));
+    uint32_t t = block_word<BITS>(w, j);
+    if constexpr (BITS != 4) asm("" : "+v"(t));
+    const uint32_t t8 = t >> 8;
+    h8 run;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        using F = DqField<BITS>;
+        const uint32_t src = F::shift(i) ? t8 : t;
+        const uint32_t q = (src & F::mask(i)) | dc.magic[i];
+        const h2 base = {(_Float16)F::base(i), (_Float16)F::base(i)};
+        const h2 wv = __builtin_elementwise_fma(__builtin_bit_cast(h2, q) - base, s2, b2);   // exact q, one rounding
+        run[2 * i] = wv[0];
+        run[2 * i + 1] = wv[1];
+    }
+    return run;
 }
 
 // dequant_chunk_f16_v with the scale and bias taken from one table word.

@@ -23,28 +23,31 @@ constexpr uint32_t kGroupMaxPairs = 8192;
 constexpr uint32_t kGroupMaxExperts = 256;
 constexpr uint32_t kGroupChunks = kGroupMaxPairs / 64;
 constexpr uint32_t kGroupThreads = 1024;
+constexpr uint32_t kGroupStateWords = 4;       // TFQ_MOE_GROUP_STATE_WORDS
 // status codes (the PrefillMoEGroupingError cases the device can detect)
 constexpr uint32_t kGroupOk = 0;
 constexpr uint32_t kGroupExpertOutOfRange = 8;
-// grouping tiles of at most kGroupStreamMax pairs run as a weight stream
-// (moe_stream_*), larger ones on the matrix-core tile (moe_grouped_*)
+// grouping tiles of at most kGroupStreamMax pairs run as stream units, larger
+// ones as wide units (see the grouped MoE units below)
 constexpr uint32_t kGroupStreamMax = 32;
-constexpr uint32_t kGroupStreamThreads = 256;  // 4 wavefronts, 64 weight rows each
-constexpr uint32_t kGroupStreamRows = 64 * (kGroupStreamThreads / 64);   // rows per block
 
-// dst[n + e] = fp16(v[e]) for e < 4 and n + e < lim: one 8-byte store when
-// all four are in range and dst + n is 8-byte aligned, else per element.
+// threadIdx.x as an opaque value: the work units of a persistent launch read
+// it through this, so the compiler rederives each unit's lane addresses
+// inside the unit instead of hoisting them out of the unit loop, where they
+// would stay live (in registers) across every other unit body.
+__device__ __forceinline__ uint32_t unit_tid() {
+    uint32_t t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// dst[n .. n+3] = fp16(v[0..3]) as one 8-byte store when n < lim: n and
+// lim are multiples of 4 (rows of d or f, multiples of 64, outputs in
+// fours) and dst is 8-byte aligned (act and partials are 16-byte aligned).
 __device__ __forceinline__ void store_f16x4(uint16_t* __restrict__ dst, uint32_t n, uint32_t lim, const float (&v)[4]) {
-    const uint16_t o0 = f2h(v[0]), o1 = f2h(v[1]), o2 = f2h(v[2]), o3 = f2h(v[3]);
-    if (n + 3 < lim && ((reinterpret_cast<uintptr_t>(dst + n) & 7u) == 0)) {
-        *reinterpret_cast<uint2*>(dst + n) =
-            make_uint2((uint32_t)o0 | ((uint32_t)o1 << 16), (uint32_t)o2 | ((uint32_t)o3 << 16));
-    } else {
-        const uint16_t o[4] = {o0, o1, o2, o3};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (n + e < lim) dst[n + e] = o[e];
-    }
+    if (n < lim)
+        *reinterpret_cast<uint2*>(dst + n) = make_uint2((uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16),
+                                                        (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16));
 }
 
 // Stable counting sort of the token-major pairs (token t, rank r) -> expert
@@ -55,7 +58,9 @@ __device__ __forceinline__ void store_f16x4(uint16_t* __restrict__ dst, uint32_t
 // over the 64-pair chunks (in order) gives each chunk's base, and an
 // exclusive scan over experts gives the offsets. Empty experts get offset
 // 0xFFFFFFFF and count 0. The tile list cuts each expert's run into
-// 128-row tiles. On an out-of-range expert index nothing is grouped and
+// 128-row tiles. n_tiles is the grouping state (kGroupStateWords words):
+// the tile count, then the grouped launches' work counters, zeroed here.
+// On an out-of-range expert index nothing is grouped and
 // *status = kGroupExpertOutOfRange.
 __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, const uint16_t* __restrict__ w,
                                           uint32_t T, uint32_t k, uint32_t E, Pair* __restrict__ sorted,
@@ -94,10 +99,8 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
             offsets[e] = 0xFFFFFFFFu;
             counts[e] = 0;
         }
-        if (tid == 0) {
-            *n_tiles = 0;
-            *status = kGroupExpertOutOfRange;
-        }
+        if (tid < kGroupStateWords) n_tiles[tid] = 0;
+        if (tid == 0) *status = kGroupExpertOutOfRange;
         return;
     }
 
@@ -169,6 +172,8 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
             tile_base[E] = carry_t;
             *n_tiles = carry_t;
             *status = kGroupOk;
+        } else if (tid < kGroupStateWords) {
+            n_tiles[tid] = 0;
         }
     }
     __syncthreads();
@@ -192,451 +197,88 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
     }
 }
 
-// The grouped GEMMs run each 128-row grouping tile as two 64-row halves
-// (block x = 2·tile + half) on the projection tile of gemm.hpp, so an
-// expert with few rows costs one half's matrix work, not a full tile's.
-// Returns false for a half with no rows (block-uniform).
+// Rows of one work unit's pairs: a run of the sorted pairs of one expert.
 struct GroupedRows {
-    uint32_t first;   // index of the half's first row in the sorted pairs
-    uint32_t count;   // rows in this half (1..64)
+    uint32_t first;   // index of the first pair in the sorted pairs
+    uint32_t count;   // pairs (1..64 on the wide role, 1..32 on the stream)
     uint32_t expert;
 };
 
-__device__ __forceinline__ bool grouped_rows(const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
-                                             uint32_t bx, GroupedRows& gr) {
-    const uint32_t tile = bx >> 1, half = bx & 1u;
-    if (tile >= *n_tiles) return false;
-    const Tile t = tiles[tile];
-    if (t.count <= kGroupStreamMax || t.count <= kProjBM * half) return false;   // small tiles: the stream
-    const uint32_t left = t.count - kProjBM * half;
-    gr = {t.start + kProjBM * half, left < kProjBM ? left : kProjBM, t.expert};
-    return true;
-}
-
-// Grouped gate/up + GeGLU over one 64-row half tile (block x) and 128
-// features of F (block y): act[p][f] = fp16(gelu(gate_e[f]·x_p) · (up_e[f]·x_p))
-// for sorted pairs p of the half, x_p = hidden row of the pair's token
-// (prefill.metal:598-637). Wave w takes features f0 + 32w .. +31 with the gate
-// rows as its first 32-output sub-tile and the up rows as its second, so each
-// lane holds gate and up of the same (pair, feature) and applies the GeGLU
-// in registers. LDS table rows 0..127: gate scales/biases, 128..255: up.
-// BITS: code width of the expert rows (2, 3 or 4; prefill.metal:1304-1450
-// for the 2/3-bit experts).
-template <int BITS = 4>
-__device__ __forceinline__ void moe_grouped_gate_up(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                    const Tile* __restrict__ tiles,
-                                                    const uint32_t* __restrict__ n_tiles,
-                                                    const uint16_t* __restrict__ hidden, uint32_t stride,
-                                                    uint16_t* __restrict__ act, uint32_t D, uint32_t F, uint32_t bx,
-                                                    uint32_t by) {
-    GroupedRows gr;
-    if (!grouped_rows(tiles, n_tiles, bx, gr)) return;
-    extern __shared__ __attribute__((aligned(16))) _Float16 proj_lds[];
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
-    const uint32_t G = D >> 6, f0 = by * 128u;
-    const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
-    const ExpertOffsets& o = pool.off;
-    const uint16_t* gs = reinterpret_cast<const uint16_t*>(blob + o.gate_s);
-    const uint16_t* gb = reinterpret_cast<const uint16_t*>(blob + o.gate_b);
-    const uint16_t* us = reinterpret_cast<const uint16_t*>(blob + o.up_s);
-    const uint16_t* ub = reinterpret_cast<const uint16_t*>(blob + o.up_b);
-    uint16_t* s_lds = reinterpret_cast<uint16_t*>(proj_lds + 2 * kProjBM * kGemmLdsStride);
-    uint16_t* b_lds = s_lds + kProjBN * G;
-    const uint32_t nf = F - f0 < 128u ? F - f0 : 128u;
-    copy_pair_to_lds<kProjThreads>(gs + (size_t)f0 * G, gb + (size_t)f0 * G, s_lds, b_lds, nf * G);
-    copy_pair_to_lds<kProjThreads>(us + (size_t)f0 * G, ub + (size_t)f0 * G, s_lds + 128u * G, b_lds + 128u * G,
-                                   nf * G);
-    const uint32_t col = lane & 31u, h = lane >> 5;
-    const uint32_t f = f0 + 32u * wave + col, fc = f < F ? f : F - 1;   // features past F: clamped, not stored
-    ProjLanes pl;
-    pl.wp0 = blob + o.gate_w + (size_t)fc * ((D >> 3) * BITS) + 4u * BITS * h;
-    pl.wp1 = blob + o.up_w + (size_t)fc * ((D >> 3) * BITS) + 4u * BITS * h;
-    pl.sidx0 = (fc - f0) * G;
-    pl.sidx1 = (128u + fc - f0) * G;
-    // rows past the half's count read its first row: their results are never stored
-    const uint32_t xrow = tid >> 2;
-    const uint32_t tok = sorted[gr.first + (xrow < gr.count ? xrow : 0u)].token;
-    const uint16_t* xp = hidden + (size_t)tok * stride + 16u * (tid & 3u);
-    // a half with at most 32 rows runs one token sub-tile (block-uniform)
-    auto run = [&](auto mi_c) {
-        constexpr int MI = decltype(mi_c)::value;
-        f32x16 acc[MI][2];
-        proj_core<false, MI, BITS>(acc, proj_lds, s_lds, b_lds, pl, xp, G);
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t m = 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
-                if (m < gr.count && f < F)
-                    act[(size_t)(gr.first + m) * F + f] = f2h(gelu_tanh(acc[i][0][r]) * acc[i][1][r]);
-            }
-    };
-    if (gr.count <= 32u) run(std::integral_constant<int, 1>{});
-    else run(std::integral_constant<int, 2>{});
-}
-
-// Grouped down projection over one 64-row half tile (block x) and 256
-// outputs of D (block y): partials[(token*k + rank)*D + d] = fp16(down_e[d]·act_p)
-// (prefill.metal:639-670). BITS as for moe_grouped_gate_up.
-template <int BITS = 4>
-__device__ __forceinline__ void moe_grouped_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                 const Tile* __restrict__ tiles,
-                                                 const uint32_t* __restrict__ n_tiles,
-                                                 const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
-                                                 uint32_t D, uint32_t F, uint32_t k, uint32_t bx, uint32_t by) {
-    GroupedRows gr;
-    if (!grouped_rows(tiles, n_tiles, bx, gr)) return;
-    extern __shared__ __attribute__((aligned(16))) _Float16 proj_lds[];
-    __shared__ uint32_t dst_row[kProjBM];
-    const uint32_t tid = threadIdx.x, wave = tid >> 6;
-    const uint32_t G = F >> 6, n0 = by * kProjBN;
-    const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
-    const ExpertOffsets& o = pool.off;
-    uint16_t* s_lds = reinterpret_cast<uint16_t*>(proj_lds + 2 * kProjBM * kGemmLdsStride);
-    uint16_t* b_lds = s_lds + kProjBN * G;
-    if (tid < gr.count) {
-        const Pair p = sorted[gr.first + tid];
-        dst_row[tid] = p.token * k + p.rank;
-    }
-    const uint32_t nrows = D - n0 < kProjBN ? D - n0 : kProjBN;
-    copy_pair_to_lds<kProjThreads>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)n0 * G,
-                                   reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)n0 * G, s_lds,
-                                   b_lds, nrows * G);
-    const ProjLanes pl = proj_lanes<2, BITS>(blob + o.down_w, (F >> 3) * BITS, n0, wave, D, 0, G);
-    const uint32_t xrow = tid >> 2;
-    const uint16_t* xp = act + (size_t)(gr.first + (xrow < gr.count ? xrow : 0u)) * F + 16u * (tid & 3u);
-    // a half with at most 32 rows runs one token sub-tile (block-uniform)
-    auto run = [&](auto mi_c) {
-        constexpr int MI = decltype(mi_c)::value;
-        f32x16 acc[MI][2];
-        proj_core<false, MI, BITS>(acc, proj_lds, s_lds, b_lds, pl, xp, G);   // its barriers publish dst_row
-        proj_for_each<2>(acc, [&](uint32_t m, uint32_t n, float v) {
-            if (m < gr.count && n0 + n < D) partials[(size_t)dst_row[m] * D + n0 + n] = f2h(v);
-        });
-    };
-    if (gr.count <= 32u) run(std::integral_constant<int, 1>{});
-    else run(std::integral_constant<int, 2>{});
-}
-
-// ------------------------------------------- weight stream for small tiles ----
-//
-// Under a skewed popularity most experts see a handful of tokens (config 3:
-// 101 of 128 experts take at most 32 of the 4096 pairs, yet hold 80% of the
-// active weights). On the matrix-core tile such an expert costs a 64-row
-// half of MFMA work and the tile's per-group barriers for a few rows; the
-// work is a weight stream instead. A grouping tile with at most
-// kGroupStreamMax pairs is skipped by the two kernels above and run here:
-// each wavefront owns 64 weight rows (four 16-row v_mfma_f32_16x16x32_f16
-// A operands) and the whole K loop, the pairs as one or two 16-token B
-// operands (NTT), so every activation load feeds four row tiles. Lane l
-// holds row l%16 of each A operand and the quarter q = l/16 of every
-// 128-code k-tile (chunk 4m + q: one 16-byte load at 4 bits, word j feeds
-// k-step j), the B lane (pair l%16 of the sub-tile, quarter q) the matching
-// 32 activations, permuted like the unpack. The block's scales and biases
-// sit in an LDS table (one word per row and group), so the loop issues only
-// 16-byte loads. Weights are dequantised as everywhere else (fp16(q·s + b),
-// one rounding), so the result differs from the tile's only in the fp32
-// summation order. DEPTH k-tiles are in flight per wave.
-
-template <int BITS, int NTT>
-struct StreamStage {
-    QChunk<BITS> w[4];
-    uint4 x[NTT][4];
-};
-
-// acc[i][j]: 16x16 D tile of row tile i and token sub-tile j (column =
-// lane % 16 = token, rows 4·(lane/16) + r). sbt[i]: the LDS table row
-// (scale | bias << 16 per group) of this lane's row in tile i, published by
-// the barrier that `publish` runs once the first DEPTH k-tiles' loads are in
-// flight.
-template <int BITS, int NTT, typename Publish, int DEPTH = (NTT == 1 ? 3 : 2)>
-__device__ __forceinline__ void stream_rows(const uint8_t* const (&wrow)[4], const uint32_t* const (&sbt)[4],
-                                            const uint16_t* const (&xrow)[NTT], uint32_t K, f32x4 (&acc)[4][NTT],
-                                            Publish publish) {
-    const uint32_t q = (threadIdx.x & 63u) >> 4;
-    const uint32_t nch = K >> 5;                       // 32-code chunks per row
-    const uint32_t nk = (nch + 3u) >> 2;               // 128-code k-tiles
-    uint32_t magic_v;
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_v));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < NTT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // k-tiles past the end re-read the last chunk (and are not computed);
-    // the missing quarters of a half-filled last k-tile are masked to zero
-    auto load = [&](uint32_t m, StreamStage<BITS, NTT>& st) {
-        const uint32_t c = 4u * m + q, cc = c < nch ? c : nch - 1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) st.w[i] = ldg_chunk<BITS, false>(wrow[i], cc);
-#pragma unroll
-        for (int j = 0; j < NTT; ++j) {
-            const uint4* xp = reinterpret_cast<const uint4*>(xrow[j] + 32u * cc);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) st.x[j][u] = xp[u];
-        }
-    };
-    auto compute = [&](uint32_t m, const StreamStage<BITS, NTT>& st, auto mask_c) {
-        constexpr bool MASK = decltype(mask_c)::value;
-        const uint32_t c = 4u * m + q, g = (c < nch ? c : nch - 1) >> 1;
-        const uint32_t mask = MASK && c >= nch ? 0u : 0xFFFFFFFFu;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            h8 a[4];
-            dequant_chunk_sb(st.w[i], sbt[i][g], magic_v, a);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const h8 ai = MASK ? mask_h8(a[u], mask) : a[u];
-#pragma unroll
-                for (int j = 0; j < NTT; ++j) {
-                    const h8 bj = perm_0415(__builtin_bit_cast(h8, st.x[j][u]));
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ai, MASK ? mask_h8(bj, mask) : bj, acc[i][j],
-                                                                       0, 0, 0);
-                }
-            }
-        }
-    };
-    // the last k-tile is masked when K is not a multiple of 128 codes
-    const uint32_t nfull = (nch & 3u) ? nk - 1 : nk;
-    StreamStage<BITS, NTT> st[DEPTH];
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) load((uint32_t)d, st[d]);
-    publish();
-    uint32_t m = 0;
-    for (; m + DEPTH <= nfull; m += DEPTH) {
-#pragma unroll
-        for (int d = 0; d < DEPTH; ++d) {
-            compute(m + (uint32_t)d, st[d], std::false_type{});
-            load(m + (uint32_t)(d + DEPTH), st[d]);
-        }
-    }
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-        const uint32_t mm = m + (uint32_t)d;
-        if (mm < nfull) compute(mm, st[d], std::false_type{});
-        else if (mm < nk) compute(mm, st[d], std::true_type{});
-    }
-}
-
-// Grouping tile `by` if it takes the weight stream (block-uniform).
-__device__ __forceinline__ bool stream_tile(const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
-                                            uint32_t by, Tile& t) {
-    if (by >= *n_tiles) return false;
-    t = tiles[by];
-    return t.count > 0 && t.count <= kGroupStreamMax;
-}
-
-// Dynamic LDS of the stream kernels: the scale/bias table of a block's
-// kGroupStreamRows rows (gate/up: the gate rows, then the up rows).
-constexpr uint32_t stream_lds_bytes(uint32_t K) { return 4u * kGroupStreamRows * (K / 64u); }
-
-// Gate/up + GeGLU of one small tile (block y) over kGroupStreamRows/2
-// features (block x): wave w takes features f = f_blk + 32w + (0..31),
-// its gate rows as row tiles 0, 1 and its up rows as row tiles 2, 3, so each
-// lane holds gate and up of the same (pair, feature).
-template <int BITS, int NTT>
-__device__ __forceinline__ void stream_gate_up_tile(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                    const Tile& t, const uint16_t* __restrict__ hidden,
-                                                    uint32_t stride, uint16_t* __restrict__ act, uint32_t D,
-                                                    uint32_t F, uint32_t bx) {
-    extern __shared__ __attribute__((aligned(16))) uint32_t stream_sb[];
-    constexpr uint32_t NF = kGroupStreamRows / 2u;                       // features per block
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t r16 = lane & 15u, q = lane >> 4;
-    const uint32_t G = D >> 6, row_bytes = (D >> 3) * BITS;
-    const uint32_t f_blk = bx * NF;
-    const uint32_t fb = f_blk + 32u * wave;
-    const uint8_t* blob = pool.base + (uint64_t)t.expert * pool.stride;
-    const ExpertOffsets& o = pool.off;
-    const uint8_t* wrow[4];
-    const uint32_t* sbt[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t f = fb + 16u * i + r16, fc = f < F ? f : F - 1;   // features past F: clamped, not stored
-        wrow[i] = blob + o.gate_w + (size_t)fc * row_bytes;
-        wrow[2 + i] = blob + o.up_w + (size_t)fc * row_bytes;
-        sbt[i] = stream_sb + (fc - f_blk) * G;
-        sbt[2 + i] = stream_sb + (NF + fc - f_blk) * G;
-    }
-    const uint16_t* xrow[NTT];
-#pragma unroll
-    for (int j = 0; j < NTT; ++j) {
-        const uint32_t p = 16u * j + r16;                                // pairs past the tile: row 0, not stored
-        xrow[j] = hidden + (size_t)sorted[t.start + (p < t.count ? p : 0u)].token * stride;
-    }
-    f32x4 acc[4][NTT];
-    stream_rows<BITS, NTT>(wrow, sbt, xrow, D, acc, [&]() {
-        const uint32_t nf = F - f_blk < NF ? F - f_blk : NF;
-        copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f_blk * G,
-                                               reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (size_t)f_blk * G,
-                                               stream_sb, nf * G);
-        copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.up_s) + (size_t)f_blk * G,
-                                               reinterpret_cast<const uint16_t*>(blob + o.up_b) + (size_t)f_blk * G,
-                                               stream_sb + NF * G, nf * G);
-        __syncthreads();
-    });
-#pragma unroll
-    for (int j = 0; j < NTT; ++j) {
-        const uint32_t p = 16u * j + r16;
-        if (p >= t.count) continue;
-        uint16_t* dst = act + (size_t)(t.start + p) * F;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            float v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = gelu_tanh(acc[i][j][r]) * acc[2 + i][j][r];
-            store_f16x4(dst, fb + 16u * i + 4u * q, F, v);
-        }
-    }
-}
-
-// Down projection of one small tile (block y) over kGroupStreamRows
-// outputs of D (block x): wave w takes rows d = d_blk + 64w + (0..63).
-template <int BITS, int NTT>
-__device__ __forceinline__ void stream_down_tile(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                 const Tile& t, const uint16_t* __restrict__ act,
-                                                 uint16_t* __restrict__ partials, uint32_t D, uint32_t F,
-                                                 uint32_t k, uint32_t bx) {
-    extern __shared__ __attribute__((aligned(16))) uint32_t stream_sb[];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t r16 = lane & 15u, q = lane >> 4;
-    const uint32_t G = F >> 6, row_bytes = (F >> 3) * BITS;
-    const uint32_t d_blk = bx * kGroupStreamRows;
-    const uint32_t db = d_blk + 64u * wave;
-    const uint8_t* blob = pool.base + (uint64_t)t.expert * pool.stride;
-    const ExpertOffsets& o = pool.off;
-    const uint8_t* wrow[4];
-    const uint32_t* sbt[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t d = db + 16u * i + r16, dc = d < D ? d : D - 1;   // rows past D: clamped, not stored
-        wrow[i] = blob + o.down_w + (size_t)dc * row_bytes;
-        sbt[i] = stream_sb + (dc - d_blk) * G;
-    }
-    const uint16_t* xrow[NTT];
-    uint32_t dst_row[NTT];          // partials row of each pair, loaded before the K loop
-#pragma unroll
-    for (int j = 0; j < NTT; ++j) {
-        const uint32_t p = 16u * j + r16, pc = p < t.count ? p : 0u;
-        xrow[j] = act + (size_t)(t.start + pc) * F;
-        const Pair pr = sorted[t.start + pc];
-        dst_row[j] = pr.token * k + pr.rank;
-    }
-    f32x4 acc[4][NTT];
-    stream_rows<BITS, NTT>(wrow, sbt, xrow, F, acc, [&]() {
-        const uint32_t nd = D - d_blk < kGroupStreamRows ? D - d_blk : kGroupStreamRows;
-        copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)d_blk * G,
-                                               reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)d_blk * G,
-                                               stream_sb, nd * G);
-        __syncthreads();
-    });
-#pragma unroll
-    for (int j = 0; j < NTT; ++j) {
-        const uint32_t p = 16u * j + r16;
-        if (p >= t.count) continue;
-        uint16_t* dst = partials + (size_t)dst_row[j] * D;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-            store_f16x4(dst, db + 16u * i + 4u * q, D, v);
-        }
-    }
-}
-
-template <int BITS>
-__device__ __forceinline__ void moe_stream_gate_up(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                   const Tile* __restrict__ tiles,
-                                                   const uint32_t* __restrict__ n_tiles,
-                                                   const uint16_t* __restrict__ hidden, uint32_t stride,
-                                                   uint16_t* __restrict__ act, uint32_t D, uint32_t F, uint32_t bx,
-                                                   uint32_t by) {
-    Tile t;
-    if (!stream_tile(tiles, n_tiles, by, t)) return;
-    if (t.count <= 16u) stream_gate_up_tile<BITS, 1>(pool, sorted, t, hidden, stride, act, D, F, bx);
-    else stream_gate_up_tile<BITS, 2>(pool, sorted, t, hidden, stride, act, D, F, bx);
-}
-
-template <int BITS>
-__device__ __forceinline__ void moe_stream_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
-                                                const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
-                                                uint32_t D, uint32_t F, uint32_t k, uint32_t bx, uint32_t by) {
-    Tile t;
-    if (!stream_tile(tiles, n_tiles, by, t)) return;
-    if (t.count <= 16u) stream_down_tile<BITS, 1>(pool, sorted, t, act, partials, D, F, k, bx);
-    else stream_down_tile<BITS, 2>(pool, sorted, t, act, partials, D, F, k, bx);
-}
-
-// ----------------------------------------------- wide role for large tiles ----
-//
-// A grouping tile of more than kGroupStreamMax pairs runs as 64-pair halves
-// (block y = 2·tile + half), each block over kGroupWideRows weight rows
-// (block x): gate/up 64 features (gate and up rows), down 128 outputs. Wave
-// w owns 32 rows as two 16-row A operands of v_mfma_f32_16x16x32_f16 (lane
-// l: row l%16, the quarter q = l/16 of every 128-code k-tile, chunk 4m + q
-// from a DEPTH-deep register ring, dequantised exactly as in the stream);
-// the half's activations (NTT 16-pair sub-tiles) are staged per k-tile into
-// a double-buffered LDS tile [64 pairs][128 codes + 8] in the unpack order,
-// from a two-deep register ring, one barrier per k-tile; the B lane (pair
-// l%16 of sub-tile j, quarter q) reads its 16 bytes of k-step u at column
-// 32q + 8u. Codes past K (a half-filled last k-tile) are zero in both
-// operands. Per k-tile a wave issues 8·NTT MFMAs and dequantises 64 codes
-// per lane.
+// f(integral_constant<B>) ... f(<E-1>)
 template <int B, int E, typename Fn>
-__device__ __forceinline__ void sfor_w(Fn&& f) {             // f(integral_constant<B>) ... f(<E-1>)
+__device__ __forceinline__ void sfor_w(Fn&& f) {
     if constexpr (B < E) {
         f(std::integral_constant<int, B>{});
         sfor_w<B + 1, E>(f);
     }
 }
 
-constexpr uint32_t kGroupWideRows = 128;                  // weight rows per block (4 waves x 32)
-constexpr uint32_t kGroupWidePairs = 64;                  // pairs per block (a half tile)
-constexpr uint32_t kWideStride = 128 + 8;                 // halves per LDS activation row
-constexpr uint32_t kWideBuf = kGroupWidePairs * kWideStride;   // halves per activation buffer
-// Dynamic LDS of the wide role: two activation buffers, then the scale/bias
-// table of the block's rows.
-constexpr uint32_t wide_lds_bytes(uint32_t K) { return 2u * kWideBuf * 2u + 4u * kGroupWideRows * (K / 64u); }
 
-// Rows of half `by` of a large tile (false: nothing to do; block-uniform).
-__device__ __forceinline__ bool wide_rows(const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
-                                          uint32_t by, GroupedRows& gr) {
-    const uint32_t tile = by >> 1, half = by & 1u;
-    if (tile >= *n_tiles) return false;
-    const Tile t = tiles[tile];
-    if (t.count <= kGroupStreamMax || t.count <= kGroupWidePairs * half) return false;
-    const uint32_t left = t.count - kGroupWidePairs * half;
-    gr = {t.start + kGroupWidePairs * half, left < kGroupWidePairs ? left : kGroupWidePairs, t.expert};
-    return true;
+// ------------------------------------------------------ grouped MoE units ----
+//
+// The grouped projections run per unit: the pairs of one grouping tile (a
+// 64-pair half of a tile of more than kGroupStreamMax pairs, or a whole
+// smaller tile) times a block of weight rows. Each of the four wavefronts owns
+// RT 16-row A operands of v_mfma_f32_16x16x32_f16 and the whole K loop; the
+// pairs are NTT 16-pair B operands. Two shapes:
+//   wide   (tiles of more than 32 pairs): RT 2, NTT 2 or 4, 128 rows per unit
+//          (gate/up: 64 features, gate and up rows; down: 128 outputs);
+//   stream (tiles of at most 32 pairs):   RT 4, NTT 1 or 2, 256 rows per unit
+//          (gate/up: 128 features; down: 256 outputs).
+// Under a skewed popularity most experts see a handful of tokens (config 3:
+// 101 of 128 experts take at most 32 of the 4096 pairs, yet hold 80% of the
+// active weights), so the stream shape spreads each activation k-tile over
+// twice the rows. Lane l holds row l%16 of each A operand and the quarter
+// q = l/16 of every 128-code k-tile (chunk 4m + q: one 16-byte load at 4 bits;
+// word u feeds k-step u), dequantised from a DEPTH-deep register ring with the
+// scale and bias of an LDS table (one word per row and group). The unit's
+// activations are staged per k-tile into a double-buffered LDS tile
+// [16·NTT pairs][128 codes + 8] in the unpack order, from a two-deep register
+// ring, one barrier per k-tile; the B lane (pair l%16 of sub-tile j, quarter
+// q) reads its 16 bytes of k-step u at column 32q + 8u. Activation codes past
+// K (a half-filled last k-tile) are staged as zeros; the weights there are
+// those of the last chunk (finite), so the products vanish. Weights are
+// dequantised as everywhere else (fp16(q·s + b), one rounding).
+constexpr uint32_t kGroupWidePairs = 64;          // pairs of a wide unit (a half tile)
+constexpr uint32_t kUnitStride = 128 + 8;         // halves per LDS activation row
+constexpr uint32_t kUnitThreads = 256;            // four wavefronts
+
+// LDS of a unit: two activation buffers of 16·NTT rows, then the scale/bias
+// table of its 64·RT weight rows.
+constexpr uint32_t unit_xbuf(int NTT) { return 16u * (uint32_t)NTT * kUnitStride; }   // halves
+constexpr uint32_t unit_lds_bytes(int RT, int NTT, uint32_t K) {
+    return 2u * unit_xbuf(NTT) * 2u + 4u * 64u * (uint32_t)RT * (K / 64u);
 }
 
-// acc[i][j]: row tile i, pair sub-tile j (16x16 D layout). xrow(p): the
-// activation row of pair p (< NTT·16; past the half's count: any valid row,
-// not stored). sbt[i]: this lane's row of the scale/bias table.
-template <int BITS, int NTT, typename XRow, typename Publish, int DEPTH = 3>
-__device__ __forceinline__ void wide_rows_loop(const uint8_t* const (&wrow)[2], const uint32_t* const (&sbt)[2],
+// acc[i][j]: row tile i, pair sub-tile j (16x16 D layout: column lane%16 =
+// pair, rows 4·(lane/16) + r). xrow(p): the activation row of pair p
+// (< 16·NTT; past the unit's count: any valid row, not stored). sbt[i]: this
+// lane's row of the scale/bias table, published by the barrier that
+// `publish` runs once the first k-tiles' loads are in flight.
+template <int BITS, int RT, int NTT, int DEPTH, typename XRow, typename Publish>
+__device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wrow)[RT], const uint32_t* const (&sbt)[RT],
                                                XRow xrow, uint32_t K, _Float16* __restrict__ xs,
-                                               f32x4 (&acc)[2][NTT], Publish publish) {
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, q = lane >> 4, r16 = lane & 15u;
+                                               f32x4 (&acc)[RT][NTT], Publish publish, uint32_t tid) {
+    const uint32_t lane = tid & 63u, q = lane >> 4, r16 = lane & 15u;
     const uint32_t nch = K >> 5, nk = (nch + 3u) >> 2;
-    constexpr uint32_t NP = NTT * 16u;                     // staged pairs
-    constexpr uint32_t PIECES = NP * 16u / kGroupStreamThreads;   // 16-byte activation pieces per thread
-    uint32_t magic_v;
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_v));
+    constexpr uint32_t PIECES = NTT;                   // 16-byte activation pieces per thread (16·NTT rows x 16)
+    constexpr uint32_t XB = unit_xbuf(NTT);
+    const DequantConsts<BITS> dc = dequant_consts<BITS>();
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RT; ++i)
 #pragma unroll
         for (int j = 0; j < NTT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // activation piece p of this thread: pair (p·256 + tid) / 16, 16-byte column (tid % 16)
+    // activation piece p of this thread: pair 16p + tid/16, 16-byte column tid % 16
     const uint16_t* xr_row[PIECES];
 #pragma unroll
-    for (uint32_t p = 0; p < PIECES; ++p) xr_row[p] = xrow((p * kGroupStreamThreads + tid) >> 4);
+    for (uint32_t p = 0; p < PIECES; ++p) xr_row[p] = xrow(16u * p + (tid >> 4));
     const uint32_t xcol = tid & 15u;
-    QChunk<BITS> wr[DEPTH][2];
+    QChunk<BITS> wr[DEPTH][RT];
     uint4 xr[2][PIECES];
-    auto load_w = [&](uint32_t m, QChunk<BITS> (&dst)[2]) {
+    auto load_w = [&](uint32_t m, QChunk<BITS> (&dst)[RT]) {
         const uint32_t c = 4u * m + q, cc = c < nch ? c : nch - 1;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) dst[i] = ldg_chunk<BITS, false>(wrow[i], cc);
+        for (int i = 0; i < RT; ++i) dst[i] = ldg_chunk<BITS, false>(wrow[i], cc);
     };
     // columns past K load a valid piece and are stored as zeros
     auto load_x = [&](uint32_t m, uint4 (&dst)[PIECES]) {
@@ -649,30 +291,32 @@ __device__ __forceinline__ void wide_rows_loop(const uint8_t* const (&wrow)[2], 
         const bool live = 128u * m + 8u * xcol < K;
 #pragma unroll
         for (uint32_t p = 0; p < PIECES; ++p) {
-            const uint32_t pr = (p * kGroupStreamThreads + tid) >> 4;
             const h8 v = live ? perm_0415(__builtin_bit_cast(h8, src[p])) : h8{};
-            *reinterpret_cast<h8*>(buf + pr * kWideStride + 8u * xcol) = v;
+            *reinterpret_cast<h8*>(buf + (16u * p + (tid >> 4)) * kUnitStride + 8u * xcol) = v;
         }
     };
-    auto compute = [&](uint32_t m, const QChunk<BITS> (&w)[2], const _Float16* buf) {
+    // per k-step u: the NTT B operands read together, the RT A operands
+    // dequantised from their block words, then RT·NTT MFMAs
+    auto compute = [&](uint32_t m, const QChunk<BITS> (&w)[RT], const _Float16* buf) {
         const uint32_t c = 4u * m + q, g = (c < nch ? c : nch - 1) >> 1;
-        const uint32_t mask = c < nch ? 0xFFFFFFFFu : 0u;
-        h8 a[2][4];
+        uint32_t sb[RT];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            dequant_chunk_sb(w[i], sbt[i][g], magic_v, a[i]);
+        for (int i = 0; i < RT; ++i) sb[i] = sbt[i][g];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) a[i][u] = mask_h8(a[i][u], mask);
+        for (int u = 0; u < 4; ++u) {
+            h8 b[NTT];
+#pragma unroll
+            for (int j = 0; j < NTT; ++j)
+                b[j] = *reinterpret_cast<const h8*>(buf + (16u * j + r16) * kUnitStride + 32u * q + 8u * u);
+            h8 a[RT];
+#pragma unroll
+            for (int i = 0; i < RT; ++i) a[i] = dequant_word_sb<BITS>(w[i], u, sb[i], dc);
+#pragma unroll
+            for (int j = 0; j < NTT; ++j)
+#pragma unroll
+                for (int i = 0; i < RT; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int j = 0; j < NTT; ++j) {
-                const h8 b = *reinterpret_cast<const h8*>(buf + (16u * j + r16) * kWideStride + 32u * q + 8u * u);
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][u], b, acc[i][j], 0, 0, 0);
-            }
     };
 
     // prologue: weights of k-tiles 0..DEPTH-1, activations of 0 and 1; stage 0
@@ -689,8 +333,8 @@ __device__ __forceinline__ void wide_rows_loop(const uint8_t* const (&wrow)[2], 
     // activations m+3)
     auto step = [&](uint32_t m, auto st_c, auto pa_c) {
         constexpr int ST = decltype(st_c)::value, PA = decltype(pa_c)::value;
-        compute(m, wr[ST], xs + PA * kWideBuf);
-        store_x(m + 1, xr[PA ^ 1], xs + (PA ^ 1) * kWideBuf);
+        compute(m, wr[ST], xs + PA * XB);
+        store_x(m + 1, xr[PA ^ 1], xs + (PA ^ 1) * XB);
         load_w(m + DEPTH, wr[ST]);
         load_x(m + 3, xr[PA ^ 1]);
         __syncthreads();
@@ -707,71 +351,90 @@ __device__ __forceinline__ void wide_rows_loop(const uint8_t* const (&wrow)[2], 
     });
 }
 
-// Gate/up + GeGLU of one large-tile half (block y) over 64 features (block
-// x): wave w takes features f_blk + 16w + (0..15), its gate rows as row tile
-// 0 and its up rows as row tile 1.
-template <int BITS, int NTT>
-__device__ __forceinline__ void wide_gate_up_half(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                  const GroupedRows& gr, const uint16_t* __restrict__ hidden,
-                                                  uint32_t stride, uint16_t* __restrict__ act, uint32_t D, uint32_t F,
-                                                  uint32_t bx) {
-    extern __shared__ __attribute__((aligned(16))) _Float16 wide_lds[];
-    constexpr uint32_t NF = kGroupWideRows / 2u;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+// ring depth of a shape: the 64-row waves hold four k-tiles of weights
+template <int RT>
+constexpr int unit_depth() { return RT == 2 ? 3 : 4; }
+
+// Gate/up + GeGLU of one unit over 32·RT features (row block bx): wave w
+// takes features f_blk + 16·(RT/2)·w + (0..16·RT/2-1), its gate rows as row
+// tiles 0..RT/2-1 and its up rows as row tiles RT/2..RT-1, so each lane holds
+// gate and up of the same (pair, feature). LDS table rows 0..NF-1: gate
+// scales/biases, NF..2NF-1: up.
+template <int BITS, int RT, int NTT>
+__device__ __forceinline__ void unit_gate_up(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                             const GroupedRows& gr, const uint16_t* __restrict__ hidden,
+                                             uint32_t stride, uint16_t* __restrict__ act, uint32_t D, uint32_t F,
+                                             uint32_t bx) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 unit_lds[];
+    constexpr uint32_t NF = 32u * RT, HT = RT / 2;
+    const uint32_t tid = unit_tid(), lane = tid & 63u, wave = tid >> 6;
     const uint32_t r16 = lane & 15u, q = lane >> 4;
     const uint32_t G = D >> 6, row_bytes = (D >> 3) * BITS;
-    const uint32_t f_blk = bx * NF, fb = f_blk + 16u * wave;
-    const uint32_t f = fb + r16, fc = f < F ? f : F - 1;                 // features past F: clamped, not stored
+    const uint32_t f_blk = bx * NF, fb = f_blk + 16u * HT * wave;
     const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
     const ExpertOffsets& o = pool.off;
-    uint32_t* sb_lds = reinterpret_cast<uint32_t*>(wide_lds + 2u * kWideBuf);
-    const uint8_t* const wrow[2] = {blob + o.gate_w + (size_t)fc * row_bytes, blob + o.up_w + (size_t)fc * row_bytes};
-    const uint32_t* const sbt[2] = {sb_lds + (fc - f_blk) * G, sb_lds + (NF + fc - f_blk) * G};
-    f32x4 acc[2][NTT];
-    wide_rows_loop<BITS, NTT>(
+    uint32_t* sb_lds = reinterpret_cast<uint32_t*>(unit_lds + 2u * unit_xbuf(NTT));
+    const uint8_t* wrow[RT];
+    const uint32_t* sbt[RT];
+#pragma unroll
+    for (uint32_t i = 0; i < HT; ++i) {
+        const uint32_t f = fb + 16u * i + r16, fc = f < F ? f : F - 1;   // features past F: clamped, not stored
+        wrow[i] = blob + o.gate_w + (size_t)fc * row_bytes;
+        wrow[HT + i] = blob + o.up_w + (size_t)fc * row_bytes;
+        sbt[i] = sb_lds + (fc - f_blk) * G;
+        sbt[HT + i] = sb_lds + (NF + fc - f_blk) * G;
+    }
+    f32x4 acc[RT][NTT];
+    unit_rows_loop<BITS, RT, NTT, unit_depth<RT>()>(
         wrow, sbt,
         [&](uint32_t p) { return hidden + (size_t)sorted[gr.first + (p < gr.count ? p : 0u)].token * stride; }, D,
-        wide_lds, acc, [&]() {
+        unit_lds, acc,
+        [&]() {
             const uint32_t nf = F - f_blk < NF ? F - f_blk : NF;
-            copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f_blk * G,
-                                                   reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (size_t)f_blk * G,
-                                                   sb_lds, nf * G);
-            copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.up_s) + (size_t)f_blk * G,
-                                                   reinterpret_cast<const uint16_t*>(blob + o.up_b) + (size_t)f_blk * G,
-                                                   sb_lds + NF * G, nf * G);
+            copy_sb_to_lds<kUnitThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f_blk * G,
+                                            reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (size_t)f_blk * G,
+                                            sb_lds, nf * G, tid);
+            copy_sb_to_lds<kUnitThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.up_s) + (size_t)f_blk * G,
+                                            reinterpret_cast<const uint16_t*>(blob + o.up_b) + (size_t)f_blk * G,
+                                            sb_lds + NF * G, nf * G, tid);
             __syncthreads();
-        });
+        },
+        tid);
 #pragma unroll
     for (int j = 0; j < NTT; ++j) {
         const uint32_t p = 16u * j + r16;
         if (p >= gr.count) continue;
         uint16_t* dst = act + (size_t)(gr.first + p) * F;
-        float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = gelu_tanh(acc[0][j][r]) * acc[1][j][r];
-        store_f16x4(dst, fb + 4u * q, F, v);
+        for (uint32_t i = 0; i < HT; ++i) {
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = gelu_tanh(acc[i][j][r]) * acc[HT + i][j][r];
+            store_f16x4(dst, fb + 16u * i + 4u * q, F, v);
+        }
     }
 }
 
-// Down projection of one large-tile half (block y) over 128 outputs of D
-// (block x): wave w takes rows d_blk + 32w + (0..31).
-template <int BITS, int NTT>
-__device__ __forceinline__ void wide_down_half(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                               const GroupedRows& gr, const uint16_t* __restrict__ act,
-                                               uint16_t* __restrict__ partials, uint32_t D, uint32_t F, uint32_t k,
-                                               uint32_t bx) {
-    extern __shared__ __attribute__((aligned(16))) _Float16 wide_lds[];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+// Down projection of one unit over 64·RT outputs of D (row block bx): wave
+// w takes rows d_blk + 16·RT·w + (0..16·RT-1).
+template <int BITS, int RT, int NTT>
+__device__ __forceinline__ void unit_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
+                                          const GroupedRows& gr, const uint16_t* __restrict__ act,
+                                          uint16_t* __restrict__ partials, uint32_t D, uint32_t F, uint32_t k,
+                                          uint32_t bx) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 unit_lds[];
+    constexpr uint32_t NR = 64u * RT;
+    const uint32_t tid = unit_tid(), lane = tid & 63u, wave = tid >> 6;
     const uint32_t r16 = lane & 15u, q = lane >> 4;
     const uint32_t G = F >> 6, row_bytes = (F >> 3) * BITS;
-    const uint32_t d_blk = bx * kGroupWideRows, db = d_blk + 32u * wave;
+    const uint32_t d_blk = bx * NR, db = d_blk + 16u * RT * wave;
     const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
     const ExpertOffsets& o = pool.off;
-    uint32_t* sb_lds = reinterpret_cast<uint32_t*>(wide_lds + 2u * kWideBuf);
-    const uint8_t* wrow[2];
-    const uint32_t* sbt[2];
+    uint32_t* sb_lds = reinterpret_cast<uint32_t*>(unit_lds + 2u * unit_xbuf(NTT));
+    const uint8_t* wrow[RT];
+    const uint32_t* sbt[RT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < RT; ++i) {
         const uint32_t d = db + 16u * i + r16, dc = d < D ? d : D - 1;   // rows past D: clamped, not stored
         wrow[i] = blob + o.down_w + (size_t)dc * row_bytes;
         sbt[i] = sb_lds + (dc - d_blk) * G;
@@ -783,80 +446,198 @@ __device__ __forceinline__ void wide_down_half(const ExpertPool& pool, const Pai
         const Pair pr = sorted[gr.first + (p < gr.count ? p : 0u)];
         dst_row[j] = pr.token * k + pr.rank;
     }
-    f32x4 acc[2][NTT];
-    wide_rows_loop<BITS, NTT>(
-        wrow, sbt, [&](uint32_t p) { return act + (size_t)(gr.first + (p < gr.count ? p : 0u)) * F; }, F, wide_lds, acc,
+    f32x4 acc[RT][NTT];
+    unit_rows_loop<BITS, RT, NTT, unit_depth<RT>()>(
+        wrow, sbt, [&](uint32_t p) { return act + (size_t)(gr.first + (p < gr.count ? p : 0u)) * F; }, F, unit_lds,
+        acc,
         [&]() {
-            const uint32_t nd = D - d_blk < kGroupWideRows ? D - d_blk : kGroupWideRows;
-            copy_sb_to_lds<kGroupStreamThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)d_blk * G,
-                                                   reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)d_blk * G,
-                                                   sb_lds, nd * G);
+            const uint32_t nd = D - d_blk < NR ? D - d_blk : NR;
+            copy_sb_to_lds<kUnitThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)d_blk * G,
+                                            reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)d_blk * G,
+                                            sb_lds, nd * G, tid);
             __syncthreads();
-        });
+        },
+        tid);
 #pragma unroll
     for (int j = 0; j < NTT; ++j) {
         const uint32_t p = 16u * j + r16;
         if (p >= gr.count) continue;
         uint16_t* dst = partials + (size_t)dst_row[j] * D;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < RT; ++i) {
             const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
             store_f16x4(dst, db + 16u * i + 4u * q, D, v);
         }
     }
 }
 
-template <int BITS>
-__device__ __forceinline__ void moe_wide_gate_up(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                 const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
-                                                 const uint16_t* __restrict__ hidden, uint32_t stride,
-                                                 uint16_t* __restrict__ act, uint32_t D, uint32_t F, uint32_t bx,
-                                                 uint32_t by) {
-    GroupedRows gr;
-    if (!wide_rows(tiles, n_tiles, by, gr)) return;
-    if (gr.count <= 32u) wide_gate_up_half<BITS, 2>(pool, sorted, gr, hidden, stride, act, D, F, bx);
-    else wide_gate_up_half<BITS, 4>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+// ------------------------------------------------ persistent unit schedule ----
+//
+// A grouped launch runs a grid of resident blocks (P = gridDim.x) over a work
+// list that every block derives from the device tile list, so no block of
+// the launch finds itself without work. A unit is (entry, row block): an
+// entry is one 64-pair half of a tile of more than kGroupStreamMax pairs
+// (wide role, wx row blocks) or one smaller tile (stream, sx row blocks).
+// Entries come in four classes, dearest first: wide halves of more than 32
+// pairs (NTT 4), the other wide halves (NTT 2), stream tiles of 17..32 pairs
+// (NTT 2), then of at most 16 (NTT 1); tile order within a class, and the
+// row blocks of an entry as consecutive units. Block b runs unit b first and
+// then takes units P, P+1, ... in the order blocks ask for them (a counter in
+// the grouping state, asked one unit ahead), so the dearest units start
+// first and the cheap ones fill the gaps at the end. The last block to leave
+// zeroes the counters for the next launch.
+constexpr uint32_t kGroupMaxTiles = kGroupMaxPairs / kGemmBM + kGroupMaxExperts;   // bound of TFQ_MOE_MAX_TILES
+static_assert(kGemmBM == 2 * kGroupWidePairs, "a grouping tile is two wide halves");
+constexpr uint32_t kGroupMaxEntries = 2u * kGroupMaxTiles;
+constexpr uint32_t kGroupNextUnit = 1, kGroupBlocksDone = 2;   // counter words of the grouping state
+
+struct UnitPlan {
+    uint32_t n_wide;      // wide entries (the first two classes)
+    uint32_t n_entries;   // all entries
+};
+
+// Wavefront 0 writes the entries ({first pair, expert | count << 16}) of the
+// first min(n_tiles[0], max_tiles) tiles into ent; ends with a barrier.
+__device__ __forceinline__ UnitPlan plan_units(const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
+                                               uint32_t max_tiles, uint2* ent) {
+    __shared__ uint32_t plan_tot[2];
+    constexpr uint32_t C = kGroupMaxTiles / 64u;          // tiles per lane
+    static_assert(kGroupMaxTiles % 64u == 0, "whole wavefront passes");
+    if (threadIdx.x < 64u) {
+        const uint32_t lane = threadIdx.x;
+        uint32_t n = *n_tiles;
+        n = n < max_tiles ? n : max_tiles;
+        n = n < kGroupMaxTiles ? n : kGroupMaxTiles;
+        Tile tl[C];
+#pragma unroll
+        for (uint32_t c = 0; c < C; ++c) {
+            const uint32_t t = 64u * c + lane;
+            tl[c] = t < n ? tiles[t] : Tile{0u, 0u, 0u, 0u};
+        }
+        // per tile the entries of each class, two classes per word (16 bits
+        // each: at most kGroupMaxEntries), scanned over the tiles in order
+        uint32_t pre_w[C], pre_s[C], carry_w = 0, carry_s = 0;
+#pragma unroll
+        for (uint32_t c = 0; c < C; ++c) {
+            const uint32_t cnt = tl[c].count;
+            const uint32_t vw = ((cnt > 32u) + (cnt > 96u)) | ((uint32_t)(cnt > 64u && cnt <= 96u) << 16);
+            const uint32_t vs = (uint32_t)(cnt > 16u && cnt <= 32u) | ((uint32_t)(cnt >= 1u && cnt <= 16u) << 16);
+            uint32_t iw = vw, is = vs;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t uw = (uint32_t)__shfl_up((int)iw, o, kWave);
+                const uint32_t us = (uint32_t)__shfl_up((int)is, o, kWave);
+                if ((int)lane >= o) {
+                    iw += uw;
+                    is += us;
+                }
+            }
+            pre_w[c] = carry_w + iw - vw;
+            pre_s[c] = carry_s + is - vs;
+            carry_w += (uint32_t)__shfl((int)iw, 63, kWave);
+            carry_s += (uint32_t)__shfl((int)is, 63, kWave);
+        }
+        const uint32_t n0 = carry_w & 0xFFFFu, n1 = carry_w >> 16, n2 = carry_s & 0xFFFFu, n3 = carry_s >> 16;
+#pragma unroll
+        for (uint32_t c = 0; c < C; ++c) {
+            const Tile t = tl[c];
+            if (t.count > kGroupStreamMax) {
+                const uint32_t p0 = pre_w[c] & 0xFFFFu;
+                const uint32_t c0 = t.count < kGroupWidePairs ? t.count : kGroupWidePairs;
+                ent[p0] = make_uint2(t.start, t.expert | (c0 << 16));
+                if (t.count > kGroupWidePairs) {
+                    const uint32_t left = t.count - kGroupWidePairs;
+                    ent[left > 32u ? p0 + 1u : n0 + (pre_w[c] >> 16)] =
+                        make_uint2(t.start + kGroupWidePairs, t.expert | (left << 16));
+                }
+            } else if (t.count > 16u) {
+                ent[n0 + n1 + (pre_s[c] & 0xFFFFu)] = make_uint2(t.start, t.expert | (t.count << 16));
+            } else if (t.count >= 1u) {
+                ent[n0 + n1 + n2 + (pre_s[c] >> 16)] = make_uint2(t.start, t.expert | (t.count << 16));
+            }
+        }
+        if (lane == 0) {
+            plan_tot[0] = n0 + n1;
+            plan_tot[1] = n0 + n1 + n2 + n3;
+        }
+    }
+    __syncthreads();
+    return {plan_tot[0], plan_tot[1]};
 }
 
-template <int BITS>
-__device__ __forceinline__ void moe_wide_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                              const Tile* __restrict__ tiles, const uint32_t* __restrict__ n_tiles,
-                                              const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
-                                              uint32_t D, uint32_t F, uint32_t k, uint32_t bx, uint32_t by) {
-    GroupedRows gr;
-    if (!wide_rows(tiles, n_tiles, by, gr)) return;
-    if (gr.count <= 32u) wide_down_half<BITS, 2>(pool, sorted, gr, act, partials, D, F, k, bx);
-    else wide_down_half<BITS, 4>(pool, sorted, gr, act, partials, D, F, k, bx);
+// The unit loop of one grouped launch: wide(rows, bx) / stream(rows, bx) run
+// one unit each (block-uniform calls). Every unit starts after a barrier, so
+// it may reuse the dynamic LDS of the one before. state: the grouping state
+// (tile count, then the counters).
+template <typename Wide, typename Stream>
+__device__ __forceinline__ void run_units(const Tile* __restrict__ tiles, uint32_t* __restrict__ state,
+                                          GroupedLaunch gl, Wide wide, Stream stream) {
+    __shared__ uint2 ent[kGroupMaxEntries];
+    __shared__ uint32_t next_unit;
+    const UnitPlan pl = plan_units(tiles, state, gl.max_tiles, ent);
+    const uint32_t P = gridDim.x, tid = threadIdx.x;
+    const uint32_t n_wu = pl.n_wide * gl.wx, n_units = n_wu + (pl.n_entries - pl.n_wide) * gl.sx;
+    uint32_t u = blockIdx.x;
+    while (u < n_units) {
+        // the next unit's number, asked for now and read after this unit
+        uint32_t ask = 0;
+        if (tid == 0) ask = atomicAdd(state + kGroupNextUnit, 1u);
+        if (u < n_wu) {
+            const uint2 e = ent[u / gl.wx];
+            wide(GroupedRows{e.x, e.y >> 16, e.y & 0xFFFFu}, u % gl.wx);
+        } else {
+            const uint32_t v = u - n_wu;
+            const uint2 e = ent[pl.n_wide + v / gl.sx];
+            stream(GroupedRows{e.x, e.y >> 16, e.y & 0xFFFFu}, v % gl.sx);
+        }
+        if (tid == 0) next_unit = ask + P;
+        __syncthreads();
+        u = next_unit;
+        __syncthreads();
+    }
+    // every block asks once more than it runs units: when the last one
+    // leaves, no block of this launch touches the counters again
+    if (tid == 0 && atomicAdd(state + kGroupBlocksDone, 1u) == P - 1u) {
+        atomicExch(state + kGroupNextUnit, 0u);
+        atomicExch(state + kGroupBlocksDone, 0u);
+    }
 }
 
-// One launch per projection runs both, so the stream's weight reads overlap
-// the tile's matrix work: blocks 0 .. max_tiles·sx - 1 are the stream's
-// (x = b mod sx, y = b / sx; sx blocks of rows), the rest the MFMA tile's
-// (x = b' mod 2·max_tiles, y = b' / 2·max_tiles; ty blocks of outputs)
-// (GroupedLaunch, abi_types.h). Either order measures the same on config 3.
-static_assert(kGroupStreamThreads == kProjThreads, "one launch runs both roles");
+static_assert(kUnitThreads == kProjThreads, "the grouped launches run kProjThreads threads");
 
 template <int BITS>
 __device__ __forceinline__ void moe_grouped_gate_up_launch(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                           const Tile* __restrict__ tiles,
-                                                           const uint32_t* __restrict__ n_tiles,
+                                                           const Tile* __restrict__ tiles, uint32_t* __restrict__ n_tiles,
                                                            const uint16_t* __restrict__ hidden, uint32_t stride,
                                                            uint16_t* __restrict__ act, uint32_t D, uint32_t F,
                                                            GroupedLaunch gl) {
-    const uint32_t b = blockIdx.x, ns = gl.max_tiles * gl.sx;
-    if (b < ns) moe_stream_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, b % gl.sx, b / gl.sx);
-    else moe_wide_gate_up<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, (b - ns) % gl.wx, (b - ns) / gl.wx);
+    run_units(
+        tiles, n_tiles, gl,
+        [&](const GroupedRows& gr, uint32_t bx) {
+            if (gr.count <= 32u) unit_gate_up<BITS, 2, 2>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+            else unit_gate_up<BITS, 2, 4>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+        },
+        [&](const GroupedRows& gr, uint32_t bx) {
+            if (gr.count <= 16u) unit_gate_up<BITS, 4, 1>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+            else unit_gate_up<BITS, 4, 2>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+        });
 }
 
 template <int BITS>
 __device__ __forceinline__ void moe_grouped_down_launch(const ExpertPool& pool, const Pair* __restrict__ sorted,
-                                                        const Tile* __restrict__ tiles,
-                                                        const uint32_t* __restrict__ n_tiles,
+                                                        const Tile* __restrict__ tiles, uint32_t* __restrict__ n_tiles,
                                                         const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
                                                         uint32_t D, uint32_t F, uint32_t k, GroupedLaunch gl) {
-    const uint32_t b = blockIdx.x, ns = gl.max_tiles * gl.sx;
-    if (b < ns) moe_stream_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, b % gl.sx, b / gl.sx);
-    else moe_wide_down<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, (b - ns) % gl.wx, (b - ns) / gl.wx);
+    run_units(
+        tiles, n_tiles, gl,
+        [&](const GroupedRows& gr, uint32_t bx) {
+            if (gr.count <= 32u) unit_down<BITS, 2, 2>(pool, sorted, gr, act, partials, D, F, k, bx);
+            else unit_down<BITS, 2, 4>(pool, sorted, gr, act, partials, D, F, k, bx);
+        },
+        [&](const GroupedRows& gr, uint32_t bx) {
+            if (gr.count <= 16u) unit_down<BITS, 4, 1>(pool, sorted, gr, act, partials, D, F, k, bx);
+            else unit_down<BITS, 4, 2>(pool, sorted, gr, act, partials, D, F, k, bx);
+        });
 }
 
 // h2[t][d] = fp16(Σ_r fma(w[t][r], partials[(t*k+r)*D + d])) in rank order

@@ -11,13 +11,13 @@ extern "C" __global__ __launch_bounds__(kGroupThreads) void tfq_moe_group(
 
 #define TFQ_GROUPED(SUFFIX, BITS)                                                                \
     extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_gate_up##SUFFIX( \
-        ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,         \
+        ExpertPool pool, const Pair* sorted, const Tile* tiles, uint32_t* n_tiles,               \
         const uint16_t* hidden, uint32_t stride, uint16_t* act, uint32_t D, uint32_t F,          \
         GroupedLaunch gl) {                                                                      \
         moe_grouped_gate_up_launch<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, gl); \
     }                                                                                            \
     extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_down##SUFFIX(  \
-        ExpertPool pool, const Pair* sorted, const Tile* tiles, const uint32_t* n_tiles,         \
+        ExpertPool pool, const Pair* sorted, const Tile* tiles, uint32_t* n_tiles,               \
         const uint16_t* act, uint16_t* partials, uint32_t D, uint32_t F, uint32_t k,             \
         GroupedLaunch gl) {                                                                      \
         moe_grouped_down_launch<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, gl); \

@@ -411,6 +411,11 @@ GROUP_ERRORS = {1: "invalidQueryCount", 2: "invalidTopK", 3: "invalidNumExperts"
                 10: "expertSortKeyCountMismatch"}
 
 
+# Bytes of the device grouping state (TFQ_MOE_GROUP_STATE_WORDS words): the
+# tile count, then the grouped launches' work counters.
+GROUP_STATE_BYTES = 16
+
+
 def max_tiles(T: int, k: int, num_experts: int) -> int:
     n = T * k
     return (n + 127) // 128 + min(num_experts, n)

@@ -501,12 +501,18 @@ int tfq_prefill_router(tfq_ctx *ctx, void *stream, const tfq_router *router,
 #define TFQ_GROUP_DUPLICATE_TOKEN_RANK 9
 #define TFQ_GROUP_SORT_KEY_COUNT_MISMATCH 10
 
+/* Words of the device grouping state (the n_tiles argument of tfq_moe_group
+ * and tfq_moe_grouped): [0] the tile count, [1..2] the work counters of the
+ * grouped launches, [3] reserved. */
+#define TFQ_MOE_GROUP_STATE_WORDS 4
+
 /* Device grouping of the token-major pairs (token t, rank r) -> expert
  * indices[t*top_k + r] with weight weights[t*top_k + r]: a stable counting
  * sort giving the order (expert, token, rank) of PrefillMoEGrouping
  * .groupTokenExpertPairs (S/Kernels/Prefill/MoE/PrefillMoEGrouping.swift:91-192,
  * no sort keys). offsets/counts [num_experts] (offset 0xFFFFFFFF for an empty
- * expert), tiles [TFQ_MOE_MAX_TILES], *n_tiles and *status on the device. An
+ * expert), tiles [TFQ_MOE_MAX_TILES], n_tiles [TFQ_MOE_GROUP_STATE_WORDS]
+ * (the tile count, then counters zeroed here) and *status on the device. An
  * out-of-range expert index groups nothing and sets *status =
  * TFQ_GROUP_EXPERT_OUT_OF_RANGE. Contract: 1 <= T*top_k <= 8192,
  * 1 <= num_experts <= 256. */
@@ -538,14 +544,17 @@ int tfq_group_pairs_host(const tfq_pair *pairs, int64_t n_pairs, int64_t query_c
  * [T*top_k][f] (row = sorted position), then down with each row written to
  * route_partials[(token*top_k + rank)*d ...] (fp16 [T*top_k][d]); rows of
  * (token, rank) slots without a pair are left untouched. max_tiles is the
- * launch bound (TFQ_MOE_MAX_TILES); the device *n_tiles decides. Replaces
+ * launch bound (TFQ_MOE_MAX_TILES, at most 320 = 8192/128 + 256,
+ * TFQ_E_UNSUPPORTED beyond); the device tile count n_tiles[0] decides. The
+ * launches take their work units from the counters n_tiles[1..2] and leave
+ * them zero, so calls on one grouping state must not overlap. Replaces
  * PrefillGroupedRoutedMoE.encodeStreamedBatched
  * (S/Kernels/Prefill/MoE/PrefillGroupedRoutedMoE.swift:446-527), and its
  * 2/3-bit forms (prefill.metal:1304-1450) when pool->weight_bits is 2 or 3.
  * Contract: d, f multiples of 64 and at most 8192 (TFQ_E_UNSUPPORTED
- * beyond); hidden rows 16-byte aligned. */
+ * beyond); hidden rows, act_scratch and route_partials 16-byte aligned. */
 int tfq_moe_grouped(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
-                    const tfq_pair *sorted, const tfq_tile *tiles, const uint32_t *n_tiles,
+                    const tfq_pair *sorted, const tfq_tile *tiles, uint32_t *n_tiles,
                     uint32_t max_tiles, const uint16_t *hidden, uint32_t hidden_stride,
                     uint32_t d, uint32_t f, uint32_t top_k, uint16_t *act_scratch,
                     uint16_t *route_partials);

@@ -253,7 +253,7 @@ def test_grouped_experts_config3_shape_sampled(ctx, stream, bits):
     hidden = synth.f16_vector(0, "c3/x", T * d)
     n, mt = T * k, ops.max_tiles(T, k, E)
     b = {n_: DeviceBuffer(sz) for n_, sz in (("sorted", n * 16), ("offsets", E * 4), ("counts", E * 4),
-                                            ("tiles", mt * 16), ("n_tiles", 4), ("status", 4))}
+                                            ("tiles", mt * 16), ("n_tiles", ops.GROUP_STATE_BYTES), ("status", 4))}
     ops.PrefillMoEGrouping(ctx).encode(stream, _dev(idx), _dev(w16), T, k, E, b["sorted"], b["offsets"],
                                        b["counts"], b["tiles"], b["n_tiles"], b["status"])
     act = _dev(np.zeros(n * f, np.uint16))

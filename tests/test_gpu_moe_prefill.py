@@ -63,7 +63,8 @@ def _device_group(ctx, stream, idx, w16, T, k, E):
     mt = ops.max_tiles(T, k, E)
     bufs = dict(sorted=_dev(np.zeros(n, ops.PAIR_DTYPE)), offsets=_dev(np.zeros(E, np.uint32)),
                 counts=_dev(np.zeros(E, np.uint32)), tiles=_dev(np.zeros(mt, ops.TILE_DTYPE)),
-                n_tiles=_dev(np.zeros(1, np.uint32)), status=_dev(np.full(1, 77, np.uint32)))
+                n_tiles=_dev(np.full(ops.GROUP_STATE_BYTES // 4, 77, np.uint32)),
+                status=_dev(np.full(1, 77, np.uint32)))
     ops.PrefillMoEGrouping(ctx).encode(stream, _dev(idx), _dev(w16), T, k, E, bufs["sorted"],
                                        bufs["offsets"], bufs["counts"], bufs["tiles"],
                                        bufs["n_tiles"], bufs["status"])
@@ -71,6 +72,7 @@ def _device_group(ctx, stream, idx, w16, T, k, E):
     out = {"sorted": bufs["sorted"].download(np.uint8, n * 16).view(ops.PAIR_DTYPE),
            "offsets": bufs["offsets"].download(np.uint32, E), "counts": bufs["counts"].download(np.uint32, E),
            "n_tiles": int(bufs["n_tiles"].download(np.uint32, 1)[0]),
+           "state": bufs["n_tiles"].download(np.uint32, ops.GROUP_STATE_BYTES // 4),
            "status": int(bufs["status"].download(np.uint32, 1)[0])}
     out["tiles"] = bufs["tiles"].download(np.uint8, mt * 16).view(ops.TILE_DTYPE)[:out["n_tiles"]]
     return out, bufs
@@ -140,17 +142,26 @@ def _synthetic_pool(num_experts, d, f):
     return pool, offsets, stride
 
 
+# Fill of output rows no pair writes: a NaN bit pattern no kernel stores (the
+# fp16 conversions produce the canonical NaN 0x7E00 at most).
+UNWRITTEN = np.uint16(0x7FFF)
+
+
 def _run_grouped(ctx, stream, pool_bytes, offs, stride, E, idx, w16, hidden16, stride_h, T, k, d, f):
     got, bufs = _device_group(ctx, stream, idx, w16, T, k, E)
     pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs)
-    act = _dev(np.zeros(T * k * f, np.uint16))
-    partials = _dev(np.full(T * k * d, np.float16(-77).view(np.uint16), np.uint16))
+    act = _dev(np.full(T * k * f, UNWRITTEN, np.uint16))
+    partials = _dev(np.full(T * k * d, UNWRITTEN, np.uint16))
     h2 = _dev(np.zeros(T * d, np.uint16))
     g = ops.PrefillGroupedRoutedMoE(ctx)
     g.encode(stream, pool, bufs["sorted"], bufs["tiles"], bufs["n_tiles"], ops.max_tiles(T, k, E),
              _dev(hidden16), stride_h, d, f, k, act, partials)
     g.encode_reduce_token_major(stream, partials, _dev(w16), h2, T, k, d)
     stream.sync()
+    # every pair's act row (sorted position) is written by gate/up
+    n = len(got["sorted"])
+    left = np.argwhere(act.download(np.uint16).reshape(T * k, f)[:n] == UNWRITTEN)
+    assert left.shape[0] == 0, f"{left.shape[0]} act entries unwritten, e.g. (row, feature) {left[:8].tolist()}"
     return got, partials.download(np.uint16), h2.download(np.uint16)
 
 
@@ -169,7 +180,7 @@ def test_grouped_partials_match_reference_small(ctx, stream):
     # partials of ~1e-6, inside fp16's subnormal range, so a relative bound is
     # not meaningful here; the config-3 test below holds the 1e-3 relative bar.
     assert np.max(np.abs(gp - rp)) <= 0.0015
-    assert np.array_equal(parts == np.float16(-77).view(np.uint16), ref == np.float16(-99).view(np.uint16))
+    assert np.array_equal(parts == UNWRITTEN, ref == np.float16(-99).view(np.uint16))
     ref_h2 = from_f16_bits(oracle.reduce_token_major(ref, w16.ravel(), T, k, d))
     assert np.max(np.abs(from_f16_bits(h2) - ref_h2)) <= 0.0015
 
@@ -203,6 +214,8 @@ def test_grouped_moe_baseline_config3_sampled(ctx, stream):
     sel = got["sorted"][np.isin(got["sorted"]["token"], toks)]
     ref = oracle.grouped_route_partials(sel.astype(oracle.PAIR_DTYPE), hidden, d,
                                         *_oracle_pool(pool_bytes, offs, stride), k, d, f, T)
+    # every (token, rank) slot has a pair here: no unit of the down launch was skipped
+    assert not np.any(parts == UNWRITTEN)
     gp, rp = from_f16_bits(parts).reshape(T, k, d), from_f16_bits(ref).reshape(T, k, d)
     rel = oracle.rel_error(gp[toks], rp[toks])
     assert rel < TOL, f"partials rel={rel}"
@@ -244,6 +257,50 @@ def test_grouped_tile_and_stream_split(ctx, stream, bits):
         assert len(rows) == c
         rel = oracle.rel_error(gp[rows], rp[rows])
         assert rel < TOL, f"expert {e} ({c} pairs): rel={rel}"
+
+
+def test_grouped_schedule_at_tile_bound(ctx, stream):
+    # 8192 pairs over 256 experts: the tile bound (TFQ_MOE_MAX_TILES = 320)
+    # and a work list of several units per resident block in both launches;
+    # every pair against the oracle and no output row left unwritten.
+    T, k, E, d, f = 1024, 8, 256, 128, 128
+    assert ops.max_tiles(T, k, E) == 320
+    pool_bytes, offs, stride = synth.expert_pool(5, "bound/experts", E, d, f)
+    idx, w16 = synth.zipf_routing(5, "bound/route", T, E, k)
+    hidden = synth.f16_vector(5, "bound/x", T * d)
+    got, parts, _ = _run_grouped(ctx, stream, pool_bytes, offs, stride, E, idx, w16, hidden, d, T, k, d, f)
+    assert got["status"] == 0
+    assert not np.any(parts == UNWRITTEN)
+    ref = oracle.grouped_route_partials(got["sorted"].astype(oracle.PAIR_DTYPE), hidden, d,
+                                        *_oracle_pool(pool_bytes, offs, stride), k, d, f, T)
+    rel = oracle.rel_error(from_f16_bits(parts), from_f16_bits(ref))
+    assert rel < TOL, f"partials rel={rel}"
+
+
+def test_grouped_repeat_on_one_grouping(ctx, stream):
+    # the grouped launches take their units from counters in the grouping
+    # state and leave them zero: two calls on one grouping give the same
+    # bits, every row written both times
+    T, k, E, d, f = 256, 8, 64, 256, 128
+    pool_bytes, offs, stride = synth.expert_pool(6, "repeat/experts", E, d, f)
+    idx, w16 = synth.zipf_routing(6, "repeat/route", T, E, k)
+    hidden = _dev(synth.f16_vector(6, "repeat/x", T * d))
+    got, bufs = _device_group(ctx, stream, idx, w16, T, k, E)
+    assert got["status"] == 0 and np.all(got["state"][1:] == 0)
+    pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs)
+    outs = []
+    for _ in range(2):
+        act = _dev(np.full(T * k * f, UNWRITTEN, np.uint16))
+        partials = _dev(np.full(T * k * d, UNWRITTEN, np.uint16))
+        ops.PrefillGroupedRoutedMoE(ctx).encode(stream, pool, bufs["sorted"], bufs["tiles"], bufs["n_tiles"],
+                                                ops.max_tiles(T, k, E), hidden, d, d, f, k, act, partials)
+        stream.sync()
+        state = bufs["n_tiles"].download(np.uint32, ops.GROUP_STATE_BYTES // 4)
+        assert state[0] == got["n_tiles"] and np.all(state[1:] == 0), state
+        outs.append((act.download(np.uint16), partials.download(np.uint16)))
+    for a, p in outs:
+        assert not np.any(a == UNWRITTEN) and not np.any(p == UNWRITTEN)
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
 
 
 def test_moe_prefill_end_to_end(ctx, stream):
