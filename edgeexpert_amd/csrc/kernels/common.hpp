@@ -50,12 +50,16 @@ __device__ __forceinline__ float seg_sum(float v) {
 
 // gelu_pytorch_tanh with the inner argument clamped to ±20
 // (S/Metal/MoE/moe.metal:53-60; the clamp is exact at fp32 saturation).
+// GELU, tanh form: 0.5·x·(1 + tanh(z)), z = sqrt(2/pi)·(x + 0.044715·x^3),
+// evaluated as x / (1 + e^(-2z)) (the same function: 0.5·(1 + tanh z) is
+// the logistic of 2z) with the hardware exp2 and reciprocal, ~1e-7
+// relative. Large negative x: e^(-2z) overflows to inf and the result is
+// -0; large positive x: x.
 __device__ __forceinline__ float gelu_tanh(float x) {
-    const float c = 0.7978845608028654f;
-    const float k3 = 0.044715f;
-    float inner = c * (x + k3 * x * x * x);
-    inner = fminf(fmaxf(inner, -20.0f), 20.0f);
-    return 0.5f * x * (1.0f + tanhf(inner));
+    constexpr float kC = -2.0f * 0.7978845608028654f * 1.4426950408889634f;   // -2·sqrt(2/pi)·log2(e)
+    constexpr float kC3 = kC * 0.044715f;
+    const float e = __builtin_amdgcn_exp2f(x * fmaf(kC3, x * x, kC));
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 __device__ __forceinline__ uint4 ldg16(const uint8_t* p) {

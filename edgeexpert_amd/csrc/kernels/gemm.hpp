@@ -34,6 +34,11 @@ __device__ __forceinline__ h8 perm_0415(h8 v) {
     return __builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7);
 }
 
+// Permute one 8-element run from natural order to (0,2,1,3,4,6,5,7).
+__device__ __forceinline__ h8 perm_0213(h8 v) {
+    return __builtin_shufflevector(v, v, 0, 2, 1, 3, 4, 6, 5, 7);
+}
+
 // 8 bf16 -> 8 fp16 (exact inside the fp16 normal range).
 __device__ __forceinline__ h8 bf16x8_to_f16(uint4 raw) {
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -389,8 +394,8 @@ __device__ __forceinline__ DequantConsts<BITS> dequant_consts() {
     DequantConsts<BITS> dc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        if (BITS == 4 && i >= 2) {
-            dc.magic[i] = dc.magic[i - 2];
+        if (BITS == 4) {
+            dc.magic[i] = 0;                 // the 4-bit path converts through FP8
         } else {
             uint32_t v;
             asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "i"(DqField<BITS>::magic(i)));
@@ -400,28 +405,55 @@ __device__ __forceinline__ DequantConsts<BITS> dequant_consts() {
     return dc;
 }
 
-// Word j of a chunk (codes 8j..8j+7, in the order 8j+0, +4, +1, +5, +2, +6,
-// +3, +7) dequantised as fp16(q·s + b) with one rounding, s and b from one
-// table word (scale | bias << 16).
+// Word j of a chunk (codes 8j..8j+7) dequantised as fp16(q·s + b) with one
+// rounding, s and b from one table word (scale | bias << 16). 4 bits: each
+// code lands in the low nibble of a byte (word & 0x0F0F0F0F and its shift by
+// 4), which read as an FP8 E4M3 number is q·2^-9 exactly (q < 8: subnormal
+// q·2^-9; q >= 8: exponent field 1, (8 + (q-8))·2^-9); the gfx950
+// conversion v_cvt_scalef32_pk_f16_fp8 with scale 2^9 turns two of them
+// into the fp16 pair q exactly, in the code order (0,2,1,3,4,6,5,7)
+// (unit_b_order). 2 and 3 bits: the fields of DqField, in the order
+// (0,4,1,5,2,6,3,7).
 template <int BITS>
 __device__ __forceinline__ h8 dequant_word_sb(const QChunk<BITS>& w, int j, uint32_t sb, const DequantConsts<BITS>& dc) {
     const h2 s2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x01000100u));
     const h2 b2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x03020302u));
     uint32_t t = block_word<BITS>(w, j);
-    if constexpr (BITS != 4) asm("" : "+v"(t));
-    const uint32_t t8 = t >> 8;
     h8 run;
+    if constexpr (BITS == 4) {
+        const uint32_t lo = t & 0x0F0F0F0Fu, hi = (t >> 4) & 0x0F0F0F0Fu;
+        const h2 q[4] = {__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false),   // codes 0, 2
+                         __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false),   // 1, 3
+                         __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true),    // 4, 6
+                         __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true)};   // 5, 7
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        using F = DqField<BITS>;
-        const uint32_t src = F::shift(i) ? t8 : t;
-        const uint32_t q = (src & F::mask(i)) | dc.magic[i];
-        const h2 base = {(_Float16)F::base(i), (_Float16)F::base(i)};
-        const h2 wv = __builtin_elementwise_fma(__builtin_bit_cast(h2, q) - base, s2, b2);   // exact q, one rounding
-        run[2 * i] = wv[0];
-        run[2 * i + 1] = wv[1];
+        for (int i = 0; i < 4; ++i) {
+            const h2 wv = __builtin_elementwise_fma(q[i], s2, b2);             // one rounding
+            run[2 * i] = wv[0];
+            run[2 * i + 1] = wv[1];
+        }
+    } else {
+        asm("" : "+v"(t));
+        const uint32_t t8 = t >> 8;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            using F = DqField<BITS>;
+            const uint32_t src = F::shift(i) ? t8 : t;
+            const uint32_t q = (src & F::mask(i)) | dc.magic[i];
+            const h2 base = {(_Float16)F::base(i), (_Float16)F::base(i)};
+            const h2 wv = __builtin_elementwise_fma(__builtin_bit_cast(h2, q) - base, s2, b2);   // exact q, one rounding
+            run[2 * i] = wv[0];
+            run[2 * i + 1] = wv[1];
+        }
     }
     return run;
+}
+
+// The activation order that matches dequant_word_sb's code order.
+template <int BITS>
+__device__ __forceinline__ h8 unit_b_order(h8 v) {
+    if constexpr (BITS == 4) return perm_0213(v);
+    else return perm_0415(v);
 }
 
 // dequant_chunk_f16_v with the scale and bias taken from one table word.

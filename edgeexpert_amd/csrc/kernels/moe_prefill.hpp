@@ -291,7 +291,7 @@ __device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wrow)[RT],
         const bool live = 128u * m + 8u * xcol < K;
 #pragma unroll
         for (uint32_t p = 0; p < PIECES; ++p) {
-            const h8 v = live ? perm_0415(__builtin_bit_cast(h8, src[p])) : h8{};
+            const h8 v = live ? unit_b_order<BITS>(__builtin_bit_cast(h8, src[p])) : h8{};
             *reinterpret_cast<h8*>(buf + (16u * p + (tid >> 4)) * kUnitStride + 8u * xcol) = v;
         }
     };
