@@ -236,6 +236,30 @@ __device__ __forceinline__ QChunk<BITS> ldg_chunk(const uint8_t* row, uint32_t c
     return q;
 }
 
+// Plain load of the chunk at byte offset off of a block-uniform base: the
+// 32-bit offset keeps the address in one vector register over the scalar
+// base (the scalar-base form of global_load).
+template <int BITS>
+__device__ __forceinline__ QChunk<BITS> ldg_chunk_at(const uint8_t* __restrict__ base, uint32_t off) {
+    QChunk<BITS> q;
+    if constexpr (BITS == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(base + off);
+        q.w[0] = v.x;
+        q.w[1] = v.y;
+        q.w[2] = v.z;
+        q.w[3] = v.w;
+    } else if constexpr (BITS == 2) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(base + off);
+        q.w[0] = v.x;
+        q.w[1] = v.y;
+    } else {
+        static_assert(BITS == 3, "2, 3 or 4 bits");
+#pragma unroll
+        for (int i = 0; i < 3; ++i) q.w[i] = *reinterpret_cast<const uint32_t*>(base + (off + 4u * i));
+    }
+    return q;
+}
+
 // Codes 8j..8j+7 of a chunk in the int4 word form: a word whose low half
 // holds codes 8j..8j+3 and whose high half holds 8j+4..8j+7, at BITS-bit
 // spacing from bit 0 and bit 16 (bits between or above the codes may hold

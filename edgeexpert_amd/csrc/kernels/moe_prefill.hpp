@@ -235,10 +235,11 @@ __device__ __forceinline__ void sfor_w(Fn&& f) {
 // activations are staged per k-tile into a double-buffered LDS tile
 // [16·NTT pairs][128 codes + 8] in the unpack order, from a two-deep register
 // ring, one barrier per k-tile; the B lane (pair l%16 of sub-tile j, quarter
-// q) reads its 16 bytes of k-step u at column 32q + 8u. Activation codes past
-// K (a half-filled last k-tile) are staged as zeros; the weights there are
-// those of the last chunk (finite), so the products vanish. Weights are
-// dequantised as everywhere else (fp16(q·s + b), one rounding).
+// q) reads its 16 bytes of k-step u at column 32q + 8u. In a half-filled
+// last k-tile the quarters past K dequantise with scale and bias 0 (exact
+// zero weights) against activations staged from column 0 (finite), so they
+// add nothing. Weights are dequantised as everywhere else (fp16(q·s + b),
+// one rounding).
 constexpr uint32_t kGroupWidePairs = 64;          // pairs of a wide unit (a half tile)
 constexpr uint32_t kUnitStride = 128 + 8;         // halves per LDS activation row
 constexpr uint32_t kUnitThreads = 256;            // four wavefronts
@@ -250,14 +251,18 @@ constexpr uint32_t unit_lds_bytes(int RT, int NTT, uint32_t K) {
     return 2u * unit_xbuf(NTT) * 2u + 4u * 64u * (uint32_t)RT * (K / 64u);
 }
 
-// acc[i][j]: row tile i, pair sub-tile j (16x16 D layout: column lane%16 =
-// pair, rows 4·(lane/16) + r). xrow(p): the activation row of pair p
-// (< 16·NTT; past the unit's count: any valid row, not stored). sbt[i]: this
-// lane's row of the scale/bias table, published by the barrier that
-// `publish` runs once the first k-tiles' loads are in flight.
-template <int BITS, int RT, int NTT, int DEPTH, typename XRow, typename Publish>
-__device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wrow)[RT], const uint32_t* const (&sbt)[RT],
-                                               XRow xrow, uint32_t K, _Float16* __restrict__ xs,
+// Global addresses are a block-uniform base (scalar registers) plus a 32-bit
+// per-lane offset, the form that costs one vector register. acc[i][j]: row
+// tile i, pair sub-tile j (16x16 D layout: column lane%16 = pair, rows
+// 4·(lane/16) + r). wbase[i] + woff[i]: this lane's weight row in tile i.
+// xbase + xoff(p) (halves): the activation row of pair p (< 16·NTT; past the
+// unit's count: any valid row, not stored). sbt[i]: this lane's row of the
+// scale/bias table, published by the barrier that `publish` runs once the
+// first k-tiles' loads are in flight.
+template <int BITS, int RT, int NTT, int DEPTH, typename XOff, typename Publish>
+__device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wbase)[RT], const uint32_t (&woff)[RT],
+                                               const uint32_t* const (&sbt)[RT], const uint16_t* __restrict__ xbase,
+                                               XOff xoff, uint32_t K, _Float16* __restrict__ xs,
                                                f32x4 (&acc)[RT][NTT], Publish publish, uint32_t tid) {
     const uint32_t lane = tid & 63u, q = lane >> 4, r16 = lane & 15u;
     const uint32_t nch = K >> 5, nk = (nch + 3u) >> 2;
@@ -269,39 +274,40 @@ __device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wrow)[RT],
 #pragma unroll
         for (int j = 0; j < NTT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     // activation piece p of this thread: pair 16p + tid/16, 16-byte column tid % 16
-    const uint16_t* xr_row[PIECES];
+    uint32_t xr_off[PIECES];
 #pragma unroll
-    for (uint32_t p = 0; p < PIECES; ++p) xr_row[p] = xrow(16u * p + (tid >> 4));
+    for (uint32_t p = 0; p < PIECES; ++p) xr_off[p] = xoff(16u * p + (tid >> 4));
     const uint32_t xcol = tid & 15u;
     QChunk<BITS> wr[DEPTH][RT];
     uint4 xr[2][PIECES];
     auto load_w = [&](uint32_t m, QChunk<BITS> (&dst)[RT]) {
         const uint32_t c = 4u * m + q, cc = c < nch ? c : nch - 1;
 #pragma unroll
-        for (int i = 0; i < RT; ++i) dst[i] = ldg_chunk<BITS, false>(wrow[i], cc);
+        for (int i = 0; i < RT; ++i) dst[i] = ldg_chunk_at<BITS>(wbase[i], woff[i] + 4u * BITS * cc);
     };
-    // columns past K load a valid piece and are stored as zeros
+    // columns past K load column 0 (in bounds; their weights are zero)
     auto load_x = [&](uint32_t m, uint4 (&dst)[PIECES]) {
         const uint32_t col = 128u * (m < nk ? m : nk - 1) + 8u * xcol;
         const uint32_t cc = col < K ? col : 0u;
 #pragma unroll
-        for (uint32_t p = 0; p < PIECES; ++p) dst[p] = *reinterpret_cast<const uint4*>(xr_row[p] + cc);
+        for (uint32_t p = 0; p < PIECES; ++p) dst[p] = *reinterpret_cast<const uint4*>(xbase + (xr_off[p] + cc));
     };
-    auto store_x = [&](uint32_t m, const uint4 (&src)[PIECES], _Float16* buf) {
-        const bool live = 128u * m + 8u * xcol < K;
+    auto store_x = [&](const uint4 (&src)[PIECES], _Float16* buf) {
 #pragma unroll
-        for (uint32_t p = 0; p < PIECES; ++p) {
-            const h8 v = live ? unit_b_order<BITS>(__builtin_bit_cast(h8, src[p])) : h8{};
-            *reinterpret_cast<h8*>(buf + (16u * p + (tid >> 4)) * kUnitStride + 8u * xcol) = v;
-        }
+        for (uint32_t p = 0; p < PIECES; ++p)
+            *reinterpret_cast<h8*>(buf + (16u * p + (tid >> 4)) * kUnitStride + 8u * xcol) =
+                unit_b_order<BITS>(__builtin_bit_cast(h8, src[p]));
     };
     // per k-step u: the NTT B operands read together, the RT A operands
-    // dequantised from their block words, then RT·NTT MFMAs
+    // dequantised from their block words, then RT·NTT MFMAs. A quarter past
+    // K (a half-filled last k-tile) takes scale and bias 0: its weights are
+    // exact zeros, and the (finite) activations staged there from column 0
+    // add nothing.
     auto compute = [&](uint32_t m, const QChunk<BITS> (&w)[RT], const _Float16* buf) {
         const uint32_t c = 4u * m + q, g = (c < nch ? c : nch - 1) >> 1;
         uint32_t sb[RT];
 #pragma unroll
-        for (int i = 0; i < RT; ++i) sb[i] = sbt[i][g];
+        for (int i = 0; i < RT; ++i) sb[i] = c < nch ? sbt[i][g] : 0u;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             h8 b[NTT];
@@ -325,7 +331,7 @@ __device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wrow)[RT],
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) load_w((uint32_t)d, wr[d]);
     publish();                                   // the scale/bias table (ends with a barrier)
-    store_x(0, xr[0], xs);
+    store_x(xr[0], xs);
     load_x(2, xr[0]);
     __syncthreads();
     // step m: k-tile m from buffer m%2 and ring stage m%DEPTH; stage k-tile
@@ -334,7 +340,7 @@ __device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wrow)[RT],
     auto step = [&](uint32_t m, auto st_c, auto pa_c) {
         constexpr int ST = decltype(st_c)::value, PA = decltype(pa_c)::value;
         compute(m, wr[ST], xs + PA * XB);
-        store_x(m + 1, xr[PA ^ 1], xs + (PA ^ 1) * XB);
+        store_x(xr[PA ^ 1], xs + (PA ^ 1) * XB);
         load_w(m + DEPTH, wr[ST]);
         load_x(m + 3, xr[PA ^ 1]);
         __syncthreads();
@@ -374,21 +380,22 @@ __device__ __forceinline__ void unit_gate_up(const ExpertPool& pool, const Pair*
     const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
     const ExpertOffsets& o = pool.off;
     uint32_t* sb_lds = reinterpret_cast<uint32_t*>(unit_lds + 2u * unit_xbuf(NTT));
-    const uint8_t* wrow[RT];
+    const uint8_t* wbase[RT];
+    uint32_t woff[RT];
     const uint32_t* sbt[RT];
 #pragma unroll
     for (uint32_t i = 0; i < HT; ++i) {
         const uint32_t f = fb + 16u * i + r16, fc = f < F ? f : F - 1;   // features past F: clamped, not stored
-        wrow[i] = blob + o.gate_w + (size_t)fc * row_bytes;
-        wrow[HT + i] = blob + o.up_w + (size_t)fc * row_bytes;
+        wbase[i] = blob + o.gate_w;
+        wbase[HT + i] = blob + o.up_w;
+        woff[i] = woff[HT + i] = fc * row_bytes;
         sbt[i] = sb_lds + (fc - f_blk) * G;
         sbt[HT + i] = sb_lds + (NF + fc - f_blk) * G;
     }
     f32x4 acc[RT][NTT];
     unit_rows_loop<BITS, RT, NTT, unit_depth<RT>()>(
-        wrow, sbt,
-        [&](uint32_t p) { return hidden + (size_t)sorted[gr.first + (p < gr.count ? p : 0u)].token * stride; }, D,
-        unit_lds, acc,
+        wbase, woff, sbt, hidden,
+        [&](uint32_t p) { return sorted[gr.first + (p < gr.count ? p : 0u)].token * stride; }, D, unit_lds, acc,
         [&]() {
             const uint32_t nf = F - f_blk < NF ? F - f_blk : NF;
             copy_sb_to_lds<kUnitThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f_blk * G,
@@ -431,12 +438,14 @@ __device__ __forceinline__ void unit_down(const ExpertPool& pool, const Pair* __
     const uint8_t* blob = pool.base + (uint64_t)gr.expert * pool.stride;
     const ExpertOffsets& o = pool.off;
     uint32_t* sb_lds = reinterpret_cast<uint32_t*>(unit_lds + 2u * unit_xbuf(NTT));
-    const uint8_t* wrow[RT];
+    const uint8_t* wbase[RT];
+    uint32_t woff[RT];
     const uint32_t* sbt[RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
         const uint32_t d = db + 16u * i + r16, dc = d < D ? d : D - 1;   // rows past D: clamped, not stored
-        wrow[i] = blob + o.down_w + (size_t)dc * row_bytes;
+        wbase[i] = blob + o.down_w;
+        woff[i] = dc * row_bytes;
         sbt[i] = sb_lds + (dc - d_blk) * G;
     }
     uint32_t dst_row[NTT];          // partials row of each pair, loaded before the K loop
@@ -448,8 +457,7 @@ __device__ __forceinline__ void unit_down(const ExpertPool& pool, const Pair* __
     }
     f32x4 acc[RT][NTT];
     unit_rows_loop<BITS, RT, NTT, unit_depth<RT>()>(
-        wrow, sbt, [&](uint32_t p) { return act + (size_t)(gr.first + (p < gr.count ? p : 0u)) * F; }, F, unit_lds,
-        acc,
+        wbase, woff, sbt, act, [&](uint32_t p) { return (gr.first + (p < gr.count ? p : 0u)) * F; }, F, unit_lds, acc,
         [&]() {
             const uint32_t nd = D - d_blk < NR ? D - d_blk : NR;
             copy_sb_to_lds<kUnitThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)d_blk * G,
