@@ -797,6 +797,12 @@ public:
         if (T == 0 || k == 0 || d == 0) return fail(TFQ_E_INVAL, "empty reduce");
         if (!partials || !w || !h2) return fail(TFQ_E_INVAL, "null pointer argument");
         void* args[] = {&partials, &w, &h2, &T, &k, &d};
+        // 8 outputs per thread when rows allow 16-byte accesses
+        if (d % 8 == 0 && aligned(partials, 16) && aligned(h2, 16)) {
+            const uint64_t n = (uint64_t)T * (d / 8);
+            if (n > 0xFFFFFFFFull) return fail(TFQ_E_UNSUPPORTED, "reduce of %llu outputs", (unsigned long long)n * 8);
+            return launch2(m_, "tfq_moe_combine_x8", (uint32_t)((n + 255) / 256), 1, 256, 0, stream, args);
+        }
         return launch2(m_, "tfq_moe_combine", (d + 255) / 256, T, 256, 0, stream, args);
     }
 

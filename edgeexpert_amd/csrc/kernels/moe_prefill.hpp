@@ -24,6 +24,7 @@ constexpr uint32_t kGroupMaxExperts = 256;
 constexpr uint32_t kGroupChunks = kGroupMaxPairs / 64;
 constexpr uint32_t kGroupThreads = 1024;
 constexpr uint32_t kGroupStateWords = 4;       // TFQ_MOE_GROUP_STATE_WORDS
+constexpr uint32_t kGroupSegments = 8;         // chunk segments of the per-expert scan
 // status codes (the PrefillMoEGroupingError cases the device can detect)
 constexpr uint32_t kGroupOk = 0;
 constexpr uint32_t kGroupExpertOutOfRange = 8;
@@ -70,6 +71,7 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
     __shared__ uint16_t cnt[kGroupChunks][kGroupMaxExperts];
     __shared__ uint8_t rank_in_chunk[kGroupMaxPairs];
     __shared__ uint32_t base[kGroupMaxExperts], tot[kGroupMaxExperts], tile_base[kGroupMaxExperts + 1];
+    __shared__ uint32_t seg_sum[kGroupSegments][kGroupMaxExperts];
     __shared__ uint32_t bad;
     constexpr uint32_t kPer = kGroupMaxPairs / kGroupThreads;     // pairs per thread (8)
     const uint32_t tid = threadIdx.x;
@@ -132,15 +134,32 @@ __device__ __forceinline__ void moe_group(const uint32_t* __restrict__ idx, cons
         }
     }
     __syncthreads();
-    // per expert: exclusive scan over the chunks (in chunk order)
-    for (uint32_t e = tid; e < E; e += kGroupThreads) {
-        uint32_t run = 0;
-        for (uint32_t c = 0; c < nchunks; ++c) {
-            const uint32_t v = cnt[c][e];
-            cnt[c][e] = (uint16_t)run;
-            run += v;
+    // per expert: exclusive scan over the chunks (in chunk order), in S
+    // segments of chunks: thread (segment sg, expert e) sums its segment,
+    // adds the sums of the segments before it and rewrites its counts as
+    // offsets (lanes of a wavefront take consecutive experts of one segment)
+    {
+        const uint32_t ep = E > 1 ? 1u << (32 - __clz((int)(E - 1))) : 1u;   // E rounded up to a power of two
+        const uint32_t S = kGroupThreads / ep < kGroupSegments ? kGroupThreads / ep : kGroupSegments;
+        const uint32_t e = tid % ep, sg = tid / ep, per = (nchunks + S - 1) / S;
+        const uint32_t c0 = sg * per, c1 = c0 + per < nchunks ? c0 + per : nchunks;
+        const bool mine = e < E && sg < S;
+        uint32_t part = 0;
+        if (mine) {
+            for (uint32_t c = c0; c < c1; ++c) part += cnt[c][e];
+            seg_sum[sg][e] = part;
         }
-        tot[e] = run;
+        __syncthreads();
+        if (mine) {
+            uint32_t run = 0;
+            for (uint32_t t = 0; t < sg; ++t) run += seg_sum[t][e];
+            for (uint32_t c = c0; c < c1; ++c) {
+                const uint32_t v = cnt[c][e];
+                cnt[c][e] = (uint16_t)run;
+                run += v;
+            }
+            if (sg == S - 1) tot[e] = run;
+        }
     }
     __syncthreads();
     // exclusive scans over the experts of the pair counts and tile counts:
@@ -513,15 +532,19 @@ __device__ __forceinline__ UnitPlan plan_units(const Tile* __restrict__ tiles, c
     static_assert(kGroupMaxTiles % 64u == 0, "whole wavefront passes");
     if (threadIdx.x < 64u) {
         const uint32_t lane = threadIdx.x;
-        uint32_t n = *n_tiles;
-        n = n < max_tiles ? n : max_tiles;
-        n = n < kGroupMaxTiles ? n : kGroupMaxTiles;
+        // the tile count and the tiles up to the launch bound in flight together
+        const uint32_t nt = *n_tiles;
+        const uint32_t mt = max_tiles < kGroupMaxTiles ? max_tiles : kGroupMaxTiles;
         Tile tl[C];
 #pragma unroll
         for (uint32_t c = 0; c < C; ++c) {
             const uint32_t t = 64u * c + lane;
-            tl[c] = t < n ? tiles[t] : Tile{0u, 0u, 0u, 0u};
+            tl[c] = t < mt ? tiles[t] : Tile{0u, 0u, 0u, 0u};
         }
+        const uint32_t n = nt < mt ? nt : mt;
+#pragma unroll
+        for (uint32_t c = 0; c < C; ++c)
+            if (64u * c + lane >= n) tl[c].count = 0;
         // per tile the entries of each class, two classes per word (16 bits
         // each: at most kGroupMaxEntries), scanned over the tiles in order
         uint32_t pre_w[C], pre_s[C], carry_w = 0, carry_s = 0;
@@ -660,6 +683,29 @@ __device__ __forceinline__ void moe_combine(const uint16_t* __restrict__ partial
     for (uint32_t r = 0; r < k; ++r)
         acc = fmaf(h2f(w[t * k + r]), h2f(partials[((size_t)t * k + r) * D + d]), acc);
     h2[(size_t)t * D + d] = f2h(acc);
+}
+
+// moe_combine over 8 outputs per thread (16-byte loads and stores): D % 8 ==
+// 0, partials and h2 16-byte aligned. Thread i: token i / (D/8), outputs
+// 8·(i mod D/8) .. +7; the same rank-order fmas as moe_combine. Grid:
+// ceil(T·D/8 / 256).
+__device__ __forceinline__ void moe_combine_x8(const uint16_t* __restrict__ partials,
+                                               const uint16_t* __restrict__ w, uint16_t* __restrict__ h2,
+                                               uint32_t T, uint32_t k, uint32_t D) {
+    const uint32_t n8 = D >> 3, i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= T * n8) return;
+    const uint32_t t = i / n8, d = 8u * (i - t * n8);
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t r = 0; r < k; ++r) {
+        const float wr = h2f(w[t * k + r]);
+        const h8 v = __builtin_bit_cast(h8, *reinterpret_cast<const uint4*>(partials + ((size_t)t * k + r) * D + d));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(wr, (float)v[e], acc[e]);
+    }
+    h8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (_Float16)acc[e];
+    *reinterpret_cast<uint4*>(h2 + (size_t)t * D + d) = __builtin_bit_cast(uint4, out);
 }
 
 }  // namespace tfq

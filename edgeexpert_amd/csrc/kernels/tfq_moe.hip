@@ -18,3 +18,9 @@ extern "C" __global__ __launch_bounds__(256) void tfq_moe_combine(const uint16_t
                                                                   uint32_t T, uint32_t k, uint32_t D) {
     moe_combine(partials, w, h2, T, k, D);
 }
+
+extern "C" __global__ __launch_bounds__(256) void tfq_moe_combine_x8(const uint16_t* partials,
+                                                                     const uint16_t* w, uint16_t* h2,
+                                                                     uint32_t T, uint32_t k, uint32_t D) {
+    moe_combine_x8(partials, w, h2, T, k, D);
+}
