@@ -22,7 +22,6 @@ constexpr uint32_t kProjMaxK = 8192;       // longest reduction (gemm.hpp kProjM
 constexpr uint32_t kUnitThreads = 256;          // grouped MoE units (moe_prefill.hpp)
 constexpr uint32_t kUnitStride = 128 + 8;       // halves per LDS activation row of a unit
 constexpr uint32_t kGroupMaxTiles = 8192 / 128 + 256;  // tiles the device planner takes (moe_prefill.hpp)
-constexpr uint32_t proj_lds_bytes(uint32_t k) { return 2u * kProjBM * 72u * 2u + 2u * kProjBN * (k / 64u) * 2u; }
 // the pipelined tile of the prefill GEMM (gemm.hpp proj_pl_lds_bytes)
 constexpr uint32_t proj_pl_lds_bytes(uint32_t k) { return 3u * kProjBM * 72u * 2u + 4u * kProjBN * (k / 64u); }
 static_assert(proj_pl_lds_bytes(kProjMaxK) <= 160u * 1024u, "pipelined tile exceeds the LDS of a CU");

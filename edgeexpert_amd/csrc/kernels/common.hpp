@@ -254,8 +254,11 @@ __device__ __forceinline__ QChunk<BITS> ldg_chunk_at(const uint8_t* __restrict__
         q.w[1] = v.y;
     } else {
         static_assert(BITS == 3, "2, 3 or 4 bits");
+        // one pointer for the three words, so that they merge into one
+        // 12-byte load (three 32-bit offsets could wrap apart)
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(base + off);
 #pragma unroll
-        for (int i = 0; i < 3; ++i) q.w[i] = *reinterpret_cast<const uint32_t*>(base + (off + 4u * i));
+        for (int i = 0; i < 3; ++i) q.w[i] = w[i];
     }
     return q;
 }

@@ -7,12 +7,14 @@
 // 3-bit and 2-bit rows (prefill.metal:711-757,1223-1450) run the same tiles
 // with the chunk load and unpack of common.hpp (template parameter BITS).
 //
-// Weights are dequantised in registers: (0x6400 | q) - 1024 gives q exactly
-// as fp16, then v_pk_fma_f16(q, s, b) rounds q·s + b once to fp16 — the fp16
-// weight tile the reference's tensor-op kernel stages (tensorops.metal:57-80).
-// Within every 8-element run along K the unpack yields element order
-// (0,4,1,5,2,6,3,7); X is stored with the same permutation, so each MFMA
-// k-slice pairs the right operands (a dot product is order-free).
+// Weights are dequantised in registers to fp16(q·s + b) with one rounding
+// (v_pk_fma_f16 of the exact code q, the scale and the bias) — the fp16
+// weight tile the reference's tensor-op kernel stages
+// (tensorops.metal:57-80); dequant_word_sb gives the code order inside each
+// 8-element run along K (4 bits: (0,2,1,3,4,6,5,7), through the gfx950 FP8
+// conversion; 2 and 3 bits: (0,4,1,5,2,6,3,7)), and X is stored with the
+// same permutation (unit_b_order), so each MFMA k-slice pairs the right
+// operands (a dot product is order-free).
 // bf16 activations are converted to fp16 while staging; the conversion is
 // exact for |x| in [2^-14, 65504] (the range of the reference's fp16 path).
 #pragma once
@@ -53,123 +55,24 @@ __device__ __forceinline__ h8 bf16x8_to_f16(uint4 raw) {
     return out;
 }
 
-// ------------------------------------------------ projection GEMM tile ----
+// ------------------------------------------------------ projection tile ----
 //
-// The weights never pass through LDS: block tile 64 tokens x 256 outputs, four
-// wavefronts, wave w owning outputs 64w..64w+63 for all 64 tokens as 2x2
-// v_mfma_f32_32x32x16_f16 tiles. The MFMA B operand of a 32-output sub-tile
-// is 8 consecutive k of one output row per lane, so each lane loads its own
-// row's 16 bytes of a group (lane half h: bytes 16h..16h+15, k-step s uses
-// word s) straight into registers, kProjDepth groups ahead (a register
-// ring), and dequantises them into B operands just before its MFMAs; nothing
-// else reads them, so they need no LDS and no barrier. The block's scales and
-// biases (256 rows x K/64 groups each, one contiguous range per array) are
-// copied to LDS once at the start. The activations, shared by all four
-// waves, are converted (bf16 -> fp16) and permuted once per block into a
-// double-buffered LDS tile (one barrier per group). Per group a wave issues
-// 16 MFMAs and reads 8 KB of LDS.
-//
-// Every global load in the loop is unconditional (groups past the end
-// re-read the last group, token rows past the end read row 0 and are zeroed
-// when staged) and the ring holds only 16-byte registers: with a fixed load
-// count per step the compiler waits for exactly the group it consumes.
-// Copies `count` halves of two arrays into LDS: 16-byte loads when both
-// sources are 16-byte aligned and count % 8 == 0 (else 2-byte loads), up to
-// eight loads per thread and array issued before the first store, so the
-// copy costs one memory latency per 8·NT chunks.
-template <uint32_t NT>
-__device__ __forceinline__ void copy_pair_to_lds(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
-                                                 uint16_t* __restrict__ da, uint16_t* __restrict__ db,
-                                                 uint32_t count) {
-    constexpr uint32_t U = 8;
-    if (((((uintptr_t)a) | ((uintptr_t)b)) & 15u) == 0 && (count & 7u) == 0) {
-        const uint32_t n16 = count >> 3;
-        const uint4* sa = reinterpret_cast<const uint4*>(a);
-        const uint4* sb = reinterpret_cast<const uint4*>(b);
-        uint4* ta = reinterpret_cast<uint4*>(da);
-        uint4* tb = reinterpret_cast<uint4*>(db);
-        for (uint32_t base = 0; base < n16; base += U * NT) {
-            uint4 va[U], vb[U];
-#pragma unroll
-            for (uint32_t u = 0; u < U; ++u) {
-                const uint32_t i = base + u * NT + threadIdx.x;
-                const uint32_t c = i < n16 ? i : n16 - 1;
-                va[u] = sa[c];
-                vb[u] = sb[c];
-            }
-#pragma unroll
-            for (uint32_t u = 0; u < U; ++u) {
-                const uint32_t i = base + u * NT + threadIdx.x;
-                if (i < n16) {
-                    ta[i] = va[u];
-                    tb[i] = vb[u];
-                }
-            }
-        }
-    } else {
-        for (uint32_t base = 0; base < count; base += U * NT) {
-            uint16_t va[U], vb[U];
-#pragma unroll
-            for (uint32_t u = 0; u < U; ++u) {
-                const uint32_t i = base + u * NT + threadIdx.x;
-                const uint32_t c = i < count ? i : count - 1;
-                va[u] = a[c];
-                vb[u] = b[c];
-            }
-#pragma unroll
-            for (uint32_t u = 0; u < U; ++u) {
-                const uint32_t i = base + u * NT + threadIdx.x;
-                if (i < count) {
-                    da[i] = va[u];
-                    db[i] = vb[u];
-                }
-            }
-        }
-    }
-}
-
+// The weights never pass through LDS: each lane loads its own row's 16 bytes
+// of a group (the MFMA B operand of a 32-output sub-tile is 8 consecutive k
+// of one output row per lane; lane half h: bytes 16h..16h+15, k-step s uses
+// word s) straight into a register ring kProjDepth groups ahead, and
+// dequantises them into B operands just before its MFMAs. The block's scales
+// and biases are copied to LDS once at the start; the activations, shared
+// by all waves, are converted (bf16 -> fp16) and permuted once per block
+// into LDS. Every global load in the loop is unconditional (groups past the
+// end re-read the last group, token rows past the end read row 0 and are
+// not stored), so the compiler waits for exactly the group it consumes.
 constexpr uint32_t kProjBM = 64;
 constexpr uint32_t kProjBN = 256;
 constexpr uint32_t kProjThreads = 256;
 constexpr uint32_t kProjGemmThreads = 512;   // the prefill GEMM's eight-wave tile
 constexpr uint32_t kProjDepth = 4;          // weight groups in flight per wave (register ring)
-constexpr uint32_t kProjXDepth = 2;         // activation groups in flight (mostly L2 hits)
-constexpr uint32_t kProjMaxK = 8192;        // scale/bias LDS: 2 x 256 x K/64 halves
-
-// Dynamic LDS of the projection tile: X double buffer, then scales, biases.
-constexpr uint32_t proj_lds_bytes(uint32_t K) {
-    return 2u * kProjBM * kGemmLdsStride * 2u + 2u * kProjBN * (K / 64u) * 2u;
-}
-
-// Dequantises the 32 codes of one chunk (16 bytes at 4 bits, 12 at 3, 8 at
-// 2) into 4 runs of 8 fp16 weights (order 0,4,1,5,2,6,3,7 inside each run),
-// with the fp16 exponent pattern held in a VGPR so that each code pair costs
-// one v_and_or_b32 (gfx9 VOP3 takes no literal and one scalar operand). Run
-// j is block_word(j): codes 8j+i and 8j+i+4 at bit BITS·i of its halves.
-template <int BITS>
-__device__ __forceinline__ void dequant_chunk_f16_v(const QChunk<BITS>& w, uint16_t s_bits, uint16_t b_bits,
-                                                    uint32_t magic_v, h8 (&out)[4]) {
-    constexpr uint32_t MA = ((1u << BITS) - 1u) * 0x00010001u;
-    const _Float16 s = __builtin_bit_cast(_Float16, s_bits);
-    const _Float16 b = __builtin_bit_cast(_Float16, b_bits);
-    const h2 s2 = {s, s}, b2 = {b, b};
-    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        uint32_t t = block_word<BITS>(w, j);
-        if constexpr (BITS != 4) asm("" : "+v"(t));
-        h8 run;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t q = ((t >> (BITS * i)) & MA) | magic_v;
-            const h2 qh = __builtin_bit_cast(h2, q) - k1024;             // exact q pair
-            const h2 wv = __builtin_elementwise_fma(qh, s2, b2);         // one rounding
-            run[2 * i] = wv[0];
-            run[2 * i + 1] = wv[1];
-        }
-        out[j] = run;
-    }
-}
+constexpr uint32_t kProjMaxK = 8192;        // scale/bias LDS: 256 rows x K/64 words
 
 // What one lane of the projection tile streams: its two weight rows (the
 // wave's 32-output sub-tiles 0 and 1; the lane's 16-byte half of each
@@ -181,133 +84,10 @@ struct ProjLanes {
     uint32_t sidx1;
 };
 
-// The K loop of the projection tile (all 256 threads): acc[i][j] receives the
-// 32x32 product of token sub-tile i (rows 32i.. of the block's 64; MI = 1:
-// only the first 32 rows, half the MFMAs and activation reads, for blocks
-// with at most 32 valid rows) and the wave's output sub-tile j. lds: the tile's dynamic LDS (X double buffer,
-// then the s/b table, filled by the caller before the call and synchronised
-// by the first barrier inside); xp: this thread's activation row (token row
-// tid/4 of the block, already clamped to a valid row) + 16·(tid%4) halves.
-template <bool X_BF16, int MI = 2, int BITS = 4>
-__device__ __forceinline__ void proj_core(f32x16 (&acc)[MI][2], _Float16* lds, const uint16_t* s_lds,
-                                          const uint16_t* b_lds, const ProjLanes& pl,
-                                          const uint16_t* __restrict__ xp, uint32_t G) {
-    _Float16* xs0 = lds;
-    _Float16* xs1 = lds + kProjBM * kGemmLdsStride;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u;
-    const uint32_t h = lane >> 5, col = lane & 31u;
-    const uint32_t xrow = tid >> 2, xq = tid & 3u;
-    uint32_t magic_v;
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_v));
-
-    QChunk<BITS> w0[kProjDepth], w1[kProjDepth];
-    uint4 xa[kProjXDepth], xb[kProjXDepth];
-    auto load_w = [&](uint32_t g, auto st_c) {
-        constexpr int ST = decltype(st_c)::value;
-        const uint32_t gg = g < G ? g : G - 1;
-        w0[ST] = ldg_chunk<BITS, false>(pl.wp0, 2u * gg);   // plain loads: the token tiles of an
-        w1[ST] = ldg_chunk<BITS, false>(pl.wp1, 2u * gg);   // output slice share them through L2
-    };
-    auto load_x = [&](uint32_t g, auto st_c) {
-        constexpr int ST = decltype(st_c)::value;
-        const uint32_t gg = g < G ? g : G - 1;
-        xa[ST] = ldg16_global(xp + 64u * gg);
-        xb[ST] = ldg16_global(xp + 64u * gg + 8u);
-    };
-    auto store_x = [&](const uint4 va, const uint4 vb, _Float16* buf) {
-        const h8 ha = X_BF16 ? bf16x8_to_f16(va) : __builtin_bit_cast(h8, va);
-        const h8 hb = X_BF16 ? bf16x8_to_f16(vb) : __builtin_bit_cast(h8, vb);
-        *reinterpret_cast<h8*>(&buf[xrow * kGemmLdsStride + 16u * xq]) = perm_0415(ha);
-        *reinterpret_cast<h8*>(&buf[xrow * kGemmLdsStride + 16u * xq + 8u]) = perm_0415(hb);
-    };
-    // B operands of one group: [sub-tile j][k-step s]; two buffers so that the
-    // next group's dequantisation overlaps this group's MFMAs
-    h8 bw[2][2][4];
-    auto dequant = [&](uint32_t g, const QChunk<BITS>& wa, const QChunk<BITS>& wb, h8 (&dst)[2][4]) {
-        const uint32_t gg = g < G ? g : G - 1;
-        dequant_chunk_f16_v(wa, s_lds[pl.sidx0 + gg], b_lds[pl.sidx0 + gg], magic_v, dst[0]);
-        dequant_chunk_f16_v(wb, s_lds[pl.sidx1 + gg], b_lds[pl.sidx1 + gg], magic_v, dst[1]);
-    };
-
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    // Step for group g (compile-time ring stage ST = g % kProjDepth): its B
-    // operands are in bw[ST & 1] (dequantised during the previous step), its
-    // activations in LDS buffer ST & 1. The step refills the weight ring stage
-    // with group g + kProjDepth, runs the 16 MFMAs of group g interleaved with
-    // the dequantisation of group g + 1 and the staging of the activations of
-    // group g + 1 (activation ring stage (g + 1) % 2) into the other LDS
-    // buffer, refills that activation stage with group g + 3, then
-    // synchronises the block.
-    // The main loop runs whole rounds with no branch inside, so the wait
-    // analysis keeps exact load counts; the last K/64 mod kProjDepth groups
-    // take the checked steps after it. Groups past the end are clamped re-reads
-    // whose results nobody uses.
-    auto step = [&](uint32_t g, auto st_c) {
-        constexpr int ST = decltype(st_c)::value;
-        constexpr int NX = (ST + 1) % kProjDepth;
-        constexpr int P = ST & 1;
-        constexpr int XS = (ST + 1) % kProjXDepth;
-        const _Float16* cur = P ? xs1 : xs0;
-        h8 a[MI][4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-                a[i][s] = *reinterpret_cast<const h8*>(&cur[(32u * i + col) * kGemmLdsStride + 32u * h + 8u * s]);
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][s], bw[P][j][s], acc[i][j], 0, 0, 0);
-        dequant(g + 1, w0[NX], w1[NX], bw[P ^ 1]);
-        store_x(xa[XS], xb[XS], P ? xs0 : xs1);
-        load_w(g + kProjDepth, st_c);
-        load_x(g + 3, std::integral_constant<int, XS>{});
-        // interleave: each MFMA followed by a share of the VALU work
-#pragma unroll
-        for (int m = 0; m < 8 * MI; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);    // VALU
-        }
-        // keep the refill loads in this step (the scheduler would otherwise
-        // sink them toward their use and shorten the prefetch)
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-    };
-    load_x(0, std::integral_constant<int, 0>{});
-    load_x(1, std::integral_constant<int, 1>{});
-    load_w(0, std::integral_constant<int, 0>{});
-    load_w(1, std::integral_constant<int, 1>{});
-    load_w(2, std::integral_constant<int, 2>{});
-    load_w(3, std::integral_constant<int, 3>{});
-    store_x(xa[0], xb[0], xs0);
-    load_x(2, std::integral_constant<int, 0>{});
-    __syncthreads();                 // scale/bias table and the first activations
-    dequant(0, w0[0], w1[0], bw[0]);
-    uint32_t g = 0;
-    for (; g + kProjDepth <= G; g += kProjDepth) {
-        step(g, std::integral_constant<int, 0>{});
-        step(g + 1, std::integral_constant<int, 1>{});
-        step(g + 2, std::integral_constant<int, 2>{});
-        step(g + 3, std::integral_constant<int, 3>{});
-    }
-    if (g < G) step(g, std::integral_constant<int, 0>{});
-    if (g + 1 < G) step(g + 1, std::integral_constant<int, 1>{});
-    if (g + 2 < G) step(g + 2, std::integral_constant<int, 2>{});
-}
-
 // ------------------------------------------- pipelined projection tile ----
 //
-// The same tile with every LDS round trip taken off the group's critical
-// path: three activation buffers, so that a group's A operands are read
+// Every LDS round trip is off the group's critical path: three activation
+// buffers, so that a group's A operands are read
 // into registers one step before its MFMAs, and a scale/bias table of one
 // word per (row, group) (scale | bias << 16) read two groups ahead. The only
 // wait left in a step is its closing barrier, by which time the step's own
@@ -456,35 +236,19 @@ __device__ __forceinline__ h8 unit_b_order(h8 v) {
     else return perm_0415(v);
 }
 
-// dequant_chunk_f16_v with the scale and bias taken from one table word.
+// A chunk's four words dequantised with the scale and bias of one table word
+// (dequant_word_sb per word: 4 bits in the code order of unit_b_order<4>).
 template <int BITS>
-__device__ __forceinline__ void dequant_chunk_sb(const QChunk<BITS>& w, uint32_t sb, uint32_t magic_v,
+__device__ __forceinline__ void dequant_chunk_sb(const QChunk<BITS>& w, uint32_t sb, const DequantConsts<BITS>& dc,
                                                  h8 (&out)[4]) {
-    constexpr uint32_t MA = ((1u << BITS) - 1u) * 0x00010001u;
-    const h2 s2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x01000100u));
-    const h2 b2 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb, sb, 0x03020302u));
-    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        uint32_t t = block_word<BITS>(w, j);
-        if constexpr (BITS != 4) asm("" : "+v"(t));
-        h8 run;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t q = ((t >> (BITS * i)) & MA) | magic_v;
-            const h2 qh = __builtin_bit_cast(h2, q) - k1024;             // exact q pair
-            const h2 wv = __builtin_elementwise_fma(qh, s2, b2);         // one rounding
-            run[2 * i] = wv[0];
-            run[2 * i + 1] = wv[1];
-        }
-        out[j] = run;
-    }
+    for (int j = 0; j < 4; ++j) out[j] = dequant_word_sb<BITS>(w, j, sb, dc);
 }
 
 // The K loop of the pipelined tile. J = 32-output sub-tiles per wave: J = 2
-// is the four-wave tile of proj_core; J = 1 runs eight waves (two per SIMD,
-// so one wave's MFMAs overlap another's dequantisation and staging; a
-// single wave does not overlap its own). With J = 1 a wave keeps two
+// runs four waves; J = 1 runs eight waves (two per SIMD, so one wave's
+// MFMAs overlap another's dequantisation and staging; a single wave does
+// not overlap its own). With J = 1 a wave keeps two
 // accumulator sets per token sub-tile (even and odd k-steps, summed at the
 // end): a 32x32 MFMA chain on one accumulator issues at half rate, four
 // independent chains per wave keep the matrix core busy; its A operands are
@@ -505,8 +269,7 @@ __device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds,
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t h = lane >> 5, col = lane & 31u;
     const uint32_t xrow = tid / (64u / XH), xq = tid % (64u / XH);
-    uint32_t magic_v;
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_v));
+    const DequantConsts<BITS> dc = dequant_consts<BITS>();
 
     constexpr int KS = J == 1 ? 2 : 1;                        // accumulator sets (k-step parity)
     constexpr int AB = J == 1 ? 1 : 2;                        // A-operand buffers
@@ -533,7 +296,7 @@ __device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds,
 #pragma unroll
         for (uint32_t u = 0; u < XV; ++u) {
             const h8 hv = X_BF16 ? bf16x8_to_f16(v[u]) : __builtin_bit_cast(h8, v[u]);
-            *reinterpret_cast<h8*>(&dst[xrow * kGemmLdsStride + XH * xq + 8u * u]) = perm_0415(hv);
+            *reinterpret_cast<h8*>(&dst[xrow * kGemmLdsStride + XH * xq + 8u * u]) = unit_b_order<BITS>(hv);
         }
     };
     auto read_a = [&](const _Float16* src, h8 (&dst)[2][4]) {
@@ -550,7 +313,7 @@ __device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds,
     };
     auto dequant = [&](int st, const uint32_t (&sw)[J], h8 (&dst)[J][4]) {
 #pragma unroll
-        for (int j = 0; j < J; ++j) dequant_chunk_sb(wr[j][st], sw[j], magic_v, dst[j]);
+        for (int j = 0; j < J; ++j) dequant_chunk_sb<BITS>(wr[j][st], sw[j], dc, dst[j]);
     };
 
 #pragma unroll

@@ -83,8 +83,7 @@ __device__ __forceinline__ void gemm_skinny(const uint16_t* __restrict__ X, cons
     const uint32_t t = t0 + r16, tc = t < M ? t : M - 1;                  // tokens past M: clamped, not stored
     const uint16_t* xrow = X + (size_t)tc * ldx;
 
-    uint32_t magic_v;
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_v));
+    const DequantConsts<BITS> dc = dequant_consts<BITS>();
 
     // tile m of this wave is tile wave + 8m of the row; a chunk past the row
     // end (the half-filled last tile, or a wave with fewer tiles) re-reads a
@@ -109,11 +108,11 @@ __device__ __forceinline__ void gemm_skinny(const uint16_t* __restrict__ X, cons
     auto compute = [&](const SkinnyStage<RT, BITS>& st) {
         h8 a[RT][4];
 #pragma unroll
-        for (int i = 0; i < RT; ++i) dequant_chunk_sb(st.w[i], st.s[i] | (st.b[i] << 16), magic_v, a[i]);
+        for (int i = 0; i < RT; ++i) dequant_chunk_sb<BITS>(st.w[i], st.s[i] | (st.b[i] << 16), dc, a[i]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const h8 xv = X_BF16 ? bf16x8_to_f16(st.x[j]) : __builtin_bit_cast(h8, st.x[j]);
-            const h8 b = mask_h8(perm_0415(xv), st.mask);
+            const h8 b = mask_h8(unit_b_order<BITS>(xv), st.mask);
 #pragma unroll
             for (int i = 0; i < RT; ++i)
                 acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(mask_h8(a[i][j], st.mask), b, acc[i], 0, 0, 0);
