@@ -868,7 +868,7 @@ public:
         std::snprintf(name, sizeof(name), "tfq_attn_combine_h%u", hd);
         uint32_t ncu = nc;
         void* a2[] = {&part_o, &part_ml, &out, &ncu};
-        return launch2(m_, name, nq, 1, hd, 0, stream, a2);
+        return launch2(m_, name, nq, hd / kAttnCombineDims, kAttnCombineThreads, 0, stream, a2);
     }
 
 private:

@@ -64,6 +64,10 @@ constexpr uint32_t xpairs_lds_bytes(uint32_t n) { return 4u * n + 16u * (n >> 5)
 // combine merges (its weight table in LDS): 65536 visible keys.
 constexpr uint32_t kAttnChunk = 64;
 constexpr uint32_t kAttnMaxChunks = 65536 / kAttnChunk;
+// The combine's block: 256 threads over 64 head dims (grid: query heads x
+// head_dim / 64).
+constexpr uint32_t kAttnCombineDims = 64;
+constexpr uint32_t kAttnCombineThreads = 256;
 
 // Gemma 4 q/k/v epilogue applied inside the decode attention kernel
 // (fused_qkv_epilogue, S/Metal/Fusions/fused.metal:86-180): per-head RMSNorm

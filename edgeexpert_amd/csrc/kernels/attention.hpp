@@ -26,7 +26,8 @@ namespace tfq {
 
 constexpr uint32_t kAttnThreads = 256;
 constexpr uint32_t kLayerTailThreads = 1024;     // threads of the one-block layer tail
-constexpr uint32_t kAttnKeyLanes = 16;
+constexpr uint32_t kAttnKeyLanes = 16;          // one DPP row per key (row16_sum)
+static_assert(kAttnChunk == kWave, "chunk softmax: one key per lane of a wavefront");
 
 // NeoX rotation of pair i at `pos`: angle = pos · theta^(-2i/HD)
 // (fused.metal:58-72; V/Reference/Attention/RoPE.swift:70-110). The angle is
@@ -67,6 +68,7 @@ __device__ __forceinline__ void wave_head_norm(const uint16_t* __restrict__ src,
 template <int HD, int G>
 struct AttnLds {
     uint16_t q[G][HD];
+    uint16_t wn[2][HD];       // q and k norm weights
     uint16_t kp[HD];
     uint16_t vp[HD];
     float rc[HD / 2];
@@ -103,47 +105,55 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
     const uint32_t pos = seq_len - 1;                  // the new token
     const bool own_pos = epi_on && pos >= c0 && pos < c0 + n;
 
-    // 1. issue the chunk's K and V loads
+    // 1. loads, in the order they are waited for: the queries (16-byte
+    // chunks; G*HD/8 <= 256 of them) and, in the block that owns it, the new
+    // token's raw k and v rows; then the chunk's K rows; then its V rows. No
+    // load is predicated (rows past the chunk's end re-read its last row and
+    // are masked afterwards, threads past the queries re-read the last chunk,
+    // blocks without the new token re-read the queries), so each wait covers
+    // exactly the loads before it: the epilogue runs while K and V stream in,
+    // the scores while V does.
+    constexpr uint32_t QCH = G * HD / 8;
+    constexpr uint32_t KVCH = 2 * (HD / 8);
+    static_assert(QCH <= kAttnThreads && KVCH <= kAttnThreads, "one chunk per thread");
+    const uint4 qraw = reinterpret_cast<const uint4*>(q + (size_t)h * G * HD)[tid < QCH ? tid : QCH - 1];
+    const uint32_t kvi = tid % KVCH;
+    const uint16_t* kvsrc = own_pos ? (kvi < HD / 8 ? kc : vc) + (size_t)pos * row + (size_t)h * HD : q;
+    const uint4 kvraw = reinterpret_cast<const uint4*>(kvsrc)[kvi % (HD / 8)];
+    const uint16_t* wsrc = epi_on ? (kvi < HD / 8 ? epi.q_norm : epi.k_norm) : q;
+    const uint4 wraw = reinterpret_cast<const uint4*>(wsrc)[kvi % (HD / 8)];
+
     const uint32_t sl = lane & (kAttnKeyLanes - 1);
     uint4 kr[KSTEPS][CPL];
 #pragma unroll
     for (uint32_t st = 0; st < KSTEPS; ++st) {
         const uint32_t j = st * (kAttnThreads / kAttnKeyLanes) + (tid >> 4);
+        const uint32_t jr = j < n ? j : n - 1;
 #pragma unroll
         for (uint32_t cc = 0; cc < CPL; ++cc)
-            kr[st][cc] = j < n ? *reinterpret_cast<const uint4*>(kbase + j * row + 8u * (sl + 16u * cc))
-                               : make_uint4(0, 0, 0, 0);
+            kr[st][cc] = *reinterpret_cast<const uint4*>(kbase + jr * row + 8u * (sl + 16u * cc));
     }
     const uint32_t vg = tid / TPR, vl = tid % TPR;
     uint4 vr[KPG];
 #pragma unroll
     for (uint32_t i = 0; i < KPG; ++i) {
         const uint32_t j = vg * KPG + i;
-        vr[i] = j < n ? *reinterpret_cast<const uint4*>(vbase + j * row + 8u * vl) : make_uint4(0, 0, 0, 0);
-    }
-
-    // the queries (16-byte chunks; G*HD/8 <= 128 of them) and, in the block
-    // that owns it, the new token's raw k and v rows
-    constexpr uint32_t QCH = G * HD / 8;
-    static_assert(QCH <= kAttnThreads && 2 * (HD / 8) <= kAttnThreads, "one chunk per thread");
-    uint4 qraw = make_uint4(0, 0, 0, 0), kvraw = make_uint4(0, 0, 0, 0);
-    if (tid < QCH) qraw = reinterpret_cast<const uint4*>(q + (size_t)h * G * HD)[tid];
-    if (own_pos && tid < 2 * (HD / 8)) {
-        const uint16_t* src = (tid < HD / 8 ? kc : vc) + (size_t)pos * row + (size_t)h * HD;
-        kvraw = reinterpret_cast<const uint4*>(src)[tid % (HD / 8)];
+        vr[i] = *reinterpret_cast<const uint4*>(vbase + (j < n ? j : n - 1) * row + 8u * vl);
     }
 
     // 2. queries (and the new token's k/v) through the epilogue
     if (tid < QCH) reinterpret_cast<uint4*>(&L.q[0][0])[tid] = qraw;
     if (epi_on) {
         rope_table(L.rc, L.rs, epi.rotated_pairs, HD, pos, epi.theta);
-        if (own_pos && tid < 2 * (HD / 8))
-            reinterpret_cast<uint4*>(tid < HD / 8 ? L.kp : L.vp)[tid % (HD / 8)] = kvraw;
+        if (tid < KVCH) {
+            reinterpret_cast<uint4*>(&L.wn[0][0])[tid] = wraw;
+            if (own_pos) reinterpret_cast<uint4*>(tid < HD / 8 ? L.kp : L.vp)[tid % (HD / 8)] = kvraw;
+        }
         __syncthreads();
         const uint32_t nvec = G + (own_pos ? 2u : 0u);
         for (uint32_t v = wave; v < nvec; v += kAttnThreads / 64) {
             uint16_t* buf = v < G ? L.q[v] : (v == G ? L.kp : L.vp);
-            const uint16_t* w = v < G ? epi.q_norm : (v == G ? epi.k_norm : nullptr);
+            const uint16_t* w = v < G ? L.wn[0] : (v == G ? L.wn[1] : nullptr);
             wave_head_norm<HD>(buf, buf, w, epi.eps);
         }
         __syncthreads();
@@ -196,7 +206,7 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float sdot = seg_sum<kAttnKeyLanes>(acc[g]);
+            const float sdot = row16_sum(acc[g]);
             if (sl == 0) L.p[g][j] = j < n ? sdot * scale : -__builtin_inff();
         }
     }
@@ -205,11 +215,9 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
     // 4. chunk softmax statistics, one wavefront per query head
     for (uint32_t g = wave; g < (uint32_t)G; g += kAttnThreads / 64) {
         const float sv = lane < kAttnChunk ? L.p[g][lane] : -__builtin_inff();
-        float m = sv;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+        const float m = wave_max(sv);
         const float e = lane < n ? expf(sv - m) : 0.0f;
-        const float l = seg_sum<kWave>(e);
+        const float l = wave_sum(e);
         if (lane < kAttnChunk) L.p[g][lane] = e;
         if (lane == 0) {
             L.ml[g][0] = m;
@@ -257,34 +265,73 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
     }
 }
 
-// Merge of the chunks of query head blockIdx.x; HD threads, d = threadIdx.x.
+// Merge of the chunks of query head blockIdx.x, head dims
+// [64·blockIdx.y, 64·blockIdx.y + 64). Thread (cg, d4) accumulates float4 d4
+// of the chunks c ≡ cg (mod 16); its first four loads are issued before the
+// weights are formed (rows past the last chunk re-read it and get weight 0),
+// so the block waits for one memory round trip, not two. The 16 partial sums
+// are added through LDS in cg order.
 template <int HD>
 __device__ __forceinline__ void attn_combine(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                                              uint16_t* __restrict__ out, uint32_t nchunks) {
+    static_assert(HD % kAttnCombineDims == 0, "head dims split in 64s");
+    constexpr uint32_t NV = kAttnCombineDims / 4;               // float4 columns per block
+    constexpr uint32_t NG = kAttnCombineThreads / NV;           // chunk groups
+    constexpr uint32_t PRE = 4;
     __shared__ float wgt[kAttnMaxChunks];
     __shared__ float tot;
-    const uint32_t qh = blockIdx.x, d = threadIdx.x;
-    const float* ml = part_ml + (size_t)qh * nchunks * 2;
-    if (threadIdx.x < 64) {
-        float m = -__builtin_inff();
-        for (uint32_t c = threadIdx.x; c < nchunks; c += 64) m = fmaxf(m, ml[2 * c]);
+    __shared__ float4 red[NG][NV];
+    const uint32_t qh = blockIdx.x, tid = threadIdx.x, d4 = tid % NV, cg = tid / NV;
+    const float4* po = reinterpret_cast<const float4*>(part_o + (size_t)qh * nchunks * HD +
+                                                       (size_t)blockIdx.y * kAttnCombineDims) + d4;
+    float4 pre[PRE];
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+    for (uint32_t i = 0; i < PRE; ++i) {
+        const uint32_t c = cg + NG * i;
+        pre[i] = po[(size_t)(c < nchunks ? c : nchunks - 1) * (HD / 4)];
+    }
+    const float* ml = part_ml + (size_t)qh * nchunks * 2;
+    if (tid < kWave) {
+        float m = -__builtin_inff();
+        for (uint32_t c = tid; c < nchunks; c += kWave) m = fmaxf(m, ml[2 * c]);
+        m = wave_max(m);
         float l = 0.0f;
-        for (uint32_t c = threadIdx.x; c < nchunks; c += 64) {
+        for (uint32_t c = tid; c < nchunks; c += kWave) {
             const float w = expf(ml[2 * c] - m);
             wgt[c] = w;
             l = fmaf(w, ml[2 * c + 1], l);
         }
-        l = seg_sum<kWave>(l);
-        if (threadIdx.x == 0) tot = l;
+        l = wave_sum(l);
+        if (tid == 0) tot = l;
     }
     __syncthreads();
-    const float* po = part_o + (size_t)qh * nchunks * HD + d;
-    float acc = 0.0f;
-#pragma unroll 8
-    for (uint32_t c = 0; c < nchunks; ++c) acc = fmaf(wgt[c], po[(size_t)c * HD], acc);
-    out[(size_t)qh * HD + d] = f2h(acc / tot);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (uint32_t i = 0; i < PRE; ++i) {
+        const uint32_t c = cg + NG * i;
+        const float w = c < nchunks ? wgt[c] : 0.0f;
+        acc.x = fmaf(w, pre[i].x, acc.x);
+        acc.y = fmaf(w, pre[i].y, acc.y);
+        acc.z = fmaf(w, pre[i].z, acc.z);
+        acc.w = fmaf(w, pre[i].w, acc.w);
+    }
+    for (uint32_t c = cg + NG * PRE; c < nchunks; c += NG) {
+        const float w = wgt[c];
+        const float4 v = po[(size_t)c * (HD / 4)];
+        acc.x = fmaf(w, v.x, acc.x);
+        acc.y = fmaf(w, v.y, acc.y);
+        acc.z = fmaf(w, v.z, acc.z);
+        acc.w = fmaf(w, v.w, acc.w);
+    }
+    red[cg][d4] = acc;
+    __syncthreads();
+    if (tid < kAttnCombineDims) {
+        const float* r = reinterpret_cast<const float*>(&red[0][0]) + tid;
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t g = 0; g < NG; ++g) s += r[g * kAttnCombineDims];
+        out[(size_t)qh * HD + (size_t)blockIdx.y * kAttnCombineDims + tid] = f2h(s / tot);
+    }
 }
 
 // Decode-layer tail (one block): recomputes the post-attention residual

@@ -48,6 +48,56 @@ __device__ __forceinline__ float seg_sum(float v) {
     return v;
 }
 
+// Cross-lane reductions on the VALU (DPP row permutations and the gfx950
+// permlane swaps) instead of LDS permutes: a few cycles per step rather than
+// an LDS round trip. Every lane receives the result; the pairing is fixed, so
+// results are deterministic (and commutative pairs make them equal in every
+// lane). Row = 16 aligned lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppRowMirror = 0x140;       // lane i <-> 15 - i
+constexpr int kDppRowHalfMirror = 0x141;   // lane i <-> 7 - i within each 8
+constexpr int kDppQuadSwap2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppQuadSwap1 = 0xB1;        // quad_perm [1,0,3,2]
+
+// After the mirror and half-mirror steps lane i of a row holds the sum of
+// lanes {i, 7-i, 8+i, 15-i} (mod the row); the two quad swaps add the four
+// disjoint such sets of a quad together.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<kDppRowMirror>(v);
+    v += dpp_mov<kDppRowHalfMirror>(v);
+    v += dpp_mov<kDppQuadSwap2>(v);
+    v += dpp_mov<kDppQuadSwap1>(v);
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_mov<kDppRowMirror>(v));
+    v = fmaxf(v, dpp_mov<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp_mov<kDppQuadSwap2>(v));
+    v = fmaxf(v, dpp_mov<kDppQuadSwap1>(v));
+    return v;
+}
+
+// v_permlane16_swap with both operands = x leaves (row0, row0, row2, row2) in
+// one result and (row1, row1, row3, row3) in the other; v_permlane32_swap does
+// the same for the two 32-lane halves. Applied to row-uniform values they
+// combine rows pairwise, then halves.
+template <bool MAX>
+__device__ __forceinline__ float rows_combine(float v) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const auto p = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    const float x0 = __builtin_bit_cast(float, (uint32_t)p[0]), x1 = __builtin_bit_cast(float, (uint32_t)p[1]);
+    v = MAX ? fmaxf(x0, x1) : x0 + x1;
+    const uint32_t c = __builtin_bit_cast(uint32_t, v);
+    const auto q = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+    const float y0 = __builtin_bit_cast(float, (uint32_t)q[0]), y1 = __builtin_bit_cast(float, (uint32_t)q[1]);
+    return MAX ? fmaxf(y0, y1) : y0 + y1;
+}
+__device__ __forceinline__ float wave_sum(float v) { return rows_combine<false>(row16_sum(v)); }
+__device__ __forceinline__ float wave_max(float v) { return rows_combine<true>(row16_max(v)); }
+
 // gelu_pytorch_tanh with the inner argument clamped to ±20
 // (S/Metal/MoE/moe.metal:53-60; the clamp is exact at fp32 saturation).
 // GELU, tanh form: 0.5·x·(1 + tanh(z)), z = sqrt(2/pi)·(x + 0.044715·x^3),

@@ -73,7 +73,7 @@ constexpr int kRowsInFlight = 1;
     }
 
 #define TFQ_ATTN_COMBINE(HD)                                                                     \
-    extern "C" __global__ __launch_bounds__(HD) void tfq_attn_combine_h##HD(                     \
+    extern "C" __global__ __launch_bounds__(kAttnCombineThreads) void tfq_attn_combine_h##HD(    \
         const float* part_o, const float* part_ml, uint16_t* out, uint32_t nchunks) {             \
         attn_combine<HD>(part_o, part_ml, out, nchunks);                                          \
     }
