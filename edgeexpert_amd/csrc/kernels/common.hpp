@@ -72,6 +72,17 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += dpp_mov<kDppQuadSwap1>(v);
     return v;
 }
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t row16_sum_u32(uint32_t v) {
+    v += dpp_mov_u32<kDppRowMirror>(v);
+    v += dpp_mov_u32<kDppRowHalfMirror>(v);
+    v += dpp_mov_u32<kDppQuadSwap2>(v);
+    v += dpp_mov_u32<kDppQuadSwap1>(v);
+    return v;
+}
 __device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, dpp_mov<kDppRowMirror>(v));
     v = fmaxf(v, dpp_mov<kDppRowHalfMirror>(v));

@@ -320,18 +320,21 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
 }
 
 // Order key of logit v at index t: larger key = ranked first. The float
-// bits are mapped to an unsigned order (sign-magnitude -> biased), and the
-// low half holds ~t so that equal logits rank by lower index. -0 ranks as
-// +0 (they compare equal, so the lower index wins), and NaN ranks below
-// -inf: router_topk_select_k8 (S/Metal/MoE/moe.metal:152-168) never prefers
-// a NaN score to a number. Every finite or infinite v gets a key > 0.
-__device__ __forceinline__ uint64_t topk_key(float v, uint32_t t) {
+// bits are mapped to an unsigned order (topk_order: sign-magnitude ->
+// biased), and the low half holds ~t so that equal logits rank by lower
+// index. -0 ranks as +0 (they compare equal, so the lower index wins), and
+// NaN ranks below -inf: router_topk_select_k8 (S/Metal/MoE/moe.metal:152-168)
+// never prefers a NaN score to a number. Every finite or infinite v gets an
+// order value > 0.
+__device__ __forceinline__ uint32_t topk_order(float v) {
     uint32_t b = __builtin_bit_cast(uint32_t, v);
     const uint32_t mag = b & 0x7FFFFFFFu;
     if (mag == 0) b = 0;
-    uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    if (mag > 0x7F800000u) o = 0;
-    return ((uint64_t)o << 32) | (uint32_t)(0xFFFFFFFFu - t);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return mag > 0x7F800000u ? 0u : o;
+}
+__device__ __forceinline__ uint64_t topk_key(float v, uint32_t t) {
+    return ((uint64_t)topk_order(v) << 32) | (uint32_t)(0xFFFFFFFFu - t);
 }
 
 // Greedy int4 LM head, rows stage (logit.metal:688-737): z = W·x for every
@@ -389,37 +392,53 @@ __device__ __forceinline__ void lm_head_greedy_reduce(const uint64_t* __restrict
     }
 }
 
-// Top-k of E <= 256 logits by (value desc, index asc), in parallel: the
-// logits become unique 64-bit order keys in LDS, and candidate t's rank is
-// the number of keys above its own (two threads per candidate when the block
-// has them, each scanning half the keys with 16-byte LDS reads; the halves
-// meet with one shuffle). Ranks are unique, so the k candidates with
-// rank < k each write their slot. `stage` holds the E logits; `sel_idx` /
-// `sel_val` receive the k winners in rank order. Ends with a block barrier.
+// Top-k of E <= 256 logits by (value desc, index asc). Logit t's rank is
+// the number of logits ordered before it: rank_t = #{o_j > o_t} +
+// #{j < t : o_j == o_t}, o = topk_order + 1 (>= 1; padding 0). The logits are
+// cut into blocks of 8; thread (row a, column c) of each 16-lane row counts,
+// for the 8 logits of block a, those of blocks c, c + 16, ... that are
+// ordered before them, the tie-break folded into a threshold per pair
+// (o_j >= o_t  <=>  o_j > o_t - 1); the row's 16 partial counts are added
+// with DPP (8-bit fields, 4 per word: a rank is at most 255). Ranks are
+// unique, so the k logits with rank < k each write their slot. `stage`
+// holds the E logits; `sel_idx` / `sel_val` receive the k winners in rank
+// order. Ends with a block barrier.
 __device__ __forceinline__ void block_topk(const float* stage, uint32_t E, uint32_t k,
                                            uint32_t* sel_idx, float* sel_val) {
-    __shared__ __attribute__((aligned(16))) uint64_t keys[kRouterMaxExperts];
-    const uint32_t ep = (E + 1) & ~1u;
-    for (uint32_t t = threadIdx.x; t < ep; t += kThreads) keys[t] = t < E ? topk_key(stage[t], t) : 0ull;
+    static_assert(kThreads == 256 && kRouterMaxExperts <= 256, "16 rows of 16 lanes, 8-bit ranks");
+    __shared__ __attribute__((aligned(16))) uint32_t ord[kRouterMaxExperts];
+    for (uint32_t t = threadIdx.x; t < kRouterMaxExperts; t += kThreads)
+        ord[t] = t < E ? topk_order(stage[t]) + 1u : 0u;
     __syncthreads();
-    const uint32_t split = (2 * E <= kThreads) ? 2u : 1u;
-    const uint32_t pairs = ep >> 1, per = (pairs + split - 1) / split;
-    for (uint32_t base = 0; base < E * split; base += kThreads) {
-        const uint32_t slot = base + threadIdx.x;
-        const uint32_t t = slot / split, half = slot % split;
-        if (t < E) {
-            const uint64_t kt = keys[t];
-            const uint32_t p0 = half * per, p1 = p0 + per < pairs ? p0 + per : pairs;
-            const ulonglong2* k2 = reinterpret_cast<const ulonglong2*>(keys);
-            uint32_t rank = 0;
-#pragma unroll 8
-            for (uint32_t p = p0; p < p1; ++p) {
-                const ulonglong2 kk = k2[p];
-                rank += kk.x > kt ? 1u : 0u;
-                rank += kk.y > kt ? 1u : 0u;
+    const uint32_t nb = (E + 7) / 8;
+    const uint32_t row = threadIdx.x / 16, col = threadIdx.x % 16;
+    for (uint32_t a = row; a < nb; a += kThreads / 16) {
+        const uint4 a0 = reinterpret_cast<const uint4*>(ord)[2 * a];
+        const uint4 a1 = reinterpret_cast<const uint4*>(ord)[2 * a + 1];
+        const uint32_t oi[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (uint32_t b = col; b < nb; b += 16) {
+            const uint4 b0 = reinterpret_cast<const uint4*>(ord)[2 * b];
+            const uint4 b1 = reinterpret_cast<const uint4*>(ord)[2 * b + 1];
+            const uint32_t oj[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+            const uint32_t lt = b < a ? 1u : 0u, le = b <= a ? 1u : 0u;
+#pragma unroll
+            for (int ii = 0; ii < 8; ++ii) {
+                // real keys have o >= 1, so their thresholds are >= 0 and
+                // padding (o = 0) never counts
+                const uint32_t t_lt = oi[ii] - lt, t_le = oi[ii] - le;
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) cnt[ii] += oj[jj] > (jj < ii ? t_le : t_lt) ? 1u : 0u;
             }
-            if (split == 2) rank += __shfl_xor(rank, 1, kWave);
-            if (half == 0 && rank < k) {
+        }
+        uint32_t lo = cnt[0] | cnt[1] << 8 | cnt[2] << 16 | cnt[3] << 24;
+        uint32_t hi = cnt[4] | cnt[5] << 8 | cnt[6] << 16 | cnt[7] << 24;
+        lo = row16_sum_u32(lo);
+        hi = row16_sum_u32(hi);
+        const uint32_t t = 8 * a + col;
+        if (col < 8 && t < E) {
+            const uint32_t rank = ((col < 4 ? lo : hi) >> (8 * (col % 4))) & 0xFFu;
+            if (rank < k) {
                 sel_idx[rank] = t;
                 sel_val[rank] = stage[t];
             }
