@@ -38,16 +38,6 @@ __device__ __forceinline__ float bf2f(uint16_t b) {
     return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
 
-// Sum over the SEG lanes of a segment; every lane of the segment receives the
-// total. The xor butterfly stays inside the segment, so segments of one wave
-// may hold different rows, and the order of additions is fixed (deterministic).
-template <int SEG>
-__device__ __forceinline__ float seg_sum(float v) {
-#pragma unroll
-    for (int m = SEG / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-    return v;
-}
-
 // Cross-lane reductions on the VALU (DPP row permutations and the gfx950
 // permlane swaps) instead of LDS permutes: a few cycles per step rather than
 // an LDS round trip. Every lane receives the result; the pairing is fixed, so
@@ -108,6 +98,31 @@ __device__ __forceinline__ float rows_combine(float v) {
 }
 __device__ __forceinline__ float wave_sum(float v) { return rows_combine<false>(row16_sum(v)); }
 __device__ __forceinline__ float wave_max(float v) { return rows_combine<true>(row16_max(v)); }
+
+// Sum over the SEG lanes of a segment (SEG a power of two, aligned); every
+// lane of the segment receives the total, bit-identical in every lane. The
+// steps stay inside the segment, so segments of one wave may hold different
+// rows (or have left a loop the others continue), and the order of additions
+// is fixed (deterministic).
+template <int SEG>
+__device__ __forceinline__ float seg_sum(float v) {
+    static_assert(SEG == 1 || SEG == 2 || SEG == 4 || SEG == 8 || SEG == 16 || SEG == 32 || SEG == 64,
+                  "segment of 1..64 lanes");
+    if constexpr (SEG == 16) {
+        return row16_sum(v);
+    } else if constexpr (SEG == 32) {
+        const uint32_t b = __builtin_bit_cast(uint32_t, row16_sum(v));
+        const auto p = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+        return __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+    } else if constexpr (SEG == 64) {
+        return wave_sum(v);
+    } else {
+        if constexpr (SEG >= 8) v += dpp_mov<kDppRowHalfMirror>(v);
+        if constexpr (SEG >= 4) v += dpp_mov<kDppQuadSwap2>(v);
+        if constexpr (SEG >= 2) v += dpp_mov<kDppQuadSwap1>(v);
+        return v;
+    }
+}
 
 // gelu_pytorch_tanh with the inner argument clamped to ±20
 // (S/Metal/MoE/moe.metal:53-60; the clamp is exact at fp32 saturation).

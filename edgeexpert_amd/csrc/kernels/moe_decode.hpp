@@ -373,12 +373,14 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
     const uint32_t wave_total = gridDim.x * nwaves;
     const uint32_t n_acts = top_k * F;
 
-    // independent loads first: the activations, the slot's expert index and weight
+    // independent loads first: the activations, the slot's expert index and
+    // routing weight (unpredicated: dead slots read slot 0)
     XStage<NT, kPhase2Chunks, false> xs;
     const NormArg copy{nullptr, nullptr, nullptr, 0.0f, kStageCopy};
     xs.load(acts, n_acts, copy);
-    const uint32_t e = live ? indices[slot] : 0u;
-    const uint16_t w_raw = live ? rw[slot] : (uint16_t)0;
+    const uint32_t e_raw = indices[live ? slot : 0u];
+    const uint16_t w_raw = rw[live ? slot : 0u];
+    const uint32_t e = live ? e_raw : 0u;
     const bool valid = live && e < pool.num_experts;
     const uint8_t* blob = pool.base + (uint64_t)(valid ? e : 0u) * pool.stride;
     const uint8_t* dw = blob + pool.off.down_w;
@@ -387,6 +389,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
 
     QChunk<BITS> wv[R][P];
     uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
+    uint16_t res[R] = {};             // the rows' residuals, loaded with their weights
     auto issue = [&](uint32_t grp) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -402,6 +405,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                     }
                 }
             }
+            if (residual && d < D) res[r] = residual[d];   // needed last: issued last
         }
     };
     issue(0);
@@ -431,16 +435,19 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                 acc[r] = __builtin_nanf("");
             }
         }
+        uint16_t res_now[R];          // issue() reloads res for the next group
+#pragma unroll
+        for (int r = 0; r < R; ++r) res_now[r] = res[r];
         issue(grp + 1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t d = wave_id + (grp * R + r) * wave_total;
             const float part = w_slot * seg_sum<SEG>(acc[r]);   // partial[slot] = w·value (moe.metal:499)
             if (d < D) {
-                float out = residual ? h2f(residual[d]) : 0.0f;
+                float out = residual ? h2f(res_now[r]) : 0.0f;
 #pragma unroll
                 for (uint32_t s = 0; s < 8; ++s) {
-                    const float ps = __shfl(part, (int)(s * SEG), kWave);
+                    const float ps = __shfl(part, (int)(s * SEG), kWave);   // v_readlane measured slower
                     if (s < top_k) out += ps;                   // fixed slot order (moe.metal:505-509)
                 }
                 if (lane == 0) y[d] = f2h(out);
