@@ -385,6 +385,111 @@ def pmc_summary(csv_path, out=sys.stdout, simds=1024, xcds=8):
         out.write(line + "\n")
 
 
+# Algorithmic bytes per launch of the kernels the traffic summary compares:
+# weights + scales/biases + activations read + outputs written, per bench.py
+# unit of work. By kernel name, or by (name, blocks) for kernels launched at
+# several shapes.
+TRAFFIC_ALG = {
+    "tfq_moe_phase1_routed_s32_p3": 17859072,
+    "tfq_moe_phase2_p3": 8 * 1115136 + 8 * 704 * 2 + 8 * 2 + 8 * 4 + 2816 * 2,
+    "tfq_router_logits_s64_p3": 128 * 2816 + 4 * 128 * 44 + 2816 * 2 + 128 * 4,
+    "tfq_attn_partial_h256_g2": 33554432,
+    "tfq_lm_head_greedy_s32_p3": 262144 * 1408 + 2 * 262144 * 88 + 2 * 2816 * 2,
+}
+TRAFFIC_ALG_GRID = {
+    ("tfq_q4_gemv_s32_p3", 352): 4471808,                                                   # config 0
+    ("tfq_gemm_q4_bf16", 256): 11534336 + 1441792 + 2883584 + 8388608,                      # config 2
+    ("tfq_q4_gemv_s32_p3", 1792): 262144 * 1408 + 2 * 262144 * 88 + 2816 * 2 + 262144 * 2,  # LM-head shape
+}
+
+
+def traffic_summary(fetch_csv, write_csv, out=sys.stdout):
+    """HBM bytes per launch from two rocprofv3 --pmc runs of this script
+    (FETCH_SIZE, then WRITE_SIZE), by (kernel, blocks). The counters are
+    scaled to bytes by what they read for the calibration kernels this
+    script launches once: tfq_read_ceiling over 64 MiB (its largest-grid
+    dispatch) and tfq_convert_bf16_f16 (32 MiB in, 32 MiB out). Ends with the
+    `traffic <kernel family> <bytes>` lines read_traffic() takes."""
+    import csv
+    import re
+
+    def load(path, counter):
+        acc, n, sizes = {}, {}, {}
+        for r in csv.DictReader(open(path, newline="")):
+            if r["Counter_Name"] != counter:
+                continue
+            name = r["Kernel_Name"].split("(")[0].strip()
+            k = (name if name in ("tfq_read_ceiling", "tfq_convert_bf16_f16") or name.startswith("__amd")
+                 else f"{name}@{int(r['Grid_Size']) // int(r['Workgroup_Size'])}")
+            v = float(r["Counter_Value"])
+            acc[k] = acc.get(k, 0.0) + v
+            n[k] = n.get(k, 0) + 1
+            sizes.setdefault(k, []).append(v)
+        return acc, n, sizes
+    f, nf, fs = load(fetch_csv, "FETCH_SIZE")
+    w, nw, ws = load(write_csv, "WRITE_SIZE")
+    cal = max((int(r["Grid_Size"]), float(r["Counter_Value"])) for r in csv.DictReader(open(fetch_csv, newline=""))
+              if r["Counter_Name"] == "FETCH_SIZE" and r["Kernel_Name"].startswith("tfq_read_ceiling"))
+    rc = cal[1] / (64 * 1024)
+    cv_f = max(fs["tfq_convert_bf16_f16"]) / (32 * 1024)
+    cv_w = max(ws["tfq_convert_bf16_f16"]) / (32 * 1024)
+    fetch_scale = (rc + cv_f) / 2
+    rows = []
+    for k in f:
+        if k.startswith("__amd") or k in ("tfq_read_ceiling", "tfq_convert_bf16_f16"):
+            continue
+        fk = f[k] / nf[k]
+        wk = w.get(k, 0.0) / max(nw.get(k, 1), 1)
+        rows.append((fk * 1024 / fetch_scale + wk * 1024 / cv_w, k, nf[k], fk, wk))
+    rows.sort(reverse=True)
+    out.write("Calibration (kernels of known size launched by bench.py in the same run):\n"
+              f"    tfq_read_ceiling, 64 MiB read (its largest-grid dispatch): FETCH_SIZE = {rc:.4f} KiB per KiB read\n"
+              f"    tfq_convert_bf16_f16, 32 MiB in / 32 out: FETCH_SIZE = {cv_f:.4f} KiB per KiB read, "
+              f"WRITE_SIZE = {cv_w:.4f} KiB per KiB written\n"
+              f"    traffic (bytes) = FETCH_SIZE[KiB] * 1024 / {fetch_scale:.4f} + WRITE_SIZE[KiB] * 1024 / {cv_w:.4f}\n\n")
+    out.write(f"{'kernel@blocks':39s} {'dispatches':>10s} {'FETCH KiB':>11s} {'WRITE KiB':>10s} {'traffic B':>12s}  "
+              f"{'algorithmic B':>13s}  ratio\n")
+    for traffic, k, n, fk, wk in rows:
+        name, blocks = k.split("@")
+        alg = TRAFFIC_ALG.get(name) or TRAFFIC_ALG_GRID.get((name, int(blocks)))
+        ratio = f"{traffic / alg:6.2f}" if alg else ""
+        out.write(f"{k:39s} {n:10d} {fk:11.1f} {wk:10.1f} {traffic:12.0f}  {alg if alg else '':>13}  {ratio}\n")
+    out.write("\nMachine-readable lines (bench.py reads `traffic <kernel family> <bytes>`):\n")
+    seen = set()
+    c0 = [t for t, k, *_ in rows if k == "tfq_q4_gemv_s32_p3@352"]
+    if c0:
+        out.write(f"traffic tfq_q4_gemv_c0 {c0[0]:.0f}\n")
+    for traffic, k, *_ in rows:
+        fam = re.sub(r"(_s\d+_p\d+|_p\d+|_h\d+_g\d+|_h\d+)$", "", k.split("@")[0])
+        if fam not in seen:
+            seen.add(fam)
+            out.write(f"traffic {fam} {traffic:.0f}\n")
+
+
+def layer_summary(trace_csv, out=sys.stdout):
+    """Per-kernel durations of the config-4 decoder layers in a rocprofv3
+    --kernel-trace CSV of this script: the window from the first norm-staged
+    QKV GEMV (1024 blocks) to the last layer tail, grouped by (kernel, grid,
+    queue), median and minimum over the layers."""
+    import csv
+    import statistics
+    rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"],
+                   int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]), int(r["Grid_Size_Y"]), int(r["Queue_Id"]))
+                  for r in csv.DictReader(open(trace_csv, newline="")))
+    t0 = min(s for s, e, n, gx, gy, q in rows if n.startswith("tfq_q4_gemv_norm_s32_p3") and gx == 1024)
+    t1 = max(e for s, e, n, gx, gy, q in rows if n.startswith("tfq_layer_tail"))
+    win = [r for r in rows if t0 <= r[0] and r[1] <= t1]
+    layers = sum(1 for r in win if r[2].startswith("tfq_layer_tail"))
+    groups = {}
+    for s, e, n, gx, gy, q in win:
+        groups.setdefault((n, gx, gy, q), []).append((e - s) / 1e3)
+    out.write(f"layers in the window: {layers}\n\n"
+              f"{'kernel':44s} {'grid':>9s} {'queue':>5s} {'median us':>10s} {'min us':>8s}\n")
+    for (n, gx, gy, q), v in groups.items():
+        if len(v) >= layers // 2:
+            out.write(f"{n[:44]:44s} {gx:5d}x{gy:<3d} {q:5d} {statistics.median(v):10.2f} {min(v):8.2f}\n")
+
+
 def bench_gemm_policy(ctx, stream, batch_avg_us):
     """The prefill GEMM's kernel choice by token count (config 2's weights,
     N 8192 x K 2816, bf16): the library's choice at token counts on both
@@ -454,11 +559,21 @@ def main():
                     help="print per (kernel, grid) statistics of a rocprofv3 kernel-trace CSV and exit")
     ap.add_argument("--b2b-gap-us", type=float, default=None,
                     help="with --trace-summary: only dispatches starting within this gap of the previous end")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print HBM bytes per launch from FETCH_SIZE / WRITE_SIZE counter CSVs and exit")
+    ap.add_argument("--layer-summary", metavar="CSV",
+                    help="print the config-4 layer's per-kernel durations from a kernel-trace CSV and exit")
     ap.add_argument("--pmc-summary", metavar="CSV",
                     help="print per (kernel, grid) averages of a rocprofv3 --pmc counter CSV and exit")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(args.pmc_summary)
+        return
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary)
+        return
+    if args.layer_summary:
+        layer_summary(args.layer_summary)
         return
     if args.trace_summary:
         trace_summary(args.trace_summary, b2b_gap_us=args.b2b_gap_us)
