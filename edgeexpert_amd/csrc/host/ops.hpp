@@ -6,6 +6,8 @@
 // pointers replace (MTLBuffer, offset) pairs.
 #pragma once
 
+#include <cmath>
+
 #include "../kernels/abi_types.h"
 #include "module.hpp"
 
@@ -860,6 +862,7 @@ public:
                                                   ((size_t)nq * nc * hd * 4 + 255) / 256 * 256);
         uint32_t ks = kv_start(seq_len, window);
         AttnEpilogue e = epi;
+        e.log2_theta = epi.q_norm ? std::log2((double)epi.theta) : 0.0;
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_attn_partial_h%u_g%u", hd, G);
         void* a1[] = {&q, &k_cache, &v_cache, &nkv, &seq_len, &ks, &scale, &e, &part_o, &part_ml};
@@ -966,7 +969,7 @@ public:
                                   v_cache + slot, qd, kvd, s.d, in_norm);
         if (rc) return rc;
         // 2. q/k/v epilogue + attention
-        const AttnEpilogue epi{w.q_norm, w.k_norm, s.eps, s.rope_theta, s.rotated_pairs, 0};
+        const AttnEpilogue epi{w.q_norm, w.k_norm, s.eps, s.rope_theta, s.rotated_pairs, 0, 0.0};
         rc = attn_.encode(stream, q, k_cache, v_cache, attn, s.head_dim, s.num_q_heads, s.num_kv_heads,
                           seq_len, s.window, s.attn_scale, epi, ws + L.parts, L.parts_bytes);
         if (rc) return rc;

@@ -435,7 +435,7 @@ int tfq_attention_decode(tfq_ctx* ctx, void* stream, const uint16_t* q, const ui
                          uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t seq_len,
                          uint32_t window, float scale, void* workspace, size_t workspace_bytes) {
     TFQ_REQUIRE_CTX(ctx);
-    const AttnEpilogue none{nullptr, nullptr, 0.0f, 0.0f, 0, 0};
+    const AttnEpilogue none{nullptr, nullptr, 0.0f, 0.0f, 0, 0, 0.0};
     // without the epilogue the kernels only read the caches
     return ctx->attn->encode(stream, q, const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache),
                              out, head_dim, num_q_heads, num_kv_heads, seq_len, window, scale, none,

@@ -81,6 +81,7 @@ struct AttnEpilogue {
     float theta;
     uint32_t rotated_pairs;
     uint32_t pad_;
+    double log2_theta;      // log2(theta), set by the launcher
 };
 
 // Up to three matrices sharing x and n (plain GEMV: 1; fused QKV: 3).

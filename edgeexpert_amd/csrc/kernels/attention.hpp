@@ -30,14 +30,21 @@ constexpr uint32_t kAttnKeyLanes = 16;          // one DPP row per key (row16_su
 static_assert(kAttnChunk == kWave, "chunk softmax: one key per lane of a wavefront");
 
 // NeoX rotation of pair i at `pos`: angle = pos · theta^(-2i/HD)
-// (fused.metal:58-72; V/Reference/Attention/RoPE.swift:70-110). The angle is
-// formed in fp64 so that it carries no fp32 error at long positions.
+// (fused.metal:58-72; V/Reference/Attention/RoPE.swift:70-110). The inverse
+// frequency 2^(-(2i/HD)·log2 theta) and the angle are formed in fp64 and the
+// angle is reduced to a fraction of a turn there, so no fp32 error grows with
+// the position; sine and cosine of the reduced angle are taken in fp32
+// (sincospi of 2·turns, ~1e-7 absolute).
 __device__ __forceinline__ void rope_table(float* __restrict__ c, float* __restrict__ s, uint32_t pairs,
-                                           uint32_t hd, uint32_t pos, float theta) {
+                                           uint32_t hd, uint32_t pos, double log2_theta) {
+    constexpr double kInvTwoPi = 0.15915494309189533577;
     for (uint32_t i = threadIdx.x; i < pairs; i += kAttnThreads) {
-        const double ang = (double)pos * pow((double)theta, -2.0 * (double)i / (double)hd);
-        c[i] = (float)cos(ang);
-        s[i] = (float)sin(ang);
+        const double inv_freq = exp2(-(2.0 * (double)i / (double)hd) * log2_theta);
+        const double turns = (double)pos * inv_freq * kInvTwoPi;
+        float sv, cv;
+        sincospif((float)(2.0 * (turns - floor(turns))), &sv, &cv);
+        c[i] = cv;
+        s[i] = sv;
     }
 }
 
@@ -144,7 +151,7 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
     // 2. queries (and the new token's k/v) through the epilogue
     if (tid < QCH) reinterpret_cast<uint4*>(&L.q[0][0])[tid] = qraw;
     if (epi_on) {
-        rope_table(L.rc, L.rs, epi.rotated_pairs, HD, pos, epi.theta);
+        rope_table(L.rc, L.rs, epi.rotated_pairs, HD, pos, epi.log2_theta);
         if (tid < KVCH) {
             reinterpret_cast<uint4*>(&L.wn[0][0])[tid] = wraw;
             if (own_pos) reinterpret_cast<uint4*>(tid < HD / 8 ? L.kp : L.vp)[tid % (HD / 8)] = kvraw;
