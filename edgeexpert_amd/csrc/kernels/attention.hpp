@@ -17,7 +17,8 @@
 // lane two 16-byte pieces of the 512-byte row, so one load instruction covers
 // 4 whole rows); for p·V, HD/8 threads own one key row with 16-byte loads and
 // 2048/HD groups of them split the chunk's keys, reduced through LDS in group
-// order. K and V loads of the whole chunk are issued before anything else.
+// order. The chunk's K loads are issued first, its V loads after the q/k/v
+// epilogue.
 #pragma once
 
 #include "common.hpp"
@@ -113,13 +114,13 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
     const bool own_pos = epi_on && pos >= c0 && pos < c0 + n;
 
     // 1. loads, in the order they are waited for: the queries (16-byte
-    // chunks; G*HD/8 <= 256 of them) and, in the block that owns it, the new
-    // token's raw k and v rows; then the chunk's K rows; then its V rows. No
-    // load is predicated (rows past the chunk's end re-read its last row and
-    // are masked afterwards, threads past the queries re-read the last chunk,
-    // blocks without the new token re-read the queries), so each wait covers
-    // exactly the loads before it: the epilogue runs while K and V stream in,
-    // the scores while V does.
+    // chunks; G*HD/8 <= 256 of them), the norm weights and, in the block that
+    // owns it, the new token's raw k and v rows; then the chunk's K rows (its
+    // V rows follow the epilogue). No load is predicated (rows past the
+    // chunk's end re-read its last row and are masked afterwards, threads
+    // past the queries re-read the last chunk, blocks without the new token
+    // re-read the queries), so each wait covers exactly the loads before it:
+    // the epilogue runs while K streams in, the scores while V does.
     constexpr uint32_t QCH = G * HD / 8;
     constexpr uint32_t KVCH = 2 * (HD / 8);
     static_assert(QCH <= kAttnThreads && KVCH <= kAttnThreads, "one chunk per thread");
@@ -140,14 +141,6 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
         for (uint32_t cc = 0; cc < CPL; ++cc)
             kr[st][cc] = *reinterpret_cast<const uint4*>(kbase + jr * row + 8u * (sl + 16u * cc));
     }
-    const uint32_t vg = tid / TPR, vl = tid % TPR;
-    uint4 vr[KPG];
-#pragma unroll
-    for (uint32_t i = 0; i < KPG; ++i) {
-        const uint32_t j = vg * KPG + i;
-        vr[i] = *reinterpret_cast<const uint4*>(vbase + (j < n ? j : n - 1) * row + 8u * vl);
-    }
-
     // 2. queries (and the new token's k/v) through the epilogue
     if (tid < QCH) reinterpret_cast<uint4*>(&L.q[0][0])[tid] = qraw;
     if (epi_on) {
@@ -180,6 +173,17 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
         }
     } else {
         __syncthreads();
+    }
+
+    // the chunk's V rows, issued after the epilogue: a wave stalls while the
+    // memory pipeline backs up under its loads, so the epilogue runs under
+    // the K stream (which alone keeps HBM busy) instead of after both
+    const uint32_t vg = tid / TPR, vl = tid % TPR;
+    uint4 vr[KPG];
+#pragma unroll
+    for (uint32_t i = 0; i < KPG; ++i) {
+        const uint32_t j = vg * KPG + i;
+        vr[i] = *reinterpret_cast<const uint4*>(vbase + (j < n ? j : n - 1) * row + 8u * vl);
     }
 
     // 3. scores
