@@ -82,16 +82,23 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
 
     QChunk<BITS> wv[R][P];
     uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
-    auto issue = [&](uint32_t grp) {
+    // issue(grp, first): the first group's loads are unconditional (rows and
+    // chunks clamped to the last), so the waits of the staging that follows
+    // them are exact (a load under a branch makes the compiler wait for
+    // everything at the join); later groups skip what they do not need.
+    auto issue = [&](uint32_t grp, auto first_c) {
+        constexpr bool FIRST = decltype(first_c)::value;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t row = seg_id + (grp * R + r) * seg_total;
-            if (row < total) {
+            const uint32_t row0 = seg_id + (grp * R + r) * seg_total;
+            const uint32_t row = FIRST && row0 >= total ? total - 1 : row0;
+            if (FIRST || row < total) {
                 const Q4Row q = resolve_row(mats, row, row_bytes, ngroups);
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
-                    const uint32_t c = sl + p * SEG;
-                    if (c < lpr) {
+                    const uint32_t c0 = sl + p * SEG;
+                    const uint32_t c = FIRST && c0 >= lpr ? lpr - 1 : c0;
+                    if (FIRST || c < lpr) {
                         wv[r][p] = ldg_chunk<BITS>(q.w, c);
                         sr[r][p] = q.s[c >> 1];
                         br[r][p] = q.b[c >> 1];
@@ -102,9 +109,9 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
     };
     XStage<NT, kStageChunks, NORM> xs;
     xs.load(x, n, mats.norm);
-    if (!STAGE_FIRST) issue(0);
+    if (!STAGE_FIRST) issue(0, std::true_type{});
     const XPairs xp = xs.pairs(x, lds_xh, n, mats.norm);
-    if (STAGE_FIRST) issue(0);
+    if (STAGE_FIRST) issue(0, std::true_type{});
 
     for (uint32_t grp = 0; seg_id + grp * R * seg_total < total; ++grp) {
         float acc[R];
@@ -123,7 +130,7 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
                 }
             }
         }
-        issue(grp + 1);
+        issue(grp + 1, std::false_type{});
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const float v = seg_sum<SEG>(acc[r]);
@@ -188,15 +195,18 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
 
     uint4 wv[R][P];
     uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
-    auto issue = [&](uint32_t grp) {
+    auto issue = [&](uint32_t grp, auto first_c) {      // first group unconditional, as in q4_rows
+        constexpr bool FIRST = decltype(first_c)::value;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t row = seg_id + (grp * R + r) * seg_total;
-            if (row < M) {
+            const uint32_t row0 = seg_id + (grp * R + r) * seg_total;
+            const uint32_t row = FIRST && row0 >= M ? M - 1 : row0;
+            if (FIRST || row < M) {
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
-                    const uint32_t c = sl + p * SEG;
-                    if (c < lpr) {
+                    const uint32_t c0 = sl + p * SEG;
+                    const uint32_t c = FIRST && c0 >= lpr ? lpr - 1 : c0;
+                    if (FIRST || c < lpr) {
                         wv[r][p] = ldg16_stream(W + (size_t)row * n + 16u * c);
                         sr[r][p] = S[(size_t)row * ngroups + (c >> 2)];
                         br[r][p] = B[(size_t)row * ngroups + (c >> 2)];
@@ -205,7 +215,7 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
             }
         }
     };
-    stage([&]() { issue(0); });
+    stage([&]() { issue(0, std::true_type{}); });
     float xr[P][16];
     float xs[P];
 #pragma unroll
@@ -229,7 +239,7 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
                 }
             }
         }
-        issue(grp + 1);
+        issue(grp + 1, std::false_type{});
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const float v = seg_sum<SEG>(acc[r]);

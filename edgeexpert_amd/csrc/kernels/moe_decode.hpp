@@ -60,17 +60,23 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
 
     QChunk<BITS> gv[R][P], uv[R][P];
     uint32_t gsr[R][P], gbr[R][P], usr[R][P], ubr[R][P];    // raw fp16 scales / biases
-    auto issue = [&](uint32_t grp) {
+    // the first group's loads are unconditional (rows and chunks clamped;
+    // dead or invalid rows read expert 0's), so the waits after them are
+    // exact; later groups skip what they do not need
+    auto issue = [&](uint32_t grp, auto first_c) {
+        constexpr bool FIRST = decltype(first_c)::value;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t row = seg_id + (grp * R + r) * seg_total;
-            if (row < total) {
+            const uint32_t row0 = seg_id + (grp * R + r) * seg_total;
+            const uint32_t row = FIRST && row0 >= total ? total - 1 : row0;
+            if (FIRST || row < total) {
                 const GateUpRow q = rowfn(row);
-                if (q.live && q.valid) {
+                if (FIRST || (q.live && q.valid)) {
 #pragma unroll
                     for (int p = 0; p < P; ++p) {
-                        const uint32_t c = sl + p * SEG;
-                        if (c < lpr) {
+                        const uint32_t c0 = sl + p * SEG;
+                        const uint32_t c = FIRST && c0 >= lpr ? lpr - 1 : c0;
+                        if (FIRST || c < lpr) {
                             gv[r][p] = ldg_chunk<BITS>(q.gw, c);
                             uv[r][p] = ldg_chunk<BITS>(q.uw, c);
                             gsr[r][p] = q.gs[c >> 1];
@@ -86,7 +92,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
     XStage<NT, kStageChunks, NORM> xs;
     xs.load(x, D, norm);
     prologue();
-    issue(0);
+    issue(0, std::true_type{});
     const XPairs xp = xs.pairs(x, lds_xh, D, norm);
     for (uint32_t grp = 0; seg_id + grp * R * seg_total < total; ++grp) {
         float ga[R], ua[R];
@@ -109,7 +115,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
                 }
             }
         }
-        issue(grp + 1);
+        issue(grp + 1, std::false_type{});
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const float g = seg_sum<SEG>(ga[r]);
@@ -269,15 +275,18 @@ __device__ __forceinline__ void q8_gate_up_act(const Q8Mat& gate, const Q8Mat& u
 
     uint4 gv[R][P], uv[R][P];
     uint32_t gsr[R][P], gbr[R][P], usr[R][P], ubr[R][P];     // raw fp16 scales / biases
-    auto issue = [&](uint32_t grp) {
+    auto issue = [&](uint32_t grp, auto first_c) {      // first group unconditional, as in gate_up_rows
+        constexpr bool FIRST = decltype(first_c)::value;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t row = seg_id + (grp * R + r) * seg_total;
-            if (row < F) {
+            const uint32_t row0 = seg_id + (grp * R + r) * seg_total;
+            const uint32_t row = FIRST && row0 >= F ? F - 1 : row0;
+            if (FIRST || row < F) {
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
-                    const uint32_t c = sl + p * SEG;
-                    if (c < lpr) {
+                    const uint32_t c0 = sl + p * SEG;
+                    const uint32_t c = FIRST && c0 >= lpr ? lpr - 1 : c0;
+                    if (FIRST || c < lpr) {
                         gv[r][p] = ldg16_stream(gate.w + (size_t)row * D + 16u * c);
                         uv[r][p] = ldg16_stream(up.w + (size_t)row * D + 16u * c);
                         gsr[r][p] = gate.s[(size_t)row * ngroups + (c >> 2)];
@@ -293,7 +302,7 @@ __device__ __forceinline__ void q8_gate_up_act(const Q8Mat& gate, const Q8Mat& u
         uint16_t* hs = reinterpret_cast<uint16_t*>(lds_x + D);
         XStage<NT, kStageChunks, NORM> st;
         st.load(x, D, norm);
-        issue(0);
+        issue(0, std::true_type{});
         st.plain(x, hs, D, norm);
         for (uint32_t i = threadIdx.x; i < D; i += NT) lds_x[i] = h2f(hs[i]);
         __syncthreads();
@@ -325,7 +334,7 @@ __device__ __forceinline__ void q8_gate_up_act(const Q8Mat& gate, const Q8Mat& u
                 }
             }
         }
-        issue(grp + 1);
+        issue(grp + 1, std::false_type{});
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const float g = seg_sum<SEG>(ga[r]);
@@ -390,15 +399,18 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
     QChunk<BITS> wv[R][P];
     uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
     uint16_t res[R] = {};             // the rows' residuals, loaded with their weights
-    auto issue = [&](uint32_t grp) {
+    auto issue = [&](uint32_t grp, auto first_c) {      // first group unconditional, as in gate_up_rows
+        constexpr bool FIRST = decltype(first_c)::value;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t d = wave_id + (grp * R + r) * wave_total;
-            if (d < D && valid) {
+            const uint32_t d0 = wave_id + (grp * R + r) * wave_total;
+            const uint32_t d = FIRST && d0 >= D ? D - 1 : d0;
+            if (FIRST || (d < D && valid)) {
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
-                    const uint32_t c = sl + p * SEG;
-                    if (c < lpr) {
+                    const uint32_t c0 = sl + p * SEG;
+                    const uint32_t c = FIRST && c0 >= lpr ? lpr - 1 : c0;
+                    if (FIRST || c < lpr) {
                         wv[r][p] = ldg_chunk<BITS>(dw + (size_t)d * row_bytes, c);
                         sr[r][p] = ds[(size_t)d * ngroups + (c >> 1)];
                         br[r][p] = db[(size_t)d * ngroups + (c >> 1)];
@@ -408,7 +420,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
             if (residual && d < D) res[r] = residual[d];   // needed last: issued last
         }
     };
-    issue(0);
+    issue(0, std::true_type{});
     const XPairs xp = xs.pairs(acts, lds_a, n_acts, copy);      // slot s owns chunks s·lpr ..
     const float w_slot = live ? h2f(w_raw) : 0.0f;
 
@@ -438,7 +450,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
         uint16_t res_now[R];          // issue() reloads res for the next group
 #pragma unroll
         for (int r = 0; r < R; ++r) res_now[r] = res[r];
-        issue(grp + 1);
+        issue(grp + 1, std::false_type{});
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t d = wave_id + (grp * R + r) * wave_total;
