@@ -218,13 +218,19 @@ __device__ __forceinline__ uint4 h8_pairs(const h8 v) {
 
 // The chunk sums of 16-byte piece q (= 4c + j) combine over the four pieces of
 // chunk c as (p0 + p1) + (p2 + p3).
+// Lane ^ 1, then lane ^ 2 inside the quad (the same sums either way): on DPP
+// quad permutations, or (DPP == false) on LDS permutes, which measured
+// faster where the staging holds four pieces per thread (routed phase 2).
+template <bool DPP = true>
 __device__ __forceinline__ float4 chunk_sums(const float s, const float sa, const float sb) {
-    float t = s + __shfl_xor(s, 1, kWave);
-    float ta = sa + __shfl_xor(sa, 1, kWave);
-    float tb = sb + __shfl_xor(sb, 1, kWave);
-    t += __shfl_xor(t, 2, kWave);
-    ta += __shfl_xor(ta, 2, kWave);
-    tb += __shfl_xor(tb, 2, kWave);
+    auto x1 = [](float v) { return DPP ? dpp_mov<kDppQuadSwap1>(v) : __shfl_xor(v, 1, kWave); };
+    auto x2 = [](float v) { return DPP ? dpp_mov<kDppQuadSwap2>(v) : __shfl_xor(v, 2, kWave); };
+    float t = s + x1(s);
+    float ta = sa + x1(sa);
+    float tb = sb + x1(sb);
+    t += x2(t);
+    ta += x2(ta);
+    tb += x2(tb);
     return make_float4(t, 1024.0f * ta, 1024.0f * tb, 0.0f);
 }
 
@@ -574,7 +580,7 @@ __device__ __forceinline__ uint4 ld16h(const uint16_t* p, uint32_t chunk) {
 // Both end with a block barrier. Inputs that are not 16-byte aligned, or
 // longer than 8·CH·NT halves, take the scalar path instead (two passes).
 // NORM == false compiles the copy-only form (NormArg ignored).
-template <uint32_t NT, uint32_t CH, bool NORM = true>
+template <uint32_t NT, uint32_t CH, bool NORM = true, bool DPP_SUMS = true>
 struct XStage {
     h8 xv[CH], av[CH], awv[CH], wv[CH];
     float inv_in;      // kStageScaled: r(h), loaded with the chunks
@@ -678,7 +684,7 @@ struct XStage {
             const h8 v = q < npc ? xv[i] : h8{};
             float s, sa, sb;
             h8_sums(v, s, sa, sb);
-            const float4 cs = chunk_sums(s, sa, sb);
+            const float4 cs = chunk_sums<DPP_SUMS>(s, sa, sb);
             if (q < npc) {
                 planes[(q & 3u) * nch + (q >> 2)] = h8_pairs(v);
                 if ((q & 3u) == 0) sums[q >> 2] = cs;

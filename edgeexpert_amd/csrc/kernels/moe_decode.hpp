@@ -390,7 +390,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
 
     // independent loads first: the activations, the slot's expert index and
     // routing weight (unpredicated: dead slots read slot 0)
-    XStage<NT, kPhase2Chunks, false> xs;
+    XStage<NT, kPhase2Chunks, false, false> xs;
     const NormArg copy{nullptr, nullptr, nullptr, 0.0f, kStageCopy};
     xs.load(acts, n_acts, copy);
     const uint32_t e_raw = indices[live ? slot : 0u];
