@@ -232,6 +232,18 @@ __device__ __forceinline__ void sfor_w(Fn&& f) {
     }
 }
 
+// f(<B>), then f(<B+1>) only if f(<B>) returned true, ...: each call sits
+// inside the branch of the one before, so the code after a call is reached
+// only through it and the compiler's waits there count its loads exactly
+// (independent branches would merge paths that issued different loads, and
+// the wait after such a join covers every load).
+template <int B, int E, typename Fn>
+__device__ __forceinline__ void sfor_while(Fn&& f) {
+    if constexpr (B < E) {
+        if (f(std::integral_constant<int, B>{})) sfor_while<B + 1, E>(f);
+    }
+}
+
 
 // ------------------------------------------------------ grouped MoE units ----
 //
@@ -370,9 +382,10 @@ __device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wbase)[RT]
         sfor_w<0, U>([&](auto c) {
             step(m + c.value, std::integral_constant<int, c.value % DEPTH>{}, std::integral_constant<int, c.value & 1>{});
         });
-    sfor_w<0, U - 1>([&](auto c) {
-        if (m + c.value < nk)
-            step(m + c.value, std::integral_constant<int, c.value % DEPTH>{}, std::integral_constant<int, c.value & 1>{});
+    sfor_while<0, U - 1>([&](auto c) {
+        if (m + c.value >= nk) return false;
+        step(m + c.value, std::integral_constant<int, c.value % DEPTH>{}, std::integral_constant<int, c.value & 1>{});
+        return true;
     });
 }
 
