@@ -381,9 +381,15 @@ __device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds,
         step(g + 2, std::integral_constant<int, 2>{});
         step(g + 3, std::integral_constant<int, 3>{});
     }
-    if (g < G) step(g, std::integral_constant<int, 0>{});
-    if (g + 1 < G) step(g + 1, std::integral_constant<int, 1>{});
-    if (g + 2 < G) step(g + 2, std::integral_constant<int, 2>{});
+    // the remaining groups nested (each step inside the branch of the one
+    // before), so that their waits count the ring's loads exactly
+    if (g < G) {
+        step(g, std::integral_constant<int, 0>{});
+        if (g + 1 < G) {
+            step(g + 1, std::integral_constant<int, 1>{});
+            if (g + 2 < G) step(g + 2, std::integral_constant<int, 2>{});
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll

@@ -222,6 +222,17 @@ def test_grouped_moe_baseline_config3_sampled(ctx, stream):
     ref_h2 = from_f16_bits(oracle.reduce_token_major(ref, w16.ravel(), T, k, d)).reshape(T, d)
     rel = oracle.rel_error(from_f16_bits(h2).reshape(T, d)[toks], ref_h2[toks])
     assert rel < TOL, f"h2 rel={rel}"
+    # and the first and last pair of every active expert: every grouping tile,
+    # both halves of the wide ones and every unit class is checked
+    srt = got["sorted"]
+    ends = sorted({i for e in np.unique(srt["expert"])
+                   for i in (int(np.flatnonzero(srt["expert"] == e)[0]), int(np.flatnonzero(srt["expert"] == e)[-1]))})
+    sel = srt[ends]
+    ref2 = oracle.grouped_route_partials(sel.astype(oracle.PAIR_DTYPE), hidden, d,
+                                         *_oracle_pool(pool_bytes, offs, stride), k, d, f, T)
+    slots = sel["token"].astype(np.int64) * k + sel["rank"].astype(np.int64)
+    rel = oracle.rel_error(gp.reshape(T * k, d)[slots], from_f16_bits(ref2).reshape(T * k, d)[slots])
+    assert rel < TOL, f"per-expert partials rel={rel}"
 
 
 @pytest.mark.parametrize("bits", [4, 3])
