@@ -255,13 +255,17 @@ __device__ __forceinline__ void dequant_chunk_sb(const QChunk<BITS>& w, uint32_t
 // then read at the start of each step (the other wave on the SIMD covers
 // that wait) to stay within 256 registers. acc[i][j]: token sub-tile i, the
 // wave's output sub-tile j; pl.wp0/sidx0 (and wp1/sidx1 for J = 2) index
-// sb_lds (filled by the caller before the call and published by the first
-// barrier inside); xp: this thread's activation row (token row
+// sb_lds, the table of `tcount` words tS[i] | tB[i] << 16 copied in here
+// once the first groups' weight and activation loads are issued (so that the
+// table's latency overlaps theirs) and published by the first barrier; xp:
+// this thread's activation row (token row
 // tid / (64/XH) of the block, clamped to a valid row) + XH·(tid % (64/XH))
 // halves, XH = halves it stages per group. lds: the three activation buffers.
 template <bool X_BF16, int J, int BITS = 4>
-__device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds, const uint32_t* sb_lds,
-                                             const ProjLanes& pl, const uint16_t* __restrict__ xp, uint32_t G) {
+__device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds, uint32_t* sb_lds,
+                                             const ProjLanes& pl, const uint16_t* __restrict__ xp, uint32_t G,
+                                             const uint16_t* __restrict__ tS, const uint16_t* __restrict__ tB,
+                                             uint32_t tcount) {
     constexpr uint32_t T = kProjBM * kGemmLdsStride;         // halves per activation buffer
     constexpr uint32_t NT = 64u * (8u / J);                  // threads of the block
     constexpr uint32_t XH = kProjBM * 64u / NT;              // activation halves staged per thread (16 or 8)
@@ -362,6 +366,7 @@ __device__ __forceinline__ void proj_core_pl(f32x16 (&acc)[2][J], _Float16* lds,
     load_w(1, std::integral_constant<int, 1>{});
     load_w(2, std::integral_constant<int, 2>{});
     load_w(3, std::integral_constant<int, 3>{});
+    copy_sb_to_lds<NT, 3>(tS, tB, sb_lds, tcount);
     store_x(xr[0], buf(0));
     store_x(xr[1], buf(1));
     load_x(2, std::integral_constant<int, 0>{});
@@ -451,13 +456,13 @@ __device__ __forceinline__ void gemm_q4_proj(const uint16_t* __restrict__ X, con
     uint32_t* sb_lds = reinterpret_cast<uint32_t*>(proj_lds + 3 * kProjBM * kGemmLdsStride);
     // scales / biases of rows n0 .. n0+255 (clamped to N): contiguous in S and B
     const uint32_t nrows = N - n0 < kProjBN ? N - n0 : kProjBN;
-    copy_sb_to_lds<kProjGemmThreads>(S + (size_t)n0 * G, B + (size_t)n0 * G, sb_lds, nrows * G);
     const ProjLanes pl = proj_lanes<1, BITS>(W, (K >> 3) * BITS, n0, wave, N, 0, G);
     // token rows past M read row 0: their results are never stored
     const uint32_t xrow = tid >> 3;
     const uint16_t* xp = X + (size_t)(m0 + xrow < M ? m0 + xrow : 0u) * ldx + 8u * (tid & 7u);
     f32x16 acc[2][1];
-    proj_core_pl<X_BF16, 1, BITS>(acc, proj_lds, sb_lds, pl, xp, G);
+    proj_core_pl<X_BF16, 1, BITS>(acc, proj_lds, sb_lds, pl, xp, G, S + (size_t)n0 * G, B + (size_t)n0 * G,
+                                  nrows * G);
     proj_for_each<1>(acc, [&](uint32_t m, uint32_t n, float v) {
         if (m0 + m < M && n0 + n < N)
             Y[(size_t)(m0 + m) * ldy + n0 + n] = X_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)v) : f2h(v);
