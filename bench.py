@@ -57,23 +57,26 @@ def moe_bytes():
 
 C4 = dict(d=2816, nq=16, nkv=8, hd=256, rotated_pairs=128, window=0, f=704, fs=2112, k=8,
           eps=1e-6, theta=10000.0, scale=1.0)
+# Gemma 4's full-attention layer form at the config-4 sizes: head_dim 512,
+# 2 kv heads, rope theta 1e6, partial rotary 0.25, no v projection
+C4_FULL = dict(C4, nkv=2, hd=512, rotated_pairs=64, theta=1e6, full=True)
 C4_CTX = 4096
 C4_LAYERS = 8
 
 
-def c4_bytes(shared_bits=4):
+def c4_bytes(shared_bits=4, shape=C4):
     """Algorithmic HBM bytes of one config-4 layer token (weights fp16 scale+bias,
     fp16 KV cache read once; activations and norm vectors are a few KB)."""
-    d, qd, kvd = C4["d"], C4["nq"] * C4["hd"], C4["nkv"] * C4["hd"]
+    d, qd, kvd = shape["d"], shape["nq"] * shape["hd"], shape["nkv"] * shape["hd"]
     q4 = lambda m, n: m * n // 2 + 2 * m * (n // 64) * 2
     qs = (lambda m, n: m * n + 2 * m * (n // 64) * 2) if shared_bits == 8 else q4
     parts = {
-        "qkv": q4(qd + 2 * kvd, d),
+        "qkv": q4(qd + (1 if shape.get("full") else 2) * kvd, d),
         "attention_kv": 2 * C4_CTX * kvd * 2,
         "o_proj": q4(d, qd),
         "router": E * d + 2 * E * (d // 64) * 2,
-        "routed": C4["k"] * 3 * q4(C4["f"], d),
-        "shared": 2 * qs(C4["fs"], d) + qs(d, C4["fs"]),
+        "routed": shape["k"] * 3 * q4(shape["f"], d),
+        "shared": 2 * qs(shape["fs"], d) + qs(d, shape["fs"]),
     }
     parts["total"] = sum(parts.values())
     return parts
@@ -195,21 +198,24 @@ def bench_bits(ctx, stream, batch_avg_us, router, hbuf):
     return out
 
 
-def bench_c4(ctx, stream, launch, batch_avg_us, shared_bits=4):
+def bench_c4(ctx, stream, launch, batch_avg_us, shared_bits=4, shape=C4):
     """Config 4's decoder layer; shared_bits 8 runs the shared expert at
-    8 bits (the reference's default width) instead of 4."""
+    8 bits (the reference's default width) instead of 4; shape C4_FULL runs
+    the full-attention layer form."""
     from edgeexpert_amd import ops, synth
     from edgeexpert_amd.runtime import DeviceBuffer, Event, Graph
     t0 = time.time()
-    w = synth.decode_layer(0, "c4", C4["d"], C4["nq"], C4["nkv"], C4["hd"], E, C4["f"], C4["fs"],
-                           shared_bits=shared_bits)
-    kvd = C4["nkv"] * C4["hd"]
-    kc = synth.f16_vector(0, "c4/kc", C4_CTX * kvd)
-    vc = synth.f16_vector(0, "c4/vc", C4_CTX * kvd)
-    spec = ops.DecodeLayerShapeSpec(d=C4["d"], num_q_heads=C4["nq"], num_kv_heads=C4["nkv"],
-                                    head_dim=C4["hd"], expert_f=C4["f"], shared_f=C4["fs"], top_k=C4["k"],
-                                    rotated_pairs=C4["rotated_pairs"], window=C4["window"], eps=C4["eps"],
-                                    rope_theta=C4["theta"], attn_scale=C4["scale"])
+    C = shape
+    tag = "c4full" if C.get("full") else "c4"
+    w = synth.decode_layer(0, tag, C["d"], C["nq"], C["nkv"], C["hd"], E, C["f"], C["fs"],
+                           shared_bits=shared_bits, v_proj=not C.get("full", False))
+    kvd = C["nkv"] * C["hd"]
+    kc = synth.f16_vector(0, tag + "/kc", C4_CTX * kvd)
+    vc = synth.f16_vector(0, tag + "/vc", C4_CTX * kvd)
+    spec = ops.DecodeLayerShapeSpec(d=C["d"], num_q_heads=C["nq"], num_kv_heads=C["nkv"],
+                                    head_dim=C["hd"], expert_f=C["f"], shared_f=C["fs"], top_k=C["k"],
+                                    rotated_pairs=C["rotated_pairs"], window=C["window"], eps=C["eps"],
+                                    rope_theta=C["theta"], attn_scale=C["scale"])
     # distinct device copies (same values, different addresses): each token's
     # layer reads weights and KV that the previous layers evicted from L2/MALL
     layers, caches = [], []
@@ -218,8 +224,8 @@ def bench_c4(ctx, stream, launch, batch_avg_us, shared_bits=4):
         caches.append((DeviceBuffer.from_array(kc), DeviceBuffer.from_array(vc)))
     ws_bytes = ops.decode_layer_workspace_bytes(spec, C4_CTX)
     ws = DeviceBuffer(ws_bytes)
-    hid = DeviceBuffer.from_array(synth.f16_vector(0, "c4/hidden", C4["d"]))
-    log(f"config 4: {C4_LAYERS} layer copies resident, set up in {time.time() - t0:.1f}s")
+    hid = DeviceBuffer.from_array(synth.f16_vector(0, tag + "/hidden", C["d"]))
+    log(f"config 4 ({tag}): {C4_LAYERS} layer copies resident, set up in {time.time() - t0:.1f}s")
     pos = C4_CTX - 1
 
     def stack():
@@ -242,22 +248,24 @@ def bench_c4(ctx, stream, launch, batch_avg_us, shared_bits=4):
     b.record(stream)
     stream.sync()
     us = a.elapsed_ms(b) * 1e3 / (reps * C4_LAYERS)
-    nb = c4_bytes(shared_bits)
+    nb = c4_bytes(shared_bits, C)
     gbs = nb["total"] / (us * 1e-6) / 1e9
     floor_us = nb["total"] / (HBM_PEAK_GBS * 1e9) * 1e6
     # attention alone (split-K partial + combine over the 4096-key cache), back to back
     att = ops.Attention(ctx)
-    q = DeviceBuffer.from_array(synth.f16_vector(0, "c4/q", C4["nq"] * C4["hd"]))
-    out = DeviceBuffer(C4["nq"] * C4["hd"] * 2)
-    aws = ops.Attention.workspace_bytes(C4["hd"], C4["nq"], C4_CTX)
+    q = DeviceBuffer.from_array(synth.f16_vector(0, tag + "/q", C["nq"] * C["hd"]))
+    out = DeviceBuffer(C["nq"] * C["hd"] * 2)
+    aws = ops.Attention.workspace_bytes(C["hd"], C["nq"], C4_CTX)
     awsb = DeviceBuffer(aws)
     attn_us = batch_avg_us(lambda i: att.encode(stream, q, caches[i % C4_LAYERS][0], caches[i % C4_LAYERS][1],
-                                                out, C4["hd"], C4["nq"], C4["nkv"], C4_CTX, awsb, aws,
+                                                out, C["hd"], C["nq"], C["nkv"], C4_CTX, awsb, aws,
                                                 scale=1.0), 64)
     attn_gbs = nb["attention_kv"] / (attn_us * 1e-6) / 1e9
-    log(f"decode layer C4 ({launch}, {shared_bits}-bit shared expert): {us:.2f} us/token ({gbs:.0f} GB/s of {nb['total']} B; "
-        f"8 TB/s floor {floor_us:.2f} us); attention alone {attn_us:.2f} us ({attn_gbs:.0f} GB/s)")
+    log(f"decode layer {tag} ({launch}, {shared_bits}-bit shared expert): {us:.2f} us/token ({gbs:.0f} GB/s of "
+        f"{nb['total']} B; 8 TB/s floor {floor_us:.2f} us); attention alone {attn_us:.2f} us ({attn_gbs:.0f} GB/s)")
     return {"us_per_token": round(us, 3), "shared_expert_bits": shared_bits, "bytes_per_token": nb["total"],
+            "attention_form": ("full: head_dim 512, 16 q / 2 kv heads, V from the k projection, rope theta 1e6, "
+                               "64 rotated pairs") if C.get("full") else "sliding: head_dim 256, 16 q / 8 kv heads",
             "gbs": round(gbs, 1),
             "hbm_floor_us": round(floor_us, 3), "frac_of_floor": round(floor_us / us, 4),
             "bytes": {k: v for k, v in nb.items() if k != "total"}, "layers_rotated": C4_LAYERS,
@@ -551,7 +559,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=8, help="untimed replays before them")
     ap.add_argument("--legs", default="all",
                     help="comma list of the extra legs to run besides the headline: c0, c2, lmhead, c3, c4, "
-                         "policy, bits, cpu (default all)")
+                         "c4full, policy, bits, cpu (default all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--launch", choices=("graph", "stream"), default="graph",
                     help="replay the 64-token step from a HIP graph, or issue it from the host")
@@ -799,6 +807,7 @@ def main():
     c3 = bench_c3(ctx, stream, batch_avg_us) if want("c3") else None
     c4 = bench_c4(ctx, stream, args.launch, batch_avg_us) if want("c4") else None
     c4_s8 = bench_c4(ctx, stream, args.launch, batch_avg_us, shared_bits=8) if want("c4") else None
+    c4_full = bench_c4(ctx, stream, args.launch, batch_avg_us, shape=C4_FULL) if want("c4full") else None
     gemm_policy = bench_gemm_policy(ctx, stream, batch_avg_us) if want("policy") else None
     bits_legs = bench_bits(ctx, stream, batch_avg_us, router, hbuf) if want("bits") else None
     if bits_legs is not None and want("c3"):
@@ -854,6 +863,7 @@ def main():
         "grouped_prefill_c3": c3,
         "decode_layer_c4": c4,
         "decode_layer_c4_int8_shared": c4_s8,
+        "decode_layer_c4_full_attention": c4_full,
         "gemm_by_token_count": gemm_policy,
         "bit_variants": bits_legs,
         "wall_s": round(wall, 4),

@@ -17,6 +17,7 @@ CODE_OBJECT_UNITS = ("tfq_gemv", "tfq_int8", "tfq_phase1", "tfq_phase1_routed", 
 CODE_OBJECT_PATHS = [os.path.join(LIB_DIR, u + ".co") for u in CODE_OBJECT_UNITS]
 CODE_OBJECT_PATH = LIB_DIR
 
+ABI_VERSION = 3          # TFQ_ABI_VERSION of include/tfq.h this binding follows
 TFQ_OK = 0
 TFQ_E_INVAL = 1
 TFQ_E_UNSUPPORTED = 2
@@ -162,6 +163,7 @@ SIGNATURES = {
     "tfq_decode_layer_workspace_bytes": [C.POINTER(DecodeLayerShape), _U32],
     "tfq_decode_layer": [_P, _P, C.POINTER(DecodeLayerWeights), C.POINTER(DecodeLayerShape), _P, _P, _P,
                          _P, _U32, _P, _P, _P, C.c_size_t],
+    "tfq_abi_version": [],
     "tfq_rt_device_count": [C.POINTER(_I)],
     "tfq_rt_set_device": [_I],
     "tfq_rt_device_info": [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t],
@@ -206,6 +208,9 @@ def _load():
             f = getattr(lib, name)
             f.argtypes = args
             f.restype = _RES.get(name, C.c_int)
+        if lib.tfq_abi_version() != ABI_VERSION:
+            raise TfqNotBuilt(f"{LIB_PATH} has ABI version {lib.tfq_abi_version()}, this binding expects "
+                              f"{ABI_VERSION}: rebuild with `python -m edgeexpert_amd.build`")
         _lib = lib
     return _lib
 

@@ -108,6 +108,19 @@ public:
         return launch_multi(stream, mats, x, n, bits);
     }
 
+    // q and k only (the full-attention layers, whose V is formed from k).
+    int encode_qk(void* stream, const tfq_q4_matrix& q, const tfq_q4_matrix& k, const uint16_t* x,
+                  uint16_t* yq, uint16_t* yk, uint32_t mq, uint32_t mkv, uint32_t n,
+                  const NormArg& stage = stage_copy(), uint32_t bits = 4) const {
+        Q4Multi mats{};
+        mats.m[0] = {static_cast<const uint8_t*>(q.weights), q.scales, q.biases, yq, nullptr, mq, 0};
+        mats.m[1] = {static_cast<const uint8_t*>(k.weights), k.scales, k.biases, yk, nullptr, mkv, 0};
+        mats.nmat = 2;
+        mats.total_rows = mq + mkv;
+        mats.norm = stage;
+        return launch_multi(stream, mats, x, n, bits);
+    }
+
 private:
     int launch_multi(void* stream, Q4Multi& mats, const uint16_t* x, uint32_t n, uint32_t bits) const {
         // the reference's attention kernels exist at 3 and 4 bits (DequantInt4GEMV.swift:149-150)
@@ -838,9 +851,13 @@ public:
         if (nkv == 0 || nq == 0 || nq % nkv != 0)
             return fail(TFQ_E_INVAL, "numQHeads must be a multiple of numKVHeads for GQA");
         const uint32_t G = nq / nkv;
-        if (hd != 128 && hd != 256) return fail(TFQ_E_UNSUPPORTED, "head_dim=%u (supported: 128, 256)", hd);
-        if (G != 1 && G != 2 && G != 4)
-            return fail(TFQ_E_UNSUPPORTED, "GQA group %u (supported: 1, 2, 4)", G);
+        if (hd != 128 && hd != 256 && hd != 512)
+            return fail(TFQ_E_UNSUPPORTED, "head_dim=%u (supported: 128, 256, 512)", hd);
+        if (hd == 512 ? (G != 1 && G != 2 && G != 4 && G != 8) : (G != 1 && G != 2 && G != 4))
+            return fail(TFQ_E_UNSUPPORTED, "GQA group %u at head_dim %u (supported: 1, 2, 4%s)", G, hd,
+                        hd == 512 ? ", 8" : "");
+        // query heads per block (attention.hpp): the 8 of a kv head at head_dim 512 in two blocks
+        const uint32_t nsub = hd == 512 && G == 8 ? 2 : 1;
         if (seq_len == 0) return fail(TFQ_E_INVAL, "attention requires at least one KV position");
         if (!q || !k_cache || !v_cache || !out || !workspace) return fail(TFQ_E_INVAL, "null pointer argument");
         if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(workspace, 16))
@@ -852,6 +869,13 @@ public:
             if (epi.rotated_pairs > hd / 2) return fail(TFQ_E_INVAL, "rotatedPairs exceeds head_dim/2");
             if (!(epi.eps > 0.0f) || !(epi.theta > 0.0f))
                 return fail(TFQ_E_INVAL, "epilogue eps and rope theta must be positive");
+            if ((epi.k_raw == nullptr) != (epi.v_raw == nullptr))
+                return fail(TFQ_E_INVAL, "staged raw k and v go together");
+            if (nsub > 1 && !epi.k_raw)
+                return fail(TFQ_E_INVAL, "head_dim %u with group %u needs the new k/v staged outside the caches",
+                            hd, G);
+            if (epi.k_raw && (!aligned(epi.k_raw, 16) || !aligned(epi.v_raw, 16)))
+                return fail(TFQ_E_INVAL, "staged k/v rows must be 16-byte aligned");
         }
         const uint32_t nc = chunks(seq_len, window);
         if (nc > kAttnMaxChunks) return fail(TFQ_E_UNSUPPORTED, "more than 65536 visible keys");
@@ -866,7 +890,10 @@ public:
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_attn_partial_h%u_g%u", hd, G);
         void* a1[] = {&q, &k_cache, &v_cache, &nkv, &seq_len, &ks, &scale, &e, &part_o, &part_ml};
-        int rc = launch2(m_, name, nc, nkv, 256, 0, stream, a1);
+        hipFunction_t pf = m_.get(name);
+        if (!pf) return fail(TFQ_E_NOT_LOADED, "kernel %s is not in the code object", name);
+        int rc = hip_check(hipModuleLaunchKernel(pf, nc, nkv, nsub, 256, 1, 1, 0, (hipStream_t)stream, a1, nullptr),
+                           name);
         if (rc) return rc;
         std::snprintf(name, sizeof(name), "tfq_attn_combine_h%u", hd);
         uint32_t ncu = nc;
@@ -898,7 +925,7 @@ public:
     }
 
     struct Layout {
-        size_t q, attn, parts, parts_bytes, o, logits, idx, w, acts, sact, h1, h2, hmid, inv, total;
+        size_t q, attn, parts, parts_bytes, o, logits, idx, w, acts, sact, h1, h2, hmid, inv, kv, total;
     };
     static Layout layout(const tfq_decode_layer_shape& s, uint32_t max_seq) {
         auto up = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -919,6 +946,7 @@ public:
         L.h2 = off;     off += up((size_t)s.d * 2);
         L.hmid = off;   off += up((size_t)s.d * 2);
         L.inv = off;    off += up(4);
+        L.kv = off;     off += up((size_t)2 * s.num_kv_heads * s.head_dim * 2);   // staged raw k, v
         L.total = off;
         return L;
     }
@@ -963,13 +991,24 @@ public:
         const uint32_t qd = s.num_q_heads * s.head_dim, kvd = s.num_kv_heads * s.head_dim;
         const size_t slot = (size_t)position * kvd;
 
-        // 1. input RMSNorm fused into the QKV GEMV; k and v land in the cache slot
+        // 1. input RMSNorm fused into the QKV GEMV; k and v land in the cache
+        //    slot, or in the workspace when the attention blocks of a kv head
+        //    all read them (head_dim 512 with group 8) or V is the k
+        //    projection (v_proj absent: the full-attention layers,
+        //    RealForwardRunner.swift:2252-2255, whose fused QKV runs k_proj as
+        //    the v projection; one k GEMV serves both here)
         const NormArg in_norm{w.input_norm, nullptr, nullptr, s.eps, kStageNorm};
-        int rc = gemv_.encode_qkv(stream, w.q_proj, w.k_proj, w.v_proj, hidden_in, q, k_cache + slot,
-                                  v_cache + slot, qd, kvd, s.d, in_norm);
+        const bool v_from_k = w.v_proj.weights == nullptr;
+        const bool staged = v_from_k || (s.head_dim == 512 && s.num_q_heads == 8 * s.num_kv_heads);
+        uint16_t* kraw = staged ? reinterpret_cast<uint16_t*>(ws + L.kv) : k_cache + slot;
+        uint16_t* vraw = !staged ? v_cache + slot : v_from_k ? kraw : kraw + kvd;
+        int rc = v_from_k ? gemv_.encode_qk(stream, w.q_proj, w.k_proj, hidden_in, q, kraw, qd, kvd, s.d, in_norm)
+                          : gemv_.encode_qkv(stream, w.q_proj, w.k_proj, w.v_proj, hidden_in, q, kraw, vraw, qd, kvd,
+                                             s.d, in_norm);
         if (rc) return rc;
         // 2. q/k/v epilogue + attention
-        const AttnEpilogue epi{w.q_norm, w.k_norm, s.eps, s.rope_theta, s.rotated_pairs, 0, 0.0};
+        const AttnEpilogue epi{w.q_norm, w.k_norm, s.eps, s.rope_theta, s.rotated_pairs, 0, 0.0,
+                               staged ? kraw : nullptr, staged ? vraw : nullptr};
         rc = attn_.encode(stream, q, k_cache, v_cache, attn, s.head_dim, s.num_q_heads, s.num_kv_heads,
                           seq_len, s.window, s.attn_scale, epi, ws + L.parts, L.parts_bytes);
         if (rc) return rc;

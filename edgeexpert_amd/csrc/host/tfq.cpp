@@ -67,11 +67,12 @@ static std::vector<std::string> kernel_names() {
                           "tfq_moe_grouped_down_b3", "tfq_moe_combine", "tfq_moe_combine_x8"})
         names.push_back(n);
     names.push_back("tfq_convert_bf16_f16");
-    for (const char* hd : {"128", "256"}) {
+    for (const char* hd : {"128", "256", "512"}) {
         for (const char* g : {"1", "2", "4"})
             names.push_back(std::string("tfq_attn_partial_h") + hd + "_g" + g);
         names.push_back(std::string("tfq_attn_combine_h") + hd);
     }
+    names.push_back("tfq_attn_partial_h512_g8");
     names.push_back("tfq_layer_tail");
     return names;
 }
@@ -435,7 +436,7 @@ int tfq_attention_decode(tfq_ctx* ctx, void* stream, const uint16_t* q, const ui
                          uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t seq_len,
                          uint32_t window, float scale, void* workspace, size_t workspace_bytes) {
     TFQ_REQUIRE_CTX(ctx);
-    const AttnEpilogue none{nullptr, nullptr, 0.0f, 0.0f, 0, 0, 0.0};
+    const AttnEpilogue none{nullptr, nullptr, 0.0f, 0.0f, 0, 0, 0.0, nullptr, nullptr};
     // without the epilogue the kernels only read the caches
     return ctx->attn->encode(stream, q, const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache),
                              out, head_dim, num_q_heads, num_kv_heads, seq_len, window, scale, none,
@@ -446,6 +447,8 @@ size_t tfq_decode_layer_workspace_bytes(const tfq_decode_layer_shape* shape, uin
     if (!shape || max_seq_len == 0) return 0;
     return DecodeLayer::layout(*shape, max_seq_len).total;
 }
+
+int tfq_abi_version(void) { return TFQ_ABI_VERSION; }
 
 int tfq_decode_layer(tfq_ctx* ctx, void* stream, const tfq_decode_layer_weights* weights,
                      const tfq_decode_layer_shape* shape, const uint16_t* hidden_in,

@@ -73,7 +73,11 @@ constexpr uint32_t kAttnCombineThreads = 256;
 // (fused_qkv_epilogue, S/Metal/Fusions/fused.metal:86-180): per-head RMSNorm
 // of q and k with the shared head-dim weights, NeoX RoPE of the first
 // rotated_pairs pairs at the new token's position, no-scale RMSNorm of v.
-// q_norm == null disables it (plain attention).
+// q_norm == null disables it (plain attention). k_raw / v_raw: the new
+// token's raw k and v rows [num_kv_heads][head_dim] when they are staged
+// outside the caches (required when a kv head's query heads are split over
+// blocks, which then all read them; v_raw == k_raw for the full-attention
+// layers that take V from the k projection); null: read from the cache slot.
 struct AttnEpilogue {
     const uint16_t* q_norm;
     const uint16_t* k_norm;
@@ -82,6 +86,8 @@ struct AttnEpilogue {
     uint32_t rotated_pairs;
     uint32_t pad_;
     double log2_theta;      // log2(theta), set by the launcher
+    const uint16_t* k_raw;
+    const uint16_t* v_raw;
 };
 
 // Up to three matrices sharing x and n (plain GEMV: 1; fused QKV: 3).

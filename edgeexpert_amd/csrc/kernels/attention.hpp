@@ -14,11 +14,14 @@
 // (V/Reference/Attention/Attention.swift:14-104) regrouped by chunk.
 //
 // Mapping inside a block (256 threads): for q·k, 16 lanes own one key (each
-// lane two 16-byte pieces of the 512-byte row, so one load instruction covers
-// 4 whole rows); for p·V, HD/8 threads own one key row with 16-byte loads and
-// 2048/HD groups of them split the chunk's keys, reduced through LDS in group
-// order. The chunk's K loads are issued first, its V loads after the q/k/v
-// epilogue.
+// lane HD/128 16-byte pieces of the row, so one load instruction covers
+// 2048/HD whole rows); for p·V, HD/8 threads own one key row with 16-byte
+// loads and 2048/HD groups of them split the chunk's keys, reduced through
+// LDS in group order. The chunk's K loads are issued first, its V loads after
+// the q/k/v epilogue. A block serves GB of the G query heads of its kv head
+// (GB = G up to head_dim 256; at head_dim 512, the full-attention layers'
+// 16 q / 2 kv heads, two blocks of 4 heads each per (chunk, kv head), which
+// keeps the query registers to 64 per lane and gives 256 blocks at 4096 keys).
 #pragma once
 
 #include "common.hpp"
@@ -73,37 +76,43 @@ __device__ __forceinline__ void wave_head_norm(const uint16_t* __restrict__ src,
     }
 }
 
-template <int HD, int G>
+template <int HD, int GB>
 struct AttnLds {
-    uint16_t q[G][HD];
+    uint16_t q[GB][HD];
     uint16_t wn[2][HD];       // q and k norm weights
     uint16_t kp[HD];
     uint16_t vp[HD];
     float rc[HD / 2];
     float rs[HD / 2];
-    float p[G][kAttnChunk];
-    float ml[G][2];
-    float red[2048 / HD][G][HD];
+    float p[GB][kAttnChunk];
+    float ml[GB][2];
+    float red[2048 / HD][GB][HD];
 };
 
-// One (chunk, kv head) block. q: fp16 [num_q_heads][HD] (raw projection when
-// the epilogue is on); part_o: fp32 [num_q_heads][nchunks][HD];
-// part_ml: fp32 [num_q_heads][nchunks][2].
-template <int HD, int G>
+// One (chunk, kv head, query-head subset) block: blockIdx = (chunk, kv head h,
+// subset z), query heads h·G + z·GB + [0, GB). q: fp16 [num_q_heads][HD] (raw
+// projection when the epilogue is on); part_o: fp32
+// [num_q_heads][nchunks][HD]; part_ml: fp32 [num_q_heads][nchunks][2].
+// With GB < G every subset block of the new token's chunk runs the k/v
+// epilogue on the staged raw rows (epi.k_raw / v_raw) and writes the same
+// words into the cache slot; nothing reads that slot from the caches.
+template <int HD, int G, int GB = G>
 __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uint16_t* __restrict__ kc,
                                              uint16_t* __restrict__ vc, uint32_t nkv, uint32_t seq_len,
                                              uint32_t kv_start, float scale, const AttnEpilogue& epi,
                                              float* __restrict__ part_o, float* __restrict__ part_ml) {
-    static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
+    static_assert(HD == 128 || HD == 256 || HD == 512, "head_dim 128, 256 or 512");
+    static_assert(GB >= 1 && G % GB == 0, "query heads split evenly over blocks");
     constexpr uint32_t CPL = HD / 128;                 // 16-byte pieces per lane per key (q·k)
     constexpr uint32_t TPR = HD / 8;                   // threads per V row
     constexpr uint32_t VGROUPS = kAttnThreads / TPR;
     constexpr uint32_t KPG = kAttnChunk / VGROUPS;     // keys per V group
     constexpr uint32_t KSTEPS = kAttnChunk / (kAttnThreads / kAttnKeyLanes);
-    __shared__ __attribute__((aligned(16))) AttnLds<HD, G> L;
+    __shared__ __attribute__((aligned(16))) AttnLds<HD, GB> L;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t chunk = blockIdx.x, h = blockIdx.y, nchunks = gridDim.x;
+    const uint32_t qh0 = h * G + (GB < G ? blockIdx.z * GB : 0u);       // first query head of the block
     const uint32_t c0 = kv_start + chunk * kAttnChunk;
     const uint32_t n = seq_len - c0 < kAttnChunk ? seq_len - c0 : kAttnChunk;
     const size_t row = (size_t)nkv * HD;               // halves between consecutive positions
@@ -121,12 +130,14 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
     // past the queries re-read the last chunk, blocks without the new token
     // re-read the queries), so each wait covers exactly the loads before it:
     // the epilogue runs while K streams in, the scores while V does.
-    constexpr uint32_t QCH = G * HD / 8;
+    constexpr uint32_t QCH = GB * HD / 8;
     constexpr uint32_t KVCH = 2 * (HD / 8);
     static_assert(QCH <= kAttnThreads && KVCH <= kAttnThreads, "one chunk per thread");
-    const uint4 qraw = reinterpret_cast<const uint4*>(q + (size_t)h * G * HD)[tid < QCH ? tid : QCH - 1];
+    const uint4 qraw = reinterpret_cast<const uint4*>(q + (size_t)qh0 * HD)[tid < QCH ? tid : QCH - 1];
     const uint32_t kvi = tid % KVCH;
-    const uint16_t* kvsrc = own_pos ? (kvi < HD / 8 ? kc : vc) + (size_t)pos * row + (size_t)h * HD : q;
+    const uint16_t* kvsrc = !own_pos ? q
+                            : epi.k_raw ? (kvi < HD / 8 ? epi.k_raw : epi.v_raw) + (size_t)h * HD
+                                        : (kvi < HD / 8 ? kc : vc) + (size_t)pos * row + (size_t)h * HD;
     const uint4 kvraw = reinterpret_cast<const uint4*>(kvsrc)[kvi % (HD / 8)];
     const uint16_t* wsrc = epi_on ? (kvi < HD / 8 ? epi.q_norm : epi.k_norm) : q;
     const uint4 wraw = reinterpret_cast<const uint4*>(wsrc)[kvi % (HD / 8)];
@@ -150,17 +161,17 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
             if (own_pos) reinterpret_cast<uint4*>(tid < HD / 8 ? L.kp : L.vp)[tid % (HD / 8)] = kvraw;
         }
         __syncthreads();
-        const uint32_t nvec = G + (own_pos ? 2u : 0u);
+        const uint32_t nvec = GB + (own_pos ? 2u : 0u);
         for (uint32_t v = wave; v < nvec; v += kAttnThreads / 64) {
-            uint16_t* buf = v < G ? L.q[v] : (v == G ? L.kp : L.vp);
-            const uint16_t* w = v < G ? L.wn[0] : (v == G ? L.wn[1] : nullptr);
+            uint16_t* buf = v < GB ? L.q[v] : (v == GB ? L.kp : L.vp);
+            const uint16_t* w = v < GB ? L.wn[0] : (v == GB ? L.wn[1] : nullptr);
             wave_head_norm<HD>(buf, buf, w, epi.eps);
         }
         __syncthreads();
-        const uint32_t nrot = G + (own_pos ? 1u : 0u);
+        const uint32_t nrot = GB + (own_pos ? 1u : 0u);
         for (uint32_t i = tid; i < nrot * epi.rotated_pairs; i += kAttnThreads) {
             const uint32_t v = i / epi.rotated_pairs, pr = i % epi.rotated_pairs;
-            uint16_t* buf = v < G ? L.q[v] : L.kp;
+            uint16_t* buf = v < GB ? L.q[v] : L.kp;
             const float x0 = h2f(buf[pr]), x1 = h2f(buf[pr + HD / 2]);
             buf[pr] = f2h(x0 * L.rc[pr] - x1 * L.rs[pr]);
             buf[pr + HD / 2] = f2h(x0 * L.rs[pr] + x1 * L.rc[pr]);
@@ -187,9 +198,9 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
     }
 
     // 3. scores
-    h2 qv[G][CPL][4];
+    h2 qv[GB][CPL][4];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < GB; ++g)
 #pragma unroll
         for (uint32_t cc = 0; cc < CPL; ++cc) {
             const uint4 raw = *reinterpret_cast<const uint4*>(&L.q[g][8u * (sl + 16u * cc)]);
@@ -201,9 +212,9 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
 #pragma unroll
     for (uint32_t st = 0; st < KSTEPS; ++st) {
         const uint32_t j = st * (kAttnThreads / kAttnKeyLanes) + (tid >> 4);
-        float acc[G];
+        float acc[GB];
 #pragma unroll
-        for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+        for (int g = 0; g < GB; ++g) acc[g] = 0.0f;
 #pragma unroll
         for (uint32_t cc = 0; cc < CPL; ++cc) {
             uint4 kk = kr[st][cc];
@@ -211,12 +222,12 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
             const h2 k4[4] = {__builtin_bit_cast(h2, kk.x), __builtin_bit_cast(h2, kk.y),
                               __builtin_bit_cast(h2, kk.z), __builtin_bit_cast(h2, kk.w)};
 #pragma unroll
-            for (int g = 0; g < G; ++g)
+            for (int g = 0; g < GB; ++g)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[g] = __builtin_amdgcn_fdot2(k4[e], qv[g][cc][e], acc[g], false);
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
+        for (int g = 0; g < GB; ++g) {
             const float sdot = row16_sum(acc[g]);
             if (sl == 0) L.p[g][j] = j < n ? sdot * scale : -__builtin_inff();
         }
@@ -224,7 +235,7 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
     __syncthreads();
 
     // 4. chunk softmax statistics, one wavefront per query head
-    for (uint32_t g = wave; g < (uint32_t)G; g += kAttnThreads / 64) {
+    for (uint32_t g = wave; g < (uint32_t)GB; g += kAttnThreads / 64) {
         const float sv = lane < kAttnChunk ? L.p[g][lane] : -__builtin_inff();
         const float m = wave_max(sv);
         const float e = lane < n ? expf(sv - m) : 0.0f;
@@ -238,9 +249,9 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
     __syncthreads();
 
     // 5. p·V
-    float o[G][8];
+    float o[GB][8];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < GB; ++g)
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
 #pragma unroll
@@ -250,27 +261,27 @@ __device__ __forceinline__ void attn_partial(const uint16_t* __restrict__ q, uin
         if (own_pos && c0 + j == pos) vv = *reinterpret_cast<const uint4*>(&L.vp[8u * vl]);
         const h8 v8 = __builtin_bit_cast(h8, vv);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
+        for (int g = 0; g < GB; ++g) {
             const float pj = L.p[g][j];
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pj, (float)v8[e], o[g][e]);
         }
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < GB; ++g)
 #pragma unroll
         for (int e = 0; e < 8; ++e) L.red[vg][g][8u * vl + e] = o[g][e];
     __syncthreads();
-    for (uint32_t i = tid; i < G * HD; i += kAttnThreads) {
+    for (uint32_t i = tid; i < GB * HD; i += kAttnThreads) {
         const uint32_t g = i / HD, d = i % HD;
         float s = 0.0f;
 #pragma unroll
         for (uint32_t r = 0; r < VGROUPS; ++r) s += L.red[r][g][d];
-        const size_t qh = (size_t)h * G + g;
+        const size_t qh = (size_t)qh0 + g;
         part_o[(qh * nchunks + chunk) * HD + d] = s;
     }
-    if (tid < (uint32_t)G) {
-        const size_t qh = (size_t)h * G + tid;
+    if (tid < (uint32_t)GB) {
+        const size_t qh = (size_t)qh0 + tid;
         part_ml[(qh * nchunks + chunk) * 2 + 0] = L.ml[tid][0];
         part_ml[(qh * nchunks + chunk) * 2 + 1] = L.ml[tid][1];
     }

@@ -65,12 +65,14 @@ constexpr int kRowsInFlight = 1;
         router_logits<SEG, P>(W, S, B, h, eff, logits, E, d, norm);                               \
     }
 
-#define TFQ_ATTN(HD, G)                                                                          \
+// GB: query heads per block (G / GB blocks per (chunk, kv head), blockIdx.z).
+#define TFQ_ATTN_GB(HD, G, GB)                                                                   \
     extern "C" __global__ __launch_bounds__(kAttnThreads) void tfq_attn_partial_h##HD##_g##G(    \
         const uint16_t* q, uint16_t* kc, uint16_t* vc, uint32_t nkv, uint32_t seq_len,           \
         uint32_t kv_start, float scale, AttnEpilogue epi, float* part_o, float* part_ml) {        \
-        attn_partial<HD, G>(q, kc, vc, nkv, seq_len, kv_start, scale, epi, part_o, part_ml);      \
+        attn_partial<HD, G, GB>(q, kc, vc, nkv, seq_len, kv_start, scale, epi, part_o, part_ml);  \
     }
+#define TFQ_ATTN(HD, G) TFQ_ATTN_GB(HD, G, G)
 
 #define TFQ_ATTN_COMBINE(HD)                                                                     \
     extern "C" __global__ __launch_bounds__(kAttnCombineThreads) void tfq_attn_combine_h##HD(    \

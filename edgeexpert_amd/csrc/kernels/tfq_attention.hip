@@ -8,8 +8,13 @@ TFQ_ATTN(128, 4)
 TFQ_ATTN(256, 1)
 TFQ_ATTN(256, 2)
 TFQ_ATTN(256, 4)
+TFQ_ATTN(512, 1)
+TFQ_ATTN(512, 2)
+TFQ_ATTN(512, 4)
+TFQ_ATTN_GB(512, 8, 4)
 TFQ_ATTN_COMBINE(128)
 TFQ_ATTN_COMBINE(256)
+TFQ_ATTN_COMBINE(512)
 
 extern "C" __global__ __launch_bounds__(kLayerTailThreads) void tfq_layer_tail(
     const uint16_t* hidden, const uint16_t* attn, const uint16_t* w_post_attn, const uint16_t* h1,

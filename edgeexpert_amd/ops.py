@@ -610,6 +610,8 @@ class DecodeLayerWeightsSpec:
             return DeviceBuffer.from_array(np.ascontiguousarray(a))
 
         def q4(t, bits=4):
+            if t is None:       # no v projection (full-attention layers): null matrix
+                return Q4Projection(None, None, None, 0, 0)
             W, S, B = t
             rows, cols = W.shape[0], W.shape[1] * 8 // bits
             return Q4Projection(buf(W), buf(S), buf(B), rows, cols)
@@ -622,7 +624,7 @@ class DecodeLayerWeightsSpec:
                         buf(w["router_gain"]) if w.get("router_gain") is not None else None)
         pool = ExpertPool(buf(w["pool"]), int(w["stride"]), E, dict(w["off"]),
                           weight_bits=int(w.get("expert_bits", 4)))
-        return cls(buf(w["input_norm"]), q4(w["q"]), q4(w["k"]), q4(w["v"]), buf(w["q_norm"]),
+        return cls(buf(w["input_norm"]), q4(w["q"]), q4(w["k"]), q4(w.get("v")), buf(w["q_norm"]),
                    buf(w["k_norm"]), q4(w["o"]), buf(w["post_attention_norm"]), buf(w["pre_ffn_norm"]),
                    buf(w["pre_ffn2_norm"]), router, pool, q4(w["shared_gate"], sb), q4(w["shared_up"], sb),
                    q4(w["shared_down"], sb), buf(w["post_ffn1_norm"]), buf(w["post_ffn2_norm"]),

@@ -237,7 +237,7 @@ def norm_weight(seed: int, label: str, n: int, lo: float = 0.5, hi: float = 1.5)
 
 def decode_layer(seed: int, label: str, d: int, nq: int, nkv: int, hd: int, num_experts: int,
                  f: int, fs: int, layer_scalar: float = 0.75, expert_bits: int = 4,
-                 shared_bits: int = 4) -> dict:
+                 shared_bits: int = 4, v_proj: bool = True) -> dict:
     """Weights of one Gemma 4 decoder layer with the BASELINE distributions:
     int4 g64 projections as in config 0, an int8 g64 router, num_experts
     routed experts in one pool, a shared expert of int4 (config 0
@@ -252,7 +252,7 @@ def decode_layer(seed: int, label: str, d: int, nq: int, nkv: int, hd: int, num_
         "input_norm": norm_weight(seed, L + "/input_norm", d),
         "q": int4_matrix(seed, L + "/q", qd, d),
         "k": int4_matrix(seed, L + "/k", kvd, d),
-        "v": int4_matrix(seed, L + "/v", kvd, d),
+        "v": int4_matrix(seed, L + "/v", kvd, d) if v_proj else None,
         "o": int4_matrix(seed, L + "/o", d, qd),
         "q_norm": norm_weight(seed, L + "/q_norm", hd),
         "k_norm": norm_weight(seed, L + "/k_norm", hd),

@@ -25,8 +25,18 @@
  *    HIP call returns TFQ_E_HIP and its code is kept for tfq_last_hip_error().
  *    Nothing aborts the process.
  *  - A context is immutable after tfq_create and may be shared by threads
- *    that use distinct streams. Calls that take a `workspace` must not run
- *    concurrently with another call using the same workspace.
+ *    that use distinct streams, with one exception: tfq_decode_layer runs its
+ *    shared expert on a side stream and fork/join events that the context
+ *    owns, so decode-layer calls on one context must not overlap (use one
+ *    context per concurrent caller). Calls that take a `workspace` must not
+ *    run concurrently with another call using the same workspace.
+ *  - ABI versions (TFQ_ABI_VERSION, tfq_abi_version()): a binding built
+ *    against one version must check the library's at load time. Version 2
+ *    widened the grouping state of tfq_moe_group / tfq_moe_grouped from 1 to
+ *    TFQ_MOE_GROUP_STATE_WORDS words and added tfq_decode_layer_weights
+ *    .shared_bits; version 3 added the staged k/v segment at the end of the
+ *    tfq_decode_layer workspace (tfq_decode_layer_workspace_bytes grew),
+ *    head_dim 512 and a NULL v_proj (V from the k projection).
  */
 #ifndef TFQ_H
 #define TFQ_H
@@ -46,6 +56,12 @@ extern "C" {
 #define TFQ_E_IO 5          /* a checkpoint file is missing, unreadable or short (tfq_loader.h) */
 
 #define TFQ_GROUP_SIZE 64
+
+/* Version of this header's structs and contracts; tfq_abi_version() returns
+ * the library's. No reference counterpart (the Swift wrappers and their
+ * shaders ship in one build). */
+#define TFQ_ABI_VERSION 3
+int tfq_abi_version(void);
 
 typedef struct tfq_ctx tfq_ctx;
 
@@ -322,8 +338,12 @@ size_t tfq_attention_workspace_bytes(uint32_t head_dim, uint32_t num_q_heads, ui
  * fp16 [capacity][num_kv_heads][head_dim]. fp32 scores and accumulation, one
  * fp16 rounding of the output. Replaces Attention.encodeFull /
  * Attention.encodeSWA (S/Kernels/Attention/Attention.swift:238-370).
- * Contract: head_dim 128 or 256; G in {1, 2, 4}; seq_len in 1...65536;
- * q, caches and workspace 16-byte aligned. */
+ * Also replaces attention_decode_gqa_full_partial + attention_decode_combine
+ * (S/Metal/Attention/attention.metal:454-615), the full-attention layers'
+ * kernel (head_dim 512).
+ * Contract: head_dim 128 or 256 with G in {1, 2, 4}, or head_dim 512 with G
+ * in {1, 2, 4, 8}; seq_len in 1...65536; q, caches and workspace 16-byte
+ * aligned. */
 int tfq_attention_decode(tfq_ctx *ctx, void *stream, const uint16_t *q, const uint16_t *k_cache,
                          const uint16_t *v_cache, uint16_t *out, uint32_t head_dim,
                          uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t seq_len,
@@ -333,7 +353,10 @@ int tfq_attention_decode(tfq_ctx *ctx, void *stream, const uint16_t *q, const ui
  * fp16, converted from the checkpoint's BF16 with tfq_convert_bf16_to_f16). */
 typedef struct {
     const uint16_t *input_norm;          /* [d] input_layernorm */
-    tfq_q4_matrix q_proj, k_proj, v_proj; /* [nq*hd][d], [nkv*hd][d], [nkv*hd][d] */
+    tfq_q4_matrix q_proj, k_proj, v_proj; /* [nq*hd][d], [nkv*hd][d], [nkv*hd][d];
+                                            v_proj.weights NULL: no v projection, V is
+                                            the k projection (the full-attention layers,
+                                            RealForwardRunner.swift:2252-2255) */
     const uint16_t *q_norm, *k_norm;     /* [head_dim] per-head q/k RMSNorm */
     tfq_q4_matrix o_proj;                /* [d][nq*hd] */
     const uint16_t *post_attention_norm; /* [d] */
@@ -376,6 +399,10 @@ size_t tfq_decode_layer_workspace_bytes(const tfq_decode_layer_shape *shape, uin
  * RealForwardRunner (S/Runtime/Inference/RealForwardRunner.swift:2265-2862:
  * gInputNorm, gQKV, gQKVEpilogue, gAttention, gOProj, gPostAttnSetup,
  * gRouter, gSharedFFN + gSharedNorm, routed phases 1/2, gTail).
+ * Full-attention layers (Gemma 4: every sixth layer, head_dim 512, 2 kv
+ * heads, rope theta 1e6, rotated_pairs = head_dim * partial_rotary / 2 = 64)
+ * pass their shape and a NULL v_proj: V = rmsnorm_head(k projection) (no
+ * scale), K = rope(rmsnorm_head(k projection, k_norm)).
  * Contract: d multiple of 64, <= 4096; attention as tfq_attention_decode;
  * experts as tfq_moe_decode; workspace 256-byte aligned. */
 int tfq_decode_layer(tfq_ctx *ctx, void *stream, const tfq_decode_layer_weights *weights,
@@ -436,11 +463,14 @@ int tfq_gemm_qg64_path(tfq_ctx *ctx, void *stream, const void *weights, const ui
 size_t tfq_prefill_shared_expert_workspace_bytes(uint32_t weight_bits, uint32_t tokens, uint32_t f);
 
 /* The shared expert over a block of `tokens` rows: y + t*y_stride =
- * shared(x + t*x_stride) for t < tokens (strides in halves), each row as
- * tfq_shared_expert_q4 / _q8 compute it for weight_bits 4 / 8. int8 weights
- * run the decode kernels over all rows in one launch each; int4 weights run
- * the prefill GEMM (gate and up into the workspace as fp16, gelu_mul, down),
- * whose kernel follows the token count. Replaces
+ * shared(x + t*x_stride) for t < tokens (strides in halves). int8 weights
+ * run the decode kernels over all rows in one launch each, so each row is
+ * bit-identical to tfq_shared_expert_q8. int4 weights run the prefill GEMM:
+ * gate and up are stored to the workspace in fp16 before gelu_mul (the
+ * rounding of the reference's GPU sequence, SharedExpertInt4.swift:30-94),
+ * then down; tfq_shared_expert_q4 keeps gate/up in fp32 instead, so the two
+ * int4 forms differ by those roundings (~8e-4 of max|y| at the config-4
+ * shapes). The GEMM kernel follows the token count. Replaces
  * PrefillSharedExpert.encodeBlock
  * (S/Kernels/Prefill/MoE/PrefillSharedExpert.swift:11-60), which encodes the
  * decode form once per row. Contract: as the decode forms; x_stride >= d and
@@ -546,7 +576,9 @@ int tfq_group_pairs_host(const tfq_pair *pairs, int64_t n_pairs, int64_t query_c
  * (token, rank) slots without a pair are left untouched. max_tiles is the
  * launch bound (TFQ_MOE_MAX_TILES, at most 320 = 8192/128 + 256,
  * TFQ_E_UNSUPPORTED beyond); the device tile count n_tiles[0] decides. The
- * launches take their work units from the counters n_tiles[1..2] and leave
+ * launches take their work units from the counters n_tiles[1..2], which must
+ * be zero on entry (tfq_moe_group zeroes them; a state built by other means
+ * must too, or blocks skip work units and rows stay unwritten), and leave
  * them zero, so calls on one grouping state must not overlap. Replaces
  * PrefillGroupedRoutedMoE.encodeStreamedBatched
  * (S/Kernels/Prefill/MoE/PrefillGroupedRoutedMoE.swift:446-527), and its

@@ -527,12 +527,14 @@ def decode_layer(w: dict, shape: dict, hidden_f16, k_cache_f16, v_cache_f16, pos
         return _ptr(a)
 
     def q4(t):
+        if t is None:       # no v projection: V from the k projection (full-attention layers)
+            return Q4(None, None, None)
         W, S, B = (_c(t[0], np.uint8), _c(t[1], np.uint16), _c(t[2], np.uint16))
         keep.extend([W, S, B])
         return Q4(_ptr(W), _ptr(S), _ptr(B))
 
     lw = LayerWeights(
-        input_norm=arr(w["input_norm"], np.uint16), q=q4(w["q"]), k=q4(w["k"]), v=q4(w["v"]), o=q4(w["o"]),
+        input_norm=arr(w["input_norm"], np.uint16), q=q4(w["q"]), k=q4(w["k"]), v=q4(w.get("v")), o=q4(w["o"]),
         q_norm=arr(w["q_norm"], np.uint16), k_norm=arr(w["k_norm"], np.uint16),
         post_attention_norm=arr(w["post_attention_norm"], np.uint16),
         pre_ffn_norm=arr(w["pre_ffn_norm"], np.uint16), pre_ffn2_norm=arr(w["pre_ffn2_norm"], np.uint16),

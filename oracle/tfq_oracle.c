@@ -920,7 +920,13 @@ void tfo_decode_layer(const tfo_layer_weights *w, const tfo_layer_shape *s,
     norm16(hidden, w->input_norm, d, eps, normed);
     tfo_gemv_int4(w->q.w, w->q.s, w->q.b, TFO_FMT_F16, normed, qd, d, q);
     tfo_gemv_int4(w->k.w, w->k.s, w->k.b, TFO_FMT_F16, normed, kvd, d, kn);
-    tfo_gemv_int4(w->v.w, w->v.s, w->v.b, TFO_FMT_F16, normed, kvd, d, vn);
+    /* v_proj exists only on the sliding-window layers; the full-attention
+     * layers run k_proj as the v projection (:2252-2255), so V is the no-scale
+     * norm of the raw k projection. */
+    if (w->v.w)
+        tfo_gemv_int4(w->v.w, w->v.s, w->v.b, TFO_FMT_F16, normed, kvd, d, vn);
+    else
+        memcpy(vn, kn, sizeof(float) * (size_t)kvd);
     round_vec(q, (size_t)qd);
     round_vec(kn, (size_t)kvd);
     round_vec(vn, (size_t)kvd);

@@ -120,3 +120,81 @@ def test_gemm_one_hot_is_bit_exact(ctx, stream, bits, path):
     stream.sync()
     got = Y.download(np.uint16, k * m).reshape(k, m)
     assert np.array_equal(got, expect), f"{np.count_nonzero(got != expect)} words differ"
+
+
+def _affine_rows(codes, bits):
+    if bits == 4:
+        return synth.pack_int4(codes)
+    return np.stack([oracle.pack_affine_codes(codes[r], bits) for r in range(codes.shape[0])])
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_grouped_down_one_hot_is_bit_exact(ctx, stream, bits):
+    # tfq_moe_grouped (gate/up then down units). Token t's hidden row is e_t;
+    # every gate weight is 16 and up row f is 1/16 at column f only, so the
+    # gate/up units give act = fp16(gelu(16)·u) = e_t exactly (gelu(16) = 16:
+    # e^(-2z) underflows) and each down partial of a pair of token t is the
+    # expert's dequantised down weight of column t: fp16(q·s + b), one
+    # rounding. Routing: rank 0 -> expert 0 (128 pairs: two 64-pair halves on
+    # wide units), rank 1 -> experts 1..15 (8-9 pairs: stream units), rank 2 ->
+    # experts 16..18 (42-43 pairs: one partly filled wide half); expert 19 idle.
+    T, k, E, D, F = 128, 3, 20, 256, 128
+    offs, stride = synth.expert_layout(D, F, align=256, bits=bits)
+    pool = np.zeros(E * stride, np.uint8)
+    gq, gs = {4: (8, 2.0), 3: (4, 4.0), 2: (2, 8.0)}[bits]
+    gate_codes = np.full((F, D), gq, np.uint32)
+    up_codes = np.zeros((F, D), np.uint32)
+    up_codes[np.arange(F), np.arange(F)] = 1
+    f16 = lambda v, shape: np.full(shape, np.float16(v).view(np.uint16), np.uint16)
+    expect = {}
+    for e in range(E):
+        codes = ((7 * np.arange(F)[None, :] + 5 * np.arange(D)[:, None] + 3 * e) % (1 << bits)).astype(np.uint32)
+        g = D * (F // 64)
+        s16 = synth.f16_bits(np.abs(synth.normal(synth.seed_key(e, f"gd{bits}/s"), g, 0.02)) * (16 >> bits))
+        b = -(1 << (bits - 1)) * synth.f16_to_f32(s16) + synth.normal(synth.seed_key(e, f"gd{bits}/b"), g, 0.002)
+        S, B = s16.reshape(D, -1), synth.f16_bits(b).reshape(D, -1)
+        w64 = (codes.astype(np.float64) * np.repeat(synth.f16_to_f32(S).astype(np.float64), 64, axis=1)
+               + np.repeat(synth.f16_to_f32(B).astype(np.float64), 64, axis=1))
+        expect[e] = w64.astype(np.float16).view(np.uint16)                     # [D][F], one rounding
+        parts = {"gate_w": _affine_rows(gate_codes, bits), "gate_s": f16(gs, (F, D // 64)),
+                 "gate_b": f16(0.0, (F, D // 64)), "up_w": _affine_rows(up_codes, bits),
+                 "up_s": f16(0.0625, (F, D // 64)), "up_b": f16(0.0, (F, D // 64)),
+                 "down_w": _affine_rows(codes, bits), "down_s": S, "down_b": B}
+        for name, arr in parts.items():
+            raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
+            o = e * stride + offs[name]
+            pool[o:o + raw.size] = raw
+    t = np.arange(T)
+    idx = np.stack([np.zeros(T, np.int64), 1 + t % 15, 16 + t % 3], axis=1).astype(np.uint32)
+    w16 = f16(1.0, (T, k))
+    hidden = np.zeros((T, D), np.uint16)
+    hidden[t, t] = ONE
+    got, bufs = _group_on_device(ctx, stream, idx, w16, T, k, E)
+    p = ops.ExpertPool(_dev(pool), stride, E, offs, weight_bits=bits)
+    act = _dev(np.full(T * k * F, 0x7FFF, np.uint16))
+    partials = _dev(np.full(T * k * D, 0x7FFF, np.uint16))
+    ops.PrefillGroupedRoutedMoE(ctx).encode(stream, p, bufs["sorted"], bufs["tiles"], bufs["n_tiles"],
+                                            ops.max_tiles(T, k, E), _dev(hidden), D, D, F, k, act, partials)
+    stream.sync()
+    parts = partials.download(np.uint16).reshape(T, k, D)
+    for tok in range(T):
+        for r in range(k):
+            want = expect[int(idx[tok, r])][:, tok]
+            bad = np.flatnonzero(parts[tok, r] != want)
+            assert bad.size == 0, (f"{bits}-bit token {tok} rank {r} expert {idx[tok, r]}: {bad.size} words differ, "
+                                   f"first d={bad[0]}: {parts[tok, r, bad[0]]:#06x} != {want[bad[0]]:#06x}")
+
+
+def _group_on_device(ctx, stream, idx, w16, T, k, E):
+    n = T * k
+    mt = ops.max_tiles(T, k, E)
+    bufs = dict(sorted=_dev(np.zeros(n, ops.PAIR_DTYPE)), offsets=_dev(np.zeros(E, np.uint32)),
+                counts=_dev(np.zeros(E, np.uint32)), tiles=_dev(np.zeros(mt, ops.TILE_DTYPE)),
+                n_tiles=_dev(np.zeros(ops.GROUP_STATE_BYTES // 4, np.uint32)), status=_dev(np.zeros(1, np.uint32)))
+    ops.PrefillMoEGrouping(ctx).encode(stream, _dev(idx), _dev(w16), T, k, E, bufs["sorted"], bufs["offsets"],
+                                       bufs["counts"], bufs["tiles"], bufs["n_tiles"], bufs["status"])
+    stream.sync()
+    assert int(bufs["status"].download(np.uint32, 1)[0]) == 0
+    counts = bufs["counts"].download(np.uint32, E)
+    assert counts[0] == T and counts[19] == 0 and set(counts[1:16]) <= {8, 9} and set(counts[16:19]) <= {42, 43}
+    return None, bufs

@@ -446,6 +446,44 @@ def test_phase1_with_selection_equals_router_select_then_phase1(ctx, stream):
         assert list(i2.download(np.uint32, K)) == list(ref_idx)
 
 
+
+@pytest.mark.parametrize("with_inf", [False, True])
+def test_phase1_selection_nan_signed_zero_and_infinities(ctx, stream, with_inf):
+    # router_topk_select_k8 (moe.metal:152-168) never prefers a NaN score,
+    # never takes -inf, and -0 == +0 ties by the lower index. Fed straight
+    # into tfq_moe_phase1_routed's selection; indices bit-exact with the
+    # oracle, weights equal where finite and NaN where the oracle's are
+    # (a +inf logit makes every softmax weight inf - inf = NaN).
+    E, D, F, K = 128, 256, 128, 8
+    pool_bytes, offs, stride = synth.expert_pool(4, "nan/experts", E, D, F)
+    pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs)
+    logits = (-1.0 - synth.uniform24(synth.seed_key(4, "nan/logits"), E)).astype(np.float32)
+    logits[3], logits[12] = 1.0, 0.5
+    logits[[7, 64]] = 0.0
+    logits[[40, 100]] = -0.0
+    logits[[2, 9, 127]] = np.nan
+    logits[[50, 51]] = -np.inf
+    if with_inf:
+        logits[20] = np.inf
+    gain16 = f16_bits(synth.uniform24(synth.seed_key(4, "nan/gain"), E, 0.5, 1.5))
+    idx, w16, wf = _dev(np.zeros(K, np.uint32)), _dev(np.zeros(K, np.uint16)), _dev(np.zeros(K, np.float32))
+    acts = _dev(np.zeros(K * F, np.uint16))
+    h16 = synth.f16_vector(4, "nan/h", D)
+    ops.MoE(ctx).encode_routed_phase1_with_selection(stream, pool, _dev(logits), _dev(gain16), E, idx, w16, _dev(h16),
+                                                     acts, D, F, K, out_weights_f32=wf)
+    stream.sync()
+    ref_idx, ref_w = oracle.topk_softmax(logits, K, from_f16_bits(gain16))
+    got_idx = list(idx.download(np.uint32, K))
+    assert got_idx == list(ref_idx)
+    assert got_idx[:6] == ([20] if with_inf else []) + [3, 12, 7, 40, 64, 100][:6 - int(with_inf)]
+    assert not set(got_idx) & {2, 9, 127, 50, 51}
+    got_w = wf.download(np.float32, K)
+    assert np.array_equal(np.isnan(got_w), np.isnan(ref_w)) and (np.all(np.isnan(ref_w)) == with_inf)
+    fin = ~np.isnan(ref_w)
+    assert np.all(np.abs(got_w[fin] - ref_w[fin]) <= 1e-6 * np.abs(ref_w[fin]))
+    assert np.array_equal(np.isnan(from_f16_bits(w16.download(np.uint16, K))), np.isnan(ref_w))
+
+
 # --------------------------------------------- fused decode token (C ABI) ----
 #
 # tfq_moe_decode_token: router GEMV (each router block also publishes its

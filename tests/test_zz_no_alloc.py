@@ -69,3 +69,43 @@ def test_noalloc_rejects_shape_beyond_scratch(ctx, stream):
         ops.moe_decode_token_noalloc(ctx, stream, router, pool, b, None, b, D, F, K, b, b)
     assert ei.value.status == TFQ_E_INVAL
     assert b"scratch" in lib().tfq_last_error_message()
+
+
+def test_noalloc_decode_token_replays_from_a_captured_graph(ctx, stream):
+    # the allocation-free call captured into a HIP graph (stream capture: a
+    # hipMalloc, or a memset node, inside it would break or corrupt the
+    # replays) and replayed three times, with eager calls of both forms
+    # between the replays; every replay equals the eager call bit for bit
+    from edgeexpert_amd.runtime import Graph
+    E, D, F, K = 128, 2816, 704, 8
+    print(f"[noalloc] graph E={E} D={D} F={F} K={K}", flush=True)
+    pool_bytes, offs, stride = synth.expert_pool(4, "noalloc-g", E, D, F)
+    pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs)
+    W, S, B = synth.int8_matrix(4, "noalloc-g/router", E, D)
+    router = ops.Router(_dev(W), _dev(S), _dev(B), E)
+    x, res = _dev(synth.f16_vector(4, "noalloc-g/h", D)), _dev(synth.f16_vector(4, "noalloc-g/r", D, std=0.1))
+    x2 = _dev(synth.f16_vector(5, "noalloc-g/h2", D))
+    y, idx, w16 = DeviceBuffer(D * 2), DeviceBuffer(K * 4), DeviceBuffer(K * 2)
+    y2, idx2, w2 = DeviceBuffer(D * 2), DeviceBuffer(K * 4), DeviceBuffer(K * 2)
+    acts, ws = DeviceBuffer(K * F * 2), DeviceBuffer(ROUTER_WORKSPACE_BYTES)
+
+    def call():
+        ops.moe_decode_token_noalloc(ctx, stream, router, pool, x, res, y, D, F, K, idx, w16)
+
+    call()
+    stream.sync()
+    eager = (y.download(np.uint16, D).copy(), idx.download(np.uint32, K).copy(), w16.download(np.uint16, K).copy())
+    g = Graph(stream, call)
+    for r in range(3):
+        y.fill(0)
+        idx.fill(0xFF)
+        w16.fill(0)
+        g.launch(stream)
+        stream.sync()
+        got = (y.download(np.uint16, D), idx.download(np.uint32, K), w16.download(np.uint16, K))
+        for a, b in zip(got, eager):
+            assert np.array_equal(a, b), f"replay {r}"
+        # eager work on the same scratch and on caller scratch between replays
+        ops.moe_decode_token_noalloc(ctx, stream, router, pool, x2, None, y2, D, F, K, idx2, w2)
+        ops.moe_decode_token(ctx, stream, router, pool, x2, None, y2, D, F, K, idx2, w2, acts, ws)
+        stream.sync()
