@@ -276,12 +276,29 @@ def bench_c4(ctx, stream, launch, batch_avg_us, shared_bits=4, shape=C4):
 def host_cpu():
     """(lscpu model name, logical CPUs visible, threads this job may use)."""
     model = "unknown"
+    fields = {}
     try:
         for line in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
-            if line.startswith("Model name:"):
-                model = line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            fields.setdefault(key.strip(), val.strip())
     except (OSError, subprocess.SubprocessError):
         pass
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    fields.setdefault("cpuinfo model name", line.split(":", 1)[1].strip())
+                    break
+    except OSError:
+        pass
+    # a virtualised host may print only "AMD EPYC": keep the BIOS name and
+    # the family/model numbers (family 26 = Zen 5) beside it
+    names = [fields.get(k) for k in ("Model name", "cpuinfo model name", "BIOS Model name")]
+    names = [n for i, n in enumerate(names) if n and n not in names[:i]]
+    if names:
+        model = " / ".join(names)
+    if fields.get("CPU family") or fields.get("Model"):
+        model += f" (family {fields.get('CPU family', '?')}, model {fields.get('Model', '?')})"
     visible = len(os.sched_getaffinity(0))
     omp = os.environ.get("OMP_NUM_THREADS", "")
     usable = min(visible, int(omp)) if omp.isdigit() and int(omp) > 0 else visible
@@ -311,22 +328,61 @@ def cpu_baseline(Wr, Sr, Br, pool_bytes, stride, offs, H, W0, S0, B0):
             ts.append(time.perf_counter() - t0)
         return float(np.median(ts)) * 1e6
 
+    # config 2: the GEMM reference (MPPPrefillInt4QMMTests.cpuReference) over
+    # a bounded sample of token rows (16 per thread), scaled to the 512 rows
+    W2, S2, B2 = synth.int4_matrix(0, "c2/w", 8192, 2816)
+    X2 = synth.bf16_to_f32(synth.bf16_vector(0, "c2/x", 512 * 2816)).reshape(512, 2816)
+    # config 3: the grouped reference (cpuSyntheticRoutePartials) over a
+    # bounded sample of the 4096 sorted pairs (8 per thread; every pair costs
+    # one full expert FFN), scaled to 4096, plus the token-major combine
+    T3, k3 = 512, 8
+    idx3, w3 = synth.zipf_routing(0, "c3/route", T3, E, k3)
+    pairs = np.array([(t, int(idx3[t, r]), r, 4) for t in range(T3) for r in range(k3)], oracle.PAIR_DTYPE)
+    sorted3 = oracle.group_pairs(pairs, T3, k3, E)["sorted"]
+    hid3 = synth.f16_vector(0, "c3/x0", T3 * D)
+    o3 = oracle.ExpertOffsets(*[int(offs[n]) for n in synth.OFFSET_ORDER])
+    parts3 = np.zeros(T3 * k3 * D, np.uint16)
+    # config 4: the decoder layer (oracle tfo_decode_layer) at position 4095
+    w4 = synth.decode_layer(0, "c4", C4["d"], C4["nq"], C4["nkv"], C4["hd"], E, C4["f"], C4["fs"])
+    kvd = C4["nkv"] * C4["hd"]
+    kc4, vc4 = synth.f16_vector(0, "c4/kc", C4_CTX * kvd), synth.f16_vector(0, "c4/vc", C4_CTX * kvd)
+    h4 = synth.f16_vector(0, "c4/hidden", C4["d"])
+
     res = {}
     for threads in sorted({1, usable}):
         tok = median_us(lambda i: oracle.baseline_moe_decode_token(Wr, Sr, Br, pool_bytes, stride, offs,
                                                                    hs[i % TOKENS], D, F, K, threads), 20)
         gemv = median_us(lambda i: oracle.baseline_gemv_int4(W0, S0, B0, x0, threads), 40)
-        res[threads] = (tok, gemv)
-        log(f"CPU baseline, {threads} thread(s): config 1 {tok:.0f} us/token, config 0 GEMV {gemv:.0f} us")
-    tok_all, gemv_all = res[usable]
-    tok_1, gemv_1 = res[1]
-    return {"value": round(tok_all, 1), "unit": "us/token", "cores": usable, "kind": "port",
+        rows2 = min(512, 16 * threads)
+        t0 = time.perf_counter()
+        oracle.gemm_int4(W2, S2, B2, X2, rows=(0, rows2), threads=threads)
+        gemm = (time.perf_counter() - t0) * 1e6 * 512 / rows2
+        n3 = min(len(sorted3), 8 * threads)
+        t0 = time.perf_counter()
+        oracle.grouped_route_partials(sorted3[:n3], hid3, D, pool_bytes, stride, o3, k3, D, F, T3, threads=threads)
+        grouped = (time.perf_counter() - t0) * 1e6 * len(sorted3) / n3
+        t0 = time.perf_counter()
+        oracle.reduce_token_major(parts3, w3, T3, k3, D)
+        grouped += (time.perf_counter() - t0) * 1e6
+        layer = median_us(lambda i: oracle.decode_layer(w4, C4, h4, kc4, vc4, C4_CTX - 1, threads=threads), 20,
+                          warm=1)
+        res[threads] = dict(config1_us_per_token=round(tok, 1), config0_gemv_us=round(gemv, 1),
+                            config2_gemm_us=round(gemm, 1), config2_rows_timed=rows2,
+                            config3_us_per_chunk=round(grouped, 1), config3_pairs_timed=n3,
+                            config4_us_per_token=round(layer, 1))
+        log(f"CPU baseline, {threads} thread(s): config 1 {tok:.0f} us/token, config 0 GEMV {gemv:.0f} us, "
+            f"config 2 GEMM {gemm / 1e6:.2f} s ({rows2} of 512 rows timed), config 3 {grouped / 1e6:.2f} s per "
+            f"512-token chunk ({n3} of {len(sorted3)} pairs timed), config 4 layer {layer / 1e3:.1f} ms/token")
+    return {"value": res[usable]["config1_us_per_token"], "unit": "us/token", "cores": usable, "kind": "port",
             "sample": f"config 1: median of 20 decode tokens (router + 8 experts; 64 rotated hidden states), "
-                      f"rows split over {usable} threads; oracle/cpu_baseline.c, gcc -O3 -march=native "
-                      f"-ffp-contract=off -fopenmp",
+                      f"rows split over {usable} threads; config 0: median of 40 GEMVs; config 2: "
+                      f"16 token rows per thread of the 512 timed once, scaled to 512; config 3: 8 sorted "
+                      f"pairs per thread of the 4096 timed once (each pair one whole expert FFN), scaled to "
+                      f"4096, plus the whole token-major combine; config 4: median of 20 layers at position "
+                      f"4095 (GEMV rows and attention heads split over the threads); oracle/cpu_baseline.c + "
+                      f"tfq_oracle.c, gcc -O3 -march=native -ffp-contract=off -fopenmp",
             "cpu_model": model, "logical_cpus_visible": visible, "threads_all_cores": usable,
-            "one_thread": {"config1_us_per_token": round(tok_1, 1), "config0_gemv_us": round(gemv_1, 1)},
-            "all_cores": {"config1_us_per_token": round(tok_all, 1), "config0_gemv_us": round(gemv_all, 1)}}
+            "one_thread": res[1], "all_cores": res[usable]}
 
 
 def trace_summary(csv_path, out=sys.stdout, b2b_gap_us=None):

@@ -102,6 +102,7 @@ def _declare(L):
         f.restype = res
         f.argtypes = list(args)
     u64p = C.POINTER(C.c_uint64)
+    d("tfo_set_threads", None, C.c_int)
     d("tfo_splitmix64_next", C.c_uint64, u64p)
     d("tfo_splitmix64_uniform", C.c_float, u64p, C.c_float, C.c_float)
     d("tfo_seedtree_key", C.c_uint64, C.c_uint64, C.c_char_p)
@@ -512,11 +513,13 @@ def attention(q, k, v, head_dim, nq, nkv, seq_len, window=0, scale=None):
 
 
 
-def decode_layer(w: dict, shape: dict, hidden_f16, k_cache_f16, v_cache_f16, position, trace=False):
+def decode_layer(w: dict, shape: dict, hidden_f16, k_cache_f16, v_cache_f16, position, trace=False, threads=None):
     """One Gemma 4 decoder layer (tfo_decode_layer). w: dict of numpy arrays
-    (fp16 bits for norms; (W, S, B) tuples for int4 matrices; 'pool', 'stride',
-    'off' for the routed experts; router_* arrays). The caches are updated in
-    place at slot `position`. Returns (out_f16, idx, weights, trace dict)."""
+    (fp16 bits for norms; (W, S, B) tuples for int4 matrices, "v" None for a
+    layer without a v projection; 'pool', 'stride', 'off' for the routed
+    experts; router_* arrays). The caches are updated in place at slot
+    `position`. threads: run the CPU-baseline build with that many row
+    threads (same results). Returns (out_f16, idx, weights, trace dict)."""
     keep = []
 
     def arr(a, dt):
@@ -558,7 +561,7 @@ def decode_layer(w: dict, shape: dict, hidden_f16, k_cache_f16, v_cache_f16, pos
     tr = {"q": np.zeros(qd, np.uint16), "attn": np.zeros(qd, np.uint16), "o": np.zeros(d, np.uint16),
           "h": np.zeros(d, np.uint16), "h1": np.zeros(d, np.uint16), "h2": np.zeros(d, np.uint16)}
     lt = LayerTrace(**{n: _ptr(a) for n, a in tr.items()})
-    lib().tfo_decode_layer(C.byref(lw), C.byref(ls), _ptr(hidden), _ptr(k_cache_f16), _ptr(v_cache_f16),
+    _lib_for(threads).tfo_decode_layer(C.byref(lw), C.byref(ls), _ptr(hidden), _ptr(k_cache_f16), _ptr(v_cache_f16),
                            int(position), _ptr(out), _ptr(idx), _ptr(wts), C.byref(lt) if trace else None)
     return out, idx, wts, (tr if trace else None)
 
@@ -601,7 +604,7 @@ def group_pairs(pairs, query_count, top_k, num_experts, tile_expert_count=16, so
 
 
 def grouped_route_partials(sorted_pairs, hidden_f16, hidden_stride, pool, stride, off, top_k, d, f,
-                           query_count, fmt=FMT_F16, bits=4):
+                           query_count, fmt=FMT_F16, bits=4, threads=None):
     """cpuSyntheticRoutePartials (T/Kernels/Prefill/PrefillGroupedRoutedMoETests.swift:229-279).
     Unwritten (token, rank) slots keep the sentinel -99 as in the reference."""
     sp = np.ascontiguousarray(sorted_pairs, dtype=PAIR_DTYPE)
@@ -609,7 +612,7 @@ def grouped_route_partials(sorted_pairs, hidden_f16, hidden_stride, pool, stride
     pool = _c(pool, np.uint8)
     out = np.full(query_count * top_k * d, np.float16(-99).view(np.uint16), np.uint16)
     o = _offsets(off)
-    lib().tfo_grouped_route_partials_bits(_ptr(sp), sp.size, _ptr(hidden_f16), hidden_stride,
+    _lib_for(threads).tfo_grouped_route_partials_bits(_ptr(sp), sp.size, _ptr(hidden_f16), hidden_stride,
                                           _ptr(pool), int(stride), C.byref(o), fmt, bits, top_k, d, f,
                                           _ptr(out))
     return out
@@ -623,7 +626,7 @@ def reduce_token_major(partials_f16, weights_f16, rows, top_k, d):
     return out
 
 
-def gemm_int4(W, S, B, X, fmt=FMT_F16, rows=None, bits=4):
+def gemm_int4(W, S, B, X, fmt=FMT_F16, rows=None, bits=4, threads=None):
     """MPPPrefillInt4QMMTests.cpuReference (T/Kernels/TensorCore/MPPPrefillInt4QMMTests.swift:80-105),
     fp32 accumulator (unrounded). rows=(r0, r1) computes a bounded sample of token rows."""
     W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16); X = _c(X, np.float32)
@@ -631,7 +634,7 @@ def gemm_int4(W, S, B, X, fmt=FMT_F16, rows=None, bits=4):
     N = W.shape[0]
     r0, r1 = (0, M) if rows is None else rows
     Y = np.zeros((M, N), np.float32)
-    lib().tfo_gemm_affine(_ptr(W), _ptr(S), _ptr(B), fmt, bits, _ptr(X), M, N, K, _ptr(Y), r0, r1)
+    _lib_for(threads).tfo_gemm_affine(_ptr(W), _ptr(S), _ptr(B), fmt, bits, _ptr(X), M, N, K, _ptr(Y), r0, r1)
     return Y
 
 
@@ -672,6 +675,7 @@ def baseline_lib(rebuild: bool = False):
     if _baseline is None or rebuild:
         subprocess.run(["make", "-s"] + (["-B"] if rebuild else []) + ["-C", _HERE, "cpu_baseline"], check=True)
         L = C.CDLL(_BASELINE_PATH)
+        _declare(L)             # the oracle's functions, built -O3 -march=native -fopenmp
         L.tfb_gemv_int4.restype = None
         L.tfb_gemv_int4.argtypes = [_P, _P, _P, C.c_int, _P, C.c_int, C.c_int, _P, C.c_int]
         L.tfb_moe_decode_token.restype = None
@@ -681,11 +685,22 @@ def baseline_lib(rebuild: bool = False):
     return _baseline
 
 
+def _lib_for(threads):
+    """The checker (threads None), or the CPU-baseline build of the same
+    functions with their row loops split over `threads` (identical results)."""
+    if threads is None:
+        return lib()
+    L = baseline_lib()
+    L.tfo_set_threads(int(threads))
+    return L
+
+
 def baseline_gemv_int4(W, S, B, x, threads=1, fmt=FMT_F16):
     """tfb_gemv_int4: DequantInt4GemvRef.apply with the rows split over `threads`."""
     W = _c(W, np.uint8); S = _c(S, np.uint16); B = _c(B, np.uint16); x = _c(x, np.float32)
     m, n = W.shape[0], W.shape[1] * 2
     y = np.zeros(m, np.float32)
+    baseline_lib().tfo_set_threads(1)       # tfb_* split the rows themselves
     baseline_lib().tfb_gemv_int4(_ptr(W), _ptr(S), _ptr(B), fmt, _ptr(x), m, n, _ptr(y), int(threads))
     return y
 
@@ -700,6 +715,7 @@ def baseline_moe_decode_token(rW, rS, rB, pool, stride, off, h, d, f, k, threads
     w = np.zeros(k, np.float32)
     y = np.zeros(d, np.float32)
     o = _offsets(off)
+    baseline_lib().tfo_set_threads(1)
     baseline_lib().tfb_moe_decode_token(_ptr(rW), _ptr(rS), _ptr(rB), rW.shape[0], _ptr(pool), int(stride),
                                         C.byref(o), fmt, _ptr(h), _ptr(r), d, f, k, _ptr(idx), _ptr(w), _ptr(y),
                                         int(threads))

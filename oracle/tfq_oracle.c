@@ -279,6 +279,15 @@ void tfo_dequantize_int8_row(const uint8_t *packed, const uint16_t *scales, cons
 /* V/Reference/Quant/DequantInt4Gemv.swift:26-40: per row, dequantise to fp32,
  * then dot in index order (the scalar loop that pins vDSP_dotpr,
  * T/Validation/Reference/DequantInt4GEMVReferenceTests.swift:13-27). */
+/* Threads the row loops below may use. Only the CPU-baseline build
+ * (cpu_baseline.c, compiled with -fopenmp) acts on it: the checker build has
+ * no OpenMP, so its `omp` pragmas are ignored and every loop stays serial.
+ * Rows, heads, token rows and expert pairs are independent, so a split
+ * changes no result (tests/test_cpu_baseline.py checks it bit for bit). */
+static int tfo_threads = 1;
+void tfo_set_threads(int n) { tfo_threads = n > 0 ? n : 1; }
+#define TFO_ROW_CHUNK 16
+
 static void gemv_affine_rows(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt, int bits,
                              const float *x, int r0, int r1, int n, float *y) {
     float *w = (float *)malloc(sizeof(float) * (size_t)n);
@@ -300,9 +309,17 @@ static void gemv_affine_rows(const uint8_t *W, const uint16_t *S, const uint16_t
     free(w);
 }
 
+/* gemv_affine_rows over [0, m), in chunks of rows split over tfo_threads. */
+static void gemv_affine_split(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt, int bits,
+                              const float *x, int m, int n, float *y) {
+#pragma omp parallel for schedule(static) num_threads(tfo_threads) if (tfo_threads > 1)
+    for (int r0 = 0; r0 < m; r0 += TFO_ROW_CHUNK)
+        gemv_affine_rows(W, S, B, fmt, bits, x, r0, r0 + TFO_ROW_CHUNK < m ? r0 + TFO_ROW_CHUNK : m, n, y);
+}
+
 void tfo_gemv_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
                    const float *x, int m, int n, float *y) {
-    gemv_affine_rows(W, S, B, fmt, 4, x, 0, m, n, y);
+    gemv_affine_split(W, S, B, fmt, 4, x, m, n, y);
 }
 
 /* The same GEMV over 2-, 3- or 4-bit rows of tfo_affine_row_bytes(n, bits)
@@ -311,7 +328,7 @@ void tfo_gemv_int4(const uint8_t *W, const uint16_t *S, const uint16_t *B, int f
  * moe.metal:644-1180). */
 void tfo_gemv_affine(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt, int bits,
                      const float *x, int m, int n, float *y) {
-    gemv_affine_rows(W, S, B, fmt, bits, x, 0, m, n, y);
+    gemv_affine_split(W, S, B, fmt, bits, x, m, n, y);
 }
 
 void tfo_gemv_int4_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
@@ -329,11 +346,11 @@ void tfo_gemv_int4_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, i
 }
 
 /* V/Reference/Quant/DequantInt8Gemv.swift:24-38 */
-void tfo_gemv_int8(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
-                   const float *x, int m, int n, float *y) {
+static void gemv_int8_rows(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                           const float *x, int r0, int r1, int n, float *y) {
     float *w = (float *)malloc(sizeof(float) * (size_t)n);
     size_t groups = (size_t)n / TFO_GROUP;
-    for (int r = 0; r < m; ++r) {
+    for (int r = r0; r < r1; ++r) {
         tfo_dequantize_int8_row(W + (size_t)r * n, S + (size_t)r * groups, B + (size_t)r * groups,
                                 fmt, n, w);
         float sum = 0.0f;
@@ -344,6 +361,13 @@ void tfo_gemv_int8(const uint8_t *W, const uint16_t *S, const uint16_t *B, int f
         y[r] = sum;
     }
     free(w);
+}
+
+void tfo_gemv_int8(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
+                   const float *x, int m, int n, float *y) {
+#pragma omp parallel for schedule(static) num_threads(tfo_threads) if (tfo_threads > 1)
+    for (int r0 = 0; r0 < m; r0 += TFO_ROW_CHUNK)
+        gemv_int8_rows(W, S, B, fmt, x, r0, r0 + TFO_ROW_CHUNK < m ? r0 + TFO_ROW_CHUNK : m, n, y);
 }
 
 void tfo_gemv_int8_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, int fmt,
@@ -703,8 +727,11 @@ void tfo_grouped_route_partials_bits(const tfo_pair *sorted, int64_t n_pairs,
                                      const uint8_t *pool, uint64_t stride,
                                      const tfo_expert_offsets *o, int fmt, int bits,
                                      int top_k, int d, int f, uint16_t *partials) {
+#pragma omp parallel num_threads(tfo_threads) if (tfo_threads > 1)
+    {
     float *x = (float *)malloc(sizeof(float) * (size_t)d);
     float *act = (float *)malloc(sizeof(float) * (size_t)f);
+#pragma omp for schedule(dynamic, 4)
     for (int64_t p = 0; p < n_pairs; ++p) {
         const tfo_pair *pr = &sorted[p];
         const uint8_t *blob = pool + (uint64_t)pr->expert * stride;
@@ -723,6 +750,7 @@ void tfo_grouped_route_partials_bits(const tfo_pair *sorted, int64_t n_pairs,
         }
     }
     free(x); free(act);
+    }
 }
 
 /* PrefillMoETests.swift:46-58 */
@@ -756,6 +784,7 @@ void tfo_gemm_affine(const uint8_t *W, const uint16_t *S, const uint16_t *B, int
     size_t row_bytes = tfo_affine_row_bytes((size_t)K, bits);
     if (row0 < 0) row0 = 0;
     if (row1 > M) row1 = M;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(tfo_threads) if (tfo_threads > 1)
     for (int t = row0; t < row1; ++t) {
         const float *xr = X + (size_t)t * K;
         for (int n = 0; n < N; ++n) {
@@ -852,8 +881,9 @@ void tfo_attention(const float *q, const float *k, const float *v, int hd, int n
     const int group = nq / nkv;
     const int start = (window > 0 && seq_len > window) ? seq_len - window : 0;
     const int n = seq_len - start;
-    double *p = (double *)malloc(sizeof(double) * (size_t)n);
+#pragma omp parallel for schedule(static, 1) num_threads(tfo_threads) if (tfo_threads > 1)
     for (int qh = 0; qh < nq; ++qh) {
+        double *p = (double *)malloc(sizeof(double) * (size_t)n);
         const int kvh = qh / group;
         const float *qv = q + (size_t)qh * hd;
         double mx = -INFINITY;
@@ -875,8 +905,8 @@ void tfo_attention(const float *q, const float *k, const float *v, int hd, int n
                 acc += p[j] * (double)v[((size_t)(start + j) * nkv + kvh) * hd + e];
             out[(size_t)qh * hd + e] = (float)(acc / sum);
         }
+        free(p);
     }
-    free(p);
 }
 
 static float r16(float x) { return tfo_f16_to_f32(tfo_f32_to_f16(x)); }

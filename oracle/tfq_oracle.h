@@ -88,6 +88,10 @@ void tfo_gemv_int8_f64(const uint8_t *W, const uint16_t *S, const uint16_t *B, i
 void tfo_gemv_affine(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt, int bits,
                      const float *x, int m, int n, float *y);
 /* Row-partitioned multithreaded variant of tfo_gemv_int4 (same per-row arithmetic). */
+/* Threads of the row loops in the CPU-baseline build (no effect in the
+ * checker build, which has no OpenMP); results do not depend on it. */
+void tfo_set_threads(int n);
+
 void tfo_gemv_int4_mt(const uint8_t *W, const uint16_t *S, const uint16_t *B, int scale_fmt,
                       const float *x, int m, int n, float *y, int threads);
 

@@ -26,3 +26,41 @@ def test_baseline_decode_token_equals_oracle(threads):
     ridx, rw = oracle.topk_softmax(oracle.router_logits(rW, rS, rB, h), K)
     assert list(idx) == list(ridx) and np.array_equal(w, rw)
     assert np.array_equal(y, oracle.moe_routed(pool, stride, offs, h, ridx, rw, D, F))
+
+
+SMALL = dict(d=256, nq=4, nkv=2, hd=128, rotated_pairs=64, window=0, f=128, fs=192, k=2,
+             eps=1e-6, theta=10000.0, scale=1.0)
+
+
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_baseline_decode_layer_equals_oracle(threads):
+    # config 4's layer in the baseline build (GEMV rows and attention heads
+    # split over threads) against the serial checker, bit for bit
+    w = synth.decode_layer(5, "cpub-layer", SMALL["d"], SMALL["nq"], SMALL["nkv"], SMALL["hd"], 8, SMALL["f"],
+                           SMALL["fs"])
+    kvd = SMALL["nkv"] * SMALL["hd"]
+    kc = synth.f16_vector(5, "cpub-layer/kc", 160 * kvd)
+    vc = synth.f16_vector(5, "cpub-layer/vc", 160 * kvd)
+    h = synth.f16_vector(5, "cpub-layer/h", SMALL["d"])
+    k1, v1, k2, v2 = kc.copy(), vc.copy(), kc.copy(), vc.copy()
+    a = oracle.decode_layer(w, SMALL, h, k1, v1, 130)
+    b = oracle.decode_layer(w, SMALL, h, k2, v2, 130, threads=threads)
+    assert np.array_equal(a[0], b[0]) and list(a[1]) == list(b[1]) and np.array_equal(a[2], b[2])
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+
+
+@pytest.mark.parametrize("threads", [1, 5])
+def test_baseline_gemm_and_grouped_equal_oracle(threads):
+    W, S, B = synth.int4_matrix(6, "cpub/gemm", 96, 512)
+    X = synth.f16_to_f32(synth.f16_vector(6, "cpub/X", 24 * 512)).reshape(24, 512)
+    assert np.array_equal(oracle.gemm_int4(W, S, B, X, threads=threads), oracle.gemm_int4(W, S, B, X))
+    T, k, E, D, F = 12, 2, 8, 128, 64
+    pool, offs, stride = synth.expert_pool(6, "cpub/pool", E, D, F)
+    idx, w16 = synth.zipf_routing(6, "cpub/route", T, E, k)
+    g = oracle.group_pairs(np.array([(t, int(idx[t, r]), r, 4) for t in range(T) for r in range(k)],
+                                    oracle.PAIR_DTYPE), T, k, E)
+    hid = synth.f16_vector(6, "cpub/hidden", T * D)
+    o = oracle.ExpertOffsets(*[int(offs[n]) for n in synth.OFFSET_ORDER])
+    a = oracle.grouped_route_partials(g["sorted"], hid, D, pool, stride, o, k, D, F, T)
+    b = oracle.grouped_route_partials(g["sorted"], hid, D, pool, stride, o, k, D, F, T, threads=threads)
+    assert np.array_equal(a, b)
