@@ -579,14 +579,30 @@ def bench_gemm_policy(ctx, stream, batch_avg_us):
         us = run(m, None)
         out["auto"][str(m)] = {"us": round(us, 2), "tflops": round(2.0 * m * N * Kd / (us * 1e-6) / 1e12, 1),
                                "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1),
-                               "kernel": "skinny" if m <= 80 else "tile"}
+                               "kernel": "gemv" if m == 1 else "skinny" if m <= 80 else "tile"}
     for m in (64, 96):
         out["forced"][str(m)] = {"skinny32_us": round(run(m, GEMM_PATH_SKINNY32), 2),
                                  "tile_us": round(run(m, GEMM_PATH_TILE), 2)}
+    # few tokens: the decode GEMV once per token against the weight stream
+    # (the reference's repeated GEMV below 32 tokens), N 2048 and 8192
+    from edgeexpert_amd._lib import GEMM_PATH_GEMV, GEMM_PATH_SKINNY
+    out["gemv_vs_skinny"] = {}
+    for n in (2048, 8192):
+        Wn, Sn, Bn = synth.int4_matrix(0, f"c2/w{n}", n, Kd) if n != N else (W, S, B)
+        bn = [tuple(DeviceBuffer.from_array(a) for a in (Wn, Sn, Bn)) for _ in range(copies)]
+        for m in (1, 2, 3, 4):
+            row = {}
+            for name, path in (("gemv", GEMM_PATH_GEMV), ("skinny", GEMM_PATH_SKINNY), ("auto", None)):
+                row[name + "_us"] = round(batch_avg_us(
+                    lambda i: q.encode(stream, *bn[i % copies], X, Y, m, n, Kd, DTYPE_BF16, path=path), 32, reps_=3), 2)
+            out["gemv_vs_skinny"][f"n{n}_m{m}"] = row
+        del bn
     log("GEMM by token count (N 8192, K 2816, bf16): " +
         ", ".join(f"M={m} {v['us']:.1f} us ({v['kernel']})" for m, v in out["auto"].items()) +
         "; forced " + ", ".join(f"M={m}: skinny {v['skinny32_us']:.1f} / tile {v['tile_us']:.1f} us"
-                                for m, v in out["forced"].items()))
+                                for m, v in out["forced"].items()) +
+        "; GEMV vs skinny " + ", ".join(f"{key}: {v['gemv_us']:.2f} / {v['skinny_us']:.2f} (auto {v['auto_us']:.2f})"
+                                         for key, v in out["gemv_vs_skinny"].items()))
     return out
 
 

@@ -33,6 +33,7 @@ GEMM_PATH_AUTO = 0
 GEMM_PATH_TILE = 1
 GEMM_PATH_SKINNY = 2
 GEMM_PATH_SKINNY32 = 3
+GEMM_PATH_GEMV = 4
 
 
 class TfqNotBuilt(RuntimeError):

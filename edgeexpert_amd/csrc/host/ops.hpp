@@ -52,6 +52,8 @@ inline int check_stage(const NormArg& na) {
     case kStageScaled:
         if (!na.inv) return fail(TFQ_E_INVAL, "scaled staging needs the exported r(h)");
         return TFQ_OK;
+    case kStageBf16:
+        return TFQ_OK;
     case kStagePostAttn:
     case kStageResidual:
         if (!na.attn || !na.attn_w)
@@ -532,7 +534,7 @@ constexpr uint32_t kSkinnyThreads = 512;    // (gemm_skinny.hpp kSkinnyThreads)
 // The prefill projection's kernel choice by token count, the role of
 // PrefillProjectionDispatchPolicy (S/Runtime/Inference/RealForwardRunner.swift:
 // 217-230, 1411-1492: repeated GEMV below 32 tokens, QMM / MPP above). Here
-// the two kernels are the few-token weight stream (gemm_skinny.hpp: every
+// one token takes the decode GEMV; the other kernels are the few-token weight stream (gemm_skinny.hpp: every
 // weight dequantised once per 16 tokens, 8 K-slices per block, N/16 or N/32
 // blocks) and the 64-token projection tile (gemm.hpp: N/256 blocks per
 // token tile). Both multiply the same fp16 weights, so the choice changes
@@ -560,6 +562,11 @@ inline uint32_t skinny_max_tokens(uint32_t n, uint32_t k) {
 }
 
 inline GemmPlan plan_gemm(uint32_t t, uint32_t n, uint32_t k) {
+    // one token: the decode GEMV (N 2048: 3.9 against 4.4 us for the weight
+    // stream, N 8192: 5.8 against 6.4 us, cold weights); from two tokens on
+    // the stream reads the weights once for up to 16 tokens and wins (N 8192,
+    // two tokens: 6.5 against 11.2 us for two GEMVs)
+    if (t == 1) return {TFQ_GEMM_PATH_GEMV};
     if (t > skinny_max_tokens(n, k)) return {TFQ_GEMM_PATH_TILE};
     // 16 rows per wave keeps more blocks for narrow matrices and few tokens;
     // 32 rows per wave halves the activation reads and wins elsewhere
@@ -598,6 +605,18 @@ public:
         if (ldy < n) return fail(TFQ_E_INVAL, "y row stride %u must be >= n", ldy);
         if (k > kProjMaxK) return fail(TFQ_E_UNSUPPORTED, "k=%u exceeds %u", k, kProjMaxK);
         if (path == TFQ_GEMM_PATH_AUTO) path = plan_gemm(t, n, k).path;
+        if (path == TFQ_GEMM_PATH_GEMV) {
+            // the decode GEMV once per token (bf16 rows converted while staged)
+            if (bits != 4 && bits != 3) return fail(TFQ_E_INVAL, "unsupported attention weight bits %u", bits);
+            const DequantInt4GEMV gemv(m_);
+            NormArg stage = stage_copy();
+            if (dtype == TFQ_DTYPE_BF16) stage.mode = kStageBf16;
+            for (uint32_t i = 0; i < t; ++i)
+                if (int rc = gemv.encode(stream, weights, scales, biases, x + (size_t)i * ldx, y + (size_t)i * ldy, n,
+                                         k, nullptr, stage, bits))
+                    return rc;
+            return TFQ_OK;
+        }
         if (path == TFQ_GEMM_PATH_SKINNY || path == TFQ_GEMM_PATH_SKINNY32) {
             const uint32_t rt = path == TFQ_GEMM_PATH_SKINNY32 ? 2 : 1;
             char sname[64];

@@ -40,8 +40,11 @@ struct Q8Mat {
 //   kStageResidual  a = h (the post-attention residual stream, no norm)
 //   kStageScaled    a = fp16(x * w * inv[0])              (w == null: no scale;
 //                   x = an exported h, inv its exported r(h))
+//   kStageBf16      a = fp16(x) for a bf16 x (round to nearest even, as the
+//                   prefill GEMM converts its activations); the GEMV then
+//                   stores its rows as bf16 too (the prefill GEMM's one-token path)
 enum StageMode : uint32_t { kStageCopy = 0, kStageNorm = 1, kStagePostAttn = 2, kStageResidual = 3,
-                            kStageScaled = 4 };
+                            kStageScaled = 4, kStageBf16 = 5 };
 
 struct NormArg {
     const uint16_t* w;

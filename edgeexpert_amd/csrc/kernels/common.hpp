@@ -38,6 +38,20 @@ __device__ __forceinline__ float bf2f(uint16_t b) {
     return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
 
+// 8 bf16 -> 8 fp16 (exact inside the fp16 normal range).
+__device__ __forceinline__ h8 bf16x8_to_f16(uint4 raw) {
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    h8 out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = __builtin_bit_cast(float, w[i] << 16);
+        const float hi = __builtin_bit_cast(float, w[i] & 0xFFFF0000u);
+        out[2 * i] = (_Float16)lo;
+        out[2 * i + 1] = (_Float16)hi;
+    }
+    return out;
+}
+
 // Cross-lane reductions on the VALU (DPP row permutations and the gfx950
 // permlane swaps) instead of LDS permutes: a few cycles per step rather than
 // an LDS round trip. Every lane receives the result; the pairing is fixed, so
@@ -523,6 +537,11 @@ __device__ __forceinline__ void stage_act_scalar(const uint16_t* __restrict__ x,
                                                  uint32_t n, const NormArg& na) {
     copy_to_lds<NT>(x, lds, n);
     __syncthreads();
+    if (na.mode == kStageBf16) {
+        for (uint32_t i = threadIdx.x; i < n; i += NT) lds[i] = f2h(bf2f(lds[i]));
+        __syncthreads();
+        return;
+    }
     if (na.mode == kStageScaled) {
         const float inv = *na.inv;
         for (uint32_t i = threadIdx.x; i < n; i += NT) {
@@ -616,6 +635,11 @@ struct XStage {
         const uint32_t nch = n >> 3;
         const bool post = na.mode == kStagePostAttn || na.mode == kStageResidual;
         const bool norm = na.mode == kStageNorm || na.mode == kStagePostAttn;
+        if (na.mode == kStageBf16) {
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i) xv[i] = bf16x8_to_f16(__builtin_bit_cast(uint4, xv[i]));
+            return;
+        }
         if (na.mode == kStageScaled) {
 #pragma unroll
             for (uint32_t i = 0; i < CH; ++i)

@@ -41,20 +41,6 @@ __device__ __forceinline__ h8 perm_0213(h8 v) {
     return __builtin_shufflevector(v, v, 0, 2, 1, 3, 4, 6, 5, 7);
 }
 
-// 8 bf16 -> 8 fp16 (exact inside the fp16 normal range).
-__device__ __forceinline__ h8 bf16x8_to_f16(uint4 raw) {
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-    h8 out;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float lo = __builtin_bit_cast(float, w[i] << 16);
-        const float hi = __builtin_bit_cast(float, w[i] & 0xFFFF0000u);
-        out[2 * i] = (_Float16)lo;
-        out[2 * i + 1] = (_Float16)hi;
-    }
-    return out;
-}
-
 // ------------------------------------------------------ projection tile ----
 //
 // The weights never pass through LDS: each lane loads its own row's 16 bytes

@@ -144,9 +144,11 @@ template <int SEG, int P, int R, bool NORM, int BITS = 4>
 __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_t* __restrict__ x,
                                               uint32_t n) {
     const uint32_t row_bytes = (n >> 3) * BITS, ngroups = n >> 6;
+    const bool out_bf16 = NORM && mats.norm.mode == kStageBf16;
     q4_rows<SEG, P, R, NORM, false, BITS>(mats, x, n, [&](uint32_t row, float v) {
         const Q4Row q = resolve_row(mats, row, row_bytes, ngroups);
-        *q.y = f2h(q.r ? h2f(*q.r) + v : v);
+        const float o = q.r ? h2f(*q.r) + v : v;
+        *q.y = out_bf16 ? __builtin_bit_cast(uint16_t, (__bf16)o) : f2h(o);
     });
 }
 

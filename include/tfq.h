@@ -426,9 +426,13 @@ int tfq_decode_layer(tfq_ctx *ctx, void *stream, const tfq_decode_layer_weights 
  * activation path; callers that need to know can run
  * tfq_convert_bf16_to_f16 with its inexact counter on X). The kernel is
  * chosen by token count, as PrefillProjectionDispatchPolicy does
- * (S/Runtime/Inference/RealForwardRunner.swift:217-230, 1411-1492): a
- * few-token weight stream below the measured crossover of the shape, the
- * 64-token MFMA tile above it. Replaces PrefillInt4QMM.encode
+ * (S/Runtime/Inference/RealForwardRunner.swift:217-230, 1411-1492): the
+ * decode GEMV for one token, a few-token weight stream below the measured
+ * crossover of the shape, the 64-token MFMA tile above it. The GEMV forms
+ * s·Σq·x + b·Σx in fp32 from the unrounded q·s, the two MFMA kernels
+ * multiply fp16(q·s + b) weights: the paths differ by those roundings and
+ * the summation order, each within the north-star bar of the CPU reference.
+ * Replaces PrefillInt4QMM.encode
  * (S/Kernels/Prefill/Primitives/PrefillPrimitives.swift:82-122) and
  * MPPPrefillInt4QMM.encode (S/Kernels/TensorCore/MPPPrefillInt4QMM.swift:34-78).
  * Contract: k % 64 == 0, k <= 8192, n >= 1, m >= 1; W and X 16-byte aligned. */
@@ -441,6 +445,8 @@ int tfq_gemm_q4g64(tfq_ctx *ctx, void *stream, const void *weights, const uint16
 #define TFQ_GEMM_PATH_TILE 1      /* the 64-token x 256-output MFMA projection tile */
 #define TFQ_GEMM_PATH_SKINNY 2    /* few-token weight stream: 16 rows x 16 tokens per wave, K split in 8 */
 #define TFQ_GEMM_PATH_SKINNY32 3  /* the same with 32 rows per wave */
+#define TFQ_GEMM_PATH_GEMV 4      /* the decode GEMV once per token (the reference's repeated
+                                     GEMV below 32 tokens, RealForwardRunner.swift:1460-1491) */
 
 /* tfq_gemm_q4g64 at `bits` = 3 or 4 bits per code (rows of k*bits/8 bytes,
  * codes packed from the least significant bit). Replaces

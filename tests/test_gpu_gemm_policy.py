@@ -14,14 +14,15 @@ import pytest
 
 import oracle
 from edgeexpert_amd import ops, synth
-from edgeexpert_amd._lib import (DTYPE_BF16, DTYPE_F16, GEMM_PATH_SKINNY, GEMM_PATH_SKINNY32,
+from edgeexpert_amd._lib import (DTYPE_BF16, DTYPE_F16, GEMM_PATH_GEMV, GEMM_PATH_SKINNY, GEMM_PATH_SKINNY32,
                                  GEMM_PATH_TILE)
 from edgeexpert_amd.runtime import DeviceBuffer
 from helpers import bf16_half_ulp, from_f16_bits
 
 pytestmark = pytest.mark.gpu
 TOL = oracle.Tolerance.north_star
-PATHS = {"skinny": GEMM_PATH_SKINNY, "skinny32": GEMM_PATH_SKINNY32, "tile": GEMM_PATH_TILE}
+PATHS = {"skinny": GEMM_PATH_SKINNY, "skinny32": GEMM_PATH_SKINNY32, "tile": GEMM_PATH_TILE,
+         "gemv": GEMM_PATH_GEMV}
 
 
 def _dev(a):
@@ -88,7 +89,7 @@ def test_forced_paths_agree(ctx, stream, n, t):
 
 @pytest.mark.parametrize("t,n,k", [(1, 100, 64), (3, 17, 704), (5, 300, 2112), (16, 64, 128), (20, 2816, 4096),
                                    (2, 96, 8192), (7, 33, 1088)])
-@pytest.mark.parametrize("path", ["skinny", "skinny32"])
+@pytest.mark.parametrize("path", ["skinny", "skinny32", "gemv"])
 def test_skinny_ragged_shapes(ctx, stream, t, n, k, path):
     # half-filled last 128-code tiles (k % 128 == 64), row counts off the
     # 16/32-row tiles, token counts off the 16-token tile, every tile count 1..8
@@ -105,7 +106,7 @@ def test_skinny_3bit(ctx, stream, t):
     X = synth.f16_vector(24, f"skinny3/x{t}", t * k).reshape(t, k)
     bufs = (_dev(W), _dev(S), _dev(B), _dev(X))
     ref = oracle.gemm_int4(W, S, B, from_f16_bits(X), bits=3)
-    for path in (None, GEMM_PATH_SKINNY, GEMM_PATH_TILE):
+    for path in (None, GEMM_PATH_SKINNY, GEMM_PATH_TILE, GEMM_PATH_GEMV):
         y = _gemm(ctx, stream, bufs, t, n, k, DTYPE_F16, bits=3, path=path)
         _check(y, ref, DTYPE_F16, f"3-bit t={t} path={path}")
 
@@ -119,3 +120,33 @@ def test_skinny_is_byte_stable_across_dispatches(ctx, stream):
     for _ in range(5):
         again = _gemm(ctx, stream, bufs, t, n, k, DTYPE_F16, path=GEMM_PATH_SKINNY)
         assert np.array_equal(again.view(np.uint32), first.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_BF16])
+def test_gemv_path_equals_decode_gemv(ctx, stream, dtype):
+    # the one-token path is the decode GEMV: on fp16 input its output equals
+    # tfq_gemv_q4g64's bit for bit; on bf16 input, that of the fp16-converted
+    # row, stored as bf16 (both against the oracle too)
+    t, n, k = 3, 2048, 2816
+    W, S, B = synth.int4_matrix(26, "gemvpath/w", n, k)
+    X16 = synth.f16_vector(26, "gemvpath/x", t * k)
+    Xb = synth.bf16_vector(26, "gemvpath/xb", t * k)
+    Wd, Sd, Bd = _dev(W), _dev(S), _dev(B)
+    X = X16 if dtype == DTYPE_F16 else Xb
+    y = _gemm(ctx, stream, (Wd, Sd, Bd, _dev(X)), t, n, k, dtype, path=GEMM_PATH_GEMV)
+    xf = from_f16_bits(X16) if dtype == DTYPE_F16 else synth.bf16_to_f32(Xb)
+    x16 = xf.astype(np.float16).view(np.uint16)
+    g = ops.DequantInt4GEMV(ctx)
+    yd = _dev(np.zeros(t * n, np.uint16))
+    xd = _dev(x16)
+    for i in range(t):
+        g.encode(stream, Wd, Sd, Bd, xd, yd, n, k, x_offset=2 * i * k, y_offset=2 * i * n)
+    stream.sync()
+    ref16 = from_f16_bits(yd.download(np.uint16, t * n)).reshape(t, n)
+    if dtype == DTYPE_F16:
+        assert np.array_equal(y.view(np.uint32), ref16.view(np.uint32))
+    else:
+        # same fp32 sums rounded to bf16 instead of fp16: within one fp16 ulp + half a bf16 ulp
+        bound = np.abs(ref16) * 2.0 ** -11 + bf16_half_ulp(np.maximum(np.abs(ref16), np.abs(y)))
+        assert np.all(np.abs(y - ref16) <= bound)
+    _check(y, oracle.gemm_int4(W, S, B, xf.reshape(t, k)), dtype, f"gemv path dtype={dtype}")
