@@ -233,21 +233,35 @@ def bench_c4(ctx, stream, launch, batch_avg_us, shared_bits=4, shape=C4):
             kb, vb = caches[L]
             layers[L].encode(stream, hid, hid, kb, vb, pos, ws, ws_bytes)
 
-    run = stack
-    if launch == "graph":
-        g = Graph(stream, stack)
-        run = lambda: g.launch(stream)
-    for _ in range(4):
-        run()
-    stream.sync()
-    reps = 32
-    a, b = Event(), Event()
-    a.record(stream)
-    for _ in range(reps):
-        run()
-    b.record(stream)
-    stream.sync()
-    us = a.elapsed_ms(b) * 1e3 / (reps * C4_LAYERS)
+    # the same 8 layers as one tfq_decode_layers call: each layer's tail is
+    # formed inside the next layer's QKV launch
+    chain = ops.DecodeLayers(ctx, [L.keep for L in layers], [spec] * C4_LAYERS)
+    cws_bytes = chain.workspace_bytes(C4_CTX)
+    cws = DeviceBuffer(cws_bytes)
+    hiddens = DeviceBuffer(C4_LAYERS * C["d"] * 2)
+
+    def chained():
+        chain.encode(stream, hid, hiddens, [c[0] for c in caches], [c[1] for c in caches], pos, cws, cws_bytes)
+
+    def time_per_layer(fn):
+        run = fn
+        if launch == "graph":
+            g = Graph(stream, fn)
+            run = lambda: g.launch(stream)
+        for _ in range(4):
+            run()
+        stream.sync()
+        reps = 32
+        a, b = Event(), Event()
+        a.record(stream)
+        for _ in range(reps):
+            run()
+        b.record(stream)
+        stream.sync()
+        return a.elapsed_ms(b) * 1e3 / (reps * C4_LAYERS)
+
+    us_calls = time_per_layer(stack)
+    us = time_per_layer(chained)
     nb = c4_bytes(shared_bits, C)
     gbs = nb["total"] / (us * 1e-6) / 1e9
     floor_us = nb["total"] / (HBM_PEAK_GBS * 1e9) * 1e6
@@ -261,9 +275,14 @@ def bench_c4(ctx, stream, launch, batch_avg_us, shared_bits=4, shape=C4):
                                                 out, C["hd"], C["nq"], C["nkv"], C4_CTX, awsb, aws,
                                                 scale=1.0), 64)
     attn_gbs = nb["attention_kv"] / (attn_us * 1e-6) / 1e9
-    log(f"decode layer {tag} ({launch}, {shared_bits}-bit shared expert): {us:.2f} us/token ({gbs:.0f} GB/s of "
-        f"{nb['total']} B; 8 TB/s floor {floor_us:.2f} us); attention alone {attn_us:.2f} us ({attn_gbs:.0f} GB/s)")
-    return {"us_per_token": round(us, 3), "shared_expert_bits": shared_bits, "bytes_per_token": nb["total"],
+    log(f"decode layer {tag} ({launch}, {shared_bits}-bit shared expert): {us:.2f} us/token per layer of a "
+        f"{C4_LAYERS}-layer chain ({gbs:.0f} GB/s of {nb['total']} B; 8 TB/s floor {floor_us:.2f} us), "
+        f"{us_calls:.2f} us as one call per layer; attention alone {attn_us:.2f} us ({attn_gbs:.0f} GB/s)")
+    return {"us_per_token": round(us, 3), "us_per_token_layer_calls": round(us_calls, 3),
+            "measure": f"per layer of {C4_LAYERS} resident layer copies chained in one tfq_decode_layers call "
+                       f"(each tail formed in the next layer's QKV launch, the last one by the tail kernel); "
+                       f"us_per_token_layer_calls: one tfq_decode_layer call per layer",
+            "shared_expert_bits": shared_bits, "bytes_per_token": nb["total"],
             "attention_form": ("full: head_dim 512, 16 q / 2 kv heads, V from the k projection, rope theta 1e6, "
                                "64 rotated pairs") if C.get("full") else "sliding: head_dim 256, 16 q / 8 kv heads",
             "gbs": round(gbs, 1),

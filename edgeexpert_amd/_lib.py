@@ -17,7 +17,7 @@ CODE_OBJECT_UNITS = ("tfq_gemv", "tfq_int8", "tfq_phase1", "tfq_phase1_routed", 
 CODE_OBJECT_PATHS = [os.path.join(LIB_DIR, u + ".co") for u in CODE_OBJECT_UNITS]
 CODE_OBJECT_PATH = LIB_DIR
 
-ABI_VERSION = 3          # TFQ_ABI_VERSION of include/tfq.h this binding follows
+ABI_VERSION = 4          # TFQ_ABI_VERSION of include/tfq.h this binding follows
 TFQ_OK = 0
 TFQ_E_INVAL = 1
 TFQ_E_UNSUPPORTED = 2
@@ -162,6 +162,9 @@ SIGNATURES = {
     "tfq_attention_decode": [_P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, C.c_float, _P,
                              C.c_size_t],
     "tfq_decode_layer_workspace_bytes": [C.POINTER(DecodeLayerShape), _U32],
+    "tfq_decode_layers_workspace_bytes": [C.POINTER(DecodeLayerShape), _U32, _U32],
+    "tfq_decode_layers": [_P, _P, _U32, C.POINTER(DecodeLayerWeights), C.POINTER(DecodeLayerShape), _P, _P,
+                          C.POINTER(_P), C.POINTER(_P), _U32, _P, C.c_size_t],
     "tfq_decode_layer": [_P, _P, C.POINTER(DecodeLayerWeights), C.POINTER(DecodeLayerShape), _P, _P, _P,
                          _P, _U32, _P, _P, _P, C.c_size_t],
     "tfq_abi_version": [],
@@ -192,6 +195,7 @@ _RES = {"tfq_destroy": None, "tfq_status_string": C.c_char_p, "tfq_expert_layout
         "tfq_moe_prefill_workspace_bytes": C.c_size_t,
         "tfq_attention_workspace_bytes": C.c_size_t,
         "tfq_decode_layer_workspace_bytes": C.c_size_t,
+        "tfq_decode_layers_workspace_bytes": C.c_size_t,
         "tfq_prefill_shared_expert_workspace_bytes": C.c_size_t,
         "tfq_last_error_message": C.c_char_p}
 

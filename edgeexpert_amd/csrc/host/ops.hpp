@@ -6,6 +6,7 @@
 // pointers replace (MTLBuffer, offset) pairs.
 #pragma once
 
+#include <algorithm>
 #include <cmath>
 
 #include "../kernels/abi_types.h"
@@ -34,11 +35,11 @@ static_assert(proj_pl_lds_bytes(kProjMaxK) <= 160u * 1024u, "pipelined tile exce
 // that adds a partial second round of blocks, each re-staging x, and leaves
 // most CUs idle while it drains.
 inline uint32_t grid_for_rows(const Module& m, hipFunction_t f, uint32_t lds, uint64_t rows,
-                              uint32_t rows_per_block) {
+                              uint32_t rows_per_block, uint32_t block = kBlock) {
     uint64_t g = (rows + rows_per_block - 1) / rows_per_block;
     if (g < 1) g = 1;
     if (!f) return (uint32_t)(g < 1024 ? g : 1024);     // launch() reports the missing kernel
-    const uint32_t cap = m.resident_blocks(f, kBlock, lds);
+    const uint32_t cap = m.resident_blocks(f, block, lds);
     return (uint32_t)(g > cap ? cap : g);
 }
 
@@ -54,6 +55,10 @@ inline int check_stage(const NormArg& na) {
         return TFQ_OK;
     case kStageBf16:
         return TFQ_OK;
+    case kStageTail:
+        if (!na.attn || !na.attn_w || !na.h1 || !na.h1_w || !na.h2 || !na.h2_w || !na.ffn_w)
+            return fail(TFQ_E_INVAL, "tail staging needs o, h1, h2 and their norm weights");
+        break;
     case kStagePostAttn:
     case kStageResidual:
         if (!na.attn || !na.attn_w)
@@ -71,8 +76,11 @@ inline int check_stage(const NormArg& na) {
 inline NormArg stage_copy() { return NormArg{nullptr, nullptr, nullptr, 0.0f, kStageCopy, nullptr, nullptr, nullptr}; }
 
 // Kernel-name infix of the GEMV-family form that stages x as `na` says:
-// "" for a plain copy, "norm_" for the forms that normalise while staging.
-inline const char* form_prefix(const NormArg& na) { return na.mode == kStageCopy ? "" : "norm_"; }
+// "" for a plain copy, "norm_" for the forms that normalise while staging,
+// "tail_" for the int4 GEMV that forms the previous layer's tail.
+inline const char* form_prefix(const NormArg& na) {
+    return na.mode == kStageCopy ? "" : na.mode == kStageTail ? "tail_" : "norm_";
+}
 
 // S/Kernels/Quant/DequantInt4GEMV.swift:5-181 (encode and encodeTgx share one kernel here:
 // x always lives in LDS) and S/Kernels/Fusions/FusedQKVGEMV.swift:4-157.
@@ -145,12 +153,14 @@ private:
         const SegShape sh = seg_shape_fit(n / 32, 2);
         char name[64];
         std::snprintf(name, sizeof(name), "tfq_q%u_gemv_%ss%u_p%u", bits, form_prefix(mats.norm), sh.seg, sh.p);
-        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
+        // the tail form runs 1024-thread blocks (entry_points.hpp kTailGemvThreads)
+        const uint32_t block = mats.norm.mode == kStageTail ? 1024u : kBlock;
+        const uint32_t rows_per_block = (block / 64) * (64 / sh.seg) * kRowsInFlight;
         uint32_t nn = n;
         void* args[] = {&mats, &x, &nn};
         hipFunction_t fn = m_.get(name);
         const uint32_t lds = xpairs_lds_bytes(n);
-        return launch(fn, grid_for_rows(m_, fn, lds, mats.total_rows, rows_per_block), kBlock, lds, stream,
+        return launch(fn, grid_for_rows(m_, fn, lds, mats.total_rows, rows_per_block, block), block, lds, stream,
                       args, name);
     }
 
@@ -943,28 +953,31 @@ public:
         if (side_) (void)hipStreamDestroy(side_);
     }
 
+    // Segments of the workspace, 256-byte aligned. The d-sized vectors that
+    // one layer leaves for the next in a chain (o, h1, h2) come first, so
+    // their offsets do not depend on the layer's attention shape.
     struct Layout {
-        size_t q, attn, parts, parts_bytes, o, logits, idx, w, acts, sact, h1, h2, hmid, inv, kv, total;
+        size_t o, h1, h2, hmid, inv, q, attn, parts, parts_bytes, logits, idx, w, acts, sact, kv, total;
     };
     static Layout layout(const tfq_decode_layer_shape& s, uint32_t max_seq) {
         auto up = [](size_t v) { return (v + 255) / 256 * 256; };
         Layout L{};
         size_t off = 0;
         const size_t qd = (size_t)s.num_q_heads * s.head_dim;
+        L.o = off;      off += up((size_t)s.d * 2);
+        L.h1 = off;     off += up((size_t)s.d * 2);
+        L.h2 = off;     off += up((size_t)s.d * 2);
+        L.hmid = off;   off += up((size_t)s.d * 2);
+        L.inv = off;    off += up(4);
         L.q = off;      off += up(qd * 2);
         L.attn = off;   off += up(qd * 2);
         L.parts = off;  L.parts_bytes = Attention::workspace_bytes(s.head_dim, s.num_q_heads, max_seq, s.window);
         off += up(L.parts_bytes);
-        L.o = off;      off += up((size_t)s.d * 2);
         L.logits = off; off += up(TFQ_ROUTER_WORKSPACE_BYTES);
         L.idx = off;    off += up((size_t)s.top_k * 4);
         L.w = off;      off += up((size_t)s.top_k * 2);
         L.acts = off;   off += up((size_t)s.top_k * s.expert_f * 2);
         L.sact = off;   off += up((size_t)s.shared_f * 2);
-        L.h1 = off;     off += up((size_t)s.d * 2);
-        L.h2 = off;     off += up((size_t)s.d * 2);
-        L.hmid = off;   off += up((size_t)s.d * 2);
-        L.inv = off;    off += up(4);
         L.kv = off;     off += up((size_t)2 * s.num_kv_heads * s.head_dim * 2);   // staged raw k, v
         L.total = off;
         return L;
@@ -974,15 +987,98 @@ public:
                const uint16_t* hidden_in, uint16_t* hidden_out, uint16_t* k_cache, uint16_t* v_cache,
                uint32_t position, uint32_t* out_indices, uint16_t* out_weights, void* workspace,
                size_t workspace_bytes) {
-        if (!hidden_in || !hidden_out || !k_cache || !v_cache || !workspace)
-            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!hidden_in || !hidden_out) return fail(TFQ_E_INVAL, "null pointer argument");
+        if (int rc = check_layer(w, s, k_cache, v_cache, workspace)) return rc;
+        for (const void* p : {(const void*)hidden_in, (const void*)hidden_out})
+            if (!aligned(p, 16)) return fail(TFQ_E_INVAL, "hidden vectors and norm weights must be 16-byte aligned");
+        const Layout L = layout(s, position + 1);
+        if (workspace_bytes < L.total) return fail(TFQ_E_INVAL, "decode-layer workspace too small");
+        if (int rc = ensure_side_stream()) return rc;
+        const NormArg in_norm{w.input_norm, nullptr, nullptr, s.eps, kStageNorm};
+        if (int rc = body(stream, w, s, hidden_in, in_norm, hidden_in, k_cache, v_cache, position, out_indices,
+                          out_weights, static_cast<char*>(workspace), L))
+            return rc;
+        return tail(stream, w, s, hidden_in, hidden_out, static_cast<char*>(workspace), L);
+    }
+
+    // n consecutive layers for one token: layer i's tail (its output, the
+    // next layer's input) is formed by layer i+1's QKV GEMV while it stages
+    // that input (kStageTail), so a chain of n layers takes n - 1 launches
+    // fewer than n calls of encode. hiddens [n][d] receives every layer's
+    // output (row i: layer i's, written by block 0 of layer i+1's QKV launch,
+    // or by the last tail). The layers share d, eps and the workspace
+    // (layout(max over the layers)); layer i+1 reads layer i's o, h1, h2
+    // from the workspace's first segments before it overwrites them.
+    int encode_chain(void* stream, uint32_t n, const tfq_decode_layer_weights* w,
+                     const tfq_decode_layer_shape* s, const uint16_t* hidden_in, uint16_t* hiddens,
+                     uint16_t* const* k_caches, uint16_t* const* v_caches, uint32_t position, void* workspace,
+                     size_t workspace_bytes) {
+        if (n == 0 || !w || !s || !k_caches || !v_caches || !hidden_in || !hiddens)
+            return fail(TFQ_E_INVAL, "null pointer argument or no layers");
+        if (!aligned(hidden_in, 16) || !aligned(hiddens, 16))
+            return fail(TFQ_E_INVAL, "hidden vectors and norm weights must be 16-byte aligned");
+        size_t need = 0;
+        for (uint32_t i = 0; i < n; ++i) {
+            if (int rc = check_layer(w[i], s[i], k_caches[i], v_caches[i], workspace)) return rc;
+            if (s[i].d != s[0].d || s[i].eps != s[0].eps)
+                return fail(TFQ_E_INVAL, "chained layers must share d and eps (layer %u differs)", i);
+            need = std::max(need, layout(s[i], position + 1).total);
+        }
+        if (workspace_bytes < need) return fail(TFQ_E_INVAL, "decode-layer workspace too small");
+        if (int rc = ensure_side_stream()) return rc;
+        char* ws = static_cast<char*>(workspace);
+        const size_t d = s[0].d;
+        for (uint32_t i = 0; i < n; ++i) {
+            const Layout L = layout(s[i], position + 1);
+            const uint16_t* hidden = i == 0 ? hidden_in : hiddens + (i - 1) * d;      // this layer's input
+            NormArg stage{w[i].input_norm, nullptr, nullptr, s[i].eps, kStageNorm};
+            const uint16_t* x = hidden;
+            if (i > 0) {
+                // the previous layer's tail, formed while staging: its input,
+                // o, h1, h2 and norms; block 0 exports its output (= `hidden`)
+                const tfq_decode_layer_weights& p = w[i - 1];
+                x = i == 1 ? hidden_in : hiddens + (i - 2) * d;
+                stage = NormArg{w[i].input_norm, reinterpret_cast<const uint16_t*>(ws + L.o), p.post_attention_norm,
+                                s[i].eps, kStageTail, nullptr, hiddens + (i - 1) * d, nullptr,
+                                reinterpret_cast<const uint16_t*>(ws + L.h1), p.post_ffn1_norm,
+                                reinterpret_cast<const uint16_t*>(ws + L.h2), p.post_ffn2_norm, p.post_ffn_norm,
+                                p.layer_scalar};
+            }
+            if (int rc = body(stream, w[i], s[i], x, stage, hidden, k_caches[i], v_caches[i], position, nullptr,
+                              nullptr, ws, L))
+                return rc;
+        }
+        const uint16_t* last_in = n == 1 ? hidden_in : hiddens + (n - 2) * d;
+        return tail(stream, w[n - 1], s[n - 1], last_in, hiddens + (n - 1) * d, ws, layout(s[n - 1], position + 1));
+    }
+
+    static size_t chain_workspace_bytes(uint32_t n, const tfq_decode_layer_shape* s, uint32_t max_seq) {
+        size_t need = 0;
+        for (uint32_t i = 0; i < n; ++i) need = std::max(need, layout(s[i], max_seq).total);
+        return need;
+    }
+
+    // Creates the side stream and its fork/join events (tfq_create calls it,
+    // so that no stream is created while the caller captures a graph).
+    int ensure_side_stream() {
+        if (side_) return TFQ_OK;
+        int rc = hip_check(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking), "hipStreamCreate");
+        if (rc) return rc;
+        rc = hip_check(hipEventCreateWithFlags(&fork_, hipEventDisableTiming), "hipEventCreate");
+        if (rc) return rc;
+        return hip_check(hipEventCreateWithFlags(&join_, hipEventDisableTiming), "hipEventCreate");
+    }
+
+    // Contract checks shared by encode and encode_chain.
+    int check_layer(const tfq_decode_layer_weights& w, const tfq_decode_layer_shape& s, const uint16_t* k_cache,
+                    const uint16_t* v_cache, const void* workspace) const {
+        if (!k_cache || !v_cache || !workspace) return fail(TFQ_E_INVAL, "null pointer argument");
         if (!w.input_norm || !w.q_norm || !w.k_norm || !w.post_attention_norm || !w.pre_ffn_norm ||
             !w.pre_ffn2_norm || !w.post_ffn1_norm || !w.post_ffn2_norm || !w.post_ffn_norm)
             return fail(TFQ_E_INVAL, "every norm weight is required");
         if (s.d == 0 || s.d % 64 || s.d > 4096) return fail(TFQ_E_INVAL, "d=%u must be a multiple of 64 <= 4096", s.d);
-        for (const void* p : {(const void*)hidden_in, (const void*)hidden_out, (const void*)w.input_norm,
-                              (const void*)w.post_attention_norm, (const void*)w.pre_ffn_norm,
-                              (const void*)w.pre_ffn2_norm, (const void*)w.post_ffn1_norm,
+        for (const void* p : {(const void*)w.input_norm, (const void*)w.post_attention_norm,
+                              (const void*)w.pre_ffn_norm, (const void*)w.pre_ffn2_norm, (const void*)w.post_ffn1_norm,
                               (const void*)w.post_ffn2_norm, (const void*)w.post_ffn_norm})
             if (!aligned(p, 16)) return fail(TFQ_E_INVAL, "hidden vectors and norm weights must be 16-byte aligned");
         if (!aligned(workspace, 256)) return fail(TFQ_E_INVAL, "workspace must be 256-byte aligned");
@@ -990,11 +1086,19 @@ public:
         const uint32_t shared_bits = w.shared_bits ? w.shared_bits : 4u;
         if (shared_bits != 4 && shared_bits != 8)
             return fail(TFQ_E_INVAL, "SharedExpert unsupported weight bits: %u", w.shared_bits);
+        return TFQ_OK;
+    }
+
+    // Steps 1-6 of one layer (everything but the tail): the QKV GEMV stages
+    // x as `qkv_stage` says (the input norm of `hidden`, or the previous
+    // layer's tail followed by it); `hidden` is the layer's input, used by
+    // the post-attention residual. Ends with `stream` waiting for the
+    // shared expert's side stream.
+    int body(void* stream, const tfq_decode_layer_weights& w, const tfq_decode_layer_shape& s, const uint16_t* x,
+             const NormArg& qkv_stage, const uint16_t* hidden, uint16_t* k_cache, uint16_t* v_cache,
+             uint32_t position, uint32_t* out_indices, uint16_t* out_weights, char* ws, const Layout& L) {
         const uint32_t seq_len = position + 1;
-        const Layout L = layout(s, seq_len);
-        if (workspace_bytes < L.total) return fail(TFQ_E_INVAL, "decode-layer workspace too small");
-        if (int rc = ensure_side_stream()) return rc;
-        char* ws = static_cast<char*>(workspace);
+        const uint32_t shared_bits = w.shared_bits ? w.shared_bits : 4u;
         uint16_t* q = reinterpret_cast<uint16_t*>(ws + L.q);
         uint16_t* attn = reinterpret_cast<uint16_t*>(ws + L.attn);
         uint16_t* o = reinterpret_cast<uint16_t*>(ws + L.o);
@@ -1016,14 +1120,13 @@ public:
         //    projection (v_proj absent: the full-attention layers,
         //    RealForwardRunner.swift:2252-2255, whose fused QKV runs k_proj as
         //    the v projection; one k GEMV serves both here)
-        const NormArg in_norm{w.input_norm, nullptr, nullptr, s.eps, kStageNorm};
         const bool v_from_k = w.v_proj.weights == nullptr;
         const bool staged = v_from_k || (s.head_dim == 512 && s.num_q_heads == 8 * s.num_kv_heads);
         uint16_t* kraw = staged ? reinterpret_cast<uint16_t*>(ws + L.kv) : k_cache + slot;
         uint16_t* vraw = !staged ? v_cache + slot : v_from_k ? kraw : kraw + kvd;
-        int rc = v_from_k ? gemv_.encode_qk(stream, w.q_proj, w.k_proj, hidden_in, q, kraw, qd, kvd, s.d, in_norm)
-                          : gemv_.encode_qkv(stream, w.q_proj, w.k_proj, w.v_proj, hidden_in, q, kraw, vraw, qd, kvd,
-                                             s.d, in_norm);
+        int rc = v_from_k ? gemv_.encode_qk(stream, w.q_proj, w.k_proj, x, q, kraw, qd, kvd, s.d, qkv_stage)
+                          : gemv_.encode_qkv(stream, w.q_proj, w.k_proj, w.v_proj, x, q, kraw, vraw, qd, kvd,
+                                             s.d, qkv_stage);
         if (rc) return rc;
         // 2. q/k/v epilogue + attention
         const AttnEpilogue epi{w.q_norm, w.k_norm, s.eps, s.rope_theta, s.rotated_pairs, 0, 0.0,
@@ -1040,9 +1143,9 @@ public:
         rc = hip_check(hipStreamWaitEvent(side_, fork_, 0), "hipStreamWaitEvent");
         if (rc) return rc;
         const NormArg dense{w.pre_ffn_norm, o, w.post_attention_norm, s.eps, kStagePostAttn};
-        rc = shared_bits == 8 ? shared8_.encode(side_, hidden_in, w.shared_gate, w.shared_up, w.shared_down, h1,
+        rc = shared_bits == 8 ? shared8_.encode(side_, hidden, w.shared_gate, w.shared_up, w.shared_down, h1,
                                                 s.d, s.shared_f, sact, dense)
-                              : shared_.encode(side_, hidden_in, w.shared_gate, w.shared_up, w.shared_down, h1,
+                              : shared_.encode(side_, hidden, w.shared_gate, w.shared_up, w.shared_down, h1,
                                                s.d, s.shared_f, sact, dense);
         if (rc) return rc;
         rc = hip_check(hipEventRecord(join_, side_), "hipEventRecord");
@@ -1052,7 +1155,7 @@ public:
         const NormArg router_x{nullptr, o, w.post_attention_norm, s.eps, kStagePostAttn, nullptr, hmid, hinv};
         const tfq_router& r = w.router;
         float* logits_used = nullptr;
-        rc = moe_.encode_router_logits(stream, r.weights, r.scales, r.biases, hidden_in, r.effective_scale,
+        rc = moe_.encode_router_logits(stream, r.weights, r.scales, r.biases, hidden, r.effective_scale,
                                        logits, r.num_experts, s.d, s.top_k, logits, router_x, &logits_used);
         if (rc) return rc;
         // 6. routed experts on pre_feedforward_layernorm_2(h), the top-k selected inside
@@ -1063,25 +1166,20 @@ public:
         if (rc) return rc;
         rc = moe_.encode_phase2(stream, w.experts, idx, acts, rw, nullptr, h2, s.d, s.expert_f, s.top_k);
         if (rc) return rc;
-        // 7. tail
-        rc = hip_check(hipStreamWaitEvent((hipStream_t)stream, join_, 0), "hipStreamWaitEvent");
-        if (rc) return rc;
-        float eps = s.eps, scalar = w.layer_scalar;
-        uint32_t d = s.d;
-        void* ta[] = {(void*)&hidden_in, &o, (void*)&w.post_attention_norm, &h1, (void*)&w.post_ffn1_norm,
-                      &h2, (void*)&w.post_ffn2_norm, (void*)&w.post_ffn_norm, &eps, &scalar, &hidden_out, &d};
-        return launch2(m_, "tfq_layer_tail", 1, 1, 1024, 0, stream, ta);
+        return hip_check(hipStreamWaitEvent((hipStream_t)stream, join_, 0), "hipStreamWaitEvent");
     }
 
-    // Creates the side stream and its fork/join events (tfq_create calls it,
-    // so that no stream is created while the caller captures a graph).
-    int ensure_side_stream() {
-        if (side_) return TFQ_OK;
-        int rc = hip_check(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking), "hipStreamCreate");
-        if (rc) return rc;
-        rc = hip_check(hipEventCreateWithFlags(&fork_, hipEventDisableTiming), "hipEventCreate");
-        if (rc) return rc;
-        return hip_check(hipEventCreateWithFlags(&join_, hipEventDisableTiming), "hipEventCreate");
+    // 7. the tail kernel: out from the layer's input `hidden` and its o, h1, h2.
+    int tail(void* stream, const tfq_decode_layer_weights& w, const tfq_decode_layer_shape& s,
+             const uint16_t* hidden, uint16_t* out, char* ws, const Layout& L) {
+        const uint16_t* o = reinterpret_cast<const uint16_t*>(ws + L.o);
+        const uint16_t* h1 = reinterpret_cast<const uint16_t*>(ws + L.h1);
+        const uint16_t* h2 = reinterpret_cast<const uint16_t*>(ws + L.h2);
+        float eps = s.eps, scalar = w.layer_scalar;
+        uint32_t d = s.d;
+        void* ta[] = {(void*)&hidden, (void*)&o, (void*)&w.post_attention_norm, (void*)&h1, (void*)&w.post_ffn1_norm,
+                      (void*)&h2, (void*)&w.post_ffn2_norm, (void*)&w.post_ffn_norm, &eps, &scalar, &out, &d};
+        return launch2(m_, "tfq_layer_tail", 1, 1, 1024, 0, stream, ta);
     }
 
 private:

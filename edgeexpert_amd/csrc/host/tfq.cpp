@@ -33,6 +33,7 @@ static std::vector<std::string> kernel_names() {
     for (const char* s : q4_shapes)
         for (const char* form : {"", "norm_"}) {
             names.push_back(std::string("tfq_q4_gemv_") + form + s);
+            if (*form) names.push_back(std::string("tfq_q4_gemv_tail_") + s);
             names.push_back(std::string("tfq_q3_gemv_") + form + s);
             for (const char* b : {"", "b2_", "b3_"}) {
                 names.push_back(std::string("tfq_moe_phase1_") + b + form + s);
@@ -459,6 +460,21 @@ int tfq_decode_layer(tfq_ctx* ctx, void* stream, const tfq_decode_layer_weights*
     if (!weights || !shape) return fail(TFQ_E_INVAL, "null weights or shape");
     return ctx->layer->encode(stream, *weights, *shape, hidden_in, hidden_out, k_cache, v_cache, position,
                               out_indices, out_weights, workspace, workspace_bytes);
+}
+
+size_t tfq_decode_layers_workspace_bytes(const tfq_decode_layer_shape* shapes, uint32_t n_layers,
+                                         uint32_t max_seq_len) {
+    if (!shapes || n_layers == 0 || max_seq_len == 0) return 0;
+    return DecodeLayer::chain_workspace_bytes(n_layers, shapes, max_seq_len);
+}
+
+int tfq_decode_layers(tfq_ctx* ctx, void* stream, uint32_t n_layers, const tfq_decode_layer_weights* weights,
+                      const tfq_decode_layer_shape* shapes, const uint16_t* hidden_in, uint16_t* hiddens,
+                      uint16_t* const* k_caches, uint16_t* const* v_caches, uint32_t position, void* workspace,
+                      size_t workspace_bytes) {
+    TFQ_REQUIRE_CTX(ctx);
+    return ctx->layer->encode_chain(stream, n_layers, weights, shapes, hidden_in, hiddens, k_caches, v_caches,
+                                    position, workspace, workspace_bytes);
 }
 
 int tfq_gemm_q4g64(tfq_ctx* ctx, void* stream, const void* weights, const uint16_t* scales,

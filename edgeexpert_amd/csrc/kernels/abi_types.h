@@ -43,8 +43,14 @@ struct Q8Mat {
 //   kStageBf16      a = fp16(x) for a bf16 x (round to nearest even, as the
 //                   prefill GEMM converts its activations); the GEMV then
 //                   stores its rows as bf16 too (the prefill GEMM's one-token path)
+//   kStageTail      out = the previous decoder layer's tail (layer_tail in
+//                   attention.hpp) from x = that layer's input hidden, attn =
+//                   its o projection (attn_w its post_attention_norm), h1 /
+//                   h2 with their output norms h1_w / h2_w, ffn_w and scalar;
+//                   block 0 stores out (the layer's output) to export_h; then
+//                   a = fp16(out * w * r(out)) (the next layer's input norm)
 enum StageMode : uint32_t { kStageCopy = 0, kStageNorm = 1, kStagePostAttn = 2, kStageResidual = 3,
-                            kStageScaled = 4, kStageBf16 = 5 };
+                            kStageScaled = 4, kStageBf16 = 5, kStageTail = 6 };
 
 struct NormArg {
     const uint16_t* w;
@@ -53,8 +59,14 @@ struct NormArg {
     float eps;
     uint32_t mode;
     const float* inv;          // kStageScaled: r(h)
-    uint16_t* export_h;        // kStagePostAttn: h and r(h) from block 0 (nullable)
+    uint16_t* export_h;        // kStagePostAttn: h and r(h) from block 0 (nullable); kStageTail: out
     float* export_inv;
+    const uint16_t* h1;        // kStageTail: shared-expert output and post_feedforward_layernorm_1
+    const uint16_t* h1_w;
+    const uint16_t* h2;        // kStageTail: routed output and post_feedforward_layernorm_2
+    const uint16_t* h2_w;
+    const uint16_t* ffn_w;     // kStageTail: post_feedforward_layernorm
+    float scalar;              // kStageTail: layer scalar
 };
 
 // Dynamic LDS of the int4 GEMV-family kernels for an activation vector of n

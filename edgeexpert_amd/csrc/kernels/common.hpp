@@ -537,6 +537,41 @@ __device__ __forceinline__ void stage_act_scalar(const uint16_t* __restrict__ x,
                                                  uint32_t n, const NormArg& na) {
     copy_to_lds<NT>(x, lds, n);
     __syncthreads();
+    if (na.mode == kStageTail) {
+        float s3[3] = {0.0f, 0.0f, 0.0f};
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            const float a = h2f(na.attn[i]), u = h2f(na.h1[i]), v = h2f(na.h2[i]);
+            s3[0] = fmaf(a, a, s3[0]);
+            s3[1] = fmaf(u, u, s3[1]);
+            s3[2] = fmaf(v, v, s3[2]);
+        }
+        block_sums<3, NT>(s3);
+        const float inv_a = 1.0f / sqrtf(s3[0] / (float)n + na.eps);
+        const float inv_1 = 1.0f / sqrtf(s3[1] / (float)n + na.eps);
+        const float inv_2 = 1.0f / sqrtf(s3[2] / (float)n + na.eps);
+        auto h12_at = [&](uint32_t i) {
+            const uint16_t a1 = f2h(h2f(na.h1[i]) * h2f(na.h1_w[i]) * inv_1);
+            const uint16_t a2 = f2h(h2f(na.h2[i]) * h2f(na.h2_w[i]) * inv_2);
+            return f2h(h2f(a1) + h2f(a2));
+        };
+        float s12 = 0.0f;
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            const uint16_t an = f2h(h2f(na.attn[i]) * h2f(na.attn_w[i]) * inv_a);
+            lds[i] = f2h(h2f(lds[i]) + h2f(an));
+            const float h12 = h2f(h12_at(i));
+            s12 = fmaf(h12, h12, s12);
+        }
+        const float inv_12 = 1.0f / sqrtf(block_sum<NT>(s12) / (float)n + na.eps);
+        const float sc = (float)(_Float16)na.scalar;
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            const uint16_t f2 = f2h(h2f(h12_at(i)) * h2f(na.ffn_w[i]) * inv_12);
+            lds[i] = f2h(h2f(f2h(h2f(lds[i]) + h2f(f2))) * sc);
+            if (na.export_h && blockIdx.x == 0) na.export_h[i] = lds[i];
+        }
+        __syncthreads();
+        rmsnorm_lds<NT>(lds, n, na.w, na.eps);
+        return;
+    }
     if (na.mode == kStageBf16) {
         for (uint32_t i = threadIdx.x; i < n; i += NT) lds[i] = f2h(bf2f(lds[i]));
         __syncthreads();
@@ -599,20 +634,38 @@ __device__ __forceinline__ uint4 ld16h(const uint16_t* p, uint32_t chunk) {
 // Both end with a block barrier. Inputs that are not 16-byte aligned, or
 // longer than 8·CH·NT halves, take the scalar path instead (two passes).
 // NORM == false compiles the copy-only form (NormArg ignored).
-template <uint32_t NT, uint32_t CH, bool NORM = true, bool DPP_SUMS = true>
+// TAIL: the kStageTail form (its five extra input vectors in registers).
+template <uint32_t NT, uint32_t CH, bool NORM = true, bool DPP_SUMS = true, bool TAIL = false>
 struct XStage {
+    static constexpr uint32_t TC = TAIL ? CH : 1;
     h8 xv[CH], av[CH], awv[CH], wv[CH];
+    h8 t1[TC], t1w[TC], t2[TC], t2w[TC], tfw[TC];   // kStageTail: h1, its norm weight, h2, its, post-FFN norm
     float inv_in;      // kStageScaled: r(h), loaded with the chunks
     bool vec;
 
     __device__ __forceinline__ void load(const uint16_t* __restrict__ x, uint32_t n, const NormArg& na) {
         const uint32_t nch = n >> 3;
-        const uintptr_t align =
+        const bool tail = TAIL && NORM && na.mode == kStageTail;
+        uintptr_t align =
             (uintptr_t)x | (uintptr_t)na.w | (uintptr_t)na.attn | (uintptr_t)na.attn_w | (uintptr_t)na.export_h;
+        if (tail)
+            align |= (uintptr_t)na.h1 | (uintptr_t)na.h1_w | (uintptr_t)na.h2 | (uintptr_t)na.h2_w | (uintptr_t)na.ffn_w;
         vec = ((NORM ? align : (uintptr_t)x) & 15u) == 0 && (n & 7u) == 0 && nch != 0 && nch <= CH * NT;
         if (!vec) return;
-        const bool post = NORM && (na.mode == kStagePostAttn || na.mode == kStageResidual);
-        const bool norm = NORM && (na.mode == kStageNorm || na.mode == kStagePostAttn || na.mode == kStageScaled);
+        const bool post = NORM && (na.mode == kStagePostAttn || na.mode == kStageResidual || tail);
+        const bool norm = NORM && (na.mode == kStageNorm || na.mode == kStagePostAttn || na.mode == kStageScaled || tail);
+        if (tail) {
+#pragma unroll
+            for (uint32_t i = 0; i < TC; ++i) {
+                const uint32_t c0 = threadIdx.x + i * NT;
+                const uint32_t c = c0 < nch ? c0 : nch - 1;
+                t1[i] = __builtin_bit_cast(h8, ld16h(na.h1, c));
+                t1w[i] = __builtin_bit_cast(h8, ld16h(na.h1_w, c));
+                t2[i] = __builtin_bit_cast(h8, ld16h(na.h2, c));
+                t2w[i] = __builtin_bit_cast(h8, ld16h(na.h2_w, c));
+                tfw[i] = __builtin_bit_cast(h8, ld16h(na.ffn_w, c));
+            }
+        }
         if (NORM && na.mode == kStageScaled) inv_in = *na.inv;
         // clamped chunk indices: every load is valid and unconditional (chunks
         // past the end are loaded twice and never stored or counted)
@@ -634,11 +687,56 @@ struct XStage {
         if (!NORM) return;
         const uint32_t nch = n >> 3;
         const bool post = na.mode == kStagePostAttn || na.mode == kStageResidual;
-        const bool norm = na.mode == kStageNorm || na.mode == kStagePostAttn;
+        const bool norm = na.mode == kStageNorm || na.mode == kStagePostAttn || (TAIL && na.mode == kStageTail);
         if (na.mode == kStageBf16) {
 #pragma unroll
             for (uint32_t i = 0; i < CH; ++i) xv[i] = bf16x8_to_f16(__builtin_bit_cast(uint4, xv[i]));
             return;
+        }
+        if (TAIL && na.mode == kStageTail) {
+            // the previous layer's tail, as layer_tail computes it (same
+            // rounding points), then its output's RMSNorm below
+            float s3[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i)
+                if (threadIdx.x + i * NT < nch)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        s3[0] = fmaf((float)av[i][e], (float)av[i][e], s3[0]);
+                        s3[1] = fmaf((float)t1[i][e], (float)t1[i][e], s3[1]);
+                        s3[2] = fmaf((float)t2[i][e], (float)t2[i][e], s3[2]);
+                    }
+            block_sums<3, NT>(s3);
+            const float inv_a = 1.0f / sqrtf(s3[0] / (float)n + na.eps);
+            const float inv_1 = 1.0f / sqrtf(s3[1] / (float)n + na.eps);
+            const float inv_2 = 1.0f / sqrtf(s3[2] / (float)n + na.eps);
+            float s12[1] = {0.0f};
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const _Float16 an = (_Float16)((float)av[i][e] * (float)awv[i][e] * inv_a);
+                    xv[i][e] = (_Float16)((float)xv[i][e] + (float)an);
+                    const _Float16 a1 = (_Float16)((float)t1[i][e] * (float)t1w[i][e] * inv_1);
+                    const _Float16 a2 = (_Float16)((float)t2[i][e] * (float)t2w[i][e] * inv_2);
+                    t1[i][e] = (_Float16)((float)a1 + (float)a2);
+                    if (threadIdx.x + i * NT < nch) s12[0] = fmaf((float)t1[i][e], (float)t1[i][e], s12[0]);
+                }
+            block_sums<1, NT>(s12);
+            const float inv_12 = 1.0f / sqrtf(s12[0] / (float)n + na.eps);
+            const float sc = (float)(_Float16)na.scalar;
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const _Float16 f2 = (_Float16)((float)t1[i][e] * (float)tfw[i][e] * inv_12);
+                    const _Float16 r = (_Float16)((float)xv[i][e] + (float)f2);
+                    xv[i][e] = (_Float16)((float)r * sc);
+                }
+            if (na.export_h && blockIdx.x == 0)
+#pragma unroll
+                for (uint32_t i = 0; i < CH; ++i)
+                    if (threadIdx.x + i * NT < nch) reinterpret_cast<h8*>(na.export_h)[threadIdx.x + i * NT] = xv[i];
         }
         if (na.mode == kStageScaled) {
 #pragma unroll

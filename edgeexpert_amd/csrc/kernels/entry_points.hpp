@@ -38,6 +38,14 @@ constexpr int kRowsInFlight = 1;
         q4_gemv_multi<SEG, P, kRowsInFlight, true, BITS>(mats, x, n);                             \
     }
 #define TFQ_Q4_GEMV(SEG, P) TFQ_GEMV_FORMS(q4, 4, SEG, P)
+// The int4 GEMV staging the previous decoder layer's tail (kStageTail; the
+// chained decode layers' fused QKV), 1024-thread blocks.
+constexpr uint32_t kTailGemvThreads = 1024;
+#define TFQ_Q4_GEMV_TAIL(SEG, P)                                                                 \
+    extern "C" __global__ __launch_bounds__(kTailGemvThreads) void tfq_q4_gemv_tail_s##SEG##_p##P( \
+        Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
+        q4_gemv_multi<SEG, P, kRowsInFlight, true, 4, true, kTailGemvThreads>(mats, x, n);        \
+    }
 #define TFQ_Q3_GEMV(SEG, P) TFQ_GEMV_FORMS(q3, 3, SEG, P)
 
 #define TFQ_Q8_GEMV(SEG, P)                                                                      \

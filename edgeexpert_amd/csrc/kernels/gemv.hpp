@@ -63,11 +63,16 @@ __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, 
 // the staging's registers are free before the weight registers fill (one
 // memory latency later start, worth it for long launches: higher occupancy).
 // BITS: code width of the weight rows (2, 3 or 4; rows of n·BITS/8 bytes).
-template <int SEG, int P, int R, bool NORM, bool STAGE_FIRST = false, int BITS = 4, typename Out>
+// TAIL: the kStageTail staging form (the previous decoder layer's tail).
+// NT: threads per block (256; 1024 for the tail form, whose staging reads
+// nine vectors: a quarter of the blocks, each staging once for four times
+// the rows, keeps that L2 traffic to a quarter).
+template <int SEG, int P, int R, bool NORM, bool STAGE_FIRST = false, int BITS = 4, bool TAIL = false,
+          uint32_t NT = kThreads, typename Out>
 __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __restrict__ x, uint32_t n,
                                         Out out) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
-    constexpr uint32_t NT = kThreads;
+    constexpr uint32_t CH = NT >= 512 ? 1 : kStageChunks;       // staged 16-byte chunks per thread
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     constexpr uint32_t nwaves = NT / 64;
@@ -107,7 +112,7 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
             }
         }
     };
-    XStage<NT, kStageChunks, NORM> xs;
+    XStage<NT, CH, NORM, true, TAIL> xs;
     xs.load(x, n, mats.norm);
     if (!STAGE_FIRST) issue(0, std::true_type{});
     const XPairs xp = xs.pairs(x, lds_xh, n, mats.norm);
@@ -140,12 +145,12 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
     }
 }
 
-template <int SEG, int P, int R, bool NORM, int BITS = 4>
+template <int SEG, int P, int R, bool NORM, int BITS = 4, bool TAIL = false, uint32_t NT = kThreads>
 __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_t* __restrict__ x,
                                               uint32_t n) {
     const uint32_t row_bytes = (n >> 3) * BITS, ngroups = n >> 6;
     const bool out_bf16 = NORM && mats.norm.mode == kStageBf16;
-    q4_rows<SEG, P, R, NORM, false, BITS>(mats, x, n, [&](uint32_t row, float v) {
+    q4_rows<SEG, P, R, NORM, false, BITS, TAIL, NT>(mats, x, n, [&](uint32_t row, float v) {
         const Q4Row q = resolve_row(mats, row, row_bytes, ngroups);
         const float o = q.r ? h2f(*q.r) + v : v;
         *q.y = out_bf16 ? __builtin_bit_cast(uint16_t, (__bf16)o) : f2h(o);

@@ -3,6 +3,7 @@
 #include "entry_points.hpp"
 
 TFQ_Q4_TABLE(TFQ_Q4_GEMV)
+TFQ_Q4_TABLE(TFQ_Q4_GEMV_TAIL)
 TFQ_Q4_TABLE(TFQ_Q3_GEMV)
 TFQ_Q4_TABLE(TFQ_LM_HEAD)
 

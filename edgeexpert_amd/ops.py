@@ -661,3 +661,29 @@ class DecodeLayer:
                                      _addr(hidden_in), _addr(hidden_out), _addr(k_cache), _addr(v_cache),
                                      position, _addr(out_indices), _addr(out_weights), _addr(workspace),
                                      workspace_bytes), "DecodeLayer.encode")
+
+
+class DecodeLayers:
+    """Consecutive decoder layers per call (tfq_decode_layers): the per-token
+    loop over layers of RealForwardRunner (RealForwardRunner.swift:2239-2862)
+    with each layer's tail formed inside the next layer's QKV launch."""
+
+    def __init__(self, context: Context, weights: list, shapes: list):
+        assert len(weights) == len(shapes) and weights
+        self.ctx = context
+        self.n = len(weights)
+        self._w = (DecodeLayerWeights * self.n)(*[w.desc() for w in weights])
+        self._s = (DecodeLayerShape * self.n)(*[s.desc() for s in shapes])
+        self.keep = weights
+
+    def workspace_bytes(self, max_seq_len: int) -> int:
+        return lib().tfq_decode_layers_workspace_bytes(self._s, self.n, max_seq_len)
+
+    def encode(self, stream, hidden_in, hiddens, k_caches, v_caches, position, workspace, workspace_bytes):
+        """hiddens: device buffer [n][d] receiving every layer's output;
+        k_caches / v_caches: one device buffer per layer."""
+        kc = (C.c_void_p * self.n)(*[_addr(b) for b in k_caches])
+        vc = (C.c_void_p * self.n)(*[_addr(b) for b in v_caches])
+        check(lib().tfq_decode_layers(self.ctx.handle, _s(stream), self.n, self._w, self._s, _addr(hidden_in),
+                                      _addr(hiddens), kc, vc, position, _addr(workspace), workspace_bytes),
+              "DecodeLayers.encode")

@@ -36,7 +36,9 @@
  *    TFQ_MOE_GROUP_STATE_WORDS words and added tfq_decode_layer_weights
  *    .shared_bits; version 3 added the staged k/v segment at the end of the
  *    tfq_decode_layer workspace (tfq_decode_layer_workspace_bytes grew),
- *    head_dim 512 and a NULL v_proj (V from the k projection).
+ *    head_dim 512 and a NULL v_proj (V from the k projection); version 4
+ *    moved the tfq_decode_layer workspace's o, h1, h2 segments to its
+ *    start and added tfq_decode_layers.
  */
 #ifndef TFQ_H
 #define TFQ_H
@@ -60,7 +62,7 @@ extern "C" {
 /* Version of this header's structs and contracts; tfq_abi_version() returns
  * the library's. No reference counterpart (the Swift wrappers and their
  * shaders ship in one build). */
-#define TFQ_ABI_VERSION 3
+#define TFQ_ABI_VERSION 4
 int tfq_abi_version(void);
 
 typedef struct tfq_ctx tfq_ctx;
@@ -410,6 +412,30 @@ int tfq_decode_layer(tfq_ctx *ctx, void *stream, const tfq_decode_layer_weights 
                      uint16_t *hidden_out, uint16_t *k_cache, uint16_t *v_cache, uint32_t position,
                      uint32_t *out_indices, uint16_t *out_weights, void *workspace,
                      size_t workspace_bytes);
+
+/* Workspace bytes of tfq_decode_layers for positions < max_seq_len. */
+size_t tfq_decode_layers_workspace_bytes(const tfq_decode_layer_shape *shapes, uint32_t n_layers,
+                                         uint32_t max_seq_len);
+
+/* n_layers consecutive decoder layers for the token at `position` (the
+ * reference's per-token loop over layers, RealForwardRunner.swift:2239-2862):
+ * layer i's input is hidden_in for i = 0, else layer i-1's output, and
+ * hiddens [n_layers][d] receives every layer's output (row n_layers-1 is the
+ * token's final hidden state). Each layer computes exactly what
+ * tfq_decode_layer computes, but the tail of layer i (its output) is formed
+ * inside layer i+1's first launch, the QKV GEMV, while it stages its input,
+ * so the chain takes n_layers - 1 launches fewer. weights / shapes [n_layers]
+ * (sliding and full-attention layers may alternate; d and eps are shared);
+ * k_caches / v_caches: host arrays of n_layers device pointers. One
+ * workspace of tfq_decode_layers_workspace_bytes serves all layers.
+ * Concurrency as tfq_decode_layer (one caller per context). No reference
+ * counterpart as one call: the reference encodes the same kernels layer by
+ * layer. */
+int tfq_decode_layers(tfq_ctx *ctx, void *stream, uint32_t n_layers,
+                      const tfq_decode_layer_weights *weights, const tfq_decode_layer_shape *shapes,
+                      const uint16_t *hidden_in, uint16_t *hiddens, uint16_t *const *k_caches,
+                      uint16_t *const *v_caches, uint32_t position, void *workspace,
+                      size_t workspace_bytes);
 
 /* ---------------------------------------------------------------- prefill -- */
 

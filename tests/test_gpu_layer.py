@@ -96,15 +96,16 @@ def test_attention_rejects_bad_contract(ctx, stream):
 
 def _layout(shape, seq):
     """Mirror of DecodeLayer::layout (edgeexpert_amd/csrc/host/ops.hpp): 256-byte
-    aligned segments q, attn, parts, o, logits, idx, w, acts, sact, h1, h2,
-    hmid, inv, kv (the staged raw k/v rows)."""
+    aligned segments o, h1, h2, hmid, inv (the vectors a chained layer leaves
+    for the next, first), q, attn, parts, logits, idx, w, acts, sact, kv (the
+    staged raw k/v rows)."""
     up = lambda v: (v + 255) // 256 * 256
     qd = shape["nq"] * shape["hd"]
-    sizes = [("q", qd * 2), ("attn", qd * 2),
+    sizes = [("o", shape["d"] * 2), ("h1", shape["d"] * 2), ("h2", shape["d"] * 2), ("hmid", shape["d"] * 2),
+             ("inv", 4), ("q", qd * 2), ("attn", qd * 2),
              ("parts", ops.Attention.workspace_bytes(shape["hd"], shape["nq"], seq, shape["window"])),
-             ("o", shape["d"] * 2), ("logits", 4096), ("idx", shape["k"] * 4), ("w", shape["k"] * 2),
-             ("acts", shape["k"] * shape["f"] * 2), ("sact", shape["fs"] * 2), ("h1", shape["d"] * 2),
-             ("h2", shape["d"] * 2), ("hmid", shape["d"] * 2), ("inv", 4),
+             ("logits", 4096), ("idx", shape["k"] * 4), ("w", shape["k"] * 2),
+             ("acts", shape["k"] * shape["f"] * 2), ("sact", shape["fs"] * 2),
              ("kv", 2 * shape["nkv"] * shape["hd"] * 2)]
     off, L = 0, {}
     for n, sz in sizes:
@@ -317,3 +318,76 @@ def test_layer_graph_replays_match_eager(ctx, stream):
         g.launch(stream)
         stream.sync()
         assert np.array_equal(ob.download(np.uint16, shape["d"]), eager), f"replay {r}"
+
+
+# ------------------------------------------------------------ layer chains ----
+#
+# tfq_decode_layers: n layers per call, layer i's tail formed inside layer
+# i+1's QKV launch (kStageTail). At d = 256 each thread of the QKV staging
+# owns the same 16-byte chunk as in the tail kernel, so the fused tail's sums
+# are the tail kernel's and the chain equals per-layer calls bit for bit; at
+# the config-4 sizes every layer's output is held to the oracle layer fed the
+# chain's previous output, as the single-layer test holds the end-to-end one.
+
+def _chain_case(ctx, stream, shapes, E, pos, cap, seed, label):
+    ws_list, specs, caches = [], [], []
+    for i, sh in enumerate(shapes):
+        w = synth.decode_layer(seed + i, f"{label}/L{i}", sh["d"], sh["nq"], sh["nkv"], sh["hd"], E, sh["f"], sh["fs"],
+                               v_proj=not sh.get("full", False))
+        kvd = sh["nkv"] * sh["hd"]
+        caches.append((synth.f16_vector(seed + i, f"{label}/L{i}/kc", cap * kvd),
+                       synth.f16_vector(seed + i, f"{label}/L{i}/vc", cap * kvd)))
+        ws_list.append(w)
+        specs.append(_spec(sh))
+    return ws_list, specs, caches
+
+
+def _run_chain(ctx, stream, ws_list, specs, caches, hidden, pos, d):
+    n = len(ws_list)
+    up = [ops.DecodeLayerWeightsSpec.upload(w) for w in ws_list]
+    chain = ops.DecodeLayers(ctx, up, specs)
+    wsb = chain.workspace_bytes(pos + 1)
+    ws = DeviceBuffer(wsb)
+    kb = [_dev(kc) for kc, _ in caches]
+    vb = [_dev(vc) for _, vc in caches]
+    hs = _dev(np.full(n * d, 0x7E00, np.uint16))
+    chain.encode(stream, _dev(hidden), hs, kb, vb, pos, ws, wsb)
+    stream.sync()
+    return from_f16_bits(hs.download(np.uint16, n * d)).reshape(n, d), hs.download(np.uint16, n * d).reshape(n, d)
+
+
+def test_layer_chain_equals_layer_calls_small(ctx, stream):
+    shapes = [SMALL, SMALL_FULL, dict(SMALL, window=64, rotated_pairs=16, theta=1e6)]
+    pos, cap, d = 70, 160, SMALL["d"]
+    ws_list, specs, caches = _chain_case(ctx, stream, shapes, 8, pos, cap, 12, "chain")
+    hidden = synth.f16_vector(12, "chain/hidden", d)
+    print(f"[chain] small 3 layers pos={pos}", flush=True)
+    _, got = _run_chain(ctx, stream, ws_list, specs, caches, hidden, pos, d)
+    h = _dev(hidden)
+    for i, (w, spec, (kc, vc)) in enumerate(zip(ws_list, specs, caches)):
+        layer = ops.DecodeLayer(ctx, ops.DecodeLayerWeightsSpec.upload(w), spec)
+        wsb = ops.decode_layer_workspace_bytes(spec, pos + 1)
+        out = _dev(np.zeros(d, np.uint16))
+        layer.encode(stream, h, out, _dev(kc), _dev(vc), pos, DeviceBuffer(wsb), wsb)
+        stream.sync()
+        ref = out.download(np.uint16, d)
+        assert np.array_equal(got[i], ref), f"layer {i}: {np.count_nonzero(got[i] != ref)} words differ"
+        h = out
+
+
+def test_layer_chain_config4_sliding_and_full(ctx, stream):
+    shapes = [CONFIG4, CONFIG4_FULL]
+    pos, cap, d = 4095, 4096, CONFIG4["d"]
+    ws_list, specs, caches = _chain_case(ctx, stream, shapes, 128, pos, cap, 13, "c4chain")
+    hidden = synth.f16_vector(13, "c4chain/hidden", d)
+    print(f"[chain] config 4 sliding + full pos={pos}", flush=True)
+    outs, _ = _run_chain(ctx, stream, ws_list, specs, caches, hidden, pos, d)
+    inp = hidden
+    for i, (w, sh, (kc, vc)) in enumerate(zip(ws_list, shapes, caches)):
+        ref = from_f16_bits(oracle.decode_layer(w, sh, inp, kc.copy(), vc.copy(), pos)[0])
+        rel = oracle.rel_error(outs[i], ref)
+        floor, trials = chain_floor(w, sh, inp, kc, vc, pos, trials=12)
+        msg = f"chain layer {i}: rel={rel:.4g}, oracle spread {floor:.4g}"
+        print(f"[chain] {msg}", flush=True)
+        assert rel < TOL or rel <= floor, msg
+        inp = synth.f16_bits(outs[i])
