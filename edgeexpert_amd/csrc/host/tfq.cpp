@@ -695,7 +695,9 @@ int tfq_read_ceiling(tfq_ctx* ctx, void* stream, const void* src, uint64_t bytes
     if (!src || !sink || sink_blocks == 0) return fail(TFQ_E_INVAL, "null pointer or empty sink");
     if (!aligned(src, 16) || bytes % 16) return fail(TFQ_E_INVAL, "src and bytes must be 16-byte aligned");
     const uint64_t n16 = bytes / 16;
-    uint64_t blocks = (n16 + 256 * 4 - 1) / (256 * 4);     // one pass: 4 loads per lane
+    // one 16-byte load per lane while the sink allows it (small reads are
+    // latency-bound: the most blocks in flight), else several per lane
+    uint64_t blocks = (n16 + 256 - 1) / 256;
     if (blocks > sink_blocks) blocks = sink_blocks;
     if (blocks < 1) blocks = 1;
     uint32_t grid = (uint32_t)blocks;
