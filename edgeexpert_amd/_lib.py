@@ -13,7 +13,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libtfq.so")
 # the code objects edgeexpert_amd.build writes (one per kernel translation unit)
 CODE_OBJECT_UNITS = ("tfq_gemv", "tfq_int8", "tfq_phase1", "tfq_phase1_routed", "tfq_moe", "tfq_gemm",
-                     "tfq_prefill", "tfq_attention")
+                     "tfq_prefill", "tfq_attention", "tfq_layer_moe")
 CODE_OBJECT_PATHS = [os.path.join(LIB_DIR, u + ".co") for u in CODE_OBJECT_UNITS]
 CODE_OBJECT_PATH = LIB_DIR
 

@@ -23,7 +23,7 @@ ARCH = "gfx950"
 KERNEL_DIR = os.path.join(CSRC, "kernels")
 # one code object per translation unit; libtfq resolves kernels across all of them
 UNITS = ("tfq_gemv", "tfq_int8", "tfq_phase1", "tfq_phase1_routed", "tfq_moe", "tfq_gemm", "tfq_prefill",
-         "tfq_attention")
+         "tfq_attention", "tfq_layer_moe")
 CODE_OBJECTS = [os.path.join(LIB_DIR, u + ".co") for u in UNITS]
 HOST_LIB = os.path.join(LIB_DIR, "libtfq.so")
 

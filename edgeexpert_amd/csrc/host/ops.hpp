@@ -429,6 +429,84 @@ public:
                       args, name);
     }
 
+    // The decoder layer's phase 1 with the int4 shared expert's gate/up/act in
+    // the same launch (moe_phase1_routed_shared): x = h (kStageScaled), the
+    // routed input normed with stage.w, the shared one with shared_norm_w;
+    // the shared expert's act lands in shared_act. 4-bit pools only.
+    int encode_phase1_shared(void* stream, const tfq_expert_pool& pool, const float* logits,
+                             const uint16_t* per_expert_scale, uint32_t num_experts, uint32_t* out_indices,
+                             uint16_t* out_weights, const uint16_t* x, uint16_t* acts, uint32_t d, uint32_t f,
+                             uint32_t top_k, const NormArg& stage, const tfq_q4_matrix& gate,
+                             const tfq_q4_matrix& up, const uint16_t* shared_norm_w, uint16_t* shared_act,
+                             uint32_t fs) const {
+        int rc = check_pool(pool, d, f, top_k);
+        if (rc) return rc;
+        if ((rc = check_stage(stage))) return rc;
+        if (pool_bits(pool) != 4) return fail(TFQ_E_UNSUPPORTED, "the fused shared form takes 4-bit experts");
+        if (stage.mode != kStageScaled) return fail(TFQ_E_INVAL, "the fused shared form stages h scaled by r(h)");
+        if (d > kMaxN) return fail(TFQ_E_UNSUPPORTED, "d=%u exceeds %u", d, kMaxN);
+        if (fs == 0 || fs % 64) return fail(TFQ_E_INVAL, "shared f=%u must be a positive multiple of 64", fs);
+        if (!logits || !out_indices || !out_weights || !x || !acts || !shared_act || !gate.weights || !up.weights ||
+            !gate.scales || !gate.biases || !up.scales || !up.biases)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(gate.weights, 16) || !aligned(up.weights, 16))
+            return fail(TFQ_E_INVAL, "gate/up weights must be 16-byte aligned");
+        if (num_experts != pool.num_experts)
+            return fail(TFQ_E_INVAL, "router has %u experts, pool %u", num_experts, pool.num_experts);
+        if (num_experts > 256 || top_k > num_experts)
+            return fail(TFQ_E_INVAL, "numExperts must be <= 256 and >= topK");
+        ExpertPool kp = kernel_pool(pool);
+        Q4Mat g = {static_cast<const uint8_t*>(gate.weights), gate.scales, gate.biases, nullptr, nullptr, fs, 0};
+        Q4Mat u = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases, nullptr, nullptr, fs, 0};
+        const SegShape sh = seg_shape_fit(d / 32, 2);
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_moe_phase1_shared_s%u_p%u", sh.seg, sh.p);
+        const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
+        hipFunction_t fn = m_.get(name);
+        const uint32_t lds = xpairs_lds_bytes(d);
+        // each part's grid as it would be launched alone
+        uint32_t shared_blocks = grid_for_rows(m_, fn, lds, fs, rows_per_block);
+        const uint32_t routed_blocks = grid_for_rows(m_, fn, lds, (uint64_t)top_k * f, rows_per_block);
+        float* no_wf = nullptr;
+        NormArg na = stage;
+        void* args[] = {&kp,     &logits, &per_expert_scale, &num_experts, &top_k, &out_indices, &out_weights,
+                        &no_wf,  &x,      &acts,             &d,           &f,     &na,          &g,
+                        &u,      &shared_norm_w, &shared_act, &fs,         &shared_blocks};
+        return launch(fn, shared_blocks + routed_blocks, kBlock, lds, stream, args, name);
+    }
+
+    // Phase 2 (no residual) with the int4 shared expert's down GEMV (rows of
+    // fs codes, fs <= 4096) into shared_y in the same launch
+    // (moe_phase2_shared). 4-bit pools only.
+    int encode_phase2_shared(void* stream, const tfq_expert_pool& pool, const uint32_t* indices,
+                             const uint16_t* acts, const uint16_t* routing_weights, uint16_t* y, uint32_t d,
+                             uint32_t f, uint32_t top_k, const tfq_q4_matrix& down, const uint16_t* shared_act,
+                             uint16_t* shared_y, uint32_t fs) const {
+        int rc = check_pool(pool, d, f, top_k);
+        if (rc) return rc;
+        if (pool_bits(pool) != 4) return fail(TFQ_E_UNSUPPORTED, "the fused shared form takes 4-bit experts");
+        if (f > 1024) return fail(TFQ_E_UNSUPPORTED, "phase 2 f=%u exceeds 1024", f);
+        if (fs == 0 || fs % 64 || fs > 4096)
+            return fail(TFQ_E_UNSUPPORTED, "shared f=%u must be a multiple of 64 up to 4096", fs);
+        if (!indices || !acts || !routing_weights || !y || !shared_act || !shared_y || !down.weights ||
+            !down.scales || !down.biases)
+            return fail(TFQ_E_INVAL, "null pointer argument");
+        if (!aligned(down.weights, 16)) return fail(TFQ_E_INVAL, "down weights must be 16-byte aligned");
+        ExpertPool kp = kernel_pool(pool);
+        Q4Mat dn = {static_cast<const uint8_t*>(down.weights), down.scales, down.biases, nullptr, nullptr, d, 0};
+        const uint32_t p2 = ((f / 32) + 7) / 8;
+        const uint32_t sp = ((fs / 32) + 31) / 32;
+        char name[64];
+        std::snprintf(name, sizeof(name), "tfq_moe_phase2_shared_p%u_sp%u", p2, sp);
+        hipFunction_t fn = m_.get(name);
+        const uint32_t lds = std::max(xpairs_lds_bytes(top_k * f), xpairs_lds_bytes(fs));
+        uint32_t shared_blocks = grid_for_rows(m_, fn, lds, d, (kBlock / 64) * 2 * kRowsInFlight);
+        const uint32_t routed_blocks = grid_for_rows(m_, fn, lds, d, (kBlock / 64) * kRowsInFlight);
+        void* args[] = {&kp, &indices, &acts, &routing_weights, &y, &d, &f, &top_k, &dn, &shared_act, &shared_y,
+                        &fs, &shared_blocks};
+        return launch(fn, shared_blocks + routed_blocks, kBlock, lds, stream, args, name);
+    }
+
 private:
     // Kernel-name infix of the pool's code width: "" (4 bits), "b2_", "b3_".
     static const char* bits_infix(const tfq_expert_pool& pool) {
@@ -936,22 +1014,23 @@ private:
 
 // One Gemma 4 decoder layer for one token (RealForwardRunner.swift:2265-2862):
 // input norm + QKV, q/k/v epilogue + attention, o projection, post-attention
-// setup, router, shared expert (on a second stream), routed experts, tail.
-// The norms that the reference runs as separate kernels are formed while
-// each consumer stages its activation vector (NormArg); the router also
-// stores the post-attention h and r(h), from which the routed experts form
-// their input without the reductions. Eight launches on `stream`, two on the
-// side stream.
+// setup, router, shared expert, routed experts, tail. The norms that the
+// reference runs as separate kernels are formed while each consumer stages
+// its activation vector (NormArg); the router also stores the post-attention
+// h and r(h), from which the expert launches form their inputs without the
+// reductions. Every launch is on `stream`, in order: with the int4 shared
+// expert and 4-bit routed experts its gate/up/act and down run inside the
+// routed phase 1 and phase 2 launches (7 launches per layer); otherwise as
+// two launches of their own before the router (9). Measured at config 4
+// (graph replay): the shared expert on a second stream, concurrent with the
+// router and the routed experts, took 66.0 µs per layer against 58.7 µs with
+// its two launches in order on the one stream (the concurrent kernels slow
+// each other more than the overlap gains).
 class DecodeLayer {
 public:
     DecodeLayer(const Module& m, DequantInt4GEMV& gemv, MoE& moe, SharedExpertInt4& shared,
                 SharedExpertInt8& shared8, Attention& attn)
         : m_(m), gemv_(gemv), moe_(moe), shared_(shared), shared8_(shared8), attn_(attn) {}
-    ~DecodeLayer() {
-        if (fork_) (void)hipEventDestroy(fork_);
-        if (join_) (void)hipEventDestroy(join_);
-        if (side_) (void)hipStreamDestroy(side_);
-    }
 
     // Segments of the workspace, 256-byte aligned. The d-sized vectors that
     // one layer leaves for the next in a chain (o, h1, h2) come first, so
@@ -993,7 +1072,6 @@ public:
             if (!aligned(p, 16)) return fail(TFQ_E_INVAL, "hidden vectors and norm weights must be 16-byte aligned");
         const Layout L = layout(s, position + 1);
         if (workspace_bytes < L.total) return fail(TFQ_E_INVAL, "decode-layer workspace too small");
-        if (int rc = ensure_side_stream()) return rc;
         const NormArg in_norm{w.input_norm, nullptr, nullptr, s.eps, kStageNorm};
         if (int rc = body(stream, w, s, hidden_in, in_norm, hidden_in, k_cache, v_cache, position, out_indices,
                           out_weights, static_cast<char*>(workspace), L))
@@ -1025,7 +1103,6 @@ public:
             need = std::max(need, layout(s[i], position + 1).total);
         }
         if (workspace_bytes < need) return fail(TFQ_E_INVAL, "decode-layer workspace too small");
-        if (int rc = ensure_side_stream()) return rc;
         char* ws = static_cast<char*>(workspace);
         const size_t d = s[0].d;
         for (uint32_t i = 0; i < n; ++i) {
@@ -1058,17 +1135,6 @@ public:
         return need;
     }
 
-    // Creates the side stream and its fork/join events (tfq_create calls it,
-    // so that no stream is created while the caller captures a graph).
-    int ensure_side_stream() {
-        if (side_) return TFQ_OK;
-        int rc = hip_check(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking), "hipStreamCreate");
-        if (rc) return rc;
-        rc = hip_check(hipEventCreateWithFlags(&fork_, hipEventDisableTiming), "hipEventCreate");
-        if (rc) return rc;
-        return hip_check(hipEventCreateWithFlags(&join_, hipEventDisableTiming), "hipEventCreate");
-    }
-
     // Contract checks shared by encode and encode_chain.
     int check_layer(const tfq_decode_layer_weights& w, const tfq_decode_layer_shape& s, const uint16_t* k_cache,
                     const uint16_t* v_cache, const void* workspace) const {
@@ -1092,8 +1158,7 @@ public:
     // Steps 1-6 of one layer (everything but the tail): the QKV GEMV stages
     // x as `qkv_stage` says (the input norm of `hidden`, or the previous
     // layer's tail followed by it); `hidden` is the layer's input, used by
-    // the post-attention residual. Ends with `stream` waiting for the
-    // shared expert's side stream.
+    // the post-attention residual.
     int body(void* stream, const tfq_decode_layer_weights& w, const tfq_decode_layer_shape& s, const uint16_t* x,
              const NormArg& qkv_stage, const uint16_t* hidden, uint16_t* k_cache, uint16_t* v_cache,
              uint32_t position, uint32_t* out_indices, uint16_t* out_weights, char* ws, const Layout& L) {
@@ -1137,21 +1202,19 @@ public:
         // 3. o projection
         rc = gemv_.encode(stream, w.o_proj.weights, w.o_proj.scales, w.o_proj.biases, attn, o, s.d, qd);
         if (rc) return rc;
-        // 4. shared expert on the side stream, input = pre_feedforward_layernorm(h)
-        rc = hip_check(hipEventRecord(fork_, (hipStream_t)stream), "hipEventRecord");
-        if (rc) return rc;
-        rc = hip_check(hipStreamWaitEvent(side_, fork_, 0), "hipStreamWaitEvent");
-        if (rc) return rc;
-        const NormArg dense{w.pre_ffn_norm, o, w.post_attention_norm, s.eps, kStagePostAttn};
-        rc = shared_bits == 8 ? shared8_.encode(side_, hidden, w.shared_gate, w.shared_up, w.shared_down, h1,
-                                                s.d, s.shared_f, sact, dense)
-                              : shared_.encode(side_, hidden, w.shared_gate, w.shared_up, w.shared_down, h1,
-                                               s.d, s.shared_f, sact, dense);
-        if (rc) return rc;
-        rc = hip_check(hipEventRecord(join_, side_), "hipEventRecord");
-        if (rc) return rc;
+        // 4. shared expert, input = pre_feedforward_layernorm(h): inside the
+        //    routed launches (fused), or here from the layer input and o
+        const bool fused = shared_bits == 4 && pool_bits(w.experts) == 4 && s.shared_f <= 4096;
+        if (!fused) {
+            const NormArg dense{w.pre_ffn_norm, o, w.post_attention_norm, s.eps, kStagePostAttn};
+            rc = shared_bits == 8 ? shared8_.encode(stream, hidden, w.shared_gate, w.shared_up, w.shared_down, h1,
+                                                    s.d, s.shared_f, sact, dense)
+                                  : shared_.encode(stream, hidden, w.shared_gate, w.shared_up, w.shared_down, h1,
+                                                   s.d, s.shared_f, sact, dense);
+            if (rc) return rc;
+        }
         // 5. router on the no-scale norm of h; its block 0 also stores h and
-        //    r(h), so the routed experts form their input without the reductions
+        //    r(h), so the expert launches form their inputs without the reductions
         const NormArg router_x{nullptr, o, w.post_attention_norm, s.eps, kStagePostAttn, nullptr, hmid, hinv};
         const tfq_router& r = w.router;
         float* logits_used = nullptr;
@@ -1161,12 +1224,18 @@ public:
         // 6. routed experts on pre_feedforward_layernorm_2(h), the top-k selected inside
         //    phase 1; phase 2 without residual
         const NormArg routed{w.pre_ffn2_norm, nullptr, nullptr, s.eps, kStageScaled, hinv, nullptr, nullptr};
+        if (fused) {
+            rc = moe_.encode_phase1_shared(stream, w.experts, logits, r.per_expert_scale, r.num_experts, idx, rw,
+                                           hmid, acts, s.d, s.expert_f, s.top_k, routed, w.shared_gate,
+                                           w.shared_up, w.pre_ffn_norm, sact, s.shared_f);
+            if (rc) return rc;
+            return moe_.encode_phase2_shared(stream, w.experts, idx, acts, rw, h2, s.d, s.expert_f, s.top_k,
+                                             w.shared_down, sact, h1, s.shared_f);
+        }
         rc = moe_.encode_phase1_routed(stream, w.experts, logits, r.per_expert_scale, r.num_experts, idx, rw,
                                        nullptr, hmid, acts, s.d, s.expert_f, s.top_k, routed);
         if (rc) return rc;
-        rc = moe_.encode_phase2(stream, w.experts, idx, acts, rw, nullptr, h2, s.d, s.expert_f, s.top_k);
-        if (rc) return rc;
-        return hip_check(hipStreamWaitEvent((hipStream_t)stream, join_, 0), "hipStreamWaitEvent");
+        return moe_.encode_phase2(stream, w.experts, idx, acts, rw, nullptr, h2, s.d, s.expert_f, s.top_k);
     }
 
     // 7. the tail kernel: out from the layer's input `hidden` and its o, h1, h2.
@@ -1190,8 +1259,6 @@ private:
     SharedExpertInt4& shared_;
     SharedExpertInt8& shared8_;
     Attention& attn_;
-    hipStream_t side_ = nullptr;
-    hipEvent_t fork_ = nullptr, join_ = nullptr;
 };
 
 }  // namespace tfq

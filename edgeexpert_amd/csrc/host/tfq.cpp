@@ -39,6 +39,7 @@ static std::vector<std::string> kernel_names() {
                 names.push_back(std::string("tfq_moe_phase1_") + b + form + s);
                 names.push_back(std::string("tfq_moe_phase1_routed_") + b + form + s);
             }
+            if (*form) names.push_back(std::string("tfq_moe_phase1_shared_") + s);
             names.push_back(std::string("tfq_gate_up_act_") + form + s);
         }
     for (const char* s : q4_shapes) names.push_back(std::string("tfq_lm_head_greedy_") + s);
@@ -50,8 +51,11 @@ static std::vector<std::string> kernel_names() {
         names.push_back(std::string("tfq_router_logits_") + s);
         names.push_back(std::string("tfq_prefill_router_logits_") + s);
     }
-    for (int p = 1; p <= 4; ++p)
+    for (int p = 1; p <= 4; ++p) {
         for (const char* b : {"", "b2_", "b3_"}) names.push_back(std::string("tfq_moe_phase2_") + b + "p" + std::to_string(p));
+        for (int sp = 1; sp <= 4; ++sp)
+            names.push_back("tfq_moe_phase2_shared_p" + std::to_string(p) + "_sp" + std::to_string(sp));
+    }
     names.push_back("tfq_router_select");
     names.push_back("tfq_read_ceiling");
     names.push_back("tfq_gelu_mul_f16");
@@ -79,8 +83,9 @@ static std::vector<std::string> kernel_names() {
 }
 
 // The code objects edgeexpert_amd/build.py writes next to libtfq.so.
-static const char* const kCodeObjects[] = {"tfq_gemv",  "tfq_int8", "tfq_phase1",  "tfq_phase1_routed",
-                                           "tfq_moe",   "tfq_gemm", "tfq_prefill", "tfq_attention"};
+static const char* const kCodeObjects[] = {"tfq_gemv", "tfq_int8",    "tfq_phase1",    "tfq_phase1_routed",
+                                           "tfq_moe",  "tfq_gemm",    "tfq_prefill",   "tfq_attention",
+                                           "tfq_layer_moe"};
 
 int Module::load(const std::string& dir) {
     int rc = hip_check(hipGetDevice(&device_), "hipGetDevice");
@@ -214,11 +219,6 @@ int tfq_create(tfq_ctx** out, const char* code_object_path) {
     c->grouped = new PrefillGroupedRoutedMoE(c->module);
     c->attn = new Attention(c->module);
     c->layer = new DecodeLayer(c->module, *c->int4, *c->moe, *c->shared, *c->shared8, *c->attn);
-    rc = c->layer->ensure_side_stream();
-    if (rc) {
-        delete c;
-        return rc;
-    }
     // the allocation-free entry point's scratch on this device; a failure is
     // reported by that entry point, not by the context
     c->scratch_status = noalloc_scratch_address(&c->scratch);

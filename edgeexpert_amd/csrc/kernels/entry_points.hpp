@@ -121,7 +121,7 @@ constexpr uint32_t kTailGemvThreads = 1024;
         uint32_t D, uint32_t F, NormArg norm) {                                                   \
         moe_phase1_routed<SEG, P, kRowsInFlight, NORM, BITS>(pool, logits, gain, E, top_k,       \
                                                              out_idx, out_w, out_wf, x, acts, D, \
-                                                             F, norm);                            \
+                                                             F, norm, blockIdx.x, gridDim.x);     \
     }
 #define TFQ_PHASE1_ROUTED(SEG, P)                                                                \
     TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_s##SEG##_p##P, false, 4, SEG, P)                \
@@ -136,12 +136,39 @@ constexpr uint32_t kTailGemvThreads = 1024;
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         ExpertPool pool, const uint32_t* indices, const uint16_t* acts, const uint16_t* rw,      \
         const uint16_t* residual, uint16_t* y, uint32_t D, uint32_t F, uint32_t top_k) {         \
-        moe_phase2<P, kRowsInFlight, BITS>(pool, indices, acts, rw, residual, y, D, F, top_k);    \
+        moe_phase2<P, kRowsInFlight, BITS>(pool, indices, acts, rw, residual, y, D, F, top_k,     \
+                                           blockIdx.x, gridDim.x);                                \
     }
 #define TFQ_PHASE2(P)                                                                            \
     TFQ_PHASE2_FORM(tfq_moe_phase2_p##P, 4, P)                                                   \
     TFQ_PHASE2_FORM(tfq_moe_phase2_b2_p##P, 2, P)                                                \
     TFQ_PHASE2_FORM(tfq_moe_phase2_b3_p##P, 3, P)
+
+#define TFQ_PHASE1_SHARED_FORM(NAME, BITS, SEG, P)                                               \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
+        ExpertPool pool, const float* logits, const uint16_t* gain, uint32_t E, uint32_t top_k,  \
+        uint32_t* out_idx, uint16_t* out_w, float* out_wf, const uint16_t* x, uint16_t* acts,    \
+        uint32_t D, uint32_t F, NormArg norm, Q4Mat sgate, Q4Mat sup, const uint16_t* snorm_w,   \
+        uint16_t* sact, uint32_t Fs, uint32_t shared_blocks) {                                    \
+        moe_phase1_routed_shared<SEG, P, kRowsInFlight, BITS>(pool, logits, gain, E, top_k,      \
+                                                              out_idx, out_w, out_wf, x, acts,   \
+                                                              D, F, norm, sgate, sup, snorm_w,   \
+                                                              sact, Fs, shared_blocks);          \
+    }
+#define TFQ_PHASE1_SHARED(SEG, P) TFQ_PHASE1_SHARED_FORM(tfq_moe_phase1_shared_s##SEG##_p##P, 4, SEG, P)
+
+#define TFQ_PHASE2_SHARED_FORM(NAME, BITS, P2, SP)                                               \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
+        ExpertPool pool, const uint32_t* indices, const uint16_t* acts, const uint16_t* rw,      \
+        uint16_t* y, uint32_t D, uint32_t F, uint32_t top_k, Q4Mat sdown, const uint16_t* sact,  \
+        uint16_t* sy, uint32_t Fs, uint32_t shared_blocks) {                                      \
+        moe_phase2_shared<P2, SP, kRowsInFlight, BITS>(pool, indices, acts, rw, y, D, F, top_k,  \
+                                                       sdown, sact, sy, Fs, shared_blocks);       \
+    }
+#define TFQ_PHASE2_SHARED_SP(P2, SP) TFQ_PHASE2_SHARED_FORM(tfq_moe_phase2_shared_p##P2##_sp##SP, 4, P2, SP)
+#define TFQ_PHASE2_SHARED(P2)                                                                    \
+    TFQ_PHASE2_SHARED_SP(P2, 1) TFQ_PHASE2_SHARED_SP(P2, 2) TFQ_PHASE2_SHARED_SP(P2, 3)          \
+    TFQ_PHASE2_SHARED_SP(P2, 4)
 
 #define TFQ_LM_HEAD(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_lm_head_greedy_s##SEG##_p##P(          \
@@ -153,7 +180,8 @@ constexpr uint32_t kTailGemvThreads = 1024;
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         Q4Mat gate, Q4Mat up, const uint16_t* x, uint16_t* act, uint32_t D, uint32_t F,          \
         NormArg norm) {                                                                           \
-        q4_gate_up_act<SEG, P, kRowsInFlight, NORM>(gate, up, x, act, D, F, norm);                \
+        q4_gate_up_act<SEG, P, kRowsInFlight, NORM>(gate, up, x, act, D, F, norm, blockIdx.x,     \
+                                                    gridDim.x);                                   \
     }
 #define TFQ_GATE_UP(SEG, P)                                                                      \
     TFQ_GATE_UP_FORM(tfq_gate_up_act_s##SEG##_p##P, false, SEG, P)                               \

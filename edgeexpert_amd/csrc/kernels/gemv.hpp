@@ -67,10 +67,13 @@ __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, 
 // NT: threads per block (256; 1024 for the tail form, whose staging reads
 // nine vectors: a quarter of the blocks, each staging once for four times
 // the rows, keeps that L2 traffic to a quarter).
+// blk / nblk: this block's index among the blocks that share the rows, and
+// their count (blockIdx.x / gridDim.x unless a launch splits its blocks
+// between two kinds of work).
 template <int SEG, int P, int R, bool NORM, bool STAGE_FIRST = false, int BITS = 4, bool TAIL = false,
           uint32_t NT = kThreads, typename Out>
 __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __restrict__ x, uint32_t n,
-                                        Out out) {
+                                        Out out, uint32_t blk, uint32_t nblk) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
     constexpr uint32_t CH = NT >= 512 ? 1 : kStageChunks;       // staged 16-byte chunks per thread
     const uint32_t lane = threadIdx.x & 63u;
@@ -81,8 +84,8 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
     const uint32_t row_bytes = (n >> 3) * BITS;
     const uint32_t ngroups = n >> 6;
     constexpr uint32_t spw = kWave / SEG;     // segments per wave
-    const uint32_t seg_id = (blockIdx.x * nwaves + wave) * spw + lane / SEG;
-    const uint32_t seg_total = gridDim.x * nwaves * spw;
+    const uint32_t seg_id = (blk * nwaves + wave) * spw + lane / SEG;
+    const uint32_t seg_total = nblk * nwaves * spw;
     const uint32_t total = mats.total_rows;
 
     QChunk<BITS> wv[R][P];
@@ -154,7 +157,7 @@ __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_
         const Q4Row q = resolve_row(mats, row, row_bytes, ngroups);
         const float o = q.r ? h2f(*q.r) + v : v;
         *q.y = out_bf16 ? __builtin_bit_cast(uint16_t, (__bf16)o) : f2h(o);
-    });
+    }, blockIdx.x, gridDim.x);
 }
 
 // ---------------------------------------------------------------- int8 ----
@@ -371,7 +374,7 @@ __device__ __forceinline__ void lm_head_greedy_rows(const Q4Multi& mats, const u
             best_v = v;
             best_row = row;
         }
-    });
+    }, blockIdx.x, gridDim.x);
     uint64_t best = best_row == 0xFFFFFFFFu ? 0ull : topk_key(best_v, best_row);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {

@@ -47,10 +47,12 @@ struct GateUpRow {
 // prologue waits for loads issued after x (expert indices, logits), so x has
 // arrived when it ends; staging it before the weight loads then keeps the
 // staging off the stall a wave takes while the memory pipeline backs up
-// under them.
+// under them. blk / nblk: this block's index among the blocks that share
+// the rows, and their count (q4_rows).
 template <int SEG, int P, int R, bool NORM, int BITS, bool X_FIRST, typename Pro, typename RowFn, typename OutFn>
 __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uint32_t D, uint32_t total,
-                                             const NormArg& norm, Pro prologue, RowFn rowfn, OutFn out) {
+                                             const NormArg& norm, Pro prologue, RowFn rowfn, OutFn out,
+                                             uint32_t blk, uint32_t nblk) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
     constexpr uint32_t NT = kThreads;
     const uint32_t lane = threadIdx.x & 63u;
@@ -59,8 +61,8 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
     const uint32_t sl = lane & (SEG - 1);
     const uint32_t lpr = D >> 5;
     constexpr uint32_t spw = kWave / SEG;
-    const uint32_t seg_id = (blockIdx.x * nwaves + wave) * spw + lane / SEG;
-    const uint32_t seg_total = gridDim.x * nwaves * spw;
+    const uint32_t seg_id = (blk * nwaves + wave) * spw + lane / SEG;
+    const uint32_t seg_total = nblk * nwaves * spw;
 
     QChunk<BITS> gv[R][P], uv[R][P];
     uint32_t gsr[R][P], gbr[R][P], usr[R][P], ubr[R][P];    // raw fp16 scales / biases
@@ -180,7 +182,8 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
             const uint32_t a = row / F;
             return expert_gate_up_row<BITS>(pool, act_slot[a], act_expert[a], row % F, top_k, D);
         },
-        [&](uint32_t row, float act) { acts[(size_t)act_slot[row / F] * F + row % F] = f2h(act); });
+        [&](uint32_t row, float act) { acts[(size_t)act_slot[row / F] * F + row % F] = f2h(act); },
+        blockIdx.x, gridDim.x);
 }
 
 // Phase 1 with the router's selection folded in: every block selects the
@@ -188,14 +191,15 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
 // block), so routing costs no launch of its own between the router GEMV and
 // the experts. Block 0 publishes indices and fp16 / fp32 weights for
 // phase 2 and the caller (MoE.encodeRouterGemma4's outputs,
-// S/Kernels/MoE/MoE.swift:147-197).
+// S/Kernels/MoE/MoE.swift:147-197). blk / nblk as in gate_up_rows (blk 0
+// publishes).
 template <int SEG, int P, int R, bool NORM, int BITS = 4>
 __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const float* __restrict__ logits,
                                                   const uint16_t* __restrict__ gain, uint32_t E, uint32_t top_k,
                                                   uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w,
                                                   float* __restrict__ out_wf, const uint16_t* __restrict__ x,
                                                   uint16_t* __restrict__ acts, uint32_t D, uint32_t F,
-                                                  const NormArg& norm) {
+                                                  const NormArg& norm, uint32_t blk, uint32_t nblk) {
     __shared__ __attribute__((aligned(16))) float stage[kRouterMaxExperts];
     __shared__ uint32_t sel_idx[kRouterMaxTopK];
     __shared__ float sel_val[kRouterMaxTopK];
@@ -208,7 +212,7 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
             block_topk(stage, E, top_k, sel_idx, sel_val);
             // phase 1 needs only the indices; the routing weights (for
             // phase 2) are formed by block 0 alone
-            if (blockIdx.x == 0) {
+            if (blk == 0) {
                 __shared__ float ex[kRouterMaxTopK];
                 __shared__ float sel_w[kRouterMaxTopK];
                 block_softmax_gain(sel_idx, sel_val, top_k, gain, ex, sel_w);
@@ -222,7 +226,7 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
         [&](uint32_t row) {
             return expert_gate_up_row<BITS>(pool, row / F, sel_idx[row / F], row % F, top_k, D);
         },
-        [&](uint32_t row, float act) { acts[(size_t)(row / F) * F + row % F] = f2h(act); });
+        [&](uint32_t row, float act) { acts[(size_t)(row / F) * F + row % F] = f2h(act); }, blk, nblk);
 }
 
 // Shared-expert gate/up/act, int4 rows: act[i] = fp16(gelu(g)·u), g =
@@ -232,7 +236,8 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
 template <int SEG, int P, int R, bool NORM>
 __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& up,
                                                const uint16_t* __restrict__ x, uint16_t* __restrict__ act,
-                                               uint32_t D, uint32_t F, const NormArg& norm) {
+                                               uint32_t D, uint32_t F, const NormArg& norm, uint32_t blk,
+                                               uint32_t nblk) {
     const uint32_t row_bytes = D >> 1;
     const uint32_t ngroups = D >> 6;
     gate_up_rows<SEG, P, R, NORM, 4, false>(
@@ -249,7 +254,7 @@ __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& u
             q.ub = up.b + (size_t)f * ngroups;
             return q;
         },
-        [&](uint32_t f, float a) { act[f] = f2h(a); });
+        [&](uint32_t f, float a) { act[f] = f2h(a); }, blk, nblk);
 }
 
 // Shared-expert gate/up/act, int8 rows (shared_int8_gate_up_act_simd,
@@ -365,13 +370,14 @@ constexpr uint32_t kPhase2Chunks = 4;     // 16-byte act pieces per thread: top_
 // Phase 2: 8 slots × 8-lane segments per wave; P chunks of 32 per lane
 // (F <= 256*P); R output rows per wave in flight. Dynamic LDS:
 // xpairs_lds_bytes(top_k*F). BITS: code width of the down rows.
+// blk / nblk as in gate_up_rows.
 template <int P, int R, int BITS = 4>
 __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint16_t* __restrict__ acts,
                                            const uint16_t* __restrict__ rw,
                                            const uint16_t* __restrict__ residual,
                                            uint16_t* __restrict__ y, uint32_t D, uint32_t F,
-                                           uint32_t top_k) {
+                                           uint32_t top_k, uint32_t blk, uint32_t nblk) {
     constexpr int SEG = 8;
     constexpr uint32_t NT = kThreads;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_a[];
@@ -384,8 +390,8 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
     const uint32_t row_bytes = (F >> 3) * BITS;
     const uint32_t ngroups = F >> 6;
     const bool live = slot < top_k;
-    const uint32_t wave_id = blockIdx.x * nwaves + wave;
-    const uint32_t wave_total = gridDim.x * nwaves;
+    const uint32_t wave_id = blk * nwaves + wave;
+    const uint32_t wave_total = nblk * nwaves;
     const uint32_t n_acts = top_k * F;
 
     // independent loads first: the activations, the slot's expert index and
@@ -473,6 +479,56 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
                 if (lane == 0) y[d] = f2h(out);
             }
         }
+    }
+}
+
+// The decoder layer's feed-forward launches with the int4 shared expert
+// folded in. Each launch splits its blocks: [0, shared_blocks) compute the
+// shared expert's part, the rest the routed experts' part (the same work as
+// moe_phase1_routed / moe_phase2 launched alone). The shared blocks depend on
+// nothing the routed blocks compute, so their weight stream runs while the
+// routed blocks select their experts (phase 1) or read the indices (phase 2).
+//
+// Phase 1 + shared gate/up/act: the shared expert's input is h's RMSNorm with
+// its own weight (pre_feedforward_layernorm), formed from the h and r(h) that
+// the router's block 0 exported — `norm` (kStageScaled) with w = snorm_w.
+template <int SEG, int P, int R, int BITS>
+__device__ __forceinline__ void moe_phase1_routed_shared(
+    const ExpertPool& pool, const float* __restrict__ logits, const uint16_t* __restrict__ gain, uint32_t E,
+    uint32_t top_k, uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w, float* __restrict__ out_wf,
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ acts, uint32_t D, uint32_t F, const NormArg& norm,
+    const Q4Mat& sgate, const Q4Mat& sup, const uint16_t* __restrict__ snorm_w, uint16_t* __restrict__ sact,
+    uint32_t Fs, uint32_t shared_blocks) {
+    if (blockIdx.x < shared_blocks) {
+        NormArg ns = norm;
+        ns.w = snorm_w;
+        q4_gate_up_act<SEG, P, R, true>(sgate, sup, x, sact, D, Fs, ns, blockIdx.x, shared_blocks);
+    } else {
+        moe_phase1_routed<SEG, P, R, true, BITS>(pool, logits, gain, E, top_k, out_idx, out_w, out_wf, x, acts, D,
+                                                 F, norm, blockIdx.x - shared_blocks, gridDim.x - shared_blocks);
+    }
+}
+
+// Phase 2 + the shared expert's down GEMV (rows of Fs codes, 32-lane
+// segments, SP chunks per lane: Fs <= 1024·SP) into sy. Dynamic LDS: the
+// larger of phase 2's and the GEMV's.
+template <int P2, int SP, int R, int BITS>
+__device__ __forceinline__ void moe_phase2_shared(const ExpertPool& pool, const uint32_t* __restrict__ indices,
+                                                  const uint16_t* __restrict__ acts, const uint16_t* __restrict__ rw,
+                                                  uint16_t* __restrict__ y, uint32_t D, uint32_t F, uint32_t top_k,
+                                                  const Q4Mat& sdown, const uint16_t* __restrict__ sact,
+                                                  uint16_t* __restrict__ sy, uint32_t Fs, uint32_t shared_blocks) {
+    if (blockIdx.x < shared_blocks) {
+        Q4Multi mats{};
+        mats.m[0] = {sdown.w, sdown.s, sdown.b, sy, nullptr, D, 0};
+        mats.nmat = 1;
+        mats.total_rows = D;
+        mats.norm = NormArg{nullptr, nullptr, nullptr, 0.0f, kStageCopy};
+        q4_rows<32, SP, R, false>(mats, sact, Fs, [&](uint32_t row, float v) { sy[row] = f2h(v); }, blockIdx.x,
+                                  shared_blocks);
+    } else {
+        moe_phase2<P2, R, BITS>(pool, indices, acts, rw, nullptr, y, D, F, top_k, blockIdx.x - shared_blocks,
+                                gridDim.x - shared_blocks);
     }
 }
 

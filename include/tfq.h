@@ -25,11 +25,9 @@
  *    HIP call returns TFQ_E_HIP and its code is kept for tfq_last_hip_error().
  *    Nothing aborts the process.
  *  - A context is immutable after tfq_create and may be shared by threads
- *    that use distinct streams, with one exception: tfq_decode_layer runs its
- *    shared expert on a side stream and fork/join events that the context
- *    owns, so decode-layer calls on one context must not overlap (use one
- *    context per concurrent caller). Calls that take a `workspace` must not
- *    run concurrently with another call using the same workspace.
+ *    that use distinct streams: every call runs on the caller's stream alone.
+ *    Calls that take a `workspace` must not run concurrently with another
+ *    call using the same workspace.
  *  - ABI versions (TFQ_ABI_VERSION, tfq_abi_version()): a binding built
  *    against one version must check the library's at load time. Version 2
  *    widened the grouping state of tfq_moe_group / tfq_moe_grouped from 1 to
@@ -194,7 +192,7 @@ typedef struct {
  * a row of n codes takes n*bits/8 bytes, codes packed from the least
  * significant bit (Quantization.swift:195-201). The decode
  * and grouped prefill entry points run every width.
- * Contract: base, stride and the *_w offsets 16-byte aligned; *_s/*_b
+ * Contract: base, stride and the *_w offsets 16-byte aligned; *_s and *_b
  * offsets 2-byte aligned. */
 typedef struct {
     const void *base;
@@ -393,9 +391,11 @@ size_t tfq_decode_layer_workspace_bytes(const tfq_decode_layer_shape *shape, uin
  *   router on rmsnorm(h) (no scale) -> top_k experts and weights
  *   h1 = shared(rmsnorm(h, pre_ffn_norm));  h2 = Σ w·expert(rmsnorm(h, pre_ffn2_norm))
  *   out = (h + rmsnorm(rmsnorm(h1, post_ffn1) + rmsnorm(h2, post_ffn2), post_ffn)) * layer_scalar
- * with fp16 rounding wherever the reference stores a buffer. The shared
- * expert runs on a second stream of the context (fork/join by events, so the
- * call can be captured into a graph); concurrent calls on one context race.
+ * with fp16 rounding wherever the reference stores a buffer. Every launch
+ * runs on `stream`, in order (the call can be captured into a graph); with
+ * the int4 shared expert (shared_f <= 4096) and 4-bit routed experts the
+ * shared expert's gate/up/act and down run inside the routed phase-1 and
+ * phase-2 launches, its input normed from the h and r(h) the router stores.
  * hidden_out may alias hidden_in. out_indices/out_weights (may be NULL)
  * receive the routing. Replaces the per-layer decode sequence of
  * RealForwardRunner (S/Runtime/Inference/RealForwardRunner.swift:2265-2862:
