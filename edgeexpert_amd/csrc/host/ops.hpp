@@ -429,22 +429,25 @@ public:
                       args, name);
     }
 
-    // The decoder layer's phase 1 with the int4 shared expert's gate/up/act in
-    // the same launch (moe_phase1_routed_shared): x = h (kStageScaled), the
-    // routed input normed with stage.w, the shared one with shared_norm_w;
-    // the shared expert's act lands in shared_act. 4-bit pools only.
+    // The decoder layer's phase 1 with the shared expert's gate/up/act in the
+    // same launch (moe_phase1_routed_shared / _shared8): x = h (kStageScaled),
+    // the routed input normed with stage.w, the shared one with
+    // shared_norm_w; the shared expert's act lands in shared_act.
+    // shared_bits 4 or 8; 4-bit pools only.
     int encode_phase1_shared(void* stream, const tfq_expert_pool& pool, const float* logits,
                              const uint16_t* per_expert_scale, uint32_t num_experts, uint32_t* out_indices,
                              uint16_t* out_weights, const uint16_t* x, uint16_t* acts, uint32_t d, uint32_t f,
                              uint32_t top_k, const NormArg& stage, const tfq_q4_matrix& gate,
                              const tfq_q4_matrix& up, const uint16_t* shared_norm_w, uint16_t* shared_act,
-                             uint32_t fs) const {
+                             uint32_t fs, uint32_t shared_bits) const {
         int rc = check_pool(pool, d, f, top_k);
         if (rc) return rc;
         if ((rc = check_stage(stage))) return rc;
         if (pool_bits(pool) != 4) return fail(TFQ_E_UNSUPPORTED, "the fused shared form takes 4-bit experts");
         if (stage.mode != kStageScaled) return fail(TFQ_E_INVAL, "the fused shared form stages h scaled by r(h)");
-        if (d > kMaxN) return fail(TFQ_E_UNSUPPORTED, "d=%u exceeds %u", d, kMaxN);
+        if (shared_bits != 4 && shared_bits != 8)
+            return fail(TFQ_E_INVAL, "SharedExpert unsupported weight bits: %u", shared_bits);
+        if (d > (shared_bits == 8 ? 4096u : kMaxN)) return fail(TFQ_E_UNSUPPORTED, "d=%u too large", d);
         if (fs == 0 || fs % 64) return fail(TFQ_E_INVAL, "shared f=%u must be a positive multiple of 64", fs);
         if (!logits || !out_indices || !out_weights || !x || !acts || !shared_act || !gate.weights || !up.weights ||
             !gate.scales || !gate.biases || !up.scales || !up.biases)
@@ -456,35 +459,47 @@ public:
         if (num_experts > 256 || top_k > num_experts)
             return fail(TFQ_E_INVAL, "numExperts must be <= 256 and >= topK");
         ExpertPool kp = kernel_pool(pool);
-        Q4Mat g = {static_cast<const uint8_t*>(gate.weights), gate.scales, gate.biases, nullptr, nullptr, fs, 0};
-        Q4Mat u = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases, nullptr, nullptr, fs, 0};
         const SegShape sh = seg_shape_fit(d / 32, 2);
+        const SegShape s8 = seg_shape(d / 16, 4);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_moe_phase1_shared_s%u_p%u", sh.seg, sh.p);
+        if (shared_bits == 8)
+            std::snprintf(name, sizeof(name), "tfq_moe_phase1_shared8_s%u_p%u_q%u_%u", sh.seg, sh.p, s8.seg, s8.p);
+        else
+            std::snprintf(name, sizeof(name), "tfq_moe_phase1_shared_s%u_p%u", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
+        const uint32_t shared_rows_per_block =
+            (kBlock / 64) * (64 / (shared_bits == 8 ? s8.seg : sh.seg)) * kRowsInFlight;
         hipFunction_t fn = m_.get(name);
-        const uint32_t lds = xpairs_lds_bytes(d);
+        const uint32_t lds = std::max(xpairs_lds_bytes(d), shared_bits == 8 ? d * 6 : 0u);
         // each part's grid as it would be launched alone
-        uint32_t shared_blocks = grid_for_rows(m_, fn, lds, fs, rows_per_block);
+        uint32_t shared_blocks = grid_for_rows(m_, fn, lds, fs, shared_rows_per_block);
         const uint32_t routed_blocks = grid_for_rows(m_, fn, lds, (uint64_t)top_k * f, rows_per_block);
         float* no_wf = nullptr;
         NormArg na = stage;
-        void* args[] = {&kp,     &logits, &per_expert_scale, &num_experts, &top_k, &out_indices, &out_weights,
-                        &no_wf,  &x,      &acts,             &d,           &f,     &na,          &g,
-                        &u,      &shared_norm_w, &shared_act, &fs,         &shared_blocks};
+        Q4Mat g4 = {static_cast<const uint8_t*>(gate.weights), gate.scales, gate.biases, nullptr, nullptr, fs, 0};
+        Q4Mat u4 = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases, nullptr, nullptr, fs, 0};
+        Q8Mat g8 = {static_cast<const uint8_t*>(gate.weights), gate.scales, gate.biases};
+        Q8Mat u8 = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases};
+        void* gp = shared_bits == 8 ? (void*)&g8 : (void*)&g4;
+        void* upp = shared_bits == 8 ? (void*)&u8 : (void*)&u4;
+        void* args[] = {&kp,    &logits, &per_expert_scale, &num_experts, &top_k, &out_indices, &out_weights,
+                        &no_wf, &x,      &acts,             &d,           &f,     &na,          gp,
+                        upp,    &shared_norm_w, &shared_act, &fs,         &shared_blocks};
         return launch(fn, shared_blocks + routed_blocks, kBlock, lds, stream, args, name);
     }
 
-    // Phase 2 (no residual) with the int4 shared expert's down GEMV (rows of
-    // fs codes, fs <= 4096) into shared_y in the same launch
-    // (moe_phase2_shared). 4-bit pools only.
+    // Phase 2 (no residual) with the shared expert's down GEMV (rows of fs
+    // codes, fs <= 4096) into shared_y in the same launch (moe_phase2_shared /
+    // _shared8). shared_bits 4 or 8; 4-bit pools only.
     int encode_phase2_shared(void* stream, const tfq_expert_pool& pool, const uint32_t* indices,
                              const uint16_t* acts, const uint16_t* routing_weights, uint16_t* y, uint32_t d,
                              uint32_t f, uint32_t top_k, const tfq_q4_matrix& down, const uint16_t* shared_act,
-                             uint16_t* shared_y, uint32_t fs) const {
+                             uint16_t* shared_y, uint32_t fs, uint32_t shared_bits) const {
         int rc = check_pool(pool, d, f, top_k);
         if (rc) return rc;
         if (pool_bits(pool) != 4) return fail(TFQ_E_UNSUPPORTED, "the fused shared form takes 4-bit experts");
+        if (shared_bits != 4 && shared_bits != 8)
+            return fail(TFQ_E_INVAL, "SharedExpert unsupported weight bits: %u", shared_bits);
         if (f > 1024) return fail(TFQ_E_UNSUPPORTED, "phase 2 f=%u exceeds 1024", f);
         if (fs == 0 || fs % 64 || fs > 4096)
             return fail(TFQ_E_UNSUPPORTED, "shared f=%u must be a multiple of 64 up to 4096", fs);
@@ -493,16 +508,22 @@ public:
             return fail(TFQ_E_INVAL, "null pointer argument");
         if (!aligned(down.weights, 16)) return fail(TFQ_E_INVAL, "down weights must be 16-byte aligned");
         ExpertPool kp = kernel_pool(pool);
-        Q4Mat dn = {static_cast<const uint8_t*>(down.weights), down.scales, down.biases, nullptr, nullptr, d, 0};
         const uint32_t p2 = ((f / 32) + 7) / 8;
-        const uint32_t sp = ((fs / 32) + 31) / 32;
+        const SegShape s8 = seg_shape(fs / 16, 4);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_moe_phase2_shared_p%u_sp%u", p2, sp);
+        if (shared_bits == 8)
+            std::snprintf(name, sizeof(name), "tfq_moe_phase2_shared8_p%u_q%u_%u", p2, s8.seg, s8.p);
+        else
+            std::snprintf(name, sizeof(name), "tfq_moe_phase2_shared_p%u_sp%u", p2, ((fs / 32) + 31) / 32);
         hipFunction_t fn = m_.get(name);
-        const uint32_t lds = std::max(xpairs_lds_bytes(top_k * f), xpairs_lds_bytes(fs));
-        uint32_t shared_blocks = grid_for_rows(m_, fn, lds, d, (kBlock / 64) * 2 * kRowsInFlight);
+        const uint32_t lds = std::max(xpairs_lds_bytes(top_k * f), shared_bits == 8 ? fs * 6 : xpairs_lds_bytes(fs));
+        const uint32_t shared_rows_per_block = (kBlock / 64) * (shared_bits == 8 ? 64 / s8.seg : 2) * kRowsInFlight;
+        uint32_t shared_blocks = grid_for_rows(m_, fn, lds, d, shared_rows_per_block);
         const uint32_t routed_blocks = grid_for_rows(m_, fn, lds, d, (kBlock / 64) * kRowsInFlight);
-        void* args[] = {&kp, &indices, &acts, &routing_weights, &y, &d, &f, &top_k, &dn, &shared_act, &shared_y,
+        Q4Mat dn4 = {static_cast<const uint8_t*>(down.weights), down.scales, down.biases, nullptr, nullptr, d, 0};
+        Q8Mat dn8 = {static_cast<const uint8_t*>(down.weights), down.scales, down.biases};
+        void* dp = shared_bits == 8 ? (void*)&dn8 : (void*)&dn4;
+        void* args[] = {&kp, &indices, &acts, &routing_weights, &y, &d, &f, &top_k, dp, &shared_act, &shared_y,
                         &fs, &shared_blocks};
         return launch(fn, shared_blocks + routed_blocks, kBlock, lds, stream, args, name);
     }
@@ -1018,10 +1039,10 @@ private:
 // reference runs as separate kernels are formed while each consumer stages
 // its activation vector (NormArg); the router also stores the post-attention
 // h and r(h), from which the expert launches form their inputs without the
-// reductions. Every launch is on `stream`, in order: with the int4 shared
-// expert and 4-bit routed experts its gate/up/act and down run inside the
-// routed phase 1 and phase 2 launches (7 launches per layer); otherwise as
-// two launches of their own before the router (9). Measured at config 4
+// reductions. Every launch is on `stream`, in order: with 4-bit routed
+// experts the shared expert's (int4 or int8) gate/up/act and down run inside
+// the routed phase 1 and phase 2 launches (7 launches per layer); otherwise
+// as two launches of their own before the router (9). Measured at config 4
 // (graph replay): the shared expert on a second stream, concurrent with the
 // router and the routed experts, took 66.0 µs per layer against 58.7 µs with
 // its two launches in order on the one stream (the concurrent kernels slow
@@ -1204,7 +1225,7 @@ public:
         if (rc) return rc;
         // 4. shared expert, input = pre_feedforward_layernorm(h): inside the
         //    routed launches (fused), or here from the layer input and o
-        const bool fused = shared_bits == 4 && pool_bits(w.experts) == 4 && s.shared_f <= 4096;
+        const bool fused = pool_bits(w.experts) == 4 && s.shared_f <= 4096;
         if (!fused) {
             const NormArg dense{w.pre_ffn_norm, o, w.post_attention_norm, s.eps, kStagePostAttn};
             rc = shared_bits == 8 ? shared8_.encode(stream, hidden, w.shared_gate, w.shared_up, w.shared_down, h1,
@@ -1227,10 +1248,10 @@ public:
         if (fused) {
             rc = moe_.encode_phase1_shared(stream, w.experts, logits, r.per_expert_scale, r.num_experts, idx, rw,
                                            hmid, acts, s.d, s.expert_f, s.top_k, routed, w.shared_gate,
-                                           w.shared_up, w.pre_ffn_norm, sact, s.shared_f);
+                                           w.shared_up, w.pre_ffn_norm, sact, s.shared_f, shared_bits);
             if (rc) return rc;
             return moe_.encode_phase2_shared(stream, w.experts, idx, acts, rw, h2, s.d, s.expert_f, s.top_k,
-                                             w.shared_down, sact, h1, s.shared_f);
+                                             w.shared_down, sact, h1, s.shared_f, shared_bits);
         }
         rc = moe_.encode_phase1_routed(stream, w.experts, logits, r.per_expert_scale, r.num_experts, idx, rw,
                                        nullptr, hmid, acts, s.d, s.expert_f, s.top_k, routed);

@@ -52,7 +52,8 @@ constexpr uint32_t kTailGemvThreads = 1024;
     extern "C" __global__ __launch_bounds__(256) void tfq_q8_gemv_s##SEG##_p##P(                 \
         const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* x,               \
         uint32_t x_stride, uint16_t* y, uint32_t y_stride, uint32_t m, uint32_t n) {              \
-        q8_gemv<SEG, P, kRowsInFlight>(W, S, B, x, x_stride, y, y_stride, m, n);                  \
+        q8_gemv<SEG, P, kRowsInFlight>(W, S, B, x, x_stride, y, y_stride, m, n, blockIdx.x,      \
+                                       gridDim.x);                                                \
     }
 
 // Shared expert, int8 rows: fused gate/up/act in the plain and norm staging forms.
@@ -60,7 +61,8 @@ constexpr uint32_t kTailGemvThreads = 1024;
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         Q8Mat gate, Q8Mat up, const uint16_t* x, uint32_t x_stride, uint16_t* act, uint32_t D,   \
         uint32_t F, NormArg norm) {                                                               \
-        q8_gate_up_act<SEG, P, kRowsInFlight, NORM>(gate, up, x, x_stride, act, D, F, norm);      \
+        q8_gate_up_act<SEG, P, kRowsInFlight, NORM>(gate, up, x, x_stride, act, D, F, norm,       \
+                                                    blockIdx.x, gridDim.x);                       \
     }
 #define TFQ_Q8_GATE_UP(SEG, P)                                                                   \
     TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_s##SEG##_p##P, false, SEG, P)                         \
@@ -169,6 +171,35 @@ constexpr uint32_t kTailGemvThreads = 1024;
 #define TFQ_PHASE2_SHARED(P2)                                                                    \
     TFQ_PHASE2_SHARED_SP(P2, 1) TFQ_PHASE2_SHARED_SP(P2, 2) TFQ_PHASE2_SHARED_SP(P2, 3)          \
     TFQ_PHASE2_SHARED_SP(P2, 4)
+
+// int8 shared expert: (SEG, P) of the routed rows (d/32 chunks) and (SEG8,
+// P8) of the shared gate/up rows (d/16 chunks) are both set by d.
+#define TFQ_PHASE1_SHARED8(SEG, P, SEG8, P8)                                                      \
+    extern "C" __global__ __launch_bounds__(256) void                                             \
+        tfq_moe_phase1_shared8_s##SEG##_p##P##_q##SEG8##_##P8(                                    \
+            ExpertPool pool, const float* logits, const uint16_t* gain, uint32_t E, uint32_t top_k, \
+            uint32_t* out_idx, uint16_t* out_w, float* out_wf, const uint16_t* x, uint16_t* acts,  \
+            uint32_t D, uint32_t F, NormArg norm, Q8Mat sgate, Q8Mat sup, const uint16_t* snorm_w,  \
+            uint16_t* sact, uint32_t Fs, uint32_t shared_blocks) {                                  \
+        moe_phase1_routed_shared8<SEG, P, SEG8, P8, kRowsInFlight>(pool, logits, gain, E, top_k,  \
+                                                                   out_idx, out_w, out_wf, x,     \
+                                                                   acts, D, F, norm, sgate, sup,  \
+                                                                   snorm_w, sact, Fs,             \
+                                                                   shared_blocks);                \
+    }
+#define TFQ_PHASE2_SHARED8_FORM(P2, SEG8, P8)                                                     \
+    extern "C" __global__ __launch_bounds__(256) void                                             \
+        tfq_moe_phase2_shared8_p##P2##_q##SEG8##_##P8(                                            \
+            ExpertPool pool, const uint32_t* indices, const uint16_t* acts, const uint16_t* rw,  \
+            uint16_t* y, uint32_t D, uint32_t F, uint32_t top_k, Q8Mat sdown, const uint16_t* sact, \
+            uint16_t* sy, uint32_t Fs, uint32_t shared_blocks) {                                    \
+        moe_phase2_shared8<P2, SEG8, P8, kRowsInFlight>(pool, indices, acts, rw, y, D, F, top_k,  \
+                                                        sdown, sact, sy, Fs, shared_blocks);      \
+    }
+#define TFQ_PHASE2_SHARED8_P1(SEG8, P8) TFQ_PHASE2_SHARED8_FORM(1, SEG8, P8)
+#define TFQ_PHASE2_SHARED8_P2(SEG8, P8) TFQ_PHASE2_SHARED8_FORM(2, SEG8, P8)
+#define TFQ_PHASE2_SHARED8_P3(SEG8, P8) TFQ_PHASE2_SHARED8_FORM(3, SEG8, P8)
+#define TFQ_PHASE2_SHARED8_P4(SEG8, P8) TFQ_PHASE2_SHARED8_FORM(4, SEG8, P8)
 
 #define TFQ_LM_HEAD(SEG, P)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void tfq_lm_head_greedy_s##SEG##_p##P(          \

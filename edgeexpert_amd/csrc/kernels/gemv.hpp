@@ -188,10 +188,12 @@ __device__ __forceinline__ void load_x16(const float* __restrict__ lds, uint32_t
 // synchronise; it calls issue0() (the first row group's loads) once its own
 // input loads are in flight, before it waits for them.
 // Emits fp32 results through `out(row, value)` from lane 0 of each segment.
+// blk / nblk as in q4_rows.
 template <int SEG, int P, int R, typename Stage, typename Out>
 __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
                                         const uint16_t* __restrict__ B, float* __restrict__ lds_x,
-                                        uint32_t M, uint32_t n, Stage stage, Out out) {
+                                        uint32_t M, uint32_t n, Stage stage, Out out, uint32_t blk,
+                                        uint32_t nblk) {
     constexpr uint32_t NT = kThreads;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
@@ -200,8 +202,8 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
     const uint32_t lpr = n >> 4;
     const uint32_t ngroups = n >> 6;
     constexpr uint32_t spw = kWave / SEG;
-    const uint32_t seg_id = (blockIdx.x * nwaves + wave) * spw + lane / SEG;
-    const uint32_t seg_total = gridDim.x * nwaves * spw;
+    const uint32_t seg_id = (blk * nwaves + wave) * spw + lane / SEG;
+    const uint32_t seg_total = nblk * nwaves * spw;
 
     uint4 wv[R][P];
     uint32_t sr[R][P], br[R][P];      // raw fp16 scale / bias
@@ -260,11 +262,12 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
 }
 
 // blockIdx.y selects the token of a block of inputs: x + y·x_stride, y + y·y_stride.
+// blk / nblk as in q4_rows.
 template <int SEG, int P, int R>
 __device__ __forceinline__ void q8_gemv(const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
                                         const uint16_t* __restrict__ B, const uint16_t* __restrict__ x,
                                         uint32_t x_stride, uint16_t* __restrict__ y, uint32_t y_stride,
-                                        uint32_t M, uint32_t n) {
+                                        uint32_t M, uint32_t n, uint32_t blk, uint32_t nblk) {
     extern __shared__ __attribute__((aligned(16))) float lds_x[];
     x += (size_t)blockIdx.y * x_stride;
     y += (size_t)blockIdx.y * y_stride;
@@ -280,7 +283,7 @@ __device__ __forceinline__ void q8_gemv(const uint8_t* __restrict__ W, const uin
             for (uint32_t i = threadIdx.x; i < n; i += kThreads) lds_x[i] = h2f(xs[i]);
             __syncthreads();
         },
-        [&](uint32_t row, float v) { y[row] = f2h(v); });
+        [&](uint32_t row, float v) { y[row] = f2h(v); }, blk, nblk);
 }
 
 // -------------------------------------------------------------- router ----
@@ -336,7 +339,7 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
             }
             __syncthreads();
         },
-        [&](uint32_t row, float v) { logits[row] = v; });
+        [&](uint32_t row, float v) { logits[row] = v; }, blockIdx.x, gridDim.x);
 }
 
 // Order key of logit v at index t: larger key = ranked first. The float

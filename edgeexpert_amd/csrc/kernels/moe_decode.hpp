@@ -265,11 +265,12 @@ __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& u
 // 16 codes per lane-chunk (q8_rows' mapping); x is staged as NormArg says
 // and held as fp32 in LDS, each lane keeping its chunks' activations in
 // registers across rows. blockIdx.y selects the token of a prefill block
-// (x + y·x_stride, act + y·F). Dynamic LDS: D floats + D halves.
+// (x + y·x_stride, act + y·F). Dynamic LDS: D floats + D halves. blk / nblk
+// as in gate_up_rows.
 template <int SEG, int P, int R, bool NORM>
 __device__ __forceinline__ void q8_gate_up_act(const Q8Mat& gate, const Q8Mat& up, const uint16_t* __restrict__ x,
                                                uint32_t x_stride, uint16_t* __restrict__ act, uint32_t D,
-                                               uint32_t F, const NormArg& norm) {
+                                               uint32_t F, const NormArg& norm, uint32_t blk, uint32_t nblk) {
     extern __shared__ __attribute__((aligned(16))) float lds_x[];
     constexpr uint32_t NT = kThreads;
     x += (size_t)blockIdx.y * x_stride;
@@ -281,8 +282,8 @@ __device__ __forceinline__ void q8_gate_up_act(const Q8Mat& gate, const Q8Mat& u
     const uint32_t lpr = D >> 4;              // 16-code chunks per row
     const uint32_t ngroups = D >> 6;
     constexpr uint32_t spw = kWave / SEG;
-    const uint32_t seg_id = (blockIdx.x * nwaves + wave) * spw + lane / SEG;
-    const uint32_t seg_total = gridDim.x * nwaves * spw;
+    const uint32_t seg_id = (blk * nwaves + wave) * spw + lane / SEG;
+    const uint32_t seg_total = nblk * nwaves * spw;
 
     uint4 gv[R][P], uv[R][P];
     uint32_t gsr[R][P], gbr[R][P], usr[R][P], ubr[R][P];     // raw fp16 scales / biases
@@ -529,6 +530,42 @@ __device__ __forceinline__ void moe_phase2_shared(const ExpertPool& pool, const 
     } else {
         moe_phase2<P2, R, BITS>(pool, indices, acts, rw, nullptr, y, D, F, top_k, blockIdx.x - shared_blocks,
                                 gridDim.x - shared_blocks);
+    }
+}
+
+// The same two launches with the int8 shared expert: its gate/up/act rows
+// (q8_gate_up_act, SEG8 x P8 lanes per row of D bytes) beside phase 1, and
+// its down rows (q8_gemv, rows of Fs bytes) beside phase 2. Dynamic LDS: the
+// larger of the two parts'.
+template <int SEG, int P, int SEG8, int P8, int R>
+__device__ __forceinline__ void moe_phase1_routed_shared8(
+    const ExpertPool& pool, const float* __restrict__ logits, const uint16_t* __restrict__ gain, uint32_t E,
+    uint32_t top_k, uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w, float* __restrict__ out_wf,
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ acts, uint32_t D, uint32_t F, const NormArg& norm,
+    const Q8Mat& sgate, const Q8Mat& sup, const uint16_t* __restrict__ snorm_w, uint16_t* __restrict__ sact,
+    uint32_t Fs, uint32_t shared_blocks) {
+    if (blockIdx.x < shared_blocks) {
+        NormArg ns = norm;
+        ns.w = snorm_w;
+        q8_gate_up_act<SEG8, P8, R, true>(sgate, sup, x, 0, sact, D, Fs, ns, blockIdx.x, shared_blocks);
+    } else {
+        moe_phase1_routed<SEG, P, R, true, 4>(pool, logits, gain, E, top_k, out_idx, out_w, out_wf, x, acts, D, F,
+                                              norm, blockIdx.x - shared_blocks, gridDim.x - shared_blocks);
+    }
+}
+
+template <int P2, int SEG8, int P8, int R>
+__device__ __forceinline__ void moe_phase2_shared8(const ExpertPool& pool, const uint32_t* __restrict__ indices,
+                                                   const uint16_t* __restrict__ acts,
+                                                   const uint16_t* __restrict__ rw, uint16_t* __restrict__ y,
+                                                   uint32_t D, uint32_t F, uint32_t top_k, const Q8Mat& sdown,
+                                                   const uint16_t* __restrict__ sact, uint16_t* __restrict__ sy,
+                                                   uint32_t Fs, uint32_t shared_blocks) {
+    if (blockIdx.x < shared_blocks) {
+        q8_gemv<SEG8, P8, R>(sdown.w, sdown.s, sdown.b, sact, 0, sy, 0, D, Fs, blockIdx.x, shared_blocks);
+    } else {
+        moe_phase2<P2, R, 4>(pool, indices, acts, rw, nullptr, y, D, F, top_k, blockIdx.x - shared_blocks,
+                             gridDim.x - shared_blocks);
     }
 }
 

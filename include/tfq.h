@@ -393,9 +393,9 @@ size_t tfq_decode_layer_workspace_bytes(const tfq_decode_layer_shape *shape, uin
  *   out = (h + rmsnorm(rmsnorm(h1, post_ffn1) + rmsnorm(h2, post_ffn2), post_ffn)) * layer_scalar
  * with fp16 rounding wherever the reference stores a buffer. Every launch
  * runs on `stream`, in order (the call can be captured into a graph); with
- * the int4 shared expert (shared_f <= 4096) and 4-bit routed experts the
- * shared expert's gate/up/act and down run inside the routed phase-1 and
- * phase-2 launches, its input normed from the h and r(h) the router stores.
+ * 4-bit routed experts and shared_f <= 4096 the shared expert's (int4 or
+ * int8) gate/up/act and down run inside the routed phase-1 and phase-2
+ * launches, its input normed from the h and r(h) the router stores.
  * hidden_out may alias hidden_in. out_indices/out_weights (may be NULL)
  * receive the routing. Replaces the per-layer decode sequence of
  * RealForwardRunner (S/Runtime/Inference/RealForwardRunner.swift:2265-2862:
