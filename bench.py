@@ -571,6 +571,26 @@ def layer_summary(trace_csv, out=sys.stdout):
     for (n, gx, gy, q), v in groups.items():
         if len(v) >= layers // 2:
             out.write(f"{n[:44]:44s} {gx:5d}x{gy:<3d} {q:5d} {statistics.median(v):10.2f} {min(v):8.2f}\n")
+    # one chained layer of the first leg (the 4-bit shared expert): the
+    # dispatches from a tail-forming QKV GEMV to the next, median over the
+    # middle layers of its chains
+    tails = [i for i, r in enumerate(rows) if r[2].startswith("tfq_q4_gemv_tail_")]
+    seqs = []
+    for a, b in zip(tails, tails[1:]):
+        seq = rows[a:b]
+        if seqs and [r[2] for r in seq] != [r[2] for r in seqs[0]]:
+            break
+        seqs.append(seq)
+    if seqs:
+        out.write(f"\none chained layer (tfq_decode_layers, {len(seqs)} layers of the first leg; median per position):\n"
+                  f"{'kernel':44s} {'grid':>9s} {'median us':>10s} {'gap before us':>14s}\n")
+        total = 0.0
+        for j, r in enumerate(seqs[0]):
+            dur = statistics.median((sq[j][1] - sq[j][0]) / 1e3 for sq in seqs)
+            gap = statistics.median((sq[j][0] - sq[j - 1][1]) / 1e3 for sq in seqs) if j else 0.0
+            total += dur
+            out.write(f"{r[2][:44]:44s} {r[3]:5d}x{r[4]:<3d} {dur:10.2f} {gap:14.2f}\n")
+        out.write(f"sum of the kernel medians: {total:.1f} us\n")
 
 
 def bench_gemm_policy(ctx, stream, batch_avg_us):
