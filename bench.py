@@ -860,18 +860,35 @@ def main():
         rbytes = (wsz + 2 * ssz) // 16 * 16
         ceil_us = batch_avg_us(lambda i: ops.read_ceiling(ctx, stream, big, rbytes, sink0, 8192,
                                                           src_offset=(i % n_copies) * (wsz + 2 * ssz)), n_copies)
-        # the launch floor: the same kernel reading one 16-byte chunk (one block)
-        floor_us = batch_avg_us(lambda i: ops.read_ceiling(ctx, stream, big, 16, sink0, 8192,
-                                                           src_offset=(i % n_copies) * (wsz + 2 * ssz)), n_copies)
+        # the launch floor: the same kernel reading one 16-byte chunk (one
+        # block), from the rotated copies (cold) and from one address (warm),
+        # back to back and replayed from a graph
+        def one_block(i, cold=True):
+            ops.read_ceiling(ctx, stream, big, 16, sink0, 8192,
+                             src_offset=(i % n_copies) * (wsz + 2 * ssz) if cold else 0)
+
+        floor_us = batch_avg_us(one_block, n_copies)
+        floor_warm_us = batch_avg_us(lambda i: one_block(i, False), n_copies)
+        g1 = Graph(stream, lambda: [one_block(i) for i in range(n_copies)])
+        g2 = Graph(stream, lambda: [one_block(i, False) for i in range(n_copies)])
+        for g in (g1, g2):
+            g.launch(stream)
+        stream.sync()
+        floor_graph_us = batch_avg_us(lambda i: g1.launch(stream), 4) / n_copies
+        floor_graph_warm_us = batch_avg_us(lambda i: g2.launch(stream), 4) / n_copies
         log(f"GEMV C0 (back-to-back): cold {cold_us:.2f} us ({cold_gbs:.0f} GB/s), warm {warm_us:.2f} us "
             f"({warm_gbs:.0f} GB/s); cold from a graph {cold_graph_us:.2f} us ({graph_gbs:.0f} GB/s); "
             f"cold read of the same bytes {ceil_us:.2f} us (GEMV at {ceil_us / cold_us:.2f} of it); "
-            f"one-block launch {floor_us:.2f} us")
+            f"one-block launch reading 16 B: cold {floor_us:.2f} / warm {floor_warm_us:.2f} us back to back, "
+            f"{floor_graph_us:.2f} / {floor_graph_warm_us:.2f} us from a graph")
         return {"shape": [2816, 2816], "bytes": gemv_bytes, "cold_us": round(cold_us, 3),
                 "cold_gbs": round(cold_gbs, 1), "cold_frac": round(cold_gbs / HBM_PEAK_GBS, 4),
                 "cold_read_ceiling_us": round(ceil_us, 3),
                 "cold_frac_of_read_ceiling": round(ceil_us / cold_us, 4),
-                "launch_floor_us": round(floor_us, 3),
+                "launch_floor_us": {"cold": round(floor_us, 3), "warm": round(floor_warm_us, 3),
+                                    "cold_graph": round(floor_graph_us, 3), "warm_graph": round(floor_graph_warm_us, 3),
+                                    "measure": "tfq_read_ceiling over 16 bytes (one block): the rotated copies' "
+                                               "first chunk (cold) or one address (warm)"},
                 "warm_us": round(warm_us, 3), "warm_gbs": round(warm_gbs, 1),
                 "cold_graph_us": round(cold_graph_us, 3), "cold_graph_frac": round(graph_gbs / HBM_PEAK_GBS, 4),
                 "copies_rotated": n_copies}
