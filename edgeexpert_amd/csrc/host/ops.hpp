@@ -16,6 +16,7 @@ namespace tfq {
 
 constexpr uint32_t kBlock = 256;          // 4 wavefronts per block for every GEMV-family kernel
 constexpr uint32_t kMaxN = 8192;          // longest reduction with x resident in LDS
+constexpr uint32_t kFixedStageMaxN = 4096; // longest x of the fixed-mode GEMV staging: 8 halves x 2 chunks x 256 threads
 constexpr uint32_t kRowsInFlight = 1;     // rows per segment in flight (entry_points.hpp kRowsInFlight)
 constexpr uint32_t kProjBM = 64;           // projection GEMM tile: tokens (gemm.hpp kProjBM)
 constexpr uint32_t kProjBN = 256;          // outputs (gemm.hpp kProjBN)
@@ -151,10 +152,28 @@ private:
                 return fail(TFQ_E_INVAL, "scales/biases/y of matrix %u are not 2-byte aligned", i);
         }
         const SegShape sh = seg_shape_fit(n / 32, 2);
+        // The plain and _rms forms fix the staging mode at compile time and
+        // take only 16-byte aligned inputs of n <= kFixedStageMaxN; other
+        // calls go to the _norm form, which reads the mode. The tail form is
+        // always fixed: its inputs must qualify.
+        const NormArg& na = mats.norm;
+        const bool vec = aligned(x, 16) && n <= kFixedStageMaxN;
+        const char* form = "norm_";
+        if (na.mode == kStageTail) {
+            for (const void* p : {(const void*)x, (const void*)na.w, (const void*)na.attn, (const void*)na.attn_w,
+                                  (const void*)na.h1, (const void*)na.h1_w, (const void*)na.h2, (const void*)na.h2_w,
+                                  (const void*)na.ffn_w, (const void*)na.export_h})
+                if (!p || !aligned(p, 16)) return fail(TFQ_E_INVAL, "tail staging needs 16-byte aligned vectors");
+            form = "tail_";
+        } else if (na.mode == kStageCopy && vec) {
+            form = "";
+        } else if (na.mode == kStageNorm && vec && aligned(na.w, 16)) {
+            form = "rms_";
+        }
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_q%u_gemv_%ss%u_p%u", bits, form_prefix(mats.norm), sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_q%u_gemv_%ss%u_p%u", bits, form, sh.seg, sh.p);
         // the tail form runs 1024-thread blocks (entry_points.hpp kTailGemvThreads)
-        const uint32_t block = mats.norm.mode == kStageTail ? 1024u : kBlock;
+        const uint32_t block = na.mode == kStageTail ? 1024u : kBlock;
         const uint32_t rows_per_block = (block / 64) * (64 / sh.seg) * kRowsInFlight;
         uint32_t nn = n;
         void* args[] = {&mats, &x, &nn};
@@ -507,6 +526,8 @@ public:
             !down.scales || !down.biases)
             return fail(TFQ_E_INVAL, "null pointer argument");
         if (!aligned(down.weights, 16)) return fail(TFQ_E_INVAL, "down weights must be 16-byte aligned");
+        // the int4 down rows stage the act with the fixed-mode copy (16-byte loads)
+        if (!aligned(shared_act, 16)) return fail(TFQ_E_INVAL, "shared act must be 16-byte aligned");
         ExpertPool kp = kernel_pool(pool);
         const uint32_t p2 = ((f / 32) + 7) / 8;
         const SegShape s8 = seg_shape(fs / 16, 4);

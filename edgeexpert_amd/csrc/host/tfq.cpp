@@ -33,7 +33,11 @@ static std::vector<std::string> kernel_names() {
     for (const char* s : q4_shapes)
         for (const char* form : {"", "norm_"}) {
             names.push_back(std::string("tfq_q4_gemv_") + form + s);
-            if (*form) names.push_back(std::string("tfq_q4_gemv_tail_") + s);
+            if (*form) {
+                names.push_back(std::string("tfq_q4_gemv_tail_") + s);
+                names.push_back(std::string("tfq_q4_gemv_rms_") + s);
+                names.push_back(std::string("tfq_q3_gemv_rms_") + s);
+            }
             names.push_back(std::string("tfq_q3_gemv_") + form + s);
             for (const char* b : {"", "b2_", "b3_"}) {
                 names.push_back(std::string("tfq_moe_phase1_") + b + form + s);

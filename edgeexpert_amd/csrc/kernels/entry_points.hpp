@@ -24,14 +24,23 @@ using namespace tfq;
 // sums are reduced and stored.
 constexpr int kRowsInFlight = 1;
 
-// Each int4 GEMV-family shape comes in two forms: plain (x staged as is) and
-// _norm (x normalised while staged, NormArg); the plain form needs fewer
-// registers and so runs more wavefronts per SIMD. The 2- and 3-bit forms of
-// a kernel carry the width in the name (tfq_q3_gemv_*, tfq_moe_phase1_b3_*).
+// Each int4 GEMV-family shape comes in three forms: plain (x staged as is),
+// _rms (x RMS-normalised while staged) and _norm (x staged as NormArg says,
+// any mode). The plain and _rms forms fix the staging mode at compile time
+// and take only 16-byte aligned inputs of n <= 4096 (the host checks, and
+// sends other calls to _norm); the plain form needs the fewest registers and
+// so runs the most wavefronts per SIMD. The 2- and 3-bit forms of a kernel
+// carry the width in the name (tfq_q3_gemv_*, tfq_moe_phase1_b3_*).
 #define TFQ_GEMV_FORMS(TAG, BITS, SEG, P)                                                        \
     extern "C" __global__ __launch_bounds__(256) void tfq_##TAG##_gemv_s##SEG##_p##P(            \
         Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
-        q4_gemv_multi<SEG, P, kRowsInFlight, false, BITS>(mats, x, n);                            \
+        q4_gemv_multi<SEG, P, kRowsInFlight, false, BITS, false, kThreads, (int)kStageCopy>(mats, x, \
+                                                                                            n);  \
+    }                                                                                            \
+    extern "C" __global__ __launch_bounds__(256) void tfq_##TAG##_gemv_rms_s##SEG##_p##P(        \
+        Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
+        q4_gemv_multi<SEG, P, kRowsInFlight, true, BITS, false, kThreads, (int)kStageNorm>(mats, x, \
+                                                                                           n);   \
     }                                                                                            \
     extern "C" __global__ __launch_bounds__(256) void tfq_##TAG##_gemv_norm_s##SEG##_p##P(       \
         Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \

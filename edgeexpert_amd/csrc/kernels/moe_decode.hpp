@@ -525,8 +525,9 @@ __device__ __forceinline__ void moe_phase2_shared(const ExpertPool& pool, const 
         mats.nmat = 1;
         mats.total_rows = D;
         mats.norm = NormArg{nullptr, nullptr, nullptr, 0.0f, kStageCopy};
-        q4_rows<32, SP, R, false>(mats, sact, Fs, [&](uint32_t row, float v) { sy[row] = f2h(v); }, blockIdx.x,
-                                  shared_blocks);
+        // sact: the workspace's 16-byte aligned act vector, Fs <= 4096
+        q4_rows<32, SP, R, false, false, 4, false, kThreads, (int)kStageCopy>(
+            mats, sact, Fs, [&](uint32_t row, float v) { sy[row] = f2h(v); }, blockIdx.x, shared_blocks);
     } else {
         moe_phase2<P2, R, BITS>(pool, indices, acts, rw, nullptr, y, D, F, top_k, blockIdx.x - shared_blocks,
                                 gridDim.x - shared_blocks);
