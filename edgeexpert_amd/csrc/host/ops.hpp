@@ -358,8 +358,20 @@ public:
         float* logits = out_logits ? out_logits : static_cast<float*>(workspace);
         *logits_used = logits;
         const SegShape sh = seg_shape(d / 16, 4);
+        // aligned inputs in the copy or post-attention mode take the form with
+        // the staging mode fixed at compile time (d <= 4096 is checked above)
+        bool vec = aligned(hidden, 16) && aligned(effective_scale, 16);
+        const char* form = "";
+        if (stage.mode == kStageCopy && vec) {
+            form = "c_";
+        } else if (stage.mode == kStagePostAttn) {
+            for (const void* p : {(const void*)stage.w, (const void*)stage.attn, (const void*)stage.attn_w,
+                                  (const void*)stage.export_h})
+                vec = vec && aligned(p, 16);
+            if (vec) form = "pa_";
+        }
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_router_logits_s%u_p%u", sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_router_logits_%ss%u_p%u", form, sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg);
         const uint32_t grid = (num_experts + rows_per_block - 1) / rows_per_block;
         NormArg na = stage;
@@ -440,7 +452,9 @@ public:
         ExpertPool kp = kernel_pool(pool);
         const uint32_t p = ((f / 32) + 7) / 8;
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_moe_phase2_%sp%u", bits_infix(pool), p);
+        // 16-byte aligned acts take the form with the staging mode fixed at compile time
+        std::snprintf(name, sizeof(name), "tfq_moe_phase2_%s%sp%u", bits_infix(pool), aligned(acts, 16) ? "" : "any_",
+                      p);
         void* args[] = {&kp, &indices, &acts, &routing_weights, &residual, &y, &d, &f, &top_k};
         hipFunction_t fn = m_.get(name);
         const uint32_t lds = xpairs_lds_bytes(top_k * f);
@@ -466,7 +480,11 @@ public:
         if (stage.mode != kStageScaled) return fail(TFQ_E_INVAL, "the fused shared form stages h scaled by r(h)");
         if (shared_bits != 4 && shared_bits != 8)
             return fail(TFQ_E_INVAL, "SharedExpert unsupported weight bits: %u", shared_bits);
-        if (d > (shared_bits == 8 ? 4096u : kMaxN)) return fail(TFQ_E_UNSUPPORTED, "d=%u too large", d);
+        // both parts stage h with the scaled mode fixed at compile time:
+        // 16-byte aligned vectors, d <= kFixedStageMaxN
+        if (d > kFixedStageMaxN) return fail(TFQ_E_UNSUPPORTED, "d=%u exceeds %u", d, kFixedStageMaxN);
+        for (const void* p : {(const void*)x, (const void*)stage.w, (const void*)shared_norm_w, (const void*)stage.inv})
+            if (!aligned(p, 16)) return fail(TFQ_E_INVAL, "h, r(h) and the norm weights must be 16-byte aligned");
         if (fs == 0 || fs % 64) return fail(TFQ_E_INVAL, "shared f=%u must be a positive multiple of 64", fs);
         if (!logits || !out_indices || !out_weights || !x || !acts || !shared_act || !gate.weights || !up.weights ||
             !gate.scales || !gate.biases || !up.scales || !up.biases)
@@ -526,8 +544,9 @@ public:
             !down.scales || !down.biases)
             return fail(TFQ_E_INVAL, "null pointer argument");
         if (!aligned(down.weights, 16)) return fail(TFQ_E_INVAL, "down weights must be 16-byte aligned");
-        // the int4 down rows stage the act with the fixed-mode copy (16-byte loads)
-        if (!aligned(shared_act, 16)) return fail(TFQ_E_INVAL, "shared act must be 16-byte aligned");
+        // both parts stage their acts with the fixed-mode copy (16-byte loads)
+        if (!aligned(shared_act, 16) || !aligned(acts, 16))
+            return fail(TFQ_E_INVAL, "acts must be 16-byte aligned");
         ExpertPool kp = kernel_pool(pool);
         const uint32_t p2 = ((f / 32) + 7) / 8;
         const SegShape s8 = seg_shape(fs / 16, 4);

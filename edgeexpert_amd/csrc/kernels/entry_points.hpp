@@ -77,12 +77,18 @@ constexpr uint32_t kTailGemvThreads = 1024;
     TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_s##SEG##_p##P, false, SEG, P)                         \
     TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_norm_s##SEG##_p##P, true, SEG, P)
 
-#define TFQ_ROUTER(SEG, P)                                                                       \
-    extern "C" __global__ __launch_bounds__(256) void tfq_router_logits_s##SEG##_p##P(           \
+// The router GEMV: any staging mode and alignment, and the copy (_c_) and
+// post-attention (_pa_) modes fixed at compile time for aligned inputs.
+#define TFQ_ROUTER_FORM(NAME, FIXED, SEG, P)                                                     \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* h,               \
         const uint16_t* eff, float* logits, uint32_t E, uint32_t d, NormArg norm) {              \
-        router_logits<SEG, P>(W, S, B, h, eff, logits, E, d, norm);                               \
+        router_logits<SEG, P, FIXED>(W, S, B, h, eff, logits, E, d, norm);                        \
     }
+#define TFQ_ROUTER(SEG, P)                                                                       \
+    TFQ_ROUTER_FORM(tfq_router_logits_s##SEG##_p##P, -1, SEG, P)                                 \
+    TFQ_ROUTER_FORM(tfq_router_logits_c_s##SEG##_p##P, (int)kStageCopy, SEG, P)                  \
+    TFQ_ROUTER_FORM(tfq_router_logits_pa_s##SEG##_p##P, (int)kStagePostAttn, SEG, P)
 
 // GB: query heads per block (G / GB blocks per (chunk, kv head), blockIdx.z).
 #define TFQ_ATTN_GB(HD, G, GB)                                                                   \
@@ -143,17 +149,22 @@ constexpr uint32_t kTailGemvThreads = 1024;
     TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_b3_s##SEG##_p##P, false, 3, SEG, P)             \
     TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_b3_norm_s##SEG##_p##P, true, 3, SEG, P)
 
-#define TFQ_PHASE2_FORM(NAME, BITS, P)                                                           \
+// Phase 2 in two forms: 16-byte aligned acts (the staging mode fixed at
+// compile time) and _any_ (any alignment).
+#define TFQ_PHASE2_FORM(NAME, BITS, P, FIXED)                                                    \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         ExpertPool pool, const uint32_t* indices, const uint16_t* acts, const uint16_t* rw,      \
         const uint16_t* residual, uint16_t* y, uint32_t D, uint32_t F, uint32_t top_k) {         \
-        moe_phase2<P, kRowsInFlight, BITS>(pool, indices, acts, rw, residual, y, D, F, top_k,     \
-                                           blockIdx.x, gridDim.x);                                \
+        moe_phase2<P, kRowsInFlight, BITS, FIXED>(pool, indices, acts, rw, residual, y, D, F,     \
+                                                  top_k, blockIdx.x, gridDim.x);                  \
     }
 #define TFQ_PHASE2(P)                                                                            \
-    TFQ_PHASE2_FORM(tfq_moe_phase2_p##P, 4, P)                                                   \
-    TFQ_PHASE2_FORM(tfq_moe_phase2_b2_p##P, 2, P)                                                \
-    TFQ_PHASE2_FORM(tfq_moe_phase2_b3_p##P, 3, P)
+    TFQ_PHASE2_FORM(tfq_moe_phase2_p##P, 4, P, (int)kStageCopy)                                  \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_b2_p##P, 2, P, (int)kStageCopy)                               \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_b3_p##P, 3, P, (int)kStageCopy)                               \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_any_p##P, 4, P, -1)                                           \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_b2_any_p##P, 2, P, -1)                                        \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_b3_any_p##P, 3, P, -1)
 
 #define TFQ_PHASE1_SHARED_FORM(NAME, BITS, SEG, P)                                               \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \

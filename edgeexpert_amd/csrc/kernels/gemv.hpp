@@ -265,8 +265,8 @@ __device__ __forceinline__ void q8_rows(const uint8_t* __restrict__ W, const uin
 }
 
 // blockIdx.y selects the token of a block of inputs: x + y·x_stride, y + y·y_stride.
-// blk / nblk as in q4_rows.
-template <int SEG, int P, int R>
+// blk / nblk as in q4_rows; FIXED = kStageCopy: x 16-byte aligned, n <= 4096.
+template <int SEG, int P, int R, int FIXED = -1>
 __device__ __forceinline__ void q8_gemv(const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
                                         const uint16_t* __restrict__ B, const uint16_t* __restrict__ x,
                                         uint32_t x_stride, uint16_t* __restrict__ y, uint32_t y_stride,
@@ -279,7 +279,7 @@ __device__ __forceinline__ void q8_gemv(const uint8_t* __restrict__ W, const uin
         [&](auto issue0) {
             uint16_t* xs = reinterpret_cast<uint16_t*>(lds_x + n);
             const NormArg copy{nullptr, nullptr, nullptr, 0.0f, kStageCopy};
-            XStage<kThreads, kStageChunks> st;
+            XStage<kThreads, kStageChunks, true, true, false, FIXED> st;
             st.load(x, n, copy);
             issue0();
             st.plain(x, xs, n, copy);
@@ -298,7 +298,9 @@ constexpr uint32_t kRouterMaxTopK = 64;
 // Dynamic LDS: d floats.
 // With norm.w set, h is first RMS-normalised (to fp16, as a separate norm
 // kernel would store it). Dynamic LDS: d floats + d halves.
-template <int SEG, int P>
+// FIXED: the staging mode when known at compile time (XStage; h, eff and the
+// norm vectors then 16-byte aligned, d <= 4096), else -1.
+template <int SEG, int P, int FIXED = -1>
 __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
                                               const uint16_t* __restrict__ B, const uint16_t* __restrict__ h,
                                               const uint16_t* __restrict__ eff,
@@ -310,16 +312,17 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
         [&](auto issue0) {
             constexpr uint32_t NT = kThreads;
             uint16_t* hs = reinterpret_cast<uint16_t*>(lds_x + d);
-            XStage<NT, kStageChunks> st;
+            XStage<NT, kStageChunks, true, true, false, FIXED> st;
             st.load(h, d, norm);
             // the effective-scale chunks are loaded with h, before the weights
-            const bool vec = (((uintptr_t)eff) & 15u) == 0 && (d & 7u) == 0 && (d >> 3) <= kStageChunks * NT;
+            const bool vec =
+                FIXED >= 0 || ((((uintptr_t)eff) & 15u) == 0 && (d & 7u) == 0 && (d >> 3) <= kStageChunks * NT);
             h8 ev[kStageChunks];
-            if (eff && vec)
+            if (FIXED >= 0 || (eff && vec))
 #pragma unroll
                 for (uint32_t i = 0; i < kStageChunks; ++i) {
                     const uint32_t c = threadIdx.x + i * NT;
-                    ev[i] = __builtin_bit_cast(h8, ld16h(eff, c < (d >> 3) ? c : (d >> 3) - 1));
+                    ev[i] = __builtin_bit_cast(h8, ld16h(eff ? eff : h, c < (d >> 3) ? c : (d >> 3) - 1));
                 }
             issue0();
             st.plain(h, hs, d, norm);

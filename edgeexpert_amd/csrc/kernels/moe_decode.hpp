@@ -48,8 +48,10 @@ struct GateUpRow {
 // arrived when it ends; staging it before the weight loads then keeps the
 // staging off the stall a wave takes while the memory pipeline backs up
 // under them. blk / nblk: this block's index among the blocks that share
-// the rows, and their count (q4_rows).
-template <int SEG, int P, int R, bool NORM, int BITS, bool X_FIRST, typename Pro, typename RowFn, typename OutFn>
+// the rows, and their count (q4_rows). FIXED: the staging mode when known at
+// compile time (XStage), else -1.
+template <int SEG, int P, int R, bool NORM, int BITS, bool X_FIRST, int FIXED, typename Pro, typename RowFn,
+          typename OutFn>
 __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uint32_t D, uint32_t total,
                                              const NormArg& norm, Pro prologue, RowFn rowfn, OutFn out,
                                              uint32_t blk, uint32_t nblk) {
@@ -95,7 +97,7 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
             }
         }
     };
-    XStage<NT, kStageChunks, NORM> xs;
+    XStage<NT, kStageChunks, NORM, true, false, FIXED> xs;
     xs.load(x, D, norm);
     prologue();
     XPairs xp;
@@ -168,7 +170,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
                                            const NormArg& norm) {
     __shared__ uint32_t act_slot[kRouterMaxTopK];
     __shared__ uint32_t act_expert[kRouterMaxTopK];
-    gate_up_rows<SEG, P, R, NORM, BITS, true>(
+    gate_up_rows<SEG, P, R, NORM, BITS, true, -1>(
         x, D, n_active * F, norm,
         [&]() {
             if (threadIdx.x < n_active) {
@@ -193,7 +195,7 @@ __device__ __forceinline__ void moe_phase1(const ExpertPool& pool, const uint32_
 // phase 2 and the caller (MoE.encodeRouterGemma4's outputs,
 // S/Kernels/MoE/MoE.swift:147-197). blk / nblk as in gate_up_rows (blk 0
 // publishes).
-template <int SEG, int P, int R, bool NORM, int BITS = 4>
+template <int SEG, int P, int R, bool NORM, int BITS = 4, int FIXED = -1>
 __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const float* __restrict__ logits,
                                                   const uint16_t* __restrict__ gain, uint32_t E, uint32_t top_k,
                                                   uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w,
@@ -203,7 +205,7 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
     __shared__ __attribute__((aligned(16))) float stage[kRouterMaxExperts];
     __shared__ uint32_t sel_idx[kRouterMaxTopK];
     __shared__ float sel_val[kRouterMaxTopK];
-    gate_up_rows<SEG, P, R, NORM, BITS, true>(
+    gate_up_rows<SEG, P, R, NORM, BITS, true, FIXED>(
         x, D, top_k * F, norm,
         [&]() {
             for (uint32_t e = threadIdx.x; e < ((E + 3) & ~3u); e += kThreads)
@@ -233,14 +235,14 @@ __device__ __forceinline__ void moe_phase1_routed(const ExpertPool& pool, const 
 // gate[i]·x and u = up[i]·x in fp32 (SharedExpertInt4.swift:30-94 computes
 // the same product; its GPU sequence stores g and u as fp16 first, which
 // moves the expert's output ~8e-4 from the CPU reference, so they stay fp32).
-template <int SEG, int P, int R, bool NORM>
+template <int SEG, int P, int R, bool NORM, int FIXED = -1>
 __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& up,
                                                const uint16_t* __restrict__ x, uint16_t* __restrict__ act,
                                                uint32_t D, uint32_t F, const NormArg& norm, uint32_t blk,
                                                uint32_t nblk) {
     const uint32_t row_bytes = D >> 1;
     const uint32_t ngroups = D >> 6;
-    gate_up_rows<SEG, P, R, NORM, 4, false>(
+    gate_up_rows<SEG, P, R, NORM, 4, false, FIXED>(
         x, D, F, norm, [] {},
         [&](uint32_t f) {
             GateUpRow q{};
@@ -267,7 +269,7 @@ __device__ __forceinline__ void q4_gate_up_act(const Q4Mat& gate, const Q4Mat& u
 // registers across rows. blockIdx.y selects the token of a prefill block
 // (x + y·x_stride, act + y·F). Dynamic LDS: D floats + D halves. blk / nblk
 // as in gate_up_rows.
-template <int SEG, int P, int R, bool NORM>
+template <int SEG, int P, int R, bool NORM, int FIXED = -1>
 __device__ __forceinline__ void q8_gate_up_act(const Q8Mat& gate, const Q8Mat& up, const uint16_t* __restrict__ x,
                                                uint32_t x_stride, uint16_t* __restrict__ act, uint32_t D,
                                                uint32_t F, const NormArg& norm, uint32_t blk, uint32_t nblk) {
@@ -312,7 +314,7 @@ __device__ __forceinline__ void q8_gate_up_act(const Q8Mat& gate, const Q8Mat& u
     };
     {
         uint16_t* hs = reinterpret_cast<uint16_t*>(lds_x + D);
-        XStage<NT, kStageChunks, NORM> st;
+        XStage<NT, kStageChunks, NORM, true, false, FIXED> st;
         st.load(x, D, norm);
         issue(0, std::true_type{});
         st.plain(x, hs, D, norm);
@@ -371,8 +373,9 @@ constexpr uint32_t kPhase2Chunks = 4;     // 16-byte act pieces per thread: top_
 // Phase 2: 8 slots × 8-lane segments per wave; P chunks of 32 per lane
 // (F <= 256*P); R output rows per wave in flight. Dynamic LDS:
 // xpairs_lds_bytes(top_k*F). BITS: code width of the down rows.
-// blk / nblk as in gate_up_rows.
-template <int P, int R, int BITS = 4>
+// blk / nblk as in gate_up_rows. FIXED = kStageCopy: acts 16-byte aligned
+// (the activation staging's loads then carry exact waits), -1: any alignment.
+template <int P, int R, int BITS = 4, int FIXED = -1>
 __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint16_t* __restrict__ acts,
                                            const uint16_t* __restrict__ rw,
@@ -397,7 +400,7 @@ __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_
 
     // independent loads first: the activations, the slot's expert index and
     // routing weight (unpredicated: dead slots read slot 0)
-    XStage<NT, kPhase2Chunks, false, false> xs;
+    XStage<NT, kPhase2Chunks, false, false, false, FIXED> xs;
     const NormArg copy{nullptr, nullptr, nullptr, 0.0f, kStageCopy};
     xs.load(acts, n_acts, copy);
     const uint32_t e_raw = indices[live ? slot : 0u];
@@ -503,10 +506,13 @@ __device__ __forceinline__ void moe_phase1_routed_shared(
     if (blockIdx.x < shared_blocks) {
         NormArg ns = norm;
         ns.w = snorm_w;
-        q4_gate_up_act<SEG, P, R, true>(sgate, sup, x, sact, D, Fs, ns, blockIdx.x, shared_blocks);
+        q4_gate_up_act<SEG, P, R, true, (int)kStageScaled>(sgate, sup, x, sact, D, Fs, ns, blockIdx.x,
+                                                           shared_blocks);
     } else {
-        moe_phase1_routed<SEG, P, R, true, BITS>(pool, logits, gain, E, top_k, out_idx, out_w, out_wf, x, acts, D,
-                                                 F, norm, blockIdx.x - shared_blocks, gridDim.x - shared_blocks);
+        moe_phase1_routed<SEG, P, R, true, BITS, (int)kStageScaled>(pool, logits, gain, E, top_k, out_idx, out_w,
+                                                                    out_wf, x, acts, D, F, norm,
+                                                                    blockIdx.x - shared_blocks,
+                                                                    gridDim.x - shared_blocks);
     }
 }
 
@@ -529,8 +535,8 @@ __device__ __forceinline__ void moe_phase2_shared(const ExpertPool& pool, const 
         q4_rows<32, SP, R, false, false, 4, false, kThreads, (int)kStageCopy>(
             mats, sact, Fs, [&](uint32_t row, float v) { sy[row] = f2h(v); }, blockIdx.x, shared_blocks);
     } else {
-        moe_phase2<P2, R, BITS>(pool, indices, acts, rw, nullptr, y, D, F, top_k, blockIdx.x - shared_blocks,
-                                gridDim.x - shared_blocks);
+        moe_phase2<P2, R, BITS, (int)kStageCopy>(pool, indices, acts, rw, nullptr, y, D, F, top_k,
+                                                 blockIdx.x - shared_blocks, gridDim.x - shared_blocks);
     }
 }
 
@@ -548,10 +554,13 @@ __device__ __forceinline__ void moe_phase1_routed_shared8(
     if (blockIdx.x < shared_blocks) {
         NormArg ns = norm;
         ns.w = snorm_w;
-        q8_gate_up_act<SEG8, P8, R, true>(sgate, sup, x, 0, sact, D, Fs, ns, blockIdx.x, shared_blocks);
+        q8_gate_up_act<SEG8, P8, R, true, (int)kStageScaled>(sgate, sup, x, 0, sact, D, Fs, ns, blockIdx.x,
+                                                             shared_blocks);
     } else {
-        moe_phase1_routed<SEG, P, R, true, 4>(pool, logits, gain, E, top_k, out_idx, out_w, out_wf, x, acts, D, F,
-                                              norm, blockIdx.x - shared_blocks, gridDim.x - shared_blocks);
+        moe_phase1_routed<SEG, P, R, true, 4, (int)kStageScaled>(pool, logits, gain, E, top_k, out_idx, out_w,
+                                                                 out_wf, x, acts, D, F, norm,
+                                                                 blockIdx.x - shared_blocks,
+                                                                 gridDim.x - shared_blocks);
     }
 }
 
@@ -563,10 +572,11 @@ __device__ __forceinline__ void moe_phase2_shared8(const ExpertPool& pool, const
                                                    const uint16_t* __restrict__ sact, uint16_t* __restrict__ sy,
                                                    uint32_t Fs, uint32_t shared_blocks) {
     if (blockIdx.x < shared_blocks) {
-        q8_gemv<SEG8, P8, R>(sdown.w, sdown.s, sdown.b, sact, 0, sy, 0, D, Fs, blockIdx.x, shared_blocks);
+        q8_gemv<SEG8, P8, R, (int)kStageCopy>(sdown.w, sdown.s, sdown.b, sact, 0, sy, 0, D, Fs, blockIdx.x,
+                                              shared_blocks);
     } else {
-        moe_phase2<P2, R, 4>(pool, indices, acts, rw, nullptr, y, D, F, top_k, blockIdx.x - shared_blocks,
-                             gridDim.x - shared_blocks);
+        moe_phase2<P2, R, 4, (int)kStageCopy>(pool, indices, acts, rw, nullptr, y, D, F, top_k,
+                                              blockIdx.x - shared_blocks, gridDim.x - shared_blocks);
     }
 }
 
