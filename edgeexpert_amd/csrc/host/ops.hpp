@@ -452,9 +452,7 @@ public:
         ExpertPool kp = kernel_pool(pool);
         const uint32_t p = ((f / 32) + 7) / 8;
         char name[64];
-        // 16-byte aligned acts take the form with the staging mode fixed at compile time
-        std::snprintf(name, sizeof(name), "tfq_moe_phase2_%s%sp%u", bits_infix(pool), aligned(acts, 16) ? "" : "any_",
-                      p);
+        std::snprintf(name, sizeof(name), "tfq_moe_phase2_%sp%u", bits_infix(pool), p);
         void* args[] = {&kp, &indices, &acts, &routing_weights, &residual, &y, &d, &f, &top_k};
         hipFunction_t fn = m_.get(name);
         const uint32_t lds = xpairs_lds_bytes(top_k * f);

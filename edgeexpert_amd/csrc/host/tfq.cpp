@@ -58,10 +58,7 @@ static std::vector<std::string> kernel_names() {
         names.push_back(std::string("tfq_prefill_router_logits_") + s);
     }
     for (int p = 1; p <= 4; ++p) {
-        for (const char* b : {"", "b2_", "b3_"}) {
-            names.push_back(std::string("tfq_moe_phase2_") + b + "p" + std::to_string(p));
-            names.push_back(std::string("tfq_moe_phase2_") + b + "any_p" + std::to_string(p));
-        }
+        for (const char* b : {"", "b2_", "b3_"}) names.push_back(std::string("tfq_moe_phase2_") + b + "p" + std::to_string(p));
         for (int sp = 1; sp <= 4; ++sp)
             names.push_back("tfq_moe_phase2_shared_p" + std::to_string(p) + "_sp" + std::to_string(sp));
         for (const char* q : {"4_1", "8_1", "16_1", "32_1", "64_1", "64_2", "64_3", "64_4"})

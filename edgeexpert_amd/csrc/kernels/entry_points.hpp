@@ -149,22 +149,21 @@ constexpr uint32_t kTailGemvThreads = 1024;
     TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_b3_s##SEG##_p##P, false, 3, SEG, P)             \
     TFQ_PHASE1_ROUTED_FORM(tfq_moe_phase1_routed_b3_norm_s##SEG##_p##P, true, 3, SEG, P)
 
-// Phase 2 in two forms: 16-byte aligned acts (the staging mode fixed at
-// compile time) and _any_ (any alignment).
-#define TFQ_PHASE2_FORM(NAME, BITS, P, FIXED)                                                    \
+// Phase 2 stages the acts with the mode read at run time: the fixed-mode
+// copy (exact waits, the staging overlapping the weight stream) measured
+// 6.17 against 6.00 us per config-1 launch; the fused launches of the
+// decoder layer fix it (faster there).
+#define TFQ_PHASE2_FORM(NAME, BITS, P)                                                           \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         ExpertPool pool, const uint32_t* indices, const uint16_t* acts, const uint16_t* rw,      \
         const uint16_t* residual, uint16_t* y, uint32_t D, uint32_t F, uint32_t top_k) {         \
-        moe_phase2<P, kRowsInFlight, BITS, FIXED>(pool, indices, acts, rw, residual, y, D, F,     \
-                                                  top_k, blockIdx.x, gridDim.x);                  \
+        moe_phase2<P, kRowsInFlight, BITS>(pool, indices, acts, rw, residual, y, D, F, top_k,     \
+                                           blockIdx.x, gridDim.x);                                \
     }
 #define TFQ_PHASE2(P)                                                                            \
-    TFQ_PHASE2_FORM(tfq_moe_phase2_p##P, 4, P, (int)kStageCopy)                                  \
-    TFQ_PHASE2_FORM(tfq_moe_phase2_b2_p##P, 2, P, (int)kStageCopy)                               \
-    TFQ_PHASE2_FORM(tfq_moe_phase2_b3_p##P, 3, P, (int)kStageCopy)                               \
-    TFQ_PHASE2_FORM(tfq_moe_phase2_any_p##P, 4, P, -1)                                           \
-    TFQ_PHASE2_FORM(tfq_moe_phase2_b2_any_p##P, 2, P, -1)                                        \
-    TFQ_PHASE2_FORM(tfq_moe_phase2_b3_any_p##P, 3, P, -1)
+    TFQ_PHASE2_FORM(tfq_moe_phase2_p##P, 4, P)                                                   \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_b2_p##P, 2, P)                                                \
+    TFQ_PHASE2_FORM(tfq_moe_phase2_b3_p##P, 3, P)
 
 #define TFQ_PHASE1_SHARED_FORM(NAME, BITS, SEG, P)                                               \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \

@@ -374,7 +374,8 @@ constexpr uint32_t kPhase2Chunks = 4;     // 16-byte act pieces per thread: top_
 // (F <= 256*P); R output rows per wave in flight. Dynamic LDS:
 // xpairs_lds_bytes(top_k*F). BITS: code width of the down rows.
 // blk / nblk as in gate_up_rows. FIXED = kStageCopy: acts 16-byte aligned
-// (the activation staging's loads then carry exact waits), -1: any alignment.
+// (the activation staging's loads then carry exact waits: the fused layer
+// launches), -1: any alignment, the mode read at run time.
 template <int P, int R, int BITS = 4, int FIXED = -1>
 __device__ __forceinline__ void moe_phase2(const ExpertPool& pool, const uint32_t* __restrict__ indices,
                                            const uint16_t* __restrict__ acts,
