@@ -748,7 +748,12 @@ int tfq_rt_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream) {
                      "hipMemcpyDtoD");
 }
 int tfq_rt_memset(void* dst, int value, size_t bytes) {
-    return hip_check(hipMemset(dst, value, bytes), "hipMemset");
+    // hipMemset of device memory may return before the fill is done, and the
+    // null stream does not order work on the non-blocking streams these
+    // bindings create: wait for it, as the header promises
+    int rc = hip_check(hipMemset(dst, value, bytes), "hipMemset");
+    if (rc) return rc;
+    return hip_check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
 }
 int tfq_rt_stream_create(void** stream) {
     return hip_check(hipStreamCreateWithFlags((hipStream_t*)stream, hipStreamNonBlocking),
