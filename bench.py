@@ -552,14 +552,15 @@ def traffic_summary(fetch_csv, write_csv, out=sys.stdout):
 def layer_summary(trace_csv, out=sys.stdout):
     """Per-kernel durations of the config-4 decoder layers in a rocprofv3
     --kernel-trace CSV of this script: the window from the first norm-staged
-    QKV GEMV (1024 blocks) to the last layer tail, grouped by (kernel, grid,
+    QKV GEMV (1024 blocks: the _rms form, or _norm) to the last layer tail, grouped by (kernel, grid,
     queue), median and minimum over the layers."""
     import csv
     import statistics
     rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"],
                    int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]), int(r["Grid_Size_Y"]), int(r["Queue_Id"]))
                   for r in csv.DictReader(open(trace_csv, newline="")))
-    t0 = min(s for s, e, n, gx, gy, q in rows if n.startswith("tfq_q4_gemv_norm_s32_p3") and gx == 1024)
+    t0 = min(s for s, e, n, gx, gy, q in rows
+             if n.startswith(("tfq_q4_gemv_rms_s32_p3", "tfq_q4_gemv_norm_s32_p3")) and gx == 1024)
     t1 = max(e for s, e, n, gx, gy, q in rows if n.startswith("tfq_layer_tail"))
     win = [r for r in rows if t0 <= r[0] and r[1] <= t1]
     layers = sum(1 for r in win if r[2].startswith("tfq_layer_tail"))
