@@ -454,6 +454,27 @@ __device__ __forceinline__ float block_sum(float v) {
     return t;
 }
 
+// block_sums for a call site that runs once per kernel (TAG names its LDS
+// array): no barrier is needed before the partials are written.
+template <int N, uint32_t NT, int TAG>
+__device__ __forceinline__ void block_sums_once(float (&v)[N]) {
+    __shared__ float partn[16][N];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] = seg_sum<kWave>(v[k]);
+    if (lane == 0)
+#pragma unroll
+        for (int k = 0; k < N; ++k) partn[wave][k] = v[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        float t = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < NT / 64; ++i) t += partn[i][k];
+        v[k] = t;
+    }
+}
+
 // N independent block sums at once (one pair of barriers for all of them).
 template <int N, uint32_t NT = kThreads>
 __device__ __forceinline__ void block_sums(float (&v)[N]) {
@@ -706,7 +727,9 @@ struct XStage {
         }
         if (TAIL && md(na) == kStageTail) {
             // the previous layer's tail, as layer_tail computes it (same
-            // rounding points), then its output's RMSNorm below
+            // rounding points), then its output's RMSNorm; waves past the
+            // vector skip the arithmetic (their chunks are never stored)
+            const uint32_t wave_base = threadIdx.x & ~63u;
             float s3[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (uint32_t i = 0; i < CH; ++i)
@@ -717,37 +740,53 @@ struct XStage {
                         s3[1] = fmaf((float)t1[i][e], (float)t1[i][e], s3[1]);
                         s3[2] = fmaf((float)t2[i][e], (float)t2[i][e], s3[2]);
                     }
-            block_sums<3, NT>(s3);
+            block_sums_once<3, NT, 0>(s3);
             const float inv_a = 1.0f / sqrtf(s3[0] / (float)n + na.eps);
             const float inv_1 = 1.0f / sqrtf(s3[1] / (float)n + na.eps);
             const float inv_2 = 1.0f / sqrtf(s3[2] / (float)n + na.eps);
             float s12[1] = {0.0f};
 #pragma unroll
             for (uint32_t i = 0; i < CH; ++i)
+                if (wave_base + i * NT < nch)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const _Float16 an = (_Float16)((float)av[i][e] * (float)awv[i][e] * inv_a);
-                    xv[i][e] = (_Float16)((float)xv[i][e] + (float)an);
-                    const _Float16 a1 = (_Float16)((float)t1[i][e] * (float)t1w[i][e] * inv_1);
-                    const _Float16 a2 = (_Float16)((float)t2[i][e] * (float)t2w[i][e] * inv_2);
-                    t1[i][e] = (_Float16)((float)a1 + (float)a2);
-                    if (threadIdx.x + i * NT < nch) s12[0] = fmaf((float)t1[i][e], (float)t1[i][e], s12[0]);
-                }
-            block_sums<1, NT>(s12);
+                    for (int e = 0; e < 8; ++e) {
+                        const _Float16 an = (_Float16)((float)av[i][e] * (float)awv[i][e] * inv_a);
+                        xv[i][e] = (_Float16)((float)xv[i][e] + (float)an);
+                        const _Float16 a1 = (_Float16)((float)t1[i][e] * (float)t1w[i][e] * inv_1);
+                        const _Float16 a2 = (_Float16)((float)t2[i][e] * (float)t2w[i][e] * inv_2);
+                        t1[i][e] = (_Float16)((float)a1 + (float)a2);
+                        if (threadIdx.x + i * NT < nch) s12[0] = fmaf((float)t1[i][e], (float)t1[i][e], s12[0]);
+                    }
+            block_sums_once<1, NT, 1>(s12);
             const float inv_12 = 1.0f / sqrtf(s12[0] / (float)n + na.eps);
             const float sc = (float)(_Float16)na.scalar;
+            float ss[1] = {0.0f};
 #pragma unroll
             for (uint32_t i = 0; i < CH; ++i)
+                if (wave_base + i * NT < nch)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const _Float16 f2 = (_Float16)((float)t1[i][e] * (float)tfw[i][e] * inv_12);
-                    const _Float16 r = (_Float16)((float)xv[i][e] + (float)f2);
-                    xv[i][e] = (_Float16)((float)r * sc);
-                }
+                    for (int e = 0; e < 8; ++e) {
+                        const _Float16 f2 = (_Float16)((float)t1[i][e] * (float)tfw[i][e] * inv_12);
+                        const _Float16 r = (_Float16)((float)xv[i][e] + (float)f2);
+                        xv[i][e] = (_Float16)((float)r * sc);
+                        if (threadIdx.x + i * NT < nch) ss[0] = fmaf((float)xv[i][e], (float)xv[i][e], ss[0]);
+                    }
             if (na.export_h && blockIdx.x == 0)
 #pragma unroll
                 for (uint32_t i = 0; i < CH; ++i)
                     if (threadIdx.x + i * NT < nch) reinterpret_cast<h8*>(na.export_h)[threadIdx.x + i * NT] = xv[i];
+            // the input RMSNorm of out
+            block_sums_once<1, NT, 2>(ss);
+            const float inv = 1.0f / sqrtf(ss[0] / (float)n + na.eps);
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i)
+                if (wave_base + i * NT < nch)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float xw = na.w ? (float)xv[i][e] * (float)wv[i][e] : (float)xv[i][e];
+                        xv[i][e] = (_Float16)(xw * inv);
+                    }
+            return;
         }
         if (md(na) == kStageScaled) {
 #pragma unroll
