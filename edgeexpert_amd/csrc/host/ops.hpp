@@ -167,6 +167,8 @@ private:
             form = "tail_";
         } else if (na.mode == kStageCopy && vec) {
             form = "";
+        } else if (na.mode == kStageCopy && bits == 4 && aligned(x, 16) && n <= 2 * kFixedStageMaxN) {
+            form = "wide_";
         } else if (na.mode == kStageNorm && vec && aligned(na.w, 16)) {
             form = "rms_";
         }

@@ -36,6 +36,7 @@ static std::vector<std::string> kernel_names() {
             if (*form) {
                 names.push_back(std::string("tfq_q4_gemv_tail_") + s);
                 names.push_back(std::string("tfq_q4_gemv_rms_") + s);
+                names.push_back(std::string("tfq_q4_gemv_wide_") + s);
                 names.push_back(std::string("tfq_q3_gemv_rms_") + s);
             }
             names.push_back(std::string("tfq_q3_gemv_") + form + s);

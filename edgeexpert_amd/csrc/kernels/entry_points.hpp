@@ -47,6 +47,13 @@ constexpr int kRowsInFlight = 1;
         q4_gemv_multi<SEG, P, kRowsInFlight, true, BITS>(mats, x, n);                             \
     }
 #define TFQ_Q4_GEMV(SEG, P) TFQ_GEMV_FORMS(q4, 4, SEG, P)
+// The plain int4 GEMV for aligned x of 4096 < n <= 8192 (four staged chunks
+// per thread; the full-attention layers' o projection, n = 16 heads x 512).
+#define TFQ_Q4_GEMV_WIDE(SEG, P)                                                                 \
+    extern "C" __global__ __launch_bounds__(256) void tfq_q4_gemv_wide_s##SEG##_p##P(            \
+        Q4Multi mats, const uint16_t* x, uint32_t n) {                                            \
+        q4_gemv_multi<SEG, P, kRowsInFlight, false, 4, false, kThreads, (int)kStageCopy, 4>(mats, x, n); \
+    }
 // The int4 GEMV staging the previous decoder layer's tail (kStageTail; the
 // chained decode layers' fused QKV), 1024-thread blocks.
 constexpr uint32_t kTailGemvThreads = 1024;

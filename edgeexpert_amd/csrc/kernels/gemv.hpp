@@ -68,16 +68,19 @@ __device__ __forceinline__ Q4Row resolve_row(const Q4Multi& mats, uint32_t row, 
 // nine vectors: a quarter of the blocks, each staging once for four times
 // the rows, keeps that L2 traffic to a quarter).
 // FIXED: the staging mode when it is known at compile time (XStage; the
-// tail form always is), -1 when the kernel reads it from mats.norm.
+// tail form always is), -1 when the kernel reads it from mats.norm. CHX:
+// staged 16-byte chunks per thread (0: 2, 1 with 512+ threads), which
+// bounds the fixed-mode staging's n at 8·CH·NT.
 // blk / nblk: this block's index among the blocks that share the rows, and
 // their count (blockIdx.x / gridDim.x unless a launch splits its blocks
 // between two kinds of work).
 template <int SEG, int P, int R, bool NORM, bool STAGE_FIRST = false, int BITS = 4, bool TAIL = false,
-          uint32_t NT = kThreads, int FIXED = (TAIL ? (int)kStageTail : -1), typename Out>
+          uint32_t NT = kThreads, int FIXED = (TAIL ? (int)kStageTail : -1), uint32_t CHX = 0, typename Out>
 __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __restrict__ x, uint32_t n,
                                         Out out, uint32_t blk, uint32_t nblk) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_xh[];
-    constexpr uint32_t CH = NT >= 512 ? 1 : kStageChunks;       // staged 16-byte chunks per thread
+    // staged 16-byte chunks per thread (CHX: chosen by the caller)
+    constexpr uint32_t CH = CHX ? CHX : NT >= 512 ? 1 : kStageChunks;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     constexpr uint32_t nwaves = NT / 64;
@@ -151,12 +154,12 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
 }
 
 template <int SEG, int P, int R, bool NORM, int BITS = 4, bool TAIL = false, uint32_t NT = kThreads,
-          int FIXED = (TAIL ? (int)kStageTail : -1)>
+          int FIXED = (TAIL ? (int)kStageTail : -1), uint32_t CHX = 0>
 __device__ __forceinline__ void q4_gemv_multi(const Q4Multi& mats, const uint16_t* __restrict__ x,
                                               uint32_t n) {
     const uint32_t row_bytes = (n >> 3) * BITS, ngroups = n >> 6;
     const bool out_bf16 = NORM && mats.norm.mode == kStageBf16;
-    q4_rows<SEG, P, R, NORM, false, BITS, TAIL, NT, FIXED>(mats, x, n, [&](uint32_t row, float v) {
+    q4_rows<SEG, P, R, NORM, false, BITS, TAIL, NT, FIXED, CHX>(mats, x, n, [&](uint32_t row, float v) {
         const Q4Row q = resolve_row(mats, row, row_bytes, ngroups);
         const float o = q.r ? h2f(*q.r) + v : v;
         *q.y = out_bf16 ? __builtin_bit_cast(uint16_t, (__bf16)o) : f2h(o);

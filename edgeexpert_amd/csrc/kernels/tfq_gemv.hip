@@ -4,6 +4,7 @@
 
 TFQ_Q4_TABLE(TFQ_Q4_GEMV)
 TFQ_Q4_TABLE(TFQ_Q4_GEMV_TAIL)
+TFQ_Q4_TABLE(TFQ_Q4_GEMV_WIDE)
 TFQ_Q4_TABLE(TFQ_Q3_GEMV)
 TFQ_Q4_TABLE(TFQ_LM_HEAD)
 
