@@ -67,6 +67,50 @@ def test_gemv_q4_production_shapes(ctx, stream, m, n):
     assert oracle.rel_error(y, ref) < TOL
 
 
+@pytest.mark.parametrize("m,n", [(256, 2816), (256, 8192), (128, 192)])
+def test_gemv_q4_staging_forms_agree(ctx, stream, m, n):
+    # a 16-byte aligned x takes the form whose staging mode is fixed at
+    # compile time (plain up to n = 4096, wide up to 8192), a 2-byte aligned x
+    # the form that reads the mode: the same arithmetic, so the same bits
+    W, S, B = synth.int4_matrix(3, f"forms/{m}x{n}", m, n)
+    x16 = synth.f16_vector(3, f"forms/x{n}", n)
+    wb, sb, bb = _dev(W), _dev(S), _dev(B)
+    outs = []
+    for off in (0, 2):
+        xb = DeviceBuffer(n * 2 + 16)
+        xb.upload(x16, offset=off)
+        yb = _dev(np.full(m, 0x7E00, np.uint16))
+        ops.DequantInt4GEMV(ctx).encode(stream, wb, sb, bb, xb, yb, m, n, x_offset=off)
+        stream.sync()
+        outs.append(yb.download(np.uint16, m))
+    assert np.array_equal(outs[0], outs[1])
+    assert oracle.rel_error(from_f16_bits(outs[0]), oracle.gemv_int4(W, S, B, from_f16_bits(x16))) < TOL
+
+
+@pytest.mark.parametrize("E,d,with_eff", [(128, 2816, False), (128, 2816, True), (8, 256, True)])
+def test_router_logits_staging_forms_agree(ctx, stream, E, d, with_eff):
+    # 16-byte aligned h (and effective scale) takes the router form whose
+    # staging mode is fixed at compile time, a 2-byte aligned h the form that
+    # reads the mode: the same logits, bit for bit
+    rW, rS, rB = synth.int8_matrix(4, f"rforms/{E}x{d}", E, d)
+    h16 = synth.f16_vector(4, f"rforms/h{d}", d)
+    eff = synth.f16_vector(4, f"rforms/eff{d}", d) if with_eff else None
+    rb = tuple(_dev(a) for a in (rW, rS, rB))
+    effb = _dev(eff) if with_eff else None
+    moe = ops.MoE(ctx)
+    outs = []
+    for off in (0, 2):
+        hb = DeviceBuffer(d * 2 + 16)
+        hb.upload(h16, offset=off)
+        lb = _dev(np.full(E, np.nan, np.float32))
+        moe.encode_router_logits(stream, *rb, hb.ptr(off), effb, lb, E, d)
+        stream.sync()
+        outs.append(lb.download(np.float32, E))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    ref = oracle.router_logits(rW, rS, rB, from_f16_bits(h16), None if eff is None else from_f16_bits(eff))
+    assert oracle.rel_error(outs[0], ref) < 1e-5
+
+
 def test_gemv_q4_baseline_config0(ctx, stream):
     # W[2816, 2816] int4 g64, fp16 scale/bias, x ~ N(0,1), seed 0.
     W, S, B = synth.int4_matrix(0, "c0/w", 2816, 2816)
