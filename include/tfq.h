@@ -84,7 +84,9 @@ const char *tfq_last_error_message(void);
  * Replaces DequantInt4GEMV.encode and .encodeTgx
  * (S/Kernels/Quant/DequantInt4GEMV.swift:84-180).
  * Contract: n % 64 == 0, n <= 8192, m >= 1, weights 16-byte aligned,
- * scales/biases/x/y 2-byte aligned. */
+ * scales/biases/x/y 2-byte aligned. A 16-byte aligned x runs the kernel form
+ * whose staging is fixed at compile time (faster); a 2-byte aligned one the
+ * form that reads it at run time. */
 int tfq_gemv_q4g64(tfq_ctx *ctx, void *stream, const void *weights, const uint16_t *scales,
                    const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m,
                    uint32_t n);
@@ -405,8 +407,9 @@ size_t tfq_decode_layer_workspace_bytes(const tfq_decode_layer_shape *shape, uin
  * heads, rope theta 1e6, rotated_pairs = head_dim * partial_rotary / 2 = 64)
  * pass their shape and a NULL v_proj: V = rmsnorm_head(k projection) (no
  * scale), K = rope(rmsnorm_head(k projection, k_norm)).
- * Contract: d multiple of 64, <= 4096; attention as tfq_attention_decode;
- * experts as tfq_moe_decode; workspace 256-byte aligned. */
+ * Contract: d multiple of 64, <= 4096; hidden vectors and norm weights
+ * 16-byte aligned; attention as tfq_attention_decode; experts as
+ * tfq_moe_decode; workspace 256-byte aligned. */
 int tfq_decode_layer(tfq_ctx *ctx, void *stream, const tfq_decode_layer_weights *weights,
                      const tfq_decode_layer_shape *shape, const uint16_t *hidden_in,
                      uint16_t *hidden_out, uint16_t *k_cache, uint16_t *v_cache, uint32_t position,
@@ -427,10 +430,10 @@ size_t tfq_decode_layers_workspace_bytes(const tfq_decode_layer_shape *shapes, u
  * so the chain takes n_layers - 1 launches fewer. weights / shapes [n_layers]
  * (sliding and full-attention layers may alternate; d and eps are shared);
  * k_caches / v_caches: host arrays of n_layers device pointers. One
- * workspace of tfq_decode_layers_workspace_bytes serves all layers.
- * Concurrency as tfq_decode_layer (one caller per context). No reference
- * counterpart as one call: the reference encodes the same kernels layer by
- * layer. */
+ * workspace of tfq_decode_layers_workspace_bytes serves all layers (calls
+ * that share it must not overlap). Contract as tfq_decode_layer, for every
+ * layer. No reference counterpart as one call: the reference encodes the
+ * same kernels layer by layer. */
 int tfq_decode_layers(tfq_ctx *ctx, void *stream, uint32_t n_layers,
                       const tfq_decode_layer_weights *weights, const tfq_decode_layer_shape *shapes,
                       const uint16_t *hidden_in, uint16_t *hiddens, uint16_t *const *k_caches,
