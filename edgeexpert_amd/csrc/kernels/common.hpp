@@ -874,10 +874,20 @@ struct XStage {
             return;
         }
         transform(n, na);
+        const uint32_t nch = n >> 3;
 #pragma unroll
         for (uint32_t i = 0; i < CH; ++i) {
             const uint32_t q = threadIdx.x + i * NT;
-            if (q < (n >> 3)) reinterpret_cast<h8*>(lds)[q] = xv[i];
+            if (TAIL) {
+                if (q < nch) reinterpret_cast<h8*>(lds)[q] = xv[i];
+            } else {
+                // a chunk past the end holds the last chunk (clamped load, the
+                // same transform) and is stored there again: the store stays
+                // unconditional, so the compiler cannot sink the chunk's load
+                // under a branch, whose join would wait for every load issued
+                // before it (the weight stream included)
+                reinterpret_cast<h8*>(lds)[q < nch ? q : nch - 1] = xv[i];
+            }
         }
         __syncthreads();
     }

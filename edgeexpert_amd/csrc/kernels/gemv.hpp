@@ -332,13 +332,15 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
             if (vec) {
 #pragma unroll
                 for (uint32_t i = 0; i < kStageChunks; ++i) {
-                    const uint32_t c = threadIdx.x + i * NT;
-                    if (c < (d >> 3)) {
-                        const h8 hv = reinterpret_cast<const h8*>(hs)[c];
+                    // clamped like the loads: chunks past the end rewrite the
+                    // last chunk's identical values, so no branch holds the
+                    // eff load (see XStage::plain)
+                    const uint32_t c0 = threadIdx.x + i * NT;
+                    const uint32_t c = c0 < (d >> 3) ? c0 : (d >> 3) - 1;
+                    const h8 hv = reinterpret_cast<const h8*>(hs)[c];
 #pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            lds_x[8 * c + e] = eff ? (float)hv[e] * (float)ev[i][e] : (float)hv[e];
-                    }
+                    for (int e = 0; e < 8; ++e)
+                        lds_x[8 * c + e] = eff ? (float)hv[e] * (float)ev[i][e] : (float)hv[e];
                 }
             } else {
                 for (uint32_t i = threadIdx.x; i < d; i += NT) {
