@@ -315,15 +315,29 @@ __device__ __forceinline__ void attn_combine(const float* __restrict__ part_o, c
     const float* ml = part_ml + (size_t)qh * nchunks * 2;
     if (tid < kWave) {
         float m = -__builtin_inff();
-        for (uint32_t c = tid; c < nchunks; c += kWave) m = fmaxf(m, ml[2 * c]);
-        m = wave_max(m);
         float l = 0.0f;
-        for (uint32_t c = tid; c < nchunks; c += kWave) {
-            const float w = expf(ml[2 * c] - m);
-            wgt[c] = w;
-            l = fmaf(w, ml[2 * c + 1], l);
+        if (nchunks <= kWave) {
+            // one chunk per lane: its (m, l) pair loaded once, unconditionally
+            // (clamped), so it shares the partials' memory round trip; the
+            // same values and operations as the loops below
+            const bool own = tid < nchunks;
+            const float2 v = reinterpret_cast<const float2*>(ml)[own ? tid : nchunks - 1];
+            m = wave_max(own ? v.x : -__builtin_inff());
+            const float w = expf(v.x - m);
+            // unguarded (slots past nchunks are never read): no branch that
+            // the compiler could sink the pair's second half under
+            wgt[tid] = own ? w : 0.0f;
+            l = wave_sum(own ? fmaf(w, v.y, 0.0f) : 0.0f);
+        } else {
+            for (uint32_t c = tid; c < nchunks; c += kWave) m = fmaxf(m, ml[2 * c]);
+            m = wave_max(m);
+            for (uint32_t c = tid; c < nchunks; c += kWave) {
+                const float w = expf(ml[2 * c] - m);
+                wgt[c] = w;
+                l = fmaf(w, ml[2 * c + 1], l);
+            }
+            l = wave_sum(l);
         }
-        l = wave_sum(l);
         if (tid == 0) tot = l;
     }
     __syncthreads();
