@@ -254,8 +254,11 @@ public:
         mats.total_rows = vocab;
         mats.norm = NormArg{norm_weight, nullptr, nullptr, eps, kStageNorm};
         const SegShape sh = seg_shape_fit(d / 32, 2);
+        // 16-byte aligned hidden state and norm weight: the form with the
+        // RMSNorm staging fixed at compile time
+        const bool fixed = aligned(hidden, 16) && aligned(norm_weight, 16) && d <= kFixedStageMaxN;
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_lm_head_greedy_s%u_p%u", sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_lm_head_greedy_%ss%u_p%u", fixed ? "rms_" : "", sh.seg, sh.p);
         hipFunction_t fn = m_.get(name);
         const uint32_t lds = xpairs_lds_bytes(d);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;

@@ -47,7 +47,10 @@ static std::vector<std::string> kernel_names() {
             if (*form) names.push_back(std::string("tfq_moe_phase1_shared_") + s);
             names.push_back(std::string("tfq_gate_up_act_") + form + s);
         }
-    for (const char* s : q4_shapes) names.push_back(std::string("tfq_lm_head_greedy_") + s);
+    for (const char* s : q4_shapes) {
+        names.push_back(std::string("tfq_lm_head_greedy_") + s);
+        names.push_back(std::string("tfq_lm_head_greedy_rms_") + s);
+    }
     names.push_back("tfq_lm_head_reduce");
     for (const char* s : q8_shapes) {
         names.push_back(std::string("tfq_q8_gemv_") + s);

@@ -227,11 +227,14 @@ constexpr uint32_t kTailGemvThreads = 1024;
 #define TFQ_PHASE2_SHARED8_P3(SEG8, P8) TFQ_PHASE2_SHARED8_FORM(3, SEG8, P8)
 #define TFQ_PHASE2_SHARED8_P4(SEG8, P8) TFQ_PHASE2_SHARED8_FORM(4, SEG8, P8)
 
-#define TFQ_LM_HEAD(SEG, P)                                                                      \
-    extern "C" __global__ __launch_bounds__(256) void tfq_lm_head_greedy_s##SEG##_p##P(          \
+#define TFQ_LM_HEAD_FORM(NAME, FIXED, SEG, P)                                                    \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         Q4Multi mats, const uint16_t* x, uint32_t n, uint64_t* summaries) {                      \
-        lm_head_greedy_rows<SEG, P, kRowsInFlight>(mats, x, n, summaries);                       \
+        lm_head_greedy_rows<SEG, P, kRowsInFlight, FIXED>(mats, x, n, summaries);                \
     }
+#define TFQ_LM_HEAD(SEG, P)                                                                      \
+    TFQ_LM_HEAD_FORM(tfq_lm_head_greedy_s##SEG##_p##P, -1, SEG, P)                               \
+    TFQ_LM_HEAD_FORM(tfq_lm_head_greedy_rms_s##SEG##_p##P, (int)kStageNorm, SEG, P)
 
 #define TFQ_GATE_UP_FORM(NAME, NORM, SEG, P)                                                     \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \

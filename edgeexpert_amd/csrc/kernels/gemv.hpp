@@ -375,15 +375,17 @@ __device__ __forceinline__ uint64_t topk_key(float v, uint32_t t) {
 // vocab row, x the RMSNorm of the hidden state staged like every GEMV input
 // (fp16, as the reference's xNormed buffer); each block writes the largest
 // finite z of its rows with the lowest row on ties as a topk_key
-// (0 = no finite z) to summaries[blockIdx.x].
-template <int SEG, int P, int R>
+// (0 = no finite z) to summaries[blockIdx.x]. FIXED = kStageNorm: the RMSNorm
+// staging with its mode fixed at compile time (x and the norm weight 16-byte
+// aligned, n <= 4096), -1: the mode read at run time.
+template <int SEG, int P, int R, int FIXED = -1>
 __device__ __forceinline__ void lm_head_greedy_rows(const Q4Multi& mats, const uint16_t* __restrict__ x,
                                                     uint32_t n, uint64_t* __restrict__ summaries) {
     // a lane's rows arrive in increasing order, so a strict > keeps the lowest
     // row among equal values (and -0 vs +0, which compare equal)
     float best_v = -__builtin_inff();
     uint32_t best_row = 0xFFFFFFFFu;
-    q4_rows<SEG, P, R, true, true>(mats, x, n, [&](uint32_t row, float v) {
+    q4_rows<SEG, P, R, true, true, 4, false, kThreads, FIXED>(mats, x, n, [&](uint32_t row, float v) {
         if (__builtin_isfinite(v) && (best_row == 0xFFFFFFFFu || v > best_v)) {
             best_v = v;
             best_row = row;

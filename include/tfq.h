@@ -147,7 +147,9 @@ int tfq_gemv_q8g64(tfq_ctx *ctx, void *stream, const uint8_t *weights, const uin
  * S/Metal/Sampling/logit.metal:688-787; its separate RMSNorm launch is
  * folded in). Contract: d % 64 == 0, d <= 8192, vocab >= 1, eps > 0,
  * weights 16-byte aligned, out_token 4-byte aligned, workspace
- * TFQ_LM_HEAD_WORKSPACE_BYTES bytes, 8-byte aligned. */
+ * TFQ_LM_HEAD_WORKSPACE_BYTES bytes, 8-byte aligned. A 16-byte aligned
+ * hidden (and norm_weight) with d <= 4096 runs the rows form whose RMSNorm
+ * staging is fixed at compile time (faster; the same token). */
 int tfq_lm_head_greedy(tfq_ctx *ctx, void *stream, const uint16_t *hidden,
                        const uint16_t *norm_weight, const void *weights, const uint16_t *scales,
                        const uint16_t *biases, uint32_t *out_token, uint32_t d, uint32_t vocab,

@@ -58,6 +58,30 @@ def test_lm_head_greedy_matches_oracle(ctx, stream, d, vocab, seed):
     assert _greedy(ctx, stream, h16, w16, W, S, B) == ref
 
 
+@pytest.mark.parametrize("d,vocab,seed", [(2816, 4099, 12), (4096, 3000, 13), (6144, 2000, 14)])
+def test_lm_head_greedy_staging_forms_agree(ctx, stream, d, vocab, seed):
+    # a 16-byte aligned hidden state and norm weight take the rows form whose
+    # RMSNorm staging is fixed at compile time (d <= 4096), a 2-byte aligned
+    # hidden state the form that reads the mode (and d 6144 both): the
+    # oracle's token either way
+    W, S, B, h16, w16 = _inputs(seed, d, vocab)
+    ref, z = oracle.lm_head_greedy(h16, w16, W, S, B)
+    assert _clear_winner(z)
+    bufs = [_dev(a) for a in (w16, W, S, B)]
+    toks = []
+    for off in (0, 2):
+        hb = DeviceBuffer(d * 2 + 16)
+        hb.upload(h16, offset=off)
+        out = _dev(np.full(1, 0xDEADBEEF, np.uint32))
+        ws = DeviceBuffer(LM_HEAD_WORKSPACE_BYTES)
+        ws.fill(0xFF)
+        ops.LMHeadGreedyInt4(ctx).encode_greedy_decode(stream, hb, *bufs, out, d, vocab, ws, 1e-6,
+                                                       hidden_offset=off)
+        stream.sync()
+        toks.append(int(out.download(np.uint32, 1)[0]))
+    assert toks == [ref, ref]
+
+
 def test_lm_head_greedy_without_norm_weight(ctx, stream):
     W, S, B, h16, _ = _inputs(7, 2816, 5000)
     ref, z = oracle.lm_head_greedy(h16, None, W, S, B)
