@@ -944,10 +944,19 @@ public:
         // grid is the blocks the GPU holds resident, at most the units the
         // tile bound allows
         const uint32_t bits = pool_bits(pool);
-        const char* gu = bits == 2 ? "tfq_moe_grouped_gate_up_b2" : bits == 3 ? "tfq_moe_grouped_gate_up_b3"
-                                                                           : "tfq_moe_grouped_gate_up";
-        const char* dn = bits == 2 ? "tfq_moe_grouped_down_b2" : bits == 3 ? "tfq_moe_grouped_down_b3"
-                                                                        : "tfq_moe_grouped_down";
+        // the _t launches stage each unit's scale/bias table through
+        // registers: 16-byte aligned scale/bias arrays (base and stride are)
+        // whose unit tables fit (d <= 3072 for gate/up, f <= 1024 for down)
+        const tfq_expert_offsets& po = pool.offsets;
+        bool sb16 = true;
+        for (uint64_t v : {po.gate_s, po.gate_b, po.up_s, po.up_b, po.down_s, po.down_b}) sb16 = sb16 && v % 16 == 0;
+        // (moe_prefill.hpp TableRegs: rows·K/64 words in U 16-byte pieces per thread)
+        auto fits = [](uint32_t rows, uint32_t K, uint32_t U) { return rows * (K / 64u) <= 8u * U * kUnitThreads; };
+        const bool tab_gu = sb16 && fits(128, d, 3), tab_dn = sb16 && fits(256, f, 2);
+        char gu[48], dn[48];
+        const char* bsuf = bits == 2 ? "_b2" : bits == 3 ? "_b3" : "";
+        std::snprintf(gu, sizeof(gu), "tfq_moe_grouped_gate_up%s%s", bsuf, tab_gu ? "_t" : "");
+        std::snprintf(dn, sizeof(dn), "tfq_moe_grouped_down%s%s", bsuf, tab_dn ? "_t" : "");
         // dynamic LDS: the largest unit (two activation buffers of 16·NTT
         // rows, then the table of 64·RT rows of K/64 words)
         auto lds_for = [](uint32_t K) {

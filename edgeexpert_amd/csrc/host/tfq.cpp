@@ -84,7 +84,9 @@ static std::vector<std::string> kernel_names() {
                                     std::to_string(c));
     for (const char* n : {"tfq_prefill_select", "tfq_moe_group", "tfq_moe_grouped_gate_up", "tfq_moe_grouped_down",
                           "tfq_moe_grouped_gate_up_b2", "tfq_moe_grouped_down_b2", "tfq_moe_grouped_gate_up_b3",
-                          "tfq_moe_grouped_down_b3", "tfq_moe_combine", "tfq_moe_combine_x8"})
+                          "tfq_moe_grouped_down_b3", "tfq_moe_grouped_gate_up_t", "tfq_moe_grouped_down_t",
+                          "tfq_moe_grouped_gate_up_b2_t", "tfq_moe_grouped_down_b2_t", "tfq_moe_grouped_gate_up_b3_t",
+                          "tfq_moe_grouped_down_b3_t", "tfq_moe_combine", "tfq_moe_combine_x8"})
         names.push_back(n);
     names.push_back("tfq_convert_bf16_f16");
     for (const char* hd : {"128", "256", "512"}) {

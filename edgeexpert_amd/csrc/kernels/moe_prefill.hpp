@@ -282,6 +282,51 @@ constexpr uint32_t unit_lds_bytes(int RT, int NTT, uint32_t K) {
     return 2u * unit_xbuf(NTT) * 2u + 4u * 64u * (uint32_t)RT * (K / 64u);
 }
 
+// A unit's scale/bias table staged through registers: the `count` scale and
+// bias words of its rows (16-byte aligned, count % 8 == 0, count <=
+// 8·U·kUnitThreads) loaded by issue() with unconditional, clamped loads
+// before the unit's weight and activation loads, and written to LDS as
+// (scale | bias << 16) words by store() once they arrive, so the wait for
+// them covers nothing issued after them (copy_sb_to_lds loads and stores in
+// one loop, whose waits covered the whole weight ring). Threads past the
+// table rewrite its last 16-byte piece with the same words.
+template <uint32_t U>
+struct TableRegs {
+    uint4 va[U], vb[U];
+    __device__ __forceinline__ void issue(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+                                          uint32_t count, uint32_t tid) {
+        const uint32_t n16 = count >> 3;
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t i = u * kUnitThreads + tid, c = i < n16 ? i : n16 - 1;
+            va[u] = reinterpret_cast<const uint4*>(a)[c];
+            vb[u] = reinterpret_cast<const uint4*>(b)[c];
+        }
+    }
+    __device__ __forceinline__ void store(uint32_t* __restrict__ dst, uint32_t count, uint32_t tid) const {
+        const uint32_t n16 = count >> 3;
+        uint4* t = reinterpret_cast<uint4*>(dst);
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t i = u * kUnitThreads + tid, c = i < n16 ? i : n16 - 1;
+            // v_perm: bytes 0-3 from the second operand, 4-7 from the first
+            t[2 * c] = make_uint4(__builtin_amdgcn_perm(vb[u].x, va[u].x, 0x05040100u),
+                                  __builtin_amdgcn_perm(vb[u].x, va[u].x, 0x07060302u),
+                                  __builtin_amdgcn_perm(vb[u].y, va[u].y, 0x05040100u),
+                                  __builtin_amdgcn_perm(vb[u].y, va[u].y, 0x07060302u));
+            t[2 * c + 1] = make_uint4(__builtin_amdgcn_perm(vb[u].z, va[u].z, 0x05040100u),
+                                      __builtin_amdgcn_perm(vb[u].z, va[u].z, 0x07060302u),
+                                      __builtin_amdgcn_perm(vb[u].w, va[u].w, 0x05040100u),
+                                      __builtin_amdgcn_perm(vb[u].w, va[u].w, 0x07060302u));
+        }
+    }
+};
+
+// Table words per 16-byte register piece of TableRegs: a unit of `rows`
+// weight rows over K/64 groups fits U pieces per thread when rows·K/64 <=
+// 8·U·kUnitThreads.
+constexpr uint32_t table_regs_fit(uint32_t rows, uint32_t K, uint32_t U) { return rows * (K / 64u) <= 8u * U * kUnitThreads; }
+
 // Global addresses are a block-uniform base (scalar registers) plus a 32-bit
 // per-lane offset, the form that costs one vector register. acc[i][j]: row
 // tile i, pair sub-tile j (16x16 D layout: column lane%16 = pair, rows
@@ -289,12 +334,13 @@ constexpr uint32_t unit_lds_bytes(int RT, int NTT, uint32_t K) {
 // xbase + xoff(p) (halves): the activation row of pair p (< 16·NTT; past the
 // unit's count: any valid row, not stored). sbt[i]: this lane's row of the
 // scale/bias table, published by the barrier that `publish` runs once the
-// first k-tiles' loads are in flight.
-template <int BITS, int RT, int NTT, int DEPTH, typename XOff, typename Publish>
+// first k-tiles' loads are in flight; `issue` runs first (the table's loads
+// when it is staged through registers).
+template <int BITS, int RT, int NTT, int DEPTH, typename XOff, typename Issue, typename Publish>
 __device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wbase)[RT], const uint32_t (&woff)[RT],
                                                const uint32_t* const (&sbt)[RT], const uint16_t* __restrict__ xbase,
                                                XOff xoff, uint32_t K, _Float16* __restrict__ xs,
-                                               f32x4 (&acc)[RT][NTT], Publish publish, uint32_t tid) {
+                                               f32x4 (&acc)[RT][NTT], Issue issue, Publish publish, uint32_t tid) {
     const uint32_t lane = tid & 63u, q = lane >> 4, r16 = lane & 15u;
     const uint32_t nch = K >> 5, nk = (nch + 3u) >> 2;
     constexpr uint32_t PIECES = NTT;                   // 16-byte activation pieces per thread (16·NTT rows x 16)
@@ -356,7 +402,9 @@ __device__ __forceinline__ void unit_rows_loop(const uint8_t* const (&wbase)[RT]
         }
     };
 
-    // prologue: weights of k-tiles 0..DEPTH-1, activations of 0 and 1; stage 0
+    // prologue: the table's loads (issue), weights of k-tiles 0..DEPTH-1,
+    // activations of 0 and 1; stage 0
+    issue();
     load_x(0, xr[0]);
     load_x(1, xr[1]);
 #pragma unroll
@@ -397,8 +445,10 @@ constexpr int unit_depth() { return RT == 2 ? 3 : 4; }
 // takes features f_blk + 16·(RT/2)·w + (0..16·RT/2-1), its gate rows as row
 // tiles 0..RT/2-1 and its up rows as row tiles RT/2..RT-1, so each lane holds
 // gate and up of the same (pair, feature). LDS table rows 0..NF-1: gate
-// scales/biases, NF..2NF-1: up.
-template <int BITS, int RT, int NTT>
+// scales/biases, NF..2NF-1: up. TAB: the table staged through registers
+// (TableRegs; 16-byte aligned scale/bias rows, table_regs_fit), else copied
+// by copy_sb_to_lds.
+template <int BITS, int RT, int NTT, bool TAB>
 __device__ __forceinline__ void unit_gate_up(const ExpertPool& pool, const Pair* __restrict__ sorted,
                                              const GroupedRows& gr, const uint16_t* __restrict__ hidden,
                                              uint32_t stride, uint16_t* __restrict__ act, uint32_t D, uint32_t F,
@@ -425,17 +475,29 @@ __device__ __forceinline__ void unit_gate_up(const ExpertPool& pool, const Pair*
         sbt[HT + i] = sb_lds + (NF + fc - f_blk) * G;
     }
     f32x4 acc[RT][NTT];
+    const uint32_t nf = F - f_blk < NF ? F - f_blk : NF;
+    const uint16_t* gs = reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f_blk * G;
+    const uint16_t* gb = reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (size_t)f_blk * G;
+    const uint16_t* us = reinterpret_cast<const uint16_t*>(blob + o.up_s) + (size_t)f_blk * G;
+    const uint16_t* ub = reinterpret_cast<const uint16_t*>(blob + o.up_b) + (size_t)f_blk * G;
+    TableRegs<TAB ? (RT == 4 ? 3u : 2u) : 1u> tg, tu;
     unit_rows_loop<BITS, RT, NTT, unit_depth<RT>()>(
         wbase, woff, sbt, hidden,
         [&](uint32_t p) { return sorted[gr.first + (p < gr.count ? p : 0u)].token * stride; }, D, unit_lds, acc,
         [&]() {
-            const uint32_t nf = F - f_blk < NF ? F - f_blk : NF;
-            copy_sb_to_lds<kUnitThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (size_t)f_blk * G,
-                                            reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (size_t)f_blk * G,
-                                            sb_lds, nf * G, tid);
-            copy_sb_to_lds<kUnitThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.up_s) + (size_t)f_blk * G,
-                                            reinterpret_cast<const uint16_t*>(blob + o.up_b) + (size_t)f_blk * G,
-                                            sb_lds + NF * G, nf * G, tid);
+            if constexpr (TAB) {
+                tg.issue(gs, gb, nf * G, tid);
+                tu.issue(us, ub, nf * G, tid);
+            }
+        },
+        [&]() {
+            if constexpr (TAB) {
+                tg.store(sb_lds, nf * G, tid);
+                tu.store(sb_lds + NF * G, nf * G, tid);
+            } else {
+                copy_sb_to_lds<kUnitThreads, 2>(gs, gb, sb_lds, nf * G, tid);
+                copy_sb_to_lds<kUnitThreads, 2>(us, ub, sb_lds + NF * G, nf * G, tid);
+            }
             __syncthreads();
         },
         tid);
@@ -455,8 +517,8 @@ __device__ __forceinline__ void unit_gate_up(const ExpertPool& pool, const Pair*
 }
 
 // Down projection of one unit over 64·RT outputs of D (row block bx): wave
-// w takes rows d_blk + 16·RT·w + (0..16·RT-1).
-template <int BITS, int RT, int NTT>
+// w takes rows d_blk + 16·RT·w + (0..16·RT-1). TAB as in unit_gate_up.
+template <int BITS, int RT, int NTT, bool TAB>
 __device__ __forceinline__ void unit_down(const ExpertPool& pool, const Pair* __restrict__ sorted,
                                           const GroupedRows& gr, const uint16_t* __restrict__ act,
                                           uint16_t* __restrict__ partials, uint32_t D, uint32_t F, uint32_t k,
@@ -488,13 +550,18 @@ __device__ __forceinline__ void unit_down(const ExpertPool& pool, const Pair* __
         dst_row[j] = pr.token * k + pr.rank;
     }
     f32x4 acc[RT][NTT];
+    const uint32_t nd = D - d_blk < NR ? D - d_blk : NR;
+    const uint16_t* ds = reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)d_blk * G;
+    const uint16_t* dbv = reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)d_blk * G;
+    TableRegs<TAB ? (RT == 4 ? 2u : 1u) : 1u> td;
     unit_rows_loop<BITS, RT, NTT, unit_depth<RT>()>(
         wbase, woff, sbt, act, [&](uint32_t p) { return (gr.first + (p < gr.count ? p : 0u)) * F; }, F, unit_lds, acc,
         [&]() {
-            const uint32_t nd = D - d_blk < NR ? D - d_blk : NR;
-            copy_sb_to_lds<kUnitThreads, 2>(reinterpret_cast<const uint16_t*>(blob + o.down_s) + (size_t)d_blk * G,
-                                            reinterpret_cast<const uint16_t*>(blob + o.down_b) + (size_t)d_blk * G,
-                                            sb_lds, nd * G, tid);
+            if constexpr (TAB) td.issue(ds, dbv, nd * G, tid);
+        },
+        [&]() {
+            if constexpr (TAB) td.store(sb_lds, nd * G, tid);
+            else copy_sb_to_lds<kUnitThreads, 2>(ds, dbv, sb_lds, nd * G, tid);
             __syncthreads();
         },
         tid);
@@ -649,7 +716,10 @@ __device__ __forceinline__ void run_units(const Tile* __restrict__ tiles, uint32
 
 static_assert(kUnitThreads == kProjThreads, "the grouped launches run kProjThreads threads");
 
-template <int BITS>
+// TAB: the units' scale/bias tables staged through registers (the host
+// picks these launches for 16-byte aligned scale/bias offsets whose tables
+// fit: d <= 3072 for gate/up, f <= 1024 for down).
+template <int BITS, bool TAB = false>
 __device__ __forceinline__ void moe_grouped_gate_up_launch(const ExpertPool& pool, const Pair* __restrict__ sorted,
                                                            const Tile* __restrict__ tiles, uint32_t* __restrict__ n_tiles,
                                                            const uint16_t* __restrict__ hidden, uint32_t stride,
@@ -658,16 +728,16 @@ __device__ __forceinline__ void moe_grouped_gate_up_launch(const ExpertPool& poo
     run_units(
         tiles, n_tiles, gl,
         [&](const GroupedRows& gr, uint32_t bx) {
-            if (gr.count <= 32u) unit_gate_up<BITS, 2, 2>(pool, sorted, gr, hidden, stride, act, D, F, bx);
-            else unit_gate_up<BITS, 2, 4>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+            if (gr.count <= 32u) unit_gate_up<BITS, 2, 2, TAB>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+            else unit_gate_up<BITS, 2, 4, TAB>(pool, sorted, gr, hidden, stride, act, D, F, bx);
         },
         [&](const GroupedRows& gr, uint32_t bx) {
-            if (gr.count <= 16u) unit_gate_up<BITS, 4, 1>(pool, sorted, gr, hidden, stride, act, D, F, bx);
-            else unit_gate_up<BITS, 4, 2>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+            if (gr.count <= 16u) unit_gate_up<BITS, 4, 1, TAB>(pool, sorted, gr, hidden, stride, act, D, F, bx);
+            else unit_gate_up<BITS, 4, 2, TAB>(pool, sorted, gr, hidden, stride, act, D, F, bx);
         });
 }
 
-template <int BITS>
+template <int BITS, bool TAB = false>
 __device__ __forceinline__ void moe_grouped_down_launch(const ExpertPool& pool, const Pair* __restrict__ sorted,
                                                         const Tile* __restrict__ tiles, uint32_t* __restrict__ n_tiles,
                                                         const uint16_t* __restrict__ act, uint16_t* __restrict__ partials,
@@ -675,12 +745,12 @@ __device__ __forceinline__ void moe_grouped_down_launch(const ExpertPool& pool, 
     run_units(
         tiles, n_tiles, gl,
         [&](const GroupedRows& gr, uint32_t bx) {
-            if (gr.count <= 32u) unit_down<BITS, 2, 2>(pool, sorted, gr, act, partials, D, F, k, bx);
-            else unit_down<BITS, 2, 4>(pool, sorted, gr, act, partials, D, F, k, bx);
+            if (gr.count <= 32u) unit_down<BITS, 2, 2, TAB>(pool, sorted, gr, act, partials, D, F, k, bx);
+            else unit_down<BITS, 2, 4, TAB>(pool, sorted, gr, act, partials, D, F, k, bx);
         },
         [&](const GroupedRows& gr, uint32_t bx) {
-            if (gr.count <= 16u) unit_down<BITS, 4, 1>(pool, sorted, gr, act, partials, D, F, k, bx);
-            else unit_down<BITS, 4, 2>(pool, sorted, gr, act, partials, D, F, k, bx);
+            if (gr.count <= 16u) unit_down<BITS, 4, 1, TAB>(pool, sorted, gr, act, partials, D, F, k, bx);
+            else unit_down<BITS, 4, 2, TAB>(pool, sorted, gr, act, partials, D, F, k, bx);
         });
 }
 

@@ -9,19 +9,24 @@ extern "C" __global__ __launch_bounds__(kGroupThreads) void tfq_moe_group(
     moe_group(idx, w, T, k, E, sorted, offsets, counts, tiles, n_tiles, status);
 }
 
-#define TFQ_GROUPED(SUFFIX, BITS)                                                                \
+// _t: the units' scale/bias tables staged through registers (aligned
+// tables that fit, chosen by the host)
+#define TFQ_GROUPED(SUFFIX, BITS, TAB)                                                           \
     extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_gate_up##SUFFIX( \
         ExpertPool pool, const Pair* sorted, const Tile* tiles, uint32_t* n_tiles,               \
         const uint16_t* hidden, uint32_t stride, uint16_t* act, uint32_t D, uint32_t F,          \
         GroupedLaunch gl) {                                                                      \
-        moe_grouped_gate_up_launch<BITS>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, gl); \
+        moe_grouped_gate_up_launch<BITS, TAB>(pool, sorted, tiles, n_tiles, hidden, stride, act, D, F, gl); \
     }                                                                                            \
     extern "C" __global__ __launch_bounds__(kProjThreads, 2) void tfq_moe_grouped_down##SUFFIX(  \
         ExpertPool pool, const Pair* sorted, const Tile* tiles, uint32_t* n_tiles,               \
         const uint16_t* act, uint16_t* partials, uint32_t D, uint32_t F, uint32_t k,             \
         GroupedLaunch gl) {                                                                      \
-        moe_grouped_down_launch<BITS>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, gl); \
+        moe_grouped_down_launch<BITS, TAB>(pool, sorted, tiles, n_tiles, act, partials, D, F, k, gl); \
     }
-TFQ_GROUPED(, 4)
-TFQ_GROUPED(_b2, 2)
-TFQ_GROUPED(_b3, 3)
+TFQ_GROUPED(, 4, false)
+TFQ_GROUPED(_b2, 2, false)
+TFQ_GROUPED(_b3, 3, false)
+TFQ_GROUPED(_t, 4, true)
+TFQ_GROUPED(_b2_t, 2, true)
+TFQ_GROUPED(_b3_t, 3, true)

@@ -270,6 +270,46 @@ def test_grouped_tile_and_stream_split(ctx, stream, bits):
         assert rel < TOL, f"expert {e} ({c} pairs): rel={rel}"
 
 
+def _repack_misaligned(pool_bytes, offs, stride, E, d, f):
+    # the same experts with every scale and bias array at a 2-byte (not
+    # 16-byte) aligned offset, weight arrays still 16-byte aligned
+    sizes = {"gate_w": f * d // 2, "gate_s": f * (d // 64) * 2, "gate_b": f * (d // 64) * 2,
+             "up_w": f * d // 2, "up_s": f * (d // 64) * 2, "up_b": f * (d // 64) * 2,
+             "down_w": d * f // 2, "down_s": d * (f // 64) * 2, "down_b": d * (f // 64) * 2}
+    new, cur = {}, 0
+    for name in synth.OFFSET_ORDER:
+        cur = (cur + 15) // 16 * 16 + (2 if name.endswith(("_s", "_b")) else 0)
+        new[name] = cur
+        cur += sizes[name]
+    new_stride = (cur + 255) // 256 * 256
+    out = np.zeros(E * new_stride, np.uint8)
+    for e in range(E):
+        for name in synth.OFFSET_ORDER:
+            src = e * stride + offs[name]
+            out[e * new_stride + new[name]:e * new_stride + new[name] + sizes[name]] = pool_bytes[src:src + sizes[name]]
+    return out, new, new_stride
+
+
+def test_grouped_table_forms_agree(ctx, stream):
+    # 16-byte aligned scale/bias arrays take the launches that stage each
+    # unit's scale/bias table through registers, 2-byte aligned ones the
+    # launches that copy it through a loop: the same table, so the same bits
+    T, k, E, d, f = 128, 8, 32, 512, 256
+    pool_bytes, offs, stride = synth.expert_pool(11, "tables/experts", E, d, f)
+    idx, w16 = synth.zipf_routing(11, "tables/route", T, E, k)
+    hidden = synth.f16_vector(11, "tables/x", T * d)
+    mis_bytes, mis_offs, mis_stride = _repack_misaligned(pool_bytes, offs, stride, E, d, f)
+    assert all(mis_offs[n] % 16 == 2 for n in synth.OFFSET_ORDER if n.endswith(("_s", "_b")))
+    got, parts, h2 = _run_grouped(ctx, stream, pool_bytes, offs, stride, E, idx, w16, hidden, d, T, k, d, f)
+    _, parts_m, h2_m = _run_grouped(ctx, stream, mis_bytes, mis_offs, mis_stride, E, idx, w16, hidden, d, T, k, d, f)
+    assert got["status"] == 0 and not np.any(parts == UNWRITTEN)
+    assert np.array_equal(parts, parts_m) and np.array_equal(h2, h2_m)
+    ref = oracle.grouped_route_partials(got["sorted"].astype(oracle.PAIR_DTYPE), hidden, d,
+                                        *_oracle_pool(pool_bytes, offs, stride), k, d, f, T)
+    rel = oracle.rel_error(from_f16_bits(parts), from_f16_bits(ref))
+    assert rel < TOL, f"partials rel={rel}"
+
+
 def test_grouped_schedule_at_tile_bound(ctx, stream):
     # 8192 pairs over 256 experts: the tile bound (TFQ_MOE_MAX_TILES = 320)
     # and a work list of several units per resident block in both launches;
