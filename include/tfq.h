@@ -621,7 +621,10 @@ int tfq_group_pairs_host(const tfq_pair *pairs, int64_t n_pairs, int64_t query_c
  * (S/Kernels/Prefill/MoE/PrefillGroupedRoutedMoE.swift:446-527), and its
  * 2/3-bit forms (prefill.metal:1304-1450) when pool->weight_bits is 2 or 3.
  * Contract: d, f multiples of 64 and at most 8192 (TFQ_E_UNSUPPORTED
- * beyond); hidden rows, act_scratch and route_partials 16-byte aligned. */
+ * beyond); hidden rows, act_scratch and route_partials 16-byte aligned.
+ * Pools whose scale/bias offsets are 16-byte aligned (d <= 3072 for gate/up,
+ * f <= 1024 for down) run launches that stage each unit's scale/bias table
+ * through registers (faster; the same bits). */
 int tfq_moe_grouped(tfq_ctx *ctx, void *stream, const tfq_expert_pool *pool,
                     const tfq_pair *sorted, const tfq_tile *tiles, uint32_t *n_tiles,
                     uint32_t max_tiles, const uint16_t *hidden, uint32_t hidden_stride,
