@@ -877,6 +877,30 @@ def main():
         stream.sync()
         floor_graph_us = batch_avg_us(lambda i: g1.launch(stream), 4) / n_copies
         floor_graph_warm_us = batch_avg_us(lambda i: g2.launch(stream), 4) / n_copies
+        # the int8 GEMV (tfq_gemv_q8g64) at the same shape: 128 rotating
+        # copies of its 8.4 MB (cold) and one copy (warm)
+        W8, S8, B8 = synth.int8_matrix(0, "c0/w8", 2816, 2816)
+        w8sz, s8sz = W8.nbytes, S8.nbytes
+        n8 = 128
+        big8 = DeviceBuffer(n8 * (w8sz + 2 * s8sz))
+        for i in range(n8):
+            base = i * (w8sz + 2 * s8sz)
+            big8.upload(W8, base)
+            big8.upload(S8, base + w8sz)
+            big8.upload(B8, base + w8sz + s8sz)
+        gemv8 = ops.DequantInt8GEMV(ctx)
+
+        def gemv8_launch(copy):
+            base = copy * (w8sz + 2 * s8sz)
+            gemv8.encode(stream, big8, big8, big8, x0, y0, 2816, 2816, weights_offset=base,
+                         scales_offset=base + w8sz, biases_offset=base + w8sz + s8sz)
+
+        gemv8_bytes = w8sz + 2 * s8sz + 2 * 2816 * 2
+        cold8_us = batch_avg_us(gemv8_launch, n8)
+        warm8_us = batch_avg_us(lambda i: gemv8_launch(0), n8)
+        del big8
+        log(f"int8 GEMV 2816x2816 (back-to-back): cold {cold8_us:.2f} us "
+            f"({gemv8_bytes / (cold8_us * 1e-6) / 1e9:.0f} GB/s), warm {warm8_us:.2f} us")
         log(f"GEMV C0 (back-to-back): cold {cold_us:.2f} us ({cold_gbs:.0f} GB/s), warm {warm_us:.2f} us "
             f"({warm_gbs:.0f} GB/s); cold from a graph {cold_graph_us:.2f} us ({graph_gbs:.0f} GB/s); "
             f"cold read of the same bytes {ceil_us:.2f} us (GEMV at {ceil_us / cold_us:.2f} of it); "
@@ -892,7 +916,10 @@ def main():
                                                "first chunk (cold) or one address (warm)"},
                 "warm_us": round(warm_us, 3), "warm_gbs": round(warm_gbs, 1),
                 "cold_graph_us": round(cold_graph_us, 3), "cold_graph_frac": round(graph_gbs / HBM_PEAK_GBS, 4),
-                "copies_rotated": n_copies}
+                "copies_rotated": n_copies,
+                "int8_gemv": {"shape": [2816, 2816], "bytes": gemv8_bytes, "cold_us": round(cold8_us, 3),
+                              "cold_gbs": round(gemv8_bytes / (cold8_us * 1e-6) / 1e9, 1),
+                              "warm_us": round(warm8_us, 3), "copies_rotated": n8}}
 
     def leg_c2():
         """Config 2: the bf16 prefill GEMM 512 x 8192 x 2816."""

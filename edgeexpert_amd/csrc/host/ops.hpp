@@ -209,8 +209,11 @@ public:
         if (!aligned(scales, 2) || !aligned(biases, 2) || !aligned(x, 2) || !aligned(y, 2))
             return fail(TFQ_E_INVAL, "fp16 operands must be 2-byte aligned");
         const SegShape sh = seg_shape(n / 16, 4);
+        // 16-byte aligned rows of x: the form with the copy staging fixed at
+        // compile time (n <= 4096 is checked above)
+        const bool fixed = aligned(x, 16) && (tokens == 1 || x_stride % 8 == 0);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_q8_gemv_s%u_p%u", sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_q8_gemv_%ss%u_p%u", fixed ? "c_" : "", sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&weights, &scales, &biases, &x, &x_stride, &y, &y_stride, &m, &n};
         hipFunction_t fn = m_.get(name);

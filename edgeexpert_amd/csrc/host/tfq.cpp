@@ -54,6 +54,7 @@ static std::vector<std::string> kernel_names() {
     names.push_back("tfq_lm_head_reduce");
     for (const char* s : q8_shapes) {
         names.push_back(std::string("tfq_q8_gemv_") + s);
+        names.push_back(std::string("tfq_q8_gemv_c_") + s);
         names.push_back(std::string("tfq_q8_gate_up_act_") + s);
         names.push_back(std::string("tfq_q8_gate_up_act_norm_") + s);
         names.push_back(std::string("tfq_router_logits_") + s);

@@ -64,13 +64,17 @@ constexpr uint32_t kTailGemvThreads = 1024;
     }
 #define TFQ_Q3_GEMV(SEG, P) TFQ_GEMV_FORMS(q3, 3, SEG, P)
 
-#define TFQ_Q8_GEMV(SEG, P)                                                                      \
-    extern "C" __global__ __launch_bounds__(256) void tfq_q8_gemv_s##SEG##_p##P(                 \
+// _c_: x 16-byte aligned (every token's row), the copy staging fixed at compile time
+#define TFQ_Q8_GEMV_FORM(NAME, FIXED, SEG, P)                                                    \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* x,               \
         uint32_t x_stride, uint16_t* y, uint32_t y_stride, uint32_t m, uint32_t n) {              \
-        q8_gemv<SEG, P, kRowsInFlight>(W, S, B, x, x_stride, y, y_stride, m, n, blockIdx.x,      \
-                                       gridDim.x);                                                \
+        q8_gemv<SEG, P, kRowsInFlight, FIXED>(W, S, B, x, x_stride, y, y_stride, m, n, blockIdx.x, \
+                                              gridDim.x);                                         \
     }
+#define TFQ_Q8_GEMV(SEG, P)                                                                      \
+    TFQ_Q8_GEMV_FORM(tfq_q8_gemv_s##SEG##_p##P, -1, SEG, P)                                      \
+    TFQ_Q8_GEMV_FORM(tfq_q8_gemv_c_s##SEG##_p##P, (int)kStageCopy, SEG, P)
 
 // Shared expert, int8 rows: fused gate/up/act in the plain and norm staging forms.
 #define TFQ_Q8_GATE_UP_FORM(NAME, NORM, SEG, P)                                                  \

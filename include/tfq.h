@@ -124,7 +124,8 @@ int tfq_gemv_qg64_qkv(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *q, const 
 
 /* y[m] = W8[m][n] · x[n]; int8 g64 weights. Replaces DequantInt8GEMV.encode
  * (S/Kernels/Quant/DequantInt8GEMV.swift:50-81).
- * Contract: n % 64 == 0, n <= 4096, weights 16-byte aligned. */
+ * Contract: n % 64 == 0, n <= 4096, weights 16-byte aligned. A 16-byte
+ * aligned x runs the form whose staging is fixed at compile time. */
 int tfq_gemv_q8g64(tfq_ctx *ctx, void *stream, const uint8_t *weights, const uint16_t *scales,
                    const uint16_t *biases, const uint16_t *x, uint16_t *y, uint32_t m,
                    uint32_t n);

@@ -197,6 +197,27 @@ def test_gemv_q8_sweep(ctx, stream, m, n):
     _q8_run_and_compare(ctx, stream, m, n, m * 1000 + n)
 
 
+@pytest.mark.parametrize("m,n", [(128, 2816), (1024, 4096), (96, 192)])
+def test_gemv_q8_staging_forms_agree(ctx, stream, m, n):
+    # a 16-byte aligned x takes the int8 GEMV form whose copy staging is
+    # fixed at compile time, a 2-byte aligned x the form that reads the
+    # staging mode: the same arithmetic, so the same bits (and the oracle's)
+    W, S, B, xr = ref_int8_rows(0x160 + m, f"int8-forms-m{m}-n{n}", m, n, -1.0, 1.0, extra=n)
+    x16 = f16_bits(xr)
+    wb, sb, bb = _dev(W), _dev(bf16_to_f16_exact(S)), _dev(bf16_to_f16_exact(B))
+    outs = []
+    for off in (0, 2):
+        xb = DeviceBuffer(n * 2 + 16)
+        xb.upload(x16, offset=off)
+        yb = _dev(np.full(m, 0x7E00, np.uint16))
+        ops.DequantInt8GEMV(ctx).encode(stream, wb, sb, bb, xb, yb, m, n, x_offset=off)
+        stream.sync()
+        outs.append(yb.download(np.uint16, m))
+    assert np.array_equal(outs[0], outs[1])
+    ref = oracle.gemv_int8(W, S, B, f16_round(xr), oracle.FMT_BF16)
+    assert oracle.rel_error(from_f16_bits(outs[0]), ref) < TOL
+
+
 # ------------------------------------------------------------- router ----
 
 def _run_router(ctx, stream, W, S16, B16, h16, eff16, gain16, E, d, k, ws=None):
