@@ -610,8 +610,11 @@ public:
         Q4Mat u = {static_cast<const uint8_t*>(up.weights), up.scales, up.biases, nullptr, nullptr, f, 0};
         NormArg na = stage;
         const SegShape sh = seg_shape_fit(d / 32, 2);
+        // an aligned x in the copy mode: the form whose staging is fixed at
+        // compile time
+        const char* form = na.mode == kStageCopy && aligned(x, 16) && d <= kFixedStageMaxN ? "c_" : form_prefix(na);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_gate_up_act_%ss%u_p%u", form_prefix(na), sh.seg, sh.p);
+        std::snprintf(name, sizeof(name), "tfq_gate_up_act_%ss%u_p%u", form, sh.seg, sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&g, &u, &x, &act_scratch, &d, &f, &na};
         hipFunction_t fn = m_.get(name);

@@ -44,7 +44,10 @@ static std::vector<std::string> kernel_names() {
                 names.push_back(std::string("tfq_moe_phase1_") + b + form + s);
                 names.push_back(std::string("tfq_moe_phase1_routed_") + b + form + s);
             }
-            if (*form) names.push_back(std::string("tfq_moe_phase1_shared_") + s);
+            if (*form) {
+                names.push_back(std::string("tfq_moe_phase1_shared_") + s);
+                names.push_back(std::string("tfq_gate_up_act_c_") + s);
+            }
             names.push_back(std::string("tfq_gate_up_act_") + form + s);
         }
     for (const char* s : q4_shapes) {

@@ -240,16 +240,18 @@ constexpr uint32_t kTailGemvThreads = 1024;
     TFQ_LM_HEAD_FORM(tfq_lm_head_greedy_s##SEG##_p##P, -1, SEG, P)                               \
     TFQ_LM_HEAD_FORM(tfq_lm_head_greedy_rms_s##SEG##_p##P, (int)kStageNorm, SEG, P)
 
-#define TFQ_GATE_UP_FORM(NAME, NORM, SEG, P)                                                     \
+// _c_: x 16-byte aligned, D <= 4096: the copy staging fixed at compile time
+#define TFQ_GATE_UP_FORM(NAME, NORM, FIXED, SEG, P)                                              \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         Q4Mat gate, Q4Mat up, const uint16_t* x, uint16_t* act, uint32_t D, uint32_t F,          \
         NormArg norm) {                                                                           \
-        q4_gate_up_act<SEG, P, kRowsInFlight, NORM>(gate, up, x, act, D, F, norm, blockIdx.x,     \
-                                                    gridDim.x);                                   \
+        q4_gate_up_act<SEG, P, kRowsInFlight, NORM, FIXED>(gate, up, x, act, D, F, norm,         \
+                                                           blockIdx.x, gridDim.x);                \
     }
 #define TFQ_GATE_UP(SEG, P)                                                                      \
-    TFQ_GATE_UP_FORM(tfq_gate_up_act_s##SEG##_p##P, false, SEG, P)                               \
-    TFQ_GATE_UP_FORM(tfq_gate_up_act_norm_s##SEG##_p##P, true, SEG, P)
+    TFQ_GATE_UP_FORM(tfq_gate_up_act_s##SEG##_p##P, false, -1, SEG, P)                           \
+    TFQ_GATE_UP_FORM(tfq_gate_up_act_norm_s##SEG##_p##P, true, -1, SEG, P)                       \
+    TFQ_GATE_UP_FORM(tfq_gate_up_act_c_s##SEG##_p##P, false, (int)kStageCopy, SEG, P)
 
 // n/32 chunks (of 32 codes) per row at every code width; (SEG, P) with SEG·P >= chunks (the host picks
 // the pair that wastes the fewest lanes).

@@ -307,7 +307,8 @@ int tfq_moe_decode_token_noalloc(tfq_ctx *ctx, void *stream, const tfq_router *r
  * Replaces SharedExpertInt4.encode (S/Kernels/MoE/SharedExpertInt4.swift:30-94),
  * whose GPU sequence rounds gate and up to fp16 before the activation (its
  * CPU reference does not; the rounding moves the output ~8e-4 from it).
- * Contract: d, f multiples of 64 and <= 8192. */
+ * Contract: d, f multiples of 64 and <= 8192. A 16-byte aligned x (d <=
+ * 4096) runs the gate/up form whose staging is fixed at compile time. */
 int tfq_shared_expert_q4(tfq_ctx *ctx, void *stream, const tfq_q4_matrix *gate,
                          const tfq_q4_matrix *up, const tfq_q4_matrix *down, const uint16_t *x,
                          uint16_t *y, uint32_t d, uint32_t f, uint16_t *act_scratch);

@@ -459,6 +459,29 @@ def test_shared_expert_int4_matches_reference(ctx, stream, d, f, seed, label):
     assert rel < TOL, f"rel={rel}"
 
 
+def test_shared_expert_int4_staging_forms_agree(ctx, stream):
+    # a 16-byte aligned x takes the gate/up form whose copy staging is fixed
+    # at compile time, a 2-byte aligned x the form that reads the mode: the
+    # same bits
+    d, f, label = 2816, 2112, "c4/shared"
+    x16 = f16_bits(synth.normal(synth.seed_key(3, label + "/x"), d))
+    mats = [synth.int4_matrix(3, label + n, r, c) for n, r, c in (("/gate", f, d), ("/up", f, d), ("/down", d, f))]
+    proj = lambda m, r, c: ops.Q4Projection(_dev(m[0]), _dev(m[1]), _dev(m[2]), rows=r, cols=c)
+    gate, up, down = proj(mats[0], f, d), proj(mats[1], f, d), proj(mats[2], d, f)
+    outs = []
+    for off in (0, 2):
+        xb = DeviceBuffer(d * 2 + 16)
+        xb.upload(x16, offset=off)
+        y = _dev(np.full(d, 0x7E00, np.uint16))
+        act = _dev(np.zeros(f, np.uint16))
+        ops.SharedExpertInt4(ctx).encode(stream, xb.ptr(off), gate, up, down, y, act)
+        stream.sync()
+        outs.append(y.download(np.uint16, d))
+    assert np.array_equal(outs[0], outs[1])
+    ref = oracle.shared_expert_int4(*mats, from_f16_bits(x16), d, f)
+    assert oracle.rel_error(from_f16_bits(outs[0]), ref) < TOL
+
+
 # -------------------------------------------------------------- loader ----
 
 def test_convert_bf16_to_f16_exact_and_counts_inexact(ctx, stream):
