@@ -658,7 +658,11 @@ public:
         NormArg na = stage;
         const SegShape sh = seg_shape(d / 16, 4);
         char name[64];
-        std::snprintf(name, sizeof(name), "tfq_q8_gate_up_act_%ss%u_p%u", form_prefix(na), sh.seg, sh.p);
+        // 16-byte aligned rows of x in the copy mode: the form whose staging is
+        // fixed at compile time (d <= 4096 is checked above)
+        const bool fixed = na.mode == kStageCopy && aligned(x, 16) && (tokens == 1 || x_stride % 8 == 0);
+        std::snprintf(name, sizeof(name), "tfq_q8_gate_up_act_%ss%u_p%u", fixed ? "c_" : form_prefix(na), sh.seg,
+                      sh.p);
         const uint32_t rows_per_block = (kBlock / 64) * (64 / sh.seg) * kRowsInFlight;
         void* args[] = {&g, &u, &x, &x_stride, &act_scratch, &d, &f, &na};
         hipFunction_t fn = m_.get(name);

@@ -59,6 +59,7 @@ static std::vector<std::string> kernel_names() {
         names.push_back(std::string("tfq_q8_gemv_") + s);
         names.push_back(std::string("tfq_q8_gemv_c_") + s);
         names.push_back(std::string("tfq_q8_gate_up_act_") + s);
+        names.push_back(std::string("tfq_q8_gate_up_act_c_") + s);
         names.push_back(std::string("tfq_q8_gate_up_act_norm_") + s);
         names.push_back(std::string("tfq_router_logits_") + s);
         names.push_back(std::string("tfq_router_logits_c_") + s);

@@ -77,16 +77,18 @@ constexpr uint32_t kTailGemvThreads = 1024;
     TFQ_Q8_GEMV_FORM(tfq_q8_gemv_c_s##SEG##_p##P, (int)kStageCopy, SEG, P)
 
 // Shared expert, int8 rows: fused gate/up/act in the plain and norm staging forms.
-#define TFQ_Q8_GATE_UP_FORM(NAME, NORM, SEG, P)                                                  \
+// _c_: x 16-byte aligned (every token's row): the copy staging fixed at compile time
+#define TFQ_Q8_GATE_UP_FORM(NAME, NORM, FIXED, SEG, P)                                           \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         Q8Mat gate, Q8Mat up, const uint16_t* x, uint32_t x_stride, uint16_t* act, uint32_t D,   \
         uint32_t F, NormArg norm) {                                                               \
-        q8_gate_up_act<SEG, P, kRowsInFlight, NORM>(gate, up, x, x_stride, act, D, F, norm,       \
-                                                    blockIdx.x, gridDim.x);                       \
+        q8_gate_up_act<SEG, P, kRowsInFlight, NORM, FIXED>(gate, up, x, x_stride, act, D, F, norm, \
+                                                           blockIdx.x, gridDim.x);                \
     }
 #define TFQ_Q8_GATE_UP(SEG, P)                                                                   \
-    TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_s##SEG##_p##P, false, SEG, P)                         \
-    TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_norm_s##SEG##_p##P, true, SEG, P)
+    TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_s##SEG##_p##P, false, -1, SEG, P)                     \
+    TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_norm_s##SEG##_p##P, true, -1, SEG, P)                 \
+    TFQ_Q8_GATE_UP_FORM(tfq_q8_gate_up_act_c_s##SEG##_p##P, false, (int)kStageCopy, SEG, P)
 
 // The router GEMV: any staging mode and alignment, and the copy (_c_) and
 // post-attention (_pa_) modes fixed at compile time for aligned inputs.

@@ -326,7 +326,9 @@ typedef tfq_q4_matrix tfq_q8_matrix;
  * fp16 [f]. Replaces SharedExpertInt8.encode
  * (S/Kernels/MoE/SharedExpertInt8.swift:90-130; kernel
  * shared_int8_gate_up_act_simd, S/Metal/Quant/dequant_int8.metal:99-154).
- * Contract: d, f multiples of 64 and <= 4096; gate/up weights 16-byte aligned. */
+ * Contract: d, f multiples of 64 and <= 4096; gate/up weights 16-byte aligned.
+ * A 16-byte aligned x runs the gate/up form whose staging is fixed at
+ * compile time. */
 int tfq_shared_expert_q8(tfq_ctx *ctx, void *stream, const tfq_q8_matrix *gate,
                          const tfq_q8_matrix *up, const tfq_q8_matrix *down, const uint16_t *x,
                          uint16_t *y, uint32_t d, uint32_t f, uint16_t *act_scratch);

@@ -73,6 +73,28 @@ def test_shared_expert_int8_matches_reference(ctx, stream, d, f, seed, label):
     assert rel_act < TOL, f"act rel={rel_act}"
 
 
+def test_shared_expert_int8_staging_forms_agree(ctx, stream):
+    # a 16-byte aligned x takes the int8 gate/up form whose copy staging is
+    # fixed at compile time, a 2-byte aligned x the form that reads the mode:
+    # the same bits (act and output)
+    d, f = 2816, 2112
+    x16 = f16_bits(synth.normal(synth.seed_key(5, "forms8/x"), d))
+    gate, up, down = _synthetic(5, "forms8", d, f, 8)
+    pg, pu, pd = _proj(gate, f, d), _proj(up, f, d), _proj(down, d, f)
+    outs = []
+    for off in (0, 2):
+        xb = DeviceBuffer(d * 2 + 16)
+        xb.upload(x16, offset=off)
+        y = _dev(np.full(d, 0x7E00, np.uint16))
+        act = _dev(np.zeros(f, np.uint16))
+        ops.SharedExpertInt8(ctx).encode(stream, xb.ptr(off), pg, pu, pd, y, act)
+        stream.sync()
+        outs.append((y.download(np.uint16, d), act.download(np.uint16, f)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    ref = oracle.shared_expert_int8(gate, up, down, from_f16_bits(x16), d, f)
+    assert oracle.rel_error(from_f16_bits(outs[0][0]), ref) < TOL
+
+
 def test_shared_expert_int8_rejects_bad_contract(ctx, stream):
     b = _dev(np.zeros(1 << 16, np.uint8))
     p = ops.Q4Projection(b, b, b, rows=64, cols=100)
