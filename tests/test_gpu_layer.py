@@ -45,6 +45,8 @@ def _run_attention(ctx, stream, q16, k16, v16, hd, nq, nkv, seq, window, scale):
 
 @pytest.mark.parametrize("hd,nq,nkv,seq,window,scale", [
     (256, 16, 8, 4096, 0, None),        # config 4 attention at full context
+    (256, 16, 8, 8192, 0, None),        # 128 chunks: the combine's general (m, l) loops and chunk loop
+    (128, 8, 2, 5000, 0, None),         # 79 chunks, ragged last one
     (256, 16, 8, 4096, 0, 1.0),         # Gemma 4 scale 1.0
     (256, 16, 8, 1000, 512, None),      # sliding window (encodeSWA)
     (256, 16, 4, 300, 0, None),         # GQA group 4
