@@ -328,6 +328,22 @@ __device__ __forceinline__ void router_logits(const uint8_t* __restrict__ W, con
                     ev[i] = __builtin_bit_cast(h8, ld16h(eff ? eff : h, c < (d >> 3) ? c : (d >> 3) - 1));
                 }
             issue0();
+            if (st.vec && vec) {
+                // the staged chunks (after the NormArg transform) times eff
+                // straight into the fp32 vector: no fp16 copy in LDS and one
+                // barrier; clamped and unconditional like the loads
+                st.transform(d, norm);
+#pragma unroll
+                for (uint32_t i = 0; i < kStageChunks; ++i) {
+                    const uint32_t c0 = threadIdx.x + i * NT;
+                    const uint32_t c = c0 < (d >> 3) ? c0 : (d >> 3) - 1;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        lds_x[8 * c + e] = eff ? (float)st.xv[i][e] * (float)ev[i][e] : (float)st.xv[i][e];
+                }
+                __syncthreads();
+                return;
+            }
             st.plain(h, hs, d, norm);
             if (vec) {
 #pragma unroll
