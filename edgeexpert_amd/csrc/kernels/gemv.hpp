@@ -285,6 +285,19 @@ __device__ __forceinline__ void q8_gemv(const uint8_t* __restrict__ W, const uin
             XStage<kThreads, kStageChunks, true, true, false, FIXED> st;
             st.load(x, n, copy);
             issue0();
+            if (st.vec) {
+                // the staged chunks widened straight into the fp32 vector
+                // (clamped and unconditional like the loads)
+#pragma unroll
+                for (uint32_t i = 0; i < kStageChunks; ++i) {
+                    const uint32_t c0 = threadIdx.x + i * kThreads;
+                    const uint32_t c = c0 < (n >> 3) ? c0 : (n >> 3) - 1;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) lds_x[8 * c + e] = (float)st.xv[i][e];
+                }
+                __syncthreads();
+                return;
+            }
             st.plain(x, xs, n, copy);
             for (uint32_t i = threadIdx.x; i < n; i += kThreads) lds_x[i] = h2f(xs[i]);
             __syncthreads();

@@ -317,8 +317,21 @@ __device__ __forceinline__ void q8_gate_up_act(const Q8Mat& gate, const Q8Mat& u
         XStage<NT, kStageChunks, NORM, true, false, FIXED> st;
         st.load(x, D, norm);
         issue(0, std::true_type{});
-        st.plain(x, hs, D, norm);
-        for (uint32_t i = threadIdx.x; i < D; i += NT) lds_x[i] = h2f(hs[i]);
+        if (st.vec) {
+            // the staged chunks (after the NormArg transform) widened straight
+            // into the fp32 vector (clamped and unconditional like the loads)
+            st.transform(D, norm);
+#pragma unroll
+            for (uint32_t i = 0; i < kStageChunks; ++i) {
+                const uint32_t c0 = threadIdx.x + i * NT;
+                const uint32_t c = c0 < (D >> 3) ? c0 : (D >> 3) - 1;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) lds_x[8 * c + e] = (float)st.xv[i][e];
+            }
+        } else {
+            st.plain(x, hs, D, norm);
+            for (uint32_t i = threadIdx.x; i < D; i += NT) lds_x[i] = h2f(hs[i]);
+        }
         __syncthreads();
     }
     float xr[P][16];
