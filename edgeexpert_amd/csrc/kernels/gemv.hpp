@@ -122,6 +122,68 @@ __device__ __forceinline__ void q4_rows(const Q4Multi& mats, const uint16_t* __r
     };
     XStage<NT, CH, NORM, true, TAIL, FIXED> xs;
     xs.load(x, n, mats.norm);
+    if constexpr (BITS != 4) {
+        // 2 and 3 bits: two row groups in flight per wave (the next group's
+        // loads issued before the current group's dot), since a group carries
+        // 3/4 or 1/2 of int4's bytes and its unpack takes longer. Every issue
+        // is unconditional (rows past the end re-read the last row, chunks
+        // past the row its last chunk), so each wait covers exactly the group
+        // it consumes; the wave-uniform group count ends the loop.
+        QChunk<BITS> w2[R][P];
+        uint32_t s2[R][P], b2[R][P];
+        auto issue2 = [&](uint32_t grp) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t row0 = seg_id + (grp * R + r) * seg_total;
+                const Q4Row q = resolve_row(mats, row0 < total ? row0 : total - 1, row_bytes, ngroups);
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const uint32_t c0 = sl + p * SEG;
+                    const uint32_t c = c0 < lpr ? c0 : lpr - 1;
+                    w2[r][p] = ldg_chunk<BITS>(q.w, c);
+                    s2[r][p] = q.s[c >> 1];
+                    b2[r][p] = q.b[c >> 1];
+                }
+            }
+        };
+        auto consume = [&](uint32_t grp, const QChunk<BITS> (&w)[R][P], const uint32_t (&s)[R][P],
+                           const uint32_t (&b)[R][P], const XPairs& xpp) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const uint32_t c = sl + p * SEG;
+                    if (c < lpr) {
+                        XChunk xc;
+                        read_xpairs(xpp, c, xc);
+                        const float d = dot_chunk<BITS>(w[r][p], xc);
+                        acc = fmaf(h2f((uint16_t)s[r][p]), d, acc);
+                        acc = fmaf(h2f((uint16_t)b[r][p]), xc.sum, acc);
+                    }
+                }
+                const float v = seg_sum<SEG>(acc);
+                const uint32_t row = seg_id + (grp * R + r) * seg_total;
+                if (sl == 0 && row < total) out(row, v);
+            }
+        };
+        // groups of the wave's first segment (the most of its segments)
+        const uint32_t seg0 = (blk * nwaves + wave) * spw;
+        const uint32_t ng = __builtin_amdgcn_readfirstlane(
+            seg0 < total ? (total - seg0 + R * seg_total - 1) / (R * seg_total) : 0u);   // wave-uniform
+        if (!STAGE_FIRST) issue(0, std::true_type{});
+        const XPairs xp2 = xs.pairs(x, lds_xh, n, mats.norm);
+        if (STAGE_FIRST) issue(0, std::true_type{});
+        uint32_t grp = 0;
+        for (; grp + 1 < ng; grp += 2) {
+            issue2(grp + 1);
+            consume(grp, wv, sr, br, xp2);
+            issue(grp + 2, std::true_type{});      // past the last group: the last row, not stored
+            consume(grp + 1, w2, s2, b2, xp2);
+        }
+        if (grp < ng) consume(grp, wv, sr, br, xp2);
+        return;
+    }
     if (!STAGE_FIRST) issue(0, std::true_type{});
     const XPairs xp = xs.pairs(x, lds_xh, n, mats.norm);
     if (STAGE_FIRST) issue(0, std::true_type{});
