@@ -35,8 +35,12 @@ def _gemv(ctx, stream, W, S, B, x16, m, n, bits):
     return from_f16_bits(y.download(np.uint16, m))
 
 
+# the last two shapes have more rows than one round of resident blocks
+# covers (40000 and 30001 rows: every wavefront runs several row groups,
+# their count odd for some wavefronts and even for others), which runs the
+# 3-bit GEMV's two-groups-in-flight loop and its last odd group
 @pytest.mark.parametrize("m,n", [(64, 64), (65, 128), (129, 320), (1024, 2816), (512, 4096), (96, 8192),
-                                 (2048, 2816)])
+                                 (2048, 2816), (40000, 2816), (30001, 512)])
 def test_gemv_b3(ctx, stream, m, n):
     W, S, B = synth.affine_matrix(3, f"b3/gemv/{m}x{n}", m, n, 3)
     x16 = synth.f16_vector(3, f"b3/x/{n}", n)
@@ -62,8 +66,9 @@ def test_gemv_b3_extreme_codes(ctx, stream):
     assert oracle.rel_error(got, ref) < TOL
 
 
-def test_qkv_b3(ctx, stream):
-    mq, mkv, n = 2048, 512, 2816
+@pytest.mark.parametrize("mq,mkv", [(2048, 512), (16384, 8192)])
+def test_qkv_b3(ctx, stream, mq, mkv):
+    n = 2816
     mats = {k: synth.affine_matrix(6, f"b3/qkv/{k}", rows, n, 3) for k, rows in (("q", mq), ("k", mkv), ("v", mkv))}
     x16 = synth.f16_vector(6, "b3/qkv/x", n)
     projs = {k: ops.Q4Projection(_dev(W), _dev(S), _dev(B), W.shape[0], n) for k, (W, S, B) in mats.items()}
@@ -74,7 +79,7 @@ def test_qkv_b3(ctx, stream):
     for k, (W, S, B) in mats.items():
         got = from_f16_bits(ys[k].download(np.uint16, W.shape[0]))
         ref = oracle.gemv_affine(W, S, B, from_f16_bits(x16), 3)
-        assert oracle.rel_error(got, ref) < TOL, k
+        assert oracle.rel_error(got, ref) < TOL, (mq, mkv, k)
 
 
 @pytest.mark.parametrize("bits", [2, 5, 0])
