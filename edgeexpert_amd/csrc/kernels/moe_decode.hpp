@@ -66,77 +66,81 @@ __device__ __forceinline__ void gate_up_rows(const uint16_t* __restrict__ x, uin
     const uint32_t seg_id = (blk * nwaves + wave) * spw + lane / SEG;
     const uint32_t seg_total = nblk * nwaves * spw;
 
-    QChunk<BITS> gv[R][P], uv[R][P];
-    uint32_t gsr[R][P], gbr[R][P], usr[R][P], ubr[R][P];    // raw fp16 scales / biases
-    // the first group's loads are unconditional (rows and chunks clamped;
-    // dead or invalid rows read expert 0's), so the waits after them are
-    // exact; later groups skip what they do not need
-    auto issue = [&](uint32_t grp, auto first_c) {
-        constexpr bool FIRST = decltype(first_c)::value;
+    // Two row groups in flight per wave (buffers A and B alternate): the next
+    // group's loads are issued before the current group's dot. Every issue is
+    // unconditional (rows past the end re-read the last row, chunks past the
+    // row its last chunk, dead or invalid rows expert 0's; none is stored),
+    // so each wait covers exactly the group it consumes, and the wave-uniform
+    // group count ends the loop without a branch around any load.
+    struct Buf {
+        QChunk<BITS> gv[R][P], uv[R][P];
+        uint32_t gs[R][P], gb[R][P], us[R][P], ub[R][P];    // raw fp16 scales / biases
+    };
+    Buf A, B;
+    auto issue = [&](uint32_t grp, Buf& f) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t row0 = seg_id + (grp * R + r) * seg_total;
-            const uint32_t row = FIRST && row0 >= total ? total - 1 : row0;
-            if (FIRST || row < total) {
-                const GateUpRow q = rowfn(row);
-                if (FIRST || (q.live && q.valid)) {
+            const GateUpRow q = rowfn(row0 < total ? row0 : total - 1);
 #pragma unroll
-                    for (int p = 0; p < P; ++p) {
-                        const uint32_t c0 = sl + p * SEG;
-                        const uint32_t c = FIRST && c0 >= lpr ? lpr - 1 : c0;
-                        if (FIRST || c < lpr) {
-                            gv[r][p] = ldg_chunk<BITS>(q.gw, c);
-                            uv[r][p] = ldg_chunk<BITS>(q.uw, c);
-                            gsr[r][p] = q.gs[c >> 1];
-                            gbr[r][p] = q.gb[c >> 1];
-                            usr[r][p] = q.us[c >> 1];
-                            ubr[r][p] = q.ub[c >> 1];
-                        }
-                    }
-                }
+            for (int p = 0; p < P; ++p) {
+                const uint32_t c0 = sl + p * SEG;
+                const uint32_t c = c0 < lpr ? c0 : lpr - 1;
+                f.gv[r][p] = ldg_chunk<BITS>(q.gw, c);
+                f.uv[r][p] = ldg_chunk<BITS>(q.uw, c);
+                f.gs[r][p] = q.gs[c >> 1];
+                f.gb[r][p] = q.gb[c >> 1];
+                f.us[r][p] = q.us[c >> 1];
+                f.ub[r][p] = q.ub[c >> 1];
             }
         }
     };
-    XStage<NT, kStageChunks, NORM, true, false, FIXED> xs;
-    xs.load(x, D, norm);
-    prologue();
-    XPairs xp;
-    if constexpr (X_FIRST) xp = xs.pairs(x, lds_xh, D, norm);
-    issue(0, std::true_type{});
-    if constexpr (!X_FIRST) xp = xs.pairs(x, lds_xh, D, norm);
-    for (uint32_t grp = 0; seg_id + grp * R * seg_total < total; ++grp) {
-        float ga[R], ua[R];
+    auto consume = [&](uint32_t grp, const Buf& f, const XPairs& xp) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            ga[r] = 0.0f;
-            ua[r] = 0.0f;
+            float ga = 0.0f, ua = 0.0f;
 #pragma unroll
             for (int p = 0; p < P; ++p) {
                 const uint32_t c = sl + p * SEG;
                 if (c < lpr) {
                     XChunk xc;
                     read_xpairs(xp, c, xc);
-                    const float gd = dot_chunk<BITS>(gv[r][p], xc);
-                    const float ud = dot_chunk<BITS>(uv[r][p], xc);
-                    ga[r] = fmaf(h2f((uint16_t)gsr[r][p]), gd, ga[r]);
-                    ga[r] = fmaf(h2f((uint16_t)gbr[r][p]), xc.sum, ga[r]);
-                    ua[r] = fmaf(h2f((uint16_t)usr[r][p]), ud, ua[r]);
-                    ua[r] = fmaf(h2f((uint16_t)ubr[r][p]), xc.sum, ua[r]);
+                    const float gd = dot_chunk<BITS>(f.gv[r][p], xc);
+                    const float ud = dot_chunk<BITS>(f.uv[r][p], xc);
+                    ga = fmaf(h2f((uint16_t)f.gs[r][p]), gd, ga);
+                    ga = fmaf(h2f((uint16_t)f.gb[r][p]), xc.sum, ga);
+                    ua = fmaf(h2f((uint16_t)f.us[r][p]), ud, ua);
+                    ua = fmaf(h2f((uint16_t)f.ub[r][p]), xc.sum, ua);
                 }
             }
-        }
-        issue(grp + 1, std::false_type{});
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float g = seg_sum<SEG>(ga[r]);
-            const float u = seg_sum<SEG>(ua[r]);
+            const float g = seg_sum<SEG>(ga);
+            const float u = seg_sum<SEG>(ua);
             const uint32_t row = seg_id + (grp * R + r) * seg_total;
             if (row < total && sl == 0) {
                 const GateUpRow q = rowfn(row);
                 if (q.live) out(row, q.valid ? gelu_tanh(g) * u : __builtin_nanf(""));
             }
         }
+    };
+    XStage<NT, kStageChunks, NORM, true, false, FIXED> xs;
+    xs.load(x, D, norm);
+    // groups of the wave's first segment (the most of its segments)
+    const uint32_t seg0 = (blk * nwaves + wave) * spw;
+    const uint32_t ng = __builtin_amdgcn_readfirstlane(
+        seg0 < total ? (total - seg0 + R * seg_total - 1) / (R * seg_total) : 0u);   // wave-uniform
+    prologue();
+    XPairs xp;
+    if constexpr (X_FIRST) xp = xs.pairs(x, lds_xh, D, norm);
+    issue(0, A);
+    if constexpr (!X_FIRST) xp = xs.pairs(x, lds_xh, D, norm);
+    uint32_t grp = 0;
+    for (; grp + 1 < ng; grp += 2) {
+        issue(grp + 1, B);
+        consume(grp, A, xp);
+        issue(grp + 2, A);      // past the last group: the last row, not stored
+        consume(grp + 1, B, xp);
     }
+    if (grp < ng) consume(grp, A, xp);
 }
 
 // Row `row` of phase 1 given the slot it belongs to and that slot's expert.
