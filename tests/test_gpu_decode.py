@@ -378,6 +378,33 @@ def test_routed_pipeline_and_hit_split_match_reference(ctx, stream):
     assert rel < TOL, f"rel={rel}"
 
 
+@pytest.mark.parametrize("F", [4096, 3968])
+def test_moe_phase1_many_row_groups_per_wave(ctx, stream, F):
+    # 8 slots x F gate/up rows: more rows than one round of resident phase-1
+    # blocks covers, so every wavefront runs several row groups (two in
+    # flight), their count even everywhere at F = 4096 and odd for some
+    # wavefronts at F = 3968. Reference: g and u from the float64 GEMV
+    # oracle, act = gelu_tanh(g)·u
+    E, D, K = 12, 256, 8
+    pool_bytes, offs, stride = synth.expert_pool(0x7A1, f"groups/experts/{F}", E, D, F)
+    pool = ops.ExpertPool(_dev(pool_bytes), stride, E, offs)
+    sel = np.array([11, 3, 7, 0, 9, 5, 2, 8], np.uint32)
+    x16 = synth.f16_vector(0x7A2, f"groups/x/{F}", D)
+    acts = _dev(np.full(K * F, 0x7E00, np.uint16))       # fp16 NaN sentinels
+    ops.MoE(ctx).encode_routed_phase1(stream, pool, _dev(sel), _dev(x16), acts, D, F, K)
+    stream.sync()
+    got = from_f16_bits(acts.download(np.uint16, K * F)).reshape(K, F)
+    x = from_f16_bits(x16)
+    for s, e in enumerate(sel):
+        blob = pool_bytes[int(e) * stride:(int(e) + 1) * stride]
+        g = oracle.gemv_int4_f64(*synth.blob_views(blob, offs, D, F, "gate"), x)
+        u = oracle.gemv_int4_f64(*synth.blob_views(blob, offs, D, F, "up"), x)
+        ref = 0.5 * g * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g + 0.044715 * g ** 3))) * u
+        assert not np.isnan(got[s]).any(), f"F={F} slot {s}: a row was not written"
+        rel = oracle.rel_error(got[s], ref)
+        assert rel < TOL, f"F={F} slot {s}: rel={rel}"
+
+
 def test_moe_baseline_config1_router_to_experts(ctx, stream):
     # 1 token, h ~ N(0,1) [2816], int8 router [128 x 2816],
     # softmax top-8, 128 int4 experts (gate/up [704 x 2816], down [2816 x 704])
