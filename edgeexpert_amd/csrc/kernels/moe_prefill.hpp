@@ -779,11 +779,28 @@ __device__ __forceinline__ void moe_combine_x8(const uint16_t* __restrict__ part
     if (i >= T * n8) return;
     const uint32_t t = i / n8, d = 8u * (i - t * n8);
     float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t r = 0; r < k; ++r) {
-        const float wr = h2f(w[t * k + r]);
-        const h8 v = __builtin_bit_cast(h8, *reinterpret_cast<const uint4*>(partials + ((size_t)t * k + r) * D + d));
+    if (k == 8) {
+        // top-8 (the model's k): the eight rows' loads in flight together,
+        // then the same fma chain in rank order (one memory round trip
+        // instead of eight)
+        h8 v[8];
+        float wr[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = fmaf(wr, (float)v[e], acc[e]);
+        for (uint32_t r = 0; r < 8; ++r) {
+            wr[r] = h2f(w[t * 8 + r]);
+            v[r] = __builtin_bit_cast(h8, *reinterpret_cast<const uint4*>(partials + ((size_t)t * 8 + r) * D + d));
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < 8; ++r)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(wr[r], (float)v[r][e], acc[e]);
+    } else {
+        for (uint32_t r = 0; r < k; ++r) {
+            const float wr = h2f(w[t * k + r]);
+            const h8 v = __builtin_bit_cast(h8, *reinterpret_cast<const uint4*>(partials + ((size_t)t * k + r) * D + d));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(wr, (float)v[e], acc[e]);
+        }
     }
     h8 out;
 #pragma unroll
